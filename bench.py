@@ -1,0 +1,268 @@
+"""Benchmark of the MI355X palette-weight GEMM path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload (one step): the Conformer feed-forward block in fp16 on
+8 windows x 188 frames x 1024 channels - H = SiLU(X W1) with a 5-bit palette
+W1 1024->4096, then Y = X + 0.5 (H W2) with a 5-bit palette W2 4096->1024.
+Inputs are seeded synthetic data resident in HBM before timing starts. One
+JSON line is printed: whole-job TFLOP/s, the roofline of the dominant kernel
+(timed with HIP events on the stream the kernels run on) and the CPU oracle's
+throughput on a bounded sample of the same workload.
+
+Other workloads (for profiling; same JSON shape):
+  single-gemm-fp32  X[256x1024] f32 x 6-bit W 1024->4096 + bias
+  small-m           5-bit 1024->4096 f16 GEMM at --rows M (HBM-bound regime)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}  # MI355X dense MFMA
+PEAK_HBM_GBS = 8000.0
+METRIC = "palette-GEMM TFLOP/s & % roofline; encoder audio-sec/sec at 1 MI355X"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="ff-block",
+                   choices=["ff-block", "single-gemm-fp32", "small-m"])
+    p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
+    p.add_argument("--cpu-sample-rows", type=int, default=0,
+                   help="rows of the CPU-oracle sample (0 = workload default)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--variant", type=int, default=-1, help="force a tile variant (sweeps)")
+    return p.parse_args()
+
+
+class Kernel:
+    """One fused palette GEMM launch of the step and its bookkeeping."""
+
+    def __init__(self, name, op, flops, nbytes, precision):
+        self.name = name
+        self.op = op
+        self.flops = flops
+        self.nbytes = nbytes
+        self.precision = precision
+        self.times_ms = []
+
+    def summary(self):
+        avg = float(np.mean(self.times_ms))
+        plan = self.op.plan()
+        return {
+            "kernel": plan.kernel.decode(),
+            "grid": list(plan.grid),
+            "avg_us": avg * 1e3,
+            "tflops": self.flops / (avg * 1e-3) / 1e12,
+            "gbs": self.nbytes / (avg * 1e-3) / 1e9,
+            "flops": self.flops,
+            "algorithmic_bytes": self.nbytes,
+        }
+
+
+def build_ff_block(abi, ctx, keep):
+    import parakeet_wgsl_amd.workloads as wl
+    ff = wl.feed_forward_block(0)
+    m = ff.x.shape[0]
+    x = keep(ctx.array(ff.x))
+    hidden = keep(ctx.empty((m, 4096), np.float16))
+    y = keep(ctx.empty((m, 1024), np.float16))
+    op1 = abi.GemmOp(ctx, a=x, packed=keep(ctx.array(ff.w1.packed)), palette=keep(ctx.array(ff.w1.palette)),
+                     output=hidden, bits=5, rows=m, inner=1024, columns=4096, activation="silu",
+                     label="ff-expand")
+    op2 = abi.GemmOp(ctx, a=hidden, packed=keep(ctx.array(ff.w2.packed)), palette=keep(ctx.array(ff.w2.palette)),
+                     output=y, bits=5, rows=m, inner=4096, columns=1024, residual=x, residual_scale=0.5,
+                     label="ff-contract")
+    e = ff.expand_case()
+    c = ff.contract_case(np.zeros((m, 4096), np.float16))
+    kernels = [Kernel("ff-expand", op1, e.flops, e.algorithmic_bytes(), "f16"),
+               Kernel("ff-contract", op2, c.flops, c.algorithmic_bytes(), "f16")]
+    config = {"workload": "conformer-ff-block-fp16", "windows": 8, "frames": 188, "rows": m,
+              "d_model": 1024, "hidden": 4096, "palette_bits": 5, "epilogues": ["silu", "0.5*residual"]}
+    return kernels, config, ff
+
+
+def build_single_gemm(abi, ctx, keep):
+    import parakeet_wgsl_amd.workloads as wl
+    case = wl.single_gemm_fp32(0)
+    out = keep(ctx.empty((case.rows, 4096), np.float32))
+    op = abi.GemmOp(ctx, a=keep(ctx.array(case.a)), packed=keep(ctx.array(case.weight.packed)),
+                    palette=keep(ctx.array(case.weight.palette)), output=out, bits=6, rows=case.rows,
+                    inner=1024, columns=4096, bias=keep(ctx.array(case.bias)), label="single-gemm-fp32")
+    config = {"workload": "single-palette-gemm-fp32", "rows": case.rows, "inner": 1024, "columns": 4096,
+              "palette_bits": 6, "epilogues": ["bias"]}
+    return [Kernel("single-gemm-fp32", op, case.flops, case.algorithmic_bytes(), "f32")], config, case
+
+
+def build_small_m(abi, ctx, keep, rows):
+    import parakeet_wgsl_amd.workloads as wl
+    case = wl.gemm_case(0, rows, 1024, 4096, 5)
+    out = keep(ctx.empty((rows, 4096), np.float16))
+    op = abi.GemmOp(ctx, a=keep(ctx.array(case.a)), packed=keep(ctx.array(case.weight.packed)),
+                    palette=keep(ctx.array(case.weight.palette)), output=out, bits=5, rows=rows,
+                    inner=1024, columns=4096, label=f"small-m-{rows}")
+    config = {"workload": "small-m-palette-gemm-fp16", "rows": rows, "inner": 1024, "columns": 4096,
+              "palette_bits": 5}
+    return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16")], config, case
+
+
+def cpu_baseline(workload, data, sample_rows):
+    """The oracle (reference semantics restated in C) on a bounded sample."""
+    from oracle import pko
+    threads = min(os.cpu_count() or 1, 16)
+    if workload == "ff-block":
+        rows = sample_rows or 128
+        x = data.x[:rows]
+        t0 = time.perf_counter()
+        h = pko.gemm(x, data.w1.packed, 5, data.w1.palette, 4096, activation="silu", mode="f16-chain",
+                     threads=threads)
+        pko.gemm(h, data.w2.packed, 5, data.w2.palette, 1024, residual=x, residual_scale=0.5,
+                 mode="f16-chain", threads=threads)
+        dt = time.perf_counter() - t0
+        flops = 2 * rows * 1024 * 4096 * 2
+        sample = f"{rows} of 1504 rows of the FF block, f16-accumulator chain (reference fp16 semantics)"
+    elif workload == "single-gemm-fp32":
+        rows = sample_rows or data.rows
+        t0 = time.perf_counter()
+        pko.gemm(data.a[:rows], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
+                 mode="f32-chain", threads=threads)
+        dt = time.perf_counter() - t0
+        flops = 2 * rows * 1024 * 4096
+        sample = f"{rows} of {data.rows} rows, f32 fma chain (reference fp32 semantics)"
+    else:
+        rows = sample_rows or data.rows
+        t0 = time.perf_counter()
+        pko.gemm(data.a[:rows], data.weight.packed, 5, data.weight.palette, 4096, mode="f16-chain",
+                 threads=threads)
+        dt = time.perf_counter() - t0
+        flops = 2 * rows * 1024 * 4096
+        sample = f"{rows} rows, f16-accumulator chain"
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": sample, "seconds": dt}
+
+
+def read_traffic(kernel_name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        table = json.load(f)
+    entry = table.get(kernel_name)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the palette path shards by windows with no exchange step)", file=sys.stderr)
+        sys.exit(2)
+
+    import parakeet_wgsl_amd.palette_abi as abi
+    ctx = abi.Context(0)
+    held = []
+
+    def keep(arr):
+        held.append(arr)
+        return arr
+
+    if args.workload == "ff-block":
+        kernels, config, data = build_ff_block(abi, ctx, keep)
+    elif args.workload == "single-gemm-fp32":
+        kernels, config, data = build_single_gemm(abi, ctx, keep)
+    else:
+        kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
+    if args.variant >= 0:
+        for k in kernels:
+            k.op.set_variant(args.variant)
+
+    stream = ctx.stream
+    for _ in range(args.warmup):
+        for k in kernels:
+            k.op.enqueue(0, stream)
+    ctx.synchronize(stream)
+
+    marks = [[ctx.event() for _ in range(len(kernels) + 1)] for _ in range(args.steps)]
+    start, end = ctx.event(), ctx.event()
+    ctx.synchronize(stream)
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for step in range(args.steps):
+        for i, k in enumerate(kernels):
+            marks[step][i].record(stream)
+            k.op.enqueue(0, stream)
+        marks[step][-1].record(stream)
+    end.record(stream)
+    end.synchronize()
+    ctx.synchronize(stream)
+    wall = time.perf_counter() - wall0
+
+    total_ms = start.elapsed_ms(end)
+    for step in range(args.steps):
+        for i, k in enumerate(kernels):
+            k.times_ms.append(marks[step][i].elapsed_ms(marks[step][i + 1]))
+    ms_per_step = total_ms / args.steps
+    flops = sum(k.flops for k in kernels)
+    value = flops / (ms_per_step * 1e-3) / 1e12
+
+    dominant = max(kernels, key=lambda k: float(np.mean(k.times_ms)))
+    dom = dominant.summary()
+    peak = PEAK_TFLOPS[dominant.precision]
+    compute_s = dominant.flops / (peak * 1e12)
+    memory_s = dominant.nbytes / (PEAK_HBM_GBS * 1e9)
+    if compute_s >= memory_s:
+        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak, "unit": "TFLOP/s",
+                    "frac": dom["tflops"] / peak}
+    else:
+        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": dom["gbs"] / PEAK_HBM_GBS}
+    roofline["kernel"] = dom["kernel"]
+    roofline["traffic"] = read_traffic(dom["kernel"])
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.workload, data, args.cpu_sample_rows)
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if dominant.precision == "f16" else "f32",
+        "data": "synthetic (seeded random palette codes, LUTs and activations)",
+        "config": config,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": {k.name: k.summary() for k in kernels},
+        "wall_ms_per_step": wall / args.steps * 1e3,
+        "device": ctx.info().name.decode(),
+    }
+    print(json.dumps(line), flush=True)
+    for k in kernels:
+        k.op.release()
+    for arr in held:
+        arr.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

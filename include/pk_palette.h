@@ -1,0 +1,256 @@
+/*
+ * pk_palette.h - C ABI of the MI355X (gfx950) palette-weight GEMM library.
+ *
+ * This is the drop-in boundary for parakeet.wgsl's palette GEMM path. Every
+ * entry point takes plain pointers and sizes; device pointers are HIP device
+ * allocations (from pk_alloc or any other allocator on the same device) and
+ * streams are hipStream_t values passed as void* (NULL = the context stream).
+ *
+ * Status codes follow the int-enum style of the reference's only native ABI
+ * (model/native/kmeans1d_sorted_unique.h:21-47): every call returns a
+ * pk_status and pk_last_error() holds the calling thread's last message.
+ * PK_RANGE_ERROR marks the failures the reference raises as RangeError
+ * (src/webgpu/kernels/gemm.ts:431-438, :982); PK_INVALID_ARGUMENT marks the
+ * ones it raises as Error.
+ *
+ * Reference interfaces replaced (parakeet.wgsl, TypeScript over WebGPU):
+ *   pk_context_*            F16GemmKernel.create / F32GemmKernel.create and
+ *                           destroy (src/webgpu/kernels/gemm.ts:519-619,
+ *                           :849-855, :3009-3095)
+ *   pk_gemm_create          F16GemmKernel.createDispatch (gemm.ts:621-704),
+ *                           F32GemmKernel.createDispatch (gemm.ts:3097-3182)
+ *                           with the contract checks requireGemmShape
+ *                           (:971-1011), requireProductionSpecialization
+ *                           (:1031-1067), requireRuntimeWeight (:1069-1161)
+ *   pk_gemm_enqueue         GemmDispatch.encode(encoder, timestampWrites,
+ *                           shape) (gemm.ts:419-463; F32 twin :2912-2960)
+ *   pk_gemm_destroy         GemmDispatch.destroy (gemm.ts:465-469)
+ *   pk_prepared_weight_*    F16GemmKernel.createPreparedPaletteWeight
+ *                           (gemm.ts:706-748), PreparedPaletteWeight (:375-385)
+ *   pk_palette_expand       PaletteWeightExpander.createPooledDispatch +
+ *                           encode (src/model/palette-expander.ts:234-303),
+ *                           shader paletteDequantWgslForScalar (:478-587)
+ *   pk_unpack_codes         the code extraction of palette-expander.ts:500-511
+ *                           exposed on its own for bit-exact checks
+ *   pk_gemm_plan            planF16SubgroupGemm / planF32SubgroupGemm
+ *                           (gemm.ts:941-969, :2317-2345): the launch grid
+ *   pk_stream_*, pk_event_* GPUQueue.onSubmittedWorkDone / GpuTimestampRecorder
+ *                           (src/webgpu/timestamp.ts:44-80) equivalents
+ *   pk_alloc / pk_upload /  GPUDevice.createBuffer / queue.writeBuffer /
+ *   pk_download / pk_free   mapAsync readback (src/webgpu/arena.ts:141-157)
+ */
+#ifndef PK_PALETTE_H
+#define PK_PALETTE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_ABI_VERSION 1
+
+typedef enum pk_status {
+  PK_OK = 0,
+  PK_INVALID_ARGUMENT = 1,
+  PK_ALLOCATION_FAILURE = 2,
+  PK_INTERNAL_ERROR = 3,
+  PK_DEVICE_ERROR = 4,
+  PK_DESTROYED = 5,
+  PK_RANGE_ERROR = 6,
+} pk_status;
+
+typedef enum pk_precision {
+  PK_PRECISION_F16 = 0, /* f16 activations/LUT/output, f32 MFMA accumulate */
+  PK_PRECISION_F32 = 1, /* f32 activations/LUT/output, f32 MFMA accumulate */
+} pk_precision;
+
+typedef enum pk_activation {
+  PK_ACTIVATION_NONE = 0,
+  PK_ACTIVATION_SILU = 1,
+  PK_ACTIVATION_RELU = 2,
+} pk_activation;
+
+/* pk_gemm_desc.flags */
+#define PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE 0x1u /* gemm.ts:204-356, :2154-2306 */
+
+typedef struct pk_context pk_context;
+typedef struct pk_gemm_op pk_gemm_op;
+typedef struct pk_prepared_weight pk_prepared_weight;
+
+/* ---- library / context --------------------------------------------------- */
+
+int pk_abi_version(void);
+const char *pk_last_error(void);
+const char *pk_status_name(int status);
+
+/* Create a context on HIP device `device` (it owns one default stream). */
+int pk_context_create(int device, pk_context **out);
+/* Destroys the context; ops and weights created from it must be destroyed
+   first. NULL is accepted. */
+int pk_context_destroy(pk_context *ctx);
+int pk_context_device(const pk_context *ctx, int *device);
+/* The context's default stream as a hipStream_t. */
+int pk_context_stream(const pk_context *ctx, void **stream);
+
+typedef struct pk_device_info {
+  char name[64];
+  char arch[32];           /* e.g. "gfx950" */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int64_t global_memory_bytes;
+  int32_t lds_bytes_per_block;
+  int32_t clock_khz;
+} pk_device_info;
+int pk_device_query(const pk_context *ctx, pk_device_info *info);
+
+/* ---- memory and streams --------------------------------------------------- */
+
+int pk_alloc(pk_context *ctx, uint64_t bytes, void **device_ptr);
+int pk_free(pk_context *ctx, void *device_ptr);
+/* Host<->device copies, ordered on `stream` and complete on return. */
+int pk_upload(pk_context *ctx, void *device_dst, const void *host_src,
+              uint64_t bytes, void *stream);
+int pk_download(pk_context *ctx, void *host_dst, const void *device_src,
+                uint64_t bytes, void *stream);
+int pk_copy_device(pk_context *ctx, void *device_dst, const void *device_src,
+                   uint64_t bytes, void *stream);
+int pk_stream_create(pk_context *ctx, void **stream);
+int pk_stream_destroy(pk_context *ctx, void *stream);
+int pk_stream_synchronize(pk_context *ctx, void *stream);
+int pk_event_create(pk_context *ctx, void **event);
+int pk_event_destroy(pk_context *ctx, void *event);
+int pk_event_record(pk_context *ctx, void *event, void *stream);
+int pk_event_synchronize(pk_context *ctx, void *event);
+int pk_event_elapsed_ms(pk_context *ctx, void *start, void *end, float *ms);
+
+/* ---- palette weights ------------------------------------------------------ */
+
+/* Packed weight in the reference package format (model/convert.py:2119-2203,
+   src/model/runtime-plan.ts:529-588): a logical [inner=K, columns=N] matrix
+   of `bits`-bit codes, K-major, cut into groups of 32 codes in 5 words
+   (5-bit) or 16 codes in 3 words (6-bit), code i of a group at bit i*bits,
+   LSB first. packed_bytes must equal K*N/codes_per_group*words*4. */
+typedef struct pk_weight_desc {
+  uint32_t struct_size;    /* sizeof(pk_weight_desc) */
+  const char *label;
+  int32_t palette_bits;    /* 5 or 6 */
+  uint32_t inner;          /* K */
+  uint32_t columns;        /* N */
+  const uint32_t *packed;  /* device */
+  uint64_t packed_bytes;
+} pk_weight_desc;
+
+/* One-time preparation of a packed weight for the fused GEMM: the codes are
+   re-ordered on the device into the MFMA operand order (same bits per code,
+   no dense expansion). Several GEMM ops may share one prepared weight. */
+int pk_prepared_weight_create(pk_context *ctx, const pk_weight_desc *desc,
+                              void *stream, pk_prepared_weight **out);
+int pk_prepared_weight_destroy(pk_prepared_weight *weight);
+/* Device bytes held by the prepared weight. */
+int pk_prepared_weight_bytes(const pk_prepared_weight *weight, uint64_t *bytes);
+
+/* ---- GEMM ----------------------------------------------------------------- */
+
+/* C[m, n] = epilogue(sum_k A[m, k] * LUT[g(n)][code(k, n)]) with the
+   reference epilogue order bias -> activation -> residual + scale * value
+   (gemm.ts:2006-2044). g(n) = min(n / palette_group_columns, groups - 1)
+   (palette-expander.ts:543-549). */
+typedef struct pk_gemm_desc {
+  uint32_t struct_size;          /* sizeof(pk_gemm_desc) */
+  uint32_t flags;                /* PK_GEMM_* */
+  const char *label;
+  int32_t precision;             /* pk_precision */
+  int32_t palette_bits;          /* 5 or 6 */
+  uint32_t rows;                 /* M capacity */
+  uint32_t inner;                /* K */
+  uint32_t columns;              /* N */
+  uint32_t palette_groups;       /* G */
+  uint32_t palette_group_columns;/* N / G */
+  const void *a;                 /* [rows, inner] f16|f32, row-major */
+  uint64_t a_bytes;
+  const uint32_t *packed;        /* reference-format codes (or NULL when prepared) */
+  uint64_t packed_bytes;
+  const void *palette;           /* [G, 2^bits] f16|f32 */
+  uint64_t palette_bytes;
+  void *output;                  /* [rows, columns] f16|f32, row-major */
+  uint64_t output_bytes;
+  const float *bias;             /* [columns] f32, or NULL */
+  uint64_t bias_bytes;
+  const void *residual;          /* [rows, columns] like output, or NULL */
+  uint64_t residual_bytes;
+  int32_t has_residual_scale;    /* 0: scale 1 when a residual is given */
+  float residual_scale;
+  int32_t activation;            /* pk_activation */
+  const pk_prepared_weight *prepared; /* optional shared prepared weight */
+} pk_gemm_desc;
+
+int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,
+                   pk_gemm_op **out);
+/* Launch on `stream` for the first `active_rows` rows (0 = all rows). */
+int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
+/* Releases the op's device resources. Idempotent: a second call is a no-op
+   returning PK_OK; enqueue after destroy returns PK_DESTROYED. The handle
+   itself stays valid until pk_gemm_release. */
+int pk_gemm_destroy(pk_gemm_op *op);
+/* Destroys (if needed) and frees the handle; it must not be used again. */
+int pk_gemm_release(pk_gemm_op *op);
+
+/* Tuning hooks: the planner picks a compiled tile shape at create time;
+   these list and force the choice (used by the benchmark's sweeps). */
+int pk_gemm_variant_count(int precision);
+int pk_gemm_set_variant(pk_gemm_op *op, int variant);
+
+typedef struct pk_gemm_plan_info {
+  uint32_t grid[3];
+  uint32_t block_threads;
+  uint32_t tile_rows;
+  uint32_t tile_columns;
+  uint32_t split_inner;          /* K slices reduced in-kernel (1 = none) */
+  uint32_t lds_bytes;
+  uint64_t flops;                /* 2*M*K*N for active rows */
+  uint64_t algorithmic_bytes;    /* compulsory HBM bytes per launch */
+  char kernel[64];
+} pk_gemm_plan_info;
+
+/* Plan of the launch pk_gemm_enqueue would make for `active_rows`. */
+int pk_gemm_plan(const pk_gemm_op *op, uint32_t active_rows,
+                 pk_gemm_plan_info *info);
+
+/* ---- expansion and unpack (bit-exact reference semantics) ---------------- */
+
+typedef enum pk_expand_layout {
+  PK_EXPAND_ROW_MAJOR = 0,  /* "k-by-output-row-major-f16|f32" */
+  PK_EXPAND_TILE_MAJOR = 1, /* "n256-k32-tile-major-f16", "n128-k32-tile-major-f32" */
+} pk_expand_layout;
+
+typedef struct pk_expand_desc {
+  uint32_t struct_size;          /* sizeof(pk_expand_desc) */
+  const char *label;
+  int32_t precision;             /* element type of palette and target */
+  int32_t palette_bits;
+  int32_t layout;                /* pk_expand_layout */
+  uint32_t inner;
+  uint32_t columns;
+  uint32_t palette_groups;
+  uint32_t palette_group_columns;
+  const uint32_t *packed;
+  uint64_t packed_bytes;
+  const void *palette;
+  uint64_t palette_bytes;
+  void *target;                  /* inner*columns elements */
+  uint64_t target_bytes;
+} pk_expand_desc;
+
+int pk_palette_expand(pk_context *ctx, const pk_expand_desc *desc, void *stream);
+
+/* codes[g*cpg + i] = code i of group g, one byte per code. */
+int pk_unpack_codes(pk_context *ctx, int palette_bits, const uint32_t *words,
+                    uint64_t group_count, uint8_t *codes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,417 @@
+/*
+ * pk_oracle.c - CPU restatement of parakeet.wgsl's palette-weight GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP product, never part of
+ * it. Built with -ffp-contract=off so every rounding written here is the
+ * rounding performed. See pk_oracle.h for the per-function reference
+ * citations and the checks that pin each function.
+ */
+#include "pk_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* binary16 conversion (IEEE 754 round-to-nearest-even, written from the    */
+/* format definition: 1 sign, 5 exponent (bias 15), 10 fraction bits).       */
+/* ------------------------------------------------------------------------ */
+
+uint16_t pko_f64_to_f16(double value) {
+  uint64_t bits;
+  memcpy(&bits, &value, sizeof bits);
+  const uint16_t sign = (uint16_t)((bits >> 48) & 0x8000u);
+  const uint64_t magnitude = bits & 0x7fffffffffffffffull;
+  const int biased = (int)(magnitude >> 52);
+  const uint64_t fraction = magnitude & ((1ull << 52) - 1);
+  if (biased == 0x7ff) {
+    return (uint16_t)(sign | (fraction ? 0x7e00u : 0x7c00u));
+  }
+  const int exponent = biased - 1023;
+  if (exponent > 15) return (uint16_t)(sign | 0x7c00u);
+  if (exponent >= -14) {
+    /* normal binary16: keep 10 fraction bits, round on the other 42 */
+    const uint64_t keep = fraction >> 42;
+    const uint64_t rest = fraction & ((1ull << 42) - 1);
+    const uint64_t half = 1ull << 41;
+    uint32_t h = ((uint32_t)(exponent + 15) << 10) | (uint32_t)keep;
+    if (rest > half || (rest == half && (keep & 1u))) h += 1u; /* may carry to inf */
+    return (uint16_t)(sign | h);
+  }
+  if (exponent < -25) return sign; /* below half the smallest subnormal */
+  /* subnormal binary16: integer multiple of 2^-24 */
+  const uint64_t significand = (1ull << 52) | fraction;
+  const int shift = 28 - exponent; /* 43..53 */
+  uint64_t q = significand >> shift;
+  const uint64_t rest = significand & ((1ull << shift) - 1);
+  const uint64_t half = 1ull << (shift - 1);
+  if (rest > half || (rest == half && (q & 1u))) q += 1u; /* 1024 = min normal */
+  return (uint16_t)(sign | (uint16_t)q);
+}
+
+double pko_f16_to_f64(uint16_t h) {
+  const double sign = (h & 0x8000u) ? -1.0 : 1.0;
+  const int biased = (h >> 10) & 0x1f;
+  const int fraction = h & 0x3ff;
+  if (biased == 0x1f) return fraction ? NAN : sign * INFINITY;
+  if (biased == 0) return sign * ldexp((double)fraction, -24);
+  return sign * ldexp((double)(fraction | 0x400), biased - 25);
+}
+
+void pko_f32_to_f16_array(const float *src, uint16_t *dst, uint64_t count) {
+  for (uint64_t i = 0; i < count; ++i) dst[i] = pko_f64_to_f16((double)src[i]);
+}
+
+void pko_f16_to_f32_array(const uint16_t *src, float *dst, uint64_t count) {
+  for (uint64_t i = 0; i < count; ++i) dst[i] = (float)pko_f16_to_f64(src[i]);
+}
+
+/* Round a double to the nearest binary16 value, returned as a double. */
+static inline double round_to_f16(double value) {
+  return pko_f16_to_f64(pko_f64_to_f16(value));
+}
+
+/* ------------------------------------------------------------------------ */
+/* Packed code format                                                        */
+/* ------------------------------------------------------------------------ */
+
+static int group_spec(int bits, uint32_t *codes_per_group,
+                      uint32_t *words_per_group) {
+  /* model/convert.py:2119-2127 palette_code_group_spec */
+  if (bits == 5) {
+    *codes_per_group = 32;
+    *words_per_group = 5;
+    return 0;
+  }
+  if (bits == 6) {
+    *codes_per_group = 16;
+    *words_per_group = 3;
+    return 0;
+  }
+  return 1;
+}
+
+int pko_pack_codes(int bits, const uint8_t *codes, uint64_t code_count,
+                   uint32_t *words) {
+  /* model/convert.py:2130-2156: code i of a group at bit i*bits, LSB first;
+     a code crossing a word boundary puts its high bits in the next word. */
+  uint32_t cpg = 0, wpg = 0;
+  if (group_spec(bits, &cpg, &wpg) || code_count % cpg) return 1;
+  const uint64_t groups = code_count / cpg;
+  const uint32_t limit = 1u << bits;
+  for (uint64_t g = 0; g < groups; ++g) {
+    uint32_t *w = words + g * wpg;
+    for (uint32_t i = 0; i < wpg; ++i) w[i] = 0;
+    for (uint32_t i = 0; i < cpg; ++i) {
+      const uint32_t code = codes[g * cpg + i];
+      if (code >= limit) return 1;
+      const uint32_t bit = i * (uint32_t)bits;
+      const uint32_t word = bit / 32, shift = bit % 32;
+      w[word] |= code << shift;
+      const int overflow = (int)(shift + (uint32_t)bits) - 32;
+      if (overflow > 0) w[word + 1] |= code >> ((uint32_t)bits - (uint32_t)overflow);
+    }
+  }
+  return 0;
+}
+
+int pko_unpack_codes(int bits, const uint32_t *words, uint64_t group_count,
+                     uint8_t *codes) {
+  /* src/model/palette-expander.ts:500-511 codeExpression, u32 arithmetic:
+     ((w[b/32] >> b%32) | (w[b/32+1] << (32 - b%32))) & mask */
+  uint32_t cpg = 0, wpg = 0;
+  if (group_spec(bits, &cpg, &wpg)) return 1;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (uint64_t g = 0; g < group_count; ++g) {
+    const uint32_t *w = words + g * wpg;
+    for (uint32_t i = 0; i < cpg; ++i) {
+      const uint32_t bit = i * (uint32_t)bits;
+      const uint32_t word = bit / 32, shift = bit % 32;
+      uint32_t value = w[word] >> shift;
+      if (shift + (uint32_t)bits > 32) value |= w[word + 1] << (32 - shift);
+      codes[g * cpg + i] = (uint8_t)(value & mask);
+    }
+  }
+  return 0;
+}
+
+uint32_t pko_palette_group(uint32_t column, uint32_t palette_group_columns,
+                           uint32_t palette_groups) {
+  /* src/model/palette-expander.ts:543-549 */
+  const uint32_t g = column / palette_group_columns;
+  return g < palette_groups - 1u ? g : palette_groups - 1u;
+}
+
+uint64_t pko_tile_major_index(uint64_t scalar_index, uint32_t inner,
+                              uint32_t columns, uint32_t tile_columns) {
+  /* src/model/runtime-plan.ts:454-490 (k tiles of 32, n tiles of
+     tile_columns, tile-major then k-in-tile then n-in-tile) */
+  const uint64_t k = scalar_index / columns;
+  const uint64_t n = scalar_index % columns;
+  const uint64_t n_tile = n / tile_columns;
+  const uint64_t k_tile = k / 32u;
+  const uint64_t k_tiles = inner / 32u;
+  const uint64_t k_in_tile = k % 32u;
+  const uint64_t n_in_tile = n % tile_columns;
+  return ((n_tile * k_tiles + k_tile) * 32u + k_in_tile) * tile_columns +
+         n_in_tile;
+}
+
+static int check_palette_geometry(int bits, uint32_t inner, uint32_t columns,
+                                  uint32_t group_columns, uint32_t groups) {
+  uint32_t cpg = 0, wpg = 0;
+  if (group_spec(bits, &cpg, &wpg)) return 1;
+  if (!inner || !columns || !groups || !group_columns) return 1;
+  if (columns % cpg) return 1;                         /* runtime-plan.ts:550 */
+  if ((uint64_t)group_columns * groups != columns) return 1; /* :576-585 */
+  return 0;
+}
+
+int pko_expand(int bits, int dtype, int tile_major, const uint32_t *packed,
+               uint32_t inner, uint32_t columns,
+               uint32_t palette_group_columns, uint32_t palette_groups,
+               const void *palette, void *out) {
+  /* src/model/palette-expander.ts:573-585: one group of codes at a time,
+     palette group taken from the group's first scalar, dense value
+     LUT[group * 2^bits + code] written row-major or tile-major
+     (n256-k32 for f16, n128-k32 for f32; runtime-plan.ts:26-37). */
+  if (check_palette_geometry(bits, inner, columns, palette_group_columns,
+                             palette_groups))
+    return 1;
+  if (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32) return 1;
+  const uint32_t tile_columns = dtype == PKO_DTYPE_F16 ? 256u : 128u;
+  if (tile_major && (inner % 32u || columns % tile_columns)) return 1;
+  uint32_t cpg = 0, wpg = 0;
+  group_spec(bits, &cpg, &wpg);
+  const uint64_t scalars = (uint64_t)inner * columns;
+  const uint64_t groups = scalars / cpg;
+  const uint32_t entries = 1u << bits;
+  uint8_t codes[32];
+  for (uint64_t g = 0; g < groups; ++g) {
+    pko_unpack_codes(bits, packed + g * wpg, 1, codes);
+    const uint64_t base = g * cpg;
+    const uint32_t pg = pko_palette_group((uint32_t)(base % columns),
+                                          palette_group_columns,
+                                          palette_groups);
+    for (uint32_t i = 0; i < cpg; ++i) {
+      const uint64_t scalar = base + i;
+      const uint64_t dst =
+          tile_major ? pko_tile_major_index(scalar, inner, columns, tile_columns)
+                     : scalar;
+      const uint32_t entry = pg * entries + codes[i];
+      if (dtype == PKO_DTYPE_F16)
+        ((uint16_t *)out)[dst] = ((const uint16_t *)palette)[entry];
+      else
+        ((float *)out)[dst] = ((const float *)palette)[entry];
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMM + epilogue                                                           */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gemm_job {
+  const pko_gemm_args *args;
+  int mode;
+  const void *dense;   /* expanded W: float (F32 chain) or double */
+  uint32_t row_begin, row_end;
+} gemm_job;
+
+/* Epilogue in f32 (gemm.ts:2006-2044 and :2847-2869): bias, then activation,
+   then residual + scale * value. */
+static inline float epilogue_f32(const pko_gemm_args *p, float value,
+                                 uint32_t m, uint32_t n) {
+  if (p->bias) value += p->bias[n];
+  if (p->activation == PKO_ACT_SILU) {
+    const float bounded = fminf(fmaxf(value, -20.0f), 20.0f);
+    value = value / (1.0f + expf(-bounded));
+  } else if (p->activation == PKO_ACT_RELU) {
+    value = fmaxf(value, 0.0f);
+  }
+  if (p->residual) {
+    const uint64_t idx = (uint64_t)m * p->columns + n;
+    const float r = p->dtype == PKO_DTYPE_F16
+                        ? (float)pko_f16_to_f64(((const uint16_t *)p->residual)[idx])
+                        : ((const float *)p->residual)[idx];
+    value = r + p->residual_scale * value;
+  }
+  return value;
+}
+
+static inline double epilogue_f64(const pko_gemm_args *p, double value,
+                                  uint32_t m, uint32_t n) {
+  if (p->bias) value += (double)p->bias[n];
+  if (p->activation == PKO_ACT_SILU) {
+    const double bounded = fmin(fmax(value, -20.0), 20.0);
+    value = value / (1.0 + exp(-bounded));
+  } else if (p->activation == PKO_ACT_RELU) {
+    value = fmax(value, 0.0);
+  }
+  if (p->residual) {
+    const uint64_t idx = (uint64_t)m * p->columns + n;
+    const double r = p->dtype == PKO_DTYPE_F16
+                         ? pko_f16_to_f64(((const uint16_t *)p->residual)[idx])
+                         : (double)((const float *)p->residual)[idx];
+    value = r + (double)p->residual_scale * value;
+  }
+  return value;
+}
+
+static inline double a_value(const pko_gemm_args *p, uint64_t idx) {
+  return p->dtype == PKO_DTYPE_F16
+             ? pko_f16_to_f64(((const uint16_t *)p->a)[idx])
+             : (double)((const float *)p->a)[idx];
+}
+
+/* f32 accumulator chain, increasing k, one fused multiply-add per step
+   (gemm.ts:2398-2420 acc = fma(vec4<f32>(a), b, acc)). */
+#define F32_CHAIN_BODY                                                       \
+  for (uint32_t k = 0; k < K; ++k) {                                         \
+    const float a = (float)a_value(p, (uint64_t)m * K + k);                  \
+    const float *wrow = w + (uint64_t)k * N;                                 \
+    for (uint32_t n = 0; n < N; ++n) acc[n] = fmaf(a, wrow[n], acc[n]);      \
+  }
+
+__attribute__((target("fma"))) static void f32_rows_fma(const pko_gemm_args *p,
+                                                        const float *w,
+                                                        float *acc, uint32_t m) {
+  const uint32_t K = p->inner, N = p->columns;
+  F32_CHAIN_BODY
+}
+
+static void f32_rows_generic(const pko_gemm_args *p, const float *w, float *acc,
+                             uint32_t m) {
+  const uint32_t K = p->inner, N = p->columns;
+  F32_CHAIN_BODY
+}
+
+static void *gemm_worker(void *opaque) {
+  gemm_job *job = (gemm_job *)opaque;
+  const pko_gemm_args *p = job->args;
+  const uint32_t K = p->inner, N = p->columns;
+  if (job->mode == PKO_MODE_F32_CHAIN) {
+    const float *w = (const float *)job->dense;
+    float *acc = (float *)malloc(sizeof(float) * N);
+    const int use_fma = __builtin_cpu_supports("fma");
+    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
+      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0f;
+      if (use_fma)
+        f32_rows_fma(p, w, acc, m);
+      else
+        f32_rows_generic(p, w, acc, m);
+      for (uint32_t n = 0; n < N; ++n) {
+        const float v = epilogue_f32(p, acc[n], m, n);
+        const uint64_t idx = (uint64_t)m * N + n;
+        if (p->dtype == PKO_DTYPE_F16)
+          ((uint16_t *)p->out)[idx] = pko_f64_to_f16((double)v);
+        else
+          ((float *)p->out)[idx] = v;
+      }
+    }
+    free(acc);
+  } else if (job->mode == PKO_MODE_F16_CHAIN) {
+    /* gemm.ts:1445-1453, :1476-1481: vec4<f16> accumulators, fma in
+       increasing k. The product of two binary16 values is exact in double
+       and, below binary16 overflow, so is its sum with a binary16
+       accumulator; one round_to_f16 per step is therefore a fused fma. */
+    const double *w = (const double *)job->dense;
+    double *acc = (double *)malloc(sizeof(double) * N);
+    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
+      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0;
+      for (uint32_t k = 0; k < K; ++k) {
+        const double a = a_value(p, (uint64_t)m * K + k);
+        const double *wrow = w + (uint64_t)k * N;
+        for (uint32_t n = 0; n < N; ++n) acc[n] = round_to_f16(a * wrow[n] + acc[n]);
+      }
+      for (uint32_t n = 0; n < N; ++n) {
+        const float v = epilogue_f32(p, (float)acc[n], m, n);
+        ((uint16_t *)p->out)[(uint64_t)m * N + n] = pko_f64_to_f16((double)v);
+      }
+    }
+    free(acc);
+  } else {
+    const double *w = (const double *)job->dense;
+    double *acc = (double *)malloc(sizeof(double) * N);
+    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
+      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0;
+      for (uint32_t k = 0; k < K; ++k) {
+        const double a = a_value(p, (uint64_t)m * K + k);
+        const double *wrow = w + (uint64_t)k * N;
+        for (uint32_t n = 0; n < N; ++n) acc[n] += a * wrow[n];
+      }
+      for (uint32_t n = 0; n < N; ++n)
+        ((double *)p->out)[(uint64_t)m * N + n] = epilogue_f64(p, acc[n], m, n);
+    }
+    free(acc);
+  }
+  return NULL;
+}
+
+int pko_gemm(const pko_gemm_args *p, int mode, int threads) {
+  if (!p || !p->packed || !p->palette || !p->a || !p->out) return 1;
+  if (check_palette_geometry(p->bits, p->inner, p->columns,
+                             p->palette_group_columns, p->palette_groups))
+    return 1;
+  if (p->dtype != PKO_DTYPE_F16 && p->dtype != PKO_DTYPE_F32) return 1;
+  if (mode == PKO_MODE_F16_CHAIN && p->dtype != PKO_DTYPE_F16) return 1;
+  if (mode < PKO_MODE_F32_CHAIN || mode > PKO_MODE_F64) return 1;
+  if (!p->rows) return 0;
+  if (threads < 1) threads = 1;
+  const uint64_t scalars = (uint64_t)p->inner * p->columns;
+
+  /* Expand the palette weight once (palette-expander.ts:573-585), widened to
+     the working precision of the chain. */
+  void *dense = NULL;
+  {
+    const size_t elem = p->dtype == PKO_DTYPE_F16 ? 2 : 4;
+    void *narrow = malloc(scalars * elem);
+    if (!narrow) return 1;
+    pko_expand(p->bits, p->dtype, 0, p->packed, p->inner, p->columns,
+               p->palette_group_columns, p->palette_groups, p->palette, narrow);
+    if (mode == PKO_MODE_F32_CHAIN) {
+      float *w = (float *)malloc(scalars * sizeof(float));
+      for (uint64_t i = 0; i < scalars; ++i)
+        w[i] = p->dtype == PKO_DTYPE_F16
+                   ? (float)pko_f16_to_f64(((uint16_t *)narrow)[i])
+                   : ((float *)narrow)[i];
+      dense = w;
+    } else {
+      double *w = (double *)malloc(scalars * sizeof(double));
+      for (uint64_t i = 0; i < scalars; ++i)
+        w[i] = p->dtype == PKO_DTYPE_F16
+                   ? pko_f16_to_f64(((uint16_t *)narrow)[i])
+                   : (double)((float *)narrow)[i];
+      dense = w;
+    }
+    free(narrow);
+  }
+
+  if ((uint32_t)threads > p->rows) threads = (int)p->rows;
+  pthread_t *tids = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
+  char *running = (char *)calloc((size_t)threads, 1);
+  gemm_job *jobs = (gemm_job *)calloc((size_t)threads, sizeof(gemm_job));
+  const uint32_t per = (p->rows + (uint32_t)threads - 1) / (uint32_t)threads;
+  for (int t = 0; t < threads; ++t) {
+    jobs[t].args = p;
+    jobs[t].mode = mode;
+    jobs[t].dense = dense;
+    jobs[t].row_begin = (uint32_t)t * per;
+    jobs[t].row_end = jobs[t].row_begin + per > p->rows ? p->rows
+                                                        : jobs[t].row_begin + per;
+    if (jobs[t].row_begin >= jobs[t].row_end) continue;
+    if (threads > 1 && pthread_create(&tids[t], NULL, gemm_worker, &jobs[t]) == 0)
+      running[t] = 1;
+    else
+      gemm_worker(&jobs[t]); /* single thread, or thread creation failed */
+  }
+  for (int t = 0; t < threads; ++t)
+    if (running[t]) pthread_join(tids[t], NULL);
+  free(running);
+  free(tids);
+  free(jobs);
+  free(dense);
+  return 0;
+}

@@ -1,0 +1,105 @@
+/*
+ * pk_oracle.h - CPU restatement of parakeet.wgsl's palette-weight GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP product
+ * is compared against; it is never linked into, loaded by or called from the
+ * product library (parakeet.wgsl_amd/csrc). Only tests/, the smoke check and
+ * the CPU-baseline leg of bench.py may load it.
+ *
+ * Every function restates one piece of the reference and cites it. The
+ * reference runs only as WGSL inside a WebGPU browser, so it cannot execute in
+ * this environment; each function's pin is listed beside it:
+ *
+ *   pko_pack_codes        model/convert.py:2130-2156 (pack_palette_codes_lsb)
+ *                         pinned: model/tests/test_convert.py:447-479 KATs,
+ *                         pack/unpack round trip, brute-force bit positions.
+ *   pko_unpack_codes      src/model/palette-expander.ts:500-511 (codeExpression)
+ *                         and model/tests/test_convert.py:90-115
+ *                         pinned: the same KATs, exhaustive 5/6-bit patterns.
+ *   pko_palette_group     src/model/palette-expander.ts:543-549
+ *                         pinned: closed form, test_convert.py:481-511 fixture.
+ *   pko_tile_major_index  src/model/runtime-plan.ts:454-490
+ *                         pinned: bijection + tile contiguity invariants of
+ *                         test/model/palette-expander.test.ts:147-247.
+ *   pko_expand            src/model/palette-expander.ts:478-587
+ *                         pinned: one-hot LUTs recover the codes exactly.
+ *   pko_gemm (F32_CHAIN)  src/webgpu/kernels/gemm.ts:2356-2599, epilogue
+ *                         :2847-2869 - pinned: exact integer-valued inputs vs
+ *                         the textbook product, constant-LUT closed form,
+ *                         brute force on tiny shapes.
+ *   pko_gemm (F16_CHAIN)  src/webgpu/kernels/gemm.ts:1362-1716 (f16
+ *                         accumulator, increasing k), epilogue :2006-2044
+ *                         pinned: exact small-integer cases, the f16 rounding
+ *                         function against every f16 value and its midpoints.
+ *   pko_gemm (F64)        reference-independent truth of the same expression.
+ *
+ * Status codes: 0 ok, 1 invalid argument.
+ */
+#ifndef PK_ORACLE_H
+#define PK_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  PKO_ACT_NONE = 0,
+  PKO_ACT_SILU = 1,
+  PKO_ACT_RELU = 2,
+};
+
+enum {
+  PKO_MODE_F32_CHAIN = 0, /* f32 accumulator, fmaf in increasing k */
+  PKO_MODE_F16_CHAIN = 1, /* f16 accumulator, one rounding per fused fma */
+  PKO_MODE_F64 = 2,       /* double accumulation, double epilogue */
+};
+
+enum {
+  PKO_DTYPE_F16 = 0,
+  PKO_DTYPE_F32 = 1,
+};
+
+typedef struct pko_gemm_args {
+  uint32_t rows;              /* M */
+  uint32_t inner;             /* K */
+  uint32_t columns;           /* N */
+  int32_t bits;               /* 5 or 6 */
+  uint32_t palette_groups;    /* G */
+  uint32_t palette_group_columns;
+  int32_t dtype;              /* PKO_DTYPE_F16: A, LUT, residual, output f16 */
+  const uint32_t *packed;     /* reference layout words */
+  const void *palette;        /* [G, 2^bits] */
+  const void *a;              /* [M, K] */
+  const float *bias;          /* [N] or NULL */
+  const void *residual;       /* [M, N] or NULL */
+  float residual_scale;
+  int32_t activation;
+  void *out;                  /* [M, N]: f16 / f32 per dtype, double for F64 */
+} pko_gemm_args;
+
+uint16_t pko_f64_to_f16(double value);
+double pko_f16_to_f64(uint16_t bits);
+void pko_f32_to_f16_array(const float *src, uint16_t *dst, uint64_t count);
+void pko_f16_to_f32_array(const uint16_t *src, float *dst, uint64_t count);
+
+int pko_pack_codes(int bits, const uint8_t *codes, uint64_t code_count,
+                   uint32_t *words);
+int pko_unpack_codes(int bits, const uint32_t *words, uint64_t group_count,
+                     uint8_t *codes);
+uint32_t pko_palette_group(uint32_t column, uint32_t palette_group_columns,
+                           uint32_t palette_groups);
+uint64_t pko_tile_major_index(uint64_t scalar_index, uint32_t inner,
+                              uint32_t columns, uint32_t tile_columns);
+int pko_expand(int bits, int dtype, int tile_major, const uint32_t *packed,
+               uint32_t inner, uint32_t columns,
+               uint32_t palette_group_columns, uint32_t palette_groups,
+               const void *palette, void *out);
+int pko_gemm(const pko_gemm_args *args, int mode, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,198 @@
+"""ctypes wrapper around liboracle.so, the CPU restatement of parakeet.wgsl's
+palette-weight GEMM path.
+
+TEST INFRASTRUCTURE ONLY. Imported by tests/, by the smoke check in
+__graft_entry__.py and by the CPU-baseline leg of bench.py, as the checker.
+The product library never loads it.
+
+Reference functions restated (see pk_oracle.h for the pins):
+  pack_codes      model/convert.py:2130-2156
+  unpack_codes    src/model/palette-expander.ts:500-511, model/tests/test_convert.py:90-115
+  palette_group   src/model/palette-expander.ts:543-549
+  tile_major_index src/model/runtime-plan.ts:454-490
+  expand          src/model/palette-expander.ts:478-587
+  gemm            src/webgpu/kernels/gemm.ts:1362-1716, :2006-2044 (f16),
+                  :2356-2599, :2847-2869 (f32)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+ACT = {"none": 0, "silu": 1, "relu": 2}
+MODE = {"f32-chain": 0, "f16-chain": 1, "f64": 2}
+DTYPE = {"f16": 0, "f32": 1}
+
+
+def build() -> None:
+    """Compile liboracle.so from pk_oracle.c with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "liboracle.so"], check=True)
+
+
+class _GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_uint32),
+        ("inner", ctypes.c_uint32),
+        ("columns", ctypes.c_uint32),
+        ("bits", ctypes.c_int32),
+        ("palette_groups", ctypes.c_uint32),
+        ("palette_group_columns", ctypes.c_uint32),
+        ("dtype", ctypes.c_int32),
+        ("packed", ctypes.c_void_p),
+        ("palette", ctypes.c_void_p),
+        ("a", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("residual_scale", ctypes.c_float),
+        ("activation", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _lib.pko_f64_to_f16.restype = ctypes.c_uint16
+        _lib.pko_f64_to_f16.argtypes = [ctypes.c_double]
+        _lib.pko_f16_to_f64.restype = ctypes.c_double
+        _lib.pko_f16_to_f64.argtypes = [ctypes.c_uint16]
+        _lib.pko_pack_codes.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+        _lib.pko_unpack_codes.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+        _lib.pko_palette_group.restype = ctypes.c_uint32
+        _lib.pko_palette_group.argtypes = [ctypes.c_uint32] * 3
+        _lib.pko_tile_major_index.restype = ctypes.c_uint64
+        _lib.pko_tile_major_index.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        _lib.pko_expand.argtypes = [
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+            ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+            ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        _lib.pko_gemm.argtypes = [ctypes.POINTER(_GemmArgs), ctypes.c_int, ctypes.c_int]
+    return _lib
+
+
+def _ptr(array: np.ndarray | None) -> int | None:
+    if array is None:
+        return None
+    assert array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data
+
+
+def codes_per_group(bits: int) -> int:
+    return {5: 32, 6: 16}[bits]
+
+
+def words_per_group(bits: int) -> int:
+    return {5: 5, 6: 3}[bits]
+
+
+def f64_to_f16_bits(value: float) -> int:
+    return int(lib().pko_f64_to_f16(float(value)))
+
+
+def f16_bits_to_f64(bits: int) -> float:
+    return float(lib().pko_f16_to_f64(int(bits)))
+
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    cpg = codes_per_group(bits)
+    if codes.size % cpg:
+        raise ValueError("code count is not group aligned")
+    words = np.zeros((codes.size // cpg, words_per_group(bits)), dtype="<u4")
+    if lib().pko_pack_codes(bits, _ptr(codes), codes.size, _ptr(words)):
+        raise ValueError("pack_codes rejected its input")
+    return words
+
+
+def unpack_codes(words: np.ndarray, bits: int) -> np.ndarray:
+    words = np.ascontiguousarray(words, dtype="<u4").reshape(-1)
+    wpg = words_per_group(bits)
+    groups = words.size // wpg
+    codes = np.empty(groups * codes_per_group(bits), dtype=np.uint8)
+    if lib().pko_unpack_codes(bits, _ptr(words), groups, _ptr(codes)):
+        raise ValueError("unpack_codes rejected its input")
+    return codes
+
+
+def palette_group(column: int, group_columns: int, groups: int) -> int:
+    return int(lib().pko_palette_group(column, group_columns, groups))
+
+
+def tile_major_index(scalar: int, inner: int, columns: int, tile_columns: int) -> int:
+    return int(lib().pko_tile_major_index(scalar, inner, columns, tile_columns))
+
+
+def expand(words, bits, inner, columns, palette, *, tile_major=False) -> np.ndarray:
+    """Dense [K, N] weights (or the tile-major scratch) from packed codes."""
+    palette = np.ascontiguousarray(palette)
+    dtype = "f16" if palette.dtype == np.float16 else "f32"
+    groups = palette.shape[0]
+    out = np.empty(inner * columns, dtype=palette.dtype)
+    words = np.ascontiguousarray(words, dtype="<u4")
+    rc = lib().pko_expand(bits, DTYPE[dtype], int(tile_major), _ptr(words), inner, columns,
+                          columns // groups, groups, _ptr(palette), _ptr(out))
+    if rc:
+        raise ValueError("expand rejected its geometry")
+    return out if tile_major else out.reshape(inner, columns)
+
+
+def gemm(a, words, bits, palette, columns, *, bias=None, residual=None,
+         residual_scale=None, activation="none", mode=None, threads=1) -> np.ndarray:
+    """Palette GEMM with the reference epilogue.
+
+    a: [M, K] float16 or float32; palette: [G, 2^bits] of the same dtype.
+    mode: "f16-chain" (reference fp16 semantics), "f32-chain" (reference fp32
+    semantics) or "f64" (double truth). Returns float16/float32 for the chain
+    modes and float64 for "f64".
+    """
+    a = np.ascontiguousarray(a)
+    palette = np.ascontiguousarray(palette)
+    dtype = "f16" if a.dtype == np.float16 else "f32"
+    if palette.dtype != a.dtype:
+        raise ValueError("palette dtype must match the activation dtype")
+    if mode is None:
+        mode = "f16-chain" if dtype == "f16" else "f32-chain"
+    rows, inner = a.shape
+    groups = palette.shape[0]
+    if mode == "f64":
+        out = np.empty((rows, columns), dtype=np.float64)
+    else:
+        out = np.empty((rows, columns), dtype=a.dtype)
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+    if residual is not None:
+        residual = np.ascontiguousarray(residual, dtype=a.dtype)
+        if residual_scale is None:
+            residual_scale = 1.0
+    words = np.ascontiguousarray(words, dtype="<u4")
+    args = _GemmArgs(
+        rows, inner, columns, bits, groups, columns // groups, DTYPE[dtype],
+        _ptr(words), _ptr(palette), _ptr(a), _ptr(bias), _ptr(residual),
+        float(residual_scale if residual_scale is not None else 0.0), ACT[activation], _ptr(out),
+    )
+    if lib().pko_gemm(ctypes.byref(args), MODE[mode], int(threads)):
+        raise ValueError("gemm rejected its arguments")
+    return out
+
+
+def relative_errors(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
+    """(norm-wise, max-wise) relative error of got against want, in double."""
+    g = np.asarray(got, dtype=np.float64)
+    w = np.asarray(want, dtype=np.float64)
+    diff = g - w
+    norm = float(np.linalg.norm(diff) / max(np.linalg.norm(w), 1e-300))
+    peak = float(np.max(np.abs(diff)) / max(np.max(np.abs(w)), 1e-300)) if w.size else 0.0
+    return norm, peak

@@ -1,0 +1,101 @@
+"""Build the in-tree native libraries of the palette GEMM package.
+
+    python parakeet.wgsl_amd/build.py            # everything
+    python parakeet.wgsl_amd/build.py --lib      # libpk_palette.so only
+
+Outputs (git-ignored, shipped with the tree):
+  lib/libpk_palette.so   HIP kernels for gfx950 + the C ABI (include/pk_palette.h)
+  lib/pk_napi.node       Node N-API addon over the C ABI
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+ADDON = os.path.join(PKG, "addon")
+LIB = os.path.join(PKG, "lib")
+OBJ = os.path.join(PKG, "_build")
+INCLUDE = os.path.join(ROOT, "include")
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Packed-f32 VALU ops are disabled for all device code (v_pk_*_f32).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", INCLUDE, "-I", CSRC,
+]
+SOURCES = ["pk_abi.cpp", "pk_codes.hip", "pk_gemm_f16.hip", "pk_gemm_f32.hip"]
+NODE_INCLUDE = "/usr/include/node"
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    noise = "is not a recognized feature for this target"
+    out = "\n".join(line for line in proc.stdout.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+
+
+def _compile(source: str) -> str:
+    src = os.path.join(CSRC, source)
+    obj = os.path.join(OBJ, os.path.splitext(source)[0] + ".o")
+    lang = ["-x", "hip"] if source.endswith(".cpp") else []
+    _run([HIPCC, *HIP_FLAGS, *lang, "-c", src, "-o", obj])
+    return obj
+
+
+def build_lib(jobs: int | None = None) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(_compile, SOURCES))
+    target = os.path.join(LIB, "libpk_palette.so")
+    tmp = target + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objects,
+          "-Wl,-soname,libpk_palette.so"])
+    os.replace(tmp, target)
+    return target
+
+
+def build_addon() -> str | None:
+    """Compile the N-API addon with gcc against the system Node headers."""
+    source = os.path.join(ADDON, "pk_napi.c")
+    if not os.path.exists(source):
+        return None
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        print("build: Node headers not found; skipping the N-API addon", file=sys.stderr)
+        return None
+    target = os.path.join(LIB, "pk_napi.node")
+    tmp = target + ".tmp"
+    cc = shutil.which("gcc") or "cc"
+    _run([cc, "-O2", "-std=gnu11", "-fPIC", "-shared", "-Wall", "-Wextra", "-DNAPI_VERSION=8",
+          "-I", NODE_INCLUDE, "-I", INCLUDE, source, "-o", tmp,
+          "-L", LIB, "-lpk_palette", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, target)
+    return target
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--lib", action="store_true", help="build only libpk_palette.so")
+    args = parser.parse_args()
+    print(build_lib())
+    if not args.lib:
+        addon = build_addon()
+        if addon:
+            print(addon)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,681 @@
+// pk_abi.cpp - C ABI of the palette GEMM library: contexts, memory, streams,
+// the reference's descriptor contract checks and launch planning.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "pk_internal.h"
+#include "pk_palette.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+  char buffer[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buffer, sizeof buffer, fmt, args);
+  va_end(args);
+  g_error = buffer;
+  return status;
+}
+
+int ok() { return PK_OK; }
+
+#define PK_HIP(call, what)                                                                  \
+  do {                                                                                      \
+    const hipError_t pk_e_ = (call);                                                        \
+    if (pk_e_ != hipSuccess)                                                                \
+      return fail(PK_DEVICE_ERROR, "%s failed: %s", (what), hipGetErrorString(pk_e_));      \
+  } while (0)
+
+const char* safe_label(const char* label) { return label ? label : "palette-gemm"; }
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// The 14 fixed production signatures (src/webgpu/kernels/gemm.ts:204-356;
+// the FP32 registry :2154-2306 has the same signatures). residual_scale < 0
+// means "no residual".
+struct Signature {
+  const char* label;
+  uint32_t rows, inner, columns;
+  int activation;
+  bool bias;
+  float residual_scale;
+};
+constexpr Signature kProductionSignatures[] = {
+    {"encoder-layer-ff-expand", 7520, 1024, 4096, PK_ACTIVATION_SILU, false, -1.0f},
+    {"encoder-layer-ff-contract", 7520, 4096, 1024, PK_ACTIVATION_NONE, false, 0.5f},
+    {"encoder-layer-attention-qkv", 7520, 1024, 3072, PK_ACTIVATION_NONE, false, -1.0f},
+    {"encoder-layer-residual-1024", 7520, 1024, 1024, PK_ACTIVATION_NONE, false, 1.0f},
+    {"encoder-layer-convolution-expand", 7520, 1024, 2048, PK_ACTIVATION_NONE, false, -1.0f},
+    {"encoder-projector", 7520, 1024, 640, PK_ACTIVATION_NONE, true, -1.0f},
+    {"subsampling-pointwise3", 12032, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-pointwise3-b2", 24064, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-pointwise3-b3", 36096, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-pointwise6", 3008, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-pointwise6-b2", 6016, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-pointwise6-b3", 9024, 256, 256, PK_ACTIVATION_RELU, true, -1.0f},
+    {"subsampling-flatten-project", 188, 4096, 1024, PK_ACTIVATION_NONE, true, -1.0f},
+    {"subsampling-flatten-project-b2", 376, 4096, 1024, PK_ACTIVATION_NONE, true, -1.0f},
+    {"subsampling-flatten-project-b3", 564, 4096, 1024, PK_ACTIVATION_NONE, true, -1.0f},
+};
+
+const char* activation_name(int a) {
+  return a == PK_ACTIVATION_SILU ? "silu" : a == PK_ACTIVATION_RELU ? "relu" : "none";
+}
+
+}  // namespace
+
+struct pk_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+};
+
+struct pk_prepared_weight {
+  pk_context* ctx = nullptr;
+  std::string label;
+  int bits = 5;
+  uint32_t inner = 0, columns = 0;
+  uint32_t* codes = nullptr;  // operand-order codes (device)
+  uint64_t bytes = 0;
+  std::atomic<int> refs{1};
+  bool owner_released = false;
+};
+
+struct pk_gemm_op {
+  pk_context* ctx = nullptr;
+  std::string label;
+  int precision = PK_PRECISION_F16;
+  int bits = 5;
+  uint32_t rows = 0;
+  pk::GemmArgs args{};
+  pk_prepared_weight* weight = nullptr;
+  int variant = 0;
+  bool destroyed = false;
+};
+
+namespace {
+
+void weight_unref(pk_prepared_weight* w) {
+  if (!w) return;
+  if (w->refs.fetch_sub(1) == 1) {
+    if (w->codes) {
+      (void)hipSetDevice(w->ctx->device);
+      (void)hipFree(w->codes);
+    }
+    delete w;
+  }
+}
+
+hipStream_t stream_or_default(pk_context* ctx, void* stream) {
+  return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+int check_ctx(const pk_context* ctx) {
+  if (!ctx) return fail(PK_INVALID_ARGUMENT, "context is null");
+  return PK_OK;
+}
+
+int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, uint32_t columns,
+                const uint32_t* packed, hipStream_t stream, pk_prepared_weight** out) {
+  auto* w = new pk_prepared_weight();
+  w->ctx = ctx;
+  w->label = safe_label(label);
+  w->bits = bits;
+  w->inner = inner;
+  w->columns = columns;
+  w->bytes = pk::operand_order_words(bits, inner, columns) * 4u;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->codes), w->bytes);
+  if (e != hipSuccess) {
+    delete w;
+    return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
+                safe_label(label), (unsigned long long)w->bytes, hipGetErrorString(e));
+  }
+  e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    (void)hipFree(w->codes);
+    delete w;
+    return fail(PK_DEVICE_ERROR, "%s: palette code preparation failed: %s", safe_label(label),
+                hipGetErrorString(e));
+  }
+  *out = w;
+  return PK_OK;
+}
+
+// Packed-code contract of requireGemmShape (gemm.ts:997-1010) and
+// validatePalettePair (runtime-plan.ts:529-588).
+int check_packed(const char* label, int bits, uint32_t inner, uint32_t columns, uint64_t packed_bytes) {
+  const uint64_t scalars = (uint64_t)inner * columns;
+  const uint32_t cpg = pk::codes_per_group(bits);
+  if (scalars % cpg != 0 || columns % cpg != 0)
+    return fail(PK_INVALID_ARGUMENT, "%s palette codes are not group aligned", label);
+  const uint64_t expected = scalars / cpg * pk::words_per_group(bits) * 4u;
+  if (packed_bytes != expected)
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid packed palette indices", label);
+  return PK_OK;
+}
+
+// Tile planner: pick the compiled tile shape whose grid best fills the 256
+// compute units, weighting smaller wavefront tiles by their extra decode and
+// LDS traffic per MFMA.
+int plan_variant(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
+  const bool f16 = precision == PK_PRECISION_F16;
+  const int count = f16 ? pk::f16_variant_count() : pk::f32_variant_count();
+  const uint32_t n_pad = pk::padded_columns(columns);
+  int best = 0;
+  double best_cost = 1e300;
+  for (int i = 0; i < count; ++i) {
+    const pk::TileShape s = f16 ? pk::f16_variant(i) : pk::f32_variant(i);
+    const double tiles = (double)((rows + s.tile_rows() - 1) / s.tile_rows()) *
+                         (double)((n_pad + s.tile_columns() - 1) / s.tile_columns());
+    // Workgroups resident per CU: one for the large tiles, up to four when a
+    // tile leaves room (registers and LDS), as measured by occupancy.
+    const int waves = s.waves_m * s.waves_n;
+    const int per_wave_acc = s.m_blocks * s.n_blocks * 16;
+    int resident = per_wave_acc >= 192 ? 1 : per_wave_acc >= 96 ? 2 : 4;
+    if (waves * resident > 16) resident = 16 / waves;
+    if (resident < 1) resident = 1;
+    const double rounds = std::ceil(tiles / ((double)cus * resident));
+    const double work = (double)s.tile_rows() * s.tile_columns() * resident;
+    const double overhead = f16 ? (1.0 + 1.0 / s.m_blocks + 0.5 / (s.n_blocks * s.waves_n / s.waves_m))
+                                : (1.0 + 0.25 / s.m_blocks);
+    const double cost = rounds * work * overhead / resident;
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = i;
+    }
+  }
+  (void)inner;
+  return best;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_abi_version(void) { return PK_ABI_VERSION; }
+
+const char* pk_last_error(void) { return g_error.c_str(); }
+
+const char* pk_status_name(int status) {
+  switch (status) {
+    case PK_OK: return "PK_OK";
+    case PK_INVALID_ARGUMENT: return "PK_INVALID_ARGUMENT";
+    case PK_ALLOCATION_FAILURE: return "PK_ALLOCATION_FAILURE";
+    case PK_INTERNAL_ERROR: return "PK_INTERNAL_ERROR";
+    case PK_DEVICE_ERROR: return "PK_DEVICE_ERROR";
+    case PK_DESTROYED: return "PK_DESTROYED";
+    case PK_RANGE_ERROR: return "PK_RANGE_ERROR";
+    default: return "PK_UNKNOWN";
+  }
+}
+
+int pk_context_create(int device, pk_context** out) {
+  if (!out) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  int count = 0;
+  PK_HIP(hipGetDeviceCount(&count), "hipGetDeviceCount");
+  if (device < 0 || device >= count)
+    return fail(PK_INVALID_ARGUMENT, "HIP device %d does not exist (%d visible)", device, count);
+  PK_HIP(hipSetDevice(device), "hipSetDevice");
+  auto* ctx = new pk_context();
+  ctx->device = device;
+  const hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(PK_DEVICE_ERROR, "hipStreamCreate failed: %s", hipGetErrorString(e));
+  }
+  *out = ctx;
+  return ok();
+}
+
+int pk_context_destroy(pk_context* ctx) {
+  if (!ctx) return ok();
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return ok();
+}
+
+int pk_context_device(const pk_context* ctx, int* device) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!device) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *device = ctx->device;
+  return ok();
+}
+
+int pk_context_stream(const pk_context* ctx, void** stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!stream) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *stream = ctx->stream;
+  return ok();
+}
+
+int pk_device_query(const pk_context* ctx, pk_device_info* info) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!info) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  hipDeviceProp_t prop;
+  PK_HIP(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
+  std::memset(info, 0, sizeof *info);
+  std::snprintf(info->name, sizeof info->name, "%s", prop.name);
+  std::snprintf(info->arch, sizeof info->arch, "%s", prop.gcnArchName);
+  info->compute_units = prop.multiProcessorCount;
+  info->wavefront_size = prop.warpSize;
+  info->global_memory_bytes = (int64_t)prop.totalGlobalMem;
+  info->lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
+  info->clock_khz = prop.clockRate;
+  return ok();
+}
+
+int pk_alloc(pk_context* ctx, uint64_t bytes, void** device_ptr) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!device_ptr) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *device_ptr = nullptr;
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  const hipError_t e = hipMalloc(device_ptr, bytes ? bytes : 1);
+  if (e != hipSuccess)
+    return fail(PK_ALLOCATION_FAILURE, "cannot allocate %llu device bytes: %s",
+                (unsigned long long)bytes, hipGetErrorString(e));
+  return ok();
+}
+
+int pk_free(pk_context* ctx, void* device_ptr) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!device_ptr) return ok();
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipFree(device_ptr), "hipFree");
+  return ok();
+}
+
+int pk_upload(pk_context* ctx, void* device_dst, const void* host_src, uint64_t bytes, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!bytes) return ok();
+  if (!device_dst || !host_src) return fail(PK_INVALID_ARGUMENT, "upload pointer is null");
+  hipStream_t st = stream_or_default(ctx, stream);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, st), "hipMemcpyAsync(upload)");
+  PK_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  return ok();
+}
+
+int pk_download(pk_context* ctx, void* host_dst, const void* device_src, uint64_t bytes, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!bytes) return ok();
+  if (!device_src || !host_dst) return fail(PK_INVALID_ARGUMENT, "download pointer is null");
+  hipStream_t st = stream_or_default(ctx, stream);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, st), "hipMemcpyAsync(download)");
+  PK_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  return ok();
+}
+
+int pk_copy_device(pk_context* ctx, void* device_dst, const void* device_src, uint64_t bytes, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!bytes) return ok();
+  if (!device_src || !device_dst) return fail(PK_INVALID_ARGUMENT, "copy pointer is null");
+  hipStream_t st = stream_or_default(ctx, stream);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipMemcpyAsync(device_dst, device_src, bytes, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync(copy)");
+  return ok();
+}
+
+int pk_stream_create(pk_context* ctx, void** stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!stream) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  hipStream_t st = nullptr;
+  PK_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = st;
+  return ok();
+}
+
+int pk_stream_destroy(pk_context* ctx, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!stream || stream == ctx->stream) return ok();
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  return ok();
+}
+
+int pk_stream_synchronize(pk_context* ctx, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipStreamSynchronize(stream_or_default(ctx, stream)), "hipStreamSynchronize");
+  return ok();
+}
+
+int pk_event_create(pk_context* ctx, void** event) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!event) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  hipEvent_t e = nullptr;
+  PK_HIP(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return ok();
+}
+
+int pk_event_destroy(pk_context* ctx, void* event) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!event) return ok();
+  PK_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+  return ok();
+}
+
+int pk_event_record(pk_context* ctx, void* event, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!event) return fail(PK_INVALID_ARGUMENT, "event is null");
+  PK_HIP(hipEventRecord(static_cast<hipEvent_t>(event), stream_or_default(ctx, stream)), "hipEventRecord");
+  return ok();
+}
+
+int pk_event_synchronize(pk_context* ctx, void* event) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!event) return fail(PK_INVALID_ARGUMENT, "event is null");
+  PK_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+  return ok();
+}
+
+int pk_event_elapsed_ms(pk_context* ctx, void* start, void* end, float* ms) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!start || !end || !ms) return fail(PK_INVALID_ARGUMENT, "event pointer is null");
+  PK_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)),
+         "hipEventElapsedTime");
+  return ok();
+}
+
+int pk_prepared_weight_create(pk_context* ctx, const pk_weight_desc* d, void* stream,
+                              pk_prepared_weight** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!d || !out) return fail(PK_INVALID_ARGUMENT, "weight descriptor or output is null");
+  *out = nullptr;
+  if (d->struct_size != sizeof(pk_weight_desc))
+    return fail(PK_INVALID_ARGUMENT, "pk_weight_desc.struct_size mismatch");
+  const char* label = safe_label(d->label);
+  if (d->palette_bits != 5 && d->palette_bits != 6)
+    return fail(PK_INVALID_ARGUMENT, "%s is not a palette-compressed weight", label);
+  if (d->inner == 0 || d->columns == 0 || d->inner % 32u != 0)
+    return fail(PK_RANGE_ERROR, "Unsupported GEMM shape for %s", label);
+  if (int s = check_packed(label, d->palette_bits, d->inner, d->columns, d->packed_bytes)) return s;
+  if (!d->packed || !aligned(d->packed, 4))
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid packed palette indices", label);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  return make_weight(ctx, label, d->palette_bits, d->inner, d->columns, d->packed,
+                     stream_or_default(ctx, stream), out);
+}
+
+int pk_prepared_weight_destroy(pk_prepared_weight* weight) {
+  if (!weight) return ok();
+  if (weight->owner_released) return ok();
+  weight->owner_released = true;
+  weight_unref(weight);
+  return ok();
+}
+
+int pk_prepared_weight_bytes(const pk_prepared_weight* weight, uint64_t* bytes) {
+  if (!weight || !bytes) return fail(PK_INVALID_ARGUMENT, "argument is null");
+  *bytes = weight->bytes;
+  return ok();
+}
+
+int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm_op** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!d || !out) return fail(PK_INVALID_ARGUMENT, "GEMM descriptor or output is null");
+  *out = nullptr;
+  if (d->struct_size != sizeof(pk_gemm_desc))
+    return fail(PK_INVALID_ARGUMENT, "pk_gemm_desc.struct_size mismatch");
+  const char* label = safe_label(d->label);
+  const bool f16 = d->precision == PK_PRECISION_F16;
+  if (!f16 && d->precision != PK_PRECISION_F32)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
+  const uint32_t elem = f16 ? 2u : 4u;
+  // requireGemmShape (gemm.ts:971-983; FP32 twin N%4)
+  if (d->rows == 0 || d->inner == 0 || d->inner % 32u != 0 || d->columns == 0 ||
+      d->columns % (f16 ? 8u : 4u) != 0)
+    return fail(PK_RANGE_ERROR, "Unsupported GEMM shape for %s", label);
+  if (d->palette_bits != 5 && d->palette_bits != 6)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported weight format", label);
+  const int bits = d->palette_bits;
+  // requireProductionSpecialization (gemm.ts:1031-1067)
+  if (!d->residual && d->has_residual_scale)
+    return fail(PK_INVALID_ARGUMENT, "%s supplies a residual scale without a residual", label);
+  if (d->activation < PK_ACTIVATION_NONE || d->activation > PK_ACTIVATION_RELU)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported activation %d", label, d->activation);
+  const float residual_scale = d->residual ? (d->has_residual_scale ? d->residual_scale : 1.0f) : -1.0f;
+  if (d->flags & PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE) {
+    bool found = false;
+    for (const Signature& s : kProductionSignatures)
+      if (s.rows == d->rows && s.inner == d->inner && s.columns == d->columns &&
+          s.activation == d->activation && s.bias == (d->bias != nullptr) &&
+          s.residual_scale == residual_scale)
+        found = true;
+    if (!found) {
+      char scale[32];
+      if (d->residual)
+        std::snprintf(scale, sizeof scale, "%g", residual_scale);
+      else
+        std::snprintf(scale, sizeof scale, "none");
+      return fail(PK_INVALID_ARGUMENT,
+                  "%s is not a fixed production GEMM signature: M=%u, K=%u, N=%u, "
+                  "activation=%s, bias=%s, residualScale=%s",
+                  label, d->rows, d->inner, d->columns, activation_name(d->activation),
+                  d->bias ? "true" : "false", scale);
+    }
+  }
+  // f16SubgroupGemmWgsl (gemm.ts:1372-1378)
+  if (d->bias && d->residual)
+    return fail(PK_INVALID_ARGUMENT, "%s cannot fuse bias and residual together", label);
+  // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
+  const uint32_t entries = 1u << bits;
+  const uint32_t cpg = pk::codes_per_group(bits);
+  if (d->palette_groups == 0 || d->palette_group_columns == 0 ||
+      (uint64_t)d->palette_group_columns * d->palette_groups != d->columns ||
+      d->palette_group_columns % cpg != 0 || !d->palette ||
+      d->palette_bytes != (uint64_t)d->palette_groups * entries * elem || !aligned(d->palette, elem))
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid transient palette weights", label);
+  if (d->prepared) {
+    const pk_prepared_weight* w = d->prepared;
+    if (w->owner_released || w->bits != bits || w->inner != d->inner || w->columns != d->columns ||
+        w->ctx != ctx)
+      return fail(PK_INVALID_ARGUMENT, "%s has a mismatched prepared palette weight", label);
+  } else {
+    if (int s = check_packed(label, bits, d->inner, d->columns, d->packed_bytes)) return s;
+    if (!d->packed || !aligned(d->packed, 4))
+      return fail(PK_INVALID_ARGUMENT, "%s has invalid packed palette indices", label);
+  }
+  // Bindings: sizes (gemm.ts:1302-1333 minBindingSize) and vector alignment.
+  const uint64_t a_need = (uint64_t)d->rows * d->inner * elem;
+  const uint64_t c_need = (uint64_t)d->rows * d->columns * elem;
+  if (!d->a || d->a_bytes < a_need || !aligned(d->a, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s input binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)a_need);
+  if (!d->output || d->output_bytes < c_need || !aligned(d->output, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s output binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)c_need);
+  if (d->bias && (d->bias_bytes < (uint64_t)d->columns * 4u || !aligned(d->bias, 16)))
+    return fail(PK_INVALID_ARGUMENT, "%s bias binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)d->columns * 4u);
+  if (d->residual && (d->residual_bytes < c_need || !aligned(d->residual, 16)))
+    return fail(PK_INVALID_ARGUMENT, "%s residual binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)c_need);
+
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  auto* op = new pk_gemm_op();
+  op->ctx = ctx;
+  op->label = label;
+  op->precision = d->precision;
+  op->bits = bits;
+  op->rows = d->rows;
+  if (d->prepared) {
+    op->weight = const_cast<pk_prepared_weight*>(d->prepared);
+    op->weight->refs.fetch_add(1);
+  } else {
+    pk_prepared_weight* w = nullptr;
+    if (int s = make_weight(ctx, label, bits, d->inner, d->columns, d->packed,
+                            stream_or_default(ctx, stream), &w)) {
+      delete op;
+      return s;
+    }
+    w->owner_released = true;  // owned by the op alone
+    op->weight = w;
+  }
+  pk::GemmArgs& a = op->args;
+  a.a = d->a;
+  a.codes = op->weight->codes;
+  a.palette = d->palette;
+  a.out = d->output;
+  a.bias = d->bias;
+  a.residual = d->residual;
+  a.residual_scale = d->residual ? residual_scale : 0.0f;
+  a.activation = d->activation;
+  a.rows = d->rows;
+  a.inner = d->inner;
+  a.columns = d->columns;
+  a.palette_groups = d->palette_groups;
+  a.palette_group_columns = d->palette_group_columns;
+  hipDeviceProp_t prop;
+  int cus = 256;
+  if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
+    cus = prop.multiProcessorCount;
+  op->variant = plan_variant(d->precision, d->rows, d->inner, d->columns, cus);
+  *out = op;
+  return ok();
+}
+
+int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  const uint32_t rows = active_rows ? active_rows : op->rows;
+  // GemmDispatch.encode (gemm.ts:427-438)
+  if (rows > op->rows)
+    return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
+  pk::GemmArgs args = op->args;
+  args.rows = rows;
+  hipStream_t st = stream_or_default(op->ctx, stream);
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  const hipError_t e = op->precision == PK_PRECISION_F16
+                           ? pk::launch_gemm_f16(op->bits, op->variant, args, st)
+                           : pk::launch_gemm_f32(op->bits, op->variant, args, st);
+  PK_HIP(e, "palette GEMM launch");
+  return ok();
+}
+
+int pk_gemm_destroy(pk_gemm_op* op) {
+  if (!op || op->destroyed) return ok();
+  op->destroyed = true;
+  weight_unref(op->weight);
+  op->weight = nullptr;
+  return ok();
+}
+
+int pk_gemm_release(pk_gemm_op* op) {
+  if (!op) return ok();
+  pk_gemm_destroy(op);
+  delete op;
+  return ok();
+}
+
+int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
+  const int count = op->precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
+  if (variant < 0 || variant >= count)
+    return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
+  op->variant = variant;
+  return ok();
+}
+
+int pk_gemm_variant_count(int precision) {
+  return precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
+}
+
+int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* info) {
+  if (!op || !info) return fail(PK_INVALID_ARGUMENT, "argument is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  const uint32_t rows = active_rows ? active_rows : op->rows;
+  if (rows > op->rows)
+    return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
+  const bool f16 = op->precision == PK_PRECISION_F16;
+  const pk::TileShape s = f16 ? pk::f16_variant(op->variant) : pk::f32_variant(op->variant);
+  std::memset(info, 0, sizeof *info);
+  const uint32_t n_pad = pk::padded_columns(op->args.columns);
+  info->grid[0] = (n_pad + s.tile_columns() - 1) / s.tile_columns();
+  info->grid[1] = (rows + s.tile_rows() - 1) / s.tile_rows();
+  info->grid[2] = 1;
+  info->block_threads = s.threads();
+  info->tile_rows = s.tile_rows();
+  info->tile_columns = s.tile_columns();
+  info->split_inner = 1;
+  const uint32_t elem = f16 ? 2u : 4u;
+  const uint32_t lut_cap = (s.tile_columns() / 16u + 2u) * (1u << op->bits);
+  info->lds_bytes = 2u * s.tile_rows() * (f16 ? 128u : 256u) + lut_cap * elem;
+  const uint64_t M = rows, K = op->args.inner, N = op->args.columns;
+  info->flops = 2ull * M * K * N;
+  uint64_t bytes = (K * N * (uint64_t)op->bits + 7u) / 8u;
+  bytes += (uint64_t)op->args.palette_groups * (1u << op->bits) * elem;
+  bytes += M * K * elem + M * N * elem;
+  if (op->args.bias) bytes += 4u * N;
+  if (op->args.residual) bytes += M * N * elem;
+  info->algorithmic_bytes = bytes;
+  std::snprintf(info->kernel, sizeof info->kernel, "%s",
+                f16 ? pk::f16_variant_name(op->bits, op->variant) : pk::f32_variant_name(op->bits, op->variant));
+  return ok();
+}
+
+int pk_palette_expand(pk_context* ctx, const pk_expand_desc* d, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!d) return fail(PK_INVALID_ARGUMENT, "expansion descriptor is null");
+  if (d->struct_size != sizeof(pk_expand_desc))
+    return fail(PK_INVALID_ARGUMENT, "pk_expand_desc.struct_size mismatch");
+  const char* label = safe_label(d->label);
+  const bool f16 = d->precision == PK_PRECISION_F16;
+  if ((!f16 && d->precision != PK_PRECISION_F32) || (d->palette_bits != 5 && d->palette_bits != 6))
+    return fail(PK_INVALID_ARGUMENT, "%s has a mismatched palette execution layout", label);
+  const uint32_t elem = f16 ? 2u : 4u;
+  const uint32_t cpg = pk::codes_per_group(d->palette_bits);
+  const uint64_t scalars = (uint64_t)d->inner * d->columns;
+  // requireTransientDescriptor (palette-expander.ts:361-420)
+  if (scalars == 0 || scalars % cpg != 0 || d->columns % cpg != 0 || d->palette_group_columns == 0 ||
+      d->columns % d->palette_group_columns != 0 || d->palette_groups == 0 ||
+      (uint64_t)d->palette_group_columns * d->palette_groups != d->columns ||
+      d->packed_bytes != scalars / cpg * pk::words_per_group(d->palette_bits) * 4u ||
+      d->palette_bytes != (uint64_t)d->palette_groups * (1u << d->palette_bits) * elem ||
+      d->target_bytes != scalars * elem || !d->packed || !d->palette || !d->target ||
+      !aligned(d->packed, 4) || !aligned(d->palette, elem) || !aligned(d->target, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid transient palette geometry", label);
+  const bool tile = d->layout == PK_EXPAND_TILE_MAJOR;
+  if (!tile && d->layout != PK_EXPAND_ROW_MAJOR)
+    return fail(PK_INVALID_ARGUMENT, "%s has unsupported expanded layout %d", label, d->layout);
+  if (tile && (d->inner % 32u != 0 || d->columns % (f16 ? 256u : 128u) != 0))
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid tile-major geometry", label);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(pk::launch_expand(d->palette_bits, f16, tile, d->packed, d->inner, d->columns,
+                           d->palette_group_columns, d->palette_groups, d->palette, d->target,
+                           stream_or_default(ctx, stream)),
+         "palette expansion launch");
+  return ok();
+}
+
+int pk_unpack_codes(pk_context* ctx, int palette_bits, const uint32_t* words, uint64_t group_count,
+                    uint8_t* codes, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (palette_bits != 5 && palette_bits != 6)
+    return fail(PK_INVALID_ARGUMENT, "Unsupported palette code width %d", palette_bits);
+  if (group_count == 0) return ok();
+  if (!words || !codes || !aligned(words, 4) || !aligned(codes, 16))
+    return fail(PK_INVALID_ARGUMENT, "unpack needs 4-byte aligned words and 16-byte aligned codes");
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(pk::launch_unpack(palette_bits, words, group_count, codes, stream_or_default(ctx, stream)),
+         "unpack launch");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,208 @@
+// pk_codes.hip - packed palette code kernels for gfx950: bit-exact unpack,
+// the reference-compatible dense expander and the one-time conversion of a
+// reference-format weight into the MFMA operand order read by the fused GEMM.
+#include "pk_internal.h"
+
+namespace pk {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Code i of a reference group: ((w[b/32] >> b%32) | (w[b/32+1] << (32-b%32)))
+// & mask with b = i*bits, computed on u32 (src/model/palette-expander.ts:500-511).
+template <int BITS>
+__device__ __forceinline__ uint32_t group_code(const uint32_t* w, int i) {
+  const int bit = i * BITS;
+  const int word = bit >> 5;
+  const int shift = bit & 31;
+  uint32_t value = w[word] >> shift;
+  if (shift + BITS > 32) value |= w[word + 1] << (32 - shift);
+  return value & ((1u << BITS) - 1u);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void unpack_kernel(const uint32_t* __restrict__ words,
+                                                          uint64_t groups,
+                                                          uint8_t* __restrict__ codes) {
+  constexpr int CPG = (int)codes_per_group(BITS);
+  constexpr int WPG = (int)words_per_group(BITS);
+  const uint64_t g = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (g >= groups) return;
+  uint32_t w[WPG + 1];
+#pragma unroll
+  for (int i = 0; i < WPG; ++i) w[i] = words[g * WPG + i];
+  w[WPG] = 0;
+  uint32_t packed[CPG / 4];
+#pragma unroll
+  for (int i = 0; i < CPG / 4; ++i) packed[i] = 0;
+#pragma unroll
+  for (int i = 0; i < CPG; ++i) packed[i / 4] |= group_code<BITS>(w, i) << (8 * (i % 4));
+  uint4* dst = reinterpret_cast<uint4*>(codes + g * CPG);
+#pragma unroll
+  for (int v = 0; v < CPG / 16; ++v)
+    dst[v] = make_uint4(packed[4 * v], packed[4 * v + 1], packed[4 * v + 2], packed[4 * v + 3]);
+}
+
+// Tile-major scratch index (src/model/runtime-plan.ts:454-490).
+__device__ __forceinline__ uint64_t tile_major_index(uint64_t scalar, uint32_t inner,
+                                                     uint32_t columns, uint32_t tile_columns) {
+  const uint64_t k = scalar / columns;
+  const uint64_t n = scalar % columns;
+  const uint64_t k_tiles = inner / 32u;
+  return (((n / tile_columns) * k_tiles + k / 32u) * 32u + k % 32u) * tile_columns +
+         n % tile_columns;
+}
+
+// One thread per code group, like paletteDequantWgslForScalar
+// (palette-expander.ts:573-585): palette group from the group's first
+// scalar, one LUT gather per code, dense row-major or tile-major stores.
+template <int BITS, typename T, bool TILE>
+__global__ __launch_bounds__(kThreads) void expand_kernel(
+    const uint32_t* __restrict__ packed, uint64_t scalar_count, uint32_t inner,
+    uint32_t columns, uint32_t group_columns, uint32_t groups,
+    const T* __restrict__ palette, T* __restrict__ target) {
+  constexpr int CPG = (int)codes_per_group(BITS);
+  constexpr int WPG = (int)words_per_group(BITS);
+  constexpr uint32_t kEntries = 1u << BITS;
+  constexpr uint32_t kTileColumns = sizeof(T) == 2 ? 256u : 128u;
+  const uint64_t g = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  const uint64_t scalar_base = g * CPG;
+  if (scalar_base >= scalar_count) return;
+  uint32_t w[WPG + 1];
+#pragma unroll
+  for (int i = 0; i < WPG; ++i) w[i] = packed[g * WPG + i];
+  w[WPG] = 0;
+  const uint32_t column = (uint32_t)(scalar_base % columns);
+  const uint32_t pg = min(column / group_columns, groups - 1u);
+  const T* lut = palette + (uint64_t)pg * kEntries;
+#pragma unroll
+  for (int v = 0; v < CPG / 4; ++v) {
+    T values[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) values[c] = lut[group_code<BITS>(w, 4 * v + c)];
+    const uint64_t first = scalar_base + 4u * v;
+    const uint64_t dst = TILE ? tile_major_index(first, inner, columns, kTileColumns) : first;
+    if constexpr (sizeof(T) == 2) {
+      uint2 bits;
+      bits.x = (uint32_t)__builtin_bit_cast(uint16_t, values[0]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, values[1]) << 16);
+      bits.y = (uint32_t)__builtin_bit_cast(uint16_t, values[2]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, values[3]) << 16);
+      *reinterpret_cast<uint2*>(target + dst) = bits;
+    } else {
+      *reinterpret_cast<float4*>(target + dst) = make_float4(values[0], values[1], values[2], values[3]);
+    }
+  }
+}
+
+// Reference format -> MFMA operand order (layout in pk_internal.h). One
+// thread per (block, lane); runs once per weight.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void operand_order_kernel(
+    const uint32_t* __restrict__ packed, uint32_t inner, uint32_t columns,
+    uint32_t k_blocks, uint64_t total_lanes, uint32_t* __restrict__ out) {
+  constexpr uint32_t CPG = codes_per_group(BITS);
+  constexpr uint32_t WPG = words_per_group(BITS);
+  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= total_lanes) return;
+  const uint32_t lane = (uint32_t)(t & 63u);
+  const uint64_t block = t >> 6;
+  const uint32_t nb = (uint32_t)(block / k_blocks);
+  const uint32_t kb = (uint32_t)(block % k_blocks);
+  const uint32_t n = nb * 32u + (lane & 31u);
+  const uint32_t k0 = kb * 64u + (lane >> 5) * 32u;
+  uint32_t w[BITS + 1];
+#pragma unroll
+  for (int q = 0; q <= BITS; ++q) w[q] = 0;
+#pragma unroll 4
+  for (uint32_t u = 0; u < 32u; ++u) {
+    const uint32_t k = k0 + u;
+    uint32_t code = 0;
+    if (k < inner && n < columns) {
+      const uint64_t scalar = (uint64_t)k * columns + n;
+      const uint64_t g = scalar / CPG;
+      const uint32_t bit = (uint32_t)(scalar % CPG) * BITS;
+      const uint32_t word = bit >> 5, shift = bit & 31u;
+      uint32_t value = packed[g * WPG + word] >> shift;
+      if (shift + BITS > 32u) value |= packed[g * WPG + word + 1] << (32u - shift);
+      code = value & ((1u << BITS) - 1u);
+    }
+    const uint32_t b = u * BITS;
+    w[b >> 5] |= code << (b & 31u);
+    if ((b & 31u) + BITS > 32u) w[(b >> 5) + 1] |= code >> (32u - (b & 31u));
+  }
+  uint32_t* base = out + block * block_words(BITS);
+  reinterpret_cast<uint4*>(base)[lane] = make_uint4(w[0], w[1], w[2], w[3]);
+  if constexpr (BITS == 5) {
+    base[256 + lane] = w[4];
+  } else {
+    reinterpret_cast<uint2*>(base + 256)[lane] = make_uint2(w[4], w[5]);
+  }
+}
+
+inline dim3 grid_for(uint64_t items) {
+  return dim3((unsigned)((items + kThreads - 1) / kThreads));
+}
+
+}  // namespace
+
+hipError_t launch_unpack(int bits, const uint32_t* words, uint64_t groups,
+                         uint8_t* codes, hipStream_t stream) {
+  if (groups == 0) return hipSuccess;
+  if (bits == 5)
+    hipLaunchKernelGGL(unpack_kernel<5>, grid_for(groups), dim3(kThreads), 0, stream, words, groups, codes);
+  else
+    hipLaunchKernelGGL(unpack_kernel<6>, grid_for(groups), dim3(kThreads), 0, stream, words, groups, codes);
+  return hipGetLastError();
+}
+
+template <int BITS, typename T>
+static void launch_expand_typed(bool tile_major, const uint32_t* packed, uint32_t inner,
+                                uint32_t columns, uint32_t group_columns, uint32_t groups,
+                                const void* palette, void* target, hipStream_t stream) {
+  const uint64_t scalars = (uint64_t)inner * columns;
+  const uint64_t code_groups = scalars / codes_per_group(BITS);
+  const dim3 grid = grid_for(code_groups);
+  if (tile_major)
+    hipLaunchKernelGGL((expand_kernel<BITS, T, true>), grid, dim3(kThreads), 0, stream, packed,
+                       scalars, inner, columns, group_columns, groups,
+                       static_cast<const T*>(palette), static_cast<T*>(target));
+  else
+    hipLaunchKernelGGL((expand_kernel<BITS, T, false>), grid, dim3(kThreads), 0, stream, packed,
+                       scalars, inner, columns, group_columns, groups,
+                       static_cast<const T*>(palette), static_cast<T*>(target));
+}
+
+hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* packed,
+                         uint32_t inner, uint32_t columns, uint32_t group_columns,
+                         uint32_t groups, const void* palette, void* target,
+                         hipStream_t stream) {
+  if (bits == 5) {
+    if (f16)
+      launch_expand_typed<5, _Float16>(tile_major, packed, inner, columns, group_columns, groups, palette, target, stream);
+    else
+      launch_expand_typed<5, float>(tile_major, packed, inner, columns, group_columns, groups, palette, target, stream);
+  } else {
+    if (f16)
+      launch_expand_typed<6, _Float16>(tile_major, packed, inner, columns, group_columns, groups, palette, target, stream);
+    else
+      launch_expand_typed<6, float>(tile_major, packed, inner, columns, group_columns, groups, palette, target, stream);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
+                                   uint32_t columns, uint32_t* codes, hipStream_t stream) {
+  const uint32_t k_blocks = padded_inner(inner) / 64u;
+  const uint64_t blocks = (uint64_t)(padded_columns(columns) / 32u) * k_blocks;
+  const uint64_t lanes = blocks * 64u;
+  if (bits == 5)
+    hipLaunchKernelGGL(operand_order_kernel<5>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
+                       inner, columns, k_blocks, lanes, codes);
+  else
+    hipLaunchKernelGGL(operand_order_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
+                       inner, columns, k_blocks, lanes, codes);
+  return hipGetLastError();
+}
+
+}  // namespace pk

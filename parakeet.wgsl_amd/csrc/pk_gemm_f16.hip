@@ -1,0 +1,300 @@
+// pk_gemm_f16.hip - fused palette-weight GEMM, f16 operands, f32 MFMA
+// accumulation, for gfx950 (CDNA4, wave64).
+//
+// C[m, n] = epilogue(sum_k A[m, k] * LUT[g(n)][code(k, n)])
+//
+// The dense weight is never materialised. Per 64-deep K step a wavefront
+//   * fetches, for each of its 32-column blocks, the block's codes in MFMA
+//     operand order (one 128-bit + one 32/64-bit coalesced load per lane),
+//   * decodes the 32 codes of its lane with v_bfe_u32 / v_alignbit_b32 and
+//     gathers them from the palette staged in LDS straight into the 8-half
+//     operand registers of v_mfma_f32_32x32x16_f16,
+//   * reads its activation fragments from an LDS tile (double buffered,
+//     16-byte chunks XOR-swizzled by row so 8 consecutive rows hit 8
+//     different bank groups),
+//   * issues m_blocks x n_blocks MFMAs per 16-deep sub-step.
+// The MFMA computes D = W^T * A^T (weights as the 32x16 "A" operand), so a
+// lane ends with 4 runs of 4 consecutive output columns of one row: the
+// epilogue (bias -> activation -> residual + scale * value, gemm.ts:2006-2044)
+// runs in f32 and stores 8 bytes per run.
+//
+// K-slot pairing: in sub-step s, lane half h, operand element t stands for
+// k = 64*kb + 32*h + 8*s + t in BOTH operands, so the hardware's own pairing
+// of A and B slots always multiplies matching k.
+#include "pk_internal.h"
+
+namespace pk {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+template <int BITS>
+__device__ __forceinline__ uint32_t lane_code(const uint32_t* w, int u) {
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  const int bit = u * BITS;
+  const int word = bit >> 5;
+  const int shift = bit & 31;
+  if (shift + BITS <= 32) return (w[word] >> shift) & mask;
+  return __builtin_amdgcn_alignbit(w[word + 1], w[word], shift) & mask;
+}
+
+__device__ __forceinline__ float silu(float v) {
+  const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
+  return v / (1.0f + expf(-bounded));
+}
+
+template <int BITS, int WM, int WN, int MB, int NB>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f16_kernel(GemmArgs args) {
+  constexpr int T = 64 * WM * WN;
+  constexpr int BM = 32 * WM * MB;
+  constexpr int BN = 32 * WN * NB;
+  constexpr int E = 1 << BITS;
+  constexpr int LUT_CAP = (BN / 16 + 2) * E;
+  constexpr int ROW_BYTES = 128;  // 64 halves of one row per K step
+  constexpr int CH = BM * 8 / T;  // 16-byte A chunks per thread per K step
+  static_assert(BM * 8 % T == 0, "A tile chunks must divide evenly");
+
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * ROW_BYTES];
+  __shared__ _Float16 lut_lds[LUT_CAP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_m = wave / WN;
+  const int wave_n = wave % WN;
+  const int j = lane & 31;
+  const int h = lane >> 5;
+
+  const uint32_t M = args.rows;
+  const uint32_t K = args.inner;
+  const uint32_t N = args.columns;
+  const uint32_t k_blocks = (K + 63u) / 64u;
+  const uint32_t n_blocks_total = (N + 31u) / 32u;
+  const uint32_t n0 = blockIdx.x * BN;
+  const uint32_t m0 = blockIdx.y * BM;
+
+  // Palette window of this tile's columns (palette-expander.ts:543-549).
+  const uint32_t gc = args.palette_group_columns;
+  const uint32_t G = args.palette_groups;
+  const uint32_t g_lo = min(n0 / gc, G - 1u);
+  const uint32_t g_hi = min((min(n0 + BN, N) - 1u) / gc, G - 1u);
+  {
+    const uint32_t entries = (g_hi - g_lo + 1u) * E;
+    const _Float16* src = static_cast<const _Float16*>(args.palette) + (uint64_t)g_lo * E;
+    for (uint32_t i = tid; i < entries; i += T) lut_lds[i] = src[i];
+  }
+  const _Float16* lut_col[NB];
+#pragma unroll
+  for (int ni = 0; ni < NB; ++ni) {
+    const uint32_t n = n0 + (wave_n * NB + ni) * 32 + j;
+    const uint32_t g = min(n / gc, G - 1u) - g_lo;
+    lut_col[ni] = lut_lds + g * E;
+  }
+
+  // Code stream of each of this wave's 32-column blocks.
+  const uint32_t nb0 = n0 / 32u + wave_n * NB;
+  uint32_t cw[NB][BITS];
+  auto load_codes = [&](uint32_t kb, uint32_t (&dst)[NB][BITS]) {
+#pragma unroll
+    for (int ni = 0; ni < NB; ++ni) {
+      const uint32_t nb = nb0 + ni;
+      if (nb < n_blocks_total) {
+        const uint32_t* blk = args.codes + ((uint64_t)nb * k_blocks + kb) * block_words(BITS);
+        const uint4 p0 = reinterpret_cast<const uint4*>(blk)[lane];
+        dst[ni][0] = p0.x;
+        dst[ni][1] = p0.y;
+        dst[ni][2] = p0.z;
+        dst[ni][3] = p0.w;
+        if constexpr (BITS == 5) {
+          dst[ni][4] = blk[256 + lane];
+        } else {
+          const uint2 p1 = reinterpret_cast<const uint2*>(blk + 256)[lane];
+          dst[ni][4] = p1.x;
+          dst[ni][5] = p1.y;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < BITS; ++q) dst[ni][q] = 0u;
+      }
+    }
+  };
+
+  // Activation tile staging: BM rows x 8 chunks of 16 bytes per K step.
+  const _Float16* a_ptr = static_cast<const _Float16*>(args.a);
+  uint4 a_stage[CH];
+  auto load_a = [&](uint32_t kb) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = tid + c * T;
+      const int r = idx >> 3;
+      const int ch = idx & 7;
+      const uint32_t m = m0 + r;
+      const uint32_t k = kb * 64u + ch * 8u;
+      if (m < M && k < K)
+        a_stage[c] = *reinterpret_cast<const uint4*>(a_ptr + (uint64_t)m * K + k);
+      else
+        a_stage[c] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = tid + c * T;
+      const int r = idx >> 3;
+      const int ch = idx & 7;
+      *reinterpret_cast<uint4*>(&a_lds[buf][r * ROW_BYTES + ((ch ^ (r & 7)) << 4)]) = a_stage[c];
+    }
+  };
+
+  float16v acc[MB][NB];
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NB; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+
+  load_codes(0, cw);
+  load_a(0);
+  store_a(0);
+  __syncthreads();
+
+  for (uint32_t kb = 0; kb < k_blocks; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < k_blocks;
+    uint32_t cn[NB][BITS];
+    if (more) {
+      load_codes(kb + 1, cn);
+      load_a(kb + 1);
+    }
+    const uint8_t* tile = a_lds[buf];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 bf[NB];
+#pragma unroll
+      for (int ni = 0; ni < NB; ++ni)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) bf[ni][t] = lut_col[ni][lane_code<BITS>(cw[ni], s * 8 + t)];
+#pragma unroll
+      for (int mi = 0; mi < MB; ++mi) {
+        const int r = (wave_m * MB + mi) * 32 + j;
+        const int ch = h * 4 + s;
+        const half8 af = *reinterpret_cast<const half8*>(&tile[r * ROW_BYTES + ((ch ^ (r & 7)) << 4)]);
+#pragma unroll
+        for (int ni = 0; ni < NB; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ni], af, acc[mi][ni], 0, 0, 0);
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int ni = 0; ni < NB; ++ni)
+#pragma unroll
+        for (int q = 0; q < BITS; ++q) cw[ni][q] = cn[ni][q];
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds row m = ... + j and, for q = 0..3, the 4 columns
+  // n = 32*block + 8*q + 4*h + {0,1,2,3}.
+  _Float16* out = static_cast<_Float16*>(args.out);
+  const _Float16* residual = static_cast<const _Float16*>(args.residual);
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi) {
+    const uint32_t m = m0 + (wave_m * MB + mi) * 32 + j;
+    if (m >= M) continue;
+#pragma unroll
+    for (int ni = 0; ni < NB; ++ni) {
+      const uint32_t nbase = n0 + (wave_n * NB + ni) * 32 + h * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t n = nbase + q * 8;
+        if (n >= N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[mi][ni][q * 4 + e];
+        if (args.bias) {
+          const float4 b = *reinterpret_cast<const float4*>(args.bias + n);
+          v[0] += b.x;
+          v[1] += b.y;
+          v[2] += b.z;
+          v[3] += b.w;
+        }
+        if (args.activation == kActSilu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = silu(v[e]);
+        } else if (args.activation == kActRelu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+        }
+        const uint64_t at = (uint64_t)m * N + n;
+        if (residual) {
+          const uint2 rb = *reinterpret_cast<const uint2*>(residual + at);
+          const _Float16 r0 = __builtin_bit_cast(_Float16, (uint16_t)(rb.x & 0xffffu));
+          const _Float16 r1 = __builtin_bit_cast(_Float16, (uint16_t)(rb.x >> 16));
+          const _Float16 r2 = __builtin_bit_cast(_Float16, (uint16_t)(rb.y & 0xffffu));
+          const _Float16 r3 = __builtin_bit_cast(_Float16, (uint16_t)(rb.y >> 16));
+          v[0] = (float)r0 + args.residual_scale * v[0];
+          v[1] = (float)r1 + args.residual_scale * v[1];
+          v[2] = (float)r2 + args.residual_scale * v[2];
+          v[3] = (float)r3 + args.residual_scale * v[3];
+        }
+        uint2 ob;
+        ob.x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
+        ob.y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[3]) << 16);
+        *reinterpret_cast<uint2*>(out + at) = ob;
+      }
+    }
+  }
+}
+
+struct Variant {
+  TileShape shape;
+  const char* name5;
+  const char* name6;
+  void (*kernel5)(GemmArgs);
+  void (*kernel6)(GemmArgs);
+};
+
+#define PK_F16_VARIANT(WM, WN, MB, NB)                                             \
+  Variant {                                                                        \
+    TileShape{WM, WN, MB, NB}, "pk_gemm_f16_b5_w" #WM "x" #WN "_m" #MB "n" #NB,    \
+        "pk_gemm_f16_b6_w" #WM "x" #WN "_m" #MB "n" #NB,                           \
+        gemm_f16_kernel<5, WM, WN, MB, NB>, gemm_f16_kernel<6, WM, WN, MB, NB>     \
+  }
+
+const Variant kVariants[] = {
+    PK_F16_VARIANT(1, 4, 8, 2),  // 256 x 256
+    PK_F16_VARIANT(1, 4, 4, 2),  // 128 x 256
+    PK_F16_VARIANT(1, 4, 6, 1),  // 192 x 128
+    PK_F16_VARIANT(1, 2, 6, 1),  // 192 x 64
+    PK_F16_VARIANT(1, 4, 3, 2),  // 96 x 256
+    PK_F16_VARIANT(1, 4, 3, 1),  // 96 x 128
+    PK_F16_VARIANT(1, 4, 2, 2),  // 64 x 256
+    PK_F16_VARIANT(1, 4, 1, 1),  // 32 x 128
+    PK_F16_VARIANT(2, 2, 4, 2),  // 256 x 128
+    PK_F16_VARIANT(1, 3, 6, 2),  // 192 x 192
+};
+
+}  // namespace
+
+int f16_variant_count() { return (int)(sizeof(kVariants) / sizeof(kVariants[0])); }
+TileShape f16_variant(int index) { return kVariants[index].shape; }
+const char* f16_variant_name(int bits, int index) {
+  return bits == 5 ? kVariants[index].name5 : kVariants[index].name6;
+}
+
+hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream) {
+  const Variant& v = kVariants[variant];
+  const uint32_t n_pad = padded_columns(args.columns);
+  const dim3 grid((n_pad + v.shape.tile_columns() - 1) / v.shape.tile_columns(),
+                  (args.rows + v.shape.tile_rows() - 1) / v.shape.tile_rows());
+  if (grid.y == 0) return hipSuccess;
+  hipLaunchKernelGGL(bits == 5 ? v.kernel5 : v.kernel6, grid, dim3(v.shape.threads()), 0, stream, args);
+  return hipGetLastError();
+}
+
+}  // namespace pk

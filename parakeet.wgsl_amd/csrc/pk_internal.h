@@ -1,0 +1,83 @@
+// pk_internal.h - shared declarations of the palette GEMM library (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pk {
+
+// Reference packed-format group geometry (model/convert.py:2119-2127).
+__host__ __device__ constexpr uint32_t codes_per_group(int bits) { return bits == 5 ? 32u : 16u; }
+__host__ __device__ constexpr uint32_t words_per_group(int bits) { return bits == 5 ? 5u : 3u; }
+
+// ---------------------------------------------------------------------------
+// MFMA-native packed layout ("operand order"), built once per weight.
+//
+// The logical [K, N] code matrix is cut into blocks of 64 k x 32 n. Inside a
+// block, lane l = 32*h + j (h in {0,1}, j in [0,32)) of a wavefront owns the
+// 32 codes of column n = 32*nb + j at k = 64*kb + 32*h + u, u = 0..31, packed
+// LSB-first at bit u*bits of a `bits`-word stream (the same bits per code as
+// the reference format, so the same number of bytes). Words 0..3 of every
+// lane are stored lane-interleaved as one 16-byte vector per lane (plane 0),
+// the remaining bits-4 words as one 4- or 8-byte vector per lane (plane 1),
+// so a wavefront fetches a block with one coalesced 128-bit load plus one
+// 32/64-bit load per lane. Blocks are ordered [nb][kb], making the stream a
+// wavefront reads along K contiguous. K pads to 64 and N to 32 with code 0.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr uint32_t block_words(int bits) { return 64u * (uint32_t)bits; }
+__host__ __device__ constexpr uint32_t padded_inner(uint32_t inner) { return (inner + 63u) / 64u * 64u; }
+__host__ __device__ constexpr uint32_t padded_columns(uint32_t columns) { return (columns + 31u) / 32u * 32u; }
+__host__ __device__ constexpr uint64_t operand_order_words(int bits, uint32_t inner, uint32_t columns) {
+  return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * block_words(bits);
+}
+
+enum Activation : int { kActNone = 0, kActSilu = 1, kActRelu = 2 };
+
+struct GemmArgs {
+  const void* a;             // [M, K]
+  const uint32_t* codes;     // operand-order codes
+  const void* palette;       // [G, 2^bits]
+  void* out;                 // [M, N]
+  const float* bias;         // [N] or null
+  const void* residual;      // [M, N] or null
+  float residual_scale;
+  int activation;
+  uint32_t rows;             // active M
+  uint32_t inner;            // K
+  uint32_t columns;          // N
+  uint32_t palette_groups;
+  uint32_t palette_group_columns;
+};
+
+// Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
+// waves_m x waves_n wavefronts; a wavefront owns m_blocks x n_blocks MFMA
+// output blocks of 32 x 32.
+struct TileShape {
+  int waves_m, waves_n, m_blocks, n_blocks;
+  __host__ __device__ constexpr int threads() const { return 64 * waves_m * waves_n; }
+  __host__ __device__ constexpr int tile_rows() const { return 32 * waves_m * m_blocks; }
+  __host__ __device__ constexpr int tile_columns() const { return 32 * waves_n * n_blocks; }
+};
+
+// Launchers. Each returns the hipError_t of the launch.
+hipError_t launch_unpack(int bits, const uint32_t* words, uint64_t groups,
+                         uint8_t* codes, hipStream_t stream);
+hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* packed,
+                         uint32_t inner, uint32_t columns, uint32_t group_columns,
+                         uint32_t groups, const void* palette, void* target,
+                         hipStream_t stream);
+hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
+                                   uint32_t columns, uint32_t* codes, hipStream_t stream);
+
+// Fused palette GEMM. `variant` indexes f16_variants() / f32_variants().
+int f16_variant_count();
+TileShape f16_variant(int index);
+const char* f16_variant_name(int bits, int index);
+hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream);
+
+int f32_variant_count();
+TileShape f32_variant(int index);
+const char* f32_variant_name(int bits, int index);
+hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream);
+
+}  // namespace pk

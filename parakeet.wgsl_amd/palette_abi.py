@@ -1,0 +1,386 @@
+"""ctypes binding of libpk_palette.so (include/pk_palette.h).
+
+A thin Python view of the C ABI, used by the tests and the benchmark. It
+raises PaletteError (or PaletteRangeError, mirroring the reference's
+RangeError cases) carrying pk_last_error() when a call fails, and it never
+falls back to anything: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libpk_palette.so")
+
+OK, INVALID_ARGUMENT, ALLOCATION_FAILURE, INTERNAL_ERROR, DEVICE_ERROR, DESTROYED, RANGE_ERROR = range(7)
+PRECISION = {"f16": 0, "f32": 1}
+ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
+REQUIRE_PRODUCTION_SIGNATURE = 0x1
+EXPAND_LAYOUT = {"row-major": 0, "tile-major": 1}
+
+
+class PaletteError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class PaletteRangeError(PaletteError):
+    pass
+
+
+class PaletteDestroyedError(PaletteError):
+    pass
+
+
+class WeightDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("palette_bits", ctypes.c_int32),
+        ("inner", ctypes.c_uint32),
+        ("columns", ctypes.c_uint32),
+        ("packed", ctypes.c_void_p),
+        ("packed_bytes", ctypes.c_uint64),
+    ]
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("palette_bits", ctypes.c_int32),
+        ("rows", ctypes.c_uint32),
+        ("inner", ctypes.c_uint32),
+        ("columns", ctypes.c_uint32),
+        ("palette_groups", ctypes.c_uint32),
+        ("palette_group_columns", ctypes.c_uint32),
+        ("a", ctypes.c_void_p),
+        ("a_bytes", ctypes.c_uint64),
+        ("packed", ctypes.c_void_p),
+        ("packed_bytes", ctypes.c_uint64),
+        ("palette", ctypes.c_void_p),
+        ("palette_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+        ("bias", ctypes.c_void_p),
+        ("bias_bytes", ctypes.c_uint64),
+        ("residual", ctypes.c_void_p),
+        ("residual_bytes", ctypes.c_uint64),
+        ("has_residual_scale", ctypes.c_int32),
+        ("residual_scale", ctypes.c_float),
+        ("activation", ctypes.c_int32),
+        ("prepared", ctypes.c_void_p),
+    ]
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("grid", ctypes.c_uint32 * 3),
+        ("block_threads", ctypes.c_uint32),
+        ("tile_rows", ctypes.c_uint32),
+        ("tile_columns", ctypes.c_uint32),
+        ("split_inner", ctypes.c_uint32),
+        ("lds_bytes", ctypes.c_uint32),
+        ("flops", ctypes.c_uint64),
+        ("algorithmic_bytes", ctypes.c_uint64),
+        ("kernel", ctypes.c_char * 64),
+    ]
+
+
+class ExpandDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("palette_bits", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("inner", ctypes.c_uint32),
+        ("columns", ctypes.c_uint32),
+        ("palette_groups", ctypes.c_uint32),
+        ("palette_group_columns", ctypes.c_uint32),
+        ("packed", ctypes.c_void_p),
+        ("packed_bytes", ctypes.c_uint64),
+        ("palette", ctypes.c_void_p),
+        ("palette_bytes", ctypes.c_uint64),
+        ("target", ctypes.c_void_p),
+        ("target_bytes", ctypes.c_uint64),
+    ]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 64),
+        ("arch", ctypes.c_char * 32),
+        ("compute_units", ctypes.c_int32),
+        ("wavefront_size", ctypes.c_int32),
+        ("global_memory_bytes", ctypes.c_int64),
+        ("lds_bytes_per_block", ctypes.c_int32),
+        ("clock_khz", ctypes.c_int32),
+    ]
+
+
+# Every function the header declares: name -> (restype, argtypes).
+_VP = ctypes.c_void_p
+_PPV = ctypes.POINTER(ctypes.c_void_p)
+SIGNATURES = {
+    "pk_abi_version": (ctypes.c_int, []),
+    "pk_last_error": (ctypes.c_char_p, []),
+    "pk_status_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "pk_context_create": (ctypes.c_int, [ctypes.c_int, _PPV]),
+    "pk_context_destroy": (ctypes.c_int, [_VP]),
+    "pk_context_device": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_int)]),
+    "pk_context_stream": (ctypes.c_int, [_VP, _PPV]),
+    "pk_device_query": (ctypes.c_int, [_VP, ctypes.POINTER(DeviceInfo)]),
+    "pk_alloc": (ctypes.c_int, [_VP, ctypes.c_uint64, _PPV]),
+    "pk_free": (ctypes.c_int, [_VP, _VP]),
+    "pk_upload": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, _VP]),
+    "pk_download": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, _VP]),
+    "pk_copy_device": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_uint64, _VP]),
+    "pk_stream_create": (ctypes.c_int, [_VP, _PPV]),
+    "pk_stream_destroy": (ctypes.c_int, [_VP, _VP]),
+    "pk_stream_synchronize": (ctypes.c_int, [_VP, _VP]),
+    "pk_event_create": (ctypes.c_int, [_VP, _PPV]),
+    "pk_event_destroy": (ctypes.c_int, [_VP, _VP]),
+    "pk_event_record": (ctypes.c_int, [_VP, _VP, _VP]),
+    "pk_event_synchronize": (ctypes.c_int, [_VP, _VP]),
+    "pk_event_elapsed_ms": (ctypes.c_int, [_VP, _VP, _VP, ctypes.POINTER(ctypes.c_float)]),
+    "pk_prepared_weight_create": (ctypes.c_int, [_VP, ctypes.POINTER(WeightDesc), _VP, _PPV]),
+    "pk_prepared_weight_destroy": (ctypes.c_int, [_VP]),
+    "pk_prepared_weight_bytes": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint64)]),
+    "pk_gemm_create": (ctypes.c_int, [_VP, ctypes.POINTER(GemmDesc), _VP, _PPV]),
+    "pk_gemm_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_gemm_destroy": (ctypes.c_int, [_VP]),
+    "pk_gemm_release": (ctypes.c_int, [_VP]),
+    "pk_gemm_variant_count": (ctypes.c_int, [ctypes.c_int]),
+    "pk_gemm_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
+    "pk_gemm_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
+    "pk_palette_expand": (ctypes.c_int, [_VP, ctypes.POINTER(ExpandDesc), _VP]),
+    "pk_unpack_codes": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_uint64, _VP, _VP]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree libpk_palette.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `python parakeet.wgsl_amd/build.py`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    if status == OK:
+        return
+    message = load().pk_last_error().decode(errors="replace")
+    if status == RANGE_ERROR:
+        raise PaletteRangeError(status, message)
+    if status == DESTROYED:
+        raise PaletteDestroyedError(status, message)
+    raise PaletteError(status, message)
+
+
+def codes_per_group(bits: int) -> int:
+    return {5: 32, 6: 16}[bits]
+
+
+def words_per_group(bits: int) -> int:
+    return {5: 5, 6: 3}[bits]
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype and shape."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx = ctx
+        if isinstance(shape, (int, np.integer)):
+            shape = (int(shape),)
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        ptr = ctypes.c_void_p()
+        check(load().pk_alloc(ctx.handle, self.nbytes, ctypes.byref(ptr)))
+        self.ptr = ptr.value
+
+    def upload(self, array: np.ndarray, stream=None) -> "DeviceArray":
+        array = np.ascontiguousarray(array, dtype=self.dtype)
+        if array.nbytes != self.nbytes:
+            raise ValueError(f"upload of {array.nbytes} bytes into {self.nbytes}")
+        check(load().pk_upload(self.ctx.handle, self.ptr, array.ctypes.data, self.nbytes, stream))
+        return self
+
+    def download(self, stream=None) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        check(load().pk_download(self.ctx.handle, out.ctypes.data, self.ptr, self.nbytes, stream))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(load().pk_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        handle = ctypes.c_void_p()
+        check(load().pk_context_create(device, ctypes.byref(handle)))
+        self.handle = handle.value
+        stream = ctypes.c_void_p()
+        check(load().pk_context_stream(self.handle, ctypes.byref(stream)))
+        self.stream = stream.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(load().pk_context_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> DeviceInfo:
+        info = DeviceInfo()
+        check(load().pk_device_query(self.handle, ctypes.byref(info)))
+        return info
+
+    def array(self, host: np.ndarray) -> DeviceArray:
+        host = np.ascontiguousarray(host)
+        return DeviceArray(self, host.shape, host.dtype).upload(host)
+
+    def empty(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, tuple(shape), dtype)
+
+    def synchronize(self, stream=None) -> None:
+        check(load().pk_stream_synchronize(self.handle, stream))
+
+    def copy(self, dst: DeviceArray, src: DeviceArray, stream=None) -> None:
+        check(load().pk_copy_device(self.handle, dst.ptr, src.ptr, min(dst.nbytes, src.nbytes), stream))
+
+    def event(self) -> "Event":
+        return Event(self)
+
+    def unpack_codes(self, bits: int, words: DeviceArray, codes: DeviceArray, stream=None) -> None:
+        groups = words.nbytes // (4 * words_per_group(bits))
+        check(load().pk_unpack_codes(self.handle, bits, words.ptr, groups, codes.ptr, stream))
+
+    def expand(self, bits: int, packed: DeviceArray, palette: DeviceArray, target: DeviceArray,
+               inner: int, columns: int, *, layout: str = "row-major", label: str = "expand",
+               stream=None) -> None:
+        precision = "f16" if palette.dtype == np.float16 else "f32"
+        groups = palette.shape[0]
+        desc = ExpandDesc(
+            ctypes.sizeof(ExpandDesc), label.encode(), PRECISION[precision], bits,
+            EXPAND_LAYOUT[layout], inner, columns, groups, columns // groups,
+            packed.ptr, packed.nbytes, palette.ptr, palette.nbytes, target.ptr, target.nbytes)
+        check(load().pk_palette_expand(self.handle, ctypes.byref(desc), stream))
+
+
+class Event:
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        handle = ctypes.c_void_p()
+        check(load().pk_event_create(ctx.handle, ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def record(self, stream=None) -> None:
+        check(load().pk_event_record(self.ctx.handle, self.handle, stream))
+
+    def synchronize(self) -> None:
+        check(load().pk_event_synchronize(self.ctx.handle, self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(load().pk_event_elapsed_ms(self.ctx.handle, self.handle, end.handle, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(load().pk_event_destroy(self.ctx.handle, self.handle))
+            self.handle = None
+
+
+class PreparedWeight:
+    def __init__(self, ctx: Context, bits: int, inner: int, columns: int, packed: DeviceArray,
+                 label: str = "prepared-weight", stream=None):
+        desc = WeightDesc(ctypes.sizeof(WeightDesc), label.encode(), bits, inner, columns,
+                          packed.ptr, packed.nbytes)
+        handle = ctypes.c_void_p()
+        check(load().pk_prepared_weight_create(ctx.handle, ctypes.byref(desc), stream, ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def nbytes(self) -> int:
+        value = ctypes.c_uint64()
+        check(load().pk_prepared_weight_bytes(self.handle, ctypes.byref(value)))
+        return int(value.value)
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(load().pk_prepared_weight_destroy(self.handle))
+            self.handle = None
+
+
+class GemmOp:
+    """One fused palette GEMM dispatch (pk_gemm_create ... pk_gemm_release)."""
+
+    def __init__(self, ctx: Context, *, a: DeviceArray, packed: DeviceArray | None, palette: DeviceArray,
+                 output: DeviceArray, bits: int, rows: int, inner: int, columns: int,
+                 bias: DeviceArray | None = None, residual: DeviceArray | None = None,
+                 residual_scale: float | None = None, activation: str = "none",
+                 prepared: PreparedWeight | None = None, label: str = "palette-gemm",
+                 production_only: bool = False, stream=None):
+        precision = "f16" if palette.dtype == np.float16 else "f32"
+        groups = palette.shape[0]
+        self.desc = GemmDesc(
+            ctypes.sizeof(GemmDesc), REQUIRE_PRODUCTION_SIGNATURE if production_only else 0,
+            label.encode(), PRECISION[precision], bits, rows, inner, columns, groups,
+            columns // groups if groups else 0,
+            a.ptr, a.nbytes,
+            packed.ptr if packed is not None else None, packed.nbytes if packed is not None else 0,
+            palette.ptr, palette.nbytes, output.ptr, output.nbytes,
+            bias.ptr if bias is not None else None, bias.nbytes if bias is not None else 0,
+            residual.ptr if residual is not None else None, residual.nbytes if residual is not None else 0,
+            int(residual_scale is not None), float(residual_scale or 0.0), ACTIVATION[activation],
+            prepared.handle if prepared is not None else None)
+        handle = ctypes.c_void_p()
+        check(load().pk_gemm_create(ctx.handle, ctypes.byref(self.desc), stream, ctypes.byref(handle)))
+        self.handle = handle.value
+        self.ctx = ctx
+
+    def enqueue(self, active_rows: int = 0, stream=None) -> None:
+        check(load().pk_gemm_enqueue(self.handle, active_rows, stream))
+
+    def plan(self, active_rows: int = 0) -> PlanInfo:
+        info = PlanInfo()
+        check(load().pk_gemm_plan(self.handle, active_rows, ctypes.byref(info)))
+        return info
+
+    def set_variant(self, variant: int) -> None:
+        check(load().pk_gemm_set_variant(self.handle, variant))
+
+    def destroy(self) -> None:
+        check(load().pk_gemm_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_gemm_release(self.handle))
+            self.handle = None
+
+
+def variant_count(precision: str) -> int:
+    return int(load().pk_gemm_variant_count(PRECISION[precision]))

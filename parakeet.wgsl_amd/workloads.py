@@ -1,0 +1,156 @@
+"""Seeded synthetic inputs for the palette GEMM workloads.
+
+The weights are random palette codes packed in the reference package format
+(model/convert.py:2130-2156: groups of 32 codes in 5 little-endian u32 words
+for 5-bit, 16 codes in 3 words for 6-bit, code i of a group at bit i*bits,
+LSB first) with random LUTs, as the benchmark configurations prescribe; no
+checkpoint is involved. Everything derives from numpy's PCG64 generator so a
+seed fixes every array.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+def codes_per_group(bits: int) -> int:
+    return {5: 32, 6: 16}[bits]
+
+
+def words_per_group(bits: int) -> int:
+    return {5: 5, 6: 3}[bits]
+
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Bit-pack codes ([K, N] K-major or flat) into [groups, words] u32 words."""
+    cpg, wpg = codes_per_group(bits), words_per_group(bits)
+    flat = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    if flat.size % cpg:
+        raise ValueError(f"{flat.size} codes are not a multiple of {cpg}")
+    if flat.size and int(flat.max()) >= 1 << bits:
+        raise ValueError(f"{bits}-bit codes must be below {1 << bits}")
+    grouped = flat.reshape(-1, cpg).astype(np.uint64)
+    # one 160- or 96-bit integer per group, then split into u32 words
+    shifts = (np.arange(cpg, dtype=np.uint64) * np.uint64(bits))
+    words = np.zeros((grouped.shape[0], wpg), dtype=np.uint64)
+    for i in range(cpg):
+        bit = int(shifts[i])
+        word, shift = divmod(bit, 32)
+        words[:, word] |= (grouped[:, i] << np.uint64(shift)) & np.uint64(0xFFFFFFFF)
+        if shift + bits > 32:
+            words[:, word + 1] |= grouped[:, i] >> np.uint64(32 - shift)
+    return words.astype("<u4")
+
+
+@dataclass
+class PaletteMatrix:
+    """A random palette weight: codes [K, N], packed words, LUT [G, 2^bits]."""
+    bits: int
+    inner: int
+    columns: int
+    codes: np.ndarray
+    packed: np.ndarray
+    palette: np.ndarray
+
+    @property
+    def groups(self) -> int:
+        return self.palette.shape[0]
+
+
+def palette_matrix(rng: np.random.Generator, bits: int, inner: int, columns: int, *,
+                   dtype=np.float16, groups: int = 1, lut_std: float = 0.02) -> PaletteMatrix:
+    codes = rng.integers(0, 1 << bits, size=(inner, columns), dtype=np.uint8)
+    palette = (rng.standard_normal((groups, 1 << bits)) * lut_std).astype(dtype)
+    return PaletteMatrix(bits, inner, columns, codes, pack_codes(codes, bits), palette)
+
+
+def normal(rng: np.random.Generator, shape, std: float = 1.0, dtype=np.float16) -> np.ndarray:
+    return (rng.standard_normal(shape) * std).astype(dtype)
+
+
+@dataclass
+class GemmCase:
+    """One palette GEMM with its epilogue operands."""
+    name: str
+    a: np.ndarray
+    weight: PaletteMatrix
+    bias: np.ndarray | None = None
+    residual: np.ndarray | None = None
+    residual_scale: float | None = None
+    activation: str = "none"
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def rows(self) -> int:
+        return self.a.shape[0]
+
+    @property
+    def flops(self) -> int:
+        return 2 * self.rows * self.weight.inner * self.weight.columns
+
+    def algorithmic_bytes(self) -> int:
+        """Compulsory HBM bytes: each tensor once, the dense weight never."""
+        e = self.a.dtype.itemsize
+        w = self.weight
+        total = (w.inner * w.columns * w.bits + 7) // 8
+        total += w.palette.size * w.palette.dtype.itemsize
+        total += self.a.size * e + self.rows * w.columns * e
+        if self.bias is not None:
+            total += 4 * w.columns
+        if self.residual is not None:
+            total += self.rows * w.columns * e
+        return total
+
+
+def single_gemm_fp32(seed: int = 0, rows: int = 256) -> GemmCase:
+    """X[256x1024] ~ N(0,1) f32, 6-bit W 1024->4096, one 64-entry f32 LUT
+    ~ N(0, 0.02), bias ~ N(0, 0.01): Y = X W + b."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (rows, 1024), 1.0, np.float32)
+    w = palette_matrix(rng, 6, 1024, 4096, dtype=np.float32)
+    bias = normal(rng, (4096,), 0.01, np.float32)
+    return GemmCase("single-gemm-fp32", x, w, bias=bias)
+
+
+@dataclass
+class FeedForwardBlock:
+    """Conformer feed-forward block: H = SiLU(X W1), Y = X + 0.5 (H W2)."""
+    x: np.ndarray
+    w1: PaletteMatrix
+    w2: PaletteMatrix
+
+    def expand_case(self) -> GemmCase:
+        return GemmCase("ff-expand", self.x, self.w1, activation="silu")
+
+    def contract_case(self, hidden: np.ndarray) -> GemmCase:
+        return GemmCase("ff-contract", hidden, self.w2, residual=self.x, residual_scale=0.5)
+
+    @property
+    def flops(self) -> int:
+        m = self.x.shape[0]
+        return 2 * m * self.w1.inner * self.w1.columns + 2 * m * self.w2.inner * self.w2.columns
+
+
+def feed_forward_block(seed: int = 0, windows: int = 8, frames: int = 188, d_model: int = 1024,
+                       hidden: int = 4096, bits: int = 5) -> FeedForwardBlock:
+    """Input [windows x frames x d_model] f16 ~ N(0,1); 5-bit W1 d->4d and W2
+    4d->d, one 32-entry f16 LUT each ~ N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (windows * frames, d_model), 1.0, np.float16)
+    w1 = palette_matrix(rng, bits, d_model, hidden, dtype=np.float16)
+    w2 = palette_matrix(rng, bits, hidden, d_model, dtype=np.float16)
+    return FeedForwardBlock(x, w1, w2)
+
+
+def gemm_case(seed: int, rows: int, inner: int, columns: int, bits: int, *, dtype=np.float16,
+              groups: int = 1, activation: str = "none", bias: bool = False,
+              residual_scale: float | None = None, a_std: float = 1.0) -> GemmCase:
+    """A generic seeded palette GEMM for parity sweeps."""
+    rng = np.random.default_rng(seed)
+    a = normal(rng, (rows, inner), a_std, dtype)
+    w = palette_matrix(rng, bits, inner, columns, dtype=dtype, groups=groups)
+    b = normal(rng, (columns,), 0.01, np.float32) if bias else None
+    r = normal(rng, (rows, columns), 1.0, dtype) if residual_scale is not None else None
+    return GemmCase(f"gemm-{rows}x{inner}x{columns}-b{bits}", a, w, bias=b, residual=r,
+                    residual_scale=residual_scale, activation=activation)

@@ -1,0 +1,328 @@
+"""Pins for the CPU oracle (oracle/pk_oracle.c) before it is trusted as the
+checker of the HIP kernels.
+
+Each check is independent of the formula it pins: the reference's own
+known-answer vectors, Python big-integer bit arithmetic, numpy's binary16
+conversion, exact integer arithmetic, closed forms and brute force.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def kats():
+    with open(os.path.join(GOLDEN, "palette_kats.json")) as f:
+        return json.load(f)
+
+
+def big_int_codes(words, bits, count):
+    """Decode a group through one little-endian Python integer."""
+    value = 0
+    for q, w in enumerate(words):
+        value |= int(w) << (32 * q)
+    mask = (1 << bits) - 1
+    return [(value >> (i * bits)) & mask for i in range(count)]
+
+
+# ---------------------------------------------------------------- packing
+
+
+@pytest.mark.parametrize("case", range(2))
+def test_pack_matches_reference_known_answers(oracle, case):
+    """model/tests/test_convert.py:447-479."""
+    kat = kats()["pack_lsb"][case]
+    codes = np.array(kat["codes"], dtype=np.uint8)
+    words = oracle.pack_codes(codes, kat["bits"])
+    assert words.dtype == np.dtype("<u4")
+    assert words.shape == (1, len(kat["words"]))
+    assert [int(w) for w in words[0]] == kat["words"]
+    assert words[0, 0].tobytes() == int(kat["words"][0]).to_bytes(4, "little")
+    np.testing.assert_array_equal(oracle.unpack_codes(words, kat["bits"]), codes)
+
+
+@pytest.mark.parametrize("bits", [5, 6])
+def test_unpack_matches_big_integer_bit_positions(oracle, bits):
+    rng = np.random.default_rng(bits)
+    cpg = oracle.codes_per_group(bits)
+    words = rng.integers(0, 2**32, size=(500, oracle.words_per_group(bits)), dtype=np.uint64).astype("<u4")
+    codes = oracle.unpack_codes(words, bits).reshape(-1, cpg)
+    for g in range(words.shape[0]):
+        assert list(codes[g]) == big_int_codes(words[g], bits, cpg)
+
+
+@pytest.mark.parametrize("bits", [5, 6])
+def test_every_code_position_and_value_round_trips(oracle, bits):
+    cpg = oracle.codes_per_group(bits)
+    for position in range(cpg):
+        for value in range(1 << bits):
+            codes = np.zeros(cpg, dtype=np.uint8)
+            codes[position] = value
+            words = oracle.pack_codes(codes, bits)
+            assert big_int_codes(words[0], bits, cpg) == list(codes)
+            np.testing.assert_array_equal(oracle.unpack_codes(words, bits), codes)
+
+
+@pytest.mark.parametrize("bits,straddlers", [(5, [6, 12, 19, 25]), (6, [5, 10])])
+def test_word_straddling_codes(oracle, bits, straddlers):
+    """Codes whose bits cross a u32 boundary keep their high bits in the next
+    word (convert.py:2152-2155)."""
+    cpg = oracle.codes_per_group(bits)
+    assert [i for i in range(cpg) if (i * bits) % 32 + bits > 32] == straddlers
+    full = np.full(cpg, (1 << bits) - 1, dtype=np.uint8)
+    words = oracle.pack_codes(full, bits)
+    assert all(int(w) == 0xFFFFFFFF for w in words[0])  # 160 or 96 bits, all used
+
+
+@pytest.mark.parametrize("bits", [5, 6])
+def test_random_round_trip(oracle, bits):
+    rng = np.random.default_rng(10 + bits)
+    codes = rng.integers(0, 1 << bits, size=64 * 96, dtype=np.uint8)
+    np.testing.assert_array_equal(oracle.unpack_codes(oracle.pack_codes(codes, bits), bits), codes)
+
+
+def test_pack_rejects_out_of_range_and_unaligned(oracle):
+    with pytest.raises(ValueError):
+        oracle.pack_codes(np.array([32] + [0] * 31, dtype=np.uint8), 5)
+    with pytest.raises(ValueError):
+        oracle.pack_codes(np.zeros(31, dtype=np.uint8), 5)
+
+
+def test_k_major_output_group_fixture(oracle):
+    """model/tests/test_convert.py:481-511: the codes of a [K, N] matrix are
+    flattened k outer, n inner, across palette groups."""
+    fx = kats()["k_major_output_groups"]
+    codes = np.array(fx["expected_codes"], dtype=np.uint8)
+    words = oracle.pack_codes(codes, fx["bits"])
+    assert list(words.shape) == fx["packed_shape"]
+    unpacked = oracle.unpack_codes(words, fx["bits"])
+    dense = np.array(fx["dense"])
+    palettes = np.array(fx["palettes"])
+    k, n = dense.shape
+    width = fx["output_group_width"]
+    for kk in range(k):
+        for nn in range(n):
+            assert palettes[nn // width][unpacked[kk * n + nn]] == dense[kk, nn]
+
+
+# ---------------------------------------------------------------- binary16
+
+
+def test_f16_rounding_every_value_and_midpoint(oracle):
+    all_bits = np.arange(0x10000, dtype=np.uint16)
+    values = all_bits.view(np.float16)
+    finite = np.isfinite(values)
+    for b in all_bits[finite][::7]:
+        v = float(np.uint16(b).view(np.float16))
+        assert oracle.f64_to_f16_bits(v) == int(b)
+        assert oracle.f16_bits_to_f64(int(b)) == v
+    # midpoints and their neighbours, against numpy's round-to-nearest-even
+    pos = values[finite & (values >= 0)].astype(np.float64)
+    pos = np.sort(pos)
+    mids = (pos[:-1] + pos[1:]) / 2
+    probes = np.concatenate([mids, np.nextafter(mids, 0), np.nextafter(mids, np.inf)])
+    probes = np.concatenate([probes, -probes, [65519.0, 65520.0, 70000.0, 2.0**-25, 2.0**-26, 3 * 2.0**-26]])
+    for p in probes[::5]:
+        assert oracle.f64_to_f16_bits(p) == int(np.float16(p).view(np.uint16)), p
+
+
+# ---------------------------------------------------------------- geometry
+
+
+def test_palette_group_closed_form(oracle):
+    for groups, group_columns in [(1, 4096), (3, 1024), (4, 16)]:
+        for n in range(0, groups * group_columns, 7):
+            assert oracle.palette_group(n, group_columns, groups) == min(n // group_columns, groups - 1)
+
+
+@pytest.mark.parametrize("tile_columns,columns", [(256, 512), (128, 256)])
+def test_tile_major_index_is_a_tile_contiguous_bijection(oracle, tile_columns, columns):
+    """runtime-plan.ts:454-490 and the invariants of
+    test/model/palette-expander.test.ts:147-247."""
+    inner = 64
+    seen = np.zeros(inner * columns, dtype=bool)
+    for s in range(inner * columns):
+        p = oracle.tile_major_index(s, inner, columns, tile_columns)
+        assert not seen[p]
+        seen[p] = True
+        k, n = divmod(s, columns)
+        tile = (n // tile_columns) * (inner // 32) + k // 32
+        assert tile * 32 * tile_columns <= p < (tile + 1) * 32 * tile_columns
+        if s % 4 == 0:
+            assert p % 4 == 0
+    assert seen.all()
+
+
+# ---------------------------------------------------------------- expansion
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("bits,groups,columns", [(5, 1, 256), (5, 3, 768), (6, 1, 256), (6, 4, 512)])
+def test_expand_one_hot_palette_recovers_codes(oracle, dtype, bits, groups, columns):
+    rng = np.random.default_rng(bits * 10 + groups)
+    inner = 64
+    codes = rng.integers(0, 1 << bits, size=(inner, columns), dtype=np.uint8)
+    words = oracle.pack_codes(codes, bits)
+    entries = 1 << bits
+    palette = (100 * np.arange(groups)[:, None] + np.arange(entries)[None, :]).astype(dtype)
+    dense = oracle.expand(words, bits, inner, columns, palette)
+    group_of = np.minimum(np.arange(columns) // (columns // groups), groups - 1)
+    np.testing.assert_array_equal(dense, (100 * group_of[None, :] + codes).astype(dtype))
+    if columns % (256 if dtype == np.float16 else 128) == 0:
+        tiled = oracle.expand(words, bits, inner, columns, palette, tile_major=True)
+        tile_columns = 256 if dtype == np.float16 else 128
+        for s in range(0, inner * columns, 97):
+            assert tiled[oracle.tile_major_index(s, inner, columns, tile_columns)] == dense.reshape(-1)[s]
+
+
+# ---------------------------------------------------------------- GEMM
+
+
+def _case(rng, rows, inner, columns, bits, dtype, groups=1, int_values=False):
+    codes = rng.integers(0, 1 << bits, size=(inner, columns), dtype=np.uint8)
+    if int_values:
+        a = rng.integers(-2, 3, size=(rows, inner)).astype(dtype)
+        palette = rng.integers(-3, 4, size=(groups, 1 << bits)).astype(dtype)
+    else:
+        a = rng.standard_normal((rows, inner)).astype(dtype)
+        palette = (rng.standard_normal((groups, 1 << bits)) * 0.02).astype(dtype)
+    return a, codes, palette
+
+
+def _dense(codes, palette):
+    groups = palette.shape[0]
+    columns = codes.shape[1]
+    g = np.minimum(np.arange(columns) // (columns // groups), groups - 1)
+    return palette[g[None, :], codes].astype(np.float64)
+
+
+@pytest.mark.parametrize("bits,groups", [(5, 1), (6, 3)])
+def test_gemm_exact_on_integer_inputs(oracle, bits, groups):
+    """Small integers keep every product and partial sum exact in binary16,
+    so all three modes equal the integer matmul; the non-square shape
+    catches transposed operands and the integer result any dropped term or
+    wrong sign."""
+    rng = np.random.default_rng(7)
+    rows, inner, columns = 5, 64, 96
+    a, codes, palette = _case(rng, rows, inner, columns, bits, np.float16, groups, int_values=True)
+    words = oracle.pack_codes(codes, bits)
+    want = a.astype(np.float64) @ _dense(codes, palette)
+    for mode in ["f16-chain", "f32-chain", "f64"]:
+        got = oracle.gemm(a, words, bits, palette, columns, mode=mode)
+        np.testing.assert_array_equal(got.astype(np.float64), want, err_msg=mode)
+
+
+def test_gemm_constant_palette_is_row_sum(oracle):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((7, 128)).astype(np.float32)
+    codes = rng.integers(0, 32, size=(128, 64), dtype=np.uint8)
+    palette = np.full((1, 32), 0.375, dtype=np.float32)
+    got = oracle.gemm(a, oracle.pack_codes(codes, 5), 5, palette, 64, mode="f64")
+    want = 0.375 * a.astype(np.float64).sum(axis=1, keepdims=True)
+    np.testing.assert_allclose(got, np.broadcast_to(want, got.shape), rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_brute_force_tiny(oracle):
+    rng = np.random.default_rng(11)
+    rows, inner, columns, bits = 3, 32, 32, 5
+    a, codes, palette = _case(rng, rows, inner, columns, bits, np.float32)
+    words = oracle.pack_codes(codes, bits)
+    # decode through big integers, independent of the oracle's unpack
+    flat = []
+    for g in range(words.shape[0]):
+        flat += big_int_codes(words[g], bits, 32)
+    w = [[float(palette[0][flat[k * columns + n]]) for n in range(columns)] for k in range(inner)]
+    got = oracle.gemm(a, words, bits, palette, columns, mode="f64")
+    for m in range(rows):
+        for n in range(columns):
+            s = 0.0
+            for k in range(inner):
+                s += float(a[m, k]) * w[k][n]
+            assert abs(got[m, n] - s) <= 1e-12 * max(1.0, abs(s))
+
+
+def test_f16_chain_is_one_rounding_per_step(oracle):
+    """Increasing-k binary16 accumulator with a fused multiply-add
+    (gemm.ts:1445-1453): emulate it with numpy's float64->float16 rounding."""
+    rng = np.random.default_rng(5)
+    rows, inner, columns, bits = 2, 64, 32, 5
+    a, codes, palette = _case(rng, rows, inner, columns, bits, np.float16)
+    words = oracle.pack_codes(codes, bits)
+    w = _dense(codes, palette)
+    got = oracle.gemm(a, words, bits, palette, columns, mode="f16-chain")
+    for m in range(rows):
+        for n in range(columns):
+            acc = np.float16(0.0)
+            for k in range(inner):
+                acc = np.float16(np.float64(a[m, k]) * w[k, n] + np.float64(acc))
+            assert got[m, n].view(np.uint16) == acc.view(np.uint16)
+
+
+def test_f32_chain_is_increasing_k_fma(oracle):
+    rng = np.random.default_rng(6)
+    rows, inner, columns, bits = 2, 64, 32, 6
+    a, codes, palette = _case(rng, rows, inner, columns, bits, np.float32)
+    words = oracle.pack_codes(codes, bits)
+    w = _dense(codes, palette)
+    got = oracle.gemm(a, words, bits, palette, columns, mode="f32-chain")
+    for m in range(rows):
+        for n in range(columns):
+            acc = np.float32(0.0)
+            for k in range(inner):
+                acc = np.float32(np.float64(a[m, k]) * w[k, n] + np.float64(acc))
+            assert got[m, n] == acc
+
+
+def test_epilogue_order_and_closed_forms(oracle):
+    """bias -> activation -> residual + scale * value (gemm.ts:2006-2044)."""
+    rng = np.random.default_rng(9)
+    rows, inner, columns, bits = 4, 64, 64, 5
+    a, codes, palette = _case(rng, rows, inner, columns, bits, np.float32)
+    words = oracle.pack_codes(codes, bits)
+    plain = oracle.gemm(a, words, bits, palette, columns, mode="f64")
+    bias = (rng.standard_normal(columns) * 0.5).astype(np.float32)
+    residual = rng.standard_normal((rows, columns)).astype(np.float32)
+
+    def silu(v):
+        b = np.clip(v, -20, 20)
+        return v / (1 + np.exp(-b))
+
+    got = oracle.gemm(a, words, bits, palette, columns, bias=bias, activation="silu", mode="f64")
+    np.testing.assert_allclose(got, silu(plain + bias), rtol=1e-12, atol=1e-14)
+    got = oracle.gemm(a, words, bits, palette, columns, bias=bias, activation="relu", mode="f64")
+    np.testing.assert_allclose(got, np.maximum(plain + bias, 0), rtol=1e-12, atol=1e-14)
+    got = oracle.gemm(a, words, bits, palette, columns, residual=residual, residual_scale=0.5,
+                      activation="silu", mode="f64")
+    np.testing.assert_allclose(got, residual + 0.5 * silu(plain), rtol=1e-12, atol=1e-14)
+    # the bias must act before the activation: a large negative bias zeroes relu
+    got = oracle.gemm(a, words, bits, palette, columns, bias=np.full(columns, -1e3, np.float32),
+                      activation="relu", mode="f64")
+    assert np.all(got == 0)
+    # the f32 epilogue matches the double one to f32 precision
+    got32 = oracle.gemm(a, words, bits, palette, columns, residual=residual, residual_scale=1.0,
+                        activation="silu", mode="f32-chain")
+    np.testing.assert_allclose(got32, residual + silu(plain), rtol=1e-5, atol=1e-6)
+
+
+def test_silu_clamps_its_exponent(oracle):
+    """SiLU evaluates exp(-clamp(v, -20, 20)) (gemm.ts:2020-2026): for very
+    negative v it is v/(1+e^20), not the exact ~0."""
+    rows, inner, columns = 1, 32, 32
+    a = np.ones((rows, inner), dtype=np.float32)
+    codes = np.zeros((inner, columns), dtype=np.uint8)
+    palette = np.zeros((1, 32), dtype=np.float32)
+    palette[0, 0] = -2.0  # every output = -64
+    got = oracle.gemm(a, oracle.pack_codes(codes, 5), 5, palette, columns, activation="silu", mode="f64")
+    np.testing.assert_allclose(got, -64.0 / (1 + np.exp(20.0)), rtol=1e-12)
+
+
+def test_threads_do_not_change_results(oracle):
+    rng = np.random.default_rng(2)
+    a, codes, palette = _case(rng, 37, 96, 64, 6, np.float16)
+    words = oracle.pack_codes(codes, 6)
+    one = oracle.gemm(a, words, 6, palette, 64, mode="f16-chain", threads=1)
+    many = oracle.gemm(a, words, 6, palette, 64, mode="f16-chain", threads=5)
+    np.testing.assert_array_equal(one.view(np.uint16), many.view(np.uint16))
