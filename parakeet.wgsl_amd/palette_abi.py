@@ -264,7 +264,7 @@ class Context:
         return DeviceArray(self, host.shape, host.dtype).upload(host)
 
     def empty(self, shape, dtype) -> DeviceArray:
-        return DeviceArray(self, tuple(shape), dtype)
+        return DeviceArray(self, shape, dtype)
 
     def synchronize(self, stream=None) -> None:
         check(load().pk_stream_synchronize(self.handle, stream))
