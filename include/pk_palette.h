@@ -197,10 +197,14 @@ int pk_gemm_destroy(pk_gemm_op *op);
 /* Destroys (if needed) and frees the handle; it must not be used again. */
 int pk_gemm_release(pk_gemm_op *op);
 
-/* Tuning hooks: the planner picks a compiled tile shape at create time;
-   these list and force the choice (used by the benchmark's sweeps). */
+/* Tuning hooks: the planner picks a compiled tile shape and a split-K
+   factor at create time; these list and force the choice (used by the
+   benchmark's sweeps). Both resize the op's split-K workspace and must not
+   be called while a launch of the op is in flight. */
 int pk_gemm_variant_count(int precision);
 int pk_gemm_set_variant(pk_gemm_op *op, int variant);
+/* 1 <= splits <= ceil(inner / 64) for f16; f32 ops take 1 only. */
+int pk_gemm_set_splits(pk_gemm_op *op, uint32_t splits);
 
 typedef struct pk_gemm_plan_info {
   uint32_t grid[3];
@@ -209,6 +213,7 @@ typedef struct pk_gemm_plan_info {
   uint32_t tile_columns;
   uint32_t split_inner;          /* K slices reduced in-kernel (1 = none) */
   uint32_t lds_bytes;
+  uint64_t workspace_bytes;      /* split-K partial tiles + tile counters */
   uint64_t flops;                /* 2*M*K*N for active rows */
   uint64_t algorithmic_bytes;    /* compulsory HBM bytes per launch */
   char kernel[64];

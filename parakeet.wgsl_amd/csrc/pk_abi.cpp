@@ -2,6 +2,7 @@
 // the reference's descriptor contract checks and launch planning.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -99,6 +100,10 @@ struct pk_gemm_op {
   pk::GemmArgs args{};
   pk_prepared_weight* weight = nullptr;
   int variant = 0;
+  uint32_t splits = 1;
+  // Split-K workspace: f32 partial tiles, then one counter per tile.
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
   bool destroyed = false;
 };
 
@@ -164,38 +169,109 @@ int check_packed(const char* label, int bits, uint32_t inner, uint32_t columns, 
   return PK_OK;
 }
 
-// Tile planner: pick the compiled tile shape whose grid best fills the 256
-// compute units, weighting smaller wavefront tiles by their extra decode and
-// LDS traffic per MFMA.
-int plan_variant(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
-  const bool f16 = precision == PK_PRECISION_F16;
-  const int count = f16 ? pk::f16_variant_count() : pk::f32_variant_count();
-  const uint32_t n_pad = pk::padded_columns(columns);
-  int best = 0;
+pk::TileShape shape_of(int precision, int variant) {
+  return precision == PK_PRECISION_F16 ? pk::f16_variant(variant) : pk::f32_variant(variant);
+}
+
+uint32_t k_blocks(uint32_t inner) { return (inner + 63u) / 64u; }
+
+// Split-K workspace: `splits` f32 partial tiles per output tile, then one
+// u32 arrival counter per output tile (256-byte aligned).
+uint64_t workspace_bytes_for(const pk::TileShape& s, uint32_t rows, uint32_t columns, uint32_t splits) {
+  if (splits <= 1) return 0;
+  const uint64_t tiles = (uint64_t)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
+  const uint64_t partial = tiles * splits * s.tile_elements() * 4u;
+  return (partial + 255u) / 256u * 256u + tiles * 4u;
+}
+
+// Launch cost model of the planner, in units of one MFMA-block K step on
+// one SIMD. A workgroup runs tile_rows x tile_columns over its K range; its
+// wavefronts are slowed by the LDS traffic per MFMA (decoded weight
+// fragments are gathered from the LDS palette, activation fragments are
+// read from the LDS tile), workgroups beyond one per compute unit run in
+// further rounds, and split-K adds its partial-tile round trip.
+double plan_cost(int precision, const pk::TileShape& s, uint32_t rows, uint32_t inner, uint32_t columns,
+                 uint32_t splits, int cus) {
+  const double tiles = (double)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
+  const double groups = tiles * splits;
+  const double rounds = std::ceil(groups / cus);
+  const double kb = std::ceil((double)k_blocks(inner) / splits);
+  const double blocks = (double)s.m_blocks * s.n_blocks;
+  double lds;
+  if (precision == PK_PRECISION_F16)
+    lds = 1.0 / s.m_blocks + 0.5 / s.n_blocks;  // per MFMA, relative to its duration
+  else
+    lds = 0.25 / s.m_blocks + 0.125 / s.n_blocks;
+  const double per_step = blocks * std::max(1.0, 0.6 + lds);
+  double cost = rounds * kb * per_step;
+  if (splits > 1) {
+    // Partial tiles written and read back: 8 bytes per output element and
+    // split, against ~64 bytes/clock/CU of cache bandwidth, in MFMA-block
+    // K steps (32 x 32 x 64 MACs).
+    const double bytes = tiles * splits * s.tile_elements() * 8.0;
+    cost += bytes / (64.0 * cus) / 128.0;
+  }
+  return cost;
+}
+
+struct Plan {
+  int variant;
+  uint32_t splits;
+};
+
+Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
+  const int count = precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
+  const uint32_t max_splits = precision == PK_PRECISION_F16 ? std::min(8u, k_blocks(inner)) : 1u;
+  Plan best{0, 1};
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
-    const pk::TileShape s = f16 ? pk::f16_variant(i) : pk::f32_variant(i);
-    const double tiles = (double)((rows + s.tile_rows() - 1) / s.tile_rows()) *
-                         (double)((n_pad + s.tile_columns() - 1) / s.tile_columns());
-    // Workgroups resident per CU: one for the large tiles, up to four when a
-    // tile leaves room (registers and LDS), as measured by occupancy.
-    const int waves = s.waves_m * s.waves_n;
-    const int per_wave_acc = s.m_blocks * s.n_blocks * 16;
-    int resident = per_wave_acc >= 192 ? 1 : per_wave_acc >= 96 ? 2 : 4;
-    if (waves * resident > 16) resident = 16 / waves;
-    if (resident < 1) resident = 1;
-    const double rounds = std::ceil(tiles / ((double)cus * resident));
-    const double work = (double)s.tile_rows() * s.tile_columns() * resident;
-    const double overhead = f16 ? (1.0 + 1.0 / s.m_blocks + 0.5 / (s.n_blocks * s.waves_n / s.waves_m))
-                                : (1.0 + 0.25 / s.m_blocks);
-    const double cost = rounds * work * overhead / resident;
-    if (cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = i;
+    const pk::TileShape s = shape_of(precision, i);
+    for (uint32_t sp = 1; sp <= max_splits; ++sp) {
+      const double cost = plan_cost(precision, s, rows, inner, columns, sp, cus);
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best = {i, sp};
+      }
     }
   }
-  (void)inner;
   return best;
+}
+
+// Applies a (variant, splits) choice: resizes the split-K workspace for the
+// op's row capacity and zeroes its counters.
+int configure_launch(pk_gemm_op* op, int variant, uint32_t splits) {
+  const pk::TileShape s = shape_of(op->precision, variant);
+  const uint64_t need = workspace_bytes_for(s, op->rows, op->args.columns, splits);
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  if (need != op->workspace_bytes) {
+    if (op->workspace) {
+      PK_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+      PK_HIP(hipFree(op->workspace), "hipFree");
+      op->workspace = nullptr;
+      op->workspace_bytes = 0;
+    }
+    if (need) {
+      const hipError_t e = hipMalloc(&op->workspace, need);
+      if (e != hipSuccess)
+        return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of split-K workspace: %s",
+                    op->label.c_str(), (unsigned long long)need, hipGetErrorString(e));
+      op->workspace_bytes = need;
+    }
+  }
+  if (op->workspace) {
+    const uint64_t tiles = (uint64_t)pk::tiles_m(s, op->rows) * pk::tiles_n(s, op->args.columns);
+    const uint64_t counters_at = need - tiles * 4u;
+    PK_HIP(hipMemset(static_cast<uint8_t*>(op->workspace) + counters_at, 0, tiles * 4u), "hipMemset");
+    op->args.partials = static_cast<float*>(op->workspace);
+    op->args.counters = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(op->workspace) + counters_at);
+  } else {
+    op->args.partials = nullptr;
+    op->args.counters = nullptr;
+  }
+  op->variant = variant;
+  op->splits = splits;
+  op->args.splits = splits;
+  return PK_OK;
 }
 
 }  // namespace
@@ -546,7 +622,13 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   int cus = 256;
   if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
     cus = prop.multiProcessorCount;
-  op->variant = plan_variant(d->precision, d->rows, d->inner, d->columns, cus);
+  a.splits = 1;
+  const Plan plan = plan_launch(d->precision, d->rows, d->inner, d->columns, cus);
+  if (int st = configure_launch(op, plan.variant, plan.splits)) {
+    weight_unref(op->weight);
+    delete op;
+    return st;
+  }
   *out = op;
   return ok();
 }
@@ -560,6 +642,8 @@ int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
     return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
   pk::GemmArgs args = op->args;
   args.rows = rows;
+  // A split never gets an empty K range.
+  args.splits = std::min(op->splits, k_blocks(op->args.inner));
   hipStream_t st = stream_or_default(op->ctx, stream);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
   const hipError_t e = op->precision == PK_PRECISION_F16
@@ -574,6 +658,13 @@ int pk_gemm_destroy(pk_gemm_op* op) {
   op->destroyed = true;
   weight_unref(op->weight);
   op->weight = nullptr;
+  if (op->workspace) {
+    (void)hipSetDevice(op->ctx->device);
+    (void)hipStreamSynchronize(op->ctx->stream);
+    (void)hipFree(op->workspace);
+    op->workspace = nullptr;
+    op->workspace_bytes = 0;
+  }
   return ok();
 }
 
@@ -587,10 +678,19 @@ int pk_gemm_release(pk_gemm_op* op) {
 int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
   const int count = op->precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
   if (variant < 0 || variant >= count)
     return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
-  op->variant = variant;
-  return ok();
+  return configure_launch(op, variant, op->splits);
+}
+
+int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  const uint32_t limit = op->precision == PK_PRECISION_F16 ? k_blocks(op->args.inner) : 1u;
+  if (splits < 1 || splits > limit)
+    return fail(PK_RANGE_ERROR, "%s split count %u outside [1, %u]", op->label.c_str(), splits, limit);
+  return configure_launch(op, op->variant, splits);
 }
 
 int pk_gemm_variant_count(int precision) {
@@ -606,16 +706,22 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   const bool f16 = op->precision == PK_PRECISION_F16;
   const pk::TileShape s = f16 ? pk::f16_variant(op->variant) : pk::f32_variant(op->variant);
   std::memset(info, 0, sizeof *info);
-  const uint32_t n_pad = pk::padded_columns(op->args.columns);
-  info->grid[0] = (n_pad + s.tile_columns() - 1) / s.tile_columns();
-  info->grid[1] = (rows + s.tile_rows() - 1) / s.tile_rows();
+  const uint32_t splits = std::min(op->splits, k_blocks(op->args.inner));
+  if (f16) {
+    info->grid[0] = pk::tiles_m(s, rows) * pk::tiles_n(s, op->args.columns) * splits;
+    info->grid[1] = 1;
+  } else {
+    info->grid[0] = pk::tiles_n(s, op->args.columns);
+    info->grid[1] = pk::tiles_m(s, rows);
+  }
   info->grid[2] = 1;
   info->block_threads = s.threads();
   info->tile_rows = s.tile_rows();
   info->tile_columns = s.tile_columns();
-  info->split_inner = 1;
+  info->split_inner = splits;
+  info->workspace_bytes = op->workspace_bytes;
   const uint32_t elem = f16 ? 2u : 4u;
-  const uint32_t lut_cap = (s.tile_columns() / 16u + 2u) * (1u << op->bits);
+  const uint32_t lut_cap = (s.tile_columns() / pk::codes_per_group(op->bits) + 1u) * (1u << op->bits);
   info->lds_bytes = 2u * s.tile_rows() * (f16 ? 128u : 256u) + lut_cap * elem;
   const uint64_t M = rows, K = op->args.inner, N = op->args.columns;
   info->flops = 2ull * M * K * N;

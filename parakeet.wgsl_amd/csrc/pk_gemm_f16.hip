@@ -3,34 +3,47 @@
 //
 // C[m, n] = epilogue(sum_k A[m, k] * LUT[g(n)][code(k, n)])
 //
-// The dense weight is never materialised. Per 64-deep K step a wavefront
-//   * fetches, for each of its 32-column blocks, the block's codes in MFMA
-//     operand order (one 128-bit + one 32/64-bit coalesced load per lane),
-//   * decodes the 32 codes of its lane with v_bfe_u32 / v_alignbit_b32 and
-//     gathers them from the palette staged in LDS straight into the 8-half
-//     operand registers of v_mfma_f32_32x32x16_f16,
-//   * reads its activation fragments from an LDS tile (double buffered,
-//     16-byte chunks XOR-swizzled by row so 8 consecutive rows hit 8
-//     different bank groups),
-//   * issues m_blocks x n_blocks MFMAs per 16-deep sub-step.
-// The MFMA computes D = W^T * A^T (weights as the 32x16 "A" operand), so a
-// lane ends with 4 runs of 4 consecutive output columns of one row: the
-// epilogue (bias -> activation -> residual + scale * value, gemm.ts:2006-2044)
-// runs in f32 and stores 8 bytes per run.
-//
+// The dense weight is never materialised. A workgroup of WM x WN wavefronts
+// owns a BM x BN output tile (BM = 32*R*WM, BN = 32*C*WN); each wavefront owns
+// R x C MFMA blocks of 32 x 32 and walks K in 64-deep blocks:
+//   * codes: per 32-column block one coalesced 16-byte + one 4/8-byte load
+//     per lane of the operand-order stream (pk_internal.h), two K blocks
+//     ahead;
+//   * activations: the BM x 64 f16 tile of K block i+3 is loaded into
+//     registers while block i is multiplied, and written to a double
+//     buffered LDS tile at the end of block i+2. Its 16-byte chunks are
+//     XOR-swizzled with (row >> 1) & 7, which keeps the 16 lanes of each
+//     ds_read_b128 phase on distinct LDS banks (64 banks of 4 bytes);
+//   * decode: each lane cuts the 8 codes of a 16-deep sub-step out of its
+//     code words (shift/mask, v_alignbit_b32 across words) and gathers them
+//     from the palette staged in LDS straight into the 8 halves of the MFMA
+//     operand. When a tile lies inside one palette group the palette sits at
+//     a fixed LDS address, so the gather address is the code alone. The
+//     fragment of sub-step s+1 is gathered while the MFMAs of s run;
+//   * v_mfma_f32_32x32x16_f16 computes D = W^T * A^T (weights as the 32 x 16
+//     "A" operand, activations as "B"), so a lane ends with 4 runs of 4
+//     consecutive output columns of one row; the epilogue regroups the tile
+//     through LDS into 16-byte row chunks for the global stores.
 // K-slot pairing: in sub-step s, lane half h, operand element t stands for
 // k = 64*kb + 32*h + 8*s + t in BOTH operands, so the hardware's own pairing
-// of A and B slots always multiplies matching k.
+// of A and B slots always multiplies matching k. The main loop is unrolled
+// by three so the rotating register sets are fixed registers: no copy ever
+// waits on a load that is still in flight.
+//
+// Epilogue (src/webgpu/kernels/gemm.ts:2006-2044): f32 value, + bias[n],
+// SiLU v/(1+exp(-clamp(v,-20,20))) or ReLU, then residual + scale * value,
+// rounded to f16.
 #include "pk_internal.h"
 
 namespace pk {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Code u (0..31) of a lane's 32-code stream, LSB first at bit u*BITS.
 template <int BITS>
-__device__ __forceinline__ uint32_t lane_code(const uint32_t* w, int u) {
+__device__ __forceinline__ uint32_t lane_code(const uint32_t (&w)[BITS], int u) {
   constexpr uint32_t mask = (1u << BITS) - 1u;
   const int bit = u * BITS;
   const int word = bit >> 5;
@@ -39,28 +52,49 @@ __device__ __forceinline__ uint32_t lane_code(const uint32_t* w, int u) {
   return __builtin_amdgcn_alignbit(w[word + 1], w[word], shift) & mask;
 }
 
+// The 8 weights of sub-step s: palette entries gathered from LDS.
+template <int BITS>
+__device__ __forceinline__ half8 decode_fragment(const uint32_t (&w)[BITS], int s,
+                                                 const _Float16* lut) {
+  half8 f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) f[t] = lut[lane_code<BITS>(w, s * 8 + t)];
+  return f;
+}
+
 __device__ __forceinline__ float silu(float v) {
   const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
   return v / (1.0f + expf(-bounded));
 }
 
-template <int BITS, int WM, int WN, int MB, int NB>
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// GENERAL: the tile's columns may span several palette groups (per-lane
+// palette base) and K may be 32 (mod 64). Otherwise (the common case) the
+// tile's one palette sits at a fixed LDS address and K is a multiple of 64.
+template <int BITS, int WM, int WN, int R, int C, bool GENERAL>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_kernel(GemmArgs args) {
   constexpr int T = 64 * WM * WN;
-  constexpr int BM = 32 * WM * MB;
-  constexpr int BN = 32 * WN * NB;
+  constexpr int BM = 32 * R * WM;
+  constexpr int BN = 32 * C * WN;
   constexpr int E = 1 << BITS;
-  constexpr int LUT_CAP = (BN / 16 + 2) * E;
-  constexpr int ROW_BYTES = 128;  // 64 halves of one row per K step
-  constexpr int CH = BM * 8 / T;  // 16-byte A chunks per thread per K step
-  static_assert(BM * 8 % T == 0, "A tile chunks must divide evenly");
+  constexpr int CPG = (int)codes_per_group(BITS);
+  constexpr int LUT_CAP = GENERAL ? (BN / CPG + 2) * E : E;
+  constexpr int ROW_BYTES = 128;  // 64 halves of one row per K block
+  constexpr int CH = BM * 8 / T;  // 16-byte activation chunks per thread per K block
+  constexpr uint32_t BW = block_words(BITS);
+  static_assert(BM * 8 % T == 0, "activation tile chunks must divide evenly");
 
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2 * BM * ROW_BYTES];
   __shared__ _Float16 lut_lds[LUT_CAP];
+  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wave_m = wave / WN;
   const int wave_n = wave % WN;
   const int j = lane & 31;
@@ -69,184 +103,352 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_kernel(GemmArgs args) {
   const uint32_t M = args.rows;
   const uint32_t K = args.inner;
   const uint32_t N = args.columns;
-  const uint32_t k_blocks = (K + 63u) / 64u;
-  const uint32_t n_blocks_total = (N + 31u) / 32u;
-  const uint32_t n0 = blockIdx.x * BN;
-  const uint32_t m0 = blockIdx.y * BM;
+  const uint32_t KB = (K + 63u) / 64u;
+  const uint32_t NBT = (N + 31u) / 32u;
+  const uint32_t S = args.splits;
+  const uint32_t TN = (NBT * 32u + BN - 1u) / BN;
+
+  // Work item: split fastest, then column tile, then row tile, laid out so
+  // that the workgroups of one XCD take consecutive items.
+  uint32_t item = xcd_local_order(blockIdx.x, gridDim.x);
+  const uint32_t split = item % S;
+  item /= S;
+  const uint32_t tile = item;
+  const uint32_t tn = item % TN;
+  const uint32_t tm = item / TN;
+  const uint32_t m0 = tm * BM;
+  const uint32_t n0 = tn * BN;
+  const uint32_t kb_begin = split * KB / S;
+  const uint32_t kb_end = (split + 1u) * KB / S;
+  const uint32_t steps = kb_end - kb_begin;
+  // K = 32 (mod 64): the last K block is half padding.
+  const bool tail_block = (K & 63u) != 0u && kb_end == KB;
 
   // Palette window of this tile's columns (palette-expander.ts:543-549).
+  // GENERAL kernels also keep E zero entries after the staged palettes:
+  // lanes gathering padded k of a K = 32 (mod 64) tail read weights from
+  // there.
   const uint32_t gc = args.palette_group_columns;
   const uint32_t G = args.palette_groups;
   const uint32_t g_lo = min(n0 / gc, G - 1u);
-  const uint32_t g_hi = min((min(n0 + BN, N) - 1u) / gc, G - 1u);
   {
+    const uint32_t g_hi = GENERAL ? min((min(n0 + BN, N) - 1u) / gc, G - 1u) : g_lo;
     const uint32_t entries = (g_hi - g_lo + 1u) * E;
     const _Float16* src = static_cast<const _Float16*>(args.palette) + (uint64_t)g_lo * E;
     for (uint32_t i = tid; i < entries; i += T) lut_lds[i] = src[i];
+    if constexpr (GENERAL)
+      for (uint32_t i = tid; i < (uint32_t)E; i += T) lut_lds[LUT_CAP - E + i] = (_Float16)0.0f;
   }
-  const _Float16* lut_col[NB];
+  const _Float16* lut_col[C];
 #pragma unroll
-  for (int ni = 0; ni < NB; ++ni) {
-    const uint32_t n = n0 + (wave_n * NB + ni) * 32 + j;
-    const uint32_t g = min(n / gc, G - 1u) - g_lo;
-    lut_col[ni] = lut_lds + g * E;
+  for (int ci = 0; ci < C; ++ci) {
+    if constexpr (GENERAL) {
+      const uint32_t n = min(n0 + (wave_n * C + ci) * 32 + j, N - 1u);
+      lut_col[ci] = lut_lds + (min(n / gc, G - 1u) - g_lo) * E;
+    } else {
+      lut_col[ci] = lut_lds;
+    }
   }
+  const _Float16* const lut_zero = lut_lds + (LUT_CAP - E);
 
-  // Code stream of each of this wave's 32-column blocks.
-  const uint32_t nb0 = n0 / 32u + wave_n * NB;
-  uint32_t cw[NB][BITS];
-  auto load_codes = [&](uint32_t kb, uint32_t (&dst)[NB][BITS]) {
+  // Code streams of this wavefront's column blocks: a wave-uniform block
+  // base plus this lane's fixed offset. Blocks past the last column block
+  // re-read the last one (their columns are never stored), so every load is
+  // unconditional.
+  const uint32_t nb0 = n0 / 32u + wave_n * C;
+  const uint32_t* code_base[C];
 #pragma unroll
-    for (int ni = 0; ni < NB; ++ni) {
-      const uint32_t nb = nb0 + ni;
-      if (nb < n_blocks_total) {
-        const uint32_t* blk = args.codes + ((uint64_t)nb * k_blocks + kb) * block_words(BITS);
-        const uint4 p0 = reinterpret_cast<const uint4*>(blk)[lane];
-        dst[ni][0] = p0.x;
-        dst[ni][1] = p0.y;
-        dst[ni][2] = p0.z;
-        dst[ni][3] = p0.w;
-        if constexpr (BITS == 5) {
-          dst[ni][4] = blk[256 + lane];
-        } else {
-          const uint2 p1 = reinterpret_cast<const uint2*>(blk + 256)[lane];
-          dst[ni][4] = p1.x;
-          dst[ni][5] = p1.y;
-        }
+  for (int ci = 0; ci < C; ++ci)
+    code_base[ci] = args.codes + (uint64_t)min(nb0 + ci, NBT - 1u) * KB * BW;
+  auto load_codes = [&](uint32_t kb, uint32_t (&dst)[C][BITS]) {
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci) {
+      const uint32_t* blk = code_base[ci] + kb * BW;
+      const uint4 p0 = reinterpret_cast<const uint4*>(blk)[lane];
+      dst[ci][0] = p0.x;
+      dst[ci][1] = p0.y;
+      dst[ci][2] = p0.z;
+      dst[ci][3] = p0.w;
+      if constexpr (BITS == 5) {
+        dst[ci][4] = blk[256 + lane];
       } else {
-#pragma unroll
-        for (int q = 0; q < BITS; ++q) dst[ni][q] = 0u;
+        const uint2 p1 = reinterpret_cast<const uint2*>(blk + 256)[lane];
+        dst[ci][4] = p1.x;
+        dst[ci][5] = p1.y;
       }
     }
   };
 
-  // Activation tile staging: BM rows x 8 chunks of 16 bytes per K step.
-  const _Float16* a_ptr = static_cast<const _Float16*>(args.a);
-  uint4 a_stage[CH];
-  auto load_a = [&](uint32_t kb) {
+  // Activation tile: chunk c of this thread is row r = (tid + c*T) / 8,
+  // 16-byte column chunk ch = (tid + c*T) % 8, at a fixed byte offset from
+  // the wave-uniform address of (m0, 64*kb). Rows past M re-read row M-1
+  // (their results are never stored). In a K = 32 (mod 64) tail, chunks
+  // past K re-read the row's chunk ch - 4 and are stored as zeros.
+  const char* a_tile = reinterpret_cast<const char*>(static_cast<const _Float16*>(args.a) + (uint64_t)m0 * K);
+  uint32_t a_off[CH], a_st[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = tid + c * T;
+    const int r = idx >> 3, ch = idx & 7;
+    a_off[c] = ((min(m0 + (uint32_t)r, M - 1u) - m0) * K + (uint32_t)ch * 8u) * 2u;
+    a_st[c] = (uint32_t)(r * ROW_BYTES + ((ch ^ ((r >> 1) & 7)) << 4));
+  }
+  auto load_a = [&](uint32_t kb, uint4 (&dst)[CH]) {
+    const char* base = a_tile + (uint64_t)kb * 128u;
+    const bool partial = GENERAL && (K & 63u) != 0u && kb + 1u == KB;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int idx = tid + c * T;
-      const int r = idx >> 3;
-      const int ch = idx & 7;
-      const uint32_t m = m0 + r;
-      const uint32_t k = kb * 64u + ch * 8u;
-      if (m < M && k < K)
-        a_stage[c] = *reinterpret_cast<const uint4*>(a_ptr + (uint64_t)m * K + k);
-      else
-        a_stage[c] = make_uint4(0u, 0u, 0u, 0u);
+      const bool pad = partial && ((tid + c * T) & 7) >= 4;
+      dst[c] = *reinterpret_cast<const uint4*>(base + (pad ? a_off[c] - 64u : a_off[c]));
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](uint32_t kb, uint32_t buf, const uint4 (&src)[CH]) {
+    const bool partial = GENERAL && (K & 63u) != 0u && kb + 1u == KB;
+    uint8_t* dst = a_lds + buf * (BM * ROW_BYTES);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int idx = tid + c * T;
-      const int r = idx >> 3;
-      const int ch = idx & 7;
-      *reinterpret_cast<uint4*>(&a_lds[buf][r * ROW_BYTES + ((ch ^ (r & 7)) << 4)]) = a_stage[c];
+      uint4 v = src[c];
+      if (partial && ((tid + c * T) & 7) >= 4) v = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(dst + a_st[c]) = v;
     }
   };
-
-  float16v acc[MB][NB];
+  // LDS byte offset of this lane's activation fragment for sub-step s of
+  // m-block 0: row wave_m*R*32 + j, chunk 4h + s (swizzled; the swizzle of
+  // rows 32*mi + j equals that of row j).
+  uint32_t a_frag_off[4];
 #pragma unroll
-  for (int mi = 0; mi < MB; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NB; ++ni)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+  for (int s = 0; s < 4; ++s)
+    a_frag_off[s] = (uint32_t)((wave_m * R * 32 + j) * ROW_BYTES + (((4 * h + s) ^ ((j >> 1) & 7)) << 4));
 
-  load_codes(0, cw);
-  load_a(0);
-  store_a(0);
-  __syncthreads();
+  floatx16 acc[R][C];
+#pragma unroll
+  for (int mi = 0; mi < R; ++mi)
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ci][v] = 0.0f;
 
-  for (uint32_t kb = 0; kb < k_blocks; ++kb) {
-    const int buf = kb & 1;
-    const bool more = kb + 1 < k_blocks;
-    uint32_t cn[NB][BITS];
-    if (more) {
-      load_codes(kb + 1, cn);
-      load_a(kb + 1);
+  // One K block per step. Codes run two blocks ahead and activations three,
+  // in three register sets each that rotate with the step index, so the
+  // loop is unrolled by three and every set is a fixed register range.
+  // Loads past the split's last block re-read that block: every step issues
+  // the same loads, which keeps the in-order load counter waits exact.
+  //   cur: codes of block i, nx1: block i+1 (loaded a step ago), nx2:
+  //   receives block i+2; a_load receives block i+3's activations, a_store
+  //   holds block i+1's and is written to LDS at the end of the step.
+  // Weight fragments alternate between frag[0] and frag[1]: sub-step s
+  // multiplies frag[s & 1] while gathering sub-step s+1 into the other, and
+  // a step ends with the next block's first fragment in frag[0].
+  const uint32_t last_kb = kb_end - 1u;
+  half8 frag[2][C];
+  auto step = [&](uint32_t i, const uint32_t (&cur)[C][BITS], const uint32_t (&nx1)[C][BITS],
+                  uint32_t (&nx2)[C][BITS], uint4 (&a_load)[CH], const uint4 (&a_store)[CH]) {
+    load_codes(min(kb_begin + i + 2u, last_kb), nx2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(min(kb_begin + i + 3u, last_kb), a_load);
+    __builtin_amdgcn_sched_barrier(0);
+    // Palettes for the gathers of this block and of the next block's first
+    // sub-step: the zero palette for lane half 1 (k >= 32) of a tail block.
+    const _Float16* lut_this[C];
+    const _Float16* lut_next[C];
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci) {
+      lut_this[ci] = lut_col[ci];
+      lut_next[ci] = lut_col[ci];
+      if constexpr (GENERAL) {
+        if (tail_block && h) {
+          if (i + 1u == steps) lut_this[ci] = lut_zero;
+          if (i + 2u == steps) lut_next[ci] = lut_zero;
+        }
+      }
     }
-    const uint8_t* tile = a_lds[buf];
+    const uint8_t* tile_a = a_lds + (i & 1u) * (BM * ROW_BYTES);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      half8 bf[NB];
+      half8 af[R];
 #pragma unroll
-      for (int ni = 0; ni < NB; ++ni)
+      for (int mi = 0; mi < R; ++mi)
+        af[mi] = *reinterpret_cast<const half8*>(tile_a + a_frag_off[s] + mi * 32 * ROW_BYTES);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) bf[ni][t] = lut_col[ni][lane_code<BITS>(cw[ni], s * 8 + t)];
+      for (int ci = 0; ci < C; ++ci)
+        frag[(s + 1) & 1][ci] = s < 3 ? decode_fragment<BITS>(cur[ci], s + 1, lut_this[ci])
+                                      : decode_fragment<BITS>(nx1[ci], 0, lut_next[ci]);
 #pragma unroll
-      for (int mi = 0; mi < MB; ++mi) {
-        const int r = (wave_m * MB + mi) * 32 + j;
-        const int ch = h * 4 + s;
-        const half8 af = *reinterpret_cast<const half8*>(&tile[r * ROW_BYTES + ((ch ^ (r & 7)) << 4)]);
+      for (int ci = 0; ci < C; ++ci)
 #pragma unroll
-        for (int ni = 0; ni < NB; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ni], af, acc[mi][ni], 0, 0, 0);
-      }
+        for (int mi = 0; mi < R; ++mi)
+          acc[mi][ci] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[s & 1][ci], af[mi], acc[mi][ci], 0, 0, 0);
     }
-    if (more) {
-      store_a(buf ^ 1);
-#pragma unroll
-      for (int ni = 0; ni < NB; ++ni)
-#pragma unroll
-        for (int q = 0; q < BITS; ++q) cw[ni][q] = cn[ni][q];
-    }
+    store_a(min(kb_begin + i + 1u, last_kb), (i + 1u) & 1u, a_store);
     __syncthreads();
+  };
+
+  if (steps > 0) {
+    uint32_t c0[C][BITS], c1[C][BITS], c2[C][BITS];
+    uint4 s0[CH], s1[CH], s2[CH];
+    load_codes(kb_begin, c0);
+    load_codes(min(kb_begin + 1u, last_kb), c1);
+    load_a(kb_begin, s0);
+    load_a(min(kb_begin + 1u, last_kb), s1);
+    load_a(min(kb_begin + 2u, last_kb), s2);
+    store_a(kb_begin, 0u, s0);
+    __syncthreads();
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci)
+      frag[0][ci] = decode_fragment<BITS>(c0[ci], 0, (GENERAL && tail_block && h && steps == 1u) ? lut_zero
+                                                                                                  : lut_col[ci]);
+
+    uint32_t i = 0;
+    for (; i + 3u <= steps; i += 3u) {
+      step(i, c0, c1, c2, s0, s1);
+      step(i + 1u, c1, c2, c0, s1, s2);
+      step(i + 2u, c2, c0, c1, s2, s0);
+    }
+    if (i < steps) step(i, c0, c1, c2, s0, s1);
+    if (i + 1u < steps) step(i + 1u, c1, c2, c0, s1, s2);
   }
 
-  // Epilogue: lane holds row m = ... + j and, for q = 0..3, the 4 columns
-  // n = 32*block + 8*q + 4*h + {0,1,2,3}.
-  _Float16* out = static_cast<_Float16*>(args.out);
-  const _Float16* residual = static_cast<const _Float16*>(args.residual);
+  // Split-K: publish this partial; only the last workgroup of the tile
+  // continues, with the sum of all partials in split order.
+  if (S > 1) {
+    constexpr int EPT = R * C * 16;  // f32 accumulator values per thread
+    float* mine = args.partials + ((uint64_t)tile * S + split) * (uint64_t)(EPT * T);
 #pragma unroll
-  for (int mi = 0; mi < MB; ++mi) {
-    const uint32_t m = m0 + (wave_m * MB + mi) * 32 + j;
-    if (m >= M) continue;
+    for (int mi = 0; mi < R; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NB; ++ni) {
-      const uint32_t nbase = n0 + (wave_n * NB + ni) * 32 + h * 4;
+      for (int ci = 0; ci < C; ++ci)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t n = nbase + q * 8;
-        if (n >= N) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[mi][ni][q * 4 + e];
-        if (args.bias) {
-          const float4 b = *reinterpret_cast<const float4*>(args.bias + n);
-          v[0] += b.x;
-          v[1] += b.y;
-          v[2] += b.z;
-          v[3] += b.w;
+        for (int q = 0; q < 4; ++q) {
+          const int e4 = (mi * C + ci) * 4 + q;
+          *reinterpret_cast<float4*>(mine + ((uint64_t)e4 * T + tid) * 4) =
+              make_float4(acc[mi][ci][4 * q], acc[mi][ci][4 * q + 1], acc[mi][ci][4 * q + 2],
+                          acc[mi][ci][4 * q + 3]);
         }
-        if (args.activation == kActSilu) {
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last_flag = atomicAdd(args.counters + tile, 1u) == S - 1u;
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    if (tid == 0) args.counters[tile] = 0u;
+    const float* base = args.partials + (uint64_t)tile * S * (uint64_t)(EPT * T);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = silu(v[e]);
-        } else if (args.activation == kActRelu) {
+    for (int mi = 0; mi < R; ++mi)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+      for (int ci = 0; ci < C; ++ci)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int e4 = (mi * C + ci) * 4 + q;
+          float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          for (uint32_t p = 0; p < S; ++p) {
+            float4 v;
+            if (p == split)
+              v = make_float4(acc[mi][ci][4 * q], acc[mi][ci][4 * q + 1], acc[mi][ci][4 * q + 2],
+                              acc[mi][ci][4 * q + 3]);
+            else
+              v = *reinterpret_cast<const float4*>(base + (uint64_t)p * (EPT * T) + ((uint64_t)e4 * T + tid) * 4);
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+          }
+          acc[mi][ci][4 * q] = sum.x;
+          acc[mi][ci][4 * q + 1] = sum.y;
+          acc[mi][ci][4 * q + 2] = sum.z;
+          acc[mi][ci][4 * q + 3] = sum.w;
         }
-        const uint64_t at = (uint64_t)m * N + n;
-        if (residual) {
-          const uint2 rb = *reinterpret_cast<const uint2*>(residual + at);
-          const _Float16 r0 = __builtin_bit_cast(_Float16, (uint16_t)(rb.x & 0xffffu));
-          const _Float16 r1 = __builtin_bit_cast(_Float16, (uint16_t)(rb.x >> 16));
-          const _Float16 r2 = __builtin_bit_cast(_Float16, (uint16_t)(rb.y & 0xffffu));
-          const _Float16 r3 = __builtin_bit_cast(_Float16, (uint16_t)(rb.y >> 16));
-          v[0] = (float)r0 + args.residual_scale * v[0];
-          v[1] = (float)r1 + args.residual_scale * v[1];
-          v[2] = (float)r2 + args.residual_scale * v[2];
-          v[3] = (float)r3 + args.residual_scale * v[3];
+  }
+
+  // Epilogue. In registers a lane holds row m = m0 + (wave_m*R + mi)*32 + j
+  // and, for q = 0..3, the 4 columns n = n0 + (wave_n*C + ci)*32 + 8q + 4h
+  // + {0..3}. The output tile goes out through an LDS staging area (the
+  // activation buffers, free after the K loop) so global traffic is 16-byte
+  // chunks along rows: a pass stages MPP m-blocks of every wavefront as
+  // row-major f16 rows of BN columns, 8-byte units XOR-swizzled by row.
+  // With a residual, its tile is first loaded the same way so that
+  // residual + scale * value is formed in f32 and rounded once.
+  {
+    constexpr int MPP = (R * 128 / BN) >= 1 ? (R * 128 / BN < R ? R * 128 / BN : R) : 1;
+    constexpr int SR = WM * MPP * 32;     // staged rows per pass
+    constexpr int ROWB = BN * 2;          // bytes per staged row
+    constexpr int CPR = BN / 8;           // 16-byte chunks per staged row
+    static_assert(SR * ROWB <= 2 * BM * ROW_BYTES, "epilogue staging exceeds the activation buffers");
+    static_assert(R % MPP == 0, "epilogue passes must cover whole m-blocks");
+    static_assert(BN >= 128, "the staging swizzle needs rows of at least 32 8-byte units");
+    auto stage_at = [&](int sr, int unit) { return sr * ROWB + ((unit ^ ((sr & 15) << 1)) << 3); };
+    auto chunk_row = [&](int sr, int mi0) {
+      return m0 + (uint32_t)(((sr / 32) / MPP * R + mi0 + (sr / 32) % MPP) * 32 + (sr & 31));
+    };
+    const _Float16* residual = static_cast<const _Float16*>(args.residual);
+    _Float16* out = static_cast<_Float16*>(args.out);
+    __syncthreads();
+#pragma unroll
+    for (int mi0 = 0; mi0 < R; mi0 += MPP) {
+      if (residual) {
+        for (int chunk = tid; chunk < SR * CPR; chunk += T) {
+          const int sr = chunk / CPR, c16 = chunk % CPR;
+          const uint32_t m = chunk_row(sr, mi0);
+          const uint32_t n = n0 + (uint32_t)c16 * 8u;
+          if (m < M && n < N)
+            *reinterpret_cast<uint4*>(a_lds + stage_at(sr, 2 * c16)) =
+                *reinterpret_cast<const uint4*>(residual + (uint64_t)m * N + n);
         }
-        uint2 ob;
-        ob.x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
-        ob.y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[3]) << 16);
-        *reinterpret_cast<uint2*>(out + at) = ob;
+        __syncthreads();
       }
+#pragma unroll
+      for (int ml = 0; ml < MPP; ++ml) {
+        const int mi = mi0 + ml;
+        if (mi >= R) break;
+        const int sr = (wave_m * MPP + ml) * 32 + j;
+#pragma unroll
+        for (int ci = 0; ci < C; ++ci) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int unit = (wave_n * C + ci) * 8 + 2 * q + h;
+            const uint32_t n = n0 + (uint32_t)unit * 4u;
+            float v0 = acc[mi][ci][4 * q], v1 = acc[mi][ci][4 * q + 1];
+            float v2 = acc[mi][ci][4 * q + 2], v3 = acc[mi][ci][4 * q + 3];
+            if (args.bias && n < N) {
+              const float4 b = *reinterpret_cast<const float4*>(args.bias + n);
+              v0 += b.x;
+              v1 += b.y;
+              v2 += b.z;
+              v3 += b.w;
+            }
+            if (args.activation == kActSilu) {
+              v0 = silu(v0);
+              v1 = silu(v1);
+              v2 = silu(v2);
+              v3 = silu(v3);
+            } else if (args.activation == kActRelu) {
+              v0 = fmaxf(v0, 0.0f);
+              v1 = fmaxf(v1, 0.0f);
+              v2 = fmaxf(v2, 0.0f);
+              v3 = fmaxf(v3, 0.0f);
+            }
+            uint2* slot = reinterpret_cast<uint2*>(a_lds + stage_at(sr, unit));
+            if (residual) {
+              const uint2 rb = *slot;
+              const float sc = args.residual_scale;
+              v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.x & 0xffffu)) + sc * v0;
+              v1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.x >> 16)) + sc * v1;
+              v2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.y & 0xffffu)) + sc * v2;
+              v3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.y >> 16)) + sc * v3;
+            }
+            *slot = make_uint2(pack_half2(v0, v1), pack_half2(v2, v3));
+          }
+        }
+      }
+      __syncthreads();
+      for (int chunk = tid; chunk < SR * CPR; chunk += T) {
+        const int sr = chunk / CPR, c16 = chunk % CPR;
+        const uint32_t m = chunk_row(sr, mi0);
+        const uint32_t n = n0 + (uint32_t)c16 * 8u;
+        if (m < M && n < N)
+          *reinterpret_cast<uint4*>(out + (uint64_t)m * N + n) =
+              *reinterpret_cast<const uint4*>(a_lds + stage_at(sr, 2 * c16));
+      }
+      __syncthreads();
     }
   }
 }
@@ -255,28 +457,28 @@ struct Variant {
   TileShape shape;
   const char* name5;
   const char* name6;
-  void (*kernel5)(GemmArgs);
-  void (*kernel6)(GemmArgs);
+  void (*single[2])(GemmArgs);  // [bits == 6]
+  void (*general[2])(GemmArgs);
 };
 
-#define PK_F16_VARIANT(WM, WN, MB, NB)                                             \
-  Variant {                                                                        \
-    TileShape{WM, WN, MB, NB}, "pk_gemm_f16_b5_w" #WM "x" #WN "_m" #MB "n" #NB,    \
-        "pk_gemm_f16_b6_w" #WM "x" #WN "_m" #MB "n" #NB,                           \
-        gemm_f16_kernel<5, WM, WN, MB, NB>, gemm_f16_kernel<6, WM, WN, MB, NB>     \
+#define PK_F16_VARIANT(WM, WN, R, C)                                                              \
+  Variant {                                                                                       \
+    TileShape{WM, WN, R, C}, "pk_gemm_f16_b5_w" #WM "x" #WN "_m" #R "n" #C,                       \
+        "pk_gemm_f16_b6_w" #WM "x" #WN "_m" #R "n" #C,                                            \
+        {gemm_f16_kernel<5, WM, WN, R, C, false>, gemm_f16_kernel<6, WM, WN, R, C, false>},       \
+        {gemm_f16_kernel<5, WM, WN, R, C, true>, gemm_f16_kernel<6, WM, WN, R, C, true>}          \
   }
 
 const Variant kVariants[] = {
-    PK_F16_VARIANT(1, 4, 8, 2),  // 256 x 256
+    PK_F16_VARIANT(1, 4, 3, 2),  // 96 x 256
     PK_F16_VARIANT(1, 4, 4, 2),  // 128 x 256
     PK_F16_VARIANT(1, 4, 6, 1),  // 192 x 128
-    PK_F16_VARIANT(1, 2, 6, 1),  // 192 x 64
-    PK_F16_VARIANT(1, 4, 3, 2),  // 96 x 256
-    PK_F16_VARIANT(1, 4, 3, 1),  // 96 x 128
+    PK_F16_VARIANT(1, 4, 4, 1),  // 128 x 128
+    PK_F16_VARIANT(1, 4, 8, 1),  // 256 x 128
     PK_F16_VARIANT(1, 4, 2, 2),  // 64 x 256
+    PK_F16_VARIANT(1, 4, 2, 1),  // 64 x 128
     PK_F16_VARIANT(1, 4, 1, 1),  // 32 x 128
     PK_F16_VARIANT(2, 2, 4, 2),  // 256 x 128
-    PK_F16_VARIANT(1, 3, 6, 2),  // 192 x 192
 };
 
 }  // namespace
@@ -289,11 +491,17 @@ const char* f16_variant_name(int bits, int index) {
 
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream) {
   const Variant& v = kVariants[variant];
-  const uint32_t n_pad = padded_columns(args.columns);
-  const dim3 grid((n_pad + v.shape.tile_columns() - 1) / v.shape.tile_columns(),
-                  (args.rows + v.shape.tile_rows() - 1) / v.shape.tile_rows());
-  if (grid.y == 0) return hipSuccess;
-  hipLaunchKernelGGL(bits == 5 ? v.kernel5 : v.kernel6, grid, dim3(v.shape.threads()), 0, stream, args);
+  const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;
+  if (groups == 0) return hipSuccess;
+  // The fast kernel needs K % 64 == 0 and every tile inside one palette
+  // group (its palette staged at a fixed LDS address); tiles start at
+  // multiples of the tile width, so the latter holds with one group or when
+  // the group width is a multiple of the tile width.
+  const bool single = (args.inner & 63u) == 0u &&
+                      (args.palette_groups == 1 ||
+                       args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
+  void (*kernel)(GemmArgs) = single ? v.single[bits == 6] : v.general[bits == 6];
+  hipLaunchKernelGGL(kernel, dim3(groups), dim3(v.shape.threads()), 0, stream, args);
   return hipGetLastError();
 }
 

@@ -47,6 +47,15 @@ struct GemmArgs {
   uint32_t columns;          // N
   uint32_t palette_groups;
   uint32_t palette_group_columns;
+  // Split-K: `splits` workgroups share one output tile, each over a
+  // contiguous range of 64-deep K blocks. With splits > 1 every workgroup
+  // writes its f32 partial tile to `partials` and bumps the tile's counter;
+  // the last one to arrive sums the partials in split order (so the result
+  // does not depend on arrival order), applies the epilogue, stores the
+  // tile and resets the counter to zero for the next launch.
+  uint32_t splits;
+  float* partials;           // [tiles][splits][tile elements] or null
+  uint32_t* counters;        // [tiles], zero between launches, or null
 };
 
 // Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
@@ -57,7 +66,29 @@ struct TileShape {
   __host__ __device__ constexpr int threads() const { return 64 * waves_m * waves_n; }
   __host__ __device__ constexpr int tile_rows() const { return 32 * waves_m * m_blocks; }
   __host__ __device__ constexpr int tile_columns() const { return 32 * waves_n * n_blocks; }
+  // f32 elements of one workgroup's split-K partial tile.
+  __host__ __device__ constexpr uint32_t tile_elements() const {
+    return (uint32_t)(tile_rows() * tile_columns());
+  }
 };
+
+// Output tiles of a launch over `rows` x `columns` (columns padded to 32).
+inline uint32_t tiles_m(const TileShape& s, uint32_t rows) {
+  return (rows + s.tile_rows() - 1) / s.tile_rows();
+}
+inline uint32_t tiles_n(const TileShape& s, uint32_t columns) {
+  return (padded_columns(columns) + s.tile_columns() - 1) / s.tile_columns();
+}
+
+// Workgroup i is dispatched to XCD i % 8 (round robin). This bijection on
+// [0, count) gives the workgroups of one XCD a contiguous range of work
+// items, so tiles that share activation rows share that XCD's L2.
+__host__ __device__ inline uint32_t xcd_local_order(uint32_t i, uint32_t count) {
+  constexpr uint32_t kXcds = 8;
+  const uint32_t xcd = i % kXcds, slot = i / kXcds;
+  const uint32_t per = count / kXcds, rem = count % kXcds;
+  return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
 
 // Launchers. Each returns the hipError_t of the launch.
 hipError_t launch_unpack(int bits, const uint32_t* words, uint64_t groups,

@@ -87,6 +87,7 @@ class PlanInfo(ctypes.Structure):
         ("tile_columns", ctypes.c_uint32),
         ("split_inner", ctypes.c_uint32),
         ("lds_bytes", ctypes.c_uint32),
+        ("workspace_bytes", ctypes.c_uint64),
         ("flops", ctypes.c_uint64),
         ("algorithmic_bytes", ctypes.c_uint64),
         ("kernel", ctypes.c_char * 64),
@@ -159,6 +160,7 @@ SIGNATURES = {
     "pk_gemm_release": (ctypes.c_int, [_VP]),
     "pk_gemm_variant_count": (ctypes.c_int, [ctypes.c_int]),
     "pk_gemm_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
+    "pk_gemm_set_splits": (ctypes.c_int, [_VP, ctypes.c_uint32]),
     "pk_gemm_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
     "pk_palette_expand": (ctypes.c_int, [_VP, ctypes.POINTER(ExpandDesc), _VP]),
     "pk_unpack_codes": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_uint64, _VP, _VP]),
@@ -372,6 +374,9 @@ class GemmOp:
 
     def set_variant(self, variant: int) -> None:
         check(load().pk_gemm_set_variant(self.handle, variant))
+
+    def set_splits(self, splits: int) -> None:
+        check(load().pk_gemm_set_splits(self.handle, splits))
 
     def destroy(self) -> None:
         check(load().pk_gemm_destroy(self.handle))

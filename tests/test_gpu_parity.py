@@ -47,8 +47,8 @@ def scope(ctx):
     s.close()
 
 
-def run_case(abi, ctx, scope, case, *, variant=None, active_rows=0, sentinel=None, prepared=None,
-             capacity=None):
+def run_case(abi, ctx, scope, case, *, variant=None, splits=None, active_rows=0, sentinel=None,
+             prepared=None, capacity=None, repeats=1):
     w = case.weight
     rows = capacity or case.rows
     a_host = case.a if capacity is None else np.concatenate(
@@ -71,7 +71,10 @@ def run_case(abi, ctx, scope, case, *, variant=None, active_rows=0, sentinel=Non
     try:
         if variant is not None:
             op.set_variant(variant)
-        op.enqueue(active_rows)
+        if splits is not None:
+            op.set_splits(splits)
+        for _ in range(repeats):
+            op.enqueue(active_rows)
         ctx.synchronize()
         return out.download()
     finally:
@@ -223,7 +226,7 @@ def test_every_tile_variant_matches(abi, ctx, scope, oracle, workloads, precisio
     case = workloads.gemm_case(5, 333, 320, 640, 5, dtype=dtype, activation="silu")
     results = []
     for variant in range(abi.variant_count(precision)):
-        results.append(run_case(abi, ctx, scope, case, variant=variant))
+        results.append(run_case(abi, ctx, scope, case, variant=variant, splits=1))
     for variant, got in enumerate(results):
         if precision == "f16":
             assert_f16_parity(oracle, got, case)
@@ -231,6 +234,24 @@ def test_every_tile_variant_matches(abi, ctx, scope, oracle, workloads, precisio
             norm, peak = oracle.relative_errors(got, oracle_gemm(oracle, case, "f32-chain"))
             assert norm <= F32_TOL and peak <= F32_TOL, (variant, norm, peak)
         np.testing.assert_array_equal(got.view(np.uint8), results[0].view(np.uint8), err_msg=str(variant))
+
+
+@pytest.mark.parametrize("variant", [0, 1, 3, 6])
+def test_split_inner_reduction(abi, ctx, scope, oracle, workloads, variant):
+    """Split-K partial tiles are summed in split order by the last
+    workgroup of each tile: every split count stays within the parity bars,
+    repeated launches (counters reset in-kernel) give identical bits, and a
+    K = 32 (mod 64) tail is handled in the last split."""
+    case = workloads.gemm_case(77, 300, 1056, 512, 5, activation="silu")
+    case_res = workloads.gemm_case(78, 129, 2048, 256, 6, residual_scale=0.5)
+    for c in (case, case_res):
+        kb = (c.weight.inner + 63) // 64
+        for splits in sorted({1, 2, 3, min(5, kb), kb}):
+            got = run_case(abi, ctx, scope, c, variant=variant, splits=splits)
+            assert_f16_parity(oracle, got, c)
+            again = run_case(abi, ctx, scope, c, variant=variant, splits=splits, repeats=3)
+            np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16),
+                                          err_msg=f"{c.name} splits={splits}")
 
 
 def test_active_rows_prefix_leaves_the_tail_untouched(abi, ctx, scope, oracle, workloads):
