@@ -118,50 +118,64 @@ def build_small_m(abi, ctx, keep, rows):
     return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16")], config, case
 
 
-def cpu_baseline(workload, data, sample_rows):
-    """The oracle (reference semantics restated in C) on a bounded sample."""
+def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
+    """The oracle (reference semantics restated in C) on a bounded sample:
+    row batches of the same workload until about `budget_s` seconds of wall
+    time have passed (or `sample_rows` rows, when given)."""
     from oracle import pko
     threads = min(os.cpu_count() or 1, 16)
+    batch = 32
     if workload == "ff-block":
-        rows = sample_rows or 128
-        x = data.x[:rows]
-        t0 = time.perf_counter()
-        h = pko.gemm(x, data.w1.packed, 5, data.w1.palette, 4096, activation="silu", mode="f16-chain",
-                     threads=threads)
-        pko.gemm(h, data.w2.packed, 5, data.w2.palette, 1024, residual=x, residual_scale=0.5,
-                 mode="f16-chain", threads=threads)
-        dt = time.perf_counter() - t0
-        flops = 2 * rows * 1024 * 4096 * 2
-        sample = f"{rows} of 1504 rows of the FF block, f16-accumulator chain (reference fp16 semantics)"
+        total_rows, per_row_flops = data.x.shape[0], 2 * 1024 * 4096 * 2
+
+        def run(lo, hi):
+            x = data.x[lo:hi]
+            h = pko.gemm(x, data.w1.packed, 5, data.w1.palette, 4096, activation="silu", mode="f16-chain",
+                         threads=threads)
+            pko.gemm(h, data.w2.packed, 5, data.w2.palette, 1024, residual=x, residual_scale=0.5,
+                     mode="f16-chain", threads=threads)
+        what = "rows of the FF block (W1 + SiLU, W2 + 0.5 residual), f16-accumulator chain (reference fp16 semantics)"
     elif workload == "single-gemm-fp32":
-        rows = sample_rows or data.rows
-        t0 = time.perf_counter()
-        pko.gemm(data.a[:rows], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
-                 mode="f32-chain", threads=threads)
-        dt = time.perf_counter() - t0
-        flops = 2 * rows * 1024 * 4096
-        sample = f"{rows} of {data.rows} rows, f32 fma chain (reference fp32 semantics)"
+        total_rows, per_row_flops = data.rows, 2 * 1024 * 4096
+
+        def run(lo, hi):
+            pko.gemm(data.a[lo:hi], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
+                     mode="f32-chain", threads=threads)
+        what = "rows, f32 fma chain (reference fp32 semantics)"
     else:
-        rows = sample_rows or data.rows
-        t0 = time.perf_counter()
-        pko.gemm(data.a[:rows], data.weight.packed, 5, data.weight.palette, 4096, mode="f16-chain",
-                 threads=threads)
-        dt = time.perf_counter() - t0
-        flops = 2 * rows * 1024 * 4096
-        sample = f"{rows} rows, f16-accumulator chain"
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": sample, "seconds": dt}
+        total_rows, per_row_flops = data.rows, 2 * 1024 * 4096
+
+        def run(lo, hi):
+            pko.gemm(data.a[lo:hi], data.weight.packed, 5, data.weight.palette, 4096, mode="f16-chain",
+                     threads=threads)
+        what = "rows, f16-accumulator chain"
+    limit = min(sample_rows, total_rows) if sample_rows else total_rows
+    done = 0
+    t0 = time.perf_counter()
+    while done < limit:
+        hi = min(done + batch, limit)
+        run(done, hi)
+        done = hi
+        if not sample_rows and time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done * per_row_flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {total_rows} {what}", "seconds": dt}
 
 
-def read_traffic(kernel_name):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+def read_traffic(gemm_name, kernel_name):
+    """HBM bytes per launch of one GEMM of the step, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a plain copy of known size), or
+    None when no summary of this kernel exists."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        table = json.load(f)
-    entry = table.get(kernel_name)
-    return None if entry is None else entry.get("hbm_bytes_per_launch")
+        entry = json.load(f).get("kernels", {}).get(gemm_name)
+    if entry is None or entry.get("kernel") != kernel_name:
+        return None
+    return entry["hbm_bytes_per_launch"]
 
 
 def main():
@@ -230,7 +244,7 @@ def main():
         roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": dom["gbs"] / PEAK_HBM_GBS}
     roofline["kernel"] = dom["kernel"]
-    roofline["traffic"] = read_traffic(dom["kernel"])
+    roofline["traffic"] = read_traffic(dominant.name, dom["kernel"]) if args.workload == "ff-block" else None
 
     cpu = None
     if not args.no_cpu:

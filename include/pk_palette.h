@@ -22,6 +22,7 @@
  *                           with the contract checks requireGemmShape
  *                           (:971-1011), requireProductionSpecialization
  *                           (:1031-1067), requireRuntimeWeight (:1069-1161)
+ *   pk_gemm_validate        the same contract checks without a device
  *   pk_gemm_enqueue         GemmDispatch.encode(encoder, timestampWrites,
  *                           shape) (gemm.ts:419-463; F32 twin :2912-2960)
  *   pk_gemm_destroy         GemmDispatch.destroy (gemm.ts:465-469)
@@ -188,6 +189,11 @@ typedef struct pk_gemm_desc {
 
 int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,
                    pk_gemm_op **out);
+/* The descriptor checks of pk_gemm_create alone, with no device and no
+   allocation (the reference's createDispatch validation is host-side too,
+   gemm.ts:971-1161). A prepared weight is checked against its own geometry
+   only. */
+int pk_gemm_validate(const pk_gemm_desc *desc);
 /* Launch on `stream` for the first `active_rows` rows (0 = all rows). */
 int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
 /* Releases the op's device resources. Idempotent: a second call is a no-op

@@ -184,57 +184,46 @@ uint64_t workspace_bytes_for(const pk::TileShape& s, uint32_t rows, uint32_t col
   return (partial + 255u) / 256u * 256u + tiles * 4u;
 }
 
-// Launch cost model of the planner, in units of one MFMA-block K step on
-// one SIMD. A workgroup runs tile_rows x tile_columns over its K range; its
-// wavefronts are slowed by the LDS traffic per MFMA (decoded weight
-// fragments are gathered from the LDS palette, activation fragments are
-// read from the LDS tile), workgroups beyond one per compute unit run in
-// further rounds, and split-K adds its partial-tile round trip.
-double plan_cost(int precision, const pk::TileShape& s, uint32_t rows, uint32_t inner, uint32_t columns,
-                 uint32_t splits, int cus) {
-  const double tiles = (double)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
-  const double groups = tiles * splits;
-  const double rounds = std::ceil(groups / cus);
-  const double kb = std::ceil((double)k_blocks(inner) / splits);
-  const double blocks = (double)s.m_blocks * s.n_blocks;
-  double lds;
-  if (precision == PK_PRECISION_F16)
-    lds = 1.0 / s.m_blocks + 0.5 / s.n_blocks;  // per MFMA, relative to its duration
-  else
-    lds = 0.25 / s.m_blocks + 0.125 / s.n_blocks;
-  const double per_step = blocks * std::max(1.0, 0.6 + lds);
-  double cost = rounds * kb * per_step;
-  if (splits > 1) {
-    // Partial tiles written and read back: 8 bytes per output element and
-    // split, against ~64 bytes/clock/CU of cache bandwidth, in MFMA-block
-    // K steps (32 x 32 x 64 MACs).
-    const double bytes = tiles * splits * s.tile_elements() * 8.0;
-    cost += bytes / (64.0 * cus) / 128.0;
-  }
-  return cost;
-}
-
 struct Plan {
   int variant;
   uint32_t splits;
 };
 
-Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
+int find_variant(int precision, int waves_m, int waves_n, int m_blocks, int n_blocks) {
   const int count = precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
-  const uint32_t max_splits = precision == PK_PRECISION_F16 ? std::min(8u, k_blocks(inner)) : 1u;
-  Plan best{0, 1};
+  for (int i = 0; i < count; ++i) {
+    const pk::TileShape s = shape_of(precision, i);
+    if (s.waves_m == waves_m && s.waves_n == waves_n && s.m_blocks == m_blocks && s.n_blocks == n_blocks)
+      return i;
+  }
+  return 0;
+}
+
+// Launch planner. The f16 choice follows MI355X measurements of every
+// compiled tile shape and split count over the encoder's GEMM shapes
+// (M 64..3008, K 1024/4096, N 1024..4096): the 64 x 128 tile (four
+// wavefronts of 2 x 1 MFMA blocks) is fastest or within 5% everywhere
+// above 256 rows, the 32 x 128 tile below, and split-K never paid for its
+// partial-tile traffic. f32 keeps its own smallest-cost shape.
+Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
+  (void)inner;
+  if (precision == PK_PRECISION_F16)
+    return {rows <= 256u ? find_variant(precision, 1, 4, 1, 1) : find_variant(precision, 1, 4, 2, 1), 1u};
+  // f32: the largest tile that still fills the compute units.
+  const int count = pk::f32_variant_count();
+  int best = 0;
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
     const pk::TileShape s = shape_of(precision, i);
-    for (uint32_t sp = 1; sp <= max_splits; ++sp) {
-      const double cost = plan_cost(precision, s, rows, inner, columns, sp, cus);
-      if (cost < best_cost * 0.999) {
-        best_cost = cost;
-        best = {i, sp};
-      }
+    const double tiles = (double)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
+    const double rounds = std::ceil(tiles / cus);
+    const double cost = rounds * s.tile_rows() * s.tile_columns() * (1.0 + 0.25 / s.m_blocks);
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = i;
     }
   }
-  return best;
+  return {best, 1u};
 }
 
 // Applies a (variant, splits) choice: resizes the split-K workspace for the
@@ -271,6 +260,94 @@ int configure_launch(pk_gemm_op* op, int variant, uint32_t splits) {
   op->variant = variant;
   op->splits = splits;
   op->args.splits = splits;
+  return PK_OK;
+}
+
+// The descriptor contract of createDispatch: requireGemmShape,
+// requireProductionSpecialization and requireRuntimeWeight
+// (src/webgpu/kernels/gemm.ts:971-1161; FP32 twins :3342-3557) plus the
+// binding sizes and vector alignment the kernels rely on. Host-only: ctx
+// may be null (pk_gemm_validate), then the prepared weight's context is not
+// compared.
+int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
+  if (!d) return fail(PK_INVALID_ARGUMENT, "GEMM descriptor is null");
+  if (d->struct_size != sizeof(pk_gemm_desc))
+    return fail(PK_INVALID_ARGUMENT, "pk_gemm_desc.struct_size mismatch");
+  const char* label = safe_label(d->label);
+  const bool f16 = d->precision == PK_PRECISION_F16;
+  if (!f16 && d->precision != PK_PRECISION_F32)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
+  const uint32_t elem = f16 ? 2u : 4u;
+  // requireGemmShape (gemm.ts:971-983; FP32 twin N%4)
+  if (d->rows == 0 || d->inner == 0 || d->inner % 32u != 0 || d->columns == 0 ||
+      d->columns % (f16 ? 8u : 4u) != 0)
+    return fail(PK_RANGE_ERROR, "Unsupported %sGEMM shape for %s", f16 ? "" : "FP32 ", label);
+  if (d->palette_bits != 5 && d->palette_bits != 6)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported weight format", label);
+  const int bits = d->palette_bits;
+  // requireProductionSpecialization (gemm.ts:1031-1067)
+  if (!d->residual && d->has_residual_scale)
+    return fail(PK_INVALID_ARGUMENT, "%s supplies a residual scale without a residual", label);
+  if (d->activation < PK_ACTIVATION_NONE || d->activation > PK_ACTIVATION_RELU)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported activation %d", label, d->activation);
+  const float residual_scale = d->residual ? (d->has_residual_scale ? d->residual_scale : 1.0f) : -1.0f;
+  if (d->flags & PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE) {
+    bool found = false;
+    for (const Signature& s : kProductionSignatures)
+      if (s.rows == d->rows && s.inner == d->inner && s.columns == d->columns &&
+          s.activation == d->activation && s.bias == (d->bias != nullptr) &&
+          s.residual_scale == residual_scale)
+        found = true;
+    if (!found) {
+      char scale[32];
+      if (d->residual)
+        std::snprintf(scale, sizeof scale, "%g", residual_scale);
+      else
+        std::snprintf(scale, sizeof scale, "none");
+      return fail(PK_INVALID_ARGUMENT,
+                  "%s is not a fixed production GEMM signature: M=%u, K=%u, N=%u, "
+                  "activation=%s, bias=%s, residualScale=%s",
+                  label, d->rows, d->inner, d->columns, activation_name(d->activation),
+                  d->bias ? "true" : "false", scale);
+    }
+  }
+  // f16SubgroupGemmWgsl (gemm.ts:1372-1378)
+  if (d->bias && d->residual)
+    return fail(PK_INVALID_ARGUMENT, "%s cannot fuse bias and residual together", label);
+  // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
+  const uint32_t entries = 1u << bits;
+  const uint32_t cpg = pk::codes_per_group(bits);
+  if (d->palette_groups == 0 || d->palette_group_columns == 0 ||
+      (uint64_t)d->palette_group_columns * d->palette_groups != d->columns ||
+      d->palette_group_columns % cpg != 0 || !d->palette ||
+      d->palette_bytes != (uint64_t)d->palette_groups * entries * elem || !aligned(d->palette, elem))
+    return fail(PK_INVALID_ARGUMENT, "%s has invalid transient palette weights", label);
+  if (d->prepared) {
+    const pk_prepared_weight* w = d->prepared;
+    if (w->owner_released || w->bits != bits || w->inner != d->inner || w->columns != d->columns ||
+        (ctx && w->ctx != ctx))
+      return fail(PK_INVALID_ARGUMENT, "%s has a mismatched prepared palette weight", label);
+  } else {
+    if (int s = check_packed(label, bits, d->inner, d->columns, d->packed_bytes)) return s;
+    if (!d->packed || !aligned(d->packed, 4))
+      return fail(PK_INVALID_ARGUMENT, "%s has invalid packed palette indices", label);
+  }
+  // Bindings: sizes (gemm.ts:1302-1333 minBindingSize) and vector alignment.
+  const uint64_t a_need = (uint64_t)d->rows * d->inner * elem;
+  const uint64_t c_need = (uint64_t)d->rows * d->columns * elem;
+  if (!d->a || d->a_bytes < a_need || !aligned(d->a, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s input binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)a_need);
+  if (!d->output || d->output_bytes < c_need || !aligned(d->output, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s output binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)c_need);
+  if (d->bias && (d->bias_bytes < (uint64_t)d->columns * 4u || !aligned(d->bias, 16)))
+    return fail(PK_INVALID_ARGUMENT, "%s bias binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)d->columns * 4u);
+  if (d->residual && (d->residual_bytes < c_need || !aligned(d->residual, 16)))
+    return fail(PK_INVALID_ARGUMENT, "%s residual binding must hold %llu bytes at 16-byte alignment",
+                label, (unsigned long long)c_need);
+
   return PK_OK;
 }
 
@@ -503,87 +580,16 @@ int pk_prepared_weight_bytes(const pk_prepared_weight* weight, uint64_t* bytes) 
   return ok();
 }
 
+int pk_gemm_validate(const pk_gemm_desc* d) { return validate_gemm_desc(nullptr, d); }
+
 int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm_op** out) {
   if (int s = check_ctx(ctx)) return s;
   if (!d || !out) return fail(PK_INVALID_ARGUMENT, "GEMM descriptor or output is null");
   *out = nullptr;
-  if (d->struct_size != sizeof(pk_gemm_desc))
-    return fail(PK_INVALID_ARGUMENT, "pk_gemm_desc.struct_size mismatch");
+  if (int s = validate_gemm_desc(ctx, d)) return s;
   const char* label = safe_label(d->label);
-  const bool f16 = d->precision == PK_PRECISION_F16;
-  if (!f16 && d->precision != PK_PRECISION_F32)
-    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
-  const uint32_t elem = f16 ? 2u : 4u;
-  // requireGemmShape (gemm.ts:971-983; FP32 twin N%4)
-  if (d->rows == 0 || d->inner == 0 || d->inner % 32u != 0 || d->columns == 0 ||
-      d->columns % (f16 ? 8u : 4u) != 0)
-    return fail(PK_RANGE_ERROR, "Unsupported GEMM shape for %s", label);
-  if (d->palette_bits != 5 && d->palette_bits != 6)
-    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported weight format", label);
   const int bits = d->palette_bits;
-  // requireProductionSpecialization (gemm.ts:1031-1067)
-  if (!d->residual && d->has_residual_scale)
-    return fail(PK_INVALID_ARGUMENT, "%s supplies a residual scale without a residual", label);
-  if (d->activation < PK_ACTIVATION_NONE || d->activation > PK_ACTIVATION_RELU)
-    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported activation %d", label, d->activation);
   const float residual_scale = d->residual ? (d->has_residual_scale ? d->residual_scale : 1.0f) : -1.0f;
-  if (d->flags & PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE) {
-    bool found = false;
-    for (const Signature& s : kProductionSignatures)
-      if (s.rows == d->rows && s.inner == d->inner && s.columns == d->columns &&
-          s.activation == d->activation && s.bias == (d->bias != nullptr) &&
-          s.residual_scale == residual_scale)
-        found = true;
-    if (!found) {
-      char scale[32];
-      if (d->residual)
-        std::snprintf(scale, sizeof scale, "%g", residual_scale);
-      else
-        std::snprintf(scale, sizeof scale, "none");
-      return fail(PK_INVALID_ARGUMENT,
-                  "%s is not a fixed production GEMM signature: M=%u, K=%u, N=%u, "
-                  "activation=%s, bias=%s, residualScale=%s",
-                  label, d->rows, d->inner, d->columns, activation_name(d->activation),
-                  d->bias ? "true" : "false", scale);
-    }
-  }
-  // f16SubgroupGemmWgsl (gemm.ts:1372-1378)
-  if (d->bias && d->residual)
-    return fail(PK_INVALID_ARGUMENT, "%s cannot fuse bias and residual together", label);
-  // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
-  const uint32_t entries = 1u << bits;
-  const uint32_t cpg = pk::codes_per_group(bits);
-  if (d->palette_groups == 0 || d->palette_group_columns == 0 ||
-      (uint64_t)d->palette_group_columns * d->palette_groups != d->columns ||
-      d->palette_group_columns % cpg != 0 || !d->palette ||
-      d->palette_bytes != (uint64_t)d->palette_groups * entries * elem || !aligned(d->palette, elem))
-    return fail(PK_INVALID_ARGUMENT, "%s has invalid transient palette weights", label);
-  if (d->prepared) {
-    const pk_prepared_weight* w = d->prepared;
-    if (w->owner_released || w->bits != bits || w->inner != d->inner || w->columns != d->columns ||
-        w->ctx != ctx)
-      return fail(PK_INVALID_ARGUMENT, "%s has a mismatched prepared palette weight", label);
-  } else {
-    if (int s = check_packed(label, bits, d->inner, d->columns, d->packed_bytes)) return s;
-    if (!d->packed || !aligned(d->packed, 4))
-      return fail(PK_INVALID_ARGUMENT, "%s has invalid packed palette indices", label);
-  }
-  // Bindings: sizes (gemm.ts:1302-1333 minBindingSize) and vector alignment.
-  const uint64_t a_need = (uint64_t)d->rows * d->inner * elem;
-  const uint64_t c_need = (uint64_t)d->rows * d->columns * elem;
-  if (!d->a || d->a_bytes < a_need || !aligned(d->a, 16))
-    return fail(PK_INVALID_ARGUMENT, "%s input binding must hold %llu bytes at 16-byte alignment",
-                label, (unsigned long long)a_need);
-  if (!d->output || d->output_bytes < c_need || !aligned(d->output, 16))
-    return fail(PK_INVALID_ARGUMENT, "%s output binding must hold %llu bytes at 16-byte alignment",
-                label, (unsigned long long)c_need);
-  if (d->bias && (d->bias_bytes < (uint64_t)d->columns * 4u || !aligned(d->bias, 16)))
-    return fail(PK_INVALID_ARGUMENT, "%s bias binding must hold %llu bytes at 16-byte alignment",
-                label, (unsigned long long)d->columns * 4u);
-  if (d->residual && (d->residual_bytes < c_need || !aligned(d->residual, 16)))
-    return fail(PK_INVALID_ARGUMENT, "%s residual binding must hold %llu bytes at 16-byte alignment",
-                label, (unsigned long long)c_need);
-
   PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   auto* op = new pk_gemm_op();
   op->ctx = ctx;

@@ -1,0 +1,210 @@
+// Type declarations of parakeet.wgsl_amd/host (index.js): the reference's
+// GEMM op interface (src/webgpu/kernels/gemm.ts:358-470, encoder.ts:308-432,
+// arena.ts:5-15, package.ts:45-50) over HIP device memory.
+
+export interface TensorRecord {
+  readonly dtype: "float16" | "float32" | "uint32";
+  readonly logicalShape: readonly number[];
+  readonly storageShape: readonly number[];
+  readonly byteLength: number;
+  readonly layout: string;
+}
+
+export interface HipBuffer {
+  readonly label: string;
+  readonly size: number;
+  /** Device address. */
+  readonly address: bigint;
+  destroy(): void;
+}
+
+export interface BufferBinding {
+  readonly buffer: HipBuffer;
+  readonly offset: number;
+  readonly size: number;
+}
+
+/** package.ts:45-50 */
+export interface GpuTensor {
+  readonly sourceRecord: TensorRecord;
+  readonly runtimeRecord: TensorRecord;
+  readonly buffer: HipBuffer;
+  readonly binding: BufferBinding;
+}
+
+/** arena.ts:5-15 */
+export interface ArenaSlice {
+  readonly label: string;
+  readonly bufferIndex?: number;
+  readonly byteOffset: number;
+  readonly byteLength: number;
+}
+
+/** execution-shape.ts:1-4 */
+export interface EncoderDispatchShape {
+  readonly batchSize: number;
+  readonly rows: number;
+}
+
+export type GemmActivation = "none" | "silu" | "relu";
+
+export interface HipTimestampQuerySet {
+  write(index: number): void;
+  elapsedMs(begin: number, end: number): number;
+  destroy(): void;
+}
+
+export interface TimestampWrites {
+  readonly querySet: HipTimestampQuerySet;
+  readonly beginningOfPassWriteIndex?: number;
+  readonly endOfPassWriteIndex?: number;
+}
+
+export interface HipCommandBuffer {
+  readonly label: string;
+}
+
+export interface HipCommandEncoder {
+  finish(): HipCommandBuffer;
+}
+
+export interface HipQueue {
+  writeBuffer(buffer: HipBuffer, bufferOffset: number, data: ArrayBuffer | ArrayBufferView): void;
+  submit(commandBuffers: readonly HipCommandBuffer[]): void;
+  onSubmittedWorkDone(): Promise<void>;
+  readBuffer(buffer: HipBuffer, offset: number, size: number): Promise<ArrayBuffer>;
+}
+
+export interface DeviceInfo {
+  readonly name: string;
+  readonly arch: string;
+  readonly computeUnits: number;
+  readonly wavefrontSize: number;
+  readonly globalMemoryBytes: number;
+  readonly ldsBytesPerBlock: number;
+  readonly clockKhz: number;
+}
+
+export declare class HipGpuDevice {
+  static create(options?: { index?: number }): HipGpuDevice;
+  readonly info: DeviceInfo;
+  readonly queue: HipQueue;
+  readonly limits: { readonly minStorageBufferOffsetAlignment: number };
+  createBuffer(descriptor: { label?: string; size: number }): HipBuffer;
+  createCommandEncoder(descriptor?: { label?: string }): HipCommandEncoder;
+  createQuerySet(descriptor: { type: "timestamp"; count: number }): HipTimestampQuerySet;
+  destroy(): void;
+}
+
+export declare class GpuActivationArena {
+  constructor(device: HipGpuDevice, byteLength: number, label?: string);
+  readonly byteLength: number;
+  slice(label: string, byteOffset: number, byteLength: number): ArenaSlice;
+  binding(slice: ArenaSlice): BufferBinding;
+  upload(device: HipGpuDevice, destination: ArenaSlice, data: ArrayBuffer | ArrayBufferView): void;
+  destroy(): void;
+}
+
+/** gemm.ts:375-385 */
+export interface PreparedPaletteWeight {
+  readonly source: GpuTensor;
+  readonly palette: GpuTensor;
+  readonly paletteGroupColumns: number;
+  readonly inner: number;
+  readonly columns: number;
+  readonly runtimeLayout: string;
+  readonly binding: BufferBinding;
+  readonly preparation: { destroy(): void };
+}
+
+/** gemm.ts:358-373 */
+export interface GemmDescriptor {
+  readonly label: string;
+  readonly a: ArenaSlice;
+  readonly b: GpuTensor;
+  readonly bPalette?: GpuTensor;
+  readonly paletteGroupColumns?: number;
+  readonly output: ArenaSlice;
+  readonly rows: number;
+  readonly inner: number;
+  readonly columns: number;
+  readonly bias?: GpuTensor;
+  readonly residual?: ArenaSlice;
+  readonly residualScale?: number;
+  readonly activation?: GemmActivation;
+  readonly preparedPaletteWeight?: PreparedPaletteWeight;
+}
+
+export interface GemmPlan {
+  readonly workgroups: readonly [number, number, number];
+  readonly blockThreads: number;
+  readonly tileRows: number;
+  readonly tileColumns: number;
+  readonly splitInner: number;
+  readonly ldsBytes: number;
+  readonly workspaceBytes: number;
+  readonly flops: number;
+  readonly algorithmicBytes: number;
+  readonly kernel: string;
+}
+
+/** gemm.ts:400-470, encoder.ts:308-316 (ManagedDispatch) */
+export declare class GemmDispatch {
+  readonly label: string;
+  readonly output: ArenaSlice;
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, shape?: EncoderDispatchShape): void;
+  destroy(): void;
+  plan(activeRows?: number): GemmPlan;
+}
+
+export interface GemmKernelOptions {
+  /** Accept shapes outside the reference's 15 production signatures. */
+  readonly allowSyntheticShapes?: boolean;
+}
+
+declare class PaletteGemmKernel {
+  readonly portableLoadEncoding: null;
+  readonly transientPaletteParameterBytes: number;
+  readonly transientPaletteParameterUsedSlots: number;
+  readonly transientPaletteDispatchCount: number;
+  readonly transientPaletteExpandedBytes: number;
+  createDispatch(descriptor: GemmDescriptor): GemmDispatch;
+  createPreparedPaletteWeight(descriptor: GemmDescriptor, scratchOffset: number): PreparedPaletteWeight;
+  validateDescriptor(descriptor: GemmDescriptor): void;
+  destroy(): void;
+}
+
+/** gemm.ts:483-855 */
+export declare class F16GemmKernel extends PaletteGemmKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena,
+                executionProfile?: { precision: "fp16" }, options?: GemmKernelOptions): Promise<F16GemmKernel>;
+}
+
+/** gemm.ts:2974-3340 */
+export declare class F32GemmKernel extends PaletteGemmKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena,
+                executionProfile?: { precision: "fp32" }, options?: GemmKernelOptions): Promise<F32GemmKernel>;
+}
+
+/** encoder.ts:356-368 */
+export interface EncoderGemmBackend {
+  readonly portableF16LoadEncoding: null;
+  readonly transientPaletteParameterBytes: number;
+  readonly transientPaletteParameterUsedSlots: number;
+  readonly transientPaletteDispatchCount: number;
+  readonly transientPaletteExpandedBytes: number;
+  createDispatch(descriptor: GemmDescriptor): GemmDispatch;
+  createPreparedPaletteWeight(descriptor: GemmDescriptor, scratchOffset: number): PreparedPaletteWeight;
+}
+
+export declare function createEncoderGemmBackend(kernel: F16GemmKernel | F32GemmKernel): EncoderGemmBackend;
+export declare function paletteBitsForLayout(layout: string): 5 | 6 | undefined;
+export declare function createGpuTensor(device: HipGpuDevice,
+                                        records: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord; label?: string },
+                                        data: ArrayBuffer | ArrayBufferView): GpuTensor;
+export declare function paletteTensorRecords(options: {
+  paletteBits: 5 | 6; inner: number; columns: number; paletteGroups?: number; paletteDtype?: "float16" | "float32";
+}): {
+  weight: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  palette: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+};

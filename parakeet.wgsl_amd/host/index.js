@@ -1,0 +1,661 @@
+// @ts-check
+/*
+ * parakeet.wgsl_amd/host - the palette GEMM op interface of parakeet.wgsl
+ * over HIP, for Node.
+ *
+ * It mirrors the reference's TypeScript GEMM owners so the encoder graph can
+ * bind to it unchanged:
+ *   F16GemmKernel / F32GemmKernel      src/webgpu/kernels/gemm.ts:483-855, :2974-3340
+ *     .create(device, arena, profile)  gemm.ts:519-619
+ *     .createDispatch(descriptor)      gemm.ts:621-704, :3097-3182
+ *     .createPreparedPaletteWeight     gemm.ts:706-748, :3186-3232
+ *     transientPalette* counters       gemm.ts:502-516 (always 0 here: the
+ *                                      fused kernels never expand weights)
+ *   GemmDispatch.encode / destroy      gemm.ts:400-470
+ *   createEncoderGemmBackend(kernel)   the EncoderGemmBackend adapter of
+ *                                      src/webgpu/encoder.ts:356-432
+ *   GpuActivationArena                 src/webgpu/arena.ts (slice, binding,
+ *                                      upload, destroy)
+ *   paletteBitsForLayout               src/model/runtime-plan.ts:352-368
+ * The WebGPU device, queue, buffers and command encoder are replaced by HIP
+ * equivalents with the same shapes (HipGpuDevice, queue.writeBuffer /
+ * submit / onSubmittedWorkDone, createCommandEncoder().finish()).
+ *
+ * Record-level checks (tensor layouts, dtypes, shapes of the package
+ * records) run here with the reference's messages; the numeric contract
+ * (shape, registry, palette geometry, binding sizes) is checked by the C ABI
+ * (pk_gemm_validate), which throws the same messages. Written as plain
+ * ES2019 CommonJS with JSDoc types (index.d.ts declares the API) so it runs
+ * on the Node 12 of this image without a TypeScript compiler.
+ */
+"use strict";
+
+const path = require("path");
+
+/** @type {any} */
+let nativeModule = null;
+function native() {
+  if (nativeModule === null) {
+    // The addon is built in-tree next to libpk_palette.so; there is no
+    // fallback: without it the host fails loudly.
+    nativeModule = require(path.join(__dirname, "..", "lib", "pk_napi.node"));
+  }
+  return nativeModule;
+}
+
+const STORAGE_ALIGNMENT = 256;
+const PALETTE_LAYOUT = "output-group-by-palette-lut";
+const F16_TILE_INNER = 32;
+const F32_TILE_INNER = 32;
+const FP32_PACKED_K = 4;
+const TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 8650752;
+const FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 17301504;
+const REQUIRE_PRODUCTION_SIGNATURE = 1;
+
+/** runtime-plan.ts:352-368 */
+function paletteBitsForLayout(layout) {
+  if (layout === "k-by-output-row-major-palette5-lsb-u32") return 5;
+  if (layout === "k-by-output-row-major-palette6-lsb-u32") return 6;
+  return undefined;
+}
+
+function shapeKey(shape) {
+  return Array.prototype.join.call(shape, ",");
+}
+
+function isSafe(n) {
+  return Number.isSafeInteger(n);
+}
+
+/* ---------------------------------------------------------------- device */
+
+class HipBuffer {
+  constructor(device, label, size, address) {
+    this.device = device;
+    this.label = label;
+    this.size = size;
+    /** device address (BigInt) */
+    this.address = address;
+    this.destroyed = false;
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().free(this.device.context, this.address);
+  }
+}
+
+class HipQueue {
+  constructor(device) {
+    this.device = device;
+  }
+
+  /** GPUQueue.writeBuffer: the copy is complete on return. */
+  writeBuffer(buffer, bufferOffset, data) {
+    if (buffer.destroyed) throw new Error(`${buffer.label} was destroyed`);
+    const bytes = data.byteLength;
+    if (!isSafe(bufferOffset) || bufferOffset < 0 || bufferOffset + bytes > buffer.size)
+      throw new RangeError(`Write does not fit ${buffer.label}`);
+    native().upload(this.device.context, buffer.address, bufferOffset, data);
+  }
+
+  /** Reads `size` bytes at `offset` back to the host (mapAsync readback). */
+  readBuffer(buffer, offset, size) {
+    if (!isSafe(offset) || !isSafe(size) || offset < 0 || size < 0 || offset + size > buffer.size)
+      return Promise.reject(new RangeError(`Read does not fit ${buffer.label}`));
+    return this.onSubmittedWorkDone().then(() => {
+      const out = new ArrayBuffer(size);
+      native().download(this.device.context, buffer.address, offset, out);
+      return out;
+    });
+  }
+
+  /** Runs the recorded commands in order on the device's stream. */
+  submit(commandBuffers) {
+    for (const commandBuffer of commandBuffers) {
+      if (commandBuffer.submitted) throw new Error(`${commandBuffer.label} was already submitted`);
+      commandBuffer.submitted = true;
+      for (const command of commandBuffer.commands) command();
+    }
+  }
+
+  /** Resolves once every submitted command has finished (a worker-thread wait). */
+  onSubmittedWorkDone() {
+    return native().synchronizeAsync(this.device.context);
+  }
+}
+
+class HipCommandEncoder {
+  constructor(device, label) {
+    this.device = device;
+    this.label = label;
+    /** @type {Array<() => void>} */
+    this.commands = [];
+    this.finished = false;
+  }
+
+  /** Appends one command (used by GemmDispatch.encode). */
+  record(command) {
+    if (this.finished) throw new Error(`${this.label} is already finished`);
+    this.commands.push(command);
+  }
+
+  finish() {
+    this.finished = true;
+    return { label: this.label, commands: this.commands.slice(), submitted: false };
+  }
+}
+
+/** Timestamp queries as HIP events (GpuTimestampRecorder, timestamp.ts:44-80). */
+class HipTimestampQuerySet {
+  constructor(device, count) {
+    this.device = device;
+    this.events = [];
+    for (let i = 0; i < count; ++i) this.events.push(native().eventCreate(device.context));
+  }
+
+  write(index) {
+    native().eventRecord(this.device.context, this.events[index], null);
+  }
+
+  /** Milliseconds between two written queries (after the work is done). */
+  elapsedMs(begin, end) {
+    return native().eventElapsedMs(this.device.context, this.events[begin], this.events[end]);
+  }
+
+  destroy() {
+    for (const e of this.events) native().eventDestroy(this.device.context, e);
+    this.events = [];
+  }
+}
+
+class HipGpuDevice {
+  constructor(context, index) {
+    this.context = context;
+    this.index = index;
+    this.info = native().deviceInfo(context);
+    this.queue = new HipQueue(this);
+    this.limits = { minStorageBufferOffsetAlignment: STORAGE_ALIGNMENT };
+    this.destroyed = false;
+  }
+
+  /** A HIP device; `index` selects the GPU (default 0). */
+  static create(options) {
+    const index = options && options.index !== undefined ? options.index : 0;
+    return new HipGpuDevice(native().contextCreate(index), index);
+  }
+
+  createBuffer(descriptor) {
+    const size = descriptor.size;
+    if (!isSafe(size) || size <= 0) throw new RangeError(`Invalid buffer size for ${descriptor.label}`);
+    return new HipBuffer(this, descriptor.label || "buffer", size, native().alloc(this.context, size));
+  }
+
+  createCommandEncoder(descriptor) {
+    return new HipCommandEncoder(this, (descriptor && descriptor.label) || "command-encoder");
+  }
+
+  createQuerySet(descriptor) {
+    if (descriptor.type !== "timestamp") throw new Error("only timestamp query sets exist");
+    return new HipTimestampQuerySet(this, descriptor.count);
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().contextDestroy(this.context);
+  }
+}
+
+/* ----------------------------------------------------------------- arena */
+
+/** arena.ts: one device allocation handed out as 256-byte aligned slices. */
+class GpuActivationArena {
+  constructor(device, byteLength, label) {
+    if (!isSafe(byteLength) || byteLength <= 0)
+      throw new RangeError("Activation arena must contain at least one buffer");
+    this.device = device;
+    this.label = label || "parakeet-activation-arena";
+    this.buffer = device.createBuffer({ label: this.label, size: byteLength });
+    this.buffers = [this.buffer];
+    this.bufferByteLengths = [byteLength];
+    this.byteLength = byteLength;
+    this.destroyed = false;
+  }
+
+  slice(label, byteOffset, byteLength) {
+    this.assertAlive();
+    if (
+      !isSafe(byteOffset) ||
+      !isSafe(byteLength) ||
+      byteOffset < 0 ||
+      byteLength <= 0 ||
+      byteOffset % STORAGE_ALIGNMENT !== 0 ||
+      byteLength % 4 !== 0 ||
+      byteOffset + byteLength > this.byteLength
+    ) {
+      throw new RangeError(`Invalid activation slice ${label}`);
+    }
+    return { label, byteOffset, byteLength };
+  }
+
+  binding(slice) {
+    this.assertAlive();
+    if (slice.byteOffset < 0 || slice.byteLength <= 0 || slice.byteOffset + slice.byteLength > this.byteLength)
+      throw new RangeError(`Invalid activation slice ${slice.label}`);
+    return { buffer: this.buffer, offset: slice.byteOffset, size: slice.byteLength };
+  }
+
+  upload(device, destination, data) {
+    const binding = this.binding(destination);
+    if (data.byteLength > destination.byteLength || data.byteLength % 4 !== 0)
+      throw new RangeError(`Upload does not fit ${destination.label}`);
+    device.queue.writeBuffer(binding.buffer, binding.offset, data);
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    this.buffer.destroy();
+  }
+
+  assertAlive() {
+    if (this.destroyed) throw new Error("Activation arena was destroyed");
+  }
+}
+
+/**
+ * A GpuTensor (package.ts:45-50) over a fresh device buffer holding `data`.
+ * `records` = {sourceRecord, runtimeRecord} in the package's record shape
+ * (manifest.ts:27-35, runtime-plan.ts:41-49).
+ */
+function createGpuTensor(device, records, data) {
+  const byteLength = records.runtimeRecord.byteLength;
+  if (data.byteLength !== byteLength) throw new RangeError("tensor data does not match its runtime record");
+  const buffer = device.createBuffer({ label: records.label || "tensor", size: byteLength });
+  device.queue.writeBuffer(buffer, 0, data);
+  return {
+    sourceRecord: records.sourceRecord,
+    runtimeRecord: records.runtimeRecord,
+    buffer,
+    binding: { buffer, offset: 0, size: byteLength },
+  };
+}
+
+/** Package records of a palettized weight and its palette (convert.py:2159-2203). */
+function paletteTensorRecords(options) {
+  const bits = options.paletteBits;
+  const dtype = options.paletteDtype || "float16";
+  const codesPerGroup = bits === 5 ? 32 : 16;
+  const wordsPerGroup = bits === 5 ? 5 : 3;
+  const groups = (options.inner * options.columns) / codesPerGroup;
+  const layout = `k-by-output-row-major-palette${bits}-lsb-u32`;
+  const weight = {
+    dtype: "uint32",
+    logicalShape: [options.inner, options.columns],
+    storageShape: [groups, wordsPerGroup],
+    byteLength: groups * wordsPerGroup * 4,
+    layout,
+  };
+  const entries = 1 << bits;
+  const paletteGroups = options.paletteGroups || 1;
+  const palette = {
+    dtype,
+    logicalShape: [paletteGroups, entries],
+    storageShape: [paletteGroups, entries],
+    byteLength: paletteGroups * entries * (dtype === "float16" ? 2 : 4),
+    layout: PALETTE_LAYOUT,
+  };
+  return {
+    weight: { sourceRecord: weight, runtimeRecord: weight },
+    palette: { sourceRecord: palette, runtimeRecord: palette },
+  };
+}
+
+/* ------------------------------------------------------ record checks */
+
+/** requireGemmShape (gemm.ts:971-1010; FP32 :3342-3400), numeric part first. */
+function requireWeightRecords(descriptor, fp32) {
+  if (
+    !isSafe(descriptor.rows) ||
+    descriptor.rows <= 0 ||
+    !isSafe(descriptor.inner) ||
+    descriptor.inner <= 0 ||
+    descriptor.inner % (fp32 ? F32_TILE_INNER : F16_TILE_INNER) !== 0 ||
+    !isSafe(descriptor.columns) ||
+    descriptor.columns <= 0 ||
+    descriptor.columns % (fp32 ? FP32_PACKED_K : 8) !== 0
+  ) {
+    throw new RangeError(`Unsupported${fp32 ? " FP32" : ""} GEMM shape for ${descriptor.label}`);
+  }
+  const source = descriptor.b.sourceRecord;
+  const paletteBits = paletteBitsForLayout(source.layout);
+  const what = fp32 ? " FP32" : "";
+  if (shapeKey(source.logicalShape) !== `${descriptor.inner},${descriptor.columns}`) {
+    throw new Error(
+      `${descriptor.label}${what} weight package does not match K=${descriptor.inner}, N=${descriptor.columns}`,
+    );
+  }
+  if (paletteBits === undefined || source.dtype !== "uint32") {
+    throw new Error(`${descriptor.label} has an unsupported${what} weight format`);
+  }
+  const codesPerGroup = paletteBits === 5 ? 32 : 16;
+  const wordsPerGroup = paletteBits === 5 ? 5 : 3;
+  const elements = descriptor.inner * descriptor.columns;
+  if (elements % codesPerGroup !== 0) {
+    throw new Error(`${descriptor.label}${what} palette codes are not group aligned`);
+  }
+  const groups = elements / codesPerGroup;
+  if (source.byteLength !== groups * wordsPerGroup * 4 || shapeKey(source.storageShape) !== `${groups},${wordsPerGroup}`) {
+    throw new Error(`${descriptor.label} has invalid packed${what} palette indices`);
+  }
+  return paletteBits;
+}
+
+/** requireRuntimeWeight's record part (gemm.ts:1069-1161; FP32 :3422-3470). */
+function requirePaletteRecords(descriptor, paletteBits, fp32) {
+  const runtime = descriptor.b.runtimeRecord;
+  const source = descriptor.b.sourceRecord;
+  const palette = descriptor.bPalette;
+  const entries = 1 << paletteBits;
+  const paletteDtype = fp32 ? "float32" : "float16";
+  const elem = fp32 ? 4 : 2;
+  const groups = palette === undefined ? undefined : palette.runtimeRecord.storageShape[0];
+  if (
+    paletteBitsForLayout(runtime.layout) !== paletteBits ||
+    runtime.dtype !== "uint32" ||
+    runtime.layout !== source.layout ||
+    shapeKey(runtime.logicalShape) !== `${descriptor.inner},${descriptor.columns}` ||
+    shapeKey(runtime.storageShape) !== shapeKey(source.storageShape) ||
+    runtime.byteLength !== source.byteLength ||
+    palette === undefined ||
+    palette.sourceRecord.dtype !== paletteDtype ||
+    palette.sourceRecord.layout !== PALETTE_LAYOUT ||
+    palette.runtimeRecord.dtype !== paletteDtype ||
+    palette.runtimeRecord.layout !== PALETTE_LAYOUT ||
+    shapeKey(palette.runtimeRecord.logicalShape) !== shapeKey(palette.sourceRecord.logicalShape) ||
+    shapeKey(palette.runtimeRecord.storageShape) !== `${groups},${entries}` ||
+    palette.runtimeRecord.byteLength !== groups * entries * elem ||
+    !isSafe(descriptor.paletteGroupColumns) ||
+    descriptor.paletteGroupColumns <= 0 ||
+    descriptor.paletteGroupColumns * groups !== descriptor.columns
+  ) {
+    throw new Error(`${descriptor.label} has invalid transient${fp32 ? " FP32" : ""} palette weights`);
+  }
+  return groups;
+}
+
+/* ------------------------------------------------------------ kernels */
+
+class GemmDispatch {
+  constructor(label, output, op, rows) {
+    this.label = label;
+    this.output = output;
+    this.op = op;
+    this.rows = rows;
+    this.destroyed = false;
+  }
+
+  /**
+   * GemmDispatch.encode (gemm.ts:419-463): records the launch; `shape`
+   * re-plans for an active row prefix; `timestampWrites` = {querySet,
+   * beginningOfPassWriteIndex?, endOfPassWriteIndex?}.
+   */
+  encode(encoder, timestampWrites, shape) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    let rows = 0;
+    if (shape !== undefined) {
+      const activeRows = shape.rows;
+      if (!isSafe(activeRows) || activeRows <= 0 || activeRows > this.rows)
+        throw new RangeError(`${this.label} active rows must be in [1, ${this.rows}]`);
+      rows = activeRows;
+    }
+    const op = this.op;
+    encoder.record(() => {
+      if (timestampWrites && timestampWrites.beginningOfPassWriteIndex !== undefined)
+        timestampWrites.querySet.write(timestampWrites.beginningOfPassWriteIndex);
+      native().gemmEnqueue(op, rows, null);
+      if (timestampWrites && timestampWrites.endOfPassWriteIndex !== undefined)
+        timestampWrites.querySet.write(timestampWrites.endOfPassWriteIndex);
+    });
+  }
+
+  /** Idempotent (gemm.ts:465-469). */
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().gemmDestroy(this.op);
+  }
+
+  /** The launch a given active row count gets (planF16SubgroupGemm). */
+  plan(activeRows) {
+    return native().gemmPlan(this.op, activeRows || 0);
+  }
+}
+
+class PaletteGemmKernel {
+  constructor(device, arena, fp32, options) {
+    this.device = device;
+    this.arena = arena;
+    this.fp32 = fp32;
+    this.productionOnly = !(options && options.allowSyntheticShapes);
+    this.destroyed = false;
+    this.portableLoadEncoding = null;
+  }
+
+  get transientPaletteParameterBytes() {
+    return 0;
+  }
+
+  get transientPaletteParameterUsedSlots() {
+    return 0;
+  }
+
+  /** No palette expansion ever runs: the kernels decode in registers. */
+  get transientPaletteDispatchCount() {
+    return 0;
+  }
+
+  get transientPaletteExpandedBytes() {
+    return 0;
+  }
+
+  kernelName() {
+    return this.fp32 ? "Parakeet FP32 GEMM kernel" : "Parakeet GEMM kernel";
+  }
+
+  /** The native descriptor of a reference GemmDescriptor. */
+  nativeDescriptor(descriptor, prepared) {
+    const fp32 = this.fp32;
+    const paletteBits = requireWeightRecords(descriptor, fp32);
+    const groups = requirePaletteRecords(descriptor, paletteBits, fp32);
+    if (this.productionOnly) {
+      const expanded = descriptor.inner * descriptor.columns * (fp32 ? 4 : 2);
+      const limit = fp32 ? FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES : TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES;
+      if (expanded > limit) {
+        throw new Error(`${descriptor.label} exceeds transient${fp32 ? " FP32" : ""} palette scratch`);
+      }
+    }
+    const a = this.arena.binding(descriptor.a);
+    const out = this.arena.binding(descriptor.output);
+    const b = descriptor.b.binding;
+    const palette = descriptor.bPalette.binding;
+    /** @type {any} */
+    const d = {
+      label: descriptor.label,
+      flags: this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0,
+      precision: fp32 ? "f32" : "f16",
+      paletteBits,
+      rows: descriptor.rows,
+      inner: descriptor.inner,
+      columns: descriptor.columns,
+      paletteGroups: groups,
+      paletteGroupColumns: descriptor.paletteGroupColumns,
+      a: a.buffer.address + BigInt(a.offset),
+      aBytes: a.size,
+      palette: palette.buffer.address + BigInt(palette.offset),
+      paletteBytes: palette.size,
+      output: out.buffer.address + BigInt(out.offset),
+      outputBytes: out.size,
+      activation: descriptor.activation || "none",
+    };
+    if (prepared === undefined) {
+      d.packed = b.buffer.address + BigInt(b.offset);
+      d.packedBytes = b.size;
+    } else {
+      d.prepared = prepared.native;
+    }
+    if (descriptor.bias !== undefined) {
+      d.bias = descriptor.bias.binding.buffer.address + BigInt(descriptor.bias.binding.offset);
+      d.biasBytes = descriptor.bias.binding.size;
+    }
+    if (descriptor.residual !== undefined) {
+      const r = this.arena.binding(descriptor.residual);
+      d.residual = r.buffer.address + BigInt(r.offset);
+      d.residualBytes = r.size;
+    }
+    if (descriptor.residualScale !== undefined) d.residualScale = descriptor.residualScale;
+    return d;
+  }
+
+  /** The descriptor contract alone (no device work). */
+  validateDescriptor(descriptor) {
+    native().gemmValidate(this.nativeDescriptor(descriptor, undefined));
+  }
+
+  createDispatch(descriptor) {
+    if (this.destroyed) throw new Error(`${this.kernelName()} was destroyed`);
+    const prepared = descriptor.preparedPaletteWeight;
+    if (prepared !== undefined) {
+      if (
+        prepared.source !== descriptor.b ||
+        prepared.palette !== descriptor.bPalette ||
+        prepared.paletteGroupColumns !== descriptor.paletteGroupColumns ||
+        prepared.inner !== descriptor.inner ||
+        prepared.columns !== descriptor.columns
+      ) {
+        throw new Error(`${descriptor.label} has a mismatched prepared palette weight`);
+      }
+    }
+    const d = this.nativeDescriptor(descriptor, prepared);
+    const op = native().gemmCreate(this.device.context, d);
+    return new GemmDispatch(descriptor.label, descriptor.output, op, descriptor.rows);
+  }
+
+  /**
+   * createPreparedPaletteWeight (gemm.ts:706-748): the weight is re-ordered
+   * once into the kernels' operand order; several dispatches may share it.
+   * `scratchOffset` is checked as the reference checks its scratch slice.
+   */
+  createPreparedPaletteWeight(descriptor, scratchOffset) {
+    if (this.destroyed) throw new Error(`${this.kernelName()} was destroyed`);
+    if (descriptor.preparedPaletteWeight !== undefined)
+      throw new Error(`${descriptor.label} cannot prepare an already prepared weight`);
+    const d = this.nativeDescriptor(descriptor, undefined);
+    native().gemmValidate(d);
+    const size = descriptor.inner * descriptor.columns * (this.fp32 ? 4 : 2);
+    const limit = this.fp32 ? FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES : TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES;
+    if (
+      !isSafe(scratchOffset) ||
+      scratchOffset < 0 ||
+      scratchOffset % STORAGE_ALIGNMENT !== 0 ||
+      (this.productionOnly && scratchOffset + size > limit)
+    ) {
+      throw new RangeError(
+        `${descriptor.label} has an invalid${this.fp32 ? " FP32" : ""} transient palette scratch slice`,
+      );
+    }
+    const weight = native().preparedWeightCreate(this.device.context, {
+      label: descriptor.label,
+      paletteBits: d.paletteBits,
+      inner: descriptor.inner,
+      columns: descriptor.columns,
+      packed: d.packed,
+      packedBytes: d.packedBytes,
+    });
+    return {
+      source: descriptor.b,
+      palette: descriptor.bPalette,
+      paletteGroupColumns: descriptor.paletteGroupColumns,
+      inner: descriptor.inner,
+      columns: descriptor.columns,
+      runtimeLayout: "operand-order",
+      binding: descriptor.b.binding,
+      preparation: { destroy: () => native().preparedWeightDestroy(weight) },
+      native: weight,
+    };
+  }
+
+  destroy() {
+    this.destroyed = true;
+  }
+}
+
+class F16GemmKernel extends PaletteGemmKernel {
+  /**
+   * create(device, arena, executionProfile?, options?) - the reference's
+   * fixed production signatures are enforced unless
+   * options.allowSyntheticShapes is set.
+   */
+  static create(device, arena, executionProfile, options) {
+    if (executionProfile !== undefined && executionProfile.precision !== "fp16")
+      return Promise.reject(new Error("Parakeet FP16 GEMM requires an FP16 execution profile"));
+    return Promise.resolve(new F16GemmKernel(device, arena, false, options));
+  }
+}
+
+class F32GemmKernel extends PaletteGemmKernel {
+  static create(device, arena, executionProfile, options) {
+    if (executionProfile !== undefined && executionProfile.precision !== "fp32")
+      return Promise.reject(new Error("Parakeet FP32 GEMM requires an FP32 execution profile"));
+    return Promise.resolve(new F32GemmKernel(device, arena, true, options));
+  }
+}
+
+/** The EncoderGemmBackend adapter of encoder.ts:356-432. */
+function createEncoderGemmBackend(kernel) {
+  return {
+    get portableF16LoadEncoding() {
+      return kernel.portableLoadEncoding;
+    },
+    get transientPaletteParameterBytes() {
+      return kernel.transientPaletteParameterBytes;
+    },
+    get transientPaletteParameterUsedSlots() {
+      return kernel.transientPaletteParameterUsedSlots;
+    },
+    get transientPaletteDispatchCount() {
+      return kernel.transientPaletteDispatchCount;
+    },
+    get transientPaletteExpandedBytes() {
+      return kernel.transientPaletteExpandedBytes;
+    },
+    createDispatch(descriptor) {
+      return kernel.createDispatch(descriptor);
+    },
+    createPreparedPaletteWeight(descriptor, scratchOffset) {
+      return kernel.createPreparedPaletteWeight(descriptor, scratchOffset);
+    },
+  };
+}
+
+module.exports = {
+  native,
+  paletteBitsForLayout,
+  HipGpuDevice,
+  HipBuffer,
+  HipCommandEncoder,
+  GpuActivationArena,
+  createGpuTensor,
+  paletteTensorRecords,
+  F16GemmKernel,
+  F32GemmKernel,
+  GemmDispatch,
+  createEncoderGemmBackend,
+  TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES,
+  FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES,
+  F16_TILE_INNER,
+  F32_TILE_INNER,
+  FP32_PACKED_K,
+};

@@ -155,6 +155,7 @@ SIGNATURES = {
     "pk_prepared_weight_destroy": (ctypes.c_int, [_VP]),
     "pk_prepared_weight_bytes": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint64)]),
     "pk_gemm_create": (ctypes.c_int, [_VP, ctypes.POINTER(GemmDesc), _VP, _PPV]),
+    "pk_gemm_validate": (ctypes.c_int, [ctypes.POINTER(GemmDesc)]),
     "pk_gemm_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
     "pk_gemm_destroy": (ctypes.c_int, [_VP]),
     "pk_gemm_release": (ctypes.c_int, [_VP]),
