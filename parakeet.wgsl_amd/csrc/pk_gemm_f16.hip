@@ -33,44 +33,12 @@
 // Epilogue (src/webgpu/kernels/gemm.ts:2006-2044): f32 value, + bias[n],
 // SiLU v/(1+exp(-clamp(v,-20,20))) or ReLU, then residual + scale * value,
 // rounded to f16.
-#include "pk_internal.h"
+#include "pk_f16_common.h"
 
 namespace pk {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-// Code u (0..31) of a lane's 32-code stream, LSB first at bit u*BITS.
-template <int BITS>
-__device__ __forceinline__ uint32_t lane_code(const uint32_t (&w)[BITS], int u) {
-  constexpr uint32_t mask = (1u << BITS) - 1u;
-  const int bit = u * BITS;
-  const int word = bit >> 5;
-  const int shift = bit & 31;
-  if (shift + BITS <= 32) return (w[word] >> shift) & mask;
-  return __builtin_amdgcn_alignbit(w[word + 1], w[word], shift) & mask;
-}
-
-// The 8 weights of sub-step s: palette entries gathered from LDS.
-template <int BITS>
-__device__ __forceinline__ half8 decode_fragment(const uint32_t (&w)[BITS], int s,
-                                                 const _Float16* lut) {
-  half8 f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) f[t] = lut[lane_code<BITS>(w, s * 8 + t)];
-  return f;
-}
-
-__device__ __forceinline__ float silu(float v) {
-  const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
-  return v / (1.0f + expf(-bounded));
-}
-
-__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
-}
+using namespace f16;
 
 // GENERAL: the tile's columns may span several palette groups (per-lane
 // palette base) and K may be 32 (mod 64). Otherwise (the common case) the
@@ -308,192 +276,51 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_kernel(GemmArgs args) {
     if (i + 1u < steps) step(i + 1u, c1, c2, c0, s1, s2);
   }
 
-  // Split-K: publish this partial; only the last workgroup of the tile
-  // continues, with the sum of all partials in split order.
-  if (S > 1) {
-    constexpr int EPT = R * C * 16;  // f32 accumulator values per thread
-    float* mine = args.partials + ((uint64_t)tile * S + split) * (uint64_t)(EPT * T);
-#pragma unroll
-    for (int mi = 0; mi < R; ++mi)
-#pragma unroll
-      for (int ci = 0; ci < C; ++ci)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int e4 = (mi * C + ci) * 4 + q;
-          *reinterpret_cast<float4*>(mine + ((uint64_t)e4 * T + tid) * 4) =
-              make_float4(acc[mi][ci][4 * q], acc[mi][ci][4 * q + 1], acc[mi][ci][4 * q + 2],
-                          acc[mi][ci][4 * q + 3]);
-        }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last_flag = atomicAdd(args.counters + tile, 1u) == S - 1u;
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    if (tid == 0) args.counters[tile] = 0u;
-    const float* base = args.partials + (uint64_t)tile * S * (uint64_t)(EPT * T);
-#pragma unroll
-    for (int mi = 0; mi < R; ++mi)
-#pragma unroll
-      for (int ci = 0; ci < C; ++ci)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int e4 = (mi * C + ci) * 4 + q;
-          float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          for (uint32_t p = 0; p < S; ++p) {
-            float4 v;
-            if (p == split)
-              v = make_float4(acc[mi][ci][4 * q], acc[mi][ci][4 * q + 1], acc[mi][ci][4 * q + 2],
-                              acc[mi][ci][4 * q + 3]);
-            else
-              v = *reinterpret_cast<const float4*>(base + (uint64_t)p * (EPT * T) + ((uint64_t)e4 * T + tid) * 4);
-            sum.x += v.x;
-            sum.y += v.y;
-            sum.z += v.z;
-            sum.w += v.w;
-          }
-          acc[mi][ci][4 * q] = sum.x;
-          acc[mi][ci][4 * q + 1] = sum.y;
-          acc[mi][ci][4 * q + 2] = sum.z;
-          acc[mi][ci][4 * q + 3] = sum.w;
-        }
-  }
+  // Split-K: only the last workgroup of the tile continues, with the sum of
+  // all partials in split order.
+  if (S > 1 && !split_k_reduce<R, C, T>(args, acc, tile, split, tid, &last_flag)) return;
 
-  // Epilogue. In registers a lane holds row m = m0 + (wave_m*R + mi)*32 + j
-  // and, for q = 0..3, the 4 columns n = n0 + (wave_n*C + ci)*32 + 8q + 4h
-  // + {0..3}. The output tile goes out through an LDS staging area (the
-  // activation buffers, free after the K loop) so global traffic is 16-byte
-  // chunks along rows: a pass stages MPP m-blocks of every wavefront as
-  // row-major f16 rows of BN columns, 8-byte units XOR-swizzled by row.
-  // With a residual, its tile is first loaded the same way so that
-  // residual + scale * value is formed in f32 and rounded once.
-  {
-    constexpr int MPP = (R * 128 / BN) >= 1 ? (R * 128 / BN < R ? R * 128 / BN : R) : 1;
-    constexpr int SR = WM * MPP * 32;     // staged rows per pass
-    constexpr int ROWB = BN * 2;          // bytes per staged row
-    constexpr int CPR = BN / 8;           // 16-byte chunks per staged row
-    static_assert(SR * ROWB <= 2 * BM * ROW_BYTES, "epilogue staging exceeds the activation buffers");
-    static_assert(R % MPP == 0, "epilogue passes must cover whole m-blocks");
-    static_assert(BN >= 128, "the staging swizzle needs rows of at least 32 8-byte units");
-    auto stage_at = [&](int sr, int unit) { return sr * ROWB + ((unit ^ ((sr & 15) << 1)) << 3); };
-    auto chunk_row = [&](int sr, int mi0) {
-      return m0 + (uint32_t)(((sr / 32) / MPP * R + mi0 + (sr / 32) % MPP) * 32 + (sr & 31));
-    };
-    const _Float16* residual = static_cast<const _Float16*>(args.residual);
-    _Float16* out = static_cast<_Float16*>(args.out);
-    __syncthreads();
-#pragma unroll
-    for (int mi0 = 0; mi0 < R; mi0 += MPP) {
-      if (residual) {
-        for (int chunk = tid; chunk < SR * CPR; chunk += T) {
-          const int sr = chunk / CPR, c16 = chunk % CPR;
-          const uint32_t m = chunk_row(sr, mi0);
-          const uint32_t n = n0 + (uint32_t)c16 * 8u;
-          if (m < M && n < N)
-            *reinterpret_cast<uint4*>(a_lds + stage_at(sr, 2 * c16)) =
-                *reinterpret_cast<const uint4*>(residual + (uint64_t)m * N + n);
-        }
-        __syncthreads();
-      }
-#pragma unroll
-      for (int ml = 0; ml < MPP; ++ml) {
-        const int mi = mi0 + ml;
-        if (mi >= R) break;
-        const int sr = (wave_m * MPP + ml) * 32 + j;
-#pragma unroll
-        for (int ci = 0; ci < C; ++ci) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int unit = (wave_n * C + ci) * 8 + 2 * q + h;
-            const uint32_t n = n0 + (uint32_t)unit * 4u;
-            float v0 = acc[mi][ci][4 * q], v1 = acc[mi][ci][4 * q + 1];
-            float v2 = acc[mi][ci][4 * q + 2], v3 = acc[mi][ci][4 * q + 3];
-            if (args.bias && n < N) {
-              const float4 b = *reinterpret_cast<const float4*>(args.bias + n);
-              v0 += b.x;
-              v1 += b.y;
-              v2 += b.z;
-              v3 += b.w;
-            }
-            if (args.activation == kActSilu) {
-              v0 = silu(v0);
-              v1 = silu(v1);
-              v2 = silu(v2);
-              v3 = silu(v3);
-            } else if (args.activation == kActRelu) {
-              v0 = fmaxf(v0, 0.0f);
-              v1 = fmaxf(v1, 0.0f);
-              v2 = fmaxf(v2, 0.0f);
-              v3 = fmaxf(v3, 0.0f);
-            }
-            uint2* slot = reinterpret_cast<uint2*>(a_lds + stage_at(sr, unit));
-            if (residual) {
-              const uint2 rb = *slot;
-              const float sc = args.residual_scale;
-              v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.x & 0xffffu)) + sc * v0;
-              v1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.x >> 16)) + sc * v1;
-              v2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.y & 0xffffu)) + sc * v2;
-              v3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rb.y >> 16)) + sc * v3;
-            }
-            *slot = make_uint2(pack_half2(v0, v1), pack_half2(v2, v3));
-          }
-        }
-      }
-      __syncthreads();
-      for (int chunk = tid; chunk < SR * CPR; chunk += T) {
-        const int sr = chunk / CPR, c16 = chunk % CPR;
-        const uint32_t m = chunk_row(sr, mi0);
-        const uint32_t n = n0 + (uint32_t)c16 * 8u;
-        if (m < M && n < N)
-          *reinterpret_cast<uint4*>(out + (uint64_t)m * N + n) =
-              *reinterpret_cast<const uint4*>(a_lds + stage_at(sr, 2 * c16));
-      }
-      __syncthreads();
-    }
-  }
+  store_tile<WM, WN, R, C, 2 * BM * ROW_BYTES>(args, acc, a_lds, m0, n0, wave_m, wave_n, j, h, tid);
 }
 
-struct Variant {
-  TileShape shape;
-  const char* name5;
-  const char* name6;
-  void (*single[2])(GemmArgs);  // [bits == 6]
-  void (*general[2])(GemmArgs);
-};
-
 #define PK_F16_VARIANT(WM, WN, R, C)                                                              \
-  Variant {                                                                                       \
+  F16Variant {                                                                                    \
     TileShape{WM, WN, R, C}, "pk_gemm_f16_b5_w" #WM "x" #WN "_m" #R "n" #C,                       \
         "pk_gemm_f16_b6_w" #WM "x" #WN "_m" #R "n" #C,                                            \
         {gemm_f16_kernel<5, WM, WN, R, C, false>, gemm_f16_kernel<6, WM, WN, R, C, false>},       \
         {gemm_f16_kernel<5, WM, WN, R, C, true>, gemm_f16_kernel<6, WM, WN, R, C, true>}          \
   }
 
-const Variant kVariants[] = {
-    PK_F16_VARIANT(1, 4, 3, 2),  // 96 x 256
-    PK_F16_VARIANT(1, 4, 4, 2),  // 128 x 256
-    PK_F16_VARIANT(1, 4, 6, 1),  // 192 x 128
-    PK_F16_VARIANT(1, 4, 4, 1),  // 128 x 128
-    PK_F16_VARIANT(1, 4, 8, 1),  // 256 x 128
-    PK_F16_VARIANT(1, 4, 2, 2),  // 64 x 256
-    PK_F16_VARIANT(1, 4, 2, 1),  // 64 x 128
+const F16Variant kVariants[] = {
     PK_F16_VARIANT(1, 4, 1, 1),  // 32 x 128
-    PK_F16_VARIANT(2, 2, 4, 2),  // 256 x 128
+    PK_F16_VARIANT(1, 4, 2, 1),  // 64 x 128
+    PK_F16_VARIANT(1, 4, 4, 1),  // 128 x 128
+    PK_F16_VARIANT(1, 4, 6, 1),  // 192 x 128
+    PK_F16_VARIANT(1, 4, 2, 2),  // 64 x 256
+    PK_F16_VARIANT(1, 4, 3, 2),  // 96 x 256
 };
+
+constexpr int kLocal = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
+
+const F16Variant& variant_at(int index) {
+  return index < kLocal ? kVariants[index] : f16_shared_variant(index - kLocal);
+}
 
 }  // namespace
 
-int f16_variant_count() { return (int)(sizeof(kVariants) / sizeof(kVariants[0])); }
-TileShape f16_variant(int index) { return kVariants[index].shape; }
+// f16 tile shapes: the per-wavefront-decode kernels of this file, then the
+// shared-decode kernels of pk_gemm_f16_shared.hip.
+int f16_variant_count() { return kLocal + f16_shared_variant_count(); }
+TileShape f16_variant(int index) { return variant_at(index).shape; }
 const char* f16_variant_name(int bits, int index) {
-  return bits == 5 ? kVariants[index].name5 : kVariants[index].name6;
+  return bits == 5 ? variant_at(index).name5 : variant_at(index).name6;
 }
 
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream) {
-  const Variant& v = kVariants[variant];
+  const F16Variant& v = variant_at(variant);
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;
   if (groups == 0) return hipSuccess;
-  // The fast kernel needs K % 64 == 0 and every tile inside one palette
+  // The fast kernels need K % 64 == 0 and every tile inside one palette
   // group (its palette staged at a fixed LDS address); tiles start at
   // multiples of the tile width, so the latter holds with one group or when
   // the group width is a multiple of the tile width.

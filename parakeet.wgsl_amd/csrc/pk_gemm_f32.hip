@@ -24,9 +24,13 @@ __device__ __forceinline__ uint32_t lane_code(const uint32_t* w, int u) {
   return __builtin_amdgcn_alignbit(w[word + 1], w[word], shift) & mask;
 }
 
+// SiLU of the reference epilogue, v / (1 + exp(-clamp(v, -20, 20)))
+// (gemm.ts:2847-2869 with the activation of :2006-2044): clamp, exp as
+// v_exp_f32 of the base-2 argument and v_rcp_f32, each within ~1 ulp.
 __device__ __forceinline__ float silu(float v) {
-  const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
-  return v / (1.0f + expf(-bounded));
+  const float bounded = __builtin_amdgcn_fmed3f(v, -20.0f, 20.0f);
+  const float e = __builtin_amdgcn_exp2f(bounded * -1.4426950408889634f);
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 template <int BITS, int WM, int WN, int MB, int NB>
