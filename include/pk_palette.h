@@ -23,7 +23,7 @@
  *                           (:971-1011), requireProductionSpecialization
  *                           (:1031-1067), requireRuntimeWeight (:1069-1161)
  *   pk_gemm_validate        the same contract checks without a device
- *   pk_gemm_enqueue         GemmDispatch.encode(encoder, timestampWrites,
+ *   pk_gemm_enqueue(_timed) GemmDispatch.encode(encoder, timestampWrites,
  *                           shape) (gemm.ts:419-463; F32 twin :2912-2960)
  *   pk_gemm_destroy         GemmDispatch.destroy (gemm.ts:465-469)
  *   pk_prepared_weight_*    F16GemmKernel.createPreparedPaletteWeight
@@ -149,7 +149,9 @@ typedef struct pk_weight_desc {
 int pk_prepared_weight_create(pk_context *ctx, const pk_weight_desc *desc,
                               void *stream, pk_prepared_weight **out);
 int pk_prepared_weight_destroy(pk_prepared_weight *weight);
-/* Device bytes held by the prepared weight. */
+/* Device bytes held by the prepared weight: the codes in MFMA operand order
+ * (as many bits per code as the packed format) plus the pair-code layout of
+ * the large-M kernels (16 bits per two codes, K and N padded to 64 and 32). */
 int pk_prepared_weight_bytes(const pk_prepared_weight *weight, uint64_t *bytes);
 
 /* ---- GEMM ----------------------------------------------------------------- */
@@ -196,6 +198,12 @@ int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,
 int pk_gemm_validate(const pk_gemm_desc *desc);
 /* Launch on `stream` for the first `active_rows` rows (0 = all rows). */
 int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
+/* pk_gemm_enqueue with the timestampWrites of GemmDispatch.encode
+   (gemm.ts:419-463): the kernel's own dispatch stamps `start_event` when it
+   begins and `end_event` when it ends (either may be NULL; both from
+   pk_event_create), so timing adds nothing to the stream. */
+int pk_gemm_enqueue_timed(pk_gemm_op *op, uint32_t active_rows, void *stream,
+                          void *start_event, void *end_event);
 /* Releases the op's device resources. Idempotent: a second call is a no-op
    returning PK_OK; enqueue after destroy returns PK_DESTROYED. The handle
    itself stays valid until pk_gemm_release. */
@@ -208,8 +216,11 @@ int pk_gemm_release(pk_gemm_op *op);
    benchmark's sweeps). Both resize the op's split-K workspace and must not
    be called while a launch of the op is in flight. */
 int pk_gemm_variant_count(int precision);
+/* Selecting a variant without a split-K path (the f16 pair-code K-split
+   variants, every f32 variant) also resets the split count to 1. */
 int pk_gemm_set_variant(pk_gemm_op *op, int variant);
-/* 1 <= splits <= ceil(inner / 64) for f16; f32 ops take 1 only. */
+/* 1 <= splits <= ceil(inner / 64) for the f16 operand-order variants;
+   other variants take 1 only (PK_RANGE_ERROR otherwise). */
 int pk_gemm_set_splits(pk_gemm_op *op, uint32_t splits);
 
 typedef struct pk_gemm_plan_info {

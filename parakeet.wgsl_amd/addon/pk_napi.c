@@ -493,14 +493,15 @@ static napi_value js_gemm_create(napi_env env, napi_callback_info info) {
   return ext;
 }
 
-/* gemmEnqueue(op, activeRows, stream?) */
+/* gemmEnqueue(op, activeRows, stream?, startEvent?, endEvent?) */
 static napi_value js_gemm_enqueue(napi_env env, napi_callback_info info) {
-  napi_value argv[3];
+  napi_value argv[5];
   uint32_t rows = 0;
-  if (!get_args(env, info, 3, argv)) return NULL;
+  if (!get_args(env, info, 5, argv)) return NULL;
   if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &rows))
     return bad_argument(env, "active rows must be a non-negative integer");
-  PK_CALL(env, pk_gemm_enqueue((pk_gemm_op *)get_external(env, argv[0]), rows, get_external(env, argv[2])));
+  PK_CALL(env, pk_gemm_enqueue_timed((pk_gemm_op *)get_external(env, argv[0]), rows, get_external(env, argv[2]),
+                                     get_external(env, argv[3]), get_external(env, argv[4])));
   return undefined(env);
 }
 

@@ -85,8 +85,9 @@ struct pk_prepared_weight {
   std::string label;
   int bits = 5;
   uint32_t inner = 0, columns = 0;
-  uint32_t* codes = nullptr;  // operand-order codes (device)
-  uint64_t bytes = 0;
+  uint32_t* codes = nullptr;      // operand-order codes (device)
+  uint8_t* pair_codes = nullptr;  // pair-code layout (device)
+  uint64_t bytes = 0;             // both layouts
   std::atomic<int> refs{1};
   bool owner_released = false;
 };
@@ -112,9 +113,10 @@ namespace {
 void weight_unref(pk_prepared_weight* w) {
   if (!w) return;
   if (w->refs.fetch_sub(1) == 1) {
-    if (w->codes) {
+    if (w->codes || w->pair_codes) {
       (void)hipSetDevice(w->ctx->device);
-      (void)hipFree(w->codes);
+      if (w->codes) (void)hipFree(w->codes);
+      if (w->pair_codes) (void)hipFree(w->pair_codes);
     }
     delete w;
   }
@@ -137,17 +139,25 @@ int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, ui
   w->bits = bits;
   w->inner = inner;
   w->columns = columns;
-  w->bytes = pk::operand_order_words(bits, inner, columns) * 4u;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->codes), w->bytes);
+  const uint64_t operand_bytes = pk::operand_order_words(bits, inner, columns) * 4u;
+  const uint64_t pair_bytes = pk::pair_code_bytes(inner, columns);
+  w->bytes = operand_bytes + pair_bytes;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->codes), operand_bytes);
+  if (e == hipSuccess) {
+    e = hipMalloc(reinterpret_cast<void**>(&w->pair_codes), pair_bytes);
+    if (e != hipSuccess) (void)hipFree(w->codes);
+  }
   if (e != hipSuccess) {
     delete w;
     return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
                 safe_label(label), (unsigned long long)w->bytes, hipGetErrorString(e));
   }
   e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
+  if (e == hipSuccess) e = pk::launch_to_pair_codes(bits, packed, inner, columns, w->pair_codes, stream);
   if (e == hipSuccess) e = hipStreamSynchronize(stream);
   if (e != hipSuccess) {
     (void)hipFree(w->codes);
+    (void)hipFree(w->pair_codes);
     delete w;
     return fail(PK_DEVICE_ERROR, "%s: palette code preparation failed: %s", safe_label(label),
                 hipGetErrorString(e));
@@ -189,26 +199,42 @@ struct Plan {
   uint32_t splits;
 };
 
-int find_variant(int precision, int waves_m, int waves_n, int m_blocks, int n_blocks) {
+int find_variant(int precision, int waves_m, int waves_n, int m_blocks, int n_blocks, int k_split = 1,
+                 bool pair_codes = false) {
   const int count = precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
   for (int i = 0; i < count; ++i) {
     const pk::TileShape s = shape_of(precision, i);
-    if (s.waves_m == waves_m && s.waves_n == waves_n && s.m_blocks == m_blocks && s.n_blocks == n_blocks)
+    const bool bytes = precision == PK_PRECISION_F16 && !pk::f16_variant_splits(i);
+    if (s.waves_m == waves_m && s.waves_n == waves_n && s.m_blocks == m_blocks && s.n_blocks == n_blocks &&
+        s.k_split == k_split && bytes == pair_codes)
       return i;
   }
   return 0;
 }
 
 // Launch planner. The f16 choice follows MI355X measurements of every
-// compiled tile shape and split count over the encoder's GEMM shapes
-// (M 64..3008, K 1024/4096, N 1024..4096): the 64 x 128 tile (four
-// wavefronts of 2 x 1 MFMA blocks) is fastest or within 5% everywhere
-// above 256 rows, the 32 x 128 tile below, and split-K never paid for its
-// partial-tile traffic. f32 keeps its own smallest-cost shape.
+// compiled tile shape over the encoder's GEMM shapes (M 64..3008, K
+// 1024/4096, N 1024..4096). The pair-code K-split kernels win everywhere;
+// the tile is the largest that still gives close to one workgroup per
+// compute unit: deep-K shapes (K >= 2048) take 96 x 64 tiles while those
+// fill the chip and 96 x 128 beyond; otherwise 192 x 128 when that makes
+// at least 3/4 of a wave of workgroups, 96 x 128 when that is still at most
+// one wave, 64 x 64 for M <= 256. f32 keeps its own smallest-cost shape.
 Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
-  (void)inner;
-  if (precision == PK_PRECISION_F16)
-    return {rows <= 256u ? find_variant(precision, 1, 4, 1, 1) : find_variant(precision, 1, 4, 2, 1), 1u};
+  if (precision == PK_PRECISION_F16) {
+    auto pair_variant = [](int wn, int r, int c, int ks) {
+      return find_variant(PK_PRECISION_F16, 1, wn, r, c, ks, true);
+    };
+    auto tiles = [&](int tile_rows, int tile_columns) {
+      return (uint64_t)((rows + tile_rows - 1) / tile_rows) * ((columns + tile_columns - 1) / tile_columns);
+    };
+    const uint64_t wave = (uint64_t)cus;
+    if (rows <= 256u) return {pair_variant(1, 2, 2, 4), 1u};
+    if (inner >= 2048u) return {tiles(96, 64) <= wave ? pair_variant(1, 3, 2, 4) : pair_variant(2, 3, 2, 2), 1u};
+    if (tiles(192, 128) * 4u >= wave * 3u) return {pair_variant(2, 6, 2, 2), 1u};
+    if (tiles(96, 128) <= wave) return {pair_variant(2, 3, 2, 2), 1u};
+    return {pair_variant(2, 6, 2, 2), 1u};
+  }
   // f32: the largest tile that still fills the compute units.
   const int count = pk::f32_variant_count();
   int best = 0;
@@ -230,6 +256,8 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
 // op's row capacity and zeroes its counters.
 int configure_launch(pk_gemm_op* op, int variant, uint32_t splits) {
   const pk::TileShape s = shape_of(op->precision, variant);
+  if (splits > 1 && !(op->precision == PK_PRECISION_F16 && pk::f16_variant_splits(variant)))
+    return fail(PK_RANGE_ERROR, "%s tile variant %d has no split-K path", op->label.c_str(), variant);
   const uint64_t need = workspace_bytes_for(s, op->rows, op->args.columns, splits);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
   if (need != op->workspace_bytes) {
@@ -613,6 +641,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   pk::GemmArgs& a = op->args;
   a.a = d->a;
   a.codes = op->weight->codes;
+  a.pair_codes = op->weight->pair_codes;
   a.palette = d->palette;
   a.out = d->output;
   a.bias = d->bias;
@@ -624,6 +653,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   a.columns = d->columns;
   a.palette_groups = d->palette_groups;
   a.palette_group_columns = d->palette_group_columns;
+  a.palette_entries = 1u << bits;
   hipDeviceProp_t prop;
   int cus = 256;
   if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
@@ -640,6 +670,10 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
 }
 
 int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
+  return pk_gemm_enqueue_timed(op, active_rows, stream, nullptr, nullptr);
+}
+
+int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, void* start_event, void* end_event) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
   const uint32_t rows = active_rows ? active_rows : op->rows;
@@ -652,9 +686,10 @@ int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
   args.splits = std::min(op->splits, k_blocks(op->args.inner));
   hipStream_t st = stream_or_default(op->ctx, stream);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  hipEvent_t start = static_cast<hipEvent_t>(start_event), stop = static_cast<hipEvent_t>(end_event);
   const hipError_t e = op->precision == PK_PRECISION_F16
-                           ? pk::launch_gemm_f16(op->bits, op->variant, args, st)
-                           : pk::launch_gemm_f32(op->bits, op->variant, args, st);
+                           ? pk::launch_gemm_f16(op->bits, op->variant, args, st, start, stop)
+                           : pk::launch_gemm_f32(op->bits, op->variant, args, st, start, stop);
   PK_HIP(e, "palette GEMM launch");
   return ok();
 }
@@ -687,7 +722,9 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
   if (variant < 0 || variant >= count)
     return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
-  return configure_launch(op, variant, op->splits);
+  // Variants without a split-K path run unsplit.
+  const bool splittable = op->precision == PK_PRECISION_F16 && pk::f16_variant_splits(variant);
+  return configure_launch(op, variant, splittable ? op->splits : 1u);
 }
 
 int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
@@ -727,8 +764,12 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   info->split_inner = splits;
   info->workspace_bytes = op->workspace_bytes;
   const uint32_t elem = f16 ? 2u : 4u;
-  const uint32_t lut_cap = (s.tile_columns() / pk::codes_per_group(op->bits) + 1u) * (1u << op->bits);
-  info->lds_bytes = 2u * s.tile_rows() * (f16 ? 128u : 256u) + lut_cap * elem;
+  if (f16) {
+    info->lds_bytes = pk::f16_variant_lds_bytes(op->variant);
+  } else {
+    const uint32_t lut_cap = (s.tile_columns() / 16u + 2u) * (1u << op->bits);
+    info->lds_bytes = 2u * s.tile_rows() * 256u + lut_cap * elem;
+  }
   const uint64_t M = rows, K = op->args.inner, N = op->args.columns;
   info->flops = 2ull * M * K * N;
   uint64_t bytes = (K * N * (uint64_t)op->bits + 7u) / 8u;

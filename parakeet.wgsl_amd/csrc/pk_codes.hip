@@ -140,6 +140,48 @@ __global__ __launch_bounds__(kThreads) void operand_order_kernel(
   }
 }
 
+// Reference format -> pair-code layout (pk_internal.h). One thread per
+// (block, lane); runs once per weight.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void pair_code_kernel(
+    const uint32_t* __restrict__ packed, uint32_t inner, uint32_t columns,
+    uint32_t k_blocks, uint64_t total_lanes, uint8_t* __restrict__ out) {
+  constexpr uint32_t CPG = codes_per_group(BITS);
+  constexpr uint32_t WPG = words_per_group(BITS);
+  constexpr uint32_t S = pair_table_side(BITS);
+  constexpr uint32_t PAD = 1u << BITS;
+  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= total_lanes) return;
+  const uint32_t lane = (uint32_t)(t & 63u);
+  const uint64_t block = t >> 6;
+  const uint32_t nb = (uint32_t)(block / k_blocks);
+  const uint32_t kb = (uint32_t)(block % k_blocks);
+  const uint32_t n = nb * 32u + (lane & 31u);
+  const uint32_t k0 = kb * 64u + (lane >> 5) * 32u;
+  auto code_at = [&](uint32_t k) -> uint32_t {
+    if (k >= inner || n >= columns) return PAD;
+    const uint64_t scalar = (uint64_t)k * columns + n;
+    const uint64_t g = scalar / CPG;
+    const uint32_t bit = (uint32_t)(scalar % CPG) * BITS;
+    const uint32_t word = bit >> 5, shift = bit & 31u;
+    uint32_t value = packed[g * WPG + word] >> shift;
+    if (shift + BITS > 32u) value |= packed[g * WPG + word + 1] << (32u - shift);
+    return value & ((1u << BITS) - 1u);
+  };
+  uint32_t w[8];
+#pragma unroll 4
+  for (uint32_t v = 0; v < 16u; ++v) {
+    const uint32_t pair = 4u * (code_at(k0 + 2u * v) + S * code_at(k0 + 2u * v + 1u));
+    if (v & 1u)
+      w[v >> 1] |= pair << 16;
+    else
+      w[v >> 1] = pair;
+  }
+  uint8_t* base = out + block * kPairBlockBytes + (uint64_t)lane * 16u;
+  reinterpret_cast<uint4*>(base)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  reinterpret_cast<uint4*>(base + 1024)[0] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
 inline dim3 grid_for(uint64_t items) {
   return dim3((unsigned)((items + kThreads - 1) / kThreads));
 }
@@ -201,6 +243,20 @@ hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t in
                        inner, columns, k_blocks, lanes, codes);
   else
     hipLaunchKernelGGL(operand_order_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
+                       inner, columns, k_blocks, lanes, codes);
+  return hipGetLastError();
+}
+
+hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
+                                uint32_t columns, uint8_t* codes, hipStream_t stream) {
+  const uint32_t k_blocks = padded_inner(inner) / 64u;
+  const uint64_t blocks = (uint64_t)(padded_columns(columns) / 32u) * k_blocks;
+  const uint64_t lanes = blocks * 64u;
+  if (bits == 5)
+    hipLaunchKernelGGL(pair_code_kernel<5>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
+                       inner, columns, k_blocks, lanes, codes);
+  else
+    hipLaunchKernelGGL(pair_code_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
                        inner, columns, k_blocks, lanes, codes);
   return hipGetLastError();
 }

@@ -1,6 +1,6 @@
 // pk_f16_common.h - device helpers shared by the f16 palette GEMM kernels
-// (pk_gemm_f16.hip, pk_gemm_f16_shared.hip): code extraction and palette
-// gathers, the split-K reduction and the LDS-staged epilogue.
+// (pk_gemm_f16.hip, pk_gemm_f16k.hip): code extraction and palette gathers,
+// the split-K reduction and the LDS-staged epilogue.
 #pragma once
 
 #include "pk_internal.h"
@@ -220,12 +220,15 @@ struct F16Variant {
   const char* name6;
   void (*single[2])(GemmArgs);  // [bits == 6]
   void (*general[2])(GemmArgs);
+  uint32_t lds_bytes;           // static LDS of the kernel
 };
 
 }  // namespace f16
 
-// Shared-decode tile shapes (pk_gemm_f16_shared.hip).
-int f16_shared_variant_count();
-const f16::F16Variant& f16_shared_variant(int index);
+// Byte-code tile shapes (pk_gemm_f16k.hip).
+int f16k_variant_count();
+const f16::F16Variant& f16k_variant(int index);
+hipError_t launch_gemm_f16k(const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
+                            hipEvent_t start, hipEvent_t stop);
 
 }  // namespace pk

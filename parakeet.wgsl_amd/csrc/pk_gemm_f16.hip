@@ -283,12 +283,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_kernel(GemmArgs args) {
   store_tile<WM, WN, R, C, 2 * BM * ROW_BYTES>(args, acc, a_lds, m0, n0, wave_m, wave_n, j, h, tid);
 }
 
+template <int WM, int WN, int R, int C>
+constexpr uint32_t kernel_lds_bytes(int bits) {
+  const int e = 1 << bits;
+  const int lut = (32 * C * WN / (int)codes_per_group(bits) + 2) * e;
+  return (uint32_t)(2 * 32 * R * WM * 128 + lut * 2 + 4);
+}
+
 #define PK_F16_VARIANT(WM, WN, R, C)                                                              \
   F16Variant {                                                                                    \
     TileShape{WM, WN, R, C}, "pk_gemm_f16_b5_w" #WM "x" #WN "_m" #R "n" #C,                       \
         "pk_gemm_f16_b6_w" #WM "x" #WN "_m" #R "n" #C,                                            \
         {gemm_f16_kernel<5, WM, WN, R, C, false>, gemm_f16_kernel<6, WM, WN, R, C, false>},       \
-        {gemm_f16_kernel<5, WM, WN, R, C, true>, gemm_f16_kernel<6, WM, WN, R, C, true>}          \
+        {gemm_f16_kernel<5, WM, WN, R, C, true>, gemm_f16_kernel<6, WM, WN, R, C, true>},         \
+        kernel_lds_bytes<WM, WN, R, C>(6)                                                         \
   }
 
 const F16Variant kVariants[] = {
@@ -303,20 +311,24 @@ const F16Variant kVariants[] = {
 constexpr int kLocal = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
 
 const F16Variant& variant_at(int index) {
-  return index < kLocal ? kVariants[index] : f16_shared_variant(index - kLocal);
+  return index < kLocal ? kVariants[index] : f16k_variant(index - kLocal);
 }
 
 }  // namespace
 
-// f16 tile shapes: the per-wavefront-decode kernels of this file, then the
-// shared-decode kernels of pk_gemm_f16_shared.hip.
-int f16_variant_count() { return kLocal + f16_shared_variant_count(); }
+// f16 tile shapes: the operand-order kernels of this file, then the
+// byte-code K-split kernels of pk_gemm_f16k.hip.
+int f16_variant_count() { return kLocal + f16k_variant_count(); }
 TileShape f16_variant(int index) { return variant_at(index).shape; }
 const char* f16_variant_name(int bits, int index) {
   return bits == 5 ? variant_at(index).name5 : variant_at(index).name6;
 }
+uint32_t f16_variant_lds_bytes(int index) { return variant_at(index).lds_bytes; }
+bool f16_variant_splits(int index) { return index < kLocal; }
 
-hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream) {
+hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
+                           hipEvent_t stop) {
+  if (variant >= kLocal) return launch_gemm_f16k(variant_at(variant), args, stream, start, stop);
   const F16Variant& v = variant_at(variant);
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;
   if (groups == 0) return hipSuccess;
@@ -328,8 +340,7 @@ hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStrea
                       (args.palette_groups == 1 ||
                        args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
   void (*kernel)(GemmArgs) = single ? v.single[bits == 6] : v.general[bits == 6];
-  hipLaunchKernelGGL(kernel, dim3(groups), dim3(v.shape.threads()), 0, stream, args);
-  return hipGetLastError();
+  return launch_timed(kernel, dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
 }
 
 }  // namespace pk

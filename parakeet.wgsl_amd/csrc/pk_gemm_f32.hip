@@ -263,14 +263,14 @@ const char* f32_variant_name(int bits, int index) {
   return bits == 5 ? kVariants[index].name5 : kVariants[index].name6;
 }
 
-hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream) {
+hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
+                           hipEvent_t stop) {
   const Variant& v = kVariants[variant];
   const uint32_t n_pad = padded_columns(args.columns);
   const dim3 grid((n_pad + v.shape.tile_columns() - 1) / v.shape.tile_columns(),
                   (args.rows + v.shape.tile_rows() - 1) / v.shape.tile_rows());
   if (grid.y == 0) return hipSuccess;
-  hipLaunchKernelGGL(bits == 5 ? v.kernel5 : v.kernel6, grid, dim3(v.shape.threads()), 0, stream, args);
-  return hipGetLastError();
+  return launch_timed(bits == 5 ? v.kernel5 : v.kernel6, grid, dim3(v.shape.threads()), stream, start, stop, args);
 }
 
 }  // namespace pk

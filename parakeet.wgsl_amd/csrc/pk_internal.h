@@ -1,6 +1,7 @@
 // pk_internal.h - shared declarations of the palette GEMM library (gfx950).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -31,11 +32,32 @@ __host__ __device__ constexpr uint64_t operand_order_words(int bits, uint32_t in
   return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * block_words(bits);
 }
 
+// ---------------------------------------------------------------------------
+// Pair-code layout, built once per weight for the large-M f16 kernels.
+//
+// Same 64 k x 32 n blocks in [nb][kb] order, 2048 bytes each, holding one
+// 16-bit value per pair of K-adjacent codes (k even, k + 1) of a column:
+// the byte offset 4 * (c0 + S * c1) of their entry in an LDS table of
+// S x S packed f16 pairs, S = 2^bits + 1, where code 2^bits stands for K
+// padding (both palette halves zero). A block is [p][lane][16 bytes] for
+// sub-step pairs p = 0, 1: 16-bit value v (0..7) of lane l = 32*h + j in
+// pair p covers column n = 32*nb + j at k = 64*kb + 32*h + 16*p + 2*v and
+// k + 1, so the 8 codes one MFMA sub-step s needs are the 8-byte half
+// (s & 1) of pair s >> 1, and one ds_read_b32 gathers a packed pair of
+// operand halves.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPairBlockBytes = 2048u;
+__host__ __device__ constexpr uint32_t pair_table_side(int bits) { return (1u << bits) + 1u; }
+__host__ __device__ constexpr uint64_t pair_code_bytes(uint32_t inner, uint32_t columns) {
+  return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * kPairBlockBytes;
+}
+
 enum Activation : int { kActNone = 0, kActSilu = 1, kActRelu = 2 };
 
 struct GemmArgs {
   const void* a;             // [M, K]
   const uint32_t* codes;     // operand-order codes
+  const uint8_t* pair_codes; // pair-code layout of the same weight
   const void* palette;       // [G, 2^bits]
   void* out;                 // [M, N]
   const float* bias;         // [N] or null
@@ -47,6 +69,7 @@ struct GemmArgs {
   uint32_t columns;          // N
   uint32_t palette_groups;
   uint32_t palette_group_columns;
+  uint32_t palette_entries;  // 2^bits
   // Split-K: `splits` workgroups share one output tile, each over a
   // contiguous range of 64-deep K blocks. With splits > 1 every workgroup
   // writes its f32 partial tile to `partials` and bumps the tile's counter;
@@ -59,11 +82,14 @@ struct GemmArgs {
 };
 
 // Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
-// waves_m x waves_n wavefronts; a wavefront owns m_blocks x n_blocks MFMA
-// output blocks of 32 x 32.
+// waves_m x waves_n x k_split wavefronts; a wavefront owns m_blocks x
+// n_blocks MFMA output blocks of 32 x 32, and with k_split > 1 the
+// k_split wavefronts of one (m, n) position each multiply their own part
+// of every K block and add their partial tiles at the end.
 struct TileShape {
   int waves_m, waves_n, m_blocks, n_blocks;
-  __host__ __device__ constexpr int threads() const { return 64 * waves_m * waves_n; }
+  int k_split = 1;
+  __host__ __device__ constexpr int threads() const { return 64 * waves_m * waves_n * k_split; }
   __host__ __device__ constexpr int tile_rows() const { return 32 * waves_m * m_blocks; }
   __host__ __device__ constexpr int tile_columns() const { return 32 * waves_n * n_blocks; }
   // f32 elements of one workgroup's split-K partial tile.
@@ -90,6 +116,18 @@ __host__ __device__ inline uint32_t xcd_local_order(uint32_t i, uint32_t count) 
   return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
+// One launch of a GEMM kernel on `stream`. With a start and/or stop event
+// the dispatch itself stamps them (hipExtLaunchKernel), so timing a kernel
+// adds no packets to the stream.
+inline hipError_t launch_timed(void (*kernel)(GemmArgs), dim3 grid, dim3 block, hipStream_t stream,
+                               hipEvent_t start, hipEvent_t stop, const GemmArgs& args) {
+  if (start || stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args);
+  return hipGetLastError();
+}
+
 // Launchers. Each returns the hipError_t of the launch.
 hipError_t launch_unpack(int bits, const uint32_t* words, uint64_t groups,
                          uint8_t* codes, hipStream_t stream);
@@ -99,16 +137,24 @@ hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* pa
                          hipStream_t stream);
 hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
                                    uint32_t columns, uint32_t* codes, hipStream_t stream);
+hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
+                                uint32_t columns, uint8_t* codes, hipStream_t stream);
 
 // Fused palette GEMM. `variant` indexes f16_variants() / f32_variants().
 int f16_variant_count();
 TileShape f16_variant(int index);
 const char* f16_variant_name(int bits, int index);
-hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream);
+uint32_t f16_variant_lds_bytes(int index);
+// True for the operand-order variants, which also run split-K across
+// workgroups; the pair-code variants split K inside the workgroup only.
+bool f16_variant_splits(int index);
+hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream,
+                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 int f32_variant_count();
 TileShape f32_variant(int index);
 const char* f32_variant_name(int bits, int index);
-hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream);
+hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream,
+                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 }  // namespace pk

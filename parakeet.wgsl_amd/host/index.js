@@ -413,11 +413,13 @@ class GemmDispatch {
     }
     const op = this.op;
     encoder.record(() => {
-      if (timestampWrites && timestampWrites.beginningOfPassWriteIndex !== undefined)
-        timestampWrites.querySet.write(timestampWrites.beginningOfPassWriteIndex);
-      native().gemmEnqueue(op, rows, null);
-      if (timestampWrites && timestampWrites.endOfPassWriteIndex !== undefined)
-        timestampWrites.querySet.write(timestampWrites.endOfPassWriteIndex);
+      // The kernel's own dispatch stamps the pass's timestamp queries.
+      const qs = timestampWrites ? timestampWrites.querySet : null;
+      const begin = qs && timestampWrites.beginningOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.beginningOfPassWriteIndex] : null;
+      const end = qs && timestampWrites.endOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.endOfPassWriteIndex] : null;
+      native().gemmEnqueue(op, rows, null, begin, end);
     });
   }
 

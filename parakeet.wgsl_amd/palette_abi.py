@@ -157,6 +157,7 @@ SIGNATURES = {
     "pk_gemm_create": (ctypes.c_int, [_VP, ctypes.POINTER(GemmDesc), _VP, _PPV]),
     "pk_gemm_validate": (ctypes.c_int, [ctypes.POINTER(GemmDesc)]),
     "pk_gemm_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_gemm_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
     "pk_gemm_destroy": (ctypes.c_int, [_VP]),
     "pk_gemm_release": (ctypes.c_int, [_VP]),
     "pk_gemm_variant_count": (ctypes.c_int, [ctypes.c_int]),
@@ -365,8 +366,14 @@ class GemmOp:
         self.handle = handle.value
         self.ctx = ctx
 
-    def enqueue(self, active_rows: int = 0, stream=None) -> None:
-        check(load().pk_gemm_enqueue(self.handle, active_rows, stream))
+    def enqueue(self, active_rows: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        """Launch; `start`/`end` events, when given, are stamped by the
+        kernel's own dispatch (pk_gemm_enqueue_timed)."""
+        if start is None and end is None:
+            check(load().pk_gemm_enqueue(self.handle, active_rows, stream))
+        else:
+            check(load().pk_gemm_enqueue_timed(self.handle, active_rows, stream,
+                                               start.handle if start else None, end.handle if end else None))
 
     def plan(self, active_rows: int = 0) -> PlanInfo:
         info = PlanInfo()

@@ -6,6 +6,8 @@ reference fp32 chain; fp16 GEMM within 1e-2 norm-wise of the reference f16
 accumulator chain (the reference's own rounding, emulated by the oracle) and
 within 2e-3 norm-wise of the fp64 truth.
 """
+import re
+
 import numpy as np
 import pytest
 
@@ -81,6 +83,37 @@ def run_case(abi, ctx, scope, case, *, variant=None, splits=None, active_rows=0,
         op.release()
 
 
+def variant_names(abi, ctx, scope, workloads, precision="f16"):
+    """Kernel name of every compiled tile variant, by index."""
+    dtype = np.float16 if precision == "f16" else np.float32
+    case = workloads.gemm_case(1, 32, 64, 64, 5, dtype=dtype)
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    out = scope.empty((case.rows, w.columns), dtype)
+    op = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=w.bits, rows=case.rows,
+                    inner=w.inner, columns=w.columns, label="variant-names")
+    try:
+        names = []
+        for v in range(abi.variant_count(precision)):
+            op.set_variant(v)
+            names.append(op.plan().kernel.decode())
+        return names
+    finally:
+        op.release()
+
+
+def k_split_of(name):
+    """Order class of a kernel: pair-code variants add their K-part partial
+    tiles at the end (pk_gemm_f16p_b*_n<WN>k<KS>_...); KS = 1 and every
+    operand-order variant accumulate all of K in one chain."""
+    m = re.search(r"_n\dk(\d)_", name)
+    return int(m.group(1)) if m else 1
+
+
+def pair_code_variants(abi, ctx, scope, workloads):
+    return [i for i, n in enumerate(variant_names(abi, ctx, scope, workloads)) if "f16p" in n]
+
+
 def oracle_gemm(oracle, case, mode, threads=8, rows=None):
     a = case.a if rows is None else case.a[rows]
     residual = case.residual if (case.residual is None or rows is None) else case.residual[rows]
@@ -144,14 +177,20 @@ def test_expansion_is_bit_exact(abi, ctx, scope, oracle, workloads, dtype, bits,
     np.testing.assert_array_equal(target.download().view(np.uint8), want.reshape(-1).view(np.uint8))
 
 
-@pytest.mark.parametrize("precision", ["f32", "f16"])
+@pytest.mark.parametrize("precision", ["f32", "f16", "f16-pair-codes"])
 @pytest.mark.parametrize("bits,inner,columns,groups", [
-    (5, 128, 256, 1), (6, 96, 48, 1), (6, 64, 3072, 3), (5, 160, 640, 1), (6, 32, 16, 1)])
+    (5, 128, 256, 1), (6, 96, 48, 1), (6, 64, 3072, 3), (5, 160, 640, 1), (6, 32, 16, 1),
+    (6, 128, 96, 3)])
 def test_prepared_operand_order_is_bit_exact(abi, ctx, scope, oracle, workloads, precision, bits, inner,
                                              columns, groups):
     """A = identity and LUT[g][c] = 64*g + c make the GEMM output each code
-    exactly, so this reads back the whole operand-order repack and the
-    in-register decode bit for bit."""
+    exactly, so this reads back the whole repack (operand order, or pair
+    codes for the K-split kernels) and the in-register decode bit for bit.
+    (6, 128, 96, 3) puts three palette groups inside one pair-code tile."""
+    variant = None
+    if precision == "f16-pair-codes":
+        variant = pair_code_variants(abi, ctx, scope, workloads)[0]
+        precision = "f16"
     if precision == "f16" and columns % 8:
         pytest.skip("f16 GEMM needs N % 8 == 0")
     dtype = np.float16 if precision == "f16" else np.float32
@@ -160,7 +199,7 @@ def test_prepared_operand_order_is_bit_exact(abi, ctx, scope, oracle, workloads,
     weight = workloads.PaletteMatrix(bits, inner, columns, codes, workloads.pack_codes(codes, bits),
                                      (64 * np.arange(groups)[:, None] + np.arange(1 << bits)[None, :]).astype(dtype))
     case = workloads.GemmCase("identity", np.eye(inner, dtype=dtype), weight)
-    got = run_case(abi, ctx, scope, case)
+    got = run_case(abi, ctx, scope, case, variant=variant)
     group_of = np.minimum(np.arange(columns) // (columns // groups), groups - 1)
     np.testing.assert_array_equal(got.astype(np.float64), (64 * group_of[None, :] + codes).astype(np.float64))
 
@@ -220,23 +259,49 @@ def test_fp16_gemm_parity(abi, ctx, scope, oracle, workloads, rows, inner, colum
 
 @pytest.mark.parametrize("precision", ["f16", "f32"])
 def test_every_tile_variant_matches(abi, ctx, scope, oracle, workloads, precision):
-    """Each compiled tile shape computes the same sums in the same k order,
-    so every variant agrees bit for bit and with the oracle."""
+    """Tile shapes with the same K order compute the same sums: every
+    variant of one order class (one accumulation chain over K, or KS K parts
+    added at the end) agrees bit for bit, and all agree with the oracle."""
     dtype = np.float16 if precision == "f16" else np.float32
     case = workloads.gemm_case(5, 333, 320, 640, 5, dtype=dtype, activation="silu")
-    results = []
-    for variant in range(abi.variant_count(precision)):
-        results.append(run_case(abi, ctx, scope, case, variant=variant, splits=1))
-    for variant, got in enumerate(results):
+    names = variant_names(abi, ctx, scope, workloads, precision)
+    first = {}
+    for variant, name in enumerate(names):
+        got = run_case(abi, ctx, scope, case, variant=variant)
         if precision == "f16":
             assert_f16_parity(oracle, got, case)
         else:
             norm, peak = oracle.relative_errors(got, oracle_gemm(oracle, case, "f32-chain"))
             assert norm <= F32_TOL and peak <= F32_TOL, (variant, norm, peak)
-        np.testing.assert_array_equal(got.view(np.uint8), results[0].view(np.uint8), err_msg=str(variant))
+        ref = first.setdefault(k_split_of(name), got)
+        np.testing.assert_array_equal(got.view(np.uint8), ref.view(np.uint8), err_msg=name)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 3, 6])
+@pytest.mark.parametrize("rows,inner,columns,bits,groups,activation,bias,scale", [
+    (1504, 1024, 4096, 5, 1, "silu", False, None),     # FF expand, 8 windows
+    (333, 1056, 640, 6, 1, "relu", True, None),        # K % 64 = 32, row tail
+    (200, 1024, 3072, 6, 3, "none", False, 0.5),       # QKV groups + residual
+    (97, 256, 96, 6, 3, "silu", True, None),           # 3 groups inside one tile
+    (64, 4096, 1024, 5, 1, "none", False, 0.5),        # FF contract shape
+])
+def test_pair_code_variants_parity(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits, groups,
+                                   activation, bias, scale):
+    """Every pair-code K-split variant against the oracle's reference f16
+    chain and the fp64 truth, including tails, multi-group tiles and every
+    epilogue, with repeated launches bit-identical."""
+    case = workloads.gemm_case(rows + inner + columns, rows, inner, columns, bits, dtype=np.float16,
+                               groups=groups, activation=activation, bias=bias, residual_scale=scale)
+    ref = oracle_gemm(oracle, case, "f16-chain")
+    truth = oracle_gemm(oracle, case, "f64")
+    for variant in pair_code_variants(abi, ctx, scope, workloads):
+        got = run_case(abi, ctx, scope, case, variant=variant, repeats=2)
+        assert np.all(np.isfinite(got.astype(np.float32))), variant
+        norm_ref, _ = oracle.relative_errors(got, ref)
+        norm_truth, _ = oracle.relative_errors(got, truth)
+        assert norm_ref <= F16_TOL_REFERENCE and norm_truth <= F16_TOL_TRUTH, (variant, norm_ref, norm_truth)
+
+
+@pytest.mark.parametrize("variant", [0, 1, 3, 5])
 def test_split_inner_reduction(abi, ctx, scope, oracle, workloads, variant):
     """Split-K partial tiles are summed in split order by the last
     workgroup of each tile: every split count stays within the parity bars,
@@ -254,6 +319,37 @@ def test_split_inner_reduction(abi, ctx, scope, oracle, workloads, variant):
                                           err_msg=f"{c.name} splits={splits}")
 
 
+@pytest.mark.parametrize("precision", ["f16", "f32"])
+def test_timed_enqueue_stamps_the_kernel(abi, ctx, scope, workloads, precision):
+    """pk_gemm_enqueue_timed (encode with timestampWrites): the dispatch
+    stamps both events, the elapsed time is positive, and the output equals
+    an untimed launch bit for bit."""
+    dtype = np.float16 if precision == "f16" else np.float32
+    case = workloads.gemm_case(9, 300, 1024, 1024, 5, dtype=dtype, activation="silu")
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    outs = [scope.empty((case.rows, w.columns), dtype) for _ in range(2)]
+    start, end = ctx.event(), ctx.event()
+    try:
+        for i, out in enumerate(outs):
+            op = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=w.bits, rows=case.rows,
+                            inner=w.inner, columns=w.columns, activation="silu", label="timed")
+            try:
+                if i == 0:
+                    op.enqueue()
+                else:
+                    op.enqueue(0, None, start, end)
+                ctx.synchronize()
+            finally:
+                op.release()
+        end.synchronize()
+        assert start.elapsed_ms(end) > 0.0
+        np.testing.assert_array_equal(outs[0].download().view(np.uint8), outs[1].download().view(np.uint8))
+    finally:
+        start.destroy()
+        end.destroy()
+
+
 def test_active_rows_prefix_leaves_the_tail_untouched(abi, ctx, scope, oracle, workloads):
     """GemmDispatch.encode(shape) re-plans for the active prefix (gemm.ts:427-451)."""
     case = workloads.gemm_case(21, 200, 1024, 1024, 5, activation="silu")
@@ -267,7 +363,8 @@ def test_prepared_weight_is_shared_and_outlives_its_owner(abi, ctx, scope, oracl
     w = workloads.palette_matrix(rng, 5, 256, 512)
     packed = scope.put(w.packed)
     prepared = abi.PreparedWeight(ctx, 5, 256, 512, packed, label="shared")
-    assert prepared.nbytes() == 256 * 512 * 5 // 8
+    # operand-order codes (bits per code, as packed) + pair codes (16 bits per two codes)
+    assert prepared.nbytes() == 256 * 512 * 5 // 8 + 256 * 512
     cases = [workloads.GemmCase(f"user{i}", workloads.normal(rng, (64 + 32 * i, 256)), w) for i in range(2)]
     outs, ops = [], []
     for case in cases:
