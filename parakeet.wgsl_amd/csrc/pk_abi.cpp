@@ -199,36 +199,44 @@ struct Plan {
   uint32_t splits;
 };
 
-int find_variant(int precision, int waves_m, int waves_n, int m_blocks, int n_blocks, int k_split = 1,
-                 bool pair_codes = false) {
+// The compiled variant of a family with a given tile shape (-1 if none).
+int find_variant(int precision, int family, int waves_m, int waves_n, int m_blocks, int n_blocks,
+                 int k_split = 1) {
   const int count = precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
   for (int i = 0; i < count; ++i) {
     const pk::TileShape s = shape_of(precision, i);
-    const bool bytes = precision == PK_PRECISION_F16 && !pk::f16_variant_splits(i);
-    if (s.waves_m == waves_m && s.waves_n == waves_n && s.m_blocks == m_blocks && s.n_blocks == n_blocks &&
-        s.k_split == k_split && bytes == pair_codes)
+    const int f = precision == PK_PRECISION_F16 ? pk::f16_variant_family(i) : 0;
+    if (f == family && s.waves_m == waves_m && s.waves_n == waves_n && s.m_blocks == m_blocks &&
+        s.n_blocks == n_blocks && s.k_split == k_split)
       return i;
   }
-  return 0;
+  return -1;
 }
 
 // Launch planner. The f16 choice follows MI355X measurements of every
-// compiled tile shape over the encoder's GEMM shapes (M 64..3008, K
-// 1024/4096, N 1024..4096). The pair-code K-split kernels win everywhere;
-// the tile is the largest that still gives close to one workgroup per
-// compute unit: deep-K shapes (K >= 2048) take 96 x 64 tiles while those
-// fill the chip and 96 x 128 beyond; otherwise 192 x 128 when that makes
-// at least 3/4 of a wave of workgroups, 96 x 128 when that is still at most
-// one wave, 64 x 64 for M <= 256. f32 keeps its own smallest-cost shape.
+// compiled tile shape over the encoder's GEMM shapes (M 1..3008, K
+// 1024/4096, N 1024..4096). Up to 64 rows, and up to 256 rows of a deep-K
+// (K >= 2048) GEMM, the small-M kernel (32-row blocks, K round robin over
+// eight wavefronts) wins; everything else goes to the pair-code K-split
+// kernels with the largest tile that still gives close to one workgroup
+// per compute unit: 64 x 64 up to 256 rows, deep-K shapes 96 x 64 while
+// those fill the chip and 96 x 128 beyond; otherwise 192 x 128 when that
+// makes at least 3/4 of a wave of workgroups, 96 x 128 when that is still at
+// most one wave. f32 keeps its own smallest-cost shape.
 Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
   if (precision == PK_PRECISION_F16) {
     auto pair_variant = [](int wn, int r, int c, int ks) {
-      return find_variant(PK_PRECISION_F16, 1, wn, r, c, ks, true);
+      const int v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, wn, r, c, ks);
+      return v < 0 ? 0 : v;
     };
     auto tiles = [&](int tile_rows, int tile_columns) {
       return (uint64_t)((rows + tile_rows - 1) / tile_rows) * ((columns + tile_columns - 1) / tile_columns);
     };
     const uint64_t wave = (uint64_t)cus;
+    if (rows <= 64u || (rows <= 256u && inner >= 2048u)) {
+      const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 1, 8);
+      return {v < 0 ? 0 : v, 1u};
+    }
     if (rows <= 256u) return {pair_variant(1, 2, 2, 4), 1u};
     if (inner >= 2048u) return {tiles(96, 64) <= wave ? pair_variant(1, 3, 2, 4) : pair_variant(2, 3, 2, 2), 1u};
     if (tiles(192, 128) * 4u >= wave * 3u) return {pair_variant(2, 6, 2, 2), 1u};

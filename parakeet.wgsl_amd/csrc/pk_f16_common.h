@@ -225,10 +225,16 @@ struct F16Variant {
 
 }  // namespace f16
 
-// Byte-code tile shapes (pk_gemm_f16k.hip).
+// Pair-code K-split tile shapes (pk_gemm_f16k.hip).
 int f16k_variant_count();
 const f16::F16Variant& f16k_variant(int index);
 hipError_t launch_gemm_f16k(const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
+                            hipEvent_t start, hipEvent_t stop);
+
+// Small-M shapes (pk_gemm_f16s.hip).
+int f16s_variant_count();
+const f16::F16Variant& f16s_variant(int index);
+hipError_t launch_gemm_f16s(int bits, const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
                             hipEvent_t start, hipEvent_t stop);
 
 }  // namespace pk

@@ -311,23 +311,32 @@ const F16Variant kVariants[] = {
 constexpr int kLocal = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
 
 const F16Variant& variant_at(int index) {
-  return index < kLocal ? kVariants[index] : f16k_variant(index - kLocal);
+  if (index < kLocal) return kVariants[index];
+  index -= kLocal;
+  if (index < f16k_variant_count()) return f16k_variant(index);
+  return f16s_variant(index - f16k_variant_count());
 }
 
 }  // namespace
 
 // f16 tile shapes: the operand-order kernels of this file, then the
-// byte-code K-split kernels of pk_gemm_f16k.hip.
-int f16_variant_count() { return kLocal + f16k_variant_count(); }
+// pair-code K-split kernels of pk_gemm_f16k.hip, then the small-M kernels
+// of pk_gemm_f16s.hip.
+int f16_variant_count() { return kLocal + f16k_variant_count() + f16s_variant_count(); }
 TileShape f16_variant(int index) { return variant_at(index).shape; }
 const char* f16_variant_name(int bits, int index) {
   return bits == 5 ? variant_at(index).name5 : variant_at(index).name6;
 }
 uint32_t f16_variant_lds_bytes(int index) { return variant_at(index).lds_bytes; }
-bool f16_variant_splits(int index) { return index < kLocal; }
+int f16_variant_family(int index) {
+  if (index < kLocal) return kFamilyOperandOrder;
+  return index < kLocal + f16k_variant_count() ? kFamilyPairCode : kFamilySmallM;
+}
 
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop) {
+  if (variant >= kLocal + f16k_variant_count())
+    return launch_gemm_f16s(bits, variant_at(variant), args, stream, start, stop);
   if (variant >= kLocal) return launch_gemm_f16k(variant_at(variant), args, stream, start, stop);
   const F16Variant& v = variant_at(variant);
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;

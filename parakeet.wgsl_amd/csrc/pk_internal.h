@@ -145,9 +145,11 @@ int f16_variant_count();
 TileShape f16_variant(int index);
 const char* f16_variant_name(int bits, int index);
 uint32_t f16_variant_lds_bytes(int index);
-// True for the operand-order variants, which also run split-K across
-// workgroups; the pair-code variants split K inside the workgroup only.
-bool f16_variant_splits(int index);
+// Kernel family of an f16 variant. Only the operand-order family also runs
+// split-K across workgroups; the others split K inside the workgroup.
+enum F16Family : int { kFamilyOperandOrder = 0, kFamilyPairCode = 1, kFamilySmallM = 2 };
+int f16_variant_family(int index);
+inline bool f16_variant_splits(int index) { return f16_variant_family(index) == kFamilyOperandOrder; }
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream,
                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 

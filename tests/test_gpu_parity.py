@@ -105,13 +105,20 @@ def variant_names(abi, ctx, scope, workloads, precision="f16"):
 def k_split_of(name):
     """Order class of a kernel: pair-code variants add their K-part partial
     tiles at the end (pk_gemm_f16p_b*_n<WN>k<KS>_...); KS = 1 and every
-    operand-order variant accumulate all of K in one chain."""
+    operand-order variant accumulate all of K in one chain; the small-M
+    variants (pk_gemm_f16s_*) add eight round-robin K partials."""
+    if "_f16s_" in name:
+        return "small-m"
     m = re.search(r"_n\dk(\d)_", name)
     return int(m.group(1)) if m else 1
 
 
 def pair_code_variants(abi, ctx, scope, workloads):
     return [i for i, n in enumerate(variant_names(abi, ctx, scope, workloads)) if "f16p" in n]
+
+
+def small_m_variants(abi, ctx, scope, workloads):
+    return [i for i, n in enumerate(variant_names(abi, ctx, scope, workloads)) if "f16s" in n]
 
 
 def oracle_gemm(oracle, case, mode, threads=8, rows=None):
@@ -177,7 +184,7 @@ def test_expansion_is_bit_exact(abi, ctx, scope, oracle, workloads, dtype, bits,
     np.testing.assert_array_equal(target.download().view(np.uint8), want.reshape(-1).view(np.uint8))
 
 
-@pytest.mark.parametrize("precision", ["f32", "f16", "f16-pair-codes"])
+@pytest.mark.parametrize("precision", ["f32", "f16", "f16-pair-codes", "f16-small-m"])
 @pytest.mark.parametrize("bits,inner,columns,groups", [
     (5, 128, 256, 1), (6, 96, 48, 1), (6, 64, 3072, 3), (5, 160, 640, 1), (6, 32, 16, 1),
     (6, 128, 96, 3)])
@@ -190,6 +197,9 @@ def test_prepared_operand_order_is_bit_exact(abi, ctx, scope, oracle, workloads,
     variant = None
     if precision == "f16-pair-codes":
         variant = pair_code_variants(abi, ctx, scope, workloads)[0]
+        precision = "f16"
+    elif precision == "f16-small-m":
+        variant = small_m_variants(abi, ctx, scope, workloads)[-1]
         precision = "f16"
     if precision == "f16" and columns % 8:
         pytest.skip("f16 GEMM needs N % 8 == 0")
@@ -294,6 +304,31 @@ def test_pair_code_variants_parity(abi, ctx, scope, oracle, workloads, rows, inn
     ref = oracle_gemm(oracle, case, "f16-chain")
     truth = oracle_gemm(oracle, case, "f64")
     for variant in pair_code_variants(abi, ctx, scope, workloads):
+        got = run_case(abi, ctx, scope, case, variant=variant, repeats=2)
+        assert np.all(np.isfinite(got.astype(np.float32))), variant
+        norm_ref, _ = oracle.relative_errors(got, ref)
+        norm_truth, _ = oracle.relative_errors(got, truth)
+        assert norm_ref <= F16_TOL_REFERENCE and norm_truth <= F16_TOL_TRUTH, (variant, norm_ref, norm_truth)
+
+
+@pytest.mark.parametrize("rows,inner,columns,bits,groups,activation,bias,scale", [
+    (64, 1024, 4096, 5, 1, "silu", False, None),       # FF expand, one third of a window
+    (188, 1024, 3072, 6, 3, "none", False, None),      # QKV of one window, 3 groups
+    (1, 4096, 1024, 5, 1, "none", False, 0.5),         # FF contract, one row
+    (37, 1056, 640, 6, 1, "relu", True, None),         # K % 64 = 32, projector-like N
+    (250, 256, 96, 6, 3, "silu", True, None),          # 3 groups of 32 columns
+    (130, 512, 2048, 5, 1, "none", False, 1.0),        # rows past a 128-row block
+])
+def test_small_m_variants_parity(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits, groups,
+                                 activation, bias, scale):
+    """Every small-M variant (eight wavefronts taking K blocks round robin,
+    activations read straight from global memory) against the oracle, with
+    repeated launches bit-identical."""
+    case = workloads.gemm_case(rows * 3 + inner + columns, rows, inner, columns, bits, dtype=np.float16,
+                               groups=groups, activation=activation, bias=bias, residual_scale=scale)
+    ref = oracle_gemm(oracle, case, "f16-chain")
+    truth = oracle_gemm(oracle, case, "f64")
+    for variant in small_m_variants(abi, ctx, scope, workloads):
         got = run_case(abi, ctx, scope, case, variant=variant, repeats=2)
         assert np.all(np.isfinite(got.astype(np.float32))), variant
         norm_ref, _ = oracle.relative_errors(got, ref)
