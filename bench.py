@@ -13,6 +13,10 @@ throughput on a bounded sample of the same workload.
 Other workloads (for profiling; same JSON shape):
   single-gemm-fp32  X[256x1024] f32 x 6-bit W 1024->4096 + bias
   small-m           5-bit 1024->4096 f16 GEMM at --rows M (HBM-bound regime)
+  conv-module       Conformer convolution module, fp16, 16 windows x 188 x 1024:
+                    P = X PW1 (6-bit 1024->2048), Z = SiLU(BN(DW9(GLU(P)))),
+                    Y = X + Z PW2 (6-bit 1024->1024); TFLOP/s counts the two
+                    GEMMs, the step time includes the fused conv tail
 """
 from __future__ import annotations
 
@@ -39,7 +43,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="ff-block",
-                   choices=["ff-block", "single-gemm-fp32", "small-m"])
+                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module"])
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
@@ -119,6 +123,36 @@ def build_small_m(abi, ctx, keep, rows):
     return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16")], config, case
 
 
+def build_conv_module(abi, ctx, keep):
+    import parakeet_wgsl_amd.workloads as wl
+    mod = wl.conv_module(0)
+    m, d = mod.x.shape
+    conv = mod.conv
+    x = keep(ctx.array(mod.x))
+    p = keep(ctx.empty((m, 2 * d), np.float16))
+    z = keep(ctx.empty((m, d), np.float16))
+    y = keep(ctx.empty((m, d), np.float16))
+    pw1 = abi.GemmOp(ctx, a=x, packed=keep(ctx.array(mod.pw1.packed)), palette=keep(ctx.array(mod.pw1.palette)),
+                     output=p, bits=6, rows=m, inner=d, columns=2 * d, label="conv-pointwise1")
+    tail = abi.ConformerConvOp(
+        ctx, pointwise_input=p, depthwise_weights=keep(ctx.array(conv.weights)),
+        batch_norm_scale=keep(ctx.array(conv.scale)), batch_norm_shift=keep(ctx.array(conv.shift)),
+        valid_lengths=keep(ctx.array(conv.valid)), output=z, batch_size=conv.batch, frames=conv.frames,
+        label="conv-glu-depthwise-bn-silu")
+    pw2 = abi.GemmOp(ctx, a=z, packed=keep(ctx.array(mod.pw2.packed)), palette=keep(ctx.array(mod.pw2.palette)),
+                     output=y, bits=6, rows=m, inner=d, columns=d, residual=x, residual_scale=1.0,
+                     label="conv-pointwise2-residual")
+    c1 = mod.pw1_case()
+    c2 = mod.pw2_case(np.zeros((m, d), np.float16))
+    kernels = [Kernel("conv-pointwise1", pw1, c1.flops, c1.algorithmic_bytes(), "f16"),
+               Kernel("conv-tail", tail, 0, conv.algorithmic_bytes(), "f16"),
+               Kernel("conv-pointwise2", pw2, c2.flops, c2.algorithmic_bytes(), "f16")]
+    config = {"workload": "conformer-conv-module-fp16", "windows": conv.batch, "frames": conv.frames, "rows": m,
+              "d_model": d, "palette_bits": 6, "depthwise_kernel": 9,
+              "epilogues": ["glu", "depthwise9", "batchnorm", "silu", "residual"]}
+    return kernels, config, mod
+
+
 def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
     """The oracle (reference semantics restated in C) on a bounded sample:
     row batches of the same workload until about `budget_s` seconds of wall
@@ -143,6 +177,21 @@ def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
             pko.gemm(data.a[lo:hi], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
                      mode="f32-chain", threads=threads)
         what = "rows, f32 fma chain (reference fp32 semantics)"
+    elif workload == "conv-module":
+        # whole windows: the depthwise convolution spans frames of one window
+        frames, conv = data.conv.frames, data.conv
+        total_rows, per_row_flops, batch = data.x.shape[0], 2 * 1024 * 2048 + 2 * 1024 * 1024, frames
+
+        def run(lo, hi):
+            x = data.x[lo:hi]
+            w = lo // frames
+            p = pko.gemm(x, data.pw1.packed, 6, data.pw1.palette, 2048, mode="f16-chain", threads=threads)
+            zz = pko.conformer_conv(p, conv.weights, conv.scale, conv.shift, conv.valid[w:w + 1], batch=1,
+                                    frames=frames)
+            pko.gemm(zz, data.pw2.packed, 6, data.pw2.palette, 1024, residual=x, residual_scale=1.0,
+                     mode="f16-chain", threads=threads)
+        what = ("rows (whole 188-frame windows) of the conv module: PW1, GLU/DW9/BN/SiLU tail, PW2 + residual; "
+                "f16-accumulator GEMM chain and f32 tail (reference fp16 semantics)")
     else:
         total_rows, per_row_flops = data.rows, 2 * 1024 * 4096
 
@@ -198,11 +247,14 @@ def main():
         kernels, config, data = build_ff_block(abi, ctx, keep)
     elif args.workload == "single-gemm-fp32":
         kernels, config, data = build_single_gemm(abi, ctx, keep)
+    elif args.workload == "conv-module":
+        kernels, config, data = build_conv_module(abi, ctx, keep)
     else:
         kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
     if args.variant >= 0:
         for k in kernels:
-            k.op.set_variant(args.variant)
+            if isinstance(k.op, abi.GemmOp):
+                k.op.set_variant(args.variant)
 
     stream = ctx.stream
     for _ in range(args.warmup):
@@ -253,7 +305,7 @@ def main():
         roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": dom["gbs"] / PEAK_HBM_GBS}
     roofline["kernel"] = dom["kernel"]
-    roofline["traffic"] = read_traffic(dominant.name, dom["kernel"]) if args.workload == "ff-block" else None
+    roofline["traffic"] = read_traffic(dominant.name, dom["kernel"])
 
     cpu = None
     if not args.no_cpu:

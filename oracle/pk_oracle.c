@@ -415,3 +415,78 @@ int pko_gemm(const pko_gemm_args *p, int mode, int threads) {
   free(dense);
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Conformer convolution tail (src/webgpu/kernels/conformer-conv.ts:495-573) */
+/* ------------------------------------------------------------------------ */
+
+static inline double conv_in(int dtype, const void *p, uint64_t idx) {
+  if (dtype == PKO_DTYPE_F16) return pko_f16_to_f64(((const uint16_t *)p)[idx]);
+  if (dtype == PKO_DTYPE_F64) return ((const double *)p)[idx];
+  return (double)((const float *)p)[idx];
+}
+
+/* sigmoid with the reference's clamp: 1 / (1 + exp(-clamp(v, -20, 20))). */
+static inline float sigmoid_f32(float v) {
+  const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
+  return 1.0f / (1.0f + expf(-bounded));
+}
+static inline double sigmoid_f64(double v) {
+  const double bounded = fmin(fmax(v, -20.0), 20.0);
+  return 1.0 / (1.0 + exp(-bounded));
+}
+
+int pko_conformer_conv(int dtype, int mode, uint32_t batch, uint32_t frames, uint32_t channels,
+                       const void *input, const void *weights, const float *scale,
+                       const float *shift, const uint32_t *valid, void *output) {
+  enum { TAPS = 9, RADIUS = 4 };
+  if (!input || !weights || !scale || !shift || !valid || !output || batch == 0 || frames == 0 ||
+      channels == 0 || (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64) ||
+      (mode != PKO_MODE_F32_CHAIN && mode != PKO_MODE_F64))
+    return 1;
+  const uint64_t in_row = 2ull * channels;
+  for (uint32_t b = 0; b < batch; ++b) {
+    for (uint32_t f = 0; f < frames; ++f) {
+      for (uint32_t c = 0; c < channels; ++c) {
+        float sum32 = 0.0f;
+        double sum64 = 0.0;
+        for (int k = 0; k < TAPS; ++k) {
+          /* GLU of frame f - 4 + k, zero outside [0, frames) and past the
+             batch item's valid length (conformer-conv.ts:520-540). */
+          const int64_t t = (int64_t)f - RADIUS + k;
+          double value = 0.0, gate = 0.0;
+          const int live = t >= 0 && t < (int64_t)frames && t < (int64_t)valid[b];
+          if (live) {
+            const uint64_t row = (uint64_t)b * frames + (uint64_t)t;
+            value = conv_in(dtype, input, row * in_row + c);
+            gate = conv_in(dtype, input, row * in_row + channels + c);
+          }
+          const double w = conv_in(dtype, weights, (uint64_t)k * channels + c);
+          if (mode == PKO_MODE_F32_CHAIN) {
+            const float glu = live ? (float)value * sigmoid_f32((float)gate) : 0.0f;
+            sum32 = fmaf(glu, (float)w, sum32);
+          } else {
+            const double glu = live ? value * sigmoid_f64(gate) : 0.0;
+            sum64 += glu * w;
+          }
+        }
+        double activated;
+        if (mode == PKO_MODE_F32_CHAIN) {
+          const float affine = sum32 * scale[c] + shift[c];
+          activated = (double)(affine * sigmoid_f32(affine));
+        } else {
+          const double affine = sum64 * (double)scale[c] + (double)shift[c];
+          activated = affine * sigmoid_f64(affine);
+        }
+        const uint64_t out_idx = ((uint64_t)b * frames + f) * channels + c;
+        if (dtype == PKO_DTYPE_F16)
+          ((uint16_t *)output)[out_idx] = pko_f64_to_f16(activated);
+        else if (dtype == PKO_DTYPE_F64)
+          ((double *)output)[out_idx] = activated;
+        else
+          ((float *)output)[out_idx] = (float)activated;
+      }
+    }
+  }
+  return 0;
+}

@@ -32,6 +32,11 @@
  *                         pinned: exact small-integer cases, the f16 rounding
  *                         function against every f16 value and its midpoints.
  *   pko_gemm (F64)        reference-independent truth of the same expression.
+ *   pko_conformer_conv    src/webgpu/kernels/conformer-conv.ts:495-573 (GLU of
+ *                         the pointwise-1 output, same-padded depthwise k9 over
+ *                         frames, folded batch norm, SiLU); pinned by closed
+ *                         forms in tests/test_oracle.py (one-hot taps, zero
+ *                         gates, frames past the valid length, the f64 twin).
  *
  * Status codes: 0 ok, 1 invalid argument.
  */
@@ -59,6 +64,7 @@ enum {
 enum {
   PKO_DTYPE_F16 = 0,
   PKO_DTYPE_F32 = 1,
+  PKO_DTYPE_F64 = 2, /* pko_conformer_conv only: double input and output */
 };
 
 typedef struct pko_gemm_args {
@@ -97,6 +103,17 @@ int pko_expand(int bits, int dtype, int tile_major, const uint32_t *packed,
                uint32_t palette_group_columns, uint32_t palette_groups,
                const void *palette, void *out);
 int pko_gemm(const pko_gemm_args *args, int mode, int threads);
+
+/* Conformer convolution tail. input [batch*frames, 2*channels] (dtype):
+   channels [0, C) are GLU values, [C, 2C) gates; weights [9, channels]
+   (dtype); scale, shift [channels] f32; valid [batch] frame counts;
+   output [batch*frames, channels] (dtype). mode PKO_MODE_F32_CHAIN: the
+   reference's f32 arithmetic (fma over taps 0..8); PKO_MODE_F64: the same
+   expression in double (output still rounded to dtype). dtype PKO_DTYPE_F64
+   takes double input and weights and writes double output (truth chains). */
+int pko_conformer_conv(int dtype, int mode, uint32_t batch, uint32_t frames, uint32_t channels,
+                       const void *input, const void *weights, const float *scale,
+                       const float *shift, const uint32_t *valid, void *output);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,7 @@ Reference functions restated (see pk_oracle.h for the pins):
   expand          src/model/palette-expander.ts:478-587
   gemm            src/webgpu/kernels/gemm.ts:1362-1716, :2006-2044 (f16),
                   :2356-2599, :2847-2869 (f32)
+  conformer_conv  src/webgpu/kernels/conformer-conv.ts:495-573
 """
 from __future__ import annotations
 
@@ -27,7 +28,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 ACT = {"none": 0, "silu": 1, "relu": 2}
 MODE = {"f32-chain": 0, "f16-chain": 1, "f64": 2}
-DTYPE = {"f16": 0, "f32": 1}
+DTYPE = {"f16": 0, "f32": 1, "f64": 2}
 
 
 def build() -> None:
@@ -80,6 +81,7 @@ def lib() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_void_p,
         ]
         _lib.pko_gemm.argtypes = [ctypes.POINTER(_GemmArgs), ctypes.c_int, ctypes.c_int]
+        _lib.pko_conformer_conv.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 6
     return _lib
 
 
@@ -185,6 +187,31 @@ def gemm(a, words, bits, palette, columns, *, bias=None, residual=None,
     )
     if lib().pko_gemm(ctypes.byref(args), MODE[mode], int(threads)):
         raise ValueError("gemm rejected its arguments")
+    return out
+
+
+def conformer_conv(pointwise, weights, scale, shift, valid, *, batch, frames, mode="f32-chain") -> np.ndarray:
+    """Conformer convolution tail (conformer-conv.ts:495-573): GLU of the
+    pointwise-1 output [batch*frames, 2C], depthwise k9 over frames (zero
+    outside [0, frames) and past each valid length), folded batch norm, SiLU.
+    mode "f32-chain" (reference arithmetic) or "f64"; the output has the
+    input's dtype (float16, float32, or float64 for truth chains)."""
+    pointwise = np.ascontiguousarray(pointwise)
+    weights = np.ascontiguousarray(weights, dtype=pointwise.dtype)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    shift = np.ascontiguousarray(shift, dtype=np.float32)
+    valid = np.ascontiguousarray(valid, dtype=np.uint32)
+    channels = pointwise.shape[1] // 2
+    if pointwise.shape != (batch * frames, 2 * channels) or weights.shape != (9, channels):
+        raise ValueError("conformer_conv shape mismatch")
+    out = np.empty((batch * frames, channels), dtype=pointwise.dtype)
+    names = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.float64): "f64"}
+    if pointwise.dtype not in names:
+        raise ValueError(f"conformer_conv takes float16/32/64 input, not {pointwise.dtype}")
+    dtype = DTYPE[names[pointwise.dtype]]
+    if lib().pko_conformer_conv(dtype, MODE[mode], batch, frames, channels, _ptr(pointwise), _ptr(weights),
+                                _ptr(scale), _ptr(shift), _ptr(valid), _ptr(out)):
+        raise ValueError("conformer_conv rejected its arguments")
     return out
 
 

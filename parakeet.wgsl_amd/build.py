@@ -32,7 +32,10 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", INCLUDE, "-I", CSRC,
 ]
-SOURCES = ["pk_abi.cpp", "pk_codes.hip", "pk_gemm_f16.hip", "pk_gemm_f16k.hip", "pk_gemm_f16s.hip", "pk_gemm_f32.hip"]
+SOURCES = [
+    "pk_abi.cpp", "pk_conv_abi.cpp", "pk_codes.hip", "pk_conv.hip", "pk_gemm_f16.hip", "pk_gemm_f16k.hip",
+    "pk_gemm_f16s.hip", "pk_gemm_f32.hip",
+]
 NODE_INCLUDE = "/usr/include/node"
 
 

@@ -10,14 +10,14 @@
 #include <cstring>
 #include <string>
 
+#include "pk_abi_internal.h"
 #include "pk_internal.h"
 #include "pk_palette.h"
 
-namespace {
+namespace pk_abi {
 
 thread_local std::string g_error;
 
-int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int status, const char* fmt, ...) {
   char buffer[512];
   va_list args;
@@ -28,18 +28,18 @@ int fail(int status, const char* fmt, ...) {
   return status;
 }
 
-int ok() { return PK_OK; }
+int check_ctx(const pk_context* ctx) {
+  if (!ctx) return fail(PK_INVALID_ARGUMENT, "context is null");
+  return PK_OK;
+}
 
-#define PK_HIP(call, what)                                                                  \
-  do {                                                                                      \
-    const hipError_t pk_e_ = (call);                                                        \
-    if (pk_e_ != hipSuccess)                                                                \
-      return fail(PK_DEVICE_ERROR, "%s failed: %s", (what), hipGetErrorString(pk_e_));      \
-  } while (0)
+}  // namespace pk_abi
+
+using namespace pk_abi;
+
+namespace {
 
 const char* safe_label(const char* label) { return label ? label : "palette-gemm"; }
-
-bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // The 14 fixed production signatures (src/webgpu/kernels/gemm.ts:204-356;
 // the FP32 registry :2154-2306 has the same signatures). residual_scale < 0
@@ -74,11 +74,6 @@ const char* activation_name(int a) {
 }
 
 }  // namespace
-
-struct pk_context {
-  int device = 0;
-  hipStream_t stream = nullptr;
-};
 
 struct pk_prepared_weight {
   pk_context* ctx = nullptr;
@@ -120,15 +115,6 @@ void weight_unref(pk_prepared_weight* w) {
     }
     delete w;
   }
-}
-
-hipStream_t stream_or_default(pk_context* ctx, void* stream) {
-  return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
-}
-
-int check_ctx(const pk_context* ctx) {
-  if (!ctx) return fail(PK_INVALID_ARGUMENT, "context is null");
-  return PK_OK;
 }
 
 int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, uint32_t columns,

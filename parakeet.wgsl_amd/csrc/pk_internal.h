@@ -159,4 +159,33 @@ const char* f32_variant_name(int bits, int index);
 hipError_t launch_gemm_f32(int bits, int variant, const GemmArgs& args, hipStream_t stream,
                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
+// Fused Conformer convolution tail (pk_conv.hip). Element type of input,
+// weights and output is f16 or f32; scale/shift are f32.
+struct ConvArgs {
+  const void* input;              // [batch * frames, 2 * channels]: values, then gates
+  const void* weights;            // [9, channels]
+  const float* scale;             // [channels] folded batch-norm scale
+  const float* shift;             // [channels] folded batch-norm shift
+  const uint32_t* valid_lengths;  // [batch]
+  void* output;                   // [batch * frames, channels]
+  uint32_t frames;
+  uint32_t channels;              // multiple of 8
+  uint32_t runs;                  // frame runs per item (set by the launcher)
+  uint32_t blocks_per_item;       // set by the launcher
+};
+
+struct ConvGeometry {
+  const char* name;
+  int channels_per_thread;
+  uint32_t runs;
+  uint32_t blocks_per_item;
+  uint32_t grid;
+  uint32_t block_threads;
+};
+
+int conv_variant_count(bool f16);
+ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch);
+hipError_t launch_conformer_conv(bool f16, int variant, const ConvArgs& args, uint32_t batch,
+                                 hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+
 }  // namespace pk

@@ -1,4 +1,4 @@
-"""ctypes binding of libpk_palette.so (include/pk_palette.h).
+"""ctypes binding of libpk_palette.so (include/pk_palette.h, include/pk_conv.h).
 
 A thin Python view of the C ABI, used by the tests and the benchmark. It
 raises PaletteError (or PaletteRangeError, mirroring the reference's
@@ -126,7 +126,46 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
-# Every function the header declares: name -> (restype, argtypes).
+class ConvDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("frames", ctypes.c_uint32),
+        ("channels", ctypes.c_uint32),
+        ("pointwise_input", ctypes.c_void_p),
+        ("pointwise_input_bytes", ctypes.c_uint64),
+        ("depthwise_weights", ctypes.c_void_p),
+        ("depthwise_weights_bytes", ctypes.c_uint64),
+        ("batch_norm_scale", ctypes.c_void_p),
+        ("batch_norm_scale_bytes", ctypes.c_uint64),
+        ("batch_norm_shift", ctypes.c_void_p),
+        ("batch_norm_shift_bytes", ctypes.c_uint64),
+        ("valid_lengths", ctypes.c_void_p),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+    ]
+
+
+class ConvPlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_uint32),
+        ("input_bytes", ctypes.c_uint64),
+        ("output_bytes", ctypes.c_uint64),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("depthwise_weight_bytes", ctypes.c_uint64),
+        ("affine_bytes", ctypes.c_uint64),
+        ("grid", ctypes.c_uint32 * 3),
+        ("block_threads", ctypes.c_uint32),
+        ("lds_bytes", ctypes.c_uint32),
+        ("algorithmic_bytes", ctypes.c_uint64),
+        ("kernel", ctypes.c_char * 64),
+    ]
+
+
+# Every function the headers declare: name -> (restype, argtypes).
 _VP = ctypes.c_void_p
 _PPV = ctypes.POINTER(ctypes.c_void_p)
 SIGNATURES = {
@@ -166,6 +205,17 @@ SIGNATURES = {
     "pk_gemm_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
     "pk_palette_expand": (ctypes.c_int, [_VP, ctypes.POINTER(ExpandDesc), _VP]),
     "pk_unpack_codes": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_uint64, _VP, _VP]),
+    "pk_conv_plan_shape": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.POINTER(ConvPlanInfo)]),
+    "pk_conv_validate": (ctypes.c_int, [ctypes.POINTER(ConvDesc)]),
+    "pk_conv_create": (ctypes.c_int, [_VP, ctypes.POINTER(ConvDesc), _PPV]),
+    "pk_conv_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_conv_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_conv_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(ConvPlanInfo)]),
+    "pk_conv_destroy": (ctypes.c_int, [_VP]),
+    "pk_conv_release": (ctypes.c_int, [_VP]),
+    "pk_conv_variant_count": (ctypes.c_int, [ctypes.c_int]),
+    "pk_conv_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
 }
 
 _lib = None
@@ -397,3 +447,65 @@ class GemmOp:
 
 def variant_count(precision: str) -> int:
     return int(load().pk_gemm_variant_count(PRECISION[precision]))
+
+
+def _slice(array):
+    """(pointer, bytes) of a DeviceArray, or (None, 0)."""
+    return (array.ptr, array.nbytes) if array is not None else (None, 0)
+
+
+def conv_desc(*, pointwise_input, depthwise_weights, batch_norm_scale, batch_norm_shift, valid_lengths, output,
+              batch_size: int, frames: int, channels: int = 0, precision: str | None = None,
+              label: str = "conformer-conv") -> ConvDesc:
+    """A pk_conv_desc over DeviceArrays (or any objects with ptr/nbytes)."""
+    if precision is None:
+        precision = "f16" if pointwise_input.dtype == np.float16 else "f32"
+    return ConvDesc(ctypes.sizeof(ConvDesc), label.encode(), PRECISION[precision], batch_size, frames, channels,
+                    *_slice(pointwise_input), *_slice(depthwise_weights), *_slice(batch_norm_scale),
+                    *_slice(batch_norm_shift), *_slice(valid_lengths), *_slice(output))
+
+
+def plan_conformer_conv(batch_size: int, frames: int, precision: str = "f16", channels: int = 0) -> ConvPlanInfo:
+    """planFusedConformerConv (conformer-conv.ts:72-115) through pk_conv_plan_shape."""
+    info = ConvPlanInfo()
+    check(load().pk_conv_plan_shape(PRECISION[precision], batch_size, frames, channels, ctypes.byref(info)))
+    return info
+
+
+class ConformerConvOp:
+    """One fused GLU / depthwise k9 / folded BN / SiLU dispatch
+    (FusedConformerConvKernel.createDispatch, conformer-conv.ts:255-344)."""
+
+    def __init__(self, ctx: Context, **descriptor):
+        self.desc = conv_desc(**descriptor)
+        handle = ctypes.c_void_p()
+        check(load().pk_conv_create(ctx.handle, ctypes.byref(self.desc), ctypes.byref(handle)))
+        self.handle = handle.value
+        self.ctx = ctx
+
+    def enqueue(self, active_batch: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_conv_enqueue(self.handle, active_batch, stream))
+        else:
+            check(load().pk_conv_enqueue_timed(self.handle, active_batch, stream,
+                                               start.handle if start else None, end.handle if end else None))
+
+    def plan(self, active_batch: int = 0) -> ConvPlanInfo:
+        info = ConvPlanInfo()
+        check(load().pk_conv_plan(self.handle, active_batch, ctypes.byref(info)))
+        return info
+
+    def set_variant(self, variant: int) -> None:
+        check(load().pk_conv_set_variant(self.handle, variant))
+
+    def destroy(self) -> None:
+        check(load().pk_conv_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_conv_release(self.handle))
+            self.handle = None
+
+
+def conv_variant_count(precision: str) -> int:
+    return int(load().pk_conv_variant_count(PRECISION[precision]))

@@ -154,3 +154,79 @@ def gemm_case(seed: int, rows: int, inner: int, columns: int, bits: int, *, dtyp
     r = normal(rng, (rows, columns), 1.0, dtype) if residual_scale is not None else None
     return GemmCase(f"gemm-{rows}x{inner}x{columns}-b{bits}", a, w, bias=b, residual=r,
                     residual_scale=residual_scale, activation=activation)
+
+
+@dataclass
+class ConvCase:
+    """Operands of the fused Conformer convolution tail: the pointwise-1 output
+    [batch*frames, 2C] (GLU values, then gates), depthwise weights [9, C],
+    folded batch-norm scale and shift [C] (f32) and valid lengths [batch]."""
+    pointwise: np.ndarray | None
+    weights: np.ndarray
+    scale: np.ndarray
+    shift: np.ndarray
+    valid: np.ndarray
+    batch: int
+    frames: int
+
+    @property
+    def channels(self) -> int:
+        return self.weights.shape[1]
+
+    def algorithmic_bytes(self, batch: int | None = None) -> int:
+        """Compulsory HBM bytes of one launch over `batch` windows: the
+        pointwise input and the output once, weights, affine, lengths."""
+        batch = self.batch if batch is None else batch
+        e = self.weights.dtype.itemsize
+        rows = batch * self.frames
+        return rows * 3 * self.channels * e + self.weights.nbytes + 8 * self.channels + 4 * batch
+
+
+def conv_case(seed: int, batch: int, frames: int, channels: int = 1024, *, dtype=np.float16,
+              valid=None, weight_std: float = 0.05, with_input: bool = True) -> ConvCase:
+    """Seeded conv-tail operands: pointwise input ~ N(0,1), depthwise weights
+    ~ N(0, weight_std), scale ~ 1 + N(0, 0.1), shift ~ N(0, 0.1); valid lengths
+    uniform integers in [ceil(frames/2), frames] unless given."""
+    rng = np.random.default_rng(seed)
+    pointwise = normal(rng, (batch * frames, 2 * channels), 1.0, dtype) if with_input else None
+    weights = normal(rng, (9, channels), weight_std, dtype)
+    scale = (1.0 + 0.1 * rng.standard_normal(channels)).astype(np.float32)
+    shift = (0.1 * rng.standard_normal(channels)).astype(np.float32)
+    if valid is None:
+        valid = rng.integers((frames + 1) // 2, frames + 1, size=batch)
+    return ConvCase(pointwise, weights, scale, shift, np.asarray(valid, dtype=np.uint32), batch, frames)
+
+
+@dataclass
+class ConvModule:
+    """Conformer convolution module after its layer norm: P = X PW1, Z =
+    SiLU(BN(DW9(GLU(P)))), Y = X + Z PW2 (src/webgpu/encoder.ts:2011-2075)."""
+    x: np.ndarray
+    pw1: PaletteMatrix
+    pw2: PaletteMatrix
+    conv: ConvCase
+
+    def pw1_case(self) -> GemmCase:
+        return GemmCase("conv-pointwise1", self.x, self.pw1)
+
+    def pw2_case(self, z: np.ndarray) -> GemmCase:
+        return GemmCase("conv-pointwise2-residual", z, self.pw2, residual=self.x, residual_scale=1.0)
+
+    @property
+    def flops(self) -> int:
+        m = self.x.shape[0]
+        return 2 * m * self.pw1.inner * self.pw1.columns + 2 * m * self.pw2.inner * self.pw2.columns
+
+
+def conv_module(seed: int = 0, windows: int = 16, frames: int = 188, d_model: int = 1024,
+                bits: int = 6) -> ConvModule:
+    """Input [windows x frames x d_model] f16 ~ N(0,1); 6-bit PW1 d->2d and
+    PW2 d->d with one 64-entry f16 LUT each ~ N(0, 0.02); depthwise k9 f16
+    weights ~ N(0, 0.05); folded BN scale ~ 1 + N(0, 0.1), shift ~ N(0, 0.1);
+    valid lengths uniform in [frames/2, frames]."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (windows * frames, d_model), 1.0, np.float16)
+    pw1 = palette_matrix(rng, bits, d_model, 2 * d_model, dtype=np.float16)
+    pw2 = palette_matrix(rng, bits, d_model, d_model, dtype=np.float16)
+    conv = conv_case(int(rng.integers(1 << 31)), windows, frames, d_model, with_input=False)
+    return ConvModule(x, pw1, pw2, conv)

@@ -1,29 +1,35 @@
 """CPU-only checks of the C-ABI library: it loads, exports exactly what
-include/pk_palette.h declares, and the binding covers every entry point.
-No compute call is made (this container has no GPU)."""
+include/*.h declares, and the binding covers every entry point. No compute
+call is made (this container has no GPU); the host-side contract checks and
+launch plans are exercised through the device-free entry points."""
 import ctypes
+import glob
 import json
 import os
 import re
 import subprocess
 
 import numpy as np
+import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "pk_palette.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(pk_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        names.update(re.findall(r"\b(pk_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ["pk_context_create", "pk_gemm_create", "pk_gemm_enqueue", "pk_gemm_destroy",
                      "pk_prepared_weight_create", "pk_palette_expand", "pk_unpack_codes",
-                     "pk_gemm_plan", "pk_last_error"]:
+                     "pk_gemm_plan", "pk_last_error", "pk_conv_create", "pk_conv_enqueue",
+                     "pk_conv_destroy", "pk_conv_plan_shape"]:
         assert required in names
 
 
@@ -49,8 +55,10 @@ def test_struct_layouts_match_the_c_compiler(abi, tmp_path):
     """Every ctypes field offset equals the C compiler's offsetof()."""
     structs = {"pk_weight_desc": abi.WeightDesc, "pk_gemm_desc": abi.GemmDesc,
                "pk_expand_desc": abi.ExpandDesc, "pk_gemm_plan_info": abi.PlanInfo,
-               "pk_device_info": abi.DeviceInfo}
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', "int main(void) {"]
+               "pk_device_info": abi.DeviceInfo, "pk_conv_desc": abi.ConvDesc,
+               "pk_conv_plan_info": abi.ConvPlanInfo}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', '#include "pk_conv.h"',
+             "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
         for field, _ in cls._fields_:
@@ -123,3 +131,117 @@ def test_algorithmic_bytes_formula(workloads):
     # 6-bit codes + 64 f32 LUT + X + Y + bias
     assert c1.algorithmic_bytes() == 1024 * 4096 * 6 // 8 + 256 + 256 * 1024 * 4 + 256 * 4096 * 4 + 4096 * 4
     assert c1.flops == 2 * 256 * 1024 * 4096
+
+
+# ------------------------------------------------------ conformer conv plan
+
+
+def test_conv_plan_matches_reference_shapes(abi):
+    """planFusedConformerConv known answers (test/webgpu/conformer-conv-kernel-shapes.test.ts:18-58):
+    batch 2 x 188 frames is 376 rows; byte lengths for fp16 and fp32."""
+    for precision, elem in (("f16", 2), ("f32", 4)):
+        plan = abi.plan_conformer_conv(2, 188, precision)
+        assert plan.rows == 376
+        assert plan.input_bytes == 376 * 2048 * elem
+        assert plan.output_bytes == 376 * 1024 * elem
+        assert plan.valid_lengths_bytes == 2 * 4
+        assert plan.depthwise_weight_bytes == 9 * 1024 * elem
+        assert plan.affine_bytes == 1024 * 4
+        assert plan.algorithmic_bytes == 376 * 3072 * elem + 9 * 1024 * elem + 2 * 4096 + 8
+        assert plan.kernel.startswith(b"pk_conformer_conv_" + precision.encode())
+        # the grid covers every (window, frame run, channel group) once
+        cpt, run = map(int, re.search(rb"_c(\d+)_f(\d+)$", plan.kernel).groups())
+        per_item = -(-188 // run) * (1024 // cpt)
+        assert plan.grid[0] == 2 * -(-per_item // plan.block_threads)
+
+
+def test_conv_plan_rejects_non_positive_shapes(abi):
+    with pytest.raises(abi.PaletteRangeError, match="batchSize must be a positive integer"):
+        abi.plan_conformer_conv(0, 188)
+    with pytest.raises(abi.PaletteRangeError, match="frames must be a positive integer"):
+        abi.plan_conformer_conv(1, 0)
+    with pytest.raises(abi.PaletteRangeError, match="multiple of 8"):
+        abi.plan_conformer_conv(1, 4, channels=12)
+
+
+class _Fake:
+    """A device slice stand-in for the host-only checks: an address and a size."""
+
+    def __init__(self, ptr, nbytes, dtype=np.float16):
+        self.ptr, self.nbytes, self.dtype = ptr, nbytes, np.dtype(dtype)
+
+
+def _conv_fakes(batch=2, frames=188, channels=1024, elem=2):
+    rows = batch * frames
+    dtype = np.float16 if elem == 2 else np.float32
+    return dict(
+        pointwise_input=_Fake(0x10000000, rows * 2 * channels * elem, dtype),
+        depthwise_weights=_Fake(0x20000000, 9 * channels * elem, dtype),
+        batch_norm_scale=_Fake(0x30000000, channels * 4, np.float32),
+        batch_norm_shift=_Fake(0x30100000, channels * 4, np.float32),
+        valid_lengths=_Fake(0x40000000, batch * 4, np.uint32),
+        output=_Fake(0x50000000, rows * channels * elem, dtype),
+        batch_size=batch, frames=frames, label="layer0-convolution-glu-depthwise-bn-silu")
+
+
+def _validate(abi, **kw):
+    desc = abi.conv_desc(**kw)
+    abi.check(abi.load().pk_conv_validate(ctypes.byref(desc)))
+
+
+def test_conv_validate_accepts_the_reference_descriptor(abi):
+    _validate(abi, **_conv_fakes())
+    _validate(abi, **_conv_fakes(elem=4))
+
+
+@pytest.mark.parametrize("role,field,message", [
+    ("pointwise input", "pointwise_input", "pointwise input needs 1540096 bytes; arena slice has 1540095"),
+    ("output", "output", "output needs 770048 bytes; arena slice has 770047"),
+    ("valid lengths", "valid_lengths", "valid lengths needs 8 bytes; arena slice has 7"),
+])
+def test_conv_validate_arena_capacity_messages(abi, role, field, message):
+    """requireArenaCapacity (conformer-conv.ts:390-401) is a RangeError."""
+    kw = _conv_fakes()
+    kw[field] = _Fake(kw[field].ptr, kw[field].nbytes - 1, kw[field].dtype)
+    with pytest.raises(abi.PaletteRangeError, match=re.escape(message)):
+        _validate(abi, **kw)
+
+
+def test_conv_validate_packed_tensor_messages(abi):
+    """requirePackedTensor (conformer-conv.ts:403-432) is an Error naming dtype,
+    layout, logical and storage shape and byte length."""
+    kw = _conv_fakes()
+    kw["depthwise_weights"] = _Fake(kw["depthwise_weights"].ptr, 9 * 1024 * 4)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "depthwise weights must be float16 kernel-channel-vec4 logical [9,1024], storage [9,256,4], "
+            "18432 bytes")) as err:
+        _validate(abi, **kw)
+    assert err.value.status == abi.INVALID_ARGUMENT
+    kw = _conv_fakes()
+    kw["batch_norm_shift"] = _Fake(kw["batch_norm_shift"].ptr, 2048)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "folded batch norm shift must be float32 channel logical [1024], storage [1024], 4096 bytes")):
+        _validate(abi, **kw)
+
+
+def test_conv_validate_rejects_aliasing_and_misalignment(abi):
+    kw = _conv_fakes()
+    kw["output"] = _Fake(kw["pointwise_input"].ptr + 4096, kw["output"].nbytes)
+    with pytest.raises(abi.PaletteError, match="must not overlap"):
+        _validate(abi, **kw)
+    kw = _conv_fakes()
+    kw["output"] = _Fake(kw["output"].ptr + 8, kw["output"].nbytes)
+    with pytest.raises(abi.PaletteError, match="aligned"):
+        _validate(abi, **kw)
+    kw = _conv_fakes()
+    kw["batch_size"] = 0
+    with pytest.raises(abi.PaletteRangeError, match="batchSize must be a positive integer"):
+        _validate(abi, **kw)
+
+
+def test_conv_null_handles(abi):
+    lib = abi.load()
+    assert lib.pk_conv_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_conv_destroy(None) == abi.OK
+    assert lib.pk_conv_release(None) == abi.OK
+    assert abi.conv_variant_count("f16") >= 1 and abi.conv_variant_count("f32") >= 1

@@ -326,3 +326,123 @@ def test_threads_do_not_change_results(oracle):
     one = oracle.gemm(a, words, 6, palette, 64, mode="f16-chain", threads=1)
     many = oracle.gemm(a, words, 6, palette, 64, mode="f16-chain", threads=5)
     np.testing.assert_array_equal(one.view(np.uint16), many.view(np.uint16))
+
+
+# ------------------------------------------------------ conformer conv tail
+
+
+def _conv_case(rng, batch, frames, channels, dtype=np.float32):
+    pointwise = rng.standard_normal((batch * frames, 2 * channels)).astype(dtype)
+    weights = (rng.standard_normal((9, channels)) * 0.3).astype(dtype)
+    scale = (1.0 + 0.1 * rng.standard_normal(channels)).astype(np.float32)
+    shift = (0.1 * rng.standard_normal(channels)).astype(np.float32)
+    return pointwise, weights, scale, shift
+
+
+def _torch_conv_module(pointwise, weights, scale, shift, valid, batch, frames):
+    """The same tail through torch's library routines in float64: glu over the
+    channel axis, masking of frames past each valid length, a same-padded
+    grouped conv1d, then silu."""
+    import torch
+    import torch.nn.functional as F
+
+    channels = weights.shape[1]
+    x = torch.from_numpy(pointwise.astype(np.float64)).reshape(batch, frames, 2 * channels)
+    glu = F.glu(x, dim=-1)
+    live = torch.arange(frames)[None, :] < torch.tensor(valid.astype(np.int64))[:, None]
+    glu = glu * live[:, :, None]
+    kernel = torch.from_numpy(weights.astype(np.float64)).t().reshape(channels, 1, 9)
+    conv = F.conv1d(glu.transpose(1, 2), kernel, padding=4, groups=channels).transpose(1, 2)
+    affine = conv * torch.from_numpy(scale.astype(np.float64)) + torch.from_numpy(shift.astype(np.float64))
+    return F.silu(affine).reshape(batch * frames, channels).numpy()
+
+
+def test_conv_matches_torch_grouped_conv1d(oracle):
+    """glu (value half first), per-frame masking, same-padded depthwise k9
+    (conformer-conv.ts:505-560) equal torch's glu + conv1d(groups=C)."""
+    rng = np.random.default_rng(10)
+    batch, frames, channels = 3, 23, 16
+    pointwise, weights, scale, shift = _conv_case(rng, batch, frames, channels)
+    valid = np.array([23, 9, 30], dtype=np.uint32)
+    want = _torch_conv_module(pointwise, weights, scale, shift, valid, batch, frames)
+    got64 = oracle.conformer_conv(pointwise, weights, scale, shift, valid, batch=batch, frames=frames, mode="f64")
+    np.testing.assert_allclose(got64, want, rtol=2e-7, atol=1e-7)
+    got32 = oracle.conformer_conv(pointwise, weights, scale, shift, valid, batch=batch, frames=frames)
+    np.testing.assert_allclose(got32, want, rtol=2e-6, atol=2e-6)
+
+
+def test_conv_f16_output_is_one_rounding_of_the_f64_result(oracle):
+    rng = np.random.default_rng(11)
+    batch, frames, channels = 2, 17, 8
+    pointwise, weights, scale, shift = _conv_case(rng, batch, frames, channels, np.float16)
+    valid = np.array([17, 12], dtype=np.uint32)
+    want = _torch_conv_module(pointwise, weights, scale, shift, valid, batch, frames).astype(np.float16)
+    got = oracle.conformer_conv(pointwise, weights, scale, shift, valid, batch=batch, frames=frames, mode="f64")
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("tap", [0, 2, 4, 8])
+def test_conv_one_hot_tap_reads_frame_minus_four_plus_tap(oracle, tap):
+    """With zero gates (sigmoid 1/2 exactly), unit scale, zero shift and the
+    single tap `tap` set to one, the pre-activation at frame f is exactly
+    value(f - 4 + tap) / 2, or 0 outside the sequence."""
+    batch, frames, channels = 1, 12, 8
+    value = np.arange(frames * channels, dtype=np.float32).reshape(frames, channels) % 7 - 3
+    pointwise = np.concatenate([value, np.zeros_like(value)], axis=1)
+    weights = np.zeros((9, channels), np.float32)
+    weights[tap] = 1.0
+    got = oracle.conformer_conv(pointwise, weights, np.ones(channels, np.float32), np.zeros(channels, np.float32),
+                                np.array([frames], np.uint32), batch=batch, frames=frames)
+    pre = np.zeros_like(value, dtype=np.float64)
+    for f in range(frames):
+        t = f - 4 + tap
+        if 0 <= t < frames:
+            pre[f] = value[t] / 2.0
+    np.testing.assert_allclose(got, pre / (1.0 + np.exp(-pre)), rtol=1e-6, atol=1e-7)
+
+
+def test_conv_gate_sigmoid_clamps_at_twenty(oracle):
+    """sigmoid(gate) uses exp(-clamp(gate, -20, 20)) (conformer-conv.ts:489-492):
+    a gate of -30 gives 1/(1+e^20), not 1/(1+e^30)."""
+    channels = 8
+    pointwise = np.zeros((1, 2 * channels), np.float64)
+    pointwise[0, :channels] = 1e6
+    pointwise[0, channels:] = -30.0
+    weights = np.zeros((9, channels))
+    weights[4] = 1.0
+    pre = 1e6 / (1.0 + np.exp(20.0))
+    for mode in ("f64", "f32-chain"):
+        got = oracle.conformer_conv(pointwise.astype(np.float32), weights.astype(np.float32),
+                                    np.ones(channels, np.float32), np.zeros(channels, np.float32),
+                                    np.array([1], np.uint32), batch=1, frames=1, mode=mode)
+        np.testing.assert_allclose(got, pre / (1.0 + np.exp(-pre)), rtol=1e-5)
+
+
+def test_conv_frames_past_valid_length_read_zero(oracle):
+    """A zero valid length leaves only silu(shift) at every frame; lengths at or
+    beyond the frame count change nothing."""
+    rng = np.random.default_rng(12)
+    batch, frames, channels = 2, 10, 8
+    pointwise, weights, scale, shift = _conv_case(rng, batch, frames, channels)
+    got = oracle.conformer_conv(pointwise, weights, scale, shift, np.array([0, 0], np.uint32),
+                                batch=batch, frames=frames, mode="f64")
+    s = shift.astype(np.float64)
+    np.testing.assert_allclose(got, np.tile(s / (1 + np.exp(-s)), (batch * frames, 1)), rtol=1e-6)
+    full = oracle.conformer_conv(pointwise, weights, scale, shift, np.array([frames, frames], np.uint32),
+                                 batch=batch, frames=frames)
+    beyond = oracle.conformer_conv(pointwise, weights, scale, shift, np.array([frames + 5, 1 << 30], np.uint32),
+                                   batch=batch, frames=frames)
+    np.testing.assert_array_equal(full, beyond)
+
+
+def test_conv_batch_items_are_independent(oracle):
+    rng = np.random.default_rng(13)
+    batch, frames, channels = 2, 9, 8
+    pointwise, weights, scale, shift = _conv_case(rng, batch, frames, channels)
+    valid = np.array([9, 7], np.uint32)
+    one = oracle.conformer_conv(pointwise, weights, scale, shift, valid, batch=batch, frames=frames)
+    changed = pointwise.copy()
+    changed[frames:] = rng.standard_normal(changed[frames:].shape)
+    two = oracle.conformer_conv(changed, weights, scale, shift, valid, batch=batch, frames=frames)
+    np.testing.assert_array_equal(one[:frames], two[:frames])
+    assert not np.array_equal(one[frames:], two[frames:])
