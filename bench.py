@@ -17,6 +17,8 @@ Other workloads (for profiling; same JSON shape):
                     P = X PW1 (6-bit 1024->2048), Z = SiLU(BN(DW9(GLU(P)))),
                     Y = X + Z PW2 (6-bit 1024->1024); TFLOP/s counts the two
                     GEMMs, the step time includes the fused conv tail
+  conv-module-fused the same module with the GLU moved into PW1's epilogue
+                    (PW1 writes [rows, 1024] GLU; the tail reads it)
 """
 from __future__ import annotations
 
@@ -43,7 +45,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="ff-block",
-                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module"])
+                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused"])
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
@@ -123,33 +125,37 @@ def build_small_m(abi, ctx, keep, rows):
     return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16")], config, case
 
 
-def build_conv_module(abi, ctx, keep):
+def build_conv_module(abi, ctx, keep, fused_glu=False):
     import parakeet_wgsl_amd.workloads as wl
     mod = wl.conv_module(0)
     m, d = mod.x.shape
     conv = mod.conv
     x = keep(ctx.array(mod.x))
-    p = keep(ctx.empty((m, 2 * d), np.float16))
+    p = keep(ctx.empty((m, d if fused_glu else 2 * d), np.float16))
     z = keep(ctx.empty((m, d), np.float16))
     y = keep(ctx.empty((m, d), np.float16))
     pw1 = abi.GemmOp(ctx, a=x, packed=keep(ctx.array(mod.pw1.packed)), palette=keep(ctx.array(mod.pw1.palette)),
-                     output=p, bits=6, rows=m, inner=d, columns=2 * d, label="conv-pointwise1")
+                     output=p, bits=6, rows=m, inner=d, columns=2 * d, label="conv-pointwise1", glu=fused_glu)
     tail = abi.ConformerConvOp(
         ctx, pointwise_input=p, depthwise_weights=keep(ctx.array(conv.weights)),
         batch_norm_scale=keep(ctx.array(conv.scale)), batch_norm_shift=keep(ctx.array(conv.shift)),
         valid_lengths=keep(ctx.array(conv.valid)), output=z, batch_size=conv.batch, frames=conv.frames,
-        label="conv-glu-depthwise-bn-silu")
+        label="conv-glu-depthwise-bn-silu", input_glu=fused_glu)
     pw2 = abi.GemmOp(ctx, a=z, packed=keep(ctx.array(mod.pw2.packed)), palette=keep(ctx.array(mod.pw2.palette)),
                      output=y, bits=6, rows=m, inner=d, columns=d, residual=x, residual_scale=1.0,
                      label="conv-pointwise2-residual")
     c1 = mod.pw1_case()
     c2 = mod.pw2_case(np.zeros((m, d), np.float16))
-    kernels = [Kernel("conv-pointwise1", pw1, c1.flops, c1.algorithmic_bytes(), "f16"),
-               Kernel("conv-tail", tail, 0, conv.algorithmic_bytes(), "f16"),
+    pw1_bytes = c1.algorithmic_bytes() - (m * d * 2 if fused_glu else 0)  # GLU output is half as wide
+    tail_bytes = conv.algorithmic_bytes() - (m * d * 2 if fused_glu else 0)
+    kernels = [Kernel("conv-pointwise1", pw1, c1.flops, pw1_bytes, "f16"),
+               Kernel("conv-tail", tail, 0, tail_bytes, "f16"),
                Kernel("conv-pointwise2", pw2, c2.flops, c2.algorithmic_bytes(), "f16")]
-    config = {"workload": "conformer-conv-module-fp16", "windows": conv.batch, "frames": conv.frames, "rows": m,
+    config = {"workload": "conformer-conv-module-fp16" + ("-fused-glu" if fused_glu else ""),
+              "windows": conv.batch, "frames": conv.frames, "rows": m,
               "d_model": d, "palette_bits": 6, "depthwise_kernel": 9,
-              "epilogues": ["glu", "depthwise9", "batchnorm", "silu", "residual"]}
+              "epilogues": (["pw1+glu", "depthwise9", "batchnorm", "silu", "residual"] if fused_glu
+                            else ["glu", "depthwise9", "batchnorm", "silu", "residual"])}
     return kernels, config, mod
 
 
@@ -177,7 +183,7 @@ def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
             pko.gemm(data.a[lo:hi], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
                      mode="f32-chain", threads=threads)
         what = "rows, f32 fma chain (reference fp32 semantics)"
-    elif workload == "conv-module":
+    elif workload in ("conv-module", "conv-module-fused"):
         # whole windows: the depthwise convolution spans frames of one window
         frames, conv = data.conv.frames, data.conv
         total_rows, per_row_flops, batch = data.x.shape[0], 2 * 1024 * 2048 + 2 * 1024 * 1024, frames
@@ -247,8 +253,8 @@ def main():
         kernels, config, data = build_ff_block(abi, ctx, keep)
     elif args.workload == "single-gemm-fp32":
         kernels, config, data = build_single_gemm(abi, ctx, keep)
-    elif args.workload == "conv-module":
-        kernels, config, data = build_conv_module(abi, ctx, keep)
+    elif args.workload in ("conv-module", "conv-module-fused"):
+        kernels, config, data = build_conv_module(abi, ctx, keep, args.workload == "conv-module-fused")
     else:
         kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
     if args.variant >= 0:

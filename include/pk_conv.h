@@ -39,15 +39,24 @@ extern "C" {
 
 typedef struct pk_conv_op pk_conv_op;
 
+/* pk_conv_desc.flags */
+/* The pointwise input already holds the GLU, [batch*frames, C] (e.g. the
+   output of a pk_gemm op with PK_GEMM_GLU), instead of [.., 2C] values and
+   gates; the convolution applies only the frame mask to it. No counterpart
+   in the reference, whose convolution kernel always forms the GLU. */
+#define PK_CONV_INPUT_GLU 0x1u
+
 typedef struct pk_conv_desc {
   uint32_t struct_size;            /* sizeof(pk_conv_desc) */
+  uint32_t flags;                  /* PK_CONV_* */
   const char *label;
   int32_t precision;               /* pk_precision */
   uint32_t batch_size;             /* windows (batch items) */
   uint32_t frames;                 /* frames per window */
   uint32_t channels;               /* C; 0 = 1024 */
-  const void *pointwise_input;     /* [batch*frames, 2C]: GLU values [0, C), gates [C, 2C) */
-  uint64_t pointwise_input_bytes;  /* capacity, >= rows*2C*elem */
+  const void *pointwise_input;     /* [batch*frames, 2C]: GLU values [0, C), gates [C, 2C)
+                                      ([batch*frames, C] GLU with PK_CONV_INPUT_GLU) */
+  uint64_t pointwise_input_bytes;  /* capacity, >= rows*2C*elem (rows*C*elem) */
   const void *depthwise_weights;   /* [9, C] channel-last ("kernel-channel-vec4") */
   uint64_t depthwise_weights_bytes;/* exactly 9*C*elem */
   const float *batch_norm_scale;   /* [C] gamma / sqrt(var + eps) */
@@ -62,7 +71,7 @@ typedef struct pk_conv_desc {
 
 typedef struct pk_conv_plan_info {
   uint32_t rows;                   /* batch * frames */
-  uint64_t input_bytes;            /* inputByteLength */
+  uint64_t input_bytes;            /* inputByteLength (of a [rows, 2C] input) */
   uint64_t output_bytes;           /* outputByteLength */
   uint64_t valid_lengths_bytes;    /* validLengthsByteLength */
   uint64_t depthwise_weight_bytes; /* depthwiseWeightByteLength */

@@ -75,6 +75,17 @@ typedef enum pk_activation {
 
 /* pk_gemm_desc.flags */
 #define PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE 0x1u /* gemm.ts:204-356, :2154-2306 */
+/* GLU epilogue, fused from the Conformer convolution that consumes the
+   pointwise-1 output (src/webgpu/kernels/conformer-conv.ts:520-535): of the
+   N columns, [0, N/2) are GLU values and [N/2, N) their gates, and the
+   output is [rows, N/2] = f16(value) * sigmoid(f16(gate)) (each half
+   rounded to f16 as the reference's pointwise buffer holds it; sigmoid with
+   the reference's clamp at +-20), rounded to f16. f16 precision only; needs
+   one palette group, N % 64 == 0, no bias, activation or residual, and no
+   shared prepared weight (the op lays out its own codes with value and gate
+   blocks interleaved). No counterpart in the reference's GEMM: there the
+   GLU runs in the convolution kernel. */
+#define PK_GEMM_GLU 0x2u
 
 typedef struct pk_context pk_context;
 typedef struct pk_gemm_op pk_gemm_op;

@@ -490,3 +490,27 @@ int pko_conformer_conv(int dtype, int mode, uint32_t batch, uint32_t frames, uin
   }
   return 0;
 }
+
+/* GLU alone: the step conformer-conv.ts:520-535 applies to each input row. */
+int pko_glu(int dtype, int mode, uint64_t rows, uint32_t channels, const void *input, void *output) {
+  if (!input || !output || channels == 0 ||
+      (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64) ||
+      (mode != PKO_MODE_F32_CHAIN && mode != PKO_MODE_F64))
+    return 1;
+  for (uint64_t r = 0; r < rows; ++r) {
+    for (uint32_t c = 0; c < channels; ++c) {
+      const double value = conv_in(dtype, input, r * 2u * channels + c);
+      const double gate = conv_in(dtype, input, r * 2u * channels + channels + c);
+      const double glu = mode == PKO_MODE_F32_CHAIN ? (double)((float)value * sigmoid_f32((float)gate))
+                                                    : value * sigmoid_f64(gate);
+      const uint64_t at = r * channels + c;
+      if (dtype == PKO_DTYPE_F16)
+        ((uint16_t *)output)[at] = pko_f64_to_f16(glu);
+      else if (dtype == PKO_DTYPE_F64)
+        ((double *)output)[at] = glu;
+      else
+        ((float *)output)[at] = (float)glu;
+    }
+  }
+  return 0;
+}

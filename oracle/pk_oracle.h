@@ -32,6 +32,10 @@
  *                         pinned: exact small-integer cases, the f16 rounding
  *                         function against every f16 value and its midpoints.
  *   pko_gemm (F64)        reference-independent truth of the same expression.
+ *   pko_glu               the GLU step of conformer-conv.ts:520-535 on its own
+ *                         (value * sigmoid(gate) of a [rows, 2C] input);
+ *                         pinned by torch's glu and the gate clamp in
+ *                         tests/test_oracle.py.
  *   pko_conformer_conv    src/webgpu/kernels/conformer-conv.ts:495-573 (GLU of
  *                         the pointwise-1 output, same-padded depthwise k9 over
  *                         frames, folded batch norm, SiLU); pinned by closed
@@ -111,6 +115,12 @@ int pko_gemm(const pko_gemm_args *args, int mode, int threads);
    reference's f32 arithmetic (fma over taps 0..8); PKO_MODE_F64: the same
    expression in double (output still rounded to dtype). dtype PKO_DTYPE_F64
    takes double input and weights and writes double output (truth chains). */
+/* GLU of a [rows, 2*channels] input (values, then gates) into [rows,
+   channels]: value * sigmoid(gate) with the reference's clamp, in f32
+   (PKO_MODE_F32_CHAIN) or double (PKO_MODE_F64), rounded to dtype
+   (PKO_DTYPE_F64: double input and output). */
+int pko_glu(int dtype, int mode, uint64_t rows, uint32_t channels, const void *input, void *output);
+
 int pko_conformer_conv(int dtype, int mode, uint32_t batch, uint32_t frames, uint32_t channels,
                        const void *input, const void *weights, const float *scale,
                        const float *shift, const uint32_t *valid, void *output);

@@ -14,6 +14,7 @@ Reference functions restated (see pk_oracle.h for the pins):
   gemm            src/webgpu/kernels/gemm.ts:1362-1716, :2006-2044 (f16),
                   :2356-2599, :2847-2869 (f32)
   conformer_conv  src/webgpu/kernels/conformer-conv.ts:495-573
+  glu             the GLU step of conformer-conv.ts:520-535
 """
 from __future__ import annotations
 
@@ -82,6 +83,8 @@ def lib() -> ctypes.CDLL:
         ]
         _lib.pko_gemm.argtypes = [ctypes.POINTER(_GemmArgs), ctypes.c_int, ctypes.c_int]
         _lib.pko_conformer_conv.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 6
+        _lib.pko_glu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p,
+                                 ctypes.c_void_p]
     return _lib
 
 
@@ -212,6 +215,20 @@ def conformer_conv(pointwise, weights, scale, shift, valid, *, batch, frames, mo
     if lib().pko_conformer_conv(dtype, MODE[mode], batch, frames, channels, _ptr(pointwise), _ptr(weights),
                                 _ptr(scale), _ptr(shift), _ptr(valid), _ptr(out)):
         raise ValueError("conformer_conv rejected its arguments")
+    return out
+
+
+def glu(pointwise, mode="f32-chain") -> np.ndarray:
+    """value * sigmoid(gate) of a [rows, 2C] input (values, then gates), with
+    the reference's gate clamp; output [rows, C] in the input's dtype."""
+    pointwise = np.ascontiguousarray(pointwise)
+    names = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.float64): "f64"}
+    if pointwise.dtype not in names or pointwise.ndim != 2 or pointwise.shape[1] % 2:
+        raise ValueError("glu takes a [rows, 2C] float16/32/64 array")
+    rows, channels = pointwise.shape[0], pointwise.shape[1] // 2
+    out = np.empty((rows, channels), dtype=pointwise.dtype)
+    if lib().pko_glu(DTYPE[names[pointwise.dtype]], MODE[mode], rows, channels, _ptr(pointwise), _ptr(out)):
+        raise ValueError("glu rejected its arguments")
     return out
 
 

@@ -1,6 +1,7 @@
 /*
  * pk_napi.c - Node-API (N-API 8) addon over the palette GEMM C ABI
- * (include/pk_palette.h). It is the thin native layer under the JavaScript
+ * (include/pk_palette.h) and the fused Conformer convolution tail
+ * (include/pk_conv.h). It is the thin native layer under the JavaScript
  * host in ../host: every function forwards to one pk_* call, converts device
  * pointers to BigInt, and turns a failing pk_status into a thrown Error
  * (RangeError for PK_RANGE_ERROR, as the reference throws RangeError for
@@ -19,6 +20,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "pk_conv.h"
 #include "pk_palette.h"
 
 #define NAPI_CALL(env, call)                                              \
@@ -537,6 +539,156 @@ static napi_value js_gemm_plan(napi_env env, napi_callback_info info) {
   return obj;
 }
 
+/* ---- Conformer convolution tail ------------------------------------------ */
+
+static void conv_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  pk_conv_release((pk_conv_op *)data);
+}
+
+static int parse_precision(napi_env env, napi_value o, int32_t *precision) {
+  char *p = prop_string(env, o, "precision");
+  *precision = !p || strcmp(p, "f16") == 0 ? PK_PRECISION_F16 : strcmp(p, "f32") == 0 ? PK_PRECISION_F32 : -1;
+  free(p);
+  return 1;
+}
+
+/* A JavaScript conv descriptor: {label, flags?, precision, batchSize, frames,
+   channels?, pointwiseInput, pointwiseInputBytes, depthwiseWeights,
+   depthwiseWeightsBytes, batchNormScale, batchNormScaleBytes,
+   batchNormShift, batchNormShiftBytes, validLengths, validLengthsBytes,
+   output, outputBytes}; device pointers are BigInt. */
+static int parse_conv_desc(napi_env env, napi_value o, pk_conv_desc *d, char **label) {
+  memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  *label = NULL;
+  uint64_t input = 0, weights = 0, scale = 0, shift = 0, valid = 0, output = 0;
+  parse_precision(env, o, &d->precision);
+  if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
+      !prop_u64(env, o, "pointwiseInput", &input) ||
+      !prop_u64(env, o, "pointwiseInputBytes", &d->pointwise_input_bytes) ||
+      !prop_u64(env, o, "depthwiseWeights", &weights) ||
+      !prop_u64(env, o, "depthwiseWeightsBytes", &d->depthwise_weights_bytes) ||
+      !prop_u64(env, o, "batchNormScale", &scale) ||
+      !prop_u64(env, o, "batchNormScaleBytes", &d->batch_norm_scale_bytes) ||
+      !prop_u64(env, o, "batchNormShift", &shift) ||
+      !prop_u64(env, o, "batchNormShiftBytes", &d->batch_norm_shift_bytes) ||
+      !prop_u64(env, o, "validLengths", &valid) || !prop_u64(env, o, "validLengthsBytes", &d->valid_lengths_bytes) ||
+      !prop_u64(env, o, "output", &output) || !prop_u64(env, o, "outputBytes", &d->output_bytes)) {
+    bad_argument(env, "convolution descriptor is missing a required field");
+    return 0;
+  }
+  prop_u32(env, o, "channels", &d->channels);
+  prop_u32(env, o, "flags", &d->flags);
+  d->pointwise_input = (const void *)(uintptr_t)input;
+  d->depthwise_weights = (const void *)(uintptr_t)weights;
+  d->batch_norm_scale = (const float *)(uintptr_t)scale;
+  d->batch_norm_shift = (const float *)(uintptr_t)shift;
+  d->valid_lengths = (const uint32_t *)(uintptr_t)valid;
+  d->output = (void *)(uintptr_t)output;
+  *label = prop_string(env, o, "label");
+  d->label = *label;
+  return 1;
+}
+
+static napi_value conv_plan_object(napi_env env, const pk_conv_plan_info *p) {
+  napi_value obj, grid, v;
+  NAPI_CALL(env, napi_create_object(env, &obj));
+  NAPI_CALL(env, napi_create_array_with_length(env, 3, &grid));
+  for (uint32_t i = 0; i < 3; ++i) napi_set_element(env, grid, i, make_number(env, p->grid[i]));
+  napi_set_named_property(env, obj, "rows", make_number(env, p->rows));
+  napi_set_named_property(env, obj, "inputByteLength", make_number(env, (double)p->input_bytes));
+  napi_set_named_property(env, obj, "outputByteLength", make_number(env, (double)p->output_bytes));
+  napi_set_named_property(env, obj, "validLengthsByteLength", make_number(env, (double)p->valid_lengths_bytes));
+  napi_set_named_property(env, obj, "depthwiseWeightByteLength", make_number(env, (double)p->depthwise_weight_bytes));
+  napi_set_named_property(env, obj, "affineByteLength", make_number(env, (double)p->affine_bytes));
+  napi_set_named_property(env, obj, "workgroups", grid);
+  napi_set_named_property(env, obj, "blockThreads", make_number(env, p->block_threads));
+  napi_set_named_property(env, obj, "workgroupStorageBytes", make_number(env, p->lds_bytes));
+  napi_set_named_property(env, obj, "algorithmicBytes", make_number(env, (double)p->algorithmic_bytes));
+  napi_create_string_utf8(env, p->kernel, NAPI_AUTO_LENGTH, &v);
+  napi_set_named_property(env, obj, "kernel", v);
+  return obj;
+}
+
+/* convPlanShape(precision, batchSize, frames, channels?) */
+static napi_value js_conv_plan_shape(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!get_args(env, info, 4, argv)) return NULL;
+  char buf[8] = {0};
+  size_t n = 0;
+  napi_get_value_string_utf8(env, argv[0], buf, sizeof buf, &n);
+  const int precision = strcmp(buf, "f32") == 0 ? PK_PRECISION_F32 : strcmp(buf, "f16") == 0 ? PK_PRECISION_F16 : -1;
+  uint32_t batch = 0, frames = 0, channels = 0;
+  if (!get_u32(env, argv[1], &batch) || !get_u32(env, argv[2], &frames))
+    return bad_argument(env, "batchSize and frames must be non-negative integers");
+  if (!is_nullish(env, argv[3]) && !get_u32(env, argv[3], &channels))
+    return bad_argument(env, "channels must be a non-negative integer");
+  pk_conv_plan_info p;
+  PK_CALL(env, pk_conv_plan_shape(precision, batch, frames, channels, &p));
+  return conv_plan_object(env, &p);
+}
+
+/* convValidate(desc) */
+static napi_value js_conv_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  pk_conv_desc d;
+  char *label;
+  if (!parse_conv_desc(env, argv[0], &d, &label)) return NULL;
+  const int status = pk_conv_validate(&d);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+/* convCreate(ctx, desc) -> op */
+static napi_value js_conv_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2], ext;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  pk_conv_desc d;
+  char *label;
+  if (!parse_conv_desc(env, argv[1], &d, &label)) return NULL;
+  pk_conv_op *op = NULL;
+  const int status = pk_conv_create((pk_context *)get_external(env, argv[0]), &d, &op);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  NAPI_CALL(env, napi_create_external(env, op, conv_finalize, NULL, &ext));
+  return ext;
+}
+
+/* convEnqueue(op, activeBatch, stream?, startEvent?, endEvent?) */
+static napi_value js_conv_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  uint32_t batch = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  PK_CALL(env, pk_conv_enqueue_timed((pk_conv_op *)get_external(env, argv[0]), batch, get_external(env, argv[2]),
+                                     get_external(env, argv[3]), get_external(env, argv[4])));
+  return undefined(env);
+}
+
+static napi_value js_conv_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_conv_destroy((pk_conv_op *)get_external(env, argv[0])));
+  return undefined(env);
+}
+
+/* convPlan(op, activeBatch?) */
+static napi_value js_conv_plan(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  uint32_t batch = 0;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  pk_conv_plan_info p;
+  PK_CALL(env, pk_conv_plan((pk_conv_op *)get_external(env, argv[0]), batch, &p));
+  return conv_plan_object(env, &p);
+}
+
 /* ---- module --------------------------------------------------------------- */
 
 static napi_value init(napi_env env, napi_value exports) {
@@ -565,6 +717,12 @@ static napi_value init(napi_env env, napi_value exports) {
       {"gemmEnqueue", js_gemm_enqueue},
       {"gemmDestroy", js_gemm_destroy},
       {"gemmPlan", js_gemm_plan},
+      {"convPlanShape", js_conv_plan_shape},
+      {"convValidate", js_conv_validate},
+      {"convCreate", js_conv_create},
+      {"convEnqueue", js_conv_enqueue},
+      {"convDestroy", js_conv_destroy},
+      {"convPlan", js_conv_plan},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
     napi_value f;

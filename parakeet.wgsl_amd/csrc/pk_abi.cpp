@@ -83,6 +83,7 @@ struct pk_prepared_weight {
   uint32_t* codes = nullptr;      // operand-order codes (device)
   uint8_t* pair_codes = nullptr;  // pair-code layout (device)
   uint64_t bytes = 0;             // both layouts
+  bool glu = false;               // GLU-interleaved pair codes only
   std::atomic<int> refs{1};
   bool owner_released = false;
 };
@@ -117,32 +118,36 @@ void weight_unref(pk_prepared_weight* w) {
   }
 }
 
+// Prepares a packed weight: both code layouts, or with `glu` only the
+// pair codes with value and gate column blocks interleaved (the GLU
+// epilogue runs in the pair-code kernels alone).
 int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, uint32_t columns,
-                const uint32_t* packed, hipStream_t stream, pk_prepared_weight** out) {
+                const uint32_t* packed, hipStream_t stream, pk_prepared_weight** out, bool glu = false) {
   auto* w = new pk_prepared_weight();
   w->ctx = ctx;
   w->label = safe_label(label);
   w->bits = bits;
   w->inner = inner;
   w->columns = columns;
-  const uint64_t operand_bytes = pk::operand_order_words(bits, inner, columns) * 4u;
+  w->glu = glu;
+  const uint64_t operand_bytes = glu ? 0 : pk::operand_order_words(bits, inner, columns) * 4u;
   const uint64_t pair_bytes = pk::pair_code_bytes(inner, columns);
   w->bytes = operand_bytes + pair_bytes;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->codes), operand_bytes);
+  hipError_t e = glu ? hipSuccess : hipMalloc(reinterpret_cast<void**>(&w->codes), operand_bytes);
   if (e == hipSuccess) {
     e = hipMalloc(reinterpret_cast<void**>(&w->pair_codes), pair_bytes);
-    if (e != hipSuccess) (void)hipFree(w->codes);
+    if (e != hipSuccess && w->codes) (void)hipFree(w->codes);
   }
   if (e != hipSuccess) {
     delete w;
     return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
                 safe_label(label), (unsigned long long)w->bytes, hipGetErrorString(e));
   }
-  e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
-  if (e == hipSuccess) e = pk::launch_to_pair_codes(bits, packed, inner, columns, w->pair_codes, stream);
+  if (!glu) e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
+  if (e == hipSuccess) e = pk::launch_to_pair_codes(bits, packed, inner, columns, w->pair_codes, stream, glu);
   if (e == hipSuccess) e = hipStreamSynchronize(stream);
   if (e != hipSuccess) {
-    (void)hipFree(w->codes);
+    if (w->codes) (void)hipFree(w->codes);
     (void)hipFree(w->pair_codes);
     delete w;
     return fail(PK_DEVICE_ERROR, "%s: palette code preparation failed: %s", safe_label(label),
@@ -336,6 +341,13 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
   // f16SubgroupGemmWgsl (gemm.ts:1372-1378)
   if (d->bias && d->residual)
     return fail(PK_INVALID_ARGUMENT, "%s cannot fuse bias and residual together", label);
+  const bool glu = (d->flags & PK_GEMM_GLU) != 0;
+  if (glu && (!f16 || d->palette_groups != 1 || d->columns % 64u != 0 || d->bias || d->residual ||
+              d->activation != PK_ACTIVATION_NONE || d->prepared))
+    return fail(PK_INVALID_ARGUMENT,
+                "%s GLU epilogue needs f16, one palette group, N %% 64 == 0, no bias, activation, residual "
+                "or shared prepared weight",
+                label);
   // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
   const uint32_t entries = 1u << bits;
   const uint32_t cpg = pk::codes_per_group(bits);
@@ -356,7 +368,7 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
   }
   // Bindings: sizes (gemm.ts:1302-1333 minBindingSize) and vector alignment.
   const uint64_t a_need = (uint64_t)d->rows * d->inner * elem;
-  const uint64_t c_need = (uint64_t)d->rows * d->columns * elem;
+  const uint64_t c_need = (uint64_t)d->rows * (glu ? d->columns / 2u : d->columns) * elem;
   if (!d->a || d->a_bytes < a_need || !aligned(d->a, 16))
     return fail(PK_INVALID_ARGUMENT, "%s input binding must hold %llu bytes at 16-byte alignment",
                 label, (unsigned long long)a_need);
@@ -625,7 +637,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   } else {
     pk_prepared_weight* w = nullptr;
     if (int s = make_weight(ctx, label, bits, d->inner, d->columns, d->packed,
-                            stream_or_default(ctx, stream), &w)) {
+                            stream_or_default(ctx, stream), &w, (d->flags & PK_GEMM_GLU) != 0)) {
       delete op;
       return s;
     }
@@ -648,12 +660,17 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   a.palette_groups = d->palette_groups;
   a.palette_group_columns = d->palette_group_columns;
   a.palette_entries = 1u << bits;
+  a.glu = (d->flags & PK_GEMM_GLU) ? 1 : 0;
   hipDeviceProp_t prop;
   int cus = 256;
   if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
     cus = prop.multiProcessorCount;
   a.splits = 1;
-  const Plan plan = plan_launch(d->precision, d->rows, d->inner, d->columns, cus);
+  Plan plan = plan_launch(d->precision, d->rows, d->inner, d->columns, cus);
+  // The GLU epilogue lives in the pair-code kernels: small-M plans take
+  // their 64 x 64 tile.
+  if (a.glu && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
+    plan = {find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4), 1u};
   if (int st = configure_launch(op, plan.variant, plan.splits)) {
     weight_unref(op->weight);
     delete op;
@@ -716,6 +733,8 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
   if (variant < 0 || variant >= count)
     return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
+  if (op->args.glu && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
+    return fail(PK_RANGE_ERROR, "%s tile variant %d has no GLU epilogue", op->label.c_str(), variant);
   // Variants without a split-K path run unsplit.
   const bool splittable = op->precision == PK_PRECISION_F16 && pk::f16_variant_splits(variant);
   return configure_launch(op, variant, splittable ? op->splits : 1u);
@@ -768,7 +787,7 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   info->flops = 2ull * M * K * N;
   uint64_t bytes = (K * N * (uint64_t)op->bits + 7u) / 8u;
   bytes += (uint64_t)op->args.palette_groups * (1u << op->bits) * elem;
-  bytes += M * K * elem + M * N * elem;
+  bytes += M * K * elem + M * (op->args.glu ? N / 2u : N) * elem;
   if (op->args.bias) bytes += 4u * N;
   if (op->args.residual) bytes += M * N * elem;
   info->algorithmic_bytes = bytes;

@@ -141,11 +141,13 @@ __global__ __launch_bounds__(kThreads) void operand_order_kernel(
 }
 
 // Reference format -> pair-code layout (pk_internal.h). One thread per
-// (block, lane); runs once per weight.
+// (block, lane); runs once per weight. With glu_interleave the physical
+// column blocks alternate the two halves of the logical columns (GLU values,
+// then their gates).
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void pair_code_kernel(
     const uint32_t* __restrict__ packed, uint32_t inner, uint32_t columns,
-    uint32_t k_blocks, uint64_t total_lanes, uint8_t* __restrict__ out) {
+    uint32_t k_blocks, uint64_t total_lanes, uint8_t* __restrict__ out, bool glu_interleave) {
   constexpr uint32_t CPG = codes_per_group(BITS);
   constexpr uint32_t WPG = words_per_group(BITS);
   constexpr uint32_t S = pair_table_side(BITS);
@@ -156,7 +158,8 @@ __global__ __launch_bounds__(kThreads) void pair_code_kernel(
   const uint64_t block = t >> 6;
   const uint32_t nb = (uint32_t)(block / k_blocks);
   const uint32_t kb = (uint32_t)(block % k_blocks);
-  const uint32_t n = nb * 32u + (lane & 31u);
+  const uint32_t logical_nb = glu_interleave ? (nb & 1u) * (columns / 64u) + (nb >> 1) : nb;
+  const uint32_t n = logical_nb * 32u + (lane & 31u);
   const uint32_t k0 = kb * 64u + (lane >> 5) * 32u;
   auto code_at = [&](uint32_t k) -> uint32_t {
     if (k >= inner || n >= columns) return PAD;
@@ -248,16 +251,17 @@ hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t in
 }
 
 hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
-                                uint32_t columns, uint8_t* codes, hipStream_t stream) {
+                                uint32_t columns, uint8_t* codes, hipStream_t stream, bool glu_interleave) {
+  if (glu_interleave && columns % 64u != 0) return hipErrorInvalidValue;
   const uint32_t k_blocks = padded_inner(inner) / 64u;
   const uint64_t blocks = (uint64_t)(padded_columns(columns) / 32u) * k_blocks;
   const uint64_t lanes = blocks * 64u;
   if (bits == 5)
     hipLaunchKernelGGL(pair_code_kernel<5>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes);
+                       inner, columns, k_blocks, lanes, codes, glu_interleave);
   else
     hipLaunchKernelGGL(pair_code_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes);
+                       inner, columns, k_blocks, lanes, codes, glu_interleave);
   return hipGetLastError();
 }
 

@@ -59,7 +59,9 @@ __device__ __forceinline__ void store_row(T* p, const float (&in)[CPT]) {
   *reinterpret_cast<V*>(p) = v;
 }
 
-template <typename T, int CPT, int F>
+// GLU_IN: the input rows already hold the GLU ([rows, C]); only the frame
+// mask is applied to them.
+template <typename T, int CPT, int F, bool GLU_IN>
 __global__ __launch_bounds__(kConvThreads) void conformer_conv_kernel(ConvArgs args) {
   const uint32_t logical = xcd_local_order(blockIdx.x, gridDim.x);
   const uint32_t item = logical / args.blocks_per_item;
@@ -73,7 +75,8 @@ __global__ __launch_bounds__(kConvThreads) void conformer_conv_kernel(ConvArgs a
   const int live_end = (int)min(args.frames, args.valid_lengths[item]);
   const int f0 = (int)run * F;
 
-  const T* in = static_cast<const T*>(args.input) + (uint64_t)item * args.frames * (2u * C) + c0;
+  constexpr uint32_t kInRows = GLU_IN ? 1u : 2u;  // input row length in channels
+  const T* in = static_cast<const T*>(args.input) + (uint64_t)item * args.frames * (kInRows * C) + c0;
   const T* weights = static_cast<const T*>(args.weights) + c0;
   T* out = static_cast<T*>(args.output) + (uint64_t)item * args.frames * C + c0;
 
@@ -84,9 +87,9 @@ __global__ __launch_bounds__(kConvThreads) void conformer_conv_kernel(ConvArgs a
   V value[F + kTaps - 1], gate[F + kTaps - 1];
 #pragma unroll
   for (int i = 0; i < F + kTaps - 1; ++i) {
-    const T* row = in + (uint64_t)min(max(f0 - kRadius + i, 0), frames - 1) * (2u * C);
+    const T* row = in + (uint64_t)min(max(f0 - kRadius + i, 0), frames - 1) * (kInRows * C);
     value[i] = *reinterpret_cast<const V*>(row);
-    gate[i] = *reinterpret_cast<const V*>(row + C);
+    if constexpr (!GLU_IN) gate[i] = *reinterpret_cast<const V*>(row + C);
   }
   float w[kTaps][CPT], scale[CPT], shift[CPT];
 #pragma unroll
@@ -100,8 +103,12 @@ __global__ __launch_bounds__(kConvThreads) void conformer_conv_kernel(ConvArgs a
     const int r = f0 - kRadius + i;
     const bool live = r >= 0 && r < live_end;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c)
-      glu[i][c] = live ? static_cast<float>(value[i][c]) * sigmoid(static_cast<float>(gate[i][c])) : 0.0f;
+    for (int c = 0; c < CPT; ++c) {
+      if constexpr (GLU_IN)
+        glu[i][c] = live ? static_cast<float>(value[i][c]) : 0.0f;
+      else
+        glu[i][c] = live ? static_cast<float>(value[i][c]) * sigmoid(static_cast<float>(gate[i][c])) : 0.0f;
+    }
   }
 
 #pragma unroll
@@ -123,13 +130,18 @@ __global__ __launch_bounds__(kConvThreads) void conformer_conv_kernel(ConvArgs a
 
 struct ConvVariant {
   const char* name;
+  const char* glu_name;
   int channels_per_thread;
   int frames_per_thread;
   void (*kernel)(ConvArgs);
+  void (*glu_kernel)(ConvArgs);  // GLU_IN
 };
 
-#define PK_CONV_VARIANT(T, TN, CPT, F) \
-  ConvVariant { "pk_conformer_conv_" TN "_c" #CPT "_f" #F, CPT, F, conformer_conv_kernel<T, CPT, F> }
+#define PK_CONV_VARIANT(T, TN, CPT, F)                                                                     \
+  ConvVariant {                                                                                            \
+    "pk_conformer_conv_" TN "_c" #CPT "_f" #F, "pk_conformer_conv_glu_" TN "_c" #CPT "_f" #F, CPT, F,      \
+        conformer_conv_kernel<T, CPT, F, false>, conformer_conv_kernel<T, CPT, F, true>                    \
+  }
 
 // First entry of each list is the default launch shape (fastest measured on
 // 16 x 188 x 1024 and 64 x 188 x 1024).
@@ -156,10 +168,11 @@ int conv_variant_count(bool f16) {
              : (int)(sizeof(kF32Variants) / sizeof(kF32Variants[0]));
 }
 
-ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch) {
+ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
+                           bool input_glu) {
   const ConvVariant& v = conv_variant_at(f16, variant);
   ConvGeometry g;
-  g.name = v.name;
+  g.name = input_glu ? v.glu_name : v.name;
   g.channels_per_thread = v.channels_per_thread;
   g.runs = (frames + v.frames_per_thread - 1) / v.frames_per_thread;
   const uint64_t threads = (uint64_t)g.runs * (channels / v.channels_per_thread);
@@ -172,15 +185,16 @@ ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t chan
 hipError_t launch_conformer_conv(bool f16, int variant, const ConvArgs& base, uint32_t batch, hipStream_t stream,
                                  hipEvent_t start, hipEvent_t stop) {
   const ConvVariant& v = conv_variant_at(f16, variant);
-  const ConvGeometry g = conv_geometry(f16, variant, base.frames, base.channels, batch);
+  const ConvGeometry g = conv_geometry(f16, variant, base.frames, base.channels, batch, base.input_glu != 0);
   if (g.grid == 0) return hipSuccess;
   ConvArgs args = base;
   args.runs = g.runs;
   args.blocks_per_item = g.blocks_per_item;
+  void (*kernel)(ConvArgs) = base.input_glu ? v.glu_kernel : v.kernel;
   if (start || stop)
-    hipExtLaunchKernelGGL(v.kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, start, stop, 0, args);
+    hipExtLaunchKernelGGL(kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, start, stop, 0, args);
   else
-    hipLaunchKernelGGL(v.kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, args);
+    hipLaunchKernelGGL(kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, args);
   return hipGetLastError();
 }
 

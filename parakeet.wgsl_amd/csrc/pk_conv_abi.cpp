@@ -29,8 +29,8 @@ const char* conv_label(const char* label) { return label ? label : "conformer-co
 
 uint32_t channels_of(uint32_t channels) { return channels ? channels : PK_CONV_DEFAULT_CHANNELS; }
 
-// Default launch shape per precision: 4 channels per thread over runs of 8
-// frames.
+// Default launch shape per precision: the first compiled variant (2
+// channels per thread over runs of 8 frames).
 int default_variant(int /*precision*/) { return 0; }
 
 struct Sizes {
@@ -58,8 +58,12 @@ int plan_sizes(const char* label, int precision, uint32_t batch, uint32_t frames
   return PK_OK;
 }
 
+// The input bytes a launch reads per window: [frames, 2C], or [frames, C]
+// of ready GLU.
+uint64_t input_bytes_of(const Sizes& s, bool input_glu) { return input_glu ? s.input / 2u : s.input; }
+
 void fill_plan(int precision, int variant, uint32_t batch, uint32_t frames, uint32_t channels, uint32_t active,
-               const Sizes& s, pk_conv_plan_info* info) {
+               const Sizes& s, bool input_glu, pk_conv_plan_info* info) {
   std::memset(info, 0, sizeof *info);
   info->rows = (uint32_t)s.rows;
   info->input_bytes = s.input;
@@ -68,13 +72,13 @@ void fill_plan(int precision, int variant, uint32_t batch, uint32_t frames, uint
   info->depthwise_weight_bytes = s.weights;
   info->affine_bytes = s.affine;
   const bool f16 = precision == PK_PRECISION_F16;
-  const pk::ConvGeometry g = pk::conv_geometry(f16, variant, frames, channels, active);
+  const pk::ConvGeometry g = pk::conv_geometry(f16, variant, frames, channels, active, input_glu);
   info->grid[0] = g.grid;
   info->grid[1] = 1;
   info->grid[2] = 1;
   info->block_threads = g.block_threads;
   info->lds_bytes = 0;
-  const uint64_t per_item = (s.input + s.output) / batch;
+  const uint64_t per_item = (input_bytes_of(s, input_glu) + s.output) / batch;
   info->algorithmic_bytes = per_item * active + s.weights + 2u * s.affine + 4ull * active;
   std::snprintf(info->kernel, sizeof info->kernel, "%s", g.name);
 }
@@ -93,15 +97,18 @@ int validate_conv_desc(const pk_conv_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "pk_conv_desc.struct_size mismatch");
   const char* label = conv_label(d->label);
   const uint32_t C = channels_of(d->channels);
+  if (d->flags & ~PK_CONV_INPUT_GLU) return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
+  const bool input_glu = (d->flags & PK_CONV_INPUT_GLU) != 0;
   Sizes s;
   if (int st = plan_sizes(label, d->precision, d->batch_size, d->frames, C, &s)) return st;
+  const uint64_t input_need = input_bytes_of(s, input_glu);
   struct Slice {
     const char* role;
     const void* ptr;
     uint64_t bytes, need;
   };
   const Slice slices[] = {
-      {"pointwise input", d->pointwise_input, d->pointwise_input_bytes, s.input},
+      {"pointwise input", d->pointwise_input, d->pointwise_input_bytes, input_need},
       {"output", d->output, d->output_bytes, s.output},
       {"valid lengths", d->valid_lengths, d->valid_lengths_bytes, s.valid},
   };
@@ -129,7 +136,7 @@ int validate_conv_desc(const pk_conv_desc* d) {
       !aligned(d->batch_norm_scale, 16) || !aligned(d->batch_norm_shift, 16) || !aligned(d->valid_lengths, 4))
     return fail(PK_INVALID_ARGUMENT, "%s bindings must be 16-byte aligned (valid lengths 4-byte)", label);
   // Frames read other frames' GLU inputs, so the output may not alias them.
-  if (overlaps(d->output, s.output, d->pointwise_input, s.input))
+  if (overlaps(d->output, s.output, d->pointwise_input, input_need))
     return fail(PK_INVALID_ARGUMENT, "%s output must not overlap the pointwise input", label);
   return PK_OK;
 }
@@ -144,7 +151,7 @@ int pk_conv_plan_shape(int precision, uint32_t batch_size, uint32_t frames, uint
   const uint32_t C = channels_of(channels);
   Sizes s;
   if (int st = plan_sizes(conv_label(nullptr), precision, batch_size, frames, C, &s)) return st;
-  fill_plan(precision, default_variant(precision), batch_size, frames, C, batch_size, s, info);
+  fill_plan(precision, default_variant(precision), batch_size, frames, C, batch_size, s, false, info);
   return ok();
 }
 
@@ -170,6 +177,7 @@ int pk_conv_create(pk_context* ctx, const pk_conv_desc* d, pk_conv_op** out) {
   a.output = d->output;
   a.frames = d->frames;
   a.channels = channels_of(d->channels);
+  a.input_glu = (d->flags & PK_CONV_INPUT_GLU) ? 1 : 0;
   *out = op;
   return ok();
 }
@@ -203,7 +211,8 @@ int pk_conv_plan(const pk_conv_op* op, uint32_t active_batch, pk_conv_plan_info*
   Sizes s;
   if (int st = plan_sizes(op->label.c_str(), op->precision, op->batch, op->args.frames, op->args.channels, &s))
     return st;
-  fill_plan(op->precision, op->variant, op->batch, op->args.frames, op->args.channels, batch, s, info);
+  fill_plan(op->precision, op->variant, op->batch, op->args.frames, op->args.channels, batch, s,
+            op->args.input_glu != 0, info);
   return ok();
 }
 

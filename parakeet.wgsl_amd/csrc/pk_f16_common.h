@@ -51,6 +51,16 @@ __device__ __forceinline__ float silu(float v) {
   return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// sigmoid(v) = 1 / (1 + exp(-clamp(v, -20, 20))), the GLU gate of the
+// reference (src/webgpu/kernels/conformer-conv.ts:489-492).
+__device__ __forceinline__ float sigmoid(float v) {
+  const float bounded = __builtin_amdgcn_fmed3f(v, -20.0f, 20.0f);
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(bounded * -1.4426950408889634f));
+}
+
+// v rounded to f16 and back: the value a reference f16 buffer would hold.
+__device__ __forceinline__ float through_f16(float v) { return (float)(_Float16)v; }
+
 __device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);

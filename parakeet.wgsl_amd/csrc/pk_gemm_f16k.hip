@@ -38,6 +38,13 @@
 //     reads are conflict-free); each thread then sums the KS partials of
 //     8 consecutive columns of one row in K-part order, applies bias,
 //     SiLU/ReLU and residual + scale * value in f32, and stores 16 bytes.
+//   * GLU epilogue (args.glu): the weight's column blocks were interleaved
+//     at preparation (block 2i = values of channels 32i.., block 2i+1 =
+//     their gates), so a tile holds both halves of its channels; a thread
+//     sums the value and gate partials of 8 channels, rounds each to f16
+//     (the reference stores the pointwise output in f16 before its GLU,
+//     conformer-conv.ts:520-535) and writes value * sigmoid(gate) to a
+//     [M, N/2] output.
 #include <utility>
 
 #include "pk_f16_common.h"
@@ -425,6 +432,51 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
                                                           acc[p0 + ml][ci][4 * q + 2], acc[p0 + ml][ci][4 * q + 3]);
         }
     __syncthreads();
+    // Sum of the KS partials of 8 columns (column block cb, quad q) of tile
+    // row 32*ml + jj.
+    auto unit_sum = [&](int cb, int ml, int jj, int q, float (&v)[8]) {
+      const int wn_u = cb / C, ci_u = cb % C;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int slot = (((k * WN + wn_u) * PM + ml) * C + ci_u) * 4 + q;
+        const float4 x0 = ex[slot * 64 + (jj ^ (q << 2))];
+        const float4 x1 = ex[slot * 64 + 32 + (jj ^ (q << 2))];
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = k == 0 ? x[e] : v[e] + x[e];
+      }
+    };
+    if constexpr (NCB % 2 == 0) {
+      if (args.glu) {
+        // Unit u covers 8 channels of one row: the value block 2*cp and the
+        // gate block 2*cp + 1 of column-block pair cp.
+        constexpr int GUNITS = PM * 32 * (NCB / 2) * 4;
+        constexpr int GUPT = (GUNITS + T - 1) / T;
+        const uint32_t NC = N / 2u;
+#pragma unroll
+        for (int it = 0; it < GUPT; ++it) {
+          const int u = tid + it * T;
+          if (GUNITS % T != 0 && u >= GUNITS) break;
+          const int q = u & 3;
+          const int rest = u >> 4;
+          const int cp = rest % (NCB / 2);
+          const int rl = (rest / (NCB / 2)) * 4 + ((u >> 2) & 3);
+          const uint32_t m = m0 + (uint32_t)(p0 * 32 + rl);
+          const uint32_t c = n0 / 2u + (uint32_t)(cp * 32 + q * 8);
+          float value[8], gate[8];
+          unit_sum(2 * cp, rl >> 5, rl & 31, q, value);
+          unit_sum(2 * cp + 1, rl >> 5, rl & 31, q, gate);
+          float g[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) g[e] = through_f16(value[e]) * sigmoid(through_f16(gate[e]));
+          if (m < M && c < NC)
+            *reinterpret_cast<uint4*>(out + (uint64_t)m * NC + c) =
+                make_uint4(pack_half2(g[0], g[1]), pack_half2(g[2], g[3]), pack_half2(g[4], g[5]),
+                           pack_half2(g[6], g[7]));
+        }
+        continue;
+      }
+    }
     // Unit u: quad q = u & 3 and row low bits u >> 2 & 3 vary fastest, so a
     // 16-lane phase reads 16 distinct bank groups and a wavefront stores
     // 4 rows x 64 contiguous bytes per column block. A thread's UPT units
@@ -449,16 +501,7 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       keep[it] = m < M && n < N;
       n_of[it] = min(n, N - 8u);
       at[it] = (uint64_t)min(m, M - 1u) * N + n_of[it];
-      const int wn_u = cb / C, ci_u = cb % C;
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int slot = (((k * WN + wn_u) * PM + ml) * C + ci_u) * 4 + q;
-        const float4 x0 = ex[slot * 64 + (jj ^ (q << 2))];
-        const float4 x1 = ex[slot * 64 + 32 + (jj ^ (q << 2))];
-        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[it][e] = k == 0 ? x[e] : v[it][e] + x[e];
-      }
+      unit_sum(cb, ml, jj, q, v[it]);
     }
     if (args.bias) {
 #pragma unroll

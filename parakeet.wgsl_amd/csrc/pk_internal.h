@@ -64,6 +64,10 @@ struct GemmArgs {
   const void* residual;      // [M, N] or null
   float residual_scale;
   int activation;
+  // GLU epilogue (pair-code kernels only): the weight's 32-column blocks
+  // alternate values and gates (launch_to_pair_codes with glu_interleave),
+  // and out is [M, N/2] = value * sigmoid(gate).
+  int glu;
   uint32_t rows;             // active M
   uint32_t inner;            // K
   uint32_t columns;          // N
@@ -137,8 +141,12 @@ hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* pa
                          hipStream_t stream);
 hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
                                    uint32_t columns, uint32_t* codes, hipStream_t stream);
+// glu_interleave: physical column block 2i takes logical block i (a GLU
+// value block) and block 2i+1 takes logical block N/64 + i (its gates);
+// needs N % 64 == 0.
 hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
-                                uint32_t columns, uint8_t* codes, hipStream_t stream);
+                                uint32_t columns, uint8_t* codes, hipStream_t stream,
+                                bool glu_interleave = false);
 
 // Fused palette GEMM. `variant` indexes f16_variants() / f32_variants().
 int f16_variant_count();
@@ -170,6 +178,7 @@ struct ConvArgs {
   void* output;                   // [batch * frames, channels]
   uint32_t frames;
   uint32_t channels;              // multiple of 8
+  int input_glu;                  // input is [batch * frames, channels] GLU
   uint32_t runs;                  // frame runs per item (set by the launcher)
   uint32_t blocks_per_item;       // set by the launcher
 };
@@ -184,7 +193,8 @@ struct ConvGeometry {
 };
 
 int conv_variant_count(bool f16);
-ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch);
+ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
+                           bool input_glu = false);
 hipError_t launch_conformer_conv(bool f16, int variant, const ConvArgs& args, uint32_t batch,
                                  hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 

@@ -133,6 +133,11 @@ export interface GemmDescriptor {
   readonly residualScale?: number;
   readonly activation?: GemmActivation;
   readonly preparedPaletteWeight?: PreparedPaletteWeight;
+  /**
+   * This library only: GLU epilogue (PK_GEMM_GLU). Columns [0, N/2) are GLU
+   * values, [N/2, N) gates; the output is [rows, N/2] value * sigmoid(gate).
+   */
+  readonly glu?: boolean;
 }
 
 export interface GemmPlan {
@@ -208,3 +213,82 @@ export declare function paletteTensorRecords(options: {
   weight: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
   palette: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
 };
+
+/* ---- Conformer convolution tail (src/webgpu/kernels/conformer-conv.ts) ---- */
+
+export declare const CONFORMER_CONV_CHANNELS: 1024;
+export declare const CONFORMER_CONV_POINTWISE_CHANNELS: 2048;
+export declare const CONFORMER_CONV_KERNEL_SIZE: 9;
+export declare const CONFORMER_DEPTHWISE_WEIGHT_LAYOUT: "kernel-channel-vec4";
+export declare const CONFORMER_FOLDED_BATCH_NORM_LAYOUT: "channel";
+
+/** conformer-conv.ts:31-45 */
+export interface ConformerConvShape {
+  readonly batchSize: number;
+  readonly frames: number;
+}
+export interface ConformerConvPlan extends ConformerConvShape {
+  readonly rows: number;
+  readonly inputByteLength: number;
+  readonly outputByteLength: number;
+  readonly validLengthsByteLength: number;
+  readonly depthwiseWeightByteLength: number;
+  readonly affineByteLength: number;
+  /** This library's launch grid (one dimension used). */
+  readonly workgroups: readonly [number, number, number];
+  /** 0: the GLU window lives in registers. */
+  readonly workgroupStorageBytes: number;
+  readonly blockThreads: number;
+  readonly algorithmicBytes: number;
+  readonly kernel: string;
+}
+
+/** conformer-conv.ts:47-64 */
+export interface FusedConformerConvDescriptor extends ConformerConvShape {
+  readonly label: string;
+  /** Profile-scalar [rows, 2048]: GLU values [0, 1024), gates [1024, 2048). */
+  readonly pointwiseInput: ArenaSlice;
+  /** Profile-scalar [9, 1024], kernel-channel-vec4. */
+  readonly depthwiseWeights: GpuTensor;
+  /** f32 [1024] gamma / sqrt(var + eps). */
+  readonly batchNormScale: GpuTensor;
+  /** f32 [1024] beta - mean * scale. */
+  readonly batchNormShift: GpuTensor;
+  /** u32 valid frames per window. */
+  readonly validLengths: ArenaSlice;
+  /** Profile-scalar [rows, 1024]; must not overlap the pointwise input. */
+  readonly output: ArenaSlice;
+  /**
+   * This library only: the pointwise input is the [rows, 1024] GLU written by
+   * a GEMM with the GLU epilogue (PK_CONV_INPUT_GLU).
+   */
+  readonly pointwiseInputIsGlu?: boolean;
+}
+
+export declare function planFusedConformerConv(shape: ConformerConvShape,
+                                               executionProfile?: { precision: "fp16" | "fp32" }): ConformerConvPlan;
+export declare function conformerConvTensorRecords(options?: { dtype?: "float16" | "float32" }): {
+  depthwiseWeights: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  batchNormScale: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  batchNormShift: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+};
+
+/** conformer-conv.ts:117-162 */
+export declare class FusedConformerConvDispatch {
+  readonly label: string;
+  readonly result: { readonly output: ArenaSlice; readonly rows: number; readonly channels: 1024 };
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, shape?: EncoderDispatchShape): void;
+  destroy(): void;
+  plan(activeBatch?: number): ConformerConvPlan;
+}
+
+/** conformer-conv.ts:174-350 */
+export declare class FusedConformerConvKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<FusedConformerConvKernel>;
+  readonly uniformParameterPoolBytes: number;
+  readonly uniformParameterPoolUsedSlots: number;
+  validateDescriptor(descriptor: FusedConformerConvDescriptor): void;
+  createDispatch(descriptor: FusedConformerConvDescriptor): FusedConformerConvDispatch;
+  destroy(): void;
+}

@@ -17,6 +17,14 @@
  *   GpuActivationArena                 src/webgpu/arena.ts (slice, binding,
  *                                      upload, destroy)
  *   paletteBitsForLayout               src/model/runtime-plan.ts:352-368
+ *   FusedConformerConvKernel           src/webgpu/kernels/conformer-conv.ts:174-350
+ *     .create(device, arena, capacity, profile)  :194-253
+ *     .createDispatch(descriptor)      :255-344 (record checks :403-432 here,
+ *                                      the numeric contract in pk_conv_validate)
+ *   FusedConformerConvDispatch.encode / destroy  :117-162
+ *   planFusedConformerConv             :72-115 (rows and byte lengths are the
+ *                                      reference's; workgroups is this
+ *                                      library's own launch)
  * The WebGPU device, queue, buffers and command encoder are replaced by HIP
  * equivalents with the same shapes (HipGpuDevice, queue.writeBuffer /
  * submit / onSubmittedWorkDone, createCommandEncoder().finish()).
@@ -51,6 +59,8 @@ const FP32_PACKED_K = 4;
 const TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 8650752;
 const FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 17301504;
 const REQUIRE_PRODUCTION_SIGNATURE = 1;
+const GEMM_GLU = 2;
+const CONV_INPUT_GLU = 1;
 
 /** runtime-plan.ts:352-368 */
 function paletteBitsForLayout(layout) {
@@ -386,6 +396,191 @@ function requirePaletteRecords(descriptor, paletteBits, fp32) {
   return groups;
 }
 
+/* ------------------------------------------------- conformer convolution */
+
+const CONFORMER_CONV_CHANNELS = 1024;
+const CONFORMER_CONV_POINTWISE_CHANNELS = 2048;
+const CONFORMER_CONV_KERNEL_SIZE = 9;
+const CONFORMER_DEPTHWISE_WEIGHT_LAYOUT = "kernel-channel-vec4";
+const CONFORMER_FOLDED_BATCH_NORM_LAYOUT = "channel";
+
+function precisionOf(executionProfile) {
+  return executionProfile === undefined || executionProfile.precision === "fp16" ? "f16" : "f32";
+}
+
+/** planFusedConformerConv (conformer-conv.ts:72-115). */
+function planFusedConformerConv(shape, executionProfile) {
+  for (const [value, name] of [[shape.batchSize, "batchSize"], [shape.frames, "frames"]]) {
+    if (!isSafe(value) || value <= 0) throw new RangeError(`${name} must be a positive integer`);
+  }
+  const plan = native().convPlanShape(precisionOf(executionProfile), shape.batchSize, shape.frames, 0);
+  return Object.assign({ batchSize: shape.batchSize, frames: shape.frames }, plan);
+}
+
+/** requirePackedTensor (conformer-conv.ts:403-432), on the tensor's runtime record. */
+function requirePackedTensor(tensor, dtype, shape, layout, byteLength, label) {
+  const record = tensor.runtimeRecord;
+  const storageShape = shape.length === 2 ? [shape[0], shape[1] / 4, 4] : shape;
+  if (
+    record.dtype !== dtype ||
+    record.layout !== layout ||
+    record.byteLength !== byteLength ||
+    shapeKey(record.logicalShape) !== shapeKey(shape) ||
+    shapeKey(record.storageShape) !== shapeKey(storageShape)
+  ) {
+    throw new Error(
+      `${label} must be ${dtype} ${layout} logical [${shape.join(",")}], ` +
+        `storage [${storageShape.join(",")}], ${byteLength} bytes`,
+    );
+  }
+}
+
+/** Package records of the depthwise weights and folded batch norm. */
+function conformerConvTensorRecords(options) {
+  const dtype = (options && options.dtype) || "float16";
+  const scalar = dtype === "float16" ? 2 : 4;
+  const weights = {
+    dtype,
+    logicalShape: [CONFORMER_CONV_KERNEL_SIZE, CONFORMER_CONV_CHANNELS],
+    storageShape: [CONFORMER_CONV_KERNEL_SIZE, CONFORMER_CONV_CHANNELS / 4, 4],
+    byteLength: CONFORMER_CONV_KERNEL_SIZE * CONFORMER_CONV_CHANNELS * scalar,
+    layout: CONFORMER_DEPTHWISE_WEIGHT_LAYOUT,
+  };
+  const affine = {
+    dtype: "float32",
+    logicalShape: [CONFORMER_CONV_CHANNELS],
+    storageShape: [CONFORMER_CONV_CHANNELS],
+    byteLength: CONFORMER_CONV_CHANNELS * 4,
+    layout: CONFORMER_FOLDED_BATCH_NORM_LAYOUT,
+  };
+  return {
+    depthwiseWeights: { sourceRecord: weights, runtimeRecord: weights },
+    batchNormScale: { sourceRecord: affine, runtimeRecord: affine },
+    batchNormShift: { sourceRecord: affine, runtimeRecord: affine },
+  };
+}
+
+function addressOf(binding) {
+  return binding.buffer.address + BigInt(binding.offset);
+}
+
+class FusedConformerConvDispatch {
+  constructor(label, result, op, batchSize) {
+    this.label = label;
+    this.result = result;
+    this.op = op;
+    this.batchSize = batchSize;
+    this.destroyed = false;
+  }
+
+  /** encode (conformer-conv.ts:128-157): shape.batchSize selects the active windows. */
+  encode(encoder, timestampWrites, shape) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    const active = shape === undefined || shape.batchSize === undefined ? this.batchSize : shape.batchSize;
+    if (!isSafe(active) || active <= 0 || active > this.batchSize)
+      throw new RangeError(`${this.label} active batch must be in [1, ${this.batchSize}]`);
+    const op = this.op;
+    encoder.record(() => {
+      const qs = timestampWrites ? timestampWrites.querySet : null;
+      const begin = qs && timestampWrites.beginningOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.beginningOfPassWriteIndex] : null;
+      const end = qs && timestampWrites.endOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.endOfPassWriteIndex] : null;
+      native().convEnqueue(op, active, null, begin, end);
+    });
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().convDestroy(this.op);
+  }
+
+  plan(activeBatch) {
+    return native().convPlan(this.op, activeBatch || 0);
+  }
+}
+
+class FusedConformerConvKernel {
+  constructor(device, arena, executionProfile) {
+    this.device = device;
+    this.arena = arena;
+    this.precision = precisionOf(executionProfile);
+    this.executionProfile = executionProfile;
+    this.destroyed = false;
+  }
+
+  /** The kernels are compiled into the library: no pipeline or uniform pool to build. */
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new FusedConformerConvKernel(device, arena, executionProfile));
+  }
+
+  get uniformParameterPoolBytes() {
+    return 0;
+  }
+
+  get uniformParameterPoolUsedSlots() {
+    return 0;
+  }
+
+  nativeDescriptor(descriptor) {
+    const plan = planFusedConformerConv(descriptor, this.executionProfile);
+    const dtype = this.precision === "f16" ? "float16" : "float32";
+    requirePackedTensor(descriptor.depthwiseWeights, dtype,
+                        [CONFORMER_CONV_KERNEL_SIZE, CONFORMER_CONV_CHANNELS], CONFORMER_DEPTHWISE_WEIGHT_LAYOUT,
+                        plan.depthwiseWeightByteLength, `${descriptor.label} depthwise weights`);
+    requirePackedTensor(descriptor.batchNormScale, "float32", [CONFORMER_CONV_CHANNELS],
+                        CONFORMER_FOLDED_BATCH_NORM_LAYOUT, plan.affineByteLength,
+                        `${descriptor.label} folded batch norm scale`);
+    requirePackedTensor(descriptor.batchNormShift, "float32", [CONFORMER_CONV_CHANNELS],
+                        CONFORMER_FOLDED_BATCH_NORM_LAYOUT, plan.affineByteLength,
+                        `${descriptor.label} folded batch norm shift`);
+    const input = this.arena.binding(descriptor.pointwiseInput);
+    const output = this.arena.binding(descriptor.output);
+    const valid = this.arena.binding(descriptor.validLengths);
+    const w = descriptor.depthwiseWeights.binding;
+    const scale = descriptor.batchNormScale.binding;
+    const shift = descriptor.batchNormShift.binding;
+    return {
+      label: descriptor.label,
+      flags: descriptor.pointwiseInputIsGlu ? CONV_INPUT_GLU : 0,
+      precision: this.precision,
+      batchSize: descriptor.batchSize,
+      frames: descriptor.frames,
+      pointwiseInput: addressOf(input),
+      pointwiseInputBytes: input.size,
+      depthwiseWeights: addressOf(w),
+      depthwiseWeightsBytes: w.size,
+      batchNormScale: addressOf(scale),
+      batchNormScaleBytes: scale.size,
+      batchNormShift: addressOf(shift),
+      batchNormShiftBytes: shift.size,
+      validLengths: addressOf(valid),
+      validLengthsBytes: valid.size,
+      output: addressOf(output),
+      outputBytes: output.size,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().convValidate(this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (conformer-conv.ts:255-344). */
+  createDispatch(descriptor) {
+    if (this.destroyed) throw new Error("Parakeet Conformer convolution kernel was destroyed");
+    const op = native().convCreate(this.device.context, this.nativeDescriptor(descriptor));
+    const rows = descriptor.batchSize * descriptor.frames;
+    return new FusedConformerConvDispatch(
+      descriptor.label, { output: descriptor.output, rows, channels: CONFORMER_CONV_CHANNELS }, op,
+      descriptor.batchSize);
+  }
+
+  destroy() {
+    this.destroyed = true;
+  }
+}
+
 /* ------------------------------------------------------------ kernels */
 
 class GemmDispatch {
@@ -486,7 +681,7 @@ class PaletteGemmKernel {
     /** @type {any} */
     const d = {
       label: descriptor.label,
-      flags: this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0,
+      flags: (this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0) | (descriptor.glu ? GEMM_GLU : 0),
       precision: fp32 ? "f32" : "f16",
       paletteBits,
       rows: descriptor.rows,
@@ -660,4 +855,13 @@ module.exports = {
   F16_TILE_INNER,
   F32_TILE_INNER,
   FP32_PACKED_K,
+  FusedConformerConvKernel,
+  FusedConformerConvDispatch,
+  planFusedConformerConv,
+  conformerConvTensorRecords,
+  CONFORMER_CONV_CHANNELS,
+  CONFORMER_CONV_POINTWISE_CHANNELS,
+  CONFORMER_CONV_KERNEL_SIZE,
+  CONFORMER_DEPTHWISE_WEIGHT_LAYOUT,
+  CONFORMER_FOLDED_BATCH_NORM_LAYOUT,
 };

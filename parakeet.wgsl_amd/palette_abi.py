@@ -19,6 +19,8 @@ OK, INVALID_ARGUMENT, ALLOCATION_FAILURE, INTERNAL_ERROR, DEVICE_ERROR, DESTROYE
 PRECISION = {"f16": 0, "f32": 1}
 ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
 REQUIRE_PRODUCTION_SIGNATURE = 0x1
+GEMM_GLU = 0x2
+CONV_INPUT_GLU = 0x1
 EXPAND_LAYOUT = {"row-major": 0, "tile-major": 1}
 
 
@@ -129,6 +131,7 @@ class DeviceInfo(ctypes.Structure):
 class ConvDesc(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
         ("label", ctypes.c_char_p),
         ("precision", ctypes.c_int32),
         ("batch_size", ctypes.c_uint32),
@@ -397,11 +400,12 @@ class GemmOp:
                  bias: DeviceArray | None = None, residual: DeviceArray | None = None,
                  residual_scale: float | None = None, activation: str = "none",
                  prepared: PreparedWeight | None = None, label: str = "palette-gemm",
-                 production_only: bool = False, stream=None):
+                 production_only: bool = False, glu: bool = False, stream=None):
         precision = "f16" if palette.dtype == np.float16 else "f32"
         groups = palette.shape[0]
+        flags = (REQUIRE_PRODUCTION_SIGNATURE if production_only else 0) | (GEMM_GLU if glu else 0)
         self.desc = GemmDesc(
-            ctypes.sizeof(GemmDesc), REQUIRE_PRODUCTION_SIGNATURE if production_only else 0,
+            ctypes.sizeof(GemmDesc), flags,
             label.encode(), PRECISION[precision], bits, rows, inner, columns, groups,
             columns // groups if groups else 0,
             a.ptr, a.nbytes,
@@ -456,11 +460,13 @@ def _slice(array):
 
 def conv_desc(*, pointwise_input, depthwise_weights, batch_norm_scale, batch_norm_shift, valid_lengths, output,
               batch_size: int, frames: int, channels: int = 0, precision: str | None = None,
-              label: str = "conformer-conv") -> ConvDesc:
-    """A pk_conv_desc over DeviceArrays (or any objects with ptr/nbytes)."""
+              label: str = "conformer-conv", input_glu: bool = False) -> ConvDesc:
+    """A pk_conv_desc over DeviceArrays (or any objects with ptr/nbytes);
+    input_glu: the pointwise input is the [rows, C] GLU (PK_CONV_INPUT_GLU)."""
     if precision is None:
         precision = "f16" if pointwise_input.dtype == np.float16 else "f32"
-    return ConvDesc(ctypes.sizeof(ConvDesc), label.encode(), PRECISION[precision], batch_size, frames, channels,
+    return ConvDesc(ctypes.sizeof(ConvDesc), CONV_INPUT_GLU if input_glu else 0, label.encode(),
+                    PRECISION[precision], batch_size, frames, channels,
                     *_slice(pointwise_input), *_slice(depthwise_weights), *_slice(batch_norm_scale),
                     *_slice(batch_norm_shift), *_slice(valid_lengths), *_slice(output))
 

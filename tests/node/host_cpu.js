@@ -93,6 +93,54 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
   // synthetic shapes are accepted when asked for
   return host.F16GemmKernel.create({}, arena, undefined, { allowSyntheticShapes: true }).then((synthetic) => {
     synthetic.validateDescriptor(descriptor({ rows: 300, inner: 1024, columns: 512, bits: 6 }));
+    return host.FusedConformerConvKernel.create({}, arena, 64);
+  }).then((conv) => {
+    // planFusedConformerConv known answers (conformer-conv-kernel-shapes.test.ts:18-58)
+    const plan = host.planFusedConformerConv({ batchSize: 2, frames: 188 });
+    assert.strictEqual(plan.rows, 376);
+    assert.strictEqual(plan.inputByteLength, 376 * host.CONFORMER_CONV_POINTWISE_CHANNELS * 2);
+    assert.strictEqual(plan.outputByteLength, 376 * host.CONFORMER_CONV_CHANNELS * 2);
+    assert.strictEqual(plan.validLengthsByteLength, 8);
+    assert.strictEqual(plan.depthwiseWeightByteLength, host.CONFORMER_CONV_KERNEL_SIZE * 1024 * 2);
+    assert.strictEqual(plan.affineByteLength, 4096);
+    const plan32 = host.planFusedConformerConv({ batchSize: 2, frames: 188 }, { precision: "fp32" });
+    assert.strictEqual(plan32.inputByteLength, 376 * 2048 * 4);
+    assert.strictEqual(plan32.depthwiseWeightByteLength, 9 * 1024 * 4);
+    assert.strictEqual(host.CONFORMER_DEPTHWISE_WEIGHT_LAYOUT, "kernel-channel-vec4");
+    assert.strictEqual(host.CONFORMER_FOLDED_BATCH_NORM_LAYOUT, "channel");
+    throwsLike(() => host.planFusedConformerConv({ batchSize: 0, frames: 188 }), RangeError,
+               "batchSize must be a positive integer");
+    throwsLike(() => host.planFusedConformerConv({ batchSize: 1, frames: 1.5 }), RangeError,
+               "frames must be a positive integer");
+    const rec = host.conformerConvTensorRecords();
+    function convDescriptor(mutate) {
+      const d = {
+        label: "layer0-convolution-glu-depthwise-bn-silu", batchSize: 2, frames: 188,
+        pointwiseInput: arena.slice("p", 0, 376 * 2048 * 2),
+        depthwiseWeights: tensor(rec.depthwiseWeights),
+        batchNormScale: tensor(rec.batchNormScale),
+        batchNormShift: tensor(rec.batchNormShift),
+        validLengths: arena.slice("v", 128 * 1024 * 1024, 8),
+        output: arena.slice("z", 256 * 1024 * 1024, 376 * 1024 * 2),
+      };
+      if (mutate) mutate(d);
+      return d;
+    }
+    conv.validateDescriptor(convDescriptor());
+    throwsLike(() => conv.validateDescriptor(convDescriptor((d) => {
+      d.output = arena.slice("z", 256 * 1024 * 1024, 376 * 1024 * 2 - 4);
+    })), RangeError, "layer0-convolution-glu-depthwise-bn-silu output needs 770048 bytes; arena slice has 770044");
+    throwsLike(() => conv.validateDescriptor(convDescriptor((d) => {
+      d.depthwiseWeights = Object.assign({}, d.depthwiseWeights, {
+        runtimeRecord: Object.assign({}, rec.depthwiseWeights.runtimeRecord, { layout: "channel" }) });
+    })), Error, "depthwise weights must be float16 kernel-channel-vec4 logical [9,1024], storage [9,256,4], 18432 bytes");
+    throwsLike(() => conv.validateDescriptor(convDescriptor((d) => {
+      d.batchNormShift = Object.assign({}, d.batchNormShift, {
+        runtimeRecord: Object.assign({}, rec.batchNormShift.runtimeRecord, { dtype: "float16" }) });
+    })), Error, "folded batch norm shift must be float32 channel logical [1024], storage [1024], 4096 bytes");
+    throwsLike(() => conv.validateDescriptor(convDescriptor((d) => {
+      d.output = arena.slice("z", 4096, 376 * 1024 * 2);
+    })), Error, "must not overlap the pointwise input");
     console.log("host_cpu ok");
   });
 }).catch((e) => { console.error(e); process.exit(1); });

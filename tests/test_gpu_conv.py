@@ -156,21 +156,23 @@ def test_conv_timed_enqueue_stamps_the_kernel(abi, ctx, scope, workloads):
         end.destroy()
 
 
-def module_on_gpu(abi, ctx, scope, module):
-    """PW1 GEMM -> fused conv tail -> PW2 GEMM + residual on one stream."""
+def module_on_gpu(abi, ctx, scope, module, fused_glu=False):
+    """PW1 GEMM -> fused conv tail -> PW2 GEMM + residual on one stream.
+    fused_glu: PW1 carries the GLU epilogue ([rows, d] output) and the tail
+    takes that GLU as its input."""
     x = scope.put(module.x)
     rows, d = module.x.shape
     conv = module.conv
-    p = scope.empty((rows, 2 * d), np.float16)
+    p = scope.empty((rows, d if fused_glu else 2 * d), np.float16)
     z = scope.empty((rows, d), np.float16)
     y = scope.empty((rows, d), np.float16)
     pw1 = abi.GemmOp(ctx, a=x, packed=scope.put(module.pw1.packed), palette=scope.put(module.pw1.palette),
                      output=p, bits=module.pw1.bits, rows=rows, inner=d, columns=2 * d,
-                     label="convolution-pointwise1")
+                     label="convolution-pointwise1", glu=fused_glu)
     tail = abi.ConformerConvOp(
         ctx, pointwise_input=p, depthwise_weights=scope.put(conv.weights), batch_norm_scale=scope.put(conv.scale),
         batch_norm_shift=scope.put(conv.shift), valid_lengths=scope.put(conv.valid), output=z,
-        batch_size=conv.batch, frames=conv.frames)
+        batch_size=conv.batch, frames=conv.frames, input_glu=fused_glu)
     pw2 = abi.GemmOp(ctx, a=z, packed=scope.put(module.pw2.packed), palette=scope.put(module.pw2.palette),
                      output=y, bits=module.pw2.bits, rows=rows, inner=d, columns=d, residual=x,
                      residual_scale=1.0, label="convolution-pointwise2-residual")
@@ -227,3 +229,117 @@ def test_conv_module_full_size(abi, ctx, scope, oracle, workloads):
     sub = workloads.ConvCase(p[rows], module.conv.weights, module.conv.scale, module.conv.shift,
                              module.conv.valid[list(windows)], len(windows), module.conv.frames)
     assert ulp_distance(z[rows], oracle_conv(oracle, sub)) <= 1
+
+
+# ------------------------------------------------ GLU epilogue (fused PW1)
+
+
+def glu_gemm_on_gpu(abi, ctx, scope, case, variant=None):
+    rows, columns = case.rows, case.weight.columns
+    out = scope.put(np.full((rows, columns // 2), np.float16(777.0)))
+    op = abi.GemmOp(ctx, a=scope.put(case.a), packed=scope.put(case.weight.packed),
+                    palette=scope.put(case.weight.palette), output=out, bits=case.weight.bits, rows=rows,
+                    inner=case.weight.inner, columns=columns, label="pointwise1-glu", glu=True)
+    try:
+        if variant is not None:
+            op.set_variant(variant)
+        op.enqueue()
+        ctx.synchronize()
+        return out.download(), op.plan().kernel.decode()
+    finally:
+        op.release()
+
+
+def assert_glu_parity(oracle, got, case):
+    w = case.weight
+    p = oracle.gemm(case.a, w.packed, w.bits, w.palette, w.columns, mode="f16-chain", threads=8)
+    norm, _ = oracle.relative_errors(got, oracle.glu(p))
+    assert norm <= F16_TOL_REFERENCE, norm
+    p64 = oracle.gemm(case.a, w.packed, w.bits, w.palette, w.columns, mode="f64", threads=8)
+    norm, _ = oracle.relative_errors(got, oracle.glu(p64, mode="f64"))
+    assert norm <= F16_TOL_TRUTH, norm
+
+
+@pytest.mark.parametrize("rows,inner,columns,bits", [
+    (376, 1024, 2048, 6),   # two windows of the convolution's pointwise-1
+    (300, 512, 256, 5),     # ragged rows
+    (64, 256, 128, 6),      # one 64-row tile, small-M plan moved to the pair-code kernels
+    (5, 128, 64, 5),        # fewer rows than a tile
+])
+def test_glu_epilogue_matches_oracle(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits):
+    case = workloads.gemm_case(30 + bits, rows, inner, columns, bits)
+    print(f"glu gemm {rows}x{inner}x{columns} b{bits}", flush=True)
+    got, _ = glu_gemm_on_gpu(abi, ctx, scope, case)
+    assert_glu_parity(oracle, got, case)
+
+
+def test_glu_epilogue_every_pair_code_variant(abi, ctx, scope, oracle, workloads):
+    """Every pair-code tile computes the GLU epilogue; other families refuse it."""
+    case = workloads.gemm_case(33, 200, 256, 512, 6)
+    ran = 0
+    for variant in range(abi.variant_count("f16")):
+        try:
+            got, kernel = glu_gemm_on_gpu(abi, ctx, scope, case, variant)
+        except abi.PaletteRangeError as e:
+            assert "has no GLU epilogue" in str(e)
+            continue
+        print(f"glu variant {variant} {kernel}", flush=True)
+        assert "_f16p_" in kernel
+        assert_glu_parity(oracle, got, case)
+        ran += 1
+    assert ran >= 8
+
+
+def test_glu_descriptor_errors(abi, ctx, scope, workloads):
+    case = workloads.gemm_case(34, 64, 128, 128, 5)
+    a, packed, palette = scope.put(case.a), scope.put(case.weight.packed), scope.put(case.weight.palette)
+    out = scope.empty((64, 64), np.float16)
+    bias = scope.put(np.zeros(128, np.float32))
+    with pytest.raises(abi.PaletteError, match="GLU epilogue needs"):
+        abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=5, rows=64, inner=128, columns=128,
+                   bias=bias, glu=True)
+    with pytest.raises(abi.PaletteError, match="output binding must hold"):
+        abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=scope.empty((64, 32), np.float16), bits=5,
+                   rows=64, inner=128, columns=128, glu=True)
+
+
+def test_conv_glu_input_matches_oracle(abi, ctx, scope, oracle, workloads):
+    """PK_CONV_INPUT_GLU: the tail over a ready [rows, C] GLU equals the oracle
+    tail over values g with saturated gates (sigmoid(40) clamps to
+    1/(1 + e^-20), 2e-9 from one)."""
+    batch, frames, channels = 3, 100, 256
+    case = workloads.conv_case(35, batch, frames, channels, valid=[100, 61, 7])
+    g = case.pointwise[:, :channels].copy()
+    out = scope.put(np.zeros((batch * frames, channels), np.float16))
+    op = abi.ConformerConvOp(
+        ctx, pointwise_input=scope.put(g), depthwise_weights=scope.put(case.weights),
+        batch_norm_scale=scope.put(case.scale), batch_norm_shift=scope.put(case.shift),
+        valid_lengths=scope.put(case.valid), output=out, batch_size=batch, frames=frames, channels=channels,
+        input_glu=True)
+    try:
+        op.enqueue()
+        ctx.synchronize()
+        assert op.plan().kernel.decode().startswith("pk_conformer_conv_glu_")
+        got = out.download()
+    finally:
+        op.release()
+    saturated = np.concatenate([g.astype(np.float32), np.full_like(g, 40.0, np.float32)], axis=1)
+    want = oracle.conformer_conv(saturated, case.weights.astype(np.float32), case.scale, case.shift, case.valid,
+                                 batch=batch, frames=frames).astype(np.float16)
+    assert ulp_distance(got, want) <= 1
+
+
+def test_fused_glu_conv_module_full_size(abi, ctx, scope, oracle, workloads):
+    """The convolution module with the GLU fused into PW1's epilogue: within
+    1e-2 of the reference chain and 2e-3 of the fp64 truth on windows 0, 7
+    and 15, like the unfused path."""
+    module = workloads.conv_module(0)
+    print("fused-GLU conv module 16x188x1024", flush=True)
+    _, _, y = module_on_gpu(abi, ctx, scope, module, fused_glu=True)
+    windows = (0, 7, 15)
+    rows, y_ref = module_on_oracle(oracle, module, windows, "reference")
+    norm, _ = oracle.relative_errors(y[rows], y_ref)
+    assert norm <= F16_TOL_REFERENCE, norm
+    rows, y_truth = module_on_oracle(oracle, module, windows, "f64")
+    norm, _ = oracle.relative_errors(y[rows], y_truth)
+    assert norm <= F16_TOL_TRUTH, norm

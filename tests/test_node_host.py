@@ -65,3 +65,25 @@ def test_node_host_gemm_matches_oracle(tmp_path, oracle, workloads, bits, activa
                         residual_scale=scale, activation=activation, mode="f64", threads=8)
     assert oracle.relative_errors(got, ref)[0] <= 1e-2
     assert oracle.relative_errors(got, truth)[0] <= 2e-3
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_conv_matches_oracle(tmp_path, oracle, workloads):
+    """The conv tail through the Node host (FusedConformerConvKernel) on 3
+    windows with an active batch of 2: within one f16 ulp of the oracle."""
+    batch, frames = 3, 188
+    case = workloads.conv_case(21, batch, frames, 1024, valid=[188, 97, 150])
+    files = {}
+    for name in ("pointwise", "weights", "scale", "shift", "valid"):
+        files[name] = str(tmp_path / f"{name}.bin")
+        np.ascontiguousarray(getattr(case, name)).tofile(files[name])
+    spec = dict(files, batchSize=batch, frames=frames, activeBatch=2, output=str(tmp_path / "out.bin"))
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print(run_node("host_gpu_conv.js", str(tmp_path / "case.json")))
+    got = np.fromfile(tmp_path / "out.bin", dtype=np.float16).reshape(batch * frames, 1024)[:2 * frames]
+    want = oracle.conformer_conv(case.pointwise[:2 * frames], case.weights, case.scale, case.shift, case.valid[:2],
+                                 batch=2, frames=frames)
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert np.all(diff <= ulp * 1.0 + 1e-12)

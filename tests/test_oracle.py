@@ -446,3 +446,39 @@ def test_conv_batch_items_are_independent(oracle):
     two = oracle.conformer_conv(changed, weights, scale, shift, valid, batch=batch, frames=frames)
     np.testing.assert_array_equal(one[:frames], two[:frames])
     assert not np.array_equal(one[frames:], two[frames:])
+
+
+def test_glu_matches_torch_glu(oracle):
+    """value half first, gate half second (conformer-conv.ts:520-535), the
+    same as torch.nn.functional.glu over the channel axis."""
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((37, 48)) * 3
+    want = F.glu(torch.from_numpy(x), dim=-1).numpy()
+    np.testing.assert_allclose(oracle.glu(x, mode="f64"), want, rtol=1e-14, atol=1e-15)
+    np.testing.assert_allclose(oracle.glu(x.astype(np.float32)), want, rtol=2e-6, atol=1e-7)
+    got16 = oracle.glu(x.astype(np.float16), mode="f64")
+    want16 = F.glu(torch.from_numpy(x.astype(np.float16).astype(np.float64)), dim=-1).numpy().astype(np.float16)
+    np.testing.assert_array_equal(got16.view(np.uint16), want16.view(np.uint16))
+
+
+def test_glu_gate_clamp(oracle):
+    x = np.array([[1e6, -30.0]])
+    for mode in ("f64", "f32-chain"):
+        np.testing.assert_allclose(oracle.glu(x.astype(np.float32) if mode != "f64" else x, mode=mode),
+                                   [[1e6 / (1 + np.exp(20.0))]], rtol=1e-5)
+
+
+def test_glu_is_the_conv_tail_with_a_center_tap(oracle):
+    """With the center tap 1, scale 1 and shift 0 the tail is silu(glu): the
+    two oracle functions agree on the GLU they form."""
+    rng = np.random.default_rng(15)
+    x = rng.standard_normal((20, 16)).astype(np.float32)
+    w = np.zeros((9, 8), np.float32)
+    w[4] = 1.0
+    tail = oracle.conformer_conv(x, w, np.ones(8, np.float32), np.zeros(8, np.float32), np.array([20], np.uint32),
+                                 batch=1, frames=20, mode="f64")
+    g = oracle.glu(x.astype(np.float64), mode="f64")
+    np.testing.assert_allclose(tail, g / (1 + np.exp(-g)), rtol=1e-6)
