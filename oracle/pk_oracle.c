@@ -514,3 +514,106 @@ int pko_glu(int dtype, int mode, uint64_t rows, uint32_t channels, const void *i
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Relative-position attention (src/webgpu/kernels/attention.ts:418-727)     */
+/* ------------------------------------------------------------------------ */
+
+static inline void store_out(int dtype, void *p, uint64_t idx, double v) {
+  if (dtype == PKO_DTYPE_F16)
+    ((uint16_t *)p)[idx] = pko_f64_to_f16(v);
+  else if (dtype == PKO_DTYPE_F64)
+    ((double *)p)[idx] = v;
+  else
+    ((float *)p)[idx] = (float)v;
+}
+
+int pko_relative_attention(int dtype, int mode, uint32_t batch, uint32_t frames, const void *qkv,
+                           const void *positions, const float *bias_u, const float *bias_v,
+                           const uint32_t *valid, void *out) {
+  enum { HEADS = 8, HEAD = 128, HIDDEN = 1024 };
+  if (!qkv || !positions || !bias_u || !bias_v || !valid || !out || batch == 0 || frames == 0 ||
+      (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64) ||
+      (mode != PKO_MODE_F32_CHAIN && mode != PKO_MODE_F64))
+    return 1;
+  const uint64_t P = 2ull * frames - 1u;
+  const float scale32 = (float)(1.0 / sqrt(128.0));
+  const double scale64 = 1.0 / sqrt(128.0);
+  float *s32 = (float *)malloc(sizeof(float) * frames);
+  double *s64 = (double *)malloc(sizeof(double) * frames);
+  if (!s32 || !s64) {
+    free(s32);
+    free(s64);
+    return 1;
+  }
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t live = valid[b] < frames ? valid[b] : frames;
+    for (uint32_t h = 0; h < HEADS; ++h) {
+      for (uint32_t q = 0; q < frames; ++q) {
+        const uint64_t qrow = (uint64_t)b * frames + q;
+        if (q >= live) {
+          for (uint32_t d = 0; d < HEAD; ++d) store_out(dtype, out, qrow * HIDDEN + h * HEAD + d, 0.0);
+          continue;
+        }
+        /* scores over the live keys */
+        for (uint32_t k = 0; k < live; ++k) {
+          const uint64_t krow = (uint64_t)b * frames + k;
+          const uint64_t rel = (uint64_t)frames - 1u - q + k;
+          float acc32 = 0.0f;
+          double acc64 = 0.0;
+          for (uint32_t d = 0; d < HEAD; ++d) {
+            const double qd = conv_in(dtype, qkv, qrow * 3u * HIDDEN + h * HEAD + d);
+            const double kd = conv_in(dtype, qkv, krow * 3u * HIDDEN + HIDDEN + h * HEAD + d);
+            const uint64_t pidx = (((uint64_t)h * 32u + d / 4u) * P + rel) * 4u + d % 4u;
+            const double rd = conv_in(dtype, positions, pidx);
+            const float u = bias_u[h * HEAD + d], v = bias_v[h * HEAD + d];
+            if (mode == PKO_MODE_F32_CHAIN) {
+              const float qu = (float)qd + u, qv = (float)qd + v;
+              acc32 = fmaf(qu, (float)kd, acc32);
+              acc32 = fmaf(qv, (float)rd, acc32);
+            } else {
+              acc64 += (qd + u) * kd + (qd + v) * rd;
+            }
+          }
+          s32[k] = acc32 * scale32;
+          s64[k] = acc64 * scale64;
+        }
+        /* softmax over k < live */
+        float max32 = -3.402823466e+38f;
+        double max64 = -HUGE_VAL;
+        for (uint32_t k = 0; k < live; ++k) {
+          if (s32[k] > max32) max32 = s32[k];
+          if (s64[k] > max64) max64 = s64[k];
+        }
+        float sum32 = 0.0f;
+        double sum64 = 0.0;
+        for (uint32_t k = 0; k < live; ++k) {
+          s32[k] = expf(s32[k] - max32);
+          s64[k] = exp(s64[k] - max64);
+          sum32 += s32[k];
+          sum64 += s64[k];
+        }
+        const float inv32 = 1.0f / sum32;
+        for (uint32_t k = 0; k < live; ++k) {
+          s32[k] = s32[k] * inv32;
+          s64[k] = s64[k] / sum64;
+        }
+        /* context */
+        for (uint32_t d = 0; d < HEAD; ++d) {
+          float o32 = 0.0f;
+          double o64 = 0.0;
+          for (uint32_t k = 0; k < live; ++k) {
+            const uint64_t krow = (uint64_t)b * frames + k;
+            const double vd = conv_in(dtype, qkv, krow * 3u * HIDDEN + 2u * HIDDEN + h * HEAD + d);
+            o32 = fmaf(s32[k], (float)vd, o32);
+            o64 += s64[k] * vd;
+          }
+          store_out(dtype, out, qrow * HIDDEN + h * HEAD + d, mode == PKO_MODE_F32_CHAIN ? (double)o32 : o64);
+        }
+      }
+    }
+  }
+  free(s32);
+  free(s64);
+  return 0;
+}

@@ -32,6 +32,11 @@
  *                         pinned: exact small-integer cases, the f16 rounding
  *                         function against every f16 value and its midpoints.
  *   pko_gemm (F64)        reference-independent truth of the same expression.
+ *   pko_relative_attention  src/webgpu/kernels/attention.ts:418-727 (Transformer-XL
+ *                         relative-position attention, 8 heads x 128); pinned by
+ *                         a float64 torch restatement, plain attention when the
+ *                         positions and biases are zero, the direction of the
+ *                         relative shift, one valid key and empty windows.
  *   pko_glu               the GLU step of conformer-conv.ts:520-535 on its own
  *                         (value * sigmoid(gate) of a [rows, 2C] input);
  *                         pinned by torch's glu and the gate clamp in
@@ -115,6 +120,24 @@ int pko_gemm(const pko_gemm_args *args, int mode, int threads);
    reference's f32 arithmetic (fma over taps 0..8); PKO_MODE_F64: the same
    expression in double (output still rounded to dtype). dtype PKO_DTYPE_F64
    takes double input and weights and writes double output (truth chains). */
+/* Relative-position self-attention of attention.ts:418-727 over 8 heads of
+   128 channels. qkv [batch*frames, 3072] (dtype; Q, K, V column blocks of
+   1024, head h at columns 128h..); positions: projected relative positions in
+   the reference's "head-vector-position-vec4" order [8][32][2T-1][4] (dtype),
+   position p holds relative distance T-1-p; bias_u, bias_v [8, 128] f32;
+   valid [batch]; out [batch*frames, 1024] (dtype). For a query q below
+   valid = min(valid[b], T):
+     score(q, k) = sum_d (q_d + u_d) k_d + (q_d + v_d) R[T-1-q+k]_d, d in
+                   order, both products per d by fma, times 1/sqrt(128),
+     p(q, k)     = exp(score - max_k score) / sum_k exp(...) over k < valid,
+     out(q)      = sum_k p(q, k) v_k (fma in key order);
+   rows q >= valid are zero. mode PKO_MODE_F32_CHAIN: the reference's f32
+   arithmetic; PKO_MODE_F64: the same in double, rounded to dtype at the
+   end (PKO_DTYPE_F64: double in and out). */
+int pko_relative_attention(int dtype, int mode, uint32_t batch, uint32_t frames, const void *qkv,
+                           const void *positions, const float *bias_u, const float *bias_v,
+                           const uint32_t *valid, void *out);
+
 /* GLU of a [rows, 2*channels] input (values, then gates) into [rows,
    channels]: value * sigmoid(gate) with the reference's clamp, in f32
    (PKO_MODE_F32_CHAIN) or double (PKO_MODE_F64), rounded to dtype

@@ -15,6 +15,7 @@ Reference functions restated (see pk_oracle.h for the pins):
                   :2356-2599, :2847-2869 (f32)
   conformer_conv  src/webgpu/kernels/conformer-conv.ts:495-573
   glu             the GLU step of conformer-conv.ts:520-535
+  relative_attention  src/webgpu/kernels/attention.ts:418-727
 """
 from __future__ import annotations
 
@@ -83,6 +84,8 @@ def lib() -> ctypes.CDLL:
         ]
         _lib.pko_gemm.argtypes = [ctypes.POINTER(_GemmArgs), ctypes.c_int, ctypes.c_int]
         _lib.pko_conformer_conv.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 6
+        _lib.pko_relative_attention.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32] + \
+            [ctypes.c_void_p] * 6
         _lib.pko_glu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p,
                                  ctypes.c_void_p]
     return _lib
@@ -215,6 +218,28 @@ def conformer_conv(pointwise, weights, scale, shift, valid, *, batch, frames, mo
     if lib().pko_conformer_conv(dtype, MODE[mode], batch, frames, channels, _ptr(pointwise), _ptr(weights),
                                 _ptr(scale), _ptr(shift), _ptr(valid), _ptr(out)):
         raise ValueError("conformer_conv rejected its arguments")
+    return out
+
+
+def relative_attention(qkv, positions, bias_u, bias_v, valid, *, batch, frames, mode="f32-chain") -> np.ndarray:
+    """Relative-position attention (attention.ts:418-727): qkv [B*T, 3072],
+    positions in head-vector-position-vec4 order [8, 32, 2T-1, 4], biases
+    [8, 128] f32, valid [B]; returns [B*T, 1024] in the input's dtype."""
+    qkv = np.ascontiguousarray(qkv)
+    names = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.float64): "f64"}
+    if qkv.dtype not in names:
+        raise ValueError(f"relative_attention takes float16/32/64, not {qkv.dtype}")
+    positions = np.ascontiguousarray(positions, dtype=qkv.dtype)
+    bias_u = np.ascontiguousarray(bias_u, dtype=np.float32)
+    bias_v = np.ascontiguousarray(bias_v, dtype=np.float32)
+    valid = np.ascontiguousarray(valid, dtype=np.uint32)
+    if qkv.shape != (batch * frames, 3072) or positions.size != 8 * 128 * (2 * frames - 1) or \
+            bias_u.size != 1024 or bias_v.size != 1024 or valid.size != batch:
+        raise ValueError("relative_attention shape mismatch")
+    out = np.empty((batch * frames, 1024), dtype=qkv.dtype)
+    if lib().pko_relative_attention(DTYPE[names[qkv.dtype]], MODE[mode], batch, frames, _ptr(qkv), _ptr(positions),
+                                    _ptr(bias_u), _ptr(bias_v), _ptr(valid), _ptr(out)):
+        raise ValueError("relative_attention rejected its arguments")
     return out
 
 

@@ -230,3 +230,74 @@ def conv_module(seed: int = 0, windows: int = 16, frames: int = 188, d_model: in
     pw2 = palette_matrix(rng, bits, d_model, d_model, dtype=np.float16)
     conv = conv_case(int(rng.integers(1 << 31)), windows, frames, d_model, with_input=False)
     return ConvModule(x, pw1, pw2, conv)
+
+
+def relative_position_table(frames: int, channels: int = 1024) -> np.ndarray:
+    """The descending Transformer-XL sinusoid table [2T-1, channels] f32 the
+    reference converter builds (model/convert.py:1143-1165): row p is relative
+    distance T-1-p, even channels sin(pos * 10000^(-c/C)), odd channels cos."""
+    if frames < 1 or channels < 2 or channels % 2:
+        raise ValueError("frames must be positive and channels a positive even number")
+    positions = np.arange(frames - 1, -frames, -1, dtype=np.float32).reshape(-1, 1)
+    exponent = np.float32(-(np.log(10_000.0) / channels))
+    div_term = np.exp(np.arange(0, channels, 2, dtype=np.float32) * exponent)
+    angles = positions * div_term.reshape(1, -1)
+    table = np.empty((2 * frames - 1, channels), dtype=np.float32)
+    table[:, 0::2] = np.sin(angles)
+    table[:, 1::2] = np.cos(angles)
+    return table
+
+
+def pack_projected_positions(projected: np.ndarray, heads: int = 8, vector_width: int = 4) -> np.ndarray:
+    """[positions, channels] -> the reference's "head-vector-position-vec4"
+    order [heads, head_size / 4, positions, 4] (model/convert.py:1196-1225)."""
+    rows, channels = projected.shape
+    head = channels // heads
+    return np.ascontiguousarray(projected.reshape(rows, heads, head // vector_width, vector_width)
+                                .transpose(1, 2, 0, 3))
+
+
+@dataclass
+class AttentionCase:
+    """Operands of the relative-position attention: qkv [B*T, 3072], projected
+    positions [2T-1, 1024] (row-major; pack_projected_positions gives the
+    reference's order), biases u, v [8, 128] f32, valid lengths [B]."""
+    qkv: np.ndarray
+    positions: np.ndarray
+    bias_u: np.ndarray
+    bias_v: np.ndarray
+    valid: np.ndarray
+    batch: int
+    frames: int
+
+    @property
+    def packed_positions(self) -> np.ndarray:
+        return pack_projected_positions(self.positions)
+
+    def flops(self, batch: int | None = None) -> int:
+        """Score (two products per key) and context FLOP of the live keys."""
+        batch = self.batch if batch is None else batch
+        live = np.minimum(self.valid[:batch].astype(np.int64), self.frames)
+        return int((live * live).sum()) * 8 * 128 * 2 * 3
+
+    def algorithmic_bytes(self, batch: int | None = None) -> int:
+        batch = self.batch if batch is None else batch
+        e = self.qkv.dtype.itemsize
+        rows = batch * self.frames
+        return rows * 3072 * e + self.positions.size * e + 2 * 4096 + 4 * batch + rows * 1024 * e
+
+
+def attention_case(seed: int, batch: int, frames: int, *, dtype=np.float16, valid=None, qkv_std: float = 0.6,
+                   position_std: float = 0.6) -> AttentionCase:
+    """Seeded attention operands: qkv ~ N(0, qkv_std) (about what a 1024-wide
+    palette projection with N(0, 0.02) centroids makes of unit inputs),
+    positions ~ N(0, position_std), u, v ~ N(0, 0.02); valid lengths uniform
+    integers in [ceil(T/2), T] unless given."""
+    rng = np.random.default_rng(seed)
+    qkv = normal(rng, (batch * frames, 3072), qkv_std, dtype)
+    positions = normal(rng, (2 * frames - 1, 1024), position_std, dtype)
+    bias_u = normal(rng, (8, 128), 0.02, np.float32)
+    bias_v = normal(rng, (8, 128), 0.02, np.float32)
+    if valid is None:
+        valid = rng.integers((frames + 1) // 2, frames + 1, size=batch)
+    return AttentionCase(qkv, positions, bias_u, bias_v, np.asarray(valid, dtype=np.uint32), batch, frames)

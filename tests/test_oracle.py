@@ -482,3 +482,120 @@ def test_glu_is_the_conv_tail_with_a_center_tap(oracle):
                                  batch=1, frames=20, mode="f64")
     g = oracle.glu(x.astype(np.float64), mode="f64")
     np.testing.assert_allclose(tail, g / (1 + np.exp(-g)), rtol=1e-6)
+
+
+# ------------------------------------------ relative-position attention
+
+
+def test_relative_position_table_known_answers(workloads):
+    """model/tests/test_convert.py:799-815: the T=3, C=4 table by its closed
+    form, the 375 x 1024 table's zero-distance row all sin 0 / cos 0."""
+    table = workloads.relative_position_table(3, 4)
+    positions = np.array([2, 1, 0, -1, -2], dtype=np.float32).reshape(-1, 1)
+    div = np.exp(np.arange(0, 4, 2, dtype=np.float32) * np.float32(-(np.log(10_000.0) / 4)))
+    want = np.empty((5, 4), np.float32)
+    want[:, 0::2] = np.sin(positions * div)
+    want[:, 1::2] = np.cos(positions * div)
+    np.testing.assert_array_equal(table, want)
+    full = workloads.relative_position_table(188)
+    assert full.shape == (375, 1024)
+    np.testing.assert_array_equal(full[187, 0::2], 0)
+    np.testing.assert_array_equal(full[187, 1::2], 1)
+
+
+def test_pack_projected_positions_known_answers(workloads):
+    """model/tests/test_convert.py:828-840: rows inside head vectors."""
+    projected = np.arange(16, dtype=np.float16).reshape(2, 8)
+    packed = workloads.pack_projected_positions(projected, heads=2)
+    assert packed.shape == (2, 1, 2, 4)
+    np.testing.assert_array_equal(packed[0, 0, 0], projected[0, 0:4])
+    np.testing.assert_array_equal(packed[0, 0, 1], projected[1, 0:4])
+    np.testing.assert_array_equal(packed[1, 0, 0], projected[0, 4:8])
+    np.testing.assert_array_equal(packed[1, 0, 1], projected[1, 4:8])
+
+
+def _torch_relative_attention(case):
+    """Float64 restatement through torch: scores from einsum over heads with
+    the relative keys gathered by index T-1-q+k, a -inf mask, torch.softmax,
+    a batched matmul with V, zero rows past the valid length."""
+    import torch
+
+    B, T = case.batch, case.frames
+    x = torch.from_numpy(case.qkv.astype(np.float64)).reshape(B, T, 3, 8, 128)
+    q, k, v = x[:, :, 0], x[:, :, 1], x[:, :, 2]                    # [B, T, H, D]
+    u = torch.from_numpy(case.bias_u.astype(np.float64))
+    w = torch.from_numpy(case.bias_v.astype(np.float64))
+    pos = torch.from_numpy(case.positions.astype(np.float64)).reshape(2 * T - 1, 8, 128)
+    idx = (T - 1 - torch.arange(T)[:, None] + torch.arange(T)[None, :])  # [Tq, Tk]
+    rel = pos[idx]                                                      # [Tq, Tk, H, D]
+    ac = torch.einsum("bqhd,bkhd->bhqk", q + u, k)
+    bd = torch.einsum("bqhd,qkhd->bhqk", q + w, rel)
+    scores = (ac + bd) / np.sqrt(128.0)
+    out = torch.zeros(B, T, 8, 128, dtype=torch.float64)
+    for b in range(B):
+        live = int(min(case.valid[b], T))
+        if live == 0:
+            continue
+        p = torch.softmax(scores[b, :, :live, :live], dim=-1)          # [H, live, live]
+        ctx = torch.matmul(p, v[b, :live].permute(1, 0, 2).contiguous())  # [H, live, D]
+        out[b, :live] = ctx.permute(1, 0, 2)
+    return out.reshape(B * T, 1024).numpy()
+
+
+def _attend(oracle, case, mode):
+    return oracle.relative_attention(case.qkv, case.packed_positions, case.bias_u, case.bias_v, case.valid,
+                                     batch=case.batch, frames=case.frames, mode=mode)
+
+
+def test_relative_attention_matches_torch(oracle, workloads):
+    case = workloads.attention_case(20, 3, 13, dtype=np.float64, valid=[13, 7, 0])
+    want = _torch_relative_attention(case)
+    np.testing.assert_allclose(_attend(oracle, case, "f64"), want, rtol=1e-11, atol=1e-13)
+    case32 = workloads.AttentionCase(case.qkv.astype(np.float32), case.positions.astype(np.float32), case.bias_u,
+                                     case.bias_v, case.valid, case.batch, case.frames)
+    np.testing.assert_allclose(_attend(oracle, case32, "f32-chain"), want, rtol=2e-5, atol=2e-6)
+
+
+def test_relative_attention_without_positions_is_plain_attention(oracle, workloads):
+    """Zero positions and biases leave scaled dot-product attention (torch's
+    scaled_dot_product_attention, default scale 1/sqrt(128))."""
+    import torch
+    import torch.nn.functional as F
+
+    case = workloads.attention_case(21, 1, 9, dtype=np.float64, valid=[9])
+    case.positions[:] = 0
+    case.bias_u[:] = 0
+    case.bias_v[:] = 0
+    x = torch.from_numpy(case.qkv).reshape(9, 3, 8, 128).permute(1, 2, 0, 3)  # [3, H, T, D]
+    want = F.scaled_dot_product_attention(x[0], x[1], x[2]).permute(1, 0, 2).reshape(9, 1024).numpy()
+    np.testing.assert_allclose(_attend(oracle, case, "f64"), want, rtol=1e-11, atol=1e-13)
+
+
+def test_relative_shift_direction(oracle, workloads):
+    """Q = K = 0, u = 0 and v = beta on one channel of head 0 with R[p] = p on
+    that channel: score(q, k) = beta (T-1-q+k) / sqrt(128), so every query's
+    weights are softmax(beta k / sqrt(128)) over the keys (the q term
+    cancels). Reversing the relative index would flip the sign of k."""
+    T, beta = 6, 3.0
+    case = workloads.attention_case(22, 1, T, dtype=np.float64, valid=[T])
+    case.qkv[:, :2048] = 0
+    case.bias_u[:] = 0
+    case.bias_v[:] = 0
+    case.bias_v[0, 5] = beta
+    case.positions[:] = 0
+    case.positions[:, 5] = np.arange(2 * T - 1)
+    got = _attend(oracle, case, "f64")
+    w = np.exp(beta * np.arange(T) / np.sqrt(128.0))
+    w /= w.sum()
+    want_head0 = w @ case.qkv[:, 2048:2048 + 128]
+    for q in range(T):
+        np.testing.assert_allclose(got[q, :128], want_head0, rtol=1e-12)
+    # the other heads see uniform weights
+    np.testing.assert_allclose(got[0, 128:256], case.qkv[:, 2048 + 128:2048 + 256].mean(axis=0), rtol=1e-12)
+
+
+def test_relative_attention_one_key_and_empty_windows(oracle, workloads):
+    case = workloads.attention_case(23, 2, 5, dtype=np.float32, valid=[1, 0])
+    got = _attend(oracle, case, "f32-chain")
+    np.testing.assert_array_equal(got[0], case.qkv[0, 2048:])  # one key: probability exactly 1
+    assert np.all(got[1:5] == 0) and np.all(got[5:] == 0)
