@@ -536,84 +536,89 @@ int pko_relative_attention(int dtype, int mode, uint32_t batch, uint32_t frames,
       (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64) ||
       (mode != PKO_MODE_F32_CHAIN && mode != PKO_MODE_F64))
     return 1;
-  const uint64_t P = 2ull * frames - 1u;
+  const uint64_t T = frames, P = 2ull * frames - 1u;
+  const int f32 = mode == PKO_MODE_F32_CHAIN;
   const float scale32 = (float)(1.0 / sqrt(128.0));
   const double scale64 = 1.0 / sqrt(128.0);
-  float *s32 = (float *)malloc(sizeof(float) * frames);
-  double *s64 = (double *)malloc(sizeof(double) * frames);
-  if (!s32 || !s64) {
-    free(s32);
-    free(s64);
+  /* one (window, head) at a time, its operands decoded once */
+  double *q = (double *)malloc(sizeof(double) * T * HEAD), *k = (double *)malloc(sizeof(double) * T * HEAD);
+  double *v = (double *)malloc(sizeof(double) * T * HEAD), *r = (double *)malloc(sizeof(double) * P * HEAD);
+  double *s = (double *)malloc(sizeof(double) * T);
+  if (!q || !k || !v || !r || !s) {
+    free(q), free(k), free(v), free(r), free(s);
     return 1;
   }
   for (uint32_t b = 0; b < batch; ++b) {
-    const uint32_t live = valid[b] < frames ? valid[b] : frames;
+    const uint64_t live = valid[b] < frames ? valid[b] : frames;
     for (uint32_t h = 0; h < HEADS; ++h) {
-      for (uint32_t q = 0; q < frames; ++q) {
-        const uint64_t qrow = (uint64_t)b * frames + q;
-        if (q >= live) {
+      for (uint64_t t = 0; t < T; ++t)
+        for (uint32_t d = 0; d < HEAD; ++d) {
+          const uint64_t row = ((uint64_t)b * T + t) * 3u * HIDDEN + h * HEAD + d;
+          q[t * HEAD + d] = conv_in(dtype, qkv, row);
+          k[t * HEAD + d] = conv_in(dtype, qkv, row + HIDDEN);
+          v[t * HEAD + d] = conv_in(dtype, qkv, row + 2u * HIDDEN);
+        }
+      /* head-vector-position-vec4: [h][d / 4][p][d % 4] */
+      for (uint64_t p = 0; p < P; ++p)
+        for (uint32_t d = 0; d < HEAD; ++d)
+          r[p * HEAD + d] = conv_in(dtype, positions, (((uint64_t)h * 32u + d / 4u) * P + p) * 4u + d % 4u);
+      const float *u = bias_u + h * HEAD, *w = bias_v + h * HEAD;
+      for (uint64_t i = 0; i < T; ++i) {
+        const uint64_t qrow = (uint64_t)b * T + i;
+        if (i >= live) {
           for (uint32_t d = 0; d < HEAD; ++d) store_out(dtype, out, qrow * HIDDEN + h * HEAD + d, 0.0);
           continue;
         }
-        /* scores over the live keys */
-        for (uint32_t k = 0; k < live; ++k) {
-          const uint64_t krow = (uint64_t)b * frames + k;
-          const uint64_t rel = (uint64_t)frames - 1u - q + k;
-          float acc32 = 0.0f;
-          double acc64 = 0.0;
-          for (uint32_t d = 0; d < HEAD; ++d) {
-            const double qd = conv_in(dtype, qkv, qrow * 3u * HIDDEN + h * HEAD + d);
-            const double kd = conv_in(dtype, qkv, krow * 3u * HIDDEN + HIDDEN + h * HEAD + d);
-            const uint64_t pidx = (((uint64_t)h * 32u + d / 4u) * P + rel) * 4u + d % 4u;
-            const double rd = conv_in(dtype, positions, pidx);
-            const float u = bias_u[h * HEAD + d], v = bias_v[h * HEAD + d];
-            if (mode == PKO_MODE_F32_CHAIN) {
-              const float qu = (float)qd + u, qv = (float)qd + v;
-              acc32 = fmaf(qu, (float)kd, acc32);
-              acc32 = fmaf(qv, (float)rd, acc32);
-            } else {
-              acc64 += (qd + u) * kd + (qd + v) * rd;
+        const double *qi = q + i * HEAD;
+        /* scores of the live keys */
+        double maximum = -HUGE_VAL;
+        for (uint64_t j = 0; j < live; ++j) {
+          const double *kj = k + j * HEAD, *rj = r + (T - 1u - i + j) * HEAD;
+          if (f32) {
+            float acc = 0.0f;
+            for (uint32_t d = 0; d < HEAD; ++d) {
+              acc = fmaf((float)qi[d] + u[d], (float)kj[d], acc);
+              acc = fmaf((float)qi[d] + w[d], (float)rj[d], acc);
             }
+            s[j] = (double)(acc * scale32);
+          } else {
+            double acc = 0.0;
+            for (uint32_t d = 0; d < HEAD; ++d) acc += (qi[d] + u[d]) * kj[d] + (qi[d] + w[d]) * rj[d];
+            s[j] = acc * scale64;
           }
-          s32[k] = acc32 * scale32;
-          s64[k] = acc64 * scale64;
+          if (s[j] > maximum) maximum = s[j];
         }
-        /* softmax over k < live */
-        float max32 = -3.402823466e+38f;
-        double max64 = -HUGE_VAL;
-        for (uint32_t k = 0; k < live; ++k) {
-          if (s32[k] > max32) max32 = s32[k];
-          if (s64[k] > max64) max64 = s64[k];
-        }
-        float sum32 = 0.0f;
-        double sum64 = 0.0;
-        for (uint32_t k = 0; k < live; ++k) {
-          s32[k] = expf(s32[k] - max32);
-          s64[k] = exp(s64[k] - max64);
-          sum32 += s32[k];
-          sum64 += s64[k];
-        }
-        const float inv32 = 1.0f / sum32;
-        for (uint32_t k = 0; k < live; ++k) {
-          s32[k] = s32[k] * inv32;
-          s64[k] = s64[k] / sum64;
+        /* softmax */
+        if (f32) {
+          float sum = 0.0f;
+          for (uint64_t j = 0; j < live; ++j) {
+            const float e = expf((float)s[j] - (float)maximum);
+            s[j] = e;
+            sum += e;
+          }
+          const float inverse = 1.0f / sum;
+          for (uint64_t j = 0; j < live; ++j) s[j] = (double)((float)s[j] * inverse);
+        } else {
+          double sum = 0.0;
+          for (uint64_t j = 0; j < live; ++j) sum += (s[j] = exp(s[j] - maximum));
+          for (uint64_t j = 0; j < live; ++j) s[j] /= sum;
         }
         /* context */
         for (uint32_t d = 0; d < HEAD; ++d) {
-          float o32 = 0.0f;
-          double o64 = 0.0;
-          for (uint32_t k = 0; k < live; ++k) {
-            const uint64_t krow = (uint64_t)b * frames + k;
-            const double vd = conv_in(dtype, qkv, krow * 3u * HIDDEN + 2u * HIDDEN + h * HEAD + d);
-            o32 = fmaf(s32[k], (float)vd, o32);
-            o64 += s64[k] * vd;
+          double o;
+          if (f32) {
+            float acc = 0.0f;
+            for (uint64_t j = 0; j < live; ++j) acc = fmaf((float)s[j], (float)v[j * HEAD + d], acc);
+            o = acc;
+          } else {
+            o = 0.0;
+            for (uint64_t j = 0; j < live; ++j) o += s[j] * v[j * HEAD + d];
           }
-          store_out(dtype, out, qrow * HIDDEN + h * HEAD + d, mode == PKO_MODE_F32_CHAIN ? (double)o32 : o64);
+          store_out(dtype, out, qrow * HIDDEN + h * HEAD + d, o);
         }
       }
     }
   }
-  free(s32);
-  free(s64);
+  free(q), free(k), free(v), free(r), free(s);
   return 0;
 }

@@ -33,7 +33,8 @@ HIP_FLAGS = [
     "-I", INCLUDE, "-I", CSRC,
 ]
 SOURCES = [
-    "pk_abi.cpp", "pk_conv_abi.cpp", "pk_codes.hip", "pk_conv.hip", "pk_gemm_f16.hip", "pk_gemm_f16k.hip",
+    "pk_abi.cpp", "pk_conv_abi.cpp", "pk_attention_abi.cpp", "pk_codes.hip", "pk_conv.hip", "pk_attention.hip",
+    "pk_gemm_f16.hip", "pk_gemm_f16k.hip",
     "pk_gemm_f16s.hip", "pk_gemm_f32.hip",
 ]
 NODE_INCLUDE = "/usr/include/node"

@@ -1,0 +1,402 @@
+// pk_attention.hip - Transformer-XL relative-position self-attention for
+// gfx950 (reference: src/webgpu/kernels/attention.ts, shader :418-727,
+// dispatch :51-316), 8 heads of 128 channels.
+//
+// For window b, head h and a query q below valid = min(valid[b], T):
+//   score(q, k) = ((q + u)·k + (q + v)·R[T-1-q+k]) / sqrt(128),
+//   out(q)      = softmax_k(score) · V over the keys k < valid,
+// rows valid <= q < T are zero. R is the projected relative-position table
+// (row p = relative distance T-1-p), in the reference's
+// "head-vector-position-vec4" order [8][32][2T-1][4] or, with the row-major
+// flag, as [2T-1, 1024] straight from a palette GEMM.
+//
+// f16 kernel (flash style, MFMA): a workgroup owns one (window, head,
+// 32-query tile) and KSPLIT wavefronts, which take the 32-key tiles
+// round robin and keep their own online-softmax state; the states meet in
+// LDS at the end. Per key tile a wavefront computes, with
+// v_mfma_f32_32x32x16_f16 (f32 accumulation):
+//   * S^T = K · (Q+u)^T: keys are rows, so a lane holds 16 keys of one
+//     query and a query's softmax needs one cross-half exchange only;
+//   * the relative term over the 64-position window the tile needs,
+//     W^T = R[p_lo .. p_lo+63] · (Q+v)^T with p_lo = T-1-q0-31+k0, written
+//     to LDS and read back along the diagonal, score(q0+j, k0+i) taking
+//     W^T[31 - j + i][j];
+//   * O^T += V^T · P^T: the V tile goes to LDS transposed with key index
+//     bits 2 and 3 swapped, which makes the probabilities a lane already
+//     holds (keys 8a + 4h + b) exactly its MFMA operand, and the V^T rows one
+//     ds_read_b128 each.
+// (Q+u) and (Q+v) are formed in f32 and rounded to f16 once per workgroup;
+// probabilities go to f16 for the PV product; everything else stays in f32.
+//
+// f32 kernel: a workgroup per (window, head, query) in the reference's own
+// arithmetic (fma chains in channel order, max / exp / sum, fma over keys).
+#include "pk_internal.h"
+
+namespace pk {
+namespace {
+
+constexpr int kHeads = 8;
+constexpr int kHead = 128;
+constexpr int kHidden = kHeads * kHead;
+constexpr int kQkvRow = 3 * kHidden;
+constexpr int kTile = 32;          // queries per workgroup and keys per tile
+constexpr int kVtStride = 40;      // halves per transposed V row (80 bytes: conflict-free b128 reads)
+constexpr int kOtStride = 129;     // floats per merged output row
+constexpr int kWaveLds = 64 * kTile * 4 + kHead * kVtStride * 2;  // diagonal window + V^T
+static_assert(kTile * kOtStride * 4 + 2 * kTile * 4 <= kWaveLds, "merge state fits a wavefront's region");
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ half8 load8(const _Float16* p) { return *reinterpret_cast<const half8*>(p); }
+
+// 8 channels d0 .. d0+7 (d0 % 8 == 0) of relative position p of one head.
+template <bool ROW_MAJOR>
+__device__ __forceinline__ half8 load_position(const _Float16* positions, uint32_t rows, int head, int p, int d0) {
+  if constexpr (ROW_MAJOR) {
+    return load8(positions + (uint64_t)p * kHidden + head * kHead + d0);
+  } else {
+    const int v = d0 / 4;  // two vec4 planes of [8][32][rows][4]
+    const half4 lo = *reinterpret_cast<const half4*>(positions + (((uint64_t)head * 32 + v) * rows + p) * 4);
+    const half4 hi = *reinterpret_cast<const half4*>(positions + (((uint64_t)head * 32 + v + 1) * rows + p) * 4);
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+}
+
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+template <int KSPLIT, bool ROW_MAJOR>
+__global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[KSPLIT * kWaveLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane & 31;
+  const int hh = lane >> 5;
+
+  const uint32_t qt = blockIdx.x % args.query_tiles;
+  const uint32_t bh = blockIdx.x / args.query_tiles;
+  const int head = (int)(bh % kHeads);
+  const uint32_t b = bh / kHeads;
+  const int T = (int)args.frames;
+  const int live = (int)min(args.frames, args.valid_lengths[b]);
+  const int q0 = (int)qt * kTile;
+  const _Float16* qkv = static_cast<const _Float16*>(args.qkv) + (uint64_t)b * T * kQkvRow + head * kHead;
+  _Float16* out = static_cast<_Float16*>(args.output) + (uint64_t)b * T * kHidden + head * kHead;
+
+  if (q0 >= live) {
+    // Every query of the tile is past the valid length: zero rows.
+    for (int c = threadIdx.x; c < kTile * (kHead / 8); c += 64 * KSPLIT) {
+      const int q = q0 + c / (kHead / 8);
+      if (q < T) *reinterpret_cast<half8*>(out + (uint64_t)q * kHidden + (c % (kHead / 8)) * 8) = half8{};
+    }
+    return;
+  }
+
+  // (Q+u)^T and (Q+v)^T operands of query q0 + j: channels 16s + 8hh + 0..7.
+  half8 qu[8], qv[8];
+  {
+    const _Float16* qrow = qkv + (uint64_t)min(q0 + j, T - 1) * kQkvRow;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int d0 = 16 * s + 8 * hh;
+      const half8 x = load8(qrow + d0);
+      const float4 u0 = *reinterpret_cast<const float4*>(args.bias_u + head * kHead + d0);
+      const float4 u1 = *reinterpret_cast<const float4*>(args.bias_u + head * kHead + d0 + 4);
+      const float4 v0 = *reinterpret_cast<const float4*>(args.bias_v + head * kHead + d0);
+      const float4 v1 = *reinterpret_cast<const float4*>(args.bias_v + head * kHead + d0 + 4);
+      const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+      const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        qu[s][t] = (_Float16)((float)x[t] + uu[t]);
+        qv[s][t] = (_Float16)((float)x[t] + vv[t]);
+      }
+    }
+  }
+
+  float* window = reinterpret_cast<float*>(smem + wave * kWaveLds);                        // [64][32]
+  _Float16* vt = reinterpret_cast<_Float16*>(smem + wave * kWaveLds + 64 * kTile * 4);     // [128][40]
+  const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
+
+  float m = -INFINITY, l = 0.0f;
+  floatx16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+
+  const int tiles = (live + kTile - 1) / kTile;
+  for (int kt = wave; kt < tiles; kt += KSPLIT) {
+    const int k0 = kt * kTile;
+    const int p_lo = T - 1 - q0 - (kTile - 1) + k0;
+    const int pmax = (int)args.position_rows - 1;
+    // S^T = K (Q+u)^T and W^T = R[p_lo ..] (Q+v)^T.
+    floatx16 ac, w0, w1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ac[r] = w0[r] = w1[r] = 0.0f;
+    const _Float16* krow = qkv + (uint64_t)min(k0 + j, T - 1) * kQkvRow + kHidden;
+    const int pa = min(max(p_lo + j, 0), pmax), pb = min(max(p_lo + kTile + j, 0), pmax);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int d0 = 16 * s + 8 * hh;
+      const half8 kv = load8(krow + d0);
+      const half8 ra = load_position<ROW_MAJOR>(static_cast<const _Float16*>(args.positions), args.position_rows,
+                                                head, pa, d0);
+      const half8 rb = load_position<ROW_MAJOR>(static_cast<const _Float16*>(args.positions), args.position_rows,
+                                                head, pb, d0);
+      ac = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qu[s], ac, 0, 0, 0);
+      w0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra, qv[s], w0, 0, 0, 0);
+      w1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(rb, qv[s], w1, 0, 0, 0);
+    }
+    // V tile -> LDS, transposed: vt[d][swap23(key)].
+    {
+      const _Float16* vrow = qkv + (uint64_t)min(k0 + j, T - 1) * kQkvRow + 2 * kHidden;
+      const int slot = (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int d0 = 16 * c + 8 * hh;
+        const half8 x = load8(vrow + d0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) vt[(d0 + t) * kVtStride + slot] = x[t];
+      }
+    }
+    // Window rows c = 32 blk + 8 (r/4) + 4 hh + r%4, column j.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 8 * (r / 4) + 4 * hh + (r % 4);
+      window[c * kTile + j] = w0[r];
+      window[(kTile + c) * kTile + j] = w1[r];
+    }
+    // LDS operations of one wavefront complete in order; the fence keeps the
+    // compiler from moving the reads above the writes.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // Scores of keys k0 + i, i = 8 (r/4) + 4 hh + r%4, for query q0 + j.
+    float sc[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r / 4) + 4 * hh + (r % 4);
+      const float rel = window[(kTile - 1 - j + i) * kTile + j];
+      sc[r] = k0 + i < live ? (ac[r] + rel) * scale : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp(m - m_new);
+    float rs = 0.0f;
+    half8 pb8[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp(sc[r] - m_new);
+      rs += p;
+      pb8[r / 8][r % 8] = (_Float16)p;
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+    m = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const half8 va = load8(vt + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb8[s], o[db], 0, 0, 0);
+      }
+    }
+    // The next tile rewrites this wavefront's window and V^T after these reads.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+
+  // Merge the KSPLIT states; wavefront w then finishes channel blocks
+  // [4w/KSPLIT, 4(w+1)/KSPLIT).
+  constexpr int DB_PER = 4 / KSPLIT;
+  float res[DB_PER][16];
+  float* ot = reinterpret_cast<float*>(smem + wave * kWaveLds);       // [32][129]
+  float* ml = ot + kTile * kOtStride;                                  // m[32], l[32]
+  if constexpr (KSPLIT == 1) {
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) res[db][r] = o[db][r] * inv;
+  } else {
+    __syncthreads();
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ot[j * kOtStride + 32 * db + 8 * (r / 4) + 4 * hh + (r % 4)] = o[db][r];
+    if (hh == 0) {
+      ml[j] = m;
+      ml[kTile + j] = l;
+    }
+    __syncthreads();
+    float mw[KSPLIT], big = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < KSPLIT; ++w) {
+      mw[w] = reinterpret_cast<const float*>(smem + w * kWaveLds)[kTile * kOtStride + j];
+      big = fmaxf(big, mw[w]);
+    }
+    float f[KSPLIT], total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KSPLIT; ++w) {
+      f[w] = fast_exp(mw[w] - big);
+      total += f[w] * reinterpret_cast<const float*>(smem + w * kWaveLds)[kTile * kOtStride + kTile + j];
+    }
+    const float inv = 1.0f / total;
+#pragma unroll
+    for (int dl = 0; dl < DB_PER; ++dl) {
+      const int db = wave * DB_PER + dl;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * db + 8 * (r / 4) + 4 * hh + (r % 4);
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KSPLIT; ++w)
+          acc += f[w] * reinterpret_cast<const float*>(smem + w * kWaveLds)[j * kOtStride + d];
+        res[dl][r] = acc * inv;
+      }
+    }
+  }
+  const int q = q0 + j;
+  if (q < T) {
+    const bool keep = q < live;
+#pragma unroll
+    for (int dl = 0; dl < DB_PER; ++dl) {
+      const int db = (KSPLIT == 1 ? 0 : wave * DB_PER) + dl;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * hh;
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = keep ? (_Float16)res[dl][4 * g + e] : (_Float16)0.0f;
+        *reinterpret_cast<half4*>(out + (uint64_t)q * kHidden + d) = h;
+      }
+    }
+  }
+}
+
+// The reference's arithmetic in f32: one workgroup of 256 threads per
+// (window, head, query); scores of all keys live in LDS (T <= kMaxFrames).
+template <bool ROW_MAJOR>
+__global__ __launch_bounds__(256) void rel_attention_f32_kernel(AttnArgs args) {
+  __shared__ float qu[kHead], qv[kHead];
+  __shared__ float scores[kAttentionMaxFrames];
+  __shared__ float red[8];
+  const int tid = threadIdx.x;
+  const int T = (int)args.frames;
+  const int q = (int)(blockIdx.x % args.frames);
+  const uint32_t bh = blockIdx.x / args.frames;
+  const int head = (int)(bh % kHeads);
+  const uint32_t b = bh / kHeads;
+  const int live = (int)min(args.frames, args.valid_lengths[b]);
+  const float* qkv = static_cast<const float*>(args.qkv) + (uint64_t)b * T * kQkvRow + head * kHead;
+  float* out = static_cast<float*>(args.output) + ((uint64_t)b * T + q) * kHidden + head * kHead;
+  const float* positions = static_cast<const float*>(args.positions);
+  if (q >= live) {
+    if (tid < kHead) out[tid] = 0.0f;
+    return;
+  }
+  if (tid < kHead) {
+    const float x = qkv[(uint64_t)q * kQkvRow + tid];
+    qu[tid] = x + args.bias_u[head * kHead + tid];
+    qv[tid] = x + args.bias_v[head * kHead + tid];
+  }
+  __syncthreads();
+  float local_max = -3.402823466e+38f;
+  for (int k = tid; k < live; k += 256) {
+    const float* key = qkv + (uint64_t)k * kQkvRow + kHidden;
+    const int rel = T - 1 - q + k;
+    float acc = 0.0f;
+    for (int d = 0; d < kHead; ++d) {
+      const float r = ROW_MAJOR ? positions[(uint64_t)rel * kHidden + head * kHead + d]
+                                : positions[(((uint64_t)head * 32 + d / 4) * args.position_rows + rel) * 4 + d % 4];
+      acc = __builtin_fmaf(qu[d], key[d], acc);
+      acc = __builtin_fmaf(qv[d], r, acc);
+    }
+    acc *= 0.08838834764831845f;
+    scores[k] = acc;
+    local_max = fmaxf(local_max, acc);
+  }
+  // workgroup max, then sum of exp
+  for (int off = 32; off > 0; off >>= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = local_max;
+  __syncthreads();
+  const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float local_sum = 0.0f;
+  for (int k = tid; k < live; k += 256) {
+    const float e = expf(scores[k] - maximum);
+    scores[k] = e;
+    local_sum += e;
+  }
+  for (int off = 32; off > 0; off >>= 1) local_sum += __shfl_xor(local_sum, off, 64);
+  __syncthreads();
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = local_sum;
+  __syncthreads();
+  const float inverse = 1.0f / (red[4] + red[5] + red[6] + red[7]);
+  if (tid < kHead) {
+    float acc = 0.0f;
+    for (int k = 0; k < live; ++k)
+      acc = __builtin_fmaf(scores[k] * inverse, qkv[(uint64_t)k * kQkvRow + 2 * kHidden + tid], acc);
+    out[tid] = acc;
+  }
+}
+
+struct AttnVariant {
+  const char* name;
+  int waves;
+  void (*packed)(AttnArgs);
+  void (*row_major)(AttnArgs);
+};
+
+#define PK_ATTN_VARIANT(K)                                                                                 \
+  AttnVariant {                                                                                            \
+    "pk_rel_attention_f16_q32_w" #K, K, rel_attention_f16_kernel<K, false>, rel_attention_f16_kernel<K, true> \
+  }
+
+const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1)};
+const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, rel_attention_f32_kernel<false>,
+                                 rel_attention_f32_kernel<true>};
+
+}  // namespace
+
+int attention_variant_count(bool f16) {
+  return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0])) : 1;
+}
+
+AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t batch) {
+  AttnGeometry g;
+  if (f16) {
+    const AttnVariant& v = kF16Variants[variant];
+    g.name = v.name;
+    g.query_tiles = (frames + kTile - 1) / kTile;
+    g.grid = batch * kHeads * g.query_tiles;
+    g.block_threads = 64 * v.waves;
+    g.lds_bytes = v.waves * kWaveLds;
+  } else {
+    g.name = kF32Variant.name;
+    g.query_tiles = frames;
+    g.grid = batch * kHeads * frames;
+    g.block_threads = 256;
+    g.lds_bytes = (2 * kHead + kAttentionMaxFrames + 8) * 4;
+  }
+  return g;
+}
+
+hipError_t launch_attention(bool f16, int variant, const AttnArgs& base, uint32_t batch, hipStream_t stream,
+                            hipEvent_t start, hipEvent_t stop) {
+  const AttnGeometry g = attention_geometry(f16, variant, base.frames, batch);
+  if (g.grid == 0) return hipSuccess;
+  AttnArgs args = base;
+  args.query_tiles = g.query_tiles;
+  const AttnVariant& v = f16 ? kF16Variants[variant] : kF32Variant;
+  void (*kernel)(AttnArgs) = base.positions_row_major ? v.row_major : v.packed;
+  if (start || stop)
+    hipExtLaunchKernelGGL(kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, start, stop, 0, args);
+  else
+    hipLaunchKernelGGL(kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, args);
+  return hipGetLastError();
+}
+
+}  // namespace pk

@@ -192,6 +192,34 @@ struct ConvGeometry {
   uint32_t block_threads;
 };
 
+// Relative-position attention (pk_attention.hip), 8 heads x 128 channels.
+constexpr uint32_t kAttentionMaxFrames = 4096;
+struct AttnArgs {
+  const void* qkv;                // [batch * frames, 3072]: Q, K, V blocks of 1024
+  const void* positions;          // [8][32][2T-1][4], or [2T-1, 1024] with positions_row_major
+  const float* bias_u;            // [8, 128]
+  const float* bias_v;            // [8, 128]
+  const uint32_t* valid_lengths;  // [batch]
+  void* output;                   // [batch * frames, 1024]
+  uint32_t frames;
+  uint32_t position_rows;         // 2 * frames - 1
+  int positions_row_major;
+  uint32_t query_tiles;           // set by the launcher
+};
+
+struct AttnGeometry {
+  const char* name;
+  uint32_t query_tiles;
+  uint32_t grid;
+  uint32_t block_threads;
+  uint32_t lds_bytes;
+};
+
+int attention_variant_count(bool f16);
+AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t batch);
+hipError_t launch_attention(bool f16, int variant, const AttnArgs& args, uint32_t batch, hipStream_t stream,
+                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+
 int conv_variant_count(bool f16);
 ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
                            bool input_glu = false);

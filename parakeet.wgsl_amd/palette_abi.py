@@ -1,4 +1,4 @@
-"""ctypes binding of libpk_palette.so (include/pk_palette.h, include/pk_conv.h).
+"""ctypes binding of libpk_palette.so (include/pk_palette.h, pk_conv.h, pk_attention.h).
 
 A thin Python view of the C ABI, used by the tests and the benchmark. It
 raises PaletteError (or PaletteRangeError, mirroring the reference's
@@ -21,6 +21,7 @@ ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
 REQUIRE_PRODUCTION_SIGNATURE = 0x1
 GEMM_GLU = 0x2
 CONV_INPUT_GLU = 0x1
+ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 EXPAND_LAYOUT = {"row-major": 0, "tile-major": 1}
 
 
@@ -168,6 +169,40 @@ class ConvPlanInfo(ctypes.Structure):
     ]
 
 
+class AttentionDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("frames", ctypes.c_uint32),
+        ("qkv", ctypes.c_void_p),
+        ("qkv_bytes", ctypes.c_uint64),
+        ("projected_positions", ctypes.c_void_p),
+        ("projected_positions_bytes", ctypes.c_uint64),
+        ("bias_u", ctypes.c_void_p),
+        ("bias_u_bytes", ctypes.c_uint64),
+        ("bias_v", ctypes.c_void_p),
+        ("bias_v_bytes", ctypes.c_uint64),
+        ("valid_lengths", ctypes.c_void_p),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+    ]
+
+
+class AttentionPlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("grid", ctypes.c_uint32 * 3),
+        ("block_threads", ctypes.c_uint32),
+        ("lds_bytes", ctypes.c_uint32),
+        ("query_tiles", ctypes.c_uint32),
+        ("algorithmic_bytes", ctypes.c_uint64),
+        ("kernel", ctypes.c_char * 64),
+    ]
+
+
 # Every function the headers declare: name -> (restype, argtypes).
 _VP = ctypes.c_void_p
 _PPV = ctypes.POINTER(ctypes.c_void_p)
@@ -219,6 +254,15 @@ SIGNATURES = {
     "pk_conv_release": (ctypes.c_int, [_VP]),
     "pk_conv_variant_count": (ctypes.c_int, [ctypes.c_int]),
     "pk_conv_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
+    "pk_attention_validate": (ctypes.c_int, [ctypes.POINTER(AttentionDesc)]),
+    "pk_attention_create": (ctypes.c_int, [_VP, ctypes.POINTER(AttentionDesc), _PPV]),
+    "pk_attention_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_attention_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_attention_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(AttentionPlanInfo)]),
+    "pk_attention_destroy": (ctypes.c_int, [_VP]),
+    "pk_attention_release": (ctypes.c_int, [_VP]),
+    "pk_attention_variant_count": (ctypes.c_int, [ctypes.c_int]),
+    "pk_attention_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
 }
 
 _lib = None
@@ -515,3 +559,54 @@ class ConformerConvOp:
 
 def conv_variant_count(precision: str) -> int:
     return int(load().pk_conv_variant_count(PRECISION[precision]))
+
+
+def attention_desc(*, qkv, projected_positions, bias_u, bias_v, valid_lengths, output, batch_size: int, frames: int,
+                   precision: str | None = None, label: str = "relative-attention",
+                   positions_row_major: bool = False) -> AttentionDesc:
+    """A pk_attention_desc over DeviceArrays (or any objects with ptr/nbytes)."""
+    if precision is None:
+        precision = "f16" if qkv.dtype == np.float16 else "f32"
+    return AttentionDesc(ctypes.sizeof(AttentionDesc), ATTENTION_POSITIONS_ROW_MAJOR if positions_row_major else 0,
+                         label.encode(), PRECISION[precision], batch_size, frames, *_slice(qkv),
+                         *_slice(projected_positions), *_slice(bias_u), *_slice(bias_v), *_slice(valid_lengths),
+                         *_slice(output))
+
+
+class RelativeAttentionOp:
+    """One relative-position attention dispatch
+    (RelativeAttentionKernel.createDispatch, attention.ts:219-314)."""
+
+    def __init__(self, ctx: Context, **descriptor):
+        self.desc = attention_desc(**descriptor)
+        handle = ctypes.c_void_p()
+        check(load().pk_attention_create(ctx.handle, ctypes.byref(self.desc), ctypes.byref(handle)))
+        self.handle = handle.value
+        self.ctx = ctx
+
+    def enqueue(self, active_batch: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_attention_enqueue(self.handle, active_batch, stream))
+        else:
+            check(load().pk_attention_enqueue_timed(self.handle, active_batch, stream,
+                                                    start.handle if start else None, end.handle if end else None))
+
+    def plan(self, active_batch: int = 0) -> AttentionPlanInfo:
+        info = AttentionPlanInfo()
+        check(load().pk_attention_plan(self.handle, active_batch, ctypes.byref(info)))
+        return info
+
+    def set_variant(self, variant: int) -> None:
+        check(load().pk_attention_set_variant(self.handle, variant))
+
+    def destroy(self) -> None:
+        check(load().pk_attention_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_attention_release(self.handle))
+            self.handle = None
+
+
+def attention_variant_count(precision: str) -> int:
+    return int(load().pk_attention_variant_count(PRECISION[precision]))

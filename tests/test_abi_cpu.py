@@ -56,9 +56,10 @@ def test_struct_layouts_match_the_c_compiler(abi, tmp_path):
     structs = {"pk_weight_desc": abi.WeightDesc, "pk_gemm_desc": abi.GemmDesc,
                "pk_expand_desc": abi.ExpandDesc, "pk_gemm_plan_info": abi.PlanInfo,
                "pk_device_info": abi.DeviceInfo, "pk_conv_desc": abi.ConvDesc,
-               "pk_conv_plan_info": abi.ConvPlanInfo}
+               "pk_conv_plan_info": abi.ConvPlanInfo, "pk_attention_desc": abi.AttentionDesc,
+               "pk_attention_plan_info": abi.AttentionPlanInfo}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', '#include "pk_conv.h"',
-             "int main(void) {"]
+             '#include "pk_attention.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
         for field, _ in cls._fields_:
@@ -245,3 +246,77 @@ def test_conv_null_handles(abi):
     assert lib.pk_conv_destroy(None) == abi.OK
     assert lib.pk_conv_release(None) == abi.OK
     assert abi.conv_variant_count("f16") >= 1 and abi.conv_variant_count("f32") >= 1
+
+
+# ---------------------------------------------- relative-position attention
+
+
+def _attention_fakes(batch=2, frames=188, elem=2):
+    rows, p = batch * frames, 2 * frames - 1
+    dtype = np.float16 if elem == 2 else np.float32
+    return dict(
+        qkv=_Fake(0x10000000, rows * 3072 * elem, dtype),
+        projected_positions=_Fake(0x20000000, p * 1024 * elem, dtype),
+        bias_u=_Fake(0x30000000, 4096, np.float32),
+        bias_v=_Fake(0x30100000, 4096, np.float32),
+        valid_lengths=_Fake(0x40000000, batch * 4, np.uint32),
+        output=_Fake(0x50000000, rows * 1024 * elem, dtype),
+        batch_size=batch, frames=frames, label="layer0-relative-attention")
+
+
+def _validate_attention(abi, **kw):
+    desc = abi.attention_desc(**kw)
+    abi.check(abi.load().pk_attention_validate(ctypes.byref(desc)))
+
+
+def test_attention_validate_accepts_reference_and_long_windows(abi):
+    _validate_attention(abi, **_attention_fakes())
+    _validate_attention(abi, **_attention_fakes(elem=4))
+    _validate_attention(abi, **_attention_fakes(batch=4, frames=750))
+
+
+@pytest.mark.parametrize("batch,frames", [(0, 188), (2, 0), (1, 4097)])
+def test_attention_shape_is_a_range_error(abi, batch, frames):
+    """createDispatch's shape check (attention.ts:222-229)."""
+    kw = _attention_fakes()
+    kw["batch_size"], kw["frames"] = batch, frames
+    with pytest.raises(abi.PaletteRangeError, match="Unsupported attention shape for layer0-relative-attention"):
+        _validate_attention(abi, **kw)
+
+
+@pytest.mark.parametrize("field,message", [
+    ("qkv", "layer0-relative-attention QKV needs 2310144 bytes; arena slice has 2310143"),
+    ("output", "layer0-relative-attention output needs 770048 bytes; arena slice has 770047"),
+    ("valid_lengths", "layer0-relative-attention valid lengths needs 8 bytes; arena slice has 7"),
+])
+def test_attention_arena_capacity_messages(abi, field, message):
+    kw = _attention_fakes()
+    kw[field] = _Fake(kw[field].ptr, kw[field].nbytes - 1, kw[field].dtype)
+    with pytest.raises(abi.PaletteRangeError, match=re.escape(message)):
+        _validate_attention(abi, **kw)
+
+
+def test_attention_tensor_messages(abi):
+    """requireProjectedPositions / requireAttentionBias (attention.ts:323-370)."""
+    kw = _attention_fakes()
+    kw["projected_positions"] = _Fake(kw["projected_positions"].ptr, 100)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "Projected positions must be float16 head-vector-position-vec4, logical [375,1024], "
+            "storage [8,32,375,4]")):
+        _validate_attention(abi, **kw)
+    kw = _attention_fakes()
+    kw["bias_v"] = _Fake(kw["bias_v"].ptr, 2048)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "layer0-relative-attention bias V must be float32 head-by-channel logical/storage [8,128]")):
+        _validate_attention(abi, **kw)
+    kw = _attention_fakes()
+    kw["output"] = _Fake(kw["qkv"].ptr + 1024, kw["output"].nbytes)
+    with pytest.raises(abi.PaletteError, match="must not overlap"):
+        _validate_attention(abi, **kw)
+
+
+def test_attention_null_handles(abi):
+    lib = abi.load()
+    assert lib.pk_attention_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_attention_destroy(None) == abi.OK
+    assert abi.attention_variant_count("f16") == 3 and abi.attention_variant_count("f32") == 1

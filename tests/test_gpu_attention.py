@@ -1,0 +1,137 @@
+"""Parity of the relative-position attention (attention.ts:418-727) against
+the CPU oracle, through the C ABI.
+
+Bars: the f16 kernel within 2e-3 norm-wise of the oracle's reference f32
+arithmetic (rounded to f16) and of the fp64 truth — the MFMA path rounds
+(q + u), (q + v) and the probabilities to f16 once, which moves results by a
+few 1e-4; rows at or past the valid length exactly zero; the f32 kernel
+within 1e-4 (norm- and max-wise) of the reference f32 arithmetic.
+"""
+import numpy as np
+import pytest
+
+from test_gpu_parity import F16_TOL_TRUTH, F32_TOL, Scope
+
+pytestmark = pytest.mark.gpu
+
+F16_ATTENTION_TOL = 2e-3
+
+
+@pytest.fixture
+def scope(ctx):
+    s = Scope(ctx)
+    yield s
+    s.close()
+
+
+def run_attention(abi, ctx, scope, case, *, row_major=False, variant=None, active_batch=0, sentinel=None):
+    dtype = case.qkv.dtype
+    out = scope.put(np.full((case.batch * case.frames, 1024), sentinel if sentinel is not None else 0, dtype))
+    positions = case.positions if row_major else case.packed_positions
+    op = abi.RelativeAttentionOp(
+        ctx, qkv=scope.put(case.qkv), projected_positions=scope.put(positions), bias_u=scope.put(case.bias_u),
+        bias_v=scope.put(case.bias_v), valid_lengths=scope.put(case.valid), output=out, batch_size=case.batch,
+        frames=case.frames, positions_row_major=row_major)
+    try:
+        if variant is not None:
+            op.set_variant(variant)
+        op.enqueue(active_batch)
+        ctx.synchronize()
+        return out.download(), op.plan().kernel.decode()
+    finally:
+        op.release()
+
+
+def oracle_attention(oracle, case, mode="f32-chain", batch=None):
+    batch = case.batch if batch is None else batch
+    rows = batch * case.frames
+    return oracle.relative_attention(case.qkv[:rows], case.packed_positions, case.bias_u, case.bias_v,
+                                     case.valid[:batch], batch=batch, frames=case.frames, mode=mode)
+
+
+def assert_attention_parity(oracle, got, case, batch=None):
+    batch = case.batch if batch is None else batch
+    want = oracle_attention(oracle, case, batch=batch)
+    if got.dtype == np.float32:
+        norm, worst = oracle.relative_errors(got, want)
+        assert norm <= F32_TOL and worst <= F32_TOL, (norm, worst)
+    else:
+        norm, _ = oracle.relative_errors(got, want)
+        assert norm <= F16_ATTENTION_TOL, norm
+        truth = oracle_attention(oracle, case, mode="f64", batch=batch)
+        norm, _ = oracle.relative_errors(got, truth)
+        assert norm <= F16_TOL_TRUTH, norm
+    for b in range(batch):
+        live = min(int(case.valid[b]), case.frames)
+        assert np.all(got[b * case.frames + live:(b + 1) * case.frames] == 0)
+
+
+SHAPES = [
+    # batch, frames, valid lengths (None: uniform in [T/2, T])
+    (4, 188, None),
+    (1, 750, [640]),
+    (3, 23, [23, 0, 40]),   # full, empty, longer than the window
+    (1, 1, [1]),
+    (2, 33, [33, 32]),      # one key past a tile edge
+    (2, 64, [64, 1]),
+]
+
+
+@pytest.mark.parametrize("row_major", [False, True])
+@pytest.mark.parametrize("batch,frames,valid", SHAPES)
+def test_f16_attention_matches_oracle(abi, ctx, scope, oracle, workloads, batch, frames, valid, row_major):
+    case = workloads.attention_case(40 + frames, batch, frames, valid=valid)
+    print(f"attention f16 B={batch} T={frames} row_major={row_major}", flush=True)
+    got, _ = run_attention(abi, ctx, scope, case, row_major=row_major)
+    assert_attention_parity(oracle, got, case)
+
+
+def test_position_layouts_give_identical_results(abi, ctx, scope, workloads):
+    case = workloads.attention_case(50, 2, 100, valid=[100, 77])
+    packed, _ = run_attention(abi, ctx, scope, case)
+    rows, _ = run_attention(abi, ctx, scope, case, row_major=True)
+    np.testing.assert_array_equal(packed.view(np.uint16), rows.view(np.uint16))
+
+
+def test_every_f16_attention_variant_matches(abi, ctx, scope, oracle, workloads):
+    case = workloads.attention_case(51, 2, 150, valid=[150, 70])
+    for variant in range(abi.attention_variant_count("f16")):
+        got, kernel = run_attention(abi, ctx, scope, case, variant=variant)
+        print(f"attention variant {variant} {kernel}", flush=True)
+        assert_attention_parity(oracle, got, case)
+
+
+@pytest.mark.parametrize("batch,frames,valid", [(2, 188, [188, 100]), (2, 23, [0, 40]), (1, 200, [200])])
+def test_f32_attention_matches_oracle(abi, ctx, scope, oracle, workloads, batch, frames, valid):
+    case = workloads.attention_case(52 + frames, batch, frames, dtype=np.float32, valid=valid)
+    for row_major in (False, True):
+        got, kernel = run_attention(abi, ctx, scope, case, row_major=row_major)
+        assert kernel == "pk_rel_attention_f32"
+        assert_attention_parity(oracle, got, case)
+
+
+def test_attention_active_batch_prefix(abi, ctx, scope, oracle, workloads):
+    """encode(shape.batchSize = 2) of a 4-window dispatch (attention.ts:67-90)."""
+    case = workloads.attention_case(53, 4, 60)
+    sentinel = np.float16(555.0)
+    got, _ = run_attention(abi, ctx, scope, case, active_batch=2, sentinel=sentinel)
+    assert_attention_parity(oracle, got[:120], case, batch=2)
+    assert np.all(got[120:] == sentinel)
+
+
+def test_attention_dispatch_errors(abi, ctx, scope, workloads):
+    case = workloads.attention_case(54, 2, 20)
+    out = scope.empty((40, 1024), np.float16)
+    op = abi.RelativeAttentionOp(
+        ctx, qkv=scope.put(case.qkv), projected_positions=scope.put(case.packed_positions),
+        bias_u=scope.put(case.bias_u), bias_v=scope.put(case.bias_v), valid_lengths=scope.put(case.valid),
+        output=out, batch_size=2, frames=20, label="layer5-relative-attention")
+    try:
+        with pytest.raises(abi.PaletteRangeError, match=r"layer5-relative-attention active batch must be in \[1, 2\]"):
+            op.enqueue(3)
+        op.destroy()
+        op.destroy()
+        with pytest.raises(abi.PaletteDestroyedError, match="layer5-relative-attention was destroyed"):
+            op.enqueue()
+    finally:
+        op.release()
