@@ -19,6 +19,11 @@ Other workloads (for profiling; same JSON shape):
                     GEMMs, the step time includes the fused conv tail
   conv-module-fused the same module with the GLU moved into PW1's epilogue
                     (PW1 writes [rows, 1024] GLU; the tail reads it)
+  rel-pos-mha       relative-position MHA block, fp16, 4 windows x --frames (188
+                    or 750) x 1024: QKV = X Wqkv (6-bit, 3 palette groups),
+                    P = table Wpos (6-bit rel-pos linear over 2T-1 sinusoid
+                    rows), C = attention(QKV, P, u, v, valid), Y = X + C Wo;
+                    TFLOP/s counts the three GEMMs and the attention products
 """
 from __future__ import annotations
 
@@ -45,7 +50,9 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="ff-block",
-                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused"])
+                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
+                            "rel-pos-mha"])
+    p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
@@ -159,6 +166,45 @@ def build_conv_module(abi, ctx, keep, fused_glu=False):
     return kernels, config, mod
 
 
+def build_mha(abi, ctx, keep, frames):
+    import parakeet_wgsl_amd.workloads as wl
+    mod = wl.mha_module(0, frames=frames)
+    m, p = mod.x.shape[0], mod.table.shape[0]
+    x = keep(ctx.array(mod.x))
+    qkv = keep(ctx.empty((m, 3072), np.float16))
+    pos = keep(ctx.empty((p, 1024), np.float16))
+    c = keep(ctx.empty((m, 1024), np.float16))
+    y = keep(ctx.empty((m, 1024), np.float16))
+    op_qkv = abi.GemmOp(ctx, a=x, packed=keep(ctx.array(mod.wqkv.packed)), palette=keep(ctx.array(mod.wqkv.palette)),
+                        output=qkv, bits=6, rows=m, inner=1024, columns=3072, label="attention-qkv")
+    op_pos = abi.GemmOp(ctx, a=keep(ctx.array(mod.table)), packed=keep(ctx.array(mod.wpos.packed)),
+                        palette=keep(ctx.array(mod.wpos.palette)), output=pos, bits=6, rows=p, inner=1024,
+                        columns=1024, label="attention-relative-positions")
+    op_att = abi.RelativeAttentionOp(ctx, qkv=qkv, projected_positions=pos, bias_u=keep(ctx.array(mod.bias_u)),
+                                     bias_v=keep(ctx.array(mod.bias_v)), valid_lengths=keep(ctx.array(mod.valid)),
+                                     output=c, batch_size=mod.batch, frames=frames, positions_row_major=True,
+                                     label="relative-attention")
+    op_out = abi.GemmOp(ctx, a=c, packed=keep(ctx.array(mod.wo.packed)), palette=keep(ctx.array(mod.wo.palette)),
+                        output=y, bits=6, rows=m, inner=1024, columns=1024, residual=x, residual_scale=1.0,
+                        label="attention-output-residual")
+
+    def gemm_case(a_rows, w, name, residual=False):
+        case = wl.GemmCase(name, np.zeros((a_rows, 1024), np.float16), w)
+        extra = a_rows * 1024 * 2 if residual else 0
+        return case.flops, case.algorithmic_bytes() + extra
+    f_qkv, b_qkv = gemm_case(m, mod.wqkv, "qkv")
+    f_pos, b_pos = gemm_case(p, mod.wpos, "pos")
+    f_out, b_out = gemm_case(m, mod.wo, "out", residual=True)
+    kernels = [Kernel("attention-qkv", op_qkv, f_qkv, b_qkv, "f16"),
+               Kernel("attention-relative-positions", op_pos, f_pos, b_pos, "f16"),
+               Kernel("relative-attention", op_att, mod.attention_flops(), op_att.plan().algorithmic_bytes, "f16"),
+               Kernel("attention-output-residual", op_out, f_out, b_out, "f16")]
+    config = {"workload": "relative-position-mha-fp16", "windows": mod.batch, "frames": frames, "rows": m,
+              "d_model": 1024, "heads": 8, "head_size": 128, "palette_bits": 6, "position_rows": p,
+              "valid_lengths": [int(v) for v in mod.valid]}
+    return kernels, config, mod
+
+
 def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
     """The oracle (reference semantics restated in C) on a bounded sample:
     row batches of the same workload until about `budget_s` seconds of wall
@@ -183,6 +229,25 @@ def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
             pko.gemm(data.a[lo:hi], data.weight.packed, 6, data.weight.palette, 4096, bias=data.bias,
                      mode="f32-chain", threads=threads)
         what = "rows, f32 fma chain (reference fp32 semantics)"
+    elif workload == "rel-pos-mha":
+        # whole windows; the rel-pos linear once, as the step does
+        import parakeet_wgsl_amd.workloads as wl
+        frames = data.frames
+        total_rows, batch = data.x.shape[0], frames
+        per_row_flops = (data.gemm_flops() + data.attention_flops()) / total_rows
+        pos = pko.gemm(data.table, data.wpos.packed, 6, data.wpos.palette, 1024, mode="f16-chain", threads=threads)
+        packed = wl.pack_projected_positions(pos)
+
+        def run(lo, hi):
+            x = data.x[lo:hi]
+            w = lo // frames
+            qkv = pko.gemm(x, data.wqkv.packed, 6, data.wqkv.palette, 3072, mode="f16-chain", threads=threads)
+            c = pko.relative_attention(qkv, packed, data.bias_u, data.bias_v, data.valid[w:w + 1], batch=1,
+                                       frames=frames)
+            pko.gemm(c, data.wo.packed, 6, data.wo.palette, 1024, residual=x, residual_scale=1.0, mode="f16-chain",
+                     threads=threads)
+        what = (f"rows (whole {frames}-frame windows) of the MHA block: QKV GEMM, relative attention (f32, one "
+                "thread), output GEMM + residual; the rel-pos linear once beforehand (reference fp16 semantics)")
     elif workload in ("conv-module", "conv-module-fused"):
         # whole windows: the depthwise convolution spans frames of one window
         frames, conv = data.conv.frames, data.conv
@@ -255,6 +320,8 @@ def main():
         kernels, config, data = build_single_gemm(abi, ctx, keep)
     elif args.workload in ("conv-module", "conv-module-fused"):
         kernels, config, data = build_conv_module(abi, ctx, keep, args.workload == "conv-module-fused")
+    elif args.workload == "rel-pos-mha":
+        kernels, config, data = build_mha(abi, ctx, keep, args.frames)
     else:
         kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
     if args.variant >= 0:

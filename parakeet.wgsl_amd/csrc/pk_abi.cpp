@@ -206,14 +206,16 @@ int find_variant(int precision, int family, int waves_m, int waves_n, int m_bloc
 
 // Launch planner. The f16 choice follows MI355X measurements of every
 // compiled tile shape over the encoder's GEMM shapes (M 1..3008, K
-// 1024/4096, N 1024..4096). Up to 64 rows, and up to 256 rows of a deep-K
-// (K >= 2048) GEMM, the small-M kernel (32-row blocks, K round robin over
-// eight wavefronts) wins; everything else goes to the pair-code K-split
-// kernels with the largest tile that still gives close to one workgroup
-// per compute unit: 64 x 64 up to 256 rows, deep-K shapes 96 x 64 while
-// those fill the chip and 96 x 128 beyond; otherwise 192 x 128 when that
-// makes at least 3/4 of a wave of workgroups, 96 x 128 when that is still at
-// most one wave. f32 keeps its own smallest-cost shape.
+// 1024/4096, N 1024..4096, the rel-pos linear's 2T-1 rows). Up to 64 rows,
+// and up to 256 rows of a deep-K (K >= 2048) GEMM, the small-M kernel
+// (32-row blocks, K round robin over eight wavefronts) wins; up to 256 rows
+// otherwise the 64 x 64 pair-code tile; deep-K shapes take 96 x 64 while
+// those fill the chip and 96 x 128 beyond. Every other shape takes the
+// candidate with the least (rounds of workgroups) x (measured time of one
+// workgroup), which puts 192 x 128 on the FF expand and convolution PW1,
+// 96 x 128 on 3000-row 1024-wide GEMMs, 64 x 64 on 752 x 1024 and the
+// small-M kernel on the 375-row rel-pos linear. f32 keeps its own
+// smallest-cost shape.
 Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
   if (precision == PK_PRECISION_F16) {
     auto pair_variant = [](int wn, int r, int c, int ks) {
@@ -230,9 +232,30 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
     }
     if (rows <= 256u) return {pair_variant(1, 2, 2, 4), 1u};
     if (inner >= 2048u) return {tiles(96, 64) <= wave ? pair_variant(1, 3, 2, 4) : pair_variant(2, 3, 2, 2), 1u};
-    if (tiles(192, 128) * 4u >= wave * 3u) return {pair_variant(2, 6, 2, 2), 1u};
-    if (tiles(96, 128) <= wave) return {pair_variant(2, 3, 2, 2), 1u};
-    return {pair_variant(2, 6, 2, 2), 1u};
+    // K < 2048: the fewest rounds of workgroups times the measured time of one
+    // workgroup of each tile at K = 1024 with one workgroup per compute unit.
+    struct Candidate {
+      int wn, r, c, ks;  // pair-code shape; wn = 0 marks the small-M RW = 2 kernel
+      int tile_rows, tile_columns;
+      double us;
+    };
+    constexpr Candidate kCandidates[] = {
+        {2, 6, 2, 2, 192, 128, 22.3}, {2, 4, 2, 2, 128, 128, 17.2}, {2, 3, 2, 2, 96, 128, 14.8},
+        {1, 3, 2, 4, 96, 64, 11.0},   {1, 2, 2, 4, 64, 64, 9.3},    {0, 2, 1, 8, 64, 32, 8.2},
+    };
+    int best = -1;
+    double best_us = 1e300;
+    for (const Candidate& c : kCandidates) {
+      const int v = c.wn ? find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, c.wn, c.r, c.c, c.ks)
+                         : find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, c.r, 1, 8);
+      if (v < 0) continue;
+      const double rounds = (double)((tiles(c.tile_rows, c.tile_columns) + wave - 1) / wave);
+      if (rounds * c.us < best_us * 0.98) {
+        best_us = rounds * c.us;
+        best = v;
+      }
+    }
+    return {best < 0 ? pair_variant(2, 6, 2, 2) : best, 1u};
   }
   // f32: the largest tile that still fills the compute units.
   const int count = pk::f32_variant_count();

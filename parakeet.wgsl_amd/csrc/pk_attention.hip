@@ -277,6 +277,198 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
   }
 }
 
+// Shared-tile variant for long windows: NQ wavefronts own 32 queries each
+// (32 NQ per workgroup) and walk every key tile together. Per tile all
+// threads stage the K rows, the V^T tile and the union of the wavefronts'
+// 64-row position windows (32 NQ + 32 rows) in LDS - K, V and R are fetched
+// once per workgroup instead of once per 32 queries - while the next
+// tile's rows are already on their way into registers.
+template <int NQ, bool ROW_MAJOR>
+__global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnArgs args) {
+  constexpr int THREADS = 64 * NQ;
+  constexpr int KSTRIDE = kHead + 8;            // halves per staged K / R row (272 bytes)
+  constexpr int RROWS = kTile * NQ + kTile;     // union of the position windows
+  constexpr int KCH = kTile * kHead / 8;        // 16-byte chunks of a K (or V) tile
+  constexpr int RCH = RROWS * kHead / 8;
+  constexpr int CHUNKS = 2 * KCH + RCH;
+  constexpr int PER = (CHUNKS + THREADS - 1) / THREADS;
+  __shared__ __attribute__((aligned(16))) _Float16 ks[kTile * KSTRIDE];
+  __shared__ __attribute__((aligned(16))) _Float16 vts[kHead * kVtStride];
+  __shared__ __attribute__((aligned(16))) _Float16 rs[RROWS * KSTRIDE];
+  __shared__ __attribute__((aligned(16))) float windows[NQ * 64 * kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int j = lane & 31;
+  const int hh = lane >> 5;
+  const uint32_t qt = blockIdx.x % args.query_tiles;
+  const uint32_t bh = blockIdx.x / args.query_tiles;
+  const int head = (int)(bh % kHeads);
+  const uint32_t b = bh / kHeads;
+  const int T = (int)args.frames;
+  const int live = (int)min(args.frames, args.valid_lengths[b]);
+  const int q0 = (int)qt * kTile * NQ;
+  const _Float16* qkv = static_cast<const _Float16*>(args.qkv) + (uint64_t)b * T * kQkvRow + head * kHead;
+  const _Float16* positions = static_cast<const _Float16*>(args.positions);
+  _Float16* out = static_cast<_Float16*>(args.output) + (uint64_t)b * T * kHidden + head * kHead;
+
+  if (q0 >= live) {
+    for (int c = tid; c < kTile * NQ * (kHead / 8); c += THREADS) {
+      const int q = q0 + c / (kHead / 8);
+      if (q < T) *reinterpret_cast<half8*>(out + (uint64_t)q * kHidden + (c % (kHead / 8)) * 8) = half8{};
+    }
+    return;
+  }
+
+  const int qw = q0 + kTile * wave;  // this wavefront's first query
+  half8 qu[8], qv[8];
+  {
+    const _Float16* qrow = qkv + (uint64_t)min(qw + j, T - 1) * kQkvRow;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int d0 = 16 * s + 8 * hh;
+      const half8 x = load8(qrow + d0);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        qu[s][t] = (_Float16)((float)x[t] + args.bias_u[head * kHead + d0 + t]);
+        qv[s][t] = (_Float16)((float)x[t] + args.bias_v[head * kHead + d0 + t]);
+      }
+    }
+  }
+
+  const int pmax = (int)args.position_rows - 1;
+  // Chunk c of key tile kt: K rows [0, KCH), V rows [KCH, 2 KCH), R rows.
+  auto fetch = [&](int kt, half8 (&reg)[PER]) {
+    const int k0 = kt * kTile;
+    const int pbase = T - q0 - kTile * NQ + k0;  // first row of the union window
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * THREADS;
+      if (c < 2 * KCH) {
+        const int kk = (c % KCH) / (kHead / 8), part = c % (kHead / 8);
+        const int block = c < KCH ? kHidden : 2 * kHidden;
+        reg[i] = load8(qkv + (uint64_t)min(k0 + kk, T - 1) * kQkvRow + block + part * 8);
+      } else if (c < CHUNKS) {
+        const int rc = c - 2 * KCH;
+        const int row = rc / (kHead / 8), part = rc % (kHead / 8);
+        reg[i] = load_position<ROW_MAJOR>(positions, args.position_rows, head, min(max(pbase + row, 0), pmax),
+                                          part * 8);
+      }
+    }
+  };
+  auto stage = [&](const half8 (&reg)[PER]) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * THREADS;
+      if (c < KCH) {
+        const int kk = c / (kHead / 8), part = c % (kHead / 8);
+        *reinterpret_cast<half8*>(ks + kk * KSTRIDE + part * 8) = reg[i];
+      } else if (c < 2 * KCH) {
+        const int kk = (c - KCH) / (kHead / 8), part = (c - KCH) % (kHead / 8);
+        const int slot = (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) vts[(part * 8 + t) * kVtStride + slot] = reg[i][t];
+      } else if (c < CHUNKS) {
+        const int rc = c - 2 * KCH;
+        *reinterpret_cast<half8*>(rs + (rc / (kHead / 8)) * KSTRIDE + (rc % (kHead / 8)) * 8) = reg[i];
+      }
+    }
+  };
+
+  float* window = windows + wave * 64 * kTile;
+  const int rbase = kTile * (NQ - 1 - wave);  // this wavefront's window inside the union
+  const float scale = 0.08838834764831845f;
+  float m = -INFINITY, l = 0.0f;
+  floatx16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+
+  const int tiles = (live + kTile - 1) / kTile;
+  half8 reg[PER];
+  fetch(0, reg);
+  for (int kt = 0; kt < tiles; ++kt) {
+    const int k0 = kt * kTile;
+    __syncthreads();  // every wavefront is done with the previous tile
+    stage(reg);
+    __syncthreads();
+    if (kt + 1 < tiles) fetch(kt + 1, reg);
+
+    floatx16 ac, w0, w1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ac[r] = w0[r] = w1[r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int d0 = 16 * s + 8 * hh;
+      const half8 kv = *reinterpret_cast<const half8*>(ks + j * KSTRIDE + d0);
+      const half8 ra = *reinterpret_cast<const half8*>(rs + (rbase + j) * KSTRIDE + d0);
+      const half8 rb = *reinterpret_cast<const half8*>(rs + (rbase + kTile + j) * KSTRIDE + d0);
+      ac = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qu[s], ac, 0, 0, 0);
+      w0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra, qv[s], w0, 0, 0, 0);
+      w1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(rb, qv[s], w1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 8 * (r / 4) + 4 * hh + (r % 4);
+      window[c * kTile + j] = w0[r];
+      window[(kTile + c) * kTile + j] = w1[r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    float sc[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r / 4) + 4 * hh + (r % 4);
+      const float rel = window[(kTile - 1 - j + i) * kTile + j];
+      sc[r] = k0 + i < live ? (ac[r] + rel) * scale : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp(m - m_new);
+    float rsum = 0.0f;
+    half8 pb8[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp(sc[r] - m_new);
+      rsum += p;
+      pb8[r / 8][r % 8] = (_Float16)p;
+    }
+    rsum += __shfl_xor(rsum, 32, 64);
+    l = l * alpha + rsum;
+    m = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const half8 va = *reinterpret_cast<const half8*>(vts + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb8[s], o[db], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+
+  const int q = qw + j;
+  if (q < T) {
+    const bool keep = q < live;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * hh;
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = keep ? (_Float16)(o[db][4 * g + e] * inv) : (_Float16)0.0f;
+        *reinterpret_cast<half4*>(out + (uint64_t)q * kHidden + d) = h;
+      }
+  }
+}
+
 // The reference's arithmetic in f32: one workgroup of 256 threads per
 // (window, head, query); scores of all keys live in LDS (T <= kMaxFrames).
 template <bool ROW_MAJOR>
@@ -346,20 +538,35 @@ __global__ __launch_bounds__(256) void rel_attention_f32_kernel(AttnArgs args) {
 struct AttnVariant {
   const char* name;
   int waves;
+  int queries;  // per workgroup
+  uint32_t lds_bytes;
   void (*packed)(AttnArgs);
   void (*row_major)(AttnArgs);
 };
 
 #define PK_ATTN_VARIANT(K)                                                                                 \
   AttnVariant {                                                                                            \
-    "pk_rel_attention_f16_q32_w" #K, K, rel_attention_f16_kernel<K, false>, rel_attention_f16_kernel<K, true> \
+    "pk_rel_attention_f16_q32_w" #K, K, kTile, (uint32_t)(K * kWaveLds), rel_attention_f16_kernel<K, false>, \
+        rel_attention_f16_kernel<K, true>                                                                  \
+  }
+#define PK_ATTN_SHARED_VARIANT(NQ)                                                                         \
+  AttnVariant {                                                                                            \
+    "pk_rel_attention_f16_q" #NQ "x32_shared", NQ, NQ * kTile,                                             \
+        (uint32_t)((kTile + (NQ + 1) * kTile) * (kHead + 8) * 2 + kHead * kVtStride * 2 + NQ * 64 * kTile * 4), \
+        rel_attention_f16_shared_kernel<NQ, false>, rel_attention_f16_shared_kernel<NQ, true>              \
   }
 
-const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1)};
-const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, rel_attention_f32_kernel<false>,
+// Index 0: up to 256 frames (key tiles split over the workgroup: most
+// workgroups); index 3: longer windows (K, V and positions shared by 64
+// queries).
+const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
+                                    PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
+const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
                                  rel_attention_f32_kernel<true>};
 
 }  // namespace
+
+int attention_default_variant(bool f16, uint32_t frames) { return f16 && frames > 256u ? 3 : 0; }
 
 int attention_variant_count(bool f16) {
   return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0])) : 1;
@@ -370,10 +577,10 @@ AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t
   if (f16) {
     const AttnVariant& v = kF16Variants[variant];
     g.name = v.name;
-    g.query_tiles = (frames + kTile - 1) / kTile;
+    g.query_tiles = (frames + v.queries - 1) / v.queries;
     g.grid = batch * kHeads * g.query_tiles;
     g.block_threads = 64 * v.waves;
-    g.lds_bytes = v.waves * kWaveLds;
+    g.lds_bytes = v.lds_bytes;
   } else {
     g.name = kF32Variant.name;
     g.query_tiles = frames;

@@ -32,9 +32,6 @@ bool overlaps(const void* a, uint64_t a_bytes, const void* b, uint64_t b_bytes) 
   return x < y + b_bytes && y < x + a_bytes;
 }
 
-// Four wavefronts per 32-query workgroup splitting the key tiles.
-int default_variant(int /*precision*/) { return 0; }
-
 int validate_attention_desc(const pk_attention_desc* d) {
   if (!d) return fail(PK_INVALID_ARGUMENT, "attention descriptor is null");
   if (d->struct_size != sizeof(pk_attention_desc))
@@ -125,7 +122,7 @@ int pk_attention_create(pk_context* ctx, const pk_attention_desc* d, pk_attentio
   op->label = attention_label(d->label);
   op->precision = d->precision;
   op->batch = d->batch_size;
-  op->variant = default_variant(d->precision);
+  op->variant = pk::attention_default_variant(d->precision == PK_PRECISION_F16, d->frames);
   pk::AttnArgs& a = op->args;
   a.qkv = d->qkv;
   a.positions = d->projected_positions;

@@ -216,6 +216,9 @@ struct AttnGeometry {
 };
 
 int attention_variant_count(bool f16);
+// Planned launch shape: key-split 32-query tiles up to 256 frames, shared
+// K/V/position tiles beyond.
+int attention_default_variant(bool f16, uint32_t frames);
 AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t batch);
 hipError_t launch_attention(bool f16, int variant, const AttnArgs& args, uint32_t batch, hipStream_t stream,
                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);

@@ -301,3 +301,46 @@ def attention_case(seed: int, batch: int, frames: int, *, dtype=np.float16, vali
     if valid is None:
         valid = rng.integers((frames + 1) // 2, frames + 1, size=batch)
     return AttentionCase(qkv, positions, bias_u, bias_v, np.asarray(valid, dtype=np.uint32), batch, frames)
+
+
+@dataclass
+class MhaModule:
+    """Relative-position multi-head attention block after its layer norm
+    (src/webgpu/encoder.ts:1930-2010): QKV = X Wqkv (3 palette groups, Q|K|V),
+    P = table(T) Wpos (the rel-pos linear over the 2T-1 sinusoid rows),
+    C = attention(QKV, P, u, v, valid), Y = X + C Wo."""
+    x: np.ndarray
+    wqkv: PaletteMatrix
+    wpos: PaletteMatrix
+    wo: PaletteMatrix
+    table: np.ndarray          # [2T-1, 1024] f16 sinusoid rows
+    bias_u: np.ndarray
+    bias_v: np.ndarray
+    valid: np.ndarray
+    batch: int
+    frames: int
+
+    def gemm_flops(self) -> int:
+        m, p = self.x.shape[0], self.table.shape[0]
+        return 2 * m * 1024 * 3072 + 2 * p * 1024 * 1024 + 2 * m * 1024 * 1024
+
+    def attention_flops(self) -> int:
+        live = np.minimum(self.valid.astype(np.int64), self.frames)
+        return int((live * live).sum()) * 8 * 128 * 2 * 3
+
+
+def mha_module(seed: int = 0, windows: int = 4, frames: int = 188, d_model: int = 1024, bits: int = 6) -> MhaModule:
+    """Input [windows x frames x 1024] f16 ~ N(0,1); 6-bit Wqkv 1024->3072
+    with three 64-entry f16 LUTs (one per Q/K/V block, the reference's QKV
+    layout), 6-bit Wpos and Wo 1024->1024, LUTs ~ N(0, 0.02); u, v ~
+    N(0, 0.02); valid lengths uniform integers in [ceil(T/2), T]."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (windows * frames, d_model), 1.0, np.float16)
+    wqkv = palette_matrix(rng, bits, d_model, 3 * d_model, dtype=np.float16, groups=3)
+    wpos = palette_matrix(rng, bits, d_model, d_model, dtype=np.float16)
+    wo = palette_matrix(rng, bits, d_model, d_model, dtype=np.float16)
+    bias_u = normal(rng, (8, 128), 0.02, np.float32)
+    bias_v = normal(rng, (8, 128), 0.02, np.float32)
+    valid = rng.integers((frames + 1) // 2, frames + 1, size=windows).astype(np.uint32)
+    table = relative_position_table(frames, d_model).astype(np.float16)
+    return MhaModule(x, wqkv, wpos, wo, table, bias_u, bias_v, valid, windows, frames)

@@ -135,3 +135,76 @@ def test_attention_dispatch_errors(abi, ctx, scope, workloads):
             op.enqueue()
     finally:
         op.release()
+
+
+# ---------------------------------------------------- the MHA block (C3)
+
+
+def mha_on_gpu(abi, ctx, scope, mod):
+    """QKV GEMM -> rel-pos linear (row-major positions) -> attention -> Wo
+    GEMM + residual, on one stream."""
+    rows, p = mod.x.shape[0], mod.table.shape[0]
+    x = scope.put(mod.x)
+    qkv = scope.empty((rows, 3072), np.float16)
+    pos = scope.empty((p, 1024), np.float16)
+    ctxt = scope.empty((rows, 1024), np.float16)
+    y = scope.empty((rows, 1024), np.float16)
+    ops = [
+        abi.GemmOp(ctx, a=x, packed=scope.put(mod.wqkv.packed), palette=scope.put(mod.wqkv.palette), output=qkv,
+                   bits=mod.wqkv.bits, rows=rows, inner=1024, columns=3072, label="attention-qkv"),
+        abi.GemmOp(ctx, a=scope.put(mod.table), packed=scope.put(mod.wpos.packed),
+                   palette=scope.put(mod.wpos.palette), output=pos, bits=mod.wpos.bits, rows=p, inner=1024,
+                   columns=1024, label="attention-relative-positions"),
+        abi.RelativeAttentionOp(ctx, qkv=qkv, projected_positions=pos, bias_u=scope.put(mod.bias_u),
+                                bias_v=scope.put(mod.bias_v), valid_lengths=scope.put(mod.valid), output=ctxt,
+                                batch_size=mod.batch, frames=mod.frames, positions_row_major=True),
+        abi.GemmOp(ctx, a=ctxt, packed=scope.put(mod.wo.packed), palette=scope.put(mod.wo.palette), output=y,
+                   bits=mod.wo.bits, rows=rows, inner=1024, columns=1024, residual=x, residual_scale=1.0,
+                   label="attention-output-residual"),
+    ]
+    try:
+        for op in ops:
+            op.enqueue()
+        ctx.synchronize()
+        return qkv.download(), pos.download(), ctxt.download(), y.download()
+    finally:
+        for op in ops:
+            op.release()
+
+
+def mha_on_oracle(oracle, workloads, mod, windows, mode):
+    """The same chain on the CPU for the given windows: "reference" = f16
+    accumulation chains for the GEMMs and the f32 attention, rounded to f16
+    between steps; "f64" = every step in double."""
+    T = mod.frames
+    rows = np.concatenate([np.arange(w * T, (w + 1) * T) for w in windows])
+    x = mod.x[rows]
+    valid = mod.valid[list(windows)]
+    if mode == "reference":
+        qkv = oracle.gemm(x, mod.wqkv.packed, 6, mod.wqkv.palette, 3072, mode="f16-chain", threads=8)
+        pos = oracle.gemm(mod.table, mod.wpos.packed, 6, mod.wpos.palette, 1024, mode="f16-chain", threads=8)
+        c = oracle.relative_attention(qkv, workloads.pack_projected_positions(pos), mod.bias_u, mod.bias_v, valid,
+                                      batch=len(windows), frames=T)
+        return rows, oracle.gemm(c, mod.wo.packed, 6, mod.wo.palette, 1024, residual=x, residual_scale=1.0,
+                                 mode="f16-chain", threads=8)
+    qkv = oracle.gemm(x, mod.wqkv.packed, 6, mod.wqkv.palette, 3072, mode="f64", threads=8)
+    pos = oracle.gemm(mod.table, mod.wpos.packed, 6, mod.wpos.palette, 1024, mode="f64", threads=8)
+    c = oracle.relative_attention(qkv, workloads.pack_projected_positions(pos), mod.bias_u, mod.bias_v, valid,
+                                  batch=len(windows), frames=T, mode="f64")
+    dense = oracle.expand(mod.wo.packed, 6, 1024, 1024, mod.wo.palette).astype(np.float64)
+    return rows, x.astype(np.float64) + c @ dense
+
+
+@pytest.mark.parametrize("frames,windows", [(188, (0, 3)), (750, (1,))])
+def test_mha_block_full_size(abi, ctx, scope, oracle, workloads, frames, windows):
+    """4 windows x T frames x 1024 through the four launches; the checked
+    windows against the oracle chain (1e-2) and the fp64 truth (2e-3)."""
+    mod = workloads.mha_module(0, frames=frames)
+    print(f"mha block 4x{frames}x1024", flush=True)
+    _, _, _, y = mha_on_gpu(abi, ctx, scope, mod)
+    rows, y_ref = mha_on_oracle(oracle, workloads, mod, windows, "reference")
+    norm, _ = oracle.relative_errors(y[rows], y_ref)
+    assert norm <= 1e-2, norm
+    rows, y_truth = mha_on_oracle(oracle, workloads, mod, windows, "f64")
+    norm, _ = oracle.relative_errors(y[rows], y_truth)
+    assert norm <= F16_TOL_TRUTH, norm
