@@ -1,7 +1,8 @@
 /*
  * pk_napi.c - Node-API (N-API 8) addon over the palette GEMM C ABI
- * (include/pk_palette.h) and the fused Conformer convolution tail
- * (include/pk_conv.h). It is the thin native layer under the JavaScript
+ * (include/pk_palette.h), the fused Conformer convolution tail
+ * (include/pk_conv.h) and the relative-position attention
+ * (include/pk_attention.h). It is the thin native layer under the JavaScript
  * host in ../host: every function forwards to one pk_* call, converts device
  * pointers to BigInt, and turns a failing pk_status into a thrown Error
  * (RangeError for PK_RANGE_ERROR, as the reference throws RangeError for
@@ -20,6 +21,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "pk_attention.h"
 #include "pk_conv.h"
 #include "pk_palette.h"
 
@@ -689,6 +691,117 @@ static napi_value js_conv_plan(napi_env env, napi_callback_info info) {
   return conv_plan_object(env, &p);
 }
 
+/* ---- relative-position attention ------------------------------------------ */
+
+static void attention_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  pk_attention_release((pk_attention_op *)data);
+}
+
+/* A JavaScript attention descriptor: {label, flags?, precision, batchSize,
+   frames, qkv, qkvBytes, projectedPositions, projectedPositionsBytes, biasU,
+   biasUBytes, biasV, biasVBytes, validLengths, validLengthsBytes, output,
+   outputBytes}; device pointers are BigInt. */
+static int parse_attention_desc(napi_env env, napi_value o, pk_attention_desc *d, char **label) {
+  memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  *label = NULL;
+  uint64_t qkv = 0, positions = 0, bu = 0, bv = 0, valid = 0, output = 0;
+  parse_precision(env, o, &d->precision);
+  if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
+      !prop_u64(env, o, "qkv", &qkv) || !prop_u64(env, o, "qkvBytes", &d->qkv_bytes) ||
+      !prop_u64(env, o, "projectedPositions", &positions) ||
+      !prop_u64(env, o, "projectedPositionsBytes", &d->projected_positions_bytes) ||
+      !prop_u64(env, o, "biasU", &bu) || !prop_u64(env, o, "biasUBytes", &d->bias_u_bytes) ||
+      !prop_u64(env, o, "biasV", &bv) || !prop_u64(env, o, "biasVBytes", &d->bias_v_bytes) ||
+      !prop_u64(env, o, "validLengths", &valid) || !prop_u64(env, o, "validLengthsBytes", &d->valid_lengths_bytes) ||
+      !prop_u64(env, o, "output", &output) || !prop_u64(env, o, "outputBytes", &d->output_bytes)) {
+    bad_argument(env, "attention descriptor is missing a required field");
+    return 0;
+  }
+  prop_u32(env, o, "flags", &d->flags);
+  d->qkv = (const void *)(uintptr_t)qkv;
+  d->projected_positions = (const void *)(uintptr_t)positions;
+  d->bias_u = (const float *)(uintptr_t)bu;
+  d->bias_v = (const float *)(uintptr_t)bv;
+  d->valid_lengths = (const uint32_t *)(uintptr_t)valid;
+  d->output = (void *)(uintptr_t)output;
+  *label = prop_string(env, o, "label");
+  d->label = *label;
+  return 1;
+}
+
+/* attentionValidate(desc) */
+static napi_value js_attention_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  pk_attention_desc d;
+  char *label;
+  if (!parse_attention_desc(env, argv[0], &d, &label)) return NULL;
+  const int status = pk_attention_validate(&d);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+/* attentionCreate(ctx, desc) -> op */
+static napi_value js_attention_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2], ext;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  pk_attention_desc d;
+  char *label;
+  if (!parse_attention_desc(env, argv[1], &d, &label)) return NULL;
+  pk_attention_op *op = NULL;
+  const int status = pk_attention_create((pk_context *)get_external(env, argv[0]), &d, &op);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  NAPI_CALL(env, napi_create_external(env, op, attention_finalize, NULL, &ext));
+  return ext;
+}
+
+/* attentionEnqueue(op, activeBatch, stream?, startEvent?, endEvent?) */
+static napi_value js_attention_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  uint32_t batch = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  PK_CALL(env, pk_attention_enqueue_timed((pk_attention_op *)get_external(env, argv[0]), batch,
+                                          get_external(env, argv[2]), get_external(env, argv[3]),
+                                          get_external(env, argv[4])));
+  return undefined(env);
+}
+
+static napi_value js_attention_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_attention_destroy((pk_attention_op *)get_external(env, argv[0])));
+  return undefined(env);
+}
+
+/* attentionPlan(op, activeBatch?) */
+static napi_value js_attention_plan(napi_env env, napi_callback_info info) {
+  napi_value argv[2], obj, grid, v;
+  uint32_t batch = 0;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  pk_attention_plan_info p;
+  PK_CALL(env, pk_attention_plan((pk_attention_op *)get_external(env, argv[0]), batch, &p));
+  NAPI_CALL(env, napi_create_object(env, &obj));
+  NAPI_CALL(env, napi_create_array_with_length(env, 3, &grid));
+  for (uint32_t i = 0; i < 3; ++i) napi_set_element(env, grid, i, make_number(env, p.grid[i]));
+  napi_set_named_property(env, obj, "workgroups", grid);
+  napi_set_named_property(env, obj, "blockThreads", make_number(env, p.block_threads));
+  napi_set_named_property(env, obj, "workgroupStorageBytes", make_number(env, p.lds_bytes));
+  napi_set_named_property(env, obj, "queryTiles", make_number(env, p.query_tiles));
+  napi_set_named_property(env, obj, "algorithmicBytes", make_number(env, (double)p.algorithmic_bytes));
+  napi_create_string_utf8(env, p.kernel, NAPI_AUTO_LENGTH, &v);
+  napi_set_named_property(env, obj, "kernel", v);
+  return obj;
+}
+
 /* ---- module --------------------------------------------------------------- */
 
 static napi_value init(napi_env env, napi_value exports) {
@@ -723,6 +836,11 @@ static napi_value init(napi_env env, napi_value exports) {
       {"convEnqueue", js_conv_enqueue},
       {"convDestroy", js_conv_destroy},
       {"convPlan", js_conv_plan},
+      {"attentionValidate", js_attention_validate},
+      {"attentionCreate", js_attention_create},
+      {"attentionEnqueue", js_attention_enqueue},
+      {"attentionDestroy", js_attention_destroy},
+      {"attentionPlan", js_attention_plan},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
     napi_value f;

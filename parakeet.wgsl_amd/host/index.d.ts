@@ -292,3 +292,60 @@ export declare class FusedConformerConvKernel {
   createDispatch(descriptor: FusedConformerConvDescriptor): FusedConformerConvDispatch;
   destroy(): void;
 }
+
+/* ---- Relative-position attention (src/webgpu/kernels/attention.ts) ---- */
+
+/** attention.ts:39-49 */
+export interface RelativeAttentionDescriptor {
+  readonly label: string;
+  /** Profile-scalar [rows, 3072]: Q, K, V blocks of 1024, head h at 128h. */
+  readonly qkv: ArenaSlice;
+  /** "head-vector-position-vec4" [8, 32, 2T-1, 4] package tensor (or, with
+   *  projectedPositionsRowMajor, a [2T-1, 1024] arena slice). */
+  readonly projectedPositions: GpuTensor | ArenaSlice;
+  readonly biasU: GpuTensor;
+  readonly biasV: GpuTensor;
+  readonly validLengths: ArenaSlice;
+  /** Profile-scalar [rows, 1024]; must not overlap qkv. */
+  readonly output: ArenaSlice;
+  readonly batchSize: number;
+  /** 1..4096 here (the reference: 1..192). */
+  readonly frames: number;
+  /** This library only: positions are a row-major [2T-1, 1024] arena slice. */
+  readonly projectedPositionsRowMajor?: boolean;
+}
+
+export interface RelativeAttentionPlan {
+  readonly workgroups: readonly [number, number, number];
+  readonly blockThreads: number;
+  readonly workgroupStorageBytes: number;
+  readonly queryTiles: number;
+  readonly algorithmicBytes: number;
+  readonly kernel: string;
+}
+
+/** attention.ts:51-97 */
+export declare class RelativeAttentionDispatch {
+  readonly label: string;
+  readonly output: ArenaSlice;
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, shape?: EncoderDispatchShape): void;
+  destroy(): void;
+  plan(activeBatch?: number): RelativeAttentionPlan;
+}
+
+/** attention.ts:105-321 */
+export declare class RelativeAttentionKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<RelativeAttentionKernel>;
+  readonly uniformParameterPoolBytes: number;
+  readonly uniformParameterPoolUsedSlots: number;
+  validateDescriptor(descriptor: RelativeAttentionDescriptor): void;
+  createDispatch(descriptor: RelativeAttentionDescriptor): RelativeAttentionDispatch;
+  destroy(): void;
+}
+
+export declare function relativeAttentionTensorRecords(frames: number, options?: { dtype?: "float16" | "float32" }): {
+  projectedPositions: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  biasU: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  biasV: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+};

@@ -25,6 +25,10 @@
  *   planFusedConformerConv             :72-115 (rows and byte lengths are the
  *                                      reference's; workgroups is this
  *                                      library's own launch)
+ *   RelativeAttentionKernel            src/webgpu/kernels/attention.ts:105-321
+ *     .create / .createDispatch        :130-314 (record checks :323-370 here,
+ *                                      the numeric contract in pk_attention_validate)
+ *   RelativeAttentionDispatch.encode / destroy   :51-97
  * The WebGPU device, queue, buffers and command encoder are replaced by HIP
  * equivalents with the same shapes (HipGpuDevice, queue.writeBuffer /
  * submit / onSubmittedWorkDone, createCommandEncoder().finish()).
@@ -581,6 +585,173 @@ class FusedConformerConvKernel {
   }
 }
 
+/* ------------------------------------------------ relative attention */
+
+const ATTENTION_POSITIONS_ROW_MAJOR = 1;
+
+/** requireProjectedPositions (attention.ts:323-353). */
+function requireProjectedPositions(tensor, positionRows, fp32) {
+  const dtype = fp32 ? "float32" : "float16";
+  const logical = [positionRows, 1024];
+  const storage = [8, 32, positionRows, 4];
+  const record = tensor.runtimeRecord;
+  if (
+    record.dtype !== dtype ||
+    record.layout !== "head-vector-position-vec4" ||
+    record.byteLength !== positionRows * 1024 * (fp32 ? 4 : 2) ||
+    shapeKey(record.logicalShape) !== shapeKey(logical) ||
+    shapeKey(record.storageShape) !== shapeKey(storage)
+  ) {
+    throw new Error(
+      `Projected positions must be ${dtype} head-vector-position-vec4, ` +
+        `logical [${logical.join(",")}], storage [${storage.join(",")}]`,
+    );
+  }
+}
+
+/** requireAttentionBias (attention.ts:355-370). */
+function requireAttentionBias(tensor, label) {
+  const record = tensor.runtimeRecord;
+  if (
+    record.dtype !== "float32" ||
+    record.layout !== "head-by-channel" ||
+    record.byteLength !== 4096 ||
+    shapeKey(record.logicalShape) !== "8,128" ||
+    shapeKey(record.storageShape) !== "8,128"
+  ) {
+    throw new Error(`${label} must be float32 head-by-channel logical/storage [8,128]`);
+  }
+}
+
+/** Package records of the projected positions and the u / v biases. */
+function relativeAttentionTensorRecords(frames, options) {
+  const dtype = (options && options.dtype) || "float16";
+  const rows = 2 * frames - 1;
+  const positions = {
+    dtype,
+    logicalShape: [rows, 1024],
+    storageShape: [8, 32, rows, 4],
+    byteLength: rows * 1024 * (dtype === "float16" ? 2 : 4),
+    layout: "head-vector-position-vec4",
+  };
+  const bias = { dtype: "float32", logicalShape: [8, 128], storageShape: [8, 128], byteLength: 4096,
+                 layout: "head-by-channel" };
+  return {
+    projectedPositions: { sourceRecord: positions, runtimeRecord: positions },
+    biasU: { sourceRecord: bias, runtimeRecord: bias },
+    biasV: { sourceRecord: bias, runtimeRecord: bias },
+  };
+}
+
+class RelativeAttentionDispatch {
+  constructor(label, output, op, batchSize) {
+    this.label = label;
+    this.output = output;
+    this.op = op;
+    this.batchSize = batchSize;
+    this.destroyed = false;
+  }
+
+  /** encode (attention.ts:62-91): shape.batchSize selects the active windows. */
+  encode(encoder, timestampWrites, shape) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    const active = shape === undefined || shape.batchSize === undefined ? this.batchSize : shape.batchSize;
+    if (!isSafe(active) || active <= 0 || active > this.batchSize)
+      throw new RangeError(`${this.label} active batch must be in [1, ${this.batchSize}]`);
+    const op = this.op;
+    encoder.record(() => {
+      const qs = timestampWrites ? timestampWrites.querySet : null;
+      const begin = qs && timestampWrites.beginningOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.beginningOfPassWriteIndex] : null;
+      const end = qs && timestampWrites.endOfPassWriteIndex !== undefined
+        ? qs.events[timestampWrites.endOfPassWriteIndex] : null;
+      native().attentionEnqueue(op, active, null, begin, end);
+    });
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().attentionDestroy(this.op);
+  }
+
+  plan(activeBatch) {
+    return native().attentionPlan(this.op, activeBatch || 0);
+  }
+}
+
+class RelativeAttentionKernel {
+  constructor(device, arena, executionProfile) {
+    this.device = device;
+    this.arena = arena;
+    this.fp32 = executionProfile !== undefined && executionProfile.precision === "fp32";
+    this.destroyed = false;
+  }
+
+  /** create (attention.ts:130-217): the kernels are compiled into the library. */
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new RelativeAttentionKernel(device, arena, executionProfile));
+  }
+
+  get uniformParameterPoolBytes() {
+    return 0;
+  }
+
+  get uniformParameterPoolUsedSlots() {
+    return 0;
+  }
+
+  nativeDescriptor(descriptor) {
+    if (!isSafe(descriptor.batchSize) || descriptor.batchSize <= 0 || !isSafe(descriptor.frames) ||
+        descriptor.frames <= 0)
+      throw new RangeError(`Unsupported attention shape for ${descriptor.label}`);
+    const rowMajor = descriptor.projectedPositionsRowMajor === true;
+    if (!rowMajor) requireProjectedPositions(descriptor.projectedPositions, descriptor.frames * 2 - 1, this.fp32);
+    requireAttentionBias(descriptor.biasU, `${descriptor.label} bias U`);
+    requireAttentionBias(descriptor.biasV, `${descriptor.label} bias V`);
+    const qkv = this.arena.binding(descriptor.qkv);
+    const output = this.arena.binding(descriptor.output);
+    const valid = this.arena.binding(descriptor.validLengths);
+    const positions = rowMajor ? this.arena.binding(descriptor.projectedPositions) : descriptor.projectedPositions.binding;
+    const u = descriptor.biasU.binding;
+    const v = descriptor.biasV.binding;
+    return {
+      label: descriptor.label,
+      flags: rowMajor ? ATTENTION_POSITIONS_ROW_MAJOR : 0,
+      precision: this.fp32 ? "f32" : "f16",
+      batchSize: descriptor.batchSize,
+      frames: descriptor.frames,
+      qkv: addressOf(qkv),
+      qkvBytes: qkv.size,
+      projectedPositions: addressOf(positions),
+      projectedPositionsBytes: positions.size,
+      biasU: addressOf(u),
+      biasUBytes: u.size,
+      biasV: addressOf(v),
+      biasVBytes: v.size,
+      validLengths: addressOf(valid),
+      validLengthsBytes: valid.size,
+      output: addressOf(output),
+      outputBytes: output.size,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().attentionValidate(this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (attention.ts:219-314). */
+  createDispatch(descriptor) {
+    if (this.destroyed) throw new Error("Parakeet relative attention kernel was destroyed");
+    const op = native().attentionCreate(this.device.context, this.nativeDescriptor(descriptor));
+    return new RelativeAttentionDispatch(descriptor.label, descriptor.output, op, descriptor.batchSize);
+  }
+
+  destroy() {
+    this.destroyed = true;
+  }
+}
+
 /* ------------------------------------------------------------ kernels */
 
 class GemmDispatch {
@@ -864,4 +1035,7 @@ module.exports = {
   CONFORMER_CONV_KERNEL_SIZE,
   CONFORMER_DEPTHWISE_WEIGHT_LAYOUT,
   CONFORMER_FOLDED_BATCH_NORM_LAYOUT,
+  RelativeAttentionKernel,
+  RelativeAttentionDispatch,
+  relativeAttentionTensorRecords,
 };

@@ -141,6 +141,33 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
     throwsLike(() => conv.validateDescriptor(convDescriptor((d) => {
       d.output = arena.slice("z", 4096, 376 * 1024 * 2);
     })), Error, "must not overlap the pointwise input");
+    return host.RelativeAttentionKernel.create({}, arena, 64);
+  }).then((attention) => {
+    const rec = host.relativeAttentionTensorRecords(188);
+    function attDescriptor(mutate) {
+      const d = {
+        label: "layer0-relative-attention", batchSize: 2, frames: 188,
+        qkv: arena.slice("qkv", 0, 376 * 3072 * 2),
+        projectedPositions: tensor(rec.projectedPositions),
+        biasU: tensor(rec.biasU), biasV: tensor(rec.biasV),
+        validLengths: arena.slice("v", 128 * 1024 * 1024, 8),
+        output: arena.slice("ctx", 256 * 1024 * 1024, 376 * 1024 * 2),
+      };
+      if (mutate) mutate(d);
+      return d;
+    }
+    attention.validateDescriptor(attDescriptor());
+    throwsLike(() => attention.validateDescriptor(attDescriptor((d) => { d.frames = 0; })), RangeError,
+               "Unsupported attention shape for layer0-relative-attention");
+    throwsLike(() => attention.validateDescriptor(attDescriptor((d) => {
+      d.qkv = arena.slice("qkv", 0, 376 * 3072 * 2 - 4);
+    })), RangeError, "layer0-relative-attention QKV needs 2310144 bytes; arena slice has 2310140");
+    throwsLike(() => attention.validateDescriptor(attDescriptor((d) => {
+      d.projectedPositions = tensor(host.relativeAttentionTensorRecords(187).projectedPositions);
+    })), Error, "Projected positions must be float16 head-vector-position-vec4, logical [375,1024], storage [8,32,375,4]");
+    throwsLike(() => attention.validateDescriptor(attDescriptor((d) => {
+      d.biasV = Object.assign({}, d.biasV, { runtimeRecord: Object.assign({}, rec.biasV.runtimeRecord, { dtype: "float16" }) });
+    })), Error, "layer0-relative-attention bias V must be float32 head-by-channel logical/storage [8,128]");
     console.log("host_cpu ok");
   });
 }).catch((e) => { console.error(e); process.exit(1); });

@@ -87,3 +87,24 @@ def test_node_host_conv_matches_oracle(tmp_path, oracle, workloads):
     diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
     ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
     assert np.all(diff <= ulp * 1.0 + 1e-12)
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_attention_matches_oracle(tmp_path, oracle, workloads):
+    """The relative attention through the Node host (RelativeAttentionKernel,
+    reference package layout for the positions) on 3 windows, active batch 2."""
+    batch, frames = 3, 188
+    case = workloads.attention_case(60, batch, frames, valid=[188, 120, 150])
+    files = {}
+    for name, arr in (("qkv", case.qkv), ("positions", case.packed_positions), ("biasU", case.bias_u),
+                      ("biasV", case.bias_v), ("valid", case.valid)):
+        files[name] = str(tmp_path / f"{name}.bin")
+        np.ascontiguousarray(arr).tofile(files[name])
+    spec = dict(files, batchSize=batch, frames=frames, activeBatch=2, output=str(tmp_path / "out.bin"))
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print(run_node("host_gpu_attention.js", str(tmp_path / "case.json")))
+    got = np.fromfile(tmp_path / "out.bin", dtype=np.float16).reshape(batch * frames, 1024)[:2 * frames]
+    want = oracle.relative_attention(case.qkv[:2 * frames], case.packed_positions, case.bias_u, case.bias_v,
+                                     case.valid[:2], batch=2, frames=frames)
+    assert oracle.relative_errors(got, want)[0] <= 2e-3
