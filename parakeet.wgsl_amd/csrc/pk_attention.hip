@@ -66,6 +66,9 @@ __device__ __forceinline__ half8 load_position(const _Float16* positions, uint32
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
+// Headroom of the lazily moved softmax maximum (natural-log units).
+constexpr float kRescaleMargin = 8.0f;
+
 template <int KSPLIT, bool ROW_MAJOR>
 __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs args) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[KSPLIT * kWaveLds];
@@ -182,7 +185,11 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
+    // The running maximum (and with it O and l) moves only when some query's
+    // scores exceed it by more than kRescaleMargin; below that the
+    // probabilities stay under e^8, well inside f16, and O / l is unchanged.
+    const bool moved = __builtin_amdgcn_ballot_w64(mx > m + kRescaleMargin) != 0;
+    const float m_new = moved ? fmaxf(m, mx) : m;
     const float alpha = fast_exp(m - m_new);
     float rs = 0.0f;
     half8 pb8[2];
@@ -195,10 +202,14 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
     rs += __shfl_xor(rs, 32, 64);
     l = l * alpha + rs;
     m = m_new;
+    if (moved) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const half8 va = load8(vt + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
@@ -278,23 +289,29 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
 }
 
 // Shared-tile variant for long windows: NQ wavefronts own 32 queries each
-// (32 NQ per workgroup) and walk every key tile together. Per tile all
-// threads stage the K rows, the V^T tile and the union of the wavefronts'
-// 64-row position windows (32 NQ + 32 rows) in LDS - K, V and R are fetched
-// once per workgroup instead of once per 32 queries - while the next
-// tile's rows are already on their way into registers.
+// (32 NQ per workgroup) and walk every key tile together, so per tile all
+// threads stage the K rows and the V^T tile once for the workgroup. The
+// relative positions need even less: wavefront w's window for key tile kt
+// is position blocks kt + NQ - 1 - w and kt + NQ - w (32 rows each, block 0
+// starting at row T - q0 - 32 NQ), so the first half is the second half it
+// used at tile kt - 1 and the second half is what wavefront w - 1 used
+// then. The workgroup keeps the blocks in a ring of NQ + 1 and stages one
+// new block per tile; each wavefront carries its second-half product over
+// as the next tile's first half (16 instead of 24 score MFMAs per tile) and
+// writes only that half of its diagonal window. The next tile's rows are on
+// their way into registers while the current one is computed, and the
+// output rescale is skipped when no query's running maximum moved.
 template <int NQ, bool ROW_MAJOR>
 __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnArgs args) {
   constexpr int THREADS = 64 * NQ;
-  constexpr int KSTRIDE = kHead + 8;            // halves per staged K / R row (272 bytes)
-  constexpr int RROWS = kTile * NQ + kTile;     // union of the position windows
-  constexpr int KCH = kTile * kHead / 8;        // 16-byte chunks of a K (or V) tile
-  constexpr int RCH = RROWS * kHead / 8;
-  constexpr int CHUNKS = 2 * KCH + RCH;
-  constexpr int PER = (CHUNKS + THREADS - 1) / THREADS;
+  constexpr int KSTRIDE = kHead + 8;     // halves per staged K / R row (272 bytes)
+  constexpr int RING = NQ + 1;           // position blocks of 32 rows held at once
+  constexpr int BCH = kTile * kHead / 8; // 16-byte chunks of one 32-row block
+  constexpr int PER = BCH / THREADS;     // chunks per thread of each of K, V, positions
+  static_assert(BCH % THREADS == 0, "a 32-row block splits evenly over the workgroup");
   __shared__ __attribute__((aligned(16))) _Float16 ks[kTile * KSTRIDE];
   __shared__ __attribute__((aligned(16))) _Float16 vts[kHead * kVtStride];
-  __shared__ __attribute__((aligned(16))) _Float16 rs[RROWS * KSTRIDE];
+  __shared__ __attribute__((aligned(16))) _Float16 rs[RING * kTile * KSTRIDE];
   __shared__ __attribute__((aligned(16))) float windows[NQ * 64 * kTile];
 
   const int tid = threadIdx.x;
@@ -338,95 +355,113 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
   }
 
   const int pmax = (int)args.position_rows - 1;
-  // Chunk c of key tile kt: K rows [0, KCH), V rows [KCH, 2 KCH), R rows.
-  auto fetch = [&](int kt, half8 (&reg)[PER]) {
+  const int pbase = T - q0 - kTile * NQ;  // first row of position block 0
+  auto position_chunk = [&](int block, int c) {
+    const int row = c / (kHead / 8), part = c % (kHead / 8);
+    return load_position<ROW_MAJOR>(positions, args.position_rows, head,
+                                    min(max(pbase + kTile * block + row, 0), pmax), part * 8);
+  };
+  auto store_position = [&](int block, int c, const half8& x) {
+    const int row = c / (kHead / 8), part = c % (kHead / 8);
+    *reinterpret_cast<half8*>(rs + ((block % RING) * kTile + row) * KSTRIDE + part * 8) = x;
+  };
+  // Per key tile kt each thread moves PER chunks of the K rows, of the V
+  // rows and of position block kt + NQ; chunk c is row c / 16, part c % 16.
+  struct Staged {
+    half8 k[PER], v[PER], r[PER];
+  };
+  auto fetch = [&](int kt, Staged& st) {
     const int k0 = kt * kTile;
-    const int pbase = T - q0 - kTile * NQ + k0;  // first row of the union window
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * THREADS;
-      if (c < 2 * KCH) {
-        const int kk = (c % KCH) / (kHead / 8), part = c % (kHead / 8);
-        const int block = c < KCH ? kHidden : 2 * kHidden;
-        reg[i] = load8(qkv + (uint64_t)min(k0 + kk, T - 1) * kQkvRow + block + part * 8);
-      } else if (c < CHUNKS) {
-        const int rc = c - 2 * KCH;
-        const int row = rc / (kHead / 8), part = rc % (kHead / 8);
-        reg[i] = load_position<ROW_MAJOR>(positions, args.position_rows, head, min(max(pbase + row, 0), pmax),
-                                          part * 8);
-      }
+      const _Float16* row = qkv + (uint64_t)min(k0 + c / (kHead / 8), T - 1) * kQkvRow + (c % (kHead / 8)) * 8;
+      st.k[i] = load8(row + kHidden);
+      st.v[i] = load8(row + 2 * kHidden);
+      st.r[i] = position_chunk(kt + NQ, c);
     }
   };
-  auto stage = [&](const half8 (&reg)[PER]) {
+  auto stage = [&](int kt, const Staged& st) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * THREADS;
-      if (c < KCH) {
-        const int kk = c / (kHead / 8), part = c % (kHead / 8);
-        *reinterpret_cast<half8*>(ks + kk * KSTRIDE + part * 8) = reg[i];
-      } else if (c < 2 * KCH) {
-        const int kk = (c - KCH) / (kHead / 8), part = (c - KCH) % (kHead / 8);
-        const int slot = (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+      const int kk = c / (kHead / 8), part = c % (kHead / 8);
+      *reinterpret_cast<half8*>(ks + kk * KSTRIDE + part * 8) = st.k[i];
+      const int slot = (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) vts[(part * 8 + t) * kVtStride + slot] = reg[i][t];
-      } else if (c < CHUNKS) {
-        const int rc = c - 2 * KCH;
-        *reinterpret_cast<half8*>(rs + (rc / (kHead / 8)) * KSTRIDE + (rc % (kHead / 8)) * 8) = reg[i];
-      }
+      for (int t = 0; t < 8; ++t) vts[(part * 8 + t) * kVtStride + slot] = st.v[i][t];
+      store_position(kt + NQ, c, st.r[i]);
     }
   };
 
+  // Position blocks 0 .. NQ-1 for the first tile (block NQ comes with it).
+  for (int c = tid; c < NQ * BCH; c += THREADS) store_position(c / BCH, c % BCH, position_chunk(c / BCH, c % BCH));
+
   float* window = windows + wave * 64 * kTile;
-  const int rbase = kTile * (NQ - 1 - wave);  // this wavefront's window inside the union
   const float scale = 0.08838834764831845f;
   float m = -INFINITY, l = 0.0f;
-  floatx16 o[4];
+  floatx16 o[4], w_prev;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
 
   const int tiles = (live + kTile - 1) / kTile;
-  half8 reg[PER];
-  fetch(0, reg);
+  Staged staged;
+  fetch(0, staged);
   for (int kt = 0; kt < tiles; ++kt) {
     const int k0 = kt * kTile;
     __syncthreads();  // every wavefront is done with the previous tile
-    stage(reg);
+    stage(kt, staged);
     __syncthreads();
-    if (kt + 1 < tiles) fetch(kt + 1, reg);
+    if (kt + 1 < tiles) fetch(kt + 1, staged);
 
-    floatx16 ac, w0, w1;
+    // S^T = K (Q+u)^T; second window half from block kt + NQ - wave.
+    const _Float16* r_new = rs + (((kt + NQ - wave) % RING) * kTile + j) * KSTRIDE;
+    floatx16 ac, w1;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ac[r] = w0[r] = w1[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) ac[r] = w1[r] = 0.0f;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int d0 = 16 * s + 8 * hh;
       const half8 kv = *reinterpret_cast<const half8*>(ks + j * KSTRIDE + d0);
-      const half8 ra = *reinterpret_cast<const half8*>(rs + (rbase + j) * KSTRIDE + d0);
-      const half8 rb = *reinterpret_cast<const half8*>(rs + (rbase + kTile + j) * KSTRIDE + d0);
+      const half8 rb = *reinterpret_cast<const half8*>(r_new + d0);
       ac = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qu[s], ac, 0, 0, 0);
-      w0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra, qv[s], w0, 0, 0, 0);
       w1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(rb, qv[s], w1, 0, 0, 0);
     }
+    // Window half L of tile kt sits in physical half (L + kt) & 1.
+    const int new_half = (1 + kt) & 1;
+    if (kt == 0) {
+      const _Float16* r_old = rs + (((NQ - 1 - wave) % RING) * kTile + j) * KSTRIDE;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int c = 8 * (r / 4) + 4 * hh + (r % 4);
-      window[c * kTile + j] = w0[r];
-      window[(kTile + c) * kTile + j] = w1[r];
+      for (int r = 0; r < 16; ++r) w_prev[r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        w_prev = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(r_old + 16 * s + 8 * hh),
+                                                        qv[s], w_prev, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) window[(8 * (r / 4) + 4 * hh + (r % 4)) * kTile + j] = w_prev[r];
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      window[(new_half * kTile + 8 * (r / 4) + 4 * hh + (r % 4)) * kTile + j] = w1[r];
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     float sc[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = 8 * (r / 4) + 4 * hh + (r % 4);
-      const float rel = window[(kTile - 1 - j + i) * kTile + j];
+      const int c = kTile - 1 - j + i;
+      const float rel = window[((((c >> 5) + kt) & 1) * kTile + (c & 31)) * kTile + j];
       sc[r] = k0 + i < live ? (ac[r] + rel) * scale : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
+    // The running maximum (and with it O and l) moves only when some query's
+    // scores exceed it by more than kRescaleMargin; below that the
+    // probabilities stay under e^8, well inside f16, and O / l is unchanged.
+    const bool moved = __builtin_amdgcn_ballot_w64(mx > m + kRescaleMargin) != 0;
+    const float m_new = moved ? fmaxf(m, mx) : m;
     const float alpha = fast_exp(m - m_new);
     float rsum = 0.0f;
     half8 pb8[2];
@@ -439,16 +474,19 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
     rsum += __shfl_xor(rsum, 32, 64);
     l = l * alpha + rsum;
     m = m_new;
+    if (moved) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const half8 va = *reinterpret_cast<const half8*>(vts + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb8[s], o[db], 0, 0, 0);
       }
-    }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
 
@@ -557,8 +595,9 @@ struct AttnVariant {
   }
 
 // Index 0: up to 256 frames (key tiles split over the workgroup: most
-// workgroups); index 3: longer windows (K, V and positions shared by 64
-// queries).
+// workgroups, 14 us at 4 x 188); index 4: longer windows (K, V and one
+// position block per tile shared by 128 queries: 70 us at 4 x 750 against
+// 101 us for index 0).
 const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
                                     PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
 const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
@@ -566,7 +605,7 @@ const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_
 
 }  // namespace
 
-int attention_default_variant(bool f16, uint32_t frames) { return f16 && frames > 256u ? 3 : 0; }
+int attention_default_variant(bool f16, uint32_t frames) { return f16 && frames > 256u ? 4 : 0; }
 
 int attention_variant_count(bool f16) {
   return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0])) : 1;
