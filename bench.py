@@ -24,6 +24,11 @@ Other workloads (for profiling; same JSON shape):
                     P = table Wpos (6-bit rel-pos linear over 2T-1 sinusoid
                     rows), C = attention(QKV, P, u, v, valid), Y = X + C Wo;
                     TFLOP/s counts the three GEMMs and the attention products
+  encoder           the 24-layer FastConformer encoder stack, fp16, 16 windows x
+                    188 frames (15 s of audio each) x 1024, random-init palette
+                    weights at the reference package's widths, on synthetic
+                    subsampled features; one step = one pass (360 launches,
+                    replayed from a HIP graph); value in audio-sec/sec
 """
 from __future__ import annotations
 
@@ -51,7 +56,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="ff-block",
                    choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
-                            "rel-pos-mha"])
+                            "rel-pos-mha", "encoder"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
@@ -284,6 +289,158 @@ def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
             "sample": f"{done} of {total_rows} {what}", "seconds": dt}
 
 
+WINDOW_SECONDS = 15.0  # audio per encoder window: 1500 fbank frames at 100/s, 8x subsampled to 188
+
+
+def encoder_dispatch_costs(abi, wl, stack):
+    """(flops, algorithmic bytes) of each of the 15 dispatches of one layer
+    over all windows: GEMMs count 2MKN and packed codes + LUT + A + output
+    (+ residual); LayerNorm reads and writes the rows once; the attention and
+    conv tail count what their own launches must move."""
+    rows, frames, batch = stack.x.shape[0], stack.frames, stack.batch
+    act = rows * 1024 * 2
+    ln = (0, 2 * act + 2 * 4096)
+
+    def gemm(name, residual=False):
+        bits, k, n, groups = wl.ENCODER_MATRICES[name]
+        nbytes = k * n * bits // 8 + groups * (1 << bits) * 2 + rows * k * 2 + rows * n * 2
+        return 2 * rows * k * n, nbytes + (rows * n * 2 if residual else 0)
+    live = np.minimum(stack.valid.astype(np.int64), frames)
+    attention = (int((live * live).sum()) * 8 * 128 * 2 * 3,
+                 rows * 3072 * 2 + (2 * frames - 1) * 1024 * 2 + 2 * 4096 + 4 * batch + act)
+    conv = (0, rows * 2048 * 2 + act + 9 * 1024 * 2 + 8 * 1024 + 4 * batch)
+    costs = [ln, gemm("ff1_linear1"), gemm("ff1_linear2", True), ln, gemm("qkv"), attention,
+             gemm("o_proj", True), ln, gemm("pointwise1"), conv, gemm("pointwise2", True), ln,
+             gemm("ff2_linear1"), gemm("ff2_linear2", True), ln]
+    assert len(costs) == len(abi.ENCODER_DISPATCHES)
+    return costs
+
+
+def encoder_cpu_baseline(stack, budget_s=20.0):
+    """The oracle's layer (reference fp16 semantics) on window 0, layer after
+    layer until about `budget_s` seconds have passed."""
+    from oracle import pko
+    threads = min(os.cpu_count() or 1, 16)
+    x = stack.x[:stack.frames]
+    done = 0
+    t0 = time.perf_counter()
+    while done < len(stack.layers) and (done == 0 or time.perf_counter() - t0 < budget_s):
+        x = pko.encoder_layer(x, stack.layers[done], stack.valid[:1], batch=1, frames=stack.frames,
+                              gemm_mode="f16-chain", threads=threads)
+        done += 1
+    dt = time.perf_counter() - t0
+    return {"value": done / len(stack.layers) * WINDOW_SECONDS / dt, "unit": "audio-sec/sec", "cores": threads,
+            "kind": "port",
+            "sample": f"{done} of {len(stack.layers)} layers of one 188-frame window (f16-accumulator GEMM chain, "
+                      "f32 LayerNorm, attention and conv tail: reference fp16 semantics)",
+            "seconds": dt}
+
+
+def run_encoder(args, abi, ctx):
+    import parakeet_wgsl_amd.workloads as wl
+    stack = wl.encoder_stack(0, windows=16, frames=188, layers=24)
+    held = []
+
+    def put(array):
+        held.append(ctx.array(np.ascontiguousarray(array)))
+        return held[-1]
+    layers = []
+    for layer in stack.layers:
+        d = {"norm_gamma": [put(g) for g in layer["norm_gamma"]], "norm_beta": [put(b) for b in layer["norm_beta"]]}
+        for key, value in layer.items():
+            if not key.startswith("norm_"):
+                d[key] = tuple(put(v) for v in value) if isinstance(value, tuple) else put(value)
+        layers.append(d)
+    x, valid = put(stack.x), put(stack.valid)
+    out = ctx.empty(stack.x.shape, np.float16)
+    held.append(out)
+    enc = abi.EncoderOp(ctx, layers=layers, valid_lengths=valid, input=x, output=out, batch_size=stack.batch,
+                        frames=stack.frames, label="encoder")
+    launches, device_bytes = enc.info()
+    stream = ctx.stream
+    for _ in range(args.warmup):
+        enc.enqueue(0, stream, graph=True)
+    ctx.synchronize(stream)
+
+    # Every TIMING_STRIDE-th pass runs eagerly with per-launch stamps; the
+    # others replay the captured graph.
+    timed_steps = list(range(0, args.steps, TIMING_STRIDE))
+    marks = {step: ([ctx.event() for _ in range(launches)], [ctx.event() for _ in range(launches)])
+             for step in timed_steps}
+    start, end = ctx.event(), ctx.event()
+    ctx.synchronize(stream)
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for step in range(args.steps):
+        if step in marks:
+            enc.enqueue_profiled(*marks[step], 0, stream)
+        else:
+            enc.enqueue(0, stream, graph=True)
+    end.record(stream)
+    end.synchronize()
+    ctx.synchronize(stream)
+    wall = time.perf_counter() - wall0
+    ms_per_step = start.elapsed_ms(end) / args.steps
+
+    per = len(abi.ENCODER_DISPATCHES)
+    durations = np.zeros((len(timed_steps), launches))
+    for i, step in enumerate(timed_steps):
+        starts, ends = marks[step]
+        durations[i] = [a.elapsed_ms(b) for a, b in zip(starts, ends)]
+    per_slot = durations.reshape(len(timed_steps), -1, per).mean(axis=(0, 1))  # ms per launch
+    costs = encoder_dispatch_costs(abi, wl, stack)
+    dispatches = {}
+    for j, name in enumerate(abi.ENCODER_DISPATCHES):
+        flops, nbytes = costs[j]
+        us = per_slot[j] * 1e3
+        dispatches[name] = {"avg_us": us, "tflops": flops / (us * 1e-6) / 1e12 if flops else 0.0,
+                            "gbs": nbytes / (us * 1e-6) / 1e9, "flops": flops, "algorithmic_bytes": nbytes}
+    j = int(np.argmax(per_slot))
+    name = abi.ENCODER_DISPATCHES[j]
+    flops, nbytes = costs[j]
+    if flops / (PEAK_TFLOPS["f16"] * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9):
+        roofline = {"bound": "mfma", "achieved": dispatches[name]["tflops"], "peak": PEAK_TFLOPS["f16"],
+                    "unit": "TFLOP/s", "frac": dispatches[name]["tflops"] / PEAK_TFLOPS["f16"]}
+    else:
+        roofline = {"bound": "hbm", "achieved": dispatches[name]["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": dispatches[name]["gbs"] / PEAK_HBM_GBS}
+    roofline["kernel"] = f"encoder.layers.*-{name}"
+    roofline["traffic"] = read_traffic(f"encoder-{name}", None)
+
+    total_flops = stack.gemm_flops() + stack.attention_flops()
+    cpu = None if args.no_cpu else encoder_cpu_baseline(stack)
+    line = {
+        "metric": METRIC,
+        "value": stack.batch * WINDOW_SECONDS / (ms_per_step * 1e-3),
+        "unit": "audio-sec/sec",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random palette codes, LUTs, norms and subsampled features)",
+        "config": {"workload": "fastconformer-encoder-24-layers-fp16", "windows": stack.batch,
+                   "frames": stack.frames, "window_seconds": WINDOW_SECONDS, "layers": len(stack.layers),
+                   "d_model": 1024, "ff_hidden": 4096, "heads": 8, "palette_bits": {"ff/qkv/pointwise": 5, "o_proj": 6},
+                   "launches_per_pass": launches, "graph_replay": True},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
+        "device_bytes": device_bytes,
+        "dispatches": dispatches,
+        "wall_ms_per_step": wall / args.steps * 1e3,
+        "device": ctx.info().name.decode(),
+    }
+    print(json.dumps(line), flush=True)
+    enc.release()
+    for arr in held:
+        arr.free()
+    ctx.close()
+
+
 def read_traffic(gemm_name, kernel_name):
     """HBM bytes per launch of one GEMM of the step, from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per dispatch, each
@@ -294,7 +451,7 @@ def read_traffic(gemm_name, kernel_name):
         return None
     with open(path) as f:
         entry = json.load(f).get("kernels", {}).get(gemm_name)
-    if entry is None or entry.get("kernel") != kernel_name:
+    if entry is None or (kernel_name is not None and entry.get("kernel") != kernel_name):
         return None
     return entry["hbm_bytes_per_launch"]
 
@@ -308,6 +465,9 @@ def main():
 
     import parakeet_wgsl_amd.palette_abi as abi
     ctx = abi.Context(0)
+    if args.workload == "encoder":
+        run_encoder(args, abi, ctx)
+        return
     held = []
 
     def keep(arr):

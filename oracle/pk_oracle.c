@@ -55,8 +55,13 @@ double pko_f16_to_f64(uint16_t h) {
   const int biased = (h >> 10) & 0x1f;
   const int fraction = h & 0x3ff;
   if (biased == 0x1f) return fraction ? NAN : sign * INFINITY;
-  if (biased == 0) return sign * ldexp((double)fraction, -24);
-  return sign * ldexp((double)(fraction | 0x400), biased - 25);
+  if (biased == 0) return sign * (double)fraction * 0x1p-24; /* exact */
+  /* normal: the same sign, exponent and fraction in binary64 fields */
+  const uint64_t bits = ((uint64_t)(h & 0x8000u) << 48) | ((uint64_t)(biased - 15 + 1023) << 52) |
+                        ((uint64_t)fraction << 42);
+  double value;
+  memcpy(&value, &bits, sizeof value);
+  return value;
 }
 
 void pko_f32_to_f16_array(const float *src, uint16_t *dst, uint64_t count) {
@@ -67,10 +72,29 @@ void pko_f16_to_f32_array(const uint16_t *src, float *dst, uint64_t count) {
   for (uint64_t i = 0; i < count; ++i) dst[i] = (float)pko_f16_to_f64(src[i]);
 }
 
-/* Round a double to the nearest binary16 value, returned as a double. */
-static inline double round_to_f16(double value) {
-  return pko_f16_to_f64(pko_f64_to_f16(value));
+/* Round a double to the nearest binary16 value (ties to even), returned as
+   a double. Adding and subtracting C = 1.5 * 2^52 * ulp rounds to a multiple
+   of ulp in the current (round-to-nearest-even) mode; ulp is 2^(e-10) for
+   binary16 normals (2^e <= |v| < 2^(e+1), e >= -14) and 2^-24 below. */
+double pko_round_f16(double value) {
+  uint64_t bits;
+  memcpy(&bits, &value, sizeof bits);
+  const int biased = (int)((bits >> 52) & 0x7ff);
+  if (biased == 0x7ff) return value; /* inf, nan */
+  int ulp_exponent = biased - 1023 - 10;
+  if (ulp_exponent < -24) ulp_exponent = -24;
+  if (ulp_exponent > 5) return (bits >> 63) ? -INFINITY : INFINITY; /* |v| >= 2^16 */
+  const uint64_t c_bits = ((uint64_t)(ulp_exponent + 52 + 1023) << 52) | (1ull << 51);
+  double c;
+  memcpy(&c, &c_bits, sizeof c);
+  const volatile double sum = value + c; /* keep the two roundings apart */
+  const double rounded = sum - c;
+  if (rounded >= 65536.0) return INFINITY;
+  if (rounded <= -65536.0) return -INFINITY;
+  return rounded == 0.0 ? copysign(0.0, value) : rounded;
 }
+
+static inline double round_to_f16(double value) { return pko_round_f16(value); }
 
 /* ------------------------------------------------------------------------ */
 /* Packed code format                                                        */
@@ -266,24 +290,31 @@ static inline double a_value(const pko_gemm_args *p, uint64_t idx) {
              : (double)((const float *)p->a)[idx];
 }
 
+/* Rows are processed in blocks of ROW_BLOCK so each expanded weight row is
+   read once per block rather than once per output row; every output element
+   still accumulates its own products in increasing k, so the arithmetic of
+   each element is that of the one-row loop. */
+#define ROW_BLOCK 8
+
 /* f32 accumulator chain, increasing k, one fused multiply-add per step
    (gemm.ts:2398-2420 acc = fma(vec4<f32>(a), b, acc)). */
 #define F32_CHAIN_BODY                                                       \
   for (uint32_t k = 0; k < K; ++k) {                                         \
-    const float a = (float)a_value(p, (uint64_t)m * K + k);                  \
     const float *wrow = w + (uint64_t)k * N;                                 \
-    for (uint32_t n = 0; n < N; ++n) acc[n] = fmaf(a, wrow[n], acc[n]);      \
+    for (uint32_t r = 0; r < rows; ++r) {                                    \
+      const float a = (float)a_value(p, (uint64_t)(m0 + r) * K + k);         \
+      float *accr = acc + (uint64_t)r * N;                                   \
+      for (uint32_t n = 0; n < N; ++n) accr[n] = fmaf(a, wrow[n], accr[n]);  \
+    }                                                                        \
   }
 
-__attribute__((target("fma"))) static void f32_rows_fma(const pko_gemm_args *p,
-                                                        const float *w,
-                                                        float *acc, uint32_t m) {
+__attribute__((target("fma"))) static void f32_rows_fma(const pko_gemm_args *p, const float *w, float *acc,
+                                                        uint32_t m0, uint32_t rows) {
   const uint32_t K = p->inner, N = p->columns;
   F32_CHAIN_BODY
 }
 
-static void f32_rows_generic(const pko_gemm_args *p, const float *w, float *acc,
-                             uint32_t m) {
+static void f32_rows_generic(const pko_gemm_args *p, const float *w, float *acc, uint32_t m0, uint32_t rows) {
   const uint32_t K = p->inner, N = p->columns;
   F32_CHAIN_BODY
 }
@@ -294,22 +325,24 @@ static void *gemm_worker(void *opaque) {
   const uint32_t K = p->inner, N = p->columns;
   if (job->mode == PKO_MODE_F32_CHAIN) {
     const float *w = (const float *)job->dense;
-    float *acc = (float *)malloc(sizeof(float) * N);
+    float *acc = (float *)malloc(sizeof(float) * N * ROW_BLOCK);
     const int use_fma = __builtin_cpu_supports("fma");
-    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
-      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0f;
+    for (uint32_t m0 = job->row_begin; m0 < job->row_end; m0 += ROW_BLOCK) {
+      const uint32_t rows = job->row_end - m0 < ROW_BLOCK ? job->row_end - m0 : ROW_BLOCK;
+      for (uint64_t i = 0; i < (uint64_t)rows * N; ++i) acc[i] = 0.0f;
       if (use_fma)
-        f32_rows_fma(p, w, acc, m);
+        f32_rows_fma(p, w, acc, m0, rows);
       else
-        f32_rows_generic(p, w, acc, m);
-      for (uint32_t n = 0; n < N; ++n) {
-        const float v = epilogue_f32(p, acc[n], m, n);
-        const uint64_t idx = (uint64_t)m * N + n;
-        if (p->dtype == PKO_DTYPE_F16)
-          ((uint16_t *)p->out)[idx] = pko_f64_to_f16((double)v);
-        else
-          ((float *)p->out)[idx] = v;
-      }
+        f32_rows_generic(p, w, acc, m0, rows);
+      for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t n = 0; n < N; ++n) {
+          const float v = epilogue_f32(p, acc[(uint64_t)r * N + n], m0 + r, n);
+          const uint64_t idx = (uint64_t)(m0 + r) * N + n;
+          if (p->dtype == PKO_DTYPE_F16)
+            ((uint16_t *)p->out)[idx] = pko_f64_to_f16((double)v);
+          else
+            ((float *)p->out)[idx] = v;
+        }
     }
     free(acc);
   } else if (job->mode == PKO_MODE_F16_CHAIN) {
@@ -318,32 +351,42 @@ static void *gemm_worker(void *opaque) {
        and, below binary16 overflow, so is its sum with a binary16
        accumulator; one round_to_f16 per step is therefore a fused fma. */
     const double *w = (const double *)job->dense;
-    double *acc = (double *)malloc(sizeof(double) * N);
-    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
-      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0;
+    double *acc = (double *)malloc(sizeof(double) * N * ROW_BLOCK);
+    for (uint32_t m0 = job->row_begin; m0 < job->row_end; m0 += ROW_BLOCK) {
+      const uint32_t rows = job->row_end - m0 < ROW_BLOCK ? job->row_end - m0 : ROW_BLOCK;
+      for (uint64_t i = 0; i < (uint64_t)rows * N; ++i) acc[i] = 0.0;
       for (uint32_t k = 0; k < K; ++k) {
-        const double a = a_value(p, (uint64_t)m * K + k);
         const double *wrow = w + (uint64_t)k * N;
-        for (uint32_t n = 0; n < N; ++n) acc[n] = round_to_f16(a * wrow[n] + acc[n]);
+        for (uint32_t r = 0; r < rows; ++r) {
+          const double a = a_value(p, (uint64_t)(m0 + r) * K + k);
+          double *accr = acc + (uint64_t)r * N;
+          for (uint32_t n = 0; n < N; ++n) accr[n] = round_to_f16(a * wrow[n] + accr[n]);
+        }
       }
-      for (uint32_t n = 0; n < N; ++n) {
-        const float v = epilogue_f32(p, (float)acc[n], m, n);
-        ((uint16_t *)p->out)[(uint64_t)m * N + n] = pko_f64_to_f16((double)v);
-      }
+      for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t n = 0; n < N; ++n) {
+          const float v = epilogue_f32(p, (float)acc[(uint64_t)r * N + n], m0 + r, n);
+          ((uint16_t *)p->out)[(uint64_t)(m0 + r) * N + n] = pko_f64_to_f16((double)v);
+        }
     }
     free(acc);
   } else {
     const double *w = (const double *)job->dense;
-    double *acc = (double *)malloc(sizeof(double) * N);
-    for (uint32_t m = job->row_begin; m < job->row_end; ++m) {
-      for (uint32_t n = 0; n < N; ++n) acc[n] = 0.0;
+    double *acc = (double *)malloc(sizeof(double) * N * ROW_BLOCK);
+    for (uint32_t m0 = job->row_begin; m0 < job->row_end; m0 += ROW_BLOCK) {
+      const uint32_t rows = job->row_end - m0 < ROW_BLOCK ? job->row_end - m0 : ROW_BLOCK;
+      for (uint64_t i = 0; i < (uint64_t)rows * N; ++i) acc[i] = 0.0;
       for (uint32_t k = 0; k < K; ++k) {
-        const double a = a_value(p, (uint64_t)m * K + k);
         const double *wrow = w + (uint64_t)k * N;
-        for (uint32_t n = 0; n < N; ++n) acc[n] += a * wrow[n];
+        for (uint32_t r = 0; r < rows; ++r) {
+          const double a = a_value(p, (uint64_t)(m0 + r) * K + k);
+          double *accr = acc + (uint64_t)r * N;
+          for (uint32_t n = 0; n < N; ++n) accr[n] += a * wrow[n];
+        }
       }
-      for (uint32_t n = 0; n < N; ++n)
-        ((double *)p->out)[(uint64_t)m * N + n] = epilogue_f64(p, acc[n], m, n);
+      for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t n = 0; n < N; ++n)
+          ((double *)p->out)[(uint64_t)(m0 + r) * N + n] = epilogue_f64(p, acc[(uint64_t)r * N + n], m0 + r, n);
     }
     free(acc);
   }
@@ -620,5 +663,50 @@ int pko_relative_attention(int dtype, int mode, uint32_t batch, uint32_t frames,
     }
   }
   free(q), free(k), free(v), free(r), free(s);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm (src/webgpu/kernels/layernorm.ts:309-390)                        */
+/* ------------------------------------------------------------------------ */
+
+int pko_layernorm(int dtype, int mode, uint64_t rows, uint32_t channels, const void *input, const float *gamma,
+                  const float *beta, float epsilon, void *output) {
+  if (!input || !gamma || !beta || !output || channels == 0 ||
+      (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64) ||
+      (mode != PKO_MODE_F32_CHAIN && mode != PKO_MODE_F64))
+    return 1;
+  for (uint64_t r = 0; r < rows; ++r) {
+    const uint64_t base = r * channels;
+    if (mode == PKO_MODE_F32_CHAIN) {
+      float sum = 0.0f, square = 0.0f;
+      for (uint32_t c = 0; c < channels; ++c) {
+        const float x = (float)conv_in(dtype, input, base + c);
+        sum += x;
+        square = fmaf(x, x, square);
+      }
+      const float inverse_channels = 1.0f / (float)channels;
+      const float mean = sum * inverse_channels;
+      const float variance = fmaxf(square * inverse_channels - mean * mean, 0.0f);
+      const float inverse_std = 1.0f / sqrtf(variance + epsilon);
+      for (uint32_t c = 0; c < channels; ++c) {
+        const float x = (float)conv_in(dtype, input, base + c);
+        store_out(dtype, output, base + c, (double)((x - mean) * inverse_std * gamma[c] + beta[c]));
+      }
+    } else {
+      double sum = 0.0, square = 0.0;
+      for (uint32_t c = 0; c < channels; ++c) {
+        const double x = conv_in(dtype, input, base + c);
+        sum += x;
+        square += x * x;
+      }
+      const double mean = sum / channels;
+      const double variance = fmax(square / channels - mean * mean, 0.0);
+      const double inverse_std = 1.0 / sqrt(variance + (double)epsilon);
+      for (uint32_t c = 0; c < channels; ++c)
+        store_out(dtype, output, base + c,
+                  (conv_in(dtype, input, base + c) - mean) * inverse_std * gamma[c] + beta[c]);
+    }
+  }
   return 0;
 }

@@ -37,6 +37,10 @@
  *                         a float64 torch restatement, plain attention when the
  *                         positions and biases are zero, the direction of the
  *                         relative shift, one valid key and empty windows.
+ *   pko_layernorm         src/webgpu/kernels/layernorm.ts:309-390 (row mean, biased
+ *                         variance as E[x^2] - mean^2 clamped at 0, rsqrt of
+ *                         variance + epsilon, gamma and beta); pinned by torch's
+ *                         layer_norm, constant rows and the unit-affine moments.
  *   pko_glu               the GLU step of conformer-conv.ts:520-535 on its own
  *                         (value * sigmoid(gate) of a [rows, 2C] input);
  *                         pinned by torch's glu and the gate clamp in
@@ -96,6 +100,9 @@ typedef struct pko_gemm_args {
 
 uint16_t pko_f64_to_f16(double value);
 double pko_f16_to_f64(uint16_t bits);
+/* The nearest binary16 value of `value` (ties to even) as a double; equal to
+   pko_f16_to_f64(pko_f64_to_f16(value)), without the bit assembly. */
+double pko_round_f16(double value);
 void pko_f32_to_f16_array(const float *src, uint16_t *dst, uint64_t count);
 void pko_f16_to_f32_array(const uint16_t *src, float *dst, uint64_t count);
 
@@ -137,6 +144,13 @@ int pko_gemm(const pko_gemm_args *args, int mode, int threads);
 int pko_relative_attention(int dtype, int mode, uint32_t batch, uint32_t frames, const void *qkv,
                            const void *positions, const float *bias_u, const float *bias_v,
                            const uint32_t *valid, void *out);
+
+/* LayerNorm of [rows, channels] (dtype) with gamma, beta [channels] f32:
+   mean = sum / C, variance = max(sum of squares / C - mean^2, 0),
+   out = (x - mean) * rsqrt(variance + epsilon) * gamma + beta; f32 sums in
+   PKO_MODE_F32_CHAIN, double in PKO_MODE_F64; output rounded to dtype. */
+int pko_layernorm(int dtype, int mode, uint64_t rows, uint32_t channels, const void *input, const float *gamma,
+                  const float *beta, float epsilon, void *output);
 
 /* GLU of a [rows, 2*channels] input (values, then gates) into [rows,
    channels]: value * sigmoid(gate) with the reference's clamp, in f32

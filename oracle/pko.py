@@ -15,7 +15,10 @@ Reference functions restated (see pk_oracle.h for the pins):
                   :2356-2599, :2847-2869 (f32)
   conformer_conv  src/webgpu/kernels/conformer-conv.ts:495-573
   glu             the GLU step of conformer-conv.ts:520-535
+  layernorm       src/webgpu/kernels/layernorm.ts:309-390
   relative_attention  src/webgpu/kernels/attention.ts:418-727
+  encoder_layer   the dispatch order of src/webgpu/encoder.ts:1868-2135,
+                  composed from the functions above
 """
 from __future__ import annotations
 
@@ -71,6 +74,8 @@ def lib() -> ctypes.CDLL:
         _lib.pko_f64_to_f16.argtypes = [ctypes.c_double]
         _lib.pko_f16_to_f64.restype = ctypes.c_double
         _lib.pko_f16_to_f64.argtypes = [ctypes.c_uint16]
+        _lib.pko_round_f16.restype = ctypes.c_double
+        _lib.pko_round_f16.argtypes = [ctypes.c_double]
         _lib.pko_pack_codes.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
         _lib.pko_unpack_codes.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
         _lib.pko_palette_group.restype = ctypes.c_uint32
@@ -86,6 +91,8 @@ def lib() -> ctypes.CDLL:
         _lib.pko_conformer_conv.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 6
         _lib.pko_relative_attention.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32] + \
             [ctypes.c_void_p] * 6
+        _lib.pko_layernorm.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32] + \
+            [ctypes.c_void_p] * 3 + [ctypes.c_float, ctypes.c_void_p]
         _lib.pko_glu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p,
                                  ctypes.c_void_p]
     return _lib
@@ -108,6 +115,10 @@ def words_per_group(bits: int) -> int:
 
 def f64_to_f16_bits(value: float) -> int:
     return int(lib().pko_f64_to_f16(float(value)))
+
+
+def round_f16(value: float) -> float:
+    return float(lib().pko_round_f16(float(value)))
 
 
 def f16_bits_to_f64(bits: int) -> float:
@@ -243,6 +254,21 @@ def relative_attention(qkv, positions, bias_u, bias_v, valid, *, batch, frames, 
     return out
 
 
+def layernorm(x, gamma, beta, *, epsilon=1e-5, mode="f32-chain") -> np.ndarray:
+    """LayerNorm over the last axis of a [rows, C] array (layernorm.ts:309-390)."""
+    x = np.ascontiguousarray(x)
+    names = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.float64): "f64"}
+    if x.dtype not in names or x.ndim != 2:
+        raise ValueError("layernorm takes a [rows, C] float16/32/64 array")
+    gamma = np.ascontiguousarray(gamma, dtype=np.float32)
+    beta = np.ascontiguousarray(beta, dtype=np.float32)
+    out = np.empty_like(x)
+    if lib().pko_layernorm(DTYPE[names[x.dtype]], MODE[mode], x.shape[0], x.shape[1], _ptr(x), _ptr(gamma),
+                           _ptr(beta), float(epsilon), _ptr(out)):
+        raise ValueError("layernorm rejected its arguments")
+    return out
+
+
 def glu(pointwise, mode="f32-chain") -> np.ndarray:
     """value * sigmoid(gate) of a [rows, 2C] input (values, then gates), with
     the reference's gate clamp; output [rows, C] in the input's dtype."""
@@ -255,6 +281,55 @@ def glu(pointwise, mode="f32-chain") -> np.ndarray:
     if lib().pko_glu(DTYPE[names[pointwise.dtype]], MODE[mode], rows, channels, _ptr(pointwise), _ptr(out)):
         raise ValueError("glu rejected its arguments")
     return out
+
+
+# name -> (bits, palette groups) of an encoder layer's matrices
+# (model/convert.py:1360-1475, encoder.ts:2458-2512).
+ENCODER_BITS = {"ff1_linear1": 5, "ff1_linear2": 5, "qkv": 5, "o_proj": 6, "pointwise1": 5, "pointwise2": 5,
+                "ff2_linear1": 5, "ff2_linear2": 5}
+
+
+def encoder_layer(x, layer, valid, *, batch, frames, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+    """One FastConformer layer over f16 features x [batch*frames, 1024], in
+    the order of createEncoderLayerDispatches (encoder.ts:1868-2135):
+      x1 = x + 0.5 FF1(LN(x)),  FF(h) = SiLU(h W1) W2
+      x2 = x1 + attention(LN(x1) Wqkv) Wo
+      x3 = x2 + SiLU(BN(DW9(GLU(LN(x2) PW1)))) PW2
+      x4 = x3 + 0.5 FF2(LN(x3));  out = LN(x4)
+    Every intermediate is stored as f16 like the reference's arena. `layer`
+    is keyed like pk_encoder_layer (norm_gamma / norm_beta [5, 1024], each
+    matrix a (packed words, palette) pair). gemm_mode "f16-chain" is the
+    reference's fp16 GEMM arithmetic, "f64" the exact sum rounded once."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+
+    def norm(i, h):
+        return layernorm(h, layer["norm_gamma"][i], layer["norm_beta"][i])
+
+    def mm(name, a, columns, **epilogue):
+        words, palette = layer[name]
+        out = gemm(a, words, ENCODER_BITS[name], palette, columns, mode=gemm_mode, threads=threads, **epilogue)
+        return out.astype(np.float16)
+
+    hidden = mm("ff1_linear1", norm(0, x), 4096, activation="silu")
+    x1 = mm("ff1_linear2", hidden, 1024, residual=x, residual_scale=0.5)
+    qkv = mm("qkv", norm(1, x1), 3072)
+    context = relative_attention(qkv, layer["projected_positions"], layer["bias_u"], layer["bias_v"], valid,
+                                 batch=batch, frames=frames)
+    x2 = mm("o_proj", context, 1024, residual=x1, residual_scale=1.0)
+    pointwise = mm("pointwise1", norm(2, x2), 2048)
+    conv = conformer_conv(pointwise, layer["depthwise"], layer["bn_scale"], layer["bn_shift"], valid,
+                          batch=batch, frames=frames)
+    x3 = mm("pointwise2", conv, 1024, residual=x2, residual_scale=1.0)
+    hidden = mm("ff2_linear1", norm(3, x3), 4096, activation="silu")
+    x4 = mm("ff2_linear2", hidden, 1024, residual=x3, residual_scale=0.5)
+    return norm(4, x4)
+
+
+def encoder(x, layers, valid, *, batch, frames, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+    """The layer stack: encoder_layer applied for each entry of `layers`."""
+    for layer in layers:
+        x = encoder_layer(x, layer, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
+    return x
 
 
 def relative_errors(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:

@@ -223,6 +223,20 @@ AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t
 hipError_t launch_attention(bool f16, int variant, const AttnArgs& args, uint32_t batch, hipStream_t stream,
                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
+// Row LayerNorm (pk_layernorm.hip).
+struct LayerNormArgs {
+  const void* input;   // [rows, channels]
+  const float* gamma;  // [channels]
+  const float* beta;   // [channels]
+  void* output;        // [rows, channels]; may be the input
+  uint32_t rows;       // active rows
+  uint32_t channels;   // multiple of 4
+  float epsilon;
+};
+uint32_t layernorm_grid(uint32_t rows);
+hipError_t launch_layernorm(bool f16, const LayerNormArgs& args, hipStream_t stream, hipEvent_t start = nullptr,
+                            hipEvent_t stop = nullptr);
+
 int conv_variant_count(bool f16);
 ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
                            bool input_glu = false);

@@ -1,4 +1,5 @@
-"""ctypes binding of libpk_palette.so (include/pk_palette.h, pk_conv.h, pk_attention.h).
+"""ctypes binding of libpk_palette.so (include/pk_palette.h, pk_conv.h, pk_attention.h,
+pk_layernorm.h, pk_encoder.h).
 
 A thin Python view of the C ABI, used by the tests and the benchmark. It
 raises PaletteError (or PaletteRangeError, mirroring the reference's
@@ -22,6 +23,16 @@ REQUIRE_PRODUCTION_SIGNATURE = 0x1
 GEMM_GLU = 0x2
 CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
+ENCODER_FUSED_GLU = 0x1
+ENCODER_CHANNELS = 1024
+ENCODER_INTERMEDIATE = 4096
+# The fifteen dispatches of one encoder layer, in launch order
+# (createEncoderLayerDispatches, encoder.ts:1868-2135).
+ENCODER_DISPATCHES = ("norm_feed_forward1", "feed-forward1-linear1", "feed-forward1-linear2-residual",
+                      "norm_self_att", "self-attention-qkv", "relative-attention",
+                      "self-attention-output-residual", "norm_conv", "convolution-pointwise1",
+                      "convolution-glu-depthwise-bn-silu", "convolution-pointwise2-residual", "norm_feed_forward2",
+                      "feed-forward2-linear1", "feed-forward2-linear2-residual", "norm_out")
 EXPAND_LAYOUT = {"row-major": 0, "tile-major": 1}
 
 
@@ -203,6 +214,67 @@ class AttentionPlanInfo(ctypes.Structure):
     ]
 
 
+class LayerNormDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("rows", ctypes.c_uint32),
+        ("channels", ctypes.c_uint32),
+        ("input", ctypes.c_void_p),
+        ("input_bytes", ctypes.c_uint64),
+        ("gamma", ctypes.c_void_p),
+        ("gamma_bytes", ctypes.c_uint64),
+        ("beta", ctypes.c_void_p),
+        ("beta_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+        ("has_epsilon", ctypes.c_int32),
+        ("epsilon", ctypes.c_float),
+    ]
+
+
+class EncoderMatrix(ctypes.Structure):
+    _fields_ = [("packed", ctypes.c_void_p), ("palette", ctypes.c_void_p)]
+
+
+class EncoderLayer(ctypes.Structure):
+    _fields_ = [
+        ("norm_gamma", ctypes.c_void_p * 5),
+        ("norm_beta", ctypes.c_void_p * 5),
+        ("ff1_linear1", EncoderMatrix),
+        ("ff1_linear2", EncoderMatrix),
+        ("qkv", EncoderMatrix),
+        ("projected_positions", ctypes.c_void_p),
+        ("bias_u", ctypes.c_void_p),
+        ("bias_v", ctypes.c_void_p),
+        ("o_proj", EncoderMatrix),
+        ("pointwise1", EncoderMatrix),
+        ("depthwise", ctypes.c_void_p),
+        ("bn_scale", ctypes.c_void_p),
+        ("bn_shift", ctypes.c_void_p),
+        ("pointwise2", EncoderMatrix),
+        ("ff2_linear1", EncoderMatrix),
+        ("ff2_linear2", EncoderMatrix),
+    ]
+
+
+class EncoderDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("frames", ctypes.c_uint32),
+        ("layers", ctypes.c_uint32),
+        ("layer", ctypes.POINTER(EncoderLayer)),
+        ("valid_lengths", ctypes.c_void_p),
+        ("input", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+    ]
+
+
 # Every function the headers declare: name -> (restype, argtypes).
 _VP = ctypes.c_void_p
 _PPV = ctypes.POINTER(ctypes.c_void_p)
@@ -263,6 +335,18 @@ SIGNATURES = {
     "pk_attention_release": (ctypes.c_int, [_VP]),
     "pk_attention_variant_count": (ctypes.c_int, [ctypes.c_int]),
     "pk_attention_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
+    "pk_layernorm_validate": (ctypes.c_int, [ctypes.POINTER(LayerNormDesc)]),
+    "pk_layernorm_create": (ctypes.c_int, [_VP, ctypes.POINTER(LayerNormDesc), _PPV]),
+    "pk_layernorm_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_layernorm_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_layernorm_destroy": (ctypes.c_int, [_VP]),
+    "pk_layernorm_release": (ctypes.c_int, [_VP]),
+    "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
+    "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
+    "pk_encoder_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, ctypes.c_int]),
+    "pk_encoder_enqueue_profiled": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _PPV, _PPV]),
+    "pk_encoder_info": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64)]),
+    "pk_encoder_destroy": (ctypes.c_int, [_VP]),
 }
 
 _lib = None
@@ -610,3 +694,111 @@ class RelativeAttentionOp:
 
 def attention_variant_count(precision: str) -> int:
     return int(load().pk_attention_variant_count(PRECISION[precision]))
+
+
+def layernorm_desc(*, input, gamma, beta, output, rows: int, channels: int, epsilon: float | None = None,
+                   precision: str | None = None, label: str = "layernorm") -> LayerNormDesc:
+    if precision is None:
+        precision = "f16" if input.dtype == np.float16 else "f32"
+    return LayerNormDesc(ctypes.sizeof(LayerNormDesc), label.encode(), PRECISION[precision], rows, channels,
+                         *_slice(input), *_slice(gamma), *_slice(beta), *_slice(output), int(epsilon is not None),
+                         float(epsilon or 0.0))
+
+
+class LayerNormOp:
+    """One LayerNorm dispatch (LayerNormKernel.createDispatch, layernorm.ts:165-240)."""
+
+    def __init__(self, ctx: Context, **descriptor):
+        self.desc = layernorm_desc(**descriptor)
+        handle = ctypes.c_void_p()
+        check(load().pk_layernorm_create(ctx.handle, ctypes.byref(self.desc), ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def enqueue(self, active_rows: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_layernorm_enqueue(self.handle, active_rows, stream))
+        else:
+            check(load().pk_layernorm_enqueue_timed(self.handle, active_rows, stream,
+                                                    start.handle if start else None, end.handle if end else None))
+
+    def destroy(self) -> None:
+        check(load().pk_layernorm_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_layernorm_release(self.handle))
+            self.handle = None
+
+
+_ENCODER_MATRICES = ("ff1_linear1", "ff1_linear2", "qkv", "o_proj", "pointwise1", "pointwise2", "ff2_linear1",
+                     "ff2_linear2")
+_ENCODER_VECTORS = ("projected_positions", "bias_u", "bias_v", "depthwise", "bn_scale", "bn_shift")
+
+
+def _addr(x) -> int | None:
+    """Device address of a DeviceArray, or an integer address as given."""
+    return x.ptr if hasattr(x, "ptr") else x
+
+
+def encoder_layer(weights: dict) -> EncoderLayer:
+    """An EncoderLayer of device pointers from a dict keyed by the
+    pk_encoder_layer field names (`norm_gamma` / `norm_beta` are lists of
+    five; each matrix is a (packed, palette) pair), holding DeviceArrays or
+    integer addresses."""
+    layer = EncoderLayer()
+    for i in range(5):
+        layer.norm_gamma[i] = _addr(weights["norm_gamma"][i])
+        layer.norm_beta[i] = _addr(weights["norm_beta"][i])
+    for name in _ENCODER_MATRICES:
+        packed, palette = weights[name]
+        setattr(layer, name, EncoderMatrix(_addr(packed), _addr(palette)))
+    for name in _ENCODER_VECTORS:
+        setattr(layer, name, _addr(weights[name]))
+    return layer
+
+
+def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = False,
+                 label: str = "encoder") -> EncoderDesc:
+    """An EncoderDesc over `layers` (dicts as encoder_layer takes); the
+    returned structure keeps its layer array alive."""
+    array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
+    desc = EncoderDesc(ctypes.sizeof(EncoderDesc), ENCODER_FUSED_GLU if fused_glu else 0, label.encode(),
+                       PRECISION["f16"], batch_size, frames, len(layers),
+                       ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),
+                       _addr(output))
+    desc._keep = array
+    return desc
+
+
+class EncoderOp:
+    """The encoder layer stack (createEncoderLayerDispatches, encoder.ts:1868-2135)
+    over device tensors."""
+
+    def __init__(self, ctx: Context, stream=None, **descriptor):
+        self.desc = encoder_desc(**descriptor)
+        handle = ctypes.c_void_p()
+        check(load().pk_encoder_create(ctx.handle, ctypes.byref(self.desc), stream, ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def enqueue(self, active_batch: int = 0, stream=None, graph: bool = False) -> None:
+        check(load().pk_encoder_enqueue(self.handle, active_batch, stream, int(graph)))
+
+    def enqueue_profiled(self, starts, ends, active_batch: int = 0, stream=None) -> None:
+        """One eager pass whose launch i stamps starts[i] / ends[i] (Events);
+        both lists hold one entry per launch of the pass."""
+        launches = self.info()[0]
+        if len(starts) != launches or len(ends) != launches:
+            raise ValueError(f"a profiled pass takes {launches} start and end events")
+        start_array = (ctypes.c_void_p * len(starts))(*[ev.handle for ev in starts])
+        end_array = (ctypes.c_void_p * len(ends))(*[ev.handle for ev in ends])
+        check(load().pk_encoder_enqueue_profiled(self.handle, active_batch, stream, start_array, end_array))
+
+    def info(self) -> tuple[int, int]:
+        launches, device_bytes = ctypes.c_uint32(), ctypes.c_uint64()
+        check(load().pk_encoder_info(self.handle, ctypes.byref(launches), ctypes.byref(device_bytes)))
+        return launches.value, device_bytes.value
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_encoder_destroy(self.handle))
+            self.handle = None

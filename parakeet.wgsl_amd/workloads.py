@@ -344,3 +344,96 @@ def mha_module(seed: int = 0, windows: int = 4, frames: int = 188, d_model: int 
     valid = rng.integers((frames + 1) // 2, frames + 1, size=windows).astype(np.uint32)
     table = relative_position_table(frames, d_model).astype(np.float16)
     return MhaModule(x, wqkv, wpos, wo, table, bias_u, bias_v, valid, windows, frames)
+
+
+# Encoder layer matrices: name -> (bits, inner, columns, palette groups), the
+# reference package's widths (model/convert.py:1360-1475, encoder.ts:2458-2512).
+ENCODER_MATRICES = {
+    "ff1_linear1": (5, 1024, 4096, 1),
+    "ff1_linear2": (5, 4096, 1024, 1),
+    "qkv": (5, 1024, 3072, 3),
+    "o_proj": (6, 1024, 1024, 1),
+    "pointwise1": (5, 1024, 2048, 1),
+    "pointwise2": (5, 1024, 1024, 1),
+    "ff2_linear1": (5, 1024, 4096, 1),
+    "ff2_linear2": (5, 4096, 1024, 1),
+}
+
+
+def random_packed_words(rng: np.random.Generator, bits: int, inner: int, columns: int) -> np.ndarray:
+    """Packed words of uniformly random codes: every bit of a packed group is
+    a code bit, so uniform words are uniform codes."""
+    count = inner * columns // codes_per_group(bits) * words_per_group(bits)
+    return rng.integers(0, 1 << 32, size=count, dtype=np.uint32)
+
+
+@dataclass
+class EncoderStack:
+    """Random-init FastConformer encoder layers over subsampled features
+    x [windows*frames, 1024] f16. Each layer is a dict keyed like
+    pk_encoder_layer: norm_gamma / norm_beta [5, 1024] f32; each matrix of
+    ENCODER_MATRICES a (packed words, palette [G, 2^bits] f16) pair;
+    projected_positions in head-vector-position-vec4 order [8, 32, 2T-1, 4]
+    f16; bias_u, bias_v [8, 128] f32; depthwise [9, 1024] f16; bn_scale,
+    bn_shift [1024] f32."""
+    x: np.ndarray
+    layers: list
+    valid: np.ndarray
+    batch: int
+    frames: int
+
+    def gemm_flops(self, batch: int | None = None) -> int:
+        rows = (self.batch if batch is None else batch) * self.frames
+        per_layer = sum(2 * rows * k * n for _, k, n, _ in ENCODER_MATRICES.values())
+        return per_layer * len(self.layers)
+
+    def attention_flops(self, batch: int | None = None) -> int:
+        batch = self.batch if batch is None else batch
+        live = np.minimum(self.valid[:batch].astype(np.int64), self.frames)
+        return int((live * live).sum()) * 8 * 128 * 2 * 3 * len(self.layers)
+
+    def weight_bytes(self) -> int:
+        """Package bytes the stack reads per pass: packed codes, LUTs,
+        positions, norms, biases, depthwise and folded batch norm."""
+        total = 0
+        for layer in self.layers:
+            for name in ENCODER_MATRICES:
+                packed, palette = layer[name]
+                total += packed.nbytes + palette.nbytes
+            for name in ("norm_gamma", "norm_beta", "projected_positions", "bias_u", "bias_v", "depthwise",
+                         "bn_scale", "bn_shift"):
+                total += layer[name].nbytes
+        return total
+
+
+def encoder_layer_weights(rng: np.random.Generator, frames: int, lut_std: float = 0.02) -> dict:
+    layer = {
+        "norm_gamma": (1.0 + 0.1 * rng.standard_normal((5, 1024))).astype(np.float32),
+        "norm_beta": (0.1 * rng.standard_normal((5, 1024))).astype(np.float32),
+    }
+    for name, (bits, inner, columns, groups) in ENCODER_MATRICES.items():
+        layer[name] = (random_packed_words(rng, bits, inner, columns),
+                       normal(rng, (groups, 1 << bits), lut_std, np.float16))
+    layer["projected_positions"] = pack_projected_positions(normal(rng, (2 * frames - 1, 1024), 0.6, np.float16))
+    layer["bias_u"] = normal(rng, (8, 128), 0.02, np.float32)
+    layer["bias_v"] = normal(rng, (8, 128), 0.02, np.float32)
+    layer["depthwise"] = normal(rng, (9, 1024), 0.05, np.float16)
+    layer["bn_scale"] = (1.0 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    layer["bn_shift"] = (0.1 * rng.standard_normal(1024)).astype(np.float32)
+    return layer
+
+
+def encoder_stack(seed: int = 0, windows: int = 16, frames: int = 188, layers: int = 24,
+                  valid=None) -> EncoderStack:
+    """Subsampled features [windows x frames x 1024] f16 ~ N(0,1) and
+    `layers` random layers: uniform 5/6-bit codes with LUTs ~ N(0, 0.02)
+    (QKV with one LUT per Q/K/V block), LayerNorm gamma ~ 1 + N(0, 0.1) and
+    beta ~ N(0, 0.1), projected positions ~ N(0, 0.6), u, v ~ N(0, 0.02),
+    depthwise ~ N(0, 0.05), folded BN scale ~ 1 + N(0, 0.1) and shift ~
+    N(0, 0.1); valid lengths uniform integers in [ceil(T/2), T] unless given."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (windows * frames, 1024), 1.0, np.float16)
+    if valid is None:
+        valid = rng.integers((frames + 1) // 2, frames + 1, size=windows)
+    stack = [encoder_layer_weights(rng, frames) for _ in range(layers)]
+    return EncoderStack(x, stack, np.asarray(valid, dtype=np.uint32), windows, frames)

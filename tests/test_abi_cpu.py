@@ -57,9 +57,12 @@ def test_struct_layouts_match_the_c_compiler(abi, tmp_path):
                "pk_expand_desc": abi.ExpandDesc, "pk_gemm_plan_info": abi.PlanInfo,
                "pk_device_info": abi.DeviceInfo, "pk_conv_desc": abi.ConvDesc,
                "pk_conv_plan_info": abi.ConvPlanInfo, "pk_attention_desc": abi.AttentionDesc,
-               "pk_attention_plan_info": abi.AttentionPlanInfo}
+               "pk_attention_plan_info": abi.AttentionPlanInfo, "pk_layernorm_desc": abi.LayerNormDesc,
+               "pk_encoder_matrix": abi.EncoderMatrix, "pk_encoder_layer": abi.EncoderLayer,
+               "pk_encoder_desc": abi.EncoderDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', '#include "pk_conv.h"',
-             '#include "pk_attention.h"', "int main(void) {"]
+             '#include "pk_attention.h"', '#include "pk_layernorm.h"', '#include "pk_encoder.h"',
+             "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
         for field, _ in cls._fields_:
@@ -320,3 +323,122 @@ def test_attention_null_handles(abi):
     assert lib.pk_attention_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
     assert lib.pk_attention_destroy(None) == abi.OK
     assert abi.attention_variant_count("f16") == 5 and abi.attention_variant_count("f32") == 1
+
+
+# ---------------------------------------------------------------- LayerNorm
+
+
+def _ln_fakes(rows=3008, channels=1024, elem=2):
+    dtype = np.float16 if elem == 2 else np.float32
+    return dict(input=_Fake(0x10000000, rows * channels * elem, dtype), gamma=_Fake(0x20000000, channels * 4),
+                beta=_Fake(0x20100000, channels * 4), output=_Fake(0x30000000, rows * channels * elem, dtype),
+                rows=rows, channels=channels, label="encoder.layers.0.norm_feed_forward1")
+
+
+def _validate_ln(abi, **kw):
+    desc = abi.layernorm_desc(**kw)
+    abi.check(abi.load().pk_layernorm_validate(ctypes.byref(desc)))
+
+
+def test_layernorm_contract_messages(abi):
+    """layernorm.ts:165-281: shape (RangeError), arena capacity (RangeError),
+    packed affine tensors (Error); in place is allowed."""
+    _validate_ln(abi, **_ln_fakes())
+    kw = _ln_fakes()
+    kw["output"] = kw["input"]
+    _validate_ln(abi, **kw)
+    kw = _ln_fakes()
+    kw["channels"] = 1022
+    with pytest.raises(abi.PaletteRangeError, match="Invalid LayerNorm shape for encoder.layers.0.norm_feed_forward1"):
+        _validate_ln(abi, **kw)
+    kw = _ln_fakes()
+    kw["output"] = _Fake(kw["output"].ptr, 100)
+    with pytest.raises(abi.PaletteRangeError, match=re.escape(
+            "encoder.layers.0.norm_feed_forward1 output needs 6160384 bytes; arena slice has 100")):
+        _validate_ln(abi, **kw)
+    kw = _ln_fakes()
+    kw["beta"] = _Fake(kw["beta"].ptr, 2048)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "encoder.layers.0.norm_feed_forward1 beta must be float32 channel logical/storage [1024], 4096 bytes")):
+        _validate_ln(abi, **kw)
+
+
+# ---------------------------------------------------------------- encoder stack
+
+
+def _encoder_fakes(layers=2, batch=16, frames=188):
+    """Nominal, aligned device addresses for every tensor of the stack."""
+    at = [0x1000000000]
+
+    def take(nbytes=1 << 20):
+        addr = at[0]
+        at[0] += (nbytes + 0xFFFF) // 0x10000 * 0x10000
+        return addr
+
+    stack = []
+    for _ in range(layers):
+        layer = {"norm_gamma": [take() for _ in range(5)], "norm_beta": [take() for _ in range(5)]}
+        for name in ("ff1_linear1", "ff1_linear2", "qkv", "o_proj", "pointwise1", "pointwise2", "ff2_linear1",
+                     "ff2_linear2"):
+            layer[name] = (take(4 << 20), take())
+        for name in ("projected_positions", "bias_u", "bias_v", "depthwise", "bn_scale", "bn_shift"):
+            layer[name] = take()
+        stack.append(layer)
+    rows = batch * frames
+    return dict(layers=stack, valid_lengths=take(), input=take(rows * 2048), output=take(rows * 2048),
+                batch_size=batch, frames=frames)
+
+
+def _validate_encoder(abi, **kw):
+    desc = abi.encoder_desc(**kw)
+    abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+
+
+@pytest.mark.parametrize("fused_glu", [False, True])
+def test_encoder_validate_accepts_the_reference_stack(abi, fused_glu):
+    """24 layers x 16 windows x 188 frames (encoder.ts:62, :68), and T=750."""
+    _validate_encoder(abi, fused_glu=fused_glu, **_encoder_fakes(layers=24))
+    _validate_encoder(abi, fused_glu=fused_glu, **_encoder_fakes(layers=1, batch=4, frames=750))
+
+
+def test_encoder_validate_names_the_failing_op(abi):
+    kw = _encoder_fakes()
+    kw["layers"][1]["qkv"] = (kw["layers"][1]["qkv"][0], 0)
+    with pytest.raises(abi.PaletteError, match=re.escape("encoder.layers.1-self-attention-qkv")):
+        _validate_encoder(abi, **kw)
+    kw = _encoder_fakes()
+    kw["layers"][0]["depthwise"] += 2  # misaligned vec4 tensor
+    with pytest.raises(abi.PaletteError, match=re.escape("encoder.layers.0-convolution-glu-depthwise-bn-silu")):
+        _validate_encoder(abi, **kw)
+    kw = _encoder_fakes(frames=4097)
+    with pytest.raises(abi.PaletteError, match="encoder.layers.0-relative-attention"):
+        _validate_encoder(abi, **kw)
+
+
+def test_encoder_validate_stack_fields(abi):
+    with pytest.raises(abi.PaletteRangeError, match="Unsupported encoder shape"):
+        _validate_encoder(abi, **_encoder_fakes(layers=0))
+    kw = _encoder_fakes()
+    kw["output"] = kw["input"] + 4096
+    with pytest.raises(abi.PaletteError, match="must not overlap its input"):
+        _validate_encoder(abi, **kw)
+    kw = _encoder_fakes()
+    kw["input"] += 8
+    with pytest.raises(abi.PaletteError, match="16-byte aligned"):
+        _validate_encoder(abi, **kw)
+    desc = abi.encoder_desc(**_encoder_fakes())
+    desc.precision = abi.PRECISION["f32"]
+    with pytest.raises(abi.PaletteError, match="runs in f16"):
+        abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+    desc = abi.encoder_desc(**_encoder_fakes())
+    desc.flags = 0x8
+    with pytest.raises(abi.PaletteError, match="unknown flags"):
+        abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+
+
+def test_encoder_null_handles(abi):
+    lib = abi.load()
+    assert lib.pk_encoder_enqueue(None, 0, None, 0) == abi.INVALID_ARGUMENT
+    assert lib.pk_encoder_info(None, None, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_encoder_destroy(None) == abi.OK
+    assert lib.pk_encoder_validate(None) == abi.INVALID_ARGUMENT

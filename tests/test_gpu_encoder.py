@@ -1,0 +1,195 @@
+"""Parity of the encoder layer stack (pk_encoder: createEncoderLayerDispatches,
+src/webgpu/encoder.ts:1868-2135) against the oracle's composition of the
+same ops (pko.encoder_layer), with f16 storage between ops as in the
+reference's arena.
+
+The oracle runs two chains: "f16-chain" GEMMs accumulate in binary16 as the
+reference's fp16 shaders do (gemm.ts:1445-1481); "f64" GEMMs sum exactly and
+round once. The device accumulates in f32, so it sits between the two and
+much nearer the exact chain. Bars (norm-wise relative error, the fp16
+tolerance of the palette GEMM path):
+  one layer:  <= 1e-2 against either chain;
+  8 layers:   <= 1e-2 against the f64 chain, and no farther from the
+              reference's f16 chain than the f64 chain itself is (x1.1);
+  24 layers:  <= 1e-2 against the f64 chain.
+Everything the stack does per window is independent of the other windows,
+so the full-size run also checks a window permutation (bit-exact), the
+active prefix, and graph replay against eager launches (bit-exact)."""
+import numpy as np
+import pytest
+
+from test_gpu_parity import Scope
+
+pytestmark = pytest.mark.gpu
+
+THREADS = 16
+
+
+@pytest.fixture
+def scope(ctx):
+    s = Scope(ctx)
+    yield s
+    s.close()
+
+
+def upload_layers(scope, layers):
+    """Device copies of each layer dict, keyed like pk_encoder_layer."""
+    out = []
+    for layer in layers:
+        d = {"norm_gamma": [scope.put(np.ascontiguousarray(g)) for g in layer["norm_gamma"]],
+             "norm_beta": [scope.put(np.ascontiguousarray(b)) for b in layer["norm_beta"]]}
+        for key, value in layer.items():
+            if key.startswith("norm_"):
+                continue
+            d[key] = tuple(scope.put(v) for v in value) if isinstance(value, tuple) else scope.put(value)
+        out.append(d)
+    return out
+
+
+class Stack:
+    """An EncoderOp over uploaded layers with its input, output and lengths."""
+
+    def __init__(self, abi, ctx, scope, stack, *, fused_glu=False):
+        self.ctx = ctx
+        self.input = scope.put(stack.x)
+        self.valid = scope.put(stack.valid)
+        self.output = scope.put(np.full_like(stack.x, 77))
+        self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
+                                input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
+                                fused_glu=fused_glu)
+
+    def run(self, active=0, graph=False):
+        self.op.enqueue(active, graph=graph)
+        self.ctx.synchronize()
+        return self.output.download()
+
+    def release(self):
+        self.op.release()
+
+
+def windows(array, frames, first, count):
+    return array[first * frames:(first + count) * frames]
+
+
+@pytest.mark.parametrize("fused_glu", [False, True], ids=["pw1-then-glu", "glu-epilogue"])
+def test_encoder_layer_matches_both_oracle_chains(abi, ctx, scope, oracle, workloads, fused_glu):
+    stack = workloads.encoder_stack(seed=11, windows=2, frames=188, layers=1)
+    enc = Stack(abi, ctx, scope, stack, fused_glu=fused_glu)
+    try:
+        assert enc.op.info()[0] == 15
+        got = enc.run()
+    finally:
+        enc.release()
+    assert np.isfinite(got).all()
+    for mode in ("f16-chain", "f64"):
+        want = oracle.encoder(stack.x, stack.layers, stack.valid, batch=2, frames=188, gemm_mode=mode,
+                              threads=THREADS)
+        norm, worst = oracle.relative_errors(got, want)
+        print(f"one layer, fused_glu={fused_glu}, vs {mode}: norm {norm:.2e} max {worst:.2e}", flush=True)
+        assert norm <= 1e-2, (mode, norm, worst)
+
+
+def test_encoder_two_layers_at_750_frames(abi, ctx, scope, oracle, workloads):
+    """The flash-style attention inside the stack at T=750 (4 x 188 + 2),
+    with one short window."""
+    stack = workloads.encoder_stack(seed=12, windows=2, frames=750, layers=2, valid=[750, 377])
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        got = enc.run()
+    finally:
+        enc.release()
+    want = oracle.encoder(stack.x, stack.layers, stack.valid, batch=2, frames=750, gemm_mode="f64",
+                          threads=THREADS)
+    norm, worst = oracle.relative_errors(got, want)
+    print(f"two layers at T=750 vs f64: norm {norm:.2e} max {worst:.2e}", flush=True)
+    assert norm <= 1e-2, (norm, worst)
+
+
+def test_encoder_24_layers_full_size(abi, ctx, scope, oracle, workloads):
+    """16 windows x 188 frames x 24 layers: graph replay, the active prefix
+    and a window permutation bit-exact, then window 0 against the f64 chain."""
+    stack = workloads.encoder_stack(seed=13, windows=16, frames=188, layers=24)
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        launches, device_bytes = enc.op.info()
+        assert launches == 24 * 15
+        eager = enc.run()
+        assert np.isfinite(eager).all()
+        graph = enc.run(graph=True)
+        np.testing.assert_array_equal(graph.view(np.uint16), eager.view(np.uint16))
+        graph_again = enc.run(graph=True)
+        np.testing.assert_array_equal(graph_again.view(np.uint16), eager.view(np.uint16))
+
+        # active prefix: the first 5 windows alone
+        prefix = enc.run(active=5)
+        np.testing.assert_array_equal(windows(prefix, 188, 0, 5).view(np.uint16),
+                                      windows(eager, 188, 0, 5).view(np.uint16))
+        prefix_graph = enc.run(active=5, graph=True)
+        np.testing.assert_array_equal(windows(prefix_graph, 188, 0, 5).view(np.uint16),
+                                      windows(eager, 188, 0, 5).view(np.uint16))
+
+        # window permutation: outputs move with their windows
+        order = np.roll(np.arange(16), 7)
+        x_perm = stack.x.reshape(16, 188, 1024)[order].reshape(-1, 1024)
+        enc.input.upload(x_perm)
+        enc.valid.upload(stack.valid[order])
+        permuted = enc.run().reshape(16, 188, 1024)
+        np.testing.assert_array_equal(permuted.view(np.uint16), eager.reshape(16, 188, 1024)[order].view(np.uint16))
+    finally:
+        enc.release()
+
+    x0 = windows(stack.x, 188, 0, 1)
+    truth = oracle.encoder(x0, stack.layers, stack.valid[:1], batch=1, frames=188, gemm_mode="f64",
+                           threads=THREADS)
+    norm, worst = oracle.relative_errors(windows(eager, 188, 0, 1), truth)
+    print(f"24 layers vs f64 chain: norm {norm:.2e} max {worst:.2e}", flush=True)
+    assert norm <= 1e-2, (norm, worst)
+
+
+def test_encoder_eight_layers_against_the_reference_chain(abi, ctx, scope, oracle, workloads):
+    """The reference's own fp16 accumulation drifts from exact sums as layers
+    stack (0.6% after one layer, about 2% after eight on these weights); the
+    device must be no farther from the f16 chain than the exact chain is."""
+    stack = workloads.encoder_stack(seed=16, windows=1, frames=188, layers=8)
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        got = enc.run()
+    finally:
+        enc.release()
+    truth = oracle.encoder(stack.x, stack.layers, stack.valid, batch=1, frames=188, gemm_mode="f64",
+                           threads=THREADS)
+    reference = oracle.encoder(stack.x, stack.layers, stack.valid, batch=1, frames=188, gemm_mode="f16-chain",
+                               threads=THREADS)
+    norm, worst = oracle.relative_errors(got, truth)
+    gap, _ = oracle.relative_errors(truth, reference)
+    norm16, worst16 = oracle.relative_errors(got, reference)
+    print(f"8 layers: vs f64 chain {norm:.2e} (max {worst:.2e}); vs f16 chain {norm16:.2e} (max {worst16:.2e}); "
+          f"f64 chain vs f16 chain {gap:.2e}", flush=True)
+    assert norm <= 1e-2, (norm, worst)
+    assert norm16 <= 1.1 * gap + 1e-3, (norm16, gap)
+
+
+def test_encoder_fused_glu_matches_unfused(abi, ctx, scope, oracle, workloads):
+    """PK_ENCODER_FUSED_GLU only moves the GLU into PW1's epilogue (one more
+    f16 rounding of the GLU); 4 layers stay within 1e-2 of the unfused stack."""
+    stack = workloads.encoder_stack(seed=14, windows=4, frames=188, layers=4)
+    outs = []
+    for fused in (False, True):
+        enc = Stack(abi, ctx, scope, stack, fused_glu=fused)
+        try:
+            outs.append(enc.run())
+        finally:
+            enc.release()
+    norm, worst = oracle.relative_errors(outs[1], outs[0])
+    print(f"fused vs unfused GLU, 4 layers: norm {norm:.2e} max {worst:.2e}", flush=True)
+    assert norm <= 1e-2, (norm, worst)
+
+
+def test_encoder_rejects_bad_active_batch(abi, ctx, scope, workloads):
+    stack = workloads.encoder_stack(seed=15, windows=2, frames=188, layers=1)
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        with pytest.raises(abi.PaletteRangeError, match=r"active batch must be in \[1, 2\]"):
+            enc.op.enqueue(3)
+    finally:
+        enc.release()

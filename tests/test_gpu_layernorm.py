@@ -1,0 +1,65 @@
+"""Parity of the row LayerNorm (layernorm.ts:309-390) against the oracle.
+
+Bars: f16 within one f16 ulp of the oracle's f32 arithmetic rounded to f16,
+or within 2^-20 absolute where (x - mean) * rstd * gamma cancels against
+beta and leaves a value whose ulp is finer than the f32 statistics (the GPU
+sums in a different order and uses v_sqrt/v_rcp); f32 within 1e-5 relative
+(norm- and max-wise)."""
+import numpy as np
+import pytest
+
+from test_gpu_conv import ulp_distance
+from test_gpu_parity import Scope
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def scope(ctx):
+    s = Scope(ctx)
+    yield s
+    s.close()
+
+
+def assert_f16_close(got, want):
+    """One f16 ulp per element, or 2^-20 absolute (cancellation)."""
+    far = np.abs(got.astype(np.float64) - want.astype(np.float64)) > 2.0 ** -20
+    assert ulp_distance(got[far], want[far]) <= 1
+
+
+def run_ln(abi, ctx, scope, x, gamma, beta, *, active=0, in_place=False, epsilon=None):
+    xin = scope.put(x)
+    out = xin if in_place else scope.put(np.full_like(x, 321))
+    op = abi.LayerNormOp(ctx, input=xin, gamma=scope.put(gamma), beta=scope.put(beta), output=out, rows=x.shape[0],
+                         channels=x.shape[1], epsilon=epsilon)
+    try:
+        op.enqueue(active)
+        ctx.synchronize()
+        return out.download()
+    finally:
+        op.release()
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("rows,channels", [(3008, 1024), (7, 1024), (5, 4), (3, 2048), (2, 4096), (9, 260)])
+def test_layernorm_matches_oracle(abi, ctx, scope, oracle, dtype, rows, channels):
+    rng = np.random.default_rng(rows + channels)
+    x = (rng.standard_normal((rows, channels)) * 2 + 0.5).astype(dtype)
+    gamma = (1 + 0.1 * rng.standard_normal(channels)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(channels)).astype(np.float32)
+    got = run_ln(abi, ctx, scope, x, gamma, beta)
+    want = oracle.layernorm(x, gamma, beta)
+    if dtype == np.float16:
+        assert_f16_close(got, want)
+    else:
+        norm, worst = oracle.relative_errors(got, want)
+        assert norm <= 1e-5 and worst <= 1e-5, (norm, worst)
+
+
+def test_layernorm_in_place_active_rows_and_epsilon(abi, ctx, scope, oracle):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((40, 1024)).astype(np.float16)
+    gamma, beta = np.ones(1024, np.float32), np.zeros(1024, np.float32)
+    got = run_ln(abi, ctx, scope, x, gamma, beta, active=25, in_place=True, epsilon=0.5)
+    assert_f16_close(got[:25], oracle.layernorm(x[:25], gamma, beta, epsilon=0.5))
+    np.testing.assert_array_equal(got[25:].view(np.uint16), x[25:].view(np.uint16))

@@ -129,6 +129,25 @@ def test_f16_rounding_every_value_and_midpoint(oracle):
         assert oracle.f64_to_f16_bits(p) == int(np.float16(p).view(np.uint16)), p
 
 
+def test_f16_round_trip_shortcut_matches_numpy(oracle):
+    """pko_round_f16 (the chain GEMM's per-step rounding) against numpy's
+    binary16 cast: every midpoint and its neighbours, subnormals, the
+    overflow threshold, signed zeros and random doubles."""
+    values = np.arange(0x10000, dtype=np.uint16).view(np.float16)
+    pos = np.sort(values[np.isfinite(values) & (values >= 0)].astype(np.float64))
+    mids = (pos[:-1] + pos[1:]) / 2
+    probes = np.concatenate([pos, mids, np.nextafter(mids, 0), np.nextafter(mids, np.inf)])
+    rng = np.random.default_rng(5)
+    probes = np.concatenate([probes, rng.standard_normal(4000) * 10.0 ** rng.uniform(-9, 5, 4000),
+                             [65519.0, 65520.0, 65535.9, 1e300, 2.0**-25, 2.0**-26, 3 * 2.0**-26, 0.0, -0.0]])
+    probes = np.concatenate([probes, -probes])
+    for p in probes[::3]:
+        with np.errstate(over="ignore"):
+            want = float(np.float64(np.float16(p)))
+        got = oracle.round_f16(p)
+        assert got == want and np.signbit(got) == np.signbit(want), (p, got, want)
+
+
 # ---------------------------------------------------------------- geometry
 
 
@@ -599,3 +618,40 @@ def test_relative_attention_one_key_and_empty_windows(oracle, workloads):
     got = _attend(oracle, case, "f32-chain")
     np.testing.assert_array_equal(got[0], case.qkv[0, 2048:])  # one key: probability exactly 1
     assert np.all(got[1:5] == 0) and np.all(got[5:] == 0)
+
+
+# ------------------------------------------------------------- LayerNorm
+
+
+def test_layernorm_matches_torch(oracle):
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((19, 1024)) * 3 + 0.7
+    gamma = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(1024)).astype(np.float32)
+    want = F.layer_norm(torch.from_numpy(x), (1024,), torch.from_numpy(gamma.astype(np.float64)),
+                        torch.from_numpy(beta.astype(np.float64)), eps=1e-5).numpy()
+    np.testing.assert_allclose(oracle.layernorm(x, gamma, beta, mode="f64"), want, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(oracle.layernorm(x.astype(np.float32), gamma, beta), want, rtol=1e-4, atol=1e-4)
+
+
+def test_layernorm_constant_rows_give_beta(oracle):
+    """Zero variance: every output is beta (rsqrt(epsilon) times zero)."""
+    x = np.full((3, 64), 2.5, np.float32)
+    gamma = np.linspace(0.5, 2, 64, dtype=np.float32)
+    beta = np.linspace(-1, 1, 64, dtype=np.float32)
+    for mode in ("f32-chain", "f64"):
+        np.testing.assert_allclose(oracle.layernorm(x, gamma, beta, mode=mode), np.tile(beta, (3, 1)), atol=1e-6)
+
+
+def test_layernorm_unit_affine_moments(oracle):
+    """gamma = 1, beta = 0: each row has mean 0 and variance var / (var + eps)."""
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((5, 256)) * np.array([[0.01], [0.1], [1], [10], [100]])
+    got = oracle.layernorm(x, np.ones(256, np.float32), np.zeros(256, np.float32), mode="f64")
+    var = x.var(axis=1)
+    np.testing.assert_allclose(got.mean(axis=1), 0, atol=1e-12)
+    # E[x^2] - mean^2 (the reference formula) costs a few 1e-9 at scale 100
+    np.testing.assert_allclose(got.var(axis=1), var / (var + 1e-5), rtol=1e-7)
