@@ -12,15 +12,20 @@
  *   LN conv -> PW1 -> GLU/DW9/BN/SiLU -> PW2 + x2     (x3)
  *   LN ff2 -> FF2 W1 + SiLU -> FF2 W2 + 0.5 x3        (x4)
  *   LN out -> next layer
- * and the encode loop that records them for the active windows. The
- * subsampling front end (src/webgpu/kernels/subsampling.ts) and the TDT
- * decoder are not part of this object: its input is the subsampled
- * [windows * frames, 1024] feature block.
+ * and the encode loop that records them for the active windows
+ * (ParakeetEncoderGraph.encode, encoder.ts:1690-1706): optionally the
+ * subsampling front end first (createSubsamplingCommands, encoder.ts:
+ * 2140-2400: fused conv0+depthwise2, pointwise3 + ReLU, depthwise5,
+ * pointwise6 + ReLU, the time mask, the flatten linear), then the layers,
+ * then optionally the projector (encoder.ts:1489-1509). Without the front
+ * end the input is the subsampled [windows * frames, 1024] feature block.
+ * The TDT decoder is not part of this object.
  */
 #ifndef PK_ENCODER_H
 #define PK_ENCODER_H
 
 #include "pk_palette.h"
+#include "pk_subsampling.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -64,6 +69,27 @@ typedef struct pk_encoder_layer {
   pk_encoder_matrix ff2_linear2;
 } pk_encoder_layer;
 
+/* The subsampling front end's package tensors (encoder.subsampling.*,
+   model/convert.py:1264-1340): conv0 and both depthwise kernels [3,3,256]
+   f16 (kh-kw-output-channel-vec4 / kh-kw-channel-vec4) with f32 biases
+   [256]; the 5-bit pointwise matrices 256->256 with f32 biases; the 5-bit
+   flatten linear 4096->1024 (columns in frequency-major order) with its f32
+   bias [1024]. */
+typedef struct pk_encoder_subsampling {
+  const void *conv0_weights;
+  const float *conv0_bias;
+  const void *depthwise2_weights;
+  const float *depthwise2_bias;
+  pk_encoder_matrix pointwise3;
+  const float *pointwise3_bias;
+  const void *depthwise5_weights;
+  const float *depthwise5_bias;
+  pk_encoder_matrix pointwise6;
+  const float *pointwise6_bias;
+  pk_encoder_matrix linear;
+  const float *linear_bias;
+} pk_encoder_subsampling;
+
 typedef struct pk_encoder_desc {
   uint32_t struct_size;          /* sizeof(pk_encoder_desc) */
   uint32_t flags;                /* PK_ENCODER_* */
@@ -74,8 +100,22 @@ typedef struct pk_encoder_desc {
   uint32_t layers;               /* 1..64 */
   const pk_encoder_layer *layer; /* host array of `layers` entries */
   const uint32_t *valid_lengths; /* device [batch] encoder frames per window */
-  const void *input;             /* device [batch*frames, 1024] f16: subsampled features (not modified) */
+  const void *input;             /* device, not modified: [batch*frames, 1024] f16 subsampled features, or
+                                    with `subsampling` the f32 feature-major fbank [batch, 128, feature_frames] */
   void *output;                  /* device [batch*frames, 1024] f16: encoder output, not overlapping input */
+  /* Front end (NULL: none). frames must be pk_subsampling_valid_length(
+     feature_frames, 3) and valid_lengths hold pk_subsampling_valid_length(
+     feature_lengths[i], 3), as uploadValidFeatureLengths derives them
+     (encoder.ts:1555-1582). */
+  const pk_encoder_subsampling *subsampling;
+  uint32_t feature_frames;       /* fbank frames per window (1501 for 15 s) */
+  const uint32_t *feature_lengths; /* device [batch] raw fbank frames per window */
+  /* Projector (projected_channels 0: none): 5-bit palette GEMM
+     1024 -> projected_channels + f32 bias, reading `output`. */
+  pk_encoder_matrix projector;
+  const float *projector_bias;
+  uint32_t projected_channels;   /* reference 640 */
+  void *projected_output;        /* device [batch*frames, projected_channels] f16 */
 } pk_encoder_desc;
 
 /* The descriptor checks of pk_encoder_create, host-only: the stack's own
@@ -94,8 +134,9 @@ int pk_encoder_enqueue(pk_encoder *enc, uint32_t active_batch, void *stream, int
 /* One eager pass whose dispatches stamp timestamps, as the reference's
    profiled encode does (encoder.ts:1641-1674 with timestampWrites per
    dispatch, test/webgpu/encoder-profile.test.ts): `start_events[i]` /
-   `end_events[i]` (from pk_event_create) belong to launch i of the pass,
-   15 per layer in the order above; either array, or any entry, may be NULL. */
+   `end_events[i]` (from pk_event_create) belong to launch i of the pass
+   (pk_encoder_info's count, in order: the six front-end launches, fifteen
+   per layer, the projector); either array, or any entry, may be NULL. */
 int pk_encoder_enqueue_profiled(pk_encoder *enc, uint32_t active_batch, void *stream,
                                 void *const *start_events, void *const *end_events);
 /* Launches in one pass and device bytes held (prepared codes + arena). */

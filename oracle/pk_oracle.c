@@ -710,3 +710,139 @@ int pko_layernorm(int dtype, int mode, uint64_t rows, uint32_t channels, const v
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Subsampling front end (src/webgpu/kernels/subsampling.ts)                 */
+/* ------------------------------------------------------------------------ */
+
+/* fused_subsampled_length / subsampled_length (subsampling.ts:1115-1121,
+   :1283-1289). */
+uint32_t pko_subsampled_length(uint32_t length, uint32_t steps) {
+  for (uint32_t s = 0; s < steps; ++s) length = (uint32_t)(((uint64_t)length + 1u) / 2u);
+  return length;
+}
+
+/* One accumulation step in the storage type's arithmetic: fmaf for the f16
+   and f32 profiles (WGSL fma on vec4<f32>), fma in double for the f64 twin. */
+static inline double acc_step(int dtype, double a, double b, double sum) {
+  if (dtype == PKO_DTYPE_F64) return fma(a, b, sum);
+  return (double)fmaf((float)a, (float)b, (float)sum);
+}
+
+/* Round an intermediate to the storage type (f16 tile, f32 tile, double). */
+static inline double to_storage(int dtype, double v) {
+  if (dtype == PKO_DTYPE_F16) return pko_round_f16(v);
+  if (dtype == PKO_DTYPE_F32) return (double)(float)v;
+  return v;
+}
+
+int pko_subsampling_fused(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                          const float *input, const void *conv0_weights, const float *conv0_bias,
+                          const void *depthwise_weights, const float *depthwise_bias, const uint32_t *valid,
+                          void *output) {
+  if (!input || !conv0_weights || !conv0_bias || !depthwise_weights || !depthwise_bias || !valid || !output ||
+      height == 0 || width == 0 || channels == 0 ||
+      (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64))
+    return 1;
+  const uint32_t h1 = pko_subsampled_length(height, 1), w1 = pko_subsampled_length(width, 1);
+  const uint32_t ho = pko_subsampled_length(h1, 1), wo = pko_subsampled_length(w1, 1);
+  double *conv0 = (double *)malloc(sizeof(double) * (uint64_t)h1 * w1 * channels);
+  if (!conv0) return 1;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t valid1 = pko_subsampled_length(valid[b], 1), valid2 = pko_subsampled_length(valid[b], 2);
+    /* conv0 + ReLU, stored in the tile's type (subsampling.ts:1152-1201) */
+    for (uint32_t y = 0; y < h1; ++y)
+      for (uint32_t x = 0; x < w1; ++x)
+        for (uint32_t c = 0; c < channels; ++c) {
+          double v = 0.0;
+          if (y < valid1) {
+            double sum = conv0_bias[c];
+            for (int ky = 0; ky < 3; ++ky) {
+              const int iy = (int)y * 2 + ky - 1;
+              if (iy < 0 || iy >= (int)height) continue;
+              for (int kx = 0; kx < 3; ++kx) {
+                const int ix = (int)x * 2 + kx - 1;
+                if (ix < 0 || ix >= (int)width) continue;
+                const double w = conv_in(dtype, conv0_weights, ((uint64_t)ky * 3 + kx) * channels + c);
+                const double f = input[((uint64_t)b * width + (uint32_t)ix) * height + (uint32_t)iy];
+                sum = acc_step(dtype, w, f, sum);
+              }
+            }
+            v = to_storage(dtype, sum > 0.0 ? sum : 0.0);
+          }
+          conv0[((uint64_t)y * w1 + x) * channels + c] = v;
+        }
+    /* depthwise2 (subsampling.ts:1205-1238) */
+    for (uint32_t y = 0; y < ho; ++y)
+      for (uint32_t x = 0; x < wo; ++x)
+        for (uint32_t c = 0; c < channels; ++c) {
+          const uint64_t out_idx = (((uint64_t)b * ho + y) * wo + x) * channels + c;
+          if (y >= valid2) {
+            store_out(dtype, output, out_idx, 0.0);
+            continue;
+          }
+          double sum = depthwise_bias[c];
+          for (int ky = 0; ky < 3; ++ky) {
+            const int iy = (int)y * 2 + ky - 1;
+            if (iy < 0 || iy >= (int)h1 || iy >= (int)valid1) continue;
+            for (int kx = 0; kx < 3; ++kx) {
+              const int ix = (int)x * 2 + kx - 1;
+              if (ix < 0 || ix >= (int)w1) continue;
+              const double w = conv_in(dtype, depthwise_weights, ((uint64_t)ky * 3 + kx) * channels + c);
+              sum = acc_step(dtype, conv0[((uint64_t)iy * w1 + (uint32_t)ix) * channels + c], w, sum);
+            }
+          }
+          store_out(dtype, output, out_idx, sum);
+        }
+  }
+  free(conv0);
+  return 0;
+}
+
+int pko_subsampling_depthwise(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                              const void *input, const void *weights, const float *bias, const uint32_t *valid,
+                              uint32_t steps, void *output) {
+  if (!input || !weights || !bias || !valid || !output || height == 0 || width == 0 || channels == 0 ||
+      steps == 0 || (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64))
+    return 1;
+  const uint32_t ho = pko_subsampled_length(height, 1), wo = pko_subsampled_length(width, 1);
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t valid_in = pko_subsampled_length(valid[b], steps - 1);
+    const uint32_t valid_out = pko_subsampled_length(valid[b], steps);
+    for (uint32_t y = 0; y < ho; ++y)
+      for (uint32_t x = 0; x < wo; ++x)
+        for (uint32_t c = 0; c < channels; ++c) {
+          const uint64_t out_idx = (((uint64_t)b * ho + y) * wo + x) * channels + c;
+          if (y >= valid_out) {
+            store_out(dtype, output, out_idx, 0.0);
+            continue;
+          }
+          double sum = bias[c];
+          for (int ky = 0; ky < 3; ++ky) {
+            const int iy = (int)y * 2 + ky - 1;
+            if (iy < 0 || iy >= (int)height || iy >= (int)valid_in) continue;
+            for (int kx = 0; kx < 3; ++kx) {
+              const int ix = (int)x * 2 + kx - 1;
+              if (ix < 0 || ix >= (int)width) continue;
+              const double v =
+                  conv_in(dtype, input, (((uint64_t)b * height + (uint32_t)iy) * width + (uint32_t)ix) * channels + c);
+              sum = acc_step(dtype, v, conv_in(dtype, weights, ((uint64_t)ky * 3 + kx) * channels + c), sum);
+            }
+          }
+          store_out(dtype, output, out_idx, sum);
+        }
+  }
+  return 0;
+}
+
+int pko_subsampling_mask(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                         void *values, const uint32_t *valid, uint32_t steps) {
+  if (!values || !valid || (dtype != PKO_DTYPE_F16 && dtype != PKO_DTYPE_F32 && dtype != PKO_DTYPE_F64)) return 1;
+  const uint64_t frame = (uint64_t)width * channels;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t keep = pko_subsampled_length(valid[b], steps);
+    for (uint32_t y = keep; y < height; ++y)
+      for (uint64_t i = 0; i < frame; ++i) store_out(dtype, values, ((uint64_t)b * height + y) * frame + i, 0.0);
+  }
+  return 0;
+}

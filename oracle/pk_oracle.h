@@ -50,6 +50,18 @@
  *                         frames, folded batch norm, SiLU); pinned by closed
  *                         forms in tests/test_oracle.py (one-hot taps, zero
  *                         gates, frames past the valid length, the f64 twin).
+ *   pko_subsampled_length src/webgpu/kernels/subsampling.ts:119-135 and the
+ *                         shaders' (length + 1) / 2 per stride-2 step; pinned by
+ *                         test/webgpu/subsampling-kernel-shapes.test.ts:27-50.
+ *   pko_subsampling_fused src/webgpu/kernels/subsampling.ts:1092-1239 (conv0
+ *                         1->C 3x3 stride 2 pad 1 + ReLU, rounded to the
+ *                         storage type, then depthwise 3x3 stride 2 + bias);
+ *   pko_subsampling_depthwise  subsampling.ts:1241-1330 (channel-last depthwise
+ *                         3x3 stride 2 + bias, no activation);
+ *   pko_subsampling_mask  subsampling.ts:1332-1430 (zero the frames at or past
+ *                         the subsampled valid length); the three are pinned by
+ *                         torch's conv2d in float64, one-hot kernels and the
+ *                         length edges in tests/test_oracle.py.
  *
  * Status codes: 0 ok, 1 invalid argument.
  */
@@ -161,6 +173,40 @@ int pko_glu(int dtype, int mode, uint64_t rows, uint32_t channels, const void *i
 int pko_conformer_conv(int dtype, int mode, uint32_t batch, uint32_t frames, uint32_t channels,
                        const void *input, const void *weights, const float *scale,
                        const float *shift, const uint32_t *valid, void *output);
+
+/* Length after `steps` same-padded stride-2 3x3 convolutions:
+   length = (length + 1) / 2 per step (floor((n + 2 - 3) / 2) + 1). */
+uint32_t pko_subsampled_length(uint32_t length, uint32_t steps);
+
+/* Fused conv0 + depthwise2 of the subsampling front end. input: f32
+   feature-major [batch, width, height] (width = mel bins, height = frames);
+   conv0_weights, depthwise_weights: [3, 3, channels] (dtype); biases f32
+   [channels]; valid: raw frame lengths [batch]; output (dtype) channel-last
+   [batch, Ho, Wo, channels] with H1 = sub(height), W1 = sub(width), Ho =
+   sub(H1), Wo = sub(W1). conv0 at (y, x) for y < min(H1, sub(L, 1)):
+   bias + fma over taps (ky, kx) in order, skipping taps outside the input,
+   then ReLU, rounded to dtype (f16 storage) or kept (f32, f64); zero
+   elsewhere. Output rows y >= sub(L, 2) are zero; the others are bias + fma
+   over the in-range conv0 taps (rows below sub(L, 1)), rounded to dtype.
+   dtype PKO_DTYPE_F64 computes in double throughout. */
+int pko_subsampling_fused(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                          const float *input, const void *conv0_weights, const float *conv0_bias,
+                          const void *depthwise_weights, const float *depthwise_bias, const uint32_t *valid,
+                          void *output);
+
+/* Channel-last depthwise 3x3 stride-2 pad-1 convolution [batch, height,
+   width, channels] -> [batch, sub(height), sub(width), channels] (dtype):
+   output rows y >= sub(L, steps) are zero; the others are bias + fma over
+   the taps in order, skipping input rows outside [0, min(height,
+   sub(L, steps - 1))) and columns outside [0, width). */
+int pko_subsampling_depthwise(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                              const void *input, const void *weights, const float *bias, const uint32_t *valid,
+                              uint32_t steps, void *output);
+
+/* Zero, in place, the rows y >= sub(L, steps) of [batch, height, width,
+   channels] values (dtype). */
+int pko_subsampling_mask(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
+                         void *values, const uint32_t *valid, uint32_t steps);
 
 #ifdef __cplusplus
 }

@@ -17,8 +17,15 @@ Reference functions restated (see pk_oracle.h for the pins):
   glu             the GLU step of conformer-conv.ts:520-535
   layernorm       src/webgpu/kernels/layernorm.ts:309-390
   relative_attention  src/webgpu/kernels/attention.ts:418-727
+  subsampled_length       src/webgpu/kernels/subsampling.ts:119-135
+  subsampling_fused       subsampling.ts:1092-1239 (conv0 + ReLU + depthwise2)
+  subsampling_depthwise   subsampling.ts:1241-1330
+  subsampling_mask        subsampling.ts:1332-1430
   encoder_layer   the dispatch order of src/webgpu/encoder.ts:1868-2135,
                   composed from the functions above
+  encoder_front_end  createSubsamplingCommands, encoder.ts:2140-2400
+  encoder_graph   ParakeetEncoderGraph.encode, encoder.ts:1690-1706 (front
+                  end, layers, projector)
 """
 from __future__ import annotations
 
@@ -74,6 +81,8 @@ def lib() -> ctypes.CDLL:
         _lib.pko_f64_to_f16.argtypes = [ctypes.c_double]
         _lib.pko_f16_to_f64.restype = ctypes.c_double
         _lib.pko_f16_to_f64.argtypes = [ctypes.c_uint16]
+        _lib.pko_subsampled_length.restype = ctypes.c_uint32
+        _lib.pko_subsampled_length.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         _lib.pko_round_f16.restype = ctypes.c_double
         _lib.pko_round_f16.argtypes = [ctypes.c_double]
         _lib.pko_pack_codes.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
@@ -95,6 +104,11 @@ def lib() -> ctypes.CDLL:
             [ctypes.c_void_p] * 3 + [ctypes.c_float, ctypes.c_void_p]
         _lib.pko_glu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p,
                                  ctypes.c_void_p]
+        _lib.pko_subsampling_fused.argtypes = [ctypes.c_int] + [ctypes.c_uint32] * 4 + [ctypes.c_void_p] * 7
+        _lib.pko_subsampling_depthwise.argtypes = [ctypes.c_int] + [ctypes.c_uint32] * 4 + [ctypes.c_void_p] * 4 + \
+            [ctypes.c_uint32, ctypes.c_void_p]
+        _lib.pko_subsampling_mask.argtypes = [ctypes.c_int] + [ctypes.c_uint32] * 4 + [ctypes.c_void_p] * 2 + \
+            [ctypes.c_uint32]
     return _lib
 
 
@@ -283,6 +297,66 @@ def glu(pointwise, mode="f32-chain") -> np.ndarray:
     return out
 
 
+_NAMES = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.float64): "f64"}
+
+
+def subsampled_length(length: int, steps: int) -> int:
+    """Frames left after `steps` same-padded stride-2 convolutions."""
+    return int(lib().pko_subsampled_length(int(length), int(steps)))
+
+
+def subsampling_fused(features, conv0_weights, conv0_bias, depthwise_weights, depthwise_bias, valid,
+                      *, dtype=np.float16) -> np.ndarray:
+    """conv0 (1 -> C, 3x3, stride 2, ReLU) then depthwise2 (3x3, stride 2)
+    of f32 feature-major features [batch, width(bins), height(frames)];
+    weights [3, 3, C] and the output [batch, Ho, Wo, C] in `dtype` (float16
+    and float32 follow the reference profiles, float64 is the double twin)."""
+    features = np.ascontiguousarray(features, dtype=np.float32)
+    batch, width, height = features.shape
+    channels = conv0_weights.shape[-1]
+    dtype = np.dtype(dtype)
+    conv0_weights = np.ascontiguousarray(conv0_weights, dtype=dtype).reshape(3, 3, channels)
+    depthwise_weights = np.ascontiguousarray(depthwise_weights, dtype=dtype).reshape(3, 3, channels)
+    conv0_bias = np.ascontiguousarray(conv0_bias, dtype=np.float32)
+    depthwise_bias = np.ascontiguousarray(depthwise_bias, dtype=np.float32)
+    valid = np.ascontiguousarray(valid, dtype=np.uint32)
+    h1, w1 = subsampled_length(height, 1), subsampled_length(width, 1)
+    out = np.empty((batch, subsampled_length(h1, 1), subsampled_length(w1, 1), channels), dtype=dtype)
+    if valid.size != batch or conv0_bias.size != channels or depthwise_bias.size != channels:
+        raise ValueError("subsampling_fused shape mismatch")
+    if lib().pko_subsampling_fused(DTYPE[_NAMES[dtype]], batch, height, width, channels, _ptr(features),
+                                   _ptr(conv0_weights), _ptr(conv0_bias), _ptr(depthwise_weights),
+                                   _ptr(depthwise_bias), _ptr(valid), _ptr(out)):
+        raise ValueError("subsampling_fused rejected its arguments")
+    return out
+
+
+def subsampling_depthwise(x, weights, bias, valid, steps) -> np.ndarray:
+    """Channel-last depthwise 3x3 stride-2 convolution of x [batch, H, W, C]
+    (float16/32/64) with the valid-length masking of stage `steps`."""
+    x = np.ascontiguousarray(x)
+    batch, height, width, channels = x.shape
+    weights = np.ascontiguousarray(weights, dtype=x.dtype).reshape(3, 3, channels)
+    bias = np.ascontiguousarray(bias, dtype=np.float32)
+    valid = np.ascontiguousarray(valid, dtype=np.uint32)
+    out = np.empty((batch, subsampled_length(height, 1), subsampled_length(width, 1), channels), dtype=x.dtype)
+    if lib().pko_subsampling_depthwise(DTYPE[_NAMES[x.dtype]], batch, height, width, channels, _ptr(x),
+                                       _ptr(weights), _ptr(bias), _ptr(valid), int(steps), _ptr(out)):
+        raise ValueError("subsampling_depthwise rejected its arguments")
+    return out
+
+
+def subsampling_mask(x, valid, steps) -> np.ndarray:
+    """A copy of x [batch, H, W, C] with rows at or past sub(L, steps) zeroed."""
+    out = np.array(x, copy=True, order="C")
+    batch, height, width, channels = out.shape
+    valid = np.ascontiguousarray(valid, dtype=np.uint32)
+    if lib().pko_subsampling_mask(DTYPE[_NAMES[out.dtype]], batch, height, width, channels, _ptr(out), _ptr(valid),
+                                  int(steps)):
+        raise ValueError("subsampling_mask rejected its arguments")
+    return out
+
+
 # name -> (bits, palette groups) of an encoder layer's matrices
 # (model/convert.py:1360-1475, encoder.ts:2458-2512).
 ENCODER_BITS = {"ff1_linear1": 5, "ff1_linear2": 5, "qkv": 5, "o_proj": 6, "pointwise1": 5, "pointwise2": 5,
@@ -330,6 +404,48 @@ def encoder(x, layers, valid, *, batch, frames, gemm_mode="f16-chain", threads=8
     for layer in layers:
         x = encoder_layer(x, layer, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
     return x
+
+
+def encoder_front_end(features, front, feature_lengths, *, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+    """The subsampling front end (encoder.ts:2140-2400) over f32
+    feature-major fbank [batch, 128, F] into [batch * sub(F, 3), 1024] f16:
+    conv0 + ReLU + depthwise2, pointwise3 + bias + ReLU, depthwise5,
+    pointwise6 + bias + ReLU, rows past sub(L, 3) zeroed, flatten (frequency
+    major) and the linear 4096 -> 1024 + bias. `front` is keyed like
+    pk_encoder_subsampling."""
+    batch = features.shape[0]
+    stage = subsampling_fused(features, front["conv0_weights"], front["conv0_bias"], front["depthwise2_weights"],
+                              front["depthwise2_bias"], feature_lengths, dtype=np.float16)
+    _, h2, w2, channels = stage.shape
+
+    def mm(name, a, columns, **epilogue):
+        words, palette = front[name]
+        out = gemm(a, words, 5, palette, columns, mode=gemm_mode, threads=threads, **epilogue)
+        return out.astype(np.float16)
+    projected = mm("pointwise3", stage.reshape(-1, channels), channels, bias=front["pointwise3_bias"],
+                   activation="relu").reshape(batch, h2, w2, channels)
+    stage = subsampling_depthwise(projected, front["depthwise5_weights"], front["depthwise5_bias"], feature_lengths, 3)
+    _, h3, w3, _ = stage.shape
+    projected = mm("pointwise6", stage.reshape(-1, channels), channels, bias=front["pointwise6_bias"],
+                   activation="relu").reshape(batch, h3, w3, channels)
+    projected = subsampling_mask(projected, feature_lengths, 3)
+    return mm("linear", projected.reshape(batch * h3, w3 * channels), 1024, bias=front["linear_bias"])
+
+
+def encoder_graph(x, layers, valid, *, batch, frames, front=None, features=None, feature_lengths=None,
+                  projector=None, projector_bias=None, gemm_mode="f16-chain", threads=8):
+    """ParakeetEncoderGraph.encode (encoder.ts:1690-1706): the front end when
+    `front` is given (from `features`; `x` is then unused), the layers, and
+    the projector when given. Returns (output, projected or None)."""
+    if front is not None:
+        x = encoder_front_end(features, front, feature_lengths, gemm_mode=gemm_mode, threads=threads)
+    out = encoder(x, layers, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
+    projected = None
+    if projector is not None:
+        words, palette = projector
+        projected = gemm(out, words, 5, palette, projector_bias.size, bias=projector_bias, mode=gemm_mode,
+                         threads=threads).astype(np.float16)
+    return out, projected
 
 
 def relative_errors(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:

@@ -1,7 +1,13 @@
-// pk_encoder_abi.cpp - the encoder layer stack composed from this library's
-// ops, in the order of createEncoderLayerDispatches
-// (src/webgpu/encoder.ts:1868-2135), with an optional HIP graph of a whole
-// pass.
+// pk_encoder_abi.cpp - the encoder graph composed from this library's ops:
+// the optional subsampling front end (createSubsamplingCommands,
+// src/webgpu/encoder.ts:2140-2400), the layer stack in the order of
+// createEncoderLayerDispatches (:1868-2135) and the optional projector
+// (:1489-1509), with an optional HIP graph of a whole pass.
+//
+// Windows are never split into microbatches: the reference runs the front
+// end three windows at a time to bound its WebGPU arena (encoder.ts:80,
+// :1599-1624); with HBM to spare here, every stage runs once over all
+// active windows, which keeps each GEMM's M large.
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -14,6 +20,7 @@
 #include "pk_encoder.h"
 #include "pk_internal.h"
 #include "pk_layernorm.h"
+#include "pk_subsampling.h"
 
 using namespace pk_abi;
 
@@ -22,6 +29,9 @@ namespace {
 constexpr uint32_t kC = PK_ENCODER_CHANNELS;
 constexpr uint32_t kHidden = PK_ENCODER_INTERMEDIATE;
 constexpr uint32_t kMaxLayers = 64;
+constexpr uint32_t kSubC = PK_SUBSAMPLING_CHANNELS;
+constexpr uint32_t kBins = PK_SUBSAMPLING_BINS;
+constexpr uint32_t kFrontLaunches = 6;
 
 struct LayerOps {
   pk_layernorm_op* norm[5] = {};
@@ -37,9 +47,20 @@ struct LayerOps {
   pk_gemm_op* ff2b = nullptr;
 };
 
+struct FrontOps {
+  pk_subsampling_op* fused = nullptr;
+  pk_gemm_op* pointwise3 = nullptr;
+  pk_subsampling_op* depthwise5 = nullptr;
+  pk_gemm_op* pointwise6 = nullptr;
+  pk_subsampling_op* mask = nullptr;
+  pk_gemm_op* linear = nullptr;
+};
+
 uint64_t packed_bytes(int bits, uint32_t inner, uint32_t columns) {
   return (uint64_t)inner * columns / pk::codes_per_group(bits) * pk::words_per_group(bits) * 4u;
 }
+
+uint32_t halve(uint32_t n, uint32_t steps) { return pk_subsampling_valid_length(n, steps); }
 
 }  // namespace
 
@@ -51,13 +72,24 @@ struct pk_encoder {
   const uint32_t* valid_lengths = nullptr;
   const void* input = nullptr;
   void* output = nullptr;
+  // front end
+  bool front = false;
+  uint32_t feature_frames = 0, front_height = 0;  // fbank frames, rows after two stride-2 stages
+  const uint32_t* feature_lengths = nullptr;
+  // projector
+  uint32_t projected_channels = 0;
+  void* projected_output = nullptr;
+
   void* arena = nullptr;
   uint64_t arena_bytes = 0, weight_bytes = 0;
   // Arena slices: four [rows, 1024] activation buffers, the FF hidden block,
-  // QKV, the attention context, the pointwise-1 output and the conv output.
+  // QKV, the attention context, the pointwise-1 output, the conv output and,
+  // with the front end, two [windows, H2, 32, 256] stage buffers.
   _Float16 *a = nullptr, *b = nullptr, *c = nullptr, *d = nullptr, *h = nullptr, *qkv = nullptr, *ctxt = nullptr,
-           *pw = nullptr, *cout = nullptr;
+           *pw = nullptr, *cout = nullptr, *s1 = nullptr, *s2 = nullptr;
+  FrontOps front_ops;
   std::vector<LayerOps> ops;
+  pk_gemm_op* projector = nullptr;
   std::map<uint32_t, hipGraphExec_t> graphs;  // per active batch
 };
 
@@ -74,8 +106,14 @@ void release_layer(LayerOps& l) {
 void release_encoder(pk_encoder* e) {
   for (auto& kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
   e->graphs.clear();
+  FrontOps& f = e->front_ops;
+  for (pk_subsampling_op* op : {f.fused, f.depthwise5, f.mask}) pk_subsampling_release(op);
+  for (pk_gemm_op* op : {f.pointwise3, f.pointwise6, f.linear}) pk_gemm_release(op);
+  f = FrontOps{};
   for (auto& l : e->ops) release_layer(l);
   e->ops.clear();
+  pk_gemm_release(e->projector);
+  e->projector = nullptr;
   if (e->arena) {
     (void)hipSetDevice(e->ctx->device);
     (void)hipFree(e->arena);
@@ -83,12 +121,177 @@ void release_encoder(pk_encoder* e) {
   }
 }
 
+// One palette GEMM of the graph, f16, over `rows` rows.
+struct GemmSpec {
+  pk_encoder_matrix matrix;
+  int bits = 5;
+  uint32_t rows = 0, inner = 0, columns = 0, groups = 1;
+  const void* a = nullptr;
+  void* out = nullptr;
+  const float* bias = nullptr;
+  const void* residual = nullptr;
+  float scale = 0.0f;
+  int activation = PK_ACTIVATION_NONE;
+  uint32_t flags = 0;
+};
+
+// With `validate_only` the descriptor is checked on the host
+// (pk_gemm_validate) and nothing is created.
+int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStream_t stream, pk_gemm_op** op,
+              bool validate_only) {
+  const uint64_t R = g.rows;
+  pk_gemm_desc d{};
+  d.struct_size = sizeof d;
+  d.flags = g.flags;
+  d.label = label.c_str();
+  d.precision = PK_PRECISION_F16;
+  d.palette_bits = g.bits;
+  d.rows = g.rows;
+  d.inner = g.inner;
+  d.columns = g.columns;
+  d.palette_groups = g.groups;
+  d.palette_group_columns = g.columns / g.groups;
+  d.a = g.a;
+  d.a_bytes = R * g.inner * 2;
+  d.packed = g.matrix.packed;
+  d.packed_bytes = packed_bytes(g.bits, g.inner, g.columns);
+  d.palette = g.matrix.palette;
+  d.palette_bytes = (uint64_t)g.groups * (1u << g.bits) * 2;
+  d.output = g.out;
+  d.output_bytes = R * ((g.flags & PK_GEMM_GLU) ? g.columns / 2 : g.columns) * 2;
+  d.bias = g.bias;
+  d.bias_bytes = g.bias ? (uint64_t)g.columns * 4u : 0;
+  d.residual = g.residual;
+  d.residual_bytes = g.residual ? R * g.columns * 2 : 0;
+  d.has_residual_scale = g.residual ? 1 : 0;
+  d.residual_scale = g.scale;
+  d.activation = g.activation;
+  if (validate_only) return pk_gemm_validate(&d);
+  const int s = pk_gemm_create(e->ctx, &d, stream, op);
+  if (s == PK_OK) {
+    e->weight_bytes += pk::pair_code_bytes(g.inner, g.columns);
+    if (!(g.flags & PK_GEMM_GLU)) e->weight_bytes += pk::operand_order_words(g.bits, g.inner, g.columns) * 4u;
+  }
+  return s;
+}
+
+// The front end over the fbank (createSubsamplingCommands, encoder.ts:
+// 2140-2400; labels follow its dispatch labels):
+//   fbank -conv0+dw2-> S1 [W, H2, 32, 256] -PW3+ReLU-> S2 -DW5-> S1
+//   [W, H3, 16, 256] -PW6+ReLU-> S2 -mask-> S2 -linear-> A [W*H3, 1024]
+int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stream, FrontOps& f,
+                bool validate_only) {
+  const std::string prefix = e->label + ".subsampling-";
+  const uint32_t h2 = e->front_height, h3 = e->frames, w2 = halve(kBins, 2), w3 = halve(kBins, 3);
+  const uint64_t stage2 = (uint64_t)e->batch * h2 * w2 * kSubC * 2, stage3 = (uint64_t)e->batch * h3 * w3 * kSubC * 2;
+  std::string label;
+  int s;
+  {
+    label = prefix + "fused-conv0-depthwise2";
+    pk_subsampling_fused_desc d{};
+    d.struct_size = sizeof d;
+    d.label = label.c_str();
+    d.precision = PK_PRECISION_F16;
+    d.batch_size = e->batch;
+    d.input_height = e->feature_frames;
+    d.input_width = kBins;
+    d.channels = kSubC;
+    d.input = static_cast<const float*>(e->input);
+    d.input_bytes = (uint64_t)e->batch * kBins * e->feature_frames * 4u;
+    d.conv0_weights = w.conv0_weights;
+    d.conv0_weights_bytes = 9ull * kSubC * 2;
+    d.conv0_bias = w.conv0_bias;
+    d.conv0_bias_bytes = kSubC * 4u;
+    d.depthwise_weights = w.depthwise2_weights;
+    d.depthwise_weights_bytes = 9ull * kSubC * 2;
+    d.depthwise_bias = w.depthwise2_bias;
+    d.depthwise_bias_bytes = kSubC * 4u;
+    d.output = e->s1;
+    d.output_bytes = stage2;
+    d.valid_lengths = e->feature_lengths;
+    d.valid_lengths_bytes = (uint64_t)e->batch * 4u;
+    if ((s = validate_only ? pk_subsampling_fused_validate(&d) : pk_subsampling_fused_create(e->ctx, &d, &f.fused)))
+      return s;
+  }
+  GemmSpec g;
+  g.matrix = w.pointwise3;
+  g.rows = e->batch * h2 * w2;
+  g.inner = g.columns = kSubC;
+  g.a = e->s1;
+  g.out = e->s2;
+  g.bias = w.pointwise3_bias;
+  g.activation = PK_ACTIVATION_RELU;
+  if ((s = make_gemm(e, prefix + "pointwise3", g, stream, &f.pointwise3, validate_only))) return s;
+  {
+    label = prefix + "depthwise5";
+    pk_subsampling_depthwise_desc d{};
+    d.struct_size = sizeof d;
+    d.label = label.c_str();
+    d.precision = PK_PRECISION_F16;
+    d.batch_size = e->batch;
+    d.input_height = h2;
+    d.input_width = w2;
+    d.channels = kSubC;
+    d.input = e->s2;
+    d.input_bytes = stage2;
+    d.weights = w.depthwise5_weights;
+    d.weights_bytes = 9ull * kSubC * 2;
+    d.bias = w.depthwise5_bias;
+    d.bias_bytes = kSubC * 4u;
+    d.output = e->s1;
+    d.output_bytes = stage3;
+    d.valid_lengths = e->feature_lengths;
+    d.valid_lengths_bytes = (uint64_t)e->batch * 4u;
+    d.valid_length_subsampling_steps = 3;
+    if ((s = validate_only ? pk_subsampling_depthwise_validate(&d)
+                           : pk_subsampling_depthwise_create(e->ctx, &d, &f.depthwise5)))
+      return s;
+  }
+  g = GemmSpec{};
+  g.matrix = w.pointwise6;
+  g.rows = e->batch * h3 * w3;
+  g.inner = g.columns = kSubC;
+  g.a = e->s1;
+  g.out = e->s2;
+  g.bias = w.pointwise6_bias;
+  g.activation = PK_ACTIVATION_RELU;
+  if ((s = make_gemm(e, prefix + "pointwise6", g, stream, &f.pointwise6, validate_only))) return s;
+  {
+    // Pointwise 6 can turn zero rows past the length into its ReLU'd bias,
+    // so its rows there are cleared before the flatten (encoder.ts:2361-2391).
+    label = prefix + "pointwise6-mask";
+    pk_subsampling_mask_desc d{};
+    d.struct_size = sizeof d;
+    d.label = label.c_str();
+    d.precision = PK_PRECISION_F16;
+    d.batch_size = e->batch;
+    d.height = h3;
+    d.width = w3;
+    d.channels = kSubC;
+    d.values = e->s2;
+    d.values_bytes = stage3;
+    d.valid_lengths = e->feature_lengths;
+    d.valid_lengths_bytes = (uint64_t)e->batch * 4u;
+    d.valid_length_subsampling_steps = 3;
+    if ((s = validate_only ? pk_subsampling_mask_validate(&d) : pk_subsampling_mask_create(e->ctx, &d, &f.mask)))
+      return s;
+  }
+  g = GemmSpec{};
+  g.matrix = w.linear;
+  g.rows = e->rows;
+  g.inner = w3 * kSubC;
+  g.columns = kC;
+  g.a = e->s2;
+  g.out = e->a;
+  g.bias = w.linear_bias;
+  return make_gemm(e, prefix + "flatten-project", g, stream, &f.linear, validate_only);
+}
+
 // The fifteen ops of layer `li` over the arena (encoder.ts:1868-2135):
-//   A (the input for layer 0) -LN-> B -W1-> H -W2(+0.5 A)-> B -LN-> C -QKV-> Q -att-> X -Wo(+B)-> C
-//   -LN-> D -PW1-> P -conv-> O -PW2(+C)-> D -LN-> B -W1-> H -W2(+0.5 D)-> B
-//   -LN-> A (the last layer writes the output instead).
-// With `validate_only` the ops' descriptors are checked on the host
-// (pk_*_validate) and nothing is created.
+//   A (the caller's input for layer 0 without the front end) -LN-> B -W1->
+//   H -W2(+0.5 A)-> B -LN-> C -QKV-> Q -att-> X -Wo(+B)-> C -LN-> D -PW1->
+//   P -conv-> O -PW2(+C)-> D -LN-> B -W1-> H -W2(+0.5 D)-> B -LN-> A (the
+//   last layer writes the output instead).
 int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream_t stream, LayerOps& l,
                 bool validate_only) {
   const uint64_t R = e->rows;
@@ -118,40 +321,22 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
   auto gemm = [&](pk_gemm_op** op, const char* suffix, const pk_encoder_matrix& m, int bits, uint32_t inner,
                   uint32_t columns, uint32_t groups, const void* a, void* out, const void* residual, float scale,
                   int activation, uint32_t flags) {
-    pk_gemm_desc d{};
-    d.struct_size = sizeof d;
-    d.flags = flags;
-    d.label = name(suffix);
-    d.precision = PK_PRECISION_F16;
-    d.palette_bits = bits;
-    d.rows = e->rows;
-    d.inner = inner;
-    d.columns = columns;
-    d.palette_groups = groups;
-    d.palette_group_columns = columns / groups;
-    d.a = a;
-    d.a_bytes = R * inner * 2;
-    d.packed = m.packed;
-    d.packed_bytes = packed_bytes(bits, inner, columns);
-    d.palette = m.palette;
-    d.palette_bytes = (uint64_t)groups * (1u << bits) * 2;
-    d.output = out;
-    d.output_bytes = R * ((flags & PK_GEMM_GLU) ? columns / 2 : columns) * 2;
-    d.residual = residual;
-    d.residual_bytes = residual ? R * columns * 2 : 0;
-    d.has_residual_scale = residual ? 1 : 0;
-    d.residual_scale = scale;
-    d.activation = activation;
-    if (validate_only) return pk_gemm_validate(&d);
-    const int s = pk_gemm_create(e->ctx, &d, stream, op);
-    if (s == PK_OK) {
-      e->weight_bytes += pk::pair_code_bytes(inner, columns);
-      if (!(flags & PK_GEMM_GLU)) e->weight_bytes += pk::operand_order_words(bits, inner, columns) * 4u;
-    }
-    return s;
+    GemmSpec g;
+    g.matrix = m;
+    g.bits = bits;
+    g.rows = e->rows;
+    g.inner = inner;
+    g.columns = columns;
+    g.groups = groups;
+    g.a = a;
+    g.out = out;
+    g.residual = residual;
+    g.scale = scale;
+    g.activation = activation;
+    g.flags = flags;
+    return make_gemm(e, prefix + suffix, g, stream, op, validate_only);
   };
-  // Layer 0 reads the caller's input in place of A.
-  const void* x = li == 0 ? e->input : e->a;
+  const void* x = (li == 0 && !e->front) ? e->input : e->a;
   int s;
   if ((s = norm(0, ".norm_feed_forward1", x, e->b))) return s;
   if ((s = gemm(&l.ff1a, "-feed-forward1-linear1", w.ff1_linear1, 5, kC, kHidden, 1, e->b, e->h, nullptr, 0.0f,
@@ -229,9 +414,26 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
   return norm(4, ".norm_out", e->b, last ? e->output : e->a);
 }
 
-// One pass over the first `batch` windows on `stream`. With `starts` /
-// `ends` (15 per layer, in dispatch order; NULL entries skip), each launch's
-// own dispatch stamps its pair of events.
+int build_projector(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, pk_gemm_op** op,
+                    bool validate_only) {
+  GemmSpec g;
+  g.matrix = d->projector;
+  g.rows = e->rows;
+  g.inner = kC;
+  g.columns = e->projected_channels;
+  g.a = e->output;
+  g.out = e->projected_output;
+  g.bias = d->projector_bias;
+  return make_gemm(e, e->label + "-projector", g, stream, op, validate_only);
+}
+
+uint32_t launch_count(const pk_encoder* e) {
+  return (e->front ? kFrontLaunches : 0u) + 15u * e->layers + (e->projected_channels ? 1u : 0u);
+}
+
+// One pass over the first `batch` windows on `stream`: the front end, the
+// layers, the projector. With `starts` / `ends` (one entry per launch, in
+// order; NULL entries skip), each launch's own dispatch stamps its events.
 int enqueue_pass(pk_encoder* e, uint32_t batch, hipStream_t stream, void* const* starts = nullptr,
                  void* const* ends = nullptr) {
   const uint32_t rows = batch * e->frames;
@@ -242,40 +444,56 @@ int enqueue_pass(pk_encoder* e, uint32_t batch, hipStream_t stream, void* const*
     ++slot;
     return s;
   };
-  auto gemm = [&](pk_gemm_op* op) {
-    const int s = pk_gemm_enqueue_timed(op, rows, stream, ev(starts), ev(ends));
+  auto gemm = [&](pk_gemm_op* op, uint32_t active_rows) {
+    const int s = pk_gemm_enqueue_timed(op, active_rows, stream, ev(starts), ev(ends));
     ++slot;
     return s;
   };
+  auto sub = [&](pk_subsampling_op* op) {
+    const int s = pk_subsampling_enqueue_timed(op, batch, stream, ev(starts), ev(ends));
+    ++slot;
+    return s;
+  };
+  int s;
+  if (e->front) {
+    const FrontOps& f = e->front_ops;
+    const uint32_t w2 = halve(kBins, 2), w3 = halve(kBins, 3);
+    if ((s = sub(f.fused)) || (s = gemm(f.pointwise3, batch * e->front_height * w2)) || (s = sub(f.depthwise5)) ||
+        (s = gemm(f.pointwise6, batch * e->frames * w3)) || (s = sub(f.mask)) || (s = gemm(f.linear, rows)))
+      return s;
+  }
   for (LayerOps& l : e->ops) {
-    int s;
-    if ((s = norm(l.norm[0])) || (s = gemm(l.ff1a)) || (s = gemm(l.ff1b)) || (s = norm(l.norm[1])) ||
-        (s = gemm(l.qkv)))
+    if ((s = norm(l.norm[0])) || (s = gemm(l.ff1a, rows)) || (s = gemm(l.ff1b, rows)) || (s = norm(l.norm[1])) ||
+        (s = gemm(l.qkv, rows)))
       return s;
     if ((s = pk_attention_enqueue_timed(l.attention, batch, stream, ev(starts), ev(ends)))) return s;
     ++slot;
-    if ((s = gemm(l.o)) || (s = norm(l.norm[2])) || (s = gemm(l.pw1))) return s;
+    if ((s = gemm(l.o, rows)) || (s = norm(l.norm[2])) || (s = gemm(l.pw1, rows))) return s;
     if ((s = pk_conv_enqueue_timed(l.conv, batch, stream, ev(starts), ev(ends)))) return s;
     ++slot;
-    if ((s = gemm(l.pw2)) || (s = norm(l.norm[3])) || (s = gemm(l.ff2a)) || (s = gemm(l.ff2b)) ||
+    if ((s = gemm(l.pw2, rows)) || (s = norm(l.norm[3])) || (s = gemm(l.ff2a, rows)) || (s = gemm(l.ff2b, rows)) ||
         (s = norm(l.norm[4])))
       return s;
   }
+  if (e->projector && (s = gemm(e->projector, rows))) return s;
   return PK_OK;
 }
 
-// Arena slices: A, B, C, D [rows, 1024], H [rows, 4096], QKV [rows, 3072],
-// the attention context [rows, 1024], the pointwise-1 output ([rows, 2048],
-// or [rows, 1024] with the GLU epilogue) and the conv output [rows, 1024],
-// each 256-byte aligned. Returns the bytes used from `base`.
+// Arena slices (256-byte aligned): A, B, C, D [rows, 1024], H [rows, 4096],
+// QKV [rows, 3072], the attention context [rows, 1024], the pointwise-1
+// output ([rows, 2048], or [rows, 1024] with the GLU epilogue), the conv
+// output [rows, 1024] and, with the front end, S1 and S2 [windows, H2, 32,
+// 256] (each later holds the [windows, H3, 16, 256] stage). Returns the
+// bytes used from `base`.
 uint64_t place_arena(pk_encoder* e, uint8_t* base) {
   const uint64_t R = e->rows;
-  const uint64_t elems[9] = {R * kC, R * kC, R * kC, R * kC, R * kHidden, R * 3 * kC, R * kC,
-                             R * (e->fused_glu ? kC : 2 * kC), R * kC};
-  _Float16** slots[9] = {&e->a, &e->b, &e->c, &e->d, &e->h, &e->qkv, &e->ctxt, &e->pw, &e->cout};
+  const uint64_t stage = e->front ? (uint64_t)e->batch * e->front_height * halve(kBins, 2) * kSubC : 0;
+  const uint64_t elems[11] = {R * kC,     R * kC, R * kC, R * kC, R * kHidden, R * 3 * kC, R * kC,
+                              R * (e->fused_glu ? kC : 2 * kC), R * kC, stage, stage};
+  _Float16** slots[11] = {&e->a, &e->b, &e->c, &e->d, &e->h, &e->qkv, &e->ctxt, &e->pw, &e->cout, &e->s1, &e->s2};
   uint64_t at = 0;
-  for (int i = 0; i < 9; ++i) {
-    if (base) *slots[i] = reinterpret_cast<_Float16*>(base + at);
+  for (int i = 0; i < 11; ++i) {
+    if (base) *slots[i] = elems[i] ? reinterpret_cast<_Float16*>(base + at) : nullptr;
     at += (elems[i] * 2 + 255u) / 256u * 256u;
   }
   return at;
@@ -293,6 +511,17 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->valid_lengths = d->valid_lengths;
   e->input = d->input;
   e->output = d->output;
+  e->front = d->subsampling != nullptr;
+  e->feature_frames = e->front ? d->feature_frames : 0;
+  e->front_height = e->front ? halve(d->feature_frames, 2) : 0;
+  e->feature_lengths = e->front ? d->feature_lengths : nullptr;
+  e->projected_channels = d->projected_channels;
+  e->projected_output = d->projected_channels ? d->projected_output : nullptr;
+}
+
+bool overlap(const void* p, uint64_t pn, const void* q, uint64_t qn) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+  return a < b + qn && b < a + pn;
 }
 
 int validate_encoder_desc(const pk_encoder_desc* d) {
@@ -310,10 +539,38 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "%s needs layer weights, valid lengths, input and output", label);
   if (!aligned(d->input, 16) || !aligned(d->output, 16))
     return fail(PK_INVALID_ARGUMENT, "%s input and output must be 16-byte aligned", label);
-  const uintptr_t bytes = (uintptr_t)d->batch_size * d->frames * kC * 2;
-  const uintptr_t in = reinterpret_cast<uintptr_t>(d->input), out = reinterpret_cast<uintptr_t>(d->output);
-  if (in < out + bytes && out < in + bytes)
+  uint64_t in_bytes = (uint64_t)d->batch_size * d->frames * kC * 2;
+  if (d->subsampling) {
+    if (d->feature_frames == 0 || halve(d->feature_frames, 3) != d->frames)
+      return fail(PK_RANGE_ERROR, "%s: %u encoder frames do not follow from %u feature frames (expected %u)", label,
+                  d->frames, d->feature_frames, halve(d->feature_frames, 3));
+    if (!d->feature_lengths || !aligned(d->feature_lengths, 4))
+      return fail(PK_INVALID_ARGUMENT, "%s: the front end needs per-window feature lengths", label);
+    in_bytes = (uint64_t)d->batch_size * kBins * d->feature_frames * 4u;
+  }
+  const uint64_t out_bytes = (uint64_t)d->batch_size * d->frames * kC * 2;
+  if (overlap(d->input, in_bytes, d->output, out_bytes))
     return fail(PK_INVALID_ARGUMENT, "%s output must not overlap its input", label);
+  if (d->projected_channels) {
+    const uint64_t proj_bytes = (uint64_t)d->batch_size * d->frames * d->projected_channels * 2;
+    if (!d->projected_output || !aligned(d->projected_output, 16))
+      return fail(PK_INVALID_ARGUMENT, "%s: the projector needs a 16-byte aligned projected output", label);
+    if (overlap(d->projected_output, proj_bytes, d->output, out_bytes) ||
+        overlap(d->projected_output, proj_bytes, d->input, in_bytes))
+      return fail(PK_INVALID_ARGUMENT, "%s projected output must not overlap the input or output", label);
+  }
+  return PK_OK;
+}
+
+// Builds (or, with `validate_only`, checks) every op of the graph.
+int build_all(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, bool validate_only) {
+  if (e->front)
+    if (int s = build_front(e, *d->subsampling, stream, e->front_ops, validate_only)) return s;
+  e->ops.resize(e->layers);
+  for (uint32_t li = 0; li < e->layers; ++li)
+    if (int s = build_layer(e, d->layer[li], li, stream, e->ops[li], validate_only)) return s;
+  if (e->projected_channels)
+    if (int s = build_projector(e, d, stream, &e->projector, validate_only)) return s;
   return PK_OK;
 }
 
@@ -330,22 +587,19 @@ int pk_encoder_create(pk_context* ctx, const pk_encoder_desc* d, void* stream, p
   auto* e = new pk_encoder();
   e->ctx = ctx;
   describe(e, d);
-  hipError_t err = hipMalloc(&e->arena, arena_bytes(e));
+  const uint64_t total = arena_bytes(e);
+  hipError_t err = hipMalloc(&e->arena, total);
   if (err != hipSuccess) {
-    const uint64_t total = arena_bytes(e);
     delete e;
     return fail(PK_ALLOCATION_FAILURE, "cannot allocate the %llu-byte encoder arena: %s", (unsigned long long)total,
                 hipGetErrorString(err));
   }
   e->arena_bytes = place_arena(e, static_cast<uint8_t*>(e->arena));
-  e->ops.resize(e->layers);
-  for (uint32_t li = 0; li < e->layers; ++li) {
-    if (int s = build_layer(e, d->layer[li], li, stream_or_default(ctx, stream), e->ops[li], false)) {
-      const std::string message = g_error;
-      release_encoder(e);
-      delete e;
-      return fail(s, "%s", message.c_str());
-    }
+  if (int s = build_all(e, d, stream_or_default(ctx, stream), false)) {
+    const std::string message = g_error;
+    release_encoder(e);
+    delete e;
+    return fail(s, "%s", message.c_str());
   }
   *out = e;
   return ok();
@@ -354,13 +608,11 @@ int pk_encoder_create(pk_context* ctx, const pk_encoder_desc* d, void* stream, p
 int pk_encoder_validate(const pk_encoder_desc* d) {
   if (int s = validate_encoder_desc(d)) return s;
   // Check every op's descriptor over an arena placed at a nominal,
-  // suitably aligned address; nothing is dereferenced.
+  // suitably aligned address; nothing is dereferenced or created.
   pk_encoder e;
   describe(&e, d);
   place_arena(&e, reinterpret_cast<uint8_t*>(uintptr_t(1) << 40));
-  LayerOps unused;
-  for (uint32_t li = 0; li < e.layers; ++li)
-    if (int s = build_layer(&e, d->layer[li], li, nullptr, unused, true)) return s;
+  if (int s = build_all(&e, d, nullptr, true)) return s;
   return ok();
 }
 
@@ -406,7 +658,7 @@ int pk_encoder_enqueue_profiled(pk_encoder* e, uint32_t active_batch, void* stre
 
 int pk_encoder_info(const pk_encoder* e, uint32_t* launches, uint64_t* device_bytes) {
   if (!e) return fail(PK_INVALID_ARGUMENT, "encoder is null");
-  if (launches) *launches = 15u * e->layers;
+  if (launches) *launches = launch_count(e);
   if (device_bytes) *device_bytes = e->arena_bytes + e->weight_bytes;
   return ok();
 }

@@ -237,6 +237,33 @@ uint32_t layernorm_grid(uint32_t rows);
 hipError_t launch_layernorm(bool f16, const LayerNormArgs& args, hipStream_t stream, hipEvent_t start = nullptr,
                             hipEvent_t stop = nullptr);
 
+// Subsampling front end convolutions (pk_subsampling.hip).
+enum SubsamplingKind { kSubsamplingFused = 0, kSubsamplingDepthwise = 1, kSubsamplingMask = 2 };
+struct SubsamplingArgs {
+  const void* input;             // fused: f32 [batch, width, height]; depthwise: [batch, H, W, C]
+  const void* weights;           // conv0 (fused) or depthwise [3, 3, C]
+  const float* bias;             // [C]
+  const void* weights2;          // fused: depthwise2 [3, 3, C]
+  const float* bias2;            // fused: [C]
+  void* output;                  // [batch, out_height, out_width, C]; mask: values in place
+  const uint32_t* valid_lengths; // raw feature frames, from valid_offset
+  uint32_t height, width;        // input (mask: values) spatial shape
+  uint32_t mid_height, mid_width;  // fused: conv0 shape
+  uint32_t out_height, out_width;
+  uint32_t channels;
+  uint32_t valid_offset;
+  uint32_t steps;                // depthwise and mask
+};
+struct SubsamplingGeometry {
+  const char* name;
+  uint32_t grid[3];
+  uint32_t block_threads;
+  uint32_t lds_bytes;
+};
+SubsamplingGeometry subsampling_geometry(int kind, bool f16, const SubsamplingArgs& args, uint32_t batch);
+hipError_t launch_subsampling(int kind, bool f16, const SubsamplingArgs& args, uint32_t batch, hipStream_t stream,
+                              hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+
 int conv_variant_count(bool f16);
 ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
                            bool input_glu = false);

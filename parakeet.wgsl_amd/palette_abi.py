@@ -1,5 +1,5 @@
 """ctypes binding of libpk_palette.so (include/pk_palette.h, pk_conv.h, pk_attention.h,
-pk_layernorm.h, pk_encoder.h).
+pk_layernorm.h, pk_subsampling.h, pk_encoder.h).
 
 A thin Python view of the C ABI, used by the tests and the benchmark. It
 raises PaletteError (or PaletteRangeError, mirroring the reference's
@@ -234,6 +234,88 @@ class LayerNormDesc(ctypes.Structure):
     ]
 
 
+class SubsamplingFusedDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("input_height", ctypes.c_uint32),
+        ("input_width", ctypes.c_uint32),
+        ("channels", ctypes.c_uint32),
+        ("input", ctypes.c_void_p),
+        ("input_bytes", ctypes.c_uint64),
+        ("conv0_weights", ctypes.c_void_p),
+        ("conv0_weights_bytes", ctypes.c_uint64),
+        ("conv0_bias", ctypes.c_void_p),
+        ("conv0_bias_bytes", ctypes.c_uint64),
+        ("depthwise_weights", ctypes.c_void_p),
+        ("depthwise_weights_bytes", ctypes.c_uint64),
+        ("depthwise_bias", ctypes.c_void_p),
+        ("depthwise_bias_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+        ("valid_lengths", ctypes.c_void_p),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("valid_length_batch_offset", ctypes.c_uint32),
+    ]
+
+
+class SubsamplingDepthwiseDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("input_height", ctypes.c_uint32),
+        ("input_width", ctypes.c_uint32),
+        ("channels", ctypes.c_uint32),
+        ("input", ctypes.c_void_p),
+        ("input_bytes", ctypes.c_uint64),
+        ("weights", ctypes.c_void_p),
+        ("weights_bytes", ctypes.c_uint64),
+        ("bias", ctypes.c_void_p),
+        ("bias_bytes", ctypes.c_uint64),
+        ("output", ctypes.c_void_p),
+        ("output_bytes", ctypes.c_uint64),
+        ("valid_lengths", ctypes.c_void_p),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("valid_length_batch_offset", ctypes.c_uint32),
+        ("valid_length_subsampling_steps", ctypes.c_uint32),
+    ]
+
+
+class SubsamplingMaskDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("height", ctypes.c_uint32),
+        ("width", ctypes.c_uint32),
+        ("channels", ctypes.c_uint32),
+        ("values", ctypes.c_void_p),
+        ("values_bytes", ctypes.c_uint64),
+        ("valid_lengths", ctypes.c_void_p),
+        ("valid_lengths_bytes", ctypes.c_uint64),
+        ("valid_length_batch_offset", ctypes.c_uint32),
+        ("valid_length_subsampling_steps", ctypes.c_uint32),
+    ]
+
+
+class SubsamplingPlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("output_height", ctypes.c_uint32),
+        ("output_width", ctypes.c_uint32),
+        ("grid", ctypes.c_uint32 * 3),
+        ("block_threads", ctypes.c_uint32),
+        ("lds_bytes", ctypes.c_uint32),
+        ("algorithmic_bytes", ctypes.c_uint64),
+        ("flops", ctypes.c_uint64),
+        ("kernel", ctypes.c_char * 64),
+    ]
+
+
 class EncoderMatrix(ctypes.Structure):
     _fields_ = [("packed", ctypes.c_void_p), ("palette", ctypes.c_void_p)]
 
@@ -259,6 +341,23 @@ class EncoderLayer(ctypes.Structure):
     ]
 
 
+class EncoderSubsampling(ctypes.Structure):
+    _fields_ = [
+        ("conv0_weights", ctypes.c_void_p),
+        ("conv0_bias", ctypes.c_void_p),
+        ("depthwise2_weights", ctypes.c_void_p),
+        ("depthwise2_bias", ctypes.c_void_p),
+        ("pointwise3", EncoderMatrix),
+        ("pointwise3_bias", ctypes.c_void_p),
+        ("depthwise5_weights", ctypes.c_void_p),
+        ("depthwise5_bias", ctypes.c_void_p),
+        ("pointwise6", EncoderMatrix),
+        ("pointwise6_bias", ctypes.c_void_p),
+        ("linear", EncoderMatrix),
+        ("linear_bias", ctypes.c_void_p),
+    ]
+
+
 class EncoderDesc(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -272,6 +371,13 @@ class EncoderDesc(ctypes.Structure):
         ("valid_lengths", ctypes.c_void_p),
         ("input", ctypes.c_void_p),
         ("output", ctypes.c_void_p),
+        ("subsampling", ctypes.POINTER(EncoderSubsampling)),
+        ("feature_frames", ctypes.c_uint32),
+        ("feature_lengths", ctypes.c_void_p),
+        ("projector", EncoderMatrix),
+        ("projector_bias", ctypes.c_void_p),
+        ("projected_channels", ctypes.c_uint32),
+        ("projected_output", ctypes.c_void_p),
     ]
 
 
@@ -341,6 +447,19 @@ SIGNATURES = {
     "pk_layernorm_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
     "pk_layernorm_destroy": (ctypes.c_int, [_VP]),
     "pk_layernorm_release": (ctypes.c_int, [_VP]),
+    "pk_subsampling_output_dimension": (ctypes.c_uint32, [ctypes.c_uint32]),
+    "pk_subsampling_valid_length": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_subsampling_fused_validate": (ctypes.c_int, [ctypes.POINTER(SubsamplingFusedDesc)]),
+    "pk_subsampling_fused_create": (ctypes.c_int, [_VP, ctypes.POINTER(SubsamplingFusedDesc), _PPV]),
+    "pk_subsampling_depthwise_validate": (ctypes.c_int, [ctypes.POINTER(SubsamplingDepthwiseDesc)]),
+    "pk_subsampling_depthwise_create": (ctypes.c_int, [_VP, ctypes.POINTER(SubsamplingDepthwiseDesc), _PPV]),
+    "pk_subsampling_mask_validate": (ctypes.c_int, [ctypes.POINTER(SubsamplingMaskDesc)]),
+    "pk_subsampling_mask_create": (ctypes.c_int, [_VP, ctypes.POINTER(SubsamplingMaskDesc), _PPV]),
+    "pk_subsampling_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_subsampling_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_subsampling_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(SubsamplingPlanInfo)]),
+    "pk_subsampling_destroy": (ctypes.c_int, [_VP]),
+    "pk_subsampling_release": (ctypes.c_int, [_VP]),
     "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
     "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
     "pk_encoder_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, ctypes.c_int]),
@@ -730,6 +849,76 @@ class LayerNormOp:
             self.handle = None
 
 
+def subsampling_fused_desc(*, input, conv0_weights, conv0_bias, depthwise_weights, depthwise_bias, output,
+                           valid_lengths, batch_size: int, input_height: int = 1501, input_width: int = 128,
+                           channels: int = 256, valid_length_batch_offset: int = 0, precision: str | None = None,
+                           label: str = "subsampling-fused-conv0-depthwise2") -> SubsamplingFusedDesc:
+    if precision is None:
+        precision = "f16" if conv0_weights.dtype == np.float16 else "f32"
+    return SubsamplingFusedDesc(ctypes.sizeof(SubsamplingFusedDesc), label.encode(), PRECISION[precision], batch_size,
+                                input_height, input_width, channels, *_slice(input), *_slice(conv0_weights),
+                                *_slice(conv0_bias), *_slice(depthwise_weights), *_slice(depthwise_bias),
+                                *_slice(output), *_slice(valid_lengths), valid_length_batch_offset)
+
+
+def subsampling_depthwise_desc(*, input, weights, bias, output, valid_lengths, batch_size: int, input_height: int,
+                               input_width: int, channels: int, steps: int, valid_length_batch_offset: int = 0,
+                               precision: str | None = None,
+                               label: str = "subsampling-depthwise") -> SubsamplingDepthwiseDesc:
+    if precision is None:
+        precision = "f16" if weights.dtype == np.float16 else "f32"
+    return SubsamplingDepthwiseDesc(ctypes.sizeof(SubsamplingDepthwiseDesc), label.encode(), PRECISION[precision],
+                                    batch_size, input_height, input_width, channels, *_slice(input),
+                                    *_slice(weights), *_slice(bias), *_slice(output), *_slice(valid_lengths),
+                                    valid_length_batch_offset, steps)
+
+
+def subsampling_mask_desc(*, values, valid_lengths, batch_size: int, height: int, width: int, channels: int,
+                          steps: int, valid_length_batch_offset: int = 0, precision: str | None = None,
+                          label: str = "subsampling-time-mask") -> SubsamplingMaskDesc:
+    if precision is None:
+        precision = "f16" if values.dtype == np.float16 else "f32"
+    return SubsamplingMaskDesc(ctypes.sizeof(SubsamplingMaskDesc), label.encode(), PRECISION[precision], batch_size,
+                               height, width, channels, *_slice(values), *_slice(valid_lengths),
+                               valid_length_batch_offset, steps)
+
+
+class SubsamplingOp:
+    """One subsampling convolution dispatch: kind "fused" (conv0 + ReLU +
+    depthwise2), "depthwise" or "mask" (subsampling.ts createDispatch)."""
+
+    _DESC = {"fused": (subsampling_fused_desc, "pk_subsampling_fused_create"),
+             "depthwise": (subsampling_depthwise_desc, "pk_subsampling_depthwise_create"),
+             "mask": (subsampling_mask_desc, "pk_subsampling_mask_create")}
+
+    def __init__(self, ctx: Context, kind: str, **descriptor):
+        make, create = self._DESC[kind]
+        self.desc = make(**descriptor)
+        handle = ctypes.c_void_p()
+        check(getattr(load(), create)(ctx.handle, ctypes.byref(self.desc), ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def enqueue(self, active_batch: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_subsampling_enqueue(self.handle, active_batch, stream))
+        else:
+            check(load().pk_subsampling_enqueue_timed(self.handle, active_batch, stream,
+                                                      start.handle if start else None, end.handle if end else None))
+
+    def plan(self, active_batch: int = 0) -> SubsamplingPlanInfo:
+        info = SubsamplingPlanInfo()
+        check(load().pk_subsampling_plan(self.handle, active_batch, ctypes.byref(info)))
+        return info
+
+    def destroy(self) -> None:
+        check(load().pk_subsampling_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_subsampling_release(self.handle))
+            self.handle = None
+
+
 _ENCODER_MATRICES = ("ff1_linear1", "ff1_linear2", "qkv", "o_proj", "pointwise1", "pointwise2", "ff2_linear1",
                      "ff2_linear2")
 _ENCODER_VECTORS = ("projected_positions", "bias_u", "bias_v", "depthwise", "bn_scale", "bn_shift")
@@ -757,16 +946,41 @@ def encoder_layer(weights: dict) -> EncoderLayer:
     return layer
 
 
+_SUBSAMPLING_MATRICES = ("pointwise3", "pointwise6", "linear")
+
+
+def encoder_subsampling(weights: dict) -> EncoderSubsampling:
+    """An EncoderSubsampling from a dict keyed by its field names (each
+    matrix a (packed, palette) pair), holding DeviceArrays or addresses."""
+    front = EncoderSubsampling()
+    for name, _ in EncoderSubsampling._fields_:
+        if name in _SUBSAMPLING_MATRICES:
+            packed, palette = weights[name]
+            setattr(front, name, EncoderMatrix(_addr(packed), _addr(palette)))
+        else:
+            setattr(front, name, _addr(weights[name]))
+    return front
+
+
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = False,
+                 subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
+                 projector=None, projector_bias=None, projected_output=None, projected_channels: int = 0,
                  label: str = "encoder") -> EncoderDesc:
-    """An EncoderDesc over `layers` (dicts as encoder_layer takes); the
-    returned structure keeps its layer array alive."""
+    """An EncoderDesc over `layers` (dicts as encoder_layer takes), with the
+    optional front end (`subsampling` dict, feature frames and lengths) and
+    projector ((packed, palette) pair, bias, output); the returned structure
+    keeps what it points to alive."""
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
+    front = encoder_subsampling(subsampling) if subsampling is not None else None
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), ENCODER_FUSED_GLU if fused_glu else 0, label.encode(),
                        PRECISION["f16"], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),
-                       _addr(output))
-    desc._keep = array
+                       _addr(output), ctypes.pointer(front) if front is not None else None, feature_frames,
+                       _addr(feature_lengths) if feature_lengths is not None else None,
+                       EncoderMatrix(*(_addr(x) for x in projector)) if projector is not None else EncoderMatrix(),
+                       _addr(projector_bias) if projector_bias is not None else None, projected_channels,
+                       _addr(projected_output) if projected_output is not None else None)
+    desc._keep = (array, front)
     return desc
 
 

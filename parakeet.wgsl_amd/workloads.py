@@ -381,11 +381,39 @@ class EncoderStack:
     valid: np.ndarray
     batch: int
     frames: int
+    # Front end (None without it): f32 feature-major fbank [windows, 128,
+    # feature_frames], raw lengths, and the weights keyed like
+    # pk_encoder_subsampling.
+    features: np.ndarray | None = None
+    feature_lengths: np.ndarray | None = None
+    subsampling: dict | None = None
+    # Projector (None without it): (packed, palette [1, 32] f16), f32 bias.
+    projector: tuple | None = None
+    projector_bias: np.ndarray | None = None
+
+    @property
+    def feature_frames(self) -> int:
+        return 0 if self.features is None else self.features.shape[2]
 
     def gemm_flops(self, batch: int | None = None) -> int:
-        rows = (self.batch if batch is None else batch) * self.frames
+        batch = self.batch if batch is None else batch
+        rows = batch * self.frames
         per_layer = sum(2 * rows * k * n for _, k, n, _ in ENCODER_MATRICES.values())
-        return per_layer * len(self.layers)
+        total = per_layer * len(self.layers)
+        if self.subsampling is not None:
+            h2 = subsampled_length(self.feature_frames, 2)
+            total += 2 * batch * (h2 * 32 + self.frames * 16) * 256 * 256 + 2 * rows * 4096 * 1024
+        if self.projector is not None:
+            total += 2 * rows * 1024 * self.projector_bias.size
+        return total
+
+    def front_end_flops(self, batch: int | None = None) -> int:
+        """Multiply-adds x 2 of the three convolutions of the front end."""
+        if self.subsampling is None:
+            return 0
+        batch = self.batch if batch is None else batch
+        h1, h2 = subsampled_length(self.feature_frames, 1), subsampled_length(self.feature_frames, 2)
+        return 2 * 9 * 256 * batch * (h1 * 64 + h2 * 32 + self.frames * 16)
 
     def attention_flops(self, batch: int | None = None) -> int:
         batch = self.batch if batch is None else batch
@@ -423,10 +451,49 @@ def encoder_layer_weights(rng: np.random.Generator, frames: int, lut_std: float 
     return layer
 
 
+def subsampled_length(length: int, steps: int) -> int:
+    """Frames after `steps` same-padded stride-2 convolutions."""
+    for _ in range(steps):
+        length = (length + 1) // 2
+    return length
+
+
+def subsampling_weights(rng: np.random.Generator) -> dict:
+    """Front-end weights keyed like pk_encoder_subsampling: conv0 and the
+    depthwise kernels [3, 3, 256] f16 ~ N(0, 0.3), biases ~ N(0, 0.05),
+    5-bit pointwise 256->256 and flatten 4096->1024 palettes (LUTs ~
+    N(0, 0.05) and N(0, 0.08), centred, so the features reach the layers
+    at about unit scale)."""
+    def kernel():
+        return normal(rng, (3, 3, 256), 0.3, np.float16)
+
+    def bias(n):
+        return normal(rng, (n,), 0.05, np.float32)
+    front = {"conv0_weights": kernel(), "conv0_bias": bias(256), "depthwise2_weights": kernel(),
+             "depthwise2_bias": bias(256)}
+    def centred_lut(std):
+        # These matrices act on ReLU outputs (all >= 0): a LUT mean would add
+        # the same offset to every output, so the random LUTs are centred.
+        lut = rng.standard_normal((1, 32)) * std
+        return (lut - lut.mean()).astype(np.float16)
+    front["pointwise3"] = (random_packed_words(rng, 5, 256, 256), centred_lut(0.05))
+    front["pointwise3_bias"] = bias(256)
+    front["depthwise5_weights"], front["depthwise5_bias"] = kernel(), bias(256)
+    front["pointwise6"] = (random_packed_words(rng, 5, 256, 256), centred_lut(0.05))
+    front["pointwise6_bias"] = bias(256)
+    front["linear"] = (random_packed_words(rng, 5, 4096, 1024), centred_lut(0.08))
+    front["linear_bias"] = bias(1024)
+    return front
+
+
 def encoder_stack(seed: int = 0, windows: int = 16, frames: int = 188, layers: int = 24,
-                  valid=None) -> EncoderStack:
+                  valid=None, front_end: bool = False, projector: bool = False,
+                  feature_lengths=None) -> EncoderStack:
     """Subsampled features [windows x frames x 1024] f16 ~ N(0,1) and
-    `layers` random layers: uniform 5/6-bit codes with LUTs ~ N(0, 0.02)
+    `layers` random layers (with `front_end`, also an fbank [windows, 128,
+    8T-3] f32 ~ N(0,1) with raw lengths uniform in [ceil(F/2), F] from which
+    the valid lengths follow, and the front-end weights; with `projector`, a
+    5-bit 1024->640 projector, LUT ~ N(0, 0.02), bias ~ N(0, 0.01)): uniform 5/6-bit codes with LUTs ~ N(0, 0.02)
     (QKV with one LUT per Q/K/V block), LayerNorm gamma ~ 1 + N(0, 0.1) and
     beta ~ N(0, 0.1), projected positions ~ N(0, 0.6), u, v ~ N(0, 0.02),
     depthwise ~ N(0, 0.05), folded BN scale ~ 1 + N(0, 0.1) and shift ~
@@ -436,4 +503,17 @@ def encoder_stack(seed: int = 0, windows: int = 16, frames: int = 188, layers: i
     if valid is None:
         valid = rng.integers((frames + 1) // 2, frames + 1, size=windows)
     stack = [encoder_layer_weights(rng, frames) for _ in range(layers)]
-    return EncoderStack(x, stack, np.asarray(valid, dtype=np.uint32), windows, frames)
+    enc = EncoderStack(x, stack, np.asarray(valid, dtype=np.uint32), windows, frames)
+    if front_end:
+        # 8T - 3 fbank frames subsample to T (1501 -> 751 -> 376 -> 188)
+        feature_frames = 8 * frames - 3
+        enc.features = rng.standard_normal((windows, 128, feature_frames)).astype(np.float32)
+        if feature_lengths is None:
+            feature_lengths = rng.integers((feature_frames + 1) // 2, feature_frames + 1, size=windows)
+        enc.feature_lengths = np.asarray(feature_lengths, dtype=np.uint32)
+        enc.valid = np.array([subsampled_length(int(n), 3) for n in enc.feature_lengths], dtype=np.uint32)
+        enc.subsampling = subsampling_weights(rng)
+    if projector:
+        enc.projector = (random_packed_words(rng, 5, 1024, 640), normal(rng, (1, 32), 0.02, np.float16))
+        enc.projector_bias = normal(rng, (640,), 0.01, np.float32)
+    return enc

@@ -58,10 +58,15 @@ def test_struct_layouts_match_the_c_compiler(abi, tmp_path):
                "pk_device_info": abi.DeviceInfo, "pk_conv_desc": abi.ConvDesc,
                "pk_conv_plan_info": abi.ConvPlanInfo, "pk_attention_desc": abi.AttentionDesc,
                "pk_attention_plan_info": abi.AttentionPlanInfo, "pk_layernorm_desc": abi.LayerNormDesc,
+               "pk_subsampling_fused_desc": abi.SubsamplingFusedDesc,
+               "pk_subsampling_depthwise_desc": abi.SubsamplingDepthwiseDesc,
+               "pk_subsampling_mask_desc": abi.SubsamplingMaskDesc,
+               "pk_subsampling_plan_info": abi.SubsamplingPlanInfo,
                "pk_encoder_matrix": abi.EncoderMatrix, "pk_encoder_layer": abi.EncoderLayer,
-               "pk_encoder_desc": abi.EncoderDesc}
+               "pk_encoder_subsampling": abi.EncoderSubsampling, "pk_encoder_desc": abi.EncoderDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', '#include "pk_conv.h"',
-             '#include "pk_attention.h"', '#include "pk_layernorm.h"', '#include "pk_encoder.h"',
+             '#include "pk_attention.h"', '#include "pk_layernorm.h"', '#include "pk_subsampling.h"',
+             '#include "pk_encoder.h"',
              "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
@@ -363,6 +368,157 @@ def test_layernorm_contract_messages(abi):
         _validate_ln(abi, **kw)
 
 
+# ---------------------------------------------------------------- subsampling
+
+
+def test_subsampling_lengths_match_reference_kats(abi):
+    """test/webgpu/subsampling-kernel-shapes.test.ts:27-50."""
+    lib = abi.load()
+    heights, widths = [1501], [128]
+    for _ in range(3):
+        heights.append(lib.pk_subsampling_output_dimension(heights[-1]))
+        widths.append(lib.pk_subsampling_output_dimension(widths[-1]))
+    assert heights == [1501, 751, 376, 188] and widths == [128, 64, 32, 16]
+    assert [lib.pk_subsampling_valid_length(1500, s) for s in (1, 2, 3)] == [750, 375, 188]
+    assert [lib.pk_subsampling_valid_length(799, s) for s in (1, 2, 3)] == [400, 200, 100]
+    assert lib.pk_subsampling_valid_length(1, 3) == 1
+    assert lib.pk_subsampling_output_dimension(0) == 0
+
+
+def _fused_fakes(batch=3, frames=1501, elem=2):
+    dtype = np.float16 if elem == 2 else np.float32
+    out_rows = abi_lengths(frames, 2)
+    return dict(input=_Fake(0x10000000, batch * frames * 128 * 4, np.float32),
+                conv0_weights=_Fake(0x20000000, 9 * 256 * elem, dtype), conv0_bias=_Fake(0x20100000, 1024),
+                depthwise_weights=_Fake(0x20200000, 9 * 256 * elem, dtype), depthwise_bias=_Fake(0x20300000, 1024),
+                output=_Fake(0x40000000, batch * out_rows * 32 * 256 * elem, dtype),
+                valid_lengths=_Fake(0x50000000, 4 * batch, np.uint32), batch_size=batch, input_height=frames,
+                label="subsampling-fused-conv0-depthwise2-batch-0-size-3")
+
+
+def abi_lengths(n, steps):
+    for _ in range(steps):
+        n = (n + 1) // 2
+    return n
+
+
+def _validate_fused(abi, **kw):
+    desc = abi.subsampling_fused_desc(**kw)
+    abi.check(abi.load().pk_subsampling_fused_validate(ctypes.byref(desc)))
+
+
+def test_subsampling_fused_contract(abi):
+    """planFusedSubsamplingConv0Depthwise2 / createDispatch
+    (subsampling.ts:145-206, :334-387): the B3 plan's byte counts
+    (subsampling-kernel-shapes.test.ts:83-110) and the reference messages."""
+    _validate_fused(abi, **_fused_fakes())
+    _validate_fused(abi, **_fused_fakes(elem=4))
+    _validate_fused(abi, **_fused_fakes(batch=1, frames=6001))  # longer windows are allowed here
+    kw = _fused_fakes()
+    kw["output"] = _Fake(kw["output"].ptr, 3 * 376 * 32 * 256 * 2 - 2)
+    with pytest.raises(abi.PaletteRangeError, match=re.escape(
+            "subsampling-fused-conv0-depthwise2-batch-0-size-3 output needs 18481152 bytes; arena slice has "
+            "18481150")):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["input"] = _Fake(kw["input"].ptr, 3 * 1501 * 128 * 4 - 4)
+    with pytest.raises(abi.PaletteRangeError, match="input needs 2305536 bytes"):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["valid_length_batch_offset"] = 3
+    with pytest.raises(abi.PaletteRangeError, match="valid lengths needs 24 bytes; arena slice has 12"):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["input_width"] = 80
+    with pytest.raises(abi.PaletteRangeError, match=re.escape("Fused conv0+depthwise2 requires fixed")):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["batch_size"] = 0
+    with pytest.raises(abi.PaletteRangeError, match="batchSize must be a positive integer"):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["conv0_weights"] = _Fake(kw["conv0_weights"].ptr, 9 * 256 * 4, np.float16)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "conv0 weights must be float16 kh-kw-output-channel-vec4 logical [3,3,256], storage [3,3,64,4], "
+            "4608 bytes")):
+        _validate_fused(abi, **kw)
+    kw = _fused_fakes()
+    kw["depthwise_bias"] = _Fake(kw["depthwise_bias"].ptr, 512)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "depthwise2 bias must be float32 output-channel logical [256], storage [256], 1024 bytes")):
+        _validate_fused(abi, **kw)
+
+
+def _dw_fakes(batch=3, elem=2):
+    dtype = np.float16 if elem == 2 else np.float32
+    return dict(input=_Fake(0x10000000, batch * 376 * 32 * 256 * elem, dtype),
+                weights=_Fake(0x20000000, 9 * 256 * elem, dtype), bias=_Fake(0x20100000, 1024),
+                output=_Fake(0x40000000, batch * 188 * 16 * 256 * elem, dtype),
+                valid_lengths=_Fake(0x50000000, 4 * batch, np.uint32), batch_size=batch, input_height=376,
+                input_width=32, channels=256, steps=3, label="subsampling-depthwise5")
+
+
+def _validate_dw(abi, **kw):
+    desc = abi.subsampling_depthwise_desc(**kw)
+    abi.check(abi.load().pk_subsampling_depthwise_validate(ctypes.byref(desc)))
+
+
+def test_subsampling_depthwise_contract(abi):
+    """planDepthwise / createDispatch (subsampling.ts:495-531, :795-853) and
+    the depthwise5 plan of subsampling-kernel-shapes.test.ts:52-81."""
+    _validate_dw(abi, **_dw_fakes())
+    _validate_dw(abi, **_dw_fakes(batch=1, elem=4))
+    kw = _dw_fakes()
+    kw["channels"] = 258
+    with pytest.raises(abi.PaletteRangeError, match="Subsampling channels must be divisible by four"):
+        _validate_dw(abi, **kw)
+    kw = _dw_fakes()
+    kw["steps"] = 0
+    with pytest.raises(abi.PaletteRangeError,
+                       match="subsampling-depthwise5 valid-length subsampling steps must be a positive integer"):
+        _validate_dw(abi, **kw)
+    kw = _dw_fakes()
+    kw["output"] = _Fake(kw["output"].ptr, 100)
+    with pytest.raises(abi.PaletteRangeError, match=re.escape(
+            "subsampling-depthwise5 output needs 4620288 bytes; arena slice has 100")):
+        _validate_dw(abi, **kw)
+    kw = _dw_fakes()
+    kw["weights"] = _Fake(kw["weights"].ptr, 100)
+    with pytest.raises(abi.PaletteError, match=re.escape(
+            "subsampling-depthwise5 weights must be float16 kh-kw-channel-vec4 logical [3,3,256], "
+            "storage [3,3,64,4], 4608 bytes")):
+        _validate_dw(abi, **kw)
+
+
+def test_subsampling_mask_contract(abi):
+    """SubsamplingTimeMaskKernel.createDispatch (subsampling.ts:698-748)."""
+    def validate(**kw):
+        base = dict(values=_Fake(0x10000000, 3 * 188 * 16 * 256 * 2), valid_lengths=_Fake(0x50000000, 12),
+                    batch_size=3, height=188, width=16, channels=256, steps=3,
+                    label="subsampling-pointwise6-mask")
+        base.update(kw)
+        desc = abi.subsampling_mask_desc(**base)
+        abi.check(abi.load().pk_subsampling_mask_validate(ctypes.byref(desc)))
+    validate()
+    with pytest.raises(abi.PaletteRangeError, match="Subsampling mask channels must be divisible by four"):
+        validate(channels=6)
+    with pytest.raises(abi.PaletteRangeError, match="height must be a positive integer"):
+        validate(height=0)
+    with pytest.raises(abi.PaletteRangeError, match="values needs 4620288 bytes; arena slice has 64"):
+        validate(values=_Fake(0x10000000, 64))
+    with pytest.raises(abi.PaletteRangeError, match="valid lengths needs 16 bytes"):
+        validate(valid_length_batch_offset=1)
+
+
+def test_subsampling_null_handles(abi):
+    lib = abi.load()
+    assert lib.pk_subsampling_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_subsampling_plan(None, 0, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_subsampling_destroy(None) == abi.OK
+    assert lib.pk_subsampling_release(None) == abi.OK
+    assert lib.pk_subsampling_fused_validate(None) == abi.INVALID_ARGUMENT
+
+
 # ---------------------------------------------------------------- encoder stack
 
 
@@ -387,6 +543,24 @@ def _encoder_fakes(layers=2, batch=16, frames=188):
     rows = batch * frames
     return dict(layers=stack, valid_lengths=take(), input=take(rows * 2048), output=take(rows * 2048),
                 batch_size=batch, frames=frames)
+
+
+def _front_fakes(kw, batch=16, feature_frames=1501):
+    at = [0x3000000000]
+
+    def take(nbytes=1 << 20):
+        addr = at[0]
+        at[0] += (nbytes + 0xFFFF) // 0x10000 * 0x10000
+        return addr
+    front = {name: take() for name in ("conv0_weights", "conv0_bias", "depthwise2_weights", "depthwise2_bias",
+                                       "pointwise3_bias", "depthwise5_weights", "depthwise5_bias",
+                                       "pointwise6_bias", "linear_bias")}
+    for name in ("pointwise3", "pointwise6", "linear"):
+        front[name] = (take(4 << 20), take())
+    kw.update(subsampling=front, feature_frames=feature_frames, feature_lengths=take(),
+              input=take(batch * 128 * feature_frames * 4), projector=(take(4 << 20), take()),
+              projector_bias=take(), projected_channels=640, projected_output=take(batch * 188 * 640 * 2))
+    return kw
 
 
 def _validate_encoder(abi, **kw):
@@ -434,6 +608,40 @@ def test_encoder_validate_stack_fields(abi):
     desc.flags = 0x8
     with pytest.raises(abi.PaletteError, match="unknown flags"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+
+
+def test_encoder_validate_front_end_and_projector(abi):
+    """The whole graph of ParakeetEncoderGraph.encode (encoder.ts:1690-1706):
+    subsampling front end, 24 layers, projector."""
+    _validate_encoder(abi, **_front_fakes(_encoder_fakes(layers=24)))
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["feature_frames"] = 1500  # 750 -> 375 -> 188 as well
+    _validate_encoder(abi, **kw)
+    kw["feature_frames"] = 1499  # -> 188 as well ((1499+1)/2 = 750)
+    _validate_encoder(abi, **kw)
+    kw["feature_frames"] = 1490  # 745 -> 373 -> 187
+    with pytest.raises(abi.PaletteRangeError, match="188 encoder frames do not follow from 1490 feature frames"):
+        _validate_encoder(abi, **kw)
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["feature_lengths"] = None
+    with pytest.raises(abi.PaletteError, match="needs per-window feature lengths"):
+        _validate_encoder(abi, **kw)
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["subsampling"]["pointwise6"] = (kw["subsampling"]["pointwise6"][0], 0)
+    with pytest.raises(abi.PaletteError, match=re.escape("encoder.subsampling-pointwise6")):
+        _validate_encoder(abi, **kw)
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["subsampling"]["conv0_bias"] += 4
+    with pytest.raises(abi.PaletteError, match=re.escape("encoder.subsampling-fused-conv0-depthwise2 conv0 bias")):
+        _validate_encoder(abi, **kw)
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["projected_output"] = kw["output"] + 1024
+    with pytest.raises(abi.PaletteError, match="projected output must not overlap"):
+        _validate_encoder(abi, **kw)
+    kw = _front_fakes(_encoder_fakes(layers=1))
+    kw["projected_channels"] = 636
+    with pytest.raises(abi.PaletteError, match="encoder-projector"):
+        _validate_encoder(abi, **kw)
 
 
 def test_encoder_null_handles(abi):

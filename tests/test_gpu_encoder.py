@@ -47,21 +47,42 @@ def upload_layers(scope, layers):
 
 
 class Stack:
-    """An EncoderOp over uploaded layers with its input, output and lengths."""
+    """An EncoderOp over uploaded layers with its input, output and lengths
+    (and the front end and projector when the stack has them)."""
 
     def __init__(self, abi, ctx, scope, stack, *, fused_glu=False):
         self.ctx = ctx
-        self.input = scope.put(stack.x)
         self.valid = scope.put(stack.valid)
         self.output = scope.put(np.full_like(stack.x, 77))
+        extra = {}
+        if stack.subsampling is not None:
+            self.input = scope.put(stack.features)
+            self.feature_lengths = scope.put(stack.feature_lengths)
+            front = {k: (tuple(scope.put(v) for v in val) if isinstance(val, tuple) else scope.put(val))
+                     for k, val in stack.subsampling.items()}
+            extra.update(subsampling=front, feature_frames=stack.feature_frames,
+                         feature_lengths=self.feature_lengths)
+        else:
+            self.input = scope.put(stack.x)
+        self.projected = None
+        if stack.projector is not None:
+            channels = stack.projector_bias.size
+            self.projected = scope.put(np.full((stack.x.shape[0], channels), 77, np.float16))
+            extra.update(projector=tuple(scope.put(v) for v in stack.projector),
+                         projector_bias=scope.put(stack.projector_bias), projected_channels=channels,
+                         projected_output=self.projected)
         self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
                                 input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
-                                fused_glu=fused_glu)
+                                fused_glu=fused_glu, **extra)
 
     def run(self, active=0, graph=False):
         self.op.enqueue(active, graph=graph)
         self.ctx.synchronize()
         return self.output.download()
+
+    def run_both(self, active=0, graph=False):
+        out = self.run(active, graph)
+        return out, self.projected.download()
 
     def release(self):
         self.op.release()
@@ -193,3 +214,75 @@ def test_encoder_rejects_bad_active_batch(abi, ctx, scope, workloads):
             enc.op.enqueue(3)
     finally:
         enc.release()
+
+
+def valid_rows(array, stack, count=None):
+    """The frames below each window's valid length (what the decoder reads)."""
+    count = stack.batch if count is None else count
+    parts = [array[b * stack.frames:b * stack.frames + int(stack.valid[b])] for b in range(count)]
+    return np.concatenate(parts)
+
+
+def test_encoder_graph_with_front_end_and_projector(abi, ctx, scope, oracle, workloads):
+    """fbank -> subsampling -> 2 layers -> projector (encoder.ts:1690-1706),
+    2 windows of 1501 fbank frames, against both oracle chains on the frames
+    below each window's length, and graph replay bit-exact."""
+    stack = workloads.encoder_stack(seed=21, windows=2, frames=188, layers=2, front_end=True, projector=True,
+                                    feature_lengths=[1501, 799])
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        assert enc.op.info()[0] == 6 + 2 * 15 + 1
+        got, projected = enc.run_both()
+        graph, graph_projected = enc.run_both(graph=True)
+        np.testing.assert_array_equal(graph.view(np.uint16), got.view(np.uint16))
+        np.testing.assert_array_equal(graph_projected.view(np.uint16), projected.view(np.uint16))
+    finally:
+        enc.release()
+    assert np.isfinite(got).all() and np.isfinite(projected).all()
+    results = {}
+    for mode in ("f64", "f16-chain"):
+        results[mode] = oracle.encoder_graph(None, stack.layers, stack.valid, batch=2, frames=188,
+                                             front=stack.subsampling, features=stack.features,
+                                             feature_lengths=stack.feature_lengths, projector=stack.projector,
+                                             projector_bias=stack.projector_bias, gemm_mode=mode, threads=THREADS)
+    truth, reference = results["f64"], results["f16-chain"]
+    for name, g, t, r in (("output", got, truth[0], reference[0]), ("projected", projected, truth[1], reference[1])):
+        norm, worst = oracle.relative_errors(valid_rows(g, stack), valid_rows(t, stack))
+        gap, _ = oracle.relative_errors(valid_rows(t, stack), valid_rows(r, stack))
+        norm16, _ = oracle.relative_errors(valid_rows(g, stack), valid_rows(r, stack))
+        every, _ = oracle.relative_errors(g, t)
+        print(f"front end + 2 layers, {name}: vs f64 chain {norm:.2e} (max {worst:.2e}, every row {every:.2e}); "
+              f"vs f16 chain {norm16:.2e}; chains apart {gap:.2e}", flush=True)
+        assert norm <= 1e-2 and every <= 1e-2, (name, norm, every)
+        assert norm16 <= 1.1 * gap + 1e-3, (name, norm16, gap)
+
+
+def test_encoder_graph_full_size(abi, ctx, scope, oracle, workloads):
+    """16 windows x 1501 fbank frames -> 24 layers -> projector: graph replay
+    and the active prefix bit-exact, window 0 against the f64 chain."""
+    stack = workloads.encoder_stack(seed=22, windows=16, frames=188, layers=24, front_end=True, projector=True)
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        launches, device_bytes = enc.op.info()
+        assert launches == 6 + 24 * 15 + 1
+        eager, eager_projected = enc.run_both()
+        graph, graph_projected = enc.run_both(graph=True)
+        np.testing.assert_array_equal(graph.view(np.uint16), eager.view(np.uint16))
+        np.testing.assert_array_equal(graph_projected.view(np.uint16), eager_projected.view(np.uint16))
+        prefix, prefix_projected = enc.run_both(active=3, graph=True)
+        np.testing.assert_array_equal(windows(prefix, 188, 0, 3).view(np.uint16),
+                                      windows(eager, 188, 0, 3).view(np.uint16))
+        np.testing.assert_array_equal(windows(prefix_projected, 188, 0, 3).view(np.uint16),
+                                      windows(eager_projected, 188, 0, 3).view(np.uint16))
+    finally:
+        enc.release()
+    assert np.isfinite(eager).all() and np.isfinite(eager_projected).all()
+    out, projected = oracle.encoder_graph(None, stack.layers, stack.valid[:1], batch=1, frames=188,
+                                          front=stack.subsampling, features=stack.features[:1],
+                                          feature_lengths=stack.feature_lengths[:1], projector=stack.projector,
+                                          projector_bias=stack.projector_bias, gemm_mode="f64", threads=THREADS)
+    for name, g, t in (("output", windows(eager, 188, 0, 1), out),
+                       ("projected", windows(eager_projected, 188, 0, 1), projected)):
+        norm, worst = oracle.relative_errors(valid_rows(g, stack, 1), valid_rows(t, stack, 1))
+        print(f"front end + 24 layers, {name} vs f64 chain: norm {norm:.2e} max {worst:.2e}", flush=True)
+        assert norm <= 1e-2, (name, norm, worst)

@@ -655,3 +655,122 @@ def test_layernorm_unit_affine_moments(oracle):
     np.testing.assert_allclose(got.mean(axis=1), 0, atol=1e-12)
     # E[x^2] - mean^2 (the reference formula) costs a few 1e-9 at scale 100
     np.testing.assert_allclose(got.var(axis=1), var / (var + 1e-5), rtol=1e-7)
+
+
+# ---------------------------------------------------------------- subsampling
+
+
+def test_subsampled_lengths_match_reference_kats(oracle):
+    """test/webgpu/subsampling-kernel-shapes.test.ts:27-50."""
+    heights, widths = [1501], [128]
+    for _ in range(3):
+        heights.append(oracle.subsampled_length(heights[-1], 1))
+        widths.append(oracle.subsampled_length(widths[-1], 1))
+    assert heights == [1501, 751, 376, 188] and widths == [128, 64, 32, 16]
+    assert [oracle.subsampled_length(1500, s) for s in (1, 2, 3)] == [750, 375, 188]
+    assert [oracle.subsampled_length(799, s) for s in (1, 2, 3)] == [400, 200, 100]
+    assert oracle.subsampled_length(1, 3) == 1
+    for n in range(1, 300):  # floor((n + 2*1 - 3) / 2) + 1
+        assert oracle.subsampled_length(n, 1) == (n + 2 - 3) // 2 + 1
+
+
+def _torch_subsampling(oracle, features, w0, b0, wd, bd, valid):
+    """conv0 + ReLU + depthwise2 with torch.nn.functional.conv2d in float64,
+    masking conv0 rows at or past sub(L, 1) and output rows past sub(L, 2)."""
+    import torch
+    x = torch.tensor(features, dtype=torch.float64).permute(0, 2, 1).unsqueeze(1)  # [B, 1, time, bins]
+    channels = w0.shape[-1]
+    k0 = torch.tensor(np.asarray(w0, np.float64)).permute(2, 0, 1).unsqueeze(1)  # [C, 1, kh, kw]
+    kd = torch.tensor(np.asarray(wd, np.float64)).permute(2, 0, 1).unsqueeze(1)
+    c0 = torch.relu(torch.nn.functional.conv2d(x, k0, torch.tensor(b0, dtype=torch.float64), stride=2, padding=1))
+    for b, length in enumerate(valid):
+        c0[b, :, oracle.subsampled_length(length, 1):] = 0
+    out = torch.nn.functional.conv2d(c0, kd, torch.tensor(bd, dtype=torch.float64), stride=2, padding=1,
+                                     groups=channels)
+    for b, length in enumerate(valid):
+        out[b, :, oracle.subsampled_length(length, 2):] = 0
+    return out.permute(0, 2, 3, 1).numpy()
+
+
+def _subsampling_case(seed, batch=3, bins=20, frames=45, channels=8):
+    rng = np.random.default_rng(seed)
+    features = rng.standard_normal((batch, bins, frames)).astype(np.float32)
+    w0 = (rng.standard_normal((3, 3, channels)) * 0.3).astype(np.float16)
+    wd = (rng.standard_normal((3, 3, channels)) * 0.3).astype(np.float16)
+    b0 = (rng.standard_normal(channels) * 0.1).astype(np.float32)
+    bd = (rng.standard_normal(channels) * 0.1).astype(np.float32)
+    valid = np.array([frames, 29, 1][:batch], np.uint32)
+    return features, w0, b0, wd, bd, valid
+
+
+def test_subsampling_fused_matches_torch_conv2d(oracle):
+    features, w0, b0, wd, bd, valid = _subsampling_case(1)
+    want = _torch_subsampling(oracle, features, w0, b0, wd, bd, valid)
+    got64 = oracle.subsampling_fused(features, w0, b0, wd, bd, valid, dtype=np.float64)
+    assert got64.shape == want.shape == (3, 12, 5, 8)
+    np.testing.assert_allclose(got64, want, rtol=0, atol=1e-12)
+    got32 = oracle.subsampling_fused(features, w0, b0, wd, bd, valid, dtype=np.float32)
+    np.testing.assert_allclose(got32, want, rtol=0, atol=1e-5)
+    got16 = oracle.subsampling_fused(features, w0, b0, wd, bd, valid, dtype=np.float16)
+    scale = np.abs(want).max()
+    assert np.abs(got16.astype(np.float64) - want).max() <= 4e-3 * scale
+    # the f16 profile rounds conv0 through f16 before the depthwise sum
+    assert not np.array_equal(got16, got32.astype(np.float16))
+
+
+def test_subsampling_fused_one_hot_taps(oracle):
+    """Centre taps of 1 and zero biases: out[y, x] = ReLU(features[4y, 4x])
+    on the rows below sub(L, 2), zero past them."""
+    features, _, _, _, _, valid = _subsampling_case(2, frames=61, bins=24)
+    one_hot = np.zeros((3, 3, 8), np.float16)
+    one_hot[1, 1] = 1
+    zero = np.zeros(8, np.float32)
+    got = oracle.subsampling_fused(features, one_hot, zero, one_hot, zero, valid, dtype=np.float16)
+    for b, length in enumerate(valid):
+        keep = oracle.subsampled_length(length, 2)
+        want = np.maximum(features[b, 0::4, 0::4].T, 0).astype(np.float16)  # [time/4, bins/4]
+        np.testing.assert_array_equal(got[b, :keep, :, 0], want[:keep])
+        assert not got[b, keep:].any()
+
+
+def test_subsampling_fused_reads_the_frame_at_an_odd_length(oracle):
+    """conv0 is masked by its own valid rows, not the features: for odd L the
+    last valid conv0 row reads feature frame L (subsampling.ts:1152-1170)."""
+    features, w0, b0, wd, bd, _ = _subsampling_case(3, batch=1, frames=45)
+    valid = np.array([29], np.uint32)
+    base = oracle.subsampling_fused(features, w0, b0, wd, bd, valid, dtype=np.float64)
+    bumped = features.copy()
+    bumped[0, :, 29] += 5.0
+    assert not np.array_equal(oracle.subsampling_fused(bumped, w0, b0, wd, bd, valid, dtype=np.float64), base)
+    later = features.copy()
+    later[0, :, 30:] += 5.0
+    np.testing.assert_array_equal(oracle.subsampling_fused(later, w0, b0, wd, bd, valid, dtype=np.float64), base)
+
+
+def test_subsampling_depthwise_matches_torch_conv2d(oracle):
+    import torch
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 23, 10, 8))
+    w = rng.standard_normal((3, 3, 8)) * 0.3
+    bias = (rng.standard_normal(8) * 0.1).astype(np.float32)
+    valid = np.array([180, 100, 1], np.uint32)  # raw lengths: stage 3 input rows 23, 13, 1
+    got = oracle.subsampling_depthwise(x, w, bias, valid, 3)
+    t = torch.tensor(x).permute(0, 3, 1, 2).clone()
+    for b, length in enumerate(valid):
+        t[b, :, oracle.subsampled_length(length, 2):] = 0
+    out = torch.nn.functional.conv2d(t, torch.tensor(w).permute(2, 0, 1).unsqueeze(1),
+                                     torch.tensor(bias, dtype=torch.float64), stride=2, padding=1, groups=8)
+    for b, length in enumerate(valid):
+        out[b, :, oracle.subsampled_length(length, 3):] = 0
+    np.testing.assert_allclose(got, out.permute(0, 2, 3, 1).numpy(), rtol=0, atol=1e-12)
+    got16 = oracle.subsampling_depthwise(x.astype(np.float16), w, bias, valid, 3)
+    np.testing.assert_allclose(got16.astype(np.float64), got, rtol=0, atol=2e-2)
+
+
+def test_subsampling_mask_zeroes_rows_past_the_length(oracle):
+    x = np.arange(2 * 9 * 3 * 4, dtype=np.float32).reshape(2, 9, 3, 4) + 1
+    got = oracle.subsampling_mask(x, np.array([60, 33], np.uint32), 3)  # lengths 8 and 5
+    np.testing.assert_array_equal(got[0, :8], x[0, :8])
+    assert not got[0, 8:].any()
+    np.testing.assert_array_equal(got[1, :5], x[1, :5])
+    assert not got[1, 5:].any()
