@@ -1,8 +1,10 @@
 /*
  * pk_napi.c - Node-API (N-API 8) addon over the palette GEMM C ABI
  * (include/pk_palette.h), the fused Conformer convolution tail
- * (include/pk_conv.h) and the relative-position attention
- * (include/pk_attention.h). It is the thin native layer under the JavaScript
+ * (include/pk_conv.h), the relative-position attention
+ * (include/pk_attention.h), the row LayerNorm (include/pk_layernorm.h), the
+ * subsampling convolutions (include/pk_subsampling.h) and the encoder graph
+ * (include/pk_encoder.h). It is the thin native layer under the JavaScript
  * host in ../host: every function forwards to one pk_* call, converts device
  * pointers to BigInt, and turns a failing pk_status into a thrown Error
  * (RangeError for PK_RANGE_ERROR, as the reference throws RangeError for
@@ -23,7 +25,10 @@
 
 #include "pk_attention.h"
 #include "pk_conv.h"
+#include "pk_encoder.h"
+#include "pk_layernorm.h"
 #include "pk_palette.h"
+#include "pk_subsampling.h"
 
 #define NAPI_CALL(env, call)                                              \
   do {                                                                    \
@@ -802,6 +807,540 @@ static napi_value js_attention_plan(napi_env env, napi_callback_info info) {
   return obj;
 }
 
+/* ---- row LayerNorm ------------------------------------------------------- */
+
+static void layernorm_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  pk_layernorm_release((pk_layernorm_op *)data);
+}
+
+/* {label, precision, rows, channels, input, inputBytes, gamma, gammaBytes,
+   beta, betaBytes, output, outputBytes, epsilon?} */
+static int parse_layernorm_desc(napi_env env, napi_value o, pk_layernorm_desc *d, char **label) {
+  memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  *label = NULL;
+  uint64_t input = 0, gamma = 0, beta = 0, output = 0;
+  parse_precision(env, o, &d->precision);
+  if (!prop_u32(env, o, "rows", &d->rows) || !prop_u32(env, o, "channels", &d->channels) ||
+      !prop_u64(env, o, "input", &input) || !prop_u64(env, o, "inputBytes", &d->input_bytes) ||
+      !prop_u64(env, o, "gamma", &gamma) || !prop_u64(env, o, "gammaBytes", &d->gamma_bytes) ||
+      !prop_u64(env, o, "beta", &beta) || !prop_u64(env, o, "betaBytes", &d->beta_bytes) ||
+      !prop_u64(env, o, "output", &output) || !prop_u64(env, o, "outputBytes", &d->output_bytes)) {
+    bad_argument(env, "LayerNorm descriptor is missing a required field");
+    return 0;
+  }
+  napi_value eps;
+  if (prop(env, o, "epsilon", &eps)) {
+    double e = 0;
+    napi_get_value_double(env, eps, &e);
+    d->has_epsilon = 1;
+    d->epsilon = (float)e;
+  }
+  d->input = (const void *)(uintptr_t)input;
+  d->gamma = (const float *)(uintptr_t)gamma;
+  d->beta = (const float *)(uintptr_t)beta;
+  d->output = (void *)(uintptr_t)output;
+  *label = prop_string(env, o, "label");
+  d->label = *label;
+  return 1;
+}
+
+static napi_value js_layernorm_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  pk_layernorm_desc d;
+  char *label;
+  if (!parse_layernorm_desc(env, argv[0], &d, &label)) return NULL;
+  const int status = pk_layernorm_validate(&d);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+static napi_value js_layernorm_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2], ext;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  pk_layernorm_desc d;
+  char *label;
+  if (!parse_layernorm_desc(env, argv[1], &d, &label)) return NULL;
+  pk_layernorm_op *op = NULL;
+  const int status = pk_layernorm_create((pk_context *)get_external(env, argv[0]), &d, &op);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  NAPI_CALL(env, napi_create_external(env, op, layernorm_finalize, NULL, &ext));
+  return ext;
+}
+
+/* layernormEnqueue(op, activeRows, stream?, startEvent?, endEvent?) */
+static napi_value js_layernorm_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  uint32_t rows = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &rows))
+    return bad_argument(env, "active rows must be a non-negative integer");
+  PK_CALL(env, pk_layernorm_enqueue_timed((pk_layernorm_op *)get_external(env, argv[0]), rows,
+                                          get_external(env, argv[2]), get_external(env, argv[3]),
+                                          get_external(env, argv[4])));
+  return undefined(env);
+}
+
+static napi_value js_layernorm_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_layernorm_destroy((pk_layernorm_op *)get_external(env, argv[0])));
+  return undefined(env);
+}
+
+/* ---- subsampling ---------------------------------------------------------- */
+
+static void subsampling_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  pk_subsampling_release((pk_subsampling_op *)data);
+}
+
+static napi_value js_subsampling_output_dimension(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  uint32_t n = 0;
+  if (!get_args(env, info, 1, argv) || !get_u32(env, argv[0], &n)) return bad_argument(env, "dimension");
+  return make_number(env, pk_subsampling_output_dimension(n));
+}
+
+static napi_value js_subsampling_valid_length(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  uint32_t n = 0, steps = 0;
+  if (!get_args(env, info, 2, argv) || !get_u32(env, argv[0], &n) || !get_u32(env, argv[1], &steps))
+    return bad_argument(env, "length and steps");
+  return make_number(env, pk_subsampling_valid_length(n, steps));
+}
+
+/* Address and byte size fields "<name>" and "<name>Bytes". */
+static int ptr_field(napi_env env, napi_value o, const char *name, const void **p, uint64_t *bytes) {
+  char key[96];
+  uint64_t a = 0;
+  snprintf(key, sizeof key, "%sBytes", name);
+  if (!prop_u64(env, o, name, &a) || !prop_u64(env, o, key, bytes)) return 0;
+  *p = (const void *)(uintptr_t)a;
+  return 1;
+}
+
+/* kind "fused": {label, precision, batchSize, inputHeight, inputWidth?,
+   channels?, input, conv0Weights, conv0Bias, depthwiseWeights,
+   depthwiseBias, output, validLengths (each with <name>Bytes),
+   validLengthBatchOffset?}; kind "depthwise": {label, precision, batchSize,
+   inputHeight, inputWidth, channels, input, weights, bias, output,
+   validLengths, validLengthBatchOffset?, validLengthSubsamplingSteps};
+   kind "mask": {label, precision, batchSize, height, width, channels,
+   values, validLengths, validLengthBatchOffset?, validLengthSubsamplingSteps}. */
+static int subsampling_call(napi_env env, napi_value kind_value, napi_value o, pk_context *ctx, int create,
+                            pk_subsampling_op **out) {
+  char kind[16] = {0};
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, kind_value, kind, sizeof kind, &len) != napi_ok) {
+    bad_argument(env, "subsampling kind must be \"fused\", \"depthwise\" or \"mask\"");
+    return -1;
+  }
+  char *label = prop_string(env, o, "label");
+  int32_t precision = PK_PRECISION_F16;
+  parse_precision(env, o, &precision);
+  int status = PK_OK, ok = 1;
+  const void *p = NULL;
+  if (strcmp(kind, "fused") == 0) {
+    pk_subsampling_fused_desc d;
+    memset(&d, 0, sizeof d);
+    d.struct_size = sizeof d;
+    d.label = label;
+    d.precision = precision;
+    d.input_width = PK_SUBSAMPLING_BINS;
+    d.channels = PK_SUBSAMPLING_CHANNELS;
+    prop_u32(env, o, "inputWidth", &d.input_width);
+    prop_u32(env, o, "channels", &d.channels);
+    prop_u32(env, o, "validLengthBatchOffset", &d.valid_length_batch_offset);
+    ok = prop_u32(env, o, "batchSize", &d.batch_size) && prop_u32(env, o, "inputHeight", &d.input_height);
+    ok = ok && ptr_field(env, o, "input", &p, &d.input_bytes);
+    d.input = (const float *)p;
+    ok = ok && ptr_field(env, o, "conv0Weights", &d.conv0_weights, &d.conv0_weights_bytes);
+    ok = ok && ptr_field(env, o, "conv0Bias", &p, &d.conv0_bias_bytes);
+    d.conv0_bias = (const float *)p;
+    ok = ok && ptr_field(env, o, "depthwiseWeights", &d.depthwise_weights, &d.depthwise_weights_bytes);
+    ok = ok && ptr_field(env, o, "depthwiseBias", &p, &d.depthwise_bias_bytes);
+    d.depthwise_bias = (const float *)p;
+    ok = ok && ptr_field(env, o, "output", &p, &d.output_bytes);
+    d.output = (void *)p;
+    ok = ok && ptr_field(env, o, "validLengths", &p, &d.valid_lengths_bytes);
+    d.valid_lengths = (const uint32_t *)p;
+    if (ok) status = create ? pk_subsampling_fused_create(ctx, &d, out) : pk_subsampling_fused_validate(&d);
+  } else if (strcmp(kind, "depthwise") == 0) {
+    pk_subsampling_depthwise_desc d;
+    memset(&d, 0, sizeof d);
+    d.struct_size = sizeof d;
+    d.label = label;
+    d.precision = precision;
+    prop_u32(env, o, "validLengthBatchOffset", &d.valid_length_batch_offset);
+    ok = prop_u32(env, o, "batchSize", &d.batch_size) && prop_u32(env, o, "inputHeight", &d.input_height) &&
+         prop_u32(env, o, "inputWidth", &d.input_width) && prop_u32(env, o, "channels", &d.channels) &&
+         prop_u32(env, o, "validLengthSubsamplingSteps", &d.valid_length_subsampling_steps);
+    ok = ok && ptr_field(env, o, "input", &d.input, &d.input_bytes);
+    ok = ok && ptr_field(env, o, "weights", &d.weights, &d.weights_bytes);
+    ok = ok && ptr_field(env, o, "bias", &p, &d.bias_bytes);
+    d.bias = (const float *)p;
+    ok = ok && ptr_field(env, o, "output", &p, &d.output_bytes);
+    d.output = (void *)p;
+    ok = ok && ptr_field(env, o, "validLengths", &p, &d.valid_lengths_bytes);
+    d.valid_lengths = (const uint32_t *)p;
+    if (ok)
+      status = create ? pk_subsampling_depthwise_create(ctx, &d, out) : pk_subsampling_depthwise_validate(&d);
+  } else if (strcmp(kind, "mask") == 0) {
+    pk_subsampling_mask_desc d;
+    memset(&d, 0, sizeof d);
+    d.struct_size = sizeof d;
+    d.label = label;
+    d.precision = precision;
+    prop_u32(env, o, "validLengthBatchOffset", &d.valid_length_batch_offset);
+    ok = prop_u32(env, o, "batchSize", &d.batch_size) && prop_u32(env, o, "height", &d.height) &&
+         prop_u32(env, o, "width", &d.width) && prop_u32(env, o, "channels", &d.channels) &&
+         prop_u32(env, o, "validLengthSubsamplingSteps", &d.valid_length_subsampling_steps);
+    ok = ok && ptr_field(env, o, "values", &p, &d.values_bytes);
+    d.values = (void *)p;
+    ok = ok && ptr_field(env, o, "validLengths", &p, &d.valid_lengths_bytes);
+    d.valid_lengths = (const uint32_t *)p;
+    if (ok) status = create ? pk_subsampling_mask_create(ctx, &d, out) : pk_subsampling_mask_validate(&d);
+  } else {
+    free(label);
+    bad_argument(env, "subsampling kind must be \"fused\", \"depthwise\" or \"mask\"");
+    return -1;
+  }
+  free(label);
+  if (!ok) {
+    bad_argument(env, "subsampling descriptor is missing a required field");
+    return -1;
+  }
+  return status;
+}
+
+/* subsamplingValidate(kind, desc) */
+static napi_value js_subsampling_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  const int status = subsampling_call(env, argv[0], argv[1], NULL, 0, NULL);
+  if (status < 0) return NULL;
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+/* subsamplingCreate(ctx, kind, desc) -> op */
+static napi_value js_subsampling_create(napi_env env, napi_callback_info info) {
+  napi_value argv[3], ext;
+  if (!get_args(env, info, 3, argv)) return NULL;
+  pk_subsampling_op *op = NULL;
+  const int status = subsampling_call(env, argv[1], argv[2], (pk_context *)get_external(env, argv[0]), 1, &op);
+  if (status < 0) return NULL;
+  if (status != PK_OK) return throw_status(env, status);
+  NAPI_CALL(env, napi_create_external(env, op, subsampling_finalize, NULL, &ext));
+  return ext;
+}
+
+/* subsamplingEnqueue(op, activeBatch, stream?, startEvent?, endEvent?) */
+static napi_value js_subsampling_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  uint32_t batch = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  PK_CALL(env, pk_subsampling_enqueue_timed((pk_subsampling_op *)get_external(env, argv[0]), batch,
+                                            get_external(env, argv[2]), get_external(env, argv[3]),
+                                            get_external(env, argv[4])));
+  return undefined(env);
+}
+
+static napi_value js_subsampling_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_subsampling_destroy((pk_subsampling_op *)get_external(env, argv[0])));
+  return undefined(env);
+}
+
+/* subsamplingPlan(op, activeBatch?) */
+static napi_value js_subsampling_plan(napi_env env, napi_callback_info info) {
+  napi_value argv[2], obj, grid, v;
+  uint32_t batch = 0;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  pk_subsampling_plan_info p;
+  PK_CALL(env, pk_subsampling_plan((pk_subsampling_op *)get_external(env, argv[0]), batch, &p));
+  NAPI_CALL(env, napi_create_object(env, &obj));
+  NAPI_CALL(env, napi_create_array_with_length(env, 3, &grid));
+  for (uint32_t i = 0; i < 3; ++i) napi_set_element(env, grid, i, make_number(env, p.grid[i]));
+  napi_set_named_property(env, obj, "workgroups", grid);
+  napi_set_named_property(env, obj, "outputHeight", make_number(env, p.output_height));
+  napi_set_named_property(env, obj, "outputWidth", make_number(env, p.output_width));
+  napi_set_named_property(env, obj, "blockThreads", make_number(env, p.block_threads));
+  napi_set_named_property(env, obj, "workgroupStorageBytes", make_number(env, p.lds_bytes));
+  napi_set_named_property(env, obj, "algorithmicBytes", make_number(env, (double)p.algorithmic_bytes));
+  napi_set_named_property(env, obj, "flops", make_number(env, (double)p.flops));
+  napi_create_string_utf8(env, p.kernel, NAPI_AUTO_LENGTH, &v);
+  napi_set_named_property(env, obj, "kernel", v);
+  return obj;
+}
+
+/* ---- encoder graph -------------------------------------------------------- */
+
+/* The JavaScript handle owns the encoder through a box so an explicit
+   destroy and the finalizer never free it twice. */
+typedef struct encoder_box {
+  pk_encoder *enc;
+} encoder_box;
+
+static void encoder_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  encoder_box *box = (encoder_box *)data;
+  if (box->enc) pk_encoder_destroy(box->enc);
+  free(box);
+}
+
+static int matrix_field(napi_env env, napi_value o, const char *name, pk_encoder_matrix *m) {
+  napi_value v;
+  uint64_t packed = 0, palette = 0;
+  if (!prop(env, o, name, &v) || !prop_u64(env, v, "packed", &packed) || !prop_u64(env, v, "palette", &palette))
+    return 0;
+  m->packed = (const uint32_t *)(uintptr_t)packed;
+  m->palette = (const void *)(uintptr_t)palette;
+  return 1;
+}
+
+static int address_field(napi_env env, napi_value o, const char *name, const void **p) {
+  uint64_t a = 0;
+  if (!prop_u64(env, o, name, &a)) return 0;
+  *p = (const void *)(uintptr_t)a;
+  return 1;
+}
+
+static int address_list(napi_env env, napi_value o, const char *name, const float **out, uint32_t count) {
+  napi_value list, item;
+  uint32_t n = 0;
+  if (!prop(env, o, name, &list) || napi_get_array_length(env, list, &n) != napi_ok || n != count) return 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    uint64_t a = 0;
+    if (napi_get_element(env, list, i, &item) != napi_ok || !get_u64(env, item, &a)) return 0;
+    out[i] = (const float *)(uintptr_t)a;
+  }
+  return 1;
+}
+
+static int parse_encoder_layer(napi_env env, napi_value o, pk_encoder_layer *l) {
+  const void *p = NULL;
+  int ok = address_list(env, o, "normGamma", l->norm_gamma, 5) && address_list(env, o, "normBeta", l->norm_beta, 5);
+  ok = ok && matrix_field(env, o, "ff1Linear1", &l->ff1_linear1) && matrix_field(env, o, "ff1Linear2", &l->ff1_linear2);
+  ok = ok && matrix_field(env, o, "qkv", &l->qkv) && address_field(env, o, "projectedPositions", &l->projected_positions);
+  ok = ok && address_field(env, o, "biasU", &p);
+  l->bias_u = (const float *)p;
+  ok = ok && address_field(env, o, "biasV", &p);
+  l->bias_v = (const float *)p;
+  ok = ok && matrix_field(env, o, "oProj", &l->o_proj) && matrix_field(env, o, "pointwise1", &l->pointwise1);
+  ok = ok && address_field(env, o, "depthwise", &l->depthwise) && address_field(env, o, "bnScale", &p);
+  l->bn_scale = (const float *)p;
+  ok = ok && address_field(env, o, "bnShift", &p);
+  l->bn_shift = (const float *)p;
+  ok = ok && matrix_field(env, o, "pointwise2", &l->pointwise2) && matrix_field(env, o, "ff2Linear1", &l->ff2_linear1) &&
+       matrix_field(env, o, "ff2Linear2", &l->ff2_linear2);
+  return ok;
+}
+
+static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subsampling *f) {
+  const void *p = NULL;
+  int ok = address_field(env, o, "conv0Weights", &f->conv0_weights) && address_field(env, o, "conv0Bias", &p);
+  f->conv0_bias = (const float *)p;
+  ok = ok && address_field(env, o, "depthwise2Weights", &f->depthwise2_weights) &&
+       address_field(env, o, "depthwise2Bias", &p);
+  f->depthwise2_bias = (const float *)p;
+  ok = ok && matrix_field(env, o, "pointwise3", &f->pointwise3) && address_field(env, o, "pointwise3Bias", &p);
+  f->pointwise3_bias = (const float *)p;
+  ok = ok && address_field(env, o, "depthwise5Weights", &f->depthwise5_weights) &&
+       address_field(env, o, "depthwise5Bias", &p);
+  f->depthwise5_bias = (const float *)p;
+  ok = ok && matrix_field(env, o, "pointwise6", &f->pointwise6) && address_field(env, o, "pointwise6Bias", &p);
+  f->pointwise6_bias = (const float *)p;
+  ok = ok && matrix_field(env, o, "linear", &f->linear) && address_field(env, o, "linearBias", &p);
+  f->linear_bias = (const float *)p;
+  return ok;
+}
+
+/* Parses an encoder descriptor: {label, fusedGlu?, batchSize, frames,
+   layers: [layer...], validLengths, input, output, subsampling?,
+   featureFrames?, featureLengths?, projector?, projectorBias?,
+   projectedChannels?, projectedOutput?}. The layer array, front end and
+   label are heap copies the caller frees with free_encoder_desc. */
+static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
+  memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  d->precision = PK_PRECISION_F16;
+  napi_value layers, item, v;
+  uint32_t n = 0;
+  bool glu = false;
+  if (prop(env, o, "fusedGlu", &v) && napi_get_value_bool(env, v, &glu) == napi_ok && glu)
+    d->flags |= PK_ENCODER_FUSED_GLU;
+  if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
+      !prop(env, o, "layers", &layers) || napi_get_array_length(env, layers, &n) != napi_ok || n == 0) {
+    bad_argument(env, "encoder descriptor is missing a required field");
+    return 0;
+  }
+  pk_encoder_layer *array = (pk_encoder_layer *)calloc(n, sizeof *array);
+  d->layer = array;
+  d->layers = n;
+  d->label = prop_string(env, o, "label");
+  for (uint32_t i = 0; i < n; ++i) {
+    if (napi_get_element(env, layers, i, &item) != napi_ok || !parse_encoder_layer(env, item, &array[i])) {
+      bad_argument(env, "encoder layer descriptor is missing a required field");
+      return 0;
+    }
+  }
+  const void *p = NULL;
+  if (!address_field(env, o, "validLengths", &p)) {
+    bad_argument(env, "encoder descriptor is missing validLengths");
+    return 0;
+  }
+  d->valid_lengths = (const uint32_t *)p;
+  if (!address_field(env, o, "input", &d->input) || !address_field(env, o, "output", &p)) {
+    bad_argument(env, "encoder descriptor is missing input or output");
+    return 0;
+  }
+  d->output = (void *)p;
+  if (prop(env, o, "subsampling", &v)) {
+    pk_encoder_subsampling *front = (pk_encoder_subsampling *)calloc(1, sizeof *front);
+    d->subsampling = front;
+    if (!parse_encoder_subsampling(env, v, front) || !prop_u32(env, o, "featureFrames", &d->feature_frames) ||
+        !address_field(env, o, "featureLengths", &p)) {
+      bad_argument(env, "encoder front end is missing a required field");
+      return 0;
+    }
+    d->feature_lengths = (const uint32_t *)p;
+  }
+  if (prop(env, o, "projector", &v)) {
+    if (!matrix_field(env, o, "projector", &d->projector) || !address_field(env, o, "projectorBias", &p) ||
+        !prop_u32(env, o, "projectedChannels", &d->projected_channels)) {
+      bad_argument(env, "encoder projector is missing a required field");
+      return 0;
+    }
+    d->projector_bias = (const float *)p;
+    if (!address_field(env, o, "projectedOutput", &p)) {
+      bad_argument(env, "encoder projector is missing projectedOutput");
+      return 0;
+    }
+    d->projected_output = (void *)p;
+  }
+  return 1;
+}
+
+static void free_encoder_desc(pk_encoder_desc *d) {
+  free((void *)d->layer);
+  free((void *)d->subsampling);
+  free((void *)d->label);
+}
+
+static napi_value js_encoder_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  pk_encoder_desc d;
+  const int parsed = parse_encoder_desc(env, argv[0], &d);
+  const int status = parsed ? pk_encoder_validate(&d) : PK_OK;
+  free_encoder_desc(&d);
+  if (!parsed) return NULL;
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+/* encoderCreate(ctx, desc) -> encoder */
+static napi_value js_encoder_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2], ext;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  pk_encoder_desc d;
+  if (!parse_encoder_desc(env, argv[1], &d)) {
+    free_encoder_desc(&d);
+    return NULL;
+  }
+  pk_encoder *enc = NULL;
+  const int status = pk_encoder_create((pk_context *)get_external(env, argv[0]), &d, NULL, &enc);
+  free_encoder_desc(&d);
+  if (status != PK_OK) return throw_status(env, status);
+  encoder_box *box = (encoder_box *)malloc(sizeof *box);
+  box->enc = enc;
+  NAPI_CALL(env, napi_create_external(env, box, encoder_finalize, NULL, &ext));
+  return ext;
+}
+
+static pk_encoder *encoder_of(napi_env env, napi_value v) {
+  encoder_box *box = (encoder_box *)get_external(env, v);
+  return box ? box->enc : NULL;
+}
+
+/* encoderEnqueue(encoder, activeBatch, stream?, useGraph?) */
+static napi_value js_encoder_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  uint32_t batch = 0;
+  bool graph = false;
+  if (!get_args(env, info, 4, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  if (!is_nullish(env, argv[3])) napi_get_value_bool(env, argv[3], &graph);
+  PK_CALL(env, pk_encoder_enqueue(encoder_of(env, argv[0]), batch, get_external(env, argv[2]), graph ? 1 : 0));
+  return undefined(env);
+}
+
+/* encoderEnqueueProfiled(encoder, activeBatch, stream?, startEvents[], endEvents[]) */
+static napi_value js_encoder_enqueue_profiled(napi_env env, napi_callback_info info) {
+  napi_value argv[5], item;
+  uint32_t batch = 0, launches = 0, n0 = 0, n1 = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  pk_encoder *enc = encoder_of(env, argv[0]);
+  PK_CALL(env, pk_encoder_info(enc, &launches, NULL));
+  if (napi_get_array_length(env, argv[3], &n0) != napi_ok || napi_get_array_length(env, argv[4], &n1) != napi_ok ||
+      n0 != launches || n1 != launches)
+    return bad_argument(env, "a profiled pass takes one start and one end event per launch");
+  void **events = (void **)calloc(2u * launches, sizeof(void *));
+  for (uint32_t i = 0; i < launches; ++i) {
+    napi_get_element(env, argv[3], i, &item);
+    events[i] = get_external(env, item);
+    napi_get_element(env, argv[4], i, &item);
+    events[launches + i] = get_external(env, item);
+  }
+  const int status = pk_encoder_enqueue_profiled(enc, batch, get_external(env, argv[2]), events, events + launches);
+  free(events);
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+/* encoderInfo(encoder) -> {launches, deviceBytes} */
+static napi_value js_encoder_info(napi_env env, napi_callback_info info) {
+  napi_value argv[1], obj;
+  uint32_t launches = 0;
+  uint64_t bytes = 0;
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_encoder_info(encoder_of(env, argv[0]), &launches, &bytes));
+  NAPI_CALL(env, napi_create_object(env, &obj));
+  napi_set_named_property(env, obj, "launches", make_number(env, launches));
+  napi_set_named_property(env, obj, "deviceBytes", make_number(env, (double)bytes));
+  return obj;
+}
+
+/* encoderDestroy(encoder): idempotent. */
+static napi_value js_encoder_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  encoder_box *box = (encoder_box *)get_external(env, argv[0]);
+  if (box && box->enc) {
+    pk_encoder *enc = box->enc;
+    box->enc = NULL;
+    PK_CALL(env, pk_encoder_destroy(enc));
+  }
+  return undefined(env);
+}
+
 /* ---- module --------------------------------------------------------------- */
 
 static napi_value init(napi_env env, napi_value exports) {
@@ -841,6 +1380,23 @@ static napi_value init(napi_env env, napi_value exports) {
       {"attentionEnqueue", js_attention_enqueue},
       {"attentionDestroy", js_attention_destroy},
       {"attentionPlan", js_attention_plan},
+      {"layernormValidate", js_layernorm_validate},
+      {"layernormCreate", js_layernorm_create},
+      {"layernormEnqueue", js_layernorm_enqueue},
+      {"layernormDestroy", js_layernorm_destroy},
+      {"subsamplingOutputDimension", js_subsampling_output_dimension},
+      {"subsamplingValidLength", js_subsampling_valid_length},
+      {"subsamplingValidate", js_subsampling_validate},
+      {"subsamplingCreate", js_subsampling_create},
+      {"subsamplingEnqueue", js_subsampling_enqueue},
+      {"subsamplingDestroy", js_subsampling_destroy},
+      {"subsamplingPlan", js_subsampling_plan},
+      {"encoderValidate", js_encoder_validate},
+      {"encoderCreate", js_encoder_create},
+      {"encoderEnqueue", js_encoder_enqueue},
+      {"encoderEnqueueProfiled", js_encoder_enqueue_profiled},
+      {"encoderInfo", js_encoder_info},
+      {"encoderDestroy", js_encoder_destroy},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
     napi_value f;

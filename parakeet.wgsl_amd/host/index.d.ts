@@ -349,3 +349,196 @@ export declare function relativeAttentionTensorRecords(frames: number, options?:
   biasU: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
   biasV: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
 };
+
+/* ---- Row LayerNorm (src/webgpu/kernels/layernorm.ts) ---- */
+
+/** layernorm.ts LayerNormDescriptor */
+export interface LayerNormDescriptor {
+  readonly label: string;
+  readonly input: ArenaSlice;
+  /** May be the input slice (in place). */
+  readonly output: ArenaSlice;
+  /** float32 "channel" [channels] package tensors. */
+  readonly gamma: GpuTensor;
+  readonly beta: GpuTensor;
+  readonly rows: number;
+  /** Multiple of 4. */
+  readonly channels: number;
+  /** Default 1e-5. */
+  readonly epsilon?: number;
+}
+
+/** layernorm.ts:29-72 */
+export declare class LayerNormDispatch {
+  readonly label: string;
+  readonly output: ArenaSlice;
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, shape?: EncoderDispatchShape): void;
+  destroy(): void;
+}
+
+/** layernorm.ts:74-247 */
+export declare class LayerNormKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<LayerNormKernel>;
+  readonly uniformParameterPoolBytes: number;
+  validateDescriptor(descriptor: LayerNormDescriptor): void;
+  createDispatch(descriptor: LayerNormDescriptor): LayerNormDispatch;
+  destroy(): void;
+}
+
+export declare function channelTensorRecords(channels: number): { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+
+/* ---- Subsampling front end (src/webgpu/kernels/subsampling.ts) ---- */
+
+/** subsampling.ts:119-122 */
+export declare function subsamplingOutputDimension(input: number): number;
+/** subsampling.ts:124-135 */
+export declare function subsamplingValidLength(featureLength: number, steps: number): number;
+
+/** subsampling.ts FusedSubsamplingConv0Depthwise2Descriptor (:98-111) */
+export interface FusedSubsamplingConv0Depthwise2Descriptor {
+  readonly label: string;
+  /** f32 feature-major [batch, 128, inputHeight]. */
+  readonly input: ArenaSlice;
+  readonly conv0Weights: GpuTensor;
+  readonly conv0Bias: GpuTensor;
+  readonly depthwiseWeights: GpuTensor;
+  readonly depthwiseBias: GpuTensor;
+  /** Channel-last [batch, Ho, Wo, 256]. */
+  readonly output: ArenaSlice;
+  readonly validLengths: ArenaSlice;
+  readonly validLengthBatchOffset?: number;
+  readonly batchSize: number;
+  /** Feature frames (the reference fixes 1501; any count here). */
+  readonly inputHeight: number;
+  /** 128 */
+  readonly inputWidth: number;
+  /** 256 */
+  readonly channels: number;
+}
+
+/** subsampling.ts DepthwiseSubsamplingDescriptor (:84-96) */
+export interface DepthwiseSubsamplingDescriptor {
+  readonly label: string;
+  readonly input: ArenaSlice;
+  readonly weights: GpuTensor;
+  readonly bias: GpuTensor;
+  readonly output: ArenaSlice;
+  readonly validLengths: ArenaSlice;
+  readonly validLengthBatchOffset?: number;
+  readonly validLengthSubsamplingSteps: number;
+  readonly batchSize: number;
+  readonly inputHeight: number;
+  readonly inputWidth: number;
+  readonly channels: number;
+}
+
+/** subsampling.ts SubsamplingTimeMaskDescriptor (:573-585) */
+export interface SubsamplingTimeMaskDescriptor {
+  readonly label: string;
+  readonly values: ArenaSlice;
+  readonly validLengths: ArenaSlice;
+  readonly batchSize: number;
+  readonly height: number;
+  readonly width: number;
+  readonly channels: number;
+  readonly validLengthBatchOffset?: number;
+  readonly validLengthSubsamplingSteps: number;
+}
+
+export interface SubsamplingPlan {
+  readonly workgroups: readonly [number, number, number];
+  readonly outputHeight: number;
+  readonly outputWidth: number;
+  readonly blockThreads: number;
+  readonly workgroupStorageBytes: number;
+  readonly algorithmicBytes: number;
+  readonly flops: number;
+  readonly kernel: string;
+}
+
+/** subsampling.ts:208-248 and :587-618; shape.batchSize (this library only) selects a prefix. */
+export declare class SubsamplingDispatch {
+  readonly label: string;
+  readonly output: ArenaSlice;
+  readonly outputHeight: number;
+  readonly outputWidth: number;
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, shape?: { batchSize?: number }): void;
+  destroy(): void;
+  plan(activeBatch?: number): SubsamplingPlan;
+}
+
+export declare class FusedSubsamplingConv0Depthwise2Kernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<FusedSubsamplingConv0Depthwise2Kernel>;
+  validateDescriptor(descriptor: FusedSubsamplingConv0Depthwise2Descriptor): void;
+  createDispatch(descriptor: FusedSubsamplingConv0Depthwise2Descriptor): SubsamplingDispatch;
+  destroy(): void;
+}
+
+export declare class DepthwiseSubsamplingKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<DepthwiseSubsamplingKernel>;
+  validateDescriptor(descriptor: DepthwiseSubsamplingDescriptor): void;
+  createDispatch(descriptor: DepthwiseSubsamplingDescriptor): SubsamplingDispatch;
+  destroy(): void;
+}
+
+export declare class SubsamplingTimeMaskKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, uniformParameterCapacity: number,
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<SubsamplingTimeMaskKernel>;
+  validateDescriptor(descriptor: SubsamplingTimeMaskDescriptor): void;
+  createDispatch(descriptor: SubsamplingTimeMaskDescriptor): SubsamplingDispatch;
+  destroy(): void;
+}
+
+export declare function subsamplingTensorRecords(options?: { dtype?: "float16" | "float32"; channels?: number }): {
+  conv0Weights: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  depthwiseWeights: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+  bias: { sourceRecord: TensorRecord; runtimeRecord: TensorRecord };
+};
+
+/* ---- Encoder graph (src/webgpu/encoder.ts) ---- */
+
+/** encoder.ts:441-479 */
+export declare function deriveEncoderValidLength(featureLength: number): number;
+export declare function deriveEncoderValidLengths(featureLengths: readonly number[], batchSize?: number): Uint32Array;
+
+/** The ParakeetGpuPackage surface the graph reads (package.ts:52-): tensors by name. */
+export interface EncoderModel {
+  tensor(name: string): GpuTensor;
+}
+
+export interface ParakeetEncoderGraphOptions {
+  /** Windows (default 16). */
+  readonly batchSize?: number;
+  /** Conformer layers (default 24). */
+  readonly layers?: number;
+  /** fbank frames per window (default 1501). */
+  readonly featureFrames?: number;
+  /** PW1's GLU epilogue (this library only). */
+  readonly fusedGlu?: boolean;
+  readonly label?: string;
+}
+
+/** encoder.ts:1200-1862 */
+export declare class ParakeetEncoderGraph {
+  static create(device: HipGpuDevice, model: EncoderModel, options?: ParakeetEncoderGraphOptions): Promise<ParakeetEncoderGraph>;
+  readonly batchSize: number;
+  readonly frames: number;
+  /** 6 front-end launches + 15 per layer + the projector. */
+  readonly dispatchCount: number;
+  readonly outputBuffer: HipBuffer;
+  readonly projectedOutputBuffer: HipBuffer;
+  uploadFeatures(features: Float32Array): void;
+  uploadValidFeatureLengths(featureLengths: readonly number[]): Uint32Array;
+  encode(encoder: HipCommandEncoder, validFeatureLengths: readonly number[],
+         options?: { useGraph?: boolean; timestamps?: { querySet: HipTimestampQuerySet; first?: number } }): Uint32Array;
+  destroy(): void;
+}
+
+export declare const PARAKEET_FEATURE_BINS: 128;
+export declare const PARAKEET_FEATURE_FRAMES: 1501;
+export declare const PARAKEET_ENCODER_FRAMES: 188;
+export declare const PARAKEET_PROJECTED_CHANNELS: 640;
+export declare const ENCODER_LAYER_DISPATCHES: 15;

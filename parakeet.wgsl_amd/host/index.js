@@ -29,6 +29,15 @@
  *     .create / .createDispatch        :130-314 (record checks :323-370 here,
  *                                      the numeric contract in pk_attention_validate)
  *   RelativeAttentionDispatch.encode / destroy   :51-97
+ *   LayerNormKernel / LayerNormDispatch  src/webgpu/kernels/layernorm.ts:29-281
+ *   FusedSubsamplingConv0Depthwise2Kernel, DepthwiseSubsamplingKernel,
+ *   SubsamplingTimeMaskKernel, SubsamplingDispatch,
+ *   subsamplingOutputDimension / subsamplingValidLength
+ *                                      src/webgpu/kernels/subsampling.ts:119-790
+ *   ParakeetEncoderGraph               src/webgpu/encoder.ts:1200-1862 (create
+ *     from a model's tensors, uploadFeatures, uploadValidFeatureLengths,
+ *     encode: front end, 24 layers, projector, as one native graph)
+ *   deriveEncoderValidLength(s)        encoder.ts:441-479
  * The WebGPU device, queue, buffers and command encoder are replaced by HIP
  * equivalents with the same shapes (HipGpuDevice, queue.writeBuffer /
  * submit / onSubmittedWorkDone, createCommandEncoder().finish()).
@@ -1008,6 +1017,661 @@ function createEncoderGemmBackend(kernel) {
   };
 }
 
+/* ------------------------------------------------------------ LayerNorm */
+
+/** layernorm.ts requirePackedTensor: a float32 "channel" record of [C]. */
+function requireChannelTensor(tensor, channels, byteLength, label) {
+  const record = tensor.runtimeRecord;
+  if (
+    record.dtype !== "float32" ||
+    record.layout !== "channel" ||
+    record.byteLength !== byteLength ||
+    shapeKey(record.logicalShape) !== String(channels) ||
+    shapeKey(record.storageShape) !== String(channels)
+  ) {
+    throw new Error(`${label} must be float32 channel logical/storage [${channels}], ${byteLength} bytes`);
+  }
+}
+
+class LayerNormDispatch {
+  constructor(label, output, op, rows) {
+    this.label = label;
+    this.output = output;
+    this.op = op;
+    this.rows = rows;
+    this.destroyed = false;
+  }
+
+  /** encode (layernorm.ts:45-66): shape.rows selects the active rows. */
+  encode(encoder, timestampWrites, shape) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    const rows = shape === undefined || shape.rows === undefined ? this.rows : shape.rows;
+    if (!isSafe(rows) || rows <= 0 || rows > this.rows)
+      throw new RangeError(`${this.label} active rows must be in [1, ${this.rows}]`);
+    const op = this.op;
+    encoder.record(() => {
+      const [begin, end] = timestampEvents(timestampWrites);
+      native().layernormEnqueue(op, rows, null, begin, end);
+    });
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().layernormDestroy(this.op);
+  }
+}
+
+class LayerNormKernel {
+  constructor(device, arena, executionProfile) {
+    this.device = device;
+    this.arena = arena;
+    this.precision = precisionOf(executionProfile);
+    this.destroyed = false;
+  }
+
+  /** create (layernorm.ts:120-162): the kernel is compiled into the library. */
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new LayerNormKernel(device, arena, executionProfile));
+  }
+
+  get uniformParameterPoolBytes() {
+    return 0;
+  }
+
+  nativeDescriptor(descriptor) {
+    if (!isSafe(descriptor.rows) || !isSafe(descriptor.channels) || descriptor.rows <= 0 ||
+        descriptor.channels <= 0 || descriptor.channels % 4 !== 0)
+      throw new RangeError(`Invalid LayerNorm shape for ${descriptor.label}`);
+    const input = this.arena.binding(descriptor.input);
+    const output = this.arena.binding(descriptor.output);
+    const affineBytes = descriptor.channels * 4;
+    requireChannelTensor(descriptor.gamma, descriptor.channels, affineBytes, `${descriptor.label} gamma`);
+    requireChannelTensor(descriptor.beta, descriptor.channels, affineBytes, `${descriptor.label} beta`);
+    return {
+      label: descriptor.label,
+      precision: this.precision,
+      rows: descriptor.rows,
+      channels: descriptor.channels,
+      input: addressOf(input),
+      inputBytes: input.size,
+      gamma: addressOf(descriptor.gamma.binding),
+      gammaBytes: descriptor.gamma.binding.size,
+      beta: addressOf(descriptor.beta.binding),
+      betaBytes: descriptor.beta.binding.size,
+      output: addressOf(output),
+      outputBytes: output.size,
+      epsilon: descriptor.epsilon === undefined ? 1e-5 : descriptor.epsilon,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().layernormValidate(this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (layernorm.ts:165-240). */
+  createDispatch(descriptor) {
+    if (this.destroyed) throw new Error("Parakeet LayerNorm kernel was destroyed");
+    const op = native().layernormCreate(this.device.context, this.nativeDescriptor(descriptor));
+    return new LayerNormDispatch(descriptor.label, descriptor.output, op, descriptor.rows);
+  }
+
+  destroy() {
+    this.destroyed = true;
+  }
+}
+
+/** Package records of a LayerNorm gamma or beta (a float32 [C] "channel" tensor). */
+function channelTensorRecords(channels) {
+  const record = {
+    dtype: "float32", logicalShape: [channels], storageShape: [channels], byteLength: channels * 4,
+    layout: "channel",
+  };
+  return { sourceRecord: record, runtimeRecord: record };
+}
+
+/** The begin / end events of a timestampWrites descriptor (or nulls). */
+function timestampEvents(timestampWrites) {
+  const qs = timestampWrites ? timestampWrites.querySet : null;
+  const begin = qs && timestampWrites.beginningOfPassWriteIndex !== undefined
+    ? qs.events[timestampWrites.beginningOfPassWriteIndex] : null;
+  const end = qs && timestampWrites.endOfPassWriteIndex !== undefined
+    ? qs.events[timestampWrites.endOfPassWriteIndex] : null;
+  return [begin, end];
+}
+
+/* ------------------------------------------------------------ subsampling */
+
+const SUBSAMPLING_CONV0_WEIGHT_LAYOUT = "kh-kw-output-channel-vec4";
+const SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT = "kh-kw-channel-vec4";
+const SUBSAMPLING_BIAS_LAYOUT = "output-channel";
+
+/** subsamplingOutputDimension (subsampling.ts:119-122). */
+function subsamplingOutputDimension(input) {
+  if (!isSafe(input) || input <= 0) throw new RangeError("subsampling input dimension must be a positive integer");
+  return native().subsamplingOutputDimension(input);
+}
+
+/** subsamplingValidLength (subsampling.ts:124-135). */
+function subsamplingValidLength(featureLength, steps) {
+  if (!isSafe(featureLength) || featureLength <= 0) throw new RangeError("featureLength must be a positive integer");
+  if (!isSafe(steps) || steps <= 0) throw new RangeError("subsampling steps must be a positive integer");
+  return native().subsamplingValidLength(featureLength, steps);
+}
+
+/** subsampling.ts requirePackedTensor (:1009-1034), [3,3,C] kernels and [C] biases. */
+function requireSubsamplingTensor(tensor, dtype, shape, layout, byteLength, label) {
+  const record = tensor.runtimeRecord;
+  const storageShape = shape.length === 3 ? [shape[0], shape[1], shape[2] / 4, 4] : shape;
+  if (
+    record.dtype !== dtype ||
+    record.layout !== layout ||
+    record.byteLength !== byteLength ||
+    shapeKey(record.logicalShape) !== shapeKey(shape) ||
+    shapeKey(record.storageShape) !== shapeKey(storageShape)
+  ) {
+    throw new Error(
+      `${label} must be ${dtype} ${layout} logical [${shape.join(",")}], ` +
+        `storage [${storageShape.join(",")}], ${byteLength} bytes`,
+    );
+  }
+}
+
+/** Package records of the subsampling kernels and biases (convert.py:1264-1340). */
+function subsamplingTensorRecords(options) {
+  const dtype = (options && options.dtype) || "float16";
+  const channels = (options && options.channels) || 256;
+  const scalar = dtype === "float16" ? 2 : 4;
+  const kernel = (layout) => {
+    const r = { dtype, logicalShape: [3, 3, channels], storageShape: [3, 3, channels / 4, 4],
+                byteLength: 9 * channels * scalar, layout };
+    return { sourceRecord: r, runtimeRecord: r };
+  };
+  const bias = { dtype: "float32", logicalShape: [channels], storageShape: [channels], byteLength: channels * 4,
+                 layout: SUBSAMPLING_BIAS_LAYOUT };
+  return {
+    conv0Weights: kernel(SUBSAMPLING_CONV0_WEIGHT_LAYOUT),
+    depthwiseWeights: kernel(SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT),
+    bias: { sourceRecord: bias, runtimeRecord: bias },
+  };
+}
+
+/** SubsamplingDispatch / SubsamplingTimeMaskDispatch (subsampling.ts:208-248, :587-618). */
+class SubsamplingDispatch {
+  constructor(label, output, op, batchSize, plan) {
+    this.label = label;
+    this.output = output;
+    this.op = op;
+    this.batchSize = batchSize;
+    this.outputHeight = plan.outputHeight;
+    this.outputWidth = plan.outputWidth;
+    this.destroyed = false;
+  }
+
+  /** encode(encoder, timestampWrites?, shape?): shape.batchSize (this
+      library's addition) selects an active prefix of the windows. */
+  encode(encoder, timestampWrites, shape) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    const active = shape === undefined || shape.batchSize === undefined ? this.batchSize : shape.batchSize;
+    if (!isSafe(active) || active <= 0 || active > this.batchSize)
+      throw new RangeError(`${this.label} active batch must be in [1, ${this.batchSize}]`);
+    const op = this.op;
+    encoder.record(() => {
+      const [begin, end] = timestampEvents(timestampWrites);
+      native().subsamplingEnqueue(op, active, null, begin, end);
+    });
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().subsamplingDestroy(this.op);
+  }
+
+  plan(activeBatch) {
+    return native().subsamplingPlan(this.op, activeBatch || 0);
+  }
+}
+
+class SubsamplingKernelBase {
+  constructor(device, arena, executionProfile) {
+    this.device = device;
+    this.arena = arena;
+    this.precision = precisionOf(executionProfile);
+    this.dtype = this.precision === "f16" ? "float16" : "float32";
+    this.destroyed = false;
+  }
+
+  get uniformParameterPoolBytes() {
+    return 0;
+  }
+
+  slice(binding) {
+    const b = this.arena.binding(binding);
+    return [addressOf(b), b.size];
+  }
+
+  create(kind, native_desc, descriptor, batchSize) {
+    if (this.destroyed) throw new Error(`${this.constructor.name} was destroyed`);
+    const op = native().subsamplingCreate(this.device.context, kind, native_desc);
+    const plan = native().subsamplingPlan(op, 0);
+    return new SubsamplingDispatch(descriptor.label, descriptor.output || descriptor.values, op, batchSize, plan);
+  }
+
+  destroy() {
+    this.destroyed = true;
+  }
+}
+
+/** FusedSubsamplingConv0Depthwise2Kernel (subsampling.ts:250-436). */
+class FusedSubsamplingConv0Depthwise2Kernel extends SubsamplingKernelBase {
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new FusedSubsamplingConv0Depthwise2Kernel(device, arena, executionProfile));
+  }
+
+  nativeDescriptor(descriptor) {
+    const scalar = this.precision === "f16" ? 2 : 4;
+    const channels = descriptor.channels;
+    requireSubsamplingTensor(descriptor.conv0Weights, this.dtype, [3, 3, channels], SUBSAMPLING_CONV0_WEIGHT_LAYOUT,
+                             9 * channels * scalar, `${descriptor.label} conv0 weights`);
+    requireSubsamplingTensor(descriptor.conv0Bias, "float32", [channels], SUBSAMPLING_BIAS_LAYOUT, channels * 4,
+                             `${descriptor.label} conv0 bias`);
+    requireSubsamplingTensor(descriptor.depthwiseWeights, this.dtype, [3, 3, channels],
+                             SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT, 9 * channels * scalar,
+                             `${descriptor.label} depthwise2 weights`);
+    requireSubsamplingTensor(descriptor.depthwiseBias, "float32", [channels], SUBSAMPLING_BIAS_LAYOUT, channels * 4,
+                             `${descriptor.label} depthwise2 bias`);
+    const [input, inputBytes] = this.slice(descriptor.input);
+    const [output, outputBytes] = this.slice(descriptor.output);
+    const [valid, validBytes] = this.slice(descriptor.validLengths);
+    const t = (x) => [addressOf(x.binding), x.binding.size];
+    const [w0, w0b] = t(descriptor.conv0Weights), [b0, b0b] = t(descriptor.conv0Bias);
+    const [wd, wdb] = t(descriptor.depthwiseWeights), [bd, bdb] = t(descriptor.depthwiseBias);
+    return {
+      label: descriptor.label, precision: this.precision, batchSize: descriptor.batchSize,
+      inputHeight: descriptor.inputHeight, inputWidth: descriptor.inputWidth, channels,
+      input, inputBytes, conv0Weights: w0, conv0WeightsBytes: w0b, conv0Bias: b0, conv0BiasBytes: b0b,
+      depthwiseWeights: wd, depthwiseWeightsBytes: wdb, depthwiseBias: bd, depthwiseBiasBytes: bdb,
+      output, outputBytes, validLengths: valid, validLengthsBytes: validBytes,
+      validLengthBatchOffset: descriptor.validLengthBatchOffset || 0,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().subsamplingValidate("fused", this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (subsampling.ts:334-425). */
+  createDispatch(descriptor) {
+    return this.create("fused", this.nativeDescriptor(descriptor), descriptor, descriptor.batchSize);
+  }
+}
+
+/** DepthwiseSubsamplingKernel (subsampling.ts:438-571). */
+class DepthwiseSubsamplingKernel extends SubsamplingKernelBase {
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new DepthwiseSubsamplingKernel(device, arena, executionProfile));
+  }
+
+  nativeDescriptor(descriptor) {
+    const scalar = this.precision === "f16" ? 2 : 4;
+    const channels = descriptor.channels;
+    if (isSafe(channels) && channels > 0 && channels % 4 === 0) {
+      requireSubsamplingTensor(descriptor.weights, this.dtype, [3, 3, channels], SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT,
+                               9 * channels * scalar, `${descriptor.label} weights`);
+      requireSubsamplingTensor(descriptor.bias, "float32", [channels], SUBSAMPLING_BIAS_LAYOUT, channels * 4,
+                               `${descriptor.label} bias`);
+    }
+    const [input, inputBytes] = this.slice(descriptor.input);
+    const [output, outputBytes] = this.slice(descriptor.output);
+    const [valid, validBytes] = this.slice(descriptor.validLengths);
+    return {
+      label: descriptor.label, precision: this.precision, batchSize: descriptor.batchSize,
+      inputHeight: descriptor.inputHeight, inputWidth: descriptor.inputWidth, channels,
+      input, inputBytes, weights: addressOf(descriptor.weights.binding), weightsBytes: descriptor.weights.binding.size,
+      bias: addressOf(descriptor.bias.binding), biasBytes: descriptor.bias.binding.size, output, outputBytes,
+      validLengths: valid, validLengthsBytes: validBytes,
+      validLengthBatchOffset: descriptor.validLengthBatchOffset || 0,
+      validLengthSubsamplingSteps: descriptor.validLengthSubsamplingSteps,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().subsamplingValidate("depthwise", this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (subsampling.ts:495-560). */
+  createDispatch(descriptor) {
+    return this.create("depthwise", this.nativeDescriptor(descriptor), descriptor, descriptor.batchSize);
+  }
+}
+
+/** SubsamplingTimeMaskKernel (subsampling.ts:620-793). */
+class SubsamplingTimeMaskKernel extends SubsamplingKernelBase {
+  static create(device, arena, uniformParameterCapacity, executionProfile) {
+    return Promise.resolve(new SubsamplingTimeMaskKernel(device, arena, executionProfile));
+  }
+
+  nativeDescriptor(descriptor) {
+    const [values, valuesBytes] = this.slice(descriptor.values);
+    const [valid, validBytes] = this.slice(descriptor.validLengths);
+    return {
+      label: descriptor.label, precision: this.precision, batchSize: descriptor.batchSize,
+      height: descriptor.height, width: descriptor.width, channels: descriptor.channels,
+      values, valuesBytes, validLengths: valid, validLengthsBytes: validBytes,
+      validLengthBatchOffset: descriptor.validLengthBatchOffset || 0,
+      validLengthSubsamplingSteps: descriptor.validLengthSubsamplingSteps,
+    };
+  }
+
+  validateDescriptor(descriptor) {
+    native().subsamplingValidate("mask", this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (subsampling.ts:698-790). */
+  createDispatch(descriptor) {
+    return this.create("mask", this.nativeDescriptor(descriptor), descriptor, descriptor.batchSize);
+  }
+}
+
+/* ---------------------------------------------------------- encoder graph */
+
+const PARAKEET_FEATURE_BINS = 128;
+const PARAKEET_FEATURE_FRAMES = 1501;
+const PARAKEET_ENCODER_FRAMES = 188;
+const PARAKEET_ENCODER_CHANNELS = 1024;
+const PARAKEET_INTERMEDIATE_CHANNELS = 4096;
+const PARAKEET_SUBSAMPLING_CHANNELS = 256;
+const PARAKEET_PROJECTED_CHANNELS = 640;
+const PARAKEET_ENCODER_LAYERS = 24;
+const ENCODER_LAYER_DISPATCHES = 15;
+
+/** deriveSubsamplingLengths / deriveEncoderValidLength (encoder.ts:441-458). */
+function deriveEncoderValidLength(featureLength) {
+  if (!isSafe(featureLength) || featureLength <= 0) throw new RangeError("featureLength must be a positive integer");
+  if (featureLength > PARAKEET_FEATURE_FRAMES)
+    throw new RangeError(`featureLength must not exceed ${PARAKEET_FEATURE_FRAMES}`);
+  return native().subsamplingValidLength(featureLength, 3);
+}
+
+/** deriveEncoderValidLengths (encoder.ts:460-479). */
+function deriveEncoderValidLengths(featureLengths, batchSize) {
+  const n = batchSize === undefined ? featureLengths.length : batchSize;
+  if (!isSafe(n) || n <= 0) throw new RangeError("batchSize must be a positive integer");
+  if (featureLengths.length !== n) throw new RangeError(`Expected ${n} feature lengths, got ${featureLengths.length}`);
+  const out = new Uint32Array(n);
+  for (let i = 0; i < n; ++i) {
+    if (featureLengths[i] === undefined) throw new RangeError(`Missing feature length ${i}`);
+    out[i] = deriveEncoderValidLength(featureLengths[i]);
+  }
+  return out;
+}
+
+/** requireTensorRecord (encoder.ts:2550-2581) on both records of a tensor. */
+function requireEncoderTensor(model, name, spec) {
+  const tensor = model.tensor(name);
+  const scalar = spec.dtype === "float16" ? 2 : 4;
+  const expected = spec.storageShape.reduce((a, b) => a * b, 1) * scalar;
+  for (const kind of ["source", "runtime"]) {
+    const record = kind === "source" ? tensor.sourceRecord : tensor.runtimeRecord;
+    if (
+      record.dtype !== spec.dtype ||
+      record.layout !== spec.layout ||
+      record.byteLength !== expected ||
+      shapeKey(record.logicalShape) !== shapeKey(spec.logicalShape) ||
+      shapeKey(record.storageShape) !== shapeKey(spec.storageShape)
+    ) {
+      throw new Error(
+        `${name} ${kind} must be ${spec.dtype} ${spec.layout}, logical ` +
+          `[${spec.logicalShape.join(",")}], storage [${spec.storageShape.join(",")}]`,
+      );
+    }
+  }
+  return addressOf(tensor.binding);
+}
+
+/** matrixTensor (encoder.ts:2458-2512): packed codes and palette addresses. */
+function encoderMatrix(model, name, inner, columns, bits, groups) {
+  const codesPerGroup = bits === 5 ? 32 : 16;
+  const wordsPerGroup = bits === 5 ? 5 : 3;
+  const packedGroups = (inner * columns) / codesPerGroup;
+  if (!isSafe(packedGroups)) throw new Error(`${name} is not palette packing aligned`);
+  const packed = requireEncoderTensor(model, name, {
+    dtype: "uint32", logicalShape: [inner, columns], storageShape: [packedGroups, wordsPerGroup],
+    layout: `k-by-output-row-major-palette${bits}-lsb-u32`,
+  });
+  const palette = requireEncoderTensor(model, `${name}.palette`, {
+    dtype: "float16", logicalShape: [groups, 1 << bits], storageShape: [groups, 1 << bits],
+    layout: "output-group-by-palette-lut",
+  });
+  return { packed, palette };
+}
+
+function channelAddress(model, name, channels, layout) {
+  return requireEncoderTensor(model, name, {
+    dtype: "float32", logicalShape: [channels], storageShape: [channels], layout,
+  });
+}
+
+function kernelAddress(model, name, layout) {
+  return requireEncoderTensor(model, name, {
+    dtype: "float16", logicalShape: [3, 3, PARAKEET_SUBSAMPLING_CHANNELS],
+    storageShape: [3, 3, PARAKEET_SUBSAMPLING_CHANNELS / 4, 4], layout,
+  });
+}
+
+/** The native descriptor of one layer from the model's tensors (encoder.ts:1868-2135). */
+function encoderLayerDescriptor(model, index, frames) {
+  const prefix = `encoder.layers.${index}`;
+  const norms = ["norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out"];
+  const m = (name, inner, columns, bits, groups) =>
+    encoderMatrix(model, `${prefix}.${name}`, inner, columns, bits || 5, groups || 1);
+  const C = PARAKEET_ENCODER_CHANNELS, H = PARAKEET_INTERMEDIATE_CHANNELS;
+  const bias = (name) => requireEncoderTensor(model, `${prefix}.self_attn.${name}`, {
+    dtype: "float32", logicalShape: [8, 128], storageShape: [8, 128], layout: "head-by-channel",
+  });
+  return {
+    normGamma: norms.map((n) => channelAddress(model, `${prefix}.${n}.weight`, C, "channel")),
+    normBeta: norms.map((n) => channelAddress(model, `${prefix}.${n}.bias`, C, "channel")),
+    ff1Linear1: m("feed_forward1.linear1.weight", C, H),
+    ff1Linear2: m("feed_forward1.linear2.weight", H, C),
+    qkv: m("self_attn.qkv.weight", C, 3 * C, 5, 3),
+    projectedPositions: requireEncoderTensor(model, `${prefix}.self_attn.projected_positions`, {
+      dtype: "float16", logicalShape: [2 * frames - 1, C], storageShape: [8, 32, 2 * frames - 1, 4],
+      layout: "head-vector-position-vec4",
+    }),
+    biasU: bias("bias_u"),
+    biasV: bias("bias_v"),
+    oProj: m("self_attn.o_proj.weight", C, C, 6),
+    pointwise1: m("conv.pointwise_conv1.weight", C, 2 * C),
+    depthwise: requireEncoderTensor(model, `${prefix}.conv.depthwise_conv.weight`, {
+      dtype: "float16", logicalShape: [9, C], storageShape: [9, C / 4, 4], layout: "kernel-channel-vec4",
+    }),
+    bnScale: channelAddress(model, `${prefix}.conv.norm.scale`, C, "channel"),
+    bnShift: channelAddress(model, `${prefix}.conv.norm.shift`, C, "channel"),
+    pointwise2: m("conv.pointwise_conv2.weight", C, C),
+    ff2Linear1: m("feed_forward2.linear1.weight", C, H),
+    ff2Linear2: m("feed_forward2.linear2.weight", H, C),
+  };
+}
+
+/** The front end's native descriptor (encoder.ts:2140-2300). */
+function encoderSubsamplingDescriptor(model) {
+  const p = "encoder.subsampling";
+  const S = PARAKEET_SUBSAMPLING_CHANNELS;
+  return {
+    conv0Weights: kernelAddress(model, `${p}.layers.0.weight`, SUBSAMPLING_CONV0_WEIGHT_LAYOUT),
+    conv0Bias: channelAddress(model, `${p}.layers.0.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
+    depthwise2Weights: kernelAddress(model, `${p}.layers.2.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT),
+    depthwise2Bias: channelAddress(model, `${p}.layers.2.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
+    pointwise3: encoderMatrix(model, `${p}.layers.3.weight`, S, S, 5, 1),
+    pointwise3Bias: channelAddress(model, `${p}.layers.3.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
+    depthwise5Weights: kernelAddress(model, `${p}.layers.5.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT),
+    depthwise5Bias: channelAddress(model, `${p}.layers.5.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
+    pointwise6: encoderMatrix(model, `${p}.layers.6.weight`, S, S, 5, 1),
+    pointwise6Bias: channelAddress(model, `${p}.layers.6.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
+    linear: encoderMatrix(model, `${p}.linear.weight`, 16 * S, PARAKEET_ENCODER_CHANNELS, 5, 1),
+    linearBias: channelAddress(model, `${p}.linear.bias`, PARAKEET_ENCODER_CHANNELS, SUBSAMPLING_BIAS_LAYOUT),
+  };
+}
+
+/**
+ * ParakeetEncoderGraph (encoder.ts:1200-1862) over this library's encoder
+ * runtime: `model.tensor(name)` returns the package's GpuTensors
+ * (package.ts:45-50) under the reference's names; the graph owns the
+ * feature input, the lengths, the encoder output and the projector output.
+ */
+class ParakeetEncoderGraph {
+  constructor(device, handle, buffers, options) {
+    this.device = device;
+    this.handle = handle;
+    this.buffers = buffers;
+    this.batchSize = options.batchSize;
+    this.frames = options.frames;
+    this.featureFrames = options.featureFrames;
+    this.layers = options.layers;
+    this.info = native().encoderInfo(handle);
+    this.destroyed = false;
+  }
+
+  /**
+   * create(device, model, options?): options.batchSize (windows, default
+   * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
+   * epilogue, no reference counterpart), options.featureFrames (default
+   * 1501).
+   */
+  static create(device, model, options) {
+    try {
+      return Promise.resolve(ParakeetEncoderGraph.build(device, model, options || {}));
+    } catch (error) {
+      return Promise.reject(error);
+    }
+  }
+
+  static build(device, model, o) {
+    const batchSize = o.batchSize === undefined ? 16 : o.batchSize;
+    const layers = o.layers === undefined ? PARAKEET_ENCODER_LAYERS : o.layers;
+    const featureFrames = o.featureFrames === undefined ? PARAKEET_FEATURE_FRAMES : o.featureFrames;
+    if (!isSafe(batchSize) || batchSize <= 0) throw new RangeError("Encoder batch capacity must be a positive integer");
+    let frames = featureFrames;
+    for (let i = 0; i < 3; ++i) frames = subsamplingOutputDimension(frames);
+    const layerDescriptors = [];
+    for (let i = 0; i < layers; ++i) layerDescriptors.push(encoderLayerDescriptor(model, i, frames));
+    const subsampling = encoderSubsamplingDescriptor(model);
+    const projector = encoderMatrix(model, "encoder_projector.weight", PARAKEET_ENCODER_CHANNELS,
+                                    PARAKEET_PROJECTED_CHANNELS, 5, 1);
+    const projectorBias = channelAddress(model, "encoder_projector.bias", PARAKEET_PROJECTED_CHANNELS,
+                                         "output-channel");
+    const rows = batchSize * frames;
+    const make = (label, size) => device.createBuffer({ label, size });
+    const buffers = {
+      features: make("fbank-feature-major", batchSize * PARAKEET_FEATURE_BINS * featureFrames * 4),
+      featureLengths: make("feature-lengths", batchSize * 4),
+      encoderLengths: make("encoder-lengths", batchSize * 4),
+      output: make("encoder-output", rows * PARAKEET_ENCODER_CHANNELS * 2),
+      projectedOutput: make("encoder-projector-output", rows * PARAKEET_PROJECTED_CHANNELS * 2),
+    };
+    let handle;
+    try {
+      handle = native().encoderCreate(device.context, {
+        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, batchSize, frames,
+        layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
+        input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
+        featureLengths: buffers.featureLengths.address, projector, projectorBias,
+        projectedChannels: PARAKEET_PROJECTED_CHANNELS, projectedOutput: buffers.projectedOutput.address,
+      });
+    } catch (error) {
+      for (const b of Object.values(buffers)) b.destroy();
+      throw error;
+    }
+    return new ParakeetEncoderGraph(device, handle, buffers, { batchSize, frames, featureFrames, layers });
+  }
+
+  /** Launches in one pass (6 front end + 15 per layer + the projector). */
+  get dispatchCount() {
+    return this.info.launches;
+  }
+
+  /** uploadFeatures (encoder.ts:1536-1553): f32 [windows, 128, F] feature-major. */
+  uploadFeatures(features) {
+    this.assertAlive();
+    const perItem = PARAKEET_FEATURE_BINS * this.featureFrames * 4;
+    if (features.byteLength <= 0 || features.byteLength > this.buffers.features.size ||
+        features.byteLength % perItem !== 0)
+      throw new RangeError(`Expected 1-${this.batchSize} complete feature items, got ${features.byteLength} bytes`);
+    this.device.queue.writeBuffer(this.buffers.features, 0, features);
+  }
+
+  /** uploadValidFeatureLengths (encoder.ts:1555-1582): raw and derived lengths. */
+  uploadValidFeatureLengths(featureLengths) {
+    this.assertAlive();
+    const n = featureLengths.length;
+    if (!isSafe(n) || n <= 0 || n > this.batchSize)
+      throw new RangeError(`Encoder active batch must be in [1, ${this.batchSize}]`);
+    const raw = new Uint32Array(n);
+    for (let i = 0; i < n; ++i) {
+      const value = featureLengths[i];
+      if (value === undefined || !isSafe(value) || value <= 0 || value > this.featureFrames)
+        throw new RangeError(`Feature length ${i} must be in [1, ${this.featureFrames}]`);
+      raw[i] = value;
+    }
+    const derived = deriveEncoderValidLengths(Array.from(raw), n);
+    this.device.queue.writeBuffer(this.buffers.featureLengths, 0, raw);
+    this.device.queue.writeBuffer(this.buffers.encoderLengths, 0, derived);
+    return derived;
+  }
+
+  /**
+   * encode(encoder, validFeatureLengths, options?) (encoder.ts:1690-1706):
+   * uploads the lengths and records one pass over the active windows;
+   * options.useGraph replays the pass from a HIP graph, options.timestamps
+   * = {querySet, first} stamps every launch (start 2i, end 2i+1 from
+   * `first`).
+   */
+  encode(encoder, validFeatureLengths, options) {
+    this.assertAlive();
+    const derived = this.uploadValidFeatureLengths(validFeatureLengths);
+    const active = derived.length;
+    const handle = this.handle;
+    const o = options || {};
+    if (o.timestamps) {
+      const qs = o.timestamps.querySet, first = o.timestamps.first || 0;
+      const n = this.info.launches;
+      if (qs.events.length < first + 2 * n) throw new RangeError(`the query set needs ${first + 2 * n} entries`);
+      const starts = [], ends = [];
+      for (let i = 0; i < n; ++i) {
+        starts.push(qs.events[first + 2 * i]);
+        ends.push(qs.events[first + 2 * i + 1]);
+      }
+      encoder.record(() => native().encoderEnqueueProfiled(handle, active, null, starts, ends));
+    } else {
+      const graph = o.useGraph === true;
+      encoder.record(() => native().encoderEnqueue(handle, active, null, graph));
+    }
+    return derived;
+  }
+
+  /** Device buffers of the encoder output [windows*188, 1024] and the projector output [.., 640]. */
+  get outputBuffer() {
+    return this.buffers.output;
+  }
+
+  get projectedOutputBuffer() {
+    return this.buffers.projectedOutput;
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().encoderDestroy(this.handle);
+    for (const b of Object.values(this.buffers)) b.destroy();
+  }
+
+  assertAlive() {
+    if (this.destroyed) throw new Error("Parakeet encoder graph was destroyed");
+  }
+}
+
 module.exports = {
   native,
   paletteBitsForLayout,
@@ -1038,4 +1702,22 @@ module.exports = {
   RelativeAttentionKernel,
   RelativeAttentionDispatch,
   relativeAttentionTensorRecords,
+  LayerNormKernel,
+  LayerNormDispatch,
+  channelTensorRecords,
+  subsamplingOutputDimension,
+  subsamplingValidLength,
+  subsamplingTensorRecords,
+  FusedSubsamplingConv0Depthwise2Kernel,
+  DepthwiseSubsamplingKernel,
+  SubsamplingTimeMaskKernel,
+  SubsamplingDispatch,
+  deriveEncoderValidLength,
+  deriveEncoderValidLengths,
+  ParakeetEncoderGraph,
+  PARAKEET_FEATURE_BINS,
+  PARAKEET_FEATURE_FRAMES,
+  PARAKEET_ENCODER_FRAMES,
+  PARAKEET_PROJECTED_CHANNELS,
+  ENCODER_LAYER_DISPATCHES,
 };

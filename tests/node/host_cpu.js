@@ -168,6 +168,89 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
     throwsLike(() => attention.validateDescriptor(attDescriptor((d) => {
       d.biasV = Object.assign({}, d.biasV, { runtimeRecord: Object.assign({}, rec.biasV.runtimeRecord, { dtype: "float16" }) });
     })), Error, "layer0-relative-attention bias V must be float32 head-by-channel logical/storage [8,128]");
-    console.log("host_cpu ok");
+    return host.LayerNormKernel.create({}, arena, 64);
+  }).then((norm) => {
+    // createDispatch checks of layernorm.ts:165-240
+    const affine = host.channelTensorRecords(1024);
+    function lnDescriptor(mutate) {
+      const d = {
+        label: "encoder.layers.0.norm_feed_forward1", rows: 3008, channels: 1024,
+        input: arena.slice("x", 0, 3008 * 1024 * 2), output: arena.slice("y", 64 * 1024 * 1024, 3008 * 1024 * 2),
+        gamma: tensor(affine), beta: tensor(affine),
+      };
+      if (mutate) mutate(d);
+      return d;
+    }
+    norm.validateDescriptor(lnDescriptor());
+    throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => { d.channels = 1022; })), RangeError,
+               "Invalid LayerNorm shape for encoder.layers.0.norm_feed_forward1");
+    throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => { d.output = arena.slice("y", 0, 1024); })),
+               RangeError, "encoder.layers.0.norm_feed_forward1 output needs 6160384 bytes; arena slice has 1024");
+    throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => { d.beta = tensor(host.channelTensorRecords(512)); })),
+               Error, "encoder.layers.0.norm_feed_forward1 beta must be float32 channel logical/storage [1024], 4096 bytes");
+    return host.FusedSubsamplingConv0Depthwise2Kernel.create({}, arena, 64);
+  }).then((fused) => {
+    // subsampling-kernel-shapes.test.ts:27-50 and createDispatch (subsampling.ts:334-387)
+    assert.deepStrictEqual([1501, 751, 376].map((n) => host.subsamplingOutputDimension(n)), [751, 376, 188]);
+    assert.deepStrictEqual([1, 2, 3].map((s) => host.subsamplingValidLength(799, s)), [400, 200, 100]);
+    assert.deepStrictEqual(Array.from(host.deriveEncoderValidLengths([1500, 799, 1])), [188, 100, 1]);
+    throwsLike(() => host.deriveEncoderValidLength(1502), RangeError, "featureLength must not exceed 1501");
+    const rec = host.subsamplingTensorRecords();
+    function fusedDescriptor(mutate) {
+      const d = {
+        label: "subsampling-fused-conv0-depthwise2-batch-0-size-3", batchSize: 3, inputHeight: 1501,
+        inputWidth: 128, channels: 256, input: arena.slice("fbank", 0, 3 * 1501 * 128 * 4),
+        conv0Weights: tensor(rec.conv0Weights), conv0Bias: tensor(rec.bias),
+        depthwiseWeights: tensor(rec.depthwiseWeights), depthwiseBias: tensor(rec.bias),
+        output: arena.slice("stage376", 64 * 1024 * 1024, 3 * 376 * 32 * 256 * 2),
+        validLengths: arena.slice("lengths", 128 * 1024 * 1024, 12),
+      };
+      if (mutate) mutate(d);
+      return d;
+    }
+    fused.validateDescriptor(fusedDescriptor());
+    throwsLike(() => fused.validateDescriptor(fusedDescriptor((d) => { d.inputWidth = 80; })), RangeError,
+               "Fused conv0+depthwise2 requires fixed");
+    throwsLike(() => fused.validateDescriptor(fusedDescriptor((d) => {
+      d.output = arena.slice("stage376", 64 * 1024 * 1024, 3 * 376 * 32 * 256 * 2 - 4);
+    })), RangeError, "output needs 18481152 bytes; arena slice has 18481148");
+    throwsLike(() => fused.validateDescriptor(fusedDescriptor((d) => { d.conv0Weights = tensor(rec.depthwiseWeights); })),
+               Error, "conv0 weights must be float16 kh-kw-output-channel-vec4 logical [3,3,256], storage [3,3,64,4], 4608 bytes");
+    return host.DepthwiseSubsamplingKernel.create({}, arena, 64).then((dw) => {
+      const d = {
+        label: "subsampling-depthwise5", batchSize: 3, inputHeight: 376, inputWidth: 32, channels: 256,
+        input: arena.slice("p376", 0, 3 * 376 * 32 * 256 * 2), weights: tensor(rec.depthwiseWeights),
+        bias: tensor(rec.bias), output: arena.slice("s188", 64 * 1024 * 1024, 3 * 188 * 16 * 256 * 2),
+        validLengths: arena.slice("lengths", 128 * 1024 * 1024, 12), validLengthSubsamplingSteps: 3,
+      };
+      dw.validateDescriptor(d);
+      throwsLike(() => dw.validateDescriptor(Object.assign({}, d, { validLengthSubsamplingSteps: 0 })), RangeError,
+                 "subsampling-depthwise5 valid-length subsampling steps must be a positive integer");
+      return host.SubsamplingTimeMaskKernel.create({}, arena, 64);
+    }).then((mask) => {
+      const d = {
+        label: "subsampling-pointwise6-mask", batchSize: 3, height: 188, width: 16, channels: 256,
+        values: arena.slice("p188", 0, 3 * 188 * 16 * 256 * 2), validLengths: arena.slice("lengths", 128 * 1024 * 1024, 12),
+        validLengthSubsamplingSteps: 3,
+      };
+      mask.validateDescriptor(d);
+      throwsLike(() => mask.validateDescriptor(Object.assign({}, d, { channels: 6 })), RangeError,
+                 "Subsampling mask channels must be divisible by four");
+    });
+  }).then(() => {
+    // ParakeetEncoderGraph.create resolves every tensor with requireTensorRecord (encoder.ts:2550-2581).
+    const model = { tensor(name) { throw new Error(`Missing tensor ${name}`); } };
+    return host.ParakeetEncoderGraph.create({}, model).then(() => assert.fail("created"), (e) => {
+      assert.ok(/Missing tensor encoder\.layers\.0\.norm_feed_forward1\.weight/.test(e.message), String(e));
+      const bad = { tensor(name) {
+        const r = { dtype: "float16", layout: "channel", byteLength: 2048, logicalShape: [1024], storageShape: [1024] };
+        return { sourceRecord: r, runtimeRecord: r, binding: { buffer: fakeBuffer, offset: 0, size: 2048 } };
+      } };
+      return host.ParakeetEncoderGraph.create({}, bad);
+    }).then(() => assert.fail("created"), (e) => {
+      assert.strictEqual(e.message, "encoder.layers.0.norm_feed_forward1.weight source must be float32 channel, " +
+                         "logical [1024], storage [1024]");
+      console.log("host_cpu ok");
+    });
   });
 }).catch((e) => { console.error(e); process.exit(1); });

@@ -108,3 +108,96 @@ def test_node_host_attention_matches_oracle(tmp_path, oracle, workloads):
     want = oracle.relative_attention(case.qkv[:2 * frames], case.packed_positions, case.bias_u, case.bias_v,
                                      case.valid[:2], batch=2, frames=frames)
     assert oracle.relative_errors(got, want)[0] <= 2e-3
+
+
+def encoder_package_tensors(stack):
+    """The stack's tensors under the reference package's names and records
+    (model/convert.py:1264-1475, :1608-1702; encoder.ts:2458-2548)."""
+    def palette(name, packed, lut, inner, columns, bits):
+        groups = lut.shape[0]
+        cpg, wpg = (32, 5) if bits == 5 else (16, 3)
+        yield name, packed, "uint32", [inner, columns], [inner * columns // cpg, wpg], \
+            f"k-by-output-row-major-palette{bits}-lsb-u32"
+        yield f"{name}.palette", lut, "float16", [groups, 1 << bits], [groups, 1 << bits], "output-group-by-palette-lut"
+
+    def channel(name, values, layout="channel"):
+        yield name, values, "float32", [values.size], [values.size], layout
+
+    frames = stack.frames
+    norms = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out")
+    matrices = {"ff1_linear1": "feed_forward1.linear1", "ff1_linear2": "feed_forward1.linear2",
+                "qkv": "self_attn.qkv", "o_proj": "self_attn.o_proj", "pointwise1": "conv.pointwise_conv1",
+                "pointwise2": "conv.pointwise_conv2", "ff2_linear1": "feed_forward2.linear1",
+                "ff2_linear2": "feed_forward2.linear2"}
+    from parakeet_wgsl_amd.workloads import ENCODER_MATRICES
+    for i, layer in enumerate(stack.layers):
+        p = f"encoder.layers.{i}"
+        for j, norm in enumerate(norms):
+            yield from channel(f"{p}.{norm}.weight", layer["norm_gamma"][j])
+            yield from channel(f"{p}.{norm}.bias", layer["norm_beta"][j])
+        for key, name in matrices.items():
+            bits, inner, columns, _ = ENCODER_MATRICES[key]
+            yield from palette(f"{p}.{name}.weight", *layer[key], inner, columns, bits)
+        yield f"{p}.self_attn.projected_positions", layer["projected_positions"], "float16", \
+            [2 * frames - 1, 1024], [8, 32, 2 * frames - 1, 4], "head-vector-position-vec4"
+        for b in ("bias_u", "bias_v"):
+            yield f"{p}.self_attn.{b}", layer[b], "float32", [8, 128], [8, 128], "head-by-channel"
+        yield f"{p}.conv.depthwise_conv.weight", layer["depthwise"], "float16", [9, 1024], [9, 256, 4], \
+            "kernel-channel-vec4"
+        yield from channel(f"{p}.conv.norm.scale", layer["bn_scale"])
+        yield from channel(f"{p}.conv.norm.shift", layer["bn_shift"])
+    f, s = stack.subsampling, "encoder.subsampling"
+    for idx, key, layout in ((0, "conv0", "kh-kw-output-channel-vec4"), (2, "depthwise2", "kh-kw-channel-vec4"),
+                             (5, "depthwise5", "kh-kw-channel-vec4")):
+        yield f"{s}.layers.{idx}.weight", f[f"{key}_weights"], "float16", [3, 3, 256], [3, 3, 64, 4], layout
+        yield from channel(f"{s}.layers.{idx}.bias", f[f"{key}_bias"], "output-channel")
+    for idx, key in ((3, "pointwise3"), (6, "pointwise6")):
+        yield from palette(f"{s}.layers.{idx}.weight", *f[key], 256, 256, 5)
+        yield from channel(f"{s}.layers.{idx}.bias", f[f"{key}_bias"], "output-channel")
+    yield from palette(f"{s}.linear.weight", *f["linear"], 4096, 1024, 5)
+    yield from channel(f"{s}.linear.bias", f["linear_bias"], "output-channel")
+    yield from palette("encoder_projector.weight", *stack.projector, 1024, 640, 5)
+    yield from channel("encoder_projector.bias", stack.projector_bias, "output-channel")
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_encoder_graph(tmp_path, abi, ctx, oracle, workloads):
+    """ParakeetEncoderGraph through the Node host (fbank -> front end -> 2
+    layers -> projector, 2 windows): eager, graph and profiled passes
+    bit-identical to each other and to the C ABI's own run of the same
+    weights, and within 1e-2 of the oracle's f64 chain on the valid frames."""
+    from test_gpu_encoder import Scope, Stack, valid_rows
+    stack = workloads.encoder_stack(seed=31, windows=2, frames=188, layers=2, front_end=True, projector=True,
+                                    feature_lengths=[1501, 700])
+    tensors = {}
+    for k, (name, array, dtype, logical, storage, layout) in enumerate(encoder_package_tensors(stack)):
+        path = str(tmp_path / f"t{k}.bin")
+        np.ascontiguousarray(array).tofile(path)
+        tensors[name] = dict(file=path, dtype=dtype, logicalShape=logical, storageShape=storage, layout=layout)
+    np.ascontiguousarray(stack.features).tofile(tmp_path / "features.bin")
+    spec = dict(tensors=tensors, features=str(tmp_path / "features.bin"), batchSize=2, layers=2,
+                featureLengths=[int(v) for v in stack.feature_lengths],
+                encoderLengths=[int(v) for v in stack.valid],
+                output=str(tmp_path / "out.bin"), projected=str(tmp_path / "projected.bin"))
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print(run_node("host_gpu_encoder.js", str(tmp_path / "case.json")))
+    got = np.fromfile(tmp_path / "out.bin", dtype=np.float16).reshape(-1, 1024)
+    projected = np.fromfile(tmp_path / "projected.bin", dtype=np.float16).reshape(-1, 640)
+    scope = Scope(ctx)
+    try:
+        enc = Stack(abi, ctx, scope, stack)
+        try:
+            want, want_projected = enc.run_both()
+        finally:
+            enc.release()
+    finally:
+        scope.close()
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    np.testing.assert_array_equal(projected.view(np.uint16), want_projected.view(np.uint16))
+    truth = oracle.encoder_graph(None, stack.layers, stack.valid, batch=2, frames=188, front=stack.subsampling,
+                                 features=stack.features, feature_lengths=stack.feature_lengths,
+                                 projector=stack.projector, projector_bias=stack.projector_bias, gemm_mode="f64",
+                                 threads=16)
+    assert oracle.relative_errors(valid_rows(got, stack), valid_rows(truth[0], stack))[0] <= 1e-2
+    assert oracle.relative_errors(valid_rows(projected, stack), valid_rows(truth[1], stack))[0] <= 1e-2
