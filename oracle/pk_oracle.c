@@ -846,3 +846,374 @@ int pko_subsampling_mask(int dtype, uint32_t batch, uint32_t height, uint32_t wi
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Greedy TDT decoder (src/webgpu/kernels/tdt-decoder.ts:1133-2010)          */
+/* ------------------------------------------------------------------------ */
+
+/* binary16 neighbours of v: *lo <= v <= *hi (equal when v is one). */
+static void f16_bracket(double v, double *lo, double *hi) {
+  const uint16_t bits = pko_f64_to_f16(v);
+  const double r = pko_f16_to_f64(bits);
+  if (r == v || isinf(r) || isnan(r)) {
+    *lo = *hi = r;
+    return;
+  }
+  /* the neighbour on the other side of v: one step in magnitude */
+  uint16_t other_bits;
+  if ((r > v) == !(bits & 0x8000u)) /* r above v in magnitude: step toward zero */
+    other_bits = (bits & 0x7fffu) ? (uint16_t)(bits - 1u) : (uint16_t)(bits ^ 0x8000u);
+  else
+    other_bits = (uint16_t)(bits + 1u);
+  const double o = pko_f16_to_f64(other_bits);
+  *lo = r < o ? r : o;
+  *hi = r < o ? o : r;
+}
+
+/* fma in binary16 with one rounding: round16(a * b + c) for binary16 a, b,
+   c. a * b is exact in double; the double sum s plus its error e (TwoSum)
+   is the exact value, and e only decides the rounding when s sits exactly
+   on a binary16 midpoint. */
+static double fma16(double a, double b, double c) {
+  const double p = a * b;
+  const double s = p + c;
+  const double t = s - p;
+  const double e = (p - (s - t)) + (c - t);
+  if (e == 0.0 || isinf(s)) return pko_round_f16(s);
+  double lo, hi;
+  f16_bracket(s, &lo, &hi);
+  if (lo != hi && s == lo + (hi - lo) / 2.0) return e > 0.0 ? hi : lo;
+  return pko_round_f16(s);
+}
+
+float pko_exp_f32(float x) {
+  /* n = rint(x / ln2); r = x - n ln2 with ln2 = 0.693145751953125 (exact in
+     f32, 12 bits) + 1.42860682030941723212e-6; e^r = sum r^i / i!, i <= 7
+     (|r| <= 0.347: truncation below 2^-27 relative). */
+  const float log2e = 1.44269502f;
+  const float ln2_hi = 0.693145751953125f;
+  const float ln2_lo = 1.42860682030941723212e-6f;
+  const float n = rintf(x * log2e);
+  float r = fmaf(-n, ln2_hi, x);
+  r = fmaf(-n, ln2_lo, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int32_t ni = (int32_t)n;
+  uint32_t scale_bits = (uint32_t)(ni + 127) << 23;
+  float scale;
+  memcpy(&scale, &scale_bits, sizeof scale);
+  return p * scale;
+}
+
+float pko_tanh_f32(float x) {
+  const float a = fabsf(x);
+  const float t = 1.0f - 2.0f / (pko_exp_f32(2.0f * a) + 1.0f);
+  return x < 0.0f ? -t : t;
+}
+
+/* 1 / (1 + exp(-clamp(v, -20, 20))) (tdt-decoder.ts:1309-1311). */
+static float tdt_sigmoid(float v) {
+  const float bounded = fminf(fmaxf(v, -20.0f), 20.0f);
+  return 1.0f / (1.0f + pko_exp_f32(-bounded));
+}
+
+/* tanh(clamp(v, -10, 10)) (tdt-decoder.ts:1318-1322). */
+static float tdt_tanh(float v) { return pko_tanh_f32(fminf(fmaxf(v, -10.0f), 10.0f)); }
+
+/* The decoder's f16 weights widened to double once per call. */
+typedef struct tdt_dense {
+  double *embedding, *lstm[2], *projector, *head;
+  const float *lstm_bias[2], *projector_bias, *head_bias;
+} tdt_dense;
+
+static double *widen16(const uint16_t *src, uint64_t count) {
+  double *out = (double *)malloc(sizeof(double) * count);
+  if (out)
+    for (uint64_t i = 0; i < count; ++i) out[i] = pko_f16_to_f64(src[i]);
+  return out;
+}
+
+static void tdt_dense_free(tdt_dense *d) {
+  free(d->embedding);
+  free(d->lstm[0]);
+  free(d->lstm[1]);
+  free(d->projector);
+  free(d->head);
+}
+
+static int tdt_dense_make(const pko_tdt_weights *w, tdt_dense *d) {
+  const uint64_t H = PKO_TDT_HIDDEN;
+  memset(d, 0, sizeof *d);
+  d->embedding = widen16(w->embedding, (uint64_t)PKO_TDT_TOKENS * H);
+  d->lstm[0] = widen16(w->lstm_weight[0], 2 * H * PKO_TDT_GATES);
+  d->lstm[1] = widen16(w->lstm_weight[1], 2 * H * PKO_TDT_GATES);
+  d->projector = widen16(w->projector_weight, H * H);
+  d->head = widen16(w->head_weight, H * PKO_TDT_HEAD);
+  d->lstm_bias[0] = w->lstm_bias[0];
+  d->lstm_bias[1] = w->lstm_bias[1];
+  d->projector_bias = w->projector_bias;
+  d->head_bias = w->head_bias;
+  if (!d->embedding || !d->lstm[0] || !d->lstm[1] || !d->projector || !d->head) {
+    tdt_dense_free(d);
+    return 1;
+  }
+  return 0;
+}
+
+/* One LSTM layer's gates (tdt-decoder.ts:1341-1382, accumulators :572-686):
+   per gate an f16 chain over even k starting at f16(bias) and one over odd k
+   starting at 0, fma in increasing k, added in f16. x[k] is the f16 input of
+   row k; `limit` rows are used (0: none). */
+static void tdt_gates(const double *weight, const float *bias, const double *x, uint32_t limit, float *gates) {
+  double even[PKO_TDT_GATES], odd[PKO_TDT_GATES];
+  for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) {
+    even[j] = pko_round_f16((double)bias[j]);
+    odd[j] = 0.0;
+  }
+  for (uint32_t k = 0; k < limit; k += 2) {
+    const double *we = weight + (uint64_t)k * PKO_TDT_GATES, *wo = we + PKO_TDT_GATES;
+    const double xe = x[k], xo = x[k + 1];
+    for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) {
+      even[j] = fma16(xe, we[j], even[j]);
+      odd[j] = fma16(xo, wo[j], odd[j]);
+    }
+  }
+  for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) gates[j] = (float)pko_round_f16(even[j] + odd[j]);
+}
+
+/* Cell update (tdt-decoder.ts:1384-1410) into h, c. */
+static void tdt_cell(const float *gates, const float *c_prev, float *h, float *c) {
+  for (uint32_t ch = 0; ch < PKO_TDT_HIDDEN; ++ch) {
+    const float ig = tdt_sigmoid(gates[ch]);
+    const float fg = tdt_sigmoid(gates[PKO_TDT_HIDDEN + ch]);
+    const float gg = tdt_tanh(gates[2 * PKO_TDT_HIDDEN + ch]);
+    const float og = tdt_sigmoid(gates[3 * PKO_TDT_HIDDEN + ch]);
+    const float cell = fmaf(fg, c_prev[ch], ig * gg);
+    c[ch] = cell;
+    h[ch] = og * tdt_tanh(cell);
+  }
+}
+
+static void tdt_predictor(const tdt_dense *w, uint32_t token, int initial, const float *state, float *cand) {
+  const uint32_t H = PKO_TDT_HIDDEN;
+  double x[2 * PKO_TDT_HIDDEN];
+  float gates[PKO_TDT_GATES];
+  /* layer 0: [embedding(token); h0], skipped for the start token (zero x, h) */
+  for (uint32_t k = 0; k < H; ++k) {
+    x[k] = initial ? 0.0 : w->embedding[(uint64_t)token * H + k];
+    x[H + k] = pko_round_f16((double)state[k]);
+  }
+  tdt_gates(w->lstm[0], w->lstm_bias[0], x, initial ? 0 : 2 * H, gates);
+  tdt_cell(gates, state + H, cand, cand + H);
+  /* layer 1: [candidate h0; h1]; the start token uses candidate h0 only */
+  for (uint32_t k = 0; k < H; ++k) {
+    x[k] = pko_round_f16((double)cand[k]);
+    x[H + k] = pko_round_f16((double)state[2 * H + k]);
+  }
+  tdt_gates(w->lstm[1], w->lstm_bias[1], x, initial ? H : 2 * H, gates);
+  tdt_cell(gates, state + 3 * H, cand + 2 * H, cand + 3 * H);
+  /* decoder projector in f32 (tdt-decoder.ts:1462-1491) */
+  for (uint32_t o = 0; o < H; ++o) {
+    float acc = w->projector_bias[o];
+    for (uint32_t k = 0; k < H; ++k) acc = fmaf(cand[2 * H + k], (float)w->projector[(uint64_t)k * H + o], acc);
+    cand[4 * H + o] = acc;
+  }
+}
+
+static float sanitize_score(float v) { return v != v ? -3.402823466e+38f : v; }
+
+static void tdt_joint(const tdt_dense *w, const uint16_t *encoder_row, const float *projection, float *scores,
+                      uint32_t *token, uint32_t *duration) {
+  const uint32_t H = PKO_TDT_HIDDEN;
+  double acc[PKO_TDT_HEAD];
+  float joint[PKO_TDT_HIDDEN];
+  for (uint32_t c = 0; c < H; ++c) {
+    const float v = (float)pko_f16_to_f64(encoder_row[c]) + projection[c];
+    joint[c] = v > 0.0f ? v : 0.0f; /* max(v, 0) */
+  }
+  for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = pko_round_f16((double)w->head_bias[o]);
+  /* f16 chains in increasing k; exact +0 inputs skipped until a -0 or NaN
+     input has been seen (tdt-decoder.ts:977-1031) */
+  int zero_skip_safe = 1;
+  for (uint32_t k = 0; k < H; ++k) {
+    uint32_t bits;
+    memcpy(&bits, &joint[k], sizeof bits);
+    const int is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
+    const int exceptional = bits == 0x80000000u || is_nan;
+    zero_skip_safe = zero_skip_safe && !exceptional;
+    if (zero_skip_safe && bits == 0u) continue;
+    const double x = pko_round_f16((double)joint[k]);
+    const double *row = w->head + (uint64_t)k * PKO_TDT_HEAD;
+    for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = fma16(x, row[o], acc[o]);
+  }
+  /* argmax over tokens and blank, then over durations: the largest value,
+     the lowest id among equal values (choose_better, :1517-1525) */
+  uint32_t best = 0xffffffffu, best_d = 0xffffffffu;
+  float best_v = -3.402823466e+38f, best_dv = -3.402823466e+38f;
+  for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) {
+    const float v = sanitize_score((float)acc[o]);
+    if (scores) scores[o] = (float)acc[o];
+    if (o <= PKO_TDT_BLANK) {
+      if (v > best_v || (v == best_v && o < best)) {
+        best_v = v;
+        best = o;
+      }
+    } else if (o < PKO_TDT_BLANK + 1 + PKO_TDT_DURATIONS) {
+      const uint32_t d = o - PKO_TDT_BLANK - 1;
+      if (v > best_dv || (v == best_dv && d < best_d)) {
+        best_dv = v;
+        best_d = d;
+      }
+    }
+  }
+  *token = best;
+  *duration = best_d;
+}
+
+void pko_tdt_predictor(const pko_tdt_weights *w, uint32_t token, int initial, const float *state, float *cand) {
+  tdt_dense d;
+  if (tdt_dense_make(w, &d)) return;
+  tdt_predictor(&d, token, initial, state, cand);
+  tdt_dense_free(&d);
+}
+
+void pko_tdt_joint(const pko_tdt_weights *w, const uint16_t *encoder_row, const float *projection, float *scores,
+                   uint32_t *token, uint32_t *duration) {
+  tdt_dense d;
+  if (tdt_dense_make(w, &d)) return;
+  tdt_joint(&d, encoder_row, projection, scores, token, duration);
+  tdt_dense_free(&d);
+}
+
+typedef struct tdt_job {
+  const tdt_dense *w;
+  uint32_t b, frames, max_tokens;
+  const uint16_t *encoder_projected;
+  const uint32_t *lengths, *starts, *ends, *flush;
+  float *state_all, *scratch_all;
+  uint32_t *tokens, *token_frames, *token_durations, *counts, *status;
+} tdt_job;
+
+/* The decode of one window (tdt-decoder.ts:1664-2010). */
+static void tdt_decode_window(const tdt_job *j) {
+  const uint32_t H = PKO_TDT_HIDDEN, b = j->b, frames = j->frames, max_tokens = j->max_tokens;
+  const tdt_dense *w = j->w;
+  float *state = j->state_all + (uint64_t)b * 4 * H;
+  float *cand = j->scratch_all + (uint64_t)b * 5 * H;
+  const uint16_t *enc = j->encoder_projected + (uint64_t)b * frames * H;
+  memset(state, 0, sizeof(float) * 4 * H);
+  uint32_t count = 0, st = 0, symbols = 0;
+  const uint32_t limit = j->lengths[b] < frames ? j->lengths[b] : frames;
+  const uint32_t encoded = limit < j->ends[b] ? limit : j->ends[b];
+  uint32_t time = j->starts[b] < encoded ? j->starts[b] : encoded;
+  uint32_t token = 0, duration = 0;
+  if (time < encoded) tdt_predictor(w, 0, 1, state, cand);
+  /* emission and the predictor update after a non-blank (:1740-1810) */
+#define TDT_EMIT(frame_value)                                                          \
+  do {                                                                                 \
+    if (count < max_tokens) {                                                          \
+      const uint64_t at = (uint64_t)b * max_tokens + count;                            \
+      j->tokens[at] = token;                                                           \
+      j->token_frames[at] = (frame_value);                                             \
+      j->token_durations[at] = duration;                                               \
+      ++count;                                                                         \
+    } else {                                                                           \
+      st |= PKO_TDT_OVERFLOW;                                                          \
+    }                                                                                  \
+  } while (0)
+#define TDT_ADVANCE_PREDICTOR()                    \
+  do {                                             \
+    memcpy(state, cand, sizeof(float) * 4 * H);    \
+    tdt_predictor(w, token, 0, state, cand);       \
+  } while (0)
+  while (time < encoded) {
+    tdt_joint(w, enc + (uint64_t)time * H, cand + 4 * H, NULL, &token, &duration);
+    const int emitted = token != PKO_TDT_BLANK;
+    if (emitted) TDT_EMIT(time);
+    symbols += 1;
+    if (duration != 0) {
+      time += duration;
+      symbols = 0;
+    } else if (!emitted || symbols >= 10) {
+      time += 1;
+      symbols = 0;
+    }
+    if (emitted) TDT_ADVANCE_PREDICTOR();
+  }
+  /* bounded end-of-stream flush (:1812-1998) */
+  if (j->flush[b] != 0 && j->starts[b] < encoded) {
+    uint32_t flush_blanks = 0, flush_time = time;
+    symbols = 0;
+    while (symbols < 10 && flush_blanks < 5) {
+      const uint32_t variation = symbols % 3;
+      if (variation == 0) {
+        const uint32_t last = limit - 1u;
+        time = flush_time < last ? flush_time : last;
+      } else if (variation == 1) {
+        time = encoded - 1u < frames - 1u ? encoded - 1u : frames - 1u;
+      } else {
+        const uint32_t m = (encoded > 2u ? encoded : 2u) - 2u;
+        time = m < frames - 1u ? m : frames - 1u;
+      }
+      tdt_joint(w, enc + (uint64_t)time * H, cand + 4 * H, NULL, &token, &duration);
+      const int emitted = token != PKO_TDT_BLANK;
+      if (!emitted) {
+        flush_blanks += 1;
+      } else {
+        flush_blanks = 0;
+        TDT_EMIT(flush_time < encoded - 1u ? flush_time : encoded - 1u);
+      }
+      const uint32_t step = duration > 1u ? duration : 1u;
+      flush_time = flush_time + step < encoded ? flush_time + step : encoded;
+      symbols += 1;
+      if (emitted) TDT_ADVANCE_PREDICTOR();
+    }
+  }
+#undef TDT_EMIT
+#undef TDT_ADVANCE_PREDICTOR
+  j->counts[b] = count;
+  j->status[b] = st;
+}
+
+static void *tdt_worker(void *opaque) {
+  tdt_decode_window((const tdt_job *)opaque);
+  return NULL;
+}
+
+int pko_tdt_decode(const pko_tdt_weights *w, uint32_t batch, uint32_t frames, uint32_t max_tokens,
+                   const uint16_t *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
+                   const uint32_t *ends, const uint32_t *flush, float *state_all, float *scratch_all,
+                   uint32_t *tokens, uint32_t *token_frames, uint32_t *token_durations, uint32_t *counts,
+                   uint32_t *status) {
+  if (!w || !encoder_projected || !lengths || !starts || !ends || !flush || !state_all || !scratch_all || !tokens ||
+      !token_frames || !token_durations || !counts || !status || frames == 0 || max_tokens == 0)
+    return 1;
+  tdt_dense d;
+  if (tdt_dense_make(w, &d)) return 1;
+  /* windows are independent: one thread each */
+  tdt_job *jobs = (tdt_job *)calloc(batch ? batch : 1, sizeof(tdt_job));
+  pthread_t *tids = (pthread_t *)calloc(batch ? batch : 1, sizeof(pthread_t));
+  char *running = (char *)calloc(batch ? batch : 1, 1);
+  for (uint32_t b = 0; b < batch; ++b) {
+    tdt_job j = {&d, b, frames, max_tokens, encoder_projected, lengths, starts, ends, flush, state_all,
+                 scratch_all, tokens, token_frames, token_durations, counts, status};
+    jobs[b] = j;
+    if (pthread_create(&tids[b], NULL, tdt_worker, &jobs[b]) == 0)
+      running[b] = 1;
+    else
+      tdt_decode_window(&jobs[b]);
+  }
+  for (uint32_t b = 0; b < batch; ++b)
+    if (running[b]) pthread_join(tids[b], NULL);
+  free(running);
+  free(tids);
+  free(jobs);
+  tdt_dense_free(&d);
+  return 0;
+}

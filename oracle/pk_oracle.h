@@ -62,6 +62,19 @@
  *                         the subsampled valid length); the three are pinned by
  *                         torch's conv2d in float64, one-hot kernels and the
  *                         length edges in tests/test_oracle.py.
+ *   pko_tdt_decode        src/webgpu/kernels/tdt-decoder.ts:1133-2010 (greedy TDT
+ *                         decode: two-layer LSTM predictor with f16 gate chains,
+ *                         f32 cell update, f32 decoder projector, ReLU joint, f16
+ *                         vocabulary head, lowest-id argmax, durations, the
+ *                         10-symbol cap and the bounded end-of-stream flush);
+ *                         pinned by closed forms (zero-weight heads that fix the
+ *                         token and duration), torch.nn.LSTM / matmul restatements
+ *                         of one predictor step and one joint, and its exp and
+ *                         tanh against the math library.
+ *   pko_exp_f32, pko_tanh_f32  the decoder's transcendental functions, written
+ *                         from range reduction and a Taylor polynomial (the
+ *                         reference uses WGSL's exp / tanh, whose last bits are
+ *                         implementation-defined); pinned against numpy.
  *
  * Status codes: 0 ok, 1 invalid argument.
  */
@@ -207,6 +220,54 @@ int pko_subsampling_depthwise(int dtype, uint32_t batch, uint32_t height, uint32
    channels] values (dtype). */
 int pko_subsampling_mask(int dtype, uint32_t batch, uint32_t height, uint32_t width, uint32_t channels,
                          void *values, const uint32_t *valid, uint32_t steps);
+
+/* ---- greedy TDT decoder ---------------------------------------------- */
+
+#define PKO_TDT_HIDDEN 640
+#define PKO_TDT_GATES 2560
+#define PKO_TDT_TOKENS 1025     /* 1024 tokens + blank (1024) */
+#define PKO_TDT_HEAD 1032       /* tokens, blank, 5 durations, 2 padding */
+#define PKO_TDT_BLANK 1024
+#define PKO_TDT_DURATIONS 5
+#define PKO_TDT_OVERFLOW 1u
+
+/* exp(x) for |x| <= 87 (normal results) in f32: n = rint(x log2 e), r = x - n ln2 (two-part
+   ln2, fmaf), e^r by a degree-7 Taylor polynomial (Horner, fmaf), times 2^n;
+   within 2 ulp of the exact value. */
+float pko_exp_f32(float x);
+/* tanh(x) = sign(x) (1 - 2 / (exp(2|x|) + 1)) in f32 (absolute error below
+   2^-23); callers clamp to [-10, 10] as the reference does. */
+float pko_tanh_f32(float x);
+
+typedef struct pko_tdt_weights {
+  const uint16_t *embedding;       /* f16 [1025, 640] token-by-channel */
+  const uint16_t *lstm_weight[2];  /* f16 [1280, 2560] k-by-ifgo (k < 640: input, k >= 640: recurrent h) */
+  const float *lstm_bias[2];       /* f32 [2560] (bias_ih + bias_hh) */
+  const uint16_t *projector_weight;/* f16 [640, 640] k-by-output */
+  const float *projector_bias;     /* f32 [640] */
+  const uint16_t *head_weight;     /* f16 [640, 1032] k-by-output (1030 used) */
+  const float *head_bias;          /* f32 [1032] */
+} pko_tdt_weights;
+
+/* Greedy TDT decode of `batch` windows (tdt-decoder.ts:1664-2010), f16
+   profile: encoder_projected f16 [batch, frames, 640]; lengths, starts, ends,
+   flush [batch]; outputs tokens / token_frames / token_durations [batch,
+   max_tokens], counts and status [batch]. state f32 [batch, 4, 640] and
+   scratch f32 [batch, 5, 640] are working memory (written). */
+int pko_tdt_decode(const pko_tdt_weights *w, uint32_t batch, uint32_t frames, uint32_t max_tokens,
+                   const uint16_t *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
+                   const uint32_t *ends, const uint32_t *flush, float *state, float *scratch, uint32_t *tokens,
+                   uint32_t *token_frames, uint32_t *token_durations, uint32_t *counts, uint32_t *status);
+
+/* One predictor step of window-independent pieces, for pins: from token
+   (ignored when initial) and the committed state [4, 640] (h0, c0, h1, c1)
+   to the candidates [5, 640] (h0, c0, h1, c1, projection). */
+void pko_tdt_predictor(const pko_tdt_weights *w, uint32_t token, int initial, const float *state, float *candidate);
+/* One joint: scores [1032] (f32 values of the f16 accumulators) of
+   relu(encoder_row + projection) through the head; returns the chosen token
+   and duration through `token` / `duration`. */
+void pko_tdt_joint(const pko_tdt_weights *w, const uint16_t *encoder_row, const float *projection, float *scores,
+                   uint32_t *token, uint32_t *duration);
 
 #ifdef __cplusplus
 }

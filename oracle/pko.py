@@ -23,6 +23,8 @@ Reference functions restated (see pk_oracle.h for the pins):
   subsampling_mask        subsampling.ts:1332-1430
   encoder_layer   the dispatch order of src/webgpu/encoder.ts:1868-2135,
                   composed from the functions above
+  tdt_decode / tdt_predictor / tdt_joint  src/webgpu/kernels/tdt-decoder.ts:1133-2010
+  exp_f32 / tanh_f32   the decoder's transcendental functions
   encoder_front_end  createSubsamplingCommands, encoder.ts:2140-2400
   encoder_graph   ParakeetEncoderGraph.encode, encoder.ts:1690-1706 (front
                   end, layers, projector)
@@ -104,6 +106,14 @@ def lib() -> ctypes.CDLL:
             [ctypes.c_void_p] * 3 + [ctypes.c_float, ctypes.c_void_p]
         _lib.pko_glu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_void_p,
                                  ctypes.c_void_p]
+        _lib.pko_exp_f32.restype = ctypes.c_float
+        _lib.pko_exp_f32.argtypes = [ctypes.c_float]
+        _lib.pko_tanh_f32.restype = ctypes.c_float
+        _lib.pko_tanh_f32.argtypes = [ctypes.c_float]
+        _lib.pko_tdt_decode.argtypes = [ctypes.POINTER(_TdtWeights)] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 12
+        _lib.pko_tdt_predictor.argtypes = [ctypes.POINTER(_TdtWeights), ctypes.c_uint32, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_void_p]
+        _lib.pko_tdt_joint.argtypes = [ctypes.POINTER(_TdtWeights)] + [ctypes.c_void_p] * 5
         _lib.pko_subsampling_fused.argtypes = [ctypes.c_int] + [ctypes.c_uint32] * 4 + [ctypes.c_void_p] * 7
         _lib.pko_subsampling_depthwise.argtypes = [ctypes.c_int] + [ctypes.c_uint32] * 4 + [ctypes.c_void_p] * 4 + \
             [ctypes.c_uint32, ctypes.c_void_p]
@@ -404,6 +414,94 @@ def encoder(x, layers, valid, *, batch, frames, gemm_mode="f16-chain", threads=8
     for layer in layers:
         x = encoder_layer(x, layer, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
     return x
+
+
+TDT_HIDDEN, TDT_GATES, TDT_HEAD, TDT_BLANK = 640, 2560, 1032, 1024
+
+
+class _TdtWeights(ctypes.Structure):
+    _fields_ = [("embedding", ctypes.c_void_p), ("lstm_weight", ctypes.c_void_p * 2),
+                ("lstm_bias", ctypes.c_void_p * 2), ("projector_weight", ctypes.c_void_p),
+                ("projector_bias", ctypes.c_void_p), ("head_weight", ctypes.c_void_p), ("head_bias", ctypes.c_void_p)]
+
+
+def _tdt_weights(weights: dict):
+    """(struct, keep-alive list) from a dict keyed like the decoder package:
+    embedding f16 [1025, 640], lstm_weight_l0/_l1 f16 [1280, 2560],
+    lstm_bias_l0/_l1 f32 [2560], projector_weight f16 [640, 640],
+    projector_bias f32 [640], head_weight f16 [640, 1032], head_bias f32 [1032]."""
+    keep = {k: np.ascontiguousarray(v) for k, v in weights.items()}
+    expect = {"embedding": (np.float16, (1025, 640)), "lstm_weight_l0": (np.float16, (1280, 2560)),
+              "lstm_weight_l1": (np.float16, (1280, 2560)), "lstm_bias_l0": (np.float32, (2560,)),
+              "lstm_bias_l1": (np.float32, (2560,)), "projector_weight": (np.float16, (640, 640)),
+              "projector_bias": (np.float32, (640,)), "head_weight": (np.float16, (640, 1032)),
+              "head_bias": (np.float32, (1032,))}
+    for name, (dtype, shape) in expect.items():
+        if keep[name].dtype != dtype or keep[name].shape != shape:
+            raise ValueError(f"decoder tensor {name} must be {np.dtype(dtype).name} {shape}")
+    w = _TdtWeights(_ptr(keep["embedding"]), (ctypes.c_void_p * 2)(_ptr(keep["lstm_weight_l0"]),
+                                                                    _ptr(keep["lstm_weight_l1"])),
+                    (ctypes.c_void_p * 2)(_ptr(keep["lstm_bias_l0"]), _ptr(keep["lstm_bias_l1"])),
+                    _ptr(keep["projector_weight"]), _ptr(keep["projector_bias"]), _ptr(keep["head_weight"]),
+                    _ptr(keep["head_bias"]))
+    return w, keep
+
+
+def exp_f32(x: float) -> float:
+    return float(lib().pko_exp_f32(float(x)))
+
+
+def tanh_f32(x: float) -> float:
+    return float(lib().pko_tanh_f32(float(x)))
+
+
+def tdt_predictor(weights: dict, token: int, state, initial: bool = False) -> np.ndarray:
+    """Candidates [5, 640] (h0, c0, h1, c1, projection) of one predictor step
+    from the committed state [4, 640] (tdt-decoder.ts:1341-1500)."""
+    w, keep = _tdt_weights(weights)
+    state = np.ascontiguousarray(state, dtype=np.float32).reshape(4, TDT_HIDDEN)
+    cand = np.empty((5, TDT_HIDDEN), dtype=np.float32)
+    lib().pko_tdt_predictor(ctypes.byref(w), int(token), int(initial), _ptr(state), _ptr(cand))
+    return cand
+
+
+def tdt_joint(weights: dict, encoder_row, projection):
+    """(scores [1032], token, duration) of one joint (tdt-decoder.ts:1605-1662)."""
+    w, keep = _tdt_weights(weights)
+    encoder_row = np.ascontiguousarray(encoder_row, dtype=np.float16)
+    projection = np.ascontiguousarray(projection, dtype=np.float32)
+    scores = np.empty(TDT_HEAD, dtype=np.float32)
+    token, duration = ctypes.c_uint32(), ctypes.c_uint32()
+    lib().pko_tdt_joint(ctypes.byref(w), _ptr(encoder_row), _ptr(projection), _ptr(scores), ctypes.byref(token),
+                        ctypes.byref(duration))
+    return scores, token.value, duration.value
+
+
+def tdt_decode(weights: dict, encoder_projected, lengths, *, max_tokens: int, starts=None, ends=None, flush=None):
+    """Greedy TDT decode (tdt-decoder.ts:1664-2010) of encoder_projected f16
+    [batch, frames, 640]; returns dict(tokens, frames, durations [batch,
+    max_tokens] u32, counts, status [batch], and the final state [batch, 4,
+    640] and predictor scratch [batch, 5, 640])."""
+    w, keep = _tdt_weights(weights)
+    enc = np.ascontiguousarray(encoder_projected, dtype=np.float16)
+    batch, frames, hidden = enc.shape
+    if hidden != TDT_HIDDEN:
+        raise ValueError("encoder_projected must be [batch, frames, 640]")
+
+    def vec(v, default):
+        return np.ascontiguousarray(np.full(batch, default) if v is None else v, dtype=np.uint32)
+    lengths = vec(lengths, frames)
+    starts, ends, flush = vec(starts, 0), vec(ends, 0xFFFFFFFF), vec(flush, 0)
+    state = np.zeros((batch, 4, TDT_HIDDEN), np.float32)
+    scratch = np.zeros((batch, 5, TDT_HIDDEN), np.float32)
+    out = {k: np.zeros((batch, max_tokens), np.uint32) for k in ("tokens", "frames", "durations")}
+    counts, status = np.zeros(batch, np.uint32), np.zeros(batch, np.uint32)
+    if lib().pko_tdt_decode(ctypes.byref(w), batch, frames, max_tokens, _ptr(enc), _ptr(lengths), _ptr(starts),
+                            _ptr(ends), _ptr(flush), _ptr(state), _ptr(scratch), _ptr(out["tokens"]),
+                            _ptr(out["frames"]), _ptr(out["durations"]), _ptr(counts), _ptr(status)):
+        raise ValueError("tdt_decode rejected its arguments")
+    out.update(counts=counts, status=status, state=state, scratch=scratch)
+    return out
 
 
 def encoder_front_end(features, front, feature_lengths, *, gemm_mode="f16-chain", threads=8) -> np.ndarray:

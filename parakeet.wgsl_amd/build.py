@@ -34,7 +34,8 @@ HIP_FLAGS = [
 ]
 SOURCES = [
     "pk_abi.cpp", "pk_conv_abi.cpp", "pk_attention_abi.cpp", "pk_layernorm_abi.cpp",
-    "pk_encoder_abi.cpp", "pk_subsampling_abi.cpp", "pk_codes.hip", "pk_conv.hip", "pk_subsampling.hip",
+    "pk_encoder_abi.cpp", "pk_subsampling_abi.cpp", "pk_tdt_abi.cpp", "pk_codes.hip", "pk_conv.hip",
+    "pk_subsampling.hip", "pk_tdt.hip",
     "pk_attention.hip", "pk_layernorm.hip",
     "pk_gemm_f16.hip", "pk_gemm_f16k.hip",
     "pk_gemm_f16s.hip", "pk_gemm_f32.hip",

@@ -264,6 +264,31 @@ SubsamplingGeometry subsampling_geometry(int kind, bool f16, const SubsamplingAr
 hipError_t launch_subsampling(int kind, bool f16, const SubsamplingArgs& args, uint32_t batch, hipStream_t stream,
                               hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
+// Greedy TDT decoder (pk_tdt.hip).
+constexpr uint32_t kTdtHidden = 640;
+constexpr uint32_t kTdtGates = 2560;
+constexpr uint32_t kTdtHead = 1032;
+constexpr uint32_t kTdtBlank = 1024;
+constexpr uint32_t kTdtThreads = 640;
+struct TdtArgs {
+  const _Float16* embedding;     // [1025, 640]
+  const _Float16* lstm[2];       // [1280, 2560] k by ifgo
+  const float* lstm_bias[2];     // [2560]
+  const _Float16* projector;     // [640, 640] k by output
+  const float* projector_bias;   // [640]
+  const _Float16* head;          // [640, 1032] k by output
+  const float* head_bias;        // [1032]
+  const _Float16* encoder;       // [batch, frames, 640]
+  const uint32_t *lengths, *starts, *ends, *flush;  // [batch]
+  float* state;                  // [batch, 4, 640]: h0, c0, h1, c1
+  float* scratch;                // [batch, 5, 640]: candidates and projection
+  uint32_t *tokens, *token_frames, *token_durations;  // [batch, max_tokens]
+  uint32_t *counts, *status;     // [batch]
+  uint32_t frames, max_tokens;
+};
+hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t stream, hipEvent_t start = nullptr,
+                             hipEvent_t stop = nullptr);
+
 int conv_variant_count(bool f16);
 ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,
                            bool input_glu = false);

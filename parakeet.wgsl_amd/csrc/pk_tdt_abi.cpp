@@ -1,0 +1,169 @@
+// pk_tdt_abi.cpp - C ABI of the greedy TDT decoder: the create and
+// createDispatch checks and the encode launch of
+// src/webgpu/kernels/tdt-decoder.ts (:39-547).
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "pk_abi_internal.h"
+#include "pk_internal.h"
+#include "pk_tdt.h"
+
+using namespace pk_abi;
+
+struct pk_tdt_op {
+  pk_context* ctx = nullptr;
+  std::string label;
+  uint32_t batch = 0;
+  pk::TdtArgs args{};
+  bool destroyed = false;
+};
+
+namespace {
+
+constexpr uint64_t H = PK_TDT_HIDDEN;
+
+// requireTensor (tdt-decoder.ts:458-478): the decoder tensor's size.
+int tensor(const void* p, uint64_t bytes, uint64_t need, const char* layout, const char* shape) {
+  if (!p || bytes != need || !aligned(p, 16))
+    return fail(PK_INVALID_ARGUMENT, "Unexpected decoder tensor %s [%s]", layout, shape);
+  return PK_OK;
+}
+
+// requireSliceBytes (tdt-decoder.ts:549-553).
+int slice(const void* p, uint64_t bytes, uint64_t need, const char* name) {
+  if (!p || bytes < need) return fail(PK_RANGE_ERROR, "%s is too small for TDT decoding", name);
+  if (!aligned(p, 4)) return fail(PK_RANGE_ERROR, "%s is not word aligned", name);
+  return PK_OK;
+}
+
+int validate(const pk_tdt_desc* d) {
+  if (!d) return fail(PK_INVALID_ARGUMENT, "TDT decoder descriptor is null");
+  if (d->struct_size != sizeof(pk_tdt_desc)) return fail(PK_INVALID_ARGUMENT, "pk_tdt_desc.struct_size mismatch");
+  if (d->precision != PK_PRECISION_F16)
+    return fail(PK_INVALID_ARGUMENT, "TDT decoder f16 profile required (precision %d)", d->precision);
+  // validateDescriptor (:507-547)
+  if (d->batch_size == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder batchSize");
+  if (d->frames == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder frames");
+  if (d->max_tokens == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder maxTokens");
+  const uint64_t B = d->batch_size;
+  int s;
+  if ((s = slice(d->encoder_projected, d->encoder_projected_bytes, B * d->frames * H * 2, "encoderProjected")) ||
+      (s = slice(d->encoded_lengths, d->encoded_lengths_bytes, B * 4, "encodedLengths")) ||
+      (s = slice(d->decode_starts, d->decode_starts_bytes, B * 4, "decodeStarts")) ||
+      (s = slice(d->decode_ends, d->decode_ends_bytes, B * 4, "decodeEnds")) ||
+      (s = slice(d->flush_finals, d->flush_finals_bytes, B * 4, "flushFinals")) ||
+      (s = slice(d->state, d->state_bytes, B * 4 * H * 4, "state")) ||
+      (s = slice(d->predictor_scratch, d->predictor_scratch_bytes, B * 5 * H * 4, "predictorScratch")) ||
+      (s = slice(d->tokens, d->tokens_bytes, B * d->max_tokens * 4, "tokens")) ||
+      (s = slice(d->token_frames, d->token_frames_bytes, B * d->max_tokens * 4, "tokenFrames")) ||
+      (s = slice(d->token_durations, d->token_durations_bytes, B * d->max_tokens * 4, "tokenDurations")) ||
+      (s = slice(d->metadata, d->metadata_bytes, B * 2 * 4, "metadata")))
+    return s;
+  // requireDecoderWeights (:378-456)
+  const pk_tdt_weights& w = d->weights;
+  if ((s = tensor(w.embedding, w.embedding_bytes, PK_TDT_TOKEN_OUTPUTS * H * 2, "token-by-channel-row-major",
+                  "1025,640")) ||
+      (s = tensor(w.lstm_weight[0], w.lstm_weight_bytes[0], 2 * H * 4 * H * 2,
+                  "input-hidden-k-by-ifgo-row-major-vec4", "1280,2560")) ||
+      (s = tensor(w.lstm_weight[1], w.lstm_weight_bytes[1], 2 * H * 4 * H * 2,
+                  "input-hidden-k-by-ifgo-row-major-vec4", "1280,2560")) ||
+      (s = tensor(w.lstm_bias[0], w.lstm_bias_bytes[0], 4 * H * 4, "ifgo-gates", "2560")) ||
+      (s = tensor(w.lstm_bias[1], w.lstm_bias_bytes[1], 4 * H * 4, "ifgo-gates", "2560")) ||
+      (s = tensor(w.projector_weight, w.projector_weight_bytes, H * H * 2, "k-by-output-row-major-vec4",
+                  "640,640")) ||
+      (s = tensor(w.projector_bias, w.projector_bias_bytes, H * 4, "output-channel", "640")) ||
+      (s = tensor(w.head_weight, w.head_weight_bytes, H * PK_TDT_HEAD_OUTPUTS * 2, "k-by-output-row-major-vec4",
+                  "640,1032")) ||
+      (s = tensor(w.head_bias, w.head_bias_bytes, PK_TDT_HEAD_OUTPUTS * 4, "output-channel-padded-vec4", "1032")))
+    return s;
+  if (!aligned(d->encoder_projected, 16) || !aligned(d->state, 16) || !aligned(d->predictor_scratch, 16))
+    return fail(PK_INVALID_ARGUMENT, "%s bindings must be 16-byte aligned", d->label ? d->label : "tdt-decoder");
+  return PK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_tdt_plan_execution(uint32_t batch_size, pk_tdt_execution_plan* plan) {
+  if (!plan) return fail(PK_INVALID_ARGUMENT, "plan output is null");
+  if (batch_size == 0) return fail(PK_RANGE_ERROR, "TDT decoder batchSize must be a positive integer");
+  plan->workgroup_count = batch_size;
+  plan->block_threads = pk::kTdtThreads;
+  plan->predictor_scratch_bytes = (uint64_t)batch_size * 5 * H * 4;
+  return ok();
+}
+
+int pk_tdt_validate(const pk_tdt_desc* d) { return validate(d); }
+
+int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!out) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  if (int s = validate(d)) return s;
+  auto* op = new pk_tdt_op();
+  op->ctx = ctx;
+  op->label = d->label ? d->label : "parakeet-persistent-tdt-decode";
+  op->batch = d->batch_size;
+  pk::TdtArgs& a = op->args;
+  const pk_tdt_weights& w = d->weights;
+  a.embedding = static_cast<const _Float16*>(w.embedding);
+  a.lstm[0] = static_cast<const _Float16*>(w.lstm_weight[0]);
+  a.lstm[1] = static_cast<const _Float16*>(w.lstm_weight[1]);
+  a.lstm_bias[0] = w.lstm_bias[0];
+  a.lstm_bias[1] = w.lstm_bias[1];
+  a.projector = static_cast<const _Float16*>(w.projector_weight);
+  a.projector_bias = w.projector_bias;
+  a.head = static_cast<const _Float16*>(w.head_weight);
+  a.head_bias = w.head_bias;
+  a.encoder = static_cast<const _Float16*>(d->encoder_projected);
+  a.lengths = d->encoded_lengths;
+  a.starts = d->decode_starts;
+  a.ends = d->decode_ends;
+  a.flush = d->flush_finals;
+  a.state = d->state;
+  a.scratch = d->predictor_scratch;
+  a.tokens = d->tokens;
+  a.token_frames = d->token_frames;
+  a.token_durations = d->token_durations;
+  a.counts = d->metadata;
+  a.status = d->metadata + d->batch_size;
+  a.frames = d->frames;
+  a.max_tokens = d->max_tokens;
+  *out = op;
+  return ok();
+}
+
+int pk_tdt_enqueue(pk_tdt_op* op, uint32_t active_batch, void* stream) {
+  return pk_tdt_enqueue_timed(op, active_batch, stream, nullptr, nullptr);
+}
+
+int pk_tdt_enqueue_timed(pk_tdt_op* op, uint32_t active_batch, void* stream, void* start_event, void* end_event) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "TDT decoder op is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  const uint32_t batch = active_batch ? active_batch : op->batch;
+  // TdtDecoderDispatch.encode (:84-130)
+  if (batch > op->batch)
+    return fail(PK_RANGE_ERROR, "%s active batch must be in [1, %u]", op->label.c_str(), op->batch);
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  PK_HIP(pk::launch_tdt_decode(op->args, batch, stream_or_default(op->ctx, stream),
+                               static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(end_event)),
+         "TDT decoder launch");
+  return ok();
+}
+
+int pk_tdt_destroy(pk_tdt_op* op) {
+  if (!op || op->destroyed) return ok();
+  op->destroyed = true;
+  return ok();
+}
+
+int pk_tdt_release(pk_tdt_op* op) {
+  if (!op) return ok();
+  pk_tdt_destroy(op);
+  delete op;
+  return ok();
+}
+
+}  // extern "C"

@@ -1,5 +1,5 @@
 """ctypes binding of libpk_palette.so (include/pk_palette.h, pk_conv.h, pk_attention.h,
-pk_layernorm.h, pk_subsampling.h, pk_encoder.h).
+pk_layernorm.h, pk_subsampling.h, pk_encoder.h, pk_tdt.h).
 
 A thin Python view of the C ABI, used by the tests and the benchmark. It
 raises PaletteError (or PaletteRangeError, mirroring the reference's
@@ -316,6 +316,45 @@ class SubsamplingPlanInfo(ctypes.Structure):
     ]
 
 
+class TdtWeights(ctypes.Structure):
+    _fields_ = [
+        ("embedding", ctypes.c_void_p),
+        ("embedding_bytes", ctypes.c_uint64),
+        ("lstm_weight", ctypes.c_void_p * 2),
+        ("lstm_weight_bytes", ctypes.c_uint64 * 2),
+        ("lstm_bias", ctypes.c_void_p * 2),
+        ("lstm_bias_bytes", ctypes.c_uint64 * 2),
+        ("projector_weight", ctypes.c_void_p),
+        ("projector_weight_bytes", ctypes.c_uint64),
+        ("projector_bias", ctypes.c_void_p),
+        ("projector_bias_bytes", ctypes.c_uint64),
+        ("head_weight", ctypes.c_void_p),
+        ("head_weight_bytes", ctypes.c_uint64),
+        ("head_bias", ctypes.c_void_p),
+        ("head_bias_bytes", ctypes.c_uint64),
+    ]
+
+
+class TdtDesc(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("label", ctypes.c_char_p),
+        ("precision", ctypes.c_int32),
+        ("batch_size", ctypes.c_uint32),
+        ("frames", ctypes.c_uint32),
+        ("max_tokens", ctypes.c_uint32),
+        ("weights", TdtWeights),
+    ] + [(name, t) for field in ("encoder_projected", "encoded_lengths", "decode_starts", "decode_ends",
+                                 "flush_finals", "state", "predictor_scratch", "tokens", "token_frames",
+                                 "token_durations", "metadata")
+         for name, t in ((field, ctypes.c_void_p), (field + "_bytes", ctypes.c_uint64))]
+
+
+class TdtExecutionPlan(ctypes.Structure):
+    _fields_ = [("workgroup_count", ctypes.c_uint32), ("block_threads", ctypes.c_uint32),
+                ("predictor_scratch_bytes", ctypes.c_uint64)]
+
+
 class EncoderMatrix(ctypes.Structure):
     _fields_ = [("packed", ctypes.c_void_p), ("palette", ctypes.c_void_p)]
 
@@ -460,6 +499,13 @@ SIGNATURES = {
     "pk_subsampling_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(SubsamplingPlanInfo)]),
     "pk_subsampling_destroy": (ctypes.c_int, [_VP]),
     "pk_subsampling_release": (ctypes.c_int, [_VP]),
+    "pk_tdt_plan_execution": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(TdtExecutionPlan)]),
+    "pk_tdt_validate": (ctypes.c_int, [ctypes.POINTER(TdtDesc)]),
+    "pk_tdt_create": (ctypes.c_int, [_VP, ctypes.POINTER(TdtDesc), _PPV]),
+    "pk_tdt_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_tdt_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_tdt_destroy": (ctypes.c_int, [_VP]),
+    "pk_tdt_release": (ctypes.c_int, [_VP]),
     "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
     "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
     "pk_encoder_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, ctypes.c_int]),
@@ -1016,3 +1062,60 @@ class EncoderOp:
         if self.handle:
             check(load().pk_encoder_destroy(self.handle))
             self.handle = None
+
+
+TDT_WEIGHT_NAMES = ("embedding", "lstm_weight_l0", "lstm_weight_l1", "lstm_bias_l0", "lstm_bias_l1",
+                    "projector_weight", "projector_bias", "head_weight", "head_bias")
+
+
+def tdt_desc(*, weights: dict, encoder_projected, encoded_lengths, decode_starts, decode_ends, flush_finals, state,
+             predictor_scratch, tokens, token_frames, token_durations, metadata, batch_size: int, frames: int,
+             max_tokens: int, label: str = "parakeet-persistent-tdt-decode") -> TdtDesc:
+    """A TdtDesc from device slices (DeviceArrays, or (address, bytes) pairs);
+    `weights` is keyed by TDT_WEIGHT_NAMES."""
+    def sl(x):
+        return tuple(x) if isinstance(x, tuple) else _slice(x)
+    w = {k: sl(weights[k]) for k in TDT_WEIGHT_NAMES}
+    tw = TdtWeights(*w["embedding"], (ctypes.c_void_p * 2)(w["lstm_weight_l0"][0], w["lstm_weight_l1"][0]),
+                    (ctypes.c_uint64 * 2)(w["lstm_weight_l0"][1], w["lstm_weight_l1"][1]),
+                    (ctypes.c_void_p * 2)(w["lstm_bias_l0"][0], w["lstm_bias_l1"][0]),
+                    (ctypes.c_uint64 * 2)(w["lstm_bias_l0"][1], w["lstm_bias_l1"][1]),
+                    *w["projector_weight"], *w["projector_bias"], *w["head_weight"], *w["head_bias"])
+    fields = []
+    for x in (encoder_projected, encoded_lengths, decode_starts, decode_ends, flush_finals, state, predictor_scratch,
+              tokens, token_frames, token_durations, metadata):
+        fields += list(sl(x))
+    return TdtDesc(ctypes.sizeof(TdtDesc), label.encode(), PRECISION["f16"], batch_size, frames, max_tokens, tw,
+                   *fields)
+
+
+class TdtDecoderOp:
+    """The greedy TDT decoder (PersistentTdtDecoderKernel.createDispatch,
+    tdt-decoder.ts:294-366)."""
+
+    def __init__(self, ctx: Context, **descriptor):
+        self.desc = tdt_desc(**descriptor)
+        handle = ctypes.c_void_p()
+        check(load().pk_tdt_create(ctx.handle, ctypes.byref(self.desc), ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def enqueue(self, active_batch: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_tdt_enqueue(self.handle, active_batch, stream))
+        else:
+            check(load().pk_tdt_enqueue_timed(self.handle, active_batch, stream,
+                                              start.handle if start else None, end.handle if end else None))
+
+    def destroy(self) -> None:
+        check(load().pk_tdt_destroy(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_tdt_release(self.handle))
+            self.handle = None
+
+
+def plan_tdt_execution(batch_size: int) -> TdtExecutionPlan:
+    plan = TdtExecutionPlan()
+    check(load().pk_tdt_plan_execution(batch_size, ctypes.byref(plan)))
+    return plan

@@ -517,3 +517,59 @@ def encoder_stack(seed: int = 0, windows: int = 16, frames: int = 188, layers: i
         enc.projector = (random_packed_words(rng, 5, 1024, 640), normal(rng, (1, 32), 0.02, np.float16))
         enc.projector_bias = normal(rng, (640,), 0.01, np.float32)
     return enc
+
+
+
+@dataclass
+class TdtCase:
+    """A TDT decoder over random weights (decoder package shapes): weights
+    keyed like palette_abi.TDT_WEIGHT_NAMES, the encoder projector's output
+    [batch, frames, 640] f16, encoded lengths, decode starts and ends,
+    flush flags."""
+    weights: dict
+    encoder_projected: np.ndarray
+    lengths: np.ndarray
+    starts: np.ndarray
+    ends: np.ndarray
+    flush: np.ndarray
+
+    @property
+    def batch(self) -> int:
+        return self.encoder_projected.shape[0]
+
+    @property
+    def frames(self) -> int:
+        return self.encoder_projected.shape[1]
+
+
+def tdt_weights(rng: np.random.Generator, blank_bias: float = 2.0) -> dict:
+    """Embedding ~ N(0, 0.5), LSTM weights ~ N(0, 0.03) and biases ~
+    N(0, 0.1), projector ~ N(0, 0.04), head ~ N(0, 0.05) with bias ~
+    N(0, 0.1) plus `blank_bias` on the blank (random heads otherwise never
+    choose blank), f16 weights and f32 biases."""
+    def n(shape, std, dtype):
+        return (rng.standard_normal(shape) * std).astype(dtype)
+    head_bias = n(1032, 0.1, np.float32)
+    head_bias[1024] += blank_bias
+    head_bias[1030:] = 0.0
+    head = n((640, 1032), 0.05, np.float16)
+    head[:, 1030:] = 0
+    return dict(embedding=n((1025, 640), 0.5, np.float16), lstm_weight_l0=n((1280, 2560), 0.03, np.float16),
+                lstm_weight_l1=n((1280, 2560), 0.03, np.float16), lstm_bias_l0=n(2560, 0.1, np.float32),
+                lstm_bias_l1=n(2560, 0.1, np.float32), projector_weight=n((640, 640), 0.04, np.float16),
+                projector_bias=n(640, 0.1, np.float32), head_weight=head, head_bias=head_bias)
+
+
+def tdt_case(seed: int = 0, batch: int = 16, frames: int = 188, *, lengths=None, starts=None, ends=None,
+             flush=None, blank_bias: float = 2.0, encoder_std: float = 0.5) -> TdtCase:
+    """Encoder projector output ~ N(0, encoder_std) f16; lengths uniform in
+    [ceil(T/2), T] unless given; starts 0, ends T, no flush unless given."""
+    rng = np.random.default_rng(seed)
+    weights = tdt_weights(rng, blank_bias)
+    enc = normal(rng, (batch, frames, 640), encoder_std, np.float16)
+    if lengths is None:
+        lengths = rng.integers((frames + 1) // 2, frames + 1, size=batch)
+
+    def vec(v, default):
+        return np.asarray(np.full(batch, default) if v is None else v, dtype=np.uint32)
+    return TdtCase(weights, enc, vec(lengths, frames), vec(starts, 0), vec(ends, frames), vec(flush, 0))

@@ -62,11 +62,13 @@ def test_struct_layouts_match_the_c_compiler(abi, tmp_path):
                "pk_subsampling_depthwise_desc": abi.SubsamplingDepthwiseDesc,
                "pk_subsampling_mask_desc": abi.SubsamplingMaskDesc,
                "pk_subsampling_plan_info": abi.SubsamplingPlanInfo,
+               "pk_tdt_weights": abi.TdtWeights, "pk_tdt_desc": abi.TdtDesc,
+               "pk_tdt_execution_plan": abi.TdtExecutionPlan,
                "pk_encoder_matrix": abi.EncoderMatrix, "pk_encoder_layer": abi.EncoderLayer,
                "pk_encoder_subsampling": abi.EncoderSubsampling, "pk_encoder_desc": abi.EncoderDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pk_palette.h"', '#include "pk_conv.h"',
              '#include "pk_attention.h"', '#include "pk_layernorm.h"', '#include "pk_subsampling.h"',
-             '#include "pk_encoder.h"',
+             '#include "pk_encoder.h"', '#include "pk_tdt.h"',
              "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
@@ -517,6 +519,64 @@ def test_subsampling_null_handles(abi):
     assert lib.pk_subsampling_destroy(None) == abi.OK
     assert lib.pk_subsampling_release(None) == abi.OK
     assert lib.pk_subsampling_fused_validate(None) == abi.INVALID_ARGUMENT
+
+
+# ---------------------------------------------------------------- TDT decoder
+
+
+def _tdt_fakes(batch=16, frames=188, max_tokens=256):
+    at = [0x6000000000]
+
+    def take(nbytes):
+        addr = at[0]
+        at[0] += (nbytes + 0xFFFF) // 0x10000 * 0x10000
+        return (addr, nbytes)
+    weights = {"embedding": take(1025 * 640 * 2), "lstm_weight_l0": take(1280 * 2560 * 2),
+               "lstm_weight_l1": take(1280 * 2560 * 2), "lstm_bias_l0": take(2560 * 4),
+               "lstm_bias_l1": take(2560 * 4), "projector_weight": take(640 * 640 * 2),
+               "projector_bias": take(640 * 4), "head_weight": take(640 * 1032 * 2), "head_bias": take(1032 * 4)}
+    return dict(weights=weights, encoder_projected=take(batch * frames * 640 * 2), encoded_lengths=take(4 * batch),
+                decode_starts=take(4 * batch), decode_ends=take(4 * batch), flush_finals=take(4 * batch),
+                state=take(batch * 4 * 640 * 4), predictor_scratch=take(batch * 5 * 640 * 4),
+                tokens=take(batch * max_tokens * 4), token_frames=take(batch * max_tokens * 4),
+                token_durations=take(batch * max_tokens * 4), metadata=take(8 * batch), batch_size=batch,
+                frames=frames, max_tokens=max_tokens)
+
+
+def _validate_tdt(abi, **kw):
+    desc = abi.tdt_desc(**kw)
+    abi.check(abi.load().pk_tdt_validate(ctypes.byref(desc)))
+
+
+def test_tdt_plan_and_contract(abi):
+    """planTdtDecoderExecution (tdt-decoder.ts:39-52) and validateDescriptor /
+    requireDecoderWeights (:378-547) with the reference's messages."""
+    plan = abi.plan_tdt_execution(16)
+    assert plan.workgroup_count == 16 and plan.predictor_scratch_bytes == 16 * 5 * 640 * 4
+    with pytest.raises(abi.PaletteRangeError, match="batchSize must be a positive integer"):
+        abi.plan_tdt_execution(0)
+    _validate_tdt(abi, **_tdt_fakes())
+    for field, message in (("batch_size", "Invalid TDT decoder batchSize"), ("frames", "Invalid TDT decoder frames"),
+                           ("max_tokens", "Invalid TDT decoder maxTokens")):
+        kw = _tdt_fakes()
+        kw[field] = 0
+        with pytest.raises(abi.PaletteRangeError, match=message):
+            _validate_tdt(abi, **kw)
+    kw = _tdt_fakes()
+    kw["predictor_scratch"] = (kw["predictor_scratch"][0], 100)
+    with pytest.raises(abi.PaletteRangeError, match="predictorScratch is too small for TDT decoding"):
+        _validate_tdt(abi, **kw)
+    kw = _tdt_fakes()
+    kw["weights"]["head_weight"] = (kw["weights"]["head_weight"][0], 640 * 1030 * 2)
+    with pytest.raises(abi.PaletteError, match=re.escape("Unexpected decoder tensor k-by-output-row-major-vec4 [640,1032]")):
+        _validate_tdt(abi, **kw)
+    kw = _tdt_fakes()
+    kw["weights"]["lstm_bias_l1"] = (kw["weights"]["lstm_bias_l1"][0], 2560 * 2)
+    with pytest.raises(abi.PaletteError, match=re.escape("Unexpected decoder tensor ifgo-gates [2560]")):
+        _validate_tdt(abi, **kw)
+    lib = abi.load()
+    assert lib.pk_tdt_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_tdt_destroy(None) == abi.OK
 
 
 # ---------------------------------------------------------------- encoder stack

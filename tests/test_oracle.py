@@ -774,3 +774,133 @@ def test_subsampling_mask_zeroes_rows_past_the_length(oracle):
     assert not got[0, 8:].any()
     np.testing.assert_array_equal(got[1, :5], x[1, :5])
     assert not got[1, 5:].any()
+
+
+# ---------------------------------------------------------------- TDT decoder
+
+
+def test_decoder_exp_and_tanh_against_the_math_library(oracle):
+    rng = np.random.default_rng(7)
+    xs = np.concatenate([np.linspace(-20, 20, 4001), rng.uniform(-87, 87, 2000), [0.0, -0.0, 1e-8, -1e-8]])
+    for x in xs.astype(np.float32):
+        got = oracle.exp_f32(x)
+        want = np.exp(np.float64(x))
+        assert abs(got - want) <= 2 * np.spacing(np.float32(want)), (x, got, want)
+    for x in np.concatenate([np.linspace(-10, 10, 4001), rng.uniform(-10, 10, 2000)]).astype(np.float32):
+        assert abs(oracle.tanh_f32(x) - np.tanh(np.float64(x))) <= 2.0 ** -23, x
+    assert oracle.tanh_f32(10.0) == pytest.approx(1.0, abs=2.0 ** -23)
+
+
+def decoder_weights(seed, *, lstm_std=0.03, head_std=0.05):
+    rng = np.random.default_rng(seed)
+
+    def n(shape, std, dtype):
+        return (rng.standard_normal(shape) * std).astype(dtype)
+    return dict(embedding=n((1025, 640), 0.5, np.float16), lstm_weight_l0=n((1280, 2560), lstm_std, np.float16),
+                lstm_weight_l1=n((1280, 2560), lstm_std, np.float16), lstm_bias_l0=n(2560, 0.1, np.float32),
+                lstm_bias_l1=n(2560, 0.1, np.float32), projector_weight=n((640, 640), 0.04, np.float16),
+                projector_bias=n(640, 0.1, np.float32), head_weight=n((640, 1032), head_std, np.float16),
+                head_bias=n(1032, 0.1, np.float32))
+
+
+def torch_lstm_layer(w_k_by_gates, bias, x, h, c):
+    """torch.nn.LSTMCell in float64 with the package's k-by-ifgo weight."""
+    import torch
+    w = torch.tensor(w_k_by_gates.astype(np.float64))
+    cell = torch.nn.LSTMCell(640, 640, dtype=torch.float64)
+    with torch.no_grad():
+        cell.weight_ih.copy_(w[:640].T)
+        cell.weight_hh.copy_(w[640:].T)
+        cell.bias_ih.copy_(torch.tensor(bias.astype(np.float64)))
+        cell.bias_hh.zero_()
+        h1, c1 = cell(torch.tensor(x, dtype=torch.float64)[None], (torch.tensor(h, dtype=torch.float64)[None],
+                                                                   torch.tensor(c, dtype=torch.float64)[None]))
+    return h1[0].numpy(), c1[0].numpy()
+
+
+def test_decoder_predictor_step_matches_torch_lstm(oracle):
+    """One predictor step (two LSTM layers + projector) against torch's
+    LSTMCell and a float64 product; the f16 gate chains stay within 1e-2."""
+    w = decoder_weights(1)
+    rng = np.random.default_rng(2)
+    state = (rng.standard_normal((4, 640)) * 0.3).astype(np.float32)
+    cand = oracle.tdt_predictor(w, 37, state)
+    x = w["embedding"][37].astype(np.float64)
+    h0, c0 = torch_lstm_layer(w["lstm_weight_l0"], w["lstm_bias_l0"], x, state[0], state[1])
+    h1, c1 = torch_lstm_layer(w["lstm_weight_l1"], w["lstm_bias_l1"], cand[0].astype(np.float64), state[2], state[3])
+    proj = cand[2].astype(np.float64) @ w["projector_weight"].astype(np.float64) + w["projector_bias"]
+    for got, want in ((cand[0], h0), (cand[1], c0), (cand[2], h1), (cand[3], c1), (cand[4], proj)):
+        assert np.abs(got - want).max() <= 1e-2 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
+    # the start token: zero input and state, gates are the f16-rounded biases
+    start = oracle.tdt_predictor(w, 0, np.zeros((4, 640), np.float32), initial=True)
+    g = w["lstm_bias_l0"].astype(np.float16).astype(np.float64)
+    sig = lambda v: 1 / (1 + np.exp(-np.clip(v, -20, 20)))  # noqa: E731
+    c_closed = sig(g[:640]) * np.tanh(g[1280:1920])
+    np.testing.assert_allclose(start[1], c_closed, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(start[0], sig(g[1920:]) * np.tanh(c_closed), rtol=0, atol=1e-6)
+
+
+def test_decoder_joint_matches_a_float64_product(oracle):
+    w = decoder_weights(3)
+    rng = np.random.default_rng(4)
+    row = (rng.standard_normal(640) * 0.5).astype(np.float16)
+    proj = (rng.standard_normal(640) * 0.5).astype(np.float32)
+    scores, token, duration = oracle.tdt_joint(w, row, proj)
+    joint = np.maximum(row.astype(np.float64) + proj, 0)
+    want = joint @ w["head_weight"].astype(np.float64) + w["head_bias"]
+    assert np.abs(scores[:1030] - want[:1030]).max() <= 2e-2 * np.abs(want).max()
+    assert token == int(np.argmax(scores[:1025])) and duration == int(np.argmax(scores[1025:1030]))
+
+
+def fixed_head(weights, token, duration, *, token_value=5.0):
+    """Zero head weights, so every joint returns the bias: `token` (or
+    blank, 1024) and `duration` win."""
+    w = dict(weights)
+    w["head_weight"] = np.zeros((640, 1032), np.float16)
+    bias = np.zeros(1032, np.float32)
+    bias[token] = token_value
+    bias[1025 + duration] = 3.0
+    w["head_bias"] = bias
+    return w
+
+
+def test_decoder_control_closed_forms(oracle):
+    """The decode loop's rules (tdt-decoder.ts:1740-1810) with a head that
+    always answers the same: durations advance time, duration 0 repeats a
+    frame up to 10 symbols, blanks advance one frame and emit nothing,
+    start/end bound the frames, max_tokens sets the overflow flag."""
+    base = decoder_weights(5, lstm_std=0.0)
+    enc = np.zeros((1, 12, 640), np.float16)
+    r = oracle.tdt_decode(fixed_head(base, 7, 2), enc, [11], max_tokens=64)
+    assert r["counts"][0] == 6 and r["status"][0] == 0
+    assert list(r["tokens"][0][:6]) == [7] * 6 and list(r["frames"][0][:6]) == [0, 2, 4, 6, 8, 10]
+    assert list(r["durations"][0][:6]) == [2] * 6
+    r = oracle.tdt_decode(fixed_head(base, 1024, 0), enc, [12], max_tokens=64)
+    assert r["counts"][0] == 0
+    r = oracle.tdt_decode(fixed_head(base, 3, 0), enc, [4], max_tokens=64)
+    assert r["counts"][0] == 40 and list(r["frames"][0][:40]) == sorted([0, 1, 2, 3] * 10)
+    r = oracle.tdt_decode(fixed_head(base, 3, 0), enc, [4], max_tokens=25)
+    assert r["counts"][0] == 25 and r["status"][0] == 1
+    r = oracle.tdt_decode(fixed_head(base, 9, 1), enc, [12], max_tokens=64, starts=[3], ends=[7])
+    assert r["counts"][0] == 4 and list(r["frames"][0][:4]) == [3, 4, 5, 6]
+    # lengths past the frame count are clamped to it
+    r = oracle.tdt_decode(fixed_head(base, 9, 1), enc, [500], max_tokens=64)
+    assert r["counts"][0] == 12
+
+
+def test_decoder_flush_and_ties(oracle):
+    """The bounded flush (:1812-1998): a non-blank head emits 10 more tokens
+    at the last valid frame; a blank head stops after 5 blanks. Equal
+    scores pick the lowest id; a NaN score never wins."""
+    base = decoder_weights(6, lstm_std=0.0)
+    enc = np.zeros((1, 12, 640), np.float16)
+    r = oracle.tdt_decode(fixed_head(base, 4, 1), enc, [6], max_tokens=64, flush=[1])
+    assert r["counts"][0] == 16 and list(r["frames"][0][6:16]) == [5] * 10
+    r = oracle.tdt_decode(fixed_head(base, 1024, 1), enc, [6], max_tokens=64, flush=[1])
+    assert r["counts"][0] == 0
+    w = fixed_head(base, 11, 3)
+    w["head_bias"][2] = 5.0  # ties token 11
+    w["head_bias"][1] = np.nan
+    w["head_bias"][1025 + 1] = 3.0  # ties duration 3
+    scores, token, duration = oracle.tdt_joint(w, np.zeros(640, np.float16), np.zeros(640, np.float32))
+    assert (token, duration) == (2, 1)
