@@ -30,6 +30,10 @@ Other workloads (for profiling; same JSON shape):
                     projector; random-init palette weights at the reference
                     package's widths; one step = one pass (367 launches,
                     replayed from a HIP graph); value in audio-sec/sec
+  transcribe        the encoder pass followed by the greedy TDT decoder over
+                    its projector output (LSTM predictor 640, joint to 1024
+                    tokens + blank and 5 durations), random-init weights; one
+                    step = encoder pass + decode; value in audio-sec/sec
 """
 from __future__ import annotations
 
@@ -57,7 +61,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="ff-block",
                    choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
-                            "rel-pos-mha", "encoder"])
+                            "rel-pos-mha", "encoder", "transcribe"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
@@ -339,9 +343,11 @@ def encoder_dispatch_costs(abi, wl, stack):
     return front, layer, projector
 
 
-def encoder_cpu_baseline(stack, budget_s=20.0):
+def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
     """The oracle (reference fp16 semantics) on window 0: the front end, then
-    layer after layer until about `budget_s` seconds have passed."""
+    layer after layer until about `budget_s` seconds have passed; with
+    `decoder` = (weights, projected window [188, 640] f16, length), also the
+    oracle's greedy decode of that window."""
     from oracle import pko
     threads = min(os.cpu_count() or 1, 16)
     t0 = time.perf_counter()
@@ -359,14 +365,20 @@ def encoder_cpu_baseline(stack, budget_s=20.0):
     layer_s = (time.perf_counter() - t0 - front_s) / done
     # one window's pass: the front end plus every layer at the measured rate
     pass_s = front_s + layer_s * len(stack.layers)
+    sample = (f"one 15-s window: the front end and {done} of {len(stack.layers)} layers timed, the pass "
+              "extrapolated to every layer (f16-accumulator GEMM chain, f32 conv, LayerNorm and attention: "
+              "reference fp16 semantics)")
+    if decoder is not None:
+        weights, projected, length = decoder
+        t1 = time.perf_counter()
+        pko.tdt_decode(weights, projected[None], [length], max_tokens=1024, flush=[1])
+        pass_s += time.perf_counter() - t1
+        sample += "; then the greedy TDT decode of that window (f16 LSTM and head chains)"
     return {"value": WINDOW_SECONDS / pass_s, "unit": "audio-sec/sec", "cores": threads, "kind": "port",
-            "sample": f"one 15-s window: the front end and {done} of {len(stack.layers)} layers timed, the pass "
-                      "extrapolated to every layer (f16-accumulator GEMM chain, f32 conv, LayerNorm and attention: "
-                      "reference fp16 semantics)",
-            "seconds": time.perf_counter() - t0}
+            "sample": sample, "seconds": time.perf_counter() - t0}
 
 
-def run_encoder(args, abi, ctx):
+def run_encoder(args, abi, ctx, decoder=False):
     import parakeet_wgsl_amd.workloads as wl
     stack = wl.encoder_stack(0, windows=16, frames=188, layers=24, front_end=True, projector=True)
     held = []
@@ -394,8 +406,24 @@ def run_encoder(args, abi, ctx):
                         projected_output=projected, label="encoder")
     launches, device_bytes = enc.info()
     stream = ctx.stream
+    tdt = None
+    if decoder:
+        # the decoder reads the projector output [windows, 188, 640] as is
+        rng = np.random.default_rng(1)
+        tdt_weights = {k: put(v) for k, v in wl.tdt_weights(rng).items()}
+        B, T, max_tokens = stack.batch, stack.frames, 1024
+        zeros = lambda shape, dtype: put(np.zeros(shape, dtype))  # noqa: E731
+        tdt_out = dict(state=zeros((B, 4, 640), np.float32), predictor_scratch=zeros((B, 5, 640), np.float32),
+                       tokens=zeros((B, max_tokens), np.uint32), token_frames=zeros((B, max_tokens), np.uint32),
+                       token_durations=zeros((B, max_tokens), np.uint32), metadata=zeros(2 * B, np.uint32))
+        tdt = abi.TdtDecoderOp(ctx, weights=tdt_weights, encoder_projected=projected, encoded_lengths=valid,
+                               decode_starts=zeros(B, np.uint32), decode_ends=put(np.full(B, T, np.uint32)),
+                               flush_finals=put(np.ones(B, np.uint32)), batch_size=B, frames=T,
+                               max_tokens=max_tokens, **tdt_out)
     for _ in range(args.warmup):
         enc.enqueue(0, stream, graph=True)
+        if tdt:
+            tdt.enqueue(0, stream)
     ctx.synchronize(stream)
 
     # Every TIMING_STRIDE-th pass runs eagerly with per-launch stamps; the
@@ -403,6 +431,7 @@ def run_encoder(args, abi, ctx):
     timed_steps = list(range(0, args.steps, TIMING_STRIDE))
     marks = {step: ([ctx.event() for _ in range(launches)], [ctx.event() for _ in range(launches)])
              for step in timed_steps}
+    tdt_marks = {step: (ctx.event(), ctx.event()) for step in timed_steps} if tdt else {}
     start, end = ctx.event(), ctx.event()
     ctx.synchronize(stream)
     wall0 = time.perf_counter()
@@ -410,8 +439,12 @@ def run_encoder(args, abi, ctx):
     for step in range(args.steps):
         if step in marks:
             enc.enqueue_profiled(*marks[step], 0, stream)
+            if tdt:
+                tdt.enqueue(0, stream, *tdt_marks[step])
         else:
             enc.enqueue(0, stream, graph=True)
+            if tdt:
+                tdt.enqueue(0, stream)
     end.record(stream)
     end.synchronize()
     ctx.synchronize(stream)
@@ -423,6 +456,7 @@ def run_encoder(args, abi, ctx):
         starts, ends = marks[step]
         durations[i] = [a.elapsed_ms(b) for a, b in zip(starts, ends)]
     durations = durations.mean(axis=0)  # ms per launch of the pass
+    decoder_ms = float(np.mean([a.elapsed_ms(b) for a, b in tdt_marks.values()])) if tdt else None
     front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, stack)
     nf, per = len(front_costs), len(abi.ENCODER_DISPATCHES)
     names = list(FRONT_DISPATCHES) + list(abi.ENCODER_DISPATCHES) + ["projector"] * len(projector_costs)
@@ -449,7 +483,18 @@ def run_encoder(args, abi, ctx):
     roofline["traffic"] = read_traffic(f"encoder-{name}", None)
 
     total_flops = stack.gemm_flops() + stack.attention_flops() + stack.front_end_flops()
-    cpu = None if args.no_cpu else encoder_cpu_baseline(stack)
+    cpu_decoder = None
+    if tdt and not args.no_cpu:
+        rng = np.random.default_rng(1)
+        window0 = projected.download()[:stack.frames]
+        cpu_decoder = (wl.tdt_weights(rng), window0, int(stack.valid[0]))
+    cpu = None if args.no_cpu else encoder_cpu_baseline(stack, decoder=cpu_decoder)
+    decoded = None
+    if tdt:
+        meta = tdt_out["metadata"].download()
+        decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:stack.batch]],
+                   "overflow_windows": int((meta[stack.batch:] != 0).sum()), "kernel": "tdt_decode_kernel",
+                   "workgroups": stack.batch, "max_tokens": 1024}
     line = {
         "metric": METRIC,
         "value": stack.batch * WINDOW_SECONDS / (ms_per_step * 1e-3),
@@ -463,21 +508,26 @@ def run_encoder(args, abi, ctx):
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded random fbank, palette codes, LUTs, norms and biases)",
-        "config": {"workload": "fastconformer-encoder-fp16", "windows": stack.batch,
+        "config": {"workload": "fastconformer-tdt-transcribe-fp16" if tdt else "fastconformer-encoder-fp16",
+                   "windows": stack.batch,
                    "window_seconds": WINDOW_SECONDS, "fbank_frames": stack.feature_frames, "mel_bins": 128,
                    "frames": stack.frames, "layers": len(stack.layers), "d_model": 1024, "ff_hidden": 4096,
                    "heads": 8, "subsampling": "dw_striding 8x, 256 channels", "projector": "1024->640",
                    "palette_bits": {"ff/qkv/pointwise/subsampling/projector": 5, "o_proj": 6},
-                   "launches_per_pass": launches, "graph_replay": True},
+                   "launches_per_pass": launches, "graph_replay": True,
+                   "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
         "device_bytes": device_bytes,
         "dispatches": dispatches,
+        "decoder": decoded,
         "wall_ms_per_step": wall / args.steps * 1e3,
         "device": ctx.info().name.decode(),
     }
     print(json.dumps(line), flush=True)
+    if tdt:
+        tdt.release()
     enc.release()
     for arr in held:
         arr.free()
@@ -508,8 +558,8 @@ def main():
 
     import parakeet_wgsl_amd.palette_abi as abi
     ctx = abi.Context(0)
-    if args.workload == "encoder":
-        run_encoder(args, abi, ctx)
+    if args.workload in ("encoder", "transcribe"):
+        run_encoder(args, abi, ctx, decoder=args.workload == "transcribe")
         return
     held = []
 

@@ -76,19 +76,27 @@ struct Shared {
   uint32_t go, emitted, token, duration, joint_time;
 };
 
-// Gates of one LSTM layer: thread t owns gates 4t..4t+3 over `limit` rows.
+// Rows of weights loaded before any is used: the k loops are latency
+// bound, so each thread keeps this many 8-byte loads in flight.
+constexpr uint32_t kBatchRows = 16;
+
+// Gates of one LSTM layer: thread t owns gates 4t..4t+3 over `limit` rows
+// (a multiple of kBatchRows).
 __device__ void lstm_gates(Shared& s, const _Float16* weight, const float* bias, uint32_t limit) {
   const uint32_t t = threadIdx.x;
   const float4 b = *reinterpret_cast<const float4*>(bias + 4 * t);
   half4 even = half4{(_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
   half4 odd = half4{0, 0, 0, 0};
   const _Float16* column = weight + 4 * t;
-#pragma unroll 8
-  for (uint32_t k = 0; k < limit; k += 2) {
-    const half4 we = load_half4(column + (uint64_t)k * kTdtGates);
-    const half4 wo = load_half4(column + (uint64_t)(k + 1) * kTdtGates);
-    even = __builtin_elementwise_fma(splat(s.x[k]), we, even);
-    odd = __builtin_elementwise_fma(splat(s.x[k + 1]), wo, odd);
+  for (uint32_t k0 = 0; k0 < limit; k0 += kBatchRows) {
+    half4 w[kBatchRows];
+#pragma unroll
+    for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(column + (uint64_t)(k0 + r) * kTdtGates);
+#pragma unroll
+    for (uint32_t r = 0; r < kBatchRows; r += 2) {
+      even = __builtin_elementwise_fma(splat(s.x[k0 + r]), w[r], even);
+      odd = __builtin_elementwise_fma(splat(s.x[k0 + r + 1]), w[r + 1], odd);
+    }
   }
   const half4 sum = even + odd;
   for (int i = 0; i < 4; ++i) s.gates[4 * t + i] = (float)sum[i];
@@ -140,11 +148,15 @@ __device__ void predictor(Shared& s, const TdtArgs& a, const float* state, float
     const float4 b = *reinterpret_cast<const float4*>(a.projector_bias + 4 * t);
     float acc[4] = {b.x, b.y, b.z, b.w};
     const float* h1 = cand + 2 * H;
-#pragma unroll 4
-    for (uint32_t k = 0; k < H; ++k) {
-      const half4 w = load_half4(a.projector + (uint64_t)k * H + 4 * t);
-      const float h = h1[k];
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(h, (float)w[i], acc[i]);
+    for (uint32_t k0 = 0; k0 < H; k0 += kBatchRows) {
+      half4 w[kBatchRows];
+#pragma unroll
+      for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(a.projector + (uint64_t)(k0 + r) * H + 4 * t);
+#pragma unroll
+      for (uint32_t r = 0; r < kBatchRows; ++r) {
+        const float h = h1[k0 + r];
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(h, (float)w[r][i], acc[i]);
+      }
     }
     for (int i = 0; i < 4; ++i) cand[4 * H + 4 * t + i] = acc[i];
   }
@@ -166,13 +178,18 @@ __device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, 
     half4 acc = half4{(_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
     bool zero_skip_safe = true;
     const _Float16* column = a.head + 4 * t;
-    for (uint32_t k = 0; k < H; ++k) {
-      const float x = s.joint[k];
-      const uint32_t bits = __float_as_uint(x);
-      const bool is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
-      zero_skip_safe = zero_skip_safe && !(bits == 0x80000000u || is_nan);
-      if (zero_skip_safe && bits == 0u) continue;
-      acc = __builtin_elementwise_fma(splat((_Float16)x), load_half4(column + (uint64_t)k * kTdtHead), acc);
+    for (uint32_t k0 = 0; k0 < H; k0 += kBatchRows) {
+      half4 w[kBatchRows];
+#pragma unroll
+      for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(column + (uint64_t)(k0 + r) * kTdtHead);
+#pragma unroll
+      for (uint32_t r = 0; r < kBatchRows; ++r) {
+        const float x = s.joint[k0 + r];
+        const uint32_t bits = __float_as_uint(x);
+        const bool is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
+        zero_skip_safe = zero_skip_safe && !(bits == 0x80000000u || is_nan);
+        if (!(zero_skip_safe && bits == 0u)) acc = __builtin_elementwise_fma(splat((_Float16)x), w[r], acc);
+      }
     }
     for (int i = 0; i < 4; ++i) s.scores[4 * t + i] = (float)acc[i];
   }
