@@ -29,6 +29,7 @@
 #include "pk_layernorm.h"
 #include "pk_palette.h"
 #include "pk_subsampling.h"
+#include "pk_tdt.h"
 
 #define NAPI_CALL(env, call)                                              \
   do {                                                                    \
@@ -1341,6 +1342,131 @@ static napi_value js_encoder_destroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* ---- greedy TDT decoder --------------------------------------------------- */
+
+static void tdt_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  pk_tdt_release((pk_tdt_op *)data);
+}
+
+/* {label, batchSize, frames, maxTokens, weights: {embedding, lstmWeight0,
+   lstmWeight1, lstmBias0, lstmBias1, projectorWeight, projectorBias,
+   headWeight, headBias}, encoderProjected, encodedLengths, decodeStarts,
+   decodeEnds, flushFinals, state, predictorScratch, tokens, tokenFrames,
+   tokenDurations, metadata}, every address with its "<name>Bytes". */
+static int parse_tdt_desc(napi_env env, napi_value o, pk_tdt_desc *d, char **label) {
+  memset(d, 0, sizeof *d);
+  d->struct_size = sizeof *d;
+  d->precision = PK_PRECISION_F16;
+  *label = NULL;
+  napi_value w;
+  const void *p = NULL;
+  int ok = prop_u32(env, o, "batchSize", &d->batch_size) && prop_u32(env, o, "frames", &d->frames) &&
+           prop_u32(env, o, "maxTokens", &d->max_tokens) && prop(env, o, "weights", &w);
+  pk_tdt_weights *t = &d->weights;
+  ok = ok && ptr_field(env, w, "embedding", &t->embedding, &t->embedding_bytes);
+  ok = ok && ptr_field(env, w, "lstmWeight0", &t->lstm_weight[0], &t->lstm_weight_bytes[0]);
+  ok = ok && ptr_field(env, w, "lstmWeight1", &t->lstm_weight[1], &t->lstm_weight_bytes[1]);
+  ok = ok && ptr_field(env, w, "lstmBias0", &p, &t->lstm_bias_bytes[0]);
+  t->lstm_bias[0] = (const float *)p;
+  ok = ok && ptr_field(env, w, "lstmBias1", &p, &t->lstm_bias_bytes[1]);
+  t->lstm_bias[1] = (const float *)p;
+  ok = ok && ptr_field(env, w, "projectorWeight", &t->projector_weight, &t->projector_weight_bytes);
+  ok = ok && ptr_field(env, w, "projectorBias", &p, &t->projector_bias_bytes);
+  t->projector_bias = (const float *)p;
+  ok = ok && ptr_field(env, w, "headWeight", &t->head_weight, &t->head_weight_bytes);
+  ok = ok && ptr_field(env, w, "headBias", &p, &t->head_bias_bytes);
+  t->head_bias = (const float *)p;
+  ok = ok && ptr_field(env, o, "encoderProjected", &d->encoder_projected, &d->encoder_projected_bytes);
+  ok = ok && ptr_field(env, o, "encodedLengths", &p, &d->encoded_lengths_bytes);
+  d->encoded_lengths = (const uint32_t *)p;
+  ok = ok && ptr_field(env, o, "decodeStarts", &p, &d->decode_starts_bytes);
+  d->decode_starts = (const uint32_t *)p;
+  ok = ok && ptr_field(env, o, "decodeEnds", &p, &d->decode_ends_bytes);
+  d->decode_ends = (const uint32_t *)p;
+  ok = ok && ptr_field(env, o, "flushFinals", &p, &d->flush_finals_bytes);
+  d->flush_finals = (const uint32_t *)p;
+  ok = ok && ptr_field(env, o, "state", &p, &d->state_bytes);
+  d->state = (float *)p;
+  ok = ok && ptr_field(env, o, "predictorScratch", &p, &d->predictor_scratch_bytes);
+  d->predictor_scratch = (float *)p;
+  ok = ok && ptr_field(env, o, "tokens", &p, &d->tokens_bytes);
+  d->tokens = (uint32_t *)p;
+  ok = ok && ptr_field(env, o, "tokenFrames", &p, &d->token_frames_bytes);
+  d->token_frames = (uint32_t *)p;
+  ok = ok && ptr_field(env, o, "tokenDurations", &p, &d->token_durations_bytes);
+  d->token_durations = (uint32_t *)p;
+  ok = ok && ptr_field(env, o, "metadata", &p, &d->metadata_bytes);
+  d->metadata = (uint32_t *)p;
+  if (!ok) {
+    bad_argument(env, "TDT decoder descriptor is missing a required field");
+    return 0;
+  }
+  *label = prop_string(env, o, "label");
+  d->label = *label;
+  return 1;
+}
+
+static napi_value js_tdt_plan_execution(napi_env env, napi_callback_info info) {
+  napi_value argv[1], obj;
+  uint32_t batch = 0;
+  if (!get_args(env, info, 1, argv)) return NULL;
+  if (!get_u32(env, argv[0], &batch)) batch = 0;
+  pk_tdt_execution_plan plan;
+  PK_CALL(env, pk_tdt_plan_execution(batch, &plan));
+  NAPI_CALL(env, napi_create_object(env, &obj));
+  napi_set_named_property(env, obj, "workgroupCount", make_number(env, plan.workgroup_count));
+  napi_set_named_property(env, obj, "blockThreads", make_number(env, plan.block_threads));
+  napi_set_named_property(env, obj, "predictorScratchByteLength", make_number(env, (double)plan.predictor_scratch_bytes));
+  return obj;
+}
+
+static napi_value js_tdt_validate(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  pk_tdt_desc d;
+  char *label;
+  if (!parse_tdt_desc(env, argv[0], &d, &label)) return NULL;
+  const int status = pk_tdt_validate(&d);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  return undefined(env);
+}
+
+static napi_value js_tdt_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2], ext;
+  if (!get_args(env, info, 2, argv)) return NULL;
+  pk_tdt_desc d;
+  char *label;
+  if (!parse_tdt_desc(env, argv[1], &d, &label)) return NULL;
+  pk_tdt_op *op = NULL;
+  const int status = pk_tdt_create((pk_context *)get_external(env, argv[0]), &d, &op);
+  free(label);
+  if (status != PK_OK) return throw_status(env, status);
+  NAPI_CALL(env, napi_create_external(env, op, tdt_finalize, NULL, &ext));
+  return ext;
+}
+
+/* tdtEnqueue(op, activeBatch, stream?, startEvent?, endEvent?) */
+static napi_value js_tdt_enqueue(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  uint32_t batch = 0;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  if (!is_nullish(env, argv[1]) && !get_u32(env, argv[1], &batch))
+    return bad_argument(env, "active batch must be a non-negative integer");
+  PK_CALL(env, pk_tdt_enqueue_timed((pk_tdt_op *)get_external(env, argv[0]), batch, get_external(env, argv[2]),
+                                    get_external(env, argv[3]), get_external(env, argv[4])));
+  return undefined(env);
+}
+
+static napi_value js_tdt_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_tdt_destroy((pk_tdt_op *)get_external(env, argv[0])));
+  return undefined(env);
+}
+
 /* ---- module --------------------------------------------------------------- */
 
 static napi_value init(napi_env env, napi_value exports) {
@@ -1397,6 +1523,11 @@ static napi_value init(napi_env env, napi_value exports) {
       {"encoderEnqueueProfiled", js_encoder_enqueue_profiled},
       {"encoderInfo", js_encoder_info},
       {"encoderDestroy", js_encoder_destroy},
+      {"tdtPlanExecution", js_tdt_plan_execution},
+      {"tdtValidate", js_tdt_validate},
+      {"tdtCreate", js_tdt_create},
+      {"tdtEnqueue", js_tdt_enqueue},
+      {"tdtDestroy", js_tdt_destroy},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
     napi_value f;

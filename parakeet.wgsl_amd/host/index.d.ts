@@ -542,3 +542,121 @@ export declare const PARAKEET_FEATURE_FRAMES: 1501;
 export declare const PARAKEET_ENCODER_FRAMES: 188;
 export declare const PARAKEET_PROJECTED_CHANNELS: 640;
 export declare const ENCODER_LAYER_DISPATCHES: 15;
+
+/* ------------------------------------------------------------ TDT decoder */
+
+export declare const TDT_DECODER_OVERFLOW: 1;
+export declare const TDT_BLANK_TOKEN: 1024;
+
+/** tdt-decoder.ts:39-52 (one workgroup per window here). */
+export interface TdtDecoderExecutionPlan {
+  readonly workgroupCount: number;
+  readonly blockThreads: number;
+  readonly predictorScratchByteLength: number;
+}
+export declare function planTdtDecoderExecution(batchSize: number): TdtDecoderExecutionPlan;
+
+/** tdt-decoder.ts:54-82: every slice comes from the kernel's arena. */
+export interface TdtDecoderDescriptor {
+  readonly label?: string;
+  readonly encoderProjected: ArenaSlice;
+  readonly encodedLengths: ArenaSlice;
+  readonly decodeStarts: ArenaSlice;
+  readonly decodeEnds: ArenaSlice;
+  readonly flushFinals: ArenaSlice;
+  readonly state: ArenaSlice;
+  readonly predictorScratch: ArenaSlice;
+  readonly tokens: ArenaSlice;
+  readonly tokenFrames: ArenaSlice;
+  readonly tokenDurations: ArenaSlice;
+  readonly metadata: ArenaSlice;
+  readonly batchSize: number;
+  readonly frames: number;
+  readonly maxTokens: number;
+}
+
+/** tdt-decoder.ts:84-137 */
+export declare class TdtDecoderDispatch {
+  readonly label: string;
+  encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, activeBatchSize?: number): void;
+  destroy(): void;
+}
+
+/** tdt-decoder.ts:139-366 (f16 profile). */
+export declare class PersistentTdtDecoderKernel {
+  static create(device: HipGpuDevice, arena: GpuActivationArena, model: EncoderModel & { readonly precision?: string },
+                executionProfile?: { precision: "fp16" }): Promise<PersistentTdtDecoderKernel>;
+  validateDescriptor(descriptor: TdtDecoderDescriptor): void;
+  createDispatch(descriptor: TdtDecoderDescriptor): TdtDecoderDispatch;
+}
+
+/* --------------------------------------------------------- package format */
+
+export interface ParakeetTensorRecord {
+  readonly shard: string;
+  readonly byteOffset: number;
+  readonly byteLength: number;
+  readonly dtype: "float16" | "float32" | "uint32";
+  readonly logicalShape: readonly number[];
+  readonly storageShape: readonly number[];
+  readonly layout: string;
+}
+export interface ParakeetFileRecord {
+  readonly name: string;
+  readonly byteLength: number;
+  readonly sha256: string;
+}
+export interface ParakeetManifest {
+  readonly format: "parakeet-webgpu-v1" | "parakeet-webgpu-fp32-v1";
+  readonly source: unknown;
+  readonly config: Readonly<Record<string, unknown>>;
+  readonly files: readonly ParakeetFileRecord[];
+  readonly tensors: Readonly<Record<string, ParakeetTensorRecord>>;
+}
+export interface RuntimePackageMemoryPlan {
+  readonly packedDownloadBytes: number;
+  readonly retainedRuntimeBytes: number;
+  readonly expandedRuntimeBytes: number;
+  readonly runtimeGpuBytes: number;
+  readonly largestRuntimeShardBytes: number;
+  readonly loaderPeakGpuBytes: number;
+  readonly runtimeBufferCount: number;
+}
+export interface RuntimePackagePlan {
+  readonly buffers: readonly { id: string; label: string; byteLength: number; tensorCount: number }[];
+  readonly tensors: ReadonlyMap<string, { name: string; sourceRecord: ParakeetTensorRecord; runtimeRecord: TensorRecord }>;
+  readonly shards: readonly ({ file: ParakeetFileRecord; hashOnly: true } |
+                             { file: ParakeetFileRecord; hashOnly: false; runtimeBufferId: string })[];
+  readonly memory: RuntimePackageMemoryPlan;
+}
+export declare const PARAKEET_FP16_PACKAGE_FORMAT: "parakeet-webgpu-v1";
+export declare const PARAKEET_FP32_PACKAGE_FORMAT: "parakeet-webgpu-fp32-v1";
+export declare const PARAKEET_FP16_MANIFEST_SHA256: string;
+export declare const PARAKEET_FP32_MANIFEST_SHA256: string;
+export declare function parseParakeetManifest(value: unknown): ParakeetManifest;
+export declare function parakeetManifestPrecision(manifest: ParakeetManifest): "fp16" | "fp32";
+export declare function parakeetManifestSha256(precision: "fp16" | "fp32"): string;
+export declare function planRuntimePackage(manifest: ParakeetManifest): RuntimePackagePlan;
+export declare function alignRuntimeOffset(value: number): number;
+
+export interface ParakeetPackageLoadOptions {
+  readonly expectedPrecision: "fp16" | "fp32";
+  /** A manifest other than the two published ones (this library only). */
+  readonly manifestSha256?: string;
+  readonly onProgress?: (progress: { phase: string; file?: string; loadedBytes: number; totalBytes: number }) => void;
+}
+
+/** package.ts:52-232 over HIP: one HBM allocation per resident shard. */
+export declare class ParakeetGpuPackage implements EncoderModel {
+  static load(device: HipGpuDevice, manifestPath: string, options: ParakeetPackageLoadOptions): Promise<ParakeetGpuPackage>;
+  readonly memory: RuntimePackageMemoryPlan;
+  readonly precision: "fp16" | "fp32";
+  readonly manifestUrl: string;
+  readonly manifestSha256: string;
+  readonly manifestListedBytes: number;
+  readonly manifest: ParakeetManifest;
+  readonly tokenizer: unknown;
+  tensor(name: string): GpuTensor;
+  releaseInitializationMetadata(): void;
+  destroy(): void;
+}

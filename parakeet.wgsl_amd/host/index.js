@@ -1672,6 +1672,161 @@ class ParakeetEncoderGraph {
   }
 }
 
+/* ------------------------------------------------------------ TDT decoder */
+
+const TDT_HIDDEN_SIZE = 640;
+const TDT_GATE_SIZE = 4 * TDT_HIDDEN_SIZE;
+const TDT_LSTM_INPUT_SIZE = 2 * TDT_HIDDEN_SIZE;
+const TDT_TOKEN_OUTPUTS = 1025;
+const TDT_BLANK_TOKEN = 1024;
+const TDT_HEAD_STORAGE_OUTPUTS = 1032;
+const TDT_DECODER_OVERFLOW = 1;
+
+/**
+ * planTdtDecoderExecution (tdt-decoder.ts:39-52). This library runs one
+ * workgroup of 640 threads per window (the reference pairs windows in a
+ * workgroup), so workgroupCount = batchSize; the scratch size is the
+ * reference's.
+ */
+function planTdtDecoderExecution(batchSize) {
+  if (!isSafe(batchSize) || batchSize <= 0) throw new RangeError("TDT decoder batchSize must be a positive integer");
+  return native().tdtPlanExecution(batchSize);
+}
+
+/** requireTensor (tdt-decoder.ts:458-478). */
+function requireDecoderTensor(tensor, dtype, storageShape, layout) {
+  const source = tensor.sourceRecord;
+  const runtime = tensor.runtimeRecord;
+  const shape = shapeKey(storageShape);
+  if (source.dtype !== dtype || shapeKey(source.storageShape) !== shape || source.layout !== layout ||
+      runtime.dtype !== dtype || shapeKey(runtime.storageShape) !== shape || runtime.layout !== layout ||
+      runtime.byteLength !== source.byteLength || runtime.byteOffset % 4 !== 0)
+    throw new Error(`Unexpected decoder tensor ${source.layout} [${source.storageShape.join(",")}]`);
+  return tensor;
+}
+
+/**
+ * requireDecoderWeights (tdt-decoder.ts:378-456): the nine decoder tensors,
+ * all in the resident decoder.bin shard buffer; returns the native weight
+ * descriptor (addresses and byte sizes).
+ */
+function requireDecoderWeights(model) {
+  const t = (name, dtype, shape, layout) => requireDecoderTensor(model.tensor(name), dtype, shape, layout);
+  const lstmLayout = "input-hidden-k-by-ifgo-row-major-vec4";
+  const tensors = {
+    embedding: t("decoder.embedding.weight", "float16", [TDT_TOKEN_OUTPUTS, TDT_HIDDEN_SIZE],
+                 "token-by-channel-row-major"),
+    lstmWeight0: t("decoder.lstm.weight_l0", "float16", [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
+    lstmWeight1: t("decoder.lstm.weight_l1", "float16", [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
+    projectorWeight: t("decoder.decoder_projector.weight", "float16", [TDT_HIDDEN_SIZE, TDT_HIDDEN_SIZE],
+                       "k-by-output-row-major-vec4"),
+    headWeight: t("joint.head.weight", "float16", [TDT_HIDDEN_SIZE, TDT_HEAD_STORAGE_OUTPUTS],
+                  "k-by-output-row-major-vec4"),
+    lstmBias0: t("decoder.lstm.bias_l0", "float32", [TDT_GATE_SIZE], "ifgo-gates"),
+    lstmBias1: t("decoder.lstm.bias_l1", "float32", [TDT_GATE_SIZE], "ifgo-gates"),
+    projectorBias: t("decoder.decoder_projector.bias", "float32", [TDT_HIDDEN_SIZE], "output-channel"),
+    headBias: t("joint.head.bias", "float32", [TDT_HEAD_STORAGE_OUTPUTS], "output-channel-padded-vec4"),
+  };
+  const buffer = tensors.embedding.buffer;
+  const weights = {};
+  for (const name of Object.keys(tensors)) {
+    const tensor = tensors[name];
+    if (tensor.sourceRecord.shard !== "decoder.bin" || tensor.runtimeRecord.bufferId !== "source-shard-decoder.bin" ||
+        tensor.buffer !== buffer)
+      throw new Error("Persistent TDT decoder requires one resident decoder source shard");
+    weights[name] = addressOf(tensor.binding);
+    weights[`${name}Bytes`] = tensor.binding.size;
+  }
+  return weights;
+}
+
+class TdtDecoderDispatch {
+  constructor(label, op, batchCapacity) {
+    this.label = label;
+    this.op = op;
+    this.batchCapacity = batchCapacity;
+    this.destroyed = false;
+  }
+
+  /** encode (tdt-decoder.ts:84-130): activeBatchSize selects a prefix of the windows. */
+  encode(encoder, timestampWrites, activeBatchSize) {
+    if (this.destroyed) throw new Error(`${this.label} was destroyed`);
+    const active = activeBatchSize === undefined ? this.batchCapacity : activeBatchSize;
+    if (!isSafe(active) || active <= 0 || active > this.batchCapacity)
+      throw new RangeError(`${this.label} active batch must be in [1, ${this.batchCapacity}]`);
+    const op = this.op;
+    encoder.record(() => {
+      const [begin, end] = timestampEvents(timestampWrites);
+      native().tdtEnqueue(op, active, null, begin, end);
+    });
+  }
+
+  destroy() {
+    if (this.destroyed) return;
+    this.destroyed = true;
+    native().tdtDestroy(this.op);
+  }
+}
+
+/**
+ * PersistentTdtDecoderKernel (tdt-decoder.ts:139-366): greedy TDT decoding
+ * with the whole autoregressive loop inside one launch, over the package's
+ * resident decoder shard. f16 profile.
+ */
+class PersistentTdtDecoderKernel {
+  constructor(device, arena, weights) {
+    this.device = device;
+    this.arena = arena;
+    this.weights = weights;
+  }
+
+  /** create(device, arena, model, executionProfile?) (:164-292). */
+  static create(device, arena, model, executionProfile) {
+    try {
+      const precision = precisionOf(executionProfile);
+      const profile = precision === "f32" ? "fp32" : "fp16";
+      if (model.precision !== undefined && model.precision !== profile)
+        throw new Error(`TDT decoder ${profile} profile cannot use ${model.precision} decoder weights`);
+      if (profile !== "fp16") throw new Error("TDT decoder fp32 profile is not built for gfx950");
+      return Promise.resolve(new PersistentTdtDecoderKernel(device, arena, requireDecoderWeights(model)));
+    } catch (error) {
+      return Promise.reject(error);
+    }
+  }
+
+  nativeDescriptor(descriptor) {
+    for (const name of ["batchSize", "frames", "maxTokens"]) {
+      const value = descriptor[name];
+      if (!isSafe(value) || value <= 0) throw new RangeError(`Invalid TDT decoder ${name}`);
+    }
+    const out = {
+      label: descriptor.label === undefined ? "parakeet-persistent-tdt-decode" : descriptor.label,
+      batchSize: descriptor.batchSize,
+      frames: descriptor.frames,
+      maxTokens: descriptor.maxTokens,
+      weights: this.weights,
+    };
+    for (const name of ["encoderProjected", "encodedLengths", "decodeStarts", "decodeEnds", "flushFinals", "state",
+                        "predictorScratch", "tokens", "tokenFrames", "tokenDurations", "metadata"]) {
+      const binding = this.arena.binding(descriptor[name]);
+      out[name] = addressOf(binding);
+      out[`${name}Bytes`] = binding.size;
+    }
+    return out;
+  }
+
+  validateDescriptor(descriptor) {
+    native().tdtValidate(this.nativeDescriptor(descriptor));
+  }
+
+  /** createDispatch (:294-366) with validateDescriptor (:507-547). */
+  createDispatch(descriptor) {
+    const nativeDescriptor = this.nativeDescriptor(descriptor);
+    const op = native().tdtCreate(this.device.context, nativeDescriptor);
+    return new TdtDecoderDispatch(nativeDescriptor.label, op, descriptor.batchSize);
+  }
+}
+
 module.exports = {
   native,
   paletteBitsForLayout,
@@ -1720,4 +1875,10 @@ module.exports = {
   PARAKEET_ENCODER_FRAMES,
   PARAKEET_PROJECTED_CHANNELS,
   ENCODER_LAYER_DISPATCHES,
+  planTdtDecoderExecution,
+  PersistentTdtDecoderKernel,
+  TdtDecoderDispatch,
+  TDT_DECODER_OVERFLOW,
+  TDT_BLANK_TOKEN,
+  ...require("./package.js"),
 };

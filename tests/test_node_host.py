@@ -201,3 +201,70 @@ def test_node_host_encoder_graph(tmp_path, abi, ctx, oracle, workloads):
                                  threads=16)
     assert oracle.relative_errors(valid_rows(got, stack), valid_rows(truth[0], stack))[0] <= 1e-2
     assert oracle.relative_errors(valid_rows(projected, stack), valid_rows(truth[1], stack))[0] <= 1e-2
+
+
+@needs_node
+def test_node_host_package_format_on_cpu(tmp_path):
+    """parseParakeetManifest / planRuntimePackage / ParakeetGpuPackage.load
+    of the Node host over the converter-shaped synthetic inventory (fp16 and
+    fp32 manifests, and a zero-filled fp16 package written to disk): the
+    reference tests' plan expectations and rejections, the loader's digest,
+    length and tokenizer checks with every buffer freed on failure, and the
+    decoder's weight-record checks."""
+    import package_fixture
+    for precision in ("fp16", "fp32"):
+        (tmp_path / f"{precision}.json").write_text(json.dumps(package_fixture.manifest(precision)))
+    manifest = package_fixture.write_package(str(tmp_path / "package"))
+    out = run_node("host_cpu_package.js", str(tmp_path / "fp16.json"), str(tmp_path / "fp32.json"), manifest)
+    assert "package checks passed" in out
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_transcribe_from_package(tmp_path, abi, ctx, oracle, workloads):
+    """End to end through the Node host: a converter-shaped synthetic
+    package (24 layers, the decoder shard) loaded by ParakeetGpuPackage,
+    ParakeetEncoderGraph over its tensors (4 windows of fbank, graph replay)
+    and PersistentTdtDecoderKernel over arena slices. The projector output is
+    bit-identical to the C ABI encoder run with the same weights, and the
+    token, frame and duration streams, counts and status flags are
+    bit-identical to the oracle's decode of that projector output."""
+    import hashlib
+    import package_fixture
+    from test_gpu_encoder import Scope, Stack
+    windows, max_tokens = 4, 2048
+    stack = workloads.encoder_stack(seed=41, windows=windows, frames=188, layers=24, front_end=True, projector=True,
+                                    feature_lengths=[1501, 1200, 801, 37])
+    tdt = workloads.tdt_weights(np.random.default_rng(42), blank_bias=1.0)
+    manifest = package_fixture.write_package(str(tmp_path / "package"), stack, tdt)
+    np.ascontiguousarray(stack.features).tofile(tmp_path / "features.bin")
+    spec = dict(manifest=manifest, manifestSha256=hashlib.sha256(open(manifest, "rb").read()).hexdigest(),
+                windows=windows, maxTokens=max_tokens, features=str(tmp_path / "features.bin"),
+                featureLengths=[int(v) for v in stack.feature_lengths], projected=str(tmp_path / "projected.bin"),
+                decoded=str(tmp_path / "decoded.json"))
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print(run_node("host_gpu_transcribe.js", str(tmp_path / "case.json"), timeout=300), flush=True)
+    projected = np.fromfile(tmp_path / "projected.bin", dtype=np.float16).reshape(windows, 188, 640)
+    scope = Scope(ctx)
+    try:
+        enc = Stack(abi, ctx, scope, stack)
+        try:
+            _, want_projected = enc.run_both()
+        finally:
+            enc.release()
+    finally:
+        scope.close()
+    np.testing.assert_array_equal(projected.reshape(-1, 640).view(np.uint16), want_projected.view(np.uint16))
+    decoded = json.loads((tmp_path / "decoded.json").read_text())
+    meta = np.asarray(decoded["metadata"], np.uint32)
+    want = oracle.tdt_decode(tdt, projected, stack.valid.astype(np.uint32), max_tokens=max_tokens,
+                             starts=np.zeros(windows, np.uint32), ends=np.full(windows, 188, np.uint32),
+                             flush=np.ones(windows, np.uint32))
+    np.testing.assert_array_equal(meta[:windows], want["counts"])
+    np.testing.assert_array_equal(meta[windows:], want["status"])
+    assert want["counts"].sum() > 0
+    for key, name in (("tokens", "tokens"), ("frames", "tokenFrames"), ("durations", "tokenDurations")):
+        got = np.asarray(decoded[name], np.uint32).reshape(windows, max_tokens)
+        for b in range(windows):
+            n = int(want["counts"][b])
+            np.testing.assert_array_equal(got[b, :n], want[key][b, :n], err_msg=f"window {b} {key}")
