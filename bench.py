@@ -40,6 +40,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -67,6 +68,8 @@ def parse_args():
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
+    p.add_argument("--dense-probe", default="", help=argparse.SUPPRESS)
     p.add_argument("--variant", type=int, default=-1, help="force a tile variant (sweeps)")
     return p.parse_args()
 
@@ -74,12 +77,13 @@ def parse_args():
 class Kernel:
     """One fused palette GEMM launch of the step and its bookkeeping."""
 
-    def __init__(self, name, op, flops, nbytes, precision):
+    def __init__(self, name, op, flops, nbytes, precision, shape=None):
         self.name = name
         self.op = op
         self.flops = flops
         self.nbytes = nbytes
         self.precision = precision
+        self.shape = shape  # (M, K, N) of a GEMM launch
         self.times_ms = []
 
     def summary(self):
@@ -111,8 +115,8 @@ def build_ff_block(abi, ctx, keep):
                      label="ff-contract")
     e = ff.expand_case()
     c = ff.contract_case(np.zeros((m, 4096), np.float16))
-    kernels = [Kernel("ff-expand", op1, e.flops, e.algorithmic_bytes(), "f16"),
-               Kernel("ff-contract", op2, c.flops, c.algorithmic_bytes(), "f16")]
+    kernels = [Kernel("ff-expand", op1, e.flops, e.algorithmic_bytes(), "f16", (m, 1024, 4096)),
+               Kernel("ff-contract", op2, c.flops, c.algorithmic_bytes(), "f16", (m, 4096, 1024))]
     config = {"workload": "conformer-ff-block-fp16", "windows": 8, "frames": 188, "rows": m,
               "d_model": 1024, "hidden": 4096, "palette_bits": 5, "epilogues": ["silu", "0.5*residual"]}
     return kernels, config, ff
@@ -127,7 +131,8 @@ def build_single_gemm(abi, ctx, keep):
                     inner=1024, columns=4096, bias=keep(ctx.array(case.bias)), label="single-gemm-fp32")
     config = {"workload": "single-palette-gemm-fp32", "rows": case.rows, "inner": 1024, "columns": 4096,
               "palette_bits": 6, "epilogues": ["bias"]}
-    return [Kernel("single-gemm-fp32", op, case.flops, case.algorithmic_bytes(), "f32")], config, case
+    return [Kernel("single-gemm-fp32", op, case.flops, case.algorithmic_bytes(), "f32", (case.rows, 1024, 4096))], \
+        config, case
 
 
 def build_small_m(abi, ctx, keep, rows):
@@ -139,7 +144,7 @@ def build_small_m(abi, ctx, keep, rows):
                     inner=1024, columns=4096, label=f"small-m-{rows}")
     config = {"workload": "small-m-palette-gemm-fp16", "rows": rows, "inner": 1024, "columns": 4096,
               "palette_bits": 5}
-    return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16")], config, case
+    return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16", (rows, 1024, 4096))], config, case
 
 
 def build_conv_module(abi, ctx, keep, fused_glu=False):
@@ -470,8 +475,14 @@ def run_encoder(args, abi, ctx, decoder=False):
         dispatches[name] = {"avg_us": us, "tflops": flops / (us * 1e-6) / 1e12 if flops else 0.0,
                             "gbs": nbytes / (us * 1e-6) / 1e9, "flops": flops, "algorithmic_bytes": nbytes,
                             "launches_per_pass": len(stack.layers) if name in abi.ENCODER_DISPATCHES else 1}
-    # dominant kernel: the dispatch kind with the most time per pass
-    name = max(dispatches, key=lambda k: dispatches[k]["avg_us"] * dispatches[k]["launches_per_pass"])
+    # dominant kernel: the launch kind with the most time per pass; the two
+    # feed-forward modules' launches of one shape count as one kind
+    def kind(k):
+        return k.replace("feed-forward2-", "feed-forward1-")
+    per_kind = {}
+    for k, d in dispatches.items():
+        per_kind[kind(k)] = per_kind.get(kind(k), 0.0) + d["avg_us"] * d["launches_per_pass"]
+    name = max(per_kind, key=per_kind.get)
     dom = dispatches[name]
     if dom["flops"] / (PEAK_TFLOPS["f16"] * 1e12) >= dom["algorithmic_bytes"] / (PEAK_HBM_GBS * 1e9):
         roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_TFLOPS["f16"], "unit": "TFLOP/s",
@@ -495,6 +506,18 @@ def run_encoder(args, abi, ctx, decoder=False):
         decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:stack.batch]],
                    "overflow_windows": int((meta[stack.batch:] != 0).sum()), "kernel": "tdt_decode_kernel",
                    "workgroups": stack.batch, "max_tokens": 1024}
+    dense = None
+    if not args.no_dense:
+        rows = stack.batch * stack.frames
+        shapes = {"feed-forward1-linear1": (1024, 4096), "feed-forward1-linear2-residual": (4096, 1024),
+                  "self-attention-qkv": (1024, 3072), "convolution-pointwise1": (1024, 2048),
+                  "self-attention-output-residual": (1024, 1024)}
+        probes = []
+        for k, (inner, columns) in shapes.items():
+            probe = Kernel(k, None, 2 * rows * inner * columns, 0, "f16", (rows, inner, columns))
+            probe.times_ms = [dispatches[k]["avg_us"] * 1e-3]
+            probes.append(probe)
+        dense = dense_reference(probes)
     line = {
         "metric": METRIC,
         "value": stack.batch * WINDOW_SECONDS / (ms_per_step * 1e-3),
@@ -521,6 +544,7 @@ def run_encoder(args, abi, ctx, decoder=False):
         "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
         "device_bytes": device_bytes,
         "dispatches": dispatches,
+        "dense_vendor_reference": dense,
         "decoder": decoded,
         "wall_ms_per_step": wall / args.steps * 1e3,
         "device": ctx.info().name.decode(),
@@ -549,8 +573,56 @@ def read_traffic(gemm_name, kernel_name):
     return entry["hbm_bytes_per_launch"]
 
 
+def dense_reference(kernels, reps=100):
+    """The vendor library's dense GEMM (torch.matmul -> hipBLASLt) at each
+    GEMM launch's shape and precision with the weights already dense: what
+    this shape class reaches without palette decoding, a context for the
+    roofline fraction (not the step's work, and not part of `value`). Timed
+    in a child process: torch carries its own HIP runtime, which does not
+    share a process with this library's."""
+    shaped = [k for k in kernels if k.shape is not None]
+    if not shaped:
+        return None
+    request = [{"name": k.name, "shape": list(k.shape), "precision": k.precision} for k in shaped]
+    proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--dense-probe", json.dumps(request),
+                           "--steps", str(reps)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                          timeout=300)
+    if proc.returncode != 0:
+        return {"error": proc.stderr.strip().splitlines()[-1] if proc.stderr.strip() else "failed"}
+    out = json.loads(proc.stdout.strip().splitlines()[-1])
+    for k in shaped:
+        out[k.name]["palette_avg_us"] = float(np.mean(k.times_ms)) * 1e3
+    return out
+
+
+def dense_probe(request, reps):
+    import torch
+    out = {}
+    for item in request:
+        m, kk, n = item["shape"]
+        dtype = torch.float16 if item["precision"] == "f16" else torch.float32
+        a = torch.randn(m, kk, device="cuda", dtype=dtype)
+        b = torch.randn(kk, n, device="cuda", dtype=dtype)
+        for _ in range(10):
+            c = a @ b
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        del a, b, c
+        out[item["name"]] = {"shape": [m, kk, n], "avg_us": us, "tflops": 2.0 * m * kk * n / us / 1e6}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse_args()
+    if args.dense_probe:
+        dense_probe(json.loads(args.dense_probe), args.steps)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the palette path shards by windows with no exchange step)", file=sys.stderr)
@@ -636,6 +708,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.workload, data, args.cpu_sample_rows)
+    dense = None if args.no_dense else dense_reference(kernels)
 
     line = {
         "metric": METRIC,
@@ -654,6 +727,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k.name: k.summary() for k in kernels},
+        "dense_vendor_reference": dense,
         "wall_ms_per_step": wall / args.steps * 1e3,
         "device": ctx.info().name.decode(),
     }

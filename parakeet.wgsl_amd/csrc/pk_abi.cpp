@@ -214,8 +214,9 @@ int find_variant(int precision, int family, int waves_m, int waves_n, int m_bloc
 // candidate with the least (rounds of workgroups) x (measured time of one
 // workgroup), which puts 192 x 128 on the FF expand and convolution PW1,
 // 96 x 128 on 3000-row 1024-wide GEMMs, 64 x 64 on 752 x 1024 and the
-// small-M kernel on the 375-row rel-pos linear. f32 keeps its own
-// smallest-cost shape.
+// small-M kernel on the 375-row rel-pos linear; 96 x 128 also takes shapes
+// whose larger tiles would leave a costly partial round (3000-row QKV).
+// f32 keeps its own smallest-cost shape.
 Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus) {
   if (precision == PK_PRECISION_F16) {
     auto pair_variant = [](int wn, int r, int c, int ks) {
@@ -254,6 +255,18 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
         best_us = rounds * c.us;
         best = v;
       }
+    }
+    // Two 96 x 128 workgroups share a compute unit (their registers and
+    // 54 KB of LDS allow it), so beyond one round that tile runs as a fluid
+    // queue: measured 10.2 us per workgroup per compute unit at K = 1024
+    // (QKV 3008 x 1024 x 3072: 768 tiles in 30.5 us against 36.6 us for
+    // 2 rounds of 192 x 128). It replaces a choice that leaves a partial
+    // round when it is predicted at least 15% faster.
+    const uint64_t t96 = tiles(96, 128);
+    if (t96 > wave) {
+      const double fluid_us = 10.2 * (double)t96 / (double)wave;
+      const int v = pair_variant(2, 3, 2, 2);
+      if (fluid_us < 0.85 * best_us) best = v;
     }
     return {best < 0 ? pair_variant(2, 6, 2, 2) : best, 1u};
   }

@@ -58,15 +58,21 @@ using namespace f16;
 // and zeros up to entry 64; entry 2^bits is the zero of K padding.
 constexpr int kLutStride = 65;
 constexpr uint32_t kLutStrideBytes = 2u * kLutStride;
-// LDS budget of the partial-tile exchange.
-constexpr int kExchangeCap = 96 * 1024;
+// LDS budget of the partial-tile exchange. The 96 x 128 tile (WN = KS = 2,
+// R = 3) keeps one m-block per pass: its registers allow two wavefronts per
+// SIMD, and with a 32 KB exchange two of its workgroups fit one compute
+// unit's LDS, so one workgroup's prologue and epilogue overlap the other's
+// K loop. The planner gives it the shapes with more tiles than compute
+// units. Every other tile runs one workgroup per compute unit and takes
+// the exchange in as few passes as 96 KB allow.
+constexpr int exchange_cap(int wn, int ks, int r) { return wn == 2 && ks == 2 && r == 3 ? 32 * 1024 : 96 * 1024; }
 
 // m-blocks per epilogue pass: the largest divisor of R whose partial tiles
 // fit the exchange budget.
-constexpr int pass_blocks(int r, int block_bytes) {
+constexpr int pass_blocks(int wn, int ks, int r, int block_bytes) {
   int best = 1;
   for (int p = 1; p <= r; ++p)
-    if (r % p == 0 && p * block_bytes <= kExchangeCap) best = p;
+    if (r % p == 0 && p * block_bytes <= exchange_cap(wn, ks, r)) best = p;
   return best;
 }
 
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int A_BYTES = BM * kRowBytes;
   constexpr int CH = BM * 8 / T;  // 16-byte activation chunks per thread per K block
   constexpr int BLOCK_EX = KS * WN * C * 4 * 64 * 16;  // exchange bytes of one m-block
-  constexpr int PM = pass_blocks(R, BLOCK_EX);
+  constexpr int PM = pass_blocks(WN, KS, R, BLOCK_EX);
   constexpr int EX_BYTES = PM * BLOCK_EX;
   constexpr int SMEM = EX_BYTES > 3 * A_BYTES ? EX_BYTES : 3 * A_BYTES;
   constexpr int GROUPS = GENERAL ? BN / 16 + 2 : 1;
@@ -554,7 +560,7 @@ template <int WN, int KS, int R, int C>
 constexpr uint32_t kernel_lds_bytes() {
   constexpr int A_BYTES = 32 * R * kRowBytes;
   constexpr int BLOCK_EX = KS * WN * C * 4 * 64 * 16;
-  constexpr int EX = pass_blocks(R, BLOCK_EX) * BLOCK_EX;
+  constexpr int EX = pass_blocks(WN, KS, R, BLOCK_EX) * BLOCK_EX;
   return (uint32_t)((EX > 3 * A_BYTES ? EX : 3 * A_BYTES) + kLutStride * 2 + 65 * 65 * 4);
 }
 
