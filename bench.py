@@ -504,8 +504,10 @@ def run_encoder(args, abi, ctx, decoder=False):
     if tdt:
         meta = tdt_out["metadata"].download()
         decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:stack.batch]],
-                   "overflow_windows": int((meta[stack.batch:] != 0).sum()), "kernel": "tdt_decode_kernel",
-                   "workgroups": stack.batch, "max_tokens": 1024}
+                   "overflow_windows": int((meta[stack.batch:] != 0).sum()),
+                   "kernel": "tdt_team_kernel" if tdt.team_size() > 1 else "tdt_decode_kernel",
+                   "workgroups_per_window": tdt.team_size(), "workgroups": stack.batch * tdt.team_size(),
+                   "max_tokens": 1024}
     dense = None
     if not args.no_dense:
         rows = stack.batch * stack.frames

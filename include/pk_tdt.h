@@ -34,6 +34,7 @@ extern "C" {
 #define PK_TDT_BLANK_TOKEN 1024
 #define PK_TDT_HEAD_OUTPUTS 1032    /* tokens, blank, 5 durations, 2 padding */
 #define PK_TDT_OVERFLOW 1u
+#define PK_TDT_SYNC_TIMEOUT 2u      /* a team barrier gave up waiting (no reference counterpart) */
 
 typedef struct pk_tdt_op pk_tdt_op;
 
@@ -100,6 +101,14 @@ int pk_tdt_create(pk_context *ctx, const pk_tdt_desc *desc, pk_tdt_op **out);
 int pk_tdt_enqueue(pk_tdt_op *op, uint32_t active_batch, void *stream);
 int pk_tdt_enqueue_timed(pk_tdt_op *op, uint32_t active_batch, void *stream, void *start_event,
                          void *end_event);
+/* No reference counterpart: how many workgroups decode one window. 0
+   chooses (16 or 8 when every workgroup of the batch can be resident
+   together, else 1), 1 runs one workgroup per window, 8 and 16 split
+   every weight matrix over a team that meets at barriers in global memory
+   (a cooperative launch). Results are bit-identical for every size. The
+   create call chooses automatically; the setter synchronizes the device. */
+int pk_tdt_set_team_size(pk_tdt_op *op, uint32_t members);
+int pk_tdt_team_size(const pk_tdt_op *op, uint32_t *members);
 /* Idempotent; enqueue after destroy returns PK_DESTROYED. */
 int pk_tdt_destroy(pk_tdt_op *op);
 int pk_tdt_release(pk_tdt_op *op);

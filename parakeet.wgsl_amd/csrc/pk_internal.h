@@ -288,6 +288,24 @@ struct TdtArgs {
 };
 hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t stream, hipEvent_t start = nullptr,
                              hipEvent_t stop = nullptr);
+// Team decoding: `members` workgroups of kTdtTeamThreads per window, each
+// streaming one slice of every weight matrix, meeting at bounded barriers
+// in global memory; launched cooperatively so every member is resident.
+constexpr uint32_t kTdtTeamThreads = 256;
+constexpr uint32_t kTdtSyncTimeout = 2u;  // status bit: a team barrier gave up waiting
+constexpr uint32_t kTdtSyncStride = 64;   // u32 words between barrier counters (256 bytes)
+struct TdtTeam {
+  uint32_t members;     // 8 or 16
+  uint32_t* sync;       // [2 * capacity * kTdtSyncStride]: counters, then abort flags; zeroed per launch
+  uint32_t* partials;   // [capacity, 2, members, 4]: per-member argmax partials, two buffers
+  uint32_t capacity;    // windows the buffers hold
+  uint32_t spin_limit;  // polls before a barrier gives up
+};
+bool tdt_team_members_supported(uint32_t members);
+// Team workgroups that can be resident at once on `device` (0 if unknown).
+uint32_t tdt_team_capacity(int device);
+hipError_t launch_tdt_team(const TdtArgs& args, const TdtTeam& team, uint32_t batch, hipStream_t stream,
+                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 int conv_variant_count(bool f16);
 ConvGeometry conv_geometry(bool f16, int variant, uint32_t frames, uint32_t channels, uint32_t batch,

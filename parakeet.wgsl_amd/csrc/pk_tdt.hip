@@ -328,6 +328,466 @@ __global__ __launch_bounds__(kTdtThreads) void tdt_decode_kernel(TdtArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------- teams
+//
+// Team decoding spreads one window over P workgroups ("members") of 256
+// threads. Member p owns hidden units [pU, pU + U) (U = 640 / P): the four
+// gate columns of those units in both LSTM layers, the same projector
+// columns, and a range of head quads. Every matrix slice streams through
+// two LDS stages (one chunk of rows in registers while the previous chunk
+// is multiplied), so a member reads 1/P of the weights per step; with the
+// workgroup ids laid out window-major, member p of every window lands on
+// the same XCD (dispatch is round robin over the eight XCDs), whose L2 then
+// holds the slices of its two member indices.
+//
+// The arithmetic is the single-workgroup kernel's, chain for chain: a gate
+// column is still one f16 chain over even rows from f16(bias) and one over
+// odd rows from zero, in increasing k; the projector and head columns are
+// the same f32 and f16 chains; the argmax combines per-member (best value,
+// lowest id) pairs, which selects the same id as one scan. Control state is
+// kept by thread 0 of every member and evolves identically; member 0
+// writes the outputs.
+//
+// Exchange between members goes through the window's state and scratch
+// slices in global memory with relaxed agent-scope atomic loads and stores
+// (coherent across the XCDs' L2s without cache maintenance), ordered by team
+// barriers: every wave's stores complete (workgroup release), then an
+// atomic arrival count and a bounded poll. Agent-scope fences would write
+// back and invalidate the XCD's whole L2 at every barrier, which measured
+// slower than one workgroup per window; the weights, read with ordinary
+// loads, stay cached. A barrier that waits
+// longer than `spin_limit` polls raises the window's abort flag and every
+// member leaves its loop at its next barrier (status kTdtSyncTimeout), so
+// every wave reaches the end. The launch is cooperative, so all members of
+// every window are resident together.
+
+constexpr uint32_t TT = kTdtTeamThreads;
+
+// Exchanged values: relaxed agent-scope atomics, coherent between XCDs.
+__device__ __forceinline__ float xload(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xstore(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t xload(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xstore(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr uint32_t kStageUnits = 6400;  // half4 units per staged chunk (51,200 bytes)
+
+struct TeamShared {
+  half4 stage[2][kStageUnits];
+  _Float16 x[2 * H];
+  float vec[H];
+  float gates[4 * 80];
+  half4 odd[80];
+  float scores[33 * 4];
+  uint32_t go, emitted, token, duration, joint_time, failed;
+};
+
+struct Slice {
+  const _Float16* base;  // matrix
+  uint32_t stride;       // halves per row
+  uint32_t quads;        // half4 units per row of the slice
+  uint32_t seg_quads;    // quads per segment (segments are `seg_stride` columns apart)
+  uint32_t seg_stride;
+  uint32_t col0;         // first column of segment 0
+  uint32_t rows;         // rows per chunk
+};
+
+constexpr uint32_t kUnitsPerThread = kStageUnits / TT;  // 25
+
+// Element offsets (relative to row 0) of this thread's units of a chunk,
+// the same for every chunk of the slice; ~0u past the chunk's units.
+__device__ __forceinline__ void slice_offsets(const Slice& sl, uint32_t (&off)[kUnitsPerThread]) {
+  const uint32_t units = sl.rows * sl.quads;
+  uint32_t r = threadIdx.x / sl.quads, q = threadIdx.x % sl.quads;
+  const uint32_t dr = TT / sl.quads, dq = TT % sl.quads;
+#pragma unroll
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+    const uint32_t u = threadIdx.x + i * TT;
+    off[i] = u < units ? r * sl.stride + sl.col0 + (q / sl.seg_quads) * sl.seg_stride + (q % sl.seg_quads) * 4u
+                       : ~0u;
+    q += dq;
+    r += dr;
+    if (q >= sl.quads) {
+      q -= sl.quads;
+      r += 1;
+    }
+  }
+}
+
+__device__ __forceinline__ void stage_load(const Slice& sl, uint32_t k0, const uint32_t (&off)[kUnitsPerThread],
+                                           half4 (&reg)[kUnitsPerThread]) {
+  const _Float16* base = sl.base + (uint64_t)k0 * sl.stride;
+#pragma unroll
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i)
+    if (off[i] != ~0u) reg[i] = load_half4(base + off[i]);
+}
+
+__device__ __forceinline__ void stage_store(half4* dst, const uint32_t (&off)[kUnitsPerThread],
+                                            const half4 (&reg)[kUnitsPerThread]) {
+#pragma unroll
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i)
+    if (off[i] != ~0u) dst[threadIdx.x + i * TT] = reg[i];
+}
+
+// Streams rows [0, limit) of the slice through the two stages and calls
+// body(stage, k0) for every chunk (all threads, after a barrier).
+template <class Body>
+__device__ void stream_slice(TeamShared& s, const Slice& sl, uint32_t limit, Body body) {
+  const uint32_t chunks = limit / sl.rows;
+  if (chunks == 0) return;
+  uint32_t off[kUnitsPerThread];
+  slice_offsets(sl, off);
+  half4 reg[kUnitsPerThread];
+  stage_load(sl, 0, off, reg);
+  for (uint32_t c = 0; c < chunks; ++c) {
+    half4* cur = s.stage[c & 1u];
+    stage_store(cur, off, reg);
+    __syncthreads();
+    if (c + 1 < chunks) stage_load(sl, (c + 1) * sl.rows, off, reg);
+    body(cur, c * sl.rows);
+  }
+  __syncthreads();
+}
+
+// One team barrier: the n-th barrier of a window waits for count >= P * n.
+__device__ bool team_barrier(TeamShared& s, const TdtTeam& tm, uint32_t b, uint32_t& n) {
+  ++n;
+  // every wave waits for its exchanged (coherent) stores to complete before
+  // the arrival; a workgroup barrier alone does not wait for them
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // one 256-byte line per counter and per flag: the windows' teams poll
+    // their own lines, never a shared one
+    uint32_t* counter = tm.sync + (uint64_t)b * kTdtSyncStride;
+    uint32_t* abort = tm.sync + ((uint64_t)tm.capacity + b) * kTdtSyncStride;
+    uint32_t failed = 0;
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t target = tm.members * n;
+    uint32_t polls = 0;
+    while (xload(counter) < target) {
+      if (xload(abort) != 0u) {
+        failed = 1;
+        break;
+      }
+      if (++polls > tm.spin_limit) {
+        __hip_atomic_fetch_or(abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        failed = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    s.failed = failed;
+  }
+  __syncthreads();
+  return s.failed == 0;
+}
+
+// Gates of this member's units in one LSTM layer, then their cell update:
+// h and c of units [u0, u0 + U) to h_out / c_out.
+__device__ void team_lstm(TeamShared& s, const _Float16* weight, const float* bias, uint32_t limit, uint32_t u0,
+                          uint32_t U, const float* c_prev, float* h_out, float* c_out) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t Q = U;  // U / 4 quads in each of the four gate segments
+  const Slice sl{weight, kTdtGates, Q, U / 4, H, u0, kStageUnits / Q};
+  const uint32_t parity = t / Q, q = t % Q;
+  const bool chain = t < 2 * Q;
+  const uint32_t col = (q / (U / 4)) * H + u0 + (q % (U / 4)) * 4;
+  half4 acc = half4{0, 0, 0, 0};
+  if (chain && parity == 0) {
+    const float4 bb = *reinterpret_cast<const float4*>(bias + col);
+    acc = half4{(_Float16)bb.x, (_Float16)bb.y, (_Float16)bb.z, (_Float16)bb.w};
+  }
+  stream_slice(s, sl, limit, [&](const half4* st, uint32_t k0) {
+    if (chain) {
+      // rows come in batches of 16 (chunks hold 80 or 160 rows): the 8 rows
+      // of this parity are read from LDS before the dependent chain runs
+      for (uint32_t r0 = 0; r0 < sl.rows; r0 += 16) {
+        half4 w[8];
+        _Float16 x[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+          const uint32_t r = r0 + 2 * i + parity;
+          w[i] = st[r * Q + q];
+          x[i] = s.x[k0 + r];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) acc = __builtin_elementwise_fma(splat(x[i]), w[i], acc);
+      }
+    }
+  });
+  if (chain && parity == 1) s.odd[q] = acc;
+  __syncthreads();
+  if (chain && parity == 0) {
+    const half4 sum = acc + s.odd[q];
+    for (int i = 0; i < 4; ++i) s.gates[4 * q + i] = (float)sum[i];
+  }
+  __syncthreads();
+  if (t < U) {
+    // unit j's gate g sits at quad g * U / 4 + j / 4, lane j % 4: index g * U + j
+    const uint32_t ch = u0 + t;
+    const float ig = sigmoid_f32(s.gates[t]);
+    const float fg = sigmoid_f32(s.gates[U + t]);
+    const float gg = clamped_tanh(s.gates[2 * U + t]);
+    const float og = sigmoid_f32(s.gates[3 * U + t]);
+    const float cell = __builtin_fmaf(fg, xload(c_prev + ch), ig * gg);
+    xstore(c_out + ch, cell);
+    xstore(h_out + ch, og * clamped_tanh(cell));
+  }
+}
+
+// prepare_predictor with this member's slices; three team barriers.
+__device__ bool team_predictor(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, uint32_t b, uint32_t& n,
+                               const float* state, float* cand, uint32_t token, bool initial, uint32_t u0,
+                               uint32_t U) {
+  const uint32_t t = threadIdx.x;
+  for (uint32_t k = t; k < H; k += TT) {
+    s.x[k] = initial ? (_Float16)0.0f : a.embedding[(uint64_t)token * H + k];
+    s.x[H + k] = (_Float16)xload(state + k);
+  }
+  __syncthreads();
+  team_lstm(s, a.lstm[0], a.lstm_bias[0], initial ? 0u : 2 * H, u0, U, state + H, cand, cand + H);
+  if (!team_barrier(s, tm, b, n)) return false;
+  for (uint32_t k = t; k < H; k += TT) {
+    s.x[k] = (_Float16)xload(cand + k);
+    s.x[H + k] = (_Float16)xload(state + 2 * H + k);
+  }
+  __syncthreads();
+  team_lstm(s, a.lstm[1], a.lstm_bias[1], initial ? H : 2 * H, u0, U, state + 3 * H, cand + 2 * H, cand + 3 * H);
+  if (!team_barrier(s, tm, b, n)) return false;
+  // decoder projector columns [u0, u0 + U): f32 fma chain over k
+  for (uint32_t k = t; k < H; k += TT) s.vec[k] = xload(cand + 2 * H + k);
+  const Slice sl{a.projector, H, U / 4, U / 4, 0, u0, kStageUnits / (U / 4)};
+  float acc = 0.0f;
+  if (t < U) acc = a.projector_bias[u0 + t];
+  stream_slice(s, sl, H, [&](const half4* st, uint32_t k0) {
+    if (t < U) {
+      for (uint32_t r0 = 0; r0 < sl.rows; r0 += 16) {
+        float w[16], h[16];
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+          w[i] = (float)st[(r0 + i) * (U / 4) + t / 4][t % 4];
+          h[i] = s.vec[k0 + r0 + i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) acc = __builtin_fmaf(h[i], w[i], acc);
+      }
+    }
+  });
+  if (t < U) xstore(cand + 4 * H + u0 + t, acc);
+  return team_barrier(s, tm, b, n);
+}
+
+// The joint over this member's head quads [hq0, hq1) and the team argmax:
+// s.token, s.duration.
+__device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, uint32_t b, uint32_t& n,
+                           uint32_t p, uint32_t buf, const _Float16* encoder_row, const float* projection,
+                           uint32_t hq0, uint32_t hq1) {
+  const uint32_t t = threadIdx.x;
+  for (uint32_t c = t; c < H; c += TT) {
+    const float v = (float)encoder_row[c] + xload(projection + c);
+    s.vec[c] = v > 0.0f ? v : 0.0f;
+  }
+  const uint32_t HQ = hq1 - hq0;  // at most 17 (16 members) or 33 (8 members)
+  const Slice sl{a.head, kTdtHead, HQ, HQ, 0, hq0 * 4, HQ * 320 <= kStageUnits ? 320u : 160u};
+  half4 acc = half4{0, 0, 0, 0};
+  if (t < HQ) {
+    const float4 bb = *reinterpret_cast<const float4*>(a.head_bias + 4 * (hq0 + t));
+    acc = half4{(_Float16)bb.x, (_Float16)bb.y, (_Float16)bb.z, (_Float16)bb.w};
+  }
+  bool zero_skip_safe = true;
+  __syncthreads();
+  stream_slice(s, sl, H, [&](const half4* st, uint32_t k0) {
+    if (t < HQ) {
+      for (uint32_t r0 = 0; r0 < sl.rows; r0 += 16) {
+        half4 w[16];
+        float xs[16];
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+          w[i] = st[(r0 + i) * HQ + t];
+          xs[i] = s.vec[k0 + r0 + i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+          const float x = xs[i];
+          const uint32_t bits = __float_as_uint(x);
+          const bool is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
+          zero_skip_safe = zero_skip_safe && !(bits == 0x80000000u || is_nan);
+          if (!(zero_skip_safe && bits == 0u)) acc = __builtin_elementwise_fma(splat((_Float16)x), w[i], acc);
+        }
+      }
+    }
+  });
+  if (t < HQ)
+    for (int i = 0; i < 4; ++i) s.scores[4 * t + i] = (float)acc[i];
+  __syncthreads();
+  uint32_t* part = tm.partials + (((uint64_t)b * 2 + buf) * tm.members) * 4;
+  if (t == 0) {
+    // this member's best token (value, lowest id) and best duration
+    float best = -3.402823466e+38f, dbest = -3.402823466e+38f;
+    uint32_t id = 0xffffffffu, d = 0xffffffffu;
+    for (uint32_t i = 0; i < 4 * HQ; ++i) {
+      const uint32_t o = 4 * hq0 + i;
+      float v = s.scores[i];
+      v = v != v ? -3.402823466e+38f : v;
+      if (o <= kTdtBlank) {
+        if (v > best || (v == best && o < id)) {
+          best = v;
+          id = o;
+        }
+      } else if (o <= kTdtBlank + 5) {
+        const uint32_t j = o - kTdtBlank - 1;
+        if (v > dbest || (v == dbest && j < d)) {
+          dbest = v;
+          d = j;
+        }
+      }
+    }
+    xstore(part + 4 * p + 0, __float_as_uint(best));
+    xstore(part + 4 * p + 1, id);
+    xstore(part + 4 * p + 2, __float_as_uint(dbest));
+    xstore(part + 4 * p + 3, d);
+  }
+  if (!team_barrier(s, tm, b, n)) return false;
+  if (t == 0) {
+    float best = -3.402823466e+38f, dbest = -3.402823466e+38f;
+    uint32_t id = 0xffffffffu, d = 0xffffffffu;
+    for (uint32_t m = 0; m < tm.members; ++m) {
+      const float v = __uint_as_float(xload(part + 4 * m + 0));
+      const uint32_t o = xload(part + 4 * m + 1);
+      if (o != 0xffffffffu && (v > best || (v == best && o < id))) {
+        best = v;
+        id = o;
+      }
+      const float dv = __uint_as_float(xload(part + 4 * m + 2));
+      const uint32_t j = xload(part + 4 * m + 3);
+      if (j != 0xffffffffu && (dv > dbest || (dv == dbest && j < d))) {
+        dbest = dv;
+        d = j;
+      }
+    }
+    s.token = id;
+    s.duration = d;
+  }
+  __syncthreads();
+  return true;
+}
+
+__global__ __launch_bounds__(kTdtTeamThreads) void tdt_team_kernel(TdtArgs a, TdtTeam tm) {
+  __shared__ TeamShared s;
+  const uint32_t P = tm.members;
+  const uint32_t b = blockIdx.x / P, p = blockIdx.x % P, t = threadIdx.x;
+  const uint32_t U = H / P, u0 = p * U;
+  const uint32_t hq0 = p * (kTdtHead / 4) / P, hq1 = (p + 1) * (kTdtHead / 4) / P;
+  float* state = a.state + (uint64_t)b * 4 * H;
+  float* cand = a.scratch + (uint64_t)b * 5 * H;
+  const _Float16* encoder = a.encoder + (uint64_t)b * a.frames * H;
+  uint32_t n = 0;  // team barriers passed
+  for (uint32_t i = t; i < U; i += TT)
+    for (uint32_t j = 0; j < 4; ++j) xstore(state + j * H + u0 + i, 0.0f);
+
+  const uint32_t limit = min(a.lengths[b], a.frames);
+  const uint32_t encoded = min(limit, a.ends[b]);
+  uint32_t time = min(a.starts[b], encoded), count = 0, st = 0, symbols = 0;
+  bool flushing = false;
+  uint32_t flush_blanks = 0, flush_time = 0, joints = 0;
+  const bool flush_requested = a.flush[b] != 0 && a.starts[b] < encoded;
+  bool alive = team_barrier(s, tm, b, n);
+  if (alive && time < encoded) alive = team_predictor(s, a, tm, b, n, state, cand, 0, true, u0, U);
+
+  const uint32_t max_steps = 11 * a.frames + 32;
+  for (uint32_t step = 0; alive && step < max_steps; ++step) {
+    if (t == 0) {
+      s.go = 0;
+      if (!flushing && time < encoded) {
+        s.go = 1;
+        s.joint_time = time;
+      } else {
+        if (!flushing && flush_requested) {
+          flushing = true;
+          symbols = 0;
+          flush_blanks = 0;
+          flush_time = time;
+        }
+        if (flushing && symbols < 10 && flush_blanks < 5) {
+          const uint32_t variation = symbols % 3;
+          if (variation == 0)
+            time = min(flush_time, limit - 1u);
+          else if (variation == 1)
+            time = min(encoded - 1u, a.frames - 1u);
+          else
+            time = min(max(encoded, 2u) - 2u, a.frames - 1u);
+          s.go = 1;
+          s.joint_time = time;
+        }
+      }
+    }
+    __syncthreads();
+    if (!s.go) break;
+    alive = team_joint(s, a, tm, b, n, p, joints & 1u, encoder + (uint64_t)s.joint_time * H, cand + 4 * H, hq0,
+                       hq1);
+    ++joints;
+    if (!alive) break;
+    if (t == 0) {
+      const uint32_t token = s.token, duration = s.duration;
+      const bool emitted = token != kTdtBlank;
+      const uint32_t frame = flushing ? min(flush_time, encoded - 1u) : time;
+      if (emitted) {
+        if (count < a.max_tokens) {
+          if (p == 0) {
+            const uint64_t at = (uint64_t)b * a.max_tokens + count;
+            a.tokens[at] = token;
+            a.token_frames[at] = frame;
+            a.token_durations[at] = duration;
+          }
+          ++count;
+        } else {
+          st |= 1u;
+        }
+      }
+      if (!flushing) {
+        symbols += 1;
+        if (duration != 0) {
+          time += duration;
+          symbols = 0;
+        } else if (!emitted || symbols >= 10) {
+          time += 1;
+          symbols = 0;
+        }
+      } else {
+        flush_blanks = emitted ? 0u : flush_blanks + 1u;
+        flush_time = min(flush_time + max(1u, duration), encoded);
+        symbols += 1;
+      }
+      s.emitted = emitted;
+    }
+    __syncthreads();
+    if (s.emitted) {
+      // commit_predictor: this member's units
+      for (uint32_t i = t; i < U; i += TT)
+        for (uint32_t j = 0; j < 4; ++j) xstore(state + j * H + u0 + i, xload(cand + j * H + u0 + i));
+      alive = team_barrier(s, tm, b, n);
+      if (alive) alive = team_predictor(s, a, tm, b, n, state, cand, s.token, false, u0, U);
+    }
+  }
+  if (t == 0 && p == 0) {
+    a.counts[b] = count;
+    a.status[b] = st | (alive ? 0u : kTdtSyncTimeout);
+  }
+}
+
+__global__ void tdt_team_clear(uint32_t* sync, uint32_t words) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < words) sync[i] = 0u;
+}
+
 }  // namespace
 
 hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t stream, hipEvent_t start,
@@ -338,6 +798,36 @@ hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t st
   else
     hipLaunchKernelGGL(tdt_decode_kernel, dim3(batch), dim3(kTdtThreads), 0, stream, args);
   return hipGetLastError();
+}
+
+
+bool tdt_team_members_supported(uint32_t members) { return members == 8 || members == 16; }
+
+uint32_t tdt_team_capacity(int device) {
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(tdt_team_kernel),
+                                                   kTdtTeamThreads, 0) != hipSuccess)
+    return 0;
+  return (uint32_t)(cus * per_cu);
+}
+
+hipError_t launch_tdt_team(const TdtArgs& args, const TdtTeam& team, uint32_t batch, hipStream_t stream,
+                           hipEvent_t start, hipEvent_t stop) {
+  if (batch == 0) return hipSuccess;
+  const uint32_t words = 2 * team.capacity * kTdtSyncStride;
+  hipLaunchKernelGGL(tdt_team_clear, dim3((words + 255) / 256), dim3(256), 0, stream, team.sync, words);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (start && (e = hipEventRecord(start, stream)) != hipSuccess) return e;
+  TdtArgs a = args;
+  TdtTeam tm = team;
+  void* params[] = {&a, &tm};
+  e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(tdt_team_kernel), dim3(batch * team.members),
+                                 dim3(kTdtTeamThreads), params, 0, stream);
+  if (e != hipSuccess) return e;
+  if (stop) e = hipEventRecord(stop, stream);
+  return e;
 }
 
 }  // namespace pk

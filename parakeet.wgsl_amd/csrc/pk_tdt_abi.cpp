@@ -16,6 +16,8 @@ struct pk_tdt_op {
   std::string label;
   uint32_t batch = 0;
   pk::TdtArgs args{};
+  pk::TdtTeam team{};   // members == 0: one workgroup per window
+  uint32_t* team_memory = nullptr;
   bool destroyed = false;
 };
 
@@ -82,6 +84,39 @@ int validate(const pk_tdt_desc* d) {
   return PK_OK;
 }
 
+// Team size of a batch: the largest supported size whose workgroups can all
+// be resident at once (0: one workgroup per window).
+uint32_t choose_members(int device, uint32_t batch) {
+  const uint32_t capacity = pk::tdt_team_capacity(device);
+  for (uint32_t m : {16u, 8u})
+    if ((uint64_t)batch * m <= capacity) return m;
+  return 0;
+}
+
+void free_team(pk_tdt_op* op) {
+  if (op->team_memory) (void)hipFree(op->team_memory);
+  op->team_memory = nullptr;
+  op->team = pk::TdtTeam{};
+}
+
+int set_team(pk_tdt_op* op, uint32_t members) {
+  free_team(op);
+  if (members == 0) return PK_OK;
+  const uint64_t sync_words = 2ull * op->batch * pk::kTdtSyncStride;
+  const uint64_t words = sync_words + (uint64_t)op->batch * 2 * members * 4;
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  const hipError_t e = hipMalloc(reinterpret_cast<void**>(&op->team_memory), words * 4);
+  if (e != hipSuccess)
+    return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate the decoder's team buffers: %s", op->label.c_str(),
+                hipGetErrorString(e));
+  op->team.members = members;
+  op->team.sync = op->team_memory;
+  op->team.partials = op->team_memory + sync_words;
+  op->team.capacity = op->batch;
+  op->team.spin_limit = 1u << 24;
+  return PK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -131,7 +166,32 @@ int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
   a.status = d->metadata + d->batch_size;
   a.frames = d->frames;
   a.max_tokens = d->max_tokens;
+  if (int st = set_team(op, choose_members(ctx->device, op->batch))) {
+    delete op;
+    return st;
+  }
   *out = op;
+  return ok();
+}
+
+int pk_tdt_set_team_size(pk_tdt_op* op, uint32_t members) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "TDT decoder op is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  if (members == 0) members = choose_members(op->ctx->device, op->batch);
+  else if (members == 1) members = 0;
+  else if (!pk::tdt_team_members_supported(members))
+    return fail(PK_RANGE_ERROR, "%s team size must be 0, 1, 8 or 16", op->label.c_str());
+  else if ((uint64_t)op->batch * members > pk::tdt_team_capacity(op->ctx->device))
+    return fail(PK_RANGE_ERROR, "%s: %u windows x %u workgroups cannot be resident together", op->label.c_str(),
+                op->batch, members);
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  PK_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return set_team(op, members);
+}
+
+int pk_tdt_team_size(const pk_tdt_op* op, uint32_t* members) {
+  if (!op || !members) return fail(PK_INVALID_ARGUMENT, "TDT decoder op or output is null");
+  *members = op->team.members ? op->team.members : 1u;
   return ok();
 }
 
@@ -147,8 +207,18 @@ int pk_tdt_enqueue_timed(pk_tdt_op* op, uint32_t active_batch, void* stream, voi
   if (batch > op->batch)
     return fail(PK_RANGE_ERROR, "%s active batch must be in [1, %u]", op->label.c_str(), op->batch);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
-  PK_HIP(pk::launch_tdt_decode(op->args, batch, stream_or_default(op->ctx, stream),
-                               static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(end_event)),
+  const hipStream_t s = stream_or_default(op->ctx, stream);
+  if (op->team.members) {
+    const hipError_t e = pk::launch_tdt_team(op->args, op->team, batch, s, static_cast<hipEvent_t>(start_event),
+                                             static_cast<hipEvent_t>(end_event));
+    if (e == hipSuccess) return ok();
+    // A stream or process where the cooperative launch is refused decodes
+    // with one workgroup per window from here on (same results).
+    (void)hipGetLastError();
+    free_team(op);
+  }
+  PK_HIP(pk::launch_tdt_decode(op->args, batch, s, static_cast<hipEvent_t>(start_event),
+                               static_cast<hipEvent_t>(end_event)),
          "TDT decoder launch");
   return ok();
 }
@@ -162,6 +232,11 @@ int pk_tdt_destroy(pk_tdt_op* op) {
 int pk_tdt_release(pk_tdt_op* op) {
   if (!op) return ok();
   pk_tdt_destroy(op);
+  if (op->team_memory) {
+    (void)hipSetDevice(op->ctx->device);
+    (void)hipDeviceSynchronize();
+  }
+  free_team(op);
   delete op;
   return ok();
 }

@@ -506,6 +506,8 @@ SIGNATURES = {
     "pk_tdt_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
     "pk_tdt_destroy": (ctypes.c_int, [_VP]),
     "pk_tdt_release": (ctypes.c_int, [_VP]),
+    "pk_tdt_set_team_size": (ctypes.c_int, [_VP, ctypes.c_uint32]),
+    "pk_tdt_team_size": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32)]),
     "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
     "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
     "pk_encoder_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, ctypes.c_int]),
@@ -1105,6 +1107,15 @@ class TdtDecoderOp:
         else:
             check(load().pk_tdt_enqueue_timed(self.handle, active_batch, stream,
                                               start.handle if start else None, end.handle if end else None))
+
+    def set_team_size(self, members: int) -> None:
+        """0 chooses, 1 runs one workgroup per window, 8 / 16 split each window over a team."""
+        check(load().pk_tdt_set_team_size(self.handle, members))
+
+    def team_size(self) -> int:
+        out = ctypes.c_uint32()
+        check(load().pk_tdt_team_size(self.handle, ctypes.byref(out)))
+        return out.value
 
     def destroy(self) -> None:
         check(load().pk_tdt_destroy(self.handle))

@@ -1,5 +1,6 @@
 """Parity of the greedy TDT decoder (PersistentTdtDecoderKernel,
-src/webgpu/kernels/tdt-decoder.ts:1133-2010) against the oracle.
+src/webgpu/kernels/tdt-decoder.ts:1133-2010) against the oracle, for one
+workgroup per window and for teams of 8 and 16 workgroups per window.
 
 The kernel evaluates every quantity with the oracle's arithmetic (f16 gate
 and head chains with one rounding per fma in increasing k, f32 cell update,
@@ -21,7 +22,7 @@ def scope(ctx):
     s.close()
 
 
-def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADBEEF):
+def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADBEEF, team=None):
     B, T = case.batch, case.frames
     weights = {k: scope.put(case.weights[k]) for k in abi.TDT_WEIGHT_NAMES}
     outs = {k: scope.put(np.full((B, max_tokens), sentinel, np.uint32)) for k in ("tokens", "frames", "durations")}
@@ -35,6 +36,9 @@ def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADB
                           token_durations=outs["durations"], metadata=metadata, batch_size=B, frames=T,
                           max_tokens=max_tokens)
     try:
+        if team is not None:
+            op.set_team_size(team)
+        print("decoder team", op.team_size(), "batch", B, "frames", T, flush=True)
         op.enqueue(active)
         ctx.synchronize()
     finally:
@@ -60,14 +64,15 @@ def assert_same_decode(got, want, batch):
             np.testing.assert_array_equal(got[key][b, :n], want[key][b, :n], err_msg=f"window {b} {key}")
 
 
+@pytest.mark.parametrize("team", [1, 8, 16], ids=["single", "team8", "team16"])
 @pytest.mark.parametrize("blank_bias", [2.0, 0.0], ids=["blank-favoured", "token-heavy"])
-def test_decoder_matches_oracle_bit_exact(abi, ctx, scope, oracle, workloads, blank_bias):
+def test_decoder_matches_oracle_bit_exact(abi, ctx, scope, oracle, workloads, blank_bias, team):
     """Three windows: a full one with the flush, a bounded [5, 90) one and a
     one-frame window with the flush; with a blank-favoured head and with a
     head that emits at nearly every step (predictor after every joint)."""
     case = workloads.tdt_case(1, 3, 188, lengths=[188, 101, 1], starts=[0, 5, 0], ends=[188, 90, 188],
                               flush=[1, 0, 1], blank_bias=blank_bias)
-    got = run_decoder(abi, scope, ctx, case, 512)
+    got = run_decoder(abi, scope, ctx, case, 512, team=team)
     want = oracle_decode(oracle, case, 512)
     print("counts", got["counts"], "oracle", want["counts"], flush=True)
     assert_same_decode(got, want, 3)
@@ -84,25 +89,28 @@ def test_decoder_overflow_and_closed_form(abi, ctx, scope, oracle, workloads):
     case.weights["head_bias"][:] = 0
     case.weights["head_bias"][7] = 5.0
     case.weights["head_bias"][1025 + 2] = 3.0
-    got = run_decoder(abi, scope, ctx, case, 16)
-    assert list(got["counts"]) == [16, 12] and list(got["status"]) == [1, 0]
+    for team in (1, 16):
+        got = run_decoder(abi, scope, ctx, case, 16, team=team)
+        assert list(got["counts"]) == [16, 12] and list(got["status"]) == [1, 0]
     assert list(got["frames"][0, :16]) == list(range(0, 32, 2))
     assert (got["tokens"][1, :12] == 7).all() and (got["durations"][1, :12] == 2).all()
     assert_same_decode(got, oracle_decode(oracle, case, 16), 2)
 
 
-def test_decoder_full_size_and_active_prefix(abi, ctx, scope, oracle, workloads):
+@pytest.mark.parametrize("team", [0, 1], ids=["chosen", "single"])
+def test_decoder_full_size_and_active_prefix(abi, ctx, scope, oracle, workloads, team):
     """16 windows x 188 frames, ragged lengths, flush on half of them, bit-exact
-    against the oracle; an active prefix of 5 leaves the other windows'
-    outputs untouched."""
+    against the oracle with the team the op chooses (16 workgroups per window
+    on a 256-CU MI355X) and with one workgroup per window; an active prefix
+    of 5 leaves the other windows' outputs untouched."""
     case = workloads.tdt_case(3, 16, 188, flush=[1, 0] * 8)
-    got = run_decoder(abi, scope, ctx, case, 1024)
+    got = run_decoder(abi, scope, ctx, case, 1024, team=team)
     want = oracle_decode(oracle, case, 1024)
     print("counts", got["counts"], flush=True)
     assert_same_decode(got, want, 16)
     np.testing.assert_array_equal(got["state"].view(np.uint32), want["state"].view(np.uint32))
     np.testing.assert_array_equal(got["scratch"].view(np.uint32), want["scratch"].view(np.uint32))
-    prefix = run_decoder(abi, scope, ctx, case, 1024, active=5)
+    prefix = run_decoder(abi, scope, ctx, case, 1024, active=5, team=team)
     np.testing.assert_array_equal(prefix["counts"][:5], want["counts"][:5])
     for b in range(5):
         n = int(want["counts"][b])
@@ -123,6 +131,9 @@ def test_decoder_dispatch_errors(abi, ctx, scope, workloads):
     try:
         with pytest.raises(abi.PaletteRangeError, match=r"tdt-errors active batch must be in \[1, 2\]"):
             op.enqueue(3)
+        with pytest.raises(abi.PaletteRangeError, match="tdt-errors team size must be 0, 1, 8 or 16"):
+            op.set_team_size(4)
+        assert op.team_size() == 16
         op.destroy()
         op.destroy()
         with pytest.raises(abi.PaletteError, match="tdt-errors was destroyed"):
