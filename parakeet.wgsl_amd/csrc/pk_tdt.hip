@@ -386,7 +386,9 @@ struct TeamShared {
   float gates[4 * 80];
   half4 odd[80];
   float scores[33 * 4];
-  uint32_t go, emitted, token, duration, joint_time, failed;
+  uint32_t part[16 * 4];
+  bool use[H];
+  uint32_t go, emitted, token, duration, joint_time, failed, first_bad;
 };
 
 struct Slice {
@@ -411,7 +413,7 @@ __device__ __forceinline__ void slice_offsets(const Slice& sl, uint32_t (&off)[k
   for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
     const uint32_t u = threadIdx.x + i * TT;
     off[i] = u < units ? r * sl.stride + sl.col0 + (q / sl.seg_quads) * sl.seg_stride + (q % sl.seg_quads) * 4u
-                       : ~0u;
+                       : ~0u;  // past the chunk: loads row 0's first quad, never stored
     q += dq;
     r += dr;
     if (q >= sl.quads) {
@@ -424,9 +426,9 @@ __device__ __forceinline__ void slice_offsets(const Slice& sl, uint32_t (&off)[k
 __device__ __forceinline__ void stage_load(const Slice& sl, uint32_t k0, const uint32_t (&off)[kUnitsPerThread],
                                            half4 (&reg)[kUnitsPerThread]) {
   const _Float16* base = sl.base + (uint64_t)k0 * sl.stride;
+  // unconditional, so all of a thread's loads issue back to back
 #pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i)
-    if (off[i] != ~0u) reg[i] = load_half4(base + off[i]);
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i) reg[i] = load_half4(base + (off[i] == ~0u ? 0u : off[i]));
 }
 
 __device__ __forceinline__ void stage_store(half4* dst, const uint32_t (&off)[kUnitsPerThread],
@@ -456,6 +458,30 @@ __device__ void stream_slice(TeamShared& s, const Slice& sl, uint32_t limit, Bod
   __syncthreads();
 }
 
+// dst[k] = src[k] for k < H (exchanged values): a thread's three loads are
+// issued before any is used.
+__device__ __forceinline__ void load_exchanged(float* dst, const float* src) {
+  const uint32_t t = threadIdx.x;
+  float v[3];
+#pragma unroll
+  for (uint32_t i = 0; i < 3; ++i)
+    if (t + i * TT < H) v[i] = xload(src + t + i * TT);
+#pragma unroll
+  for (uint32_t i = 0; i < 3; ++i)
+    if (t + i * TT < H) dst[t + i * TT] = v[i];
+}
+
+__device__ __forceinline__ void load_exchanged_f16(_Float16* dst, const float* src) {
+  const uint32_t t = threadIdx.x;
+  float v[3];
+#pragma unroll
+  for (uint32_t i = 0; i < 3; ++i)
+    if (t + i * TT < H) v[i] = xload(src + t + i * TT);
+#pragma unroll
+  for (uint32_t i = 0; i < 3; ++i)
+    if (t + i * TT < H) dst[t + i * TT] = (_Float16)v[i];
+}
+
 // One team barrier: the n-th barrier of a window waits for count >= P * n.
 __device__ bool team_barrier(TeamShared& s, const TdtTeam& tm, uint32_t b, uint32_t& n) {
   ++n;
@@ -473,7 +499,7 @@ __device__ bool team_barrier(TeamShared& s, const TdtTeam& tm, uint32_t b, uint3
     const uint32_t target = tm.members * n;
     uint32_t polls = 0;
     while (xload(counter) < target) {
-      if (xload(abort) != 0u) {
+      if ((polls & 31u) == 31u && xload(abort) != 0u) {
         failed = 1;
         break;
       }
@@ -548,22 +574,18 @@ __device__ bool team_predictor(TeamShared& s, const TdtArgs& a, const TdtTeam& t
                                const float* state, float* cand, uint32_t token, bool initial, uint32_t u0,
                                uint32_t U) {
   const uint32_t t = threadIdx.x;
-  for (uint32_t k = t; k < H; k += TT) {
-    s.x[k] = initial ? (_Float16)0.0f : a.embedding[(uint64_t)token * H + k];
-    s.x[H + k] = (_Float16)xload(state + k);
-  }
+  for (uint32_t k = t; k < H; k += TT) s.x[k] = initial ? (_Float16)0.0f : a.embedding[(uint64_t)token * H + k];
+  load_exchanged_f16(s.x + H, state);
   __syncthreads();
   team_lstm(s, a.lstm[0], a.lstm_bias[0], initial ? 0u : 2 * H, u0, U, state + H, cand, cand + H);
   if (!team_barrier(s, tm, b, n)) return false;
-  for (uint32_t k = t; k < H; k += TT) {
-    s.x[k] = (_Float16)xload(cand + k);
-    s.x[H + k] = (_Float16)xload(state + 2 * H + k);
-  }
+  load_exchanged_f16(s.x, cand);
+  load_exchanged_f16(s.x + H, state + 2 * H);
   __syncthreads();
   team_lstm(s, a.lstm[1], a.lstm_bias[1], initial ? H : 2 * H, u0, U, state + 3 * H, cand + 2 * H, cand + 3 * H);
   if (!team_barrier(s, tm, b, n)) return false;
   // decoder projector columns [u0, u0 + U): f32 fma chain over k
-  for (uint32_t k = t; k < H; k += TT) s.vec[k] = xload(cand + 2 * H + k);
+  load_exchanged(s.vec, cand + 2 * H);
   const Slice sl{a.projector, H, U / 4, U / 4, 0, u0, kStageUnits / (U / 4)};
   float acc = 0.0f;
   if (t < U) acc = a.projector_bias[u0 + t];
@@ -591,9 +613,26 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
                            uint32_t p, uint32_t buf, const _Float16* encoder_row, const float* projection,
                            uint32_t hq0, uint32_t hq1) {
   const uint32_t t = threadIdx.x;
+  load_exchanged(s.vec, projection);
+  __syncthreads();
   for (uint32_t c = t; c < H; c += TT) {
-    const float v = (float)encoder_row[c] + xload(projection + c);
+    const float v = (float)encoder_row[c] + s.vec[c];
     s.vec[c] = v > 0.0f ? v : 0.0f;
+  }
+  __syncthreads();
+  // The head chain skips an exact +0 input while no -0 or NaN has appeared
+  // at or before it: s.x holds the f16 inputs, s.use whether row k enters
+  // the chain (the first -0 / NaN row found by a min-reduction).
+  if (t == 0) s.first_bad = H;
+  __syncthreads();
+  for (uint32_t c = t; c < H; c += TT) {
+    const uint32_t bits = __float_as_uint(s.vec[c]);
+    if (bits == 0x80000000u || (bits & 0x7fffffffu) > 0x7f800000u) atomicMin(&s.first_bad, c);
+  }
+  __syncthreads();
+  for (uint32_t c = t; c < H; c += TT) {
+    s.x[c] = (_Float16)s.vec[c];
+    s.use[c] = __float_as_uint(s.vec[c]) != 0u || c >= s.first_bad;
   }
   const uint32_t HQ = hq1 - hq0;  // at most 17 (16 members) or 33 (8 members)
   const Slice sl{a.head, kTdtHead, HQ, HQ, 0, hq0 * 4, HQ * 320 <= kStageUnits ? 320u : 160u};
@@ -602,25 +641,23 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
     const float4 bb = *reinterpret_cast<const float4*>(a.head_bias + 4 * (hq0 + t));
     acc = half4{(_Float16)bb.x, (_Float16)bb.y, (_Float16)bb.z, (_Float16)bb.w};
   }
-  bool zero_skip_safe = true;
   __syncthreads();
   stream_slice(s, sl, H, [&](const half4* st, uint32_t k0) {
     if (t < HQ) {
       for (uint32_t r0 = 0; r0 < sl.rows; r0 += 16) {
         half4 w[16];
-        float xs[16];
+        _Float16 xs[16];
+        bool use[16];
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i) {
           w[i] = st[(r0 + i) * HQ + t];
-          xs[i] = s.vec[k0 + r0 + i];
+          xs[i] = s.x[k0 + r0 + i];
+          use[i] = s.use[k0 + r0 + i];
         }
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i) {
-          const float x = xs[i];
-          const uint32_t bits = __float_as_uint(x);
-          const bool is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
-          zero_skip_safe = zero_skip_safe && !(bits == 0x80000000u || is_nan);
-          if (!(zero_skip_safe && bits == 0u)) acc = __builtin_elementwise_fma(splat((_Float16)x), w[i], acc);
+          const half4 next = __builtin_elementwise_fma(splat(xs[i]), w[i], acc);
+          acc = use[i] ? next : acc;
         }
       }
     }
@@ -656,18 +693,20 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
     xstore(part + 4 * p + 3, d);
   }
   if (!team_barrier(s, tm, b, n)) return false;
+  if (t < 4 * tm.members) s.part[t] = xload(part + t);  // every partial in one round trip
+  __syncthreads();
   if (t == 0) {
     float best = -3.402823466e+38f, dbest = -3.402823466e+38f;
     uint32_t id = 0xffffffffu, d = 0xffffffffu;
     for (uint32_t m = 0; m < tm.members; ++m) {
-      const float v = __uint_as_float(xload(part + 4 * m + 0));
-      const uint32_t o = xload(part + 4 * m + 1);
+      const float v = __uint_as_float(s.part[4 * m + 0]);
+      const uint32_t o = s.part[4 * m + 1];
       if (o != 0xffffffffu && (v > best || (v == best && o < id))) {
         best = v;
         id = o;
       }
-      const float dv = __uint_as_float(xload(part + 4 * m + 2));
-      const uint32_t j = xload(part + 4 * m + 3);
+      const float dv = __uint_as_float(s.part[4 * m + 2]);
+      const uint32_t j = s.part[4 * m + 3];
       if (j != 0xffffffffu && (dv > dbest || (dv == dbest && j < d))) {
         dbest = dv;
         d = j;
