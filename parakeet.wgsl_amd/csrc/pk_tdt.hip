@@ -72,8 +72,9 @@ struct Shared {
   float gates[kTdtGates]; // f32 values of the f16 gate sums
   float joint[H];         // relu(encoder + projection)
   float scores[kTdtHead]; // f32 values of the f16 head accumulators
+  bool use[H];            // head row k enters the chain (the +0-skip rule)
   // control, written by thread 0
-  uint32_t go, emitted, token, duration, joint_time;
+  uint32_t go, emitted, token, duration, joint_time, first_bad;
 };
 
 // Rows of weights loaded before any is used: the k loops are latency
@@ -172,11 +173,24 @@ __device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, 
     const float v = (float)encoder_row[c] + projection[c];
     s.joint[c] = v > 0.0f ? v : 0.0f;
   }
+  if (t == 0) s.first_bad = H;
+  __syncthreads();
+  // An exact +0 input is skipped while no -0 or NaN has appeared at or
+  // before it: find the first such row, then flag every row and keep the
+  // f16 inputs, so the chain below selects instead of branching.
+  for (uint32_t c = t; c < H; c += kThreads) {
+    const uint32_t bits = __float_as_uint(s.joint[c]);
+    if (bits == 0x80000000u || (bits & 0x7fffffffu) > 0x7f800000u) atomicMin(&s.first_bad, c);
+  }
+  __syncthreads();
+  for (uint32_t c = t; c < H; c += kThreads) {
+    s.x[c] = (_Float16)s.joint[c];
+    s.use[c] = __float_as_uint(s.joint[c]) != 0u || c >= s.first_bad;
+  }
   __syncthreads();
   if (t < kTdtHead / 4) {
     const float4 b = *reinterpret_cast<const float4*>(a.head_bias + 4 * t);
     half4 acc = half4{(_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-    bool zero_skip_safe = true;
     const _Float16* column = a.head + 4 * t;
     for (uint32_t k0 = 0; k0 < H; k0 += kBatchRows) {
       half4 w[kBatchRows];
@@ -184,11 +198,8 @@ __device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, 
       for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(column + (uint64_t)(k0 + r) * kTdtHead);
 #pragma unroll
       for (uint32_t r = 0; r < kBatchRows; ++r) {
-        const float x = s.joint[k0 + r];
-        const uint32_t bits = __float_as_uint(x);
-        const bool is_nan = (bits & 0x7fffffffu) > 0x7f800000u;
-        zero_skip_safe = zero_skip_safe && !(bits == 0x80000000u || is_nan);
-        if (!(zero_skip_safe && bits == 0u)) acc = __builtin_elementwise_fma(splat((_Float16)x), w[r], acc);
+        const half4 next = __builtin_elementwise_fma(splat(s.x[k0 + r]), w[r], acc);
+        acc = s.use[k0 + r] ? next : acc;
       }
     }
     for (int i = 0; i < 4; ++i) s.scores[4 * t + i] = (float)acc[i];
