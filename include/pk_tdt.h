@@ -90,7 +90,8 @@ typedef struct pk_tdt_desc {
 } pk_tdt_desc;
 
 typedef struct pk_tdt_execution_plan {
-  uint32_t workgroup_count;      /* this library: one workgroup per window */
+  uint32_t workgroup_count;      /* one workgroup per window; an op in team mode
+                                    launches pk_tdt_team_size() per window */
   uint32_t block_threads;
   uint64_t predictor_scratch_bytes;
 } pk_tdt_execution_plan;

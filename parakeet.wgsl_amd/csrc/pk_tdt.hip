@@ -665,11 +665,11 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
           xs[i] = s.x[k0 + r0 + i];
           use[i] = s.use[k0 + r0 + i];
         }
+        // the flag is the same for every lane: a scalar branch skips the
+        // row without touching the dependent chain
 #pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-          const half4 next = __builtin_elementwise_fma(splat(xs[i]), w[i], acc);
-          acc = use[i] ? next : acc;
-        }
+        for (uint32_t i = 0; i < 16; ++i)
+          if (__builtin_amdgcn_readfirstlane((int)use[i])) acc = __builtin_elementwise_fma(splat(xs[i]), w[i], acc);
       }
     }
   });
@@ -677,11 +677,12 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
     for (int i = 0; i < 4; ++i) s.scores[4 * t + i] = (float)acc[i];
   __syncthreads();
   uint32_t* part = tm.partials + (((uint64_t)b * 2 + buf) * tm.members) * 4;
-  if (t == 0) {
-    // this member's best token (value, lowest id) and best duration
+  if (t < 64) {
+    // this member's best token (value, lowest id) and best duration: each
+    // lane scans scores t, t + 64, t + 128, then a shuffle reduction
     float best = -3.402823466e+38f, dbest = -3.402823466e+38f;
     uint32_t id = 0xffffffffu, d = 0xffffffffu;
-    for (uint32_t i = 0; i < 4 * HQ; ++i) {
+    for (uint32_t i = t; i < 4 * HQ; i += 64) {
       const uint32_t o = 4 * hq0 + i;
       float v = s.scores[i];
       v = v != v ? -3.402823466e+38f : v;
@@ -698,10 +699,26 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
         }
       }
     }
-    xstore(part + 4 * p + 0, __float_as_uint(best));
-    xstore(part + 4 * p + 1, id);
-    xstore(part + 4 * p + 2, __float_as_uint(dbest));
-    xstore(part + 4 * p + 3, d);
+    for (int offset = 32; offset > 0; offset >>= 1) {
+      const float ov = __shfl_xor(best, offset, 64);
+      const uint32_t oid = __shfl_xor(id, offset, 64);
+      if (ov > best || (ov == best && oid < id)) {
+        best = ov;
+        id = oid;
+      }
+      const float odv = __shfl_xor(dbest, offset, 64);
+      const uint32_t od = __shfl_xor(d, offset, 64);
+      if (odv > dbest || (odv == dbest && od < d)) {
+        dbest = odv;
+        d = od;
+      }
+    }
+    if (t == 0) {
+      xstore(part + 4 * p + 0, __float_as_uint(best));
+      xstore(part + 4 * p + 1, id);
+      xstore(part + 4 * p + 2, __float_as_uint(dbest));
+      xstore(part + 4 * p + 3, d);
+    }
   }
   if (!team_barrier(s, tm, b, n)) return false;
   if (t < 4 * tm.members) s.part[t] = xload(part + t);  // every partial in one round trip
