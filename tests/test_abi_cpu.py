@@ -710,3 +710,14 @@ def test_encoder_null_handles(abi):
     assert lib.pk_encoder_info(None, None, None) == abi.INVALID_ARGUMENT
     assert lib.pk_encoder_destroy(None) == abi.OK
     assert lib.pk_encoder_validate(None) == abi.INVALID_ARGUMENT
+
+
+def test_tdt_team_size_arguments(abi):
+    """The team-size calls (no reference counterpart) reject a null op and a
+    null output before touching a device."""
+    lib = abi.load()
+    out = ctypes.c_uint32()
+    with pytest.raises(abi.PaletteError, match="TDT decoder op is null"):
+        abi.check(lib.pk_tdt_set_team_size(None, 16))
+    with pytest.raises(abi.PaletteError, match="TDT decoder op or output is null"):
+        abi.check(lib.pk_tdt_team_size(None, ctypes.byref(out)))
