@@ -131,6 +131,19 @@ int pk_copy_device(pk_context *ctx, void *device_dst, const void *device_src,
 int pk_stream_create(pk_context *ctx, void **stream);
 int pk_stream_destroy(pk_context *ctx, void *stream);
 int pk_stream_synchronize(pk_context *ctx, void *stream);
+
+/* No reference counterpart (a WebGPU command buffer is re-encoded per
+   submit): records the enqueues a caller makes on `stream` between begin
+   and end (this thread only) into a HIP graph of kernel nodes, which
+   pk_graph_launch replays on any stream of the context. For callers whose
+   step is a few launches, as a serving loop: replays skip the per-launch
+   host cost. A graph replays the ops as they were when captured (their
+   buffers and active sizes); timed enqueues cannot be captured. */
+typedef struct pk_graph pk_graph;
+int pk_graph_begin_capture(pk_context *ctx, void *stream);
+int pk_graph_end_capture(pk_context *ctx, void *stream, pk_graph **out);
+int pk_graph_launch(pk_graph *graph, void *stream);
+int pk_graph_destroy(pk_graph *graph);
 int pk_event_create(pk_context *ctx, void **event);
 int pk_event_destroy(pk_context *ctx, void *event);
 int pk_event_record(pk_context *ctx, void *event, void *stream);

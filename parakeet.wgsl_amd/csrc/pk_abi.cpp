@@ -577,6 +577,49 @@ int pk_stream_synchronize(pk_context* ctx, void* stream) {
   return ok();
 }
 
+struct pk_graph {
+  pk_context* ctx = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+int pk_graph_begin_capture(pk_context* ctx, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  PK_HIP(hipStreamBeginCapture(stream_or_default(ctx, stream), hipStreamCaptureModeThreadLocal),
+         "hipStreamBeginCapture");
+  return ok();
+}
+
+int pk_graph_end_capture(pk_context* ctx, void* stream, pk_graph** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!out) return fail(PK_INVALID_ARGUMENT, "graph output is null");
+  *out = nullptr;
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  hipGraph_t graph = nullptr;
+  PK_HIP(hipStreamEndCapture(stream_or_default(ctx, stream), &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  PK_HIP(inst, "hipGraphInstantiate");
+  *out = new pk_graph{ctx, exec};
+  return ok();
+}
+
+int pk_graph_launch(pk_graph* graph, void* stream) {
+  if (!graph) return fail(PK_INVALID_ARGUMENT, "graph is null");
+  PK_HIP(hipSetDevice(graph->ctx->device), "hipSetDevice");
+  PK_HIP(hipGraphLaunch(graph->exec, stream_or_default(graph->ctx, stream)), "hipGraphLaunch");
+  return ok();
+}
+
+int pk_graph_destroy(pk_graph* graph) {
+  if (!graph) return ok();
+  (void)hipSetDevice(graph->ctx->device);
+  (void)hipGraphExecDestroy(graph->exec);
+  delete graph;
+  return ok();
+}
+
 int pk_event_create(pk_context* ctx, void** event) {
   if (int s = check_ctx(ctx)) return s;
   if (!event) return fail(PK_INVALID_ARGUMENT, "output pointer is null");

@@ -507,6 +507,10 @@ SIGNATURES = {
     "pk_tdt_destroy": (ctypes.c_int, [_VP]),
     "pk_tdt_release": (ctypes.c_int, [_VP]),
     "pk_tdt_set_team_size": (ctypes.c_int, [_VP, ctypes.c_uint32]),
+    "pk_graph_begin_capture": (ctypes.c_int, [_VP, _VP]),
+    "pk_graph_end_capture": (ctypes.c_int, [_VP, _VP, _PPV]),
+    "pk_graph_launch": (ctypes.c_int, [_VP, _VP]),
+    "pk_graph_destroy": (ctypes.c_int, [_VP]),
     "pk_tdt_team_size": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32)]),
     "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
     "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
@@ -1123,6 +1127,37 @@ class TdtDecoderOp:
     def release(self) -> None:
         if self.handle:
             check(load().pk_tdt_release(self.handle))
+            self.handle = None
+
+
+class Graph:
+    """pk_graph: the enqueues made on `stream` inside `with Graph.capture(ctx, stream) as g:`,
+    replayed by g.launch()."""
+
+    def __init__(self, ctx: "Context", stream=None):
+        self.ctx, self.stream, self.handle = ctx, stream, None
+
+    @classmethod
+    def capture(cls, ctx: "Context", stream=None) -> "Graph":
+        return cls(ctx, stream)
+
+    def __enter__(self) -> "Graph":
+        check(load().pk_graph_begin_capture(self.ctx.handle, self.stream))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        handle = ctypes.c_void_p()
+        status = load().pk_graph_end_capture(self.ctx.handle, self.stream, ctypes.byref(handle))
+        if exc_type is None:
+            check(status)
+            self.handle = handle.value
+
+    def launch(self, stream=None) -> None:
+        check(load().pk_graph_launch(self.handle, self.stream if stream is None else stream))
+
+    def release(self) -> None:
+        if self.handle:
+            load().pk_graph_destroy(self.handle)
             self.handle = None
 
 

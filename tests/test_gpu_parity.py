@@ -514,3 +514,54 @@ def test_feed_forward_block_full_size(abi, ctx, scope, oracle, workloads):
     assert_f16_parity(oracle, h[rows], ff.expand_case(), rows=rows)
     contract = ff.contract_case(h)
     assert_f16_parity(oracle, out[rows], contract, rows=rows)
+
+
+def test_feed_forward_block_graph_replay_matches_eager(abi, ctx, workloads):
+    """pk_graph_* (no reference counterpart): the FF block's two launches
+    captured once and replayed three times, with eager passes on other
+    inputs in between, give the eager result bit for bit every time."""
+    ff = workloads.feed_forward_block(0)
+    m = ff.x.shape[0]
+    held = []
+
+    def keep(a):
+        held.append(a)
+        return a
+    try:
+        x = keep(ctx.array(ff.x))
+        hidden = keep(ctx.empty((m, 4096), np.float16))
+        y = keep(ctx.empty((m, 1024), np.float16))
+        op1 = abi.GemmOp(ctx, a=x, packed=keep(ctx.array(ff.w1.packed)), palette=keep(ctx.array(ff.w1.palette)),
+                         output=hidden, bits=5, rows=m, inner=1024, columns=4096, activation="silu",
+                         label="ff-expand")
+        op2 = abi.GemmOp(ctx, a=hidden, packed=keep(ctx.array(ff.w2.packed)), palette=keep(ctx.array(ff.w2.palette)),
+                         output=y, bits=5, rows=m, inner=4096, columns=1024, residual=x, residual_scale=0.5,
+                         label="ff-contract")
+        stream = ctx.stream
+        op1.enqueue(0, stream)
+        op2.enqueue(0, stream)
+        ctx.synchronize(stream)
+        eager = y.download()
+        graph = abi.Graph.capture(ctx, stream)
+        with graph:
+            op1.enqueue(0, stream)
+            op2.enqueue(0, stream)
+        try:
+            for replay in range(3):
+                x.upload(np.flip(ff.x, axis=0).copy())       # other input, eager
+                op1.enqueue(0, stream)
+                op2.enqueue(0, stream)
+                ctx.synchronize(stream)
+                x.upload(ff.x)
+                y.upload(np.zeros((m, 1024), np.float16))
+                graph.launch()
+                ctx.synchronize(stream)
+                print("graph replay", replay, flush=True)
+                np.testing.assert_array_equal(y.download().view(np.uint16), eager.view(np.uint16))
+        finally:
+            graph.release()
+        op1.release()
+        op2.release()
+    finally:
+        for a in held:
+            a.free()
