@@ -1460,6 +1460,25 @@ static napi_value js_tdt_enqueue(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* tdtSetTeamSize(op, members): 0 chooses, 1 one workgroup per window, 8 or 16 */
+static napi_value js_tdt_set_team_size(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  uint32_t members = 0;
+  if (!get_args(env, info, 2, argv) || !get_u32(env, argv[1], &members))
+    return bad_argument(env, "team size must be a non-negative integer");
+  PK_CALL(env, pk_tdt_set_team_size((pk_tdt_op *)get_external(env, argv[0]), members));
+  return undefined(env);
+}
+
+/* tdtTeamSize(op) -> workgroups per window of the next launch */
+static napi_value js_tdt_team_size(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  uint32_t members = 0;
+  if (!get_args(env, info, 1, argv)) return NULL;
+  PK_CALL(env, pk_tdt_team_size((const pk_tdt_op *)get_external(env, argv[0]), &members));
+  return make_number(env, members);
+}
+
 static napi_value js_tdt_destroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return NULL;
@@ -1528,6 +1547,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"tdtCreate", js_tdt_create},
       {"tdtEnqueue", js_tdt_enqueue},
       {"tdtDestroy", js_tdt_destroy},
+      {"tdtSetTeamSize", js_tdt_set_team_size},
+      {"tdtTeamSize", js_tdt_team_size},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
     napi_value f;

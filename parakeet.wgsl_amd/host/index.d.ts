@@ -578,6 +578,10 @@ export interface TdtDecoderDescriptor {
 /** tdt-decoder.ts:84-137 */
 export declare class TdtDecoderDispatch {
   readonly label: string;
+  /** Workgroups per window of the next launch (this library only). */
+  readonly teamSize: number;
+  /** 0 chooses, 1 one workgroup per window, 8 or 16 a team (this library only). */
+  setTeamSize(members: number): void;
   encode(encoder: HipCommandEncoder, timestampWrites?: TimestampWrites, activeBatchSize?: number): void;
   destroy(): void;
 }

@@ -1766,6 +1766,16 @@ class TdtDecoderDispatch {
     this.destroyed = true;
     native().tdtDestroy(this.op);
   }
+
+  /** Workgroups per window of the next launch (no reference counterpart). */
+  get teamSize() {
+    return native().tdtTeamSize(this.op);
+  }
+
+  /** 0 chooses, 1 one workgroup per window, 8 or 16 a team (no reference counterpart). */
+  setTeamSize(members) {
+    native().tdtSetTeamSize(this.op, members);
+  }
 }
 
 /**

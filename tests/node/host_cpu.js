@@ -9,6 +9,7 @@ const host = require(path.join(__dirname, "..", "..", "parakeet.wgsl_amd", "host
 const native = host.native();
 assert.strictEqual(native.abiVersion(), 1);
 for (const name of ["contextCreate", "gemmCreate", "gemmValidate", "gemmEnqueue", "gemmDestroy", "gemmPlan",
+                    "tdtCreate", "tdtEnqueue", "tdtSetTeamSize", "tdtTeamSize",
                     "preparedWeightCreate", "synchronizeAsync", "alloc", "upload", "download"]) {
   assert.strictEqual(typeof native[name], "function", name);
 }

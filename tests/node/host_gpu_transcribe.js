@@ -54,6 +54,7 @@ async function main() {
   arena.upload(device, descriptor.state, new Float32Array(windows * 4 * 640));
   const kernel = await host.PersistentTdtDecoderKernel.create(device, arena, pkg);
   const dispatch = kernel.createDispatch(descriptor);
+  console.log(`decoder team size ${dispatch.teamSize}`);
   encoder = device.createCommandEncoder({ label: "decode" });
   dispatch.encode(encoder);
   device.queue.submit([encoder.finish()]);
@@ -64,7 +65,7 @@ async function main() {
     out[name] = Array.from(new Uint32Array(await read(name)));
   }
   fs.writeFileSync(spec.decoded, JSON.stringify(out));
-  console.log("counts", out.metadata.slice(0, windows).join(","));
+  console.log("counts", out.metadata.slice(0, windows).join(","), `team size after the launch ${dispatch.teamSize}`);
   dispatch.destroy();
   dispatch.destroy();
   arena.destroy();
