@@ -2,15 +2,21 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Default workload (one step): the Conformer feed-forward block in fp16 on
-8 windows x 188 frames x 1024 channels - H = SiLU(X W1) with a 5-bit palette
-W1 1024->4096, then Y = X + 0.5 (H W2) with a 5-bit palette W2 4096->1024.
-Inputs are seeded synthetic data resident in HBM before timing starts. One
-JSON line is printed: whole-job TFLOP/s, the roofline of the dominant kernel
-(timed with HIP events on the stream the kernels run on) and the CPU oracle's
-throughput on a bounded sample of the same workload.
+Default workload (one step = one encoder pass): the FastConformer encoder in
+fp16 over 16 windows of 15 s - the 8x subsampling front end over a 128-bin x
+1501-frame fbank, 24 layers at 188 frames x 1024 channels whose eight palette
+GEMMs per layer carry every projection, and the 1024->640 projector - with
+random-init palette weights at the reference package's widths. Inputs are
+seeded synthetic data resident in HBM before timing starts. One JSON line is
+printed: encoder audio-sec/sec, the roofline of the dominant palette GEMM
+(timed with HIP events stamped by its own dispatches on the stream it runs
+on), the CPU oracle's throughput on a bounded sample of the same workload at
+one thread and at all threads, and, under "ff_block", the palette-GEMM
+TFLOP/s of the Conformer feed-forward block (8 windows x 188 frames: H =
+SiLU(X W1), 5-bit 1024->4096, then Y = X + 0.5 (H W2), 5-bit 4096->1024).
 
 Other workloads (for profiling; same JSON shape):
+  ff-block          the feed-forward block above as the step, TFLOP/s
   single-gemm-fp32  X[256x1024] f32 x 6-bit W 1024->4096 + bias
   small-m           5-bit 1024->4096 f16 GEMM at --rows M (HBM-bound regime)
   conv-module       Conformer convolution module, fp16, 16 windows x 188 x 1024:
@@ -53,6 +59,9 @@ PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}  # MI355X dense MFMA
 PEAK_HBM_GBS = 8000.0
 METRIC = "palette-GEMM TFLOP/s & % roofline; encoder audio-sec/sec at 1 MI355X"
 TIMING_STRIDE = 5  # one step in five carries the per-kernel start/end stamps
+# roofline.traffic is looked up, not measured in the run it is reported with
+TRAFFIC_SOURCE = ("looked up in profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of the same "
+                  "command, scaled by the counters' reading of a plain copy")
 
 
 def parse_args():
@@ -60,7 +69,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="ff-block",
+    p.add_argument("--workload", default="encoder",
                    choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
                             "rel-pos-mha", "encoder", "transcribe"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
@@ -69,6 +78,7 @@ def parse_args():
                    help="rows of the CPU-oracle sample (0 = workload default)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
+    p.add_argument("--no-ff-block", action="store_true", help="encoder workloads: skip the FF block's extra line")
     p.add_argument("--graph", action="store_true",
                    help="replay the unstamped steps from a HIP graph (measured slower than eager launches for "
                         "two-launch steps)")
@@ -223,12 +233,36 @@ def build_mha(abi, ctx, keep, frames):
     return kernels, config, mod
 
 
-def cpu_baseline(workload, data, sample_rows, budget_s=10.0):
+def host_info():
+    """The CPU the baseline runs on: usable threads, logical CPUs, model name."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": usable, "logical_cpus": os.cpu_count(), "model": model}
+
+
+def all_threads():
+    """Threads of the all-core CPU leg: the usable CPUs, at most 16 (the
+    share of one GPU's host)."""
+    return max(1, min(host_info()["nproc"], 16))
+
+
+def cpu_baseline(workload, data, sample_rows, budget_s=10.0, threads=None):
     """The oracle (reference semantics restated in C) on a bounded sample:
     row batches of the same workload until about `budget_s` seconds of wall
     time have passed (or `sample_rows` rows, when given)."""
     from oracle import pko
-    threads = min(os.cpu_count() or 1, 16)
+    threads = threads or all_threads()
     batch = 32
     if workload == "ff-block":
         total_rows, per_row_flops = data.x.shape[0], 2 * 1024 * 4096 * 2
@@ -352,12 +386,31 @@ def encoder_dispatch_costs(abi, wl, stack):
 
 
 def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
-    """The oracle (reference fp16 semantics) on window 0: the front end, then
-    layer after layer until about `budget_s` seconds have passed; with
-    `decoder` = (weights, projected window [188, 640] f16, length), also the
-    oracle's greedy decode of that window."""
+    """The oracle (reference fp16 semantics) on window 0 at all threads (the
+    front end, then layer after layer for about `budget_s` seconds) and at
+    one thread (one layer, the pass extrapolated with the all-thread leg's
+    front-end-to-layer ratio); with `decoder` = (weights, projected window
+    [188, 640] f16, length), also the oracle's greedy decode of that window
+    (one thread in both legs)."""
     from oracle import pko
-    threads = min(os.cpu_count() or 1, 16)
+    main, x0, ratio, decode_s = encoder_cpu_leg(stack, all_threads(), budget_s, decoder)
+    t0 = time.perf_counter()
+    pko.encoder_layer(x0, stack.layers[0], stack.valid[:1], batch=1, frames=stack.frames, gemm_mode="f16-chain",
+                      threads=1)
+    layer_s = time.perf_counter() - t0
+    pass_s = layer_s * (len(stack.layers) + ratio) + decode_s
+    main["single_thread"] = {
+        "value": WINDOW_SECONDS / pass_s, "unit": "audio-sec/sec", "cores": 1, "kind": "port",
+        "sample": ("one 15-s window: layer 0 timed at one thread, the pass extrapolated to every layer and the "
+                   f"front end (front end = {ratio:.2f} layers, from the all-thread leg)"
+                   + ("; plus the decode time of the all-thread leg" if decoder is not None else "")),
+        "seconds": layer_s}
+    main["host"] = host_info()
+    return main
+
+
+def encoder_cpu_leg(stack, threads, budget_s, decoder):
+    from oracle import pko
     t0 = time.perf_counter()
     if stack.subsampling is not None:
         x = pko.encoder_front_end(stack.features[:1], stack.subsampling, stack.feature_lengths[:1],
@@ -365,6 +418,7 @@ def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
     else:
         x = stack.x[:stack.frames]
     front_s = time.perf_counter() - t0
+    x0 = x
     done = 0
     while done < len(stack.layers) and (done == 0 or time.perf_counter() - t0 < budget_s):
         x = pko.encoder_layer(x, stack.layers[done], stack.valid[:1], batch=1, frames=stack.frames,
@@ -376,14 +430,17 @@ def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
     sample = (f"one 15-s window: the front end and {done} of {len(stack.layers)} layers timed, the pass "
               "extrapolated to every layer (f16-accumulator GEMM chain, f32 conv, LayerNorm and attention: "
               "reference fp16 semantics)")
+    decode_s = 0.0
     if decoder is not None:
         weights, projected, length = decoder
         t1 = time.perf_counter()
         pko.tdt_decode(weights, projected[None], [length], max_tokens=1024, flush=[1])
-        pass_s += time.perf_counter() - t1
-        sample += "; then the greedy TDT decode of that window (f16 LSTM and head chains)"
-    return {"value": WINDOW_SECONDS / pass_s, "unit": "audio-sec/sec", "cores": threads, "kind": "port",
-            "sample": sample, "seconds": time.perf_counter() - t0}
+        decode_s = time.perf_counter() - t1
+        pass_s += decode_s
+        sample += "; then the greedy TDT decode of that window (f16 LSTM and head chains, one thread)"
+    leg = {"value": WINDOW_SECONDS / pass_s, "unit": "audio-sec/sec", "cores": threads, "kind": "port",
+           "sample": sample, "seconds": time.perf_counter() - t0}
+    return leg, x0, front_s / layer_s, decode_s
 
 
 def run_encoder(args, abi, ctx, decoder=False):
@@ -495,6 +552,7 @@ def run_encoder(args, abi, ctx, decoder=False):
                     "frac": dom["gbs"] / PEAK_HBM_GBS}
     roofline["kernel"] = f"encoder.layers.*-{name}" if name in abi.ENCODER_DISPATCHES else f"encoder.{name}"
     roofline["traffic"] = read_traffic(f"encoder-{name}", None)
+    roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
 
     total_flops = stack.gemm_flops() + stack.attention_flops() + stack.front_end_flops()
     cpu_decoder = None
@@ -523,6 +581,7 @@ def run_encoder(args, abi, ctx, decoder=False):
             probe.times_ms = [dispatches[k]["avg_us"] * 1e-3]
             probes.append(probe)
         dense = dense_reference(probes)
+    ff_block = None if args.no_ff_block else ff_block_summary(abi, ctx, args)
     line = {
         "metric": METRIC,
         "value": stack.batch * WINDOW_SECONDS / (ms_per_step * 1e-3),
@@ -547,6 +606,8 @@ def run_encoder(args, abi, ctx, decoder=False):
         "roofline": roofline,
         "cpu_baseline": cpu,
         "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
+        "gemm_tflops": gemm_tflops(dispatches),
+        "ff_block": ff_block,
         "device_bytes": device_bytes,
         "dispatches": dispatches,
         "dense_vendor_reference": dense,
@@ -561,6 +622,37 @@ def run_encoder(args, abi, ctx, decoder=False):
     for arr in held:
         arr.free()
     ctx.close()
+
+
+def gemm_tflops(dispatches):
+    """Palette-GEMM TFLOP/s over the pass: every palette GEMM launch's FLOP
+    over the sum of their stamped durations."""
+    gemms = {k: d for k, d in dispatches.items()
+             if d["flops"] and k not in ("relative-attention", "subsampling-fused-conv0-depthwise2",
+                                         "subsampling-depthwise5")}
+    flops = sum(d["flops"] * d["launches_per_pass"] for d in gemms.values())
+    us = sum(d["avg_us"] * d["launches_per_pass"] for d in gemms.values())
+    return flops / (us * 1e-6) / 1e12 if us else None
+
+
+def ff_block_summary(abi, ctx, args):
+    """The FF block (palette-GEMM TFLOP/s of two back-to-back launches) in
+    the same process, as the encoder's extra line."""
+    held = []
+
+    def keep(arr):
+        held.append(arr)
+        return arr
+    kernels, config, _ = build_ff_block(abi, ctx, keep)
+    try:
+        step = measure_kernel_step(ctx, kernels, max(args.steps, 20), max(args.warmup, 5))
+        return {"value": step["value"], "unit": "TFLOP/s", "ms_per_step": step["ms_per_step"], "config": config,
+                "roofline": step["roofline"], "kernels": {k.name: k.summary() for k in kernels}}
+    finally:
+        for k in kernels:
+            k.op.release()
+        for arr in held:
+            arr.free()
 
 
 def read_traffic(gemm_name, kernel_name):
@@ -623,6 +715,83 @@ def dense_probe(request, reps):
     print(json.dumps(out), flush=True)
 
 
+def measure_kernel_step(ctx, kernels, steps, warmup, use_graph=False):
+    """Runs `warmup` then `steps` steps of the kernels' launches in order on
+    the context's stream; returns the step time (events around the timed
+    region), the per-launch stamped durations and the dominant kernel's
+    roofline."""
+    import parakeet_wgsl_amd.palette_abi as abi
+    stream = ctx.stream
+    for _ in range(warmup):
+        for k in kernels:
+            k.op.enqueue(0, stream)
+    ctx.synchronize(stream)
+    # With --graph the unstamped steps replay the step's launches from a HIP
+    # graph (pk_graph_*); the stamped ones always run eagerly. For the FF
+    # block a replay measured 57.8 us per step against 53.1 us for the two
+    # eager launches, so eager is the default.
+    graph = None
+    if use_graph:
+        graph = abi.Graph.capture(ctx, stream)
+        with graph:
+            for k in kernels:
+                k.op.enqueue(0, stream)
+        graph.launch()
+        ctx.synchronize(stream)
+
+    # Per-kernel durations: every TIMING_STRIDE-th step of the timed region,
+    # each launch's own dispatch stamps a start and an end event
+    # (pk_gemm_enqueue_timed). Stamping costs the stream a few microseconds
+    # per launch, so the other steps run unstamped and the step time stays
+    # that of the plain launches.
+    timed_steps = list(range(0, steps, TIMING_STRIDE))
+    marks = {step: [(ctx.event(), ctx.event()) for _ in kernels] for step in timed_steps}
+    start, end = ctx.event(), ctx.event()
+    ctx.synchronize(stream)
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for step in range(steps):
+        stamps = marks.get(step)
+        if stamps:
+            for i, k in enumerate(kernels):
+                k.op.enqueue(0, stream, *stamps[i])
+        elif graph is not None:
+            graph.launch()
+        else:
+            for k in kernels:
+                k.op.enqueue(0, stream)
+    end.record(stream)
+    end.synchronize()
+    ctx.synchronize(stream)
+    wall = time.perf_counter() - wall0
+
+    total_ms = start.elapsed_ms(end)
+    for step in timed_steps:
+        for i, k in enumerate(kernels):
+            k.times_ms.append(marks[step][i][0].elapsed_ms(marks[step][i][1]))
+    ms_per_step = total_ms / steps
+    flops = sum(k.flops for k in kernels)
+    value = flops / (ms_per_step * 1e-3) / 1e12
+
+    dominant = max(kernels, key=lambda k: float(np.mean(k.times_ms)))
+    dom = dominant.summary()
+    peak = PEAK_TFLOPS[dominant.precision]
+    compute_s = dominant.flops / (peak * 1e12)
+    memory_s = dominant.nbytes / (PEAK_HBM_GBS * 1e9)
+    if compute_s >= memory_s:
+        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak, "unit": "TFLOP/s",
+                    "frac": dom["tflops"] / peak}
+    else:
+        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": dom["gbs"] / PEAK_HBM_GBS}
+    roofline["kernel"] = dom["kernel"]
+    roofline["traffic"] = read_traffic(dominant.name, dom["kernel"])
+    roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
+
+    return {"ms_per_step": ms_per_step, "wall": wall, "value": value, "dominant": dominant, "dom": dom,
+            "roofline": roofline, "graph": graph}
+
+
 def main():
     args = parse_args()
     if args.dense_probe:
@@ -659,75 +828,16 @@ def main():
             if isinstance(k.op, abi.GemmOp):
                 k.op.set_variant(args.variant)
 
-    stream = ctx.stream
-    for _ in range(args.warmup):
-        for k in kernels:
-            k.op.enqueue(0, stream)
-    ctx.synchronize(stream)
-    # With --graph the unstamped steps replay the step's launches from a HIP
-    # graph (pk_graph_*); the stamped ones always run eagerly. For the FF
-    # block a replay measured 57.8 us per step against 53.1 us for the two
-    # eager launches, so eager is the default.
-    graph = None
-    if args.graph:
-        graph = abi.Graph.capture(ctx, stream)
-        with graph:
-            for k in kernels:
-                k.op.enqueue(0, stream)
-        graph.launch()
-        ctx.synchronize(stream)
-
-    # Per-kernel durations: every TIMING_STRIDE-th step of the timed region,
-    # each launch's own dispatch stamps a start and an end event
-    # (pk_gemm_enqueue_timed). Stamping costs the stream a few microseconds
-    # per launch, so the other steps run unstamped and the step time stays
-    # that of the plain launches.
-    timed_steps = list(range(0, args.steps, TIMING_STRIDE))
-    marks = {step: [(ctx.event(), ctx.event()) for _ in kernels] for step in timed_steps}
-    start, end = ctx.event(), ctx.event()
-    ctx.synchronize(stream)
-    wall0 = time.perf_counter()
-    start.record(stream)
-    for step in range(args.steps):
-        stamps = marks.get(step)
-        if stamps:
-            for i, k in enumerate(kernels):
-                k.op.enqueue(0, stream, *stamps[i])
-        elif graph is not None:
-            graph.launch()
-        else:
-            for k in kernels:
-                k.op.enqueue(0, stream)
-    end.record(stream)
-    end.synchronize()
-    ctx.synchronize(stream)
-    wall = time.perf_counter() - wall0
-
-    total_ms = start.elapsed_ms(end)
-    for step in timed_steps:
-        for i, k in enumerate(kernels):
-            k.times_ms.append(marks[step][i][0].elapsed_ms(marks[step][i][1]))
-    ms_per_step = total_ms / args.steps
-    flops = sum(k.flops for k in kernels)
-    value = flops / (ms_per_step * 1e-3) / 1e12
-
-    dominant = max(kernels, key=lambda k: float(np.mean(k.times_ms)))
-    dom = dominant.summary()
-    peak = PEAK_TFLOPS[dominant.precision]
-    compute_s = dominant.flops / (peak * 1e12)
-    memory_s = dominant.nbytes / (PEAK_HBM_GBS * 1e9)
-    if compute_s >= memory_s:
-        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak, "unit": "TFLOP/s",
-                    "frac": dom["tflops"] / peak}
-    else:
-        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": dom["gbs"] / PEAK_HBM_GBS}
-    roofline["kernel"] = dom["kernel"]
-    roofline["traffic"] = read_traffic(dominant.name, dom["kernel"])
+    step = measure_kernel_step(ctx, kernels, args.steps, args.warmup, args.graph)
+    dominant, dom, roofline = step["dominant"], step["dom"], step["roofline"]
+    ms_per_step, wall, graph = step["ms_per_step"], step["wall"], step["graph"]
+    value = step["value"]
 
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.workload, data, args.cpu_sample_rows)
+        cpu["single_thread"] = cpu_baseline(args.workload, data, args.cpu_sample_rows, threads=1)
+        cpu["host"] = host_info()
     dense = None if args.no_dense else dense_reference(kernels)
 
     line = {

@@ -99,8 +99,11 @@ const char *pk_status_name(int status);
 
 /* Create a context on HIP device `device` (it owns one default stream). */
 int pk_context_create(int device, pk_context **out);
-/* Destroys the context; ops and weights created from it must be destroyed
-   first. NULL is accepted. */
+/* Drops the owner's handle of the context (the reference's device destroy).
+   Calls that take the context fail with PK_DESTROYED from then on. Ops,
+   prepared weights, graphs and encoders made on it keep its stream and
+   device alive until they are released, so they may be released in any
+   order afterwards. Call it once per context; NULL is accepted. */
 int pk_context_destroy(pk_context *ctx);
 int pk_context_device(const pk_context *ctx, int *device);
 /* The context's default stream as a hipStream_t. */

@@ -106,11 +106,16 @@ int pk_tdt_enqueue_timed(pk_tdt_op *op, uint32_t active_batch, void *stream, voi
    chooses (16 or 8 when every workgroup of the batch can be resident
    together, else 1), 1 runs one workgroup per window, 8 and 16 split
    every weight matrix over a team that meets at barriers in global memory
-   (a cooperative launch). Results are bit-identical for every size. The
-   create call chooses automatically; the setter synchronizes the device. */
+   (bounded waits: a barrier that never completes sets the window's
+   PK_TDT_SYNC_TIMEOUT status). Results are bit-identical for every size.
+   The create call chooses automatically; the setter synchronizes the
+   device. A team launch that the runtime refuses returns PK_DEVICE_ERROR
+   and leaves the team size as it was. */
 int pk_tdt_set_team_size(pk_tdt_op *op, uint32_t members);
 int pk_tdt_team_size(const pk_tdt_op *op, uint32_t *members);
-/* Idempotent; enqueue after destroy returns PK_DESTROYED. */
+/* Idempotent; frees the team buffers (after the device has drained), and
+   enqueue after destroy returns PK_DESTROYED. Enqueue on a stream that is
+   capturing a graph returns PK_INVALID_ARGUMENT. */
 int pk_tdt_destroy(pk_tdt_op *op);
 int pk_tdt_release(pk_tdt_op *op);
 

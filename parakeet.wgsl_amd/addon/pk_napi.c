@@ -373,10 +373,20 @@ static napi_value js_event_elapsed_ms(napi_env env, napi_callback_info info) {
 
 /* ---- prepared weights ----------------------------------------------------- */
 
+/* The JavaScript handle holds the weight through a box: the explicit destroy
+   releases the owner's reference and empties the box, the finalizer
+   releases only a weight still in the box. An op created from the weight
+   keeps its own reference, so the weight may outlive the handle. */
+typedef struct weight_box {
+  pk_prepared_weight *w;
+} weight_box;
+
 static void weight_finalize(napi_env env, void *data, void *hint) {
   (void)env;
   (void)hint;
-  pk_prepared_weight_destroy((pk_prepared_weight *)data);
+  weight_box *box = (weight_box *)data;
+  if (box->w) pk_prepared_weight_destroy(box->w);
+  free(box);
 }
 
 /* preparedWeightCreate(ctx, {label, paletteBits, inner, columns, packed, packedBytes}) */
@@ -398,14 +408,26 @@ static napi_value js_prepared_weight_create(napi_env env, napi_callback_info inf
   const int status = pk_prepared_weight_create((pk_context *)get_external(env, argv[0]), &d, NULL, &w);
   free(label);
   if (status != PK_OK) return throw_status(env, status);
-  NAPI_CALL(env, napi_create_external(env, w, weight_finalize, NULL, &ext));
+  weight_box *box = (weight_box *)malloc(sizeof *box);
+  if (!box) {
+    pk_prepared_weight_destroy(w);
+    napi_throw_error(env, "PK_ALLOCATION_FAILURE", "cannot allocate the weight handle");
+    return NULL;
+  }
+  box->w = w;
+  NAPI_CALL(env, napi_create_external(env, box, weight_finalize, NULL, &ext));
   return ext;
 }
 
 static napi_value js_prepared_weight_destroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return NULL;
-  PK_CALL(env, pk_prepared_weight_destroy((pk_prepared_weight *)get_external(env, argv[0])));
+  weight_box *box = (weight_box *)get_external(env, argv[0]);
+  if (box && box->w) {
+    pk_prepared_weight *w = box->w;
+    box->w = NULL;
+    PK_CALL(env, pk_prepared_weight_destroy(w));
+  }
   return undefined(env);
 }
 
@@ -463,7 +485,14 @@ static int parse_gemm_desc(napi_env env, napi_value o, pk_gemm_desc *d, char **l
     d->has_residual_scale = 1;
     d->residual_scale = (float)scale;
   }
-  if (prop(env, o, "prepared", &v)) d->prepared = (const pk_prepared_weight *)get_external(env, v);
+  if (prop(env, o, "prepared", &v)) {
+    const weight_box *box = (const weight_box *)get_external(env, v);
+    if (!box || !box->w) {
+      napi_throw_error(env, "PK_DESTROYED", "prepared palette weight was destroyed");
+      return 0;
+    }
+    d->prepared = box->w;
+  }
   d->a = (const void *)(uintptr_t)a;
   d->packed = (const uint32_t *)(uintptr_t)packed;
   d->palette = (const void *)(uintptr_t)palette;

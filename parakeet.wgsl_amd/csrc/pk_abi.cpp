@@ -30,7 +30,21 @@ int fail(int status, const char* fmt, ...) {
 
 int check_ctx(const pk_context* ctx) {
   if (!ctx) return fail(PK_INVALID_ARGUMENT, "context is null");
+  if (ctx->destroyed.load()) return fail(PK_DESTROYED, "context was destroyed");
   return PK_OK;
+}
+
+pk_context* ctx_retain(pk_context* ctx) {
+  if (ctx) ctx->refs.fetch_add(1);
+  return ctx;
+}
+
+void ctx_release(pk_context* ctx) {
+  if (!ctx || ctx->refs.fetch_sub(1) != 1) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
 }
 
 }  // namespace pk_abi
@@ -76,7 +90,7 @@ const char* activation_name(int a) {
 }  // namespace
 
 struct pk_prepared_weight {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   int bits = 5;
   uint32_t inner = 0, columns = 0;
@@ -89,7 +103,7 @@ struct pk_prepared_weight {
 };
 
 struct pk_gemm_op {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   int precision = PK_PRECISION_F16;
   int bits = 5;
@@ -139,9 +153,10 @@ int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, ui
     if (e != hipSuccess && w->codes) (void)hipFree(w->codes);
   }
   if (e != hipSuccess) {
+    const unsigned long long want = (unsigned long long)w->bytes;
     delete w;
     return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
-                safe_label(label), (unsigned long long)w->bytes, hipGetErrorString(e));
+                safe_label(label), want, hipGetErrorString(e));
   }
   if (!glu) e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
   if (e == hipSuccess) e = pk::launch_to_pair_codes(bits, packed, inner, columns, w->pair_codes, stream, glu);
@@ -463,10 +478,10 @@ int pk_context_create(int device, pk_context** out) {
 
 int pk_context_destroy(pk_context* ctx) {
   if (!ctx) return ok();
+  if (ctx->destroyed.exchange(true)) return ok();
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
-  (void)hipStreamDestroy(ctx->stream);
-  delete ctx;
+  ctx_release(ctx);
   return ok();
 }
 
@@ -578,7 +593,7 @@ int pk_stream_synchronize(pk_context* ctx, void* stream) {
 }
 
 struct pk_graph {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   hipGraphExec_t exec = nullptr;
 };
 
@@ -601,7 +616,10 @@ int pk_graph_end_capture(pk_context* ctx, void* stream, pk_graph** out) {
   const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   (void)hipGraphDestroy(graph);
   PK_HIP(inst, "hipGraphInstantiate");
-  *out = new pk_graph{ctx, exec};
+  auto* g = new pk_graph();
+  g->ctx = ctx;
+  g->exec = exec;
+  *out = g;
   return ok();
 }
 

@@ -4,14 +4,22 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <string>
 
 #include "pk_palette.h"
 
+// A context is reference counted: pk_context_destroy drops the owner's
+// reference, and every op, prepared weight, graph or encoder made on it
+// holds one more until it is freed. The stream and the object go away with
+// the last reference, so an object released after its context (a
+// finalizer that runs late) still finds the device id and the stream.
 struct pk_context {
   int device = 0;
   hipStream_t stream = nullptr;
+  std::atomic<int> refs{1};
+  std::atomic<bool> destroyed{false};
 };
 
 namespace pk_abi {
@@ -21,7 +29,34 @@ extern thread_local std::string g_error;
 // Sets the calling thread's last error message and returns `status`.
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 inline int ok() { return PK_OK; }
+// Null check for calls that take a context; a destroyed context is refused
+// with PK_DESTROYED.
 int check_ctx(const pk_context* ctx);
+
+// Reference counting of contexts (see pk_context).
+pk_context* ctx_retain(pk_context* ctx);
+void ctx_release(pk_context* ctx);
+
+// The context member of an op: holds a reference from assignment until the
+// op is deleted.
+class CtxRef {
+ public:
+  CtxRef() = default;
+  CtxRef(const CtxRef&) = delete;
+  CtxRef& operator=(const CtxRef&) = delete;
+  ~CtxRef() { ctx_release(p_); }
+  CtxRef& operator=(pk_context* c) {
+    ctx_retain(c);
+    ctx_release(p_);
+    p_ = c;
+    return *this;
+  }
+  pk_context* operator->() const { return p_; }
+  operator pk_context*() const { return p_; }
+
+ private:
+  pk_context* p_ = nullptr;
+};
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

@@ -14,7 +14,7 @@
 using namespace pk_abi;
 
 struct pk_attention_op {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   int precision = PK_PRECISION_F16;
   uint32_t batch = 0;

@@ -65,7 +65,7 @@ uint32_t halve(uint32_t n, uint32_t steps) { return pk_subsampling_valid_length(
 }  // namespace
 
 struct pk_encoder {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   uint32_t batch = 0, frames = 0, layers = 0, rows = 0;
   bool fused_glu = false;

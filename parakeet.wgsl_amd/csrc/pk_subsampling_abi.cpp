@@ -14,7 +14,7 @@
 using namespace pk_abi;
 
 struct pk_subsampling_op {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   int kind = pk::kSubsamplingFused;
   int precision = PK_PRECISION_F16;

@@ -370,8 +370,12 @@ __global__ __launch_bounds__(kTdtThreads) void tdt_decode_kernel(TdtArgs a) {
 // loads, stay cached. A barrier that waits
 // longer than `spin_limit` polls raises the window's abort flag and every
 // member leaves its loop at its next barrier (status kTdtSyncTimeout), so
-// every wave reaches the end. The launch is cooperative, so all members of
-// every window are resident together.
+// every wave reaches the end. The launch is an ordinary one whose grid
+// never exceeds the workgroups the device holds at once (the occupancy
+// bound checked at launch), so on an otherwise idle device every member is
+// resident; a member that is not (another kernel holds its compute unit)
+// only delays the barrier until it is scheduled, and the bounded poll turns
+// a wait that never ends into the timeout status.
 
 constexpr uint32_t TT = kTdtTeamThreads;
 
@@ -882,19 +886,20 @@ uint32_t tdt_team_capacity(int device) {
 hipError_t launch_tdt_team(const TdtArgs& args, const TdtTeam& team, uint32_t batch, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop) {
   if (batch == 0) return hipSuccess;
+  if (!tdt_team_members_supported(team.members) || batch > team.capacity) return hipErrorInvalidValue;
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if ((uint64_t)batch * team.members > tdt_team_capacity(device)) return hipErrorInvalidConfiguration;
   const uint32_t words = 2 * team.capacity * kTdtSyncStride;
   hipLaunchKernelGGL(tdt_team_clear, dim3((words + 255) / 256), dim3(256), 0, stream, team.sync, words);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (start && (e = hipEventRecord(start, stream)) != hipSuccess) return e;
-  TdtArgs a = args;
-  TdtTeam tm = team;
-  void* params[] = {&a, &tm};
-  e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(tdt_team_kernel), dim3(batch * team.members),
-                                 dim3(kTdtTeamThreads), params, 0, stream);
-  if (e != hipSuccess) return e;
-  if (stop) e = hipEventRecord(stop, stream);
-  return e;
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const dim3 grid(batch * team.members), block(kTdtTeamThreads);
+  if (start || stop)
+    hipExtLaunchKernelGGL(tdt_team_kernel, grid, block, 0, stream, start, stop, 0, args, team);
+  else
+    hipLaunchKernelGGL(tdt_team_kernel, grid, block, 0, stream, args, team);
+  return hipGetLastError();
 }
 
 }  // namespace pk

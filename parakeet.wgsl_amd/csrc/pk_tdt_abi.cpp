@@ -12,7 +12,7 @@
 using namespace pk_abi;
 
 struct pk_tdt_op {
-  pk_context* ctx = nullptr;
+  pk_abi::CtxRef ctx;
   std::string label;
   uint32_t batch = 0;
   pk::TdtArgs args{};
@@ -93,8 +93,14 @@ uint32_t choose_members(int device, uint32_t batch) {
   return 0;
 }
 
+// Frees the team buffers once no launch can still use them (hipFree alone
+// would not order the free after work enqueued on another stream).
 void free_team(pk_tdt_op* op) {
-  if (op->team_memory) (void)hipFree(op->team_memory);
+  if (op->team_memory) {
+    (void)hipSetDevice(op->ctx->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(op->team_memory);
+  }
   op->team_memory = nullptr;
   op->team = pk::TdtTeam{};
 }
@@ -185,7 +191,6 @@ int pk_tdt_set_team_size(pk_tdt_op* op, uint32_t members) {
     return fail(PK_RANGE_ERROR, "%s: %u windows x %u workgroups cannot be resident together", op->label.c_str(),
                 op->batch, members);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
-  PK_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
   return set_team(op, members);
 }
 
@@ -208,14 +213,21 @@ int pk_tdt_enqueue_timed(pk_tdt_op* op, uint32_t active_batch, void* stream, voi
     return fail(PK_RANGE_ERROR, "%s active batch must be in [1, %u]", op->label.c_str(), op->batch);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
   const hipStream_t s = stream_or_default(op->ctx, stream);
+  // The decode is data dependent and its team buffers can be replaced by
+  // pk_tdt_set_team_size, so it is never recorded into a graph.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  PK_HIP(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+  if (capture != hipStreamCaptureStatusNone)
+    return fail(PK_INVALID_ARGUMENT, "%s cannot be enqueued on a capturing stream", op->label.c_str());
   if (op->team.members) {
+    // A refused team launch is an error: the op keeps its team size, and a
+    // caller that wants one workgroup per window sets team size 1.
     const hipError_t e = pk::launch_tdt_team(op->args, op->team, batch, s, static_cast<hipEvent_t>(start_event),
                                              static_cast<hipEvent_t>(end_event));
-    if (e == hipSuccess) return ok();
-    // A stream or process where the cooperative launch is refused decodes
-    // with one workgroup per window from here on (same results).
-    (void)hipGetLastError();
-    free_team(op);
+    if (e != hipSuccess)
+      return fail(PK_DEVICE_ERROR, "%s: team launch (%u x %u workgroups) failed: %s", op->label.c_str(), batch,
+                  op->team.members, hipGetErrorString(e));
+    return ok();
   }
   PK_HIP(pk::launch_tdt_decode(op->args, batch, s, static_cast<hipEvent_t>(start_event),
                                static_cast<hipEvent_t>(end_event)),
@@ -226,17 +238,13 @@ int pk_tdt_enqueue_timed(pk_tdt_op* op, uint32_t active_batch, void* stream, voi
 int pk_tdt_destroy(pk_tdt_op* op) {
   if (!op || op->destroyed) return ok();
   op->destroyed = true;
+  free_team(op);
   return ok();
 }
 
 int pk_tdt_release(pk_tdt_op* op) {
   if (!op) return ok();
   pk_tdt_destroy(op);
-  if (op->team_memory) {
-    (void)hipSetDevice(op->ctx->device);
-    (void)hipDeviceSynchronize();
-  }
-  free_team(op);
   delete op;
   return ok();
 }

@@ -66,6 +66,7 @@ async function main() {
   }
   fs.writeFileSync(spec.decoded, JSON.stringify(out));
   console.log("counts", out.metadata.slice(0, windows).join(","), `team size after the launch ${dispatch.teamSize}`);
+  if (dispatch.teamSize !== 16) throw new Error(`decoder ran with team size ${dispatch.teamSize}, expected 16`);
   dispatch.destroy();
   dispatch.destroy();
   arena.destroy();

@@ -38,9 +38,14 @@ def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADB
     try:
         if team is not None:
             op.set_team_size(team)
-        print("decoder team", op.team_size(), "batch", B, "frames", T, flush=True)
+        before = op.team_size()
+        print("decoder team", before, "batch", B, "frames", T, flush=True)
         op.enqueue(active)
         ctx.synchronize()
+        # A refused team launch is an error, never a silent change of mode.
+        assert op.team_size() == before
+        if team:  # 0 lets the op choose
+            assert op.team_size() == team
     finally:
         op.release()
     meta = metadata.download()
