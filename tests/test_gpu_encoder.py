@@ -162,9 +162,17 @@ def test_encoder_24_layers_full_size(abi, ctx, scope, oracle, workloads):
     x0 = windows(stack.x, 188, 0, 1)
     truth = oracle.encoder(x0, stack.layers, stack.valid[:1], batch=1, frames=188, gemm_mode="f64",
                            threads=THREADS)
-    norm, worst = oracle.relative_errors(windows(eager, 188, 0, 1), truth)
-    print(f"24 layers vs f64 chain: norm {norm:.2e} max {worst:.2e}", flush=True)
+    reference = oracle.encoder(x0, stack.layers, stack.valid[:1], batch=1, frames=188, gemm_mode="f16-chain",
+                               threads=THREADS)
+    got0 = windows(eager, 188, 0, 1)
+    norm, worst = oracle.relative_errors(got0, truth)
+    norm16, _ = oracle.relative_errors(got0, reference)
+    gap, _ = oracle.relative_errors(truth, reference)
+    print(f"24 layers: vs f64 chain {norm:.2e} (max {worst:.2e}); vs f16 chain {norm16:.2e}; chains apart {gap:.2e}",
+          flush=True)
     assert norm <= 1e-2, (norm, worst)
+    # the reference's own f16 accumulation: no farther from it than the exact chain is
+    assert norm16 <= 1.1 * gap + 1e-3, (norm16, gap)
 
 
 def test_encoder_eight_layers_against_the_reference_chain(abi, ctx, scope, oracle, workloads):
@@ -277,12 +285,18 @@ def test_encoder_graph_full_size(abi, ctx, scope, oracle, workloads):
     finally:
         enc.release()
     assert np.isfinite(eager).all() and np.isfinite(eager_projected).all()
-    out, projected = oracle.encoder_graph(None, stack.layers, stack.valid[:1], batch=1, frames=188,
-                                          front=stack.subsampling, features=stack.features[:1],
-                                          feature_lengths=stack.feature_lengths[:1], projector=stack.projector,
-                                          projector_bias=stack.projector_bias, gemm_mode="f64", threads=THREADS)
-    for name, g, t in (("output", windows(eager, 188, 0, 1), out),
-                       ("projected", windows(eager_projected, 188, 0, 1), projected)):
+    chains = {mode: oracle.encoder_graph(None, stack.layers, stack.valid[:1], batch=1, frames=188,
+                                         front=stack.subsampling, features=stack.features[:1],
+                                         feature_lengths=stack.feature_lengths[:1], projector=stack.projector,
+                                         projector_bias=stack.projector_bias, gemm_mode=mode, threads=THREADS)
+              for mode in ("f64", "f16-chain")}
+    for i, (name, g) in enumerate((("output", windows(eager, 188, 0, 1)),
+                                   ("projected", windows(eager_projected, 188, 0, 1)))):
+        t, r = chains["f64"][i], chains["f16-chain"][i]
         norm, worst = oracle.relative_errors(valid_rows(g, stack, 1), valid_rows(t, stack, 1))
-        print(f"front end + 24 layers, {name} vs f64 chain: norm {norm:.2e} max {worst:.2e}", flush=True)
+        norm16, _ = oracle.relative_errors(valid_rows(g, stack, 1), valid_rows(r, stack, 1))
+        gap, _ = oracle.relative_errors(valid_rows(t, stack, 1), valid_rows(r, stack, 1))
+        print(f"front end + 24 layers, {name}: vs f64 chain {norm:.2e} (max {worst:.2e}); vs f16 chain "
+              f"{norm16:.2e}; chains apart {gap:.2e}", flush=True)
         assert norm <= 1e-2, (name, norm, worst)
+        assert norm16 <= 1.1 * gap + 1e-3, (name, norm16, gap)
