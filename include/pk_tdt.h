@@ -119,6 +119,21 @@ int pk_tdt_team_size(const pk_tdt_op *op, uint32_t *members);
 int pk_tdt_destroy(pk_tdt_op *op);
 int pk_tdt_release(pk_tdt_op *op);
 
+/* No counterpart in the reference: the whole decode of `desc` as one call
+   that allocates nothing, for callers that cannot allocate device memory
+   (code under HIP graph capture, tight serving loops, harnesses that forbid
+   hipMalloc). It validates like pk_tdt_create, then launches like
+   pk_tdt_enqueue of every window with team size `members` (0 chooses, 1,
+   8 or 16; bit-identical results for each), taking the team's barrier
+   counters and argmax partials from a static device array of the library
+   (64 KB per GPU, held until the process ends) instead of buffers of an
+   op. At most PK_TDT_STATIC_MAX_WINDOWS windows (PK_RANGE_ERROR beyond).
+   Every call on one GPU shares that array: calls whose decodes overlap on
+   the same GPU (other streams, other threads) race and must be ordered by
+   the caller. */
+#define PK_TDT_STATIC_MAX_WINDOWS 64u
+int pk_tdt_decode_static(pk_context *ctx, const pk_tdt_desc *desc, uint32_t members, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

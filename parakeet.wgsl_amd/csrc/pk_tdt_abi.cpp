@@ -3,6 +3,7 @@
 // src/webgpu/kernels/tdt-decoder.ts (:39-547).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 
 #include "pk_abi_internal.h"
@@ -123,31 +124,9 @@ int set_team(pk_tdt_op* op, uint32_t members) {
   return PK_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int pk_tdt_plan_execution(uint32_t batch_size, pk_tdt_execution_plan* plan) {
-  if (!plan) return fail(PK_INVALID_ARGUMENT, "plan output is null");
-  if (batch_size == 0) return fail(PK_RANGE_ERROR, "TDT decoder batchSize must be a positive integer");
-  plan->workgroup_count = batch_size;
-  plan->block_threads = pk::kTdtThreads;
-  plan->predictor_scratch_bytes = (uint64_t)batch_size * 5 * H * 4;
-  return ok();
-}
-
-int pk_tdt_validate(const pk_tdt_desc* d) { return validate(d); }
-
-int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
-  if (int s = check_ctx(ctx)) return s;
-  if (!out) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
-  *out = nullptr;
-  if (int s = validate(d)) return s;
-  auto* op = new pk_tdt_op();
-  op->ctx = ctx;
-  op->label = d->label ? d->label : "parakeet-persistent-tdt-decode";
-  op->batch = d->batch_size;
-  pk::TdtArgs& a = op->args;
+// Kernel arguments of a validated descriptor.
+pk::TdtArgs args_of(const pk_tdt_desc* d) {
+  pk::TdtArgs a{};
   const pk_tdt_weights& w = d->weights;
   a.embedding = static_cast<const _Float16*>(w.embedding);
   a.lstm[0] = static_cast<const _Float16*>(w.lstm_weight[0]);
@@ -172,6 +151,69 @@ int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
   a.status = d->metadata + d->batch_size;
   a.frames = d->frames;
   a.max_tokens = d->max_tokens;
+  return a;
+}
+
+// Team buffers of pk_tdt_decode_static: the barrier counters and abort
+// flags of up to kStaticWindows windows (two 256-byte lines each), then the
+// argmax partials of teams of up to 16 members (two buffers of four words
+// per member). One copy per GPU, held until the process ends; the launch
+// clears the counters and flags with a kernel, the partials are written
+// before they are read.
+constexpr uint32_t kStaticWindows = PK_TDT_STATIC_MAX_WINDOWS;
+constexpr uint32_t kStaticSyncWords = 2 * kStaticWindows * pk::kTdtSyncStride;
+constexpr uint32_t kStaticPartialWords = kStaticWindows * 2 * 16 * 4;
+
+}  // namespace
+
+static __device__ __align__(256) uint32_t scratch[kStaticSyncWords + kStaticPartialWords];
+
+namespace {
+
+// The device address of `scratch` on each GPU, looked up once per device
+// with that device current (the host symbol is not a device address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint32_t* g_scratch[kMaxDevices] = {};
+
+int scratch_address(int device, uint32_t** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(PK_INVALID_ARGUMENT, "device %d is outside the static decoder buffers' table", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    PK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    g_scratch[device] = static_cast<uint32_t*>(p);
+  }
+  *out = g_scratch[device];
+  return PK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_tdt_plan_execution(uint32_t batch_size, pk_tdt_execution_plan* plan) {
+  if (!plan) return fail(PK_INVALID_ARGUMENT, "plan output is null");
+  if (batch_size == 0) return fail(PK_RANGE_ERROR, "TDT decoder batchSize must be a positive integer");
+  plan->workgroup_count = batch_size;
+  plan->block_threads = pk::kTdtThreads;
+  plan->predictor_scratch_bytes = (uint64_t)batch_size * 5 * H * 4;
+  return ok();
+}
+
+int pk_tdt_validate(const pk_tdt_desc* d) { return validate(d); }
+
+int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!out) return fail(PK_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  if (int s = validate(d)) return s;
+  auto* op = new pk_tdt_op();
+  op->ctx = ctx;
+  op->label = d->label ? d->label : "parakeet-persistent-tdt-decode";
+  op->batch = d->batch_size;
+  op->args = args_of(d);
   if (int st = set_team(op, choose_members(ctx->device, op->batch))) {
     delete op;
     return st;
@@ -246,6 +288,42 @@ int pk_tdt_release(pk_tdt_op* op) {
   if (!op) return ok();
   pk_tdt_destroy(op);
   delete op;
+  return ok();
+}
+
+int pk_tdt_decode_static(pk_context* ctx, const pk_tdt_desc* d, uint32_t members, void* stream) {
+  if (int s = check_ctx(ctx)) return s;
+  if (int s = validate(d)) return s;
+  const char* label = d->label ? d->label : "parakeet-persistent-tdt-decode";
+  const uint32_t batch = d->batch_size;
+  if (batch > kStaticWindows)
+    return fail(PK_RANGE_ERROR, "%s: %u windows exceed the %u of the static decoder buffers", label, batch,
+                kStaticWindows);
+  if (members == 0) members = choose_members(ctx->device, batch);
+  else if (members == 1) members = 0;
+  else if (!pk::tdt_team_members_supported(members))
+    return fail(PK_RANGE_ERROR, "%s team size must be 0, 1, 8 or 16", label);
+  else if ((uint64_t)batch * members > pk::tdt_team_capacity(ctx->device))
+    return fail(PK_RANGE_ERROR, "%s: %u windows x %u workgroups cannot be resident together", label, batch, members);
+  PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  const hipStream_t st = stream_or_default(ctx, stream);
+  const pk::TdtArgs args = args_of(d);
+  if (members == 0) {
+    PK_HIP(pk::launch_tdt_decode(args, batch, st), "TDT decoder launch");
+    return ok();
+  }
+  uint32_t* buffers = nullptr;
+  if (int s = scratch_address(ctx->device, &buffers)) return s;
+  pk::TdtTeam team{};
+  team.members = members;
+  team.sync = buffers;
+  team.partials = buffers + kStaticSyncWords;
+  team.capacity = batch;
+  team.spin_limit = 1u << 24;
+  const hipError_t e = pk::launch_tdt_team(args, team, batch, st);
+  if (e != hipSuccess)
+    return fail(PK_DEVICE_ERROR, "%s: team launch (%u x %u workgroups) failed: %s", label, batch, members,
+                hipGetErrorString(e));
   return ok();
 }
 

@@ -512,6 +512,7 @@ SIGNATURES = {
     "pk_graph_launch": (ctypes.c_int, [_VP, _VP]),
     "pk_graph_destroy": (ctypes.c_int, [_VP]),
     "pk_tdt_team_size": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32)]),
+    "pk_tdt_decode_static": (ctypes.c_int, [_VP, ctypes.POINTER(TdtDesc), ctypes.c_uint32, _VP]),
     "pk_encoder_validate": (ctypes.c_int, [ctypes.POINTER(EncoderDesc)]),
     "pk_encoder_create": (ctypes.c_int, [_VP, ctypes.POINTER(EncoderDesc), _VP, _PPV]),
     "pk_encoder_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, ctypes.c_int]),
@@ -1093,6 +1094,16 @@ def tdt_desc(*, weights: dict, encoder_projected, encoded_lengths, decode_starts
         fields += list(sl(x))
     return TdtDesc(ctypes.sizeof(TdtDesc), label.encode(), PRECISION["f16"], batch_size, frames, max_tokens, tw,
                    *fields)
+
+
+TDT_STATIC_MAX_WINDOWS = 64  # PK_TDT_STATIC_MAX_WINDOWS
+
+
+def tdt_decode_static(ctx: Context, members: int = 0, stream=None, **descriptor) -> None:
+    """pk_tdt_decode_static: the whole decode of a descriptor with no op and
+    no allocation (the team buffers are the library's static array)."""
+    desc = tdt_desc(**descriptor)
+    check(load().pk_tdt_decode_static(ctx.handle, ctypes.byref(desc), members, stream))
 
 
 class TdtDecoderOp:
