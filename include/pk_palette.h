@@ -176,9 +176,10 @@ typedef struct pk_weight_desc {
 int pk_prepared_weight_create(pk_context *ctx, const pk_weight_desc *desc,
                               void *stream, pk_prepared_weight **out);
 int pk_prepared_weight_destroy(pk_prepared_weight *weight);
-/* Device bytes held by the prepared weight: the codes in MFMA operand order
- * (as many bits per code as the packed format) plus the pair-code layout of
- * the large-M kernels (16 bits per two codes, K and N padded to 64 and 32). */
+/* Device bytes held by the prepared weight: its codes in MFMA operand order,
+ * the one layout every kernel reads, as many bits per code as the packed
+ * format (K and N padded to 64 and 32): K * N * bits / 8 at the encoder's
+ * shapes. */
 int pk_prepared_weight_bytes(const pk_prepared_weight *weight, uint64_t *bytes);
 
 /* ---- GEMM ----------------------------------------------------------------- */

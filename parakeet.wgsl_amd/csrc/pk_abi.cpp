@@ -94,10 +94,10 @@ struct pk_prepared_weight {
   std::string label;
   int bits = 5;
   uint32_t inner = 0, columns = 0;
-  uint32_t* codes = nullptr;      // operand-order codes (device)
-  uint8_t* pair_codes = nullptr;  // pair-code layout (device)
-  uint64_t bytes = 0;             // both layouts
-  bool glu = false;               // GLU-interleaved pair codes only
+  uint32_t* codes = nullptr;      // operand-order codes (device), split into `parts` K parts
+  int parts = 1;                  // the one layout held: what the planned kernel reads
+  uint64_t bytes = 0;
+  bool glu = false;               // column blocks interleaved for the GLU epilogue
   std::atomic<int> refs{1};
   bool owner_released = false;
 };
@@ -118,25 +118,28 @@ struct pk_gemm_op {
   bool destroyed = false;
 };
 
+uint64_t pk_abi::gemm_weight_bytes(const pk_gemm_op* op) { return op && op->weight ? op->weight->bytes : 0; }
+
 namespace {
 
 void weight_unref(pk_prepared_weight* w) {
   if (!w) return;
   if (w->refs.fetch_sub(1) == 1) {
-    if (w->codes || w->pair_codes) {
+    if (w->codes) {
       (void)hipSetDevice(w->ctx->device);
-      if (w->codes) (void)hipFree(w->codes);
-      if (w->pair_codes) (void)hipFree(w->pair_codes);
+      (void)hipFree(w->codes);
     }
     delete w;
   }
 }
 
-// Prepares a packed weight: both code layouts, or with `glu` only the
-// pair codes with value and gate column blocks interleaved (the GLU
-// epilogue runs in the pair-code kernels alone).
+// Prepares a packed weight in the one layout its kernel reads: the codes in
+// operand order split into `parts` K parts (pk_internal.h), with `glu` the
+// value and gate column blocks interleaved (the GLU epilogue runs in the
+// pair-code kernels alone).
 int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, uint32_t columns,
-                const uint32_t* packed, hipStream_t stream, pk_prepared_weight** out, bool glu = false) {
+                const uint32_t* packed, hipStream_t stream, pk_prepared_weight** out, bool glu = false,
+                int parts = 1) {
   auto* w = new pk_prepared_weight();
   w->ctx = ctx;
   w->label = safe_label(label);
@@ -144,32 +147,54 @@ int make_weight(pk_context* ctx, const char* label, int bits, uint32_t inner, ui
   w->inner = inner;
   w->columns = columns;
   w->glu = glu;
-  const uint64_t operand_bytes = glu ? 0 : pk::operand_order_words(bits, inner, columns) * 4u;
-  const uint64_t pair_bytes = pk::pair_code_bytes(inner, columns);
-  w->bytes = operand_bytes + pair_bytes;
-  hipError_t e = glu ? hipSuccess : hipMalloc(reinterpret_cast<void**>(&w->codes), operand_bytes);
-  if (e == hipSuccess) {
-    e = hipMalloc(reinterpret_cast<void**>(&w->pair_codes), pair_bytes);
-    if (e != hipSuccess && w->codes) (void)hipFree(w->codes);
-  }
+  w->parts = parts;
+  w->bytes = pk::operand_order_words(bits, inner, columns, parts) * 4u;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->codes), w->bytes);
   if (e != hipSuccess) {
     const unsigned long long want = (unsigned long long)w->bytes;
     delete w;
     return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
                 safe_label(label), want, hipGetErrorString(e));
   }
-  if (!glu) e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream);
-  if (e == hipSuccess) e = pk::launch_to_pair_codes(bits, packed, inner, columns, w->pair_codes, stream, glu);
+  e = pk::launch_to_operand_order(bits, packed, inner, columns, w->codes, stream, glu, parts);
   if (e == hipSuccess) e = hipStreamSynchronize(stream);
   if (e != hipSuccess) {
-    if (w->codes) (void)hipFree(w->codes);
-    (void)hipFree(w->pair_codes);
+    (void)hipFree(w->codes);
     delete w;
     return fail(PK_DEVICE_ERROR, "%s: palette code preparation failed: %s", safe_label(label),
                 hipGetErrorString(e));
   }
   *out = w;
   return PK_OK;
+}
+
+// Moves an op's own weight to the layout of `parts` (a variant switch to a
+// kernel that reads another split): the new layout is derived on the device
+// from the old one, which is then freed, so the weight still holds one.
+int relayout_weight(pk_prepared_weight* w, int parts, hipStream_t stream) {
+  if (w->parts == parts) return PK_OK;
+  const uint64_t bytes = pk::operand_order_words(w->bits, w->inner, w->columns, parts) * 4u;
+  uint32_t* codes = nullptr;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&codes), bytes);
+  if (e != hipSuccess)
+    return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of prepared palette codes: %s",
+                w->label.c_str(), (unsigned long long)bytes, hipGetErrorString(e));
+  const uint64_t blocks = (uint64_t)(pk::padded_columns(w->columns) / 32u) * (pk::padded_inner(w->inner) / 64u);
+  e = pk::launch_relayout(w->bits, w->codes, w->parts, codes, parts, blocks, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    (void)hipFree(codes);
+    return fail(PK_DEVICE_ERROR, "%s: palette code relayout failed: %s", w->label.c_str(), hipGetErrorString(e));
+  }
+  (void)hipFree(w->codes);
+  w->codes = codes;
+  w->parts = parts;
+  w->bytes = bytes;
+  return PK_OK;
+}
+
+int variant_parts(int precision, int variant) {
+  return precision == PK_PRECISION_F16 ? pk::f16_variant_parts(variant) : 1;
 }
 
 // Packed-code contract of requireGemmShape (gemm.ts:997-1010) and
@@ -255,13 +280,20 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
       int tile_rows, tile_columns;
       double us;
     };
+    // The 192 x 256 tile without a K split (four wavefronts of 192 x 64)
+    // measured 28.5 us per workgroup; it is a candidate for the wide GEMMs
+    // (N >= 3072) at K = 1024 only, where it was measured against the others
+    // (FF expand 3008 x 1024 x 4096: 34.7 us against 42.1 us for two rounds of
+    // 192 x 128; QKV 3008 x 1024 x 3072: 29.3 us against 30.5 us).
     constexpr Candidate kCandidates[] = {
         {2, 6, 2, 2, 192, 128, 22.3}, {2, 4, 2, 2, 128, 128, 17.2}, {2, 3, 2, 2, 96, 128, 14.8},
         {1, 3, 2, 4, 96, 64, 11.0},   {1, 2, 2, 4, 64, 64, 9.3},    {0, 2, 1, 8, 64, 32, 8.2},
+        {4, 6, 2, 1, 192, 256, 28.5},
     };
     int best = -1;
     double best_us = 1e300;
     for (const Candidate& c : kCandidates) {
+      if (c.tile_columns == 256 && (columns < 3072u || inner < 1024u)) continue;
       const int v = c.wn ? find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, c.wn, c.r, c.c, c.ks)
                          : find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, c.r, 1, 8);
       if (v < 0) continue;
@@ -300,6 +332,31 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
     }
   }
   return {best, 1u};
+}
+
+// The plan of one op: plan_launch, with a GLU epilogue moved to the
+// pair-code kernels (small-M plans take their 64 x 64 tile), and with a
+// shared prepared weight restricted to the tiles that read the layout it
+// holds (`required_parts`, 0 = any).
+Plan plan_op(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus, bool glu,
+             int required_parts) {
+  Plan plan = plan_launch(precision, rows, inner, columns, cus);
+  if (glu && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
+    plan = {find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4), 1u};
+  if (required_parts && variant_parts(precision, plan.variant) != required_parts) {
+    int v = -1;
+    if (required_parts == 2)
+      v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 2, 3, 2, 2);  // 96 x 128
+    else if (required_parts == 4)
+      v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4);  // 64 x 64
+    else if (!glu && rows <= 256u)
+      v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 2, 1, 8);    // small-M 64 x 32
+    else
+      v = columns >= 3072u && !glu ? find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 4, 6, 2, 1)
+                                   : find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 4, 6, 1, 1);
+    if (v >= 0) plan = {v, 1u};
+  }
+  return plan;
 }
 
 // Applies a (variant, splits) choice: resizes the split-K workspace for the
@@ -728,13 +785,22 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   op->precision = d->precision;
   op->bits = bits;
   op->rows = d->rows;
+  hipDeviceProp_t prop;
+  int cus = 256;
+  if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
+    cus = prop.multiProcessorCount;
+  const bool glu = (d->flags & PK_GEMM_GLU) != 0;
+  // The plan comes first: the weight is prepared in the one layout the
+  // planned kernel reads (a shared prepared weight fixes it instead).
+  const Plan plan = plan_op(d->precision, d->rows, d->inner, d->columns, cus, glu,
+                            d->prepared ? d->prepared->parts : 0);
   if (d->prepared) {
     op->weight = const_cast<pk_prepared_weight*>(d->prepared);
     op->weight->refs.fetch_add(1);
   } else {
     pk_prepared_weight* w = nullptr;
-    if (int s = make_weight(ctx, label, bits, d->inner, d->columns, d->packed,
-                            stream_or_default(ctx, stream), &w, (d->flags & PK_GEMM_GLU) != 0)) {
+    if (int s = make_weight(ctx, label, bits, d->inner, d->columns, d->packed, stream_or_default(ctx, stream), &w,
+                            glu, variant_parts(d->precision, plan.variant))) {
       delete op;
       return s;
     }
@@ -744,7 +810,6 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   pk::GemmArgs& a = op->args;
   a.a = d->a;
   a.codes = op->weight->codes;
-  a.pair_codes = op->weight->pair_codes;
   a.palette = d->palette;
   a.out = d->output;
   a.bias = d->bias;
@@ -757,17 +822,8 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   a.palette_groups = d->palette_groups;
   a.palette_group_columns = d->palette_group_columns;
   a.palette_entries = 1u << bits;
-  a.glu = (d->flags & PK_GEMM_GLU) ? 1 : 0;
-  hipDeviceProp_t prop;
-  int cus = 256;
-  if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
-    cus = prop.multiProcessorCount;
+  a.glu = glu ? 1 : 0;
   a.splits = 1;
-  Plan plan = plan_launch(d->precision, d->rows, d->inner, d->columns, cus);
-  // The GLU epilogue lives in the pair-code kernels: small-M plans take
-  // their 64 x 64 tile.
-  if (a.glu && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
-    plan = {find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4), 1u};
   if (int st = configure_launch(op, plan.variant, plan.splits)) {
     weight_unref(op->weight);
     delete op;
@@ -832,6 +888,17 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
     return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
   if (op->args.glu && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no GLU epilogue", op->label.c_str(), variant);
+  // A variant that reads another split of the codes: an op alone on its
+  // weight moves it to that layout; a weight shared with other ops stays.
+  const int parts = variant_parts(op->precision, variant);
+  if (parts != op->weight->parts) {
+    if (!(op->weight->owner_released && op->weight->refs.load() == 1))
+      return fail(PK_RANGE_ERROR, "%s tile variant %d reads codes split into %d K parts; the shared prepared weight "
+                  "holds %d", op->label.c_str(), variant, parts, op->weight->parts);
+    PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+    if (int s = relayout_weight(op->weight, parts, op->ctx->stream)) return s;
+    op->args.codes = op->weight->codes;
+  }
   // Variants without a split-K path run unsplit.
   const bool splittable = op->precision == PK_PRECISION_F16 && pk::f16_variant_splits(variant);
   return configure_launch(op, variant, splittable ? op->splits : 1u);

@@ -33,6 +33,9 @@ inline int ok() { return PK_OK; }
 // with PK_DESTROYED.
 int check_ctx(const pk_context* ctx);
 
+// Device bytes of the prepared codes a GEMM op reads (its one layout).
+uint64_t gemm_weight_bytes(const pk_gemm_op* op);
+
 // Reference counting of contexts (see pk_context).
 pk_context* ctx_retain(pk_context* ctx);
 void ctx_release(pk_context* ctx);

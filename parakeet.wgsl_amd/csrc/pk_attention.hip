@@ -594,10 +594,12 @@ struct AttnVariant {
         rel_attention_f16_shared_kernel<NQ, false>, rel_attention_f16_shared_kernel<NQ, true>              \
   }
 
-// Index 0: up to 256 frames (key tiles split over the workgroup: most
-// workgroups, 14 us at 4 x 188); index 4: longer windows (K, V and one
-// position block per tile shared by 128 queries: 70 us at 4 x 750 against
-// 101 us for index 0).
+// Index 0: up to 256 frames while one round of its workgroups fills the
+// device (key tiles split over the workgroup: 13 us at 4 x 188, 12.6 us at
+// 1 x 188); index 1 up to a round and a half (21 us at 8 x 188 against 29 us
+// for index 0); index 4 beyond that and for longer windows (K, V and one
+// position block per tile shared by 128 queries: 28.5 us at 16 x 188
+// against 41.8 us for index 0, 77 us at 4 x 750 against 96 us).
 const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
                                     PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
 const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
@@ -605,7 +607,12 @@ const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_
 
 }  // namespace
 
-int attention_default_variant(bool f16, uint32_t frames) { return f16 && frames > 256u ? 4 : 0; }
+int attention_default_variant(bool f16, uint32_t frames, uint32_t batch) {
+  if (!f16) return 0;
+  if (frames > 256u) return 4;
+  const uint64_t workgroups = (uint64_t)batch * kHeads * ((frames + kTile - 1) / kTile);
+  return workgroups <= 256u ? 0 : workgroups <= 384u ? 1 : 4;
+}
 
 int attention_variant_count(bool f16) {
   return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0])) : 1;

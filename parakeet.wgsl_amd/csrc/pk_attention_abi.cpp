@@ -122,7 +122,7 @@ int pk_attention_create(pk_context* ctx, const pk_attention_desc* d, pk_attentio
   op->label = attention_label(d->label);
   op->precision = d->precision;
   op->batch = d->batch_size;
-  op->variant = pk::attention_default_variant(d->precision == PK_PRECISION_F16, d->frames);
+  op->variant = pk::attention_default_variant(d->precision == PK_PRECISION_F16, d->frames, d->batch_size);
   pk::AttnArgs& a = op->args;
   a.qkv = d->qkv;
   a.positions = d->projected_positions;

@@ -95,63 +95,101 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   }
 }
 
-// Reference format -> MFMA operand order (layout in pk_internal.h). One
-// thread per (block, lane); runs once per weight.
-template <int BITS>
-__global__ __launch_bounds__(kThreads) void operand_order_kernel(
-    const uint32_t* __restrict__ packed, uint32_t inner, uint32_t columns,
-    uint32_t k_blocks, uint64_t total_lanes, uint32_t* __restrict__ out) {
-  constexpr uint32_t CPG = codes_per_group(BITS);
-  constexpr uint32_t WPG = words_per_group(BITS);
-  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= total_lanes) return;
-  const uint32_t lane = (uint32_t)(t & 63u);
-  const uint64_t block = t >> 6;
-  const uint32_t nb = (uint32_t)(block / k_blocks);
-  const uint32_t kb = (uint32_t)(block % k_blocks);
-  const uint32_t n = nb * 32u + (lane & 31u);
-  const uint32_t k0 = kb * 64u + (lane >> 5) * 32u;
-  uint32_t w[BITS + 1];
+// A lane's 32 codes into its words of a block in the P-part layout
+// (pk_internal.h): P = 1 packs them LSB-first into BITS words (words 0-3
+// lane-interleaved as plane 0, the rest as plane 1); P = 2 or 4 stores the
+// 16-bit pair slots 4 * (c0 | c1 << BITS) of part p at [p][lane].
+template <int BITS, int P>
+__device__ __forceinline__ void store_lane_codes(const uint32_t (&code)[32], uint32_t* base, uint32_t lane) {
+  constexpr uint32_t PW = parts_words(BITS, P);
+  constexpr int PER = 32 / P;
 #pragma unroll
-  for (int q = 0; q <= BITS; ++q) w[q] = 0;
-#pragma unroll 4
-  for (uint32_t u = 0; u < 32u; ++u) {
-    const uint32_t k = k0 + u;
-    uint32_t code = 0;
-    if (k < inner && n < columns) {
-      const uint64_t scalar = (uint64_t)k * columns + n;
-      const uint64_t g = scalar / CPG;
-      const uint32_t bit = (uint32_t)(scalar % CPG) * BITS;
-      const uint32_t word = bit >> 5, shift = bit & 31u;
-      uint32_t value = packed[g * WPG + word] >> shift;
-      if (shift + BITS > 32u) value |= packed[g * WPG + word + 1] << (32u - shift);
-      code = value & ((1u << BITS) - 1u);
+  for (int p = 0; p < P; ++p) {
+    uint32_t w[PW + 1];
+#pragma unroll
+    for (uint32_t q = 0; q <= PW; ++q) w[q] = 0;
+    if constexpr (P > 1) {
+#pragma unroll
+      for (int e = 0; e < PER / 2; ++e)
+        w[e >> 1] |= (4u * (code[p * PER + 2 * e] | (code[p * PER + 2 * e + 1] << BITS))) << (16 * (e & 1));
+    } else {
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const uint32_t b = (uint32_t)u * BITS;
+        w[b >> 5] |= code[p * PER + u] << (b & 31u);
+        if ((b & 31u) + BITS > 32u) w[(b >> 5) + 1] |= code[p * PER + u] >> (32u - (b & 31u));
+      }
     }
-    const uint32_t b = u * BITS;
-    w[b >> 5] |= code << (b & 31u);
-    if ((b & 31u) + BITS > 32u) w[(b >> 5) + 1] |= code >> (32u - (b & 31u));
-  }
-  uint32_t* base = out + block * block_words(BITS);
-  reinterpret_cast<uint4*>(base)[lane] = make_uint4(w[0], w[1], w[2], w[3]);
-  if constexpr (BITS == 5) {
-    base[256 + lane] = w[4];
-  } else {
-    reinterpret_cast<uint2*>(base + 256)[lane] = make_uint2(w[4], w[5]);
+    if constexpr (P == 1) {
+      reinterpret_cast<uint4*>(base)[lane] = make_uint4(w[0], w[1], w[2], w[3]);
+      if constexpr (BITS == 5)
+        base[256 + lane] = w[4];
+      else
+        reinterpret_cast<uint2*>(base + 256)[lane] = make_uint2(w[4], w[5]);
+    } else {
+      uint32_t* dst = base + ((uint64_t)p * 64u + lane) * PW;
+#pragma unroll
+      for (uint32_t q = 0; q < PW; ++q) dst[q] = w[q];
+    }
   }
 }
 
-// Reference format -> pair-code layout (pk_internal.h). One thread per
-// (block, lane); runs once per weight. With glu_interleave the physical
-// column blocks alternate the two halves of the logical columns (GLU values,
-// then their gates).
-template <int BITS>
-__global__ __launch_bounds__(kThreads) void pair_code_kernel(
+// The inverse: a lane's 32 codes from its words of a block.
+template <int BITS, int P>
+__device__ __forceinline__ void load_lane_codes(const uint32_t* base, uint32_t lane, uint32_t (&code)[32]) {
+  constexpr uint32_t PW = parts_words(BITS, P);
+  constexpr int PER = 32 / P;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    uint32_t w[PW + 1];
+    if constexpr (P == 1) {
+      const uint4 v = reinterpret_cast<const uint4*>(base)[lane];
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
+      if constexpr (BITS == 5) {
+        w[4] = base[256 + lane];
+      } else {
+        const uint2 x = reinterpret_cast<const uint2*>(base + 256)[lane];
+        w[4] = x.x;
+        w[5] = x.y;
+      }
+    } else {
+      const uint32_t* src = base + ((uint64_t)p * 64u + lane) * PW;
+#pragma unroll
+      for (uint32_t q = 0; q < PW; ++q) w[q] = src[q];
+    }
+    w[PW] = 0;
+    if constexpr (P > 1) {
+#pragma unroll
+      for (int e = 0; e < PER / 2; ++e) {
+        const uint32_t field = ((w[e >> 1] >> (16 * (e & 1))) & 0xffffu) >> 2;
+        code[p * PER + 2 * e] = field & ((1u << BITS) - 1u);
+        code[p * PER + 2 * e + 1] = field >> BITS;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const uint32_t b = (uint32_t)u * BITS;
+        uint32_t v = w[b >> 5] >> (b & 31u);
+        if ((b & 31u) + BITS > 32u) v |= w[(b >> 5) + 1] << (32u - (b & 31u));
+        code[p * PER + u] = v & ((1u << BITS) - 1u);
+      }
+    }
+  }
+}
+
+// Reference format -> MFMA operand order with P parts (layout in
+// pk_internal.h). One thread per (block, lane); runs once per weight. With
+// glu_interleave the physical column blocks alternate the two halves of the
+// logical columns (GLU values, then their gates).
+template <int BITS, int P>
+__global__ __launch_bounds__(kThreads) void operand_order_kernel(
     const uint32_t* __restrict__ packed, uint32_t inner, uint32_t columns,
-    uint32_t k_blocks, uint64_t total_lanes, uint8_t* __restrict__ out, bool glu_interleave) {
+    uint32_t k_blocks, uint64_t total_lanes, uint32_t* __restrict__ out, bool glu_interleave) {
   constexpr uint32_t CPG = codes_per_group(BITS);
   constexpr uint32_t WPG = words_per_group(BITS);
-  constexpr uint32_t S = pair_table_side(BITS);
-  constexpr uint32_t PAD = 1u << BITS;
   const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
   if (t >= total_lanes) return;
   const uint32_t lane = (uint32_t)(t & 63u);
@@ -161,28 +199,35 @@ __global__ __launch_bounds__(kThreads) void pair_code_kernel(
   const uint32_t logical_nb = glu_interleave ? (nb & 1u) * (columns / 64u) + (nb >> 1) : nb;
   const uint32_t n = logical_nb * 32u + (lane & 31u);
   const uint32_t k0 = kb * 64u + (lane >> 5) * 32u;
-  auto code_at = [&](uint32_t k) -> uint32_t {
-    if (k >= inner || n >= columns) return PAD;
-    const uint64_t scalar = (uint64_t)k * columns + n;
-    const uint64_t g = scalar / CPG;
-    const uint32_t bit = (uint32_t)(scalar % CPG) * BITS;
-    const uint32_t word = bit >> 5, shift = bit & 31u;
-    uint32_t value = packed[g * WPG + word] >> shift;
-    if (shift + BITS > 32u) value |= packed[g * WPG + word + 1] << (32u - shift);
-    return value & ((1u << BITS) - 1u);
-  };
-  uint32_t w[8];
-#pragma unroll 4
-  for (uint32_t v = 0; v < 16u; ++v) {
-    const uint32_t pair = 4u * (code_at(k0 + 2u * v) + S * code_at(k0 + 2u * v + 1u));
-    if (v & 1u)
-      w[v >> 1] |= pair << 16;
-    else
-      w[v >> 1] = pair;
+  uint32_t code[32];
+#pragma unroll
+  for (uint32_t u = 0; u < 32u; ++u) {
+    const uint32_t k = k0 + u;
+    code[u] = 0;
+    if (k < inner && n < columns) {
+      const uint64_t scalar = (uint64_t)k * columns + n;
+      const uint64_t g = scalar / CPG;
+      const uint32_t bit = (uint32_t)(scalar % CPG) * BITS;
+      const uint32_t word = bit >> 5, shift = bit & 31u;
+      uint32_t value = packed[g * WPG + word] >> shift;
+      if (shift + BITS > 32u) value |= packed[g * WPG + word + 1] << (32u - shift);
+      code[u] = value & ((1u << BITS) - 1u);
+    }
   }
-  uint8_t* base = out + block * kPairBlockBytes + (uint64_t)lane * 16u;
-  reinterpret_cast<uint4*>(base)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  reinterpret_cast<uint4*>(base + 1024)[0] = make_uint4(w[4], w[5], w[6], w[7]);
+  store_lane_codes<BITS, P>(code, out + block * block_words(BITS, P), lane);
+}
+
+// One P-part layout -> another, one thread per (block, lane).
+template <int BITS, int PS, int PD>
+__global__ __launch_bounds__(kThreads) void relayout_kernel(const uint32_t* __restrict__ src,
+                                                            uint32_t* __restrict__ dst, uint64_t total_lanes) {
+  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= total_lanes) return;
+  const uint32_t lane = (uint32_t)(t & 63u);
+  const uint64_t block = t >> 6;
+  uint32_t code[32];
+  load_lane_codes<BITS, PS>(src + block * block_words(BITS, PS), lane, code);
+  store_lane_codes<BITS, PD>(code, dst + block * block_words(BITS, PD), lane);
 }
 
 inline dim3 grid_for(uint64_t items) {
@@ -237,32 +282,59 @@ hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* pa
 }
 
 hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
-                                   uint32_t columns, uint32_t* codes, hipStream_t stream) {
+                                   uint32_t columns, uint32_t* codes, hipStream_t stream, bool glu_interleave,
+                                   int parts) {
+  if (glu_interleave && columns % 64u != 0) return hipErrorInvalidValue;
+  if (bits != 5 && bits != 6) return hipErrorInvalidValue;
   const uint32_t k_blocks = padded_inner(inner) / 64u;
   const uint64_t blocks = (uint64_t)(padded_columns(columns) / 32u) * k_blocks;
   const uint64_t lanes = blocks * 64u;
-  if (bits == 5)
-    hipLaunchKernelGGL(operand_order_kernel<5>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes);
-  else
-    hipLaunchKernelGGL(operand_order_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid_for(lanes), dim3(kThreads), 0, stream, packed, inner, columns, k_blocks, lanes,
+                       codes, glu_interleave);
+  };
+  switch (parts * 10 + bits) {
+    case 15: go(operand_order_kernel<5, 1>); break;
+    case 16: go(operand_order_kernel<6, 1>); break;
+    case 25: go(operand_order_kernel<5, 2>); break;
+    case 26: go(operand_order_kernel<6, 2>); break;
+    case 45: go(operand_order_kernel<5, 4>); break;
+    case 46: go(operand_order_kernel<6, 4>); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
-                                uint32_t columns, uint8_t* codes, hipStream_t stream, bool glu_interleave) {
-  if (glu_interleave && columns % 64u != 0) return hipErrorInvalidValue;
-  const uint32_t k_blocks = padded_inner(inner) / 64u;
-  const uint64_t blocks = (uint64_t)(padded_columns(columns) / 32u) * k_blocks;
-  const uint64_t lanes = blocks * 64u;
-  if (bits == 5)
-    hipLaunchKernelGGL(pair_code_kernel<5>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes, glu_interleave);
-  else
-    hipLaunchKernelGGL(pair_code_kernel<6>, grid_for(lanes), dim3(kThreads), 0, stream, packed,
-                       inner, columns, k_blocks, lanes, codes, glu_interleave);
+namespace {
+template <int BITS, int PS>
+hipError_t relayout_from(const uint32_t* src, uint32_t* dst, int dst_parts, uint64_t lanes, hipStream_t stream) {
+  switch (dst_parts) {
+    case 1: hipLaunchKernelGGL((relayout_kernel<BITS, PS, 1>), grid_for(lanes), dim3(kThreads), 0, stream, src, dst, lanes); break;
+    case 2: hipLaunchKernelGGL((relayout_kernel<BITS, PS, 2>), grid_for(lanes), dim3(kThreads), 0, stream, src, dst, lanes); break;
+    case 4: hipLaunchKernelGGL((relayout_kernel<BITS, PS, 4>), grid_for(lanes), dim3(kThreads), 0, stream, src, dst, lanes); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
+}
+template <int BITS>
+hipError_t relayout_bits(const uint32_t* src, int src_parts, uint32_t* dst, int dst_parts, uint64_t lanes,
+                         hipStream_t stream) {
+  switch (src_parts) {
+    case 1: return relayout_from<BITS, 1>(src, dst, dst_parts, lanes, stream);
+    case 2: return relayout_from<BITS, 2>(src, dst, dst_parts, lanes, stream);
+    case 4: return relayout_from<BITS, 4>(src, dst, dst_parts, lanes, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+}  // namespace
+
+hipError_t launch_relayout(int bits, const uint32_t* src, int src_parts, uint32_t* dst, int dst_parts,
+                           uint64_t blocks, hipStream_t stream) {
+  const uint64_t lanes = blocks * 64u;
+  if (lanes == 0) return hipSuccess;
+  if (bits == 5) return relayout_bits<5>(src, src_parts, dst, dst_parts, lanes, stream);
+  if (bits == 6) return relayout_bits<6>(src, src_parts, dst, dst_parts, lanes, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace pk

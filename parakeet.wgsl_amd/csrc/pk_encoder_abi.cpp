@@ -168,10 +168,7 @@ int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStr
   d.activation = g.activation;
   if (validate_only) return pk_gemm_validate(&d);
   const int s = pk_gemm_create(e->ctx, &d, stream, op);
-  if (s == PK_OK) {
-    e->weight_bytes += pk::pair_code_bytes(g.inner, g.columns);
-    if (!(g.flags & PK_GEMM_GLU)) e->weight_bytes += pk::operand_order_words(g.bits, g.inner, g.columns) * 4u;
-  }
+  if (s == PK_OK) e->weight_bytes += gemm_weight_bytes(*op);
   return s;
 }
 

@@ -238,7 +238,7 @@ struct F16Variant {
 // Pair-code K-split tile shapes (pk_gemm_f16k.hip).
 int f16k_variant_count();
 const f16::F16Variant& f16k_variant(int index);
-hipError_t launch_gemm_f16k(const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
+hipError_t launch_gemm_f16k(int bits, const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
                             hipEvent_t start, hipEvent_t stop);
 
 // Small-M shapes (pk_gemm_f16s.hip).

@@ -337,7 +337,7 @@ hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStrea
                            hipEvent_t stop) {
   if (variant >= kLocal + f16k_variant_count())
     return launch_gemm_f16s(bits, variant_at(variant), args, stream, start, stop);
-  if (variant >= kLocal) return launch_gemm_f16k(variant_at(variant), args, stream, start, stop);
+  if (variant >= kLocal) return launch_gemm_f16k(bits, variant_at(variant), args, stream, start, stop);
   const F16Variant& v = variant_at(variant);
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;
   if (groups == 0) return hipSuccess;

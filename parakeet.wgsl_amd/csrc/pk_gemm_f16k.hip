@@ -15,12 +15,17 @@
 // wavefronts, not by all four; the KS partial tiles are added through LDS
 // at the end.
 //
-//   * codes: pair-code layout (pk_internal.h), one coalesced 8- or 16-byte
-//     load per lane and column block, CLA K blocks ahead. A 16-bit field is
-//     the LDS byte offset of a packed pair of palette entries, so one
-//     extract and one ds_read_b32 yield a whole operand register (two
-//     halves); the S x S pair table (S = 2^bits + 1) is built in LDS by
-//     each workgroup from the tile's palette.
+//   * codes: the operand-order layout split into KS parts (pk_internal.h):
+//     a wavefront of K part kp loads only its own part, one coalesced run
+//     per lane and column block (16 + 4/8 bytes with one part, 16 bytes with
+//     two, 8 with four), CLA K blocks ahead. With one part (the packed
+//     density) two K-adjacent codes are next to each other, so their
+//     2*bits-bit field c0 | c1 << bits, at a fixed bit, indexes a packed
+//     pair of palette entries: one extract (plus a funnel shift where the
+//     field crosses a word) and one ds_read_b32 yield a whole operand
+//     register (two halves); with two or four parts each pair is a 16-bit
+//     slot that already holds the entry's byte offset. The 2^bits x 2^bits
+//     pair table is built in LDS by each workgroup from the tile's palette.
 //   * activations: the BM x 64 tile of K block i+4 is loaded into registers
 //     while block i is multiplied and written to a ring of three LDS tiles
 //     at the end of block i+2; 16-byte chunks are XOR-swizzled with
@@ -55,7 +60,7 @@ namespace {
 using namespace f16;
 
 // Each staged palette group occupies 65 LDS entries: its 2^bits centroids
-// and zeros up to entry 64; entry 2^bits is the zero of K padding.
+// and zeros up to entry 64.
 constexpr int kLutStride = 65;
 constexpr uint32_t kLutStrideBytes = 2u * kLutStride;
 // LDS budget of the partial-tile exchange. The 96 x 128 tile (WN = KS = 2,
@@ -94,16 +99,17 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Instruction interleave of one sub-step (one scheduling region, fenced by
 // sched_barrier): the R*C MFMAs are spread over the region. The first two
 // thirds of the MFMA slots each carry an even share of the next sub-step's
-// LDS work - pair-offset extracts, palette-pair gathers and activation
-// fragment reads - so it issues in the shadow of the MFMA pipe and has the
-// last third of the region to land; the last third carries the VMEM loads
-// (sub-step 0) and the activation tile's LDS stores (last sub-step).
-template <int R, int C, int VMEM, int DSW>
+// LDS work - pair-offset extracts (VPP VALU per pair), palette-pair gathers
+// and activation fragment reads - so it issues in the shadow of the MFMA
+// pipe and has the last third of the region to land; the last third
+// carries the VMEM loads (sub-step 0) and the activation tile's LDS stores
+// (last sub-step).
+template <int R, int C, int VMEM, int DSW, int VPP>
 __device__ __forceinline__ void interleave_sub_step() {
   constexpr int NM = R * C;
   constexpr int NL = (2 * NM) / 3 > 0 ? (2 * NM) / 3 : 1;
   constexpr int NT = NM - NL > 0 ? NM - NL : 1;
-  constexpr int V_PER = (4 * C + NL - 1) / NL;
+  constexpr int V_PER = (4 * VPP * C + NL - 1) / NL;
   constexpr int D_PER = (4 * C + R + NL - 1) / NL;
   constexpr int M_PER = (VMEM + NT - 1) / NT;
   constexpr int W_PER = (DSW + NT - 1) / NT;
@@ -121,8 +127,9 @@ __device__ __forceinline__ void interleave_sub_step() {
 }
 
 // GENERAL: the tile's columns may span palette groups (per-lane palette
-// base) or K may be 32 (mod 64) (the last K block's upper half is zeroed).
-template <int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA>
+// base) or K may be 32 (mod 64) (the last K block's upper half is zeroed,
+// so the code-0 padding of the operand order multiplies zeros).
+template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA>
 __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int T = 256;
   constexpr int BM = 32 * R;
@@ -136,7 +143,12 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int EX_BYTES = PM * BLOCK_EX;
   constexpr int SMEM = EX_BYTES > 3 * A_BYTES ? EX_BYTES : 3 * A_BYTES;
   constexpr int GROUPS = GENERAL ? BN / 16 + 2 : 1;
-  constexpr int PAIRS = GENERAL ? 1 : 65 * 65;  // pair table of the tile's palette
+  constexpr uint32_t E = 1u << BITS;               // palette entries
+  constexpr int PAIRS = GENERAL ? 1 : (int)(E * E);  // pair table of the tile's palette
+  constexpr uint32_t BLOCK_WORDS = block_words(BITS, KS);
+  // 32-bit words of this wavefront's K part of one block.
+  constexpr int LW = (int)parts_words(BITS, KS);
+  constexpr uint32_t FIELD_MASK = (1u << (2 * BITS)) - 1u;
   static_assert(WN * KS == 4, "a workgroup is four wavefronts");
   static_assert(KS == 1 || KS == 2 || KS == 4, "K parts split the four sub-steps evenly");
   static_assert(BM * 8 % T == 0, "activation tile chunks must divide evenly");
@@ -179,15 +191,11 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   // Palettes of the tile's columns (palette-expander.ts:543-549).
   const uint32_t gc = args.palette_group_columns;
   const uint32_t G = args.palette_groups;
-  const uint32_t E = args.palette_entries;
   const uint32_t g_lo = min(n0 / gc, G - 1u);
   // Staged in the prologue, while the first global loads are in flight:
   // the palettes of the tile's groups and, for single-group tiles, the
-  // table of packed palette pairs, entry c0 + S*c1 = LUT[c0] | LUT[c1] << 16
-  // for S = 2^bits + 1 (entry 2^bits of a staged palette is the zero of K
-  // padding).
-  const uint32_t S = E + 1u;
-  const uint32_t pair_magic = ((1u << 20) + S - 1u) / S;  // p / S = p * pair_magic >> 20 for p < S*S
+  // table of packed palette pairs, entry c0 | c1 << bits = LUT[c0] |
+  // LUT[c1] << 16.
   auto stage_palettes = [&]() {
     const uint32_t g_hi = GENERAL ? min((min(n0 + BN, N) - 1u) / gc, G - 1u) : g_lo;
     const uint32_t entries = (g_hi - g_lo + 1u) * kLutStride;
@@ -200,10 +208,8 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       __syncthreads();
       const uint16_t* lut16 = reinterpret_cast<const uint16_t*>(lut_lds);
 #pragma unroll 4
-      for (uint32_t p = tid; p < S * S; p += T) {
-        const uint32_t c1 = (p * pair_magic) >> 20, c0 = p - c1 * S;
-        pair_lds[p] = (uint32_t)lut16[c0] | ((uint32_t)lut16[c1] << 16);
-      }
+      for (uint32_t p = tid; p < E * E; p += T)
+        pair_lds[p] = (uint32_t)lut16[p & (E - 1u)] | ((uint32_t)lut16[p >> BITS] << 16);
     }
   };
   const uint8_t* lut_bytes = reinterpret_cast<const uint8_t*>(lut_lds);
@@ -219,42 +225,41 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
     }
   }
 
-  // Pair codes of this wavefront's column blocks and K part. Blocks past
-  // the last column block re-read the last one (never stored).
-  typedef uint32_t Codes[C][2 * SPW];
+  // Codes of this wavefront's column blocks and K part. Blocks past the
+  // last column block re-read the last one (never stored).
+  typedef uint32_t Codes[C][LW];
   const uint32_t nb0 = n0 / 32u + (uint32_t)(wn * C);
-  uint32_t lane_off;
-  if constexpr (KS == 4)
-    lane_off = (uint32_t)((kp >> 1) * 1024 + lane * 16 + (kp & 1) * 8);
-  else if constexpr (KS == 2)
-    lane_off = (uint32_t)(kp * 1024 + lane * 16);
-  else
-    lane_off = (uint32_t)(lane * 16);
-  const uint8_t* code_base[C];
+  const uint32_t* code_base[C];
 #pragma unroll
   for (int ci = 0; ci < C; ++ci)
-    code_base[ci] = args.pair_codes + (uint64_t)min(nb0 + ci, NBT - 1u) * KB * kPairBlockBytes + lane_off;
+    code_base[ci] = args.codes + (uint64_t)min(nb0 + ci, NBT - 1u) * KB * BLOCK_WORDS;
   auto load_codes = [&](uint32_t kb, Codes& dst) {
 #pragma unroll
     for (int ci = 0; ci < C; ++ci) {
-      const uint8_t* p = code_base[ci] + (uint64_t)kb * kPairBlockBytes;
-      if constexpr (SPW == 1) {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        dst[ci][0] = v.x;
-        dst[ci][1] = v.y;
-      } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
+      const uint32_t* blk = code_base[ci] + (uint64_t)kb * BLOCK_WORDS;
+      if constexpr (KS == 1) {
+        const uint4 p0 = reinterpret_cast<const uint4*>(blk)[lane];
+        dst[ci][0] = p0.x;
+        dst[ci][1] = p0.y;
+        dst[ci][2] = p0.z;
+        dst[ci][3] = p0.w;
+        if constexpr (BITS == 5) {
+          dst[ci][4] = blk[256 + lane];
+        } else {
+          const uint2 p1 = reinterpret_cast<const uint2*>(blk + 256)[lane];
+          dst[ci][4] = p1.x;
+          dst[ci][5] = p1.y;
+        }
+      } else if constexpr (LW == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(blk + ((uint32_t)kp * 64u + (uint32_t)lane) * 4u);
         dst[ci][0] = v.x;
         dst[ci][1] = v.y;
         dst[ci][2] = v.z;
         dst[ci][3] = v.w;
-        if constexpr (SPW == 4) {
-          const uint4 w = *reinterpret_cast<const uint4*>(p + 1024);
-          dst[ci][4] = w.x;
-          dst[ci][5] = w.y;
-          dst[ci][6] = w.z;
-          dst[ci][7] = w.w;
-        }
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(blk + ((uint32_t)kp * 64u + (uint32_t)lane) * 2u);
+        dst[ci][0] = v.x;
+        dst[ci][1] = v.y;
       }
     }
   };
@@ -305,27 +310,46 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
     for (int mi = 0; mi < R; ++mi) dst[mi] = *reinterpret_cast<const half8*>(t + mi * 32 * kRowBytes);
   };
   // Weight fragment of local sub-step ls: register e of column block ci is
-  // the packed pair (halves 2e, 2e+1) at 16-bit value e of the sub-step's
-  // 8 bytes. Single-group tiles gather it whole from the pair table; GENERAL
-  // tiles split the pair offset into its two codes and gather each from
-  // the lane's own group palette.
-  auto gather = [&](const Codes& cw, int ls, half8 (&dst)[C]) {
+  // the packed pair (halves 2e, 2e+1) of codes 8 ls + 2e, + 1 of the
+  // wavefront's part, i.e. the 2*bits-bit field at bit 2 bits (4 ls + e)
+  // of its words (with one part: words 0-3 and 4(-5), contiguous), or with
+  // two or four parts the 16-bit slot 4 ls + e holding four times that
+  // field. Single-group
+  // tiles gather it whole from the pair table; GENERAL tiles split the
+  // field into its two codes and gather each from the lane's own group
+  // palette.
+  auto gather = [&](const Codes& cw, auto lsc, half8 (&dst)[C]) {
+    constexpr int ls = decltype(lsc)::value;
 #pragma unroll
     for (int ci = 0; ci < C; ++ci) {
       typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
       u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t off = (cw[ci][2 * ls + (e >> 1)] >> (16 * (e & 1))) & 0xffffu;
-        if constexpr (GENERAL) {
-          const uint32_t c1 = ((off >> 2) * pair_magic) >> 20, c0 = (off >> 2) - c1 * S;
-          const uint8_t* lut = lut_bytes + lut_base[ci];
-          w[e] = (uint32_t)*reinterpret_cast<const uint16_t*>(lut + 2u * c0) |
-                 ((uint32_t)*reinterpret_cast<const uint16_t*>(lut + 2u * c1) << 16);
+      static_for<4>([&](auto ec) {
+        constexpr int e = decltype(ec)::value;
+        uint32_t offset;  // 4 * field: the byte offset of the pair's table entry
+        if constexpr (KS > 1) {
+          // 16-bit pair slots that already hold the offset: slot 4 ls + e
+          constexpr int slot = 4 * ls + e;
+          offset = (cw[ci][slot >> 1] >> (16 * (slot & 1))) & 0xffffu;
         } else {
-          w[e] = *reinterpret_cast<const uint32_t*>(pair_bytes + off);
+          constexpr int bit = 2 * BITS * (4 * ls + e);
+          constexpr int wi = bit >> 5, sh = bit & 31;
+          uint32_t field;
+          if constexpr (sh + 2 * BITS <= 32)
+            field = (cw[ci][wi] >> sh) & FIELD_MASK;
+          else
+            field = __builtin_amdgcn_alignbit(cw[ci][wi + 1], cw[ci][wi], (uint32_t)sh) & FIELD_MASK;
+          offset = 4u * field;
         }
-      }
+        if constexpr (GENERAL) {
+          const uint32_t field = offset >> 2;
+          const uint8_t* lut = lut_bytes + lut_base[ci];
+          w[e] = (uint32_t)*reinterpret_cast<const uint16_t*>(lut + 2u * (field & (E - 1u))) |
+                 ((uint32_t)*reinterpret_cast<const uint16_t*>(lut + 2u * (field >> BITS)) << 16);
+        } else {
+          w[e] = *reinterpret_cast<const uint32_t*>(pair_bytes + offset);
+        }
+      });
       dst[ci] = __builtin_bit_cast(half8, w);
     }
   };
@@ -368,10 +392,10 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       }
       if constexpr (ls + 1 < SPW) {
         read_a(BUF, ls + 1, af[g ^ 1]);
-        gather(cs[I % NCS], ls + 1, bf[g ^ 1]);
+        gather(cs[I % NCS], std::integral_constant<int, ls + 1>{}, bf[g ^ 1]);
       } else {
         read_a((BUF + 1) % 3, 0, af[g ^ 1]);
-        gather(cs[(I + 1) % NCS], 0, bf[g ^ 1]);
+        gather(cs[(I + 1) % NCS], std::integral_constant<int, 0>{}, bf[g ^ 1]);
       }
 #pragma unroll
       for (int ci = 0; ci < C; ++ci)
@@ -380,7 +404,7 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
           acc[mi][ci] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[g][ci], af[g][mi], acc[mi][ci], 0, 0, 0);
       if constexpr (ls + 1 == SPW) store_a(min(i + 2u, last), (BUF + 2) % 3, sa[(I + 2) % 3]);
       if constexpr (SCHED) {
-        interleave_sub_step<R, C, ls == 0 ? CH + C * (SPW == 4 ? 2 : 1) : 0, ls + 1 == SPW ? CH : 0>();
+        interleave_sub_step<R, C, ls == 0 ? CH + C * (KS == 1 ? 2 : 1) : 0, ls + 1 == SPW ? CH : 0, KS == 1 ? 2 : 1>();
         if constexpr (ls + 1 < SPW) __builtin_amdgcn_sched_barrier(0);
       }
     });
@@ -398,7 +422,7 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   load_a(min(3u, last), sa[0]);
   __syncthreads();
   read_a(0, 0, af[0]);
-  gather(cs[0], 0, bf[0]);
+  gather(cs[0], std::integral_constant<int, 0>{}, bf[0]);
 
   uint32_t i = 0;
   for (; i + 6u <= KB; i += 6u) {
@@ -561,16 +585,16 @@ constexpr uint32_t kernel_lds_bytes() {
   constexpr int A_BYTES = 32 * R * kRowBytes;
   constexpr int BLOCK_EX = KS * WN * C * 4 * 64 * 16;
   constexpr int EX = pass_blocks(WN, KS, R, BLOCK_EX) * BLOCK_EX;
-  return (uint32_t)((EX > 3 * A_BYTES ? EX : 3 * A_BYTES) + kLutStride * 2 + 65 * 65 * 4);
+  return (uint32_t)((EX > 3 * A_BYTES ? EX : 3 * A_BYTES) + kLutStride * 2 + 64 * 64 * 4);
 }
 
-#define PK_F16K_VARIANT(WN, KS, R, C, S, CLA, TAG)                                                    \
-  F16Variant {                                                                                        \
-    TileShape{1, WN, R, C, KS}, "pk_gemm_f16p_b5_n" #WN "k" #KS "_m" #R "n" #C TAG,                   \
-        "pk_gemm_f16p_b6_n" #WN "k" #KS "_m" #R "n" #C TAG,                                           \
-        {gemm_f16k_kernel<WN, KS, R, C, false, S, CLA>, gemm_f16k_kernel<WN, KS, R, C, false, S, CLA>}, \
-        {gemm_f16k_kernel<WN, KS, R, C, true, S, CLA>, gemm_f16k_kernel<WN, KS, R, C, true, S, CLA>},   \
-        kernel_lds_bytes<WN, KS, R, C>()                                                              \
+#define PK_F16K_VARIANT(WN, KS, R, C, S, CLA, TAG)                                                          \
+  F16Variant {                                                                                              \
+    TileShape{1, WN, R, C, KS}, "pk_gemm_f16p_b5_n" #WN "k" #KS "_m" #R "n" #C TAG,                         \
+        "pk_gemm_f16p_b6_n" #WN "k" #KS "_m" #R "n" #C TAG,                                                 \
+        {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA>, gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA>}, \
+        {gemm_f16k_kernel<5, WN, KS, R, C, true, S, CLA>, gemm_f16k_kernel<6, WN, KS, R, C, true, S, CLA>},   \
+        kernel_lds_bytes<WN, KS, R, C>()                                                                    \
   }
 
 const F16Variant kVariants[] = {
@@ -582,6 +606,9 @@ const F16Variant kVariants[] = {
     PK_F16K_VARIANT(1, 4, 4, 2, true, 5, ""),  // 128 x 64
     PK_F16K_VARIANT(1, 4, 3, 2, true, 5, ""),  // 96 x 64
     PK_F16K_VARIANT(1, 4, 2, 2, true, 5, ""),  // 64 x 64
+    PK_F16K_VARIANT(4, 1, 6, 2, true, 2, ""),  // 192 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 4, 2, true, 2, ""),  // 128 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 3, 2, true, 5, ""),  // 96 x 256, no K split
 };
 
 }  // namespace
@@ -592,15 +619,15 @@ const f16::F16Variant& f16k_variant(int index) { return kVariants[index]; }
 // Launch of a byte-code tile variant: a 1-D grid of row tiles x column
 // tiles; the `single` kernel needs K % 64 == 0 and every tile inside one
 // palette group.
-hipError_t launch_gemm_f16k(const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
+hipError_t launch_gemm_f16k(int bits, const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
                             hipEvent_t start, hipEvent_t stop) {
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns);
   if (groups == 0) return hipSuccess;
   const bool single = (args.inner & 63u) == 0u &&
                       (args.palette_groups == 1 ||
                        args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
-  return launch_timed(single ? v.single[0] : v.general[0], dim3(groups), dim3(v.shape.threads()), stream, start,
-                      stop, args);
+  return launch_timed(single ? v.single[bits == 6] : v.general[bits == 6], dim3(groups), dim3(v.shape.threads()),
+                      stream, start, stop, args);
 }
 
 }  // namespace pk

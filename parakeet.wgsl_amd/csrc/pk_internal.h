@@ -24,32 +24,32 @@ __host__ __device__ constexpr uint32_t words_per_group(int bits) { return bits =
 // so a wavefront fetches a block with one coalesced 128-bit load plus one
 // 32/64-bit load per lane. Blocks are ordered [nb][kb], making the stream a
 // wavefront reads along K contiguous. K pads to 64 and N to 32 with code 0.
+//
+// Split into P parts (P = 2 or 4, for kernels whose workgroup splits each
+// K block over P wavefronts): a lane's 32 codes form P parts of 32 / P
+// K-consecutive codes, part p holding k = 64*kb + 32*h + 32p/P + u', in its
+// own parts_words(bits, P) words: each pair of codes (k even, k + 1) is a
+// 16-bit slot holding 4 * (c0 | c1 << bits), the byte offset of the pair's
+// entry in a 2^bits x 2^bits LDS table (one byte per weight). A block is
+// [part][lane][words], so the wavefront of part p reads one contiguous 16-
+// or 8-byte run per lane and nothing else, and decodes a pair with one
+// extract.
+//
+// A weight is prepared once in the one layout (P) its GEMM's kernel reads:
+// P = 1 at the packed format's density (5/8 or 6/8 byte per weight), P = 2
+// or 4 at one byte.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr uint32_t block_words(int bits) { return 64u * (uint32_t)bits; }
+__host__ __device__ constexpr uint32_t parts_words(int bits, int parts) {
+  return parts == 1 ? (uint32_t)bits : parts == 2 ? 4u : 2u;
+}
+__host__ __device__ constexpr uint32_t block_words(int bits, int parts = 1) {
+  return 64u * (uint32_t)parts * parts_words(bits, parts);
+}
 __host__ __device__ constexpr uint32_t padded_inner(uint32_t inner) { return (inner + 63u) / 64u * 64u; }
 __host__ __device__ constexpr uint32_t padded_columns(uint32_t columns) { return (columns + 31u) / 32u * 32u; }
-__host__ __device__ constexpr uint64_t operand_order_words(int bits, uint32_t inner, uint32_t columns) {
-  return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * block_words(bits);
-}
-
-// ---------------------------------------------------------------------------
-// Pair-code layout, built once per weight for the large-M f16 kernels.
-//
-// Same 64 k x 32 n blocks in [nb][kb] order, 2048 bytes each, holding one
-// 16-bit value per pair of K-adjacent codes (k even, k + 1) of a column:
-// the byte offset 4 * (c0 + S * c1) of their entry in an LDS table of
-// S x S packed f16 pairs, S = 2^bits + 1, where code 2^bits stands for K
-// padding (both palette halves zero). A block is [p][lane][16 bytes] for
-// sub-step pairs p = 0, 1: 16-bit value v (0..7) of lane l = 32*h + j in
-// pair p covers column n = 32*nb + j at k = 64*kb + 32*h + 16*p + 2*v and
-// k + 1, so the 8 codes one MFMA sub-step s needs are the 8-byte half
-// (s & 1) of pair s >> 1, and one ds_read_b32 gathers a packed pair of
-// operand halves.
-// ---------------------------------------------------------------------------
-constexpr uint32_t kPairBlockBytes = 2048u;
-__host__ __device__ constexpr uint32_t pair_table_side(int bits) { return (1u << bits) + 1u; }
-__host__ __device__ constexpr uint64_t pair_code_bytes(uint32_t inner, uint32_t columns) {
-  return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * kPairBlockBytes;
+__host__ __device__ constexpr uint64_t operand_order_words(int bits, uint32_t inner, uint32_t columns,
+                                                           int parts = 1) {
+  return (uint64_t)(padded_columns(columns) / 32u) * (padded_inner(inner) / 64u) * block_words(bits, parts);
 }
 
 enum Activation : int { kActNone = 0, kActSilu = 1, kActRelu = 2 };
@@ -57,7 +57,6 @@ enum Activation : int { kActNone = 0, kActSilu = 1, kActRelu = 2 };
 struct GemmArgs {
   const void* a;             // [M, K]
   const uint32_t* codes;     // operand-order codes
-  const uint8_t* pair_codes; // pair-code layout of the same weight
   const void* palette;       // [G, 2^bits]
   void* out;                 // [M, N]
   const float* bias;         // [N] or null
@@ -65,7 +64,7 @@ struct GemmArgs {
   float residual_scale;
   int activation;
   // GLU epilogue (pair-code kernels only): the weight's 32-column blocks
-  // alternate values and gates (launch_to_pair_codes with glu_interleave),
+  // alternate values and gates (launch_to_operand_order with glu_interleave),
   // and out is [M, N/2] = value * sigmoid(gate).
   int glu;
   uint32_t rows;             // active M
@@ -139,14 +138,16 @@ hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* pa
                          uint32_t inner, uint32_t columns, uint32_t group_columns,
                          uint32_t groups, const void* palette, void* target,
                          hipStream_t stream);
-hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
-                                   uint32_t columns, uint32_t* codes, hipStream_t stream);
 // glu_interleave: physical column block 2i takes logical block i (a GLU
 // value block) and block 2i+1 takes logical block N/64 + i (its gates);
-// needs N % 64 == 0.
-hipError_t launch_to_pair_codes(int bits, const uint32_t* packed, uint32_t inner,
-                                uint32_t columns, uint8_t* codes, hipStream_t stream,
-                                bool glu_interleave = false);
+// needs N % 64 == 0. `parts` selects the P-part split (1, 2 or 4).
+hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
+                                   uint32_t columns, uint32_t* codes, hipStream_t stream,
+                                   bool glu_interleave = false, int parts = 1);
+// The same codes moved from one P-part split to another (no packed source
+// needed); `blocks` = operand-order blocks of the weight.
+hipError_t launch_relayout(int bits, const uint32_t* src, int src_parts, uint32_t* dst, int dst_parts,
+                           uint64_t blocks, hipStream_t stream);
 
 // Fused palette GEMM. `variant` indexes f16_variants() / f32_variants().
 int f16_variant_count();
@@ -158,6 +159,11 @@ uint32_t f16_variant_lds_bytes(int index);
 enum F16Family : int { kFamilyOperandOrder = 0, kFamilyPairCode = 1, kFamilySmallM = 2 };
 int f16_variant_family(int index);
 inline bool f16_variant_splits(int index) { return f16_variant_family(index) == kFamilyOperandOrder; }
+// Parts of the code layout an f16 variant reads (pk_internal.h layout): its
+// K split for the pair-code family, 1 for every other kernel.
+inline int f16_variant_parts(int index) {
+  return f16_variant_family(index) == kFamilyPairCode ? f16_variant(index).k_split : 1;
+}
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream,
                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
@@ -216,9 +222,10 @@ struct AttnGeometry {
 };
 
 int attention_variant_count(bool f16);
-// Planned launch shape: key-split 32-query tiles up to 256 frames, shared
-// K/V/position tiles beyond.
-int attention_default_variant(bool f16, uint32_t frames);
+// Planned launch shape: key-split 32-query tiles for windows up to 256
+// frames while their workgroups fill about one round of the device, shared
+// K/V/position tiles beyond (longer windows or more windows).
+int attention_default_variant(bool f16, uint32_t frames, uint32_t batch);
 AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t batch);
 hipError_t launch_attention(bool f16, int variant, const AttnArgs& args, uint32_t batch, hipStream_t stream,
                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);

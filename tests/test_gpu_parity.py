@@ -184,19 +184,24 @@ def test_expansion_is_bit_exact(abi, ctx, scope, oracle, workloads, dtype, bits,
     np.testing.assert_array_equal(target.download().view(np.uint8), want.reshape(-1).view(np.uint8))
 
 
-@pytest.mark.parametrize("precision", ["f32", "f16", "f16-pair-codes", "f16-small-m"])
+@pytest.mark.parametrize("precision", ["f32", "f16", "f16-pair-codes", "f16-pair-codes-k1", "f16-pair-codes-k4",
+                                       "f16-small-m"])
 @pytest.mark.parametrize("bits,inner,columns,groups", [
     (5, 128, 256, 1), (6, 96, 48, 1), (6, 64, 3072, 3), (5, 160, 640, 1), (6, 32, 16, 1),
     (6, 128, 96, 3)])
 def test_prepared_operand_order_is_bit_exact(abi, ctx, scope, oracle, workloads, precision, bits, inner,
                                              columns, groups):
     """A = identity and LUT[g][c] = 64*g + c make the GEMM output each code
-    exactly, so this reads back the whole repack (operand order, or pair
-    codes for the K-split kernels) and the in-register decode bit for bit.
+    exactly, so this reads back the whole operand-order repack and every
+    family's in-register decode (the pair-table fields of the K-split
+    kernels included) bit for bit.
     (6, 128, 96, 3) puts three palette groups inside one pair-code tile."""
     variant = None
-    if precision == "f16-pair-codes":
-        variant = pair_code_variants(abi, ctx, scope, workloads)[0]
+    if precision.startswith("f16-pair-codes"):
+        # one K-split variant per code layout: 2 parts, 1 part, 4 parts
+        want = {"f16-pair-codes": 2, "f16-pair-codes-k1": 1, "f16-pair-codes-k4": 4}[precision]
+        names = variant_names(abi, ctx, scope, workloads)
+        variant = next(i for i in pair_code_variants(abi, ctx, scope, workloads) if k_split_of(names[i]) == want)
         precision = "f16"
     elif precision == "f16-small-m":
         variant = small_m_variants(abi, ctx, scope, workloads)[-1]
@@ -398,8 +403,8 @@ def test_prepared_weight_is_shared_and_outlives_its_owner(abi, ctx, scope, oracl
     w = workloads.palette_matrix(rng, 5, 256, 512)
     packed = scope.put(w.packed)
     prepared = abi.PreparedWeight(ctx, 5, 256, 512, packed, label="shared")
-    # operand-order codes (bits per code, as packed) + pair codes (16 bits per two codes)
-    assert prepared.nbytes() == 256 * 512 * 5 // 8 + 256 * 512
+    # one layout: operand-order codes, as many bits per code as the packed format
+    assert prepared.nbytes() == 256 * 512 * 5 // 8
     cases = [workloads.GemmCase(f"user{i}", workloads.normal(rng, (64 + 32 * i, 256)), w) for i in range(2)]
     outs, ops = [], []
     for case in cases:
