@@ -73,6 +73,10 @@ def parse_args():
                    choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
                             "rel-pos-mha", "encoder", "transcribe"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
+    p.add_argument("--windows", type=int, default=16,
+                   help="encoder / transcribe: windows the graph holds (40 is the reference's largest batch)")
+    p.add_argument("--active", type=int, default=0,
+                   help="encoder / transcribe: active windows of each pass (a prefix; 0 = all)")
     p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
@@ -443,9 +447,36 @@ def encoder_cpu_leg(stack, threads, budget_s, decoder):
     return leg, x0, front_s / layer_s, decode_s
 
 
+class ActivePrefix:
+    """The first `active` windows of an encoder stack, for the per-pass costs
+    of an active-prefix pass."""
+
+    def __init__(self, stack, active):
+        self.frames, self.batch = stack.frames, active
+        self.x = stack.x[:active * stack.frames]
+        self.valid = stack.valid[:active]
+        self.layers, self.subsampling = stack.layers, stack.subsampling
+        self.feature_frames = stack.feature_frames
+        self.projector, self.projector_bias = stack.projector, stack.projector_bias
+        self._stack = stack
+
+    def gemm_flops(self):
+        return self._stack.gemm_flops() * self.batch // self._stack.batch
+
+    def front_end_flops(self):
+        return self._stack.front_end_flops() * self.batch // self._stack.batch
+
+    def attention_flops(self):
+        live = np.minimum(self.valid.astype(np.int64), self.frames)
+        return int((live * live).sum()) * 8 * 128 * 2 * 3 * len(self.layers)
+
+
 def run_encoder(args, abi, ctx, decoder=False):
     import parakeet_wgsl_amd.workloads as wl
-    stack = wl.encoder_stack(0, windows=16, frames=188, layers=24, front_end=True, projector=True)
+    stack = wl.encoder_stack(0, windows=args.windows, frames=188, layers=24, front_end=True, projector=True)
+    active = args.active or stack.batch
+    if not 1 <= active <= stack.batch:
+        raise SystemExit(f"--active must be in [1, {stack.batch}]")
     held = []
 
     def put(array):
@@ -486,9 +517,9 @@ def run_encoder(args, abi, ctx, decoder=False):
                                flush_finals=put(np.ones(B, np.uint32)), batch_size=B, frames=T,
                                max_tokens=max_tokens, **tdt_out)
     for _ in range(args.warmup):
-        enc.enqueue(0, stream, graph=True)
+        enc.enqueue(active, stream, graph=True)
         if tdt:
-            tdt.enqueue(0, stream)
+            tdt.enqueue(active, stream)
     ctx.synchronize(stream)
 
     # Every TIMING_STRIDE-th pass runs eagerly with per-launch stamps; the
@@ -503,13 +534,13 @@ def run_encoder(args, abi, ctx, decoder=False):
     start.record(stream)
     for step in range(args.steps):
         if step in marks:
-            enc.enqueue_profiled(*marks[step], 0, stream)
+            enc.enqueue_profiled(*marks[step], active, stream)
             if tdt:
-                tdt.enqueue(0, stream, *tdt_marks[step])
+                tdt.enqueue(active, stream, *tdt_marks[step])
         else:
-            enc.enqueue(0, stream, graph=True)
+            enc.enqueue(active, stream, graph=True)
             if tdt:
-                tdt.enqueue(0, stream)
+                tdt.enqueue(active, stream)
     end.record(stream)
     end.synchronize()
     ctx.synchronize(stream)
@@ -522,7 +553,8 @@ def run_encoder(args, abi, ctx, decoder=False):
         durations[i] = [a.elapsed_ms(b) for a, b in zip(starts, ends)]
     durations = durations.mean(axis=0)  # ms per launch of the pass
     decoder_ms = float(np.mean([a.elapsed_ms(b) for a, b in tdt_marks.values()])) if tdt else None
-    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, stack)
+    run = ActivePrefix(stack, active)
+    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, run)
     nf, per = len(front_costs), len(abi.ENCODER_DISPATCHES)
     names = list(FRONT_DISPATCHES) + list(abi.ENCODER_DISPATCHES) + ["projector"] * len(projector_costs)
     costs = front_costs + layer_costs + projector_costs
@@ -554,7 +586,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     roofline["traffic"] = read_traffic(f"encoder-{name}", None)
     roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
 
-    total_flops = stack.gemm_flops() + stack.attention_flops() + stack.front_end_flops()
+    total_flops = run.gemm_flops() + run.attention_flops() + run.front_end_flops()
     cpu_decoder = None
     if tdt and not args.no_cpu:
         rng = np.random.default_rng(1)
@@ -564,14 +596,14 @@ def run_encoder(args, abi, ctx, decoder=False):
     decoded = None
     if tdt:
         meta = tdt_out["metadata"].download()
-        decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:stack.batch]],
-                   "overflow_windows": int((meta[stack.batch:] != 0).sum()),
+        decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:active]],
+                   "overflow_windows": int((meta[stack.batch:stack.batch + active] != 0).sum()),
                    "kernel": "tdt_team_kernel" if tdt.team_size() > 1 else "tdt_decode_kernel",
-                   "workgroups_per_window": tdt.team_size(), "workgroups": stack.batch * tdt.team_size(),
+                   "workgroups_per_window": tdt.team_size(), "workgroups": active * tdt.team_size(),
                    "max_tokens": 1024}
     dense = None
     if not args.no_dense:
-        rows = stack.batch * stack.frames
+        rows = active * stack.frames
         shapes = {"feed-forward1-linear1": (1024, 4096), "feed-forward1-linear2-residual": (4096, 1024),
                   "self-attention-qkv": (1024, 3072), "convolution-pointwise1": (1024, 2048),
                   "self-attention-output-residual": (1024, 1024)}
@@ -584,7 +616,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     ff_block = None if args.no_ff_block else ff_block_summary(abi, ctx, args)
     line = {
         "metric": METRIC,
-        "value": stack.batch * WINDOW_SECONDS / (ms_per_step * 1e-3),
+        "value": active * WINDOW_SECONDS / (ms_per_step * 1e-3),
         "unit": "audio-sec/sec",
         "n_gpus": 1,
         "steps": args.steps,
@@ -596,7 +628,7 @@ def run_encoder(args, abi, ctx, decoder=False):
         "dtype": "f16",
         "data": "synthetic (seeded random fbank, palette codes, LUTs, norms and biases)",
         "config": {"workload": "fastconformer-tdt-transcribe-fp16" if tdt else "fastconformer-encoder-fp16",
-                   "windows": stack.batch,
+                   "windows": active, "capacity_windows": stack.batch,
                    "window_seconds": WINDOW_SECONDS, "fbank_frames": stack.feature_frames, "mel_bins": 128,
                    "frames": stack.frames, "layers": len(stack.layers), "d_model": 1024, "ff_hidden": 4096,
                    "heads": 8, "subsampling": "dw_striding 8x, 256 channels", "projector": "1024->640",

@@ -224,7 +224,12 @@ int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,
    gemm.ts:971-1161). A prepared weight is checked against its own geometry
    only. */
 int pk_gemm_validate(const pk_gemm_desc *desc);
-/* Launch on `stream` for the first `active_rows` rows (0 = all rows). */
+/* Launch on `stream` for the first `active_rows` rows (0 = all rows). An f16
+   prefix is planned for its own row count (the reference re-plans the grid
+   per active batch, gemm.ts:427-451): among the tiles that read the codes
+   the op holds, so no extra layout is prepared; the choice is cached per op.
+   A prefix launched on another tile than the full rows may differ from the
+   full-rows result in the last bits (another K summation order). */
 int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
 /* pk_gemm_enqueue with the timestampWrites of GemmDispatch.encode
    (gemm.ts:419-463): the kernel's own dispatch stamps `start_event` when it
@@ -241,8 +246,11 @@ int pk_gemm_release(pk_gemm_op *op);
 
 /* Tuning hooks: the planner picks a compiled tile shape and a split-K
    factor at create time; these list and force the choice (used by the
-   benchmark's sweeps). Both resize the op's split-K workspace and must not
-   be called while a launch of the op is in flight. */
+   benchmark's sweeps) for every active row count. Both resize the op's
+   split-K workspace, and a variant that reads another split of the codes
+   re-lays the op's own weight out on the device (PK_RANGE_ERROR for a
+   weight shared with other ops); neither may be called while a launch of
+   the op is in flight. */
 int pk_gemm_variant_count(int precision);
 /* Selecting a variant without a split-K path (the f16 pair-code K-split
    variants, every f32 variant) also resets the split count to 1. */

@@ -112,6 +112,13 @@ struct pk_gemm_op {
   pk_prepared_weight* weight = nullptr;
   int variant = 0;
   uint32_t splits = 1;
+  int cus = 256;
+  // A variant chosen by pk_gemm_set_variant / pk_gemm_set_splits runs at
+  // every active row count; otherwise an active prefix is re-planned among
+  // the kernels that read the weight's layout (the last choice cached).
+  bool forced = false;
+  uint32_t active_rows_planned = 0;
+  int active_variant = 0;
   // Split-K workspace: f32 partial tiles, then one counter per tile.
   void* workspace = nullptr;
   uint64_t workspace_bytes = 0;
@@ -344,17 +351,38 @@ Plan plan_op(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int
   if (glu && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
     plan = {find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4), 1u};
   if (required_parts && variant_parts(precision, plan.variant) != required_parts) {
-    int v = -1;
-    if (required_parts == 2)
-      v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 2, 3, 2, 2);  // 96 x 128
-    else if (required_parts == 4)
-      v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4);  // 64 x 64
-    else if (!glu && rows <= 256u)
-      v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 2, 1, 8);    // small-M 64 x 32
-    else
-      v = columns >= 3072u && !glu ? find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 4, 6, 2, 1)
-                                   : find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 4, 6, 1, 1);
-    if (v >= 0) plan = {v, 1u};
+    if (required_parts == 1 && !glu && (rows <= 64u || (rows <= 256u && inner >= 2048u))) {
+      const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 2, 1, 8);  // small-M 64 x 32
+      if (v >= 0) return {v, 1u};
+    }
+    // The tiles that read this layout, by (rounds of workgroups) x (time of
+    // one workgroup at K = 1024: measured for the tiles the unrestricted plan
+    // uses, scaled by tile area for the others).
+    struct Tile {
+      int wn, ks, r, c;
+      double us;
+    };
+    constexpr Tile kTiles[] = {
+        {4, 1, 6, 2, 28.5}, {4, 1, 4, 2, 20.0}, {4, 1, 3, 2, 16.0}, {4, 1, 6, 1, 20.0},  // one part
+        {2, 2, 6, 2, 22.3}, {2, 2, 4, 2, 17.2}, {2, 2, 3, 2, 14.8}, {2, 2, 6, 1, 14.0},  // two parts
+        {1, 4, 4, 2, 13.0}, {1, 4, 3, 2, 11.0}, {1, 4, 2, 2, 9.3},                       // four parts
+    };
+    int best = -1;
+    double best_us = 1e300;
+    for (const Tile& t : kTiles) {
+      if (t.ks != required_parts) continue;
+      const int v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, t.wn, t.r, t.c, t.ks);
+      if (v < 0) continue;
+      const pk::TileShape s = pk::f16_variant(v);
+      if (glu && (s.tile_columns() / 32) % 2 != 0) continue;
+      const uint64_t tiles = (uint64_t)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
+      const double us = (double)((tiles + cus - 1) / cus) * t.us;
+      if (us < best_us * 0.98) {
+        best_us = us;
+        best = v;
+      }
+    }
+    if (best >= 0) plan = {best, 1u};
   }
   return plan;
 }
@@ -790,6 +818,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
     cus = prop.multiProcessorCount;
   const bool glu = (d->flags & PK_GEMM_GLU) != 0;
+  op->cus = cus;
   // The plan comes first: the weight is prepared in the one layout the
   // planned kernel reads (a shared prepared weight fixes it instead).
   const Plan plan = plan_op(d->precision, d->rows, d->inner, d->columns, cus, glu,
@@ -837,6 +866,25 @@ int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
   return pk_gemm_enqueue_timed(op, active_rows, stream, nullptr, nullptr);
 }
 
+// The variant that runs `rows` active rows: the op's own (planned at its
+// row capacity, or forced), or for an f16 prefix the plan of that row count
+// among the kernels that read the weight's layout (the reference re-plans
+// the grid of one pipeline, gemm.ts:427-451; here the tile may change too).
+int planned_variant(const pk_gemm_op* op, uint32_t rows) {
+  if (op->forced || rows == op->rows || op->precision != PK_PRECISION_F16) return op->variant;
+  return plan_op(op->precision, rows, op->args.inner, op->args.columns, op->cus, op->args.glu != 0, op->weight->parts)
+      .variant;
+}
+
+int variant_for_rows(pk_gemm_op* op, uint32_t rows) {
+  if (op->forced || rows == op->rows || op->precision != PK_PRECISION_F16) return op->variant;
+  if (rows != op->active_rows_planned) {
+    op->active_variant = planned_variant(op, rows);
+    op->active_rows_planned = rows;
+  }
+  return op->active_variant;
+}
+
 int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, void* start_event, void* end_event) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
@@ -844,6 +892,7 @@ int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, vo
   // GemmDispatch.encode (gemm.ts:427-438)
   if (rows > op->rows)
     return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
+  const int variant = variant_for_rows(op, rows);
   pk::GemmArgs args = op->args;
   args.rows = rows;
   // A split never gets an empty K range.
@@ -852,8 +901,8 @@ int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, vo
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
   hipEvent_t start = static_cast<hipEvent_t>(start_event), stop = static_cast<hipEvent_t>(end_event);
   const hipError_t e = op->precision == PK_PRECISION_F16
-                           ? pk::launch_gemm_f16(op->bits, op->variant, args, st, start, stop)
-                           : pk::launch_gemm_f32(op->bits, op->variant, args, st, start, stop);
+                           ? pk::launch_gemm_f16(op->bits, variant, args, st, start, stop)
+                           : pk::launch_gemm_f32(op->bits, variant, args, st, start, stop);
   PK_HIP(e, "palette GEMM launch");
   return ok();
 }
@@ -901,7 +950,9 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
   }
   // Variants without a split-K path run unsplit.
   const bool splittable = op->precision == PK_PRECISION_F16 && pk::f16_variant_splits(variant);
-  return configure_launch(op, variant, splittable ? op->splits : 1u);
+  if (int s = configure_launch(op, variant, splittable ? op->splits : 1u)) return s;
+  op->forced = true;
+  return ok();
 }
 
 int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
@@ -910,7 +961,9 @@ int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
   const uint32_t limit = op->precision == PK_PRECISION_F16 ? k_blocks(op->args.inner) : 1u;
   if (splits < 1 || splits > limit)
     return fail(PK_RANGE_ERROR, "%s split count %u outside [1, %u]", op->label.c_str(), splits, limit);
-  return configure_launch(op, op->variant, splits);
+  if (int s = configure_launch(op, op->variant, splits)) return s;
+  op->forced = true;
+  return ok();
 }
 
 int pk_gemm_variant_count(int precision) {
@@ -924,7 +977,8 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   if (rows > op->rows)
     return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
   const bool f16 = op->precision == PK_PRECISION_F16;
-  const pk::TileShape s = f16 ? pk::f16_variant(op->variant) : pk::f32_variant(op->variant);
+  const int variant = planned_variant(op, rows);
+  const pk::TileShape s = f16 ? pk::f16_variant(variant) : pk::f32_variant(variant);
   std::memset(info, 0, sizeof *info);
   const uint32_t splits = std::min(op->splits, k_blocks(op->args.inner));
   if (f16) {
@@ -942,7 +996,7 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   info->workspace_bytes = op->workspace_bytes;
   const uint32_t elem = f16 ? 2u : 4u;
   if (f16) {
-    info->lds_bytes = pk::f16_variant_lds_bytes(op->variant);
+    info->lds_bytes = pk::f16_variant_lds_bytes(variant);
   } else {
     const uint32_t lut_cap = (s.tile_columns() / 16u + 2u) * (1u << op->bits);
     info->lds_bytes = 2u * s.tile_rows() * 256u + lut_cap * elem;
@@ -956,7 +1010,7 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   if (op->args.residual) bytes += M * N * elem;
   info->algorithmic_bytes = bytes;
   std::snprintf(info->kernel, sizeof info->kernel, "%s",
-                f16 ? pk::f16_variant_name(op->bits, op->variant) : pk::f32_variant_name(op->bits, op->variant));
+                f16 ? pk::f16_variant_name(op->bits, variant) : pk::f32_variant_name(op->bits, variant));
   return ok();
 }
 
