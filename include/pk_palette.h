@@ -226,10 +226,10 @@ int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,
 int pk_gemm_validate(const pk_gemm_desc *desc);
 /* Launch on `stream` for the first `active_rows` rows (0 = all rows). An f16
    prefix is planned for its own row count (the reference re-plans the grid
-   per active batch, gemm.ts:427-451): among the tiles that read the codes
-   the op holds, so no extra layout is prepared; the choice is cached per op.
-   A prefix launched on another tile than the full rows may differ from the
-   full-rows result in the last bits (another K summation order). */
+   per active batch, gemm.ts:427-451): the tile shape may change, but not the
+   kernel family or K split, so the codes the op holds serve it and a
+   prefix's outputs are bit-identical to the same rows of a full launch; the
+   choice is cached per op. */
 int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
 /* pk_gemm_enqueue with the timestampWrites of GemmDispatch.encode
    (gemm.ts:419-463): the kernel's own dispatch stamps `start_event` when it

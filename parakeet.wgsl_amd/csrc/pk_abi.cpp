@@ -341,6 +341,38 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
   return {best, 1u};
 }
 
+// The pair-code tile with K split `ks` (the layout of that many parts) that
+// takes `rows` x `columns` in the least (rounds of workgroups) x (time of one
+// workgroup at K = 1024: measured for the tiles the unrestricted plan uses,
+// scaled by tile area for the others); -1 if none.
+int best_pair_tile(uint32_t rows, uint32_t columns, int cus, bool glu, int ks) {
+  struct Tile {
+    int wn, ks, r, c;
+    double us;
+  };
+  constexpr Tile kTiles[] = {
+      {4, 1, 6, 2, 28.5}, {4, 1, 4, 2, 20.0}, {4, 1, 3, 2, 16.0}, {4, 1, 6, 1, 20.0},  // one part
+      {2, 2, 6, 2, 22.3}, {2, 2, 4, 2, 17.2}, {2, 2, 3, 2, 14.8}, {2, 2, 6, 1, 14.0},  // two parts
+      {1, 4, 4, 2, 13.0}, {1, 4, 3, 2, 11.0}, {1, 4, 2, 2, 9.3},                       // four parts
+  };
+  int best = -1;
+  double best_us = 1e300;
+  for (const Tile& t : kTiles) {
+    if (t.ks != ks) continue;
+    const int v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, t.wn, t.r, t.c, t.ks);
+    if (v < 0) continue;
+    const pk::TileShape s = pk::f16_variant(v);
+    if (glu && (s.tile_columns() / 32) % 2 != 0) continue;
+    const uint64_t tiles = (uint64_t)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
+    const double us = (double)((tiles + cus - 1) / cus) * t.us;
+    if (us < best_us * 0.98) {
+      best_us = us;
+      best = v;
+    }
+  }
+  return best;
+}
+
 // The plan of one op: plan_launch, with a GLU epilogue moved to the
 // pair-code kernels (small-M plans take their 64 x 64 tile), and with a
 // shared prepared weight restricted to the tiles that read the layout it
@@ -355,34 +387,8 @@ Plan plan_op(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int
       const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 2, 1, 8);  // small-M 64 x 32
       if (v >= 0) return {v, 1u};
     }
-    // The tiles that read this layout, by (rounds of workgroups) x (time of
-    // one workgroup at K = 1024: measured for the tiles the unrestricted plan
-    // uses, scaled by tile area for the others).
-    struct Tile {
-      int wn, ks, r, c;
-      double us;
-    };
-    constexpr Tile kTiles[] = {
-        {4, 1, 6, 2, 28.5}, {4, 1, 4, 2, 20.0}, {4, 1, 3, 2, 16.0}, {4, 1, 6, 1, 20.0},  // one part
-        {2, 2, 6, 2, 22.3}, {2, 2, 4, 2, 17.2}, {2, 2, 3, 2, 14.8}, {2, 2, 6, 1, 14.0},  // two parts
-        {1, 4, 4, 2, 13.0}, {1, 4, 3, 2, 11.0}, {1, 4, 2, 2, 9.3},                       // four parts
-    };
-    int best = -1;
-    double best_us = 1e300;
-    for (const Tile& t : kTiles) {
-      if (t.ks != required_parts) continue;
-      const int v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, t.wn, t.r, t.c, t.ks);
-      if (v < 0) continue;
-      const pk::TileShape s = pk::f16_variant(v);
-      if (glu && (s.tile_columns() / 32) % 2 != 0) continue;
-      const uint64_t tiles = (uint64_t)pk::tiles_m(s, rows) * pk::tiles_n(s, columns);
-      const double us = (double)((tiles + cus - 1) / cus) * t.us;
-      if (us < best_us * 0.98) {
-        best_us = us;
-        best = v;
-      }
-    }
-    if (best >= 0) plan = {best, 1u};
+    const int v = best_pair_tile(rows, columns, cus, glu, required_parts);
+    if (v >= 0) plan = {v, 1u};
   }
   return plan;
 }
@@ -870,10 +876,17 @@ int pk_gemm_enqueue(pk_gemm_op* op, uint32_t active_rows, void* stream) {
 // row capacity, or forced), or for an f16 prefix the plan of that row count
 // among the kernels that read the weight's layout (the reference re-plans
 // the grid of one pipeline, gemm.ts:427-451; here the tile may change too).
+// A prefix keeps the op's kernel family and K split, so every row is summed
+// over K in the same order as in a full-rows launch and the prefix's outputs
+// are bit-identical to the same rows of the full launch: only a pair-code
+// tile shape changes (the small-M and operand-order kernels take any row
+// count as they are).
 int planned_variant(const pk_gemm_op* op, uint32_t rows) {
-  if (op->forced || rows == op->rows || op->precision != PK_PRECISION_F16) return op->variant;
-  return plan_op(op->precision, rows, op->args.inner, op->args.columns, op->cus, op->args.glu != 0, op->weight->parts)
-      .variant;
+  if (op->forced || rows == op->rows || op->precision != PK_PRECISION_F16 ||
+      pk::f16_variant_family(op->variant) != pk::kFamilyPairCode)
+    return op->variant;
+  const int v = best_pair_tile(rows, op->args.columns, op->cus, op->args.glu != 0, pk::f16_variant(op->variant).k_split);
+  return v >= 0 ? v : op->variant;
 }
 
 int variant_for_rows(pk_gemm_op* op, uint32_t rows) {

@@ -570,3 +570,39 @@ def test_feed_forward_block_graph_replay_matches_eager(abi, ctx, workloads):
     finally:
         for a in held:
             a.free()
+
+
+@pytest.mark.parametrize("rows,inner,columns,bits,active", [
+    (3008, 1024, 4096, 5, 188),    # FF expand: 192 x 256 tile at full rows, a smaller one for one window
+    (3008, 4096, 1024, 5, 376),    # FF contract: two-part K split at both row counts
+    (3008, 1024, 1024, 6, 752),    # output projection, 6-bit
+])
+def test_active_prefix_is_replanned_and_bit_identical(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits,
+                                                      active):
+    """An active prefix runs the tile planned for its own row count (the
+    reference re-plans per active batch, gemm.ts:427-451) within the op's
+    kernel family and K split, so its rows are bit-identical to the same rows
+    of a full launch, and the rows past the prefix stay untouched."""
+    case = workloads.gemm_case(61, rows, inner, columns, bits, activation="silu" if columns == 4096 else "none")
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    full = scope.put(np.zeros((rows, columns), np.float16))
+    prefix = scope.put(np.full((rows, columns), 7.0, np.float16))
+    ops = [abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=o, bits=bits, rows=rows, inner=inner,
+                      columns=columns, activation=case.activation, label="active-prefix") for o in (full, prefix)]
+    try:
+        plan_full, plan_prefix = ops[0].plan(0), ops[1].plan(active)
+        print("full:", plan_full.kernel.decode(), list(plan_full.grid), "prefix:", plan_prefix.kernel.decode(),
+              list(plan_prefix.grid), flush=True)
+        assert k_split_of(plan_full.kernel.decode()) == k_split_of(plan_prefix.kernel.decode())
+        ops[0].enqueue(0)
+        ops[1].enqueue(active)
+        ctx.synchronize()
+    finally:
+        for op in ops:
+            op.release()
+    got_full, got_prefix = full.download(), prefix.download()
+    np.testing.assert_array_equal(got_prefix[:active].view(np.uint16), got_full[:active].view(np.uint16))
+    assert (got_prefix[active:] == np.float16(7.0)).all()
+    sub = workloads.GemmCase("prefix", case.a[:active], w, activation=case.activation)
+    assert_f16_parity(oracle, got_prefix[:active], sub)
