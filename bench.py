@@ -19,6 +19,10 @@ Other workloads (for profiling; same JSON shape):
   ff-block          the feed-forward block above as the step, TFLOP/s
   single-gemm-fp32  X[256x1024] f32 x 6-bit W 1024->4096 + bias
   small-m           5-bit 1024->4096 f16 GEMM at --rows M (HBM-bound regime)
+  weight-stream     every palette GEMM of the 24 encoder layers (192 distinct
+                    weights, 365 MB packed) at --rows M: one grouped small-M
+                    launch per step (value, GB/s), and the same GEMMs as 192
+                    single launches replayed from a HIP graph
   conv-module       Conformer convolution module, fp16, 16 windows x 188 x 1024:
                     P = X PW1 (6-bit 1024->2048), Z = SiLU(BN(DW9(GLU(P)))),
                     Y = X + Z PW2 (6-bit 1024->1024); TFLOP/s counts the two
@@ -70,14 +74,14 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="encoder",
-                   choices=["ff-block", "single-gemm-fp32", "small-m", "conv-module", "conv-module-fused",
-                            "rel-pos-mha", "encoder", "transcribe"])
+                   choices=["ff-block", "single-gemm-fp32", "small-m", "weight-stream", "conv-module",
+                            "conv-module-fused", "rel-pos-mha", "encoder", "transcribe"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
     p.add_argument("--windows", type=int, default=16,
                    help="encoder / transcribe: windows the graph holds (40 is the reference's largest batch)")
     p.add_argument("--active", type=int, default=0,
                    help="encoder / transcribe: active windows of each pass (a prefix; 0 = all)")
-    p.add_argument("--rows", type=int, default=64, help="M for --workload small-m")
+    p.add_argument("--rows", type=int, default=64, help="M for --workload small-m and weight-stream")
     p.add_argument("--cpu-sample-rows", type=int, default=0,
                    help="rows of the CPU-oracle sample (0 = workload default)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -656,6 +660,191 @@ def run_encoder(args, abi, ctx, decoder=False):
     ctx.close()
 
 
+WEIGHT_STREAM_EPILOGUES = {"ff1_linear1": ("silu", None), "ff2_linear1": ("silu", None),
+                           "ff1_linear2": ("none", 0.5), "ff2_linear2": ("none", 0.5),
+                           "o_proj": ("none", 1.0), "pointwise2": ("none", 1.0)}
+
+
+def copy_bandwidth(ctx, nbytes=1 << 30, reps=10):
+    """Device-to-device copy (pk_copy_device = hipMemcpyAsync) of `nbytes`:
+    read + write bytes per second, the box's own streaming ceiling."""
+    src, dst = ctx.empty((nbytes // 2,), np.float16), ctx.empty((nbytes // 2,), np.float16)
+    try:
+        for _ in range(2):
+            ctx.copy(dst, src)
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.synchronize()
+        e0.record()
+        for _ in range(reps):
+            ctx.copy(dst, src)
+        e1.record()
+        e1.synchronize()
+        return 2.0 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    finally:
+        src.free()
+        dst.free()
+
+
+def run_weight_stream(args, abi, ctx):
+    """Every palette GEMM of the 24-layer encoder (8 per layer: 192 distinct
+    weights, 365 MB of packed codes, more than the 256 MB last-level cache)
+    at --rows rows: the small-M weight-streaming regime. Two steps are timed:
+    the 192 GEMMs as one grouped small-M launch (pk_gemm_group), and the 192
+    GEMMs as single launches, each on its planned kernel, replayed from a HIP
+    graph (a batch-1 pass launches them one by one)."""
+    import parakeet_wgsl_amd.workloads as wl
+    rows = args.rows
+    rng = np.random.default_rng(0)
+    held = []
+
+    def put(host):
+        held.append(ctx.array(np.ascontiguousarray(host)))
+        return held[-1]
+    x_host, h_host = wl.normal(rng, (rows, 1024), 1.0), wl.normal(rng, (rows, 4096), 1.0)
+    x, h = put(x_host), put(h_host)
+    grouped, single, host_layer0 = [], [], []
+    flops = nbytes = packed_bytes = 0
+    for layer in range(24):
+        for name, (bits, inner, columns, groups) in wl.ENCODER_MATRICES.items():
+            words = wl.random_packed_words(rng, bits, inner, columns)
+            palette_host = wl.normal(rng, (groups, 1 << bits), 0.02)
+            if layer == 0:
+                host_layer0.append((name, bits, inner, columns, words, palette_host))
+            packed, palette = put(words), put(palette_host)
+            activation, scale = WEIGHT_STREAM_EPILOGUES.get(name, ("none", None))
+            a = x if inner == 1024 else h
+            for ops in (grouped, single):
+                out = ctx.empty((rows, columns), np.float16)
+                held.append(out)
+                ops.append(abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=bits, rows=rows,
+                                      inner=inner, columns=columns, residual=x if scale is not None else None,
+                                      residual_scale=scale, activation=activation, label=f"layer{layer}-{name}"))
+            packed_bytes += words.nbytes
+            flops += 2 * rows * inner * columns
+            nbytes += gemm_cost(rows, inner, columns, bits, groups, residual=scale is not None)[1] - 2 * rows * inner
+    # every GEMM reads one of two activation inputs, which count once
+    nbytes += 2 * rows * (1024 + 4096)
+    small = abi.small_m_variants()
+    for op in grouped:
+        op.set_variant(small[0])  # the small-M code layout (one K part) that group members read
+    group = abi.GemmGroup(ctx, grouped, label="encoder-weights")
+    if args.variant >= 0:
+        group.set_variant(args.variant)
+    for op in grouped:
+        op.release()
+    stream = ctx.stream
+
+    # grouped: one launch per step, each stamped by its own dispatch
+    for _ in range(args.warmup):
+        group.enqueue(0, stream)
+    marks = [(ctx.event(), ctx.event()) for _ in range(args.steps)]
+    start, end = ctx.event(), ctx.event()
+    ctx.synchronize(stream)
+    start.record(stream)
+    for s, e in marks:
+        group.enqueue(0, stream, s, e)
+    end.record(stream)
+    end.synchronize()
+    group_ms = start.elapsed_ms(end) / args.steps
+    kernel_ms = float(np.mean([s.elapsed_ms(e) for s, e in marks]))
+    plan = group.plan()
+
+    # single launches: the 192 GEMMs captured into one graph per step
+    for _ in range(2):
+        for op in single:
+            op.enqueue(0, stream)
+    graph = abi.Graph.capture(ctx, stream)
+    with graph:
+        for op in single:
+            op.enqueue(0, stream)
+    for _ in range(args.warmup):
+        graph.launch()
+    ctx.synchronize(stream)
+    start.record(stream)
+    for _ in range(args.steps):
+        graph.launch()
+    end.record(stream)
+    end.synchronize()
+    single_ms = start.elapsed_ms(end) / args.steps
+    single_kernels = sorted({op.plan().kernel.decode() for op in single})
+
+    copy_gbs = copy_bandwidth(ctx)
+    gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+    compute_s, memory_s = flops / (PEAK_TFLOPS["f16"] * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)
+    if compute_s >= memory_s:
+        tflops = flops / (kernel_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS["f16"], "unit": "TFLOP/s",
+                    "frac": tflops / PEAK_TFLOPS["f16"]}
+    else:
+        roofline = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}
+    roofline["kernel"] = plan.kernel.decode()
+    roofline["traffic"] = read_traffic(f"weight-stream-{rows}", plan.kernel.decode())
+    roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = weight_stream_cpu_baseline(host_layer0, x_host, h_host, rows, all_threads())
+        cpu["single_thread"] = weight_stream_cpu_baseline(host_layer0, x_host, h_host, rows, 1, budget_s=5.0)
+        cpu["host"] = host_info()
+    line = {
+        "metric": METRIC,
+        "value": nbytes / (group_ms * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": group_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random palette codes, LUTs and activations)",
+        "config": {"workload": "encoder-weight-stream-fp16", "rows": rows, "layers": 24,
+                   "gemms": len(single), "matrices_per_layer": list(wl.ENCODER_MATRICES),
+                   "packed_weight_bytes": packed_bytes, "algorithmic_bytes": nbytes, "flops": flops,
+                   "cache_note": "the 192 distinct weights (365 MB packed) exceed the 256 MB last-level cache; "
+                                 "each step streams every weight once"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "grouped": {"kernel": plan.kernel.decode(), "grid": list(plan.grid), "block": plan.block_threads,
+                    "kernel_us": kernel_ms * 1e3, "gbs": gbs, "frac_of_copy": gbs / copy_gbs,
+                    "tflops": flops / (kernel_ms * 1e-3) / 1e12},
+        "single_launches": {"ms_per_step": single_ms, "gbs": nbytes / (single_ms * 1e-3) / 1e9,
+                            "launches": len(single), "kernels": single_kernels, "graph_replay": True},
+        "copy_gbs": copy_gbs,
+        "copy_note": "hipMemcpyAsync device-to-device of 1 GiB, read + write bytes",
+        "device": ctx.info().name.decode(),
+    }
+    print(json.dumps(line), flush=True)
+    graph.release()
+    group.release()
+    for op in single:
+        op.release()
+    for arr in held:
+        arr.free()
+    ctx.close()
+
+
+def weight_stream_cpu_baseline(host_layer0, x, h, rows, threads, budget_s=10.0):
+    """The oracle (reference fp16 semantics) on layer 0's eight GEMMs at the
+    same rows, GEMM after GEMM until about `budget_s` seconds have passed:
+    algorithmic bytes per second."""
+    from oracle import pko
+    done_bytes, done = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or done == 0:
+        name, bits, inner, columns, words, palette = host_layer0[done % len(host_layer0)]
+        activation, scale = WEIGHT_STREAM_EPILOGUES.get(name, ("none", None))
+        a = x if inner == 1024 else h
+        pko.gemm(a, words, bits, palette, columns, activation=activation,
+                 residual=x if scale is not None else None, residual_scale=scale, mode="f16-chain", threads=threads)
+        done_bytes += gemm_cost(rows, inner, columns, bits, palette.shape[0], residual=scale is not None)[1]
+        done += 1
+    dt = time.perf_counter() - t0
+    return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{done} GEMMs of layer 0's eight at {rows} rows (f16-accumulator chain)", "seconds": dt}
+
+
 def gemm_tflops(dispatches):
     """Palette-GEMM TFLOP/s over the pass: every palette GEMM launch's FLOP
     over the sum of their stamped durations."""
@@ -838,6 +1027,9 @@ def main():
     ctx = abi.Context(0)
     if args.workload in ("encoder", "transcribe"):
         run_encoder(args, abi, ctx, decoder=args.workload == "transcribe")
+        return
+    if args.workload == "weight-stream":
+        run_weight_stream(args, abi, ctx)
         return
     held = []
 

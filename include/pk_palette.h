@@ -90,6 +90,7 @@ typedef enum pk_activation {
 typedef struct pk_context pk_context;
 typedef struct pk_gemm_op pk_gemm_op;
 typedef struct pk_prepared_weight pk_prepared_weight;
+typedef struct pk_gemm_group pk_gemm_group;
 
 /* ---- library / context --------------------------------------------------- */
 
@@ -252,6 +253,17 @@ int pk_gemm_release(pk_gemm_op *op);
    weight shared with other ops); neither may be called while a launch of
    the op is in flight. */
 int pk_gemm_variant_count(int precision);
+typedef struct pk_gemm_variant_desc {
+  uint32_t tile_rows;
+  uint32_t tile_columns;
+  uint32_t block_threads;
+  uint32_t k_split;     /* wavefronts that share each output tile over K */
+  uint32_t code_parts;  /* K parts of the prepared code layout it reads */
+  int32_t groupable;    /* 1: a pk_gemm_group can run it */
+  char kernel5[64];     /* kernel name for 5-bit and 6-bit weights */
+  char kernel6[64];
+} pk_gemm_variant_desc;
+int pk_gemm_variant_describe(int precision, int variant, pk_gemm_variant_desc *desc);
 /* Selecting a variant without a split-K path (the f16 pair-code K-split
    variants, every f32 variant) also resets the split count to 1. */
 int pk_gemm_set_variant(pk_gemm_op *op, int variant);
@@ -275,6 +287,44 @@ typedef struct pk_gemm_plan_info {
 /* Plan of the launch pk_gemm_enqueue would make for `active_rows`. */
 int pk_gemm_plan(const pk_gemm_op *op, uint32_t active_rows,
                  pk_gemm_plan_info *info);
+
+/* ---- GEMM groups ----------------------------------------------------------
+
+   No counterpart in the reference, which dispatches one GEMM at a time. For
+   callers with many independent GEMMs of few rows (a batch-1 stream's
+   projections that do not feed each other, every layer's rel-pos linear of
+   one window length, weight-streaming servers): one launch of the small-M
+   kernel runs them all, so the per-launch latency is paid once and the
+   weight streams of all members overlap on the device.
+
+   A group holds a snapshot of its members' bindings (input, output, bias,
+   residual, palette, epilogue) taken at create; members run concurrently,
+   so no member may read a buffer another member writes. Members must be
+   f16 ops without the GLU epilogue whose prepared weights hold the codes in
+   one K part (the layout of the small-M kernels: an op planned on them, or
+   switched to one with pk_gemm_set_variant); PK_RANGE_ERROR names the first
+   member that is not. The group keeps each member's prepared weight alive;
+   the ops themselves may be released, and a member op's weight can no
+   longer be re-laid out by pk_gemm_set_variant while the group lives. At
+   most 65535 members of at most 2,097,152 columns each. */
+int pk_gemm_group_create(pk_context *ctx, pk_gemm_op *const *ops, uint32_t count,
+                         const char *label, pk_gemm_group **out);
+/* Launches every member on its first `active_rows` rows (0 = the smallest
+   row capacity among the members; PK_RANGE_ERROR above it). */
+int pk_gemm_group_enqueue(pk_gemm_group *group, uint32_t active_rows, void *stream);
+int pk_gemm_group_enqueue_timed(pk_gemm_group *group, uint32_t active_rows, void *stream,
+                                void *start_event, void *end_event);
+/* Forces one small-M variant (an index of pk_gemm_variant_count(F16)) for
+   every row count, or -1 to return to the planned one; PK_RANGE_ERROR for a
+   variant of another kernel family. */
+int pk_gemm_group_set_variant(pk_gemm_group *group, int variant);
+/* The launch pk_gemm_group_enqueue would make: grid, tile, LDS, the
+   members' summed flops and algorithmic bytes, and the kernel name. */
+int pk_gemm_group_plan(const pk_gemm_group *group, uint32_t active_rows,
+                       pk_gemm_plan_info *info);
+/* Waits for the context's stream, frees the group's tables, drops its
+   weight references and frees the handle, which must not be used again. */
+int pk_gemm_group_destroy(pk_gemm_group *group);
 
 /* ---- expansion and unpack (bit-exact reference semantics) ---------------- */
 

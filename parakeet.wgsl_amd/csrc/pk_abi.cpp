@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "pk_abi_internal.h"
 #include "pk_internal.h"
@@ -223,6 +224,28 @@ pk::TileShape shape_of(int precision, int variant) {
 
 uint32_t k_blocks(uint32_t inner) { return (inner + 63u) / 64u; }
 
+// Column-group widths (blocks of 32 columns) a GEMM group keeps item lists
+// for: those of the small-M variants.
+constexpr uint32_t kGroupWidths[3] = {1u, 2u, 4u};
+
+int group_width_index(uint32_t column_blocks) {
+  for (int i = 0; i < 3; ++i)
+    if (kGroupWidths[i] == column_blocks) return i;
+  return -1;
+}
+
+// Compulsory HBM bytes of one launch over `rows` rows: the packed codes at
+// the format's density, the palettes, A, the output (+ bias, residual).
+uint64_t algorithmic_bytes(const pk::GemmArgs& a, int bits, uint64_t rows, uint32_t elem) {
+  const uint64_t K = a.inner, N = a.columns;
+  uint64_t bytes = (K * N * (uint64_t)bits + 7u) / 8u;
+  bytes += (uint64_t)a.palette_groups * (1u << bits) * elem;
+  bytes += rows * K * elem + rows * (a.glu ? N / 2u : N) * elem;
+  if (a.bias) bytes += 4u * N;
+  if (a.residual) bytes += rows * N * elem;
+  return bytes;
+}
+
 // Split-K workspace: `splits` f32 partial tiles per output tile, then one
 // u32 arrival counter per output tile (256-byte aligned).
 uint64_t workspace_bytes_for(const pk::TileShape& s, uint32_t rows, uint32_t columns, uint32_t splits) {
@@ -254,9 +277,12 @@ int find_variant(int precision, int family, int waves_m, int waves_n, int m_bloc
 // Launch planner. The f16 choice follows MI355X measurements of every
 // compiled tile shape over the encoder's GEMM shapes (M 1..3008, K
 // 1024/4096, N 1024..4096, the rel-pos linear's 2T-1 rows). Up to 64 rows,
-// and up to 256 rows of a deep-K (K >= 2048) GEMM, the small-M kernel
-// (32-row blocks, K round robin over eight wavefronts) wins; up to 256 rows
-// otherwise the 64 x 64 pair-code tile; deep-K shapes take 96 x 64 while
+// and up to 256 rows of a deep-K (K >= 2048) or at most 1024 columns wide
+// GEMM, the small-M kernel (32-row blocks, K round robin over eight
+// wavefronts) wins (output projection at 188 rows: 5.96 us against 7.88 us
+// for the 64 x 64 pair-code tile); up to 256 rows otherwise the 64 x 64
+// pair-code tile (FF expand at 188 rows: 8.30 us against 8.84 us for the
+// best small-M shape); deep-K shapes take 96 x 64 while
 // those fill the chip and 96 x 128 beyond. Every other shape takes the
 // candidate with the least (rounds of workgroups) x (measured time of one
 // workgroup), which puts 192 x 128 on the FF expand and convolution PW1,
@@ -278,7 +304,13 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
       const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 1, 8);
       return {v < 0 ? 0 : v, 1u};
     }
-    if (rows <= 256u) return {pair_variant(1, 2, 2, 4), 1u};
+    if (rows <= 256u) {
+      if (columns <= 1024u) {
+        const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 1, 8);
+        if (v >= 0) return {v, 1u};
+      }
+      return {pair_variant(1, 2, 2, 4), 1u};
+    }
     if (inner >= 2048u) return {tiles(96, 64) <= wave ? pair_variant(1, 3, 2, 4) : pair_variant(2, 3, 2, 2), 1u};
     // K < 2048: the fewest rounds of workgroups times the measured time of one
     // workgroup of each tile at K = 1024 with one workgroup per compute unit.
@@ -983,6 +1015,30 @@ int pk_gemm_variant_count(int precision) {
   return precision == PK_PRECISION_F16 ? pk::f16_variant_count() : pk::f32_variant_count();
 }
 
+int pk_gemm_variant_describe(int precision, int variant, pk_gemm_variant_desc* desc) {
+  if (!desc) return fail(PK_INVALID_ARGUMENT, "argument is null");
+  if (precision != PK_PRECISION_F16 && precision != PK_PRECISION_F32)
+    return fail(PK_INVALID_ARGUMENT, "unsupported precision %d", precision);
+  const bool f16 = precision == PK_PRECISION_F16;
+  const int count = f16 ? pk::f16_variant_count() : pk::f32_variant_count();
+  if (variant < 0 || variant >= count)
+    return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
+  const pk::TileShape s = shape_of(precision, variant);
+  std::memset(desc, 0, sizeof *desc);
+  desc->tile_rows = s.tile_rows();
+  desc->tile_columns = s.tile_columns();
+  desc->block_threads = s.threads();
+  desc->k_split = s.k_split;
+  desc->code_parts = variant_parts(precision, variant);
+  desc->groupable = f16 && pk::f16_variant_family(variant) == pk::kFamilySmallM &&
+                    group_width_index((uint32_t)s.n_blocks) >= 0;
+  std::snprintf(desc->kernel5, sizeof desc->kernel5, "%s",
+                f16 ? pk::f16_variant_name(5, variant) : pk::f32_variant_name(5, variant));
+  std::snprintf(desc->kernel6, sizeof desc->kernel6, "%s",
+                f16 ? pk::f16_variant_name(6, variant) : pk::f32_variant_name(6, variant));
+  return ok();
+}
+
 int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* info) {
   if (!op || !info) return fail(PK_INVALID_ARGUMENT, "argument is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
@@ -995,7 +1051,7 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   std::memset(info, 0, sizeof *info);
   const uint32_t splits = std::min(op->splits, k_blocks(op->args.inner));
   if (f16) {
-    info->grid[0] = pk::tiles_m(s, rows) * pk::tiles_n(s, op->args.columns) * splits;
+    info->grid[0] = pk::f16_variant_grid(variant, rows, op->args.columns, splits);
     info->grid[1] = 1;
   } else {
     info->grid[0] = pk::tiles_n(s, op->args.columns);
@@ -1014,16 +1070,213 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
     const uint32_t lut_cap = (s.tile_columns() / 16u + 2u) * (1u << op->bits);
     info->lds_bytes = 2u * s.tile_rows() * 256u + lut_cap * elem;
   }
-  const uint64_t M = rows, K = op->args.inner, N = op->args.columns;
-  info->flops = 2ull * M * K * N;
-  uint64_t bytes = (K * N * (uint64_t)op->bits + 7u) / 8u;
-  bytes += (uint64_t)op->args.palette_groups * (1u << op->bits) * elem;
-  bytes += M * K * elem + M * (op->args.glu ? N / 2u : N) * elem;
-  if (op->args.bias) bytes += 4u * N;
-  if (op->args.residual) bytes += M * N * elem;
-  info->algorithmic_bytes = bytes;
+  info->flops = 2ull * rows * op->args.inner * op->args.columns;
+  info->algorithmic_bytes = algorithmic_bytes(op->args, op->bits, rows, elem);
   std::snprintf(info->kernel, sizeof info->kernel, "%s",
                 f16 ? pk::f16_variant_name(op->bits, variant) : pk::f32_variant_name(op->bits, variant));
+  return ok();
+}
+
+}  // extern "C"
+
+// A group of independent f16 GEMMs run by one small-M launch. Device table:
+// the members' launch arguments, then one item list per column-group width
+// of the small-M variants (1, 2 and 4 blocks of 32 columns).
+struct pk_gemm_group {
+  pk_abi::CtxRef ctx;
+  std::string label;
+  std::vector<pk_prepared_weight*> weights;  // one reference each
+  std::vector<pk::SmallMMember> members;
+  uint32_t capacity = 0;
+  int forced = -1;
+  void* table = nullptr;
+  uint32_t* items[3] = {};
+  uint32_t items_count[3] = {};
+};
+
+namespace {
+
+// The small-M variant a group runs: K over four wavefronts, each reusing
+// its activation fragments over four column blocks, code loads four K
+// blocks ahead. Measured on MI355X over the encoder's 192 weights (365 MB)
+// against every other small-M shape at 16, 64 and 188 rows, it was the
+// fastest at each (16 rows: 105 us; 64 rows, two row groups whose second
+// code read hits L2: 202 us; 188 rows: 534 us).
+int plan_group(uint32_t rows) {
+  (void)rows;
+  const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 4, 4);
+  return v < 0 ? find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 1, 8) : v;
+}
+
+int group_variant(const pk_gemm_group* g, uint32_t rows) { return g->forced >= 0 ? g->forced : plan_group(rows); }
+
+}  // namespace
+
+extern "C" {
+
+int pk_gemm_group_create(pk_context* ctx, pk_gemm_op* const* ops, uint32_t count, const char* label,
+                         pk_gemm_group** out) {
+  if (int s = check_ctx(ctx)) return s;
+  if (!out || !ops) return fail(PK_INVALID_ARGUMENT, "argument is null");
+  *out = nullptr;
+  const char* name = label ? label : "palette-gemm-group";
+  if (count == 0 || count > 65535u)
+    return fail(PK_RANGE_ERROR, "%s member count %u outside [1, 65535]", name, count);
+  uint32_t capacity = UINT32_MAX;
+  for (uint32_t i = 0; i < count; ++i) {
+    const pk_gemm_op* op = ops[i];
+    if (!op) return fail(PK_INVALID_ARGUMENT, "%s member %u is null", name, i);
+    if (op->destroyed) return fail(PK_DESTROYED, "%s member %u (%s) was destroyed", name, i, op->label.c_str());
+    if (op->ctx != ctx)
+      return fail(PK_INVALID_ARGUMENT, "%s member %u (%s) belongs to another context", name, i, op->label.c_str());
+    if (op->precision != PK_PRECISION_F16 || op->args.glu)
+      return fail(PK_RANGE_ERROR, "%s member %u (%s) is not an f16 GEMM without GLU epilogue", name, i,
+                  op->label.c_str());
+    if (op->weight->parts != 1)
+      return fail(PK_RANGE_ERROR,
+                  "%s member %u (%s) holds codes split into %d K parts; group members need the small-M "
+                  "layout (one part)",
+                  name, i, op->label.c_str(), op->weight->parts);
+    if (pk::padded_columns(op->args.columns) / 32u > 65536u)
+      return fail(PK_RANGE_ERROR, "%s member %u (%s) has more than 65536 column blocks", name, i,
+                  op->label.c_str());
+    capacity = std::min(capacity, op->rows);
+  }
+  auto* g = new pk_gemm_group();
+  g->ctx = ctx;
+  g->label = name;
+  g->capacity = capacity;
+  for (uint32_t i = 0; i < count; ++i) {
+    pk::SmallMMember m{};
+    m.args = ops[i]->args;
+    m.args.splits = 1;
+    m.args.partials = nullptr;
+    m.args.counters = nullptr;
+    m.bits = ops[i]->bits;
+    g->members.push_back(m);
+    ops[i]->weight->refs.fetch_add(1);
+    g->weights.push_back(ops[i]->weight);
+  }
+  // Items: deepest K first (their workgroups run longest), then member and
+  // column group order.
+  std::vector<uint32_t> order(count);
+  for (uint32_t i = 0; i < count; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+    return g->members[x].args.inner > g->members[y].args.inner;
+  });
+  std::vector<uint32_t> lists[3];
+  for (int w = 0; w < 3; ++w) {
+    for (uint32_t i : order) {
+      const uint32_t groups = (pk::padded_columns(g->members[i].args.columns) / 32u + kGroupWidths[w] - 1u) /
+                              kGroupWidths[w];
+      for (uint32_t cg = 0; cg < groups; ++cg) lists[w].push_back(i << 16 | cg);
+    }
+    g->items_count[w] = (uint32_t)lists[w].size();
+  }
+  const uint64_t member_bytes = (uint64_t)count * sizeof(pk::SmallMMember);
+  uint64_t bytes = (member_bytes + 255u) / 256u * 256u;
+  uint64_t at[3];
+  for (int w = 0; w < 3; ++w) {
+    at[w] = bytes;
+    bytes += ((uint64_t)g->items_count[w] * 4u + 255u) / 256u * 256u;
+  }
+  auto release = [&](int status) {
+    for (pk_prepared_weight* w : g->weights) weight_unref(w);
+    if (g->table) (void)hipFree(g->table);
+    delete g;
+    return status;
+  };
+  if (hipSetDevice(ctx->device) != hipSuccess) return release(fail(PK_DEVICE_ERROR, "hipSetDevice failed"));
+  hipError_t e = hipMalloc(&g->table, bytes);
+  if (e != hipSuccess) {
+    g->table = nullptr;
+    return release(fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of group tables: %s", name,
+                        (unsigned long long)bytes, hipGetErrorString(e)));
+  }
+  auto* base = static_cast<uint8_t*>(g->table);
+  e = hipMemcpy(base, g->members.data(), member_bytes, hipMemcpyHostToDevice);
+  for (int w = 0; w < 3 && e == hipSuccess; ++w) {
+    g->items[w] = reinterpret_cast<uint32_t*>(base + at[w]);
+    e = hipMemcpy(g->items[w], lists[w].data(), (uint64_t)g->items_count[w] * 4u, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess)
+    return release(fail(PK_DEVICE_ERROR, "%s: group table upload failed: %s", name, hipGetErrorString(e)));
+  *out = g;
+  return ok();
+}
+
+int pk_gemm_group_enqueue(pk_gemm_group* group, uint32_t active_rows, void* stream) {
+  return pk_gemm_group_enqueue_timed(group, active_rows, stream, nullptr, nullptr);
+}
+
+int pk_gemm_group_enqueue_timed(pk_gemm_group* g, uint32_t active_rows, void* stream, void* start_event,
+                                void* end_event) {
+  if (!g) return fail(PK_INVALID_ARGUMENT, "GEMM group is null");
+  if (int s = check_ctx(g->ctx)) return s;
+  const uint32_t rows = active_rows ? active_rows : g->capacity;
+  if (rows > g->capacity)
+    return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", g->label.c_str(), g->capacity);
+  const int variant = group_variant(g, rows);
+  const pk::TileShape s = pk::f16_variant(variant);
+  const int w = group_width_index((uint32_t)s.n_blocks);
+  if (w < 0) return fail(PK_INTERNAL_ERROR, "%s: variant %d has no group item list", g->label.c_str(), variant);
+  pk::SmallMGroupArgs args{};
+  args.members = static_cast<const pk::SmallMMember*>(g->table);
+  args.items = g->items[w];
+  args.items_count = g->items_count[w];
+  args.rows = rows;
+  args.row_groups = pk::tiles_m(s, rows);
+  PK_HIP(hipSetDevice(g->ctx->device), "hipSetDevice");
+  PK_HIP(pk::launch_gemm_f16_group(variant, args, stream_or_default(g->ctx, stream),
+                                   static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(end_event)),
+         "palette GEMM group launch");
+  return ok();
+}
+
+int pk_gemm_group_set_variant(pk_gemm_group* g, int variant) {
+  if (!g) return fail(PK_INVALID_ARGUMENT, "GEMM group is null");
+  if (variant == -1) {
+    g->forced = -1;
+    return ok();
+  }
+  if (variant < 0 || variant >= pk::f16_variant_count() || pk::f16_variant_family(variant) != pk::kFamilySmallM ||
+      group_width_index((uint32_t)pk::f16_variant(variant).n_blocks) < 0)
+    return fail(PK_RANGE_ERROR, "%s: variant %d is not a small-M variant", g->label.c_str(), variant);
+  g->forced = variant;
+  return ok();
+}
+
+int pk_gemm_group_plan(const pk_gemm_group* g, uint32_t active_rows, pk_gemm_plan_info* info) {
+  if (!g || !info) return fail(PK_INVALID_ARGUMENT, "argument is null");
+  const uint32_t rows = active_rows ? active_rows : g->capacity;
+  if (rows > g->capacity)
+    return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", g->label.c_str(), g->capacity);
+  const int variant = group_variant(g, rows);
+  const pk::TileShape s = pk::f16_variant(variant);
+  const int w = group_width_index((uint32_t)s.n_blocks);
+  std::memset(info, 0, sizeof *info);
+  info->grid[0] = pk::small_m_grid(s, w < 0 ? 0u : g->items_count[w], rows);
+  info->grid[1] = info->grid[2] = 1;
+  info->block_threads = s.threads();
+  info->tile_rows = s.tile_rows();
+  info->tile_columns = s.tile_columns();
+  info->split_inner = 1;
+  info->lds_bytes = pk::f16_variant_lds_bytes(variant);
+  for (const pk::SmallMMember& m : g->members) {
+    info->flops += 2ull * rows * m.args.inner * m.args.columns;
+    info->algorithmic_bytes += algorithmic_bytes(m.args, m.bits, rows, 2u);
+  }
+  std::snprintf(info->kernel, sizeof info->kernel, "%s", pk::f16_group_kernel_name(variant));
+  return ok();
+}
+
+int pk_gemm_group_destroy(pk_gemm_group* g) {
+  if (!g) return ok();
+  (void)hipSetDevice(g->ctx->device);
+  (void)hipStreamSynchronize(g->ctx->stream);
+  if (g->table) (void)hipFree(g->table);
+  for (pk_prepared_weight* w : g->weights) weight_unref(w);
+  delete g;
   return ok();
 }
 

@@ -246,5 +246,8 @@ int f16s_variant_count();
 const f16::F16Variant& f16s_variant(int index);
 hipError_t launch_gemm_f16s(int bits, const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
                             hipEvent_t start, hipEvent_t stop);
+const char* f16s_group_name(int index);
+hipError_t launch_gemm_f16s_group(int index, const SmallMGroupArgs& group, hipStream_t stream, hipEvent_t start,
+                                  hipEvent_t stop);
 
 }  // namespace pk

@@ -333,6 +333,23 @@ int f16_variant_family(int index) {
   return index < kLocal + f16k_variant_count() ? kFamilyPairCode : kFamilySmallM;
 }
 
+uint32_t f16_variant_grid(int index, uint32_t rows, uint32_t columns, uint32_t splits) {
+  const TileShape s = f16_variant(index);
+  if (f16_variant_family(index) == kFamilySmallM) return small_m_grid(s, tiles_n(s, columns), rows);
+  return tiles_m(s, rows) * tiles_n(s, columns) * splits;
+}
+
+const char* f16_group_kernel_name(int index) {
+  return f16_variant_family(index) == kFamilySmallM ? f16s_group_name(index - kLocal - f16k_variant_count())
+                                                     : nullptr;
+}
+
+hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStream_t stream, hipEvent_t start,
+                                 hipEvent_t stop) {
+  if (f16_variant_family(index) != kFamilySmallM) return hipErrorInvalidValue;
+  return launch_gemm_f16s_group(index - kLocal - f16k_variant_count(), group, stream, start, stop);
+}
+
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop) {
   if (variant >= kLocal + f16k_variant_count())

@@ -109,6 +109,12 @@ inline uint32_t tiles_n(const TileShape& s, uint32_t columns) {
   return (padded_columns(columns) + s.tile_columns() - 1) / s.tile_columns();
 }
 
+// Workgroups of a small-M launch over `column_groups` column groups of
+// `s`: whole rounds of the eight XCDs per row group (pk_gemm_f16s.hip).
+inline uint32_t small_m_grid(const TileShape& s, uint32_t column_groups, uint32_t rows) {
+  return (column_groups + 7u) / 8u * 8u * tiles_m(s, rows);
+}
+
 // Workgroup i is dispatched to XCD i % 8 (round robin). This bijection on
 // [0, count) gives the workgroups of one XCD a contiguous range of work
 // items, so tiles that share activation rows share that XCD's L2.
@@ -166,6 +172,28 @@ inline int f16_variant_parts(int index) {
 }
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream,
                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Workgroups of one launch of an f16 variant.
+uint32_t f16_variant_grid(int index, uint32_t rows, uint32_t columns, uint32_t splits);
+
+// A group of independent f16 GEMMs run by one launch of a small-M variant:
+// `items` lists (member << 16 | column group) over the members' column
+// groups of that variant's width; every member takes `rows` rows and
+// reads operand-order codes of one part.
+struct SmallMMember {
+  GemmArgs args;
+  int bits;
+  int reserved;
+};
+struct SmallMGroupArgs {
+  const SmallMMember* members;
+  const uint32_t* items;
+  uint32_t items_count;
+  uint32_t rows;
+  uint32_t row_groups;  // tiles_m of the variant at `rows`
+};
+const char* f16_group_kernel_name(int index);
+hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStream_t stream,
+                                 hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 int f32_variant_count();
 TileShape f32_variant(int index);

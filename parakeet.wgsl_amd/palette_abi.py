@@ -108,6 +108,19 @@ class PlanInfo(ctypes.Structure):
     ]
 
 
+class VariantDesc(ctypes.Structure):
+    _fields_ = [
+        ("tile_rows", ctypes.c_uint32),
+        ("tile_columns", ctypes.c_uint32),
+        ("block_threads", ctypes.c_uint32),
+        ("k_split", ctypes.c_uint32),
+        ("code_parts", ctypes.c_uint32),
+        ("groupable", ctypes.c_int32),
+        ("kernel5", ctypes.c_char * 64),
+        ("kernel6", ctypes.c_char * 64),
+    ]
+
+
 class ExpandDesc(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -455,9 +468,16 @@ SIGNATURES = {
     "pk_gemm_destroy": (ctypes.c_int, [_VP]),
     "pk_gemm_release": (ctypes.c_int, [_VP]),
     "pk_gemm_variant_count": (ctypes.c_int, [ctypes.c_int]),
+    "pk_gemm_variant_describe": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(VariantDesc)]),
     "pk_gemm_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
     "pk_gemm_set_splits": (ctypes.c_int, [_VP, ctypes.c_uint32]),
     "pk_gemm_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
+    "pk_gemm_group_create": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), ctypes.c_uint32, ctypes.c_char_p, _PPV]),
+    "pk_gemm_group_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
+    "pk_gemm_group_enqueue_timed": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP, _VP, _VP]),
+    "pk_gemm_group_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
+    "pk_gemm_group_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
+    "pk_gemm_group_destroy": (ctypes.c_int, [_VP]),
     "pk_palette_expand": (ctypes.c_int, [_VP, ctypes.POINTER(ExpandDesc), _VP]),
     "pk_unpack_codes": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_uint64, _VP, _VP]),
     "pk_conv_plan_shape": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -749,8 +769,53 @@ class GemmOp:
             self.handle = None
 
 
+class GemmGroup:
+    """Independent f16 GEMM ops launched as one small-M kernel
+    (pk_gemm_group_create ... pk_gemm_group_destroy). The group snapshots
+    the ops' bindings and keeps their prepared weights alive."""
+
+    def __init__(self, ctx: Context, ops, label: str = "palette-gemm-group"):
+        self.ctx = ctx
+        handles = (_VP * len(ops))(*[op.handle for op in ops])
+        handle = ctypes.c_void_p()
+        check(load().pk_gemm_group_create(ctx.handle, handles, len(ops), label.encode(), ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def enqueue(self, active_rows: int = 0, stream=None, start: "Event" = None, end: "Event" = None) -> None:
+        if start is None and end is None:
+            check(load().pk_gemm_group_enqueue(self.handle, active_rows, stream))
+        else:
+            check(load().pk_gemm_group_enqueue_timed(self.handle, active_rows, stream,
+                                                     start.handle if start else None, end.handle if end else None))
+
+    def plan(self, active_rows: int = 0) -> PlanInfo:
+        info = PlanInfo()
+        check(load().pk_gemm_group_plan(self.handle, active_rows, ctypes.byref(info)))
+        return info
+
+    def set_variant(self, variant: int) -> None:
+        """A small-M variant index, or -1 for the planned one."""
+        check(load().pk_gemm_group_set_variant(self.handle, variant))
+
+    def release(self) -> None:
+        if self.handle:
+            check(load().pk_gemm_group_destroy(self.handle))
+            self.handle = None
+
+
 def variant_count(precision: str) -> int:
     return int(load().pk_gemm_variant_count(PRECISION[precision]))
+
+
+def describe_variant(precision: str, variant: int) -> VariantDesc:
+    desc = VariantDesc()
+    check(load().pk_gemm_variant_describe(PRECISION[precision], variant, ctypes.byref(desc)))
+    return desc
+
+
+def small_m_variants() -> list:
+    """f16 variants a GemmGroup can run (the small-M kernels), by index."""
+    return [v for v in range(variant_count("f16")) if describe_variant("f16", v).groupable]
 
 
 def _slice(array):

@@ -113,6 +113,33 @@ def test_plan_of_variants_is_listed(abi):
     assert abi.variant_count("f32") >= 1
 
 
+def test_variant_descriptions(abi):
+    """Every compiled variant describes itself without a device: kernel
+    names per code width, tile, K split, the code layout it reads, and
+    whether a GEMM group can run it (the small-M kernels only)."""
+    lib = abi.load()
+    groupable = []
+    for v in range(abi.variant_count("f16")):
+        d = abi.describe_variant("f16", v)
+        k5, k6 = d.kernel5.decode(), d.kernel6.decode()
+        assert k5.startswith("pk_gemm_f16") and k6.startswith("pk_gemm_f16") and "_b5_" in k5 and "_b6_" in k6, v
+        assert d.tile_rows % 32 == 0 and d.tile_columns % 32 == 0 and d.block_threads % 64 == 0, v
+        small = k5.startswith("pk_gemm_f16s_")
+        assert bool(d.groupable) == small, v
+        # pair-code kernels read codes split into their K split's parts; all others one part
+        assert d.code_parts == (d.k_split if k5.startswith("pk_gemm_f16p_") else 1), v
+        if small:
+            groupable.append(v)
+    assert groupable == abi.small_m_variants() and groupable
+    d = abi.describe_variant("f32", 0)
+    assert d.kernel5.decode().startswith("pk_gemm_f32") and not d.groupable and d.code_parts == 1
+    assert lib.pk_gemm_variant_describe(abi.PRECISION["f16"], abi.variant_count("f16"), ctypes.byref(d)) \
+        == abi.RANGE_ERROR
+    assert lib.pk_gemm_group_create(None, None, 0, None, None) == abi.INVALID_ARGUMENT
+    assert lib.pk_gemm_group_destroy(None) == abi.OK
+    assert lib.pk_gemm_group_set_variant(None, 0) == abi.INVALID_ARGUMENT
+
+
 def test_workload_packer_matches_oracle(oracle, workloads):
     rng = np.random.default_rng(4)
     for bits in (5, 6):

@@ -106,9 +106,10 @@ def k_split_of(name):
     """Order class of a kernel: pair-code variants add their K-part partial
     tiles at the end (pk_gemm_f16p_b*_n<WN>k<KS>_...); KS = 1 and every
     operand-order variant accumulate all of K in one chain; the small-M
-    variants (pk_gemm_f16s_*) add eight round-robin K partials."""
-    if "_f16s_" in name:
-        return "small-m"
+    variants (pk_gemm_f16s_b*_k<W>_...) add W round-robin K partials."""
+    m = re.search(r"_f16s_(?:b\d_|group_)k(\d+)_", name)
+    if m:
+        return "small-m-k" + m.group(1)
     m = re.search(r"_n\dk(\d)_", name)
     return int(m.group(1)) if m else 1
 
@@ -606,3 +607,118 @@ def test_active_prefix_is_replanned_and_bit_identical(abi, ctx, scope, oracle, w
     assert (got_prefix[active:] == np.float16(7.0)).all()
     sub = workloads.GemmCase("prefix", case.a[:active], w, activation=case.activation)
     assert_f16_parity(oracle, got_prefix[:active], sub)
+
+
+GROUP_MEMBERS = [  # inner, columns, bits, palette groups, activation, bias, residual scale
+    (1024, 4096, 5, 1, "silu", False, None),   # FF expand
+    (4096, 1024, 5, 1, "none", False, 0.5),    # FF contract + 0.5 residual
+    (1024, 3072, 5, 3, "none", False, None),   # QKV, 3 palette groups
+    (1024, 1024, 6, 1, "none", False, 1.0),    # output projection + residual
+    (1056, 640, 6, 1, "relu", True, None),     # K % 64 = 32, bias
+    (256, 96, 6, 3, "silu", True, None),       # 3 palette groups of 32 columns
+]
+
+
+def group_fixture(abi, ctx, scope, workloads, rows, sentinel=0.0):
+    """GEMM cases of GROUP_MEMBERS at `rows`, each bound twice: ops for the
+    group and ops for single launches (own outputs), every op on the small-M
+    layout."""
+    small = small_m_variants(abi, ctx, scope, workloads)
+    cases, grouped, single = [], [], []
+    for i, (k, n, bits, groups, act, bias, scale) in enumerate(GROUP_MEMBERS):
+        case = workloads.gemm_case(rows * 7 + i, rows, k, n, bits, groups=groups, activation=act, bias=bias,
+                                   residual_scale=scale)
+        cases.append(case)
+        a, palette = scope.put(case.a), scope.put(case.weight.palette)
+        bias_d, res = scope.put(case.bias), scope.put(case.residual)
+        for ops in (grouped, single):
+            out = scope.put(np.full((rows, n), sentinel, np.float16))
+            op = abi.GemmOp(ctx, a=a, packed=scope.put(case.weight.packed), palette=palette, output=out, bits=bits,
+                            rows=rows, inner=k, columns=n, bias=bias_d, residual=res, residual_scale=scale,
+                            activation=act, label=f"member-{i}")
+            op.set_variant(small[0])  # one K part: the layout group members read
+            ops.append((op, out))
+    return small, cases, grouped, single
+
+
+@pytest.mark.parametrize("rows", [16, 64, 188])
+def test_gemm_group_matches_single_launches(abi, ctx, scope, oracle, workloads, rows):
+    """One group launch of independent GEMMs (5- and 6-bit, several palette
+    groups, a K % 64 = 32 tail, every epilogue) gives each member the bits of
+    that member launched alone on the same small-M variant, for every
+    small-M variant, and the planned launch meets the oracle's bars."""
+    small, cases, grouped, single = group_fixture(abi, ctx, scope, workloads, rows)
+    group = abi.GemmGroup(ctx, [op for op, _ in grouped], label="parity-group")
+    try:
+        planned = group.plan()
+        print("rows", rows, "planned", planned.kernel.decode(), list(planned.grid), flush=True)
+        group.enqueue()
+        ctx.synchronize()
+        for case, (_, out) in zip(cases, grouped):
+            assert_f16_parity(oracle, out.download(), case)
+        for variant in small:
+            group.set_variant(variant)
+            group.enqueue()
+            for op, _ in single:
+                op.set_variant(variant)
+                op.enqueue()
+            ctx.synchronize()
+            for i, ((_, g_out), (_, s_out)) in enumerate(zip(grouped, single)):
+                np.testing.assert_array_equal(g_out.download().view(np.uint16), s_out.download().view(np.uint16),
+                                              err_msg=f"variant {variant} member {i}")
+    finally:
+        group.release()
+        for op, _ in grouped + single:
+            op.release()
+
+
+def test_gemm_group_prefix_and_lifetime(abi, ctx, scope, oracle, workloads):
+    """An active prefix leaves every member's tail untouched and matches the
+    full launch's rows bit for bit; the group outlives the ops it was made
+    from (it holds their prepared weights)."""
+    rows, active = 96, 40
+    small, cases, grouped, single = group_fixture(abi, ctx, scope, workloads, rows, sentinel=7.0)
+    group = abi.GemmGroup(ctx, [op for op, _ in grouped])
+    try:
+        for op, _ in grouped:
+            op.release()
+        group.enqueue(active)
+        for op, _ in single:
+            op.enqueue()
+        ctx.synchronize()
+        for i, ((_, g_out), (_, s_out)) in enumerate(zip(grouped, single)):
+            got, full = g_out.download(), s_out.download()
+            assert (got[active:] == np.float16(7.0)).all(), i
+            sub = workloads.GemmCase("prefix", cases[i].a[:active], cases[i].weight, bias=cases[i].bias,
+                                     residual=None if cases[i].residual is None else cases[i].residual[:active],
+                                     residual_scale=cases[i].residual_scale, activation=cases[i].activation)
+            assert_f16_parity(oracle, got[:active], sub)
+    finally:
+        group.release()
+        for op, _ in single:
+            op.release()
+
+
+def test_gemm_group_errors(abi, ctx, scope, workloads):
+    """Members on another code layout, rows past the capacity and variants of
+    other kernel families are refused with PK_RANGE_ERROR."""
+    case = workloads.gemm_case(3, 188, 1024, 1024, 5)
+    a, palette = scope.put(case.a), scope.put(case.weight.palette)
+    out = scope.empty((188, 1024), np.float16)
+    op = abi.GemmOp(ctx, a=a, packed=scope.put(case.weight.packed), palette=palette, output=out, bits=5, rows=188,
+                    inner=1024, columns=1024, label="pair-layout")
+    try:
+        if k_split_of(op.plan().kernel.decode()) in (2, 4):
+            with pytest.raises(abi.PaletteRangeError, match="member 0 \\(pair-layout\\) holds codes split into"):
+                abi.GemmGroup(ctx, [op])
+        op.set_variant(small_m_variants(abi, ctx, scope, workloads)[0])
+        group = abi.GemmGroup(ctx, [op])
+        try:
+            with pytest.raises(abi.PaletteRangeError, match=r"active rows must be in \[1, 188\]"):
+                group.enqueue(189)
+            with pytest.raises(abi.PaletteRangeError, match="is not a small-M variant"):
+                group.set_variant(0)
+        finally:
+            group.release()
+    finally:
+        op.release()
