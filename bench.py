@@ -87,6 +87,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
     p.add_argument("--no-ff-block", action="store_true", help="encoder workloads: skip the FF block's extra line")
+    p.add_argument("--fused-norms", action="store_true",
+                   help="encoder workloads: run the four LayerNorms that feed a GEMM inside those GEMMs "
+                        "(PK_GEMM_ROW_NORM; default: separate launches, as the reference does)")
     p.add_argument("--graph", action="store_true",
                    help="replay the unstamped steps from a HIP graph (measured slower than eager launches for "
                         "two-launch steps)")
@@ -347,6 +350,9 @@ def cpu_baseline(workload, data, sample_rows, budget_s=10.0, threads=None):
 WINDOW_SECONDS = 15.0  # audio per encoder window: 1500 fbank frames at 100/s, 8x subsampled to 188
 
 
+# The LayerNorms that run inside the GEMM after them with --fused-norms.
+FUSED_NORMS = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2")
+
 FRONT_DISPATCHES = ("subsampling-fused-conv0-depthwise2", "subsampling-pointwise3", "subsampling-depthwise5",
                     "subsampling-pointwise6", "subsampling-pointwise6-mask", "subsampling-flatten-project")
 
@@ -503,8 +509,9 @@ def run_encoder(args, abi, ctx, decoder=False):
                         frames=stack.frames, subsampling=front, feature_frames=stack.feature_frames,
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
-                        projected_output=projected, label="encoder")
+                        projected_output=projected, fused_norms=args.fused_norms, label="encoder")
     launches, device_bytes = enc.info()
+    fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
     stream = ctx.stream
     tdt = None
     if decoder:
@@ -568,6 +575,11 @@ def run_encoder(args, abi, ctx, decoder=False):
     dispatches = {}
     for name, ms, (flops, nbytes) in zip(names, per_kind_ms, costs):
         us = ms * 1e3
+        if name in fused_norms:
+            # runs inside the GEMM after it; the slot's two events are back to back
+            dispatches[name] = {"avg_us": us, "fused_into_next_gemm": True, "flops": 0, "algorithmic_bytes": 0,
+                                "launches_per_pass": 0}
+            continue
         dispatches[name] = {"avg_us": us, "tflops": flops / (us * 1e-6) / 1e12 if flops else 0.0,
                             "gbs": nbytes / (us * 1e-6) / 1e9, "flops": flops, "algorithmic_bytes": nbytes,
                             "launches_per_pass": len(stack.layers) if name in abi.ENCODER_DISPATCHES else 1}
@@ -637,7 +649,11 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "frames": stack.frames, "layers": len(stack.layers), "d_model": 1024, "ff_hidden": 4096,
                    "heads": 8, "subsampling": "dw_striding 8x, 256 channels", "projector": "1024->640",
                    "palette_bits": {"ff/qkv/pointwise/subsampling/projector": 5, "o_proj": 6},
-                   "launches_per_pass": launches, "graph_replay": True,
+                   "dispatch_slots_per_pass": launches,
+                   "launches_per_pass": launches - len(fused_norms) * len(stack.layers),
+                   "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
+                                 if args.fused_norms else "separate launches",
+                   "graph_replay": True,
                    "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -5,8 +5,9 @@
  * events and status codes as pk_palette.h.
  *
  * Reference interfaces replaced: the encoder graph of src/webgpu/encoder.ts -
- * createEncoderLayerDispatches (:1868-2135), fifteen dispatches per layer in
- * this order:
+ * createEncoderLayerDispatches (:1868-2135), fifteen dispatch slots per
+ * layer in this order (with PK_ENCODER_FUSED_NORMS the four LayerNorms that
+ * feed a GEMM run inside that GEMM and their slots launch nothing):
  *   LN ff1 -> FF1 W1 + SiLU -> FF1 W2 + 0.5 x         (x1)
  *   LN att -> QKV -> relative attention -> Wo + x1    (x2)
  *   LN conv -> PW1 -> GLU/DW9/BN/SiLU -> PW2 + x2     (x3)
@@ -36,6 +37,13 @@ extern "C" {
 
 /* pk_encoder_desc.flags */
 #define PK_ENCODER_FUSED_GLU 0x1u  /* PW1 carries the GLU epilogue (PK_GEMM_GLU) */
+/* Run the LayerNorms before FF1 W1, QKV, PW1 and FF2 W1 inside the GEMMs
+   that read them (PK_GEMM_ROW_NORM; not for PW1 with PK_ENCODER_FUSED_GLU):
+   96 fewer launches per 24-layer pass, but each of those GEMMs does the
+   row statistics of every column tile again; on 16 windows the pass is
+   about 5% slower than with the separate LayerNorm launches, which stay
+   the default. */
+#define PK_ENCODER_FUSED_NORMS 0x2u
 
 typedef struct pk_encoder pk_encoder;
 
@@ -125,7 +133,7 @@ typedef struct pk_encoder_desc {
    message. */
 int pk_encoder_validate(const pk_encoder_desc *desc);
 /* Prepares every layer's codes, allocates the activation arena and creates
-   the fifteen ops per layer. */
+   the ops of every layer (fifteen, or eleven with fused norms). */
 int pk_encoder_create(pk_context *ctx, const pk_encoder_desc *desc, void *stream, pk_encoder **out);
 /* One encoder pass over the first `active_batch` windows (0 = all). With
    `use_graph` the pass is captured once per active batch into a HIP graph
@@ -134,12 +142,15 @@ int pk_encoder_enqueue(pk_encoder *enc, uint32_t active_batch, void *stream, int
 /* One eager pass whose dispatches stamp timestamps, as the reference's
    profiled encode does (encoder.ts:1641-1674 with timestampWrites per
    dispatch, test/webgpu/encoder-profile.test.ts): `start_events[i]` /
-   `end_events[i]` (from pk_event_create) belong to launch i of the pass
-   (pk_encoder_info's count, in order: the six front-end launches, fifteen
-   per layer, the projector); either array, or any entry, may be NULL. */
+   `end_events[i]` (from pk_event_create) belong to dispatch slot i of the
+   pass (pk_encoder_info's count, in order: the six front-end launches,
+   fifteen per layer, the projector); a LayerNorm slot fused into the GEMM
+   after it records both of its events back to back on the stream. Either
+   array, or any entry, may be NULL. */
 int pk_encoder_enqueue_profiled(pk_encoder *enc, uint32_t active_batch, void *stream,
                                 void *const *start_events, void *const *end_events);
-/* Launches in one pass and device bytes held (prepared codes + arena). */
+/* Dispatch slots of one pass (the profiled pass's event count) and device
+   bytes held (prepared codes, the fused norms' column sums, the arena). */
 int pk_encoder_info(const pk_encoder *enc, uint32_t *launches, uint64_t *device_bytes);
 int pk_encoder_destroy(pk_encoder *enc);
 

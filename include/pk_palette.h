@@ -86,6 +86,22 @@ typedef enum pk_activation {
    blocks interleaved). No counterpart in the reference's GEMM: there the
    GLU runs in the convolution kernel. */
 #define PK_GEMM_GLU 0x2u
+/* Row LayerNorm fused into the GEMM's input. No counterpart in the
+   reference's GEMM: there a LayerNorm dispatch writes the normalised rows
+   and the GEMM reads them (layernorm.ts:29-281 before the projections of
+   encoder.ts:1897-2116). With this flag the op multiplies LN(A) instead of
+   A: LN(a)_k = (a_k - mean) * rstd * gamma_k + beta_k, mean and variance
+   max(E[a^2] - mean^2, 0) over the K channels of the row, rstd =
+   1 / sqrt(variance + epsilon) (layernorm.ts:309-390), with no pass that
+   writes the normalised rows. The kernel multiplies f16(a_k *
+   f16(gamma_k)) and finishes each output as rstd * (acc - mean * G_n) +
+   B_n with G = f16(gamma) . W and B = beta . W, computed once at create;
+   the normalised row is thus not rounded to f16 as the reference's
+   LayerNorm output is. f16 only; needs K % 64 == 0, K <= 2048, the packed
+   codes (no shared prepared weight), no GLU epilogue, and one palette group
+   or groups whose width is a multiple of 256 columns. Runs on the pair-code
+   kernels. */
+#define PK_GEMM_ROW_NORM 0x4u
 
 typedef struct pk_context pk_context;
 typedef struct pk_gemm_op pk_gemm_op;
@@ -216,6 +232,12 @@ typedef struct pk_gemm_desc {
   float residual_scale;
   int32_t activation;            /* pk_activation */
   const pk_prepared_weight *prepared; /* optional shared prepared weight */
+  /* PK_GEMM_ROW_NORM only: the LayerNorm's parameters. */
+  const float *norm_gamma;       /* [inner] f32 */
+  uint64_t norm_gamma_bytes;
+  const float *norm_beta;        /* [inner] f32 */
+  uint64_t norm_beta_bytes;
+  float norm_epsilon;            /* 0 selects 1e-5 */
 } pk_gemm_desc;
 
 int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,

@@ -450,7 +450,7 @@ static int parse_gemm_desc(napi_env env, napi_value o, pk_gemm_desc *d, char **l
   memset(d, 0, sizeof *d);
   d->struct_size = sizeof *d;
   *label = NULL;
-  uint64_t a = 0, packed = 0, palette = 0, output = 0, bias = 0, residual = 0;
+  uint64_t a = 0, packed = 0, palette = 0, output = 0, bias = 0, residual = 0, norm_gamma = 0, norm_beta = 0;
   char *precision = prop_string(env, o, "precision");
   char *activation = prop_string(env, o, "activation");
   d->precision = !precision || strcmp(precision, "f16") == 0 ? PK_PRECISION_F16
@@ -485,6 +485,16 @@ static int parse_gemm_desc(napi_env env, napi_value o, pk_gemm_desc *d, char **l
     d->has_residual_scale = 1;
     d->residual_scale = (float)scale;
   }
+  if (prop_u64(env, o, "normGamma", &norm_gamma)) prop_u64(env, o, "normGammaBytes", &d->norm_gamma_bytes);
+  if (prop_u64(env, o, "normBeta", &norm_beta)) prop_u64(env, o, "normBetaBytes", &d->norm_beta_bytes);
+  if (prop(env, o, "normEpsilon", &v)) {
+    double epsilon;
+    if (napi_get_value_double(env, v, &epsilon) != napi_ok) {
+      bad_argument(env, "normEpsilon must be a number");
+      return 0;
+    }
+    d->norm_epsilon = (float)epsilon;
+  }
   if (prop(env, o, "prepared", &v)) {
     const weight_box *box = (const weight_box *)get_external(env, v);
     if (!box || !box->w) {
@@ -498,6 +508,8 @@ static int parse_gemm_desc(napi_env env, napi_value o, pk_gemm_desc *d, char **l
   d->palette = (const void *)(uintptr_t)palette;
   d->output = (void *)(uintptr_t)output;
   d->bias = (const float *)(uintptr_t)bias;
+  d->norm_gamma = (const float *)(uintptr_t)norm_gamma;
+  d->norm_beta = (const float *)(uintptr_t)norm_beta;
   d->residual = (const void *)(uintptr_t)residual;
   *label = prop_string(env, o, "label");
   d->label = *label;
@@ -1199,7 +1211,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
   return ok;
 }
 
-/* Parses an encoder descriptor: {label, fusedGlu?, batchSize, frames,
+/* Parses an encoder descriptor: {label, fusedGlu?, fusedNorms?, batchSize, frames,
    layers: [layer...], validLengths, input, output, subsampling?,
    featureFrames?, featureLengths?, projector?, projectorBias?,
    projectedChannels?, projectedOutput?}. The layer array, front end and
@@ -1213,6 +1225,9 @@ static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   bool glu = false;
   if (prop(env, o, "fusedGlu", &v) && napi_get_value_bool(env, v, &glu) == napi_ok && glu)
     d->flags |= PK_ENCODER_FUSED_GLU;
+  bool fused_norms = false;
+  if (prop(env, o, "fusedNorms", &v) && napi_get_value_bool(env, v, &fused_norms) == napi_ok && fused_norms)
+    d->flags |= PK_ENCODER_FUSED_NORMS;
   if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
       !prop(env, o, "layers", &layers) || napi_get_array_length(env, layers, &n) != napi_ok || n == 0) {
     bad_argument(env, "encoder descriptor is missing a required field");

@@ -123,6 +123,8 @@ struct pk_gemm_op {
   // Split-K workspace: f32 partial tiles, then one counter per tile.
   void* workspace = nullptr;
   uint64_t workspace_bytes = 0;
+  // Fused row LayerNorm (PK_GEMM_ROW_NORM): G and B [2N] f32, then f16 gamma [K].
+  void* norm_buffer = nullptr;
   bool destroyed = false;
 };
 
@@ -405,14 +407,14 @@ int best_pair_tile(uint32_t rows, uint32_t columns, int cus, bool glu, int ks) {
   return best;
 }
 
-// The plan of one op: plan_launch, with a GLU epilogue moved to the
-// pair-code kernels (small-M plans take their 64 x 64 tile), and with a
+// The plan of one op: plan_launch, with a GLU epilogue or a fused row norm
+// moved to the pair-code kernels (small-M plans take their 64 x 64 tile), and with a
 // shared prepared weight restricted to the tiles that read the layout it
 // holds (`required_parts`, 0 = any).
 Plan plan_op(int precision, uint32_t rows, uint32_t inner, uint32_t columns, int cus, bool glu,
-             int required_parts) {
+             int required_parts, bool pair_only = false) {
   Plan plan = plan_launch(precision, rows, inner, columns, cus);
-  if (glu && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
+  if ((glu || pair_only) && pk::f16_variant_family(plan.variant) != pk::kFamilyPairCode)
     plan = {find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 1, 2, 2, 4), 1u};
   if (required_parts && variant_parts(precision, plan.variant) != required_parts) {
     if (required_parts == 1 && !glu && (rows <= 64u || (rows <= 256u && inner >= 2048u))) {
@@ -522,6 +524,20 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
                 "%s GLU epilogue needs f16, one palette group, N %% 64 == 0, no bias, activation, residual "
                 "or shared prepared weight",
                 label);
+  const bool norm = (d->flags & PK_GEMM_ROW_NORM) != 0;
+  if (norm) {
+    if (!f16 || glu || d->prepared || d->inner % 64u != 0 || d->inner > pk::kNormMaxInner ||
+        (d->palette_groups != 1 && d->palette_group_columns % 256u != 0))
+      return fail(PK_INVALID_ARGUMENT,
+                  "%s row norm needs f16, K %% 64 == 0, K <= %u, packed codes, no GLU epilogue and one palette "
+                  "group or groups of a multiple of 256 columns",
+                  label, pk::kNormMaxInner);
+    const uint64_t need = (uint64_t)d->inner * 4u;
+    if (!d->norm_gamma || !d->norm_beta || d->norm_gamma_bytes < need || d->norm_beta_bytes < need ||
+        !aligned(d->norm_gamma, 4) || !aligned(d->norm_beta, 4) || !(d->norm_epsilon >= 0.0f))
+      return fail(PK_INVALID_ARGUMENT, "%s row norm needs gamma and beta of %llu bytes and epsilon >= 0", label,
+                  (unsigned long long)need);
+  }
   // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
   const uint32_t entries = 1u << bits;
   const uint32_t cpg = pk::codes_per_group(bits);
@@ -856,11 +872,12 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   if (hipGetDeviceProperties(&prop, ctx->device) == hipSuccess && prop.multiProcessorCount > 0)
     cus = prop.multiProcessorCount;
   const bool glu = (d->flags & PK_GEMM_GLU) != 0;
+  const bool norm = (d->flags & PK_GEMM_ROW_NORM) != 0;
   op->cus = cus;
   // The plan comes first: the weight is prepared in the one layout the
   // planned kernel reads (a shared prepared weight fixes it instead).
   const Plan plan = plan_op(d->precision, d->rows, d->inner, d->columns, cus, glu,
-                            d->prepared ? d->prepared->parts : 0);
+                            d->prepared ? d->prepared->parts : 0, norm);
   if (d->prepared) {
     op->weight = const_cast<pk_prepared_weight*>(d->prepared);
     op->weight->refs.fetch_add(1);
@@ -891,7 +908,35 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   a.palette_entries = 1u << bits;
   a.glu = glu ? 1 : 0;
   a.splits = 1;
+  if (norm) {
+    // G and B (2N f32), then gamma as f16 (K halves), from the packed codes.
+    const uint64_t sums = (uint64_t)d->columns * 8u;
+    hipError_t e = hipMalloc(&op->norm_buffer, sums + (uint64_t)d->inner * 2u);
+    if (e != hipSuccess) {
+      op->norm_buffer = nullptr;
+      weight_unref(op->weight);
+      delete op;
+      return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate the row norm's column sums: %s", label,
+                  hipGetErrorString(e));
+    }
+    float* column_sums = static_cast<float*>(op->norm_buffer);
+    void* gamma16 = static_cast<uint8_t*>(op->norm_buffer) + sums;
+    const hipStream_t st = stream_or_default(ctx, stream);
+    e = pk::launch_norm_prepare(bits, d->packed, d->inner, d->columns, d->palette_group_columns, d->palette_groups,
+                                d->palette, d->norm_gamma, d->norm_beta, gamma16, column_sums, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+      (void)hipFree(op->norm_buffer);
+      weight_unref(op->weight);
+      delete op;
+      return fail(PK_DEVICE_ERROR, "%s: row norm preparation failed: %s", label, hipGetErrorString(e));
+    }
+    a.norm_columns = column_sums;
+    a.norm_gamma = static_cast<const _Float16*>(gamma16);
+    a.norm_epsilon = d->norm_epsilon > 0.0f ? d->norm_epsilon : 1e-5f;
+  }
   if (int st = configure_launch(op, plan.variant, plan.splits)) {
+    if (op->norm_buffer) (void)hipFree(op->norm_buffer);
     weight_unref(op->weight);
     delete op;
     return st;
@@ -957,6 +1002,12 @@ int pk_gemm_destroy(pk_gemm_op* op) {
   op->destroyed = true;
   weight_unref(op->weight);
   op->weight = nullptr;
+  if (op->norm_buffer) {
+    (void)hipSetDevice(op->ctx->device);
+    (void)hipStreamSynchronize(op->ctx->stream);
+    (void)hipFree(op->norm_buffer);
+    op->norm_buffer = nullptr;
+  }
   if (op->workspace) {
     (void)hipSetDevice(op->ctx->device);
     (void)hipStreamSynchronize(op->ctx->stream);
@@ -982,6 +1033,8 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
     return fail(PK_RANGE_ERROR, "tile variant %d outside [0, %d)", variant, count);
   if (op->args.glu && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no GLU epilogue", op->label.c_str(), variant);
+  if (op->args.norm_columns && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
+    return fail(PK_RANGE_ERROR, "%s tile variant %d has no fused row norm", op->label.c_str(), variant);
   // A variant that reads another split of the codes: an op alone on its
   // weight moves it to that layout; a weight shared with other ops stays.
   const int parts = variant_parts(op->precision, variant);
@@ -1129,8 +1182,8 @@ int pk_gemm_group_create(pk_context* ctx, pk_gemm_op* const* ops, uint32_t count
     if (op->destroyed) return fail(PK_DESTROYED, "%s member %u (%s) was destroyed", name, i, op->label.c_str());
     if (op->ctx != ctx)
       return fail(PK_INVALID_ARGUMENT, "%s member %u (%s) belongs to another context", name, i, op->label.c_str());
-    if (op->precision != PK_PRECISION_F16 || op->args.glu)
-      return fail(PK_RANGE_ERROR, "%s member %u (%s) is not an f16 GEMM without GLU epilogue", name, i,
+    if (op->precision != PK_PRECISION_F16 || op->args.glu || op->args.norm_columns)
+      return fail(PK_RANGE_ERROR, "%s member %u (%s) is not an f16 GEMM without GLU epilogue or row norm", name, i,
                   op->label.c_str());
     if (op->weight->parts != 1)
       return fail(PK_RANGE_ERROR,

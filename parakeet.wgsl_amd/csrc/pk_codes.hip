@@ -337,4 +337,55 @@ hipError_t launch_relayout(int bits, const uint32_t* src, int src_parts, uint32_
   return hipErrorInvalidValue;
 }
 
+namespace {
+
+// Fused row LayerNorm preparation of one weight: gamma16[k] = f16(gamma[k])
+// and, per column n, G_n = sum_k f16(gamma_k) W_kn and B_n = sum_k beta_k W_kn
+// in k order (f32), W_kn = LUT[g(n)][code(k, n)] from the reference-format
+// codes (flat index k * N + n).
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void norm_prepare_kernel(const uint32_t* __restrict__ packed, uint32_t inner,
+                                                               uint32_t columns, uint32_t group_columns,
+                                                               uint32_t groups, const _Float16* __restrict__ palette,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ beta,
+                                                               _Float16* __restrict__ gamma16, float* __restrict__ sums) {
+  constexpr uint32_t CPG = codes_per_group(BITS);
+  constexpr uint32_t WPG = words_per_group(BITS);
+  constexpr uint32_t E = 1u << BITS;
+  const uint32_t n = blockIdx.x * kThreads + threadIdx.x;
+  for (uint32_t k = n; k < inner; k += gridDim.x * kThreads) gamma16[k] = (_Float16)gamma[k];
+  if (n >= columns) return;
+  const _Float16* lut = palette + (uint64_t)min(n / group_columns, groups - 1u) * E;
+  float g = 0.0f, b = 0.0f;
+  for (uint32_t k = 0; k < inner; ++k) {
+    const uint64_t i = (uint64_t)k * columns + n;
+    const uint32_t* w = packed + (i / CPG) * WPG;
+    const float wv = (float)lut[group_code<BITS>(w, (int)(i % CPG))];
+    g = __builtin_fmaf((float)(_Float16)gamma[k], wv, g);
+    b = __builtin_fmaf(beta[k], wv, b);
+  }
+  sums[n] = g;
+  sums[columns + n] = b;
+}
+
+}  // namespace
+
+hipError_t launch_norm_prepare(int bits, const uint32_t* packed, uint32_t inner, uint32_t columns,
+                               uint32_t group_columns, uint32_t groups, const void* palette, const float* gamma,
+                               const float* beta, void* gamma16, float* sums, hipStream_t stream) {
+  const dim3 grid((max(columns, inner) + kThreads - 1) / kThreads);
+  const _Float16* lut = static_cast<const _Float16*>(palette);
+  _Float16* g16 = static_cast<_Float16*>(gamma16);
+  if (bits == 5)
+    hipLaunchKernelGGL(norm_prepare_kernel<5>, grid, dim3(kThreads), 0, stream, packed, inner, columns,
+                       group_columns, groups, lut, gamma, beta, g16, sums);
+  else if (bits == 6)
+    hipLaunchKernelGGL(norm_prepare_kernel<6>, grid, dim3(kThreads), 0, stream, packed, inner, columns,
+                       group_columns, groups, lut, gamma, beta, g16, sums);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 }  // namespace pk

@@ -69,6 +69,7 @@ struct pk_encoder {
   std::string label;
   uint32_t batch = 0, frames = 0, layers = 0, rows = 0;
   bool fused_glu = false;
+  bool fused_norms = false;
   const uint32_t* valid_lengths = nullptr;
   const void* input = nullptr;
   void* output = nullptr;
@@ -133,6 +134,8 @@ struct GemmSpec {
   float scale = 0.0f;
   int activation = PK_ACTIVATION_NONE;
   uint32_t flags = 0;
+  const float* norm_gamma = nullptr;  // with PK_GEMM_ROW_NORM
+  const float* norm_beta = nullptr;
 };
 
 // With `validate_only` the descriptor is checked on the host
@@ -166,6 +169,13 @@ int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStr
   d.has_residual_scale = g.residual ? 1 : 0;
   d.residual_scale = g.scale;
   d.activation = g.activation;
+  if (g.flags & PK_GEMM_ROW_NORM) {
+    d.norm_gamma = g.norm_gamma;
+    d.norm_gamma_bytes = (uint64_t)g.inner * 4u;
+    d.norm_beta = g.norm_beta;
+    d.norm_beta_bytes = (uint64_t)g.inner * 4u;
+    d.norm_epsilon = 1e-5f;
+  }
   if (validate_only) return pk_gemm_validate(&d);
   const int s = pk_gemm_create(e->ctx, &d, stream, op);
   if (s == PK_OK) e->weight_bytes += gemm_weight_bytes(*op);
@@ -288,7 +298,9 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
 //   A (the caller's input for layer 0 without the front end) -LN-> B -W1->
 //   H -W2(+0.5 A)-> B -LN-> C -QKV-> Q -att-> X -Wo(+B)-> C -LN-> D -PW1->
 //   P -conv-> O -PW2(+C)-> D -LN-> B -W1-> H -W2(+0.5 D)-> B -LN-> A (the
-//   last layer writes the output instead).
+//   last layer writes the output instead). With PK_ENCODER_FUSED_NORMS the
+//   four LayerNorms before W1, QKV, PW1 and W1 are not created: those GEMMs
+//   read the LayerNorm's input (A, B, C, D) with PK_GEMM_ROW_NORM.
 int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream_t stream, LayerOps& l,
                 bool validate_only) {
   const uint64_t R = e->rows;
@@ -315,10 +327,19 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
     d.output_bytes = R * kC * 2;
     return validate_only ? pk_layernorm_validate(&d) : pk_layernorm_create(e->ctx, &d, &l.norm[i]);
   };
+  // LayerNorm i runs inside the GEMM it feeds (not with the GLU epilogue).
+  auto fused = [&](int i) { return e->fused_norms && !(i == 2 && e->fused_glu); };
+  int norm_of = -1;  // the LayerNorm the next gemm() call fuses
   auto gemm = [&](pk_gemm_op** op, const char* suffix, const pk_encoder_matrix& m, int bits, uint32_t inner,
                   uint32_t columns, uint32_t groups, const void* a, void* out, const void* residual, float scale,
                   int activation, uint32_t flags) {
     GemmSpec g;
+    if (norm_of >= 0) {
+      flags |= PK_GEMM_ROW_NORM;
+      g.norm_gamma = w.norm_gamma[norm_of];
+      g.norm_beta = w.norm_beta[norm_of];
+      norm_of = -1;
+    }
     g.matrix = m;
     g.bits = bits;
     g.rows = e->rows;
@@ -335,16 +356,26 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
   };
   const void* x = (li == 0 && !e->front) ? e->input : e->a;
   int s;
-  if ((s = norm(0, ".norm_feed_forward1", x, e->b))) return s;
-  if ((s = gemm(&l.ff1a, "-feed-forward1-linear1", w.ff1_linear1, 5, kC, kHidden, 1, e->b, e->h, nullptr, 0.0f,
-                PK_ACTIVATION_SILU, 0)))
+  // The input of a fused LayerNorm's GEMM, or the separate LayerNorm.
+  auto norm_into = [&](int i, const char* suffix, const void* in, void* out) -> const void* {
+    if (fused(i)) {
+      norm_of = i;
+      return in;
+    }
+    s = norm(i, suffix, in, out);
+    return out;
+  };
+  s = PK_OK;
+  const void* in = norm_into(0, ".norm_feed_forward1", x, e->b);
+  if (s || (s = gemm(&l.ff1a, "-feed-forward1-linear1", w.ff1_linear1, 5, kC, kHidden, 1, in, e->h, nullptr, 0.0f,
+                     PK_ACTIVATION_SILU, 0)))
     return s;
   if ((s = gemm(&l.ff1b, "-feed-forward1-linear2-residual", w.ff1_linear2, 5, kHidden, kC, 1, e->h, e->b, x, 0.5f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  if ((s = norm(1, ".norm_self_att", e->b, e->c))) return s;
-  if ((s = gemm(&l.qkv, "-self-attention-qkv", w.qkv, 5, kC, 3 * kC, 3, e->c, e->qkv, nullptr, 0.0f,
-                PK_ACTIVATION_NONE, 0)))
+  in = norm_into(1, ".norm_self_att", e->b, e->c);
+  if (s || (s = gemm(&l.qkv, "-self-attention-qkv", w.qkv, 5, kC, 3 * kC, 3, in, e->qkv, nullptr, 0.0f,
+                     PK_ACTIVATION_NONE, 0)))
     return s;
   {
     pk_attention_desc d{};
@@ -370,9 +401,9 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
   if ((s = gemm(&l.o, "-self-attention-output-residual", w.o_proj, 6, kC, kC, 1, e->ctxt, e->c, e->b, 1.0f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  if ((s = norm(2, ".norm_conv", e->c, e->d))) return s;
-  if ((s = gemm(&l.pw1, "-convolution-pointwise1", w.pointwise1, 5, kC, 2 * kC, 1, e->d, e->pw, nullptr, 0.0f,
-                PK_ACTIVATION_NONE, e->fused_glu ? PK_GEMM_GLU : 0u)))
+  in = norm_into(2, ".norm_conv", e->c, e->d);
+  if (s || (s = gemm(&l.pw1, "-convolution-pointwise1", w.pointwise1, 5, kC, 2 * kC, 1, in, e->pw, nullptr, 0.0f,
+                     PK_ACTIVATION_NONE, e->fused_glu ? PK_GEMM_GLU : 0u)))
     return s;
   {
     pk_conv_desc d{};
@@ -400,9 +431,9 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
   if ((s = gemm(&l.pw2, "-convolution-pointwise2-residual", w.pointwise2, 5, kC, kC, 1, e->cout, e->d, e->c, 1.0f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  if ((s = norm(3, ".norm_feed_forward2", e->d, e->b))) return s;
-  if ((s = gemm(&l.ff2a, "-feed-forward2-linear1", w.ff2_linear1, 5, kC, kHidden, 1, e->b, e->h, nullptr, 0.0f,
-                PK_ACTIVATION_SILU, 0)))
+  in = norm_into(3, ".norm_feed_forward2", e->d, e->b);
+  if (s || (s = gemm(&l.ff2a, "-feed-forward2-linear1", w.ff2_linear1, 5, kC, kHidden, 1, in, e->h, nullptr, 0.0f,
+                     PK_ACTIVATION_SILU, 0)))
     return s;
   if ((s = gemm(&l.ff2b, "-feed-forward2-linear2-residual", w.ff2_linear2, 5, kHidden, kC, 1, e->h, e->b, e->d,
                 0.5f, PK_ACTIVATION_NONE, 0)))
@@ -436,8 +467,18 @@ int enqueue_pass(pk_encoder* e, uint32_t batch, hipStream_t stream, void* const*
   const uint32_t rows = batch * e->frames;
   uint32_t slot = 0;
   auto ev = [&](void* const* list) { return list ? list[slot] : nullptr; };
+  // A LayerNorm slot: its launch, or for a LayerNorm fused into the next
+  // GEMM its two events back to back.
   auto norm = [&](pk_layernorm_op* op) {
-    const int s = pk_layernorm_enqueue_timed(op, rows, stream, ev(starts), ev(ends));
+    int s = PK_OK;
+    if (op) {
+      s = pk_layernorm_enqueue_timed(op, rows, stream, ev(starts), ev(ends));
+    } else {
+      hipError_t err = hipSuccess;
+      if (ev(starts)) err = hipEventRecord(static_cast<hipEvent_t>(ev(starts)), stream);
+      if (err == hipSuccess && ev(ends)) err = hipEventRecord(static_cast<hipEvent_t>(ev(ends)), stream);
+      if (err != hipSuccess) s = fail(PK_DEVICE_ERROR, "event record failed: %s", hipGetErrorString(err));
+    }
     ++slot;
     return s;
   };
@@ -505,6 +546,7 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->layers = d->layers;
   e->rows = d->batch_size * d->frames;
   e->fused_glu = (d->flags & PK_ENCODER_FUSED_GLU) != 0;
+  e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
   e->valid_lengths = d->valid_lengths;
   e->input = d->input;
   e->output = d->output;
@@ -526,7 +568,8 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
   if (d->struct_size != sizeof(pk_encoder_desc))
     return fail(PK_INVALID_ARGUMENT, "pk_encoder_desc.struct_size mismatch");
   const char* label = d->label ? d->label : "encoder";
-  if (d->flags & ~PK_ENCODER_FUSED_GLU) return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
+  if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS))
+    return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if (d->precision != PK_PRECISION_F16)
     return fail(PK_INVALID_ARGUMENT, "%s: the encoder stack runs in f16", label);
   if (d->batch_size == 0 || d->frames == 0 || d->layers == 0 || d->layers > kMaxLayers)

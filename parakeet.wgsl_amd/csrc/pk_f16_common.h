@@ -231,6 +231,7 @@ struct F16Variant {
   void (*single[2])(GemmArgs);  // [bits == 6]
   void (*general[2])(GemmArgs);
   uint32_t lds_bytes;           // static LDS of the kernel
+  void (*normed[2])(GemmArgs);  // fused row LayerNorm (single path), or null
 };
 
 }  // namespace f16

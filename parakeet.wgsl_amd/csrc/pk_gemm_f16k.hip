@@ -50,6 +50,13 @@
 //     (the reference stores the pointwise output in f16 before its GLU,
 //     conformer-conv.ts:520-535) and writes value * sigmoid(gate) to a
 //     [M, N/2] output.
+//   * fused row LayerNorm (NORM, args.norm_columns; see GemmArgs): the
+//     activation staging multiplies each chunk by gamma (packed f16, gamma
+//     staged in LDS) and adds the chunk's sum and sum of squares to the
+//     staging thread's row accumulators (v_dot2_f32_f16); the eight threads
+//     of a row combine them after the K loop into mean and rstd, and the
+//     epilogue finishes rstd * (acc - mean * G_n) + B_n before bias and
+//     activation.
 #include <utility>
 
 #include "pk_f16_common.h"
@@ -104,7 +111,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // pipe and has the last third of the region to land; the last third
 // carries the VMEM loads (sub-step 0) and the activation tile's LDS stores
 // (last sub-step).
-template <int R, int C, int VMEM, int DSW, int VPP>
+template <int R, int C, int VMEM, int DSW, int VPP, int XV = 0>
 __device__ __forceinline__ void interleave_sub_step() {
   constexpr int NM = R * C;
   constexpr int NL = (2 * NM) / 3 > 0 ? (2 * NM) / 3 : 1;
@@ -113,6 +120,7 @@ __device__ __forceinline__ void interleave_sub_step() {
   constexpr int D_PER = (4 * C + R + NL - 1) / NL;
   constexpr int M_PER = (VMEM + NT - 1) / NT;
   constexpr int W_PER = (DSW + NT - 1) / NT;
+  constexpr int X_PER = (XV + NT - 1) / NT;  // staging VALU (fused row norm) beside the stores
   constexpr int kMfma = 0x008, kValu = 0x002, kVmemRead = 0x020, kDsRead = 0x100, kDsWrite = 0x200;
   for (int x = 0; x < NL; ++x) {
     __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
@@ -122,6 +130,7 @@ __device__ __forceinline__ void interleave_sub_step() {
   for (int x = NL; x < NM; ++x) {
     __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
     if constexpr (M_PER > 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, M_PER, 0);
+    if constexpr (X_PER > 0) __builtin_amdgcn_sched_group_barrier(kValu, X_PER, 0);
     if constexpr (W_PER > 0) __builtin_amdgcn_sched_group_barrier(kDsWrite, W_PER, 0);
   }
 }
@@ -129,7 +138,7 @@ __device__ __forceinline__ void interleave_sub_step() {
 // GENERAL: the tile's columns may span palette groups (per-lane palette
 // base) or K may be 32 (mod 64) (the last K block's upper half is zeroed,
 // so the code-0 padding of the operand order multiplies zeros).
-template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA>
+template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA, bool NORM = false>
 __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int T = 256;
   constexpr int BM = 32 * R;
@@ -152,10 +161,16 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   static_assert(WN * KS == 4, "a workgroup is four wavefronts");
   static_assert(KS == 1 || KS == 2 || KS == 4, "K parts split the four sub-steps evenly");
   static_assert(BM * 8 % T == 0, "activation tile chunks must divide evenly");
+  static_assert(!(NORM && GENERAL), "the fused row norm runs on the fixed-palette path");
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   __shared__ __attribute__((aligned(16))) _Float16 lut_lds[GROUPS * kLutStride];
   __shared__ __attribute__((aligned(16))) uint32_t pair_lds[PAIRS];
+  // Fused row norm: gamma of every K channel (f16) and (mean, rstd) of
+  // every tile row.
+  __shared__ __attribute__((aligned(16))) _Float16 gamma_lds[NORM ? kNormMaxInner : 1];
+  __shared__ float2 row_stats[NORM ? BM : 1];
+  __shared__ float2 column_gb[NORM ? BN : 1];  // (G_n, B_n) of the tile's columns
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -197,6 +212,13 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   // table of packed palette pairs, entry c0 | c1 << bits = LUT[c0] |
   // LUT[c1] << 16.
   auto stage_palettes = [&]() {
+    if constexpr (NORM) {
+      for (uint32_t i = tid; i < K; i += T) gamma_lds[i] = args.norm_gamma[i];
+      for (uint32_t i = tid; i < (uint32_t)BN; i += T) {
+        const uint32_t n = min(n0 + i, N - 1u);
+        column_gb[i] = make_float2(args.norm_columns[n], args.norm_columns[N + n]);
+      }
+    }
     const uint32_t g_hi = GENERAL ? min((min(n0 + BN, N) - 1u) / gc, G - 1u) : g_lo;
     const uint32_t entries = (g_hi - g_lo + 1u) * kLutStride;
     const _Float16* src = static_cast<const _Float16*>(args.palette);
@@ -286,14 +308,44 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       dst[c] = *reinterpret_cast<const uint4*>(base + (pad ? a_off[c] - 64u : a_off[c]));
     }
   };
-  auto store_a = [&](uint32_t kb, int buf, const uint4 (&src)[CH]) {
+  // Fused row norm: this thread's share of the sum and the sum of squares
+  // of rows (tid >> 3) + 32c, over the K blocks it stages.
+  float row_sum[NORM ? CH : 1], row_sq[NORM ? CH : 1];
+#pragma unroll
+  for (int c = 0; c < (NORM ? CH : 1); ++c) row_sum[c] = row_sq[c] = 0.0f;
+  // Stores K block `want` (clamped to the last block).
+  auto store_a = [&](uint32_t want, int buf, const uint4 (&src)[CH]) {
+    const uint32_t kb = min(want, KB - 1u);
     const bool partial = GENERAL && (K & 63u) != 0u && kb + 1u == KB;
     uint8_t* dst = smem + buf * A_BYTES;
+    if constexpr (NORM) {
+      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+      const uint4 g4 = *reinterpret_cast<const uint4*>(gamma_lds + kb * 64u + (uint32_t)(tid & 7) * 8u);
+      const half2v g[4] = {__builtin_bit_cast(half2v, g4.x), __builtin_bit_cast(half2v, g4.y),
+                           __builtin_bit_cast(half2v, g4.z), __builtin_bit_cast(half2v, g4.w)};
+      const half2v one = {(_Float16)1.0f, (_Float16)1.0f};
+      // Clamped repeats of the last block enter the statistics too; they are
+      // taken out once after the K loop.
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      uint4 v = src[c];
-      if (partial && ((tid + c * T) & 7) >= 4) v = make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint4*>(dst + a_st[c]) = v;
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t w[4] = {src[c].x, src[c].y, src[c].z, src[c].w};
+        uint32_t y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2v x = __builtin_bit_cast(half2v, w[e]);
+          row_sum[c] = __builtin_amdgcn_fdot2(x, one, row_sum[c], false);
+          row_sq[c] = __builtin_amdgcn_fdot2(x, x, row_sq[c], false);
+          y[e] = __builtin_bit_cast(uint32_t, x * g[e]);
+        }
+        *reinterpret_cast<uint4*>(dst + a_st[c]) = make_uint4(y[0], y[1], y[2], y[3]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        uint4 v = src[c];
+        if (partial && ((tid + c * T) & 7) >= 4) v = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(dst + a_st[c]) = v;
+      }
     }
   };
   // LDS offset of this lane's activation fragment in local sub-step ls of
@@ -402,9 +454,10 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
 #pragma unroll
         for (int mi = 0; mi < R; ++mi)
           acc[mi][ci] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[g][ci], af[g][mi], acc[mi][ci], 0, 0, 0);
-      if constexpr (ls + 1 == SPW) store_a(min(i + 2u, last), (BUF + 2) % 3, sa[(I + 2) % 3]);
+      if constexpr (ls + 1 == SPW) store_a(i + 2u, (BUF + 2) % 3, sa[(I + 2) % 3]);
       if constexpr (SCHED) {
-        interleave_sub_step<R, C, ls == 0 ? CH + C * (KS == 1 ? 2 : 1) : 0, ls + 1 == SPW ? CH : 0, KS == 1 ? 2 : 1>();
+        interleave_sub_step<R, C, ls == 0 ? CH + C * (KS == 1 ? 2 : 1) : 0, ls + 1 == SPW ? CH : 0, KS == 1 ? 2 : 1,
+                            NORM && ls + 1 == SPW ? 12 * CH : 0>();
         if constexpr (ls + 1 < SPW) __builtin_amdgcn_sched_barrier(0);
       }
     });
@@ -418,7 +471,7 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   load_a(min(2u, last), sa[2]);
   stage_palettes();
   store_a(0u, 0, sa[0]);
-  store_a(min(1u, last), 1, sa[1]);
+  store_a(1u, 1, sa[1]);
   load_a(min(3u, last), sa[0]);
   __syncthreads();
   read_a(0, 0, af[0]);
@@ -438,6 +491,64 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   if (i + 2u < KB) step(Step<2>{}, i + 2u);
   if (i + 3u < KB) step(Step<3>{}, i + 3u);
   if (i + 4u < KB) step(Step<4>{}, i + 4u);
+
+  if constexpr (NORM) {
+    // Every K-block index from 0 to KB + 1 is staged once, the two past the
+    // end as repeats of the last block, which every activation register set
+    // holds when the loop ends (loads past the end are clamped to it): the
+    // repeats' share is taken out of the sums here.
+    {
+      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+      const half2v one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t w[4] = {sa[0][c].x, sa[0][c].y, sa[0][c].z, sa[0][c].w};
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2v x = __builtin_bit_cast(half2v, w[e]);
+          s1 = __builtin_amdgcn_fdot2(x, one, s1, false);
+          s2 = __builtin_amdgcn_fdot2(x, x, s2, false);
+        }
+        row_sum[c] -= 2.0f * s1;
+        row_sq[c] -= 2.0f * s2;
+      }
+    }
+    // The eight threads of a row (consecutive lanes) combine their shares;
+    // mean, variance max(E[x^2] - mean^2, 0) and 1 / sqrt(variance + eps)
+    // as the reference LayerNorm (layernorm.ts:309-390). The first barrier
+    // of the epilogue orders these stores before the reads.
+    const float inverse_k = 1.0f / (float)K;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float sm = row_sum[c], sq = row_sq[c];
+#pragma unroll
+      for (int off = 1; off < 8; off <<= 1) {
+        sm += __shfl_xor(sm, off, 64);
+        sq += __shfl_xor(sq, off, 64);
+      }
+      if ((tid & 7) == 0) {
+        const float mean = sm * inverse_k;
+        const float variance = fmaxf(sq * inverse_k - mean * mean, 0.0f);
+        row_stats[(tid >> 3) + 32 * c] = make_float2(mean, 1.0f / __builtin_sqrtf(variance + args.norm_epsilon));
+      }
+    }
+  }
+
+  // Fused row norm: every epilogue unit of this thread covers the same 8
+  // columns (quad tid & 3 of column block (tid >> 4) % NCB; NCB divides 16),
+  // so their G and B are read once.
+  float norm_g[NORM ? 8 : 1], norm_b[NORM ? 8 : 1];
+  if constexpr (NORM) {
+    static_assert(16 % NCB == 0, "a thread's epilogue units share their columns");
+    const int c0 = ((tid >> 4) % NCB) * 32 + (tid & 3) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float2 gb = column_gb[c0 + e];
+      norm_g[e] = gb.x;
+      norm_b[e] = gb.y;
+    }
+  }
 
   const _Float16* residual = static_cast<const _Float16*>(args.residual);
   _Float16* out = static_cast<_Float16*>(args.out);
@@ -532,6 +643,12 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       n_of[it] = min(n, N - 8u);
       at[it] = (uint64_t)min(m, M - 1u) * N + n_of[it];
       unit_sum(cb, ml, jj, q, v[it]);
+      if constexpr (NORM) {
+        // rstd * (acc - mean * G_n) + B_n: the GEMM of the normalised row.
+        const float2 st = row_stats[p0 * 32 + rl];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[it][e] = st.y * (v[it][e] - st.x * norm_g[e]) + norm_b[e];
+      }
     }
     if (args.bias) {
 #pragma unroll
@@ -594,7 +711,9 @@ constexpr uint32_t kernel_lds_bytes() {
         "pk_gemm_f16p_b6_n" #WN "k" #KS "_m" #R "n" #C TAG,                                                 \
         {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA>, gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA>}, \
         {gemm_f16k_kernel<5, WN, KS, R, C, true, S, CLA>, gemm_f16k_kernel<6, WN, KS, R, C, true, S, CLA>},   \
-        kernel_lds_bytes<WN, KS, R, C>()                                                                    \
+        kernel_lds_bytes<WN, KS, R, C>(),                                                                   \
+        {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA, true>,                                            \
+         gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA, true>}                                            \
   }
 
 const F16Variant kVariants[] = {
@@ -626,6 +745,11 @@ hipError_t launch_gemm_f16k(int bits, const f16::F16Variant& v, const GemmArgs& 
   const bool single = (args.inner & 63u) == 0u &&
                       (args.palette_groups == 1 ||
                        args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
+  if (args.norm_columns) {
+    // The fused row norm needs the fixed-palette path and K staged in LDS.
+    if (!single || args.inner > kNormMaxInner || !v.normed[bits == 6]) return hipErrorInvalidValue;
+    return launch_timed(v.normed[bits == 6], dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
+  }
   return launch_timed(single ? v.single[bits == 6] : v.general[bits == 6], dim3(groups), dim3(v.shape.threads()),
                       stream, start, stop, args);
 }

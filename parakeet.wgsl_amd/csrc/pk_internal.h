@@ -54,6 +54,10 @@ __host__ __device__ constexpr uint64_t operand_order_words(int bits, uint32_t in
 
 enum Activation : int { kActNone = 0, kActSilu = 1, kActRelu = 2 };
 
+// Largest K of a GEMM with the fused row LayerNorm (its gamma is staged in
+// LDS as f16).
+constexpr uint32_t kNormMaxInner = 2048;
+
 struct GemmArgs {
   const void* a;             // [M, K]
   const uint32_t* codes;     // operand-order codes
@@ -82,6 +86,16 @@ struct GemmArgs {
   uint32_t splits;
   float* partials;           // [tiles][splits][tile elements] or null
   uint32_t* counters;        // [tiles], zero between launches, or null
+  // Row LayerNorm fused into the input (pair-code kernels; K % 64 == 0,
+  // one palette group per tile). With norm_columns set the GEMM multiplies
+  // LN(A), LN(a)_k = (a_k - mean) * rstd * gamma_k + beta_k with mean and
+  // variance over the K channels of the row, without a separate pass: the
+  // kernel stages a_k * gamma_k (gamma as f16) and the row's sum and sum
+  // of squares, and finishes each output as rstd * (acc - mean * G_n) + B_n
+  // with G = gamma . W and B = beta . W (norm_columns = G then B, 2N f32).
+  const _Float16* norm_gamma;  // [K] or null
+  const float* norm_columns;   // [2N] or null
+  float norm_epsilon;
 };
 
 // Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
@@ -150,6 +164,12 @@ hipError_t launch_expand(int bits, bool f16, bool tile_major, const uint32_t* pa
 hipError_t launch_to_operand_order(int bits, const uint32_t* packed, uint32_t inner,
                                    uint32_t columns, uint32_t* codes, hipStream_t stream,
                                    bool glu_interleave = false, int parts = 1);
+// Fused row LayerNorm of a GEMM's input (GemmArgs::norm_columns): writes
+// gamma16 = f16(gamma) [K] and sums = G then B [2N] from the reference-format
+// codes and the f16 palette.
+hipError_t launch_norm_prepare(int bits, const uint32_t* packed, uint32_t inner, uint32_t columns,
+                               uint32_t group_columns, uint32_t groups, const void* palette, const float* gamma,
+                               const float* beta, void* gamma16, float* sums, hipStream_t stream);
 // The same codes moved from one P-part split to another (no packed source
 // needed); `blocks` = operand-order blocks of the weight.
 hipError_t launch_relayout(int bits, const uint32_t* src, int src_parts, uint32_t* dst, int dst_parts,

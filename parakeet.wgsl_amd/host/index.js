@@ -73,6 +73,7 @@ const TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 8650752;
 const FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 17301504;
 const REQUIRE_PRODUCTION_SIGNATURE = 1;
 const GEMM_GLU = 2;
+const GEMM_ROW_NORM = 4;
 const CONV_INPUT_GLU = 1;
 
 /** runtime-plan.ts:352-368 */
@@ -861,7 +862,8 @@ class PaletteGemmKernel {
     /** @type {any} */
     const d = {
       label: descriptor.label,
-      flags: (this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0) | (descriptor.glu ? GEMM_GLU : 0),
+      flags: (this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0) | (descriptor.glu ? GEMM_GLU : 0) |
+        (descriptor.rowNorm ? GEMM_ROW_NORM : 0),
       precision: fp32 ? "f32" : "f16",
       paletteBits,
       rows: descriptor.rows,
@@ -893,6 +895,15 @@ class PaletteGemmKernel {
       d.residualBytes = r.size;
     }
     if (descriptor.residualScale !== undefined) d.residualScale = descriptor.residualScale;
+    if (descriptor.rowNorm) {
+      // {gamma, beta, epsilon?}: the op multiplies LayerNorm(a) (no reference counterpart)
+      const { gamma, beta, epsilon } = descriptor.rowNorm;
+      d.normGamma = gamma.binding.buffer.address + BigInt(gamma.binding.offset);
+      d.normGammaBytes = gamma.binding.size;
+      d.normBeta = beta.binding.buffer.address + BigInt(beta.binding.offset);
+      d.normBetaBytes = beta.binding.size;
+      if (epsilon !== undefined) d.normEpsilon = epsilon;
+    }
     return d;
   }
 
@@ -1537,8 +1548,9 @@ class ParakeetEncoderGraph {
   /**
    * create(device, model, options?): options.batchSize (windows, default
    * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
-   * epilogue, no reference counterpart), options.featureFrames (default
-   * 1501).
+   * epilogue) and options.fusedNorms (the four LayerNorms that feed a GEMM
+   * run inside it), neither with a reference counterpart,
+   * options.featureFrames (default 1501).
    */
   static create(device, model, options) {
     try {
@@ -1574,7 +1586,7 @@ class ParakeetEncoderGraph {
     let handle;
     try {
       handle = native().encoderCreate(device.context, {
-        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, batchSize, frames,
+        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, fusedNorms: o.fusedNorms === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
         featureLengths: buffers.featureLengths.address, projector, projectorBias,

@@ -21,9 +21,11 @@ PRECISION = {"f16": 0, "f32": 1}
 ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
 REQUIRE_PRODUCTION_SIGNATURE = 0x1
 GEMM_GLU = 0x2
+GEMM_ROW_NORM = 0x4
 CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 ENCODER_FUSED_GLU = 0x1
+ENCODER_FUSED_NORMS = 0x2
 ENCODER_CHANNELS = 1024
 ENCODER_INTERMEDIATE = 4096
 # The fifteen dispatches of one encoder layer, in launch order
@@ -90,6 +92,11 @@ class GemmDesc(ctypes.Structure):
         ("residual_scale", ctypes.c_float),
         ("activation", ctypes.c_int32),
         ("prepared", ctypes.c_void_p),
+        ("norm_gamma", ctypes.c_void_p),
+        ("norm_gamma_bytes", ctypes.c_uint64),
+        ("norm_beta", ctypes.c_void_p),
+        ("norm_beta_bytes", ctypes.c_uint64),
+        ("norm_epsilon", ctypes.c_float),
     ]
 
 
@@ -720,10 +727,15 @@ class GemmOp:
                  bias: DeviceArray | None = None, residual: DeviceArray | None = None,
                  residual_scale: float | None = None, activation: str = "none",
                  prepared: PreparedWeight | None = None, label: str = "palette-gemm",
-                 production_only: bool = False, glu: bool = False, stream=None):
+                 production_only: bool = False, glu: bool = False, stream=None,
+                 norm_gamma: DeviceArray | None = None, norm_beta: DeviceArray | None = None,
+                 norm_epsilon: float = 0.0):
+        """With norm_gamma / norm_beta (f32 [inner]) the op multiplies the
+        row LayerNorm of `a` (PK_GEMM_ROW_NORM)."""
         precision = "f16" if palette.dtype == np.float16 else "f32"
         groups = palette.shape[0]
-        flags = (REQUIRE_PRODUCTION_SIGNATURE if production_only else 0) | (GEMM_GLU if glu else 0)
+        flags = ((REQUIRE_PRODUCTION_SIGNATURE if production_only else 0) | (GEMM_GLU if glu else 0) |
+                 (GEMM_ROW_NORM if norm_gamma is not None else 0))
         self.desc = GemmDesc(
             ctypes.sizeof(GemmDesc), flags,
             label.encode(), PRECISION[precision], bits, rows, inner, columns, groups,
@@ -734,7 +746,10 @@ class GemmOp:
             bias.ptr if bias is not None else None, bias.nbytes if bias is not None else 0,
             residual.ptr if residual is not None else None, residual.nbytes if residual is not None else 0,
             int(residual_scale is not None), float(residual_scale or 0.0), ACTIVATION[activation],
-            prepared.handle if prepared is not None else None)
+            prepared.handle if prepared is not None else None,
+            norm_gamma.ptr if norm_gamma is not None else None, norm_gamma.nbytes if norm_gamma is not None else 0,
+            norm_beta.ptr if norm_beta is not None else None, norm_beta.nbytes if norm_beta is not None else 0,
+            float(norm_epsilon))
         handle = ctypes.c_void_p()
         check(load().pk_gemm_create(ctx.handle, ctypes.byref(self.desc), stream, ctypes.byref(handle)))
         self.handle = handle.value
@@ -1081,7 +1096,7 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
 
 
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = False,
-                 subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
+                 fused_norms: bool = False, subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
                  projector=None, projector_bias=None, projected_output=None, projected_channels: int = 0,
                  label: str = "encoder") -> EncoderDesc:
     """An EncoderDesc over `layers` (dicts as encoder_layer takes), with the
@@ -1090,7 +1105,8 @@ def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frame
     keeps what it points to alive."""
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
-    desc = EncoderDesc(ctypes.sizeof(EncoderDesc), ENCODER_FUSED_GLU if fused_glu else 0, label.encode(),
+    flags = (ENCODER_FUSED_GLU if fused_glu else 0) | (ENCODER_FUSED_NORMS if fused_norms else 0)
+    desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
                        PRECISION["f16"], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),
                        _addr(output), ctypes.pointer(front) if front is not None else None, feature_frames,

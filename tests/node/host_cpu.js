@@ -85,6 +85,16 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
       Error, "has invalid transient palette weights");
   throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu", mutate: (d) => { d.paletteGroupColumns = 1024; } })),
       Error, "has invalid transient palette weights");
+  // rowNorm (PK_GEMM_ROW_NORM, no reference counterpart): f32 gamma and beta of K channels
+  const normTensor = (size) => ({ binding: { buffer: fakeBuffer, offset: 0, size } });
+  kernel.validateDescriptor(descriptor({ activation: "silu",
+    mutate: (d) => { d.rowNorm = { gamma: normTensor(4096), beta: normTensor(4096), epsilon: 1e-5 }; } }));
+  throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu",
+    mutate: (d) => { d.rowNorm = { gamma: normTensor(4096), beta: normTensor(4092) }; } })),
+      Error, "row norm needs gamma and beta of 4096 bytes");
+  throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu",
+    mutate: (d) => { d.rowNorm = { gamma: normTensor(4096), beta: normTensor(4096), epsilon: -1 }; } })),
+      Error, "epsilon >= 0");
   // arena.ts slice rules
   throwsLike(() => arena.slice("x", 100, 64), RangeError, "Invalid activation slice x");
   // the counters of a fused kernel: nothing is ever expanded

@@ -50,7 +50,7 @@ class Stack:
     """An EncoderOp over uploaded layers with its input, output and lengths
     (and the front end and projector when the stack has them)."""
 
-    def __init__(self, abi, ctx, scope, stack, *, fused_glu=False):
+    def __init__(self, abi, ctx, scope, stack, *, fused_glu=False, fused_norms=False):
         self.ctx = ctx
         self.valid = scope.put(stack.valid)
         self.output = scope.put(np.full_like(stack.x, 77))
@@ -73,7 +73,7 @@ class Stack:
                          projected_output=self.projected)
         self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
                                 input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
-                                fused_glu=fused_glu, **extra)
+                                fused_glu=fused_glu, fused_norms=fused_norms, **extra)
 
     def run(self, active=0, graph=False):
         self.op.enqueue(active, graph=graph)
@@ -92,10 +92,11 @@ def windows(array, frames, first, count):
     return array[first * frames:(first + count) * frames]
 
 
-@pytest.mark.parametrize("fused_glu", [False, True], ids=["pw1-then-glu", "glu-epilogue"])
-def test_encoder_layer_matches_both_oracle_chains(abi, ctx, scope, oracle, workloads, fused_glu):
+@pytest.mark.parametrize("fused_glu,fused_norms", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["separate-norms", "glu-epilogue", "fused-norms", "glu-epilogue-fused-norms"])
+def test_encoder_layer_matches_both_oracle_chains(abi, ctx, scope, oracle, workloads, fused_glu, fused_norms):
     stack = workloads.encoder_stack(seed=11, windows=2, frames=188, layers=1)
-    enc = Stack(abi, ctx, scope, stack, fused_glu=fused_glu)
+    enc = Stack(abi, ctx, scope, stack, fused_glu=fused_glu, fused_norms=fused_norms)
     try:
         assert enc.op.info()[0] == 15
         got = enc.run()
@@ -106,7 +107,8 @@ def test_encoder_layer_matches_both_oracle_chains(abi, ctx, scope, oracle, workl
         want = oracle.encoder(stack.x, stack.layers, stack.valid, batch=2, frames=188, gemm_mode=mode,
                               threads=THREADS)
         norm, worst = oracle.relative_errors(got, want)
-        print(f"one layer, fused_glu={fused_glu}, vs {mode}: norm {norm:.2e} max {worst:.2e}", flush=True)
+        print(f"one layer, fused_glu={fused_glu}, fused_norms={fused_norms}, vs {mode}: norm {norm:.2e} "
+              f"max {worst:.2e}", flush=True)
         assert norm <= 1e-2, (mode, norm, worst)
 
 
@@ -212,6 +214,31 @@ def test_encoder_fused_glu_matches_unfused(abi, ctx, scope, oracle, workloads):
     norm, worst = oracle.relative_errors(outs[1], outs[0])
     print(f"fused vs unfused GLU, 4 layers: norm {norm:.2e} max {worst:.2e}", flush=True)
     assert norm <= 1e-2, (norm, worst)
+
+
+def test_encoder_fused_norms_match_separate_norms(abi, ctx, scope, oracle, workloads):
+    """The four LayerNorms that feed a GEMM, run inside it
+    (PK_ENCODER_FUSED_NORMS) or as the reference's separate dispatches:
+    8 layers agree within 1e-2, both stay within 1e-2 of the f64 chain, and
+    the fused stack is no farther from it than the separate one by more than
+    the f16 rounding the separate LayerNorm output adds."""
+    stack = workloads.encoder_stack(seed=16, windows=4, frames=188, layers=8)
+    outs = []
+    for fused in (True, False):
+        enc = Stack(abi, ctx, scope, stack, fused_norms=fused)
+        try:
+            outs.append(enc.run())
+        finally:
+            enc.release()
+    want = oracle.encoder(stack.x, stack.layers, stack.valid, batch=4, frames=188, gemm_mode="f64", threads=THREADS)
+    norm, worst = oracle.relative_errors(outs[0], outs[1])
+    fused_err, _ = oracle.relative_errors(outs[0], want)
+    separate_err, _ = oracle.relative_errors(outs[1], want)
+    print(f"fused vs separate norms, 8 layers: {norm:.2e} (max {worst:.2e}); vs f64 chain: fused {fused_err:.2e}, "
+          f"separate {separate_err:.2e}", flush=True)
+    assert norm <= 1e-2, (norm, worst)
+    assert fused_err <= 1e-2 and separate_err <= 1e-2
+    assert fused_err <= separate_err + 2e-3, (fused_err, separate_err)
 
 
 def test_encoder_rejects_bad_active_batch(abi, ctx, scope, workloads):

@@ -722,3 +722,83 @@ def test_gemm_group_errors(abi, ctx, scope, workloads):
             group.release()
     finally:
         op.release()
+
+
+@pytest.mark.parametrize("rows,inner,columns,bits,groups,activation,scale", [
+    (3008, 1024, 4096, 5, 1, "silu", None),    # FF expand of the encoder (LayerNorm -> W1 -> SiLU)
+    (752, 1024, 3072, 5, 3, "none", None),     # QKV, 3 palette groups of 1024 columns
+    (333, 1024, 2048, 6, 1, "none", None),     # row tail, 6-bit
+    (188, 2048, 1024, 5, 1, "none", 0.5),      # K = 2048, residual epilogue
+])
+def test_row_norm_fused_gemm(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits, groups, activation, scale):
+    """PK_GEMM_ROW_NORM: the op multiplies LayerNorm(A) without a pass that
+    writes it. Against the oracle's LayerNorm (f32 statistics, f16 output,
+    layernorm.ts:309-390) followed by the GEMM, in the reference f16 chain
+    and in f64, on every pair-code tile (the kernels that run it), with a
+    row mean far from zero so the mean-correction term matters."""
+    rng = np.random.default_rng(rows + inner)
+    case = workloads.gemm_case(rows + inner + columns, rows, inner, columns, bits, groups=groups,
+                               activation=activation, residual_scale=scale)
+    x = (rng.standard_normal((rows, inner)) * 1.5 + 0.7).astype(np.float16)
+    gamma = (1.0 + 0.2 * rng.standard_normal(inner)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(inner)).astype(np.float32)
+    ln = oracle.layernorm(x, gamma, beta)
+    ref_case = workloads.GemmCase("ln-gemm", ln, case.weight, residual=case.residual, residual_scale=scale,
+                                  activation=activation)
+    ref = oracle_gemm(oracle, ref_case, "f16-chain")
+    truth = oracle_gemm(oracle, ref_case, "f64")
+    w = case.weight
+    a, palette = scope.put(x), scope.put(w.palette)
+    g_d, b_d = scope.put(gamma), scope.put(beta)
+    res = scope.put(case.residual)
+    out = scope.put(np.zeros((rows, columns), np.float16))
+    op = abi.GemmOp(ctx, a=a, packed=scope.put(w.packed), palette=palette, output=out, bits=bits, rows=rows,
+                    inner=inner, columns=columns, residual=res, residual_scale=scale, activation=activation,
+                    norm_gamma=g_d, norm_beta=b_d, label="row-norm")
+    try:
+        planned = op.plan().kernel.decode()
+        assert planned.startswith("pk_gemm_f16p_"), planned
+        variants = [planned] + [n for n in pair_code_names(abi) if n != planned]
+        for name in variants:
+            op.set_variant(pair_code_index(abi, name))
+            op.enqueue()
+            ctx.synchronize()
+            got = out.download()
+            assert np.all(np.isfinite(got.astype(np.float32))), name
+            norm_ref, _ = oracle.relative_errors(got, ref)
+            norm_truth, _ = oracle.relative_errors(got, truth)
+            print(name, f"vs f16 chain {norm_ref:.2e}, vs f64 {norm_truth:.2e}", flush=True)
+            assert norm_ref <= F16_TOL_REFERENCE and norm_truth <= F16_TOL_TRUTH, (name, norm_ref, norm_truth)
+        with pytest.raises(abi.PaletteRangeError, match="has no fused row norm"):
+            op.set_variant(abi.small_m_variants()[0])
+    finally:
+        op.release()
+
+
+def pair_code_names(abi):
+    return [abi.describe_variant("f16", v).kernel5.decode() for v in range(abi.variant_count("f16"))
+            if abi.describe_variant("f16", v).kernel5.decode().startswith("pk_gemm_f16p_")]
+
+
+def pair_code_index(abi, name5):
+    for v in range(abi.variant_count("f16")):
+        d = abi.describe_variant("f16", v)
+        if d.kernel5.decode() == name5 or d.kernel6.decode() == name5:
+            return v
+    raise KeyError(name5)
+
+
+def test_row_norm_contract_errors(abi, ctx, scope, workloads):
+    """The fused row norm's own checks: K % 64, no GLU, gamma / beta sizes."""
+    case = workloads.gemm_case(4, 64, 1024, 1024, 5)
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    out = scope.empty((64, 1024), np.float16)
+    g = scope.put(np.ones(1024, np.float32))
+    short = scope.put(np.ones(512, np.float32))
+    with pytest.raises(abi.PaletteError, match="row norm needs gamma and beta"):
+        abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=5, rows=64, inner=1024,
+                   columns=1024, norm_gamma=g, norm_beta=short, label="lbl")
+    with pytest.raises(abi.PaletteError, match="row norm needs f16"):
+        abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=scope.empty((64, 512), np.float16), bits=5,
+                   rows=64, inner=1024, columns=1024, glu=True, norm_gamma=g, norm_beta=g, label="lbl")
