@@ -87,6 +87,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
     p.add_argument("--no-ff-block", action="store_true", help="encoder workloads: skip the FF block's extra line")
+    p.add_argument("--unchained-norms", action="store_true",
+                   help="encoder workloads: launch every LayerNorm on its own (default: each layer's last "
+                        "LayerNorm also writes the next layer's first)")
     p.add_argument("--fused-norms", action="store_true",
                    help="encoder workloads: run the four LayerNorms that feed a GEMM inside those GEMMs "
                         "(PK_GEMM_ROW_NORM; default: separate launches, as the reference does)")
@@ -509,9 +512,12 @@ def run_encoder(args, abi, ctx, decoder=False):
                         frames=stack.frames, subsampling=front, feature_frames=stack.feature_frames,
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
-                        projected_output=projected, fused_norms=args.fused_norms, label="encoder")
+                        projected_output=projected, fused_norms=args.fused_norms,
+                        unchained_norms=args.unchained_norms, label="encoder")
     launches, device_bytes = enc.info()
     fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
+    # the LN ff1 of layers after the first runs in the LN out launch before it
+    chained = not (args.fused_norms or args.unchained_norms) and len(stack.layers) > 1
     stream = ctx.stream
     tdt = None
     if decoder:
@@ -575,6 +581,25 @@ def run_encoder(args, abi, ctx, decoder=False):
     dispatches = {}
     for name, ms, (flops, nbytes) in zip(names, per_kind_ms, costs):
         us = ms * 1e3
+        if chained and name == "norm_feed_forward1":
+            # layer 0's own launch; later layers' slots are empty (written by norm_out)
+            us = durations[nf + list(abi.ENCODER_DISPATCHES).index(name)] * 1e3
+            dispatches[name] = {"avg_us": us, "gbs": nbytes / (us * 1e-6) / 1e9, "flops": 0,
+                                "algorithmic_bytes": nbytes, "launches_per_pass": 1,
+                                "later_layers_chained_into_norm_out": True}
+            continue
+        if chained and name == "norm_out":
+            # LN out of layer l and LN ff1 of layer l + 1 in one launch: the rows
+            # read once and written twice, two gamma / beta pairs (the last
+            # layer: LN out alone); averaged over the layers
+            n = len(stack.layers)
+            act = (nbytes - 2 * 4096) / 2
+            both = 3 * act + 4 * 4096
+            avg = ((n - 1) * both + nbytes) / n
+            dispatches[name] = {"avg_us": us, "gbs": avg / (us * 1e-6) / 1e9, "flops": 0,
+                                "algorithmic_bytes": avg, "launches_per_pass": n,
+                                "chains_next_norm_feed_forward1": True}
+            continue
         if name in fused_norms:
             # runs inside the GEMM after it; the slot's two events are back to back
             dispatches[name] = {"avg_us": us, "fused_into_next_gemm": True, "flops": 0, "algorithmic_bytes": 0,
@@ -650,9 +675,11 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "heads": 8, "subsampling": "dw_striding 8x, 256 channels", "projector": "1024->640",
                    "palette_bits": {"ff/qkv/pointwise/subsampling/projector": 5, "o_proj": 6},
                    "dispatch_slots_per_pass": launches,
-                   "launches_per_pass": launches - len(fused_norms) * len(stack.layers),
+                   "launches_per_pass": launches - len(fused_norms) * len(stack.layers) -
+                                        (len(stack.layers) - 1 if chained else 0),
                    "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
-                                 if args.fused_norms else "separate launches",
+                                 if args.fused_norms else "separate launches" if not chained else
+                                 "separate launches; each layer's last LayerNorm also writes the next layer's first",
                    "graph_replay": True,
                    "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,

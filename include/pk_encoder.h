@@ -6,8 +6,11 @@
  *
  * Reference interfaces replaced: the encoder graph of src/webgpu/encoder.ts -
  * createEncoderLayerDispatches (:1868-2135), fifteen dispatch slots per
- * layer in this order (with PK_ENCODER_FUSED_NORMS the four LayerNorms that
- * feed a GEMM run inside that GEMM and their slots launch nothing):
+ * layer in this order (after the first layer the LN ff1 slot launches
+ * nothing: the LN out before it wrote that LayerNorm too, unless
+ * PK_ENCODER_UNCHAINED_NORMS; with PK_ENCODER_FUSED_NORMS the four
+ * LayerNorms that feed a GEMM run inside that GEMM and their slots launch
+ * nothing):
  *   LN ff1 -> FF1 W1 + SiLU -> FF1 W2 + 0.5 x         (x1)
  *   LN att -> QKV -> relative attention -> Wo + x1    (x2)
  *   LN conv -> PW1 -> GLU/DW9/BN/SiLU -> PW2 + x2     (x3)
@@ -44,6 +47,12 @@ extern "C" {
    about 5% slower than with the separate LayerNorm launches, which stay
    the default. */
 #define PK_ENCODER_FUSED_NORMS 0x2u
+/* Without this flag (and without PK_ENCODER_FUSED_NORMS), the last
+   LayerNorm of each layer also writes the next layer's first LayerNorm
+   (LN ff1 of its own output) in the same launch, so layers after the
+   first launch nothing in their LN ff1 slot: 23 fewer launches per 24-layer
+   pass, bit-identical outputs. This flag keeps one launch per LayerNorm. */
+#define PK_ENCODER_UNCHAINED_NORMS 0x4u
 
 typedef struct pk_encoder pk_encoder;
 

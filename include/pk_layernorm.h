@@ -42,6 +42,19 @@ typedef struct pk_layernorm_desc {
   uint64_t output_bytes;       /* capacity */
   int32_t has_epsilon;         /* 0: epsilon 1e-5 (the reference default) */
   float epsilon;
+  /* Optional chained LayerNorm, no reference counterpart (the reference
+     runs two dispatches): with next_output set, the same launch also
+     writes next_output = LayerNorm(output as stored) with next_gamma /
+     next_beta ([channels] f32) and the same epsilon, bit-identical to a
+     second LayerNorm over the output. Rows of at most 4096 bytes (2048 f16
+     or 1024 f32 channels); next_output must not overlap output and must be
+     the input or not overlap it. NULL next_output: none. */
+  const float *next_gamma;
+  uint64_t next_gamma_bytes;   /* exactly 4 * channels */
+  const float *next_beta;
+  uint64_t next_beta_bytes;    /* exactly 4 * channels */
+  void *next_output;           /* [rows, channels] */
+  uint64_t next_output_bytes;  /* capacity */
 } pk_layernorm_desc;
 
 int pk_layernorm_validate(const pk_layernorm_desc *desc);

@@ -858,12 +858,14 @@ static void layernorm_finalize(napi_env env, void *data, void *hint) {
 }
 
 /* {label, precision, rows, channels, input, inputBytes, gamma, gammaBytes,
-   beta, betaBytes, output, outputBytes, epsilon?} */
+   beta, betaBytes, output, outputBytes, epsilon?, nextGamma?,
+   nextGammaBytes?, nextBeta?, nextBetaBytes?, nextOutput?,
+   nextOutputBytes?} (the next* fields: a chained LayerNorm) */
 static int parse_layernorm_desc(napi_env env, napi_value o, pk_layernorm_desc *d, char **label) {
   memset(d, 0, sizeof *d);
   d->struct_size = sizeof *d;
   *label = NULL;
-  uint64_t input = 0, gamma = 0, beta = 0, output = 0;
+  uint64_t input = 0, gamma = 0, beta = 0, output = 0, next_gamma = 0, next_beta = 0, next_output = 0;
   parse_precision(env, o, &d->precision);
   if (!prop_u32(env, o, "rows", &d->rows) || !prop_u32(env, o, "channels", &d->channels) ||
       !prop_u64(env, o, "input", &input) || !prop_u64(env, o, "inputBytes", &d->input_bytes) ||
@@ -880,10 +882,16 @@ static int parse_layernorm_desc(napi_env env, napi_value o, pk_layernorm_desc *d
     d->has_epsilon = 1;
     d->epsilon = (float)e;
   }
+  if (prop_u64(env, o, "nextGamma", &next_gamma)) prop_u64(env, o, "nextGammaBytes", &d->next_gamma_bytes);
+  if (prop_u64(env, o, "nextBeta", &next_beta)) prop_u64(env, o, "nextBetaBytes", &d->next_beta_bytes);
+  if (prop_u64(env, o, "nextOutput", &next_output)) prop_u64(env, o, "nextOutputBytes", &d->next_output_bytes);
   d->input = (const void *)(uintptr_t)input;
   d->gamma = (const float *)(uintptr_t)gamma;
   d->beta = (const float *)(uintptr_t)beta;
   d->output = (void *)(uintptr_t)output;
+  d->next_gamma = (const float *)(uintptr_t)next_gamma;
+  d->next_beta = (const float *)(uintptr_t)next_beta;
+  d->next_output = (void *)(uintptr_t)next_output;
   *label = prop_string(env, o, "label");
   d->label = *label;
   return 1;
@@ -1211,7 +1219,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
   return ok;
 }
 
-/* Parses an encoder descriptor: {label, fusedGlu?, fusedNorms?, batchSize, frames,
+/* Parses an encoder descriptor: {label, fusedGlu?, fusedNorms?, unchainedNorms?, batchSize, frames,
    layers: [layer...], validLengths, input, output, subsampling?,
    featureFrames?, featureLengths?, projector?, projectorBias?,
    projectedChannels?, projectedOutput?}. The layer array, front end and
@@ -1225,9 +1233,12 @@ static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   bool glu = false;
   if (prop(env, o, "fusedGlu", &v) && napi_get_value_bool(env, v, &glu) == napi_ok && glu)
     d->flags |= PK_ENCODER_FUSED_GLU;
-  bool fused_norms = false;
+  bool fused_norms = false, unchained_norms = false;
   if (prop(env, o, "fusedNorms", &v) && napi_get_value_bool(env, v, &fused_norms) == napi_ok && fused_norms)
     d->flags |= PK_ENCODER_FUSED_NORMS;
+  if (prop(env, o, "unchainedNorms", &v) && napi_get_value_bool(env, v, &unchained_norms) == napi_ok &&
+      unchained_norms)
+    d->flags |= PK_ENCODER_UNCHAINED_NORMS;
   if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
       !prop(env, o, "layers", &layers) || napi_get_array_length(env, layers, &n) != napi_ok || n == 0) {
     bad_argument(env, "encoder descriptor is missing a required field");

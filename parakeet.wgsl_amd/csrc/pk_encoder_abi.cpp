@@ -70,6 +70,7 @@ struct pk_encoder {
   uint32_t batch = 0, frames = 0, layers = 0, rows = 0;
   bool fused_glu = false;
   bool fused_norms = false;
+  bool chained_norms = true;  // norm_out also writes the next layer's norm_feed_forward1
   const uint32_t* valid_lengths = nullptr;
   const void* input = nullptr;
   void* output = nullptr;
@@ -300,9 +301,12 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
 //   P -conv-> O -PW2(+C)-> D -LN-> B -W1-> H -W2(+0.5 D)-> B -LN-> A (the
 //   last layer writes the output instead). With PK_ENCODER_FUSED_NORMS the
 //   four LayerNorms before W1, QKV, PW1 and W1 are not created: those GEMMs
-//   read the LayerNorm's input (A, B, C, D) with PK_GEMM_ROW_NORM.
-int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream_t stream, LayerOps& l,
-                bool validate_only) {
+//   read the LayerNorm's input (A, B, C, D) with PK_GEMM_ROW_NORM. Otherwise,
+//   unless PK_ENCODER_UNCHAINED_NORMS, the last LayerNorm of a layer also
+//   writes B = LN ff1(A) of the layer `next` (a chained LayerNorm) and that
+//   layer creates no LayerNorm of its own there.
+int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer* next, uint32_t li,
+                hipStream_t stream, LayerOps& l, bool validate_only) {
   const uint64_t R = e->rows;
   const std::string prefix = e->label + ".layers." + std::to_string(li);
   std::string label;
@@ -310,7 +314,7 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
     label = prefix + suffix;
     return label.c_str();
   };
-  auto norm = [&](int i, const char* suffix, const void* in, void* out) {
+  auto norm = [&](int i, const char* suffix, const void* in, void* out, void* chained_out = nullptr) {
     pk_layernorm_desc d{};
     d.struct_size = sizeof d;
     d.label = name(suffix);
@@ -325,6 +329,14 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
     d.beta_bytes = kC * 4;
     d.output = out;
     d.output_bytes = R * kC * 2;
+    if (chained_out) {
+      d.next_gamma = next->norm_gamma[0];
+      d.next_gamma_bytes = kC * 4;
+      d.next_beta = next->norm_beta[0];
+      d.next_beta_bytes = kC * 4;
+      d.next_output = chained_out;
+      d.next_output_bytes = R * kC * 2;
+    }
     return validate_only ? pk_layernorm_validate(&d) : pk_layernorm_create(e->ctx, &d, &l.norm[i]);
   };
   // LayerNorm i runs inside the GEMM it feeds (not with the GLU epilogue).
@@ -366,7 +378,9 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
     return out;
   };
   s = PK_OK;
-  const void* in = norm_into(0, ".norm_feed_forward1", x, e->b);
+  // A chained LayerNorm of the layer before wrote B = LN ff1(A) already.
+  const bool chained_in = e->chained_norms && li > 0;
+  const void* in = chained_in ? e->b : norm_into(0, ".norm_feed_forward1", x, e->b);
   if (s || (s = gemm(&l.ff1a, "-feed-forward1-linear1", w.ff1_linear1, 5, kC, kHidden, 1, in, e->h, nullptr, 0.0f,
                      PK_ACTIVATION_SILU, 0)))
     return s;
@@ -439,7 +453,7 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, uint32_t li, hipStream
                 0.5f, PK_ACTIVATION_NONE, 0)))
     return s;
   const bool last = li + 1 == e->layers;
-  return norm(4, ".norm_out", e->b, last ? e->output : e->a);
+  return norm(4, ".norm_out", e->b, last ? e->output : e->a, e->chained_norms && next ? e->b : nullptr);
 }
 
 int build_projector(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, pk_gemm_op** op,
@@ -547,6 +561,7 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->rows = d->batch_size * d->frames;
   e->fused_glu = (d->flags & PK_ENCODER_FUSED_GLU) != 0;
   e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
+  e->chained_norms = (d->flags & (PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS)) == 0;
   e->valid_lengths = d->valid_lengths;
   e->input = d->input;
   e->output = d->output;
@@ -568,7 +583,7 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
   if (d->struct_size != sizeof(pk_encoder_desc))
     return fail(PK_INVALID_ARGUMENT, "pk_encoder_desc.struct_size mismatch");
   const char* label = d->label ? d->label : "encoder";
-  if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS))
+  if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS))
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if (d->precision != PK_PRECISION_F16)
     return fail(PK_INVALID_ARGUMENT, "%s: the encoder stack runs in f16", label);
@@ -608,7 +623,9 @@ int build_all(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, bool 
     if (int s = build_front(e, *d->subsampling, stream, e->front_ops, validate_only)) return s;
   e->ops.resize(e->layers);
   for (uint32_t li = 0; li < e->layers; ++li)
-    if (int s = build_layer(e, d->layer[li], li, stream, e->ops[li], validate_only)) return s;
+    if (int s = build_layer(e, d->layer[li], li + 1 < e->layers ? &d->layer[li + 1] : nullptr, li, stream, e->ops[li],
+                            validate_only))
+      return s;
   if (e->projected_channels)
     if (int s = build_projector(e, d, stream, &e->projector, validate_only)) return s;
   return PK_OK;

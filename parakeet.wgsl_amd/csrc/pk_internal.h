@@ -287,7 +287,14 @@ struct LayerNormArgs {
   uint32_t rows;       // active rows
   uint32_t channels;   // multiple of 4
   float epsilon;
+  // Chained LayerNorm (null next_output: none): next_output =
+  // LayerNorm(output as stored) with next_gamma / next_beta and the same
+  // epsilon; rows of at most kLayerNormChainBytes.
+  const float* next_gamma;
+  const float* next_beta;
+  void* next_output;
 };
+constexpr uint32_t kLayerNormChainBytes = 4096;
 uint32_t layernorm_grid(uint32_t rows);
 hipError_t launch_layernorm(bool f16, const LayerNormArgs& args, hipStream_t stream, hipEvent_t start = nullptr,
                             hipEvent_t stop = nullptr);

@@ -10,20 +10,25 @@
 // trip before its two sums are reduced across the wavefront with cross-lane
 // exchanges (no LDS, no barrier). The lane then normalises the vectors it
 // still holds in registers (the first 4 KB of a row: 2048 f16 or 1024 f32
-// channels) or re-reads from L2 beyond that.
+// channels) or re-reads from L2 beyond that. A chained launch (rows of at
+// most 4 KB) then normalises the rounded output it still holds with a
+// second gamma and beta, loaded in the first burst too: the sums run over
+// the same values in the same lane order as a separate launch over the
+// stored output, so both outputs are bit-identical to two launches.
 #include "pk_internal.h"
 
 namespace pk {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
-constexpr uint32_t kHeldBytes = 4096;  // bytes of a row kept in registers
-
-template <typename T, int VEC>
+// HELD_BYTES: bytes of a row kept in registers, 2 KB for rows that fit
+// (fewer registers, more waves per SIMD) or kLayerNormChainBytes.
+template <typename T, int VEC, uint32_t HELD_BYTES, bool CHAIN>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void layernorm_kernel(LayerNormArgs args) {
   typedef T V __attribute__((ext_vector_type(VEC)));
-  constexpr int kHeld = (int)(kHeldBytes / (64u * VEC * sizeof(T)));  // vectors a lane keeps
+  constexpr int kHeld = (int)(HELD_BYTES / (64u * VEC * sizeof(T)));  // vectors a lane keeps
   constexpr int F4 = VEC / 4;                                 // float4s of gamma per vector
+  constexpr int kNext = CHAIN ? kHeld : 1;
   const int lane = threadIdx.x & 63;
   const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= args.rows) return;
@@ -35,67 +40,94 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layernorm_kernel(LayerNorm
 
   V held[kHeld];
   float4 g_held[kHeld][F4], b_held[kHeld][F4];
+  float4 g_next[kNext][F4], b_next[kNext][F4];
 #pragma unroll
   for (int i = 0; i < kHeld; ++i) {
     const uint32_t v = lane + 64u * i;
     if (v < vectors) held[i] = in[v];
   }
+  auto load_affine = [&](const float* g, const float* b, int count, float4 (*gd)[F4], float4 (*bd)[F4]) {
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
 #pragma unroll
-  for (int i = 0; i < kHeld; ++i) {
-    const uint32_t v = lane + 64u * i;
-    if (v < vectors)
+    for (int i = 0; i < count; ++i) {
+      const uint32_t v = lane + 64u * i;
+      if (v < vectors)
 #pragma unroll
-      for (int f = 0; f < F4; ++f) {
-        g_held[i][f] = gamma[v * F4 + f];
-        b_held[i][f] = beta[v * F4 + f];
-      }
-  }
-  float sum = 0.0f, square = 0.0f;
-  auto accumulate = [&](const V& x) {
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      const float xc = (float)x[c];
-      sum += xc;
-      square = __builtin_fmaf(xc, xc, square);
+        for (int f = 0; f < F4; ++f) {
+          gd[i][f] = g4[v * F4 + f];
+          bd[i][f] = b4[v * F4 + f];
+        }
     }
   };
-#pragma unroll
-  for (int i = 0; i < kHeld; ++i)
-    if (lane + 64u * i < vectors) accumulate(held[i]);
-  for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) accumulate(in[v]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    sum += __shfl_xor(sum, off, 64);
-    square += __shfl_xor(square, off, 64);
-  }
-  const float inverse_channels = 1.0f / (float)args.channels;
-  const float mean = sum * inverse_channels;
-  const float variance = fmaxf(square * inverse_channels - mean * mean, 0.0f);
-  const float inverse_std = 1.0f / __builtin_sqrtf(variance + args.epsilon);
+  load_affine(args.gamma, args.beta, kHeld, g_held, b_held);
+  if constexpr (CHAIN) load_affine(args.next_gamma, args.next_beta, kNext, g_next, b_next);
 
-  auto normalize = [&](uint32_t v, const V& x, const float4 (&g4)[F4], const float4 (&b4)[F4]) {
+  // Mean and 1 / sqrt(variance + epsilon) of the row whose held vectors are
+  // `x` (and, past those, re-read from `rest`).
+  auto statistics = [&](const V (&x)[kHeld], const V* rest) {
+    float sum = 0.0f, square = 0.0f;
+    auto accumulate = [&](const V& xv) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        const float xc = (float)xv[c];
+        sum += xc;
+        square = __builtin_fmaf(xc, xc, square);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i)
+      if (lane + 64u * i < vectors) accumulate(x[i]);
+    for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) accumulate(rest[v]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      sum += __shfl_xor(sum, off, 64);
+      square += __shfl_xor(square, off, 64);
+    }
+    const float inverse_channels = 1.0f / (float)args.channels;
+    const float mean = sum * inverse_channels;
+    const float variance = fmaxf(square * inverse_channels - mean * mean, 0.0f);
+    return make_float2(mean, 1.0f / __builtin_sqrtf(variance + args.epsilon));
+  };
+  auto normalize = [&](const V& x, float2 st, const float4 (&g4)[F4], const float4 (&b4)[F4]) {
     V y;
 #pragma unroll
     for (int f = 0; f < F4; ++f) {
       const float gg[4] = {g4[f].x, g4[f].y, g4[f].z, g4[f].w}, bb[4] = {b4[f].x, b4[f].y, b4[f].z, b4[f].w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) y[4 * f + c] = (T)(((float)x[4 * f + c] - mean) * inverse_std * gg[c] + bb[c]);
+      for (int c = 0; c < 4; ++c) y[4 * f + c] = (T)(((float)x[4 * f + c] - st.x) * st.y * gg[c] + bb[c]);
     }
-    out[v] = y;
+    return y;
   };
+
+  const float2 st = statistics(held, in);
 #pragma unroll
   for (int i = 0; i < kHeld; ++i) {
     const uint32_t v = lane + 64u * i;
-    if (v < vectors) normalize(v, held[i], g_held[i], b_held[i]);
-  }
-  for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) {
-    float4 g4[F4], b4[F4];
-#pragma unroll
-    for (int f = 0; f < F4; ++f) {
-      g4[f] = gamma[v * F4 + f];
-      b4[f] = beta[v * F4 + f];
+    if (v < vectors) {
+      held[i] = normalize(held[i], st, g_held[i], b_held[i]);
+      out[v] = held[i];
     }
-    normalize(v, in[v], g4, b4);
+  }
+  if constexpr (CHAIN) {
+    // The whole row is held (the host checks its size): normalise it again.
+    V* next = static_cast<V*>(args.next_output) + (uint64_t)row * vectors;
+    const float2 st2 = statistics(held, nullptr);
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i) {
+      const uint32_t v = lane + 64u * i;
+      if (v < vectors) next[v] = normalize(held[i], st2, g_next[i], b_next[i]);
+    }
+  } else {
+    for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) {
+      float4 g4[F4], b4[F4];
+#pragma unroll
+      for (int f = 0; f < F4; ++f) {
+        g4[f] = gamma[v * F4 + f];
+        b4[f] = beta[v * F4 + f];
+      }
+      out[v] = normalize(in[v], st, g4, b4);
+    }
   }
 }
 
@@ -109,9 +141,23 @@ hipError_t launch_layernorm(bool f16, const LayerNormArgs& args, hipStream_t str
   if (grid == 0) return hipSuccess;
   // 16-byte f16 vectors need rows of whole vectors (the bindings are
   // 16-byte aligned).
-  void (*kernel)(LayerNormArgs) = !f16                     ? layernorm_kernel<float, 4>
-                                  : args.channels % 8u == 0u ? layernorm_kernel<_Float16, 8>
-                                                             : layernorm_kernel<_Float16, 4>;
+  const bool chain = args.next_output != nullptr;
+  const uint64_t row_bytes = (uint64_t)args.channels * (f16 ? 2u : 4u);
+  if (chain && row_bytes > kLayerNormChainBytes) return hipErrorInvalidValue;
+  const bool small = row_bytes <= 2048u;
+  const int shape = !f16 ? 0 : args.channels % 8u == 0u ? 1 : 2;  // f32 x4, f16 x8, f16 x4
+  typedef void (*Kernel)(LayerNormArgs);
+  static const Kernel kernels[3][2][2] = {
+      {{layernorm_kernel<float, 4, kLayerNormChainBytes, false>, layernorm_kernel<float, 4, kLayerNormChainBytes, true>},
+       {layernorm_kernel<float, 4, 2048, false>, layernorm_kernel<float, 4, 2048, true>}},
+      {{layernorm_kernel<_Float16, 8, kLayerNormChainBytes, false>,
+        layernorm_kernel<_Float16, 8, kLayerNormChainBytes, true>},
+       {layernorm_kernel<_Float16, 8, 2048, false>, layernorm_kernel<_Float16, 8, 2048, true>}},
+      {{layernorm_kernel<_Float16, 4, kLayerNormChainBytes, false>,
+        layernorm_kernel<_Float16, 4, kLayerNormChainBytes, true>},
+       {layernorm_kernel<_Float16, 4, 2048, false>, layernorm_kernel<_Float16, 4, 2048, true>}},
+  };
+  const Kernel kernel = kernels[shape][small][chain];
   if (start || stop)
     hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, stream, start, stop, 0, args);
   else

@@ -53,6 +53,25 @@ int validate_layernorm_desc(const pk_layernorm_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "%s bindings must be 16-byte aligned", label);
   if (d->has_epsilon && !(d->epsilon >= 0.0f))
     return fail(PK_INVALID_ARGUMENT, "%s epsilon must be a non-negative number", label);
+  if (d->next_output) {
+    // The chained LayerNorm holds the whole row in registers.
+    if ((uint64_t)d->channels * elem > pk::kLayerNormChainBytes)
+      return fail(PK_RANGE_ERROR, "%s chained LayerNorm needs rows of at most %u bytes", label,
+                  pk::kLayerNormChainBytes);
+    if (d->next_output_bytes < bytes)
+      return fail(PK_RANGE_ERROR, "%s next output needs %llu bytes; arena slice has %llu", label,
+                  (unsigned long long)bytes, (unsigned long long)d->next_output_bytes);
+    if (!d->next_gamma || d->next_gamma_bytes != affine || !d->next_beta || d->next_beta_bytes != affine)
+      return fail(PK_INVALID_ARGUMENT, "%s next gamma and beta must be float32 [%u], %llu bytes", label, d->channels,
+                  (unsigned long long)affine);
+    if (!aligned(d->next_output, 16) || !aligned(d->next_gamma, 16) || !aligned(d->next_beta, 16))
+      return fail(PK_INVALID_ARGUMENT, "%s bindings must be 16-byte aligned", label);
+    const auto at = [](const void* p) { return reinterpret_cast<uintptr_t>(p); };
+    const auto overlap = [&](const void* p, const void* q) { return at(p) < at(q) + bytes && at(q) < at(p) + bytes; };
+    if (overlap(d->next_output, d->output) || (d->next_output != d->input && overlap(d->next_output, d->input)))
+      return fail(PK_INVALID_ARGUMENT, "%s next output must not overlap the output, and be the input or not overlap it",
+                  label);
+  }
   return PK_OK;
 }
 
@@ -79,6 +98,9 @@ int pk_layernorm_create(pk_context* ctx, const pk_layernorm_desc* d, pk_layernor
   op->args.rows = d->rows;
   op->args.channels = d->channels;
   op->args.epsilon = d->has_epsilon ? d->epsilon : 1e-5f;
+  op->args.next_gamma = d->next_output ? d->next_gamma : nullptr;
+  op->args.next_beta = d->next_output ? d->next_beta : nullptr;
+  op->args.next_output = d->next_output;
   *out = op;
   return ok();
 }

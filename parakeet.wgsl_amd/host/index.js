@@ -1099,7 +1099,7 @@ class LayerNormKernel {
     const affineBytes = descriptor.channels * 4;
     requireChannelTensor(descriptor.gamma, descriptor.channels, affineBytes, `${descriptor.label} gamma`);
     requireChannelTensor(descriptor.beta, descriptor.channels, affineBytes, `${descriptor.label} beta`);
-    return {
+    const d = {
       label: descriptor.label,
       precision: this.precision,
       rows: descriptor.rows,
@@ -1114,6 +1114,20 @@ class LayerNormKernel {
       outputBytes: output.size,
       epsilon: descriptor.epsilon === undefined ? 1e-5 : descriptor.epsilon,
     };
+    if (descriptor.next) {
+      // {gamma, beta, output}: the same dispatch also writes LayerNorm(output)
+      // with these parameters (a chained LayerNorm, no reference counterpart)
+      const { gamma, beta } = descriptor.next;
+      requireChannelTensor(gamma, descriptor.channels, affineBytes, `${descriptor.label} next gamma`);
+      requireChannelTensor(beta, descriptor.channels, affineBytes, `${descriptor.label} next beta`);
+      const next = this.arena.binding(descriptor.next.output);
+      Object.assign(d, {
+        nextGamma: addressOf(gamma.binding), nextGammaBytes: gamma.binding.size,
+        nextBeta: addressOf(beta.binding), nextBetaBytes: beta.binding.size,
+        nextOutput: addressOf(next), nextOutputBytes: next.size,
+      });
+    }
+    return d;
   }
 
   validateDescriptor(descriptor) {
@@ -1548,9 +1562,11 @@ class ParakeetEncoderGraph {
   /**
    * create(device, model, options?): options.batchSize (windows, default
    * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
-   * epilogue) and options.fusedNorms (the four LayerNorms that feed a GEMM
-   * run inside it), neither with a reference counterpart,
-   * options.featureFrames (default 1501).
+   * epilogue), options.fusedNorms (the four LayerNorms that feed a GEMM
+   * run inside it) and options.unchainedNorms (one launch per LayerNorm;
+   * by default a layer's last LayerNorm also writes the next layer's
+   * first), none with a reference counterpart, options.featureFrames
+   * (default 1501).
    */
   static create(device, model, options) {
     try {
@@ -1586,7 +1602,8 @@ class ParakeetEncoderGraph {
     let handle;
     try {
       handle = native().encoderCreate(device.context, {
-        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, fusedNorms: o.fusedNorms === true, batchSize, frames,
+        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, fusedNorms: o.fusedNorms === true,
+        unchainedNorms: o.unchainedNorms === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
         featureLengths: buffers.featureLengths.address, projector, projectorBias,

@@ -26,6 +26,7 @@ CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 ENCODER_FUSED_GLU = 0x1
 ENCODER_FUSED_NORMS = 0x2
+ENCODER_UNCHAINED_NORMS = 0x4
 ENCODER_CHANNELS = 1024
 ENCODER_INTERMEDIATE = 4096
 # The fifteen dispatches of one encoder layer, in launch order
@@ -251,6 +252,12 @@ class LayerNormDesc(ctypes.Structure):
         ("output_bytes", ctypes.c_uint64),
         ("has_epsilon", ctypes.c_int32),
         ("epsilon", ctypes.c_float),
+        ("next_gamma", ctypes.c_void_p),
+        ("next_gamma_bytes", ctypes.c_uint64),
+        ("next_beta", ctypes.c_void_p),
+        ("next_beta_bytes", ctypes.c_uint64),
+        ("next_output", ctypes.c_void_p),
+        ("next_output_bytes", ctypes.c_uint64),
     ]
 
 
@@ -949,12 +956,15 @@ def attention_variant_count(precision: str) -> int:
 
 
 def layernorm_desc(*, input, gamma, beta, output, rows: int, channels: int, epsilon: float | None = None,
-                   precision: str | None = None, label: str = "layernorm") -> LayerNormDesc:
+                   precision: str | None = None, label: str = "layernorm", next_gamma=None, next_beta=None,
+                   next_output=None) -> LayerNormDesc:
+    """A pk_layernorm_desc; with next_gamma / next_beta / next_output the
+    launch also writes the LayerNorm of its output (a chained LayerNorm)."""
     if precision is None:
         precision = "f16" if input.dtype == np.float16 else "f32"
     return LayerNormDesc(ctypes.sizeof(LayerNormDesc), label.encode(), PRECISION[precision], rows, channels,
                          *_slice(input), *_slice(gamma), *_slice(beta), *_slice(output), int(epsilon is not None),
-                         float(epsilon or 0.0))
+                         float(epsilon or 0.0), *_slice(next_gamma), *_slice(next_beta), *_slice(next_output))
 
 
 class LayerNormOp:
@@ -1096,7 +1106,7 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
 
 
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = False,
-                 fused_norms: bool = False, subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
+                 fused_norms: bool = False, unchained_norms: bool = False, subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
                  projector=None, projector_bias=None, projected_output=None, projected_channels: int = 0,
                  label: str = "encoder") -> EncoderDesc:
     """An EncoderDesc over `layers` (dicts as encoder_layer takes), with the
@@ -1105,7 +1115,8 @@ def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frame
     keeps what it points to alive."""
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
-    flags = (ENCODER_FUSED_GLU if fused_glu else 0) | (ENCODER_FUSED_NORMS if fused_norms else 0)
+    flags = ((ENCODER_FUSED_GLU if fused_glu else 0) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
+             (ENCODER_UNCHAINED_NORMS if unchained_norms else 0))
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
                        PRECISION["f16"], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),

@@ -199,6 +199,22 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
                RangeError, "encoder.layers.0.norm_feed_forward1 output needs 6160384 bytes; arena slice has 1024");
     throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => { d.beta = tensor(host.channelTensorRecords(512)); })),
                Error, "encoder.layers.0.norm_feed_forward1 beta must be float32 channel logical/storage [1024], 4096 bytes");
+    // a chained LayerNorm (no reference counterpart): its output may be the input, never the output
+    norm.validateDescriptor(lnDescriptor((d) => {
+      d.next = { gamma: tensor(affine), beta: tensor(affine), output: d.input };
+    }));
+    throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => {
+      d.next = { gamma: tensor(affine), beta: tensor(affine), output: arena.slice("z", 64 * 1024 * 1024 + 2048, 3008 * 1024 * 2) };
+    })), Error, "next output must not overlap the output");
+    const wide = host.channelTensorRecords(4096);
+    throwsLike(() => norm.validateDescriptor(lnDescriptor((d) => {
+      d.channels = 4096;
+      d.input = arena.slice("x", 0, 3008 * 4096 * 2);
+      d.output = arena.slice("y", 64 * 1024 * 1024, 3008 * 4096 * 2);
+      d.gamma = tensor(wide);
+      d.beta = tensor(wide);
+      d.next = { gamma: tensor(wide), beta: tensor(wide), output: d.input };
+    })), RangeError, "chained LayerNorm needs rows of at most 4096 bytes");
     return host.FusedSubsamplingConv0Depthwise2Kernel.create({}, arena, 64);
   }).then((fused) => {
     // subsampling-kernel-shapes.test.ts:27-50 and createDispatch (subsampling.ts:334-387)

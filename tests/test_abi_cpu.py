@@ -397,6 +397,36 @@ def test_layernorm_contract_messages(abi):
         _validate_ln(abi, **kw)
 
 
+def test_chained_layernorm_contract(abi):
+    """A chained LayerNorm (no reference counterpart): rows of at most 4 KB,
+    next gamma / beta of C f32 channels, next output capacity, and the next
+    output neither overlapping the output nor partly overlapping the input
+    (the input itself is allowed)."""
+    def chained(**over):
+        kw = _ln_fakes(**{k: over.pop(k) for k in ("rows", "channels", "elem") if k in over})
+        c = kw["channels"]
+        kw.update(next_gamma=_Fake(0x20200000, c * 4), next_beta=_Fake(0x20300000, c * 4),
+                  next_output=_Fake(0x40000000, kw["output"].nbytes, kw["output"].dtype))
+        kw.update(over)
+        return kw
+    name = "encoder.layers.0.norm_feed_forward1"
+    _validate_ln(abi, **chained())
+    kw = chained()
+    kw["next_output"] = kw["input"]
+    _validate_ln(abi, **kw)
+    _validate_ln(abi, **chained(channels=1024, elem=4))
+    with pytest.raises(abi.PaletteRangeError, match=f"{name} chained LayerNorm needs rows of at most 4096 bytes"):
+        _validate_ln(abi, **chained(channels=2048, elem=4))
+    with pytest.raises(abi.PaletteRangeError, match=f"{name} next output needs 6160384 bytes; arena slice has 64"):
+        _validate_ln(abi, **chained(next_output=_Fake(0x40000000, 64)))
+    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} next gamma and beta must be float32 [1024], 4096")):
+        _validate_ln(abi, **chained(next_beta=_Fake(0x20300000, 2048)))
+    kw = chained()
+    for bad in (kw["output"].ptr + 2048, kw["input"].ptr + 2048):
+        with pytest.raises(abi.PaletteError, match="next output must not overlap the output"):
+            _validate_ln(abi, **chained(next_output=_Fake(bad, kw["output"].nbytes)))
+
+
 # ---------------------------------------------------------------- subsampling
 
 

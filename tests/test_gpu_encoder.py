@@ -50,7 +50,7 @@ class Stack:
     """An EncoderOp over uploaded layers with its input, output and lengths
     (and the front end and projector when the stack has them)."""
 
-    def __init__(self, abi, ctx, scope, stack, *, fused_glu=False, fused_norms=False):
+    def __init__(self, abi, ctx, scope, stack, *, fused_glu=False, fused_norms=False, unchained_norms=False):
         self.ctx = ctx
         self.valid = scope.put(stack.valid)
         self.output = scope.put(np.full_like(stack.x, 77))
@@ -73,7 +73,8 @@ class Stack:
                          projected_output=self.projected)
         self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
                                 input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
-                                fused_glu=fused_glu, fused_norms=fused_norms, **extra)
+                                fused_glu=fused_glu, fused_norms=fused_norms, unchained_norms=unchained_norms,
+                                **extra)
 
     def run(self, active=0, graph=False):
         self.op.enqueue(active, graph=graph)
@@ -239,6 +240,25 @@ def test_encoder_fused_norms_match_separate_norms(abi, ctx, scope, oracle, workl
     assert norm <= 1e-2, (norm, worst)
     assert fused_err <= 1e-2 and separate_err <= 1e-2
     assert fused_err <= separate_err + 2e-3, (fused_err, separate_err)
+
+
+def test_encoder_chained_norms_match_unchained(abi, ctx, scope, workloads):
+    """Each layer's last LayerNorm also writing the next layer's first one
+    in the same launch (the default) gives bit-identical outputs to one
+    launch per LayerNorm (PK_ENCODER_UNCHAINED_NORMS), for all windows and
+    for an active prefix."""
+    stack = workloads.encoder_stack(seed=17, windows=3, frames=188, layers=3)
+    outs = []
+    for unchained in (False, True):
+        enc = Stack(abi, ctx, scope, stack, unchained_norms=unchained)
+        try:
+            assert enc.op.info()[0] == 15 * 3  # dispatch slots, launching or not
+            outs.append((enc.run(), enc.run(active=2)))
+        finally:
+            enc.release()
+    for got, want in zip(outs[0], outs[1]):
+        assert np.isfinite(got).all()
+        np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
 def test_encoder_rejects_bad_active_batch(abi, ctx, scope, workloads):
