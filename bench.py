@@ -162,16 +162,56 @@ def build_single_gemm(abi, ctx, keep):
         config, case
 
 
+class RotatingOp:
+    """Launches a list of same-shape GEMM ops in turn, one per enqueue, so
+    consecutive steps read different weights."""
+
+    def __init__(self, ops):
+        self.ops = ops
+        self.next = 0
+
+    def enqueue(self, *args):
+        op = self.ops[self.next]
+        self.next = (self.next + 1) % len(self.ops)
+        op.enqueue(*args)
+
+    def plan(self, *args):
+        return self.ops[0].plan(*args)
+
+    def set_variant(self, variant):
+        for op in self.ops:
+            op.set_variant(variant)
+
+    def release(self):
+        for op in self.ops:
+            op.release()
+
+
+SMALL_M_WEIGHTS = 128  # distinct 2.6 MB weights: 336 MB, past the 256 MB MALL
+
+
 def build_small_m(abi, ctx, keep, rows):
+    """The small-M GEMM over SMALL_M_WEIGHTS distinct weights launched in
+    turn: no step finds its weight in the memory-side cache, as a model's
+    weights streamed once per token would not."""
     import parakeet_wgsl_amd.workloads as wl
     case = wl.gemm_case(0, rows, 1024, 4096, 5)
+    rng = np.random.default_rng(1)
+    a = keep(ctx.array(case.a))
     out = keep(ctx.empty((rows, 4096), np.float16))
-    op = abi.GemmOp(ctx, a=keep(ctx.array(case.a)), packed=keep(ctx.array(case.weight.packed)),
-                    palette=keep(ctx.array(case.weight.palette)), output=out, bits=5, rows=rows,
-                    inner=1024, columns=4096, label=f"small-m-{rows}")
+    ops = []
+    for i in range(SMALL_M_WEIGHTS):
+        packed = case.weight.packed if i == 0 else wl.random_packed_words(rng, 5, 1024, 4096)
+        ops.append(abi.GemmOp(ctx, a=a, packed=keep(ctx.array(packed)),
+                              palette=keep(ctx.array(case.weight.palette)), output=out, bits=5, rows=rows,
+                              inner=1024, columns=4096, label=f"small-m-{rows}-{i}"))
     config = {"workload": "small-m-palette-gemm-fp16", "rows": rows, "inner": 1024, "columns": 4096,
-              "palette_bits": 5}
-    return [Kernel(f"small-m-{rows}", op, case.flops, case.algorithmic_bytes(), "f16", (rows, 1024, 4096))], config, case
+              "palette_bits": 5, "distinct_weights": SMALL_M_WEIGHTS,
+              "rotation": f"each step launches the next of {SMALL_M_WEIGHTS} distinct weights "
+                          f"({SMALL_M_WEIGHTS * case.weight.packed.nbytes / 1e6:.0f} MB of packed codes in turn; "
+                          "activations and output shared)"}
+    return [Kernel(f"small-m-{rows}", RotatingOp(ops), case.flops, case.algorithmic_bytes(), "f16",
+                   (rows, 1024, 4096))], config, case
 
 
 def build_conv_module(abi, ctx, keep, fused_glu=False):
@@ -1092,7 +1132,7 @@ def main():
         kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
     if args.variant >= 0:
         for k in kernels:
-            if isinstance(k.op, abi.GemmOp):
+            if isinstance(k.op, (abi.GemmOp, RotatingOp)):
                 k.op.set_variant(args.variant)
 
     step = measure_kernel_step(ctx, kernels, args.steps, args.warmup, args.graph)

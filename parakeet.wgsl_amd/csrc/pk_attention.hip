@@ -298,8 +298,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
 // then. The workgroup keeps the blocks in a ring of NQ + 1 and stages one
 // new block per tile; each wavefront carries its second-half product over
 // as the next tile's first half (16 instead of 24 score MFMAs per tile) and
-// writes only that half of its diagonal window. The next tile's rows are on
-// their way into registers while the current one is computed, and the
+// writes only that half of its diagonal window. The next two tiles' rows are
+// on their way into registers while the current one is computed, and the
 // output rescale is skipped when no query's running maximum moved.
 template <int NQ, bool ROW_MAJOR>
 __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnArgs args) {
@@ -313,6 +313,7 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
   __shared__ __attribute__((aligned(16))) _Float16 vts[kHead * kVtStride];
   __shared__ __attribute__((aligned(16))) _Float16 rs[RING * kTile * KSTRIDE];
   __shared__ __attribute__((aligned(16))) float windows[NQ * 64 * kTile];
+  __shared__ __attribute__((aligned(16))) float uv[2 * kHead];  // u, then v, of this head
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -339,21 +340,6 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
   }
 
   const int qw = q0 + kTile * wave;  // this wavefront's first query
-  half8 qu[8], qv[8];
-  {
-    const _Float16* qrow = qkv + (uint64_t)min(qw + j, T - 1) * kQkvRow;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int d0 = 16 * s + 8 * hh;
-      const half8 x = load8(qrow + d0);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        qu[s][t] = (_Float16)((float)x[t] + args.bias_u[head * kHead + d0 + t]);
-        qv[s][t] = (_Float16)((float)x[t] + args.bias_v[head * kHead + d0 + t]);
-      }
-    }
-  }
-
   const int pmax = (int)args.position_rows - 1;
   const int pbase = T - q0 - kTile * NQ;  // first row of position block 0
   auto position_chunk = [&](int block, int c) {
@@ -366,7 +352,10 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
     *reinterpret_cast<half8*>(rs + ((block % RING) * kTile + row) * KSTRIDE + part * 8) = x;
   };
   // Per key tile kt each thread moves PER chunks of the K rows, of the V
-  // rows and of position block kt + NQ; chunk c is row c / 16, part c % 16.
+  // rows and of position block kt + NQ. K and position chunk c is row c / 16,
+  // part c % 16; V chunk c is row c % 32, part c / 32, so that the 64 lanes
+  // of one transposed 2-byte store write 32 banks, lane pairs sharing a
+  // dword (part-major lanes put a whole wavefront on four banks).
   struct Staged {
     half8 k[PER], v[PER], r[PER];
   };
@@ -377,7 +366,7 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
       const int c = tid + i * THREADS;
       const _Float16* row = qkv + (uint64_t)min(k0 + c / (kHead / 8), T - 1) * kQkvRow + (c % (kHead / 8)) * 8;
       st.k[i] = load8(row + kHidden);
-      st.v[i] = load8(row + 2 * kHidden);
+      st.v[i] = load8(qkv + (uint64_t)min(k0 + c % kTile, T - 1) * kQkvRow + 2 * kHidden + (c / kTile) * 8);
       st.r[i] = position_chunk(kt + NQ, c);
     }
   };
@@ -387,15 +376,69 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
       const int c = tid + i * THREADS;
       const int kk = c / (kHead / 8), part = c % (kHead / 8);
       *reinterpret_cast<half8*>(ks + kk * KSTRIDE + part * 8) = st.k[i];
-      const int slot = (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+      const int vk = c % kTile, vpart = c / kTile;
+      const int slot = (vk & ~12) | ((vk & 4) << 1) | ((vk & 8) >> 1);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) vts[(part * 8 + t) * kVtStride + slot] = st.v[i][t];
+      for (int t = 0; t < 8; ++t) vts[(vpart * 8 + t) * kVtStride + slot] = st.v[i][t];
       store_position(kt + NQ, c, st.r[i]);
     }
   };
 
-  // Position blocks 0 .. NQ-1 for the first tile (block NQ comes with it).
-  for (int c = tid; c < NQ * BCH; c += THREADS) store_position(c / BCH, c % BCH, position_chunk(c / BCH, c % BCH));
+  // Prologue loads, issued together so that one memory latency covers them:
+  // position blocks 0 .. NQ-1 (block NQ comes with the first tile), this
+  // wavefront's query rows with u and v, then the first two tiles' rows
+  // (tile kt's registers are set kt % 2, refilled with tile kt + 2 as soon
+  // as they are staged; fetches are unconditional, past the last tile they
+  // re-read it and are never staged, so each wait counts only older loads).
+  const int tiles = (live + kTile - 1) / kTile;
+  constexpr int PRE = NQ * BCH / THREADS;
+  static_assert((NQ * BCH) % THREADS == 0, "the prologue's position blocks split evenly");
+  half8 pre[PRE];
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int c = tid + i * THREADS;
+    pre[i] = position_chunk(c / BCH, c % BCH);
+  }
+  half8 qx[8];
+  const _Float16* qrow = qkv + (uint64_t)min(qw + j, T - 1) * kQkvRow;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) qx[s] = load8(qrow + 16 * s + 8 * hh);
+  // u and v of the head: one value per thread into LDS (every wavefront
+  // needs all 256; loading them per lane cost more than the query rows).
+  constexpr int UVN = 2 * kHead / THREADS;
+  static_assert((2 * kHead) % THREADS == 0, "u and v split evenly over the workgroup");
+  float uv_value[UVN];
+#pragma unroll
+  for (int i = 0; i < UVN; ++i) {
+    const int c = tid + i * THREADS;
+    uv_value[i] = c < kHead ? args.bias_u[head * kHead + c] : args.bias_v[head * kHead + c - kHead];
+  }
+  Staged staged[2];
+  fetch(0, staged[0]);
+  fetch(min(1, tiles - 1), staged[1]);
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int c = tid + i * THREADS;
+    store_position(c / BCH, c % BCH, pre[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < UVN; ++i) uv[tid + i * THREADS] = uv_value[i];
+  __syncthreads();
+  half8 qu[8], qv[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int d0 = 16 * s + 8 * hh;
+    const float4 u0 = *reinterpret_cast<const float4*>(uv + d0), u1 = *reinterpret_cast<const float4*>(uv + d0 + 4);
+    const float4 v0 = *reinterpret_cast<const float4*>(uv + kHead + d0);
+    const float4 v1 = *reinterpret_cast<const float4*>(uv + kHead + d0 + 4);
+    const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      qu[s][t] = (_Float16)((float)qx[s][t] + uu[t]);
+      qv[s][t] = (_Float16)((float)qx[s][t] + vv[t]);
+    }
+  }
 
   float* window = windows + wave * 64 * kTile;
   const float scale = 0.08838834764831845f;
@@ -406,15 +449,13 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
 
-  const int tiles = (live + kTile - 1) / kTile;
-  Staged staged;
-  fetch(0, staged);
-  for (int kt = 0; kt < tiles; ++kt) {
+  auto tile = [&](auto slot, int kt) {
+    constexpr int SL = decltype(slot)::value;
     const int k0 = kt * kTile;
     __syncthreads();  // every wavefront is done with the previous tile
-    stage(kt, staged);
+    stage(kt, staged[SL]);
     __syncthreads();
-    if (kt + 1 < tiles) fetch(kt + 1, staged);
+    fetch(min(kt + 2, tiles - 1), staged[SL]);
 
     // S^T = K (Q+u)^T; second window half from block kt + NQ - wave.
     const _Float16* r_new = rs + (((kt + NQ - wave) % RING) * kTile + j) * KSTRIDE;
@@ -488,6 +529,10 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb8[s], o[db], 0, 0, 0);
       }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  for (int kt = 0; kt < tiles; kt += 2) {
+    tile(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < tiles) tile(std::integral_constant<int, 1>{}, kt + 1);
   }
 
   const int q = qw + j;
@@ -590,16 +635,20 @@ struct AttnVariant {
 #define PK_ATTN_SHARED_VARIANT(NQ)                                                                         \
   AttnVariant {                                                                                            \
     "pk_rel_attention_f16_q" #NQ "x32_shared", NQ, NQ * kTile,                                             \
-        (uint32_t)((kTile + (NQ + 1) * kTile) * (kHead + 8) * 2 + kHead * kVtStride * 2 + NQ * 64 * kTile * 4), \
+        (uint32_t)((kTile + (NQ + 1) * kTile) * (kHead + 8) * 2 + kHead * kVtStride * 2 + NQ * 64 * kTile * 4 + \
+                   2 * kHead * 4),                                                                         \
         rel_attention_f16_shared_kernel<NQ, false>, rel_attention_f16_shared_kernel<NQ, true>              \
   }
 
-// Index 0: up to 256 frames while one round of its workgroups fills the
-// device (key tiles split over the workgroup: 13 us at 4 x 188, 12.6 us at
-// 1 x 188); index 1 up to a round and a half (21 us at 8 x 188 against 29 us
-// for index 0); index 4 beyond that and for longer windows (K, V and one
-// position block per tile shared by 128 queries: 28.5 us at 16 x 188
-// against 41.8 us for index 0, 77 us at 4 x 750 against 96 us).
+// Planned (32-query tiles = windows x 8 heads x ceil(T / 32), measured at
+// T = 188 on one MI355X): index 0 while one round of its workgroups fills
+// the device (4 windows: 13.5 us against 18.1 us for index 3); index 3 up to
+// 384 tiles (8 windows: 18.7 us against 21.1 us for index 1 and 20.3 us for
+// index 4); index 4 up to 1152 (12 / 16 / 24 windows: 20.9 / 21.7 / 36.4
+// us); index 3 beyond (40 windows: 45.1 us against 55.8 us, where index 4's
+// half-empty second query block per window and head costs more than its
+// shared staging saves); index 4 for windows longer than 256 frames (4 x 750:
+// 55.2 us against 63.2 us for index 3 and 95.8 us for index 0).
 const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
                                     PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
 const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
@@ -610,8 +659,8 @@ const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_
 int attention_default_variant(bool f16, uint32_t frames, uint32_t batch) {
   if (!f16) return 0;
   if (frames > 256u) return 4;
-  const uint64_t workgroups = (uint64_t)batch * kHeads * ((frames + kTile - 1) / kTile);
-  return workgroups <= 256u ? 0 : workgroups <= 384u ? 1 : 4;
+  const uint64_t tiles = (uint64_t)batch * kHeads * ((frames + kTile - 1) / kTile);
+  return tiles <= 256u ? 0 : tiles <= 384u ? 3 : tiles <= 1152u ? 4 : 3;
 }
 
 int attention_variant_count(bool f16) {
