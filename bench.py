@@ -87,6 +87,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
     p.add_argument("--no-ff-block", action="store_true", help="encoder workloads: skip the FF block's extra line")
+    p.add_argument("--separate-glu", action="store_true",
+                   help="encoder workloads: the convolution forms the GLU from PW1's values and gates, as the "
+                        "reference does (PK_ENCODER_SEPARATE_GLU; default: PW1's epilogue writes the GLU)")
     p.add_argument("--unchained-norms", action="store_true",
                    help="encoder workloads: launch every LayerNorm on its own (default: each layer's last "
                         "LayerNorm also writes the next layer's first)")
@@ -406,7 +409,7 @@ def gemm_cost(rows, inner, columns, bits=5, groups=1, residual=False, bias=False
     return 2 * rows * inner * columns, nbytes + (rows * columns * 2 if residual else 0) + (4 * columns if bias else 0)
 
 
-def encoder_dispatch_costs(abi, wl, stack):
+def encoder_dispatch_costs(abi, wl, stack, fused_glu=False):
     """(flops, algorithmic bytes) per dispatch kind: the front end's six, one
     layer's fifteen (over all windows) and the projector. LayerNorm reads and
     writes the rows once; the attention and the convolutions count what
@@ -421,9 +424,12 @@ def encoder_dispatch_costs(abi, wl, stack):
     live = np.minimum(stack.valid.astype(np.int64), frames)
     attention = (int((live * live).sum()) * 8 * 128 * 2 * 3,
                  rows * 3072 * 2 + (2 * frames - 1) * 1024 * 2 + 2 * 4096 + 4 * batch + act)
-    conv = (0, rows * 2048 * 2 + act + 9 * 1024 * 2 + 8 * 1024 + 4 * batch)
+    conv = (0, rows * (1024 if fused_glu else 2048) * 2 + act + 9 * 1024 * 2 + 8 * 1024 + 4 * batch)
+    pointwise1 = gemm("pointwise1")
+    if fused_glu:  # the GLU output is half as wide
+        pointwise1 = (pointwise1[0], pointwise1[1] - rows * 1024 * 2)
     layer = [ln, gemm("ff1_linear1"), gemm("ff1_linear2", True), ln, gemm("qkv"), attention,
-             gemm("o_proj", True), ln, gemm("pointwise1"), conv, gemm("pointwise2", True), ln,
+             gemm("o_proj", True), ln, pointwise1, conv, gemm("pointwise2", True), ln,
              gemm("ff2_linear1"), gemm("ff2_linear2", True), ln]
     assert len(layer) == len(abi.ENCODER_DISPATCHES)
     front = []
@@ -553,7 +559,7 @@ def run_encoder(args, abi, ctx, decoder=False):
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
                         projected_output=projected, fused_norms=args.fused_norms,
-                        unchained_norms=args.unchained_norms, label="encoder")
+                        unchained_norms=args.unchained_norms, fused_glu=not args.separate_glu, label="encoder")
     launches, device_bytes = enc.info()
     fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
     # the LN ff1 of layers after the first runs in the LN out launch before it
@@ -611,7 +617,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     durations = durations.mean(axis=0)  # ms per launch of the pass
     decoder_ms = float(np.mean([a.elapsed_ms(b) for a, b in tdt_marks.values()])) if tdt else None
     run = ActivePrefix(stack, active)
-    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, run)
+    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, run, not args.separate_glu)
     nf, per = len(front_costs), len(abi.ENCODER_DISPATCHES)
     names = list(FRONT_DISPATCHES) + list(abi.ENCODER_DISPATCHES) + ["projector"] * len(projector_costs)
     costs = front_costs + layer_costs + projector_costs
@@ -720,6 +726,7 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
                                  if args.fused_norms else "separate launches" if not chained else
                                  "separate launches; each layer's last LayerNorm also writes the next layer's first",
+                   "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu else "in PW1's epilogue",
                    "graph_replay": True,
                    "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,

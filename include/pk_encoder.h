@@ -39,9 +39,18 @@ extern "C" {
 #define PK_ENCODER_INTERMEDIATE 4096
 
 /* pk_encoder_desc.flags */
-#define PK_ENCODER_FUSED_GLU 0x1u  /* PW1 carries the GLU epilogue (PK_GEMM_GLU) */
+/* PW1 carries the GLU epilogue (PK_GEMM_GLU) and the convolution reads the
+   [rows, 1024] GLU (PK_CONV_INPUT_GLU). This is the default; the flag is
+   still accepted. */
+#define PK_ENCODER_FUSED_GLU 0x1u
+/* Keep the reference's order instead: PW1 writes values and gates
+   ([rows, 2048]) and the convolution forms the GLU in f32. The default
+   rounds the GLU to f16 once more and was measured 80 us faster per
+   16-window pass (PW1 and the convolution tail both move less). Not with
+   PK_ENCODER_FUSED_GLU. */
+#define PK_ENCODER_SEPARATE_GLU 0x8u
 /* Run the LayerNorms before FF1 W1, QKV, PW1 and FF2 W1 inside the GEMMs
-   that read them (PK_GEMM_ROW_NORM; not for PW1 with PK_ENCODER_FUSED_GLU):
+   that read them (PK_GEMM_ROW_NORM; PW1 only with PK_ENCODER_SEPARATE_GLU):
    96 fewer launches per 24-layer pass, but each of those GEMMs does the
    row statistics of every column tile again; on 16 windows the pass is
    about 5% slower than with the separate LayerNorm launches, which stay

@@ -1230,9 +1230,9 @@ static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   d->precision = PK_PRECISION_F16;
   napi_value layers, item, v;
   uint32_t n = 0;
-  bool glu = false;
-  if (prop(env, o, "fusedGlu", &v) && napi_get_value_bool(env, v, &glu) == napi_ok && glu)
-    d->flags |= PK_ENCODER_FUSED_GLU;
+  bool glu = true;
+  if (prop(env, o, "fusedGlu", &v) && napi_get_value_bool(env, v, &glu) == napi_ok && !glu)
+    d->flags |= PK_ENCODER_SEPARATE_GLU;
   bool fused_norms = false, unchained_norms = false;
   if (prop(env, o, "fusedNorms", &v) && napi_get_value_bool(env, v, &fused_norms) == napi_ok && fused_norms)
     d->flags |= PK_ENCODER_FUSED_NORMS;

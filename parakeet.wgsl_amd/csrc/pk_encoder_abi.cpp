@@ -68,7 +68,7 @@ struct pk_encoder {
   pk_abi::CtxRef ctx;
   std::string label;
   uint32_t batch = 0, frames = 0, layers = 0, rows = 0;
-  bool fused_glu = false;
+  bool fused_glu = true;
   bool fused_norms = false;
   bool chained_norms = true;  // norm_out also writes the next layer's norm_feed_forward1
   const uint32_t* valid_lengths = nullptr;
@@ -559,7 +559,7 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->frames = d->frames;
   e->layers = d->layers;
   e->rows = d->batch_size * d->frames;
-  e->fused_glu = (d->flags & PK_ENCODER_FUSED_GLU) != 0;
+  e->fused_glu = (d->flags & PK_ENCODER_SEPARATE_GLU) == 0;
   e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
   e->chained_norms = (d->flags & (PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS)) == 0;
   e->valid_lengths = d->valid_lengths;
@@ -583,8 +583,11 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
   if (d->struct_size != sizeof(pk_encoder_desc))
     return fail(PK_INVALID_ARGUMENT, "pk_encoder_desc.struct_size mismatch");
   const char* label = d->label ? d->label : "encoder";
-  if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS))
+  if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_SEPARATE_GLU | PK_ENCODER_FUSED_NORMS |
+                   PK_ENCODER_UNCHAINED_NORMS))
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
+  if ((d->flags & PK_ENCODER_FUSED_GLU) && (d->flags & PK_ENCODER_SEPARATE_GLU))
+    return fail(PK_INVALID_ARGUMENT, "%s: PK_ENCODER_FUSED_GLU and PK_ENCODER_SEPARATE_GLU exclude each other", label);
   if (d->precision != PK_PRECISION_F16)
     return fail(PK_INVALID_ARGUMENT, "%s: the encoder stack runs in f16", label);
   if (d->batch_size == 0 || d->frames == 0 || d->layers == 0 || d->layers > kMaxLayers)

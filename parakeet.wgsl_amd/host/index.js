@@ -1562,7 +1562,8 @@ class ParakeetEncoderGraph {
   /**
    * create(device, model, options?): options.batchSize (windows, default
    * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
-   * epilogue), options.fusedNorms (the four LayerNorms that feed a GEMM
+   * epilogue; default true, false keeps the GLU in the convolution),
+   * options.fusedNorms (the four LayerNorms that feed a GEMM
    * run inside it) and options.unchainedNorms (one launch per LayerNorm;
    * by default a layer's last LayerNorm also writes the next layer's
    * first), none with a reference counterpart, options.featureFrames
@@ -1602,7 +1603,7 @@ class ParakeetEncoderGraph {
     let handle;
     try {
       handle = native().encoderCreate(device.context, {
-        label: o.label || "encoder", fusedGlu: o.fusedGlu === true, fusedNorms: o.fusedNorms === true,
+        label: o.label || "encoder", fusedGlu: o.fusedGlu !== false, fusedNorms: o.fusedNorms === true,
         unchainedNorms: o.unchainedNorms === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,

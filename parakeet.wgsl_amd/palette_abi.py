@@ -26,6 +26,7 @@ CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 ENCODER_FUSED_GLU = 0x1
 ENCODER_FUSED_NORMS = 0x2
+ENCODER_SEPARATE_GLU = 0x8
 ENCODER_UNCHAINED_NORMS = 0x4
 ENCODER_CHANNELS = 1024
 ENCODER_INTERMEDIATE = 4096
@@ -1105,7 +1106,7 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
     return front
 
 
-def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = False,
+def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = True,
                  fused_norms: bool = False, unchained_norms: bool = False, subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
                  projector=None, projector_bias=None, projected_output=None, projected_channels: int = 0,
                  label: str = "encoder") -> EncoderDesc:
@@ -1115,7 +1116,7 @@ def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frame
     keeps what it points to alive."""
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
-    flags = ((ENCODER_FUSED_GLU if fused_glu else 0) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
+    flags = ((0 if fused_glu else ENCODER_SEPARATE_GLU) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
              (ENCODER_UNCHAINED_NORMS if unchained_norms else 0))
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
                        PRECISION["f16"], batch_size, frames, len(layers),

@@ -722,9 +722,15 @@ def test_encoder_validate_stack_fields(abi):
     with pytest.raises(abi.PaletteError, match="runs in f16"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
-    desc.flags = 0x8
+    desc.flags = 0x10
     with pytest.raises(abi.PaletteError, match="unknown flags"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+    desc = abi.encoder_desc(**_encoder_fakes())
+    desc.flags = abi.ENCODER_FUSED_GLU | abi.ENCODER_SEPARATE_GLU
+    with pytest.raises(abi.PaletteError, match="exclude each other"):
+        abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+    desc.flags = abi.ENCODER_FUSED_GLU  # the default, still accepted
+    abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
 
 
 def test_encoder_validate_front_end_and_projector(abi):
