@@ -728,6 +728,7 @@ const F16Variant kVariants[] = {
     PK_F16K_VARIANT(4, 1, 6, 2, true, 2, ""),  // 192 x 256, no K split
     PK_F16K_VARIANT(4, 1, 4, 2, true, 2, ""),  // 128 x 256, no K split
     PK_F16K_VARIANT(4, 1, 3, 2, true, 5, ""),  // 96 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 5, 2, true, 2, ""),  // 160 x 256, no K split
 };
 
 }  // namespace
