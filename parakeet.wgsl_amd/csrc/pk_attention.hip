@@ -175,13 +175,21 @@ __global__ __launch_bounds__(64 * KSPLIT) void rel_attention_f16_kernel(AttnArgs
     // compiler from moving the reads above the writes.
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // Scores of keys k0 + i, i = 8 (r/4) + 4 hh + r%4, for query q0 + j.
+    // All sixteen reads go out before the first use: left to itself the
+    // compiler waits on each read in turn (a full LDS round trip apiece).
+    float rel[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r / 4) + 4 * hh + (r % 4);
+      rel[r] = window[(kTile - 1 - j + i) * kTile + j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float sc[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = 8 * (r / 4) + 4 * hh + (r % 4);
-      const float rel = window[(kTile - 1 - j + i) * kTile + j];
-      sc[r] = k0 + i < live ? (ac[r] + rel) * scale : -INFINITY;
+      sc[r] = k0 + i < live ? (ac[r] + rel[r]) * scale : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -487,14 +495,28 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
     for (int r = 0; r < 16; ++r)
       window[(new_half * kTile + 8 * (r / 4) + 4 * hh + (r % 4)) * kTile + j] = w1[r];
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // All sixteen reads go out before the first use (see the kernel above),
+    // and with them the V^T operands of the PV product, which do not wait
+    // for the softmax.
+    float rel[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = kTile - 1 - j + 8 * (r / 4) + 4 * hh + (r % 4);
+      rel[r] = window[((((c >> 5) + kt) & 1) * kTile + (c & 31)) * kTile + j];
+    }
+    half8 va[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        va[db][s] = *reinterpret_cast<const half8*>(vts + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
+    __builtin_amdgcn_sched_barrier(0);
     float sc[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = 8 * (r / 4) + 4 * hh + (r % 4);
-      const int c = kTile - 1 - j + i;
-      const float rel = window[((((c >> 5) + kt) & 1) * kTile + (c & 31)) * kTile + j];
-      sc[r] = k0 + i < live ? (ac[r] + rel) * scale : -INFINITY;
+      sc[r] = k0 + i < live ? (ac[r] + rel[r]) * scale : -INFINITY;
       mx = fmaxf(mx, sc[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -524,10 +546,7 @@ __global__ __launch_bounds__(64 * NQ) void rel_attention_f16_shared_kernel(AttnA
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const half8 va = *reinterpret_cast<const half8*>(vts + (32 * db + j) * kVtStride + 16 * s + 8 * hh);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb8[s], o[db], 0, 0, 0);
-      }
+      for (int s = 0; s < 2; ++s) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][s], pb8[s], o[db], 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   };
   for (int kt = 0; kt < tiles; kt += 2) {
@@ -642,13 +661,14 @@ struct AttnVariant {
 
 // Planned (32-query tiles = windows x 8 heads x ceil(T / 32), measured at
 // T = 188 on one MI355X): index 0 while one round of its workgroups fills
-// the device (4 windows: 13.5 us against 18.1 us for index 3); index 3 up to
-// 384 tiles (8 windows: 18.7 us against 21.1 us for index 1 and 20.3 us for
-// index 4); index 4 up to 1152 (12 / 16 / 24 windows: 20.9 / 21.7 / 36.4
-// us); index 3 beyond (40 windows: 45.1 us against 55.8 us, where index 4's
-// half-empty second query block per window and head costs more than its
-// shared staging saves); index 4 for windows longer than 256 frames (4 x 750:
-// 55.2 us against 63.2 us for index 3 and 95.8 us for index 0).
+// the device (4 windows: 12.3 us against 15.9 us for index 3); index 3 up to
+// 384 tiles (8 windows: 16.0 us against 18.3 us for index 4 and 19.9 us for
+// index 1); index 4 below 1152 (12 / 16 windows: 19.1 / 19.6 us); index 3
+// from 1152 (24 windows: 32.4 against 33.5 us; 40 windows: 39.5 against
+// 51.3 us, where index 4's half-empty second query block per window and
+// head costs more than its shared staging saves); index 4 for windows
+// longer than 256 frames (4 x 750: 46.2 us against 50.6 us for index 3 and
+// 86.9 us for index 0).
 const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
                                     PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
 const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
@@ -660,7 +680,7 @@ int attention_default_variant(bool f16, uint32_t frames, uint32_t batch) {
   if (!f16) return 0;
   if (frames > 256u) return 4;
   const uint64_t tiles = (uint64_t)batch * kHeads * ((frames + kTile - 1) / kTile);
-  return tiles <= 256u ? 0 : tiles <= 384u ? 3 : tiles <= 1152u ? 4 : 3;
+  return tiles <= 256u ? 0 : tiles <= 384u ? 3 : tiles < 1152u ? 4 : 3;
 }
 
 int attention_variant_count(bool f16) {
