@@ -87,6 +87,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-dense", action="store_true", help="skip the dense vendor GEMM reference")
     p.add_argument("--no-ff-block", action="store_true", help="encoder workloads: skip the FF block's extra line")
+    p.add_argument("--precision", choices=["f16", "f32"], default="f16",
+                   help="encoder workload: f32 runs the reference's fp32 profile (f32 activations, palettes, "
+                        "positions and depthwise weights)")
     p.add_argument("--separate-glu", action="store_true",
                    help="encoder workloads: the convolution forms the GLU from PW1's values and gates, as the "
                         "reference does (PK_ENCODER_SEPARATE_GLU; default: PW1's epilogue writes the GLU)")
@@ -403,31 +406,33 @@ FRONT_DISPATCHES = ("subsampling-fused-conv0-depthwise2", "subsampling-pointwise
                     "subsampling-pointwise6", "subsampling-pointwise6-mask", "subsampling-flatten-project")
 
 
-def gemm_cost(rows, inner, columns, bits=5, groups=1, residual=False, bias=False):
-    """2MKN and compulsory bytes: packed codes, LUT, A, output (+ residual, bias)."""
-    nbytes = inner * columns * bits // 8 + groups * (1 << bits) * 2 + rows * inner * 2 + rows * columns * 2
-    return 2 * rows * inner * columns, nbytes + (rows * columns * 2 if residual else 0) + (4 * columns if bias else 0)
+def gemm_cost(rows, inner, columns, bits=5, groups=1, residual=False, bias=False, elem=2):
+    """2MKN and compulsory bytes: packed codes, LUT, A, output (+ residual,
+    bias), activations and LUT of `elem` bytes."""
+    nbytes = inner * columns * bits // 8 + groups * (1 << bits) * elem + rows * inner * elem + rows * columns * elem
+    return 2 * rows * inner * columns, nbytes + (rows * columns * elem if residual else 0) + (4 * columns if bias else 0)
 
 
 def encoder_dispatch_costs(abi, wl, stack, fused_glu=False):
     """(flops, algorithmic bytes) per dispatch kind: the front end's six, one
     layer's fifteen (over all windows) and the projector. LayerNorm reads and
     writes the rows once; the attention and the convolutions count what
-    their launches must move."""
+    their launches must move. Element bytes follow the stack's precision."""
     rows, frames, batch = stack.x.shape[0], stack.frames, stack.batch
-    act = rows * 1024 * 2
+    e = stack.x.dtype.itemsize
+    act = rows * 1024 * e
     ln = (0, 2 * act + 2 * 4096)
 
     def gemm(name, residual=False):
         bits, k, n, groups = wl.ENCODER_MATRICES[name]
-        return gemm_cost(rows, k, n, bits, groups, residual)
+        return gemm_cost(rows, k, n, bits, groups, residual, elem=e)
     live = np.minimum(stack.valid.astype(np.int64), frames)
     attention = (int((live * live).sum()) * 8 * 128 * 2 * 3,
-                 rows * 3072 * 2 + (2 * frames - 1) * 1024 * 2 + 2 * 4096 + 4 * batch + act)
-    conv = (0, rows * (1024 if fused_glu else 2048) * 2 + act + 9 * 1024 * 2 + 8 * 1024 + 4 * batch)
+                 rows * 3072 * e + (2 * frames - 1) * 1024 * e + 2 * 4096 + 4 * batch + act)
+    conv = (0, rows * (1024 if fused_glu else 2048) * e + act + 9 * 1024 * e + 8 * 1024 + 4 * batch)
     pointwise1 = gemm("pointwise1")
     if fused_glu:  # the GLU output is half as wide
-        pointwise1 = (pointwise1[0], pointwise1[1] - rows * 1024 * 2)
+        pointwise1 = (pointwise1[0], pointwise1[1] - rows * 1024 * e)
     layer = [ln, gemm("ff1_linear1"), gemm("ff1_linear2", True), ln, gemm("qkv"), attention,
              gemm("o_proj", True), ln, pointwise1, conv, gemm("pointwise2", True), ln,
              gemm("ff2_linear1"), gemm("ff2_linear2", True), ln]
@@ -436,15 +441,16 @@ def encoder_dispatch_costs(abi, wl, stack, fused_glu=False):
     if stack.subsampling is not None:
         f = stack.feature_frames
         h1, h2 = wl.subsampled_length(f, 1), wl.subsampled_length(f, 2)
-        stage2, stage3 = batch * h2 * 32 * 256 * 2, batch * frames * 16 * 256 * 2
-        kernel = 9 * 256 * 2 + 1024
+        stage2, stage3 = batch * h2 * 32 * 256 * e, batch * frames * 16 * 256 * e
+        kernel = 9 * 256 * e + 1024
         front = [(2 * 9 * 256 * batch * (h1 * 64 + h2 * 32), batch * 128 * f * 4 + stage2 + 2 * kernel + 4 * batch),
-                 gemm_cost(batch * h2 * 32, 256, 256, bias=True),
+                 gemm_cost(batch * h2 * 32, 256, 256, bias=True, elem=e),
                  (2 * 9 * 256 * batch * frames * 16, stage2 + stage3 + kernel + 4 * batch),
-                 gemm_cost(batch * frames * 16, 256, 256, bias=True),
+                 gemm_cost(batch * frames * 16, 256, 256, bias=True, elem=e),
                  (0, stage3 + 4 * batch),
-                 gemm_cost(rows, 4096, 1024, bias=True)]
-    projector = [gemm_cost(rows, 1024, stack.projector_bias.size, bias=True)] if stack.projector is not None else []
+                 gemm_cost(rows, 4096, 1024, bias=True, elem=e)]
+    projector = [gemm_cost(rows, 1024, stack.projector_bias.size, bias=True, elem=e)] \
+        if stack.projector is not None else []
     return front, layer, projector
 
 
@@ -458,8 +464,8 @@ def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
     from oracle import pko
     main, x0, ratio, decode_s = encoder_cpu_leg(stack, all_threads(), budget_s, decoder)
     t0 = time.perf_counter()
-    pko.encoder_layer(x0, stack.layers[0], stack.valid[:1], batch=1, frames=stack.frames, gemm_mode="f16-chain",
-                      threads=1)
+    pko.encoder_layer(x0, stack.layers[0], stack.valid[:1], batch=1, frames=stack.frames, threads=1,
+                      dtype=stack.x.dtype)
     layer_s = time.perf_counter() - t0
     pass_s = layer_s * (len(stack.layers) + ratio) + decode_s
     main["single_thread"] = {
@@ -474,10 +480,11 @@ def encoder_cpu_baseline(stack, budget_s=20.0, decoder=None):
 
 def encoder_cpu_leg(stack, threads, budget_s, decoder):
     from oracle import pko
+    dtype = stack.x.dtype  # f16: the reference's fp16 chain; f32: its fp32 profile
     t0 = time.perf_counter()
     if stack.subsampling is not None:
-        x = pko.encoder_front_end(stack.features[:1], stack.subsampling, stack.feature_lengths[:1],
-                                  gemm_mode="f16-chain", threads=threads)
+        x = pko.encoder_front_end(stack.features[:1], stack.subsampling, stack.feature_lengths[:1], threads=threads,
+                                  dtype=dtype)
     else:
         x = stack.x[:stack.frames]
     front_s = time.perf_counter() - t0
@@ -485,14 +492,15 @@ def encoder_cpu_leg(stack, threads, budget_s, decoder):
     done = 0
     while done < len(stack.layers) and (done == 0 or time.perf_counter() - t0 < budget_s):
         x = pko.encoder_layer(x, stack.layers[done], stack.valid[:1], batch=1, frames=stack.frames,
-                              gemm_mode="f16-chain", threads=threads)
+                              threads=threads, dtype=dtype)
         done += 1
     layer_s = (time.perf_counter() - t0 - front_s) / done
     # one window's pass: the front end plus every layer at the measured rate
     pass_s = front_s + layer_s * len(stack.layers)
     sample = (f"one 15-s window: the front end and {done} of {len(stack.layers)} layers timed, the pass "
-              "extrapolated to every layer (f16-accumulator GEMM chain, f32 conv, LayerNorm and attention: "
-              "reference fp16 semantics)")
+              "extrapolated to every layer " + ("(f16-accumulator GEMM chain, f32 conv, LayerNorm and attention: "
+                                                "reference fp16 semantics)" if dtype == np.float16 else
+                                                "(f32 storage and arithmetic: the reference's fp32 profile)"))
     decode_s = 0.0
     if decoder is not None:
         weights, projected, length = decoder
@@ -533,6 +541,11 @@ class ActivePrefix:
 def run_encoder(args, abi, ctx, decoder=False):
     import parakeet_wgsl_amd.workloads as wl
     stack = wl.encoder_stack(0, windows=args.windows, frames=188, layers=24, front_end=True, projector=True)
+    f32 = args.precision == "f32"
+    if f32:
+        if decoder or args.fused_norms:
+            raise SystemExit("--precision f32 runs the encoder workload without the f16-only fusions")
+        stack = wl.as_f32_profile(stack)
     active = args.active or stack.batch
     if not 1 <= active <= stack.batch:
         raise SystemExit(f"--active must be in [1, {stack.batch}]")
@@ -551,15 +564,16 @@ def run_encoder(args, abi, ctx, decoder=False):
         layers.append(d)
     front = {key: upload(value) for key, value in stack.subsampling.items()}
     features, feature_lengths, valid = put(stack.features), put(stack.feature_lengths), put(stack.valid)
-    out = ctx.empty(stack.x.shape, np.float16)
-    projected = ctx.empty((stack.x.shape[0], stack.projector_bias.size), np.float16)
+    out = ctx.empty(stack.x.shape, stack.x.dtype)
+    projected = ctx.empty((stack.x.shape[0], stack.projector_bias.size), stack.x.dtype)
     held += [out, projected]
     enc = abi.EncoderOp(ctx, layers=layers, valid_lengths=valid, input=features, output=out, batch_size=stack.batch,
                         frames=stack.frames, subsampling=front, feature_frames=stack.feature_frames,
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
                         projected_output=projected, fused_norms=args.fused_norms,
-                        unchained_norms=args.unchained_norms, fused_glu=not args.separate_glu, label="encoder")
+                        unchained_norms=args.unchained_norms, fused_glu=not args.separate_glu, label="encoder",
+                        precision=args.precision)
     launches, device_bytes = enc.info()
     fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
     # the LN ff1 of layers after the first runs in the LN out launch before it
@@ -617,7 +631,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     durations = durations.mean(axis=0)  # ms per launch of the pass
     decoder_ms = float(np.mean([a.elapsed_ms(b) for a, b in tdt_marks.values()])) if tdt else None
     run = ActivePrefix(stack, active)
-    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, run, not args.separate_glu)
+    front_costs, layer_costs, projector_costs = encoder_dispatch_costs(abi, wl, run, not (args.separate_glu or f32))
     nf, per = len(front_costs), len(abi.ENCODER_DISPATCHES)
     names = list(FRONT_DISPATCHES) + list(abi.ENCODER_DISPATCHES) + ["projector"] * len(projector_costs)
     costs = front_costs + layer_costs + projector_costs
@@ -663,14 +677,15 @@ def run_encoder(args, abi, ctx, decoder=False):
         per_kind[kind(k)] = per_kind.get(kind(k), 0.0) + d["avg_us"] * d["launches_per_pass"]
     name = max(per_kind, key=per_kind.get)
     dom = dispatches[name]
-    if dom["flops"] / (PEAK_TFLOPS["f16"] * 1e12) >= dom["algorithmic_bytes"] / (PEAK_HBM_GBS * 1e9):
-        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_TFLOPS["f16"], "unit": "TFLOP/s",
-                    "frac": dom["tflops"] / PEAK_TFLOPS["f16"]}
+    peak = PEAK_TFLOPS[args.precision]
+    if dom["flops"] / (peak * 1e12) >= dom["algorithmic_bytes"] / (PEAK_HBM_GBS * 1e9):
+        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak, "unit": "TFLOP/s",
+                    "frac": dom["tflops"] / peak}
     else:
         roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": dom["gbs"] / PEAK_HBM_GBS}
     roofline["kernel"] = f"encoder.layers.*-{name}" if name in abi.ENCODER_DISPATCHES else f"encoder.{name}"
-    roofline["traffic"] = read_traffic(f"encoder-{name}", None)
+    roofline["traffic"] = read_traffic(f"encoder-{name}", None) if not f32 else None
     roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
 
     total_flops = run.gemm_flops() + run.attention_flops() + run.front_end_flops()
@@ -689,7 +704,7 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "workgroups_per_window": tdt.team_size(), "workgroups": active * tdt.team_size(),
                    "max_tokens": 1024}
     dense = None
-    if not args.no_dense:
+    if not args.no_dense and not f32:
         rows = active * stack.frames
         shapes = {"feed-forward1-linear1": (1024, 4096), "feed-forward1-linear2-residual": (4096, 1024),
                   "self-attention-qkv": (1024, 3072), "convolution-pointwise1": (1024, 2048),
@@ -712,9 +727,9 @@ def run_encoder(args, abi, ctx, decoder=False):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": args.precision,
         "data": "synthetic (seeded random fbank, palette codes, LUTs, norms and biases)",
-        "config": {"workload": "fastconformer-tdt-transcribe-fp16" if tdt else "fastconformer-encoder-fp16",
+        "config": {"workload": "fastconformer-tdt-transcribe-fp16" if tdt else f"fastconformer-encoder-fp{32 if f32 else 16}",
                    "windows": active, "capacity_windows": stack.batch,
                    "window_seconds": WINDOW_SECONDS, "fbank_frames": stack.feature_frames, "mel_bins": 128,
                    "frames": stack.frames, "layers": len(stack.layers), "d_model": 1024, "ff_hidden": 4096,
@@ -726,7 +741,8 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
                                  if args.fused_norms else "separate launches" if not chained else
                                  "separate launches; each layer's last LayerNorm also writes the next layer's first",
-                   "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu else "in PW1's epilogue",
+                   "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu
+                          else "in the convolution (the fp32 profile)" if f32 else "in PW1's epilogue",
                    "graph_replay": True,
                    "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,

@@ -66,7 +66,10 @@ extern "C" {
 typedef struct pk_encoder pk_encoder;
 
 /* One palette matrix in the reference package format: packed codes
-   (K*N*bits/8 bytes) and its palette ([groups, 2^bits] f16). */
+   (K*N*bits/8 bytes) and its palette ([groups, 2^bits] in the encoder's
+   precision). Below, "f16" tensors (palettes, projected positions,
+   depthwise and front-end convolution weights, activations) are f32 with
+   PK_PRECISION_F32, the reference's fp32 profile (encoder.ts:947-1165). */
 typedef struct pk_encoder_matrix {
   const uint32_t *packed;
   const void *palette;
@@ -120,7 +123,9 @@ typedef struct pk_encoder_desc {
   uint32_t struct_size;          /* sizeof(pk_encoder_desc) */
   uint32_t flags;                /* PK_ENCODER_* */
   const char *label;
-  int32_t precision;             /* PK_PRECISION_F16 */
+  int32_t precision;             /* PK_PRECISION_F16, or PK_PRECISION_F32 (the fp32 profile: f32 GEMMs,
+                                    LayerNorm, attention, convolution and front end; the GLU stays in the
+                                    convolution; not with PK_ENCODER_FUSED_GLU or PK_ENCODER_FUSED_NORMS) */
   uint32_t batch_size;           /* windows */
   uint32_t frames;               /* encoder frames per window (188) */
   uint32_t layers;               /* 1..64 */

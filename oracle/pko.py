@@ -373,26 +373,43 @@ ENCODER_BITS = {"ff1_linear1": 5, "ff1_linear2": 5, "qkv": 5, "o_proj": 6, "poin
                 "ff2_linear1": 5, "ff2_linear2": 5}
 
 
-def encoder_layer(x, layer, valid, *, batch, frames, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+def _chain(dtype, gemm_mode):
+    """The storage dtype and GEMM mode of an encoder chain: f16 storage with
+    the reference's f16 GEMM arithmetic by default, f32 storage (the
+    reference's fp32 profile, encoder.ts:947-1165) with its f32 chain."""
+    dtype = np.dtype(dtype)
+    if dtype not in (np.dtype(np.float16), np.dtype(np.float32)):
+        raise ValueError("the encoder chain stores float16 or float32")
+    if gemm_mode is None:
+        gemm_mode = "f16-chain" if dtype == np.float16 else "f32-chain"
+    return dtype, gemm_mode
+
+
+def encoder_layer(x, layer, valid, *, batch, frames, gemm_mode=None, threads=8, dtype=np.float16) -> np.ndarray:
     """One FastConformer layer over f16 features x [batch*frames, 1024], in
     the order of createEncoderLayerDispatches (encoder.ts:1868-2135):
       x1 = x + 0.5 FF1(LN(x)),  FF(h) = SiLU(h W1) W2
       x2 = x1 + attention(LN(x1) Wqkv) Wo
       x3 = x2 + SiLU(BN(DW9(GLU(LN(x2) PW1)))) PW2
       x4 = x3 + 0.5 FF2(LN(x3));  out = LN(x4)
-    Every intermediate is stored as f16 like the reference's arena. `layer`
-    is keyed like pk_encoder_layer (norm_gamma / norm_beta [5, 1024], each
-    matrix a (packed words, palette) pair). gemm_mode "f16-chain" is the
-    reference's fp16 GEMM arithmetic, "f64" the exact sum rounded once."""
-    x = np.ascontiguousarray(x, dtype=np.float16)
+    Every intermediate is stored in `dtype` (f16 by default, f32 for the
+    reference's fp32 profile) like the reference's arena. `layer` is keyed
+    like pk_encoder_layer (norm_gamma / norm_beta [5, 1024], each matrix a
+    (packed words, palette) pair; palettes, positions and depthwise weights
+    are taken in `dtype`). gemm_mode "f16-chain" is the reference's fp16 GEMM
+    arithmetic, "f32-chain" its fp32 one (the defaults), "f64" the exact sum
+    rounded once."""
+    dtype, gemm_mode = _chain(dtype, gemm_mode)
+    x = np.ascontiguousarray(x, dtype=dtype)
 
     def norm(i, h):
         return layernorm(h, layer["norm_gamma"][i], layer["norm_beta"][i])
 
     def mm(name, a, columns, **epilogue):
         words, palette = layer[name]
-        out = gemm(a, words, ENCODER_BITS[name], palette, columns, mode=gemm_mode, threads=threads, **epilogue)
-        return out.astype(np.float16)
+        out = gemm(a, words, ENCODER_BITS[name], np.asarray(palette, dtype=dtype), columns, mode=gemm_mode,
+                   threads=threads, **epilogue)
+        return out.astype(dtype)
 
     hidden = mm("ff1_linear1", norm(0, x), 4096, activation="silu")
     x1 = mm("ff1_linear2", hidden, 1024, residual=x, residual_scale=0.5)
@@ -409,10 +426,11 @@ def encoder_layer(x, layer, valid, *, batch, frames, gemm_mode="f16-chain", thre
     return norm(4, x4)
 
 
-def encoder(x, layers, valid, *, batch, frames, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+def encoder(x, layers, valid, *, batch, frames, gemm_mode=None, threads=8, dtype=np.float16) -> np.ndarray:
     """The layer stack: encoder_layer applied for each entry of `layers`."""
     for layer in layers:
-        x = encoder_layer(x, layer, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
+        x = encoder_layer(x, layer, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads,
+                          dtype=dtype)
     return x
 
 
@@ -504,22 +522,25 @@ def tdt_decode(weights: dict, encoder_projected, lengths, *, max_tokens: int, st
     return out
 
 
-def encoder_front_end(features, front, feature_lengths, *, gemm_mode="f16-chain", threads=8) -> np.ndarray:
+def encoder_front_end(features, front, feature_lengths, *, gemm_mode=None, threads=8,
+                      dtype=np.float16) -> np.ndarray:
     """The subsampling front end (encoder.ts:2140-2400) over f32
     feature-major fbank [batch, 128, F] into [batch * sub(F, 3), 1024] f16:
     conv0 + ReLU + depthwise2, pointwise3 + bias + ReLU, depthwise5,
     pointwise6 + bias + ReLU, rows past sub(L, 3) zeroed, flatten (frequency
     major) and the linear 4096 -> 1024 + bias. `front` is keyed like
-    pk_encoder_subsampling."""
+    pk_encoder_subsampling; stages stored in `dtype` (as encoder_layer)."""
+    dtype, gemm_mode = _chain(dtype, gemm_mode)
     batch = features.shape[0]
     stage = subsampling_fused(features, front["conv0_weights"], front["conv0_bias"], front["depthwise2_weights"],
-                              front["depthwise2_bias"], feature_lengths, dtype=np.float16)
+                              front["depthwise2_bias"], feature_lengths, dtype=dtype)
     _, h2, w2, channels = stage.shape
 
     def mm(name, a, columns, **epilogue):
         words, palette = front[name]
-        out = gemm(a, words, 5, palette, columns, mode=gemm_mode, threads=threads, **epilogue)
-        return out.astype(np.float16)
+        out = gemm(a, words, 5, np.asarray(palette, dtype=dtype), columns, mode=gemm_mode, threads=threads,
+                   **epilogue)
+        return out.astype(dtype)
     projected = mm("pointwise3", stage.reshape(-1, channels), channels, bias=front["pointwise3_bias"],
                    activation="relu").reshape(batch, h2, w2, channels)
     stage = subsampling_depthwise(projected, front["depthwise5_weights"], front["depthwise5_bias"], feature_lengths, 3)
@@ -531,18 +552,20 @@ def encoder_front_end(features, front, feature_lengths, *, gemm_mode="f16-chain"
 
 
 def encoder_graph(x, layers, valid, *, batch, frames, front=None, features=None, feature_lengths=None,
-                  projector=None, projector_bias=None, gemm_mode="f16-chain", threads=8):
+                  projector=None, projector_bias=None, gemm_mode=None, threads=8, dtype=np.float16):
     """ParakeetEncoderGraph.encode (encoder.ts:1690-1706): the front end when
     `front` is given (from `features`; `x` is then unused), the layers, and
-    the projector when given. Returns (output, projected or None)."""
+    the projector when given, every stage stored in `dtype`. Returns
+    (output, projected or None)."""
+    dtype, gemm_mode = _chain(dtype, gemm_mode)
     if front is not None:
-        x = encoder_front_end(features, front, feature_lengths, gemm_mode=gemm_mode, threads=threads)
-    out = encoder(x, layers, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads)
+        x = encoder_front_end(features, front, feature_lengths, gemm_mode=gemm_mode, threads=threads, dtype=dtype)
+    out = encoder(x, layers, valid, batch=batch, frames=frames, gemm_mode=gemm_mode, threads=threads, dtype=dtype)
     projected = None
     if projector is not None:
         words, palette = projector
-        projected = gemm(out, words, 5, palette, projector_bias.size, bias=projector_bias, mode=gemm_mode,
-                         threads=threads).astype(np.float16)
+        projected = gemm(out, words, 5, np.asarray(palette, dtype=dtype), projector_bias.size, bias=projector_bias,
+                         mode=gemm_mode, threads=threads).astype(dtype)
     return out, projected
 
 

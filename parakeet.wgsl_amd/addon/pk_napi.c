@@ -1219,7 +1219,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
   return ok;
 }
 
-/* Parses an encoder descriptor: {label, fusedGlu?, fusedNorms?, unchainedNorms?, batchSize, frames,
+/* Parses an encoder descriptor: {label, precision?, fusedGlu?, fusedNorms?, unchainedNorms?, batchSize, frames,
    layers: [layer...], validLengths, input, output, subsampling?,
    featureFrames?, featureLengths?, projector?, projectorBias?,
    projectedChannels?, projectedOutput?}. The layer array, front end and
@@ -1227,7 +1227,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
 static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   memset(d, 0, sizeof *d);
   d->struct_size = sizeof *d;
-  d->precision = PK_PRECISION_F16;
+  parse_precision(env, o, &d->precision); /* "f16" (default) or "f32", the fp32 profile */
   napi_value layers, item, v;
   uint32_t n = 0;
   bool glu = true;

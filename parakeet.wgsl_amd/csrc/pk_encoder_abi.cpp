@@ -68,6 +68,8 @@ struct pk_encoder {
   pk_abi::CtxRef ctx;
   std::string label;
   uint32_t batch = 0, frames = 0, layers = 0, rows = 0;
+  int precision = PK_PRECISION_F16;  // of the activations, palettes and per-channel tensors
+  uint64_t elem = 2;                 // bytes per element in that precision
   bool fused_glu = true;
   bool fused_norms = false;
   bool chained_norms = true;  // norm_out also writes the next layer's norm_feed_forward1
@@ -87,7 +89,7 @@ struct pk_encoder {
   // Arena slices: four [rows, 1024] activation buffers, the FF hidden block,
   // QKV, the attention context, the pointwise-1 output, the conv output and,
   // with the front end, two [windows, H2, 32, 256] stage buffers.
-  _Float16 *a = nullptr, *b = nullptr, *c = nullptr, *d = nullptr, *h = nullptr, *qkv = nullptr, *ctxt = nullptr,
+  void *a = nullptr, *b = nullptr, *c = nullptr, *d = nullptr, *h = nullptr, *qkv = nullptr, *ctxt = nullptr,
            *pw = nullptr, *cout = nullptr, *s1 = nullptr, *s2 = nullptr;
   FrontOps front_ops;
   std::vector<LayerOps> ops;
@@ -123,7 +125,7 @@ void release_encoder(pk_encoder* e) {
   }
 }
 
-// One palette GEMM of the graph, f16, over `rows` rows.
+// One palette GEMM of the graph, in the encoder's precision, over `rows` rows.
 struct GemmSpec {
   pk_encoder_matrix matrix;
   int bits = 5;
@@ -148,7 +150,7 @@ int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStr
   d.struct_size = sizeof d;
   d.flags = g.flags;
   d.label = label.c_str();
-  d.precision = PK_PRECISION_F16;
+  d.precision = e->precision;
   d.palette_bits = g.bits;
   d.rows = g.rows;
   d.inner = g.inner;
@@ -156,17 +158,17 @@ int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStr
   d.palette_groups = g.groups;
   d.palette_group_columns = g.columns / g.groups;
   d.a = g.a;
-  d.a_bytes = R * g.inner * 2;
+  d.a_bytes = R * g.inner * e->elem;
   d.packed = g.matrix.packed;
   d.packed_bytes = packed_bytes(g.bits, g.inner, g.columns);
   d.palette = g.matrix.palette;
-  d.palette_bytes = (uint64_t)g.groups * (1u << g.bits) * 2;
+  d.palette_bytes = (uint64_t)g.groups * (1u << g.bits) * e->elem;
   d.output = g.out;
-  d.output_bytes = R * ((g.flags & PK_GEMM_GLU) ? g.columns / 2 : g.columns) * 2;
+  d.output_bytes = R * ((g.flags & PK_GEMM_GLU) ? g.columns / 2 : g.columns) * e->elem;
   d.bias = g.bias;
   d.bias_bytes = g.bias ? (uint64_t)g.columns * 4u : 0;
   d.residual = g.residual;
-  d.residual_bytes = g.residual ? R * g.columns * 2 : 0;
+  d.residual_bytes = g.residual ? R * g.columns * e->elem : 0;
   d.has_residual_scale = g.residual ? 1 : 0;
   d.residual_scale = g.scale;
   d.activation = g.activation;
@@ -191,7 +193,8 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
                 bool validate_only) {
   const std::string prefix = e->label + ".subsampling-";
   const uint32_t h2 = e->front_height, h3 = e->frames, w2 = halve(kBins, 2), w3 = halve(kBins, 3);
-  const uint64_t stage2 = (uint64_t)e->batch * h2 * w2 * kSubC * 2, stage3 = (uint64_t)e->batch * h3 * w3 * kSubC * 2;
+  const uint64_t stage2 = (uint64_t)e->batch * h2 * w2 * kSubC * e->elem;
+  const uint64_t stage3 = (uint64_t)e->batch * h3 * w3 * kSubC * e->elem;
   std::string label;
   int s;
   {
@@ -199,7 +202,7 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
     pk_subsampling_fused_desc d{};
     d.struct_size = sizeof d;
     d.label = label.c_str();
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.batch_size = e->batch;
     d.input_height = e->feature_frames;
     d.input_width = kBins;
@@ -207,11 +210,11 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
     d.input = static_cast<const float*>(e->input);
     d.input_bytes = (uint64_t)e->batch * kBins * e->feature_frames * 4u;
     d.conv0_weights = w.conv0_weights;
-    d.conv0_weights_bytes = 9ull * kSubC * 2;
+    d.conv0_weights_bytes = 9ull * kSubC * e->elem;
     d.conv0_bias = w.conv0_bias;
     d.conv0_bias_bytes = kSubC * 4u;
     d.depthwise_weights = w.depthwise2_weights;
-    d.depthwise_weights_bytes = 9ull * kSubC * 2;
+    d.depthwise_weights_bytes = 9ull * kSubC * e->elem;
     d.depthwise_bias = w.depthwise2_bias;
     d.depthwise_bias_bytes = kSubC * 4u;
     d.output = e->s1;
@@ -235,7 +238,7 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
     pk_subsampling_depthwise_desc d{};
     d.struct_size = sizeof d;
     d.label = label.c_str();
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.batch_size = e->batch;
     d.input_height = h2;
     d.input_width = w2;
@@ -243,7 +246,7 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
     d.input = e->s2;
     d.input_bytes = stage2;
     d.weights = w.depthwise5_weights;
-    d.weights_bytes = 9ull * kSubC * 2;
+    d.weights_bytes = 9ull * kSubC * e->elem;
     d.bias = w.depthwise5_bias;
     d.bias_bytes = kSubC * 4u;
     d.output = e->s1;
@@ -271,7 +274,7 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
     pk_subsampling_mask_desc d{};
     d.struct_size = sizeof d;
     d.label = label.c_str();
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.batch_size = e->batch;
     d.height = h3;
     d.width = w3;
@@ -318,24 +321,24 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     pk_layernorm_desc d{};
     d.struct_size = sizeof d;
     d.label = name(suffix);
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.rows = e->rows;
     d.channels = kC;
     d.input = in;
-    d.input_bytes = R * kC * 2;
+    d.input_bytes = R * kC * e->elem;
     d.gamma = w.norm_gamma[i];
     d.gamma_bytes = kC * 4;
     d.beta = w.norm_beta[i];
     d.beta_bytes = kC * 4;
     d.output = out;
-    d.output_bytes = R * kC * 2;
+    d.output_bytes = R * kC * e->elem;
     if (chained_out) {
       d.next_gamma = next->norm_gamma[0];
       d.next_gamma_bytes = kC * 4;
       d.next_beta = next->norm_beta[0];
       d.next_beta_bytes = kC * 4;
       d.next_output = chained_out;
-      d.next_output_bytes = R * kC * 2;
+      d.next_output_bytes = R * kC * e->elem;
     }
     return validate_only ? pk_layernorm_validate(&d) : pk_layernorm_create(e->ctx, &d, &l.norm[i]);
   };
@@ -395,13 +398,13 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     pk_attention_desc d{};
     d.struct_size = sizeof d;
     d.label = name("-relative-attention");
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.batch_size = e->batch;
     d.frames = e->frames;
     d.qkv = e->qkv;
-    d.qkv_bytes = R * 3 * kC * 2;
+    d.qkv_bytes = R * 3 * kC * e->elem;
     d.projected_positions = w.projected_positions;
-    d.projected_positions_bytes = (2ull * e->frames - 1u) * kC * 2;
+    d.projected_positions_bytes = (2ull * e->frames - 1u) * kC * e->elem;
     d.bias_u = w.bias_u;
     d.bias_u_bytes = 4096;
     d.bias_v = w.bias_v;
@@ -409,7 +412,7 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     d.valid_lengths = e->valid_lengths;
     d.valid_lengths_bytes = (uint64_t)e->batch * 4u;
     d.output = e->ctxt;
-    d.output_bytes = R * kC * 2;
+    d.output_bytes = R * kC * e->elem;
     if ((s = validate_only ? pk_attention_validate(&d) : pk_attention_create(e->ctx, &d, &l.attention))) return s;
   }
   if ((s = gemm(&l.o, "-self-attention-output-residual", w.o_proj, 6, kC, kC, 1, e->ctxt, e->c, e->b, 1.0f,
@@ -424,14 +427,14 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     d.struct_size = sizeof d;
     d.flags = e->fused_glu ? PK_CONV_INPUT_GLU : 0u;
     d.label = name("-convolution-glu-depthwise-bn-silu");
-    d.precision = PK_PRECISION_F16;
+    d.precision = e->precision;
     d.batch_size = e->batch;
     d.frames = e->frames;
     d.channels = kC;
     d.pointwise_input = e->pw;
-    d.pointwise_input_bytes = R * (e->fused_glu ? kC : 2 * kC) * 2;
+    d.pointwise_input_bytes = R * (e->fused_glu ? kC : 2 * kC) * e->elem;
     d.depthwise_weights = w.depthwise;
-    d.depthwise_weights_bytes = 9ull * kC * 2;
+    d.depthwise_weights_bytes = 9ull * kC * e->elem;
     d.batch_norm_scale = w.bn_scale;
     d.batch_norm_scale_bytes = kC * 4;
     d.batch_norm_shift = w.bn_shift;
@@ -439,7 +442,7 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     d.valid_lengths = e->valid_lengths;
     d.valid_lengths_bytes = (uint64_t)e->batch * 4u;
     d.output = e->cout;
-    d.output_bytes = R * kC * 2;
+    d.output_bytes = R * kC * e->elem;
     if ((s = validate_only ? pk_conv_validate(&d) : pk_conv_create(e->ctx, &d, &l.conv))) return s;
   }
   if ((s = gemm(&l.pw2, "-convolution-pointwise2-residual", w.pointwise2, 5, kC, kC, 1, e->cout, e->d, e->c, 1.0f,
@@ -542,11 +545,11 @@ uint64_t place_arena(pk_encoder* e, uint8_t* base) {
   const uint64_t stage = e->front ? (uint64_t)e->batch * e->front_height * halve(kBins, 2) * kSubC : 0;
   const uint64_t elems[11] = {R * kC,     R * kC, R * kC, R * kC, R * kHidden, R * 3 * kC, R * kC,
                               R * (e->fused_glu ? kC : 2 * kC), R * kC, stage, stage};
-  _Float16** slots[11] = {&e->a, &e->b, &e->c, &e->d, &e->h, &e->qkv, &e->ctxt, &e->pw, &e->cout, &e->s1, &e->s2};
+  void** slots[11] = {&e->a, &e->b, &e->c, &e->d, &e->h, &e->qkv, &e->ctxt, &e->pw, &e->cout, &e->s1, &e->s2};
   uint64_t at = 0;
   for (int i = 0; i < 11; ++i) {
-    if (base) *slots[i] = elems[i] ? reinterpret_cast<_Float16*>(base + at) : nullptr;
-    at += (elems[i] * 2 + 255u) / 256u * 256u;
+    if (base) *slots[i] = elems[i] ? static_cast<void*>(base + at) : nullptr;
+    at += (elems[i] * e->elem + 255u) / 256u * 256u;
   }
   return at;
 }
@@ -559,7 +562,10 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->frames = d->frames;
   e->layers = d->layers;
   e->rows = d->batch_size * d->frames;
-  e->fused_glu = (d->flags & PK_ENCODER_SEPARATE_GLU) == 0;
+  e->precision = d->precision;
+  e->elem = d->precision == PK_PRECISION_F32 ? 4u : 2u;
+  // The GLU epilogue and the fused row norm are f16 kernels.
+  e->fused_glu = (d->flags & PK_ENCODER_SEPARATE_GLU) == 0 && d->precision == PK_PRECISION_F16;
   e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
   e->chained_norms = (d->flags & (PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS)) == 0;
   e->valid_lengths = d->valid_lengths;
@@ -588,8 +594,11 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if ((d->flags & PK_ENCODER_FUSED_GLU) && (d->flags & PK_ENCODER_SEPARATE_GLU))
     return fail(PK_INVALID_ARGUMENT, "%s: PK_ENCODER_FUSED_GLU and PK_ENCODER_SEPARATE_GLU exclude each other", label);
-  if (d->precision != PK_PRECISION_F16)
-    return fail(PK_INVALID_ARGUMENT, "%s: the encoder stack runs in f16", label);
+  if (d->precision != PK_PRECISION_F16 && d->precision != PK_PRECISION_F32)
+    return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
+  if (d->precision == PK_PRECISION_F32 && (d->flags & (PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS)))
+    return fail(PK_INVALID_ARGUMENT, "%s: the GLU epilogue and the fused LayerNorms need f16", label);
+  const uint64_t elem = d->precision == PK_PRECISION_F32 ? 4u : 2u;
   if (d->batch_size == 0 || d->frames == 0 || d->layers == 0 || d->layers > kMaxLayers)
     return fail(PK_RANGE_ERROR, "Unsupported encoder shape for %s: %u windows x %u frames x %u layers", label,
                 d->batch_size, d->frames, d->layers);
@@ -597,7 +606,7 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "%s needs layer weights, valid lengths, input and output", label);
   if (!aligned(d->input, 16) || !aligned(d->output, 16))
     return fail(PK_INVALID_ARGUMENT, "%s input and output must be 16-byte aligned", label);
-  uint64_t in_bytes = (uint64_t)d->batch_size * d->frames * kC * 2;
+  uint64_t in_bytes = (uint64_t)d->batch_size * d->frames * kC * elem;
   if (d->subsampling) {
     if (d->feature_frames == 0 || halve(d->feature_frames, 3) != d->frames)
       return fail(PK_RANGE_ERROR, "%s: %u encoder frames do not follow from %u feature frames (expected %u)", label,
@@ -606,11 +615,11 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
       return fail(PK_INVALID_ARGUMENT, "%s: the front end needs per-window feature lengths", label);
     in_bytes = (uint64_t)d->batch_size * kBins * d->feature_frames * 4u;
   }
-  const uint64_t out_bytes = (uint64_t)d->batch_size * d->frames * kC * 2;
+  const uint64_t out_bytes = (uint64_t)d->batch_size * d->frames * kC * elem;
   if (overlap(d->input, in_bytes, d->output, out_bytes))
     return fail(PK_INVALID_ARGUMENT, "%s output must not overlap its input", label);
   if (d->projected_channels) {
-    const uint64_t proj_bytes = (uint64_t)d->batch_size * d->frames * d->projected_channels * 2;
+    const uint64_t proj_bytes = (uint64_t)d->batch_size * d->frames * d->projected_channels * elem;
     if (!d->projected_output || !aligned(d->projected_output, 16))
       return fail(PK_INVALID_ARGUMENT, "%s: the projector needs a 16-byte aligned projected output", label);
     if (overlap(d->projected_output, proj_bytes, d->output, out_bytes) ||

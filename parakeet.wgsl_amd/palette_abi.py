@@ -1107,19 +1107,22 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
 
 
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = True,
-                 fused_norms: bool = False, unchained_norms: bool = False, subsampling: dict | None = None, feature_frames: int = 0, feature_lengths=None,
-                 projector=None, projector_bias=None, projected_output=None, projected_channels: int = 0,
-                 label: str = "encoder") -> EncoderDesc:
+                 fused_norms: bool = False, unchained_norms: bool = False, subsampling: dict | None = None,
+                 feature_frames: int = 0, feature_lengths=None, projector=None, projector_bias=None,
+                 projected_output=None, projected_channels: int = 0, label: str = "encoder",
+                 precision: str = "f16") -> EncoderDesc:
     """An EncoderDesc over `layers` (dicts as encoder_layer takes), with the
     optional front end (`subsampling` dict, feature frames and lengths) and
     projector ((packed, palette) pair, bias, output); the returned structure
-    keeps what it points to alive."""
+    keeps what it points to alive. `precision` "f32" is the reference's fp32
+    profile: activations, palettes, positions and depthwise weights in f32
+    (the GLU then stays in the convolution)."""
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
     flags = ((0 if fused_glu else ENCODER_SEPARATE_GLU) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
              (ENCODER_UNCHAINED_NORMS if unchained_norms else 0))
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
-                       PRECISION["f16"], batch_size, frames, len(layers),
+                       PRECISION[precision], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),
                        _addr(output), ctypes.pointer(front) if front is not None else None, feature_frames,
                        _addr(feature_lengths) if feature_lengths is not None else None,

@@ -519,6 +519,26 @@ def encoder_stack(seed: int = 0, windows: int = 16, frames: int = 188, layers: i
     return enc
 
 
+def as_f32_profile(stack: EncoderStack) -> EncoderStack:
+    """The same stack for the reference's fp32 profile (encoder.ts:947-1165):
+    every f16 tensor (features, palettes, projected positions, depthwise and
+    front-end convolution weights) widened to f32, which holds its values
+    exactly; packed codes and the f32 per-channel tensors as they are."""
+    def widen(v):
+        if isinstance(v, np.ndarray) and v.dtype == np.float16:
+            return v.astype(np.float32)
+        if isinstance(v, tuple):
+            return tuple(widen(u) for u in v)
+        if isinstance(v, dict):
+            return {k: widen(u) for k, u in v.items()}
+        return v
+    out = EncoderStack(widen(stack.x), [widen(layer) for layer in stack.layers], stack.valid, stack.batch,
+                       stack.frames)
+    for name in ("features", "feature_lengths", "subsampling", "projector", "projector_bias"):
+        if hasattr(stack, name):
+            setattr(out, name, widen(getattr(stack, name)))
+    return out
+
 
 @dataclass
 class TdtCase:

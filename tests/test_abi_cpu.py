@@ -639,8 +639,9 @@ def test_tdt_plan_and_contract(abi):
 # ---------------------------------------------------------------- encoder stack
 
 
-def _encoder_fakes(layers=2, batch=16, frames=188):
-    """Nominal, aligned device addresses for every tensor of the stack."""
+def _encoder_fakes(layers=2, batch=16, frames=188, elem=2):
+    """Nominal, aligned device addresses for every tensor of the stack
+    (activations of `elem` bytes)."""
     at = [0x1000000000]
 
     def take(nbytes=1 << 20):
@@ -658,7 +659,7 @@ def _encoder_fakes(layers=2, batch=16, frames=188):
             layer[name] = take()
         stack.append(layer)
     rows = batch * frames
-    return dict(layers=stack, valid_lengths=take(), input=take(rows * 2048), output=take(rows * 2048),
+    return dict(layers=stack, valid_lengths=take(), input=take(rows * 1024 * elem), output=take(rows * 1024 * elem),
                 batch_size=batch, frames=frames)
 
 
@@ -718,8 +719,8 @@ def test_encoder_validate_stack_fields(abi):
     with pytest.raises(abi.PaletteError, match="16-byte aligned"):
         _validate_encoder(abi, **kw)
     desc = abi.encoder_desc(**_encoder_fakes())
-    desc.precision = abi.PRECISION["f32"]
-    with pytest.raises(abi.PaletteError, match="runs in f16"):
+    desc.precision = 7
+    with pytest.raises(abi.PaletteError, match="unsupported precision 7"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
     desc.flags = 0x10
@@ -731,6 +732,13 @@ def test_encoder_validate_stack_fields(abi):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc.flags = abi.ENCODER_FUSED_GLU  # the default, still accepted
     abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+    # the fp32 profile: accepted, without the f16-only fusions
+    _validate_encoder(abi, precision="f32", **_encoder_fakes(layers=24, elem=4))
+    for flags in (abi.ENCODER_FUSED_GLU, abi.ENCODER_FUSED_NORMS):
+        desc = abi.encoder_desc(precision="f32", **_encoder_fakes(elem=4))
+        desc.flags = flags
+        with pytest.raises(abi.PaletteError, match="need f16"):
+            abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
 
 
 def test_encoder_validate_front_end_and_projector(abi):

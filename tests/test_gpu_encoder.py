@@ -51,6 +51,7 @@ class Stack:
     (and the front end and projector when the stack has them)."""
 
     def __init__(self, abi, ctx, scope, stack, *, fused_glu=True, fused_norms=False, unchained_norms=False):
+        precision = "f32" if stack.x.dtype == np.float32 else "f16"
         self.ctx = ctx
         self.valid = scope.put(stack.valid)
         self.output = scope.put(np.full_like(stack.x, 77))
@@ -67,14 +68,14 @@ class Stack:
         self.projected = None
         if stack.projector is not None:
             channels = stack.projector_bias.size
-            self.projected = scope.put(np.full((stack.x.shape[0], channels), 77, np.float16))
+            self.projected = scope.put(np.full((stack.x.shape[0], channels), 77, stack.x.dtype))
             extra.update(projector=tuple(scope.put(v) for v in stack.projector),
                          projector_bias=scope.put(stack.projector_bias), projected_channels=channels,
                          projected_output=self.projected)
         self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
                                 input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
                                 fused_glu=fused_glu, fused_norms=fused_norms, unchained_norms=unchained_norms,
-                                **extra)
+                                precision=precision, **extra)
 
     def run(self, active=0, graph=False):
         self.op.enqueue(active, graph=graph)
@@ -260,6 +261,34 @@ def test_encoder_chained_norms_match_unchained(abi, ctx, scope, workloads):
     for got, want in zip(outs[0], outs[1]):
         assert np.isfinite(got).all()
         np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_encoder_f32_profile_matches_oracle(abi, ctx, scope, oracle, workloads):
+    """The reference's fp32 profile (encoder.ts:947-1165): front end, two
+    layers and the projector with f32 activations, palettes, positions and
+    depthwise weights (the GLU in the convolution) against the oracle's f32
+    chain and the exact one, on the frames below each window's length:
+    within 1e-4 of both (measured in the test's output)."""
+    stack = workloads.as_f32_profile(workloads.encoder_stack(seed=41, windows=2, frames=188, layers=2,
+                                                             front_end=True, projector=True))
+    enc = Stack(abi, ctx, scope, stack)
+    try:
+        got, projected = enc.run_both()
+        again, _ = enc.run_both(graph=True)
+    finally:
+        enc.release()
+    assert got.dtype == np.float32 and np.isfinite(got).all()
+    np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+    for mode in ("f32-chain", "f64"):
+        want, want_projected = oracle.encoder_graph(None, stack.layers, stack.valid, batch=2, frames=188,
+                                                    front=stack.subsampling, features=stack.features,
+                                                    feature_lengths=stack.feature_lengths,
+                                                    projector=stack.projector, projector_bias=stack.projector_bias,
+                                                    gemm_mode=mode, threads=THREADS, dtype=np.float32)
+        norm, worst = oracle.relative_errors(valid_rows(got, stack), valid_rows(want, stack))
+        pnorm, _ = oracle.relative_errors(valid_rows(projected, stack), valid_rows(want_projected, stack))
+        print(f"f32 profile vs {mode}: output norm {norm:.2e} (max {worst:.2e}), projected {pnorm:.2e}", flush=True)
+        assert norm <= 1e-4 and pnorm <= 1e-4, (mode, norm, worst, pnorm)
 
 
 def test_encoder_rejects_bad_active_batch(abi, ctx, scope, workloads):

@@ -55,13 +55,15 @@ class _Attention:
         self.valid, self.batch, self.frames = valid, batch, frames
 
 
-def torch_encoder_layer(x, layer, valid, batch, frames, mistake=None):
-    """One layer through torch in float64, f16 storage between dispatches."""
+def torch_encoder_layer(x, layer, valid, batch, frames, mistake=None, storage="f16"):
+    """One layer through torch in float64, f16 (or, for the fp32 profile,
+    f32) storage between dispatches."""
     import torch
     import torch.nn.functional as F
+    stored = torch.float16 if storage == "f16" else torch.float32
 
     def f16(t):
-        return t.to(torch.float16).to(torch.float64)
+        return t.to(stored).to(torch.float64)
 
     def tensor(a):
         return torch.from_numpy(np.asarray(a, dtype=np.float64))
@@ -129,16 +131,18 @@ def test_encoder_layer_planted_mistakes_fail(oracle, one_layer, mistake):
     assert norm > 10 * BAR, (mistake, norm)
 
 
-def torch_front_end(oracle, features, front, lengths, mistake=None):
-    """The front end through torch in float64 with the f16 profile's
-    storage: conv0 + ReLU (rounded to f16) + depthwise2, pointwise3 + bias +
-    ReLU, depthwise5 over the rows below sub(L, 2), pointwise6 + bias + ReLU,
-    rows past sub(L, 3) zeroed, the frequency-major flatten and the linear."""
+def torch_front_end(oracle, features, front, lengths, mistake=None, storage="f16"):
+    """The front end through torch in float64 with the f16 (or f32)
+    profile's storage: conv0 + ReLU (rounded to the storage type) +
+    depthwise2, pointwise3 + bias + ReLU, depthwise5 over the rows below
+    sub(L, 2), pointwise6 + bias + ReLU, rows past sub(L, 3) zeroed, the
+    frequency-major flatten and the linear."""
     import torch
     import torch.nn.functional as F
+    stored = torch.float16 if storage == "f16" else torch.float32
 
     def f16(t):
-        return t.to(torch.float16).to(torch.float64)
+        return t.to(stored).to(torch.float64)
 
     def kernel(w):  # [3, 3, C] -> [C, 1, 3, 3]
         return torch.from_numpy(np.asarray(w, np.float64)).permute(2, 0, 1).unsqueeze(1)
@@ -249,3 +253,39 @@ def test_f32_chain_keeps_the_small_terms():
     a, words, _ = _ones_case(pko, 64, 0)
     got = pko.gemm(a.astype(np.float32), words, 5, np.ones((1, 32), np.float32), 32, mode="f32-chain")
     assert (got == 2111.0).all()
+
+
+# The fp32 profile (encoder.ts:947-1165): the same restatements with f32
+# storage between dispatches against the oracle's f32 chain; only f32
+# arithmetic in the oracle's LayerNorm, attention and convolution separates
+# them (measured 2e-6 for the layer and 1e-7 for the front end, norm-wise),
+# so the bar is 1e-4, and a planted mistake
+# still misses it by orders of magnitude.
+BAR32 = 1e-4
+
+
+def test_encoder_layer_f32_storage_matches_torch_restatement(oracle, one_layer):
+    s = one_layer
+    got = oracle.encoder_layer(s.x, s.layers[0], s.valid, batch=s.batch, frames=s.frames, gemm_mode="f64",
+                               threads=THREADS, dtype=np.float32)
+    assert got.dtype == np.float32
+    want = torch_encoder_layer(s.x, s.layers[0], s.valid, s.batch, s.frames, storage="f32")
+    norm, worst = oracle.relative_errors(got, want)
+    print(f"f32 encoder layer vs torch float64 restatement: norm {norm:.2e} max {worst:.2e}")
+    assert norm <= BAR32, (norm, worst)
+    wrong = torch_encoder_layer(s.x, s.layers[0], s.valid, s.batch, s.frames, mistake="swapped-norm", storage="f32")
+    assert oracle.relative_errors(got, wrong)[0] > 10 * BAR32
+
+
+def test_front_end_f32_storage_matches_torch_restatement(oracle, front_case):
+    s = front_case
+    got = oracle.encoder_front_end(s.features, s.subsampling, s.feature_lengths, gemm_mode="f64", threads=THREADS,
+                                   dtype=np.float32)
+    assert got.dtype == np.float32
+    want = torch_front_end(oracle, s.features, s.subsampling, s.feature_lengths, storage="f32")
+    norm, worst = oracle.relative_errors(got, want)
+    print(f"f32 front end vs torch float64 restatement: norm {norm:.2e} max {worst:.2e}")
+    assert norm <= BAR32, (norm, worst)
+    wrong = torch_front_end(oracle, s.features, s.subsampling, s.feature_lengths, mistake="time-major-flatten",
+                            storage="f32")
+    assert oracle.relative_errors(got, wrong)[0] > 10 * BAR32
