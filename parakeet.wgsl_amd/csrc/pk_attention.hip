@@ -28,8 +28,9 @@
 // (Q+u) and (Q+v) are formed in f32 and rounded to f16 once per workgroup;
 // probabilities go to f16 for the PV product; everything else stays in f32.
 //
-// f32 kernel: a workgroup per (window, head, query) in the reference's own
-// arithmetic (fma chains in channel order, max / exp / sum, fma over keys).
+// f32 kernels: a flash kernel on f32 MFMAs (planned), and a workgroup per
+// (window, head, query) in the reference's own arithmetic (fma chains in
+// channel order, max / exp / sum, fma over keys).
 #include "pk_internal.h"
 
 namespace pk {
@@ -637,6 +638,204 @@ __global__ __launch_bounds__(256) void rel_attention_f32_kernel(AttnArgs args) {
   }
 }
 
+// f32 flash kernel on v_mfma_f32_32x32x2_f32: a wavefront owns one
+// (window, head, 32-query tile) and walks the key tiles in order, four
+// independent wavefronts per workgroup. The products are the f16 kernel's
+// (S^T = K (Q+u)^T, the 64-position window W^T = R (Q+v)^T read back along
+// the diagonal, O^T += V^T P^T), with three changes for single-K f32 MFMAs:
+//   * lane half h supplies channel 64h + s to product s of the 64 that make
+//     up a 128-channel dot product, so each lane reads 64 contiguous
+//     channels of its key, position and query rows;
+//   * the window's lower 32 rows are the previous tile's upper 32 (p_lo
+//     moves by 32 per key tile), so only 32 new positions are multiplied per
+//     tile;
+//   * PV product t takes keys 8(t/4) + 4h + t%4 in slot h, the keys whose
+//     probabilities lane half h already holds in register t, and output
+//     block e takes channel 4c + e in row c, so each lane reads V as one
+//     float4 of 4 consecutive channels per key and writes O as float4s.
+// All arithmetic is f32 (MFMA products accumulate in f32 in hardware
+// order); results stay within a few 1e-6 of the reference order.
+constexpr int kF32Waves = 4;
+
+template <bool ROW_MAJOR>
+__device__ __forceinline__ float4 load_position_f32(const float* positions, uint32_t rows, int head, int p, int d0) {
+  if constexpr (ROW_MAJOR)
+    return *reinterpret_cast<const float4*>(positions + (uint64_t)p * kHidden + head * kHead + d0);
+  else
+    return *reinterpret_cast<const float4*>(positions + (((uint64_t)head * 32 + d0 / 4) * rows + p) * 4);
+}
+
+template <bool ROW_MAJOR>
+__global__ __launch_bounds__(64 * kF32Waves) void rel_attention_f32_mfma_kernel(AttnArgs args) {
+  __shared__ __attribute__((aligned(16))) float windows[kF32Waves * 64 * kTile];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane & 31;
+  const int hh = lane >> 5;
+  // No workgroup barrier below: a wavefront past the last item just ends.
+  const uint32_t item = blockIdx.x * kF32Waves + (uint32_t)wave;
+  if (item >= args.work_items) return;
+  const uint32_t qt = item % args.query_tiles;
+  const uint32_t bh = item / args.query_tiles;
+  const int head = (int)(bh % kHeads);
+  const uint32_t b = bh / kHeads;
+  const int T = (int)args.frames;
+  const int live = (int)min(args.frames, args.valid_lengths[b]);
+  const int q0 = (int)qt * kTile;
+  const float* qkv = static_cast<const float*>(args.qkv) + (uint64_t)b * T * kQkvRow + head * kHead;
+  float* out = static_cast<float*>(args.output) + (uint64_t)b * T * kHidden + head * kHead;
+
+  if (q0 >= live) {
+    for (int c = lane; c < kTile * (kHead / 4); c += 64) {
+      const int q = q0 + c / (kHead / 4);
+      if (q < T) *reinterpret_cast<float4*>(out + (uint64_t)q * kHidden + (c % (kHead / 4)) * 4) = float4{};
+    }
+    return;
+  }
+
+  const int d_half = 64 * hh;  // channels d_half + s of product s
+  float qu[64], qv[64];
+  {
+    const float* qrow = qkv + (uint64_t)min(q0 + j, T - 1) * kQkvRow + d_half;
+    const float* bu = args.bias_u + head * kHead + d_half;
+    const float* bv = args.bias_v + head * kHead + d_half;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float4 x = *reinterpret_cast<const float4*>(qrow + 4 * g);
+      const float4 u = *reinterpret_cast<const float4*>(bu + 4 * g);
+      const float4 v = *reinterpret_cast<const float4*>(bv + 4 * g);
+      qu[4 * g] = x.x + u.x;
+      qu[4 * g + 1] = x.y + u.y;
+      qu[4 * g + 2] = x.z + u.z;
+      qu[4 * g + 3] = x.w + u.w;
+      qv[4 * g] = x.x + v.x;
+      qv[4 * g + 1] = x.y + v.y;
+      qv[4 * g + 2] = x.z + v.z;
+      qv[4 * g + 3] = x.w + v.w;
+    }
+  }
+
+  const float* positions = static_cast<const float*>(args.positions);
+  const int pmax = (int)args.position_rows - 1;
+  // 32 window rows p_first .. p_first + 31 for the 32 queries: R (Q+v)^T.
+  // Rows outside [0, 2T-2] are clamped; they only meet masked keys or
+  // queries past the valid length.
+  auto window_rows = [&](int p_first) {
+    floatx16 w;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w[r] = 0.0f;
+    const int p = min(max(p_first + j, 0), pmax);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float4 x = load_position_f32<ROW_MAJOR>(positions, args.position_rows, head, p, d_half + 4 * g);
+      w = __builtin_amdgcn_mfma_f32_32x32x2f32(x.x, qv[4 * g], w, 0, 0, 0);
+      w = __builtin_amdgcn_mfma_f32_32x32x2f32(x.y, qv[4 * g + 1], w, 0, 0, 0);
+      w = __builtin_amdgcn_mfma_f32_32x32x2f32(x.z, qv[4 * g + 2], w, 0, 0, 0);
+      w = __builtin_amdgcn_mfma_f32_32x32x2f32(x.w, qv[4 * g + 3], w, 0, 0, 0);
+    }
+    return w;
+  };
+
+  float* window = windows + wave * 64 * kTile;  // [64][32]
+  const float scale = 0.08838834764831845f;      // 1 / sqrt(128)
+  float m = -INFINITY, l = 0.0f;
+  floatx16 o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[e][r] = 0.0f;
+
+  const int tiles = (live + kTile - 1) / kTile;
+  floatx16 w_low = window_rows(T - 1 - q0 - (kTile - 1));
+  for (int kt = 0; kt < tiles; ++kt) {
+    const int k0 = kt * kTile;
+    const int p_lo = T - 1 - q0 - (kTile - 1) + k0;
+    floatx16 ac;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ac[r] = 0.0f;
+    const float* krow = qkv + (uint64_t)min(k0 + j, T - 1) * kQkvRow + kHidden + d_half;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float4 x = *reinterpret_cast<const float4*>(krow + 4 * g);
+      ac = __builtin_amdgcn_mfma_f32_32x32x2f32(x.x, qu[4 * g], ac, 0, 0, 0);
+      ac = __builtin_amdgcn_mfma_f32_32x32x2f32(x.y, qu[4 * g + 1], ac, 0, 0, 0);
+      ac = __builtin_amdgcn_mfma_f32_32x32x2f32(x.z, qu[4 * g + 2], ac, 0, 0, 0);
+      ac = __builtin_amdgcn_mfma_f32_32x32x2f32(x.w, qu[4 * g + 3], ac, 0, 0, 0);
+    }
+    const floatx16 w_high = window_rows(p_lo + kTile);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 8 * (r / 4) + 4 * hh + (r % 4);
+      window[c * kTile + j] = w_low[r];
+      window[(kTile + c) * kTile + j] = w_high[r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    float rel[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r / 4) + 4 * hh + (r % 4);
+      rel[r] = window[(kTile - 1 - j + i) * kTile + j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float sc[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r / 4) + 4 * hh + (r % 4);
+      sc[r] = k0 + i < live ? (ac[r] + rel[r]) * scale : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const bool moved = __builtin_amdgcn_ballot_w64(mx > m + kRescaleMargin) != 0;
+    const float m_new = moved ? fmaxf(m, mx) : m;
+    const float alpha = fast_exp(m - m_new);
+    float rs = 0.0f;
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp(sc[r] - m_new);
+      rs += p[r];
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+    m = m_new;
+    if (moved) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[e][r] *= alpha;
+    }
+    // O^T += V^T P^T: product t pairs key 8(t/4) + 4 hh + t%4 (slot hh) with
+    // channels 4j .. 4j+3 of that key, one per output block.
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int key = min(k0 + 8 * (t / 4) + 4 * hh + (t % 4), T - 1);
+      const float4 v = *reinterpret_cast<const float4*>(qkv + (uint64_t)key * kQkvRow + 2 * kHidden + 4 * j);
+      o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, p[t], o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, p[t], o[1], 0, 0, 0);
+      o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, p[t], o[2], 0, 0, 0);
+      o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, p[t], o[3], 0, 0, 0);
+    }
+    // The next tile rewrites the window after these reads.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    w_low = w_high;
+  }
+
+  // Block e, register r of lane (j, hh): channel 4 (8(r/4) + 4hh + r%4) + e
+  // of query q0 + j.
+  const int q = q0 + j;
+  if (q < T) {
+    const bool keep = q < live;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 8 * (r / 4) + 4 * hh + (r % 4);
+      const float4 y = keep ? float4{o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv} : float4{};
+      *reinterpret_cast<float4*>(out + (uint64_t)q * kHidden + 4 * c) = y;
+    }
+  }
+}
+
 struct AttnVariant {
   const char* name;
   int waves;
@@ -671,8 +870,13 @@ struct AttnVariant {
 // 86.9 us for index 0).
 const AttnVariant kF16Variants[] = {PK_ATTN_VARIANT(4), PK_ATTN_VARIANT(2), PK_ATTN_VARIANT(1),
                                     PK_ATTN_SHARED_VARIANT(2), PK_ATTN_SHARED_VARIANT(4)};
-const AttnVariant kF32Variant = {"pk_rel_attention_f32", 4, 1, 0, rel_attention_f32_kernel<false>,
-                                 rel_attention_f32_kernel<true>};
+// f32: index 0 the MFMA kernel (planned), index 1 one workgroup per query in
+// the reference's own operation order.
+const AttnVariant kF32Variants[] = {
+    {"pk_rel_attention_f32_mfma", kF32Waves, kTile, (uint32_t)(kF32Waves * 64 * kTile * 4),
+     rel_attention_f32_mfma_kernel<false>, rel_attention_f32_mfma_kernel<true>},
+    {"pk_rel_attention_f32", 4, 1, (uint32_t)((2 * kHead + kAttentionMaxFrames + 8) * 4), rel_attention_f32_kernel<false>,
+     rel_attention_f32_kernel<true>}};
 
 }  // namespace
 
@@ -684,7 +888,8 @@ int attention_default_variant(bool f16, uint32_t frames, uint32_t batch) {
 }
 
 int attention_variant_count(bool f16) {
-  return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0])) : 1;
+  return f16 ? (int)(sizeof(kF16Variants) / sizeof(kF16Variants[0]))
+             : (int)(sizeof(kF32Variants) / sizeof(kF32Variants[0]));
 }
 
 AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t batch) {
@@ -696,12 +901,20 @@ AttnGeometry attention_geometry(bool f16, int variant, uint32_t frames, uint32_t
     g.grid = batch * kHeads * g.query_tiles;
     g.block_threads = 64 * v.waves;
     g.lds_bytes = v.lds_bytes;
+  } else if (variant == 0) {
+    const AttnVariant& v = kF32Variants[0];
+    g.name = v.name;
+    g.query_tiles = (frames + kTile - 1) / kTile;
+    g.grid = (batch * kHeads * g.query_tiles + kF32Waves - 1) / kF32Waves;
+    g.block_threads = 64 * kF32Waves;
+    g.lds_bytes = v.lds_bytes;
   } else {
-    g.name = kF32Variant.name;
+    const AttnVariant& v = kF32Variants[1];
+    g.name = v.name;
     g.query_tiles = frames;
     g.grid = batch * kHeads * frames;
     g.block_threads = 256;
-    g.lds_bytes = (2 * kHead + kAttentionMaxFrames + 8) * 4;
+    g.lds_bytes = v.lds_bytes;
   }
   return g;
 }
@@ -712,7 +925,8 @@ hipError_t launch_attention(bool f16, int variant, const AttnArgs& base, uint32_
   if (g.grid == 0) return hipSuccess;
   AttnArgs args = base;
   args.query_tiles = g.query_tiles;
-  const AttnVariant& v = f16 ? kF16Variants[variant] : kF32Variant;
+  args.work_items = batch * kHeads * g.query_tiles;
+  const AttnVariant& v = f16 ? kF16Variants[variant] : kF32Variants[variant];
   void (*kernel)(AttnArgs) = base.positions_row_major ? v.row_major : v.packed;
   if (start || stop)
     hipExtLaunchKernelGGL(kernel, dim3(g.grid), dim3(g.block_threads), 0, stream, start, stop, 0, args);

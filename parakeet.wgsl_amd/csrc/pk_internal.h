@@ -259,6 +259,7 @@ struct AttnArgs {
   uint32_t position_rows;         // 2 * frames - 1
   int positions_row_major;
   uint32_t query_tiles;           // set by the launcher
+  uint32_t work_items;            // (window, head, query tile) items, set by the launcher
 };
 
 struct AttnGeometry {

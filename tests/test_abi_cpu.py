@@ -356,7 +356,7 @@ def test_attention_null_handles(abi):
     lib = abi.load()
     assert lib.pk_attention_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
     assert lib.pk_attention_destroy(None) == abi.OK
-    assert abi.attention_variant_count("f16") == 5 and abi.attention_variant_count("f32") == 1
+    assert abi.attention_variant_count("f16") == 5 and abi.attention_variant_count("f32") == 2
 
 
 # ---------------------------------------------------------------- LayerNorm

@@ -103,11 +103,31 @@ def test_every_f16_attention_variant_matches(abi, ctx, scope, oracle, workloads)
 
 @pytest.mark.parametrize("batch,frames,valid", [(2, 188, [188, 100]), (2, 23, [0, 40]), (1, 200, [200])])
 def test_f32_attention_matches_oracle(abi, ctx, scope, oracle, workloads, batch, frames, valid):
+    """Both f32 kernels: the planned MFMA flash kernel and the one in the
+    reference's own operation order."""
     case = workloads.attention_case(52 + frames, batch, frames, dtype=np.float32, valid=valid)
+    names = ["pk_rel_attention_f32_mfma", "pk_rel_attention_f32"]
+    assert abi.attention_variant_count("f32") == len(names)
     for row_major in (False, True):
         got, kernel = run_attention(abi, ctx, scope, case, row_major=row_major)
-        assert kernel == "pk_rel_attention_f32"
+        assert kernel == names[0]
         assert_attention_parity(oracle, got, case)
+        for variant, name in enumerate(names):
+            print(f"attention f32 B={batch} T={frames} row_major={row_major} variant {variant}", flush=True)
+            got, kernel = run_attention(abi, ctx, scope, case, row_major=row_major, variant=variant)
+            assert kernel == name
+            assert_attention_parity(oracle, got, case)
+
+
+@pytest.mark.parametrize("batch,frames,valid", [(4, 750, [750, 640, 1, 31]), (3, 64, [64, 33, 32])])
+def test_f32_mfma_attention_long_and_edge_windows(abi, ctx, scope, oracle, workloads, batch, frames, valid):
+    """The MFMA kernel at T = 750 (24 key tiles, 1499 position rows) and at
+    tile edges (valid lengths 1, 31, 32, 33)."""
+    case = workloads.attention_case(56 + frames, batch, frames, dtype=np.float32, valid=valid)
+    print(f"attention f32 mfma B={batch} T={frames}", flush=True)
+    got, kernel = run_attention(abi, ctx, scope, case, row_major=True)
+    assert kernel == "pk_rel_attention_f32_mfma"
+    assert_attention_parity(oracle, got, case)
 
 
 def test_attention_active_batch_prefix(abi, ctx, scope, oracle, workloads):
