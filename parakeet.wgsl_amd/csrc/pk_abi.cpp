@@ -314,6 +314,20 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
       return {pair_variant(1, 2, 2, 4), 1u};
     }
     if (inner >= 2048u) return {tiles(96, 64) <= wave ? pair_variant(1, 3, 2, 4) : pair_variant(2, 3, 2, 2), 1u};
+    // K <= 256 (the subsampling pointwise convolutions, K = N = 256 over
+    // tens of thousands of rows): a workgroup's fixed costs outweigh its K
+    // loop, so the K = 1024 figures below mislead. Measured on one MI355X:
+    // 48,128 rows 17.8 us on one round of 192 x 256 against 20.0 us for
+    // 96 x 128 and 23.7 us for 192 x 128; 192,512 rows 64.0 us for the
+    // 96 x 128 queue against 65.2 us for 192 x 256 and 83.2 us for 192 x 128.
+    if (inner <= 256u) {
+      const uint64_t wide = tiles(192, 256);
+      if (columns >= 256u && 2u * wide > wave && wide <= wave) {
+        const int v = find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, 4, 6, 2, 1);
+        if (v >= 0) return {v, 1u};
+      }
+      if (tiles(96, 128) > wave) return {pair_variant(2, 3, 2, 2), 1u};
+    }
     // K < 2048: the fewest rounds of workgroups times the measured time of one
     // workgroup of each tile at K = 1024 with one workgroup per compute unit.
     struct Candidate {

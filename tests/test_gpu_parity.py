@@ -273,6 +273,31 @@ def test_fp16_gemm_parity(abi, ctx, scope, oracle, workloads, rows, inner, colum
     assert_f16_parity(oracle, got, case)
 
 
+@pytest.mark.parametrize("rows,kernel", [(24768, "pk_gemm_f16p_b5_n4k1_m6n2"), (50000, "pk_gemm_f16p_b5_n2k2_m3n2")])
+def test_subsampling_pointwise_plan(abi, ctx, scope, oracle, workloads, rows, kernel):
+    """K = N = 256 at the subsampling's row counts: one round of 192 x 256
+    tiles, or the 96 x 128 queue beyond a round (on 256 compute units),
+    checked against the oracle on the first, a middle and the last row
+    blocks."""
+    case = workloads.gemm_case(rows, rows, 256, 256, 5, dtype=np.float16, activation="relu", bias=True)
+    w = case.weight
+    out = scope.empty((rows, 256), np.float16)
+    op = abi.GemmOp(ctx, a=scope.put(case.a), packed=scope.put(w.packed), palette=scope.put(w.palette),
+                    output=out, bits=5, rows=rows, inner=256, columns=256, bias=scope.put(case.bias),
+                    activation="relu", label="subsampling-pointwise")
+    try:
+        planned = op.plan().kernel.decode()
+        print(f"pointwise rows={rows} planned {planned}", flush=True)
+        assert planned == kernel
+        op.enqueue()
+        ctx.synchronize()
+        got = out.download()
+    finally:
+        op.release()
+    pick = np.r_[0:400, rows // 2 - 200:rows // 2 + 200, rows - 400:rows]
+    assert_f16_parity(oracle, got[pick], case, rows=pick)
+
+
 @pytest.mark.parametrize("precision", ["f16", "f32"])
 def test_every_tile_variant_matches(abi, ctx, scope, oracle, workloads, precision):
     """Tile shapes with the same K order compute the same sums: every
