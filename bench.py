@@ -93,6 +93,9 @@ def parse_args():
     p.add_argument("--separate-glu", action="store_true",
                    help="encoder workloads: the convolution forms the GLU from PW1's values and gates, as the "
                         "reference does (PK_ENCODER_SEPARATE_GLU; default: PW1's epilogue writes the GLU)")
+    p.add_argument("--post-norms", action="store_true",
+                   help="encoder workloads: each residual GEMM writes the LayerNorm after it "
+                        "(PK_ENCODER_POST_NORMS; default: separate LayerNorm launches)")
     p.add_argument("--unchained-norms", action="store_true",
                    help="encoder workloads: launch every LayerNorm on its own (default: each layer's last "
                         "LayerNorm also writes the next layer's first)")
@@ -401,6 +404,9 @@ WINDOW_SECONDS = 15.0  # audio per encoder window: 1500 fbank frames at 100/s, 8
 
 # The LayerNorms that run inside the GEMM after them with --fused-norms.
 FUSED_NORMS = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2")
+# LayerNorm slot -> the residual GEMM that writes it (PK_GEMM_POST_NORM)
+POST_NORMS = {"norm_self_att": "feed-forward1-linear2-residual", "norm_conv": "self-attention-output-residual",
+              "norm_feed_forward2": "convolution-pointwise2-residual", "norm_out": "feed-forward2-linear2-residual"}
 
 FRONT_DISPATCHES = ("subsampling-fused-conv0-depthwise2", "subsampling-pointwise3", "subsampling-depthwise5",
                     "subsampling-pointwise6", "subsampling-pointwise6-mask", "subsampling-flatten-project")
@@ -543,7 +549,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     stack = wl.encoder_stack(0, windows=args.windows, frames=188, layers=24, front_end=True, projector=True)
     f32 = args.precision == "f32"
     if f32:
-        if decoder or args.fused_norms:
+        if decoder or args.fused_norms or args.post_norms:
             raise SystemExit("--precision f32 runs the encoder workload without the f16-only fusions")
         stack = wl.as_f32_profile(stack)
     active = args.active or stack.batch
@@ -572,12 +578,15 @@ def run_encoder(args, abi, ctx, decoder=False):
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
                         projected_output=projected, fused_norms=args.fused_norms,
-                        unchained_norms=args.unchained_norms, fused_glu=not args.separate_glu, label="encoder",
+                        unchained_norms=args.unchained_norms, post_norms=args.post_norms,
+                        fused_glu=not args.separate_glu, label="encoder",
                         precision=args.precision)
     launches, device_bytes = enc.info()
     fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
     # the LN ff1 of layers after the first runs in the LN out launch before it
     chained = not (args.fused_norms or args.unchained_norms) and len(stack.layers) > 1
+    # the LayerNorms after the residual GEMMs, written by those GEMMs
+    post = args.post_norms
     stream = ctx.stream
     tdt = None
     if decoder:
@@ -641,6 +650,23 @@ def run_encoder(args, abi, ctx, decoder=False):
     dispatches = {}
     for name, ms, (flops, nbytes) in zip(names, per_kind_ms, costs):
         us = ms * 1e3
+        if post and name in POST_NORMS:
+            # written by the residual GEMM before it; the slot's two events are
+            # back to back. That GEMM's bytes gain the LayerNorm's outputs and
+            # parameters (its input is the GEMM's own output): for LN out also
+            # the chained LN ff1 of the next layer, averaged over the layers
+            act = (nbytes - 2 * 4096) / 2
+            extra = act + 2 * 4096
+            if chained and name == "norm_out":
+                n = len(stack.layers)
+                extra = ((n - 1) * 2 * extra + extra) / n
+            gemm = dispatches[POST_NORMS[name]]
+            gemm["algorithmic_bytes"] += extra
+            gemm["gbs"] = gemm["algorithmic_bytes"] / (gemm["avg_us"] * 1e-6) / 1e9
+            gemm["writes_layernorm"] = name
+            dispatches[name] = {"avg_us": us, "written_by": POST_NORMS[name], "flops": 0, "algorithmic_bytes": 0,
+                                "launches_per_pass": 0}
+            continue
         if chained and name == "norm_feed_forward1":
             # layer 0's own launch; later layers' slots are empty (written by norm_out)
             us = durations[nf + list(abi.ENCODER_DISPATCHES).index(name)] * 1e3
@@ -737,10 +763,14 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "palette_bits": {"ff/qkv/pointwise/subsampling/projector": 5, "o_proj": 6},
                    "dispatch_slots_per_pass": launches,
                    "launches_per_pass": launches - len(fused_norms) * len(stack.layers) -
-                                        (len(stack.layers) - 1 if chained else 0),
+                                        (len(stack.layers) - 1 if chained else 0) -
+                                        (len(POST_NORMS) * len(stack.layers) if post else 0),
                    "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
-                                 if args.fused_norms else "separate launches" if not chained else
-                                 "separate launches; each layer's last LayerNorm also writes the next layer's first",
+                                 if args.fused_norms else
+                                 ("the four after the residual GEMMs written by those GEMMs (PK_GEMM_POST_NORM)"
+                                  + ("; each layer's last also writes the next layer's first" if chained else "")
+                                  if post else "separate launches" if not chained else
+                                  "separate launches; each layer's last LayerNorm also writes the next layer's first"),
                    "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu
                           else "in the convolution (the fp32 profile)" if f32 else "in PW1's epilogue",
                    "graph_replay": True,

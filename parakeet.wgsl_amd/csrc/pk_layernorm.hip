@@ -3,7 +3,8 @@
 //
 // mean = sum(x) / C, variance = max(sum(x^2) / C - mean^2, 0),
 // out = (x - mean) * rsqrt(variance + epsilon) * gamma + beta, statistics in
-// f32, output rounded to the storage type. One wavefront per row: each lane
+// f32, output rounded to the storage type (the arithmetic of pk_rownorm.h,
+// which the GEMM's post-norm epilogue shares). One wavefront per row: each lane
 // loads 16-byte vectors (8 f16 or 4 f32 channels; 4 f16 channels when the
 // row length is not a multiple of 8) at a stride of 64 vectors, together
 // with the gamma and beta of those channels, so a row costs one memory round
@@ -16,6 +17,7 @@
 // the same values in the same lane order as a separate launch over the
 // stored output, so both outputs are bit-identical to two launches.
 #include "pk_internal.h"
+#include "pk_rownorm.h"
 
 namespace pk {
 namespace {
@@ -67,37 +69,14 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layernorm_kernel(LayerNorm
   // `x` (and, past those, re-read from `rest`).
   auto statistics = [&](const V (&x)[kHeld], const V* rest) {
     float sum = 0.0f, square = 0.0f;
-    auto accumulate = [&](const V& xv) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        const float xc = (float)xv[c];
-        sum += xc;
-        square = __builtin_fmaf(xc, xc, square);
-      }
-    };
 #pragma unroll
     for (int i = 0; i < kHeld; ++i)
-      if (lane + 64u * i < vectors) accumulate(x[i]);
-    for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) accumulate(rest[v]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      sum += __shfl_xor(sum, off, 64);
-      square += __shfl_xor(square, off, 64);
-    }
-    const float inverse_channels = 1.0f / (float)args.channels;
-    const float mean = sum * inverse_channels;
-    const float variance = fmaxf(square * inverse_channels - mean * mean, 0.0f);
-    return make_float2(mean, 1.0f / __builtin_sqrtf(variance + args.epsilon));
+      if (lane + 64u * i < vectors) rownorm_accumulate<VEC>(x[i], sum, square);
+    for (uint32_t v = lane + 64u * kHeld; v < vectors; v += 64u) rownorm_accumulate<VEC>(rest[v], sum, square);
+    return rownorm_finish(sum, square, args.channels, args.epsilon);
   };
   auto normalize = [&](const V& x, float2 st, const float4 (&g4)[F4], const float4 (&b4)[F4]) {
-    V y;
-#pragma unroll
-    for (int f = 0; f < F4; ++f) {
-      const float gg[4] = {g4[f].x, g4[f].y, g4[f].z, g4[f].w}, bb[4] = {b4[f].x, b4[f].y, b4[f].z, b4[f].w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) y[4 * f + c] = (T)(((float)x[4 * f + c] - st.x) * st.y * gg[c] + bb[c]);
-    }
-    return y;
+    return rownorm_apply<T, VEC>(x, st, g4, b4);
   };
 
   const float2 st = statistics(held, in);
