@@ -87,7 +87,9 @@ int pk_attention_release(pk_attention_op *op);
 /* Tuning hooks: f16 launch shapes - 0..2: one 32-query tile per workgroup
    with 4, 2 or 1 wavefronts splitting the key tiles (planned up to 256
    frames); 3, 4: 2 or 4 wavefronts of 32 queries sharing each staged K, V
-   and position tile (4 planned beyond 256 frames). */
+   and position tile (4 planned beyond 256 frames). f32 - 0: the flash
+   kernel on f32 MFMAs, a wavefront per 32-query tile (planned); 1: one
+   workgroup per query in the reference's own operation order. */
 int pk_attention_variant_count(int precision);
 int pk_attention_set_variant(pk_attention_op *op, int variant);
 
