@@ -124,10 +124,11 @@ def test_f32_mfma_attention_long_and_edge_windows(abi, ctx, scope, oracle, workl
     """The MFMA kernel at T = 750 (24 key tiles, 1499 position rows) and at
     tile edges (valid lengths 1, 31, 32, 33)."""
     case = workloads.attention_case(56 + frames, batch, frames, dtype=np.float32, valid=valid)
-    print(f"attention f32 mfma B={batch} T={frames}", flush=True)
-    got, kernel = run_attention(abi, ctx, scope, case, row_major=True)
-    assert kernel == "pk_rel_attention_f32_mfma"
-    assert_attention_parity(oracle, got, case)
+    for row_major in (True, False):
+        print(f"attention f32 mfma B={batch} T={frames} row_major={row_major}", flush=True)
+        got, kernel = run_attention(abi, ctx, scope, case, row_major=row_major)
+        assert kernel == "pk_rel_attention_f32_mfma"
+        assert_attention_parity(oracle, got, case)
 
 
 def test_attention_active_batch_prefix(abi, ctx, scope, oracle, workloads):
