@@ -114,9 +114,9 @@ typedef enum pk_activation {
    over the stored output rows, and of a chained one. The workgroups that
    share a band of output rows count themselves in as they finish; the
    last one normalises the band, so no workgroup waits for another. f16
-   only; needs N % 8 == 0, N <= 1024, the packed codes or a prepared weight
-   of two or four K parts, no GLU epilogue or row norm, one palette group
-   or groups whose width is a multiple of the tile width, and no split-K
+   only; needs N % 8 == 0, N <= 1024, K % 64 == 0, the packed codes or a
+   prepared weight of two or four K parts, no GLU epilogue or row norm, one
+   palette group or groups of a multiple of 128 columns, and no split-K
    launch. post_output must not overlap the input or the residual and is
    either the output itself or apart from it; post_next_output follows the
    same rule and is apart from post_output. Runs on the pair-code kernels

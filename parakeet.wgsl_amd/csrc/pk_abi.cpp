@@ -569,6 +569,12 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
                   "%s post norm needs f16, N %% 8 == 0, N <= %u, no GLU epilogue or row norm, and codes in two or "
                   "four K parts",
                   label, pk::kPostNormMaxColumns);
+    // The post-norm kernels are the fixed-palette ones: whole 64-deep K
+    // blocks and every tile (64 or 128 columns) inside one palette group.
+    if (d->inner % 64u != 0 || (d->palette_groups != 1 && d->palette_group_columns % 128u != 0))
+      return fail(PK_INVALID_ARGUMENT,
+                  "%s post norm needs K %% 64 == 0 and one palette group or groups of a multiple of 128 columns",
+                  label);
     const uint64_t need = (uint64_t)d->columns * 4u;
     const uint64_t rows_need = (uint64_t)d->rows * d->columns * 2u;
     const uint64_t in_need = (uint64_t)d->rows * d->inner * 2u;

@@ -487,6 +487,10 @@ def test_post_norm_gemm_contract(abi):
     both.norm_gamma, both.norm_gamma_bytes, both.norm_beta, both.norm_beta_bytes = 0x1c000000, 4096, 0x1c100000, 4096
     with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs f16")):
         validate(both)
+    odd_k = _post_norm_desc(abi)
+    odd_k.inner, odd_k.a_bytes, odd_k.packed_bytes = 1056, 96 * 1056 * 2, 1056 * 1024 * 5 // 8
+    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs K % 64 == 0")):
+        validate(odd_k)
     with pytest.raises(abi.PaletteError, match=f"{name} post norm needs gamma and beta of 4096 bytes"):
         validate(_post_norm_desc(abi, gamma_bytes=2048))
     with pytest.raises(abi.PaletteError, match=f"{name} post norm needs gamma and beta of 4096 bytes"):
