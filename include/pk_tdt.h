@@ -18,7 +18,10 @@
  * durations [batch, max_tokens]; metadata [2 * batch] (counts, then status
  * flags, PK_TDT_OVERFLOW when a window had more tokens than max_tokens);
  * state [batch, 4, 640] (committed h0, c0, h1, c1) and predictor scratch
- * [batch, 5, 640] (candidates and the projection), both f32. f16 profile.
+ * [batch, 5, 640] (candidates and the projection), both f32. Both
+ * execution profiles (tdt-decoder.ts:196-218): PK_PRECISION_F16 takes f16
+ * weights and encoder rows with f16 chains, PK_PRECISION_F32 f32 weights and
+ * encoder rows with f32 chains; biases are f32 in both.
  */
 #ifndef PK_TDT_H
 #define PK_TDT_H
@@ -41,17 +44,18 @@ typedef struct pk_tdt_op pk_tdt_op;
 /* The decoder package tensors (model/convert.py:1608-1702), device
    pointers: */
 typedef struct pk_tdt_weights {
-  const void *embedding;         /* f16 [1025, 640] token-by-channel-row-major */
+  /* weights: f16 in the f16 profile, f32 in the f32 profile */
+  const void *embedding;         /* [1025, 640] token-by-channel-row-major */
   uint64_t embedding_bytes;
-  const void *lstm_weight[2];    /* f16 [1280, 2560] input-hidden-k-by-ifgo-row-major-vec4 */
+  const void *lstm_weight[2];    /* [1280, 2560] input-hidden-k-by-ifgo-row-major-vec4 */
   uint64_t lstm_weight_bytes[2];
   const float *lstm_bias[2];     /* f32 [2560] ifgo-gates (input + recurrent bias) */
   uint64_t lstm_bias_bytes[2];
-  const void *projector_weight;  /* f16 [640, 640] k-by-output-row-major-vec4 */
+  const void *projector_weight;  /* [640, 640] k-by-output-row-major-vec4 */
   uint64_t projector_weight_bytes;
   const float *projector_bias;   /* f32 [640] output-channel */
   uint64_t projector_bias_bytes;
-  const void *head_weight;       /* f16 [640, 1032] k-by-output-row-major-vec4 */
+  const void *head_weight;       /* [640, 1032] k-by-output-row-major-vec4 */
   uint64_t head_weight_bytes;
   const float *head_bias;        /* f32 [1032] output-channel-padded-vec4 */
   uint64_t head_bias_bytes;
@@ -60,12 +64,12 @@ typedef struct pk_tdt_weights {
 typedef struct pk_tdt_desc {
   uint32_t struct_size;          /* sizeof(pk_tdt_desc) */
   const char *label;
-  int32_t precision;             /* PK_PRECISION_F16 */
+  int32_t precision;             /* PK_PRECISION_F16 or PK_PRECISION_F32 */
   uint32_t batch_size;
   uint32_t frames;
   uint32_t max_tokens;
   pk_tdt_weights weights;
-  const void *encoder_projected; /* f16 [batch, frames, 640] */
+  const void *encoder_projected; /* [batch, frames, 640], the profile's element */
   uint64_t encoder_projected_bytes;
   const uint32_t *encoded_lengths; /* [batch] */
   uint64_t encoded_lengths_bytes;
@@ -108,6 +112,8 @@ int pk_tdt_enqueue_timed(pk_tdt_op *op, uint32_t active_batch, void *stream, voi
    every weight matrix over a team that meets at barriers in global memory
    (bounded waits: a barrier that never completes sets the window's
    PK_TDT_SYNC_TIMEOUT status). Results are bit-identical for every size.
+   Teams are built for the f16 profile: an f32 op always runs one
+   workgroup per window (0 chooses 1; 8 and 16 return PK_RANGE_ERROR).
    The create call chooses automatically; the setter synchronizes the
    device. A team launch that the runtime refuses returns PK_DEVICE_ERROR
    and leaves the team size as it was. */

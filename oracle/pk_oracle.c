@@ -926,18 +926,35 @@ static float tdt_sigmoid(float v) {
 /* tanh(clamp(v, -10, 10)) (tdt-decoder.ts:1318-1322). */
 static float tdt_tanh(float v) { return pko_tanh_f32(fminf(fmaxf(v, -10.0f), 10.0f)); }
 
-/* The decoder's f16 weights widened to double once per call. */
+/* The decoder's weights widened to double once per call (exact for f16 and
+   f32 values); f32 selects the f32 profile's chains. */
 typedef struct tdt_dense {
   double *embedding, *lstm[2], *projector, *head;
   const float *lstm_bias[2], *projector_bias, *head_bias;
+  int f32;
 } tdt_dense;
 
-static double *widen16(const uint16_t *src, uint64_t count) {
+static double *widen(const void *src, uint64_t count, int f32) {
   double *out = (double *)malloc(sizeof(double) * count);
   if (out)
-    for (uint64_t i = 0; i < count; ++i) out[i] = pko_f16_to_f64(src[i]);
+    for (uint64_t i = 0; i < count; ++i)
+      out[i] = f32 ? (double)((const float *)src)[i] : pko_f16_to_f64(((const uint16_t *)src)[i]);
   return out;
 }
+
+/* Element i of a row in the profile's element, as a double. */
+static double tdt_element(const void *row, uint64_t i, int f32) {
+  return f32 ? (double)((const float *)row)[i] : pko_f16_to_f64(((const uint16_t *)row)[i]);
+}
+
+/* One step of a chain: fma with one rounding in the profile's format. */
+static double tdt_fma(double a, double b, double c, int f32) {
+  return f32 ? (double)fmaf((float)a, (float)b, (float)c) : fma16(a, b, c);
+}
+
+/* A chain input or a bias as the chain sees it (rounded to f16 in the f16
+   profile, the f32 value in the f32 profile). */
+static double tdt_input(float v, int f32) { return f32 ? (double)v : pko_round_f16((double)v); }
 
 static void tdt_dense_free(tdt_dense *d) {
   free(d->embedding);
@@ -950,11 +967,13 @@ static void tdt_dense_free(tdt_dense *d) {
 static int tdt_dense_make(const pko_tdt_weights *w, tdt_dense *d) {
   const uint64_t H = PKO_TDT_HIDDEN;
   memset(d, 0, sizeof *d);
-  d->embedding = widen16(w->embedding, (uint64_t)PKO_TDT_TOKENS * H);
-  d->lstm[0] = widen16(w->lstm_weight[0], 2 * H * PKO_TDT_GATES);
-  d->lstm[1] = widen16(w->lstm_weight[1], 2 * H * PKO_TDT_GATES);
-  d->projector = widen16(w->projector_weight, H * H);
-  d->head = widen16(w->head_weight, H * PKO_TDT_HEAD);
+  const int f32 = w->f32 != 0;
+  d->f32 = f32;
+  d->embedding = widen(w->embedding, (uint64_t)PKO_TDT_TOKENS * H, f32);
+  d->lstm[0] = widen(w->lstm_weight[0], 2 * H * PKO_TDT_GATES, f32);
+  d->lstm[1] = widen(w->lstm_weight[1], 2 * H * PKO_TDT_GATES, f32);
+  d->projector = widen(w->projector_weight, H * H, f32);
+  d->head = widen(w->head_weight, H * PKO_TDT_HEAD, f32);
   d->lstm_bias[0] = w->lstm_bias[0];
   d->lstm_bias[1] = w->lstm_bias[1];
   d->projector_bias = w->projector_bias;
@@ -966,25 +985,29 @@ static int tdt_dense_make(const pko_tdt_weights *w, tdt_dense *d) {
   return 0;
 }
 
-/* One LSTM layer's gates (tdt-decoder.ts:1341-1382, accumulators :572-686):
-   per gate an f16 chain over even k starting at f16(bias) and one over odd k
-   starting at 0, fma in increasing k, added in f16. x[k] is the f16 input of
-   row k; `limit` rows are used (0: none). */
-static void tdt_gates(const double *weight, const float *bias, const double *x, uint32_t limit, float *gates) {
+/* One LSTM layer's gates (tdt-decoder.ts:1341-1382, accumulators :572-686
+   in f16, :595-614 and :642-666 in f32): per gate a chain over even k
+   starting at the bias and one over odd k starting at 0, fma in increasing
+   k, the two added at the end, all in the profile's format (the bias
+   rounded to f16 in the f16 profile). x[k] is the chain input of row k;
+   `limit` rows are used (0: none). */
+static void tdt_gates(const double *weight, const float *bias, const double *x, uint32_t limit, float *gates,
+                      int f32) {
   double even[PKO_TDT_GATES], odd[PKO_TDT_GATES];
   for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) {
-    even[j] = pko_round_f16((double)bias[j]);
+    even[j] = tdt_input(bias[j], f32);
     odd[j] = 0.0;
   }
   for (uint32_t k = 0; k < limit; k += 2) {
     const double *we = weight + (uint64_t)k * PKO_TDT_GATES, *wo = we + PKO_TDT_GATES;
     const double xe = x[k], xo = x[k + 1];
     for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) {
-      even[j] = fma16(xe, we[j], even[j]);
-      odd[j] = fma16(xo, wo[j], odd[j]);
+      even[j] = tdt_fma(xe, we[j], even[j], f32);
+      odd[j] = tdt_fma(xo, wo[j], odd[j], f32);
     }
   }
-  for (uint32_t j = 0; j < PKO_TDT_GATES; ++j) gates[j] = (float)pko_round_f16(even[j] + odd[j]);
+  for (uint32_t j = 0; j < PKO_TDT_GATES; ++j)
+    gates[j] = f32 ? (float)even[j] + (float)odd[j] : (float)pko_round_f16(even[j] + odd[j]);
 }
 
 /* Cell update (tdt-decoder.ts:1384-1410) into h, c. */
@@ -1004,19 +1027,20 @@ static void tdt_predictor(const tdt_dense *w, uint32_t token, int initial, const
   const uint32_t H = PKO_TDT_HIDDEN;
   double x[2 * PKO_TDT_HIDDEN];
   float gates[PKO_TDT_GATES];
+  const int f32 = w->f32;
   /* layer 0: [embedding(token); h0], skipped for the start token (zero x, h) */
   for (uint32_t k = 0; k < H; ++k) {
     x[k] = initial ? 0.0 : w->embedding[(uint64_t)token * H + k];
-    x[H + k] = pko_round_f16((double)state[k]);
+    x[H + k] = tdt_input(state[k], f32);
   }
-  tdt_gates(w->lstm[0], w->lstm_bias[0], x, initial ? 0 : 2 * H, gates);
+  tdt_gates(w->lstm[0], w->lstm_bias[0], x, initial ? 0 : 2 * H, gates, f32);
   tdt_cell(gates, state + H, cand, cand + H);
   /* layer 1: [candidate h0; h1]; the start token uses candidate h0 only */
   for (uint32_t k = 0; k < H; ++k) {
-    x[k] = pko_round_f16((double)cand[k]);
-    x[H + k] = pko_round_f16((double)state[2 * H + k]);
+    x[k] = tdt_input(cand[k], f32);
+    x[H + k] = tdt_input(state[2 * H + k], f32);
   }
-  tdt_gates(w->lstm[1], w->lstm_bias[1], x, initial ? H : 2 * H, gates);
+  tdt_gates(w->lstm[1], w->lstm_bias[1], x, initial ? H : 2 * H, gates, f32);
   tdt_cell(gates, state + 3 * H, cand + 2 * H, cand + 3 * H);
   /* decoder projector in f32 (tdt-decoder.ts:1462-1491) */
   for (uint32_t o = 0; o < H; ++o) {
@@ -1028,18 +1052,20 @@ static void tdt_predictor(const tdt_dense *w, uint32_t token, int initial, const
 
 static float sanitize_score(float v) { return v != v ? -3.402823466e+38f : v; }
 
-static void tdt_joint(const tdt_dense *w, const uint16_t *encoder_row, const float *projection, float *scores,
+static void tdt_joint(const tdt_dense *w, const void *encoder_row, const float *projection, float *scores,
                       uint32_t *token, uint32_t *duration) {
   const uint32_t H = PKO_TDT_HIDDEN;
+  const int f32 = w->f32;
   double acc[PKO_TDT_HEAD];
   float joint[PKO_TDT_HIDDEN];
   for (uint32_t c = 0; c < H; ++c) {
-    const float v = (float)pko_f16_to_f64(encoder_row[c]) + projection[c];
+    const float v = (float)tdt_element(encoder_row, c, f32) + projection[c];
     joint[c] = v > 0.0f ? v : 0.0f; /* max(v, 0) */
   }
-  for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = pko_round_f16((double)w->head_bias[o]);
-  /* f16 chains in increasing k; exact +0 inputs skipped until a -0 or NaN
-     input has been seen (tdt-decoder.ts:977-1031) */
+  for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = tdt_input(w->head_bias[o], f32);
+  /* chains in increasing k in the profile's format; exact +0 inputs skipped
+     until a -0 or NaN input has been seen (tdt-decoder.ts:977-1031 in f16,
+     :877-919 and :1033-1058 in f32) */
   int zero_skip_safe = 1;
   for (uint32_t k = 0; k < H; ++k) {
     uint32_t bits;
@@ -1048,9 +1074,9 @@ static void tdt_joint(const tdt_dense *w, const uint16_t *encoder_row, const flo
     const int exceptional = bits == 0x80000000u || is_nan;
     zero_skip_safe = zero_skip_safe && !exceptional;
     if (zero_skip_safe && bits == 0u) continue;
-    const double x = pko_round_f16((double)joint[k]);
+    const double x = tdt_input(joint[k], f32);
     const double *row = w->head + (uint64_t)k * PKO_TDT_HEAD;
-    for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = fma16(x, row[o], acc[o]);
+    for (uint32_t o = 0; o < PKO_TDT_HEAD; ++o) acc[o] = tdt_fma(x, row[o], acc[o], f32);
   }
   /* argmax over tokens and blank, then over durations: the largest value,
      the lowest id among equal values (choose_better, :1517-1525) */
@@ -1083,7 +1109,7 @@ void pko_tdt_predictor(const pko_tdt_weights *w, uint32_t token, int initial, co
   tdt_dense_free(&d);
 }
 
-void pko_tdt_joint(const pko_tdt_weights *w, const uint16_t *encoder_row, const float *projection, float *scores,
+void pko_tdt_joint(const pko_tdt_weights *w, const void *encoder_row, const float *projection, float *scores,
                    uint32_t *token, uint32_t *duration) {
   tdt_dense d;
   if (tdt_dense_make(w, &d)) return;
@@ -1094,7 +1120,7 @@ void pko_tdt_joint(const pko_tdt_weights *w, const uint16_t *encoder_row, const 
 typedef struct tdt_job {
   const tdt_dense *w;
   uint32_t b, frames, max_tokens;
-  const uint16_t *encoder_projected;
+  const void *encoder_projected;
   const uint32_t *lengths, *starts, *ends, *flush;
   float *state_all, *scratch_all;
   uint32_t *tokens, *token_frames, *token_durations, *counts, *status;
@@ -1106,7 +1132,8 @@ static void tdt_decode_window(const tdt_job *j) {
   const tdt_dense *w = j->w;
   float *state = j->state_all + (uint64_t)b * 4 * H;
   float *cand = j->scratch_all + (uint64_t)b * 5 * H;
-  const uint16_t *enc = j->encoder_projected + (uint64_t)b * frames * H;
+  const size_t element = w->f32 ? 4 : 2;
+  const unsigned char *enc = (const unsigned char *)j->encoder_projected + (uint64_t)b * frames * H * element;
   memset(state, 0, sizeof(float) * 4 * H);
   uint32_t count = 0, st = 0, symbols = 0;
   const uint32_t limit = j->lengths[b] < frames ? j->lengths[b] : frames;
@@ -1133,7 +1160,7 @@ static void tdt_decode_window(const tdt_job *j) {
     tdt_predictor(w, token, 0, state, cand);       \
   } while (0)
   while (time < encoded) {
-    tdt_joint(w, enc + (uint64_t)time * H, cand + 4 * H, NULL, &token, &duration);
+    tdt_joint(w, enc + (uint64_t)time * H * element, cand + 4 * H, NULL, &token, &duration);
     const int emitted = token != PKO_TDT_BLANK;
     if (emitted) TDT_EMIT(time);
     symbols += 1;
@@ -1161,7 +1188,7 @@ static void tdt_decode_window(const tdt_job *j) {
         const uint32_t m = (encoded > 2u ? encoded : 2u) - 2u;
         time = m < frames - 1u ? m : frames - 1u;
       }
-      tdt_joint(w, enc + (uint64_t)time * H, cand + 4 * H, NULL, &token, &duration);
+      tdt_joint(w, enc + (uint64_t)time * H * element, cand + 4 * H, NULL, &token, &duration);
       const int emitted = token != PKO_TDT_BLANK;
       if (!emitted) {
         flush_blanks += 1;
@@ -1187,7 +1214,7 @@ static void *tdt_worker(void *opaque) {
 }
 
 int pko_tdt_decode(const pko_tdt_weights *w, uint32_t batch, uint32_t frames, uint32_t max_tokens,
-                   const uint16_t *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
+                   const void *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
                    const uint32_t *ends, const uint32_t *flush, float *state_all, float *scratch_all,
                    uint32_t *tokens, uint32_t *token_frames, uint32_t *token_durations, uint32_t *counts,
                    uint32_t *status) {

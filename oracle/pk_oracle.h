@@ -63,9 +63,10 @@
  *                         torch's conv2d in float64, one-hot kernels and the
  *                         length edges in tests/test_oracle.py.
  *   pko_tdt_decode        src/webgpu/kernels/tdt-decoder.ts:1133-2010 (greedy TDT
- *                         decode: two-layer LSTM predictor with f16 gate chains,
- *                         f32 cell update, f32 decoder projector, ReLU joint, f16
- *                         vocabulary head, lowest-id argmax, durations, the
+ *                         decode: two-layer LSTM predictor with gate chains in
+ *                         the profile's format (f16 or f32), f32 cell update,
+ *                         f32 decoder projector, ReLU joint, vocabulary head in
+ *                         the profile's format, lowest-id argmax, durations, the
  *                         10-symbol cap and the bounded end-of-stream flush);
  *                         pinned by closed forms (zero-weight heads that fix the
  *                         token and duration), torch.nn.LSTM / matmul restatements
@@ -240,22 +241,28 @@ float pko_exp_f32(float x);
 float pko_tanh_f32(float x);
 
 typedef struct pko_tdt_weights {
-  const uint16_t *embedding;       /* f16 [1025, 640] token-by-channel */
-  const uint16_t *lstm_weight[2];  /* f16 [1280, 2560] k-by-ifgo (k < 640: input, k >= 640: recurrent h) */
+  /* weights: f16 (uint16_t bits) in the f16 profile, f32 when f32 != 0 */
+  const void *embedding;           /* [1025, 640] token-by-channel */
+  const void *lstm_weight[2];      /* [1280, 2560] k-by-ifgo (k < 640: input, k >= 640: recurrent h) */
   const float *lstm_bias[2];       /* f32 [2560] (bias_ih + bias_hh) */
-  const uint16_t *projector_weight;/* f16 [640, 640] k-by-output */
+  const void *projector_weight;    /* [640, 640] k-by-output */
   const float *projector_bias;     /* f32 [640] */
-  const uint16_t *head_weight;     /* f16 [640, 1032] k-by-output (1030 used) */
+  const void *head_weight;         /* [640, 1032] k-by-output (1030 used) */
   const float *head_bias;          /* f32 [1032] */
+  int32_t f32;                     /* 0: f16 profile, 1: f32 profile (tdt-decoder.ts:196-218) */
 } pko_tdt_weights;
 
-/* Greedy TDT decode of `batch` windows (tdt-decoder.ts:1664-2010), f16
-   profile: encoder_projected f16 [batch, frames, 640]; lengths, starts, ends,
-   flush [batch]; outputs tokens / token_frames / token_durations [batch,
-   max_tokens], counts and status [batch]. state f32 [batch, 4, 640] and
-   scratch f32 [batch, 5, 640] are working memory (written). */
+/* Greedy TDT decode of `batch` windows (tdt-decoder.ts:1664-2010):
+   encoder_projected [batch, frames, 640] in the profile's element (f16 bits
+   or f32); lengths, starts, ends, flush [batch]; outputs tokens /
+   token_frames / token_durations [batch, max_tokens], counts and status
+   [batch]. state f32 [batch, 4, 640] and scratch f32 [batch, 5, 640] are
+   working memory (written). The f16 profile runs every chain in binary16
+   (inputs and biases rounded to f16), the f32 profile in binary32 with
+   nothing rounded (the f32 readers and chains, :595-614, :700-716,
+   :1033-1058, :1092-1104). */
 int pko_tdt_decode(const pko_tdt_weights *w, uint32_t batch, uint32_t frames, uint32_t max_tokens,
-                   const uint16_t *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
+                   const void *encoder_projected, const uint32_t *lengths, const uint32_t *starts,
                    const uint32_t *ends, const uint32_t *flush, float *state, float *scratch, uint32_t *tokens,
                    uint32_t *token_frames, uint32_t *token_durations, uint32_t *counts, uint32_t *status);
 
@@ -263,10 +270,11 @@ int pko_tdt_decode(const pko_tdt_weights *w, uint32_t batch, uint32_t frames, ui
    (ignored when initial) and the committed state [4, 640] (h0, c0, h1, c1)
    to the candidates [5, 640] (h0, c0, h1, c1, projection). */
 void pko_tdt_predictor(const pko_tdt_weights *w, uint32_t token, int initial, const float *state, float *candidate);
-/* One joint: scores [1032] (f32 values of the f16 accumulators) of
-   relu(encoder_row + projection) through the head; returns the chosen token
-   and duration through `token` / `duration`. */
-void pko_tdt_joint(const pko_tdt_weights *w, const uint16_t *encoder_row, const float *projection, float *scores,
+/* One joint: scores [1032] (f32 values of the head accumulators) of
+   relu(encoder_row + projection) through the head (encoder_row in the
+   profile's element); returns the chosen token and duration through
+   `token` / `duration`. */
+void pko_tdt_joint(const pko_tdt_weights *w, const void *encoder_row, const float *projection, float *scores,
                    uint32_t *token, uint32_t *duration);
 
 #ifdef __cplusplus

@@ -440,19 +440,23 @@ TDT_HIDDEN, TDT_GATES, TDT_HEAD, TDT_BLANK = 640, 2560, 1032, 1024
 class _TdtWeights(ctypes.Structure):
     _fields_ = [("embedding", ctypes.c_void_p), ("lstm_weight", ctypes.c_void_p * 2),
                 ("lstm_bias", ctypes.c_void_p * 2), ("projector_weight", ctypes.c_void_p),
-                ("projector_bias", ctypes.c_void_p), ("head_weight", ctypes.c_void_p), ("head_bias", ctypes.c_void_p)]
+                ("projector_bias", ctypes.c_void_p), ("head_weight", ctypes.c_void_p), ("head_bias", ctypes.c_void_p),
+                ("f32", ctypes.c_int32)]
 
 
 def _tdt_weights(weights: dict):
-    """(struct, keep-alive list) from a dict keyed like the decoder package:
-    embedding f16 [1025, 640], lstm_weight_l0/_l1 f16 [1280, 2560],
-    lstm_bias_l0/_l1 f32 [2560], projector_weight f16 [640, 640],
-    projector_bias f32 [640], head_weight f16 [640, 1032], head_bias f32 [1032]."""
+    """(struct, keep-alive list, element dtype) from a dict keyed like the
+    decoder package: embedding [1025, 640], lstm_weight_l0/_l1 [1280, 2560],
+    lstm_bias_l0/_l1 f32 [2560], projector_weight [640, 640], projector_bias
+    f32 [640], head_weight [640, 1032], head_bias f32 [1032]. The weights are
+    all f16 (the f16 profile) or all f32 (the f32 profile), which the
+    embedding's dtype selects (tdt-decoder.ts:196-218, :378-405)."""
     keep = {k: np.ascontiguousarray(v) for k, v in weights.items()}
-    expect = {"embedding": (np.float16, (1025, 640)), "lstm_weight_l0": (np.float16, (1280, 2560)),
-              "lstm_weight_l1": (np.float16, (1280, 2560)), "lstm_bias_l0": (np.float32, (2560,)),
-              "lstm_bias_l1": (np.float32, (2560,)), "projector_weight": (np.float16, (640, 640)),
-              "projector_bias": (np.float32, (640,)), "head_weight": (np.float16, (640, 1032)),
+    wt = np.float32 if keep["embedding"].dtype == np.float32 else np.float16
+    expect = {"embedding": (wt, (1025, 640)), "lstm_weight_l0": (wt, (1280, 2560)),
+              "lstm_weight_l1": (wt, (1280, 2560)), "lstm_bias_l0": (np.float32, (2560,)),
+              "lstm_bias_l1": (np.float32, (2560,)), "projector_weight": (wt, (640, 640)),
+              "projector_bias": (np.float32, (640,)), "head_weight": (wt, (640, 1032)),
               "head_bias": (np.float32, (1032,))}
     for name, (dtype, shape) in expect.items():
         if keep[name].dtype != dtype or keep[name].shape != shape:
@@ -461,8 +465,8 @@ def _tdt_weights(weights: dict):
                                                                     _ptr(keep["lstm_weight_l1"])),
                     (ctypes.c_void_p * 2)(_ptr(keep["lstm_bias_l0"]), _ptr(keep["lstm_bias_l1"])),
                     _ptr(keep["projector_weight"]), _ptr(keep["projector_bias"]), _ptr(keep["head_weight"]),
-                    _ptr(keep["head_bias"]))
-    return w, keep
+                    _ptr(keep["head_bias"]), int(wt == np.float32))
+    return w, keep, wt
 
 
 def exp_f32(x: float) -> float:
@@ -476,7 +480,7 @@ def tanh_f32(x: float) -> float:
 def tdt_predictor(weights: dict, token: int, state, initial: bool = False) -> np.ndarray:
     """Candidates [5, 640] (h0, c0, h1, c1, projection) of one predictor step
     from the committed state [4, 640] (tdt-decoder.ts:1341-1500)."""
-    w, keep = _tdt_weights(weights)
+    w, keep, _ = _tdt_weights(weights)
     state = np.ascontiguousarray(state, dtype=np.float32).reshape(4, TDT_HIDDEN)
     cand = np.empty((5, TDT_HIDDEN), dtype=np.float32)
     lib().pko_tdt_predictor(ctypes.byref(w), int(token), int(initial), _ptr(state), _ptr(cand))
@@ -484,9 +488,10 @@ def tdt_predictor(weights: dict, token: int, state, initial: bool = False) -> np
 
 
 def tdt_joint(weights: dict, encoder_row, projection):
-    """(scores [1032], token, duration) of one joint (tdt-decoder.ts:1605-1662)."""
-    w, keep = _tdt_weights(weights)
-    encoder_row = np.ascontiguousarray(encoder_row, dtype=np.float16)
+    """(scores [1032], token, duration) of one joint (tdt-decoder.ts:1605-1662);
+    encoder_row in the weights' element type."""
+    w, keep, wt = _tdt_weights(weights)
+    encoder_row = np.ascontiguousarray(encoder_row, dtype=wt)
     projection = np.ascontiguousarray(projection, dtype=np.float32)
     scores = np.empty(TDT_HEAD, dtype=np.float32)
     token, duration = ctypes.c_uint32(), ctypes.c_uint32()
@@ -496,12 +501,13 @@ def tdt_joint(weights: dict, encoder_row, projection):
 
 
 def tdt_decode(weights: dict, encoder_projected, lengths, *, max_tokens: int, starts=None, ends=None, flush=None):
-    """Greedy TDT decode (tdt-decoder.ts:1664-2010) of encoder_projected f16
-    [batch, frames, 640]; returns dict(tokens, frames, durations [batch,
+    """Greedy TDT decode (tdt-decoder.ts:1664-2010) of encoder_projected
+    [batch, frames, 640] in the weights' element type (f16 or f32 profile);
+    returns dict(tokens, frames, durations [batch,
     max_tokens] u32, counts, status [batch], and the final state [batch, 4,
     640] and predictor scratch [batch, 5, 640])."""
-    w, keep = _tdt_weights(weights)
-    enc = np.ascontiguousarray(encoder_projected, dtype=np.float16)
+    w, keep, wt = _tdt_weights(weights)
+    enc = np.ascontiguousarray(encoder_projected, dtype=wt)
     batch, frames, hidden = enc.shape
     if hidden != TDT_HIDDEN:
         raise ValueError("encoder_projected must be [batch, frames, 640]")

@@ -1436,7 +1436,8 @@ static void tdt_finalize(napi_env env, void *data, void *hint) {
   pk_tdt_release((pk_tdt_op *)data);
 }
 
-/* {label, batchSize, frames, maxTokens, weights: {embedding, lstmWeight0,
+/* {label, precision? ("f16" default, or "f32": the fp32 profile), batchSize,
+   frames, maxTokens, weights: {embedding, lstmWeight0,
    lstmWeight1, lstmBias0, lstmBias1, projectorWeight, projectorBias,
    headWeight, headBias}, encoderProjected, encodedLengths, decodeStarts,
    decodeEnds, flushFinals, state, predictorScratch, tokens, tokenFrames,
@@ -1445,6 +1446,7 @@ static int parse_tdt_desc(napi_env env, napi_value o, pk_tdt_desc *d, char **lab
   memset(d, 0, sizeof *d);
   d->struct_size = sizeof *d;
   d->precision = PK_PRECISION_F16;
+  parse_precision(env, o, &d->precision);
   *label = NULL;
   napi_value w;
   const void *p = NULL;

@@ -355,14 +355,16 @@ constexpr uint32_t kTdtHead = 1032;
 constexpr uint32_t kTdtBlank = 1024;
 constexpr uint32_t kTdtThreads = 640;
 struct TdtArgs {
-  const _Float16* embedding;     // [1025, 640]
-  const _Float16* lstm[2];       // [1280, 2560] k by ifgo
+  // Weights and encoder rows are f16 in the f16 profile and f32 in the f32
+  // profile (launch_tdt_decode's `f32`); biases, state and scratch are f32.
+  const void* embedding;         // [1025, 640]
+  const void* lstm[2];           // [1280, 2560] k by ifgo
   const float* lstm_bias[2];     // [2560]
-  const _Float16* projector;     // [640, 640] k by output
+  const void* projector;         // [640, 640] k by output
   const float* projector_bias;   // [640]
-  const _Float16* head;          // [640, 1032] k by output
+  const void* head;              // [640, 1032] k by output
   const float* head_bias;        // [1032]
-  const _Float16* encoder;       // [batch, frames, 640]
+  const void* encoder;           // [batch, frames, 640]
   const uint32_t *lengths, *starts, *ends, *flush;  // [batch]
   float* state;                  // [batch, 4, 640]: h0, c0, h1, c1
   float* scratch;                // [batch, 5, 640]: candidates and projection
@@ -370,11 +372,13 @@ struct TdtArgs {
   uint32_t *counts, *status;     // [batch]
   uint32_t frames, max_tokens;
 };
-hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t stream, hipEvent_t start = nullptr,
-                             hipEvent_t stop = nullptr);
-// Team decoding: `members` workgroups of kTdtTeamThreads per window, each
-// streaming one slice of every weight matrix, meeting at bounded barriers
-// in global memory; launched cooperatively so every member is resident.
+// One workgroup per window; `f32` selects the f32 profile's kernel.
+hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, bool f32, hipStream_t stream,
+                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Team decoding (f16 profile): `members` workgroups of kTdtTeamThreads per
+// window, each streaming one slice of every weight matrix, meeting at
+// bounded barriers in global memory; an ordinary launch whose grid fits the
+// workgroups the device holds at once.
 constexpr uint32_t kTdtTeamThreads = 256;
 constexpr uint32_t kTdtSyncTimeout = 2u;  // status bit: a team barrier gave up waiting
 constexpr uint32_t kTdtSyncStride = 64;   // u32 words between barrier counters (256 bytes)

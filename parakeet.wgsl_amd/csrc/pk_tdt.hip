@@ -9,15 +9,22 @@
 // without leaving the kernel. The predictor runs only after a non-blank
 // emission, as in the reference.
 //
-// Arithmetic is the shader's, term for term: every gate is an f16 chain
-// over even rows starting at f16(bias) plus one over odd rows starting at
-// zero, fma in increasing k (v_pk_fma_f16, one rounding), added in f16; the
-// head is an f16 chain over k skipping exact +0 joint inputs until a -0 or
-// NaN input is seen; the projector is an f32 fma chain; the cell update and
-// the activations are f32 with exp written out (range reduction and a
-// degree-7 Taylor polynomial) rather than taken from a library, so the
-// decode is reproducible to the bit. Contraction is off in this file: every
-// fused multiply-add is written as one.
+// Arithmetic is the shader's, term for term, in both execution profiles
+// (tdt-decoder.ts:1155-1190 picks the readers and chains by precision):
+// every gate is a chain over even rows starting at the bias plus one over
+// odd rows starting at zero, fma in increasing k (one rounding each), the
+// two added at the end; the head is a chain over k skipping exact +0 joint
+// inputs until a -0 or NaN input is seen; the projector is an f32 fma chain;
+// the cell update and the activations are f32 with exp written out (range
+// reduction and a degree-7 Taylor polynomial) rather than taken from a
+// library, so the decode is reproducible to the bit. In the f16 profile
+// (weights, encoder rows and chains in f16: v_pk_fma_f16) the chain inputs
+// and the biases are rounded to f16 (:572-666, :687-742, :977-1031); in the
+// f32 profile (f32 weights and encoder rows, :595-614, :642-666, :700-716,
+// :743-771, :1033-1058) every chain is f32 and nothing is rounded. The
+// kernels are templates over the profile (`ProfileF16`, `ProfileF32`).
+// Contraction is off in this file: every fused multiply-add is written as
+// one.
 #include "pk_internal.h"
 
 #pragma clang fp contract(off)
@@ -26,6 +33,27 @@ namespace pk {
 namespace {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+// W: weight and encoder-row element; W4: four weights (one 8- or 16-byte
+// load); X: a chain input as staged in LDS; A4: four chain accumulators.
+struct ProfileF16 {
+  typedef _Float16 W;
+  typedef half4 W4;
+  typedef _Float16 X;
+  typedef half4 A4;
+};
+struct ProfileF32 {
+  typedef float W;
+  typedef float4v W4;
+  typedef float X;
+  typedef float4v A4;
+};
+
+template <class P>
+__device__ __forceinline__ const typename P::W* wptr(const void* p) {
+  return static_cast<const typename P::W*>(p);
+}
 
 constexpr uint32_t H = kTdtHidden;
 constexpr uint32_t kThreads = kTdtThreads;
@@ -63,15 +91,30 @@ __device__ __forceinline__ float sigmoid_f32(float v) {
 
 __device__ __forceinline__ float clamped_tanh(float v) { return tanh_f32(fminf(fmaxf(v, -10.0f), 10.0f)); }
 
-__device__ __forceinline__ half4 splat(_Float16 x) { return half4{x, x, x, x}; }
+template <class V, class S>
+__device__ __forceinline__ V splat(S x) {
+  return V{x, x, x, x};
+}
 
-__device__ __forceinline__ half4 load_half4(const _Float16* p) { return *reinterpret_cast<const half4*>(p); }
+template <class V, class S>
+__device__ __forceinline__ V load4(const S* p) {
+  return *reinterpret_cast<const V*>(p);
+}
 
+// Four f32 biases as chain accumulators (rounded to f16 in that profile).
+template <class A4>
+__device__ __forceinline__ A4 bias4(const float* p) {
+  const float4 b = *reinterpret_cast<const float4*>(p);
+  typedef decltype(A4{}[0]) E;
+  return A4{(E)b.x, (E)b.y, (E)b.z, (E)b.w};
+}
+
+template <class P>
 struct Shared {
-  _Float16 x[2 * H];      // LSTM layer inputs (f16)
-  float gates[kTdtGates]; // f32 values of the f16 gate sums
+  typename P::X x[2 * H]; // LSTM layer inputs
+  float gates[kTdtGates]; // f32 values of the gate sums
   float joint[H];         // relu(encoder + projection)
-  float scores[kTdtHead]; // f32 values of the f16 head accumulators
+  float scores[kTdtHead]; // f32 values of the head accumulators
   bool use[H];            // head row k enters the chain (the +0-skip rule)
   // control, written by thread 0
   uint32_t go, emitted, token, duration, joint_time, first_bad;
@@ -83,29 +126,32 @@ constexpr uint32_t kBatchRows = 16;
 
 // Gates of one LSTM layer: thread t owns gates 4t..4t+3 over `limit` rows
 // (a multiple of kBatchRows).
-__device__ void lstm_gates(Shared& s, const _Float16* weight, const float* bias, uint32_t limit) {
+template <class P>
+__device__ void lstm_gates(Shared<P>& s, const void* weight, const float* bias, uint32_t limit) {
+  typedef typename P::A4 A4;
+  typedef typename P::W4 W4;
   const uint32_t t = threadIdx.x;
-  const float4 b = *reinterpret_cast<const float4*>(bias + 4 * t);
-  half4 even = half4{(_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-  half4 odd = half4{0, 0, 0, 0};
-  const _Float16* column = weight + 4 * t;
+  A4 even = bias4<A4>(bias + 4 * t);
+  A4 odd = A4{0, 0, 0, 0};
+  const typename P::W* column = wptr<P>(weight) + 4 * t;
   for (uint32_t k0 = 0; k0 < limit; k0 += kBatchRows) {
-    half4 w[kBatchRows];
+    W4 w[kBatchRows];
 #pragma unroll
-    for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(column + (uint64_t)(k0 + r) * kTdtGates);
+    for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load4<W4>(column + (uint64_t)(k0 + r) * kTdtGates);
 #pragma unroll
     for (uint32_t r = 0; r < kBatchRows; r += 2) {
-      even = __builtin_elementwise_fma(splat(s.x[k0 + r]), w[r], even);
-      odd = __builtin_elementwise_fma(splat(s.x[k0 + r + 1]), w[r + 1], odd);
+      even = __builtin_elementwise_fma(splat<A4>(s.x[k0 + r]), w[r], even);
+      odd = __builtin_elementwise_fma(splat<A4>(s.x[k0 + r + 1]), w[r + 1], odd);
     }
   }
-  const half4 sum = even + odd;
+  const A4 sum = even + odd;
   for (int i = 0; i < 4; ++i) s.gates[4 * t + i] = (float)sum[i];
 }
 
 // Cell update of one layer (threads 0..159, four channels each): h and c to
 // the candidate slots of `cand`.
-__device__ void lstm_cell(Shared& s, const float* c_prev, float* h_out, float* c_out) {
+template <class P>
+__device__ void lstm_cell(Shared<P>& s, const float* c_prev, float* h_out, float* c_out) {
   const uint32_t t = threadIdx.x;
   if (t < H / 4) {
     for (int i = 0; i < 4; ++i) {
@@ -123,12 +169,15 @@ __device__ void lstm_cell(Shared& s, const float* c_prev, float* h_out, float* c
 
 // prepare_predictor (tdt-decoder.ts:1341-1500): candidates from `token`
 // and the committed state.
-__device__ void predictor(Shared& s, const TdtArgs& a, const float* state, float* cand, uint32_t token,
+template <class P>
+__device__ void predictor(Shared<P>& s, const TdtArgs& a, const float* state, float* cand, uint32_t token,
                           bool initial) {
+  typedef typename P::X X;
   const uint32_t t = threadIdx.x;
+  const typename P::W* embedding = wptr<P>(a.embedding);
   for (uint32_t k = t; k < H; k += kThreads) {
-    s.x[k] = initial ? (_Float16)0.0f : a.embedding[(uint64_t)token * H + k];
-    s.x[H + k] = (_Float16)state[k];
+    s.x[k] = initial ? (X)0.0f : (X)embedding[(uint64_t)token * H + k];
+    s.x[H + k] = (X)state[k];
   }
   __syncthreads();
   lstm_gates(s, a.lstm[0], a.lstm_bias[0], initial ? 0u : 2 * H);
@@ -136,8 +185,8 @@ __device__ void predictor(Shared& s, const TdtArgs& a, const float* state, float
   lstm_cell(s, state + H, cand, cand + H);
   __syncthreads();
   for (uint32_t k = t; k < H; k += kThreads) {
-    s.x[k] = (_Float16)cand[k];
-    s.x[H + k] = (_Float16)state[2 * H + k];
+    s.x[k] = (X)cand[k];
+    s.x[H + k] = (X)state[2 * H + k];
   }
   __syncthreads();
   lstm_gates(s, a.lstm[1], a.lstm_bias[1], initial ? H : 2 * H);
@@ -149,10 +198,12 @@ __device__ void predictor(Shared& s, const TdtArgs& a, const float* state, float
     const float4 b = *reinterpret_cast<const float4*>(a.projector_bias + 4 * t);
     float acc[4] = {b.x, b.y, b.z, b.w};
     const float* h1 = cand + 2 * H;
+    const typename P::W* projector = wptr<P>(a.projector);
     for (uint32_t k0 = 0; k0 < H; k0 += kBatchRows) {
-      half4 w[kBatchRows];
+      typename P::W4 w[kBatchRows];
 #pragma unroll
-      for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(a.projector + (uint64_t)(k0 + r) * H + 4 * t);
+      for (uint32_t r = 0; r < kBatchRows; ++r)
+        w[r] = load4<typename P::W4>(projector + (uint64_t)(k0 + r) * H + 4 * t);
 #pragma unroll
       for (uint32_t r = 0; r < kBatchRows; ++r) {
         const float h = h1[k0 + r];
@@ -166,7 +217,10 @@ __device__ void predictor(Shared& s, const TdtArgs& a, const float* state, float
 
 // run_joint_pair for one window (tdt-decoder.ts:1605-1662, head :977-1031)
 // and the argmax (:773-853, :1517-1603): s.token, s.duration.
-__device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, const float* projection) {
+template <class P>
+__device__ void joint(Shared<P>& s, const TdtArgs& a, const typename P::W* encoder_row, const float* projection) {
+  typedef typename P::A4 A4;
+  typedef typename P::W4 W4;
   const uint32_t t = threadIdx.x;
   for (uint32_t c = t; c < H; c += kThreads) {
     // max(v, 0) as a comparison: -0 and NaN give +0 (the oracle's rule)
@@ -177,28 +231,27 @@ __device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, 
   __syncthreads();
   // An exact +0 input is skipped while no -0 or NaN has appeared at or
   // before it: find the first such row, then flag every row and keep the
-  // f16 inputs, so the chain below selects instead of branching.
+  // chain inputs, so the chain below selects instead of branching.
   for (uint32_t c = t; c < H; c += kThreads) {
     const uint32_t bits = __float_as_uint(s.joint[c]);
     if (bits == 0x80000000u || (bits & 0x7fffffffu) > 0x7f800000u) atomicMin(&s.first_bad, c);
   }
   __syncthreads();
   for (uint32_t c = t; c < H; c += kThreads) {
-    s.x[c] = (_Float16)s.joint[c];
+    s.x[c] = (typename P::X)s.joint[c];
     s.use[c] = __float_as_uint(s.joint[c]) != 0u || c >= s.first_bad;
   }
   __syncthreads();
   if (t < kTdtHead / 4) {
-    const float4 b = *reinterpret_cast<const float4*>(a.head_bias + 4 * t);
-    half4 acc = half4{(_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-    const _Float16* column = a.head + 4 * t;
+    A4 acc = bias4<A4>(a.head_bias + 4 * t);
+    const typename P::W* column = wptr<P>(a.head) + 4 * t;
     for (uint32_t k0 = 0; k0 < H; k0 += kBatchRows) {
-      half4 w[kBatchRows];
+      W4 w[kBatchRows];
 #pragma unroll
-      for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load_half4(column + (uint64_t)(k0 + r) * kTdtHead);
+      for (uint32_t r = 0; r < kBatchRows; ++r) w[r] = load4<W4>(column + (uint64_t)(k0 + r) * kTdtHead);
 #pragma unroll
       for (uint32_t r = 0; r < kBatchRows; ++r) {
-        const half4 next = __builtin_elementwise_fma(splat(s.x[k0 + r]), w[r], acc);
+        const A4 next = __builtin_elementwise_fma(splat<A4>(s.x[k0 + r]), w[r], acc);
         acc = s.use[k0 + r] ? next : acc;
       }
     }
@@ -243,12 +296,13 @@ __device__ void joint(Shared& s, const TdtArgs& a, const _Float16* encoder_row, 
   __syncthreads();
 }
 
+template <class P>
 __global__ __launch_bounds__(kTdtThreads) void tdt_decode_kernel(TdtArgs a) {
-  __shared__ Shared s;
+  __shared__ Shared<P> s;
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   float* state = a.state + (uint64_t)b * 4 * H;
   float* cand = a.scratch + (uint64_t)b * 5 * H;
-  const _Float16* encoder = a.encoder + (uint64_t)b * a.frames * H;
+  const typename P::W* encoder = wptr<P>(a.encoder) + (uint64_t)b * a.frames * H;
   for (uint32_t i = t; i < 4 * H; i += kThreads) state[i] = 0.0f;
 
   // control state, thread 0 only
@@ -443,7 +497,7 @@ __device__ __forceinline__ void stage_load(const Slice& sl, uint32_t k0, const u
   const _Float16* base = sl.base + (uint64_t)k0 * sl.stride;
   // unconditional, so all of a thread's loads issue back to back
 #pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i) reg[i] = load_half4(base + (off[i] == ~0u ? 0u : off[i]));
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i) reg[i] = load4<half4>(base + (off[i] == ~0u ? 0u : off[i]));
 }
 
 __device__ __forceinline__ void stage_store(half4* dst, const uint32_t (&off)[kUnitsPerThread],
@@ -560,7 +614,7 @@ __device__ void team_lstm(TeamShared& s, const _Float16* weight, const float* bi
           x[i] = s.x[k0 + r];
         }
 #pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) acc = __builtin_elementwise_fma(splat(x[i]), w[i], acc);
+        for (uint32_t i = 0; i < 8; ++i) acc = __builtin_elementwise_fma(splat<half4>(x[i]), w[i], acc);
       }
     }
   });
@@ -589,19 +643,22 @@ __device__ bool team_predictor(TeamShared& s, const TdtArgs& a, const TdtTeam& t
                                const float* state, float* cand, uint32_t token, bool initial, uint32_t u0,
                                uint32_t U) {
   const uint32_t t = threadIdx.x;
-  for (uint32_t k = t; k < H; k += TT) s.x[k] = initial ? (_Float16)0.0f : a.embedding[(uint64_t)token * H + k];
+  const _Float16* embedding = static_cast<const _Float16*>(a.embedding);
+  for (uint32_t k = t; k < H; k += TT) s.x[k] = initial ? (_Float16)0.0f : embedding[(uint64_t)token * H + k];
   load_exchanged_f16(s.x + H, state);
   __syncthreads();
-  team_lstm(s, a.lstm[0], a.lstm_bias[0], initial ? 0u : 2 * H, u0, U, state + H, cand, cand + H);
+  team_lstm(s, static_cast<const _Float16*>(a.lstm[0]), a.lstm_bias[0], initial ? 0u : 2 * H, u0, U, state + H, cand,
+            cand + H);
   if (!team_barrier(s, tm, b, n)) return false;
   load_exchanged_f16(s.x, cand);
   load_exchanged_f16(s.x + H, state + 2 * H);
   __syncthreads();
-  team_lstm(s, a.lstm[1], a.lstm_bias[1], initial ? H : 2 * H, u0, U, state + 3 * H, cand + 2 * H, cand + 3 * H);
+  team_lstm(s, static_cast<const _Float16*>(a.lstm[1]), a.lstm_bias[1], initial ? H : 2 * H, u0, U, state + 3 * H,
+            cand + 2 * H, cand + 3 * H);
   if (!team_barrier(s, tm, b, n)) return false;
   // decoder projector columns [u0, u0 + U): f32 fma chain over k
   load_exchanged(s.vec, cand + 2 * H);
-  const Slice sl{a.projector, H, U / 4, U / 4, 0, u0, kStageUnits / (U / 4)};
+  const Slice sl{static_cast<const _Float16*>(a.projector), H, U / 4, U / 4, 0, u0, kStageUnits / (U / 4)};
   float acc = 0.0f;
   if (t < U) acc = a.projector_bias[u0 + t];
   stream_slice(s, sl, H, [&](const half4* st, uint32_t k0) {
@@ -650,7 +707,7 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
     s.use[c] = __float_as_uint(s.vec[c]) != 0u || c >= s.first_bad;
   }
   const uint32_t HQ = hq1 - hq0;  // at most 17 (16 members) or 33 (8 members)
-  const Slice sl{a.head, kTdtHead, HQ, HQ, 0, hq0 * 4, HQ * 320 <= kStageUnits ? 320u : 160u};
+  const Slice sl{static_cast<const _Float16*>(a.head), kTdtHead, HQ, HQ, 0, hq0 * 4, HQ * 320 <= kStageUnits ? 320u : 160u};
   half4 acc = half4{0, 0, 0, 0};
   if (t < HQ) {
     const float4 bb = *reinterpret_cast<const float4*>(a.head_bias + 4 * (hq0 + t));
@@ -673,7 +730,7 @@ __device__ bool team_joint(TeamShared& s, const TdtArgs& a, const TdtTeam& tm, u
         // row without touching the dependent chain
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i)
-          if (__builtin_amdgcn_readfirstlane((int)use[i])) acc = __builtin_elementwise_fma(splat(xs[i]), w[i], acc);
+          if (__builtin_amdgcn_readfirstlane((int)use[i])) acc = __builtin_elementwise_fma(splat<half4>(xs[i]), w[i], acc);
       }
     }
   });
@@ -759,7 +816,7 @@ __global__ __launch_bounds__(kTdtTeamThreads) void tdt_team_kernel(TdtArgs a, Td
   const uint32_t hq0 = p * (kTdtHead / 4) / P, hq1 = (p + 1) * (kTdtHead / 4) / P;
   float* state = a.state + (uint64_t)b * 4 * H;
   float* cand = a.scratch + (uint64_t)b * 5 * H;
-  const _Float16* encoder = a.encoder + (uint64_t)b * a.frames * H;
+  const _Float16* encoder = static_cast<const _Float16*>(a.encoder) + (uint64_t)b * a.frames * H;
   uint32_t n = 0;  // team barriers passed
   for (uint32_t i = t; i < U; i += TT)
     for (uint32_t j = 0; j < 4; ++j) xstore(state + j * H + u0 + i, 0.0f);
@@ -861,16 +918,23 @@ __global__ void tdt_team_clear(uint32_t* sync, uint32_t words) {
 
 }  // namespace
 
-hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, hipStream_t stream, hipEvent_t start,
+hipError_t launch_tdt_decode(const TdtArgs& args, uint32_t batch, bool f32, hipStream_t stream, hipEvent_t start,
                              hipEvent_t stop) {
   if (batch == 0) return hipSuccess;
-  if (start || stop)
-    hipExtLaunchKernelGGL(tdt_decode_kernel, dim3(batch), dim3(kTdtThreads), 0, stream, start, stop, 0, args);
-  else
-    hipLaunchKernelGGL(tdt_decode_kernel, dim3(batch), dim3(kTdtThreads), 0, stream, args);
+  const dim3 grid(batch), block(kTdtThreads);
+  if (f32) {
+    if (start || stop)
+      hipExtLaunchKernelGGL(tdt_decode_kernel<ProfileF32>, grid, block, 0, stream, start, stop, 0, args);
+    else
+      hipLaunchKernelGGL(tdt_decode_kernel<ProfileF32>, grid, block, 0, stream, args);
+  } else {
+    if (start || stop)
+      hipExtLaunchKernelGGL(tdt_decode_kernel<ProfileF16>, grid, block, 0, stream, start, stop, 0, args);
+    else
+      hipLaunchKernelGGL(tdt_decode_kernel<ProfileF16>, grid, block, 0, stream, args);
+  }
   return hipGetLastError();
 }
-
 
 bool tdt_team_members_supported(uint32_t members) { return members == 8 || members == 16; }
 

@@ -17,6 +17,7 @@ struct pk_tdt_op {
   std::string label;
   uint32_t batch = 0;
   pk::TdtArgs args{};
+  bool f32 = false;     // the f32 profile (one workgroup per window)
   pk::TdtTeam team{};   // members == 0: one workgroup per window
   uint32_t* team_memory = nullptr;
   bool destroyed = false;
@@ -43,15 +44,18 @@ int slice(const void* p, uint64_t bytes, uint64_t need, const char* name) {
 int validate(const pk_tdt_desc* d) {
   if (!d) return fail(PK_INVALID_ARGUMENT, "TDT decoder descriptor is null");
   if (d->struct_size != sizeof(pk_tdt_desc)) return fail(PK_INVALID_ARGUMENT, "pk_tdt_desc.struct_size mismatch");
-  if (d->precision != PK_PRECISION_F16)
-    return fail(PK_INVALID_ARGUMENT, "TDT decoder f16 profile required (precision %d)", d->precision);
+  // the profile's weight and encoder-row element (tdt-decoder.ts:196-218,
+  // requireDecoderWeights :378-405)
+  if (d->precision != PK_PRECISION_F16 && d->precision != PK_PRECISION_F32)
+    return fail(PK_INVALID_ARGUMENT, "TDT decoder precision must be f16 or f32 (precision %d)", d->precision);
+  const uint64_t e = d->precision == PK_PRECISION_F32 ? 4 : 2;
   // validateDescriptor (:507-547)
   if (d->batch_size == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder batchSize");
   if (d->frames == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder frames");
   if (d->max_tokens == 0) return fail(PK_RANGE_ERROR, "Invalid TDT decoder maxTokens");
   const uint64_t B = d->batch_size;
   int s;
-  if ((s = slice(d->encoder_projected, d->encoder_projected_bytes, B * d->frames * H * 2, "encoderProjected")) ||
+  if ((s = slice(d->encoder_projected, d->encoder_projected_bytes, B * d->frames * H * e, "encoderProjected")) ||
       (s = slice(d->encoded_lengths, d->encoded_lengths_bytes, B * 4, "encodedLengths")) ||
       (s = slice(d->decode_starts, d->decode_starts_bytes, B * 4, "decodeStarts")) ||
       (s = slice(d->decode_ends, d->decode_ends_bytes, B * 4, "decodeEnds")) ||
@@ -65,18 +69,18 @@ int validate(const pk_tdt_desc* d) {
     return s;
   // requireDecoderWeights (:378-456)
   const pk_tdt_weights& w = d->weights;
-  if ((s = tensor(w.embedding, w.embedding_bytes, PK_TDT_TOKEN_OUTPUTS * H * 2, "token-by-channel-row-major",
+  if ((s = tensor(w.embedding, w.embedding_bytes, PK_TDT_TOKEN_OUTPUTS * H * e, "token-by-channel-row-major",
                   "1025,640")) ||
-      (s = tensor(w.lstm_weight[0], w.lstm_weight_bytes[0], 2 * H * 4 * H * 2,
+      (s = tensor(w.lstm_weight[0], w.lstm_weight_bytes[0], 2 * H * 4 * H * e,
                   "input-hidden-k-by-ifgo-row-major-vec4", "1280,2560")) ||
-      (s = tensor(w.lstm_weight[1], w.lstm_weight_bytes[1], 2 * H * 4 * H * 2,
+      (s = tensor(w.lstm_weight[1], w.lstm_weight_bytes[1], 2 * H * 4 * H * e,
                   "input-hidden-k-by-ifgo-row-major-vec4", "1280,2560")) ||
       (s = tensor(w.lstm_bias[0], w.lstm_bias_bytes[0], 4 * H * 4, "ifgo-gates", "2560")) ||
       (s = tensor(w.lstm_bias[1], w.lstm_bias_bytes[1], 4 * H * 4, "ifgo-gates", "2560")) ||
-      (s = tensor(w.projector_weight, w.projector_weight_bytes, H * H * 2, "k-by-output-row-major-vec4",
+      (s = tensor(w.projector_weight, w.projector_weight_bytes, H * H * e, "k-by-output-row-major-vec4",
                   "640,640")) ||
       (s = tensor(w.projector_bias, w.projector_bias_bytes, H * 4, "output-channel", "640")) ||
-      (s = tensor(w.head_weight, w.head_weight_bytes, H * PK_TDT_HEAD_OUTPUTS * 2, "k-by-output-row-major-vec4",
+      (s = tensor(w.head_weight, w.head_weight_bytes, H * PK_TDT_HEAD_OUTPUTS * e, "k-by-output-row-major-vec4",
                   "640,1032")) ||
       (s = tensor(w.head_bias, w.head_bias_bytes, PK_TDT_HEAD_OUTPUTS * 4, "output-channel-padded-vec4", "1032")))
     return s;
@@ -86,8 +90,10 @@ int validate(const pk_tdt_desc* d) {
 }
 
 // Team size of a batch: the largest supported size whose workgroups can all
-// be resident at once (0: one workgroup per window).
-uint32_t choose_members(int device, uint32_t batch) {
+// be resident at once (0: one workgroup per window, always for the f32
+// profile, whose kernel has no team form).
+uint32_t choose_members(int device, uint32_t batch, bool f32) {
+  if (f32) return 0;
   const uint32_t capacity = pk::tdt_team_capacity(device);
   for (uint32_t m : {16u, 8u})
     if ((uint64_t)batch * m <= capacity) return m;
@@ -128,16 +134,16 @@ int set_team(pk_tdt_op* op, uint32_t members) {
 pk::TdtArgs args_of(const pk_tdt_desc* d) {
   pk::TdtArgs a{};
   const pk_tdt_weights& w = d->weights;
-  a.embedding = static_cast<const _Float16*>(w.embedding);
-  a.lstm[0] = static_cast<const _Float16*>(w.lstm_weight[0]);
-  a.lstm[1] = static_cast<const _Float16*>(w.lstm_weight[1]);
+  a.embedding = w.embedding;
+  a.lstm[0] = w.lstm_weight[0];
+  a.lstm[1] = w.lstm_weight[1];
   a.lstm_bias[0] = w.lstm_bias[0];
   a.lstm_bias[1] = w.lstm_bias[1];
-  a.projector = static_cast<const _Float16*>(w.projector_weight);
+  a.projector = w.projector_weight;
   a.projector_bias = w.projector_bias;
-  a.head = static_cast<const _Float16*>(w.head_weight);
+  a.head = w.head_weight;
   a.head_bias = w.head_bias;
-  a.encoder = static_cast<const _Float16*>(d->encoder_projected);
+  a.encoder = d->encoder_projected;
   a.lengths = d->encoded_lengths;
   a.starts = d->decode_starts;
   a.ends = d->decode_ends;
@@ -214,7 +220,8 @@ int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
   op->label = d->label ? d->label : "parakeet-persistent-tdt-decode";
   op->batch = d->batch_size;
   op->args = args_of(d);
-  if (int st = set_team(op, choose_members(ctx->device, op->batch))) {
+  op->f32 = d->precision == PK_PRECISION_F32;
+  if (int st = set_team(op, choose_members(ctx->device, op->batch, op->f32))) {
     delete op;
     return st;
   }
@@ -225,10 +232,13 @@ int pk_tdt_create(pk_context* ctx, const pk_tdt_desc* d, pk_tdt_op** out) {
 int pk_tdt_set_team_size(pk_tdt_op* op, uint32_t members) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "TDT decoder op is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
-  if (members == 0) members = choose_members(op->ctx->device, op->batch);
+  if (members == 0) members = choose_members(op->ctx->device, op->batch, op->f32);
   else if (members == 1) members = 0;
   else if (!pk::tdt_team_members_supported(members))
     return fail(PK_RANGE_ERROR, "%s team size must be 0, 1, 8 or 16", op->label.c_str());
+  else if (op->f32)
+    return fail(PK_RANGE_ERROR, "%s: team decoding is built for the f16 profile (f32 team size 1)",
+                op->label.c_str());
   else if ((uint64_t)op->batch * members > pk::tdt_team_capacity(op->ctx->device))
     return fail(PK_RANGE_ERROR, "%s: %u windows x %u workgroups cannot be resident together", op->label.c_str(),
                 op->batch, members);
@@ -271,7 +281,7 @@ int pk_tdt_enqueue_timed(pk_tdt_op* op, uint32_t active_batch, void* stream, voi
                   op->team.members, hipGetErrorString(e));
     return ok();
   }
-  PK_HIP(pk::launch_tdt_decode(op->args, batch, s, static_cast<hipEvent_t>(start_event),
+  PK_HIP(pk::launch_tdt_decode(op->args, batch, op->f32, s, static_cast<hipEvent_t>(start_event),
                                static_cast<hipEvent_t>(end_event)),
          "TDT decoder launch");
   return ok();
@@ -299,17 +309,20 @@ int pk_tdt_decode_static(pk_context* ctx, const pk_tdt_desc* d, uint32_t members
   if (batch > kStaticWindows)
     return fail(PK_RANGE_ERROR, "%s: %u windows exceed the %u of the static decoder buffers", label, batch,
                 kStaticWindows);
-  if (members == 0) members = choose_members(ctx->device, batch);
+  const bool f32 = d->precision == PK_PRECISION_F32;
+  if (members == 0) members = choose_members(ctx->device, batch, f32);
   else if (members == 1) members = 0;
   else if (!pk::tdt_team_members_supported(members))
     return fail(PK_RANGE_ERROR, "%s team size must be 0, 1, 8 or 16", label);
+  else if (f32)
+    return fail(PK_RANGE_ERROR, "%s: team decoding is built for the f16 profile (f32 team size 1)", label);
   else if ((uint64_t)batch * members > pk::tdt_team_capacity(ctx->device))
     return fail(PK_RANGE_ERROR, "%s: %u windows x %u workgroups cannot be resident together", label, batch, members);
   PK_HIP(hipSetDevice(ctx->device), "hipSetDevice");
   const hipStream_t st = stream_or_default(ctx, stream);
   const pk::TdtArgs args = args_of(d);
   if (members == 0) {
-    PK_HIP(pk::launch_tdt_decode(args, batch, st), "TDT decoder launch");
+    PK_HIP(pk::launch_tdt_decode(args, batch, f32, st), "TDT decoder launch");
     return ok();
   }
   uint32_t* buffers = nullptr;

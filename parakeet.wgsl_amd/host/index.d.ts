@@ -519,13 +519,18 @@ export interface ParakeetEncoderGraphOptions {
   /** PW1's GLU epilogue (this library only). */
   readonly fusedGlu?: boolean;
   readonly label?: string;
+  /** encoder.ts:1299-1305: fp16 (default) or fp32 (an fp32 package; f32 outputs). */
+  readonly executionProfile?: { precision: "fp16" | "fp32" };
 }
 
 /** encoder.ts:1200-1862 */
 export declare class ParakeetEncoderGraph {
-  static create(device: HipGpuDevice, model: EncoderModel, options?: ParakeetEncoderGraphOptions): Promise<ParakeetEncoderGraph>;
+  static create(device: HipGpuDevice, model: EncoderModel & { readonly precision?: string },
+                options?: ParakeetEncoderGraphOptions): Promise<ParakeetEncoderGraph>;
   readonly batchSize: number;
   readonly frames: number;
+  /** "f16" or "f32": the element of the output buffers. */
+  readonly precision: "f16" | "f32";
   /** 6 front-end launches + 15 per layer + the projector. */
   readonly dispatchCount: number;
   readonly outputBuffer: HipBuffer;
@@ -586,10 +591,10 @@ export declare class TdtDecoderDispatch {
   destroy(): void;
 }
 
-/** tdt-decoder.ts:139-366 (f16 profile). */
+/** tdt-decoder.ts:139-366 (fp16 and fp32 profiles; teams are fp16 only). */
 export declare class PersistentTdtDecoderKernel {
   static create(device: HipGpuDevice, arena: GpuActivationArena, model: EncoderModel & { readonly precision?: string },
-                executionProfile?: { precision: "fp16" }): Promise<PersistentTdtDecoderKernel>;
+                executionProfile?: { precision: "fp16" | "fp32" }): Promise<PersistentTdtDecoderKernel>;
   validateDescriptor(descriptor: TdtDecoderDescriptor): void;
   createDispatch(descriptor: TdtDecoderDescriptor): TdtDecoderDispatch;
 }

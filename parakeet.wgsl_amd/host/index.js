@@ -1479,8 +1479,13 @@ function requireEncoderTensor(model, name, spec) {
   return addressOf(tensor.binding);
 }
 
+/** executionDtype (encoder.ts:2625-2631): the profile's activation and palette dtype. */
+function executionDtype(precision) {
+  return precision === "f32" ? "float32" : "float16";
+}
+
 /** matrixTensor (encoder.ts:2458-2512): packed codes and palette addresses. */
-function encoderMatrix(model, name, inner, columns, bits, groups) {
+function encoderMatrix(model, name, inner, columns, bits, groups, precision) {
   const codesPerGroup = bits === 5 ? 32 : 16;
   const wordsPerGroup = bits === 5 ? 5 : 3;
   const packedGroups = (inner * columns) / codesPerGroup;
@@ -1490,7 +1495,7 @@ function encoderMatrix(model, name, inner, columns, bits, groups) {
     layout: `k-by-output-row-major-palette${bits}-lsb-u32`,
   });
   const palette = requireEncoderTensor(model, `${name}.palette`, {
-    dtype: "float16", logicalShape: [groups, 1 << bits], storageShape: [groups, 1 << bits],
+    dtype: executionDtype(precision), logicalShape: [groups, 1 << bits], storageShape: [groups, 1 << bits],
     layout: "output-group-by-palette-lut",
   });
   return { packed, palette };
@@ -1502,19 +1507,20 @@ function channelAddress(model, name, channels, layout) {
   });
 }
 
-function kernelAddress(model, name, layout) {
+function kernelAddress(model, name, layout, precision) {
   return requireEncoderTensor(model, name, {
-    dtype: "float16", logicalShape: [3, 3, PARAKEET_SUBSAMPLING_CHANNELS],
+    dtype: executionDtype(precision), logicalShape: [3, 3, PARAKEET_SUBSAMPLING_CHANNELS],
     storageShape: [3, 3, PARAKEET_SUBSAMPLING_CHANNELS / 4, 4], layout,
   });
 }
 
 /** The native descriptor of one layer from the model's tensors (encoder.ts:1868-2135). */
-function encoderLayerDescriptor(model, index, frames) {
+function encoderLayerDescriptor(model, index, frames, precision) {
   const prefix = `encoder.layers.${index}`;
   const norms = ["norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out"];
   const m = (name, inner, columns, bits, groups) =>
-    encoderMatrix(model, `${prefix}.${name}`, inner, columns, bits || 5, groups || 1);
+    encoderMatrix(model, `${prefix}.${name}`, inner, columns, bits || 5, groups || 1, precision);
+  const dtype = executionDtype(precision);
   const C = PARAKEET_ENCODER_CHANNELS, H = PARAKEET_INTERMEDIATE_CHANNELS;
   const bias = (name) => requireEncoderTensor(model, `${prefix}.self_attn.${name}`, {
     dtype: "float32", logicalShape: [8, 128], storageShape: [8, 128], layout: "head-by-channel",
@@ -1526,7 +1532,7 @@ function encoderLayerDescriptor(model, index, frames) {
     ff1Linear2: m("feed_forward1.linear2.weight", H, C),
     qkv: m("self_attn.qkv.weight", C, 3 * C, 5, 3),
     projectedPositions: requireEncoderTensor(model, `${prefix}.self_attn.projected_positions`, {
-      dtype: "float16", logicalShape: [2 * frames - 1, C], storageShape: [8, 32, 2 * frames - 1, 4],
+      dtype, logicalShape: [2 * frames - 1, C], storageShape: [8, 32, 2 * frames - 1, 4],
       layout: "head-vector-position-vec4",
     }),
     biasU: bias("bias_u"),
@@ -1534,7 +1540,7 @@ function encoderLayerDescriptor(model, index, frames) {
     oProj: m("self_attn.o_proj.weight", C, C, 6),
     pointwise1: m("conv.pointwise_conv1.weight", C, 2 * C),
     depthwise: requireEncoderTensor(model, `${prefix}.conv.depthwise_conv.weight`, {
-      dtype: "float16", logicalShape: [9, C], storageShape: [9, C / 4, 4], layout: "kernel-channel-vec4",
+      dtype, logicalShape: [9, C], storageShape: [9, C / 4, 4], layout: "kernel-channel-vec4",
     }),
     bnScale: channelAddress(model, `${prefix}.conv.norm.scale`, C, "channel"),
     bnShift: channelAddress(model, `${prefix}.conv.norm.shift`, C, "channel"),
@@ -1545,21 +1551,21 @@ function encoderLayerDescriptor(model, index, frames) {
 }
 
 /** The front end's native descriptor (encoder.ts:2140-2300). */
-function encoderSubsamplingDescriptor(model) {
+function encoderSubsamplingDescriptor(model, precision) {
   const p = "encoder.subsampling";
   const S = PARAKEET_SUBSAMPLING_CHANNELS;
   return {
-    conv0Weights: kernelAddress(model, `${p}.layers.0.weight`, SUBSAMPLING_CONV0_WEIGHT_LAYOUT),
+    conv0Weights: kernelAddress(model, `${p}.layers.0.weight`, SUBSAMPLING_CONV0_WEIGHT_LAYOUT, precision),
     conv0Bias: channelAddress(model, `${p}.layers.0.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
-    depthwise2Weights: kernelAddress(model, `${p}.layers.2.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT),
+    depthwise2Weights: kernelAddress(model, `${p}.layers.2.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT, precision),
     depthwise2Bias: channelAddress(model, `${p}.layers.2.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
-    pointwise3: encoderMatrix(model, `${p}.layers.3.weight`, S, S, 5, 1),
+    pointwise3: encoderMatrix(model, `${p}.layers.3.weight`, S, S, 5, 1, precision),
     pointwise3Bias: channelAddress(model, `${p}.layers.3.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
-    depthwise5Weights: kernelAddress(model, `${p}.layers.5.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT),
+    depthwise5Weights: kernelAddress(model, `${p}.layers.5.weight`, SUBSAMPLING_DEPTHWISE_WEIGHT_LAYOUT, precision),
     depthwise5Bias: channelAddress(model, `${p}.layers.5.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
-    pointwise6: encoderMatrix(model, `${p}.layers.6.weight`, S, S, 5, 1),
+    pointwise6: encoderMatrix(model, `${p}.layers.6.weight`, S, S, 5, 1, precision),
     pointwise6Bias: channelAddress(model, `${p}.layers.6.bias`, S, SUBSAMPLING_BIAS_LAYOUT),
-    linear: encoderMatrix(model, `${p}.linear.weight`, 16 * S, PARAKEET_ENCODER_CHANNELS, 5, 1),
+    linear: encoderMatrix(model, `${p}.linear.weight`, 16 * S, PARAKEET_ENCODER_CHANNELS, 5, 1, precision),
     linearBias: channelAddress(model, `${p}.linear.bias`, PARAKEET_ENCODER_CHANNELS, SUBSAMPLING_BIAS_LAYOUT),
   };
 }
@@ -1579,6 +1585,7 @@ class ParakeetEncoderGraph {
     this.frames = options.frames;
     this.featureFrames = options.featureFrames;
     this.layers = options.layers;
+    this.precision = options.precision;
     this.info = native().encoderInfo(handle);
     this.destroyed = false;
   }
@@ -1593,7 +1600,10 @@ class ParakeetEncoderGraph {
    * first) and options.postNorms (the residual GEMMs write the LayerNorms
    * after them; measured slower, off by default),
    * none with a reference counterpart, options.featureFrames (default
-   * 1501).
+   * 1501), and options.executionProfile (encoder.ts:1299-1305: {precision:
+   * "fp16"} by default, or {precision: "fp32"} for an fp32 package: f32
+   * activations, palettes, positions and convolution weights, and f32
+   * encoder and projector outputs).
    */
   static create(device, model, options) {
     try {
@@ -1604,6 +1614,12 @@ class ParakeetEncoderGraph {
   }
 
   static build(device, model, o) {
+    const precision = precisionOf(o.executionProfile);
+    const profile = precision === "f32" ? "fp32" : "fp16";
+    // requireEncoderConfig (encoder.ts:2584-2593)
+    if (model.precision !== undefined && model.precision !== profile)
+      throw new Error(`Parakeet ${profile} encoder cannot use ${model.precision} model weights`);
+    const elem = precision === "f32" ? 4 : 2;
     const batchSize = o.batchSize === undefined ? 16 : o.batchSize;
     const layers = o.layers === undefined ? PARAKEET_ENCODER_LAYERS : o.layers;
     const featureFrames = o.featureFrames === undefined ? PARAKEET_FEATURE_FRAMES : o.featureFrames;
@@ -1611,10 +1627,10 @@ class ParakeetEncoderGraph {
     let frames = featureFrames;
     for (let i = 0; i < 3; ++i) frames = subsamplingOutputDimension(frames);
     const layerDescriptors = [];
-    for (let i = 0; i < layers; ++i) layerDescriptors.push(encoderLayerDescriptor(model, i, frames));
-    const subsampling = encoderSubsamplingDescriptor(model);
+    for (let i = 0; i < layers; ++i) layerDescriptors.push(encoderLayerDescriptor(model, i, frames, precision));
+    const subsampling = encoderSubsamplingDescriptor(model, precision);
     const projector = encoderMatrix(model, "encoder_projector.weight", PARAKEET_ENCODER_CHANNELS,
-                                    PARAKEET_PROJECTED_CHANNELS, 5, 1);
+                                    PARAKEET_PROJECTED_CHANNELS, 5, 1, precision);
     const projectorBias = channelAddress(model, "encoder_projector.bias", PARAKEET_PROJECTED_CHANNELS,
                                          "output-channel");
     const rows = batchSize * frames;
@@ -1623,13 +1639,13 @@ class ParakeetEncoderGraph {
       features: make("fbank-feature-major", batchSize * PARAKEET_FEATURE_BINS * featureFrames * 4),
       featureLengths: make("feature-lengths", batchSize * 4),
       encoderLengths: make("encoder-lengths", batchSize * 4),
-      output: make("encoder-output", rows * PARAKEET_ENCODER_CHANNELS * 2),
-      projectedOutput: make("encoder-projector-output", rows * PARAKEET_PROJECTED_CHANNELS * 2),
+      output: make("encoder-output", rows * PARAKEET_ENCODER_CHANNELS * elem),
+      projectedOutput: make("encoder-projector-output", rows * PARAKEET_PROJECTED_CHANNELS * elem),
     };
     let handle;
     try {
       handle = native().encoderCreate(device.context, {
-        label: o.label || "encoder", fusedGlu: o.fusedGlu !== false, fusedNorms: o.fusedNorms === true,
+        label: o.label || "encoder", precision, fusedGlu: o.fusedGlu !== false, fusedNorms: o.fusedNorms === true,
         unchainedNorms: o.unchainedNorms === true, postNorms: o.postNorms === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
@@ -1640,7 +1656,7 @@ class ParakeetEncoderGraph {
       for (const b of Object.values(buffers)) b.destroy();
       throw error;
     }
-    return new ParakeetEncoderGraph(device, handle, buffers, { batchSize, frames, featureFrames, layers });
+    return new ParakeetEncoderGraph(device, handle, buffers, { batchSize, frames, featureFrames, layers, precision });
   }
 
   /** Launches in one pass (6 front end + 15 per layer + the projector). */
@@ -1707,7 +1723,8 @@ class ParakeetEncoderGraph {
     return derived;
   }
 
-  /** Device buffers of the encoder output [windows*188, 1024] and the projector output [.., 640]. */
+  /** Device buffers of the encoder output [windows*188, 1024] and the projector output [.., 640],
+   * f16 in the fp16 profile and f32 in the fp32 profile. */
   get outputBuffer() {
     return this.buffers.output;
   }
@@ -1766,17 +1783,18 @@ function requireDecoderTensor(tensor, dtype, storageShape, layout) {
  * all in the resident decoder.bin shard buffer; returns the native weight
  * descriptor (addresses and byte sizes).
  */
-function requireDecoderWeights(model) {
+function requireDecoderWeights(model, precision) {
   const t = (name, dtype, shape, layout) => requireDecoderTensor(model.tensor(name), dtype, shape, layout);
   const lstmLayout = "input-hidden-k-by-ifgo-row-major-vec4";
+  const weightDtype = executionDtype(precision);
   const tensors = {
-    embedding: t("decoder.embedding.weight", "float16", [TDT_TOKEN_OUTPUTS, TDT_HIDDEN_SIZE],
+    embedding: t("decoder.embedding.weight", weightDtype, [TDT_TOKEN_OUTPUTS, TDT_HIDDEN_SIZE],
                  "token-by-channel-row-major"),
-    lstmWeight0: t("decoder.lstm.weight_l0", "float16", [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
-    lstmWeight1: t("decoder.lstm.weight_l1", "float16", [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
-    projectorWeight: t("decoder.decoder_projector.weight", "float16", [TDT_HIDDEN_SIZE, TDT_HIDDEN_SIZE],
+    lstmWeight0: t("decoder.lstm.weight_l0", weightDtype, [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
+    lstmWeight1: t("decoder.lstm.weight_l1", weightDtype, [TDT_LSTM_INPUT_SIZE, TDT_GATE_SIZE], lstmLayout),
+    projectorWeight: t("decoder.decoder_projector.weight", weightDtype, [TDT_HIDDEN_SIZE, TDT_HIDDEN_SIZE],
                        "k-by-output-row-major-vec4"),
-    headWeight: t("joint.head.weight", "float16", [TDT_HIDDEN_SIZE, TDT_HEAD_STORAGE_OUTPUTS],
+    headWeight: t("joint.head.weight", weightDtype, [TDT_HIDDEN_SIZE, TDT_HEAD_STORAGE_OUTPUTS],
                   "k-by-output-row-major-vec4"),
     lstmBias0: t("decoder.lstm.bias_l0", "float32", [TDT_GATE_SIZE], "ifgo-gates"),
     lstmBias1: t("decoder.lstm.bias_l1", "float32", [TDT_GATE_SIZE], "ifgo-gates"),
@@ -1837,13 +1855,16 @@ class TdtDecoderDispatch {
 /**
  * PersistentTdtDecoderKernel (tdt-decoder.ts:139-366): greedy TDT decoding
  * with the whole autoregressive loop inside one launch, over the package's
- * resident decoder shard. f16 profile.
+ * resident decoder shard; the fp16 profile (f16 weights and encoder rows)
+ * or the fp32 profile (f32 weights and encoder rows, one workgroup per
+ * window).
  */
 class PersistentTdtDecoderKernel {
-  constructor(device, arena, weights) {
+  constructor(device, arena, weights, precision) {
     this.device = device;
     this.arena = arena;
     this.weights = weights;
+    this.precision = precision;
   }
 
   /** create(device, arena, model, executionProfile?) (:164-292). */
@@ -1853,8 +1874,8 @@ class PersistentTdtDecoderKernel {
       const profile = precision === "f32" ? "fp32" : "fp16";
       if (model.precision !== undefined && model.precision !== profile)
         throw new Error(`TDT decoder ${profile} profile cannot use ${model.precision} decoder weights`);
-      if (profile !== "fp16") throw new Error("TDT decoder fp32 profile is not built for gfx950");
-      return Promise.resolve(new PersistentTdtDecoderKernel(device, arena, requireDecoderWeights(model)));
+      return Promise.resolve(new PersistentTdtDecoderKernel(device, arena, requireDecoderWeights(model, precision),
+                                                            precision));
     } catch (error) {
       return Promise.reject(error);
     }
@@ -1867,6 +1888,7 @@ class PersistentTdtDecoderKernel {
     }
     const out = {
       label: descriptor.label === undefined ? "parakeet-persistent-tdt-decode" : descriptor.label,
+      precision: this.precision,
       batchSize: descriptor.batchSize,
       frames: descriptor.frames,
       maxTokens: descriptor.maxTokens,

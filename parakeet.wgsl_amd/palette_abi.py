@@ -1200,9 +1200,10 @@ TDT_WEIGHT_NAMES = ("embedding", "lstm_weight_l0", "lstm_weight_l1", "lstm_bias_
 
 def tdt_desc(*, weights: dict, encoder_projected, encoded_lengths, decode_starts, decode_ends, flush_finals, state,
              predictor_scratch, tokens, token_frames, token_durations, metadata, batch_size: int, frames: int,
-             max_tokens: int, label: str = "parakeet-persistent-tdt-decode") -> TdtDesc:
+             max_tokens: int, label: str = "parakeet-persistent-tdt-decode", precision: str = "f16") -> TdtDesc:
     """A TdtDesc from device slices (DeviceArrays, or (address, bytes) pairs);
-    `weights` is keyed by TDT_WEIGHT_NAMES."""
+    `weights` is keyed by TDT_WEIGHT_NAMES; `precision` "f16" or "f32" is the
+    execution profile (weights and encoder rows in that element)."""
     def sl(x):
         return tuple(x) if isinstance(x, tuple) else _slice(x)
     w = {k: sl(weights[k]) for k in TDT_WEIGHT_NAMES}
@@ -1215,7 +1216,7 @@ def tdt_desc(*, weights: dict, encoder_projected, encoded_lengths, decode_starts
     for x in (encoder_projected, encoded_lengths, decode_starts, decode_ends, flush_finals, state, predictor_scratch,
               tokens, token_frames, token_durations, metadata):
         fields += list(sl(x))
-    return TdtDesc(ctypes.sizeof(TdtDesc), label.encode(), PRECISION["f16"], batch_size, frames, max_tokens, tw,
+    return TdtDesc(ctypes.sizeof(TdtDesc), label.encode(), PRECISION[precision], batch_size, frames, max_tokens, tw,
                    *fields)
 
 

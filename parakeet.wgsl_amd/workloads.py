@@ -544,8 +544,8 @@ def as_f32_profile(stack: EncoderStack) -> EncoderStack:
 class TdtCase:
     """A TDT decoder over random weights (decoder package shapes): weights
     keyed like palette_abi.TDT_WEIGHT_NAMES, the encoder projector's output
-    [batch, frames, 640] f16, encoded lengths, decode starts and ends,
-    flush flags."""
+    [batch, frames, 640] (f16, or f32 for the f32 profile), encoded
+    lengths, decode starts and ends, flush flags."""
     weights: dict
     encoder_projected: np.ndarray
     lengths: np.ndarray
@@ -562,31 +562,35 @@ class TdtCase:
         return self.encoder_projected.shape[1]
 
 
-def tdt_weights(rng: np.random.Generator, blank_bias: float = 2.0) -> dict:
+def tdt_weights(rng: np.random.Generator, blank_bias: float = 2.0, precision: str = "f16") -> dict:
     """Embedding ~ N(0, 0.5), LSTM weights ~ N(0, 0.03) and biases ~
     N(0, 0.1), projector ~ N(0, 0.04), head ~ N(0, 0.05) with bias ~
     N(0, 0.1) plus `blank_bias` on the blank (random heads otherwise never
-    choose blank), f16 weights and f32 biases."""
+    choose blank); weights in the profile's element (f16 or f32), f32
+    biases."""
+    wt = np.float32 if precision == "f32" else np.float16
+
     def n(shape, std, dtype):
         return (rng.standard_normal(shape) * std).astype(dtype)
     head_bias = n(1032, 0.1, np.float32)
     head_bias[1024] += blank_bias
     head_bias[1030:] = 0.0
-    head = n((640, 1032), 0.05, np.float16)
+    head = n((640, 1032), 0.05, wt)
     head[:, 1030:] = 0
-    return dict(embedding=n((1025, 640), 0.5, np.float16), lstm_weight_l0=n((1280, 2560), 0.03, np.float16),
-                lstm_weight_l1=n((1280, 2560), 0.03, np.float16), lstm_bias_l0=n(2560, 0.1, np.float32),
-                lstm_bias_l1=n(2560, 0.1, np.float32), projector_weight=n((640, 640), 0.04, np.float16),
+    return dict(embedding=n((1025, 640), 0.5, wt), lstm_weight_l0=n((1280, 2560), 0.03, wt),
+                lstm_weight_l1=n((1280, 2560), 0.03, wt), lstm_bias_l0=n(2560, 0.1, np.float32),
+                lstm_bias_l1=n(2560, 0.1, np.float32), projector_weight=n((640, 640), 0.04, wt),
                 projector_bias=n(640, 0.1, np.float32), head_weight=head, head_bias=head_bias)
 
 
 def tdt_case(seed: int = 0, batch: int = 16, frames: int = 188, *, lengths=None, starts=None, ends=None,
-             flush=None, blank_bias: float = 2.0, encoder_std: float = 0.5) -> TdtCase:
-    """Encoder projector output ~ N(0, encoder_std) f16; lengths uniform in
-    [ceil(T/2), T] unless given; starts 0, ends T, no flush unless given."""
+             flush=None, blank_bias: float = 2.0, encoder_std: float = 0.5, precision: str = "f16") -> TdtCase:
+    """Encoder projector output ~ N(0, encoder_std) in the profile's element
+    (f16 or f32); lengths uniform in [ceil(T/2), T] unless given; starts 0,
+    ends T, no flush unless given."""
     rng = np.random.default_rng(seed)
-    weights = tdt_weights(rng, blank_bias)
-    enc = normal(rng, (batch, frames, 640), encoder_std, np.float16)
+    weights = tdt_weights(rng, blank_bias, precision)
+    enc = normal(rng, (batch, frames, 640), encoder_std, np.float32 if precision == "f32" else np.float16)
     if lengths is None:
         lengths = rng.integers((frames + 1) // 2, frames + 1, size=batch)
 

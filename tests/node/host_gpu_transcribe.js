@@ -1,6 +1,7 @@
 // GPU run of the Node host end to end: ParakeetGpuPackage.load of a
 // synthetic package -> ParakeetEncoderGraph (fbank -> 24 layers ->
-// projector, graph replay) -> PersistentTdtDecoderKernel over arena slices.
+// projector, graph replay) -> PersistentTdtDecoderKernel over arena slices,
+// in the package's execution profile (spec.precision "fp16" or "fp32").
 // Writes the projector output and the decoder outputs for
 // tests/test_node_host.py to check. argv: <case.json>
 "use strict";
@@ -11,12 +12,14 @@ const host = require(path.join(__dirname, "..", "..", "parakeet.wgsl_amd", "host
 async function main() {
   const spec = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
   const device = host.HipGpuDevice.create();
+  const precision = spec.precision || "fp16";
+  const executionProfile = { precision };
   const pkg = await host.ParakeetGpuPackage.load(device, spec.manifest, {
-    expectedPrecision: "fp16", manifestSha256: spec.manifestSha256,
+    expectedPrecision: precision, manifestSha256: spec.manifestSha256,
   });
   console.log(`loaded ${pkg.memory.runtimeBufferCount} shards, ${pkg.memory.retainedRuntimeBytes} bytes`);
   const windows = spec.windows;
-  const graph = await host.ParakeetEncoderGraph.create(device, pkg, { batchSize: windows });
+  const graph = await host.ParakeetEncoderGraph.create(device, pkg, { batchSize: windows, executionProfile });
   const features = fs.readFileSync(spec.features);
   graph.uploadFeatures(new Uint8Array(features.buffer, features.byteOffset, features.byteLength));
   let encoder = device.createCommandEncoder({ label: "encode" });
@@ -24,7 +27,7 @@ async function main() {
   device.queue.submit([encoder.finish()]);
   await device.queue.onSubmittedWorkDone();
   const frames = graph.frames;
-  const projectedBytes = windows * frames * 640 * 2;
+  const projectedBytes = windows * frames * 640 * (precision === "fp32" ? 4 : 2);
   const projected = await device.queue.readBuffer(graph.projectedOutputBuffer, 0, projectedBytes);
   fs.writeFileSync(spec.projected, Buffer.from(projected));
   console.log("encoded", Array.from(lengths).join(","));
@@ -52,7 +55,7 @@ async function main() {
   arena.upload(device, descriptor.decodeEnds, new Uint32Array(windows).fill(frames));
   arena.upload(device, descriptor.flushFinals, new Uint32Array(windows).fill(1));
   arena.upload(device, descriptor.state, new Float32Array(windows * 4 * 640));
-  const kernel = await host.PersistentTdtDecoderKernel.create(device, arena, pkg);
+  const kernel = await host.PersistentTdtDecoderKernel.create(device, arena, pkg, executionProfile);
   const dispatch = kernel.createDispatch(descriptor);
   console.log(`decoder team size ${dispatch.teamSize}`);
   encoder = device.createCommandEncoder({ label: "decode" });
@@ -66,7 +69,9 @@ async function main() {
   }
   fs.writeFileSync(spec.decoded, JSON.stringify(out));
   console.log("counts", out.metadata.slice(0, windows).join(","), `team size after the launch ${dispatch.teamSize}`);
-  if (dispatch.teamSize !== 16) throw new Error(`decoder ran with team size ${dispatch.teamSize}, expected 16`);
+  const expectedTeam = precision === "fp32" ? 1 : 16;
+  if (dispatch.teamSize !== expectedTeam)
+    throw new Error(`decoder ran with team size ${dispatch.teamSize}, expected ${expectedTeam}`);
   dispatch.destroy();
   dispatch.destroy();
   arena.destroy();

@@ -188,13 +188,15 @@ def _values(entry: Entry, stack, tdt: dict, rng) -> np.ndarray:
     return value
 
 
-def write_package(directory: str, stack=None, tdt: dict | None = None, seed: int = 0, frames: int = 188) -> str:
-    """Writes the shards, tokenizer.json and manifest.json; returns the
-    manifest path. Without a stack every tensor is zero."""
+def write_package(directory: str, stack=None, tdt: dict | None = None, seed: int = 0, frames: int = 188,
+                  precision: str = "fp16") -> str:
+    """Writes the shards, tokenizer.json and manifest.json of an fp16 or fp32
+    package; returns the manifest path. Without a stack every tensor is zero;
+    an fp32 package takes an f32-profile stack and f32 decoder weights."""
     os.makedirs(directory, exist_ok=True)
     rng = np.random.default_rng(seed)
     frames = stack.frames if stack is not None else frames
-    shards = shard_inventory("fp16", frames)
+    shards = shard_inventory(precision, frames)
     tensors, sizes = layout_records(shards)
     files = []
     for shard, entries in sorted(shards.items()):
@@ -225,5 +227,5 @@ def write_package(directory: str, stack=None, tdt: dict | None = None, seed: int
                   "sha256": hashlib.sha256(tokenizer).hexdigest()})
     path = os.path.join(directory, "manifest.json")
     with open(path, "w") as out:
-        json.dump(manifest("fp16", files, frames), out)
+        json.dump(manifest(precision, files, frames), out)
     return path

@@ -1,12 +1,13 @@
 """Parity of the greedy TDT decoder (PersistentTdtDecoderKernel,
 src/webgpu/kernels/tdt-decoder.ts:1133-2010) against the oracle, for one
-workgroup per window and for teams of 8 and 16 workgroups per window.
+workgroup per window and for teams of 8 and 16 workgroups per window (f16
+profile), and for the f32 profile (:196-218, one workgroup per window).
 
-The kernel evaluates every quantity with the oracle's arithmetic (f16 gate
-and head chains with one rounding per fma in increasing k, f32 cell update,
-projector and joint, the same exp / tanh), so the bar is bit-exact: the
-token, frame and duration sequences, the counts and status flags, and the
-final state and predictor scratch of every window."""
+The kernel evaluates every quantity with the oracle's arithmetic (gate and
+head chains in the profile's format with one rounding per fma in increasing
+k, f32 cell update, projector and joint, the same exp / tanh), so the bar is
+bit-exact: the token, frame and duration sequences, the counts and status
+flags, and the final state and predictor scratch of every window."""
 import numpy as np
 import pytest
 
@@ -22,7 +23,7 @@ def scope(ctx):
     s.close()
 
 
-def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADBEEF, team=None):
+def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADBEEF, team=None, precision="f16"):
     B, T = case.batch, case.frames
     weights = {k: scope.put(case.weights[k]) for k in abi.TDT_WEIGHT_NAMES}
     outs = {k: scope.put(np.full((B, max_tokens), sentinel, np.uint32)) for k in ("tokens", "frames", "durations")}
@@ -34,12 +35,12 @@ def run_decoder(abi, scope, ctx, case, max_tokens, *, active=0, sentinel=0xDEADB
                           decode_ends=scope.put(case.ends), flush_finals=scope.put(case.flush), state=state,
                           predictor_scratch=scratch, tokens=outs["tokens"], token_frames=outs["frames"],
                           token_durations=outs["durations"], metadata=metadata, batch_size=B, frames=T,
-                          max_tokens=max_tokens)
+                          max_tokens=max_tokens, precision=precision)
     try:
         if team is not None:
             op.set_team_size(team)
         before = op.team_size()
-        print("decoder team", before, "batch", B, "frames", T, flush=True)
+        print("decoder", precision, "team", before, "batch", B, "frames", T, flush=True)
         op.enqueue(active)
         ctx.synchronize()
         # A refused team launch is an error, never a silent change of mode.
@@ -145,3 +146,32 @@ def test_decoder_dispatch_errors(abi, ctx, scope, workloads):
             op.enqueue()
     finally:
         op.release()
+
+
+@pytest.mark.parametrize("blank_bias", [2.0, 0.0], ids=["blank-favoured", "token-heavy"])
+def test_decoder_f32_profile_matches_oracle_bit_exact(abi, ctx, scope, oracle, workloads, blank_bias):
+    """The f32 profile (f32 weights and encoder rows, f32 chains): the three
+    edge windows of the f16 test, bit-exact with the oracle's f32 decode."""
+    case = workloads.tdt_case(11, 3, 188, lengths=[188, 101, 1], starts=[0, 5, 0], ends=[188, 90, 188],
+                              flush=[1, 0, 1], blank_bias=blank_bias, precision="f32")
+    assert case.weights["head_weight"].dtype == np.float32 and case.encoder_projected.dtype == np.float32
+    got = run_decoder(abi, scope, ctx, case, 512, precision="f32")
+    want = oracle_decode(oracle, case, 512)
+    print("counts", got["counts"], "oracle", want["counts"], flush=True)
+    assert_same_decode(got, want, 3)
+    np.testing.assert_array_equal(got["scratch"].view(np.uint32), want["scratch"].view(np.uint32))
+
+
+def test_decoder_f32_profile_full_size(abi, ctx, scope, oracle, workloads):
+    """16 windows x 188 frames in the f32 profile: the op chooses one
+    workgroup per window (teams are f16 only) and matches the oracle bit for
+    bit, final state included; teams of 8 / 16 are refused."""
+    case = workloads.tdt_case(12, 16, 188, flush=[0, 1] * 8, blank_bias=1.0, precision="f32")
+    got = run_decoder(abi, scope, ctx, case, 1024, precision="f32")
+    want = oracle_decode(oracle, case, 1024)
+    print("counts", got["counts"], flush=True)
+    assert_same_decode(got, want, 16)
+    np.testing.assert_array_equal(got["state"].view(np.uint32), want["state"].view(np.uint32))
+    np.testing.assert_array_equal(got["scratch"].view(np.uint32), want["scratch"].view(np.uint32))
+    with pytest.raises(abi.PaletteRangeError, match="team decoding is built for the f16 profile"):
+        run_decoder(abi, scope, ctx, case, 1024, precision="f32", team=16)

@@ -221,30 +221,38 @@ def test_node_host_package_format_on_cpu(tmp_path):
 
 @needs_node
 @pytest.mark.gpu
-def test_node_host_transcribe_from_package(tmp_path, abi, ctx, oracle, workloads):
+@pytest.mark.parametrize("precision", ["fp16", "fp32"])
+def test_node_host_transcribe_from_package(tmp_path, abi, ctx, oracle, workloads, precision):
     """End to end through the Node host: a converter-shaped synthetic
-    package (24 layers, the decoder shard) loaded by ParakeetGpuPackage,
+    package (24 layers, the decoder shard; parakeet-webgpu-v1 or
+    parakeet-webgpu-fp32-v1) loaded by ParakeetGpuPackage,
     ParakeetEncoderGraph over its tensors (4 windows of fbank, graph replay)
-    and PersistentTdtDecoderKernel over arena slices. The projector output is
-    bit-identical to the C ABI encoder run with the same weights, and the
-    token, frame and duration streams, counts and status flags are
-    bit-identical to the oracle's decode of that projector output."""
+    and PersistentTdtDecoderKernel over arena slices, in the package's
+    execution profile. The projector output is bit-identical to the C ABI
+    encoder run with the same weights, and the token, frame and duration
+    streams, counts and status flags are bit-identical to the oracle's decode
+    of that projector output."""
     import hashlib
     import package_fixture
     from test_gpu_encoder import Scope, Stack
     windows, max_tokens = 4, 2048
+    f32 = precision == "fp32"
     stack = workloads.encoder_stack(seed=41, windows=windows, frames=188, layers=24, front_end=True, projector=True,
                                     feature_lengths=[1501, 1200, 801, 37])
-    tdt = workloads.tdt_weights(np.random.default_rng(42), blank_bias=1.0)
-    manifest = package_fixture.write_package(str(tmp_path / "package"), stack, tdt)
+    if f32:
+        stack = workloads.as_f32_profile(stack)
+    tdt = workloads.tdt_weights(np.random.default_rng(42), blank_bias=1.0, precision="f32" if f32 else "f16")
+    manifest = package_fixture.write_package(str(tmp_path / "package"), stack, tdt, precision=precision)
     np.ascontiguousarray(stack.features).tofile(tmp_path / "features.bin")
-    spec = dict(manifest=manifest, manifestSha256=hashlib.sha256(open(manifest, "rb").read()).hexdigest(),
+    spec = dict(precision=precision, manifest=manifest,
+                manifestSha256=hashlib.sha256(open(manifest, "rb").read()).hexdigest(),
                 windows=windows, maxTokens=max_tokens, features=str(tmp_path / "features.bin"),
                 featureLengths=[int(v) for v in stack.feature_lengths], projected=str(tmp_path / "projected.bin"),
                 decoded=str(tmp_path / "decoded.json"))
     (tmp_path / "case.json").write_text(json.dumps(spec))
     print(run_node("host_gpu_transcribe.js", str(tmp_path / "case.json"), timeout=300), flush=True)
-    projected = np.fromfile(tmp_path / "projected.bin", dtype=np.float16).reshape(windows, 188, 640)
+    element = np.float32 if f32 else np.float16
+    projected = np.fromfile(tmp_path / "projected.bin", dtype=element).reshape(windows, 188, 640)
     scope = Scope(ctx)
     try:
         enc = Stack(abi, ctx, scope, stack)
@@ -254,7 +262,8 @@ def test_node_host_transcribe_from_package(tmp_path, abi, ctx, oracle, workloads
             enc.release()
     finally:
         scope.close()
-    np.testing.assert_array_equal(projected.reshape(-1, 640).view(np.uint16), want_projected.view(np.uint16))
+    bits = np.uint32 if f32 else np.uint16
+    np.testing.assert_array_equal(projected.reshape(-1, 640).view(bits), want_projected.view(bits))
     decoded = json.loads((tmp_path / "decoded.json").read_text())
     meta = np.asarray(decoded["metadata"], np.uint32)
     want = oracle.tdt_decode(tdt, projected, stack.valid.astype(np.uint32), max_tokens=max_tokens,

@@ -904,3 +904,93 @@ def test_decoder_flush_and_ties(oracle):
     w["head_bias"][1025 + 1] = 3.0  # ties duration 3
     scores, token, duration = oracle.tdt_joint(w, np.zeros(640, np.float16), np.zeros(640, np.float32))
     assert (token, duration) == (2, 1)
+
+
+# ---------------------------------------------------------------- TDT decoder, f32 profile
+
+
+def decoder_weights_f32(seed, **kw):
+    """The f16 test weights widened to f32, plus f32 detail below f16's
+    precision so that an f16 rounding anywhere shows."""
+    w = decoder_weights(seed, **kw)
+    rng = np.random.default_rng(seed + 1000)
+    out = {}
+    for k, v in w.items():
+        v = v.astype(np.float32)
+        if not k.endswith("bias"):
+            v = v + (rng.standard_normal(v.shape) * 1e-4 * np.abs(v).max()).astype(np.float32)
+        out[k] = v
+    return out
+
+
+def test_decoder_f32_predictor_step_matches_torch_lstm(oracle):
+    """The f32 profile's predictor step against torch's LSTMCell and a float64
+    projector product at f32 tolerance (an f16 rounding of a chain input, a
+    bias or an accumulator would leave errors near 1e-3)."""
+    w = decoder_weights_f32(1)
+    rng = np.random.default_rng(2)
+    state = (rng.standard_normal((4, 640)) * 0.3).astype(np.float32)
+    cand = oracle.tdt_predictor(w, 37, state)
+    x = w["embedding"][37].astype(np.float64)
+    h0, c0 = torch_lstm_layer(w["lstm_weight_l0"], w["lstm_bias_l0"], x, state[0], state[1])
+    h1, c1 = torch_lstm_layer(w["lstm_weight_l1"], w["lstm_bias_l1"], cand[0].astype(np.float64), state[2], state[3])
+    proj = cand[2].astype(np.float64) @ w["projector_weight"].astype(np.float64) + w["projector_bias"]
+    for got, want in ((cand[0], h0), (cand[1], c0), (cand[2], h1), (cand[3], c1), (cand[4], proj)):
+        assert np.abs(got - want).max() <= 2e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
+    # the start token: the gates are the f32 biases themselves, not f16-rounded
+    start = oracle.tdt_predictor(w, 0, np.zeros((4, 640), np.float32), initial=True)
+    g = w["lstm_bias_l0"].astype(np.float64)
+    sig = lambda v: 1 / (1 + np.exp(-np.clip(v, -20, 20)))  # noqa: E731
+    c_closed = sig(g[:640]) * np.tanh(g[1280:1920])
+    np.testing.assert_allclose(start[1], c_closed, rtol=0, atol=2e-7)
+    np.testing.assert_allclose(start[0], sig(g[1920:]) * np.tanh(c_closed), rtol=0, atol=2e-7)
+
+
+def test_decoder_f32_joint_matches_a_float64_product(oracle):
+    w = decoder_weights_f32(3)
+    rng = np.random.default_rng(4)
+    row = (rng.standard_normal(640) * 0.5).astype(np.float32)
+    proj = (rng.standard_normal(640) * 0.5).astype(np.float32)
+    scores, token, duration = oracle.tdt_joint(w, row, proj)
+    joint = np.maximum((row + proj).astype(np.float64), 0)
+    want = joint @ w["head_weight"].astype(np.float64) + w["head_bias"]
+    assert np.abs(scores[:1030] - want[:1030]).max() <= 1e-5 * np.abs(want).max()
+    assert token == int(np.argmax(scores[:1025])) and duration == int(np.argmax(scores[1025:1030]))
+
+
+def test_decoder_f32_chain_order_closed_forms(oracle):
+    """Values that only f32 holds fix the f32 chains' order and rounding:
+    the head column 2^24, 1, -2^24 over k = 0, 1, 2 with unit inputs gives 0
+    in one increasing-k chain with one rounding per fma (2^24 + 1 rounds to
+    2^24), where the exact sum is 1 and a decreasing chain gives 1. The
+    same values on LSTM rows 0 (even), 1 (odd), 2 (even) of the g gate give
+    gate 1 with the even / odd split (even: 2^24 - 2^24 = 0, odd: 1) and 0
+    in one chain."""
+    w = {k: np.zeros_like(v) for k, v in decoder_weights_f32(9, lstm_std=0.0).items()}
+    big = np.float32(2.0 ** 24)
+    w["head_weight"][0, 5], w["head_weight"][1, 5], w["head_weight"][2, 5] = big, 1.0, -big
+    w["head_weight"][:3, 6] = [1.0, 1.0, 1.0]  # a column the chain sums exactly: 3
+    scores, token, _ = oracle.tdt_joint(w, np.ones(640, np.float32), np.zeros(640, np.float32))
+    assert scores[5] == 0.0 and scores[6] == 3.0 and token == 6
+    # LSTM layer 0, g gate of channel 0 (column 1280): x = embedding row (ones), h0 = 0
+    w["embedding"][3] = 1.0
+    w["lstm_weight_l0"][0, 1280], w["lstm_weight_l0"][1, 1280], w["lstm_weight_l0"][2, 1280] = big, 1.0, -big
+    cand = oracle.tdt_predictor(w, 3, np.zeros((4, 640), np.float32))
+    # i = f = o = sigmoid(0) = 1/2, g = tanh(1), c_prev = 0: c = tanh(1) / 2
+    assert cand[1, 0] == pytest.approx(0.5 * np.tanh(1.0), abs=2e-7)
+    assert cand[1, 1] == 0.0
+
+
+def test_decoder_f32_control_closed_forms(oracle):
+    """The decode loop is shared by both profiles: a fixed f32 head answers
+    token 7 with duration 2, and f32 encoder rows are read as f32."""
+    base = decoder_weights_f32(5, lstm_std=0.0)
+    head = fixed_head({k: v for k, v in base.items()}, 7, 2)
+    head["head_weight"] = head["head_weight"].astype(np.float32)
+    enc = np.zeros((1, 12, 640), np.float32)
+    r = oracle.tdt_decode(head, enc, [11], max_tokens=64)
+    assert r["counts"][0] == 6 and list(r["frames"][0][:6]) == [0, 2, 4, 6, 8, 10]
+    with pytest.raises(ValueError, match="must be float32"):
+        bad = dict(head)
+        bad["head_weight"] = bad["head_weight"].astype(np.float16)
+        oracle.tdt_decode(bad, enc, [11], max_tokens=64)
