@@ -725,7 +725,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     if tdt:
         meta = tdt_out["metadata"].download()
         decoded = {"avg_ms": decoder_ms, "tokens_per_window": [int(v) for v in meta[:active]],
-                   "overflow_windows": int((meta[stack.batch:stack.batch + active] != 0).sum()),
+                   **abi.decode_tdt_status(meta[stack.batch:stack.batch + active]),
                    "kernel": "tdt_team_kernel" if tdt.team_size() > 1 else "tdt_decode_kernel",
                    "workgroups_per_window": tdt.team_size(), "workgroups": active * tdt.team_size(),
                    "max_tokens": 1024}

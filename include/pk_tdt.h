@@ -114,6 +114,13 @@ int pk_tdt_enqueue_timed(pk_tdt_op *op, uint32_t active_batch, void *stream, voi
    PK_TDT_SYNC_TIMEOUT status). Results are bit-identical for every size.
    Teams are built for the f16 profile: an f32 op always runs one
    workgroup per window (0 chooses 1; 8 and 16 return PK_RANGE_ERROR).
+   A team launch is an ordinary launch whose grid fits the workgroups an
+   idle device holds at once: kernels running on other streams at the same
+   time can keep members from being resident, and a barrier that then
+   waits 2^24 polls gives up, so a team decode that overlaps other work can
+   end with PK_TDT_SYNC_TIMEOUT in its windows' status words. Callers check
+   the status words (overflow and sync timeout are separate bits) and
+   decode such windows again, or use team size 1, which never waits.
    The create call chooses automatically; the setter synchronizes the
    device. A team launch that the runtime refuses returns PK_DEVICE_ERROR
    and leaves the team size as it was. */
@@ -136,7 +143,9 @@ int pk_tdt_release(pk_tdt_op *op);
    op. At most PK_TDT_STATIC_MAX_WINDOWS windows (PK_RANGE_ERROR beyond).
    Every call on one GPU shares that array: calls whose decodes overlap on
    the same GPU (other streams, other threads) race and must be ordered by
-   the caller. */
+   the caller. The call may be recorded into a HIP graph (the counters are
+   cleared by a kernel, not a memset); a team replayed beside other work
+   can end with PK_TDT_SYNC_TIMEOUT as described at pk_tdt_set_team_size. */
 #define PK_TDT_STATIC_MAX_WINDOWS 64u
 int pk_tdt_decode_static(pk_context *ctx, const pk_tdt_desc *desc, uint32_t members, void *stream);
 

@@ -137,10 +137,7 @@ namespace {
 void weight_unref(pk_prepared_weight* w) {
   if (!w) return;
   if (w->refs.fetch_sub(1) == 1) {
-    if (w->codes) {
-      (void)hipSetDevice(w->ctx->device);
-      (void)hipFree(w->codes);
-    }
+    free_after_drain(w->ctx->device, w->codes);
     delete w;
   }
 }
@@ -198,7 +195,7 @@ int relayout_weight(pk_prepared_weight* w, int parts, hipStream_t stream) {
     (void)hipFree(codes);
     return fail(PK_DEVICE_ERROR, "%s: palette code relayout failed: %s", w->label.c_str(), hipGetErrorString(e));
   }
-  (void)hipFree(w->codes);
+  free_after_drain(w->ctx->device, w->codes);
   w->codes = codes;
   w->parts = parts;
   w->bytes = bytes;
@@ -1108,25 +1105,15 @@ int pk_gemm_destroy(pk_gemm_op* op) {
   op->destroyed = true;
   weight_unref(op->weight);
   op->weight = nullptr;
-  if (op->norm_buffer) {
-    (void)hipSetDevice(op->ctx->device);
-    (void)hipStreamSynchronize(op->ctx->stream);
-    (void)hipFree(op->norm_buffer);
-    op->norm_buffer = nullptr;
-  }
-  if (op->post_counters) {
-    (void)hipSetDevice(op->ctx->device);
-    (void)hipStreamSynchronize(op->ctx->stream);
-    (void)hipFree(op->post_counters);
-    op->post_counters = nullptr;
-  }
-  if (op->workspace) {
-    (void)hipSetDevice(op->ctx->device);
-    (void)hipStreamSynchronize(op->ctx->stream);
-    (void)hipFree(op->workspace);
-    op->workspace = nullptr;
-    op->workspace_bytes = 0;
-  }
+  // the op may have been enqueued on a caller's stream: every free waits
+  // for the device to drain
+  free_after_drain(op->ctx->device, op->norm_buffer);
+  op->norm_buffer = nullptr;
+  free_after_drain(op->ctx->device, op->post_counters);
+  op->post_counters = nullptr;
+  free_after_drain(op->ctx->device, op->workspace);
+  op->workspace = nullptr;
+  op->workspace_bytes = 0;
   return ok();
 }
 
@@ -1439,9 +1426,7 @@ int pk_gemm_group_plan(const pk_gemm_group* g, uint32_t active_rows, pk_gemm_pla
 
 int pk_gemm_group_destroy(pk_gemm_group* g) {
   if (!g) return ok();
-  (void)hipSetDevice(g->ctx->device);
-  (void)hipStreamSynchronize(g->ctx->stream);
-  if (g->table) (void)hipFree(g->table);
+  free_after_drain(g->ctx->device, g->table);
   for (pk_prepared_weight* w : g->weights) weight_unref(w);
   delete g;
   return ok();

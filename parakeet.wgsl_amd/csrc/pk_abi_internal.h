@@ -67,6 +67,17 @@ inline hipStream_t stream_or_default(pk_context* ctx, void* stream) {
   return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }
 
+// Frees device memory that launches on any stream may still read (an op's
+// buffers, a weight shared by ops enqueued on callers' streams): the
+// device drains first, since hipFree alone is not ordered after work
+// enqueued on other streams.
+inline void free_after_drain(int device, void* p) {
+  if (!p) return;
+  (void)hipSetDevice(device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(p);
+}
+
 }  // namespace pk_abi
 
 #define PK_HIP(call, what)                                                                       \

@@ -119,11 +119,8 @@ void release_encoder(pk_encoder* e) {
   e->ops.clear();
   pk_gemm_release(e->projector);
   e->projector = nullptr;
-  if (e->arena) {
-    (void)hipSetDevice(e->ctx->device);
-    (void)hipFree(e->arena);
-    e->arena = nullptr;
-  }
+  free_after_drain(e->ctx->device, e->arena);
+  e->arena = nullptr;
 }
 
 // One palette GEMM of the graph, in the encoder's precision, over `rows` rows.

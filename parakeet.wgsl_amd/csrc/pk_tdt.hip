@@ -418,7 +418,8 @@ __global__ __launch_bounds__(kTdtThreads) void tdt_decode_kernel(TdtArgs a) {
 // slices in global memory with relaxed agent-scope atomic loads and stores
 // (coherent across the XCDs' L2s without cache maintenance), ordered by team
 // barriers: every wave's stores complete (workgroup release), then an
-// atomic arrival count and a bounded poll. Agent-scope fences would write
+// atomic arrival count and a bounded poll (team_barrier states what of the
+// code generation this ordering rests on). Agent-scope fences would write
 // back and invalidate the XCD's whole L2 at every barrier, which measured
 // slower than one workgroup per window; the weights, read with ordinary
 // loads, stay cached. A barrier that waits
@@ -552,10 +553,26 @@ __device__ __forceinline__ void load_exchanged_f16(_Float16* dst, const float* s
 }
 
 // One team barrier: the n-th barrier of a window waits for count >= P * n.
+//
+// Ordering. The exchanged values and the counter are relaxed agent-scope
+// atomics, which order nothing among themselves in the C++ / HIP model;
+// what orders them here is gfx950's code generation, on which this relies:
+// (1) a relaxed agent-scope store or load is a global store / load with the
+// sc1 bit, performed at the agent's coherence point rather than in an
+// XCD's L2; (2) vmcnt counts stores as well as loads (gfx9), so
+// s_waitcnt(0) returns only once every earlier store of the wave has been
+// acknowledged there; (3) a member polls the counter until it reaches the
+// target before any load that follows the barrier issues. The signal
+// fences keep the compiler from moving exchanged accesses across the
+// arrival or above the end of the poll. Formal release / acquire at agent
+// scope would add an L2 write-back and invalidate to every barrier, and the
+// invalidate evicts the weight slices the members re-read from their XCD's
+// L2 at every step (measured slower than one workgroup per window).
 __device__ bool team_barrier(TeamShared& s, const TdtTeam& tm, uint32_t b, uint32_t& n) {
   ++n;
   // every wave waits for its exchanged (coherent) stores to complete before
   // the arrival; a workgroup barrier alone does not wait for them
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -582,6 +599,7 @@ __device__ bool team_barrier(TeamShared& s, const TdtTeam& tm, uint32_t b, uint3
     s.failed = failed;
   }
   __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return s.failed == 0;
 }
 

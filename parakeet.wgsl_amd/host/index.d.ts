@@ -551,6 +551,10 @@ export declare const ENCODER_LAYER_DISPATCHES: 15;
 /* ------------------------------------------------------------ TDT decoder */
 
 export declare const TDT_DECODER_OVERFLOW: 1;
+/** A team barrier gave up waiting (this library only). */
+export declare const TDT_DECODER_SYNC_TIMEOUT: 2;
+/** The causes in one window's status word. */
+export declare function decodeTdtStatus(word: number): { overflow: boolean; syncTimeout: boolean; unknown: number };
 export declare const TDT_BLANK_TOKEN: 1024;
 
 /** tdt-decoder.ts:39-52 (one workgroup per window here). */

@@ -1754,6 +1754,24 @@ const TDT_TOKEN_OUTPUTS = 1025;
 const TDT_BLANK_TOKEN = 1024;
 const TDT_HEAD_STORAGE_OUTPUTS = 1032;
 const TDT_DECODER_OVERFLOW = 1;
+/** Status bit of a team barrier that gave up waiting (no reference counterpart). */
+const TDT_DECODER_SYNC_TIMEOUT = 2;
+
+/**
+ * The causes in one window's status word (the metadata's second half):
+ * overflow (more tokens than maxTokens, tdt-decoder.ts:1756-1775),
+ * syncTimeout (a team barrier gave up: the window's outputs are incomplete
+ * and it must be decoded again) and any bits this library does not define.
+ */
+function decodeTdtStatus(word) {
+  if (!isSafe(word) || word < 0 || word > 0xffffffff) throw new RangeError("TDT status must be a u32 word");
+  const known = TDT_DECODER_OVERFLOW | TDT_DECODER_SYNC_TIMEOUT;
+  return {
+    overflow: (word & TDT_DECODER_OVERFLOW) !== 0,
+    syncTimeout: (word & TDT_DECODER_SYNC_TIMEOUT) !== 0,
+    unknown: ((word >>> 0) & ~known) >>> 0,
+  };
+}
 
 /**
  * planTdtDecoderExecution (tdt-decoder.ts:39-52). This library runs one
@@ -1967,6 +1985,8 @@ module.exports = {
   PersistentTdtDecoderKernel,
   TdtDecoderDispatch,
   TDT_DECODER_OVERFLOW,
+  TDT_DECODER_SYNC_TIMEOUT,
+  decodeTdtStatus,
   TDT_BLANK_TOKEN,
   ...require("./package.js"),
 };

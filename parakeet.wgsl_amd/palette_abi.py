@@ -1221,6 +1221,20 @@ def tdt_desc(*, weights: dict, encoder_projected, encoded_lengths, decode_starts
 
 
 TDT_STATIC_MAX_WINDOWS = 64  # PK_TDT_STATIC_MAX_WINDOWS
+TDT_OVERFLOW = 1       # PK_TDT_OVERFLOW: more tokens than max_tokens (tdt-decoder.ts:1756-1775)
+TDT_SYNC_TIMEOUT = 2   # PK_TDT_SYNC_TIMEOUT: a team barrier gave up waiting (no reference counterpart)
+
+
+def decode_tdt_status(status) -> dict:
+    """Counts of the decoder's per-window status words by cause: windows
+    whose tokens overflowed max_tokens, windows whose team barrier timed out
+    (their outputs are incomplete and must be decoded again), and windows
+    with bits this library does not define."""
+    words = np.asarray(status, dtype=np.uint32).reshape(-1)
+    known = TDT_OVERFLOW | TDT_SYNC_TIMEOUT
+    return {"overflow_windows": int(((words & TDT_OVERFLOW) != 0).sum()),
+            "sync_timeout_windows": int(((words & TDT_SYNC_TIMEOUT) != 0).sum()),
+            "unknown_status_windows": int(((words & ~np.uint32(known)) != 0).sum())}
 
 
 def tdt_decode_static(ctx: Context, members: int = 0, stream=None, **descriptor) -> None:

@@ -294,6 +294,22 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
     }).then(() => assert.fail("created"), (e) => {
       assert.strictEqual(e.message, "encoder.layers.0.norm_feed_forward1.weight source must be float32 channel, " +
                          "logical [1024], storage [1024]");
+      // requireEncoderConfig (encoder.ts:2588-2593): the profile must match the package
+      const fp16Model = { precision: "fp16", tensor() { throw new Error("no tensor expected"); } };
+      return host.ParakeetEncoderGraph.create({}, fp16Model, { executionProfile: { precision: "fp32" } });
+    }).then(() => assert.fail("created"), (e) => {
+      assert.strictEqual(e.message, "Parakeet fp32 encoder cannot use fp16 model weights");
+      const fp32Model = { precision: "fp32", tensor() { throw new Error("no tensor expected"); } };
+      return host.PersistentTdtDecoderKernel.create({}, arena, fp32Model, { precision: "fp16" });
+    }).then(() => assert.fail("created"), (e) => {
+      assert.strictEqual(e.message, "TDT decoder fp16 profile cannot use fp32 decoder weights");
+      // status words: overflow and team sync timeout are separate causes
+      assert.strictEqual(host.TDT_DECODER_SYNC_TIMEOUT, 2);
+      assert.deepStrictEqual(host.decodeTdtStatus(0), { overflow: false, syncTimeout: false, unknown: 0 });
+      assert.deepStrictEqual(host.decodeTdtStatus(1), { overflow: true, syncTimeout: false, unknown: 0 });
+      assert.deepStrictEqual(host.decodeTdtStatus(2), { overflow: false, syncTimeout: true, unknown: 0 });
+      assert.deepStrictEqual(host.decodeTdtStatus(0x80000003), { overflow: true, syncTimeout: true, unknown: 0x80000000 });
+      assert.throws(() => host.decodeTdtStatus(-1), RangeError);
       console.log("host_cpu ok");
     });
   });

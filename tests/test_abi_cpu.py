@@ -663,18 +663,20 @@ def test_subsampling_null_handles(abi):
 # ---------------------------------------------------------------- TDT decoder
 
 
-def _tdt_fakes(batch=16, frames=188, max_tokens=256):
+def _tdt_fakes(batch=16, frames=188, max_tokens=256, elem=2):
+    """Nominal addresses and sizes of a decoder descriptor; `elem` is the
+    profile's weight and encoder-row element (2: f16, 4: f32)."""
     at = [0x6000000000]
 
     def take(nbytes):
         addr = at[0]
         at[0] += (nbytes + 0xFFFF) // 0x10000 * 0x10000
         return (addr, nbytes)
-    weights = {"embedding": take(1025 * 640 * 2), "lstm_weight_l0": take(1280 * 2560 * 2),
-               "lstm_weight_l1": take(1280 * 2560 * 2), "lstm_bias_l0": take(2560 * 4),
-               "lstm_bias_l1": take(2560 * 4), "projector_weight": take(640 * 640 * 2),
-               "projector_bias": take(640 * 4), "head_weight": take(640 * 1032 * 2), "head_bias": take(1032 * 4)}
-    return dict(weights=weights, encoder_projected=take(batch * frames * 640 * 2), encoded_lengths=take(4 * batch),
+    weights = {"embedding": take(1025 * 640 * elem), "lstm_weight_l0": take(1280 * 2560 * elem),
+               "lstm_weight_l1": take(1280 * 2560 * elem), "lstm_bias_l0": take(2560 * 4),
+               "lstm_bias_l1": take(2560 * 4), "projector_weight": take(640 * 640 * elem),
+               "projector_bias": take(640 * 4), "head_weight": take(640 * 1032 * elem), "head_bias": take(1032 * 4)}
+    return dict(weights=weights, encoder_projected=take(batch * frames * 640 * elem), encoded_lengths=take(4 * batch),
                 decode_starts=take(4 * batch), decode_ends=take(4 * batch), flush_finals=take(4 * batch),
                 state=take(batch * 4 * 640 * 4), predictor_scratch=take(batch * 5 * 640 * 4),
                 tokens=take(batch * max_tokens * 4), token_frames=take(batch * max_tokens * 4),
@@ -716,6 +718,41 @@ def test_tdt_plan_and_contract(abi):
     lib = abi.load()
     assert lib.pk_tdt_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
     assert lib.pk_tdt_destroy(None) == abi.OK
+
+
+def test_tdt_f32_profile_contract(abi):
+    """The f32 profile (tdt-decoder.ts:196-218, :378-405): f32 weights and
+    encoder rows are twice the f16 sizes; an f16-sized tensor in an f32
+    descriptor, or the reverse, is the reference's "Unexpected decoder
+    tensor" error, and a short f32 encoder slice its range error."""
+    _validate_tdt(abi, precision="f32", **_tdt_fakes(elem=4))
+    kw = _tdt_fakes(elem=2)
+    kw["encoder_projected"] = _tdt_fakes(elem=4)["encoder_projected"]  # slices first, then the f16-sized weights
+    with pytest.raises(abi.PaletteError, match=re.escape("Unexpected decoder tensor token-by-channel-row-major [1025,640]")):
+        _validate_tdt(abi, precision="f32", **kw)
+    with pytest.raises(abi.PaletteError, match="Unexpected decoder tensor"):
+        _validate_tdt(abi, **_tdt_fakes(elem=4))
+    kw = _tdt_fakes(elem=4)
+    kw["encoder_projected"] = (kw["encoder_projected"][0], 16 * 188 * 640 * 2)
+    with pytest.raises(abi.PaletteRangeError, match="encoderProjected is too small for TDT decoding"):
+        _validate_tdt(abi, precision="f32", **kw)
+    desc = abi.tdt_desc(**_tdt_fakes())
+    desc.precision = 7
+    with pytest.raises(abi.PaletteError, match="TDT decoder precision must be f16 or f32"):
+        abi.check(abi.load().pk_tdt_validate(ctypes.byref(desc)))
+
+
+def test_tdt_status_decoding(abi):
+    """Overflow and team sync timeout are separate bits of a window's
+    status word, counted apart (a timed-out window must be decoded again;
+    an overflowed one is complete up to max_tokens)."""
+    assert (abi.TDT_OVERFLOW, abi.TDT_SYNC_TIMEOUT) == (1, 2)
+    got = abi.decode_tdt_status(np.array([0, 1, 2, 3, 0, 2, 8], np.uint32))
+    assert got == {"overflow_windows": 2, "sync_timeout_windows": 3, "unknown_status_windows": 1}
+    assert abi.decode_tdt_status([]) == {"overflow_windows": 0, "sync_timeout_windows": 0,
+                                         "unknown_status_windows": 0}
+    header = open(os.path.join(ROOT, "include", "pk_tdt.h")).read()
+    assert re.search(r"#define PK_TDT_OVERFLOW 1u", header) and re.search(r"#define PK_TDT_SYNC_TIMEOUT 2u", header)
 
 
 # ---------------------------------------------------------------- encoder stack

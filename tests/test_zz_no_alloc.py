@@ -1,7 +1,8 @@
 """The allocation-free decoder entry point (pk_tdt_decode_static) against
 the op path it varies (pk_tdt_create + pk_tdt_enqueue), bit-exact: two calls
 in a row, the second over fewer windows, so the second reuses the static team
-buffers the first left behind."""
+buffers the first left behind; and the call recorded into a HIP graph,
+replayed beside eager work."""
 import numpy as np
 import pytest
 
@@ -96,3 +97,38 @@ def test_static_decode_rejects_more_windows_than_its_buffers(abi, ctx, scope, wo
     out = _slices(scope, case, 16)
     with pytest.raises(abi.PaletteError, match="exceed the 64 of the static decoder buffers"):
         abi.tdt_decode_static(ctx, 0, None, **inputs, **out)
+
+
+@pytest.mark.parametrize("members", [16, 1], ids=["team16", "single"])
+def test_static_decode_replays_from_a_graph(abi, ctx, scope, workloads, members):
+    """pk_tdt_decode_static recorded into a HIP graph (the code it serves):
+    three replays, each after eager work on the same stream (another
+    decode through the op path and a reset of the outputs), each bit-exact
+    with the op path's decode of the captured inputs."""
+    max_tokens = 512
+    case = workloads.tdt_case(6, 6, 150, lengths=[150, 90, 1, 75, 149, 120], flush=[1, 0, 1, 1, 0, 1],
+                              blank_bias=0.5)
+    inputs = _descriptor(abi, scope, case, max_tokens)
+    want, _ = _op_decode(abi, ctx, scope, inputs, case, max_tokens)
+    other = workloads.tdt_case(7, 4, 100)
+    other_inputs = _descriptor(abi, scope, other, 256)
+    out = _slices(scope, case, max_tokens)
+    stream = ctx.stream
+    abi.tdt_decode_static(ctx, members, stream, **inputs, **out)  # the device address lookup happens eagerly
+    ctx.synchronize(stream)
+    graph = abi.Graph.capture(ctx, stream)
+    with graph:
+        abi.tdt_decode_static(ctx, members, stream, **inputs, **out)
+    try:
+        for replay in range(3):
+            _op_decode(abi, ctx, scope, other_inputs, other, 256)  # eager work between the replays
+            for key in ("tokens", "token_frames", "token_durations"):
+                out[key].upload(np.full((case.batch, max_tokens), SENTINEL, np.uint32))
+            out["metadata"].upload(np.full(2 * case.batch, SENTINEL, np.uint32))
+            out["state"].upload(np.full((case.batch, 4, 640), 7.0, np.float32))
+            graph.launch()
+            ctx.synchronize(stream)
+            print("graph replay", replay, "members", members, flush=True)
+            _assert_same(_download(out, case.batch), want)
+    finally:
+        graph.release()
