@@ -93,9 +93,6 @@ def parse_args():
     p.add_argument("--separate-glu", action="store_true",
                    help="encoder workloads: the convolution forms the GLU from PW1's values and gates, as the "
                         "reference does (PK_ENCODER_SEPARATE_GLU; default: PW1's epilogue writes the GLU)")
-    p.add_argument("--post-norms", action="store_true",
-                   help="encoder workloads: each residual GEMM writes the LayerNorm after it "
-                        "(PK_ENCODER_POST_NORMS; default: separate LayerNorm launches)")
     p.add_argument("--unchained-norms", action="store_true",
                    help="encoder workloads: launch every LayerNorm on its own (default: each layer's last "
                         "LayerNorm also writes the next layer's first)")
@@ -107,6 +104,9 @@ def parse_args():
                         "two-launch steps)")
     p.add_argument("--dense-probe", default="", help=argparse.SUPPRESS)
     p.add_argument("--variant", type=int, default=-1, help="force a tile variant (sweeps)")
+    p.add_argument("--split-trace", default="",
+                   help="CPU only: per launch kind of a rocprofv3 kernel trace (CSV) of the encoder bench run "
+                        "with the given --steps / --warmup")
     return p.parse_args()
 
 
@@ -404,12 +404,133 @@ WINDOW_SECONDS = 15.0  # audio per encoder window: 1500 fbank frames at 100/s, 8
 
 # The LayerNorms that run inside the GEMM after them with --fused-norms.
 FUSED_NORMS = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2")
-# LayerNorm slot -> the residual GEMM that writes it (PK_GEMM_POST_NORM)
-POST_NORMS = {"norm_self_att": "feed-forward1-linear2-residual", "norm_conv": "self-attention-output-residual",
-              "norm_feed_forward2": "convolution-pointwise2-residual", "norm_out": "feed-forward2-linear2-residual"}
 
 FRONT_DISPATCHES = ("subsampling-fused-conv0-depthwise2", "subsampling-pointwise3", "subsampling-depthwise5",
                     "subsampling-pointwise6", "subsampling-pointwise6-mask", "subsampling-flatten-project")
+
+# The layer GEMMs as the encoder creates them (dispatch kind -> weight key,
+# K, N, palette groups, activation, residual scale): the roofline's
+# back-to-back loop rebuilds the dominant kind's op at the pass's shape.
+LAYER_GEMMS = {
+    "feed-forward1-linear1": ("ff1_linear1", 1024, 4096, 1, "silu", None),
+    "feed-forward1-linear2-residual": ("ff1_linear2", 4096, 1024, 1, "none", 0.5),
+    "self-attention-qkv": ("qkv", 1024, 3072, 3, "none", None),
+    "self-attention-output-residual": ("o_proj", 1024, 1024, 1, "none", 1.0),
+    "convolution-pointwise2-residual": ("pointwise2", 1024, 1024, 1, "none", 1.0),
+}
+ROOFLINE_LOOP = (5, 50)  # warm-up and timed launches of the back-to-back loop
+
+
+def launch_sequence(layers, chained=True, fused_norms=()):
+    """The dispatch kinds of one encoder pass in launch order: the front
+    end, every layer's launched slots (a chained LN ff1 of a later layer or
+    a fused LayerNorm launches nothing) and the projector."""
+    from parakeet_wgsl_amd.palette_abi import ENCODER_DISPATCHES
+    seq = list(FRONT_DISPATCHES)
+    for layer in range(layers):
+        for name in ENCODER_DISPATCHES:
+            if chained and layer > 0 and name == "norm_feed_forward1":
+                continue
+            if name in fused_norms:
+                continue
+            seq.append(name)
+    seq.append("projector")
+    return seq
+
+
+def kernel_family(kind):
+    """Substring the kernel name of a launch of `kind` carries."""
+    if kind.startswith("norm_"):
+        return "layernorm_kernel"
+    if kind == "relative-attention":
+        return "attention"
+    if kind == "convolution-glu-depthwise-bn-silu":
+        return "conformer_conv_kernel"
+    if kind in ("subsampling-fused-conv0-depthwise2", "subsampling-depthwise5", "subsampling-pointwise6-mask"):
+        return "subsampling_"
+    return "gemm_f16"
+
+
+def split_trace(path, warmup, steps, layers=24):
+    """Per launch kind of the encoder bench, from a rocprofv3 kernel trace
+    (CSV) of `bench.py --no-cpu --no-dense --no-ff-block --steps S --warmup
+    W`: passes start at the fused subsampling kernel; each pass's launches
+    are mapped to kinds in launch order (every kernel name checked against
+    its kind), the passes split into graph replays and the stamped passes
+    (every TIMING_STRIDE-th timed step), and the launches after the last
+    pass that run the dominant kernel form the roofline's back-to-back
+    loop. Prints a markdown table."""
+    import csv
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    seq = launch_sequence(layers)
+    starts = [i for i, r in enumerate(rows) if "subsampling_fused_kernel" in r["Kernel_Name"]]
+    if len(starts) != warmup + steps:
+        raise SystemExit(f"{len(starts)} passes in the trace, expected {warmup + steps}")
+    per = {"graph": {}, "stamped": {}}
+    sums = {"graph": [], "stamped": []}
+    for p, i in enumerate(starts):
+        seg = rows[i:i + len(seq)]
+        kind = "stamped" if p >= warmup and (p - warmup) % TIMING_STRIDE == 0 else "graph"
+        total = 0.0
+        for name, r in zip(seq, seg):
+            if kernel_family(name) not in r["Kernel_Name"]:
+                raise SystemExit(f"pass {p}: {name} ran {r['Kernel_Name']}")
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            per[kind].setdefault(name, []).append(us)
+            total += us
+        sums[kind].append(total / 1e3)
+    tail = rows[starts[-1] + len(seq):]
+    print("| launch kind | launches | stamped passes us | graph passes us | grid |")
+    print("|---|---:|---:|---:|---:|")
+    grids = {}
+    for name, r in zip(seq, rows[starts[-1]:starts[-1] + len(seq)]):
+        grids.setdefault(name, r["Grid_Size_X"])
+    for name in dict.fromkeys(seq):
+        st, gr = per["stamped"].get(name, []), per["graph"].get(name, [])
+        print(f"| {name} | {len(st) + len(gr)} | {np.mean(st):.2f} | {np.mean(gr):.2f} | {grids[name]} |")
+    print()
+    print(f"kernel time per pass: stamped {np.mean(sums['stamped']):.3f} ms, graph {np.mean(sums['graph']):.3f} ms")
+    loop_warm, loop_n = ROOFLINE_LOOP
+    if len(tail) >= loop_warm + loop_n:
+        loop = tail[:loop_warm + loop_n]
+        names = {r["Kernel_Name"] for r in loop}
+        us = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in loop[loop_warm:]])
+        print(f"roofline loop: {loop_n} back-to-back launches of {sorted(names)} (grid {loop[-1]['Grid_Size_X']}): "
+              f"avg {us.mean():.2f} us, min {us.min():.2f}, max {us.max():.2f}")
+
+
+def roofline_loop(ctx, abi, kind, layer0, a_rows, stream):
+    """Average duration of `kind`'s GEMM (rebuilt from LAYER_GEMMS with layer
+    0's weights at the pass's shape) over ROOFLINE_LOOP back-to-back launches
+    on `stream`, timed by one pair of events around the loop: the condition
+    of the graph replay, where every launch follows the last with no gap."""
+    key, inner, columns, groups, activation, scale = LAYER_GEMMS[kind]
+    packed, palette = layer0[key]
+    rows = a_rows.shape[0]
+    dtype = a_rows.dtype
+    a = a_rows if inner == a_rows.shape[1] else ctx.empty((rows, inner), dtype)
+    out = ctx.empty((rows, columns), dtype)
+    residual = a_rows if scale is not None else None
+    op = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=out, bits=5 if key != "o_proj" else 6,
+                    rows=rows, inner=inner, columns=columns, activation=activation, residual=residual,
+                    residual_scale=scale, label=f"roofline-loop-{kind}")
+    try:
+        warm, n = ROOFLINE_LOOP
+        for _ in range(warm):
+            op.enqueue(0, stream)
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record(stream)
+        for _ in range(n):
+            op.enqueue(0, stream)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / n * 1e3
+    finally:
+        op.release()
+        if a is not a_rows:
+            a.free()
+        out.free()
 
 
 def gemm_cost(rows, inner, columns, bits=5, groups=1, residual=False, bias=False, elem=2):
@@ -549,7 +670,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     stack = wl.encoder_stack(0, windows=args.windows, frames=188, layers=24, front_end=True, projector=True)
     f32 = args.precision == "f32"
     if f32:
-        if decoder or args.fused_norms or args.post_norms:
+        if decoder or args.fused_norms:
             raise SystemExit("--precision f32 runs the encoder workload without the f16-only fusions")
         stack = wl.as_f32_profile(stack)
     active = args.active or stack.batch
@@ -578,15 +699,13 @@ def run_encoder(args, abi, ctx, decoder=False):
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
                         projected_output=projected, fused_norms=args.fused_norms,
-                        unchained_norms=args.unchained_norms, post_norms=args.post_norms,
+                        unchained_norms=args.unchained_norms,
                         fused_glu=not args.separate_glu, label="encoder",
                         precision=args.precision)
     launches, device_bytes = enc.info()
     fused_norms = set(FUSED_NORMS) if args.fused_norms else set()
     # the LN ff1 of layers after the first runs in the LN out launch before it
     chained = not (args.fused_norms or args.unchained_norms) and len(stack.layers) > 1
-    # the LayerNorms after the residual GEMMs, written by those GEMMs
-    post = args.post_norms
     stream = ctx.stream
     tdt = None
     if decoder:
@@ -650,23 +769,6 @@ def run_encoder(args, abi, ctx, decoder=False):
     dispatches = {}
     for name, ms, (flops, nbytes) in zip(names, per_kind_ms, costs):
         us = ms * 1e3
-        if post and name in POST_NORMS:
-            # written by the residual GEMM before it; the slot's two events are
-            # back to back. That GEMM's bytes gain the LayerNorm's outputs and
-            # parameters (its input is the GEMM's own output): for LN out also
-            # the chained LN ff1 of the next layer, averaged over the layers
-            act = (nbytes - 2 * 4096) / 2
-            extra = act + 2 * 4096
-            if chained and name == "norm_out":
-                n = len(stack.layers)
-                extra = ((n - 1) * 2 * extra + extra) / n
-            gemm = dispatches[POST_NORMS[name]]
-            gemm["algorithmic_bytes"] += extra
-            gemm["gbs"] = gemm["algorithmic_bytes"] / (gemm["avg_us"] * 1e-6) / 1e9
-            gemm["writes_layernorm"] = name
-            dispatches[name] = {"avg_us": us, "written_by": POST_NORMS[name], "flops": 0, "algorithmic_bytes": 0,
-                                "launches_per_pass": 0}
-            continue
         if chained and name == "norm_feed_forward1":
             # layer 0's own launch; later layers' slots are empty (written by norm_out)
             us = durations[nf + list(abi.ENCODER_DISPATCHES).index(name)] * 1e3
@@ -704,12 +806,26 @@ def run_encoder(args, abi, ctx, decoder=False):
     name = max(per_kind, key=per_kind.get)
     dom = dispatches[name]
     peak = PEAK_TFLOPS[args.precision]
+    # The roofline times the dominant launch kind back to back (the graph
+    # replay's condition: measured 6-10% slower per launch than the same
+    # kernel isolated between stamped launches); the stamped in-pass figure
+    # is kept beside it.
+    loop_us = None
+    if name in LAYER_GEMMS:
+        loop_us = roofline_loop(ctx, abi, name, layers[0], out, stream)
+    us = loop_us if loop_us is not None else dom["avg_us"]
     if dom["flops"] / (peak * 1e12) >= dom["algorithmic_bytes"] / (PEAK_HBM_GBS * 1e9):
-        roofline = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak, "unit": "TFLOP/s",
-                    "frac": dom["tflops"] / peak}
+        achieved = dom["flops"] / (us * 1e-6) / 1e12
+        roofline = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak}
     else:
-        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": dom["gbs"] / PEAK_HBM_GBS}
+        achieved = dom["algorithmic_bytes"] / (us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": achieved / PEAK_HBM_GBS}
+    roofline["avg_us"] = us
+    roofline["timing"] = (f"{ROOFLINE_LOOP[1]} back-to-back launches of the kind's op at the pass's shape, one event "
+                          "pair around the loop" if loop_us is not None else
+                          "per-launch stamps of the stamped passes")
+    roofline["in_pass_stamped_us"] = dom["avg_us"]
     roofline["kernel"] = f"encoder.layers.*-{name}" if name in abi.ENCODER_DISPATCHES else f"encoder.{name}"
     roofline["traffic"] = read_traffic(f"encoder-{name}", None) if not f32 else None
     roofline["traffic_source"] = TRAFFIC_SOURCE if roofline["traffic"] is not None else None
@@ -763,14 +879,11 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "palette_bits": {"ff/qkv/pointwise/subsampling/projector": 5, "o_proj": 6},
                    "dispatch_slots_per_pass": launches,
                    "launches_per_pass": launches - len(fused_norms) * len(stack.layers) -
-                                        (len(stack.layers) - 1 if chained else 0) -
-                                        (len(POST_NORMS) * len(stack.layers) if post else 0),
+                                        (len(stack.layers) - 1 if chained else 0),
                    "layernorms": "four of five per layer inside the GEMM they feed (PK_GEMM_ROW_NORM)"
                                  if args.fused_norms else
-                                 ("the four after the residual GEMMs written by those GEMMs (PK_GEMM_POST_NORM)"
-                                  + ("; each layer's last also writes the next layer's first" if chained else "")
-                                  if post else "separate launches" if not chained else
-                                  "separate launches; each layer's last LayerNorm also writes the next layer's first"),
+                                 "separate launches" if not chained else
+                                 "separate launches; each layer's last LayerNorm also writes the next layer's first",
                    "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu
                           else "in the convolution (the fp32 profile)" if f32 else "in PW1's epilogue",
                    "graph_replay": True,
@@ -1151,6 +1264,9 @@ def measure_kernel_step(ctx, kernels, steps, warmup, use_graph=False):
 
 def main():
     args = parse_args()
+    if args.split_trace:
+        split_trace(args.split_trace, args.warmup, args.steps)
+        return
     if args.dense_probe:
         dense_probe(json.loads(args.dense_probe), args.steps)
         return

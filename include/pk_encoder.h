@@ -8,9 +8,7 @@
  * createEncoderLayerDispatches (:1868-2135), fifteen dispatch slots per
  * layer in this order (after the first layer the LN ff1 slot launches
  * nothing: the LN out before it wrote that LayerNorm too, unless
- * PK_ENCODER_UNCHAINED_NORMS; with PK_ENCODER_POST_NORMS the LN att,
- * LN conv, LN ff2 and LN out slots launch nothing either, their LayerNorms
- * written by the residual GEMM before them; with
+ * PK_ENCODER_UNCHAINED_NORMS; with
  * PK_ENCODER_FUSED_NORMS the four LayerNorms that feed a GEMM run inside
  * that GEMM and their slots launch nothing):
  *   LN ff1 -> FF1 W1 + SiLU -> FF1 W2 + 0.5 x         (x1)
@@ -64,17 +62,6 @@ extern "C" {
    first launch nothing in their LN ff1 slot: 23 fewer launches per 24-layer
    pass, bit-identical outputs. This flag keeps one launch per LayerNorm. */
 #define PK_ENCODER_UNCHAINED_NORMS 0x4u
-/* Have each of the four residual GEMMs write the LayerNorm after it (LN att
-   after FF1 W2, LN conv after Wo, LN ff2 after PW2, LN out after FF2 W2
-   with its chained LN ff1) from its finished output rows
-   (PK_GEMM_POST_NORM): 96 fewer launches per 24-layer pass, bit-identical
-   outputs, those slots launch nothing. f16 only, not with
-   PK_ENCODER_FUSED_NORMS. Measured slower on 16 windows (9.1 against
-   7.3 ms per pass): the last workgroup of each row band normalises the
-   band's 96 rows alone while the rest of the device idles, 20-40 us per
-   GEMM against about 6 us for a LayerNorm launch and its gap. Separate
-   LayerNorm launches stay the default. */
-#define PK_ENCODER_POST_NORMS 0x10u
 
 typedef struct pk_encoder pk_encoder;
 

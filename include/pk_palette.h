@@ -102,30 +102,6 @@ typedef enum pk_activation {
    or groups whose width is a multiple of 256 columns. Runs on the pair-code
    kernels. */
 #define PK_GEMM_ROW_NORM 0x4u
-/* Row LayerNorm of the finished output rows, fused into the GEMM. No
-   counterpart in the reference's GEMM: there the GEMM writes its rows and a
-   LayerNorm dispatch reads them back (gemm.ts:2006-2044 then
-   layernorm.ts:29-281, as after every residual projection of
-   encoder.ts:1897-2116). With this flag the op also writes post_output =
-   LN(output row) with post_gamma / post_beta (mean and variance of the N
-   output channels, layernorm.ts:309-390), and with post_next_output set
-   also post_next_output = LN'(post_output row) with post_next_gamma /
-   post_next_beta: the bits of a separate LayerNorm launch (pk_layernorm.h)
-   over the stored output rows, and of a chained one. The workgroups that
-   share a band of output rows count themselves in as they finish; the
-   last one normalises the band, so no workgroup waits for another. f16
-   only; needs N % 8 == 0, N <= 1024, K % 64 == 0, the packed codes or a
-   prepared weight of two or four K parts, no GLU epilogue or row norm, one
-   palette group or groups of a multiple of 128 columns, and no split-K
-   launch. post_output must not overlap the input or the residual and is
-   either the output itself or apart from it; post_next_output follows the
-   same rule and is apart from post_output. Runs on the pair-code kernels
-   with two or four K parts. Measured on one MI355X: a 3008 x 1024 x 1024
-   residual GEMM takes about 20 us longer (40 us with the chained second
-   LayerNorm) than without it, more than a separate LayerNorm launch and
-   its gap (about 6 us): the band's last workgroup normalises its rows
-   alone. Calls of one op that overlap in time race on its band counters. */
-#define PK_GEMM_POST_NORM 0x8u
 
 typedef struct pk_context pk_context;
 typedef struct pk_gemm_op pk_gemm_op;
@@ -262,21 +238,6 @@ typedef struct pk_gemm_desc {
   const float *norm_beta;        /* [inner] f32 */
   uint64_t norm_beta_bytes;
   float norm_epsilon;            /* 0 selects 1e-5 */
-  /* PK_GEMM_POST_NORM only: the LayerNorm of the output rows, and the
-     optional chained second one. */
-  const float *post_gamma;       /* [columns] f32 */
-  uint64_t post_gamma_bytes;
-  const float *post_beta;        /* [columns] f32 */
-  uint64_t post_beta_bytes;
-  float post_epsilon;            /* 0 selects 1e-5 */
-  void *post_output;             /* [rows, columns] f16 */
-  uint64_t post_output_bytes;
-  const float *post_next_gamma;  /* [columns] f32, or NULL: no second LayerNorm */
-  uint64_t post_next_gamma_bytes;
-  const float *post_next_beta;   /* [columns] f32 */
-  uint64_t post_next_beta_bytes;
-  void *post_next_output;        /* [rows, columns] f16 */
-  uint64_t post_next_output_bytes;
 } pk_gemm_desc;
 
 int pk_gemm_create(pk_context *ctx, const pk_gemm_desc *desc, void *stream,

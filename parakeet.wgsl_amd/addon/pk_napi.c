@@ -495,33 +495,6 @@ static int parse_gemm_desc(napi_env env, napi_value o, pk_gemm_desc *d, char **l
     }
     d->norm_epsilon = (float)epsilon;
   }
-  /* PK_GEMM_POST_NORM: postGamma, postBeta, postOutput (+Bytes), postEpsilon,
-     and the chained postNextGamma, postNextBeta, postNextOutput (+Bytes). */
-  uint64_t post_gamma = 0, post_beta = 0, post_output = 0, post_next_gamma = 0, post_next_beta = 0,
-           post_next_output = 0;
-  if (prop_u64(env, o, "postGamma", &post_gamma)) prop_u64(env, o, "postGammaBytes", &d->post_gamma_bytes);
-  if (prop_u64(env, o, "postBeta", &post_beta)) prop_u64(env, o, "postBetaBytes", &d->post_beta_bytes);
-  if (prop_u64(env, o, "postOutput", &post_output)) prop_u64(env, o, "postOutputBytes", &d->post_output_bytes);
-  if (prop_u64(env, o, "postNextGamma", &post_next_gamma))
-    prop_u64(env, o, "postNextGammaBytes", &d->post_next_gamma_bytes);
-  if (prop_u64(env, o, "postNextBeta", &post_next_beta))
-    prop_u64(env, o, "postNextBetaBytes", &d->post_next_beta_bytes);
-  if (prop_u64(env, o, "postNextOutput", &post_next_output))
-    prop_u64(env, o, "postNextOutputBytes", &d->post_next_output_bytes);
-  if (prop(env, o, "postEpsilon", &v)) {
-    double epsilon;
-    if (napi_get_value_double(env, v, &epsilon) != napi_ok) {
-      bad_argument(env, "postEpsilon must be a number");
-      return 0;
-    }
-    d->post_epsilon = (float)epsilon;
-  }
-  d->post_gamma = (const float *)(uintptr_t)post_gamma;
-  d->post_beta = (const float *)(uintptr_t)post_beta;
-  d->post_output = (void *)(uintptr_t)post_output;
-  d->post_next_gamma = (const float *)(uintptr_t)post_next_gamma;
-  d->post_next_beta = (const float *)(uintptr_t)post_next_beta;
-  d->post_next_output = (void *)(uintptr_t)post_next_output;
   if (prop(env, o, "prepared", &v)) {
     const weight_box *box = (const weight_box *)get_external(env, v);
     if (!box || !box->w) {
@@ -1246,7 +1219,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
   return ok;
 }
 
-/* Parses an encoder descriptor: {label, precision?, fusedGlu?, fusedNorms?, unchainedNorms?, postNorms?,
+/* Parses an encoder descriptor: {label, precision?, fusedGlu?, fusedNorms?, unchainedNorms?,
    batchSize, frames,
    layers: [layer...], validLengths, input, output, subsampling?,
    featureFrames?, featureLengths?, projector?, projectorBias?,
@@ -1267,9 +1240,6 @@ static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   if (prop(env, o, "unchainedNorms", &v) && napi_get_value_bool(env, v, &unchained_norms) == napi_ok &&
       unchained_norms)
     d->flags |= PK_ENCODER_UNCHAINED_NORMS;
-  bool post_norms = false;
-  if (prop(env, o, "postNorms", &v) && napi_get_value_bool(env, v, &post_norms) == napi_ok && post_norms)
-    d->flags |= PK_ENCODER_POST_NORMS;
   if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
       !prop(env, o, "layers", &layers) || napi_get_array_length(env, layers, &n) != napi_ok || n == 0) {
     bad_argument(env, "encoder descriptor is missing a required field");

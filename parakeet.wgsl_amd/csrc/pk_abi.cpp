@@ -125,8 +125,6 @@ struct pk_gemm_op {
   uint64_t workspace_bytes = 0;
   // Fused row LayerNorm (PK_GEMM_ROW_NORM): G and B [2N] f32, then f16 gamma [K].
   void* norm_buffer = nullptr;
-  // Post-norm (PK_GEMM_POST_NORM): one band counter per 64 rows of capacity.
-  void* post_counters = nullptr;
   bool destroyed = false;
 };
 
@@ -558,57 +556,6 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
       return fail(PK_INVALID_ARGUMENT, "%s row norm needs gamma and beta of %llu bytes and epsilon >= 0", label,
                   (unsigned long long)need);
   }
-  const bool post = (d->flags & PK_GEMM_POST_NORM) != 0;
-  if (post) {
-    if (!f16 || glu || norm || d->columns % 8u != 0 || d->columns > pk::kPostNormMaxColumns ||
-        (d->prepared && d->prepared->parts == 1))
-      return fail(PK_INVALID_ARGUMENT,
-                  "%s post norm needs f16, N %% 8 == 0, N <= %u, no GLU epilogue or row norm, and codes in two or "
-                  "four K parts",
-                  label, pk::kPostNormMaxColumns);
-    // The post-norm kernels are the fixed-palette ones: whole 64-deep K
-    // blocks and every tile (64 or 128 columns) inside one palette group.
-    if (d->inner % 64u != 0 || (d->palette_groups != 1 && d->palette_group_columns % 128u != 0))
-      return fail(PK_INVALID_ARGUMENT,
-                  "%s post norm needs K %% 64 == 0 and one palette group or groups of a multiple of 128 columns",
-                  label);
-    const uint64_t need = (uint64_t)d->columns * 4u;
-    const uint64_t rows_need = (uint64_t)d->rows * d->columns * 2u;
-    const uint64_t in_need = (uint64_t)d->rows * d->inner * 2u;
-    auto apart = [](const void* p, uint64_t pn, const void* q, uint64_t qn) {
-      const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
-      return a + pn <= b || b + qn <= a;
-    };
-    // A LayerNorm output: apart from the input and the residual, the output
-    // itself or apart from it, and apart from `other` when given.
-    auto placed = [&](const void* out, const void* other) {
-      return apart(out, rows_need, d->a, in_need) && (!d->residual || apart(out, rows_need, d->residual, rows_need)) &&
-             (out == d->output || apart(out, rows_need, d->output, rows_need)) &&
-             (!other || apart(out, rows_need, other, rows_need));
-    };
-    if (!d->post_gamma || !d->post_beta || d->post_gamma_bytes < need || d->post_beta_bytes < need ||
-        !aligned(d->post_gamma, 16) || !aligned(d->post_beta, 16) || !(d->post_epsilon >= 0.0f))
-      return fail(PK_INVALID_ARGUMENT, "%s post norm needs gamma and beta of %llu bytes at 16-byte alignment and "
-                  "epsilon >= 0", label, (unsigned long long)need);
-    if (!d->post_output || d->post_output_bytes < rows_need || !aligned(d->post_output, 16))
-      return fail(PK_INVALID_ARGUMENT, "%s post norm output must hold %llu bytes at 16-byte alignment", label,
-                  (unsigned long long)rows_need);
-    if (!placed(d->post_output, nullptr))
-      return fail(PK_INVALID_ARGUMENT, "%s post norm output must not overlap the input or the residual, and be the "
-                  "output or not overlap it", label);
-    if (d->post_next_gamma || d->post_next_beta || d->post_next_output) {
-      if (!d->post_next_gamma || !d->post_next_beta || d->post_next_gamma_bytes < need ||
-          d->post_next_beta_bytes < need || !aligned(d->post_next_gamma, 16) || !aligned(d->post_next_beta, 16))
-        return fail(PK_INVALID_ARGUMENT, "%s post norm next gamma and beta must hold %llu bytes at 16-byte "
-                    "alignment", label, (unsigned long long)need);
-      if (!d->post_next_output || d->post_next_output_bytes < rows_need || !aligned(d->post_next_output, 16))
-        return fail(PK_INVALID_ARGUMENT, "%s post norm next output must hold %llu bytes at 16-byte alignment",
-                    label, (unsigned long long)rows_need);
-      if (!placed(d->post_next_output, d->post_output))
-        return fail(PK_INVALID_ARGUMENT, "%s post norm next output must not overlap the input, the residual or the "
-                    "post norm output, and be the output or not overlap it", label);
-    }
-  }
   // requireRuntimeWeight (gemm.ts:1069-1161): palette geometry and storage
   const uint32_t entries = 1u << bits;
   const uint32_t cpg = pk::codes_per_group(bits);
@@ -944,21 +891,11 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
     cus = prop.multiProcessorCount;
   const bool glu = (d->flags & PK_GEMM_GLU) != 0;
   const bool norm = (d->flags & PK_GEMM_ROW_NORM) != 0;
-  const bool post = (d->flags & PK_GEMM_POST_NORM) != 0;
   op->cus = cus;
   // The plan comes first: the weight is prepared in the one layout the
-  // planned kernel reads (a shared prepared weight fixes it instead). A
-  // post norm runs on the pair-code tiles of two or four K parts.
+  // planned kernel reads (a shared prepared weight fixes it instead).
   Plan plan = plan_op(d->precision, d->rows, d->inner, d->columns, cus, glu,
-                      d->prepared ? d->prepared->parts : 0, norm || post);
-  if (post && !pk::f16_variant_post(plan.variant)) {
-    const int v = best_pair_tile(d->rows, d->columns, cus, false, d->prepared ? d->prepared->parts : 2);
-    if (v < 0 || !pk::f16_variant_post(v)) {
-      delete op;
-      return fail(PK_INTERNAL_ERROR, "%s: no post-norm tile for %u x %u", label, d->rows, d->columns);
-    }
-    plan = {v, 1u};
-  }
+                      d->prepared ? d->prepared->parts : 0, norm);
   if (d->prepared) {
     op->weight = const_cast<pk_prepared_weight*>(d->prepared);
     op->weight->refs.fetch_add(1);
@@ -1016,29 +953,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
     a.norm_gamma = static_cast<const _Float16*>(gamma16);
     a.norm_epsilon = d->norm_epsilon > 0.0f ? d->norm_epsilon : 1e-5f;
   }
-  if (post) {
-    const uint64_t bytes = ((uint64_t)d->rows + 63u) / 64u * 4u;
-    hipError_t e = hipMalloc(&op->post_counters, bytes);
-    if (e == hipSuccess) e = hipMemset(op->post_counters, 0, bytes);
-    if (e != hipSuccess) {
-      if (op->post_counters) (void)hipFree(op->post_counters);
-      if (op->norm_buffer) (void)hipFree(op->norm_buffer);
-      weight_unref(op->weight);
-      delete op;
-      return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate the post norm's band counters: %s", label,
-                  hipGetErrorString(e));
-    }
-    a.post_gamma = d->post_gamma;
-    a.post_beta = d->post_beta;
-    a.post_output = d->post_output;
-    a.post_next_gamma = d->post_next_output ? d->post_next_gamma : nullptr;
-    a.post_next_beta = d->post_next_output ? d->post_next_beta : nullptr;
-    a.post_next_output = d->post_next_output;
-    a.post_epsilon = d->post_epsilon > 0.0f ? d->post_epsilon : 1e-5f;
-    a.band_counters = static_cast<uint32_t*>(op->post_counters);
-  }
   if (int st = configure_launch(op, plan.variant, plan.splits)) {
-    if (op->post_counters) (void)hipFree(op->post_counters);
     if (op->norm_buffer) (void)hipFree(op->norm_buffer);
     weight_unref(op->weight);
     delete op;
@@ -1109,8 +1024,6 @@ int pk_gemm_destroy(pk_gemm_op* op) {
   // for the device to drain
   free_after_drain(op->ctx->device, op->norm_buffer);
   op->norm_buffer = nullptr;
-  free_after_drain(op->ctx->device, op->post_counters);
-  op->post_counters = nullptr;
   free_after_drain(op->ctx->device, op->workspace);
   op->workspace = nullptr;
   op->workspace_bytes = 0;
@@ -1134,8 +1047,6 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no GLU epilogue", op->label.c_str(), variant);
   if (op->args.norm_columns && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no fused row norm", op->label.c_str(), variant);
-  if (op->args.post_output && !pk::f16_variant_post(variant))
-    return fail(PK_RANGE_ERROR, "%s tile variant %d has no post-norm epilogue", op->label.c_str(), variant);
   // A variant that reads another split of the codes: an op alone on its
   // weight moves it to that layout; a weight shared with other ops stays.
   const int parts = variant_parts(op->precision, variant);
@@ -1283,8 +1194,8 @@ int pk_gemm_group_create(pk_context* ctx, pk_gemm_op* const* ops, uint32_t count
     if (op->destroyed) return fail(PK_DESTROYED, "%s member %u (%s) was destroyed", name, i, op->label.c_str());
     if (op->ctx != ctx)
       return fail(PK_INVALID_ARGUMENT, "%s member %u (%s) belongs to another context", name, i, op->label.c_str());
-    if (op->precision != PK_PRECISION_F16 || op->args.glu || op->args.norm_columns || op->args.post_output)
-      return fail(PK_RANGE_ERROR, "%s member %u (%s) is not an f16 GEMM without GLU epilogue, row norm or post norm",
+    if (op->precision != PK_PRECISION_F16 || op->args.glu || op->args.norm_columns)
+      return fail(PK_RANGE_ERROR, "%s member %u (%s) is not an f16 GEMM without GLU epilogue or row norm",
                   name, i, op->label.c_str());
     if (op->weight->parts != 1)
       return fail(PK_RANGE_ERROR,

@@ -73,7 +73,6 @@ struct pk_encoder {
   bool fused_glu = true;
   bool fused_norms = false;
   bool chained_norms = true;  // norm_out also writes the next layer's norm_feed_forward1
-  bool post_norms = false;    // the residual GEMMs write the LayerNorms after them
   const uint32_t* valid_lengths = nullptr;
   const void* input = nullptr;
   void* output = nullptr;
@@ -137,14 +136,6 @@ struct GemmSpec {
   uint32_t flags = 0;
   const float* norm_gamma = nullptr;  // with PK_GEMM_ROW_NORM
   const float* norm_beta = nullptr;
-  // With PK_GEMM_POST_NORM: the LayerNorm of the output rows, and the
-  // optional chained one.
-  const float* post_gamma = nullptr;
-  const float* post_beta = nullptr;
-  void* post_output = nullptr;
-  const float* post_next_gamma = nullptr;
-  const float* post_next_beta = nullptr;
-  void* post_next_output = nullptr;
 };
 
 // With `validate_only` the descriptor is checked on the host
@@ -184,24 +175,6 @@ int make_gemm(pk_encoder* e, const std::string& label, const GemmSpec& g, hipStr
     d.norm_beta = g.norm_beta;
     d.norm_beta_bytes = (uint64_t)g.inner * 4u;
     d.norm_epsilon = 1e-5f;
-  }
-  if (g.flags & PK_GEMM_POST_NORM) {
-    const uint64_t rows_bytes = R * g.columns * e->elem;
-    d.post_gamma = g.post_gamma;
-    d.post_gamma_bytes = (uint64_t)g.columns * 4u;
-    d.post_beta = g.post_beta;
-    d.post_beta_bytes = (uint64_t)g.columns * 4u;
-    d.post_epsilon = 1e-5f;
-    d.post_output = g.post_output;
-    d.post_output_bytes = rows_bytes;
-    if (g.post_next_output) {
-      d.post_next_gamma = g.post_next_gamma;
-      d.post_next_gamma_bytes = (uint64_t)g.columns * 4u;
-      d.post_next_beta = g.post_next_beta;
-      d.post_next_beta_bytes = (uint64_t)g.columns * 4u;
-      d.post_next_output = g.post_next_output;
-      d.post_next_output_bytes = rows_bytes;
-    }
   }
   if (validate_only) return pk_gemm_validate(&d);
   const int s = pk_gemm_create(e->ctx, &d, stream, op);
@@ -331,11 +304,7 @@ int build_front(pk_encoder* e, const pk_encoder_subsampling& w, hipStream_t stre
 //   read the LayerNorm's input (A, B, C, D) with PK_GEMM_ROW_NORM. Otherwise,
 //   unless PK_ENCODER_UNCHAINED_NORMS, the last LayerNorm of a layer also
 //   writes B = LN ff1(A) of the layer `next` (a chained LayerNorm) and that
-//   layer creates no LayerNorm of its own there. With PK_ENCODER_POST_NORMS
-//   the LayerNorms after the four residual GEMMs (LN att, LN conv, LN ff2
-//   and LN out with its chained LN ff1) are not created either: each
-//   residual GEMM writes them from its finished rows (PK_GEMM_POST_NORM),
-//   into the same buffers.
+//   layer creates no LayerNorm of its own there.
 int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer* next, uint32_t li,
                 hipStream_t stream, LayerOps& l, bool validate_only) {
   const uint64_t R = e->rows;
@@ -373,11 +342,6 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
   // LayerNorm i runs inside the GEMM it feeds (not with the GLU epilogue).
   auto fused = [&](int i) { return e->fused_norms && !(i == 2 && e->fused_glu); };
   int norm_of = -1;  // the LayerNorm the next gemm() call fuses
-  // The LayerNorm the next gemm() call writes from its output rows, where,
-  // and where its chained successor (the next layer's LN ff1) goes.
-  int post_of = -1;
-  void* post_out = nullptr;
-  void* post_next = nullptr;
   auto gemm = [&](pk_gemm_op** op, const char* suffix, const pk_encoder_matrix& m, int bits, uint32_t inner,
                   uint32_t columns, uint32_t groups, const void* a, void* out, const void* residual, float scale,
                   int activation, uint32_t flags) {
@@ -387,19 +351,6 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
       g.norm_gamma = w.norm_gamma[norm_of];
       g.norm_beta = w.norm_beta[norm_of];
       norm_of = -1;
-    }
-    if (post_of >= 0) {
-      flags |= PK_GEMM_POST_NORM;
-      g.post_gamma = w.norm_gamma[post_of];
-      g.post_beta = w.norm_beta[post_of];
-      g.post_output = post_out;
-      if (post_next) {
-        g.post_next_gamma = next->norm_gamma[0];
-        g.post_next_beta = next->norm_beta[0];
-        g.post_next_output = post_next;
-      }
-      post_of = -1;
-      post_next = nullptr;
     }
     g.matrix = m;
     g.bits = bits;
@@ -433,18 +384,10 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
   if (s || (s = gemm(&l.ff1a, "-feed-forward1-linear1", w.ff1_linear1, 5, kC, kHidden, 1, in, e->h, nullptr, 0.0f,
                      PK_ACTIVATION_SILU, 0)))
     return s;
-  // A LayerNorm that the residual GEMM before it writes (post norm).
-  auto post = [&](int i, void* out, void* chained_out = nullptr) {
-    post_of = i;
-    post_out = out;
-    post_next = chained_out;
-  };
-  const bool pn = e->post_norms;
-  if (pn) post(1, e->c);
   if ((s = gemm(&l.ff1b, "-feed-forward1-linear2-residual", w.ff1_linear2, 5, kHidden, kC, 1, e->h, e->b, x, 0.5f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  in = pn ? e->c : norm_into(1, ".norm_self_att", e->b, e->c);
+  in = norm_into(1, ".norm_self_att", e->b, e->c);
   if (s || (s = gemm(&l.qkv, "-self-attention-qkv", w.qkv, 5, kC, 3 * kC, 3, in, e->qkv, nullptr, 0.0f,
                      PK_ACTIVATION_NONE, 0)))
     return s;
@@ -469,11 +412,10 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     d.output_bytes = R * kC * e->elem;
     if ((s = validate_only ? pk_attention_validate(&d) : pk_attention_create(e->ctx, &d, &l.attention))) return s;
   }
-  if (pn) post(2, e->d);
   if ((s = gemm(&l.o, "-self-attention-output-residual", w.o_proj, 6, kC, kC, 1, e->ctxt, e->c, e->b, 1.0f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  in = pn ? e->d : norm_into(2, ".norm_conv", e->c, e->d);
+  in = norm_into(2, ".norm_conv", e->c, e->d);
   if (s || (s = gemm(&l.pw1, "-convolution-pointwise1", w.pointwise1, 5, kC, 2 * kC, 1, in, e->pw, nullptr, 0.0f,
                      PK_ACTIVATION_NONE, e->fused_glu ? PK_GEMM_GLU : 0u)))
     return s;
@@ -500,22 +442,20 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     d.output_bytes = R * kC * e->elem;
     if ((s = validate_only ? pk_conv_validate(&d) : pk_conv_create(e->ctx, &d, &l.conv))) return s;
   }
-  if (pn) post(3, e->b);
   if ((s = gemm(&l.pw2, "-convolution-pointwise2-residual", w.pointwise2, 5, kC, kC, 1, e->cout, e->d, e->c, 1.0f,
                 PK_ACTIVATION_NONE, 0)))
     return s;
-  in = pn ? e->b : norm_into(3, ".norm_feed_forward2", e->d, e->b);
+  in = norm_into(3, ".norm_feed_forward2", e->d, e->b);
   if (s || (s = gemm(&l.ff2a, "-feed-forward2-linear1", w.ff2_linear1, 5, kC, kHidden, 1, in, e->h, nullptr, 0.0f,
                      PK_ACTIVATION_SILU, 0)))
     return s;
   const bool last = li + 1 == e->layers;
   void* out_norm = last ? e->output : e->a;
   void* chained_ff1 = e->chained_norms && next ? e->b : nullptr;
-  if (pn) post(4, out_norm, chained_ff1);
   if ((s = gemm(&l.ff2b, "-feed-forward2-linear2-residual", w.ff2_linear2, 5, kHidden, kC, 1, e->h, e->b, e->d,
                 0.5f, PK_ACTIVATION_NONE, 0)))
     return s;
-  return pn ? PK_OK : norm(4, ".norm_out", e->b, out_norm, chained_ff1);
+  return norm(4, ".norm_out", e->b, out_norm, chained_ff1);
 }
 
 int build_projector(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, pk_gemm_op** op,
@@ -627,8 +567,6 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->fused_glu = (d->flags & PK_ENCODER_SEPARATE_GLU) == 0 && d->precision == PK_PRECISION_F16;
   e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
   e->chained_norms = (d->flags & (PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS)) == 0;
-  // The residual GEMMs' post norms (f16 kernels).
-  e->post_norms = (d->flags & PK_ENCODER_POST_NORMS) != 0;
   e->valid_lengths = d->valid_lengths;
   e->input = d->input;
   e->output = d->output;
@@ -651,17 +589,15 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "pk_encoder_desc.struct_size mismatch");
   const char* label = d->label ? d->label : "encoder";
   if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_SEPARATE_GLU | PK_ENCODER_FUSED_NORMS |
-                   PK_ENCODER_UNCHAINED_NORMS | PK_ENCODER_POST_NORMS))
+                   PK_ENCODER_UNCHAINED_NORMS))
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if ((d->flags & PK_ENCODER_FUSED_GLU) && (d->flags & PK_ENCODER_SEPARATE_GLU))
     return fail(PK_INVALID_ARGUMENT, "%s: PK_ENCODER_FUSED_GLU and PK_ENCODER_SEPARATE_GLU exclude each other", label);
   if (d->precision != PK_PRECISION_F16 && d->precision != PK_PRECISION_F32)
     return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
   if (d->precision == PK_PRECISION_F32 &&
-      (d->flags & (PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS | PK_ENCODER_POST_NORMS)))
+      (d->flags & (PK_ENCODER_FUSED_GLU | PK_ENCODER_FUSED_NORMS)))
     return fail(PK_INVALID_ARGUMENT, "%s: the GLU epilogue and the fused LayerNorms need f16", label);
-  if ((d->flags & PK_ENCODER_FUSED_NORMS) && (d->flags & PK_ENCODER_POST_NORMS))
-    return fail(PK_INVALID_ARGUMENT, "%s: PK_ENCODER_FUSED_NORMS and PK_ENCODER_POST_NORMS exclude each other", label);
   const uint64_t elem = d->precision == PK_PRECISION_F32 ? 4u : 2u;
   if (d->batch_size == 0 || d->frames == 0 || d->layers == 0 || d->layers > kMaxLayers)
     return fail(PK_RANGE_ERROR, "Unsupported encoder shape for %s: %u windows x %u frames x %u layers", label,

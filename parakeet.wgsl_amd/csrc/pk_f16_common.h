@@ -232,7 +232,6 @@ struct F16Variant {
   void (*general[2])(GemmArgs);
   uint32_t lds_bytes;           // static LDS of the kernel
   void (*normed[2])(GemmArgs);  // fused row LayerNorm (single path), or null
-  void (*post[2])(GemmArgs);    // post-norm epilogue (single path), or null
 };
 
 }  // namespace f16

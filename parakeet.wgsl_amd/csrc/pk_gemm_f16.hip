@@ -333,10 +333,6 @@ int f16_variant_family(int index) {
   return index < kLocal + f16k_variant_count() ? kFamilyPairCode : kFamilySmallM;
 }
 
-bool f16_variant_post(int index) {
-  return f16_variant_family(index) == kFamilyPairCode && variant_at(index).post[0] != nullptr;
-}
-
 uint32_t f16_variant_grid(int index, uint32_t rows, uint32_t columns, uint32_t splits) {
   const TileShape s = f16_variant(index);
   if (f16_variant_family(index) == kFamilySmallM) return small_m_grid(s, tiles_n(s, columns), rows);
@@ -356,8 +352,6 @@ hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStr
 
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop) {
-  // The post-norm epilogue exists on pair-code tiles only.
-  if (args.post_output && f16_variant_family(variant) != kFamilyPairCode) return hipErrorInvalidValue;
   if (variant >= kLocal + f16k_variant_count())
     return launch_gemm_f16s(bits, variant_at(variant), args, stream, start, stop);
   if (variant >= kLocal) return launch_gemm_f16k(bits, variant_at(variant), args, stream, start, stop);

@@ -60,7 +60,6 @@
 #include <utility>
 
 #include "pk_f16_common.h"
-#include "pk_rownorm.h"
 
 namespace pk {
 namespace {
@@ -136,122 +135,11 @@ __device__ __forceinline__ void interleave_sub_step() {
   }
 }
 
-typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
-
-// Post-norm output traffic: relaxed agent-scope atomics, which other XCDs'
-// workgroups read coherently without any cache write-back or invalidate.
-__device__ __forceinline__ void coherent_store(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t coherent_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Post-norm tail (GemmArgs::post_output) of a workgroup of row tile tm,
-// after its output tile went out with coherent stores: the workgroup counts
-// itself into the row tile's band counter once all its stores have
-// completed, and the last of the TN column tiles to arrive (no workgroup
-// ever waits for another) resets the counter and normalises the band's
-// rows. One wavefront per row, rows wave, wave + 4, ..., read back six
-// at a time with coherent loads and taken through each stage together; each lane holds vectors lane and lane + 64
-// of 8 channels, so the sums, the reduction and the rounding are the
-// LayerNorm kernel's (pk_rownorm.h) and the outputs are bit-identical to a
-// separate LayerNorm launch over the stored rows.
-template <int BM>
-__device__ __forceinline__ void post_norm_band(const GemmArgs& args, const _Float16* out, uint32_t m0, uint32_t tm,
-                                               uint32_t TN, uint32_t& last) {
-  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-  constexpr int H = (int)(kPostNormMaxColumns / 512u);  // vectors a lane holds
-  constexpr int RB = 6;                                 // rows per wavefront per read-back
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(args.band_counters + tm, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           TN - 1u;
-  __syncthreads();
-  if (!last) return;
-  if (threadIdx.x == 0) __hip_atomic_store(args.band_counters + tm, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  const int lane = threadIdx.x & 63;
-  const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t N = args.columns;
-  const uint32_t rows = min((uint32_t)BM, args.rows - m0);
-  const uint32_t vectors = N / 8u;
-  const bool chain = args.post_next_output != nullptr;
-  float4 g[H][2], b[H][2], gn[H][2], bn[H][2];
-#pragma unroll
-  for (int h = 0; h < H; ++h) {
-    const uint32_t v = lane + 64u * h;
-    if (v < vectors) {
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        g[h][f] = reinterpret_cast<const float4*>(args.post_gamma)[2 * v + f];
-        b[h][f] = reinterpret_cast<const float4*>(args.post_beta)[2 * v + f];
-        if (chain) {
-          gn[h][f] = reinterpret_cast<const float4*>(args.post_next_gamma)[2 * v + f];
-          bn[h][f] = reinterpret_cast<const float4*>(args.post_next_beta)[2 * v + f];
-        }
-      }
-    }
-  }
-  half8* post = static_cast<half8*>(args.post_output);
-  half8* next = static_cast<half8*>(args.post_next_output);
-  for (uint32_t r0 = wave; r0 < rows; r0 += 4u * RB) {
-    // RB rows at once through every stage (reads, sums, the butterflies,
-    // the outputs), so their latencies overlap.
-    half8 x[RB][H];
-    uint64_t at[RB];
-    bool live[RB];
-#pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      // Rows past the band re-read its last row and store nothing.
-      const uint32_t r = r0 + 4u * i;
-      live[i] = r < rows;
-      at[i] = (uint64_t)(m0 + min(r, rows - 1u)) * vectors;
-      const uint64_t* src = reinterpret_cast<const uint64_t*>(out) + 2 * at[i];
-#pragma unroll
-      for (int h = 0; h < H; ++h) {
-        const uint32_t v = lane + 64u * h;
-        if (v < vectors) {
-          const u64x2 raw = {coherent_load(src + 2 * v), coherent_load(src + 2 * v + 1)};
-          x[i][h] = __builtin_bit_cast(half8, raw);
-        }
-      }
-    }
-    auto normalise = [&](const float4 (&gg)[H][2], const float4 (&bb)[H][2], half8* dst) {
-      float sum[RB], square[RB];
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        sum[i] = square[i] = 0.0f;
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-          if (lane + 64u * h < vectors) rownorm_accumulate<8>(x[i][h], sum[i], square[i]);
-      }
-      rownorm_reduce<RB>(sum, square);
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const float2 st = rownorm_stats(sum[i], square[i], N, args.post_epsilon);
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-          const uint32_t v = lane + 64u * h;
-          if (v < vectors) {
-            x[i][h] = rownorm_apply<_Float16, 8>(x[i][h], st, gg[h], bb[h]);
-            if (live[i]) dst[at[i] + v] = x[i][h];
-          }
-        }
-      }
-    };
-    normalise(g, b, post);
-    if (chain) normalise(gn, bn, next);
-  }
-}
 
 // GENERAL: the tile's columns may span palette groups (per-lane palette
 // base) or K may be 32 (mod 64) (the last K block's upper half is zeroed,
-// so the code-0 padding of the operand order multiplies zeros). POST: the
-// post-norm tail (post_norm_band) after coherent output stores.
-template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA, bool NORM = false,
-          bool POST = false>
+// so the code-0 padding of the operand order multiplies zeros).
+template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA, bool NORM = false>
 __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int T = 256;
   constexpr int BM = 32 * R;
@@ -275,7 +163,6 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   static_assert(KS == 1 || KS == 2 || KS == 4, "K parts split the four sub-steps evenly");
   static_assert(BM * 8 % T == 0, "activation tile chunks must divide evenly");
   static_assert(!(NORM && GENERAL), "the fused row norm runs on the fixed-palette path");
-  static_assert(!(POST && (GENERAL || NORM)), "the post-norm tail runs on the plain fixed-palette path");
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   __shared__ __attribute__((aligned(16))) _Float16 lut_lds[GROUPS * kLutStride];
@@ -285,7 +172,6 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) _Float16 gamma_lds[NORM ? kNormMaxInner : 1];
   __shared__ float2 row_stats[NORM ? BM : 1];
   __shared__ float2 column_gb[NORM ? BN : 1];  // (G_n, B_n) of the tile's columns
-  __shared__ uint32_t band_last;                // post-norm: this workgroup completes its band
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -809,16 +695,9 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       if (keep[it]) {
         const uint4 y = make_uint4(pack_half2(v[it][0], v[it][1]), pack_half2(v[it][2], v[it][3]),
                                    pack_half2(v[it][4], v[it][5]), pack_half2(v[it][6], v[it][7]));
-        if constexpr (POST) {
-          uint64_t* dst = reinterpret_cast<uint64_t*>(out + at[it]);
-          coherent_store(dst, (uint64_t)y.x | (uint64_t)y.y << 32);
-          coherent_store(dst + 1, (uint64_t)y.z | (uint64_t)y.w << 32);
-        } else {
-          *reinterpret_cast<uint4*>(out + at[it]) = y;
-        }
+        *reinterpret_cast<uint4*>(out + at[it]) = y;
       }
   }
-  if constexpr (POST) post_norm_band<BM>(args, out, m0, tm, TN, band_last);
 }
 
 template <int WN, int KS, int R, int C>
@@ -829,12 +708,7 @@ constexpr uint32_t kernel_lds_bytes() {
   return (uint32_t)((EX > 3 * A_BYTES ? EX : 3 * A_BYTES) + kLutStride * 2 + 64 * 64 * 4);
 }
 
-#define PK_F16K_POST(WN, KS, R, C, S, CLA)                                                     \
-  {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA, false, true>,                              \
-   gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA, false, true>}
-#define PK_F16K_NO_POST \
-  { nullptr, nullptr }
-#define PK_F16K_VARIANT(WN, KS, R, C, S, CLA, TAG, POST)                                                        \
+#define PK_F16K_VARIANT(WN, KS, R, C, S, CLA, TAG)                                                              \
   F16Variant {                                                                                              \
     TileShape{1, WN, R, C, KS}, "pk_gemm_f16p_b5_n" #WN "k" #KS "_m" #R "n" #C TAG,                         \
         "pk_gemm_f16p_b6_n" #WN "k" #KS "_m" #R "n" #C TAG,                                                 \
@@ -843,24 +717,21 @@ constexpr uint32_t kernel_lds_bytes() {
         kernel_lds_bytes<WN, KS, R, C>(),                                                                   \
         {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA, true>,                                            \
          gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA, true>},                                           \
-        POST                                                                                                \
   }
 
-// Post-norm kernels for the K-split tiles (two or four parts), the ones the
-// residual GEMMs of 1024 columns are planned on.
 const F16Variant kVariants[] = {
-    PK_F16K_VARIANT(2, 2, 6, 2, true, 2, "", PK_F16K_POST(2, 2, 6, 2, true, 2)),  // 192 x 128
-    PK_F16K_VARIANT(4, 1, 6, 1, true, 5, "", PK_F16K_NO_POST),                    // 192 x 128, no K split
-    PK_F16K_VARIANT(2, 2, 4, 2, true, 5, "", PK_F16K_POST(2, 2, 4, 2, true, 5)),  // 128 x 128
-    PK_F16K_VARIANT(2, 2, 3, 2, true, 5, "", PK_F16K_POST(2, 2, 3, 2, true, 5)),  // 96 x 128
-    PK_F16K_VARIANT(2, 2, 6, 1, true, 5, "", PK_F16K_POST(2, 2, 6, 1, true, 5)),  // 192 x 64
-    PK_F16K_VARIANT(1, 4, 4, 2, true, 5, "", PK_F16K_POST(1, 4, 4, 2, true, 5)),  // 128 x 64
-    PK_F16K_VARIANT(1, 4, 3, 2, true, 5, "", PK_F16K_POST(1, 4, 3, 2, true, 5)),  // 96 x 64
-    PK_F16K_VARIANT(1, 4, 2, 2, true, 5, "", PK_F16K_POST(1, 4, 2, 2, true, 5)),  // 64 x 64
-    PK_F16K_VARIANT(4, 1, 6, 2, true, 2, "", PK_F16K_NO_POST),                    // 192 x 256, no K split
-    PK_F16K_VARIANT(4, 1, 4, 2, true, 2, "", PK_F16K_NO_POST),                    // 128 x 256, no K split
-    PK_F16K_VARIANT(4, 1, 3, 2, true, 5, "", PK_F16K_NO_POST),                    // 96 x 256, no K split
-    PK_F16K_VARIANT(4, 1, 5, 2, true, 2, "", PK_F16K_NO_POST),                    // 160 x 256, no K split
+    PK_F16K_VARIANT(2, 2, 6, 2, true, 2, ""),  // 192 x 128
+    PK_F16K_VARIANT(4, 1, 6, 1, true, 5, ""),  // 192 x 128, no K split
+    PK_F16K_VARIANT(2, 2, 4, 2, true, 5, ""),  // 128 x 128
+    PK_F16K_VARIANT(2, 2, 3, 2, true, 5, ""),  // 96 x 128
+    PK_F16K_VARIANT(2, 2, 6, 1, true, 5, ""),  // 192 x 64
+    PK_F16K_VARIANT(1, 4, 4, 2, true, 5, ""),  // 128 x 64
+    PK_F16K_VARIANT(1, 4, 3, 2, true, 5, ""),  // 96 x 64
+    PK_F16K_VARIANT(1, 4, 2, 2, true, 5, ""),  // 64 x 64
+    PK_F16K_VARIANT(4, 1, 6, 2, true, 2, ""),  // 192 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 4, 2, true, 2, ""),  // 128 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 3, 2, true, 5, ""),  // 96 x 256, no K split
+    PK_F16K_VARIANT(4, 1, 5, 2, true, 2, ""),  // 160 x 256, no K split
 };
 
 }  // namespace
@@ -882,14 +753,6 @@ hipError_t launch_gemm_f16k(int bits, const f16::F16Variant& v, const GemmArgs& 
     // The fused row norm needs the fixed-palette path and K staged in LDS.
     if (!single || args.inner > kNormMaxInner || !v.normed[bits == 6]) return hipErrorInvalidValue;
     return launch_timed(v.normed[bits == 6], dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
-  }
-  if (args.post_output) {
-    // The post-norm tail: fixed-palette path, rows of whole 16-byte vectors
-    // that a wavefront holds, a band counter per row tile.
-    if (!single || !v.post[bits == 6] || args.glu || args.splits > 1 || !args.band_counters ||
-        args.columns % 8u != 0 || args.columns > kPostNormMaxColumns)
-      return hipErrorInvalidValue;
-    return launch_timed(v.post[bits == 6], dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
   }
   return launch_timed(single ? v.single[bits == 6] : v.general[bits == 6], dim3(groups), dim3(v.shape.threads()),
                       stream, start, stop, args);

@@ -96,26 +96,8 @@ struct GemmArgs {
   const _Float16* norm_gamma;  // [K] or null
   const float* norm_columns;   // [2N] or null
   float norm_epsilon;
-  // Post-norm (pair-code kernels with a post variant; f16, N % 8 == 0,
-  // N <= kPostNormMaxColumns): the output tiles go out as agent-coherent
-  // stores, each workgroup then counts itself into its row tile's
-  // band_counters entry, and the last of the row tile's column tiles reads
-  // the band's finished rows back and writes post_output = LayerNorm(row)
-  // (with post_next_output set, also LayerNorm'(post_output row)), with the
-  // arithmetic of the LayerNorm kernel; it resets the counter to zero.
-  const float* post_gamma;       // [N] or null
-  const float* post_beta;        // [N]
-  void* post_output;             // [M, N]
-  const float* post_next_gamma;  // [N] or null
-  const float* post_next_beta;   // [N]
-  void* post_next_output;        // [M, N]
-  float post_epsilon;
-  uint32_t* band_counters;       // [row tiles], zero between launches
 };
 
-// Widest row the post-norm epilogue holds in registers (2 KB of f16, two
-// 8-channel vectors per lane, as the LayerNorm kernel holds such rows).
-constexpr uint32_t kPostNormMaxColumns = 1024;
 
 // Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
 // waves_m x waves_n x k_split wavefronts; a wavefront owns m_blocks x
@@ -204,8 +186,6 @@ uint32_t f16_variant_lds_bytes(int index);
 enum F16Family : int { kFamilyOperandOrder = 0, kFamilyPairCode = 1, kFamilySmallM = 2 };
 int f16_variant_family(int index);
 inline bool f16_variant_splits(int index) { return f16_variant_family(index) == kFamilyOperandOrder; }
-// Whether an f16 variant has the post-norm epilogue (GemmArgs::post_output).
-bool f16_variant_post(int index);
 // Parts of the code layout an f16 variant reads (pk_internal.h layout): its
 // K split for the pair-code family, 1 for every other kernel.
 inline int f16_variant_parts(int index) {

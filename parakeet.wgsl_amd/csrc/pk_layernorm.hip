@@ -3,8 +3,8 @@
 //
 // mean = sum(x) / C, variance = max(sum(x^2) / C - mean^2, 0),
 // out = (x - mean) * rsqrt(variance + epsilon) * gamma + beta, statistics in
-// f32, output rounded to the storage type (the arithmetic of pk_rownorm.h,
-// which the GEMM's post-norm epilogue shares). One wavefront per row: each lane
+// f32, output rounded to the storage type (the arithmetic of pk_rownorm.h).
+// One wavefront per row: each lane
 // loads 16-byte vectors (8 f16 or 4 f32 channels; 4 f16 channels when the
 // row length is not a multiple of 8) at a stride of 64 vectors, together
 // with the gamma and beta of those channels, so a row costs one memory round

@@ -1,7 +1,5 @@
-// pk_rownorm.h - the per-row LayerNorm arithmetic (reference:
-// src/webgpu/kernels/layernorm.ts, shader :309-390) shared by the LayerNorm
-// kernel and the GEMM epilogue that normalises finished row bands, so both
-// produce the same bits from the same row:
+// pk_rownorm.h - the per-row LayerNorm arithmetic of the LayerNorm kernel
+// (reference: src/webgpu/kernels/layernorm.ts, shader :309-390):
 //   mean = sum(x) / C, variance = max(sum(x^2) / C - mean^2, 0),
 //   out = (x - mean) * rsqrt(variance + epsilon) * gamma + beta,
 // statistics in f32, one wavefront per row, a lane summing its vectors in

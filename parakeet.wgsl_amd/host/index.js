@@ -74,7 +74,6 @@ const FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 17301504;
 const REQUIRE_PRODUCTION_SIGNATURE = 1;
 const GEMM_GLU = 2;
 const GEMM_ROW_NORM = 4;
-const GEMM_POST_NORM = 8;
 const CONV_INPUT_GLU = 1;
 
 /** runtime-plan.ts:352-368 */
@@ -864,7 +863,7 @@ class PaletteGemmKernel {
     const d = {
       label: descriptor.label,
       flags: (this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0) | (descriptor.glu ? GEMM_GLU : 0) |
-        (descriptor.rowNorm ? GEMM_ROW_NORM : 0) | (descriptor.postNorm ? GEMM_POST_NORM : 0),
+        (descriptor.rowNorm ? GEMM_ROW_NORM : 0),
       precision: fp32 ? "f32" : "f16",
       paletteBits,
       rows: descriptor.rows,
@@ -904,29 +903,6 @@ class PaletteGemmKernel {
       d.normBeta = beta.binding.buffer.address + BigInt(beta.binding.offset);
       d.normBetaBytes = beta.binding.size;
       if (epsilon !== undefined) d.normEpsilon = epsilon;
-    }
-    if (descriptor.postNorm) {
-      // {gamma, beta, output, epsilon?, next?: {gamma, beta, output}}: the op also writes the LayerNorm
-      // of its output rows, and a chained second one (no reference counterpart)
-      const { gamma, beta, output, epsilon, next } = descriptor.postNorm;
-      const place = (tensor) => tensor.binding.buffer.address + BigInt(tensor.binding.offset);
-      const o = this.arena.binding(output);
-      d.postGamma = place(gamma);
-      d.postGammaBytes = gamma.binding.size;
-      d.postBeta = place(beta);
-      d.postBetaBytes = beta.binding.size;
-      d.postOutput = o.buffer.address + BigInt(o.offset);
-      d.postOutputBytes = o.size;
-      if (epsilon !== undefined) d.postEpsilon = epsilon;
-      if (next) {
-        const n = this.arena.binding(next.output);
-        d.postNextGamma = place(next.gamma);
-        d.postNextGammaBytes = next.gamma.binding.size;
-        d.postNextBeta = place(next.beta);
-        d.postNextBetaBytes = next.beta.binding.size;
-        d.postNextOutput = n.buffer.address + BigInt(n.offset);
-        d.postNextOutputBytes = n.size;
-      }
     }
     return d;
   }
@@ -1595,11 +1571,9 @@ class ParakeetEncoderGraph {
    * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
    * epilogue; default true, false keeps the GLU in the convolution),
    * options.fusedNorms (the four LayerNorms that feed a GEMM
-   * run inside it), options.unchainedNorms (one launch per LayerNorm;
+   * run inside it) and options.unchainedNorms (one launch per LayerNorm;
    * by default a layer's last LayerNorm also writes the next layer's
-   * first) and options.postNorms (the residual GEMMs write the LayerNorms
-   * after them; measured slower, off by default),
-   * none with a reference counterpart, options.featureFrames (default
+   * first), none with a reference counterpart, options.featureFrames (default
    * 1501), and options.executionProfile (encoder.ts:1299-1305: {precision:
    * "fp16"} by default, or {precision: "fp32"} for an fp32 package: f32
    * activations, palettes, positions and convolution weights, and f32
@@ -1646,7 +1620,7 @@ class ParakeetEncoderGraph {
     try {
       handle = native().encoderCreate(device.context, {
         label: o.label || "encoder", precision, fusedGlu: o.fusedGlu !== false, fusedNorms: o.fusedNorms === true,
-        unchainedNorms: o.unchainedNorms === true, postNorms: o.postNorms === true, batchSize, frames,
+        unchainedNorms: o.unchainedNorms === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
         featureLengths: buffers.featureLengths.address, projector, projectorBias,

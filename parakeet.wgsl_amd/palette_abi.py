@@ -22,14 +22,12 @@ ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
 REQUIRE_PRODUCTION_SIGNATURE = 0x1
 GEMM_GLU = 0x2
 GEMM_ROW_NORM = 0x4
-GEMM_POST_NORM = 0x8
 CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 ENCODER_FUSED_GLU = 0x1
 ENCODER_FUSED_NORMS = 0x2
 ENCODER_SEPARATE_GLU = 0x8
 ENCODER_UNCHAINED_NORMS = 0x4
-ENCODER_POST_NORMS = 0x10
 ENCODER_CHANNELS = 1024
 ENCODER_INTERMEDIATE = 4096
 # The fifteen dispatches of one encoder layer, in launch order
@@ -101,19 +99,6 @@ class GemmDesc(ctypes.Structure):
         ("norm_beta", ctypes.c_void_p),
         ("norm_beta_bytes", ctypes.c_uint64),
         ("norm_epsilon", ctypes.c_float),
-        ("post_gamma", ctypes.c_void_p),
-        ("post_gamma_bytes", ctypes.c_uint64),
-        ("post_beta", ctypes.c_void_p),
-        ("post_beta_bytes", ctypes.c_uint64),
-        ("post_epsilon", ctypes.c_float),
-        ("post_output", ctypes.c_void_p),
-        ("post_output_bytes", ctypes.c_uint64),
-        ("post_next_gamma", ctypes.c_void_p),
-        ("post_next_gamma_bytes", ctypes.c_uint64),
-        ("post_next_beta", ctypes.c_void_p),
-        ("post_next_beta_bytes", ctypes.c_uint64),
-        ("post_next_output", ctypes.c_void_p),
-        ("post_next_output_bytes", ctypes.c_uint64),
     ]
 
 
@@ -752,23 +737,14 @@ class GemmOp:
                  prepared: PreparedWeight | None = None, label: str = "palette-gemm",
                  production_only: bool = False, glu: bool = False, stream=None,
                  norm_gamma: DeviceArray | None = None, norm_beta: DeviceArray | None = None,
-                 norm_epsilon: float = 0.0, post_gamma: DeviceArray | None = None,
-                 post_beta: DeviceArray | None = None, post_output: DeviceArray | None = None,
-                 post_epsilon: float = 0.0, post_next_gamma: DeviceArray | None = None,
-                 post_next_beta: DeviceArray | None = None, post_next_output: DeviceArray | None = None):
+                 norm_epsilon: float = 0.0):
         """With norm_gamma / norm_beta (f32 [inner]) the op multiplies the
-        row LayerNorm of `a` (PK_GEMM_ROW_NORM). With post_gamma / post_beta
-        (f32 [columns]) and post_output it also writes the LayerNorm of its
-        output rows, and with post_next_* a chained second one
-        (PK_GEMM_POST_NORM)."""
+        row LayerNorm of `a` (PK_GEMM_ROW_NORM)."""
         precision = "f16" if palette.dtype == np.float16 else "f32"
         groups = palette.shape[0]
         flags = ((REQUIRE_PRODUCTION_SIGNATURE if production_only else 0) | (GEMM_GLU if glu else 0) |
-                 (GEMM_ROW_NORM if norm_gamma is not None else 0) |
-                 (GEMM_POST_NORM if post_output is not None else 0))
+                 (GEMM_ROW_NORM if norm_gamma is not None else 0))
 
-        def ref(x):
-            return (x.ptr, x.nbytes) if x is not None else (None, 0)
         self.desc = GemmDesc(
             ctypes.sizeof(GemmDesc), flags,
             label.encode(), PRECISION[precision], bits, rows, inner, columns, groups,
@@ -782,8 +758,7 @@ class GemmOp:
             prepared.handle if prepared is not None else None,
             norm_gamma.ptr if norm_gamma is not None else None, norm_gamma.nbytes if norm_gamma is not None else 0,
             norm_beta.ptr if norm_beta is not None else None, norm_beta.nbytes if norm_beta is not None else 0,
-            float(norm_epsilon), *ref(post_gamma), *ref(post_beta), float(post_epsilon), *ref(post_output),
-            *ref(post_next_gamma), *ref(post_next_beta), *ref(post_next_output))
+            float(norm_epsilon))
         handle = ctypes.c_void_p()
         check(load().pk_gemm_create(ctx.handle, ctypes.byref(self.desc), stream, ctypes.byref(handle)))
         self.handle = handle.value
@@ -1133,7 +1108,7 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
 
 
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = True,
-                 fused_norms: bool = False, unchained_norms: bool = False, post_norms: bool = False,
+                 fused_norms: bool = False, unchained_norms: bool = False,
                  subsampling: dict | None = None,
                  feature_frames: int = 0, feature_lengths=None, projector=None, projector_bias=None,
                  projected_output=None, projected_channels: int = 0, label: str = "encoder",
@@ -1147,7 +1122,7 @@ def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frame
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
     flags = ((0 if fused_glu else ENCODER_SEPARATE_GLU) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
-             (ENCODER_UNCHAINED_NORMS if unchained_norms else 0) | (ENCODER_POST_NORMS if post_norms else 0))
+             (ENCODER_UNCHAINED_NORMS if unchained_norms else 0))
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
                        PRECISION[precision], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),

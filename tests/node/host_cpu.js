@@ -95,23 +95,6 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
   throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu",
     mutate: (d) => { d.rowNorm = { gamma: normTensor(4096), beta: normTensor(4096), epsilon: -1 }; } })),
       Error, "epsilon >= 0");
-  // postNorm (PK_GEMM_POST_NORM, no reference counterpart): f32 gamma / beta of N channels, the
-  // normalised rows apart from the input and the residual, the chained rows apart from the first
-  const contract = (mutate) => descriptor({ label: "encoder-layer-ff-contract", inner: 4096, columns: 1024,
-                                            residual: true, residualScale: 0.5, mutate });
-  const post = (o) => (d) => {
-    d.postNorm = Object.assign({ gamma: normTensor(4096), beta: normTensor(4096),
-                                 output: arena.slice("n", 768 * 1024 * 1024, 7520 * 1024 * 2) }, o);
-  };
-  kernel.validateDescriptor(contract(post({})));
-  kernel.validateDescriptor(contract(post({ next: { gamma: normTensor(4096), beta: normTensor(4096),
-                                                    output: arena.slice("c", 256 * 1024 * 1024, 7520 * 1024 * 2) } })));
-  throwsLike(() => kernel.validateDescriptor(contract(post({ beta: normTensor(2048) }))), Error,
-             "post norm needs gamma and beta of 4096 bytes");
-  throwsLike(() => kernel.validateDescriptor(contract(post({ output: arena.slice("r", 512 * 1024 * 1024, 7520 * 1024 * 2) }))),
-             Error, "post norm output must not overlap the input or the residual");
-  throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu", mutate: post({}) })), Error,
-             "post norm needs f16, N % 8 == 0, N <= 1024");
   // arena.ts slice rules
   throwsLike(() => arena.slice("x", 100, 64), RangeError, "Invalid activation slice x");
   // the counters of a fused kernel: nothing is ever expanded

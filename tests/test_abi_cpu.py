@@ -427,88 +427,6 @@ def test_chained_layernorm_contract(abi):
             _validate_ln(abi, **chained(next_output=_Fake(bad, kw["output"].nbytes)))
 
 
-def _post_norm_desc(abi, rows=96, columns=1024, precision="f16", flags=None, **over):
-    """A GEMM descriptor with PK_GEMM_POST_NORM over stand-in addresses
-    (the host-only check never touches them): X [rows, 1024] @ W (5-bit) +
-    residual, LayerNorm of the output rows into a buffer of its own."""
-    elem = 2 if precision == "f16" else 4
-    inner = 1024
-    mb = 1 << 24
-    f = dict(a=0x10000000, residual=0x12000000, output=0x14000000, post_output=0x16000000,
-             gamma=0x18000000, beta=0x18100000, packed=0x19000000, palette=0x1a000000,
-             next_gamma=0, next_beta=0, next_output=0)
-    f.update(over)
-    rows_bytes = rows * columns * 2
-    d = abi.GemmDesc()
-    d.struct_size = ctypes.sizeof(abi.GemmDesc)
-    d.flags = abi.GEMM_POST_NORM if flags is None else flags
-    d.label = b"encoder.layers.0-feed-forward1-linear2-residual"
-    d.precision = abi.PRECISION[precision]
-    d.palette_bits, d.rows, d.inner, d.columns = 5, rows, inner, columns
-    d.palette_groups, d.palette_group_columns = 1, columns
-    d.a, d.a_bytes = f["a"], rows * inner * elem
-    d.packed, d.packed_bytes = f["packed"], inner * columns * 5 // 8
-    d.palette, d.palette_bytes = f["palette"], 32 * elem
-    d.output, d.output_bytes = f["output"], rows * columns * elem
-    d.residual, d.residual_bytes = f["residual"], rows * columns * elem
-    d.has_residual_scale, d.residual_scale = 1, 0.5
-    d.post_gamma, d.post_gamma_bytes = f["gamma"], over.get("gamma_bytes", columns * 4)
-    d.post_beta, d.post_beta_bytes = f["beta"], columns * 4
-    d.post_output, d.post_output_bytes = f["post_output"], over.get("post_output_bytes", rows_bytes)
-    if f["next_output"]:
-        d.post_next_gamma, d.post_next_gamma_bytes = f["next_gamma"], columns * 4
-        d.post_next_beta, d.post_next_beta_bytes = f["next_beta"], over.get("next_beta_bytes", columns * 4)
-        d.post_next_output, d.post_next_output_bytes = f["next_output"], rows_bytes
-    assert mb > rows_bytes
-    return d
-
-
-def test_post_norm_gemm_contract(abi):
-    """PK_GEMM_POST_NORM (no reference counterpart): f16, N % 8 == 0 and
-    N <= 1024, gamma / beta of N f32 channels, output capacity, and the
-    aliasing rules (the LayerNorm outputs apart from the input and the
-    residual, the GEMM output itself or apart from it, the chained output
-    apart from the first)."""
-    lib = abi.load()
-    name = "encoder.layers.0-feed-forward1-linear2-residual"
-
-    def validate(d):
-        abi.check(lib.pk_gemm_validate(ctypes.byref(d)))
-
-    validate(_post_norm_desc(abi))
-    validate(_post_norm_desc(abi, post_output=0x14000000))  # in place over the output
-    validate(_post_norm_desc(abi, next_gamma=0x18200000, next_beta=0x18300000, next_output=0x14000000))
-    validate(_post_norm_desc(abi, columns=512))
-    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs f16, N % 8 == 0, N <= 1024")):
-        validate(_post_norm_desc(abi, precision="f32"))
-    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs f16, N % 8 == 0, N <= 1024")):
-        validate(_post_norm_desc(abi, columns=2048))
-    both = _post_norm_desc(abi, flags=abi.GEMM_POST_NORM | abi.GEMM_ROW_NORM)
-    both.norm_gamma, both.norm_gamma_bytes, both.norm_beta, both.norm_beta_bytes = 0x1c000000, 4096, 0x1c100000, 4096
-    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs f16")):
-        validate(both)
-    odd_k = _post_norm_desc(abi)
-    odd_k.inner, odd_k.a_bytes, odd_k.packed_bytes = 1056, 96 * 1056 * 2, 1056 * 1024 * 5 // 8
-    with pytest.raises(abi.PaletteError, match=re.escape(f"{name} post norm needs K % 64 == 0")):
-        validate(odd_k)
-    with pytest.raises(abi.PaletteError, match=f"{name} post norm needs gamma and beta of 4096 bytes"):
-        validate(_post_norm_desc(abi, gamma_bytes=2048))
-    with pytest.raises(abi.PaletteError, match=f"{name} post norm needs gamma and beta of 4096 bytes"):
-        validate(_post_norm_desc(abi, gamma=0x18000004))
-    with pytest.raises(abi.PaletteError, match=f"{name} post norm output must hold 196608 bytes"):
-        validate(_post_norm_desc(abi, post_output_bytes=4096))
-    for bad in (0x10000000 + 4096, 0x12000000, 0x14000000 + 2048):
-        with pytest.raises(abi.PaletteError, match="post norm output must not overlap the input or the residual"):
-            validate(_post_norm_desc(abi, post_output=bad))
-    with pytest.raises(abi.PaletteError, match="post norm next gamma and beta must hold 4096 bytes"):
-        validate(_post_norm_desc(abi, next_gamma=0x18200000, next_beta=0x18300000, next_output=0x1b000000,
-                                 next_beta_bytes=64))
-    for bad in (0x16000000, 0x12000000 + 64):
-        with pytest.raises(abi.PaletteError, match="post norm next output must not overlap the input, the residual "
-                                                   "or the post norm output"):
-            validate(_post_norm_desc(abi, next_gamma=0x18200000, next_beta=0x18300000, next_output=bad))
-
-
 # ---------------------------------------------------------------- subsampling
 
 
@@ -842,7 +760,7 @@ def test_encoder_validate_stack_fields(abi):
     with pytest.raises(abi.PaletteError, match="unsupported precision 7"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
-    desc.flags = 0x20
+    desc.flags = 0x10
     with pytest.raises(abi.PaletteError, match="unknown flags"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
@@ -851,10 +769,6 @@ def test_encoder_validate_stack_fields(abi):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc.flags = abi.ENCODER_FUSED_GLU  # the default, still accepted
     abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
-    _validate_encoder(abi, post_norms=True, **_encoder_fakes())  # the residual GEMMs write the LayerNorms after them
-    _validate_encoder(abi, post_norms=True, unchained_norms=True, **_encoder_fakes())
-    with pytest.raises(abi.PaletteError, match="PK_ENCODER_FUSED_NORMS and PK_ENCODER_POST_NORMS exclude each other"):
-        _validate_encoder(abi, post_norms=True, fused_norms=True, **_encoder_fakes())
     # the fp32 profile: accepted, without the f16-only fusions
     _validate_encoder(abi, precision="f32", **_encoder_fakes(layers=24, elem=4))
     for flags in (abi.ENCODER_FUSED_GLU, abi.ENCODER_FUSED_NORMS):
