@@ -93,6 +93,9 @@ def parse_args():
     p.add_argument("--separate-glu", action="store_true",
                    help="encoder workloads: the convolution forms the GLU from PW1's values and gates, as the "
                         "reference does (PK_ENCODER_SEPARATE_GLU; default: PW1's epilogue writes the GLU)")
+    p.add_argument("--prefix-same-plan", action="store_true",
+                   help="encoder workloads with --active below --windows: the prefix keeps the capacity's kernels "
+                        "(PK_ENCODER_PREFIX_SAME_PLAN; default: the plans of a graph built for the active windows)")
     p.add_argument("--unchained-norms", action="store_true",
                    help="encoder workloads: launch every LayerNorm on its own (default: each layer's last "
                         "LayerNorm also writes the next layer's first)")
@@ -500,14 +503,14 @@ def split_trace(path, warmup, steps, layers=24):
               f"avg {us.mean():.2f} us, min {us.min():.2f}, max {us.max():.2f}")
 
 
-def roofline_loop(ctx, abi, kind, layer0, a_rows, stream):
+def roofline_loop(ctx, abi, kind, layer0, a_rows, rows, stream):
     """Average duration of `kind`'s GEMM (rebuilt from LAYER_GEMMS with layer
-    0's weights at the pass's shape) over ROOFLINE_LOOP back-to-back launches
-    on `stream`, timed by one pair of events around the loop: the condition
-    of the graph replay, where every launch follows the last with no gap."""
+    0's weights at the pass's shape: `rows` active rows of `a_rows`) over
+    ROOFLINE_LOOP back-to-back launches on `stream`, timed by one pair of
+    events around the loop: the condition of the graph replay, where every
+    launch follows the last with no gap."""
     key, inner, columns, groups, activation, scale = LAYER_GEMMS[kind]
     packed, palette = layer0[key]
-    rows = a_rows.shape[0]
     dtype = a_rows.dtype
     a = a_rows if inner == a_rows.shape[1] else ctx.empty((rows, inner), dtype)
     out = ctx.empty((rows, columns), dtype)
@@ -699,7 +702,7 @@ def run_encoder(args, abi, ctx, decoder=False):
                         feature_lengths=feature_lengths, projector=upload(stack.projector),
                         projector_bias=put(stack.projector_bias), projected_channels=stack.projector_bias.size,
                         projected_output=projected, fused_norms=args.fused_norms,
-                        unchained_norms=args.unchained_norms,
+                        unchained_norms=args.unchained_norms, prefix_same_plan=args.prefix_same_plan,
                         fused_glu=not args.separate_glu, label="encoder",
                         precision=args.precision)
     launches, device_bytes = enc.info()
@@ -812,7 +815,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     # is kept beside it.
     loop_us = None
     if name in LAYER_GEMMS:
-        loop_us = roofline_loop(ctx, abi, name, layers[0], out, stream)
+        loop_us = roofline_loop(ctx, abi, name, layers[0], out, active * stack.frames, stream)
     us = loop_us if loop_us is not None else dom["avg_us"]
     if dom["flops"] / (peak * 1e12) >= dom["algorithmic_bytes"] / (PEAK_HBM_GBS * 1e9):
         achieved = dom["flops"] / (us * 1e-6) / 1e12
@@ -887,6 +890,9 @@ def run_encoder(args, abi, ctx, decoder=False):
                    "glu": "in the convolution (PK_ENCODER_SEPARATE_GLU)" if args.separate_glu
                           else "in the convolution (the fp32 profile)" if f32 else "in PW1's epilogue",
                    "graph_replay": True,
+                   "prefix_plans": None if active == stack.batch else
+                                   ("the capacity's kernels" if args.prefix_same_plan else
+                                    f"those of a graph built for {active} windows"),
                    "decoder": "greedy TDT, LSTM 2 x 640, joint 1024 + blank, 5 durations" if tdt else None},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -42,6 +42,12 @@ extern "C" {
    "head-vector-position-vec4" order [8][32][2T-1][4]. No counterpart in the
    reference, whose converter packs the table offline. */
 #define PK_ATTENTION_POSITIONS_ROW_MAJOR 0x1u
+/* An active batch below batch_size runs the variant that pk_attention_create
+   plans for a descriptor of that many windows (as a dedicated op would;
+   outputs bit-identical to such an op), not the op's own. No counterpart
+   in the reference, whose one pipeline serves every active batch
+   (attention.ts:62-91). pk_attention_set_variant overrides it. */
+#define PK_ATTENTION_PLAN_ACTIVE 0x2u
 
 typedef struct pk_attention_op pk_attention_op;
 

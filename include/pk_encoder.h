@@ -62,6 +62,18 @@ extern "C" {
    first launch nothing in their LN ff1 slot: 23 fewer launches per 24-layer
    pass, bit-identical outputs. This flag keeps one launch per LayerNorm. */
 #define PK_ENCODER_UNCHAINED_NORMS 0x4u
+/* By default an active batch a below batch_size runs every GEMM and the
+   attention with the plan a graph built for a windows would use
+   (pk_gemm_prepare_rows for every a at create, PK_ATTENTION_PLAN_ACTIVE):
+   a prefix runs as fast as a dedicated graph and its outputs are
+   bit-identical to that graph's, within tolerance of the same windows of a
+   full pass; the GEMMs whose prefix plans read codes in other K parts keep
+   copies of their codes (device_bytes counts them). With this flag a
+   prefix keeps each op's kernel family and K split, as the reference's
+   single pipeline per dispatch does (encoder.ts:197-200, gemm.ts:427-451):
+   outputs bit-identical to the same windows of a full pass, at up to
+   1.7x the time of a dedicated graph for small prefixes. */
+#define PK_ENCODER_PREFIX_SAME_PLAN 0x10u
 
 typedef struct pk_encoder pk_encoder;
 

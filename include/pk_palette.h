@@ -252,8 +252,22 @@ int pk_gemm_validate(const pk_gemm_desc *desc);
    per active batch, gemm.ts:427-451): the tile shape may change, but not the
    kernel family or K split, so the codes the op holds serve it and a
    prefix's outputs are bit-identical to the same rows of a full launch; the
-   choice is cached per op. */
+   choice is cached per op. A row count given to pk_gemm_prepare_rows runs
+   its prepared plan instead. */
 int pk_gemm_enqueue(pk_gemm_op *op, uint32_t active_rows, void *stream);
+/* No reference counterpart (there one pipeline serves every active batch,
+   gemm.ts:427-451): prepares each of `count` active row counts to run the
+   plan that pk_gemm_create makes for a descriptor of that many rows - its
+   tile, kernel family and K split - so such a prefix is as fast as a
+   dedicated op and its outputs are bit-identical to that op's (and within
+   the GEMM's tolerance of the same rows of a full launch). A plan that
+   reads the codes split into other K parts gets a copy of the codes in
+   that layout, derived on the device from the op's own and kept by the op
+   (up to two copies). Call before launches that use those row counts (not
+   while a launch of the op is in flight); pk_gemm_set_variant and
+   pk_gemm_set_splits drop the prepared plans. Row counts must be in
+   [1, rows] (PK_RANGE_ERROR); repeated counts are prepared once. */
+int pk_gemm_prepare_rows(pk_gemm_op *op, const uint32_t *active_rows, uint32_t count);
 /* pk_gemm_enqueue with the timestampWrites of GemmDispatch.encode
    (gemm.ts:419-463): the kernel's own dispatch stamps `start_event` when it
    begins and `end_event` when it ends (either may be NULL; both from

@@ -1219,7 +1219,7 @@ static int parse_encoder_subsampling(napi_env env, napi_value o, pk_encoder_subs
   return ok;
 }
 
-/* Parses an encoder descriptor: {label, precision?, fusedGlu?, fusedNorms?, unchainedNorms?,
+/* Parses an encoder descriptor: {label, precision?, fusedGlu?, fusedNorms?, unchainedNorms?, prefixSamePlan?,
    batchSize, frames,
    layers: [layer...], validLengths, input, output, subsampling?,
    featureFrames?, featureLengths?, projector?, projectorBias?,
@@ -1240,6 +1240,9 @@ static int parse_encoder_desc(napi_env env, napi_value o, pk_encoder_desc *d) {
   if (prop(env, o, "unchainedNorms", &v) && napi_get_value_bool(env, v, &unchained_norms) == napi_ok &&
       unchained_norms)
     d->flags |= PK_ENCODER_UNCHAINED_NORMS;
+  bool same_plan = false;
+  if (prop(env, o, "prefixSamePlan", &v) && napi_get_value_bool(env, v, &same_plan) == napi_ok && same_plan)
+    d->flags |= PK_ENCODER_PREFIX_SAME_PLAN;
   if (!prop_u32(env, o, "batchSize", &d->batch_size) || !prop_u32(env, o, "frames", &d->frames) ||
       !prop(env, o, "layers", &layers) || napi_get_array_length(env, layers, &n) != napi_ok || n == 0) {
     bad_argument(env, "encoder descriptor is missing a required field");

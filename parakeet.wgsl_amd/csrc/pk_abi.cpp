@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -125,10 +126,24 @@ struct pk_gemm_op {
   uint64_t workspace_bytes = 0;
   // Fused row LayerNorm (PK_GEMM_ROW_NORM): G and B [2N] f32, then f16 gamma [K].
   void* norm_buffer = nullptr;
+  // Active row counts given to pk_gemm_prepare_rows: the variant a
+  // dedicated op of that many rows plans and the codes it reads (the
+  // weight's own layout, or one of `layouts`: the same codes split into 1,
+  // 2 or 4 K parts, owned by the op).
+  struct RowPlan {
+    int variant;
+    const uint32_t* codes;
+  };
+  std::map<uint32_t, RowPlan> row_plans;
+  uint32_t* layouts[3] = {};
+  uint64_t layout_bytes = 0;
+  bool shared_weight = false;  // created over a pk_prepared_weight of the caller
   bool destroyed = false;
 };
 
-uint64_t pk_abi::gemm_weight_bytes(const pk_gemm_op* op) { return op && op->weight ? op->weight->bytes : 0; }
+uint64_t pk_abi::gemm_weight_bytes(const pk_gemm_op* op) {
+  return op && op->weight ? op->weight->bytes + op->layout_bytes : 0;
+}
 
 namespace {
 
@@ -899,6 +914,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   if (d->prepared) {
     op->weight = const_cast<pk_prepared_weight*>(d->prepared);
     op->weight->refs.fetch_add(1);
+    op->shared_weight = true;
   } else {
     pk_prepared_weight* w = nullptr;
     if (int s = make_weight(ctx, label, bits, d->inner, d->columns, d->packed, stream_or_default(ctx, stream), &w,
@@ -993,6 +1009,55 @@ int variant_for_rows(pk_gemm_op* op, uint32_t rows) {
   return op->active_variant;
 }
 
+// The prepared plan of `rows` active rows (pk_gemm_prepare_rows), or null.
+const pk_gemm_op::RowPlan* row_plan(const pk_gemm_op* op, uint32_t rows) {
+  if (op->forced || rows == op->rows) return nullptr;
+  const auto it = op->row_plans.find(rows);
+  return it == op->row_plans.end() ? nullptr : &it->second;
+}
+
+int layout_index(int parts) { return parts == 1 ? 0 : parts == 2 ? 1 : 2; }
+
+// The op's codes split into `parts` K parts: the weight's own layout, or a
+// copy the op derives from it on the device once and keeps.
+int codes_in_layout(pk_gemm_op* op, int parts, const uint32_t** out) {
+  pk_prepared_weight* w = op->weight;
+  if (parts == w->parts) {
+    *out = w->codes;
+    return PK_OK;
+  }
+  uint32_t*& dst = op->layouts[layout_index(parts)];
+  if (!dst) {
+    const uint64_t bytes = pk::operand_order_words(w->bits, w->inner, w->columns, parts) * 4u;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&dst), bytes);
+    if (e != hipSuccess) {
+      dst = nullptr;
+      return fail(PK_ALLOCATION_FAILURE, "%s: cannot allocate %llu bytes of codes in %d K parts: %s",
+                  op->label.c_str(), (unsigned long long)bytes, parts, hipGetErrorString(e));
+    }
+    const uint64_t blocks = (uint64_t)(pk::padded_columns(w->columns) / 32u) * (pk::padded_inner(w->inner) / 64u);
+    e = pk::launch_relayout(w->bits, w->codes, w->parts, dst, parts, blocks, op->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(op->ctx->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(dst);
+      dst = nullptr;
+      return fail(PK_DEVICE_ERROR, "%s: palette code relayout failed: %s", op->label.c_str(), hipGetErrorString(e));
+    }
+    op->layout_bytes += bytes;
+  }
+  *out = dst;
+  return PK_OK;
+}
+
+void drop_row_plans(pk_gemm_op* op) {
+  op->row_plans.clear();
+  for (uint32_t*& l : op->layouts) {
+    free_after_drain(op->ctx->device, l);
+    l = nullptr;
+  }
+  op->layout_bytes = 0;
+}
+
 int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, void* start_event, void* end_event) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
@@ -1000,9 +1065,11 @@ int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, vo
   // GemmDispatch.encode (gemm.ts:427-438)
   if (rows > op->rows)
     return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
-  const int variant = variant_for_rows(op, rows);
+  const pk_gemm_op::RowPlan* prepared = row_plan(op, rows);
+  const int variant = prepared ? prepared->variant : variant_for_rows(op, rows);
   pk::GemmArgs args = op->args;
   args.rows = rows;
+  if (prepared) args.codes = prepared->codes;
   // A split never gets an empty K range.
   args.splits = std::min(op->splits, k_blocks(op->args.inner));
   hipStream_t st = stream_or_default(op->ctx, stream);
@@ -1027,6 +1094,7 @@ int pk_gemm_destroy(pk_gemm_op* op) {
   free_after_drain(op->ctx->device, op->workspace);
   op->workspace = nullptr;
   op->workspace_bytes = 0;
+  drop_row_plans(op);
   return ok();
 }
 
@@ -1047,6 +1115,9 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no GLU epilogue", op->label.c_str(), variant);
   if (op->args.norm_columns && pk::f16_variant_family(variant) != pk::kFamilyPairCode)
     return fail(PK_RANGE_ERROR, "%s tile variant %d has no fused row norm", op->label.c_str(), variant);
+  // A forced variant runs at every row count: prepared row plans go (the
+  // relayout below may free the codes they read).
+  drop_row_plans(op);
   // A variant that reads another split of the codes: an op alone on its
   // weight moves it to that layout; a weight shared with other ops stays.
   const int parts = variant_parts(op->precision, variant);
@@ -1065,6 +1136,29 @@ int pk_gemm_set_variant(pk_gemm_op* op, int variant) {
   return ok();
 }
 
+int pk_gemm_prepare_rows(pk_gemm_op* op, const uint32_t* active_rows, uint32_t count) {
+  if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
+  if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
+  if (count && !active_rows) return fail(PK_INVALID_ARGUMENT, "%s: active row list is null", op->label.c_str());
+  for (uint32_t i = 0; i < count; ++i)
+    if (active_rows[i] == 0 || active_rows[i] > op->rows)
+      return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
+  PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint32_t rows = active_rows[i];
+    if (rows == op->rows || op->row_plans.count(rows)) continue;
+    // The plan of pk_gemm_create for a descriptor of `rows` rows (a shared
+    // prepared weight keeps its layout there too).
+    const Plan plan = plan_op(op->precision, rows, op->args.inner, op->args.columns, op->cus, op->args.glu != 0,
+                              op->shared_weight ? op->weight->parts : 0, op->args.norm_columns != nullptr);
+    if (plan.splits != 1) continue;  // a split-K plan would need its own workspace: keep the prefix plan
+    const uint32_t* codes = nullptr;
+    if (int s = codes_in_layout(op, variant_parts(op->precision, plan.variant), &codes)) return s;
+    op->row_plans[rows] = pk_gemm_op::RowPlan{plan.variant, codes};
+  }
+  return ok();
+}
+
 int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
   if (!op) return fail(PK_INVALID_ARGUMENT, "GEMM op is null");
   if (op->destroyed) return fail(PK_DESTROYED, "%s was destroyed", op->label.c_str());
@@ -1072,6 +1166,7 @@ int pk_gemm_set_splits(pk_gemm_op* op, uint32_t splits) {
   if (splits < 1 || splits > limit)
     return fail(PK_RANGE_ERROR, "%s split count %u outside [1, %u]", op->label.c_str(), splits, limit);
   if (int s = configure_launch(op, op->variant, splits)) return s;
+  drop_row_plans(op);
   op->forced = true;
   return ok();
 }
@@ -1111,7 +1206,8 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   if (rows > op->rows)
     return fail(PK_RANGE_ERROR, "%s active rows must be in [1, %u]", op->label.c_str(), op->rows);
   const bool f16 = op->precision == PK_PRECISION_F16;
-  const int variant = planned_variant(op, rows);
+  const pk_gemm_op::RowPlan* prepared = row_plan(op, rows);
+  const int variant = prepared ? prepared->variant : planned_variant(op, rows);
   const pk::TileShape s = f16 ? pk::f16_variant(variant) : pk::f32_variant(variant);
   std::memset(info, 0, sizeof *info);
   const uint32_t splits = std::min(op->splits, k_blocks(op->args.inner));

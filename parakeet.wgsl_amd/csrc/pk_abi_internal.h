@@ -33,7 +33,8 @@ inline int ok() { return PK_OK; }
 // with PK_DESTROYED.
 int check_ctx(const pk_context* ctx);
 
-// Device bytes of the prepared codes a GEMM op reads (its one layout).
+// Device bytes of the prepared codes a GEMM op reads (its own layout and
+// the copies in other layouts that its prepared row plans read).
 uint64_t gemm_weight_bytes(const pk_gemm_op* op);
 
 // Reference counting of contexts (see pk_context).

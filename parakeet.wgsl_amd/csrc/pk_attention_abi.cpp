@@ -20,6 +20,7 @@ struct pk_attention_op {
   uint32_t batch = 0;
   pk::AttnArgs args{};
   int variant = 0;
+  bool plan_active = false;  // PK_ATTENTION_PLAN_ACTIVE (until a variant is forced)
   bool destroyed = false;
 };
 
@@ -37,7 +38,7 @@ int validate_attention_desc(const pk_attention_desc* d) {
   if (d->struct_size != sizeof(pk_attention_desc))
     return fail(PK_INVALID_ARGUMENT, "pk_attention_desc.struct_size mismatch");
   const char* label = attention_label(d->label);
-  if (d->flags & ~PK_ATTENTION_POSITIONS_ROW_MAJOR)
+  if (d->flags & ~(PK_ATTENTION_POSITIONS_ROW_MAJOR | PK_ATTENTION_PLAN_ACTIVE))
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if (d->precision != PK_PRECISION_F16 && d->precision != PK_PRECISION_F32)
     return fail(PK_INVALID_ARGUMENT, "%s has an unsupported precision %d", label, d->precision);
@@ -89,10 +90,17 @@ int validate_attention_desc(const pk_attention_desc* d) {
   return PK_OK;
 }
 
+// The variant that runs `batch` windows: the op's own, or with
+// PK_ATTENTION_PLAN_ACTIVE the one created for that many windows.
+int variant_for(const pk_attention_op* op, uint32_t batch) {
+  if (!op->plan_active || batch == op->batch) return op->variant;
+  return pk::attention_default_variant(op->precision == PK_PRECISION_F16, op->args.frames, batch);
+}
+
 void fill_plan(const pk_attention_op* op, uint32_t batch, pk_attention_plan_info* info) {
   std::memset(info, 0, sizeof *info);
   const bool f16 = op->precision == PK_PRECISION_F16;
-  const pk::AttnGeometry g = pk::attention_geometry(f16, op->variant, op->args.frames, batch);
+  const pk::AttnGeometry g = pk::attention_geometry(f16, variant_for(op, batch), op->args.frames, batch);
   info->grid[0] = g.grid;
   info->grid[1] = 1;
   info->grid[2] = 1;
@@ -123,6 +131,7 @@ int pk_attention_create(pk_context* ctx, const pk_attention_desc* d, pk_attentio
   op->precision = d->precision;
   op->batch = d->batch_size;
   op->variant = pk::attention_default_variant(d->precision == PK_PRECISION_F16, d->frames, d->batch_size);
+  op->plan_active = (d->flags & PK_ATTENTION_PLAN_ACTIVE) != 0;
   pk::AttnArgs& a = op->args;
   a.qkv = d->qkv;
   a.positions = d->projected_positions;
@@ -151,7 +160,7 @@ int pk_attention_enqueue_timed(pk_attention_op* op, uint32_t active_batch, void*
     return fail(PK_RANGE_ERROR, "%s active batch must be in [1, %u]", op->label.c_str(), op->batch);
   PK_HIP(hipSetDevice(op->ctx->device), "hipSetDevice");
   const hipError_t e =
-      pk::launch_attention(op->precision == PK_PRECISION_F16, op->variant, op->args, batch,
+      pk::launch_attention(op->precision == PK_PRECISION_F16, variant_for(op, batch), op->args, batch,
                            stream_or_default(op->ctx, stream), static_cast<hipEvent_t>(start_event),
                            static_cast<hipEvent_t>(end_event));
   PK_HIP(e, "relative attention launch");
@@ -192,6 +201,7 @@ int pk_attention_set_variant(pk_attention_op* op, int variant) {
   if (variant < 0 || variant >= count)
     return fail(PK_RANGE_ERROR, "attention variant %d outside [0, %d)", variant, count);
   op->variant = variant;
+  op->plan_active = false;
   return ok();
 }
 

@@ -73,6 +73,7 @@ struct pk_encoder {
   bool fused_glu = true;
   bool fused_norms = false;
   bool chained_norms = true;  // norm_out also writes the next layer's norm_feed_forward1
+  bool prefix_same_plan = false;  // prefixes keep the capacity's kernel families (PK_ENCODER_PREFIX_SAME_PLAN)
   const uint32_t* valid_lengths = nullptr;
   const void* input = nullptr;
   void* output = nullptr;
@@ -395,6 +396,7 @@ int build_layer(pk_encoder* e, const pk_encoder_layer& w, const pk_encoder_layer
     pk_attention_desc d{};
     d.struct_size = sizeof d;
     d.label = name("-relative-attention");
+    d.flags = e->prefix_same_plan ? 0u : PK_ATTENTION_PLAN_ACTIVE;
     d.precision = e->precision;
     d.batch_size = e->batch;
     d.frames = e->frames;
@@ -567,6 +569,7 @@ void describe(pk_encoder* e, const pk_encoder_desc* d) {
   e->fused_glu = (d->flags & PK_ENCODER_SEPARATE_GLU) == 0 && d->precision == PK_PRECISION_F16;
   e->fused_norms = (d->flags & PK_ENCODER_FUSED_NORMS) != 0;
   e->chained_norms = (d->flags & (PK_ENCODER_FUSED_NORMS | PK_ENCODER_UNCHAINED_NORMS)) == 0;
+  e->prefix_same_plan = (d->flags & PK_ENCODER_PREFIX_SAME_PLAN) != 0;
   e->valid_lengths = d->valid_lengths;
   e->input = d->input;
   e->output = d->output;
@@ -589,7 +592,7 @@ int validate_encoder_desc(const pk_encoder_desc* d) {
     return fail(PK_INVALID_ARGUMENT, "pk_encoder_desc.struct_size mismatch");
   const char* label = d->label ? d->label : "encoder";
   if (d->flags & ~(PK_ENCODER_FUSED_GLU | PK_ENCODER_SEPARATE_GLU | PK_ENCODER_FUSED_NORMS |
-                   PK_ENCODER_UNCHAINED_NORMS))
+                   PK_ENCODER_UNCHAINED_NORMS | PK_ENCODER_PREFIX_SAME_PLAN))
     return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if ((d->flags & PK_ENCODER_FUSED_GLU) && (d->flags & PK_ENCODER_SEPARATE_GLU))
     return fail(PK_INVALID_ARGUMENT, "%s: PK_ENCODER_FUSED_GLU and PK_ENCODER_SEPARATE_GLU exclude each other", label);
@@ -640,7 +643,29 @@ int build_all(pk_encoder* e, const pk_encoder_desc* d, hipStream_t stream, bool 
       return s;
   if (e->projected_channels)
     if (int s = build_projector(e, d, stream, &e->projector, validate_only)) return s;
-  return PK_OK;
+  if (validate_only || e->prefix_same_plan || e->batch == 1) return PK_OK;
+  // Every active batch below the capacity runs the GEMM plans of a graph
+  // built for that many windows.
+  auto prepare = [&](pk_gemm_op* op, uint32_t rows_per_window) -> int {
+    if (!op) return PK_OK;
+    std::vector<uint32_t> rows;
+    for (uint32_t a = 1; a < e->batch; ++a) rows.push_back(a * rows_per_window);
+    const uint64_t before = gemm_weight_bytes(op);
+    const int s = pk_gemm_prepare_rows(op, rows.data(), (uint32_t)rows.size());
+    e->weight_bytes += gemm_weight_bytes(op) - before;
+    return s;
+  };
+  int s = PK_OK;
+  if (e->front) {
+    const FrontOps& f = e->front_ops;
+    if ((s = prepare(f.pointwise3, e->front_height * halve(kBins, 2))) ||
+        (s = prepare(f.pointwise6, e->frames * halve(kBins, 3))) || (s = prepare(f.linear, e->frames)))
+      return s;
+  }
+  for (LayerOps& l : e->ops)
+    for (pk_gemm_op* op : {l.ff1a, l.ff1b, l.qkv, l.o, l.pw1, l.pw2, l.ff2a, l.ff2b})
+      if ((s = prepare(op, e->frames))) return s;
+  return prepare(e->projector, e->frames);
 }
 
 }  // namespace

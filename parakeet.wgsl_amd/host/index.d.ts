@@ -518,6 +518,8 @@ export interface ParakeetEncoderGraphOptions {
   readonly featureFrames?: number;
   /** PW1's GLU epilogue (this library only). */
   readonly fusedGlu?: boolean;
+  /** Active prefixes keep the capacity's kernels (this library only; default: a dedicated graph's plans). */
+  readonly prefixSamePlan?: boolean;
   readonly label?: string;
   /** encoder.ts:1299-1305: fp16 (default) or fp32 (an fp32 package; f32 outputs). */
   readonly executionProfile?: { precision: "fp16" | "fp32" };

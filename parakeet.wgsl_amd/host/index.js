@@ -1571,9 +1571,12 @@ class ParakeetEncoderGraph {
    * 16), options.layers (default 24), options.fusedGlu (PW1's GLU
    * epilogue; default true, false keeps the GLU in the convolution),
    * options.fusedNorms (the four LayerNorms that feed a GEMM
-   * run inside it) and options.unchainedNorms (one launch per LayerNorm;
+   * run inside it), options.unchainedNorms (one launch per LayerNorm;
    * by default a layer's last LayerNorm also writes the next layer's
-   * first), none with a reference counterpart, options.featureFrames (default
+   * first) and options.prefixSamePlan (active windows below the capacity
+   * keep the capacity's kernels, bit-identical to the full pass's windows;
+   * by default they run the plans of a graph built for that many windows),
+   * none with a reference counterpart, options.featureFrames (default
    * 1501), and options.executionProfile (encoder.ts:1299-1305: {precision:
    * "fp16"} by default, or {precision: "fp32"} for an fp32 package: f32
    * activations, palettes, positions and convolution weights, and f32
@@ -1620,7 +1623,7 @@ class ParakeetEncoderGraph {
     try {
       handle = native().encoderCreate(device.context, {
         label: o.label || "encoder", precision, fusedGlu: o.fusedGlu !== false, fusedNorms: o.fusedNorms === true,
-        unchainedNorms: o.unchainedNorms === true, batchSize, frames,
+        unchainedNorms: o.unchainedNorms === true, prefixSamePlan: o.prefixSamePlan === true, batchSize, frames,
         layers: layerDescriptors, validLengths: buffers.encoderLengths.address,
         input: buffers.features.address, output: buffers.output.address, subsampling, featureFrames,
         featureLengths: buffers.featureLengths.address, projector, projectorBias,

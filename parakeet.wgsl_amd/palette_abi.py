@@ -24,10 +24,12 @@ GEMM_GLU = 0x2
 GEMM_ROW_NORM = 0x4
 CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
+ATTENTION_PLAN_ACTIVE = 0x2
 ENCODER_FUSED_GLU = 0x1
 ENCODER_FUSED_NORMS = 0x2
 ENCODER_SEPARATE_GLU = 0x8
 ENCODER_UNCHAINED_NORMS = 0x4
+ENCODER_PREFIX_SAME_PLAN = 0x10
 ENCODER_CHANNELS = 1024
 ENCODER_INTERMEDIATE = 4096
 # The fifteen dispatches of one encoder layer, in launch order
@@ -486,6 +488,7 @@ SIGNATURES = {
     "pk_gemm_variant_describe": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(VariantDesc)]),
     "pk_gemm_set_variant": (ctypes.c_int, [_VP, ctypes.c_int]),
     "pk_gemm_set_splits": (ctypes.c_int, [_VP, ctypes.c_uint32]),
+    "pk_gemm_prepare_rows": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32]),
     "pk_gemm_plan": (ctypes.c_int, [_VP, ctypes.c_uint32, ctypes.POINTER(PlanInfo)]),
     "pk_gemm_group_create": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), ctypes.c_uint32, ctypes.c_char_p, _PPV]),
     "pk_gemm_group_enqueue": (ctypes.c_int, [_VP, ctypes.c_uint32, _VP]),
@@ -784,6 +787,12 @@ class GemmOp:
     def set_splits(self, splits: int) -> None:
         check(load().pk_gemm_set_splits(self.handle, splits))
 
+    def prepare_rows(self, rows) -> None:
+        """pk_gemm_prepare_rows: these active row counts run the plan of an op
+        created for that many rows."""
+        array = (ctypes.c_uint32 * len(rows))(*[int(r) for r in rows])
+        check(load().pk_gemm_prepare_rows(self.handle, array, len(rows)))
+
     def destroy(self) -> None:
         check(load().pk_gemm_destroy(self.handle))
 
@@ -908,11 +917,12 @@ def conv_variant_count(precision: str) -> int:
 
 def attention_desc(*, qkv, projected_positions, bias_u, bias_v, valid_lengths, output, batch_size: int, frames: int,
                    precision: str | None = None, label: str = "relative-attention",
-                   positions_row_major: bool = False) -> AttentionDesc:
+                   positions_row_major: bool = False, plan_active: bool = False) -> AttentionDesc:
     """A pk_attention_desc over DeviceArrays (or any objects with ptr/nbytes)."""
     if precision is None:
         precision = "f16" if qkv.dtype == np.float16 else "f32"
-    return AttentionDesc(ctypes.sizeof(AttentionDesc), ATTENTION_POSITIONS_ROW_MAJOR if positions_row_major else 0,
+    flags = (ATTENTION_POSITIONS_ROW_MAJOR if positions_row_major else 0) | (ATTENTION_PLAN_ACTIVE if plan_active else 0)
+    return AttentionDesc(ctypes.sizeof(AttentionDesc), flags,
                          label.encode(), PRECISION[precision], batch_size, frames, *_slice(qkv),
                          *_slice(projected_positions), *_slice(bias_u), *_slice(bias_v), *_slice(valid_lengths),
                          *_slice(output))
@@ -1108,7 +1118,7 @@ def encoder_subsampling(weights: dict) -> EncoderSubsampling:
 
 
 def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frames: int, fused_glu: bool = True,
-                 fused_norms: bool = False, unchained_norms: bool = False,
+                 fused_norms: bool = False, unchained_norms: bool = False, prefix_same_plan: bool = False,
                  subsampling: dict | None = None,
                  feature_frames: int = 0, feature_lengths=None, projector=None, projector_bias=None,
                  projected_output=None, projected_channels: int = 0, label: str = "encoder",
@@ -1122,7 +1132,8 @@ def encoder_desc(*, layers, valid_lengths, input, output, batch_size: int, frame
     array = (EncoderLayer * len(layers))(*[encoder_layer(w) for w in layers])
     front = encoder_subsampling(subsampling) if subsampling is not None else None
     flags = ((0 if fused_glu else ENCODER_SEPARATE_GLU) | (ENCODER_FUSED_NORMS if fused_norms else 0) |
-             (ENCODER_UNCHAINED_NORMS if unchained_norms else 0))
+             (ENCODER_UNCHAINED_NORMS if unchained_norms else 0) |
+             (ENCODER_PREFIX_SAME_PLAN if prefix_same_plan else 0))
     desc = EncoderDesc(ctypes.sizeof(EncoderDesc), flags, label.encode(),
                        PRECISION[precision], batch_size, frames, len(layers),
                        ctypes.cast(array, ctypes.POINTER(EncoderLayer)), _addr(valid_lengths), _addr(input),

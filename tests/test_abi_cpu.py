@@ -634,6 +634,7 @@ def test_tdt_plan_and_contract(abi):
     with pytest.raises(abi.PaletteError, match=re.escape("Unexpected decoder tensor ifgo-gates [2560]")):
         _validate_tdt(abi, **kw)
     lib = abi.load()
+    assert lib.pk_gemm_prepare_rows(None, None, 0) == abi.INVALID_ARGUMENT
     assert lib.pk_tdt_enqueue(None, 0, None) == abi.INVALID_ARGUMENT
     assert lib.pk_tdt_destroy(None) == abi.OK
 
@@ -760,7 +761,7 @@ def test_encoder_validate_stack_fields(abi):
     with pytest.raises(abi.PaletteError, match="unsupported precision 7"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
-    desc.flags = 0x10
+    desc.flags = 0x20
     with pytest.raises(abi.PaletteError, match="unknown flags"):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc = abi.encoder_desc(**_encoder_fakes())
@@ -769,6 +770,7 @@ def test_encoder_validate_stack_fields(abi):
         abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
     desc.flags = abi.ENCODER_FUSED_GLU  # the default, still accepted
     abi.check(abi.load().pk_encoder_validate(ctypes.byref(desc)))
+    _validate_encoder(abi, prefix_same_plan=True, **_encoder_fakes())  # prefixes keep the capacity's kernels
     # the fp32 profile: accepted, without the f16-only fusions
     _validate_encoder(abi, precision="f32", **_encoder_fakes(layers=24, elem=4))
     for flags in (abi.ENCODER_FUSED_GLU, abi.ENCODER_FUSED_NORMS):

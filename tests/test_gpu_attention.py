@@ -229,3 +229,35 @@ def test_mha_block_full_size(abi, ctx, scope, oracle, workloads, frames, windows
     rows, y_truth = mha_on_oracle(oracle, workloads, mod, windows, "f64")
     norm, _ = oracle.relative_errors(y[rows], y_truth)
     assert norm <= F16_TOL_TRUTH, norm
+
+
+@pytest.mark.parametrize("active", [1, 5])
+def test_attention_plan_active_matches_a_dedicated_op(abi, ctx, scope, oracle, workloads, active):
+    """PK_ATTENTION_PLAN_ACTIVE: 16 windows x 188 frames, an active prefix
+    runs the variant an op created for that many windows plans, bit-identical
+    to that op and within tolerance of the oracle; rows past the prefix stay
+    untouched."""
+    case = workloads.attention_case(71, 16, 188)
+    inputs = dict(qkv=scope.put(case.qkv), projected_positions=scope.put(case.packed_positions),
+                  bias_u=scope.put(case.bias_u), bias_v=scope.put(case.bias_v), valid_lengths=scope.put(case.valid),
+                  frames=case.frames)
+    sentinel = np.float16(3.0)
+    out = scope.put(np.full((16 * 188, 1024), sentinel, np.float16))
+    op = abi.RelativeAttentionOp(ctx, output=out, batch_size=16, plan_active=True, **inputs)
+    dedicated_out = scope.put(np.zeros((active * 188, 1024), np.float16))
+    dedicated = abi.RelativeAttentionOp(ctx, output=dedicated_out, batch_size=active, **inputs)
+    try:
+        print("prefix", op.plan(active).kernel.decode(), "dedicated", dedicated.plan().kernel.decode(),
+              "capacity", op.plan().kernel.decode(), flush=True)
+        assert op.plan(active).kernel == dedicated.plan().kernel
+        op.enqueue(active)
+        dedicated.enqueue()
+        ctx.synchronize()
+    finally:
+        op.release()
+        dedicated.release()
+    got = out.download()
+    np.testing.assert_array_equal(got[:active * 188].view(np.uint16), dedicated_out.download().view(np.uint16))
+    assert (got[active * 188:] == sentinel).all()
+    want = oracle_attention(oracle, case, batch=active)
+    assert oracle.relative_errors(got[:active * 188], want)[0] <= F16_ATTENTION_TOL

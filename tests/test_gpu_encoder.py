@@ -50,7 +50,8 @@ class Stack:
     """An EncoderOp over uploaded layers with its input, output and lengths
     (and the front end and projector when the stack has them)."""
 
-    def __init__(self, abi, ctx, scope, stack, *, fused_glu=True, fused_norms=False, unchained_norms=False):
+    def __init__(self, abi, ctx, scope, stack, *, fused_glu=True, fused_norms=False, unchained_norms=False,
+                 prefix_same_plan=False):
         precision = "f32" if stack.x.dtype == np.float32 else "f16"
         self.ctx = ctx
         self.valid = scope.put(stack.valid)
@@ -75,7 +76,7 @@ class Stack:
         self.op = abi.EncoderOp(ctx, layers=upload_layers(scope, stack.layers), valid_lengths=self.valid,
                                 input=self.input, output=self.output, batch_size=stack.batch, frames=stack.frames,
                                 fused_glu=fused_glu, fused_norms=fused_norms, unchained_norms=unchained_norms,
-                                precision=precision, **extra)
+                                prefix_same_plan=prefix_same_plan, precision=precision, **extra)
 
     def run(self, active=0, graph=False):
         self.op.enqueue(active, graph=graph)
@@ -132,9 +133,11 @@ def test_encoder_two_layers_at_750_frames(abi, ctx, scope, oracle, workloads):
 
 def test_encoder_24_layers_full_size(abi, ctx, scope, oracle, workloads):
     """16 windows x 188 frames x 24 layers: graph replay, the active prefix
-    and a window permutation bit-exact, then window 0 against the f64 chain."""
+    (PK_ENCODER_PREFIX_SAME_PLAN: the capacity's kernel families, so the
+    same bits as the full pass's windows) and a window permutation
+    bit-exact, then window 0 against the f64 chain."""
     stack = workloads.encoder_stack(seed=13, windows=16, frames=188, layers=24)
-    enc = Stack(abi, ctx, scope, stack)
+    enc = Stack(abi, ctx, scope, stack, prefix_same_plan=True)
     try:
         launches, device_bytes = enc.op.info()
         assert launches == 24 * 15
@@ -342,9 +345,22 @@ def test_encoder_graph_with_front_end_and_projector(abi, ctx, scope, oracle, wor
         assert norm16 <= 1.1 * gap + 1e-3, (name, norm16, gap)
 
 
+def first_windows(stack, n):
+    """The first n windows of a stack, with the same weights."""
+    import copy
+    sub = copy.copy(stack)
+    sub.x, sub.valid, sub.batch = stack.x[:n * stack.frames], stack.valid[:n], n
+    if stack.features is not None:
+        sub.features, sub.feature_lengths = stack.features[:n], stack.feature_lengths[:n]
+    return sub
+
+
 def test_encoder_graph_full_size(abi, ctx, scope, oracle, workloads):
     """16 windows x 1501 fbank frames -> 24 layers -> projector: graph replay
-    and the active prefix bit-exact, window 0 against the f64 chain."""
+    bit-exact; an active prefix of 3 (the default plans of a graph built for
+    3 windows, eager and replayed) bit-exact with a 3-window encoder over the
+    same weights and within 5e-3 of the full pass's windows; window 0
+    against the f64 chain."""
     stack = workloads.encoder_stack(seed=22, windows=16, frames=188, layers=24, front_end=True, projector=True)
     enc = Stack(abi, ctx, scope, stack)
     try:
@@ -354,13 +370,24 @@ def test_encoder_graph_full_size(abi, ctx, scope, oracle, workloads):
         graph, graph_projected = enc.run_both(graph=True)
         np.testing.assert_array_equal(graph.view(np.uint16), eager.view(np.uint16))
         np.testing.assert_array_equal(graph_projected.view(np.uint16), eager_projected.view(np.uint16))
-        prefix, prefix_projected = enc.run_both(active=3, graph=True)
-        np.testing.assert_array_equal(windows(prefix, 188, 0, 3).view(np.uint16),
-                                      windows(eager, 188, 0, 3).view(np.uint16))
-        np.testing.assert_array_equal(windows(prefix_projected, 188, 0, 3).view(np.uint16),
-                                      windows(eager_projected, 188, 0, 3).view(np.uint16))
+        prefix, prefix_projected = enc.run_both(active=3)
+        prefix_graph, prefix_graph_projected = enc.run_both(active=3, graph=True)
     finally:
         enc.release()
+    small = Stack(abi, ctx, scope, first_windows(stack, 3))
+    try:
+        dedicated, dedicated_projected = small.run_both(graph=True)
+    finally:
+        small.release()
+    for got, got_projected in ((prefix, prefix_projected), (prefix_graph, prefix_graph_projected)):
+        np.testing.assert_array_equal(windows(got, 188, 0, 3).view(np.uint16), dedicated.view(np.uint16))
+        np.testing.assert_array_equal(windows(got_projected, 188, 0, 3).view(np.uint16),
+                                      dedicated_projected.view(np.uint16))
+    for got, full in ((prefix, eager), (prefix_projected, eager_projected)):
+        apart, _ = oracle.relative_errors(valid_rows(windows(got, 188, 0, 3), stack, 3),
+                                          valid_rows(windows(full, 188, 0, 3), stack, 3))
+        print(f"prefix of 3 against the full pass's windows: {apart:.2e}", flush=True)
+        assert apart <= 5e-3, apart
     assert np.isfinite(eager).all() and np.isfinite(eager_projected).all()
     chains = {mode: oracle.encoder_graph(None, stack.layers, stack.valid[:1], batch=1, frames=188,
                                          front=stack.subsampling, features=stack.features[:1],

@@ -827,3 +827,56 @@ def test_row_norm_contract_errors(abi, ctx, scope, workloads):
     with pytest.raises(abi.PaletteError, match="row norm needs f16"):
         abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=scope.empty((64, 512), np.float16), bits=5,
                    rows=64, inner=1024, columns=1024, glu=True, norm_gamma=g, norm_beta=g, label="lbl")
+
+
+@pytest.mark.parametrize("rows,inner,columns,bits,active", [
+    (3008, 1024, 4096, 5, (188, 752)),   # FF expand: a 64 x 64 four-part tile at one window
+    (3008, 4096, 1024, 5, (188, 1504)),  # FF contract: the small-M kernel at one window
+    (3008, 1024, 1024, 6, (188, 564)),   # output projection, 6-bit
+])
+def test_prepared_rows_run_the_dedicated_plan(abi, ctx, scope, oracle, workloads, rows, inner, columns, bits,
+                                             active):
+    """pk_gemm_prepare_rows: a prepared active row count runs the plan of an
+    op created for that many rows (its kernel family, K split and a copy of
+    the codes in that layout), bit-identical to such a dedicated op, within
+    tolerance of the oracle; the rows past the prefix stay untouched, and
+    forcing a variant drops the prepared plans."""
+    case = workloads.gemm_case(63, rows, inner, columns, bits, activation="silu" if columns == 4096 else "none")
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    prefix = scope.put(np.full((rows, columns), 7.0, np.float16))
+    op = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=prefix, bits=bits, rows=rows, inner=inner,
+                    columns=columns, activation=case.activation, label="prepared-rows")
+    try:
+        op.prepare_rows(list(active) + [active[0]])  # a repeated count is prepared once
+        for m in active:
+            dedicated_out = scope.put(np.zeros((m, columns), np.float16))
+            dedicated = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=dedicated_out, bits=bits, rows=m,
+                                   inner=inner, columns=columns, activation=case.activation, label="dedicated")
+            try:
+                plan_d, plan_p = dedicated.plan(0), op.plan(m)
+                print(m, "rows: dedicated", plan_d.kernel.decode(), list(plan_d.grid), "prepared",
+                      plan_p.kernel.decode(), list(plan_p.grid), flush=True)
+                assert plan_d.kernel == plan_p.kernel and list(plan_d.grid) == list(plan_p.grid)
+                prefix.upload(np.full((rows, columns), 7.0, np.float16))
+                op.enqueue(m)
+                dedicated.enqueue(0)
+                ctx.synchronize()
+            finally:
+                dedicated.release()
+            got = prefix.download()
+            np.testing.assert_array_equal(got[:m].view(np.uint16), dedicated_out.download().view(np.uint16))
+            assert (got[m:] == np.float16(7.0)).all()
+            assert_f16_parity(oracle, got[:m], workloads.GemmCase("prefix", case.a[:m], w, activation=case.activation))
+        op.set_variant(9)  # forced: every row count runs it, the prepared plans are gone
+        assert op.plan(active[0]).kernel == op.plan(0).kernel == abi.describe_variant("f16", 9).__getattribute__(
+            f"kernel{bits}")
+    finally:
+        op.release()
+    with pytest.raises(abi.PaletteRangeError, match=r"prepared-rows active rows must be in \[1, 3008\]"):
+        bad = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=prefix, bits=bits, rows=rows, inner=inner,
+                         columns=columns, activation=case.activation, label="prepared-rows")
+        try:
+            bad.prepare_rows([rows + 1])
+        finally:
+            bad.release()
