@@ -58,8 +58,9 @@ let nativeModule = null;
 function native() {
   if (nativeModule === null) {
     // The addon is built in-tree next to libpk_palette.so; there is no
-    // fallback: without it the host fails loudly.
-    nativeModule = require(path.join(__dirname, "..", "lib", "pk_napi.node"));
+    // fallback: without it the host fails loudly. PK_NAPI_ADDON names another
+    // build of it (the host-side sanitizer build of the CPU tests).
+    nativeModule = require(process.env.PK_NAPI_ADDON || path.join(__dirname, "..", "lib", "pk_napi.node"));
   }
   return nativeModule;
 }
