@@ -1,0 +1,119 @@
+"""CPU tests of bench.py's host logic: the encoder's launch order and the
+split of a rocprofv3 kernel trace per launch kind (no GPU, no profiler: the
+trace is synthetic)."""
+import csv
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+from parakeet_wgsl_amd.palette_abi import ENCODER_DISPATCHES  # noqa: E402
+
+KERNEL = {
+    "layernorm_kernel": "void pk::(anonymous namespace)::layernorm_kernel<_Float16, 8, 2048, false>(pk::LayerNormArgs)",
+    "attention": "void pk::(anonymous namespace)::rel_attention_f16_shared_kernel<4, false>(pk::AttentionArgs)",
+    "conformer_conv_kernel": "void pk::(anonymous namespace)::conformer_conv_kernel<_Float16, 2, 8, true>(pk::ConvArgs)",
+    "subsampling_": "void pk::(anonymous namespace)::subsampling_depthwise_kernel<_Float16>(pk::SubsamplingArgs)",
+    "gemm_f16": "void pk::(anonymous namespace)::gemm_f16k_kernel<5, 2, 2, 3, 2, false, true, 5, false>(pk::GemmArgs)",
+}
+FUSED = "void pk::(anonymous namespace)::subsampling_fused_kernel<_Float16, 4>(pk::SubsamplingArgs)"
+LOOP = "void pk::(anonymous namespace)::gemm_f16k_kernel<5, 4, 1, 6, 2, false, true, 2, false>(pk::GemmArgs)"
+PREP = "void pk::(anonymous namespace)::operand_order_kernel<5, 1>(pk::OrderArgs)"
+
+
+def test_launch_sequence_counts():
+    """344 launches per pass at 24 layers: 6 front-end, 15 slots per layer
+    less the 23 chained LN ff1 slots, the projector."""
+    seq = bench.launch_sequence(24)
+    assert len(seq) == 6 + 24 * len(ENCODER_DISPATCHES) - 23 + 1 == 344
+    assert seq[0] == "subsampling-fused-conv0-depthwise2" and seq[-1] == "projector"
+    assert seq.count("norm_feed_forward1") == 1
+    assert len(bench.launch_sequence(24, chained=False)) == 367
+    fused = bench.launch_sequence(2, fused_norms=bench.FUSED_NORMS)
+    assert not any(n in fused for n in bench.FUSED_NORMS)
+
+
+def kernel_for(kind):
+    if kind == "subsampling-fused-conv0-depthwise2":
+        return FUSED
+    return KERNEL[bench.kernel_family(kind)]
+
+
+def write_trace(path, layers, warmup, steps, duration_us, rows=None):
+    """A kernel trace of `warmup + steps` passes; each launch of `kind` lasts
+    duration_us(kind, stamped) (stamped passes: every TIMING_STRIDE-th timed
+    one), then one op preparation and the roofline loop."""
+    seq = bench.launch_sequence(layers)
+    t = 1_000_000
+    out = []
+
+    def add(name, us, grid=65536):
+        nonlocal t
+        out.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000),
+                    "Grid_Size_X": grid})
+        t += int(us * 1000) + 500
+
+    for p in range(warmup + steps):
+        stamped = p >= warmup and (p - warmup) % bench.TIMING_STRIDE == 0
+        for kind in seq:
+            add(kernel_for(kind), duration_us(kind, stamped))
+    add(PREP, 20.0)
+    warm, n = bench.ROOFLINE_LOOP
+    for i in range(warm + n):
+        add(LOOP, 40.0 if i < warm else 30.0)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(out[0]))
+        w.writeheader()
+        # the profiler writes rows out of start order; the splitter sorts them
+        for r in reversed(out):
+            w.writerow(r)
+
+
+def test_split_trace_kinds_and_loop(tmp_path, capsys):
+    """Per-kind averages over stamped and graph passes come out as written,
+    and the roofline loop is the last ROOFLINE_LOOP[1] GEMM launches, not
+    the op preparation before them."""
+    path = tmp_path / "trace.csv"
+
+    def duration(kind, stamped):
+        return (10.0 if kind.startswith("norm_") else 20.0) + (1.0 if stamped else 0.0)
+
+    write_trace(path, 2, 3, 10, duration)
+    bench.split_trace(str(path), 3, 10, layers=2)
+    out = capsys.readouterr().out
+    row = next(line for line in out.splitlines() if line.startswith("| norm_self_att |"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    assert cells[1] == "26" and cells[2] == "11.00" and cells[3] == "10.00"
+    row = next(line for line in out.splitlines() if line.startswith("| feed-forward1-linear1 |"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    assert cells[2] == "21.00" and cells[3] == "20.00"
+    loop = next(line for line in out.splitlines() if line.startswith("roofline loop"))
+    assert "avg 30.00 us" in loop and "operand_order" not in loop and "of 55 " in loop
+
+
+def test_split_trace_rejects_wrong_pass_count(tmp_path):
+    path = tmp_path / "trace.csv"
+    write_trace(path, 1, 1, 5, lambda kind, stamped: 5.0)
+    with pytest.raises(SystemExit, match="passes in the trace"):
+        bench.split_trace(str(path), 1, 4, layers=1)
+
+
+def test_split_trace_checks_kernel_names(tmp_path):
+    """A launch whose kernel does not belong to its kind stops the split."""
+    path = tmp_path / "trace.csv"
+    write_trace(path, 1, 1, 2, lambda kind, stamped: 5.0)
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    seq = bench.launch_sequence(1)
+    i = seq.index("relative-attention")
+    rows[i]["Kernel_Name"] = KERNEL["gemm_f16"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    with pytest.raises(SystemExit, match="relative-attention ran"):
+        bench.split_trace(str(path), 1, 2, layers=1)
