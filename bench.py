@@ -111,6 +111,15 @@ def parse_args():
     p.add_argument("--split-trace", default="",
                    help="CPU only: per launch kind of a rocprofv3 kernel trace (CSV) of the encoder bench run "
                         "with the given --steps / --warmup")
+    p.add_argument("--roofline-kind", default="",
+                   help="encoder workloads: describe this launch kind in `roofline` instead of the one with the "
+                        "most time per pass (to profile the same back-to-back loop as another run's line)")
+    p.add_argument("--split-counters", default="",
+                   help="CPU only: FETCH,WRITE,COPY_FETCH,COPY_WRITE - four rocprofv3 --pmc counter CSVs (the "
+                        "encoder bench run with the given --steps / --warmup, FETCH_SIZE then WRITE_SIZE, and the "
+                        "copy of COPY_COMMAND for each counter): HBM bytes per launch kind of the last pass")
+    p.add_argument("--bench-json", default="",
+                   help="with --split-counters: a bench line of the same workload, for the algorithmic bytes")
     return p.parse_args()
 
 
@@ -509,6 +518,86 @@ def split_trace(path, warmup, steps, layers=24):
               f"first start to last end over {loop_n}: {span:.2f} us")
 
 
+# The calibration copy for the HBM counters: 256 MiB read and 256 MiB
+# written per torch.neg dispatch (profiled with one counter per run).
+COPY_COMMAND = ("import torch; a=torch.ones(128<<20,dtype=torch.float16,device='cuda'); b=torch.empty_like(a); "
+                "[torch.neg(a,out=b) for _ in range(4)]; torch.cuda.synchronize(); print('copy done')")
+COPY_KIB = 256 * 1024
+
+
+def read_counters(path):
+    """(dispatch id, kernel name, counter value summed over the rows of the
+    dispatch) in dispatch order, from a rocprofv3 --pmc CSV."""
+    import csv
+    per, names = {}, {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = int(r["Dispatch_Id"])
+            per[d] = per.get(d, 0.0) + float(r["Counter_Value"])
+            names[d] = r["Kernel_Name"]
+    return [(d, names[d], per[d]) for d in sorted(per)]
+
+
+def copy_factor(path):
+    """True KiB of the calibration copy over what the counter reads for it
+    (the torch.neg dispatches after the first)."""
+    values = [v for _, name, v in read_counters(path) if "neg" in name]
+    if len(values) < 2:
+        raise SystemExit(f"{path}: no calibration copy dispatches")
+    return COPY_KIB / float(np.mean(values[1:]))
+
+
+def split_counters(fetch_path, write_path, copy_fetch, copy_write, warmup, steps, bench_json="", layers=24):
+    """HBM bytes per launch kind of the encoder bench's last pass, from
+    rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs (CSV, KiB per dispatch)
+    of `bench.py --no-cpu --no-dense --no-ff-block --steps S --warmup W`,
+    each scaled by what the same counter reads for the calibration copy
+    (COPY_COMMAND). The pass's launches are mapped to kinds in launch order
+    (every kernel name checked against its kind), layer kinds averaged over
+    the layers. Prints a markdown table and the traffic.json entries of the
+    GEMM kinds."""
+    seq = launch_sequence(layers)
+    factors = {"fetch": copy_factor(copy_fetch), "write": copy_factor(copy_write)}
+    kib = {}
+    for counter, path in (("fetch", fetch_path), ("write", write_path)):
+        rows = read_counters(path)
+        starts = [i for i, (_, name, _) in enumerate(rows) if "subsampling_fused_kernel" in name]
+        if len(starts) != warmup + steps:
+            raise SystemExit(f"{path}: {len(starts)} passes, expected {warmup + steps}")
+        last = rows[starts[-1]:starts[-1] + len(seq)]
+        per = {}
+        for kind, (d, name, value) in zip(seq, last):
+            if kernel_family(kind) not in name:
+                raise SystemExit(f"{path}: dispatch {d} of {kind} ran {name}")
+            per.setdefault(kind, []).append(value)
+        kib[counter] = {kind: float(np.mean(v)) for kind, v in per.items()}
+    algorithmic = {}
+    if bench_json:
+        with open(bench_json) as f:
+            line = json.loads(f.read().strip().splitlines()[-1])
+        algorithmic = {k: v["algorithmic_bytes"] for k, v in line["dispatches"].items()}
+    print(f"scale: FETCH_SIZE x {factors['fetch']:.3f}, WRITE_SIZE x {factors['write']:.3f} "
+          f"(the calibration copy: {COPY_KIB} KiB each way)")
+    print()
+    print("| launch kind | launches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes | algorithmic | ratio |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    entries = {}
+    for kind in dict.fromkeys(seq):
+        f, w = kib["fetch"][kind], kib["write"][kind]
+        hbm = (f * factors["fetch"] + w * factors["write"]) * 1024
+        alg = algorithmic.get(kind)
+        ratio = f"{hbm / alg:.2f}" if alg else ""
+        alg_text = f"{alg / 1e6:.1f} MB" if alg else ""
+        print(f"| {kind} | {seq.count(kind)} | {f:,.0f} | {w:,.0f} | {hbm / 1e6:.1f} MB | {alg_text} | {ratio} |")
+        if kernel_family(kind) == "gemm_f16":
+            entries[f"encoder-{kind}"] = {"fetch_kib": round(f), "write_kib": round(w),
+                                          "fetch_factor": round(factors["fetch"], 3),
+                                          "write_factor": round(factors["write"], 3),
+                                          "hbm_bytes_per_launch": hbm, "algorithmic_bytes": alg}
+    print()
+    print("traffic.json entries:", json.dumps(entries))
+
+
 def roofline_loop(ctx, abi, kind, layer0, a_rows, rows, stream):
     """Average duration of `kind`'s GEMM (rebuilt from LAYER_GEMMS with layer
     0's weights at the pass's shape: `rows` active rows of `a_rows`) over
@@ -813,6 +902,10 @@ def run_encoder(args, abi, ctx, decoder=False):
     for k, d in dispatches.items():
         per_kind[kind(k)] = per_kind.get(kind(k), 0.0) + d["avg_us"] * d["launches_per_pass"]
     name = max(per_kind, key=per_kind.get)
+    if args.roofline_kind:
+        if args.roofline_kind not in dispatches:
+            raise SystemExit(f"--roofline-kind {args.roofline_kind}: not a launch kind of this pass")
+        name = args.roofline_kind
     dom = dispatches[name]
     peak = PEAK_TFLOPS[args.precision]
     # The roofline times the dominant launch kind back to back (the graph
@@ -1278,6 +1371,9 @@ def main():
     args = parse_args()
     if args.split_trace:
         split_trace(args.split_trace, args.warmup, args.steps)
+        return
+    if args.split_counters:
+        split_counters(*args.split_counters.split(","), args.warmup, args.steps, args.bench_json)
         return
     if args.dense_probe:
         dense_probe(json.loads(args.dense_probe), args.steps)

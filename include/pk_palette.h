@@ -102,6 +102,16 @@ typedef enum pk_activation {
    or groups whose width is a multiple of 256 columns. Runs on the pair-code
    kernels. */
 #define PK_GEMM_ROW_NORM 0x4u
+/* A store hint with no counterpart in the reference. The f16 pair-code
+   kernels store their output non-temporally unless this flag is set: the
+   output is mostly read by workgroups on other XCDs than the one that
+   wrote each line, and streamed lines need no write-back from L2 when the
+   kernel ends. With the flag the stores stay ordinary: for an output that
+   a bandwidth-bound launch reads next and finds in the memory-side cache
+   (the encoder's first subsampling pointwise GEMM, read by the depthwise
+   convolution). Results are the same either way;
+   pk_gemm_plan_info.stream_stores tells which a launch uses. */
+#define PK_GEMM_CACHED_OUTPUT 0x8u
 
 typedef struct pk_context pk_context;
 typedef struct pk_gemm_op pk_gemm_op;
@@ -318,6 +328,8 @@ typedef struct pk_gemm_plan_info {
   uint64_t flops;                /* 2*M*K*N for active rows */
   uint64_t algorithmic_bytes;    /* compulsory HBM bytes per launch */
   char kernel[64];
+  uint32_t stream_stores;        /* 1: non-temporal output stores (PK_GEMM_CACHED_OUTPUT) */
+  uint32_t reserved;
 } pk_gemm_plan_info;
 
 /* Plan of the launch pk_gemm_enqueue would make for `active_rows`. */

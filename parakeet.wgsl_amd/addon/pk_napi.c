@@ -585,6 +585,8 @@ static napi_value js_gemm_plan(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, obj, "algorithmicBytes", make_number(env, (double)p.algorithmic_bytes));
   napi_create_string_utf8(env, p.kernel, NAPI_AUTO_LENGTH, &v);
   napi_set_named_property(env, obj, "kernel", v);
+  napi_get_boolean(env, p.stream_stores != 0, &v);
+  napi_set_named_property(env, obj, "streamStores", v);
   return obj;
 }
 

@@ -115,6 +115,7 @@ struct pk_gemm_op {
   int variant = 0;
   uint32_t splits = 1;
   int cus = 256;
+  bool cached_output = false;  // PK_GEMM_CACHED_OUTPUT
   // A variant chosen by pk_gemm_set_variant / pk_gemm_set_splits runs at
   // every active row count; otherwise an active prefix is re-planned among
   // the kernels that read the weight's layout (the last choice cached).
@@ -237,6 +238,10 @@ pk::TileShape shape_of(int precision, int variant) {
 }
 
 uint32_t k_blocks(uint32_t inner) { return (inner + 63u) / 64u; }
+
+// f16 outputs are stored non-temporally unless the op keeps them cached
+// (GemmArgs::stream_out).
+bool stream_outputs(const pk_gemm_op* op) { return op->precision == PK_PRECISION_F16 && !op->cached_output; }
 
 // Column-group widths (blocks of 32 columns) a GEMM group keeps item lists
 // for: those of the small-M variants.
@@ -527,6 +532,8 @@ int validate_gemm_desc(const pk_context* ctx, const pk_gemm_desc* d) {
   if (d->activation < PK_ACTIVATION_NONE || d->activation > PK_ACTIVATION_RELU)
     return fail(PK_INVALID_ARGUMENT, "%s has an unsupported activation %d", label, d->activation);
   const float residual_scale = d->residual ? (d->has_residual_scale ? d->residual_scale : 1.0f) : -1.0f;
+  if (d->flags & ~(PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE | PK_GEMM_GLU | PK_GEMM_ROW_NORM | PK_GEMM_CACHED_OUTPUT))
+    return fail(PK_INVALID_ARGUMENT, "%s has unknown flags 0x%x", label, d->flags);
   if (d->flags & PK_GEMM_REQUIRE_PRODUCTION_SIGNATURE) {
     bool found = false;
     for (const Signature& s : kProductionSignatures)
@@ -907,6 +914,7 @@ int pk_gemm_create(pk_context* ctx, const pk_gemm_desc* d, void* stream, pk_gemm
   const bool glu = (d->flags & PK_GEMM_GLU) != 0;
   const bool norm = (d->flags & PK_GEMM_ROW_NORM) != 0;
   op->cus = cus;
+  op->cached_output = (d->flags & PK_GEMM_CACHED_OUTPUT) != 0;
   // The plan comes first: the weight is prepared in the one layout the
   // planned kernel reads (a shared prepared weight fixes it instead).
   Plan plan = plan_op(d->precision, d->rows, d->inner, d->columns, cus, glu,
@@ -1070,6 +1078,7 @@ int pk_gemm_enqueue_timed(pk_gemm_op* op, uint32_t active_rows, void* stream, vo
   pk::GemmArgs args = op->args;
   args.rows = rows;
   if (prepared) args.codes = prepared->codes;
+  args.stream_out = stream_outputs(op);
   // A split never gets an empty K range.
   args.splits = std::min(op->splits, k_blocks(op->args.inner));
   hipStream_t st = stream_or_default(op->ctx, stream);
@@ -1235,6 +1244,10 @@ int pk_gemm_plan(const pk_gemm_op* op, uint32_t active_rows, pk_gemm_plan_info* 
   info->algorithmic_bytes = algorithmic_bytes(op->args, op->bits, rows, elem);
   std::snprintf(info->kernel, sizeof info->kernel, "%s",
                 f16 ? pk::f16_variant_name(op->bits, variant) : pk::f32_variant_name(op->bits, variant));
+  pk::GemmArgs launched = op->args;
+  launched.rows = rows;
+  launched.stream_out = stream_outputs(op);
+  info->stream_stores = f16 && pk::f16_variant_streams(op->bits, variant, launched);
   return ok();
 }
 

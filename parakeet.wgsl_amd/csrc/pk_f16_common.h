@@ -232,7 +232,22 @@ struct F16Variant {
   void (*general[2])(GemmArgs);
   uint32_t lds_bytes;           // static LDS of the kernel
   void (*normed[2])(GemmArgs);  // fused row LayerNorm (single path), or null
+  void (*streamed[2])(GemmArgs);  // single path with non-temporal output stores, or null
 };
+
+// The `single` kernels need K % 64 == 0 and every tile inside one palette
+// group (its palette staged at a fixed LDS address); tiles start at
+// multiples of the tile width, so the latter holds with one group or when
+// the group width is a multiple of the tile width.
+inline bool single_path(const TileShape& s, const GemmArgs& a) {
+  return (a.inner & 63u) == 0u &&
+         (a.palette_groups == 1 || a.palette_group_columns % (uint32_t)s.tile_columns() == 0);
+}
+
+// Whether a launch of `v` with `a` runs its non-temporal-store kernel.
+inline bool streams(const F16Variant& v, int bits, const GemmArgs& a) {
+  return a.stream_out && !a.norm_columns && v.streamed[bits == 6] && single_path(v.shape, a);
+}
 
 }  // namespace f16
 

@@ -350,6 +350,11 @@ hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStr
   return launch_gemm_f16s_group(index - kLocal - f16k_variant_count(), group, stream, start, stop);
 }
 
+bool f16_variant_streams(int bits, int variant, const GemmArgs& args) {
+  return variant >= kLocal && variant < kLocal + f16k_variant_count() &&
+         f16::streams(variant_at(variant), bits, args);
+}
+
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop) {
   if (variant >= kLocal + f16k_variant_count())
@@ -358,14 +363,7 @@ hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStrea
   const F16Variant& v = variant_at(variant);
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns) * args.splits;
   if (groups == 0) return hipSuccess;
-  // The fast kernels need K % 64 == 0 and every tile inside one palette
-  // group (its palette staged at a fixed LDS address); tiles start at
-  // multiples of the tile width, so the latter holds with one group or when
-  // the group width is a multiple of the tile width.
-  const bool single = (args.inner & 63u) == 0u &&
-                      (args.palette_groups == 1 ||
-                       args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
-  void (*kernel)(GemmArgs) = single ? v.single[bits == 6] : v.general[bits == 6];
+  void (*kernel)(GemmArgs) = f16::single_path(v.shape, args) ? v.single[bits == 6] : v.general[bits == 6];
   return launch_timed(kernel, dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
 }
 

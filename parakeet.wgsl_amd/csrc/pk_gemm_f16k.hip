@@ -139,7 +139,8 @@ __device__ __forceinline__ void interleave_sub_step() {
 // GENERAL: the tile's columns may span palette groups (per-lane palette
 // base) or K may be 32 (mod 64) (the last K block's upper half is zeroed,
 // so the code-0 padding of the operand order multiplies zeros).
-template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA, bool NORM = false>
+template <int BITS, int WN, int KS, int R, int C, bool GENERAL, bool SCHED, int CLA, bool NORM = false,
+          bool STREAM = false>
 __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
   constexpr int T = 256;
   constexpr int BM = 32 * R;
@@ -611,10 +612,14 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
           float g[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) g[e] = through_f16(value[e]) * sigmoid(through_f16(gate[e]));
-          if (m < M && c < NC)
-            *reinterpret_cast<uint4*>(out + (uint64_t)m * NC + c) =
-                make_uint4(pack_half2(g[0], g[1]), pack_half2(g[2], g[3]), pack_half2(g[4], g[5]),
-                           pack_half2(g[6], g[7]));
+          if (m < M && c < NC) {
+            const uint4 y = make_uint4(pack_half2(g[0], g[1]), pack_half2(g[2], g[3]), pack_half2(g[4], g[5]),
+                                       pack_half2(g[6], g[7]));
+            if constexpr (STREAM)
+              stream_store(reinterpret_cast<uint4*>(out + (uint64_t)m * NC + c), y);
+            else
+              *reinterpret_cast<uint4*>(out + (uint64_t)m * NC + c) = y;
+          }
         }
         continue;
       }
@@ -695,7 +700,10 @@ __global__ __launch_bounds__(256) void gemm_f16k_kernel(GemmArgs args) {
       if (keep[it]) {
         const uint4 y = make_uint4(pack_half2(v[it][0], v[it][1]), pack_half2(v[it][2], v[it][3]),
                                    pack_half2(v[it][4], v[it][5]), pack_half2(v[it][6], v[it][7]));
-        *reinterpret_cast<uint4*>(out + at[it]) = y;
+        if constexpr (STREAM)
+          stream_store(reinterpret_cast<uint4*>(out + at[it]), y);
+        else
+          *reinterpret_cast<uint4*>(out + at[it]) = y;
       }
   }
 }
@@ -717,6 +725,8 @@ constexpr uint32_t kernel_lds_bytes() {
         kernel_lds_bytes<WN, KS, R, C>(),                                                                   \
         {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA, true>,                                            \
          gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA, true>},                                           \
+        {gemm_f16k_kernel<5, WN, KS, R, C, false, S, CLA, false, true>,                                     \
+         gemm_f16k_kernel<6, WN, KS, R, C, false, S, CLA, false, true>},                                    \
   }
 
 const F16Variant kVariants[] = {
@@ -746,16 +756,15 @@ hipError_t launch_gemm_f16k(int bits, const f16::F16Variant& v, const GemmArgs& 
                             hipEvent_t start, hipEvent_t stop) {
   const uint32_t groups = tiles_m(v.shape, args.rows) * tiles_n(v.shape, args.columns);
   if (groups == 0) return hipSuccess;
-  const bool single = (args.inner & 63u) == 0u &&
-                      (args.palette_groups == 1 ||
-                       args.palette_group_columns % (uint32_t)v.shape.tile_columns() == 0);
+  const bool single = f16::single_path(v.shape, args);
   if (args.norm_columns) {
     // The fused row norm needs the fixed-palette path and K staged in LDS.
     if (!single || args.inner > kNormMaxInner || !v.normed[bits == 6]) return hipErrorInvalidValue;
     return launch_timed(v.normed[bits == 6], dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
   }
-  return launch_timed(single ? v.single[bits == 6] : v.general[bits == 6], dim3(groups), dim3(v.shape.threads()),
-                      stream, start, stop, args);
+  void (*kernel)(GemmArgs) = single ? v.single[bits == 6] : v.general[bits == 6];
+  if (f16::streams(v, bits, args)) kernel = v.streamed[bits == 6];
+  return launch_timed(kernel, dim3(groups), dim3(v.shape.threads()), stream, start, stop, args);
 }
 
 }  // namespace pk

@@ -96,7 +96,31 @@ struct GemmArgs {
   const _Float16* norm_gamma;  // [K] or null
   const float* norm_columns;   // [2N] or null
   float norm_epsilon;
+  // Set by the host for f16 ops unless they keep their output cached
+  // (PK_GEMM_CACHED_OUTPUT): the launch then runs a kernel instantiation
+  // whose output stores are non-temporal (stream_store), where one is
+  // compiled. The next launch mostly reads an output from other XCDs than
+  // the one that wrote each line, and streamed lines need no write-back
+  // from L2 when the kernel ends: on the 16-window encoder pass this takes
+  // 0.3-1.4 us off each layer GEMM (1.6% off the pass); at 1 and 4 windows
+  // the pass time is unchanged within 0.3%. A runtime branch between the
+  // two store kinds would not do: the compiler merges the two stores into
+  // one and drops the non-temporal hint.
+  int stream_out;
 };
+
+// A store of an output that no later instruction of this kernel reads,
+// marked non-temporal (global_store ... nt).
+template <class T>
+__device__ __forceinline__ void stream_store(T* p, const T& v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "dword, dwordx2 or dwordx4 stores");
+  if constexpr (sizeof(T) == 4) {
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, v), reinterpret_cast<uint32_t*>(p));
+  } else {
+    typedef uint32_t words __attribute__((ext_vector_type(sizeof(T) / 4)));
+    __builtin_nontemporal_store(__builtin_bit_cast(words, v), reinterpret_cast<words*>(p));
+  }
+}
 
 
 // Tile shapes compiled for the fused GEMM. Every variant is one workgroup of
@@ -193,6 +217,10 @@ inline int f16_variant_parts(int index) {
 }
 hipError_t launch_gemm_f16(int bits, int variant, const GemmArgs& args, hipStream_t stream,
                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Whether launch_gemm_f16 runs `variant` with non-temporal output stores
+// for `args` (stream_out set and a streamed kernel compiled for it: the
+// pair-code family's single-path kernels).
+bool f16_variant_streams(int bits, int variant, const GemmArgs& args);
 // Workgroups of one launch of an f16 variant.
 uint32_t f16_variant_grid(int index, uint32_t rows, uint32_t columns, uint32_t splits);
 

@@ -138,6 +138,12 @@ export interface GemmDescriptor {
    * values, [N/2, N) gates; the output is [rows, N/2] value * sigmoid(gate).
    */
   readonly glu?: boolean;
+  /**
+   * This library only: keep the output stores ordinary
+   * (PK_GEMM_CACHED_OUTPUT); the f16 pair-code kernels otherwise store the
+   * output non-temporally.
+   */
+  readonly cachedOutput?: boolean;
 }
 
 export interface GemmPlan {
@@ -151,6 +157,8 @@ export interface GemmPlan {
   readonly flops: number;
   readonly algorithmicBytes: number;
   readonly kernel: string;
+  /** The launch stores its output non-temporally (see cachedOutput). */
+  readonly streamStores: boolean;
 }
 
 /** gemm.ts:400-470, encoder.ts:308-316 (ManagedDispatch) */

@@ -75,6 +75,7 @@ const FP32_TRANSIENT_PALETTE_WEIGHT_SCRATCH_BYTES = 17301504;
 const REQUIRE_PRODUCTION_SIGNATURE = 1;
 const GEMM_GLU = 2;
 const GEMM_ROW_NORM = 4;
+const GEMM_CACHED_OUTPUT = 8;
 const CONV_INPUT_GLU = 1;
 
 /** runtime-plan.ts:352-368 */
@@ -864,7 +865,7 @@ class PaletteGemmKernel {
     const d = {
       label: descriptor.label,
       flags: (this.productionOnly ? REQUIRE_PRODUCTION_SIGNATURE : 0) | (descriptor.glu ? GEMM_GLU : 0) |
-        (descriptor.rowNorm ? GEMM_ROW_NORM : 0),
+        (descriptor.rowNorm ? GEMM_ROW_NORM : 0) | (descriptor.cachedOutput ? GEMM_CACHED_OUTPUT : 0),
       precision: fp32 ? "f32" : "f16",
       paletteBits,
       rows: descriptor.rows,

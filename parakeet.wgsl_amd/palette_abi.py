@@ -22,6 +22,7 @@ ACTIVATION = {"none": 0, "silu": 1, "relu": 2}
 REQUIRE_PRODUCTION_SIGNATURE = 0x1
 GEMM_GLU = 0x2
 GEMM_ROW_NORM = 0x4
+GEMM_CACHED_OUTPUT = 0x8
 CONV_INPUT_GLU = 0x1
 ATTENTION_POSITIONS_ROW_MAJOR = 0x1
 ATTENTION_PLAN_ACTIVE = 0x2
@@ -116,6 +117,8 @@ class PlanInfo(ctypes.Structure):
         ("flops", ctypes.c_uint64),
         ("algorithmic_bytes", ctypes.c_uint64),
         ("kernel", ctypes.c_char * 64),
+        ("stream_stores", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
     ]
 
 
@@ -740,13 +743,15 @@ class GemmOp:
                  prepared: PreparedWeight | None = None, label: str = "palette-gemm",
                  production_only: bool = False, glu: bool = False, stream=None,
                  norm_gamma: DeviceArray | None = None, norm_beta: DeviceArray | None = None,
-                 norm_epsilon: float = 0.0):
+                 norm_epsilon: float = 0.0, cached_output: bool = False):
         """With norm_gamma / norm_beta (f32 [inner]) the op multiplies the
-        row LayerNorm of `a` (PK_GEMM_ROW_NORM)."""
+        row LayerNorm of `a` (PK_GEMM_ROW_NORM); cached_output keeps the
+        output stores ordinary (PK_GEMM_CACHED_OUTPUT), which are otherwise
+        non-temporal on the f16 pair-code kernels."""
         precision = "f16" if palette.dtype == np.float16 else "f32"
         groups = palette.shape[0]
         flags = ((REQUIRE_PRODUCTION_SIGNATURE if production_only else 0) | (GEMM_GLU if glu else 0) |
-                 (GEMM_ROW_NORM if norm_gamma is not None else 0))
+                 (GEMM_ROW_NORM if norm_gamma is not None else 0) | (GEMM_CACHED_OUTPUT if cached_output else 0))
 
         self.desc = GemmDesc(
             ctypes.sizeof(GemmDesc), flags,

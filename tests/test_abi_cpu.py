@@ -174,6 +174,33 @@ def test_algorithmic_bytes_formula(workloads):
 # ------------------------------------------------------ conformer conv plan
 
 
+def test_gemm_flags_contract(abi):
+    """pk_gemm_validate (no device) accepts every defined GEMM flag alone and
+    refuses an unknown bit by name."""
+    lib = abi.load()
+
+    def desc(flags):
+        d = abi.GemmDesc()
+        d.struct_size = ctypes.sizeof(abi.GemmDesc)
+        d.flags = flags
+        d.label = b"lbl"
+        d.precision = abi.PRECISION["f16"]
+        d.palette_bits, d.rows, d.inner, d.columns = 5, 64, 256, 512
+        d.palette_groups, d.palette_group_columns = 1, 512
+        base = 0x2000000000
+        d.a, d.a_bytes = base, 64 * 256 * 2
+        d.packed, d.packed_bytes = base + (1 << 24), 256 * 512 // 32 * 20
+        d.palette, d.palette_bytes = base + (2 << 24), 32 * 2
+        d.output, d.output_bytes = base + (3 << 24), 64 * 512 * 2
+        d.activation = abi.ACTIVATION["none"]
+        return d
+
+    for flags in (0, abi.GEMM_CACHED_OUTPUT):
+        abi.check(lib.pk_gemm_validate(ctypes.byref(desc(flags))))
+    with pytest.raises(abi.PaletteError, match="lbl has unknown flags 0x10"):
+        abi.check(lib.pk_gemm_validate(ctypes.byref(desc(0x10))))
+
+
 def test_conv_plan_matches_reference_shapes(abi):
     """planFusedConformerConv known answers (test/webgpu/conformer-conv-kernel-shapes.test.ts:18-58):
     batch 2 x 188 frames is 376 rows; byte lengths for fp16 and fp32."""

@@ -2,6 +2,7 @@
 split of a rocprofv3 kernel trace per launch kind (no GPU, no profiler: the
 trace is synthetic)."""
 import csv
+import json
 import os
 import sys
 
@@ -117,3 +118,42 @@ def test_split_trace_checks_kernel_names(tmp_path):
         w.writerows(rows)
     with pytest.raises(SystemExit, match="relative-attention ran"):
         bench.split_trace(str(path), 1, 2, layers=1)
+
+
+def write_counters(path, names_values, counter):
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        for d, (name, value) in enumerate(names_values, 1):
+            # two rows per dispatch: the splitter sums them
+            for half in (value / 2, value / 2):
+                w.writerow({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": half})
+
+
+def test_split_counters_scales_by_the_calibration_copy(tmp_path, capsys):
+    """HBM bytes per kind = FETCH x (copy KiB / copy FETCH) + WRITE x (copy
+    KiB / copy WRITE), from the last pass; the first copy dispatch is
+    skipped."""
+    layers, warmup, steps = 1, 1, 2
+    seq = bench.launch_sequence(layers)
+    passes = []
+    for p in range(warmup + steps):
+        passes += [(kernel_for(kind), 100.0 * (p + 1)) for kind in seq]
+    write_counters(tmp_path / "f.csv", passes, "FETCH_SIZE")
+    write_counters(tmp_path / "w.csv", [(n, v / 2) for n, v in passes], "WRITE_SIZE")
+    neg = "void at::native::vectorized_elementwise_kernel<neg_kernel>"
+    write_counters(tmp_path / "cf.csv", [(neg, 1.0), (neg, bench.COPY_KIB / 2), (neg, bench.COPY_KIB / 2)], "FETCH_SIZE")
+    write_counters(tmp_path / "cw.csv", [(neg, bench.COPY_KIB)] * 3, "WRITE_SIZE")
+    bench.split_counters(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "cf.csv"),
+                         str(tmp_path / "cw.csv"), warmup, steps, layers=layers)
+    out = capsys.readouterr().out
+    assert "FETCH_SIZE x 2.000, WRITE_SIZE x 1.000" in out
+    row = next(line for line in out.splitlines() if line.startswith("| feed-forward1-linear1 |"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    # last pass: FETCH 300 KiB x 2 + WRITE 150 KiB x 1 = 750 KiB
+    assert cells[1] == "1" and cells[2] == "300" and cells[3] == "150"
+    assert cells[4] == f"{750 * 1024 / 1e6:.1f} MB"
+    entries = json.loads(out.split("traffic.json entries:", 1)[1])
+    assert entries["encoder-feed-forward1-linear1"]["hbm_bytes_per_launch"] == 750 * 1024
+    assert "encoder-relative-attention" not in entries

@@ -829,6 +829,46 @@ def test_row_norm_contract_errors(abi, ctx, scope, workloads):
                    rows=64, inner=1024, columns=1024, glu=True, norm_gamma=g, norm_beta=g, label="lbl")
 
 
+@pytest.mark.parametrize("rows,inner,columns,activation,glu", [
+    (3008, 1024, 4096, "silu", False),
+    (752, 1024, 2048, "none", True),
+])
+def test_streamed_output_stores_match_plain_stores(abi, ctx, scope, oracle, workloads, rows, inner, columns,
+                                                   activation, glu):
+    """The f16 pair-code kernels store their output non-temporally unless
+    the op keeps it cached (PK_GEMM_CACHED_OUTPUT); both ops run the same
+    variant and grid, the streamed instantiation differing only in its
+    stores, so the outputs are bit-identical (with the GLU epilogue too),
+    and the streamed output is within tolerance of the oracle on sampled
+    rows."""
+    case = workloads.gemm_case(64, rows, inner, columns, 5, activation=activation)
+    w = case.weight
+    a, packed, palette = scope.put(case.a), scope.put(w.packed), scope.put(w.palette)
+    width = columns // 2 if glu else columns
+    outs, plans = {}, {}
+    for cached in (False, True):
+        outs[cached] = scope.put(np.full((rows, width), 7.0, np.float16))
+        op = abi.GemmOp(ctx, a=a, packed=packed, palette=palette, output=outs[cached], bits=5, rows=rows,
+                        inner=inner, columns=columns, activation=activation, glu=glu, cached_output=cached,
+                        label="cached-output" if cached else "streamed-output")
+        try:
+            plans[cached] = op.plan()
+            op.enqueue(0)
+            ctx.synchronize()
+        finally:
+            op.release()
+    streamed, plain = plans[False], plans[True]
+    print("streamed:", streamed.kernel.decode(), list(streamed.grid), streamed.stream_stores,
+          "cached:", plain.kernel.decode(), list(plain.grid), plain.stream_stores, flush=True)
+    assert streamed.stream_stores == 1 and plain.stream_stores == 0
+    assert streamed.kernel == plain.kernel and list(streamed.grid) == list(plain.grid)
+    first, second = outs[False].download(), outs[True].download()
+    np.testing.assert_array_equal(first.view(np.uint16), second.view(np.uint16))
+    if not glu:
+        sample = [0, 1, 191, 192, rows // 2, rows - 2, rows - 1]
+        assert_f16_parity(oracle, first[sample], case, rows=sample)
+
+
 @pytest.mark.parametrize("rows,inner,columns,bits,active", [
     (3008, 1024, 4096, 5, (188, 752)),   # FF expand: a 64 x 64 four-part tile at one window
     (3008, 4096, 1024, 5, (188, 1504)),  # FF contract: the small-M kernel at one window
