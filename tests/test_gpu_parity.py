@@ -131,9 +131,9 @@ def oracle_gemm(oracle, case, mode, threads=8, rows=None):
                        mode=mode, threads=threads)
 
 
-def assert_f16_parity(oracle, got, case, rows=None):
-    ref = oracle_gemm(oracle, case, "f16-chain", rows=rows)
-    truth = oracle_gemm(oracle, case, "f64", rows=rows)
+def assert_f16_parity(oracle, got, case, rows=None, threads=8):
+    ref = oracle_gemm(oracle, case, "f16-chain", threads=threads, rows=rows)
+    truth = oracle_gemm(oracle, case, "f64", threads=threads, rows=rows)
     assert np.all(np.isfinite(got.astype(np.float32)))
     norm_ref, _ = oracle.relative_errors(got, ref)
     norm_truth, max_truth = oracle.relative_errors(got, truth)
@@ -520,8 +520,8 @@ def test_production_signature_is_accepted(abi, ctx, scope, workloads):
 
 def test_feed_forward_block_full_size(abi, ctx, scope, oracle, workloads):
     """8 windows x 188 frames x 1024: H = SiLU(X W1) and Y = X + 0.5 H W2 run
-    back to back on the device; sampled rows are checked against the oracle
-    (the full f16 chain is minutes of CPU), every row for finiteness."""
+    back to back on the device; every row of H and Y is checked against the
+    oracle (about 15 s of CPU at 16 threads)."""
     ff = workloads.feed_forward_block(0)
     m = ff.x.shape[0]
     x = scope.put(ff.x)
@@ -541,10 +541,10 @@ def test_feed_forward_block_full_size(abi, ctx, scope, oracle, workloads):
     op1.release()
     op2.release()
     assert np.all(np.isfinite(h.astype(np.float32))) and np.all(np.isfinite(out.astype(np.float32)))
-    rows = np.unique(np.concatenate([np.arange(0, m, 47), [m - 1]]))
-    assert_f16_parity(oracle, h[rows], ff.expand_case(), rows=rows)
-    contract = ff.contract_case(h)
-    assert_f16_parity(oracle, out[rows], contract, rows=rows)
+    print("FF block", m, "rows: expand", flush=True)
+    assert_f16_parity(oracle, h, ff.expand_case(), threads=16)
+    print("FF block: contract", flush=True)
+    assert_f16_parity(oracle, out, ff.contract_case(h), threads=16)
 
 
 def test_feed_forward_block_graph_replay_matches_eager(abi, ctx, workloads):
