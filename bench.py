@@ -20,6 +20,12 @@ Other workloads (for profiling; same JSON shape):
   ff-block          the feed-forward block above as the step, TFLOP/s
   single-gemm-fp32  X[256x1024] f32 x 6-bit W 1024->4096 + bias
   small-m           5-bit 1024->4096 f16 GEMM at --rows M (HBM-bound regime)
+  layer-gemms       the six palette GEMM shapes of an encoder layer at --rows M
+                    (3008 = 16 windows), one launch each per step: FF expand +
+                    SiLU, FF contract + 0.5 residual, QKV (3 palette groups),
+                    the 6-bit output projection + residual, PW1 + GLU, PW2 +
+                    residual; with --variant V every shape that V can run is
+                    forced onto it (tile sweeps)
   weight-stream     every palette GEMM of the 24 encoder layers (192 distinct
                     weights, 365 MB packed) at --rows M: one grouped small-M
                     launch per step (value, GB/s), and the same GEMMs as 192
@@ -76,7 +82,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="encoder",
                    choices=["ff-block", "single-gemm-fp32", "small-m", "weight-stream", "conv-module",
-                            "conv-module-fused", "rel-pos-mha", "encoder", "transcribe"])
+                            "conv-module-fused", "rel-pos-mha", "layer-gemms", "encoder", "transcribe"])
     p.add_argument("--frames", type=int, default=188, help="T for --workload rel-pos-mha")
     p.add_argument("--windows", type=int, default=16,
                    help="encoder / transcribe: windows the graph holds (40 is the reference's largest batch)")
@@ -234,6 +240,41 @@ def build_small_m(abi, ctx, keep, rows):
                           "activations and output shared)"}
     return [Kernel(f"small-m-{rows}", RotatingOp(ops), case.flops, case.algorithmic_bytes(), "f16",
                    (rows, 1024, 4096))], config, case
+
+
+# The palette GEMMs of one encoder layer: name, K, N, bits, palette groups,
+# activation, residual scale, GLU epilogue.
+LAYER_GEMM_SHAPES = (
+    ("ff-expand", 1024, 4096, 5, 1, "silu", None, False),
+    ("ff-contract", 4096, 1024, 5, 1, "none", 0.5, False),
+    ("qkv", 1024, 3072, 5, 3, "none", None, False),
+    ("output-projection", 1024, 1024, 6, 1, "none", 1.0, False),
+    ("pointwise1-glu", 1024, 2048, 5, 1, "none", None, True),
+    ("pointwise2", 1024, 1024, 5, 1, "none", 1.0, False),
+)
+
+
+def build_layer_gemms(abi, ctx, keep, rows):
+    """One launch of each palette GEMM shape of an encoder layer at `rows`
+    rows, seeded random operands (the FF expand's case is the CPU leg's)."""
+    import parakeet_wgsl_amd.workloads as wl
+    kernels, first = [], None
+    for seed, (name, inner, columns, bits, groups, activation, scale, glu) in enumerate(LAYER_GEMM_SHAPES):
+        case = wl.gemm_case(seed, rows, inner, columns, bits, groups=groups, activation=activation,
+                            residual_scale=scale)
+        first = first or case
+        width = columns // 2 if glu else columns
+        out = keep(ctx.empty((rows, width), np.float16))
+        op = abi.GemmOp(ctx, a=keep(ctx.array(case.a)), packed=keep(ctx.array(case.weight.packed)),
+                        palette=keep(ctx.array(case.weight.palette)), output=out, bits=bits, rows=rows,
+                        inner=inner, columns=columns, activation=activation,
+                        residual=keep(ctx.array(case.residual)) if scale is not None else None,
+                        residual_scale=scale, glu=glu, label=f"layer-{name}")
+        nbytes = case.algorithmic_bytes() - (rows * (columns - width) * 2)
+        kernels.append(Kernel(name, op, case.flops, nbytes, "f16", (rows, inner, columns)))
+    config = {"workload": "encoder-layer-gemms-fp16", "rows": rows,
+              "shapes": {n: [k, c] for n, k, c, *_ in LAYER_GEMM_SHAPES}}
+    return kernels, config, first
 
 
 def build_conv_module(abi, ctx, keep, fused_glu=False):
@@ -1408,12 +1449,19 @@ def main():
         kernels, config, data = build_conv_module(abi, ctx, keep, args.workload == "conv-module-fused")
     elif args.workload == "rel-pos-mha":
         kernels, config, data = build_mha(abi, ctx, keep, args.frames)
+    elif args.workload == "layer-gemms":
+        kernels, config, data = build_layer_gemms(abi, ctx, keep, args.rows)
     else:
         kernels, config, data = build_small_m(abi, ctx, keep, args.rows)
     if args.variant >= 0:
         for k in kernels:
             if isinstance(k.op, (abi.GemmOp, RotatingOp)):
-                k.op.set_variant(args.variant)
+                try:
+                    k.op.set_variant(args.variant)
+                except abi.PaletteRangeError:
+                    if args.workload != "layer-gemms":
+                        raise
+                    k.name += " (planned: the forced variant cannot run it)"
 
     step = measure_kernel_step(ctx, kernels, args.steps, args.warmup, args.graph)
     dominant, dom, roofline = step["dominant"], step["dom"], step["roofline"]

@@ -360,9 +360,10 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
     // and 50.8 us for two rounds of 160 x 256; at 7520 rows 81.4 us on three
     // rounds of 160 x 256 against 88.4 us on three of 192 x 256 (inside the
     // encoder pass, same box); QKV 3008 x 1024 x 3072 29.2 us on 192
-    // workgroups of 192 x 256 against 30.3 us for 96 x 128. The 160 x 256 QKV
-    // (228 workgroups) measured 26.6 us alone but 28.6 us against 27.2 us
-    // inside the encoder pass, so it is not planned for 3072 columns.
+    // workgroups of 192 x 256 against 30.3 us for 96 x 128, and with the
+    // non-temporal output stores 27.1 us on 228 workgroups of 160 x 256
+    // against 27.6 us on 192 x 256 inside the encoder pass (three runs each,
+    // interleaved on one box; pass 7.13 against 7.16 ms).
     constexpr Candidate kCandidates[] = {
         {2, 6, 2, 2, 192, 128, 22.3}, {2, 4, 2, 2, 128, 128, 17.2}, {2, 3, 2, 2, 96, 128, 14.8},
         {1, 3, 2, 4, 96, 64, 11.0},   {1, 2, 2, 4, 64, 64, 9.3},    {0, 2, 1, 8, 64, 32, 8.2},
@@ -372,7 +373,7 @@ Plan plan_launch(int precision, uint32_t rows, uint32_t inner, uint32_t columns,
     double best_us = 1e300;
     for (const Candidate& c : kCandidates) {
       if (c.tile_columns == 256 && (columns < 3072u || inner < 1024u)) continue;
-      if (c.tile_columns == 256 && c.tile_rows == 160 && columns < 4096u) continue;
+      if (c.tile_columns == 256 && c.tile_rows == 160 && columns < 3072u) continue;
       const int v = c.wn ? find_variant(PK_PRECISION_F16, pk::kFamilyPairCode, 1, c.wn, c.r, c.c, c.ks)
                          : find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, c.r, 1, 8);
       if (v < 0) continue;
