@@ -95,6 +95,8 @@ host.F16GemmKernel.create({}, arena).then((kernel) => {
   throwsLike(() => kernel.validateDescriptor(descriptor({ activation: "silu",
     mutate: (d) => { d.rowNorm = { gamma: normTensor(4096), beta: normTensor(4096), epsilon: -1 }; } })),
       Error, "epsilon >= 0");
+  // cachedOutput (PK_GEMM_CACHED_OUTPUT, no reference counterpart): a store hint the contract accepts
+  kernel.validateDescriptor(descriptor({ activation: "silu", mutate: (d) => { d.cachedOutput = true; } }));
   // arena.ts slice rules
   throwsLike(() => arena.slice("x", 100, 64), RangeError, "Invalid activation slice x");
   // the counters of a fused kernel: nothing is ever expanded

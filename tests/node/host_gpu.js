@@ -55,6 +55,10 @@ async function main() {
   fs.writeFileSync(spec.output, Buffer.from(result));
   const ms = timestamps.elapsedMs(0, 1);
   assert.ok(ms > 0, `timestamp ${ms}`);
+  // the plan names the launch's kernel and whether its output stores are non-temporal
+  const plan = dispatch.plan(spec.activeRows);
+  assert.strictEqual(typeof plan.kernel, "string");
+  assert.strictEqual(typeof plan.streamStores, "boolean");
   // encode after destroy throws the reference's error; destroy is idempotent
   dispatch.destroy();
   dispatch.destroy();
