@@ -1165,13 +1165,14 @@ class EncoderOp:
         check(load().pk_encoder_enqueue(self.handle, active_batch, stream, int(graph)))
 
     def enqueue_profiled(self, starts, ends, active_batch: int = 0, stream=None) -> None:
-        """One eager pass whose launch i stamps starts[i] / ends[i] (Events);
-        both lists hold one entry per launch of the pass."""
+        """One eager pass whose launch i stamps starts[i] / ends[i] (Events,
+        or None for a launch that stamps nothing); both lists hold one entry
+        per launch of the pass."""
         launches = self.info()[0]
         if len(starts) != launches or len(ends) != launches:
             raise ValueError(f"a profiled pass takes {launches} start and end events")
-        start_array = (ctypes.c_void_p * len(starts))(*[ev.handle for ev in starts])
-        end_array = (ctypes.c_void_p * len(ends))(*[ev.handle for ev in ends])
+        start_array = (ctypes.c_void_p * len(starts))(*[ev.handle if ev is not None else None for ev in starts])
+        end_array = (ctypes.c_void_p * len(ends))(*[ev.handle if ev is not None else None for ev in ends])
         check(load().pk_encoder_enqueue_profiled(self.handle, active_batch, stream, start_array, end_array))
 
     def info(self) -> tuple[int, int]:

@@ -45,9 +45,11 @@ def kernel_for(kind):
 
 
 def write_trace(path, layers, warmup, steps, duration_us, rows=None):
-    """A kernel trace of `warmup + steps` passes; each launch of `kind` lasts
-    duration_us(kind, stamped) (stamped passes: every TIMING_STRIDE-th timed
-    one), then one op preparation and the roofline loop."""
+    """A kernel trace of `warmup + PROFILE_PASSES + steps` passes; each
+    launch of `kind` lasts duration_us(kind, pass kind) ("profiled" for the
+    passes after the warm-up, "stamped" for every TIMING_STRIDE-th timed
+    one, "graph" for the rest), then one op preparation and the roofline
+    loop."""
     seq = bench.launch_sequence(layers)
     t = 1_000_000
     out = []
@@ -58,10 +60,12 @@ def write_trace(path, layers, warmup, steps, duration_us, rows=None):
                     "Grid_Size_X": grid})
         t += int(us * 1000) + 500
 
-    for p in range(warmup + steps):
-        stamped = p >= warmup and (p - warmup) % bench.TIMING_STRIDE == 0
+    for p in range(warmup + bench.PROFILE_PASSES + steps):
+        timed = p - warmup - bench.PROFILE_PASSES
+        pass_kind = ("profiled" if warmup <= p < warmup + bench.PROFILE_PASSES else
+                     "stamped" if timed >= 0 and timed % bench.TIMING_STRIDE == 0 else "graph")
         for kind in seq:
-            add(kernel_for(kind), duration_us(kind, stamped))
+            add(kernel_for(kind), duration_us(kind, pass_kind))
     add(PREP, 20.0)
     warm, n = bench.ROOFLINE_LOOP
     for i in range(warm + n):
@@ -75,30 +79,33 @@ def write_trace(path, layers, warmup, steps, duration_us, rows=None):
 
 
 def test_split_trace_kinds_and_loop(tmp_path, capsys):
-    """Per-kind averages over stamped and graph passes come out as written,
-    and the roofline loop is the last ROOFLINE_LOOP[1] GEMM launches, not
-    the op preparation before them."""
+    """Per-kind averages over the profiled passes, the timed stamped steps
+    and the graph passes come out as written, and the roofline loop is the
+    last ROOFLINE_LOOP[1] GEMM launches, not the op preparation before
+    them."""
     path = tmp_path / "trace.csv"
+    extra = {"profiled": 2.0, "stamped": 1.0, "graph": 0.0}
 
-    def duration(kind, stamped):
-        return (10.0 if kind.startswith("norm_") else 20.0) + (1.0 if stamped else 0.0)
+    def duration(kind, pass_kind):
+        return (10.0 if kind.startswith("norm_") else 20.0) + extra[pass_kind]
 
     write_trace(path, 2, 3, 10, duration)
     bench.split_trace(str(path), 3, 10, layers=2)
     out = capsys.readouterr().out
+    passes = 3 + bench.PROFILE_PASSES + 10
     row = next(line for line in out.splitlines() if line.startswith("| norm_self_att |"))
     cells = [c.strip() for c in row.strip("|").split("|")]
-    assert cells[1] == "26" and cells[2] == "11.00" and cells[3] == "10.00"
+    assert cells[1] == str(2 * passes) and cells[2:5] == ["12.00", "11.00", "10.00"]
     row = next(line for line in out.splitlines() if line.startswith("| feed-forward1-linear1 |"))
     cells = [c.strip() for c in row.strip("|").split("|")]
-    assert cells[2] == "21.00" and cells[3] == "20.00"
+    assert cells[2:5] == ["22.00", "21.00", "20.00"]
     loop = next(line for line in out.splitlines() if line.startswith("roofline loop"))
     assert "avg 30.00 us" in loop and "operand_order" not in loop and "of 55 " in loop
 
 
 def test_split_trace_rejects_wrong_pass_count(tmp_path):
     path = tmp_path / "trace.csv"
-    write_trace(path, 1, 1, 5, lambda kind, stamped: 5.0)
+    write_trace(path, 1, 1, 5, lambda kind, pass_kind: 5.0)
     with pytest.raises(SystemExit, match="passes in the trace"):
         bench.split_trace(str(path), 1, 4, layers=1)
 
@@ -106,7 +113,7 @@ def test_split_trace_rejects_wrong_pass_count(tmp_path):
 def test_split_trace_checks_kernel_names(tmp_path):
     """A launch whose kernel does not belong to its kind stops the split."""
     path = tmp_path / "trace.csv"
-    write_trace(path, 1, 1, 2, lambda kind, stamped: 5.0)
+    write_trace(path, 1, 1, 2, lambda kind, pass_kind: 5.0)
     with open(path) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
     seq = bench.launch_sequence(1)
@@ -138,7 +145,8 @@ def test_split_counters_scales_by_the_calibration_copy(tmp_path, capsys):
     layers, warmup, steps = 1, 1, 2
     seq = bench.launch_sequence(layers)
     passes = []
-    for p in range(warmup + steps):
+    total = warmup + bench.PROFILE_PASSES + steps
+    for p in range(total):
         passes += [(kernel_for(kind), 100.0 * (p + 1)) for kind in seq]
     write_counters(tmp_path / "f.csv", passes, "FETCH_SIZE")
     write_counters(tmp_path / "w.csv", [(n, v / 2) for n, v in passes], "WRITE_SIZE")
@@ -151,9 +159,10 @@ def test_split_counters_scales_by_the_calibration_copy(tmp_path, capsys):
     assert "FETCH_SIZE x 2.000, WRITE_SIZE x 1.000" in out
     row = next(line for line in out.splitlines() if line.startswith("| feed-forward1-linear1 |"))
     cells = [c.strip() for c in row.strip("|").split("|")]
-    # last pass: FETCH 300 KiB x 2 + WRITE 150 KiB x 1 = 750 KiB
-    assert cells[1] == "1" and cells[2] == "300" and cells[3] == "150"
-    assert cells[4] == f"{750 * 1024 / 1e6:.1f} MB"
+    # last pass: FETCH 100 t KiB x 2 + WRITE 50 t KiB x 1 = 250 t KiB
+    fetch, write = 100 * total, 50 * total
+    assert cells[1] == "1" and cells[2] == f"{fetch:,}" and cells[3] == f"{write:,}"
+    assert cells[4] == f"{250 * total * 1024 / 1e6:.1f} MB"
     entries = json.loads(out.split("traffic.json entries:", 1)[1])
-    assert entries["encoder-feed-forward1-linear1"]["hbm_bytes_per_launch"] == 750 * 1024
+    assert entries["encoder-feed-forward1-linear1"]["hbm_bytes_per_launch"] == 250 * total * 1024
     assert "encoder-relative-attention" not in entries
