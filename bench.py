@@ -976,10 +976,11 @@ def run_encoder(args, abi, ctx, decoder=False):
     timed_us = [marks[step][0][i].elapsed_ms(marks[step][1][i]) * 1e3 for step in timed_steps for i in stamped_slots]
     decoder_ms = float(np.mean([a.elapsed_ms(b) for a, b in tdt_marks.values()])) if tdt else None
     # The roofline takes the dominant launch kind's average stamped duration
-    # in the timed region (an event pair around each of its launches in the
-    # stamped passes). The same op launched back to back after the timed
-    # region is kept beside it: its inputs stay cached between launches, so
-    # it runs 2-9% faster than inside the pass.
+    # in the timed region (timed_us: an event pair around each of its
+    # launches in the stamped steps, whose other launches run unstamped).
+    # The same op launched back to back after the timed region is kept
+    # beside it: its inputs stay cached between launches, so it runs faster
+    # than inside the pass.
     loop_us = None
     if name in LAYER_GEMMS:
         loop_us = roofline_loop(ctx, abi, name, layers[0], out, active * stack.frames, stream)
