@@ -498,6 +498,22 @@ def launch_sequence(layers, chained=True, fused_norms=()):
     return seq
 
 
+def roofline_slots(layers, projectors, name, dispatches, launches):
+    """Dispatch slots of an encoder pass (front end, 15 per layer, the
+    projector) whose launch kind is `name`'s, the two FF modules' launches of
+    one shape counting as one kind; slots of kinds that launch nothing
+    (a LayerNorm inside the next GEMM) are left out."""
+    from parakeet_wgsl_amd.palette_abi import ENCODER_DISPATCHES
+    slot_kinds = list(FRONT_DISPATCHES) + list(ENCODER_DISPATCHES) * layers + ["projector"] * projectors
+    if len(slot_kinds) != launches:
+        raise SystemExit(f"{len(slot_kinds)} dispatch slots, the encoder reports {launches}")
+
+    def kind(k):
+        return k.replace("feed-forward2-", "feed-forward1-")
+    return [i for i, k in enumerate(slot_kinds) if kind(k) == kind(name) and k in dispatches
+            and dispatches[k].get("launches_per_pass", 1) > 0]
+
+
 def kernel_family(kind):
     """Substring the kernel name of a launch of `kind` carries."""
     if kind.startswith("norm_"):
@@ -944,12 +960,7 @@ def run_encoder(args, abi, ctx, decoder=False):
     # The timed region: graph replays, and every TIMING_STRIDE-th step an
     # eager pass whose launches of the dominant kind stamp events (the
     # roofline's durations); the other launches of that pass stamp nothing.
-    slot_kinds = (list(FRONT_DISPATCHES) + list(abi.ENCODER_DISPATCHES) * len(stack.layers) +
-                  ["projector"] * len(projector_costs))
-    if len(slot_kinds) != launches:
-        raise SystemExit(f"{len(slot_kinds)} dispatch slots, the encoder reports {launches}")
-    stamped_slots = [i for i, k in enumerate(slot_kinds) if kind(k) == kind(name) and k in dispatches
-                     and dispatches[k].get("launches_per_pass", 1) > 0]
+    stamped_slots = roofline_slots(len(stack.layers), len(projector_costs), name, dispatches, launches)
     timed_steps = list(range(0, args.steps, TIMING_STRIDE))
     marks = {step: ([ctx.event() if i in stamped_slots else None for i in range(launches)],
                     [ctx.event() if i in stamped_slots else None for i in range(launches)])

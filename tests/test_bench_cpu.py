@@ -166,3 +166,22 @@ def test_split_counters_scales_by_the_calibration_copy(tmp_path, capsys):
     entries = json.loads(out.split("traffic.json entries:", 1)[1])
     assert entries["encoder-feed-forward1-linear1"]["hbm_bytes_per_launch"] == 250 * total * 1024
     assert "encoder-relative-attention" not in entries
+
+
+def test_roofline_slots_pick_both_ff_modules():
+    """The stamped slots of the timed region are the roofline kind's
+    launches in both FF modules of every layer, and nothing else."""
+    from parakeet_wgsl_amd.palette_abi import ENCODER_DISPATCHES
+    layers = 3
+    launches = len(bench.FRONT_DISPATCHES) + len(ENCODER_DISPATCHES) * layers + 1
+    dispatches = {k: {"launches_per_pass": layers} for k in ENCODER_DISPATCHES}
+    slots = bench.roofline_slots(layers, 1, "feed-forward1-linear2-residual", dispatches, launches)
+    kinds = list(bench.FRONT_DISPATCHES) + list(ENCODER_DISPATCHES) * layers + ["projector"]
+    assert len(slots) == 2 * layers
+    assert {kinds[i] for i in slots} == {"feed-forward1-linear2-residual", "feed-forward2-linear2-residual"}
+    # a fused LayerNorm's slot launches nothing and is never stamped
+    dispatches["norm_self_att"]["launches_per_pass"] = 0
+    assert bench.roofline_slots(layers, 1, "norm_self_att", dispatches, launches) == []
+    with pytest.raises(SystemExit, match="dispatch slots"):
+        bench.roofline_slots(layers, 1, "projector", dispatches, launches + 1)
+
