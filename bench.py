@@ -961,9 +961,10 @@ def run_encoder(args, abi, ctx, decoder=False):
     # eager pass whose launches of the dominant kind stamp events (the
     # roofline's durations); the other launches of that pass stamp nothing.
     stamped_slots = roofline_slots(len(stack.layers), len(projector_costs), name, dispatches, launches)
+    stamped = set(stamped_slots)
     timed_steps = list(range(0, args.steps, TIMING_STRIDE))
-    marks = {step: ([ctx.event() if i in stamped_slots else None for i in range(launches)],
-                    [ctx.event() if i in stamped_slots else None for i in range(launches)])
+    marks = {step: ([ctx.event() if i in stamped else None for i in range(launches)],
+                    [ctx.event() if i in stamped else None for i in range(launches)])
              for step in timed_steps}
     tdt_marks = {step: (ctx.event(), ctx.event()) for step in timed_steps} if tdt else {}
     start, end = ctx.event(), ctx.event()
