@@ -87,6 +87,21 @@ class Stack:
         out = self.run(active, graph)
         return out, self.projected.download()
 
+    def run_profiled(self, stamped):
+        """One eager pass whose launches in `stamped` (slot indices) stamp
+        their own events, the others none; returns the output and the
+        stamped durations in ms."""
+        launches = self.op.info()[0]
+        starts = [self.ctx.event() if i in stamped else None for i in range(launches)]
+        ends = [self.ctx.event() if i in stamped else None for i in range(launches)]
+        self.op.enqueue_profiled(starts, ends)
+        self.ctx.synchronize()
+        durations = [starts[i].elapsed_ms(ends[i]) for i in sorted(stamped)]
+        for ev in starts + ends:
+            if ev is not None:
+                ev.destroy()
+        return self.output.download(), durations
+
     def release(self):
         self.op.release()
 
@@ -324,6 +339,16 @@ def test_encoder_graph_with_front_end_and_projector(abi, ctx, scope, oracle, wor
         graph, graph_projected = enc.run_both(graph=True)
         np.testing.assert_array_equal(graph.view(np.uint16), got.view(np.uint16))
         np.testing.assert_array_equal(graph_projected.view(np.uint16), projected.view(np.uint16))
+        # stamped passes (every launch, or a few with the others unstamped, as
+        # bench.py's timed steps run) compute the same pass
+        launches = enc.op.info()[0]
+        for stamped in (set(range(launches)), {7, 8, 8 + 15}):
+            profiled, durations = enc.run_profiled(stamped)
+            np.testing.assert_array_equal(profiled.view(np.uint16), got.view(np.uint16))
+            # (a chained LayerNorm slot launches nothing: its two events are back to back)
+            assert len(durations) == len(stamped) and all(d >= 0 for d in durations), durations
+            if len(stamped) == 3:
+                assert all(d > 0 for d in durations), durations
     finally:
         enc.release()
     assert np.isfinite(got).all() and np.isfinite(projected).all()
