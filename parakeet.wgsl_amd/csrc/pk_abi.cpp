@@ -1271,19 +1271,46 @@ struct pk_gemm_group {
 
 namespace {
 
+// The launch arguments of `g` on `variant` at `rows`.
+pk::SmallMGroupArgs group_args(const pk_gemm_group* g, int variant, uint32_t rows) {
+  const pk::TileShape s = pk::f16_variant(variant);
+  const int w = group_width_index((uint32_t)s.n_blocks);
+  pk::SmallMGroupArgs args{};
+  args.members = static_cast<const pk::SmallMMember*>(g->table);
+  args.items = w < 0 ? nullptr : g->items[w];
+  args.items_count = w < 0 ? 0u : g->items_count[w];
+  args.rows = rows;
+  args.row_groups = pk::tiles_m(s, rows);
+  args.persistent = 1u;
+  for (const pk::SmallMMember& m : g->members)
+    if (!pk::f16_group_streams(variant, m.args.inner, m.args.palette_groups, m.args.palette_group_columns))
+      args.persistent = 0u;
+  return args;
+}
+
 // The small-M variant a group runs: K over four wavefronts, each reusing
-// its activation fragments over four column blocks, code loads four K
-// blocks ahead. Measured on MI355X over the encoder's 192 weights (365 MB)
-// against every other small-M shape at 16, 64 and 188 rows, it was the
-// fastest at each (16 rows: 105 us; 64 rows, two row groups whose second
-// code read hits L2: 202 us; 188 rows: 534 us).
-int plan_group(uint32_t rows) {
-  (void)rows;
+// its activation fragments over four column blocks (32 x 128). Measured on
+// MI355X over the encoder's 192 weights (365 MB), kernel-stamped: the
+// persistent form (one round of resident workgroups, the next item's loads
+// under the current item's last blocks; code loads two blocks ahead) ran
+// 100.4 us at 16 rows and 192.7 us at 64, against 115.6 and 228.3 us for
+// the one-shot launch with code loads four blocks ahead, the fastest
+// one-shot shape at 16, 64 and 188 rows. Groups with a member the
+// persistent kernel cannot run (K not a multiple of 512, an item across
+// palette groups) take that one-shot variant.
+int plan_group(const pk_gemm_group* g, uint32_t rows) {
+  const int count = pk::f16_variant_count();
+  for (int i = 0; i < count; ++i) {
+    const pk::TileShape s = pk::f16_variant(i);
+    if (pk::f16_group_persistent(i) && s.m_blocks == 1 && s.n_blocks == 4 && s.k_split == 4 &&
+        group_args(g, i, rows).persistent)
+      return i;
+  }
   const int v = find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 4, 4);
   return v < 0 ? find_variant(PK_PRECISION_F16, pk::kFamilySmallM, 1, 1, 1, 1, 8) : v;
 }
 
-int group_variant(const pk_gemm_group* g, uint32_t rows) { return g->forced >= 0 ? g->forced : plan_group(rows); }
+int group_variant(const pk_gemm_group* g, uint32_t rows) { return g->forced >= 0 ? g->forced : plan_group(g, rows); }
 
 }  // namespace
 
@@ -1395,12 +1422,7 @@ int pk_gemm_group_enqueue_timed(pk_gemm_group* g, uint32_t active_rows, void* st
   const pk::TileShape s = pk::f16_variant(variant);
   const int w = group_width_index((uint32_t)s.n_blocks);
   if (w < 0) return fail(PK_INTERNAL_ERROR, "%s: variant %d has no group item list", g->label.c_str(), variant);
-  pk::SmallMGroupArgs args{};
-  args.members = static_cast<const pk::SmallMMember*>(g->table);
-  args.items = g->items[w];
-  args.items_count = g->items_count[w];
-  args.rows = rows;
-  args.row_groups = pk::tiles_m(s, rows);
+  const pk::SmallMGroupArgs args = group_args(g, variant, rows);
   PK_HIP(hipSetDevice(g->ctx->device), "hipSetDevice");
   PK_HIP(pk::launch_gemm_f16_group(variant, args, stream_or_default(g->ctx, stream),
                                    static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(end_event)),
@@ -1430,7 +1452,8 @@ int pk_gemm_group_plan(const pk_gemm_group* g, uint32_t active_rows, pk_gemm_pla
   const pk::TileShape s = pk::f16_variant(variant);
   const int w = group_width_index((uint32_t)s.n_blocks);
   std::memset(info, 0, sizeof *info);
-  info->grid[0] = pk::small_m_grid(s, w < 0 ? 0u : g->items_count[w], rows);
+  const char* kernel = nullptr;
+  info->grid[0] = w < 0 ? 0u : pk::f16_group_launch_plan(variant, group_args(g, variant, rows), &kernel);
   info->grid[1] = info->grid[2] = 1;
   info->block_threads = s.threads();
   info->tile_rows = s.tile_rows();
@@ -1441,7 +1464,7 @@ int pk_gemm_group_plan(const pk_gemm_group* g, uint32_t active_rows, pk_gemm_pla
     info->flops += 2ull * rows * m.args.inner * m.args.columns;
     info->algorithmic_bytes += algorithmic_bytes(m.args, m.bits, rows, 2u);
   }
-  std::snprintf(info->kernel, sizeof info->kernel, "%s", pk::f16_group_kernel_name(variant));
+  std::snprintf(info->kernel, sizeof info->kernel, "%s", kernel ? kernel : pk::f16_group_kernel_name(variant));
   return ok();
 }
 

@@ -263,6 +263,9 @@ const f16::F16Variant& f16s_variant(int index);
 hipError_t launch_gemm_f16s(int bits, const f16::F16Variant& v, const GemmArgs& args, hipStream_t stream,
                             hipEvent_t start, hipEvent_t stop);
 const char* f16s_group_name(int index);
+bool f16s_group_persistent(int index);
+bool f16s_group_streams(int index, uint32_t inner, uint32_t palette_groups, uint32_t palette_group_columns);
+uint32_t f16s_group_launch(int index, const SmallMGroupArgs& g, void (**kernel)(SmallMGroupArgs), const char** name);
 hipError_t launch_gemm_f16s_group(int index, const SmallMGroupArgs& group, hipStream_t stream, hipEvent_t start,
                                   hipEvent_t stop);
 

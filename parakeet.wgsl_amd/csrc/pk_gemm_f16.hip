@@ -344,6 +344,22 @@ const char* f16_group_kernel_name(int index) {
                                                      : nullptr;
 }
 
+bool f16_group_persistent(int index) {
+  return f16_variant_family(index) == kFamilySmallM && f16s_group_persistent(index - kLocal - f16k_variant_count());
+}
+
+bool f16_group_streams(int index, uint32_t inner, uint32_t palette_groups, uint32_t palette_group_columns) {
+  return f16_variant_family(index) == kFamilySmallM &&
+         f16s_group_streams(index - kLocal - f16k_variant_count(), inner, palette_groups, palette_group_columns);
+}
+
+uint32_t f16_group_launch_plan(int index, const SmallMGroupArgs& group, const char** kernel) {
+  void (*fn)(SmallMGroupArgs) = nullptr;
+  *kernel = nullptr;
+  if (f16_variant_family(index) != kFamilySmallM) return 0;
+  return f16s_group_launch(index - kLocal - f16k_variant_count(), group, &fn, kernel);
+}
+
 hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStream_t stream, hipEvent_t start,
                                  hipEvent_t stop) {
   if (f16_variant_family(index) != kFamilySmallM) return hipErrorInvalidValue;

@@ -239,8 +239,17 @@ struct SmallMGroupArgs {
   uint32_t items_count;
   uint32_t rows;
   uint32_t row_groups;  // tiles_m of the variant at `rows`
+  uint32_t persistent;  // 1: every member fits the variant's persistent kernel
 };
 const char* f16_group_kernel_name(int index);
+// Whether small-M variant `index` has a persistent group kernel.
+bool f16_group_persistent(int index);
+// Whether a member of K `inner` and the given palette grouping fits the
+// persistent group kernel of small-M variant `index` (false for a variant
+// without one).
+bool f16_group_streams(int index, uint32_t inner, uint32_t palette_groups, uint32_t palette_group_columns);
+// Grid (x) and kernel name of the launch launch_gemm_f16_group makes.
+uint32_t f16_group_launch_plan(int index, const SmallMGroupArgs& group, const char** kernel);
 hipError_t launch_gemm_f16_group(int index, const SmallMGroupArgs& group, hipStream_t stream,
                                  hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 

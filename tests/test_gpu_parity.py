@@ -106,8 +106,9 @@ def k_split_of(name):
     """Order class of a kernel: pair-code variants add their K-part partial
     tiles at the end (pk_gemm_f16p_b*_n<WN>k<KS>_...); KS = 1 and every
     operand-order variant accumulate all of K in one chain; the small-M
-    variants (pk_gemm_f16s_b*_k<W>_...) add W round-robin K partials."""
-    m = re.search(r"_f16s_(?:b\d_|group_)k(\d+)_", name)
+    variants (pk_gemm_f16s_{b*,group,stream}_k<W>_...) add W round-robin K
+    partials."""
+    m = re.search(r"_f16s_(?:b\d_|group_|stream_)k(\d+)_", name)
     if m:
         return "small-m-k" + m.group(1)
     m = re.search(r"_n\dk(\d)_", name)
@@ -721,6 +722,80 @@ def test_gemm_group_prefix_and_lifetime(abi, ctx, scope, oracle, workloads):
     finally:
         group.release()
         for op, _ in single:
+            op.release()
+
+
+# Members a persistent group kernel can run (K a multiple of 512: 64 x four
+# wavefronts x two blocks ahead; items inside one palette group): both code
+# widths and every epilogue in one launch.
+STREAM_MEMBERS = [
+    (1024, 4096, 5, 1, "silu", True, None),    # FF expand + SiLU
+    (4096, 1024, 5, 1, "none", False, 0.5),    # FF contract + 0.5 residual
+    (1024, 3072, 5, 3, "none", False, None),   # QKV, 3 palette groups
+    (1024, 1024, 6, 1, "none", False, 1.0),    # output projection + residual
+    (1536, 512, 6, 1, "relu", True, None),     # K = 3 x 512, bias, ReLU
+]
+
+
+@pytest.mark.parametrize("rows", [16, 64, 100])
+def test_gemm_group_persistent_matches_one_shot(abi, ctx, scope, oracle, workloads, rows):
+    """The persistent group kernels (one round of resident workgroups, each
+    walking several work items and loading the next item's palette, first
+    code blocks and activations while it multiplies the current item's last
+    blocks) give every member the bits of a one-shot group launch of the
+    same tile and K split (how far ahead codes are loaded changes no sum).
+    Copies of the members make about 1,600 items of 128 columns, so that
+    every workgroup runs several (the planned grid is checked to be smaller
+    than the item count); 100 rows end in a partial row group. One copy of
+    each member also meets the oracle's bars."""
+    small = small_m_variants(abi, ctx, scope, workloads)
+    items_per_copy = sum(-(-n // 128) for _, n, *_ in STREAM_MEMBERS) * -(-rows // 32)
+    cases, ops, outs = [], [], []
+    for copy in range(-(-1600 // items_per_copy)):
+        for i, (k, n, bits, groups, act, bias, scale) in enumerate(STREAM_MEMBERS):
+            case = workloads.gemm_case(rows * 53 + copy * 11 + i, rows, k, n, bits, groups=groups, activation=act,
+                                       bias=bias, residual_scale=scale)
+            out = scope.put(np.full((rows, n), 7.0, np.float16))
+            op = abi.GemmOp(ctx, a=scope.put(case.a), packed=scope.put(case.weight.packed),
+                            palette=scope.put(case.weight.palette), output=out, bits=bits, rows=rows, inner=k,
+                            columns=n, bias=scope.put(case.bias), residual=scope.put(case.residual),
+                            residual_scale=scale, activation=act, label=f"stream-{copy}-{i}")
+            op.set_variant(small[0])
+            cases.append(case)
+            ops.append(op)
+            outs.append(out)
+    group = abi.GemmGroup(ctx, ops, label="stream-group")
+    try:
+        kinds = {}
+        for v in abi.small_m_variants():
+            group.set_variant(v)
+            plan = group.plan()
+            d = abi.describe_variant("f16", v)
+            kinds[v] = (plan.kernel.decode(), plan.grid[0], (d.tile_rows, d.tile_columns, d.k_split))
+        persistent = [v for v, (name, _, _) in kinds.items() if "_stream_" in name]
+        assert persistent, kinds
+        for v in persistent:
+            name, grid, shape = kinds[v]
+            partner = next(p for p, (n, _, s) in kinds.items() if s == shape and "_group_" in n)
+            print("rows", rows, name, "grid", grid, "against", kinds[partner][0], "grid", kinds[partner][1],
+                  flush=True)
+            assert grid < kinds[partner][1], (grid, kinds[partner][1])
+            results = []
+            for variant in (partner, v):
+                for out in outs:
+                    out.upload(np.full(out.shape, 7.0, np.float16))
+                group.set_variant(variant)
+                group.enqueue()
+                ctx.synchronize()
+                results.append([out.download() for out in outs])
+            for i, (want, got) in enumerate(zip(*results)):
+                np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16),
+                                              err_msg=f"{name} member {i}")
+        for i in range(len(STREAM_MEMBERS)):
+            assert_f16_parity(oracle, results[1][i], cases[i])
+    finally:
+        group.release()
+        for op in ops:
             op.release()
 
 
