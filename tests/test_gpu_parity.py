@@ -780,17 +780,20 @@ def test_gemm_group_persistent_matches_one_shot(abi, ctx, scope, oracle, workloa
             print("rows", rows, name, "grid", grid, "against", kinds[partner][0], "grid", kinds[partner][1],
                   flush=True)
             assert grid < kinds[partner][1], (grid, kinds[partner][1])
+            # the persistent kernel twice more (launch after launch)
             results = []
-            for variant in (partner, v):
+            for variant, launches in ((partner, 1), (v, 1), (v, 2)):
                 for out in outs:
                     out.upload(np.full(out.shape, 7.0, np.float16))
                 group.set_variant(variant)
-                group.enqueue()
+                for _ in range(launches):
+                    group.enqueue()
                 ctx.synchronize()
                 results.append([out.download() for out in outs])
-            for i, (want, got) in enumerate(zip(*results)):
-                np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16),
-                                              err_msg=f"{name} member {i}")
+            for run in results[1:]:
+                for i, (want, got) in enumerate(zip(results[0], run)):
+                    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16),
+                                                  err_msg=f"{name} member {i}")
         for i in range(len(STREAM_MEMBERS)):
             assert_f16_parity(oracle, results[1][i], cases[i])
     finally:
