@@ -733,7 +733,7 @@ STREAM_MEMBERS = [
     (4096, 1024, 5, 1, "none", False, 0.5),    # FF contract + 0.5 residual
     (1024, 3072, 5, 3, "none", False, None),   # QKV, 3 palette groups
     (1024, 1024, 6, 1, "none", False, 1.0),    # output projection + residual
-    (1536, 512, 6, 1, "relu", True, None),     # K = 3 x 512, bias, ReLU
+    (2048, 512, 6, 1, "relu", True, None),     # K = 2048, bias, ReLU
 ]
 
 
