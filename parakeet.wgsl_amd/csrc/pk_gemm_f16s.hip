@@ -380,8 +380,9 @@ __global__ __launch_bounds__(64 * W) void gemm_f16s_group_kernel(SmallMGroupArgs
 // issues the next item's palette entry, first D code blocks and first
 // activation fragments into the registers those blocks free; each item's
 // bias and residual are staged in LDS before its K loop, so that the
-// epilogue issues no load (its waits would reach the prefetched ones). Same K blocks per wavefront,
-// same MFMA and reduction order: every output equals the one-shot kernel's.
+// epilogue issues no load (its waits would reach the prefetched ones).
+// Same K blocks per wavefront, same MFMA and reduction order: every output
+// equals the one-shot kernel's.
 //
 // Fixed-palette body only; the host runs it when every member has
 // K % (64 * W * D) == 0 (each wavefront takes a whole number of groups of
