@@ -618,8 +618,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC, OCC
         load_codes(ahead, ahead_block + (uint32_t)u, cr[u]);
       }
     }
-    // The pair table was last read by this item's gathers; the palette area
-    // by its pair table build.
+    // The palette area was last read by this item's pair table build (before
+    // the barrier ahead of the K loop): the next item's entries go in now.
     if ((uint32_t)it < (1u << nxt.bits)) sh.lut[it] = pv;
 
     __syncthreads();  // the partials overwrite the pair table
