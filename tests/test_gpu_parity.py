@@ -802,6 +802,63 @@ def test_gemm_group_persistent_matches_one_shot(abi, ctx, scope, oracle, workloa
             op.release()
 
 
+@pytest.mark.parametrize("active", [33, 1])
+def test_gemm_group_persistent_prefix(abi, ctx, scope, workloads, active):
+    """An active prefix on the planned persistent kernel (a partial last row
+    group, or one row): rows past it keep their sentinel, and the prefix
+    equals both the full launch's rows and the one-shot launch of the same
+    tile bit for bit, over enough items that every workgroup runs several."""
+    capacity = 96
+    small = small_m_variants(abi, ctx, scope, workloads)
+    items_per_copy = sum(-(-n // 128) for _, n, *_ in STREAM_MEMBERS) * -(-active // 32)
+    ops, outs = [], []
+    for copy in range(-(-1600 // items_per_copy)):
+        for i, (k, n, bits, groups, act, bias, scale) in enumerate(STREAM_MEMBERS):
+            case = workloads.gemm_case(active * 71 + copy * 13 + i, capacity, k, n, bits, groups=groups,
+                                       activation=act, bias=bias, residual_scale=scale)
+            out = scope.put(np.full((capacity, n), 7.0, np.float16))
+            op = abi.GemmOp(ctx, a=scope.put(case.a), packed=scope.put(case.weight.packed),
+                            palette=scope.put(case.weight.palette), output=out, bits=bits, rows=capacity, inner=k,
+                            columns=n, bias=scope.put(case.bias), residual=scope.put(case.residual),
+                            residual_scale=scale, activation=act, label=f"prefix-{copy}-{i}")
+            op.set_variant(small[0])
+            ops.append(op)
+            outs.append(out)
+    group = abi.GemmGroup(ctx, ops, label="stream-prefix")
+    try:
+        plan = group.plan(active)
+        planned = plan.kernel.decode()
+        assert "_stream_" in planned, planned
+        kinds = {}
+        for v in abi.small_m_variants():
+            group.set_variant(v)
+            e = abi.describe_variant("f16", v)
+            kinds[v] = (group.plan(active).kernel.decode(), (e.tile_rows, e.tile_columns, e.k_split))
+        group.set_variant(-1)
+        shape = next(sh for name, sh in kinds.values() if name == planned)
+        partner = next(v for v, (name, sh) in kinds.items() if sh == shape and "_group_" in name)
+        print("active", active, planned, "grid", plan.grid[0], flush=True)
+        runs = []
+        for variant, rows in ((-1, active), (-1, 0), (partner, active)):
+            for out in outs:
+                out.upload(np.full(out.shape, 7.0, np.float16))
+            group.set_variant(variant)
+            group.enqueue(rows)
+            ctx.synchronize()
+            runs.append([out.download() for out in outs])
+        group.set_variant(-1)
+        for i, (prefix, full, one_shot) in enumerate(zip(*runs)):
+            assert (prefix[active:] == np.float16(7.0)).all(), i
+            np.testing.assert_array_equal(prefix[:active].view(np.uint16), full[:active].view(np.uint16),
+                                          err_msg=f"member {i} prefix against full")
+            np.testing.assert_array_equal(prefix.view(np.uint16), one_shot.view(np.uint16),
+                                          err_msg=f"member {i} persistent against one-shot")
+    finally:
+        group.release()
+        for op in ops:
+            op.release()
+
+
 def test_gemm_group_errors(abi, ctx, scope, workloads):
     """Members on another code layout, rows past the capacity and variants of
     other kernel families are refused with PK_RANGE_ERROR."""
